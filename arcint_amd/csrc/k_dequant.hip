@@ -1,0 +1,118 @@
+// k_dequant.hip - dequantize_row_* of ggml on gfx950, bit-exact.
+//
+// Each thread expands one 32-weight group (one 64-weight chunk for Q4_K) of
+// one block in the evaluation order of ggml's dequantize_row_* (restated in
+// tools/mtp_fit.py:360-409; kernel forms at P02:2956-2984 (Q4_0),
+// P02:4359-4378 (Q8_0), P01:2199-2247 (Q4_K, Q6_K), P01:3390-3398 (IQ4_XS)).
+// Every product here is exact in fp32 except the last multiply (Q6_K,
+// IQ4_XS) or the last subtract (Q4_K), so contraction is switched off to
+// keep that single rounding where ggml has it.
+#include "qmm_device.h"
+
+namespace qmm {
+namespace {
+
+#pragma clang fp contract(off)
+
+__global__ void k_deq_q4_0(WView w, int64_t nblk, float * __restrict__ y) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblk) return;
+    const uint4 q = ld16(w.p[0] + i * 16);
+    const float d = h2f(reinterpret_cast<const uint16_t *>(w.p[1])[i]);
+    const uint32_t qs[4] = { q.x, q.y, q.z, q.w };
+    float * o = y + i * 32;
+    for (int j = 0; j < 16; ++j) {
+        const uint32_t b = (qs[j >> 2] >> (8 * (j & 3))) & 0xffu;
+        o[j]      = (float)((int)(b & 0xfu) - 8) * d;
+        o[j + 16] = (float)((int)(b >> 4) - 8) * d;
+    }
+}
+
+__global__ void k_deq_q8_0(WView w, int64_t nblk, float * __restrict__ y) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblk) return;
+    const int8_t * q = reinterpret_cast<const int8_t *>(w.p[0] + i * 32);
+    const float d = h2f(reinterpret_cast<const uint16_t *>(w.p[1])[i]);
+    float * o = y + i * 32;
+    for (int j = 0; j < 32; ++j) o[j] = (float)q[j] * d;
+}
+
+// thread = (block, chunk c of 64 weights)
+__global__ void k_deq_q4_K(WView w, int64_t nblk, float * __restrict__ y) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nblk * 4) return;
+    const int64_t i = t >> 2;
+    const int c = (int)(t & 3);
+    const uint8_t * b = w.p[0] + i * 144;
+    const float d = h2f(reinterpret_cast<const uint16_t *>(b)[0]);
+    const float dmin = h2f(reinterpret_cast<const uint16_t *>(b)[1]);
+    const uint8_t * s = b + 4;
+    int sc[2], m[2];
+    for (int h = 0; h < 2; ++h) {
+        const int j = 2 * c + h;
+        if (j < 4) { sc[h] = s[j] & 63; m[h] = s[j + 4] & 63; }
+        else { sc[h] = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4); m[h] = (s[j + 4] >> 4) | ((s[j] >> 6) << 4); }
+    }
+    const float d1 = d * (float)sc[0], m1 = dmin * (float)m[0];
+    const float d2 = d * (float)sc[1], m2 = dmin * (float)m[1];
+    const uint8_t * q = b + 16 + 32 * c;
+    float * o = y + i * 256 + 64 * c;
+    for (int l = 0; l < 32; ++l) o[l] = d1 * (float)(q[l] & 0xF) - m1;
+    for (int l = 0; l < 32; ++l) o[32 + l] = d2 * (float)(q[l] >> 4) - m2;
+}
+
+// thread = (block, 32-weight group r = 32g + l within half n)
+__global__ void k_deq_q6_K(WView w, int64_t nblk, float * __restrict__ y) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nblk * 8) return;
+    const int64_t i = t >> 3;
+    const int grp = (int)(t & 7), n = grp >> 2, g = grp & 3;
+    const uint8_t * ql = w.p[0] + i * 128 + 64 * n + 32 * (g & 1);
+    const uint8_t * qh = w.p[1] + i * 64 + 32 * n;
+    const int8_t * sc = reinterpret_cast<const int8_t *>(w.p[2] + i * 16) + 8 * n + 2 * g;
+    const float d = h2f(reinterpret_cast<const uint16_t *>(w.p[3])[i]);
+    float * o = y + i * 256 + 128 * n + 32 * g;
+    for (int l = 0; l < 32; ++l) {
+        const int lo = (g < 2) ? (ql[l] & 0xF) : (ql[l] >> 4);
+        const int q = lo | (((qh[l] >> (2 * g)) & 3) << 4);
+        o[l] = d * (float)sc[l >> 4] * (float)(q - 32);
+    }
+}
+
+// thread = (block, 32-weight sub-block ib)
+__global__ void k_deq_iq4_xs(WView w, int64_t nblk, float * __restrict__ y) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nblk * 8) return;
+    const int64_t i = t >> 3;
+    const int ib = (int)(t & 7);
+    const uint8_t * hdr = w.p[1] + i * 8;
+    const float d = h2f(reinterpret_cast<const uint16_t *>(hdr)[0]);
+    const uint32_t sh = reinterpret_cast<const uint16_t *>(hdr)[1];
+    const int ls = ((hdr[4 + ib / 2] >> (4 * (ib & 1))) & 0xF) | (((sh >> (2 * ib)) & 3) << 4);
+    const float dl = d * (float)(ls - 32);
+    const uint8_t * qs = w.p[0] + i * 128 + 16 * ib;
+    float * o = y + i * 256 + 32 * ib;
+    for (int j = 0; j < 16; ++j) {
+        o[j]      = dl * (float)kKvalues[qs[j] & 0xF];
+        o[j + 16] = dl * (float)kKvalues[qs[j] >> 4];
+    }
+}
+
+}  // namespace
+
+hipError_t launch_dequant(int type, const WView & w, int64_t nblk, float * y, hipStream_t s) {
+    if (nblk <= 0) return hipSuccess;
+    const int tpb = 256;
+    auto grid = [&](int64_t n) { return dim3((unsigned)((n + tpb - 1) / tpb)); };
+    switch (type) {
+        case QMM_TYPE_Q4_0:   k_deq_q4_0<<<grid(nblk), tpb, 0, s>>>(w, nblk, y); break;
+        case QMM_TYPE_Q8_0:   k_deq_q8_0<<<grid(nblk), tpb, 0, s>>>(w, nblk, y); break;
+        case QMM_TYPE_Q4_K:   k_deq_q4_K<<<grid(nblk * 4), tpb, 0, s>>>(w, nblk, y); break;
+        case QMM_TYPE_Q6_K:   k_deq_q6_K<<<grid(nblk * 8), tpb, 0, s>>>(w, nblk, y); break;
+        case QMM_TYPE_IQ4_XS: k_deq_iq4_xs<<<grid(nblk * 8), tpb, 0, s>>>(w, nblk, y); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace qmm

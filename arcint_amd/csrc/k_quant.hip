@@ -1,0 +1,157 @@
+// k_quant.hip - activation quantization on gfx950, bit-exact with ggml-cpu's
+// from_float for the vec_dot type:
+//   q8_0  x86 quantize_row_q8_0 (restated at 0000-03-...patch:646-669):
+//         d = fp16(amax / 127), codes = round-half-even(x * (127 / amax))
+//   q8_K  quantize_row_q8_K_ref (restated at 0000-03-...patch:673-683):
+//         mx = first element of largest |x|, iscale = -127 / mx,
+//         codes = min(127, round-half-even(iscale * x)), d = 1 / iscale,
+//         bsums = sums of 16 codes; an all-zero block stays zero.
+// Divisions are IEEE (hipcc's default correctly-rounded f32 divide) and no
+// multiply is contracted, so every code and scale equals the CPU's.
+#include "qmm_device.h"
+
+namespace qmm {
+namespace {
+
+#pragma clang fp contract(off)
+
+__device__ __forceinline__ const float * col_ptr(const F32Cols & s, int64_t c) {
+    const int64_t i1 = c % s.ne1, r = c / s.ne1, i2 = r % s.ne2, i3 = r / s.ne2;
+    return reinterpret_cast<const float *>(s.base + i1 * s.nb1 + i2 * s.nb2 + i3 * s.nb3);
+}
+
+// 8 lanes per 32-weight block, 4 weights per lane
+__global__ void k_quant_q8_0(F32Cols src, int64_t K, int64_t ncols, ActBuf a, int want_h) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t kq = K / 4;
+    const bool live = t < ncols * kq;              // groups of 8 lanes are all live or all dead
+    const int64_t c = live ? t / kq : 0, k = live ? (t % kq) * 4 : 0;
+    float v[4] = { 0.f, 0.f, 0.f, 0.f };
+    if (live) {
+        const float * x = col_ptr(src, c) + k;
+        for (int i = 0; i < 4; ++i) v[i] = x[i];
+    }
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    for (int o = 1; o < 8; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    const _Float16 dh = (_Float16)(amax / 127.f);
+    const float mul = amax != 0.0f ? 127.f / amax : 0.0f;
+    int q[4], s = 0;
+    for (int i = 0; i < 4; ++i) {
+        float r = __builtin_rintf(v[i] * mul);
+        r = fminf(fmaxf(r, -128.f), 127.f);
+        q[i] = (int)r;
+        s += q[i];
+    }
+    for (int o = 1; o < 8; o <<= 1) s += __shfl_xor(s, o, 64);
+    if (!live) return;
+    const int64_t base = c * K + k;
+    const uint32_t packed = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
+                            ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
+    *reinterpret_cast<uint32_t *>(a.codes + base) = packed;
+    if (want_h) {
+        for (int i = 0; i < 4; ++i) a.hcodes[base + i] = (_Float16)q[i];
+    }
+    if ((t & 7) == 0) {
+        const int64_t b = c * (K / 32) + k / 32;
+        a.d[b] = (float)dh;
+        a.sums[b] = (int16_t)s;
+    }
+}
+
+// one wave per 256-weight super-block, 4 weights per lane
+__global__ void k_quant_q8_K(F32Cols src, int64_t K, int64_t ncols, ActBuf a, int want_h) {
+    const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int lane = threadIdx.x & 63;
+    const int64_t nsb = K / 256;
+    if (wave >= ncols * nsb) return;               // whole waves only
+    const int64_t c = wave / nsb, sb = wave % nsb;
+    const float * x = col_ptr(src, c) + sb * 256 + 4 * lane;
+    float v[4];
+    for (int i = 0; i < 4; ++i) v[i] = x[i];
+    // first index of the largest |x| (ggml: `if (ax > amax)` in order)
+    float ba = -1.0f;
+    int bi = 0;
+    for (int i = 0; i < 4; ++i) {
+        const float av = fabsf(v[i]);
+        if (av > ba) { ba = av; bi = 4 * lane + i; }
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        const float oa = __shfl_xor(ba, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (oa > ba || (oa == ba && oi < bi)) { ba = oa; bi = oi; }
+    }
+    const float pick = (bi & 3) == 0 ? v[0] : (bi & 3) == 1 ? v[1] : (bi & 3) == 2 ? v[2] : v[3];
+    const float mx = __shfl(pick, bi >> 2, 64);
+    const int64_t base = c * K + sb * 256 + 4 * lane;
+    int q[4] = { 0, 0, 0, 0 };
+    float dv = 0.0f;
+    if (ba != 0.0f) {
+        const float iscale = -127.f / mx;
+        for (int i = 0; i < 4; ++i) {
+            const int r = (int)__builtin_rintf(iscale * v[i]);
+            q[i] = r > 127 ? 127 : r;
+        }
+        dv = 1.0f / iscale;
+    }
+    int s = q[0] + q[1] + q[2] + q[3];
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    const uint32_t packed = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
+                            ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
+    *reinterpret_cast<uint32_t *>(a.codes + base) = packed;
+    if (want_h) {
+        for (int i = 0; i < 4; ++i) a.hcodes[base + i] = (_Float16)q[i];
+    }
+    if ((lane & 3) == 0) a.sums[c * (K / 16) + sb * 16 + (lane >> 2)] = (int16_t)s;
+    if (lane == 0) a.d[c * nsb + sb] = dv;
+}
+
+// ActBuf -> ggml block bytes, one thread per block
+__global__ void k_act_blocks(ActBuf a, uint8_t * __restrict__ out) {
+    const int bs = act_block(a.vdt);
+    const int64_t nb = a.ncols * (a.K / bs);
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nb) return;
+    const int8_t * codes = a.codes + i * bs;       // blocks of one column are contiguous
+    if (a.vdt == QMM_TYPE_Q8_0) {
+        uint8_t * o = out + i * 34;
+        const uint16_t h = __builtin_bit_cast(uint16_t, (_Float16)a.d[i]);
+        o[0] = (uint8_t)(h & 0xff);
+        o[1] = (uint8_t)(h >> 8);
+        for (int j = 0; j < 32; ++j) o[2 + j] = (uint8_t)codes[j];
+    } else {
+        uint8_t * o = out + i * 292;
+        const uint32_t db = __builtin_bit_cast(uint32_t, a.d[i]);
+        for (int j = 0; j < 4; ++j) o[j] = (uint8_t)(db >> (8 * j));
+        for (int j = 0; j < 256; ++j) o[4 + j] = (uint8_t)codes[j];
+        for (int j = 0; j < 16; ++j) {
+            const uint16_t v = (uint16_t)a.sums[i * 16 + j];
+            o[260 + 2 * j] = (uint8_t)(v & 0xff);
+            o[261 + 2 * j] = (uint8_t)(v >> 8);
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_quantize(const F32Cols & src, int64_t K, int64_t ncols, const ActBuf & a, bool want_h, hipStream_t s) {
+    if (ncols <= 0 || K <= 0) return hipSuccess;
+    const int tpb = 256;
+    if (a.vdt == QMM_TYPE_Q8_0) {
+        const int64_t n = ncols * (K / 4);
+        k_quant_q8_0<<<dim3((unsigned)((n + tpb - 1) / tpb)), tpb, 0, s>>>(src, K, ncols, a, want_h ? 1 : 0);
+    } else {
+        const int64_t n = ncols * (K / 256) * 64;
+        k_quant_q8_K<<<dim3((unsigned)((n + tpb - 1) / tpb)), tpb, 0, s>>>(src, K, ncols, a, want_h ? 1 : 0);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_act_to_blocks(const ActBuf & a, void * out, hipStream_t s) {
+    const int64_t nb = a.ncols * (a.K / act_block(a.vdt));
+    if (nb <= 0) return hipSuccess;
+    k_act_blocks<<<dim3((unsigned)((nb + 255) / 256)), 256, 0, s>>>(a, (uint8_t *)out);
+    return hipGetLastError();
+}
+
+}  // namespace qmm

@@ -1,0 +1,614 @@
+// qmm_api.cpp - the C ABI of libqmm (include/qmm.h): device context, buffers,
+// GGUF <-> planar repack, op validation and dispatch.  Host C++ calling HIP
+// directly; one in-order stream per context, like one ggml backend.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "qmm_internal.h"
+
+using namespace qmm;
+
+struct qmm_buffer {
+    void * ptr = nullptr;
+    size_t size = 0;
+};
+
+struct qmm_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    std::string err;
+    std::string path = "none";
+    // activation scratch
+    void * act = nullptr;
+    size_t act_cap = 0;
+    // activation dedup inside qmm_graph_compute
+    uint64_t graph_gen = 0;
+    bool in_graph = false;
+    struct ActKey {
+        const qmm_buffer * buf = nullptr;
+        size_t offs = 0;
+        int64_t ne[4] = { 0, 0, 0, 0 };
+        size_t nb[4] = { 0, 0, 0, 0 };
+        int vdt = 0;
+        bool hcodes = false;
+        uint64_t gen = 0;
+        bool valid = false;
+    } key;
+    ActBuf cached{};
+    // MoE route scratch: ids copy, tasks, task count
+    void * route = nullptr;
+    size_t route_cap = 0;
+    // downgrade counter (paths slower than the type promises)
+    int64_t downgrades = 0;
+    std::string downgrade_names;
+};
+
+namespace {
+
+int fail(qmm_ctx * ctx, int code, const char * fmt, ...) {
+    if (ctx) {
+        char buf[512];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(buf, sizeof(buf), fmt, ap);
+        va_end(ap);
+        ctx->err = buf;
+    }
+    return code;
+}
+
+#define QMM_HIP(ctx, expr)                                                                        \
+    do {                                                                                          \
+        const hipError_t e_ = (expr);                                                             \
+        if (e_ != hipSuccess) return fail((ctx), QMM_ERR_DEVICE, "%s: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+const TypeLayout kLayouts[] = {
+    { QMM_TYPE_Q4_0, 32, 18, 2, { { 2, 16 }, { 0, 2 }, { 0, 0 }, { 0, 0 } } },
+    { QMM_TYPE_Q8_0, 32, 34, 2, { { 2, 32 }, { 0, 2 }, { 0, 0 }, { 0, 0 } } },
+    { QMM_TYPE_Q4_K, 256, 144, 1, { { 0, 144 }, { 0, 0 }, { 0, 0 }, { 0, 0 } } },
+    { QMM_TYPE_Q6_K, 256, 210, 4, { { 0, 128 }, { 128, 64 }, { 192, 16 }, { 208, 2 } } },
+    { QMM_TYPE_IQ4_XS, 256, 136, 2, { { 8, 128 }, { 0, 8 }, { 0, 0 }, { 0, 0 } } },
+};
+
+bool is_quant(int type) { return type_layout(type) != nullptr; }
+
+size_t plain_elem(int type) {
+    switch (type) {
+        case QMM_TYPE_F32: return 4;
+        case QMM_TYPE_F16: return 2;
+        case QMM_TYPE_I32: return 4;
+        default: return 0;
+    }
+}
+
+int64_t nelements(const int64_t ne[4]) { return ne[0] * ne[1] * ne[2] * ne[3]; }
+
+bool contiguous(const qmm_tensor * t) {
+    const TypeLayout * L = type_layout(t->type);
+    size_t s = L ? (size_t)L->bytes : plain_elem(t->type);
+    int64_t n0 = L ? t->ne[0] / L->blck : t->ne[0];
+    if (t->nb[0] != s) return false;
+    size_t expect = s * (size_t)n0;
+    for (int i = 1; i < 4; ++i) {
+        if (t->ne[i] > 1 && t->nb[i] != expect) return false;
+        expect *= (size_t)t->ne[i];
+    }
+    return true;
+}
+
+WView weight_view(const qmm_tensor * t, int64_t rows_per_mat) {
+    const TypeLayout & L = *type_layout(t->type);
+    const int64_t nblk = nelements(t->ne) / L.blck;
+    size_t off[4];
+    planes_alloc(L, nblk, off);
+    WView w{};
+    const uint8_t * base = (const uint8_t *)t->buffer->ptr + t->offs;
+    for (int q = 0; q < 4; ++q) w.p[q] = q < L.nfields ? base + off[q] : nullptr;
+    w.bpr = t->ne[0] / L.blck;
+    w.rows_per_mat = rows_per_mat;
+    return w;
+}
+
+// activation scratch layout for ncols columns of K
+size_t act_bytes(int vdt, int64_t K, int64_t ncols, bool hcodes, size_t * o_h, size_t * o_d, size_t * o_s) {
+    size_t off = align_up((size_t)(K * ncols), kPlaneAlign);
+    *o_h = off;
+    if (hcodes) off = align_up(off + (size_t)(K * ncols) * 2, kPlaneAlign);
+    *o_d = off;
+    off = align_up(off + (size_t)(ncols * (K / act_block(vdt))) * 4, kPlaneAlign);
+    *o_s = off;
+    off = align_up(off + (size_t)(ncols * (K / act_sum_block(vdt))) * 2, kPlaneAlign);
+    return off;
+}
+
+int ensure(qmm_ctx * ctx, void ** p, size_t * cap, size_t need) {
+    if (need <= *cap) return QMM_OK;
+    if (*p) {
+        QMM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        QMM_HIP(ctx, hipFree(*p));
+        *p = nullptr;
+        *cap = 0;
+        ctx->key.valid = false;
+    }
+    size_t sz = std::max(need, (size_t)(*cap * 3 / 2));
+    QMM_HIP(ctx, hipMalloc(p, sz));
+    *cap = sz;
+    return QMM_OK;
+}
+
+F32Cols f32_cols(const qmm_tensor * t) {
+    F32Cols c;
+    c.base = (const char *)t->buffer->ptr + t->offs;
+    c.ne1 = t->ne[1];
+    c.ne2 = t->ne[2];
+    c.nb1 = t->nb[1];
+    c.nb2 = t->nb[2];
+    c.nb3 = t->nb[3];
+    return c;
+}
+
+// Quantize src1 (all its columns) with the vec_dot type of `type`, reusing
+// the previous result inside one graph when src1 is the same tensor.
+int quantize_src1(qmm_ctx * ctx, int type, const qmm_tensor * src1, bool hcodes, ActBuf * out) {
+    const int vdt = vec_dot_type(type);
+    const int64_t K = src1->ne[0], ncols = src1->ne[1] * src1->ne[2] * src1->ne[3];
+    auto & k = ctx->key;
+    if (ctx->in_graph && k.valid && k.gen == ctx->graph_gen && k.buf == src1->buffer && k.offs == src1->offs &&
+        k.vdt == vdt && (k.hcodes || !hcodes) && !memcmp(k.ne, src1->ne, sizeof(k.ne)) &&
+        !memcmp(k.nb, src1->nb, sizeof(k.nb))) {
+        *out = ctx->cached;
+        return QMM_OK;
+    }
+    size_t oh, od, os;
+    const size_t need = act_bytes(vdt, K, ncols, hcodes, &oh, &od, &os);
+    int rc = ensure(ctx, &ctx->act, &ctx->act_cap, need);
+    if (rc) return rc;
+    uint8_t * b = (uint8_t *)ctx->act;
+    ActBuf a;
+    a.codes = (int8_t *)b;
+    a.hcodes = hcodes ? (_Float16 *)(b + oh) : nullptr;
+    a.d = (float *)(b + od);
+    a.sums = (int16_t *)(b + os);
+    a.K = K;
+    a.ncols = ncols;
+    a.vdt = vdt;
+    QMM_HIP(ctx, launch_quantize(f32_cols(src1), K, ncols, a, hcodes, ctx->stream));
+    k.buf = src1->buffer;
+    k.offs = src1->offs;
+    memcpy(k.ne, src1->ne, sizeof(k.ne));
+    memcpy(k.nb, src1->nb, sizeof(k.nb));
+    k.vdt = vdt;
+    k.hcodes = hcodes;
+    k.gen = ctx->graph_gen;
+    k.valid = true;
+    ctx->cached = a;
+    *out = a;
+    return QMM_OK;
+}
+
+bool ranges_overlap(const qmm_tensor * a, const qmm_tensor * b) {
+    if (!a || !b || a->buffer != b->buffer) return false;
+    auto span = [](const qmm_tensor * t) {
+        size_t last = 0;
+        for (int i = 0; i < 4; ++i) last += (size_t)(t->ne[i] - 1) * t->nb[i];
+        return last + t->nb[0];
+    };
+    const size_t a0 = a->offs, a1 = a->offs + span(a), b0 = b->offs, b1 = b->offs + span(b);
+    return a0 < b1 && b0 < a1;
+}
+
+bool check_f32(const qmm_tensor * t) {
+    return t && t->buffer && t->type == QMM_TYPE_F32 && t->nb[0] == sizeof(float) && t->ne[0] > 0;
+}
+
+void note_downgrade(qmm_ctx * ctx, const char * key) {
+    ctx->downgrades++;
+    ctx->downgrade_names = key;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+namespace qmm {
+
+const TypeLayout * type_layout(int type) {
+    for (const auto & L : kLayouts)
+        if (L.type == type) return &L;
+    return nullptr;
+}
+
+size_t plane_bytes(const TypeLayout & L, int q, int64_t nblk) { return (size_t)L.f[q].size * (size_t)nblk; }
+
+size_t planes_alloc(const TypeLayout & L, int64_t nblk, size_t plane_off[4]) {
+    size_t off = 0;
+    for (int q = 0; q < 4; ++q) {
+        plane_off[q] = off;
+        if (q < L.nfields) off = align_up(off + plane_bytes(L, q, nblk), kPlaneAlign);
+    }
+    return off;
+}
+
+}  // namespace qmm
+
+// ---------------------------------------------------------------------------
+extern "C" {
+
+int qmm_ctx_create(int device, qmm_ctx ** out) {
+    if (!out) return QMM_ERR_INVALID;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) return QMM_ERR_DEVICE;
+    qmm_ctx * ctx = new qmm_ctx();
+    ctx->device = device;
+    if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreate(&ctx->ev0) != hipSuccess || hipEventCreate(&ctx->ev1) != hipSuccess) {
+        delete ctx;
+        return QMM_ERR_DEVICE;
+    }
+    *out = ctx;
+    return QMM_OK;
+}
+
+void qmm_ctx_free(qmm_ctx * ctx) {
+    if (!ctx) return;
+    hipSetDevice(ctx->device);
+    if (ctx->stream) hipStreamSynchronize(ctx->stream);
+    if (ctx->act) hipFree(ctx->act);
+    if (ctx->route) hipFree(ctx->route);
+    if (ctx->ev0) hipEventDestroy(ctx->ev0);
+    if (ctx->ev1) hipEventDestroy(ctx->ev1);
+    if (ctx->stream) hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+const char * qmm_last_error(qmm_ctx * ctx) { return ctx ? ctx->err.c_str() : "no context"; }
+const char * qmm_last_path(qmm_ctx * ctx) { return ctx ? ctx->path.c_str() : "none"; }
+
+int qmm_buffer_alloc(qmm_ctx * ctx, size_t size, qmm_buffer ** out) {
+    if (!ctx || !out) return QMM_ERR_INVALID;
+    *out = nullptr;
+    QMM_HIP(ctx, hipSetDevice(ctx->device));
+    qmm_buffer * b = new qmm_buffer();
+    const hipError_t e = hipMalloc(&b->ptr, std::max<size_t>(size, 256));
+    if (e != hipSuccess) {
+        delete b;
+        return fail(ctx, QMM_ERR_NOMEM, "hipMalloc(%zu): %s", size, hipGetErrorString(e));
+    }
+    b->size = size;
+    *out = b;
+    return QMM_OK;
+}
+
+void qmm_buffer_free(qmm_ctx * ctx, qmm_buffer * buf) {
+    if (!buf) return;
+    if (ctx) {
+        hipStreamSynchronize(ctx->stream);
+        if (ctx->key.buf == buf) ctx->key.valid = false;
+    }
+    hipFree(buf->ptr);
+    delete buf;
+}
+
+size_t qmm_buffer_size(const qmm_buffer * buf) { return buf ? buf->size : 0; }
+void * qmm_buffer_base(const qmm_buffer * buf) { return buf ? buf->ptr : nullptr; }
+
+int qmm_type_block(int32_t type, size_t * block_bytes) {
+    if (const TypeLayout * L = type_layout(type)) {
+        if (block_bytes) *block_bytes = (size_t)L->bytes;
+        return L->blck;
+    }
+    const size_t e = plain_elem(type);
+    if (!e) return 0;
+    if (block_bytes) *block_bytes = e;
+    return 1;
+}
+
+size_t qmm_tensor_nbytes(int32_t type, const int64_t ne[4]) {
+    size_t bb = 0;
+    const int bl = qmm_type_block(type, &bb);
+    if (!bl || ne[0] % bl) return 0;
+    return (size_t)(nelements(ne) / bl) * bb;
+}
+
+size_t qmm_tensor_alloc_size(int32_t type, const int64_t ne[4]) {
+    const TypeLayout * L = type_layout(type);
+    if (!L) return qmm_tensor_nbytes(type, ne);
+    if (ne[0] % L->blck) return 0;
+    size_t off[4];
+    return planes_alloc(*L, nelements(ne) / L->blck, off);
+}
+
+static int tensor_io(qmm_ctx * ctx, const qmm_tensor * t, void * host, size_t offset, size_t size, bool write) {
+    if (!ctx || !t || !t->buffer || (!host && size)) return fail(ctx, QMM_ERR_INVALID, "tensor io: null argument");
+    QMM_HIP(ctx, hipSetDevice(ctx->device));
+    if (!contiguous(t)) return fail(ctx, QMM_ERR_INVALID, "tensor io: tensor is not contiguous");
+    const size_t total = qmm_tensor_nbytes(t->type, t->ne);
+    if (offset > total || size > total - offset) return fail(ctx, QMM_ERR_INVALID, "tensor io: range past the tensor");
+    const size_t alloc = qmm_tensor_alloc_size(t->type, t->ne);
+    if (t->offs + alloc > t->buffer->size) return fail(ctx, QMM_ERR_INVALID, "tensor io: tensor past its buffer");
+    uint8_t * dev = (uint8_t *)t->buffer->ptr + t->offs;
+    if (write) ctx->key.valid = false;
+    const TypeLayout * L = type_layout(t->type);
+    if (!L || L->nfields == 1) {   // the device bytes are the GGUF bytes
+        if (write) QMM_HIP(ctx, hipMemcpyAsync(dev + offset, host, size, hipMemcpyHostToDevice, ctx->stream));
+        else QMM_HIP(ctx, hipMemcpyAsync(host, dev + offset, size, hipMemcpyDeviceToHost, ctx->stream));
+        QMM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        return QMM_OK;
+    }
+    if (offset % L->bytes || size % L->bytes)
+        return fail(ctx, QMM_ERR_INVALID, "tensor io: offset %zu / size %zu not whole %d-byte blocks", offset, size, L->bytes);
+    const int64_t nblk = nelements(t->ne) / L->blck, b0 = (int64_t)(offset / L->bytes), nb = (int64_t)(size / L->bytes);
+    size_t poff[4];
+    planes_alloc(*L, nblk, poff);
+    // staged in pieces so that large tensors do not need one huge host copy
+    const int64_t piece = 1 << 18;
+    std::vector<uint8_t> stage;
+    uint8_t * h = (uint8_t *)host;
+    for (int64_t s0 = 0; s0 < nb; s0 += piece) {
+        const int64_t n = std::min(piece, nb - s0);
+        for (int q = 0; q < L->nfields; ++q) {
+            const Field f = L->f[q];
+            stage.resize((size_t)(n * f.size));
+            uint8_t * pd = dev + poff[q] + (size_t)(b0 + s0) * f.size;
+            if (write) {
+                for (int64_t i = 0; i < n; ++i) memcpy(&stage[(size_t)(i * f.size)], h + (size_t)(s0 + i) * L->bytes + f.off, (size_t)f.size);
+                QMM_HIP(ctx, hipMemcpyAsync(pd, stage.data(), stage.size(), hipMemcpyHostToDevice, ctx->stream));
+                QMM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+            } else {
+                QMM_HIP(ctx, hipMemcpyAsync(stage.data(), pd, stage.size(), hipMemcpyDeviceToHost, ctx->stream));
+                QMM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+                for (int64_t i = 0; i < n; ++i) memcpy(h + (size_t)(s0 + i) * L->bytes + f.off, &stage[(size_t)(i * f.size)], (size_t)f.size);
+            }
+        }
+    }
+    return QMM_OK;
+}
+
+int qmm_tensor_set(qmm_ctx * ctx, const qmm_tensor * t, const void * data, size_t offset, size_t size) {
+    return tensor_io(ctx, t, const_cast<void *>(data), offset, size, true);
+}
+
+int qmm_tensor_get(qmm_ctx * ctx, const qmm_tensor * t, void * data, size_t offset, size_t size) {
+    return tensor_io(ctx, t, data, offset, size, false);
+}
+
+int qmm_buffer_copy(qmm_ctx * ctx, qmm_buffer * dst, size_t dst_off, const qmm_buffer * src, size_t src_off, size_t size) {
+    if (!ctx || !dst || !src || dst_off + size > dst->size || src_off + size > src->size)
+        return fail(ctx, QMM_ERR_INVALID, "buffer copy out of range");
+    QMM_HIP(ctx, hipMemcpyAsync((uint8_t *)dst->ptr + dst_off, (const uint8_t *)src->ptr + src_off, size,
+                                hipMemcpyDeviceToDevice, ctx->stream));
+    return QMM_OK;
+}
+
+// ---- validation ------------------------------------------------------------
+
+static bool why(char * reason, size_t len, const char * msg) {
+    if (reason && len) snprintf(reason, len, "%s", msg);
+    return false;
+}
+
+static bool mul_mat_ok(const qmm_tensor * s0, const qmm_tensor * s1, const qmm_tensor * d, char * reason, size_t len) {
+    if (!s0 || !s1 || !d || !s0->buffer || !s1->buffer || !d->buffer) return why(reason, len, "null tensor or buffer");
+    const TypeLayout * L = type_layout(s0->type);
+    if (!L) return why(reason, len, "src0 type is not Q4_0/Q8_0/Q4_K/Q6_K/IQ4_XS");
+    if (s0->ne[0] % L->blck) return why(reason, len, "ne00 is not a multiple of the block size");
+    if (!contiguous(s0)) return why(reason, len, "src0 is not contiguous");
+    if (!check_f32(s1) || !check_f32(d)) return why(reason, len, "src1/dst must be f32 with nb[0] == 4");
+    if (s1->ne[0] != s0->ne[0]) return why(reason, len, "src1 ne0 != src0 ne0");
+    if (s1->ne[0] % 256 && vec_dot_type(s0->type) == QMM_TYPE_Q8_K) return why(reason, len, "K is not a multiple of 256");
+    if (s0->ne[2] <= 0 || s0->ne[3] <= 0 || s1->ne[2] % s0->ne[2] || s1->ne[3] % s0->ne[3])
+        return why(reason, len, "src1 dims 2/3 do not broadcast src0");
+    if (d->ne[0] != s0->ne[1] || d->ne[1] != s1->ne[1] || d->ne[2] != s1->ne[2] || d->ne[3] != s1->ne[3])
+        return why(reason, len, "dst shape is not [M, N, ne12, ne13]");
+    if (d->nb[1] % 4 || d->nb[2] % 4 || d->nb[3] % 4) return why(reason, len, "dst strides are not whole floats");
+    if (s1->nb[1] % 4 || s1->nb[2] % 4 || s1->nb[3] % 4 || s1->offs % 4) return why(reason, len, "src1 strides are not whole floats");
+    return true;
+}
+
+static bool mul_mat_id_ok(const qmm_tensor * s0, const qmm_tensor * s1, const qmm_tensor * ids, const qmm_tensor * d,
+                          char * reason, size_t len) {
+    if (!s0 || !s1 || !ids || !d || !s0->buffer || !s1->buffer || !ids->buffer || !d->buffer)
+        return why(reason, len, "null tensor or buffer");
+    const TypeLayout * L = type_layout(s0->type);
+    if (!L) return why(reason, len, "src0 type is not Q4_0/Q8_0/Q4_K/Q6_K/IQ4_XS");
+    if (s0->ne[0] % L->blck || !contiguous(s0)) return why(reason, len, "src0 must be contiguous whole blocks");
+    if (s0->ne[3] != 1) return why(reason, len, "src0 must be [K, M, n_as]");
+    if (!check_f32(s1) || !check_f32(d)) return why(reason, len, "src1/dst must be f32 with nb[0] == 4");
+    if (ids->type != QMM_TYPE_I32 || ids->nb[0] != 4) return why(reason, len, "ids must be i32");
+    if (s1->ne[0] != s0->ne[0]) return why(reason, len, "src1 ne0 != src0 ne0");
+    if (s1->ne[0] % 256 && vec_dot_type(s0->type) == QMM_TYPE_Q8_K) return why(reason, len, "K is not a multiple of 256");
+    const int64_t n_used = ids->ne[0], T = ids->ne[1];
+    if (s1->ne[2] != T || s1->ne[3] != 1) return why(reason, len, "src1 must be [K, ne11, T]");
+    if (s1->ne[1] != 1 && s1->ne[1] != n_used) return why(reason, len, "src1 ne11 must be 1 or n_used");
+    if (d->ne[0] != s0->ne[1] || d->ne[1] != n_used || d->ne[2] != T) return why(reason, len, "dst must be [M, n_used, T]");
+    if (s0->ne[2] > 8192) return why(reason, len, "more than 8192 experts");
+    if (d->nb[1] % 4 || d->nb[2] % 4) return why(reason, len, "dst strides are not whole floats");
+    if (s1->nb[1] % 4 || s1->nb[2] % 4 || s1->offs % 4) return why(reason, len, "src1 strides are not whole floats");
+    return true;
+}
+
+int qmm_supports_op(qmm_ctx *, int32_t op, const qmm_tensor * src0, const qmm_tensor * src1, const qmm_tensor * ids,
+                    const qmm_tensor * dst, char * reason, size_t reason_len) {
+    if (op == QMM_OP_MUL_MAT) return mul_mat_ok(src0, src1, dst, reason, reason_len) ? 1 : 0;
+    if (op == QMM_OP_MUL_MAT_ID) return mul_mat_id_ok(src0, src1, ids, dst, reason, reason_len) ? 1 : 0;
+    why(reason, reason_len, "op is not MUL_MAT or MUL_MAT_ID");
+    return 0;
+}
+
+// ---- ops ---------------------------------------------------------------------
+
+// columns at or above which a 2-D batch goes to the MFMA GEMM
+static int64_t gemm_min_cols() {
+    static int64_t v = [] {
+        const char * e = getenv("QMM_GEMM_MIN_COLS");
+        return e ? std::max<int64_t>(1, atoll(e)) : (int64_t)1 << 40;
+    }();
+    return v;
+}
+
+int qmm_mul_mat(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1, const qmm_tensor * dst) {
+    if (!ctx) return QMM_ERR_INVALID;
+    char reason[160];
+    if (!mul_mat_ok(src0, src1, dst, reason, sizeof(reason))) return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat: %s", reason);
+    QMM_HIP(ctx, hipSetDevice(ctx->device));
+    const int64_t K = src0->ne[0], M = src0->ne[1];
+    const int64_t N = src1->ne[1];
+    const bool use_gemm = N >= gemm_min_cols();
+    ActBuf a;
+    int rc = quantize_src1(ctx, src0->type, src1, use_gemm, &a);
+    if (rc) return rc;
+    const WView w = weight_view(src0, M);
+    float * d = (float *)((uint8_t *)dst->buffer->ptr + dst->offs);
+    GemvDense dn;
+    dn.ne11 = N;
+    dn.ne12 = src1->ne[2];
+    dn.ne13 = src1->ne[3];
+    dn.r2 = src1->ne[2] / src0->ne[2];
+    dn.r3 = src1->ne[3] / src0->ne[3];
+    dn.ne02 = src0->ne[2];
+    dn.d_nb1 = (int64_t)(dst->nb[1] / 4);
+    dn.d_nb2 = (int64_t)(dst->nb[2] / 4);
+    dn.d_nb3 = (int64_t)(dst->nb[3] / 4);
+    const int nc = (int)std::min<int64_t>(N, kMaxTaskCols);
+    ctx->path = N <= kMaxTaskCols ? "gemv" : "gemv-tasks";
+    if (N > kMaxTaskCols) note_downgrade(ctx, "mul_mat: many columns on the GEMV");
+    QMM_HIP(ctx, launch_gemv_any(src0->type, w, M, K, a, nullptr, 0, nullptr, nc, &dn, d, ctx->stream));
+    return QMM_OK;
+}
+
+int qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1, const qmm_tensor * ids,
+                   const qmm_tensor * dst) {
+    if (!ctx) return QMM_ERR_INVALID;
+    char reason[160];
+    if (!mul_mat_id_ok(src0, src1, ids, dst, reason, sizeof(reason)))
+        return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat_id: %s", reason);
+    QMM_HIP(ctx, hipSetDevice(ctx->device));
+    const int64_t K = src0->ne[0], M = src0->ne[1], n_as = src0->ne[2];
+    const int64_t n_used = ids->ne[0], T = ids->ne[1], ne11 = src1->ne[1];
+    ActBuf a;
+    int rc = quantize_src1(ctx, src0->type, src1, false, &a);
+    if (rc) return rc;
+    const int64_t npairs = n_used * T;
+    const int64_t max_tasks = npairs / kMaxTaskCols + std::min(n_as, npairs) + 1;
+    const size_t o_tasks = align_up((size_t)npairs * 4, 256);
+    const size_t o_cnt = align_up(o_tasks + (size_t)max_tasks * sizeof(GemvTask), 256);
+    rc = ensure(ctx, &ctx->route, &ctx->route_cap, o_cnt + 256);
+    if (rc) return rc;
+    uint8_t * rb = (uint8_t *)ctx->route;
+    RouteArgs r;
+    r.ids = (const int32_t *)((const uint8_t *)ids->buffer->ptr + ids->offs);
+    r.ids_nb0 = ids->nb[0];
+    r.ids_nb1 = ids->nb[1];
+    r.n_used = n_used;
+    r.T = T;
+    r.ne11 = ne11;
+    r.n_as = n_as;
+    r.dst_nb1 = (int64_t)(dst->nb[1] / 4);
+    r.dst_nb2 = (int64_t)(dst->nb[2] / 4);
+    float * d = (float *)((uint8_t *)dst->buffer->ptr + dst->offs);
+    GemvTask * tasks = (GemvTask *)(rb + o_tasks);
+    int32_t * ntasks = (int32_t *)(rb + o_cnt);
+    QMM_HIP(ctx, launch_route(r, (int32_t *)rb, tasks, ntasks, d, M, ctx->stream));
+    const WView w = weight_view(src0, M);
+    const int nc = (int)std::min<int64_t>(kMaxTaskCols, T);
+    ctx->path = "gemv-id";
+    QMM_HIP(ctx, launch_gemv_any(src0->type, w, M, K, a, tasks, (int)max_tasks, ntasks, nc, nullptr, d, ctx->stream));
+    return QMM_OK;
+}
+
+int qmm_graph_compute(qmm_ctx * ctx, const qmm_node * nodes, int n_nodes) {
+    if (!ctx || (!nodes && n_nodes)) return QMM_ERR_INVALID;
+    ctx->graph_gen++;
+    ctx->in_graph = true;
+    int rc = QMM_OK;
+    for (int i = 0; i < n_nodes && rc == QMM_OK; ++i) {
+        const qmm_node & n = nodes[i];
+        if (n.op == QMM_OP_MUL_MAT) rc = qmm_mul_mat(ctx, n.src0, n.src1, n.dst);
+        else if (n.op == QMM_OP_MUL_MAT_ID) rc = qmm_mul_mat_id(ctx, n.src0, n.src1, n.ids, n.dst);
+        else rc = fail(ctx, QMM_ERR_UNSUPPORTED, "graph node %d: unsupported op %d", i, n.op);
+        // a node that writes over the cached activations' source invalidates them
+        if (ctx->key.valid) {
+            qmm_tensor src{};
+            src.type = QMM_TYPE_F32;
+            src.buffer = const_cast<qmm_buffer *>(ctx->key.buf);
+            src.offs = ctx->key.offs;
+            memcpy(src.ne, ctx->key.ne, sizeof(src.ne));
+            memcpy(src.nb, ctx->key.nb, sizeof(src.nb));
+            if (ranges_overlap(&src, n.dst)) ctx->key.valid = false;
+        }
+    }
+    ctx->in_graph = false;
+    return rc;
+}
+
+int qmm_dequantize(qmm_ctx * ctx, const qmm_tensor * src, const qmm_tensor * dst) {
+    if (!ctx || !src || !dst || !src->buffer || !dst->buffer) return fail(ctx, QMM_ERR_INVALID, "dequantize: null argument");
+    const TypeLayout * L = type_layout(src->type);
+    if (!L || src->ne[0] % L->blck || !contiguous(src)) return fail(ctx, QMM_ERR_UNSUPPORTED, "dequantize: unsupported source");
+    if (dst->type != QMM_TYPE_F32 || !contiguous(dst) || nelements(dst->ne) != nelements(src->ne))
+        return fail(ctx, QMM_ERR_INVALID, "dequantize: dst must be contiguous f32 with as many elements");
+    QMM_HIP(ctx, hipSetDevice(ctx->device));
+    const WView w = weight_view(src, src->ne[1]);
+    float * y = (float *)((uint8_t *)dst->buffer->ptr + dst->offs);
+    QMM_HIP(ctx, launch_dequant(src->type, w, nelements(src->ne) / L->blck, y, ctx->stream));
+    return QMM_OK;
+}
+
+int qmm_quantize_act(qmm_ctx * ctx, int32_t act_type, const qmm_tensor * src, void * out, size_t out_size) {
+    if (!ctx || !check_f32(src) || !out) return fail(ctx, QMM_ERR_INVALID, "quantize_act: bad argument");
+    if (act_type != QMM_TYPE_Q8_0 && act_type != QMM_TYPE_Q8_K) return fail(ctx, QMM_ERR_INVALID, "quantize_act: type");
+    const int bs = act_block(act_type), bb = act_type == QMM_TYPE_Q8_0 ? 34 : 292;
+    const int64_t K = src->ne[0], ncols = src->ne[1] * src->ne[2] * src->ne[3];
+    if (K % bs) return fail(ctx, QMM_ERR_INVALID, "quantize_act: K %% %d != 0", bs);
+    const size_t need = (size_t)(ncols * (K / bs)) * bb;
+    if (out_size < need) return fail(ctx, QMM_ERR_INVALID, "quantize_act: out needs %zu bytes", need);
+    QMM_HIP(ctx, hipSetDevice(ctx->device));
+    ctx->key.valid = false;
+    ActBuf a;
+    int rc = quantize_src1(ctx, act_type == QMM_TYPE_Q8_0 ? QMM_TYPE_Q4_0 : QMM_TYPE_Q4_K, src, true, &a);
+    if (rc) return rc;
+    void * tmp = nullptr;
+    QMM_HIP(ctx, hipMalloc(&tmp, need));
+    hipError_t e = launch_act_to_blocks(a, tmp, ctx->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(out, tmp, need, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    hipFree(tmp);
+    if (e != hipSuccess) return fail(ctx, QMM_ERR_DEVICE, "quantize_act: %s", hipGetErrorString(e));
+    return QMM_OK;
+}
+
+int qmm_synchronize(qmm_ctx * ctx) {
+    if (!ctx) return QMM_ERR_INVALID;
+    QMM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return QMM_OK;
+}
+
+int64_t qmm_downgrades(qmm_ctx * ctx, char * buf, size_t buf_len) {
+    if (!ctx) return -1;
+    if (buf && buf_len) snprintf(buf, buf_len, "%s", ctx->downgrade_names.c_str());
+    return ctx->downgrades;
+}
+
+int qmm_timer_begin(qmm_ctx * ctx) {
+    if (!ctx) return QMM_ERR_INVALID;
+    QMM_HIP(ctx, hipEventRecord(ctx->ev0, ctx->stream));
+    return QMM_OK;
+}
+
+float qmm_timer_end(qmm_ctx * ctx) {
+    if (!ctx) return -1.0f;
+    if (hipEventRecord(ctx->ev1, ctx->stream) != hipSuccess || hipEventSynchronize(ctx->ev1) != hipSuccess) return -1.0f;
+    float ms = -1.0f;
+    if (hipEventElapsedTime(&ms, ctx->ev0, ctx->ev1) != hipSuccess) return -1.0f;
+    return ms;
+}
+
+}  // extern "C"

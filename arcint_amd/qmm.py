@@ -1,0 +1,264 @@
+"""ctypes binding of libqmm (include/qmm.h), shaped like a ggml backend.
+
+    be = Backend(0)                         # ggml_backend_*_init
+    buf = be.alloc_buffer(n)                # ggml_backend_buft_alloc_buffer
+    w = be.tensor(buf, Q4_K, (K, M))        # a ggml_tensor view in the buffer
+    be.set_tensor(w, gguf_bytes)            # ggml_backend_tensor_set
+    be.mul_mat(w, x, y)                     # GGML_OP_MUL_MAT
+    be.mul_mat_id(w, x, ids, y)             # GGML_OP_MUL_MAT_ID
+    be.graph_compute([...])                 # ggml_backend_graph_compute
+
+There is no CPU fallback: without the built library or a HIP device every
+entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libqmm.so")
+
+F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, Q8_K, IQ4_XS, I32 = 0, 1, 2, 8, 12, 14, 15, 23, 26
+OP_MUL_MAT, OP_MUL_MAT_ID = 1, 2
+QUANT_TYPES = (Q4_0, Q8_0, Q4_K, Q6_K, IQ4_XS)
+
+# every symbol include/qmm.h declares
+EXPORTS = (
+    "qmm_ctx_create", "qmm_ctx_free", "qmm_last_error", "qmm_buffer_alloc", "qmm_buffer_free",
+    "qmm_buffer_size", "qmm_buffer_base", "qmm_tensor_alloc_size", "qmm_tensor_nbytes", "qmm_type_block",
+    "qmm_tensor_set", "qmm_tensor_get", "qmm_supports_op", "qmm_mul_mat", "qmm_mul_mat_id",
+    "qmm_graph_compute", "qmm_dequantize", "qmm_quantize_act", "qmm_synchronize", "qmm_downgrades",
+    "qmm_last_path", "qmm_timer_begin", "qmm_timer_end", "qmm_buffer_copy",
+)
+
+
+class QmmError(RuntimeError):
+    pass
+
+
+class CTensor(C.Structure):
+    _fields_ = [("type", C.c_int32), ("ne", C.c_int64 * 4), ("nb", C.c_size_t * 4),
+                ("buffer", C.c_void_p), ("offs", C.c_size_t)]
+
+
+class CNode(C.Structure):
+    _fields_ = [("op", C.c_int32), ("src0", C.POINTER(CTensor)), ("src1", C.POINTER(CTensor)),
+                ("ids", C.POINTER(CTensor)), ("dst", C.POINTER(CTensor))]
+
+
+_lib = None
+
+
+def load() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise QmmError(f"{LIB_PATH} is not built; run python -m arcint_amd.build")
+        L = C.CDLL(LIB_PATH)
+        vp, sz, i32, i64 = C.c_void_p, C.c_size_t, C.c_int32, C.c_int64
+        T = C.POINTER(CTensor)
+        L.qmm_ctx_create.argtypes = [C.c_int, C.POINTER(vp)]
+        L.qmm_ctx_free.argtypes = [vp]
+        L.qmm_last_error.argtypes = [vp]
+        L.qmm_last_error.restype = C.c_char_p
+        L.qmm_last_path.argtypes = [vp]
+        L.qmm_last_path.restype = C.c_char_p
+        L.qmm_buffer_alloc.argtypes = [vp, sz, C.POINTER(vp)]
+        L.qmm_buffer_free.argtypes = [vp, vp]
+        L.qmm_buffer_size.argtypes = [vp]
+        L.qmm_buffer_size.restype = sz
+        L.qmm_buffer_base.argtypes = [vp]
+        L.qmm_buffer_base.restype = vp
+        L.qmm_tensor_alloc_size.argtypes = [i32, C.POINTER(i64)]
+        L.qmm_tensor_alloc_size.restype = sz
+        L.qmm_tensor_nbytes.argtypes = [i32, C.POINTER(i64)]
+        L.qmm_tensor_nbytes.restype = sz
+        L.qmm_type_block.argtypes = [i32, C.POINTER(sz)]
+        L.qmm_tensor_set.argtypes = [vp, T, vp, sz, sz]
+        L.qmm_tensor_get.argtypes = [vp, T, vp, sz, sz]
+        L.qmm_supports_op.argtypes = [vp, i32, T, T, T, T, C.c_char_p, sz]
+        L.qmm_mul_mat.argtypes = [vp, T, T, T]
+        L.qmm_mul_mat_id.argtypes = [vp, T, T, T, T]
+        L.qmm_graph_compute.argtypes = [vp, C.POINTER(CNode), C.c_int]
+        L.qmm_dequantize.argtypes = [vp, T, T]
+        L.qmm_quantize_act.argtypes = [vp, i32, T, vp, sz]
+        L.qmm_synchronize.argtypes = [vp]
+        L.qmm_downgrades.argtypes = [vp, C.c_char_p, sz]
+        L.qmm_downgrades.restype = i64
+        L.qmm_timer_begin.argtypes = [vp]
+        L.qmm_timer_end.argtypes = [vp]
+        L.qmm_timer_end.restype = C.c_float
+        L.qmm_buffer_copy.argtypes = [vp, vp, sz, vp, sz, sz]
+        _lib = L
+    return _lib
+
+
+def _ne4(ne) -> tuple:
+    ne = tuple(int(v) for v in ne)
+    return ne + (1,) * (4 - len(ne))
+
+
+def type_block(qtype: int) -> tuple[int, int]:
+    bb = C.c_size_t(0)
+    bl = load().qmm_type_block(qtype, C.byref(bb))
+    if not bl:
+        raise QmmError(f"unknown type {qtype}")
+    return bl, bb.value
+
+
+def nbytes(qtype: int, ne) -> int:
+    arr = (C.c_int64 * 4)(*_ne4(ne))
+    return load().qmm_tensor_nbytes(qtype, arr)
+
+
+def alloc_size(qtype: int, ne) -> int:
+    arr = (C.c_int64 * 4)(*_ne4(ne))
+    return load().qmm_tensor_alloc_size(qtype, arr)
+
+
+@dataclass
+class Buffer:
+    ptr: int
+    size: int
+
+
+class Tensor:
+    """A view {type, ne, nb, buffer, offs}; nb defaults to the contiguous strides."""
+
+    def __init__(self, buf: Buffer, qtype: int, ne, offs: int = 0, nb=None):
+        self.buf = buf
+        self.type = qtype
+        self.ne = _ne4(ne)
+        bl, bb = type_block(qtype)
+        if nb is None:
+            nb = [bb, bb * (self.ne[0] // bl)]
+            nb.append(nb[1] * self.ne[1])
+            nb.append(nb[2] * self.ne[2])
+        self.nb = tuple(int(v) for v in nb)
+        self.offs = int(offs)
+        self.c = CTensor(qtype, (C.c_int64 * 4)(*self.ne), (C.c_size_t * 4)(*self.nb), buf.ptr, self.offs)
+
+    @property
+    def nbytes(self) -> int:
+        return nbytes(self.type, self.ne)
+
+
+class Backend:
+    def __init__(self, device: int = 0):
+        self.L = load()
+        h = C.c_void_p()
+        rc = self.L.qmm_ctx_create(device, C.byref(h))
+        if rc != 0:
+            raise QmmError(f"qmm_ctx_create({device}) failed with {rc}: no HIP device?")
+        self.h = h
+        self._bufs: list[Buffer] = []
+
+    def close(self):
+        if self.h:
+            for b in self._bufs:
+                self.L.qmm_buffer_free(self.h, C.c_void_p(b.ptr))
+            self._bufs = []
+            self.L.qmm_ctx_free(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def _check(self, rc: int, what: str):
+        if rc != 0:
+            raise QmmError(f"{what}: status {rc}: {self.L.qmm_last_error(self.h).decode()}")
+
+    # ---- memory ----
+    def alloc_buffer(self, size: int) -> Buffer:
+        p = C.c_void_p()
+        self._check(self.L.qmm_buffer_alloc(self.h, size, C.byref(p)), "alloc_buffer")
+        b = Buffer(p.value, size)
+        self._bufs.append(b)
+        return b
+
+    def free_buffer(self, b: Buffer):
+        self.L.qmm_buffer_free(self.h, C.c_void_p(b.ptr))
+        self._bufs = [x for x in self._bufs if x.ptr != b.ptr]
+
+    def tensor(self, buf: Buffer, qtype: int, ne, offs: int = 0, nb=None) -> Tensor:
+        return Tensor(buf, qtype, ne, offs, nb)
+
+    def new_tensor(self, qtype: int, ne) -> Tensor:
+        """A contiguous tensor in a buffer of its own."""
+        buf = self.alloc_buffer(alloc_size(qtype, ne))
+        return Tensor(buf, qtype, ne)
+
+    def set_tensor(self, t: Tensor, data, offset: int = 0):
+        a = np.ascontiguousarray(data)
+        self._check(self.L.qmm_tensor_set(self.h, C.byref(t.c), a.ctypes.data, offset, a.nbytes), "set_tensor")
+
+    def get_tensor(self, t: Tensor, offset: int = 0, size: int | None = None) -> np.ndarray:
+        size = t.nbytes - offset if size is None else size
+        out = np.empty(size, np.uint8)
+        self._check(self.L.qmm_tensor_get(self.h, C.byref(t.c), out.ctypes.data, offset, size), "get_tensor")
+        return out
+
+    def get_f32(self, t: Tensor) -> np.ndarray:
+        return self.get_tensor(t).view(np.float32)
+
+    # ---- ops ----
+    def supports_op(self, op: int, src0: Tensor, src1: Tensor, ids: Tensor | None, dst: Tensor):
+        buf = C.create_string_buffer(256)
+        ok = self.L.qmm_supports_op(self.h, op, C.byref(src0.c), C.byref(src1.c),
+                                    C.byref(ids.c) if ids else None, C.byref(dst.c), buf, 256)
+        return bool(ok), buf.value.decode()
+
+    def mul_mat(self, src0: Tensor, src1: Tensor, dst: Tensor):
+        self._check(self.L.qmm_mul_mat(self.h, C.byref(src0.c), C.byref(src1.c), C.byref(dst.c)), "mul_mat")
+
+    def mul_mat_id(self, src0: Tensor, src1: Tensor, ids: Tensor, dst: Tensor):
+        self._check(self.L.qmm_mul_mat_id(self.h, C.byref(src0.c), C.byref(src1.c), C.byref(ids.c), C.byref(dst.c)),
+                    "mul_mat_id")
+
+    def graph_compute(self, nodes):
+        """nodes: list of (op, src0, src1, ids_or_None, dst)."""
+        arr = (CNode * len(nodes))()
+        for i, (op, s0, s1, ids, d) in enumerate(nodes):
+            arr[i] = CNode(op, C.pointer(s0.c), C.pointer(s1.c), C.pointer(ids.c) if ids else None, C.pointer(d.c))
+        self._check(self.L.qmm_graph_compute(self.h, arr, len(nodes)), "graph_compute")
+
+    def dequantize(self, src: Tensor, dst: Tensor):
+        self._check(self.L.qmm_dequantize(self.h, C.byref(src.c), C.byref(dst.c)), "dequantize")
+
+    def quantize_act(self, act_type: int, src: Tensor) -> np.ndarray:
+        bs, bb = (32, 34) if act_type == Q8_0 else (256, 292)
+        n = src.ne[0] // bs * src.ne[1] * src.ne[2] * src.ne[3] * bb
+        out = np.empty(n, np.uint8)
+        self._check(self.L.qmm_quantize_act(self.h, act_type, C.byref(src.c), out.ctypes.data, n), "quantize_act")
+        return out
+
+    def synchronize(self):
+        self._check(self.L.qmm_synchronize(self.h), "synchronize")
+
+    def downgrades(self) -> tuple[int, str]:
+        buf = C.create_string_buffer(256)
+        n = self.L.qmm_downgrades(self.h, buf, 256)
+        return int(n), buf.value.decode()
+
+    def last_path(self) -> str:
+        return self.L.qmm_last_path(self.h).decode()
+
+    def timer_begin(self):
+        self._check(self.L.qmm_timer_begin(self.h), "timer_begin")
+
+    def timer_end(self) -> float:
+        ms = self.L.qmm_timer_end(self.h)
+        if ms < 0:
+            raise QmmError("timer_end failed")
+        return ms
+
+    def copy(self, dst: Buffer, dst_off: int, src: Buffer, src_off: int, size: int):
+        self._check(self.L.qmm_buffer_copy(self.h, C.c_void_p(dst.ptr), dst_off, C.c_void_p(src.ptr), src_off, size),
+                    "buffer_copy")

@@ -1,0 +1,178 @@
+/*
+ * qmm.h - C ABI of libqmm, an MI355X (gfx950) implementation of ggml's
+ * quantized matrix product: GGML_OP_MUL_MAT and GGML_OP_MUL_MAT_ID on GGUF
+ * block-quant weights (Q4_0, Q8_0, Q4_K, Q6_K, IQ4_XS) with f32 activations.
+ *
+ * The entry points mirror what a ggml backend exposes for this op, so that a
+ * ggml backend adaptor (or a ctypes harness) can bind them with plain
+ * pointers and sizes.  Reference interfaces replaced, by entry point (paths
+ * relative to the arcint tree; P01/P02 = contrib/llama.cpp/patches/
+ * 0000-01-kquant-integer-dpas.patch / 0000-02-lowbit-iq-types.patch):
+ *
+ *   qmm_ctx_create/free          ggml_backend_opencl init / free; the device
+ *                                context that owns the queue and scratch
+ *                                (P01:43-60 prealloc_kq_* buffers)
+ *   qmm_buffer_alloc/free        ggml_backend_buffer_type alloc_buffer / free
+ *   qmm_tensor_alloc_size        buffer type get_alloc_size (planar layouts
+ *                                need more than ggml_nbytes)
+ *   qmm_tensor_set/get           buffer set_tensor / get_tensor: GGUF block
+ *                                bytes in, device planes, exact bytes back
+ *                                (P02:1556-1790)
+ *   qmm_supports_op              ggml_opencl_supports_op for MUL_MAT /
+ *                                MUL_MAT_ID (P01:615-660)
+ *   qmm_mul_mat                  ggml_cl_mul_mat (P01:1135-1160)
+ *   qmm_mul_mat_id               ggml_cl_mul_mat_id (P01:1316-1325)
+ *   qmm_graph_compute            ggml_backend_opencl_graph_compute over a node
+ *                                list, graph_gen++ per call (P01:609-612);
+ *                                activation dedup keyed per graph (P01:683-717)
+ *   qmm_dequantize               dequantize_row_* of ggml (bit-exact gate;
+ *                                tools/mtp_fit.py:338-409 restates them)
+ *   qmm_quantize_act             ggml-cpu's from_float for the vec_dot type
+ *                                (quantize_row_q8_0 / quantize_row_q8_K,
+ *                                restated at 0000-03-...patch:646-683)
+ *   qmm_synchronize              ggml_backend_synchronize (clFinish)
+ *   qmm_last_error               the reason behind a failed status (the
+ *                                reference aborts via GGML_ASSERT/CL_CHECK)
+ *   qmm_downgrades               ggml_backend_opencl_downgrades() (0100-...patch:11-23)
+ *
+ * Conventions (ggml's): a tensor is { type, ne[4], nb[4], data }.  For a
+ * quantized type ne[0] is the row length in weights and must be a multiple
+ * of the block size; nb[] are the strides of the GGUF byte layout.  The
+ * device keeps quantized tensors in its own planar layout, so data of a
+ * quantized tensor must be written and read through qmm_tensor_set/get.
+ *   MUL_MAT:    src0 [K, M, ne02, ne03] quantized, src1 [K, N, ne12, ne13]
+ *               f32, dst [M, N, ne12, ne13] f32; dst[m,n] = sum_k src0[k,m] *
+ *               src1[k,n], src0 broadcast over dims 2 and 3 (ne12 % ne02 == 0).
+ *   MUL_MAT_ID: src0 [K, M, n_as] quantized experts, src1 [K, ne11, T] f32
+ *               with ne11 == 1 (broadcast) or ne11 == n_used, ids [n_used, T]
+ *               i32, dst [M, n_used, T]; dst[:, i, t] = src0[:, :, ids[i,t]] *
+ *               src1[:, i % ne11, t]; a negative id writes a zero row.
+ * Threading: one in-order HIP stream per context; a context is not
+ * thread-safe, like a ggml backend.
+ */
+#ifndef QMM_H
+#define QMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml_type ids (tools/coder_mtp_gguf.py:49-54) */
+enum qmm_type {
+    QMM_TYPE_F32    = 0,
+    QMM_TYPE_F16    = 1,
+    QMM_TYPE_Q4_0   = 2,
+    QMM_TYPE_Q8_0   = 8,
+    QMM_TYPE_Q4_K   = 12,
+    QMM_TYPE_Q6_K   = 14,
+    QMM_TYPE_Q8_K   = 15,
+    QMM_TYPE_IQ4_XS = 23,
+    QMM_TYPE_I32    = 26,
+};
+
+/* ggml_op ids are not stable across ggml versions; the ABI uses its own */
+enum qmm_op {
+    QMM_OP_NONE       = 0,
+    QMM_OP_MUL_MAT    = 1,
+    QMM_OP_MUL_MAT_ID = 2,
+};
+
+enum qmm_status {
+    QMM_OK            = 0,
+    QMM_ERR_INVALID   = 1,   /* shape / type / stride precondition */
+    QMM_ERR_UNSUPPORTED = 2, /* qmm_supports_op would say no */
+    QMM_ERR_DEVICE    = 3,   /* a HIP call failed */
+    QMM_ERR_NOMEM     = 4,
+};
+
+typedef struct qmm_ctx    qmm_ctx;
+typedef struct qmm_buffer qmm_buffer;
+
+/* A non-owning view, like ggml_tensor: data lives at buffer + offs. */
+typedef struct qmm_tensor {
+    int32_t      type;   /* enum qmm_type */
+    int64_t      ne[4];
+    size_t       nb[4];  /* byte strides of the logical (GGUF) layout */
+    qmm_buffer * buffer;
+    size_t       offs;
+} qmm_tensor;
+
+/* One node of an op graph (ggml_tensor's op + src[0..2]). */
+typedef struct qmm_node {
+    int32_t      op;     /* enum qmm_op */
+    qmm_tensor * src0;
+    qmm_tensor * src1;
+    qmm_tensor * ids;    /* MUL_MAT_ID only */
+    qmm_tensor * dst;
+} qmm_node;
+
+/* ---- context and memory ------------------------------------------------ */
+int    qmm_ctx_create(int device, qmm_ctx ** out);
+void   qmm_ctx_free(qmm_ctx * ctx);
+const char * qmm_last_error(qmm_ctx * ctx);  /* never NULL */
+
+int    qmm_buffer_alloc(qmm_ctx * ctx, size_t size, qmm_buffer ** out);
+void   qmm_buffer_free(qmm_ctx * ctx, qmm_buffer * buf);
+size_t qmm_buffer_size(const qmm_buffer * buf);
+/* device address of the buffer (for harnesses that share device memory) */
+void * qmm_buffer_base(const qmm_buffer * buf);
+
+/* bytes a contiguous tensor of this type and shape occupies on the device */
+size_t qmm_tensor_alloc_size(int32_t type, const int64_t ne[4]);
+/* bytes of the GGUF layout (ggml_nbytes of a contiguous tensor) */
+size_t qmm_tensor_nbytes(int32_t type, const int64_t ne[4]);
+/* block size (weights per block) and block bytes of a type; 0 if unknown */
+int    qmm_type_block(int32_t type, size_t * block_bytes);
+
+/* Write / read `size` bytes at byte `offset` of the tensor's GGUF layout.
+ * For quantized types offset and size must be multiples of the block bytes.
+ * Both are synchronous with respect to the host buffer. */
+int    qmm_tensor_set(qmm_ctx * ctx, const qmm_tensor * t, const void * data, size_t offset, size_t size);
+int    qmm_tensor_get(qmm_ctx * ctx, const qmm_tensor * t, void * data, size_t offset, size_t size);
+
+/* ---- ops --------------------------------------------------------------- */
+/* 1 when the op is taken; otherwise 0 and, if reason != NULL, why. */
+int    qmm_supports_op(qmm_ctx * ctx, int32_t op, const qmm_tensor * src0, const qmm_tensor * src1,
+                       const qmm_tensor * ids, const qmm_tensor * dst, char * reason, size_t reason_len);
+
+/* Enqueue on the context's stream; asynchronous (call qmm_synchronize). */
+int    qmm_mul_mat(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1, const qmm_tensor * dst);
+int    qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1,
+                      const qmm_tensor * ids, const qmm_tensor * dst);
+/* Runs the nodes in order; bumps the graph generation first, so one
+ * activation quantization serves every node of the graph that reads the same
+ * src1 with the same vec_dot type. */
+int    qmm_graph_compute(qmm_ctx * ctx, const qmm_node * nodes, int n_nodes);
+
+/* dst (f32, contiguous, ne = src ne) = dequantize_row_<type>(src) */
+int    qmm_dequantize(qmm_ctx * ctx, const qmm_tensor * src, const qmm_tensor * dst);
+/* Quantize f32 src [K, N] (rows of K) with ggml-cpu's from_float for
+ * act_type (QMM_TYPE_Q8_0 or QMM_TYPE_Q8_K) and write the ggml block bytes
+ * (block_q8_0 / block_q8_K, N*K/bs blocks) to host memory `out`. */
+int    qmm_quantize_act(qmm_ctx * ctx, int32_t act_type, const qmm_tensor * src, void * out, size_t out_size);
+
+int    qmm_synchronize(qmm_ctx * ctx);
+
+/* ---- observability and timing ----------------------------------------- */
+/* Number of ops that took a slower path than their type promises (the
+ * reference's DOWNGRADE keys); names of the last few in `buf`. */
+int64_t qmm_downgrades(qmm_ctx * ctx, char * buf, size_t buf_len);
+/* Name of the kernel path the last mul_mat / mul_mat_id took. */
+const char * qmm_last_path(qmm_ctx * ctx);
+
+/* HIP events on the context's stream: begin records, end records and waits,
+ * returning the elapsed milliseconds (device time between the two). */
+int    qmm_timer_begin(qmm_ctx * ctx);
+float  qmm_timer_end(qmm_ctx * ctx);
+
+/* Copy between device buffers on the context's stream (harness plumbing). */
+int    qmm_buffer_copy(qmm_ctx * ctx, qmm_buffer * dst, size_t dst_off, const qmm_buffer * src, size_t src_off, size_t size);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QMM_H */

@@ -1,0 +1,295 @@
+"""GPU parity: libqmm on the HIP device against the CPU oracle, through the C ABI.
+
+Bars: dequantization and activation quantization bit-exact (byte equality);
+set_tensor / get_tensor byte-exact; MUL_MAT / MUL_MAT_ID within a max
+relative error of 1e-3 in fp32 (denominator floored at 5 % of the output
+rms, see conftest.rel_err) - the integer dots are exact on both sides, the
+expected error is ~1e-6.  Each case prints its name first so that a fault
+names it."""
+import sys
+
+import numpy as np
+import pytest
+
+from arcint_amd import qmm, synth
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+TYPES = [qmm.Q4_0, qmm.Q8_0, qmm.Q4_K, qmm.Q6_K, qmm.IQ4_XS]
+TOL = 1e-3
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def be():
+    b = qmm.Backend(0)
+    yield b
+    b.close()
+
+
+class Scope:
+    """Buffers allocated for one test, freed at its end."""
+
+    def __init__(self, be):
+        self.be = be
+        self.bufs = []
+
+    def weights(self, qtype, raw, ne):
+        t = self.be.new_tensor(qtype, ne)
+        self.bufs.append(t.buf)
+        self.be.set_tensor(t, raw)
+        return t
+
+    def f32(self, arr):
+        arr = np.ascontiguousarray(arr, np.float32)
+        t = self.be.new_tensor(qmm.F32, tuple(reversed(arr.shape)))
+        self.bufs.append(t.buf)
+        self.be.set_tensor(t, arr.view(np.uint8).ravel())
+        return t
+
+    def i32(self, arr):
+        arr = np.ascontiguousarray(arr, np.int32)
+        t = self.be.new_tensor(qmm.I32, tuple(reversed(arr.shape)))
+        self.bufs.append(t.buf)
+        self.be.set_tensor(t, arr.view(np.uint8).ravel())
+        return t
+
+    def empty_f32(self, ne):
+        t = self.be.new_tensor(qmm.F32, ne)
+        self.bufs.append(t.buf)
+        return t
+
+    def close(self):
+        for b in self.bufs:
+            self.be.free_buffer(b)
+
+
+@pytest.fixture
+def sc(be):
+    s = Scope(be)
+    yield s
+    s.close()
+
+
+def special_blocks(qtype, nblk, seed):
+    """random blocks with some scales set to 0, the smallest subnormal and the fp16 max"""
+    blck, bb = synth.BLOCK[qtype]
+    raw = synth.weights(qtype, 1, blck * nblk, seed).reshape(nblk, bb).copy()
+    doff = 208 if qtype == qmm.Q6_K else 0
+    for i, bits in enumerate([0x0000, 0x8000, 0x0001, 0x7BFF, 0x03FF, 0xFBFF]):
+        raw[i, doff:doff + 2] = np.frombuffer(np.uint16(bits).tobytes(), np.uint8)
+        if qtype == qmm.Q4_K:
+            raw[i, 2:4] = np.frombuffer(np.uint16(bits).tobytes(), np.uint8)
+    return raw.ravel()
+
+
+# ------------------------------------------------------------------ memory
+@pytest.mark.parametrize("qtype", TYPES)
+def test_set_get_roundtrip(be, sc, qtype):
+    say("set_get", qtype)
+    blck, bb = synth.BLOCK[qtype]
+    K, M = blck * 4, 37
+    raw = synth.weights(qtype, M, K, seed=21)
+    w = sc.weights(qtype, raw, (K, M))
+    assert np.array_equal(be.get_tensor(w), raw)
+    # partial writes and reads at block granularity
+    part = synth.weights(qtype, 1, blck * 7, seed=22)
+    be.set_tensor(w, part, offset=bb * 11)
+    raw2 = raw.copy()
+    raw2[bb * 11:bb * 18] = part
+    assert np.array_equal(be.get_tensor(w), raw2)
+    assert np.array_equal(be.get_tensor(w, offset=bb * 5, size=bb * 20), raw2[bb * 5:bb * 25])
+    with pytest.raises(qmm.QmmError):
+        be.set_tensor(w, part[:bb - 1], offset=0)
+
+
+# ------------------------------------------------------------------ bit-exact
+@pytest.mark.parametrize("qtype", TYPES)
+def test_dequant_bit_exact(be, sc, orc, qtype):
+    say("dequant", qtype)
+    blck, bb = synth.BLOCK[qtype]
+    nblk = 4096 if blck == 32 else 1024
+    raw = special_blocks(qtype, nblk, seed=31)
+    n = nblk * blck
+    w = sc.weights(qtype, raw, (n // 8, 8))
+    y = sc.empty_f32((n // 8, 8))
+    be.dequantize(w, y)
+    be.synchronize()
+    got = be.get_tensor(y).view(np.uint32)
+    ref = orc.dequantize(qtype, raw, n).view(np.uint32)
+    assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} of {n} values differ"
+
+
+def act_cases(K, seed):
+    g = np.random.default_rng(seed)
+    x = g.standard_normal((6, K)).astype(np.float32)
+    x[1, :] = 0.0                                      # all-zero blocks
+    x[2, :] = np.round(x[2, :] * 4) / 4                # many exact ties after scaling
+    x[2, 0:256:32] = 127.0 / 4
+    x[3, :] = 1.0
+    x[4, 5], x[4, 100] = -9.0, 9.0                     # equal |x|, opposite signs: first wins
+    x[4, 300], x[4, 301] = 9.0, -9.0
+    x[5, :] *= 1e-30                                   # tiny values
+    return x
+
+
+@pytest.mark.parametrize("act", [qmm.Q8_0, qmm.Q8_K])
+def test_quantize_act_bit_exact(be, sc, orc, act):
+    say("quantize_act", act)
+    K = 1024
+    x = act_cases(K, seed=41)
+    xt = sc.f32(x)
+    got = be.quantize_act(act, xt)
+    ref = np.concatenate([orc.quantize_q8_0(r) if act == qmm.Q8_0 else orc.quantize_q8_K(r) for r in x])
+    assert np.array_equal(got, ref)
+
+
+# ------------------------------------------------------------------ MUL_MAT
+def run_mul_mat(be, sc, orc, qtype, M, K, N, seed):
+    raw = synth.weights(qtype, M, K, seed)
+    x = synth.activations(N, K, seed + 1)
+    w = sc.weights(qtype, raw, (K, M))
+    xt = sc.f32(x)
+    y = sc.empty_f32((M, N))
+    be.mul_mat(w, xt, y)
+    be.synchronize()
+    got = be.get_f32(y).reshape(N, M)
+    ref = orc.mul_mat(qtype, raw, M, K, x)
+    return got, ref
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("N", [1, 2, 3, 4, 5, 8])
+def test_mul_mat_gemv(be, sc, orc, qtype, N):
+    M, K = 300, 2048
+    say("gemv", qtype, M, K, N)
+    got, ref = run_mul_mat(be, sc, orc, qtype, M, K, N, seed=51)
+    assert rel_err(got, ref) <= TOL
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("K", [256, 512, 768, 5120])
+def test_mul_mat_k_shapes(be, sc, orc, qtype, K):
+    M, N = 129, 1
+    say("gemv-k", qtype, M, K, N)
+    got, ref = run_mul_mat(be, sc, orc, qtype, M, K, N, seed=52)
+    assert rel_err(got, ref) <= TOL
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("N", [9, 16, 37])
+def test_mul_mat_many_columns(be, sc, orc, qtype, N):
+    M, K = 96, 1024
+    say("gemv-many", qtype, M, K, N)
+    got, ref = run_mul_mat(be, sc, orc, qtype, M, K, N, seed=53)
+    assert rel_err(got, ref) <= TOL
+
+
+def test_mul_mat_broadcast_and_strides(be, sc, orc):
+    say("broadcast")
+    qtype, K, M, N = qmm.Q4_K, 512, 64, 3
+    raw = synth.weights(qtype, 2 * M, K, seed=61)          # ne02 = 2 matrices
+    w = sc.weights(qtype, raw, (K, M, 2))
+    x = synth.activations(4 * N, K, seed=62).reshape(4, N, K)   # ne12 = 4 -> r2 = 2
+    xt = sc.f32(x)
+    y = sc.empty_f32((M, N, 4))
+    be.mul_mat(w, xt, y)
+    be.synchronize()
+    got = be.get_f32(y).reshape(4, N, M)
+    rb = synth.row_bytes(qtype, K) * M
+    for i2 in range(4):
+        ref = orc.mul_mat(qtype, raw[(i2 // 2) * rb:(i2 // 2 + 1) * rb], M, K, x[i2])
+        assert rel_err(got[i2], ref) <= TOL
+    # a strided src1 view (every other column) and a padded dst
+    xs = synth.activations(2 * N, K, seed=63)
+    xst = sc.f32(xs)
+    view = qmm.Tensor(xst.buf, qmm.F32, (K, N), nb=(4, 8 * K, 8 * K * N, 8 * K * N))
+    ypad = sc.empty_f32((M + 5, N))
+    yview = qmm.Tensor(ypad.buf, qmm.F32, (M, N), nb=(4, 4 * (M + 5), 4 * (M + 5) * N, 4 * (M + 5) * N))
+    be.mul_mat(w, view, yview)
+    be.synchronize()
+    got = be.get_f32(ypad).reshape(N, M + 5)[:, :M]
+    ref = orc.mul_mat(qtype, raw[:rb], M, K, xs[0::2])
+    assert rel_err(got, ref) <= TOL
+
+
+# ------------------------------------------------------------------ MUL_MAT_ID
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("T", [1, 4, 19])
+@pytest.mark.parametrize("bcast", [True, False])
+def test_mul_mat_id(be, sc, orc, qtype, T, bcast):
+    E, n_used, M = 16, 4, 96
+    K = 512
+    say("mul_mat_id", qtype, T, bcast)
+    raw = synth.weights(qtype, E * M, K, seed=71)
+    ids = synth.moe_ids(T, E, n_used, seed=72)
+    if T >= 4:
+        ids[1, 2] = -1                                   # a negative id writes zeros
+    ne11 = 1 if bcast else n_used
+    x = synth.activations(T * ne11, K, seed=73).reshape(T, ne11, K)
+    w = sc.weights(qtype, raw, (K, M, E))
+    xt = sc.f32(x)
+    it = sc.i32(ids)
+    y = sc.empty_f32((M, n_used, T))
+    be.mul_mat_id(w, xt, it, y)
+    be.synchronize()
+    got = be.get_f32(y).reshape(T, n_used, M)
+    ref = orc.mul_mat_id(qtype, raw, M, K, E, x, ids)
+    assert rel_err(got, ref) <= TOL
+    if T >= 4:
+        assert not got[1, 2].any()
+
+
+def test_mul_mat_id_all_tokens_one_expert(be, sc, orc):
+    # more than 8 pairs on one expert: several tasks per expert
+    qtype, E, n_used, M, K, T = qmm.Q4_K, 4, 2, 64, 256, 40
+    say("mul_mat_id-hot")
+    raw = synth.weights(qtype, E * M, K, seed=74)
+    ids = np.tile(np.array([[3, 1]], np.int32), (T, 1))
+    x = synth.activations(T, K, seed=75).reshape(T, 1, K)
+    w = sc.weights(qtype, raw, (K, M, E))
+    y = sc.empty_f32((M, n_used, T))
+    be.mul_mat_id(w, sc.f32(x), sc.i32(ids), y)
+    be.synchronize()
+    got = be.get_f32(y).reshape(T, n_used, M)
+    assert rel_err(got, orc.mul_mat_id(qtype, raw, M, K, E, x, ids)) <= TOL
+
+
+# ------------------------------------------------------------------ graph
+def test_graph_activation_dedup(be, sc, orc):
+    say("graph")
+    K, M, N = 1024, 80, 2
+    ra = synth.weights(qmm.Q4_K, M, K, seed=81)
+    rb = synth.weights(qmm.Q6_K, M, K, seed=82)
+    rc = synth.weights(qmm.Q4_0, M, K, seed=83)
+    x = synth.activations(N, K, seed=84)
+    wa, wb, wc = sc.weights(qmm.Q4_K, ra, (K, M)), sc.weights(qmm.Q6_K, rb, (K, M)), sc.weights(qmm.Q4_0, rc, (K, M))
+    xt = sc.f32(x)
+    ya, yb, yc = sc.empty_f32((M, N)), sc.empty_f32((M, N)), sc.empty_f32((M, N))
+    be.graph_compute([(qmm.OP_MUL_MAT, wa, xt, None, ya), (qmm.OP_MUL_MAT, wb, xt, None, yb),
+                      (qmm.OP_MUL_MAT, wc, xt, None, yc)])
+    be.synchronize()
+    assert rel_err(be.get_f32(ya).reshape(N, M), orc.mul_mat(qmm.Q4_K, ra, M, K, x)) <= TOL
+    assert rel_err(be.get_f32(yb).reshape(N, M), orc.mul_mat(qmm.Q6_K, rb, M, K, x)) <= TOL
+    assert rel_err(be.get_f32(yc).reshape(N, M), orc.mul_mat(qmm.Q4_0, rc, M, K, x)) <= TOL
+
+
+# ------------------------------------------------------------------ full sizes
+FULL = [
+    (qmm.Q4_0, 4096, 4096), (qmm.Q4_0, 11008, 4096), (qmm.Q4_0, 4096, 11008),
+    (qmm.Q4_K, 17408, 5120), (qmm.Q6_K, 5120, 17408), (qmm.Q4_K, 12288, 5120),
+    (qmm.IQ4_XS, 14336, 4096), (qmm.IQ4_XS, 4096, 14336), (qmm.Q8_0, 14336, 4096), (qmm.Q8_0, 4096, 14336),
+]
+
+
+@pytest.mark.parametrize("qtype,M,K", FULL)
+@pytest.mark.parametrize("N", [1, 4, 8])
+def test_full_size_gemv(be, sc, orc, qtype, M, K, N):
+    say("full", qtype, M, K, N)
+    got, ref = run_mul_mat(be, sc, orc, qtype, M, K, N, seed=91)
+    assert rel_err(got, ref) <= TOL
