@@ -17,6 +17,9 @@
 // MUL_MAT derives its task from the grid, MUL_MAT_ID reads device-built tasks.
 #include "qmm_device.h"
 
+#include <algorithm>
+#include <cstdlib>
+
 namespace qmm {
 namespace {
 
@@ -26,7 +29,9 @@ constexpr int kWaves = kThreads / 64;
 struct GemvParams {
     WView w;
     int64_t M, K;
-    ActBuf a;
+    ActBuf a;                    // pre-quantized activations (fused == 0)
+    F32Cols src;                 // f32 activations quantized in LDS (fused == 1)
+    int fused;
     const GemvTask * tasks;      // list mode when non-null
     const int32_t * ntasks_dev;
     // dense mode: task y -> batch b = y / tpb, columns (y % tpb) * NC ...
@@ -35,6 +40,7 @@ struct GemvParams {
     float * dst;
     int kc;                      // weights per LDS chunk
     int lpr_log2;                // lanes per row = 1 << lpr_log2
+    int riw;                     // row iterations per wave
 };
 
 // activation chunk in LDS: NC columns of codes, then scales, then sums
@@ -248,18 +254,89 @@ template <> struct GV<QMM_TYPE_IQ4_XS> {
     }
 };
 
-template <int NC> constexpr int rows_iter() { return NC <= 4 ? 4 : 2; }
-template <int TYPE, int NC> constexpr int unroll() {
-    return TYPE == QMM_TYPE_Q6_K ? 2 : (NC <= 2 ? 4 : 2);
+// prefetch depth (items in flight per lane) by type
+template <int TYPE> constexpr int depth() { return TYPE == QMM_TYPE_Q6_K ? 3 : 4; }
+
+// Quantize columns [0, nc) of the activation chunk [k0, k0 + kcur) into LDS
+// (codes, scales, sums), exactly as the stand-alone pre-pass does.
+template <int NC, int BS, int SS>
+__device__ void quantize_chunk(const GemvParams & p, const int64_t * s_col, int nc, int64_t k0, int kcur,
+                               uint8_t * lds) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    int8_t * codes = reinterpret_cast<int8_t *>(lds);
+    float * ds = reinterpret_cast<float *>(lds + (size_t)NC * p.kc);
+    int16_t * ss = reinterpret_cast<int16_t *>(lds + (size_t)NC * p.kc + (size_t)NC * (p.kc / BS) * 4);
+    if constexpr (BS == 256) {
+        const int nsb = kcur / 256;
+        for (int it = wave; it < nc * nsb; it += kWaves) {          // one wave per super-block
+            const int j = it / nsb, sb = it - j * nsb;
+            const float * x = f32_col(p.src, s_col[j]) + k0 + sb * 256 + 4 * lane;
+            float v[4] = { x[0], x[1], x[2], x[3] };
+            float d;
+            int bs;
+            const uint32_t q = quant_q8_K_wave(v, lane, &d, &bs);
+            *reinterpret_cast<uint32_t *>(codes + (size_t)j * p.kc + sb * 256 + 4 * lane) = q;
+            if ((lane & 3) == 0) ss[j * (p.kc / SS) + sb * 16 + (lane >> 2)] = (int16_t)bs;
+            if (lane == 0) ds[j * (p.kc / BS) + sb] = d;
+        }
+    } else {
+        const int nb = kcur / 32;                                   // 8 lanes per block
+        for (int it = tid >> 3; it < ((nc * nb + 7) & ~7); it += kThreads / 8) {
+            const bool live = it < nc * nb;
+            const int j = live ? it / nb : 0, b = live ? it - j * nb : 0, q4 = tid & 7;
+            float v[4] = { 0.f, 0.f, 0.f, 0.f };
+            if (live) {
+                const float * x = f32_col(p.src, s_col[j]) + k0 + b * 32 + 4 * q4;
+                v[0] = x[0]; v[1] = x[1]; v[2] = x[2]; v[3] = x[3];
+            }
+            float d;
+            int sm;
+            const uint32_t q = quant_q8_0_lane(v, &d, &sm);
+            if (live) {
+                *reinterpret_cast<uint32_t *>(codes + (size_t)j * p.kc + b * 32 + 4 * q4) = q;
+                if (q4 == 0) {
+                    ds[j * (p.kc / BS) + b] = d;
+                    ss[j * (p.kc / SS) + b] = (int16_t)sm;
+                }
+            }
+        }
+    }
 }
 
+// copy pre-quantized columns of the chunk into LDS
+template <int NC, int BS, int SS>
+__device__ void stage_chunk(const GemvParams & p, const int64_t * s_col, int nc, int64_t k0, int kcur, uint8_t * lds) {
+    const int tid = threadIdx.x;
+    const int n16 = kcur / 16;
+    for (int i = tid; i < nc * n16; i += kThreads) {
+        const int j = i / n16, o = (i - j * n16) * 16;
+        *reinterpret_cast<uint4 *>(lds + (size_t)j * p.kc + o) =
+            *reinterpret_cast<const uint4 *>(p.a.codes + s_col[j] * p.K + k0 + o);
+    }
+    const int nd = kcur / BS, ns = kcur / SS;
+    float * ld = reinterpret_cast<float *>(lds + (size_t)NC * p.kc);
+    int16_t * ls = reinterpret_cast<int16_t *>(lds + (size_t)NC * p.kc + (size_t)NC * (p.kc / BS) * 4);
+    for (int i = tid; i < nc * nd; i += kThreads) {
+        const int j = i / nd, o = i - j * nd;
+        ld[j * (p.kc / BS) + o] = p.a.d[s_col[j] * (p.K / BS) + k0 / BS + o];
+    }
+    for (int i = tid; i < nc * ns; i += kThreads) {
+        const int j = i / ns, o = i - j * ns;
+        ls[j * (p.kc / SS) + o] = p.a.sums[s_col[j] * (p.K / SS) + k0 / SS + o];
+    }
+}
+
+// One work-group: rows [row0, row0 + 4 * riw * RG) of one task's matrix.
+// Each lane streams its items (row iteration ri, unit iteration i) with
+// depth() weight units in flight; at the end of every row the LPR lanes of
+// the row reduce their partial sums, which accumulate per row in LDS across
+// K chunks and are written once at the end.
 template <int TYPE, int NC>
 __global__ __launch_bounds__(kThreads) void k_gemv(GemvParams p) {
     using T = GV<TYPE>;
-    constexpr int RI = rows_iter<NC>();
-    constexpr int UF = unroll<TYPE, NC>();
+    constexpr int D = depth<TYPE>();
     extern __shared__ __align__(16) uint8_t lds[];
-    __shared__ int64_t s_coff[NC];     // code offset of each column in the ActBuf
+    __shared__ int64_t s_col[NC];      // activation column ids
     __shared__ int64_t s_doff[NC];
 
     int mat, nc;
@@ -269,7 +346,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv(GemvParams p) {
         mat = t.mat;
         nc = t.ncols;
         if (threadIdx.x < NC && (int)threadIdx.x < nc) {
-            s_coff[threadIdx.x] = (int64_t)t.col[threadIdx.x] * p.K;
+            s_col[threadIdx.x] = t.col[threadIdx.x];
             s_doff[threadIdx.x] = t.dst_off[threadIdx.x];
         }
     } else {
@@ -280,7 +357,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv(GemvParams p) {
         nc = (int)((p.ne11 - first) < NC ? (p.ne11 - first) : NC);
         if (threadIdx.x < NC && (int)threadIdx.x < nc) {
             const int64_t i1 = first + threadIdx.x;
-            s_coff[threadIdx.x] = (b * p.ne11 + i1) * p.K;
+            s_col[threadIdx.x] = b * p.ne11 + i1;
             s_doff[threadIdx.x] = i1 * p.d_nb1 + i2 * p.d_nb2 + i3 * p.d_nb3;
         }
     }
@@ -289,72 +366,73 @@ __global__ __launch_bounds__(kThreads) void k_gemv(GemvParams p) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int lprl = p.lpr_log2, LPR = 1 << lprl, RG = 64 >> lprl;
     const int rl = lane & (LPR - 1), rs = lane >> lprl;
-    const int64_t rows_per_wave = (int64_t)RI * RG;
-    const int64_t row_base = (int64_t)blockIdx.x * kWaves * rows_per_wave + wave * rows_per_wave;
+    const int rows_wg = kWaves * p.riw * RG;
+    const int64_t row0 = (int64_t)blockIdx.x * rows_wg;
     const int64_t bpr = p.w.bpr;
     const XL<NC, T::BS, T::SS> x{ lds, p.kc };
-
-    float acc[RI][NC];
-#pragma unroll
-    for (int r = 0; r < RI; ++r)
-#pragma unroll
-        for (int j = 0; j < NC; ++j) acc[r][j] = 0.0f;
+    const size_t xbytes = (size_t)NC * p.kc + (size_t)NC * (p.kc / T::BS) * 4 + (size_t)NC * (p.kc / T::SS) * 2;
+    float * rowacc = reinterpret_cast<float *>(lds + ((xbytes + 15) & ~(size_t)15));   // [rows_wg][NC]
 
     for (int64_t k0 = 0; k0 < p.K; k0 += p.kc) {
         const int kcur = (int)((p.K - k0) < p.kc ? (p.K - k0) : p.kc);
         __syncthreads();
-        {   // stage the chunk of every column: codes, scales, sums
-            const int n16 = kcur / 16;
-            for (int i = tid; i < nc * n16; i += kThreads) {
-                const int j = i / n16, o = (i - j * n16) * 16;
-                *reinterpret_cast<uint4 *>(lds + (size_t)j * p.kc + o) =
-                    *reinterpret_cast<const uint4 *>(p.a.codes + s_coff[j] + k0 + o);
-            }
-            const int nd = kcur / T::BS, ns = kcur / T::SS;
-            float * ld = reinterpret_cast<float *>(lds + (size_t)NC * p.kc);
-            int16_t * ls = reinterpret_cast<int16_t *>(lds + (size_t)NC * p.kc + (size_t)NC * (p.kc / T::BS) * 4);
-            for (int i = tid; i < nc * nd; i += kThreads) {
-                const int j = i / nd, o = i - j * nd;
-                ld[j * (p.kc / T::BS) + o] = p.a.d[s_coff[j] / T::BS + k0 / T::BS + o];
-            }
-            for (int i = tid; i < nc * ns; i += kThreads) {
-                const int j = i / ns, o = i - j * ns;
-                ls[j * (p.kc / T::SS) + o] = p.a.sums[s_coff[j] / T::SS + k0 / T::SS + o];
-            }
-        }
+        if (p.fused) quantize_chunk<NC, T::BS, T::SS>(p, s_col, nc, k0, kcur, lds);
+        else stage_chunk<NC, T::BS, T::SS>(p, s_col, nc, k0, kcur, lds);
         __syncthreads();
 
         const int nunits = (kcur / T::BLK) * T::UPB;
+        const int upl = (nunits + LPR - 1) >> lprl;           // unit iterations per row
+        const int nitems = p.riw * upl;
+        const int64_t kblk0 = k0 / T::BLK;
+        auto item = [&](int t, int64_t & blk, int & u, int & rloc) -> bool {
+            const int ri = t / upl, i = t - ri * upl;
+            rloc = (wave * p.riw + ri) * RG + rs;
+            u = rl + (i << lprl);
+            const int64_t row = row0 + rloc;
+            blk = ((int64_t)mat * p.M + row) * bpr + kblk0 + u / T::UPB;
+            return row < p.M && u < nunits;
+        };
+        typename T::W buf[D];
 #pragma unroll
-        for (int r = 0; r < RI; ++r) {
-            const int64_t row = row_base + (int64_t)r * RG + rs;
-            if (row < p.M) {
-                const int64_t blk0 = ((int64_t)mat * p.M + row) * bpr + k0 / T::BLK;
-                for (int u0 = rl; u0 < nunits; u0 += LPR * UF) {
-                    typename T::W wv[UF];
+        for (int j = 0; j < D; ++j) {
+            int64_t blk;
+            int u, rloc;
+            if (j < nitems && item(j, blk, u, rloc)) T::load(buf[j], p.w, blk, u % T::UPB);
+        }
+        float acc[NC];
 #pragma unroll
-                    for (int f = 0; f < UF; ++f) {
-                        const int u = u0 + f * LPR;
-                        if (u < nunits) T::load(wv[f], p.w, blk0 + u / T::UPB, u % T::UPB);
-                    }
+        for (int j = 0; j < NC; ++j) acc[j] = 0.0f;
+        for (int t0 = 0; t0 < nitems; t0 += D) {
 #pragma unroll
-                    for (int f = 0; f < UF; ++f) {
-                        const int u = u0 + f * LPR;
-                        if (u < nunits) T::template dot<NC>(wv[f], u / T::UPB, u % T::UPB, x, nc, acc[r]);
+            for (int j = 0; j < D; ++j) {
+                const int t = t0 + j;
+                if (t < nitems) {
+                    const typename T::W cur = buf[j];
+                    int64_t blk;
+                    int u, rloc;
+                    if (t + D < nitems && item(t + D, blk, u, rloc)) T::load(buf[j], p.w, blk, u % T::UPB);
+                    const bool ok = item(t, blk, u, rloc);
+                    if (ok) T::template dot<NC>(cur, u / T::UPB, u % T::UPB, x, nc, acc);
+                    if ((t % upl) == upl - 1) {        // last unit iteration of a row (uniform)
+#pragma unroll
+                        for (int c = 0; c < NC; ++c) {
+                            const float v = group_sum(acc[c], LPR);
+                            acc[c] = 0.0f;
+                            if (c < nc && rl == 0 && rloc < rows_wg) {
+                                float & r = rowacc[rloc * NC + c];
+                                r = (k0 == 0) ? v : r + v;
+                            }
+                        }
                     }
                 }
             }
         }
     }
-
-#pragma unroll
-    for (int r = 0; r < RI; ++r) {
-        const int64_t row = row_base + (int64_t)r * RG + rs;
-#pragma unroll
-        for (int j = 0; j < NC; ++j) {
-            const float v = group_sum(acc[r][j], LPR);
-            if (j < nc && rl == 0 && row < p.M) p.dst[s_doff[j] + row] = v;
-        }
+    __syncthreads();
+    for (int i = tid; i < rows_wg * nc; i += kThreads) {
+        const int c = i / rows_wg, r = i - c * rows_wg;
+        const int64_t row = row0 + r;
+        if (row < p.M) p.dst[s_doff[c] + row] = rowacc[r * NC + c];
     }
 }
 
@@ -362,7 +440,13 @@ template <int TYPE>
 hipError_t launch_t(const GemvParams & p, int nc, int64_t rows_per_wg, int64_t ntasks, size_t lds_bytes, hipStream_t s) {
     const dim3 grid((unsigned)((p.M + rows_per_wg - 1) / rows_per_wg), (unsigned)ntasks);
     switch (nc) {
-#define QMM_NC(N) case N: k_gemv<TYPE, N><<<grid, kThreads, lds_bytes, s>>>(p); break;
+#define QMM_NC(N)                                                                                         \
+    case N:                                                                                               \
+        if (lds_bytes > 65536)                                                                            \
+            (void)hipFuncSetAttribute((const void *)k_gemv<TYPE, N>, hipFuncAttributeMaxDynamicSharedMemorySize, \
+                                      (int)lds_bytes);                                                    \
+        k_gemv<TYPE, N><<<grid, kThreads, lds_bytes, s>>>(p);                                             \
+        break;
         QMM_NC(1) QMM_NC(2) QMM_NC(3) QMM_NC(4) QMM_NC(5) QMM_NC(6) QMM_NC(7) QMM_NC(8)
 #undef QMM_NC
         default: return hipErrorInvalidValue;
@@ -382,18 +466,25 @@ TypeShape type_shape(int type) {
     }
 }
 
+int env_int(const char * name, int dflt) {
+    const char * e = getenv(name);
+    return e ? atoi(e) : dflt;
+}
+
 }  // namespace
 
-hipError_t launch_gemv_any(int type, const WView & w, int64_t M, int64_t K, const ActBuf & a,
+hipError_t launch_gemv_any(int type, const WView & w, int64_t M, int64_t K, const ActBuf * a, const F32Cols * src,
                            const GemvTask * tasks, int ntasks_max, const int32_t * ntasks_dev, int nc,
                            const GemvDense * dense, float * dst, hipStream_t s) {
     const TypeShape ts = type_shape(type);
-    if (!ts.blk || nc < 1 || nc > kMaxTaskCols || K % ts.blk) return hipErrorInvalidValue;
+    if (!ts.blk || nc < 1 || nc > kMaxTaskCols || K % ts.blk || (!a && !src)) return hipErrorInvalidValue;
     GemvParams p{};
     p.w = w;
     p.M = M;
     p.K = K;
-    p.a = a;
+    if (a) p.a = *a;
+    if (src) p.src = *src;
+    p.fused = a ? 0 : 1;
     p.tasks = tasks;
     p.ntasks_dev = ntasks_dev;
     p.dst = dst;
@@ -416,15 +507,24 @@ hipError_t launch_gemv_any(int type, const WView & w, int64_t M, int64_t K, cons
     int lprl = 0;
     while ((1 << lprl) < units && lprl < 6) ++lprl;
     p.lpr_log2 = lprl;
+    const int RG = 64 >> lprl;
+    // rows per wave: aim at ~1024 work-groups over all tasks
+    int riw = env_int("QMM_GEMV_RIW", 0);
+    if (riw <= 0) {
+        const int64_t target = std::max<int64_t>(1, 1024 / ntasks);
+        riw = (int)((M + (int64_t)kWaves * RG * target - 1) / ((int64_t)kWaves * RG * target));
+        riw = std::max(1, std::min(riw, 16));
+    }
+    p.riw = riw;
+    const int64_t rows_per_wg = (int64_t)kWaves * riw * RG;
     // LDS chunk: up to 48 KB of activations per work-group
     const double per_k = 1.0 + 4.0 / ts.bs + 2.0 / ts.ss;
     int64_t kc = (int64_t)(49152.0 / (nc * per_k));
     kc = kc / 256 * 256;
     if (kc >= K || kc <= 0) kc = K;
     p.kc = (int)kc;
-    const size_t lds_bytes = (size_t)nc * kc + (size_t)nc * (kc / ts.bs) * 4 + (size_t)nc * (kc / ts.ss) * 2 + 16;
-    const int RI = nc <= 4 ? 4 : 2;
-    const int64_t rows_per_wg = (int64_t)kWaves * RI * (64 >> lprl);
+    const size_t xbytes = (size_t)nc * kc + (size_t)nc * (kc / ts.bs) * 4 + (size_t)nc * (kc / ts.ss) * 2;
+    const size_t lds_bytes = ((xbytes + 15) & ~(size_t)15) + (size_t)rows_per_wg * nc * 4;
     switch (type) {
         case QMM_TYPE_Q4_0:   return launch_t<QMM_TYPE_Q4_0>(p, nc, rows_per_wg, ntasks, lds_bytes, s);
         case QMM_TYPE_Q8_0:   return launch_t<QMM_TYPE_Q8_0>(p, nc, rows_per_wg, ntasks, lds_bytes, s);

@@ -15,11 +15,6 @@ namespace {
 
 #pragma clang fp contract(off)
 
-__device__ __forceinline__ const float * col_ptr(const F32Cols & s, int64_t c) {
-    const int64_t i1 = c % s.ne1, r = c / s.ne1, i2 = r % s.ne2, i3 = r / s.ne2;
-    return reinterpret_cast<const float *>(s.base + i1 * s.nb1 + i2 * s.nb2 + i3 * s.nb3);
-}
-
 // 8 lanes per 32-weight block, 4 weights per lane
 __global__ void k_quant_q8_0(F32Cols src, int64_t K, int64_t ncols, ActBuf a, int want_h) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -28,32 +23,21 @@ __global__ void k_quant_q8_0(F32Cols src, int64_t K, int64_t ncols, ActBuf a, in
     const int64_t c = live ? t / kq : 0, k = live ? (t % kq) * 4 : 0;
     float v[4] = { 0.f, 0.f, 0.f, 0.f };
     if (live) {
-        const float * x = col_ptr(src, c) + k;
+        const float * x = f32_col(src, c) + k;
         for (int i = 0; i < 4; ++i) v[i] = x[i];
     }
-    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    for (int o = 1; o < 8; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
-    const _Float16 dh = (_Float16)(amax / 127.f);
-    const float mul = amax != 0.0f ? 127.f / amax : 0.0f;
-    int q[4], s = 0;
-    for (int i = 0; i < 4; ++i) {
-        float r = __builtin_rintf(v[i] * mul);
-        r = fminf(fmaxf(r, -128.f), 127.f);
-        q[i] = (int)r;
-        s += q[i];
-    }
-    for (int o = 1; o < 8; o <<= 1) s += __shfl_xor(s, o, 64);
+    float d;
+    int s;
+    const uint32_t packed = quant_q8_0_lane(v, &d, &s);
     if (!live) return;
     const int64_t base = c * K + k;
-    const uint32_t packed = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
-                            ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
     *reinterpret_cast<uint32_t *>(a.codes + base) = packed;
     if (want_h) {
-        for (int i = 0; i < 4; ++i) a.hcodes[base + i] = (_Float16)q[i];
+        for (int i = 0; i < 4; ++i) a.hcodes[base + i] = (_Float16)(int8_t)(packed >> (8 * i));
     }
     if ((t & 7) == 0) {
         const int64_t b = c * (K / 32) + k / 32;
-        a.d[b] = (float)dh;
+        a.d[b] = d;
         a.sums[b] = (int16_t)s;
     }
 }
@@ -65,45 +49,19 @@ __global__ void k_quant_q8_K(F32Cols src, int64_t K, int64_t ncols, ActBuf a, in
     const int64_t nsb = K / 256;
     if (wave >= ncols * nsb) return;               // whole waves only
     const int64_t c = wave / nsb, sb = wave % nsb;
-    const float * x = col_ptr(src, c) + sb * 256 + 4 * lane;
+    const float * x = f32_col(src, c) + sb * 256 + 4 * lane;
     float v[4];
     for (int i = 0; i < 4; ++i) v[i] = x[i];
-    // first index of the largest |x| (ggml: `if (ax > amax)` in order)
-    float ba = -1.0f;
-    int bi = 0;
-    for (int i = 0; i < 4; ++i) {
-        const float av = fabsf(v[i]);
-        if (av > ba) { ba = av; bi = 4 * lane + i; }
-    }
-    for (int o = 32; o > 0; o >>= 1) {
-        const float oa = __shfl_xor(ba, o, 64);
-        const int oi = __shfl_xor(bi, o, 64);
-        if (oa > ba || (oa == ba && oi < bi)) { ba = oa; bi = oi; }
-    }
-    const float pick = (bi & 3) == 0 ? v[0] : (bi & 3) == 1 ? v[1] : (bi & 3) == 2 ? v[2] : v[3];
-    const float mx = __shfl(pick, bi >> 2, 64);
+    float d;
+    int s;
+    const uint32_t packed = quant_q8_K_wave(v, lane, &d, &s);
     const int64_t base = c * K + sb * 256 + 4 * lane;
-    int q[4] = { 0, 0, 0, 0 };
-    float dv = 0.0f;
-    if (ba != 0.0f) {
-        const float iscale = -127.f / mx;
-        for (int i = 0; i < 4; ++i) {
-            const int r = (int)__builtin_rintf(iscale * v[i]);
-            q[i] = r > 127 ? 127 : r;
-        }
-        dv = 1.0f / iscale;
-    }
-    int s = q[0] + q[1] + q[2] + q[3];
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
-    const uint32_t packed = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
-                            ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
     *reinterpret_cast<uint32_t *>(a.codes + base) = packed;
     if (want_h) {
-        for (int i = 0; i < 4; ++i) a.hcodes[base + i] = (_Float16)q[i];
+        for (int i = 0; i < 4; ++i) a.hcodes[base + i] = (_Float16)(int8_t)(packed >> (8 * i));
     }
     if ((lane & 3) == 0) a.sums[c * (K / 16) + sb * 16 + (lane >> 2)] = (int16_t)s;
-    if (lane == 0) a.d[c * nsb + sb] = dv;
+    if (lane == 0) a.d[c * nsb + sb] = d;
 }
 
 // ActBuf -> ggml block bytes, one thread per block

@@ -48,6 +48,10 @@ struct qmm_ctx {
     // downgrade counter (paths slower than the type promises)
     int64_t downgrades = 0;
     std::string downgrade_names;
+    // main-kernel timing (qmm_kernel_timing)
+    bool ktime = false;
+    std::vector<hipEvent_t> kev;   // pairs
+    size_t kev_used = 0;
 };
 
 namespace {
@@ -209,6 +213,21 @@ bool check_f32(const qmm_tensor * t) {
     return t && t->buffer && t->type == QMM_TYPE_F32 && t->nb[0] == sizeof(float) && t->ne[0] > 0;
 }
 
+// event pair around the main kernel of an op when timing is on
+int ktime_mark(qmm_ctx * ctx, bool begin) {
+    if (!ctx->ktime) return QMM_OK;
+    if (begin && ctx->kev_used + 2 > ctx->kev.size()) {
+        for (int i = 0; i < 64; ++i) {
+            hipEvent_t e;
+            QMM_HIP(ctx, hipEventCreate(&e));
+            ctx->kev.push_back(e);
+        }
+    }
+    QMM_HIP(ctx, hipEventRecord(ctx->kev[ctx->kev_used], ctx->stream));
+    ctx->kev_used++;
+    return QMM_OK;
+}
+
 void note_downgrade(qmm_ctx * ctx, const char * key) {
     ctx->downgrades++;
     ctx->downgrade_names = key;
@@ -263,6 +282,7 @@ void qmm_ctx_free(qmm_ctx * ctx) {
     if (ctx->stream) hipStreamSynchronize(ctx->stream);
     if (ctx->act) hipFree(ctx->act);
     if (ctx->route) hipFree(ctx->route);
+    for (hipEvent_t e : ctx->kev) (void)hipEventDestroy(e);
     if (ctx->ev0) hipEventDestroy(ctx->ev0);
     if (ctx->ev1) hipEventDestroy(ctx->ev1);
     if (ctx->stream) hipStreamDestroy(ctx->stream);
@@ -337,14 +357,14 @@ static int tensor_io(qmm_ctx * ctx, const qmm_tensor * t, void * host, size_t of
     uint8_t * dev = (uint8_t *)t->buffer->ptr + t->offs;
     if (write) ctx->key.valid = false;
     const TypeLayout * L = type_layout(t->type);
+    if (L && (offset % L->bytes || size % L->bytes))
+        return fail(ctx, QMM_ERR_INVALID, "tensor io: offset %zu / size %zu not whole %d-byte blocks", offset, size, L->bytes);
     if (!L || L->nfields == 1) {   // the device bytes are the GGUF bytes
         if (write) QMM_HIP(ctx, hipMemcpyAsync(dev + offset, host, size, hipMemcpyHostToDevice, ctx->stream));
         else QMM_HIP(ctx, hipMemcpyAsync(host, dev + offset, size, hipMemcpyDeviceToHost, ctx->stream));
         QMM_HIP(ctx, hipStreamSynchronize(ctx->stream));
         return QMM_OK;
     }
-    if (offset % L->bytes || size % L->bytes)
-        return fail(ctx, QMM_ERR_INVALID, "tensor io: offset %zu / size %zu not whole %d-byte blocks", offset, size, L->bytes);
     const int64_t nblk = nelements(t->ne) / L->blck, b0 = (int64_t)(offset / L->bytes), nb = (int64_t)(size / L->bytes);
     size_t poff[4];
     planes_alloc(*L, nblk, poff);
@@ -462,9 +482,12 @@ int qmm_mul_mat(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1,
     const int64_t K = src0->ne[0], M = src0->ne[1];
     const int64_t N = src1->ne[1];
     const bool use_gemm = N >= gemm_min_cols();
-    ActBuf a;
-    int rc = quantize_src1(ctx, src0->type, src1, use_gemm, &a);
-    if (rc) return rc;
+    // up to 8 columns per batch: one task, the GEMV quantizes x in LDS itself
+    const bool fused = N <= kMaxTaskCols && !use_gemm;
+    ActBuf a{};
+    int rc;
+    if (!fused && (rc = quantize_src1(ctx, src0->type, src1, use_gemm, &a))) return rc;
+    const F32Cols xs = f32_cols(src1);
     const WView w = weight_view(src0, M);
     float * d = (float *)((uint8_t *)dst->buffer->ptr + dst->offs);
     GemvDense dn;
@@ -478,10 +501,12 @@ int qmm_mul_mat(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1,
     dn.d_nb2 = (int64_t)(dst->nb[2] / 4);
     dn.d_nb3 = (int64_t)(dst->nb[3] / 4);
     const int nc = (int)std::min<int64_t>(N, kMaxTaskCols);
-    ctx->path = N <= kMaxTaskCols ? "gemv" : "gemv-tasks";
+    ctx->path = fused ? "gemv-fused" : "gemv-tasks";
     if (N > kMaxTaskCols) note_downgrade(ctx, "mul_mat: many columns on the GEMV");
-    QMM_HIP(ctx, launch_gemv_any(src0->type, w, M, K, a, nullptr, 0, nullptr, nc, &dn, d, ctx->stream));
-    return QMM_OK;
+    if ((rc = ktime_mark(ctx, true))) return rc;
+    QMM_HIP(ctx, launch_gemv_any(src0->type, w, M, K, fused ? nullptr : &a, &xs, nullptr, 0, nullptr, nc, &dn, d,
+                                 ctx->stream));
+    return ktime_mark(ctx, false);
 }
 
 int qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1, const qmm_tensor * ids,
@@ -493,9 +518,12 @@ int qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * sr
     QMM_HIP(ctx, hipSetDevice(ctx->device));
     const int64_t K = src0->ne[0], M = src0->ne[1], n_as = src0->ne[2];
     const int64_t n_used = ids->ne[0], T = ids->ne[1], ne11 = src1->ne[1];
-    ActBuf a;
-    int rc = quantize_src1(ctx, src0->type, src1, false, &a);
-    if (rc) return rc;
+    // few tokens: each work-group quantizes its task's columns itself
+    const bool fused = T < 16;
+    ActBuf a{};
+    int rc = QMM_OK;
+    if (!fused && (rc = quantize_src1(ctx, src0->type, src1, false, &a))) return rc;
+    const F32Cols xs = f32_cols(src1);
     const int64_t npairs = n_used * T;
     const int64_t max_tasks = npairs / kMaxTaskCols + std::min(n_as, npairs) + 1;
     const size_t o_tasks = align_up((size_t)npairs * 4, 256);
@@ -519,9 +547,11 @@ int qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * sr
     QMM_HIP(ctx, launch_route(r, (int32_t *)rb, tasks, ntasks, d, M, ctx->stream));
     const WView w = weight_view(src0, M);
     const int nc = (int)std::min<int64_t>(kMaxTaskCols, T);
-    ctx->path = "gemv-id";
-    QMM_HIP(ctx, launch_gemv_any(src0->type, w, M, K, a, tasks, (int)max_tasks, ntasks, nc, nullptr, d, ctx->stream));
-    return QMM_OK;
+    ctx->path = fused ? "gemv-id-fused" : "gemv-id";
+    if ((rc = ktime_mark(ctx, true))) return rc;
+    QMM_HIP(ctx, launch_gemv_any(src0->type, w, M, K, fused ? nullptr : &a, &xs, tasks, (int)max_tasks, ntasks, nc,
+                                 nullptr, d, ctx->stream));
+    return ktime_mark(ctx, false);
 }
 
 int qmm_graph_compute(qmm_ctx * ctx, const qmm_node * nodes, int n_nodes) {
@@ -595,6 +625,28 @@ int64_t qmm_downgrades(qmm_ctx * ctx, char * buf, size_t buf_len) {
     if (!ctx) return -1;
     if (buf && buf_len) snprintf(buf, buf_len, "%s", ctx->downgrade_names.c_str());
     return ctx->downgrades;
+}
+
+int qmm_kernel_timing(qmm_ctx * ctx, int enable) {
+    if (!ctx) return QMM_ERR_INVALID;
+    QMM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    ctx->ktime = enable != 0;
+    ctx->kev_used = 0;
+    return QMM_OK;
+}
+
+int qmm_kernel_time(qmm_ctx * ctx, double * total_ms, int64_t * launches) {
+    if (!ctx || !total_ms || !launches) return QMM_ERR_INVALID;
+    QMM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    double t = 0.0;
+    for (size_t i = 0; i + 1 < ctx->kev_used; i += 2) {
+        float ms = 0.0f;
+        QMM_HIP(ctx, hipEventElapsedTime(&ms, ctx->kev[i], ctx->kev[i + 1]));
+        t += ms;
+    }
+    *total_ms = t;
+    *launches = (int64_t)(ctx->kev_used / 2);
+    return QMM_OK;
 }
 
 int qmm_timer_begin(qmm_ctx * ctx) {

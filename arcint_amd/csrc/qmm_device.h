@@ -61,3 +61,80 @@ __device__ __forceinline__ float group_sum(float v, int width) {
 }
 
 }  // namespace qmm
+
+namespace qmm {
+
+// ---------------------------------------------------------------------------
+// Activation quantizers, shared by the stand-alone pre-pass (k_quant.hip) and
+// the GEMV's fused in-LDS quantization, so both are bit-identical with
+// ggml-cpu's from_float (see k_quant.hip for the exact forms).
+// ---------------------------------------------------------------------------
+#pragma clang fp contract(off)
+
+// q8_0 over 8 lanes (4 values each) of one 32-weight block; lane-group
+// aligned (lanes 8g..8g+7).  Returns this lane's four codes packed; *d and
+// *s (block scale, block code sum) are valid in every lane of the group.
+__device__ __forceinline__ uint32_t quant_q8_0_lane(const float v[4], float * d, int * s) {
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    for (int o = 1; o < 8; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    const _Float16 dh = (_Float16)(amax / 127.f);
+    const float mul = amax != 0.0f ? 127.f / amax : 0.0f;
+    int q[4], sum = 0;
+    for (int i = 0; i < 4; ++i) {
+        float r = __builtin_rintf(v[i] * mul);
+        r = fminf(fmaxf(r, -128.f), 127.f);
+        q[i] = (int)r;
+        sum += q[i];
+    }
+    for (int o = 1; o < 8; o <<= 1) sum += __shfl_xor(sum, o, 64);
+    *d = (float)dh;
+    *s = sum;
+    return (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) | ((uint32_t)(q[2] & 0xff) << 16) |
+           ((uint32_t)(q[3] & 0xff) << 24);
+}
+
+// q8_K over a whole wave (4 values per lane, lane-major) of one 256-weight
+// super-block.  Returns this lane's codes; *d is the block scale (all lanes),
+// *bsum the sum of lanes 4b..4b+3's codes (valid in every lane of the quad).
+__device__ __forceinline__ uint32_t quant_q8_K_wave(const float v[4], int lane, float * d, int * bsum) {
+    float ba = -1.0f;
+    int bi = 0;
+    for (int i = 0; i < 4; ++i) {
+        const float av = fabsf(v[i]);
+        if (av > ba) { ba = av; bi = 4 * lane + i; }
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        const float oa = __shfl_xor(ba, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (oa > ba || (oa == ba && oi < bi)) { ba = oa; bi = oi; }
+    }
+    const float pick = (bi & 3) == 0 ? v[0] : (bi & 3) == 1 ? v[1] : (bi & 3) == 2 ? v[2] : v[3];
+    const float mx = __shfl(pick, bi >> 2, 64);
+    int q[4] = { 0, 0, 0, 0 };
+    float dv = 0.0f;
+    if (ba != 0.0f) {
+        const float iscale = -127.f / mx;
+        for (int i = 0; i < 4; ++i) {
+            const int r = (int)__builtin_rintf(iscale * v[i]);
+            q[i] = r > 127 ? 127 : r;
+        }
+        dv = 1.0f / iscale;
+    }
+    int s = q[0] + q[1] + q[2] + q[3];
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    *d = dv;
+    *bsum = s;
+    return (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) | ((uint32_t)(q[2] & 0xff) << 16) |
+           ((uint32_t)(q[3] & 0xff) << 24);
+}
+
+#pragma clang fp contract(fast)
+
+// f32 column c of an activation tensor (columns (i1, i2, i3), i1 fastest)
+__device__ __forceinline__ const float * f32_col(const F32Cols & s, int64_t c) {
+    const int64_t i1 = c % s.ne1, r = c / s.ne1, i2 = r % s.ne2, i3 = r / s.ne2;
+    return reinterpret_cast<const float *>(s.base + i1 * s.nb1 + i2 * s.nb2 + i3 * s.nb3);
+}
+
+}  // namespace qmm

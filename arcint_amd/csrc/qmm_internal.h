@@ -107,10 +107,12 @@ struct GemvDense {
 };
 
 // GEMV: dst[dst_off + m] for m < M, rows of matrix `mat` of each task.
+// Activations come pre-quantized (`a`) or as f32 columns (`src`) that every
+// work-group quantizes into LDS itself (bit-identical to the pre-pass).
 // List mode (tasks != nullptr): `ntasks_dev` (optional) bounds the task list
 // on the device, ntasks_max sizes the grid.  Dense mode (tasks == nullptr):
 // tasks of up to nc columns are derived from `dense`.
-hipError_t launch_gemv_any(int type, const WView & w, int64_t M, int64_t K, const ActBuf & a,
+hipError_t launch_gemv_any(int type, const WView & w, int64_t M, int64_t K, const ActBuf * a, const F32Cols * src,
                            const GemvTask * tasks, int ntasks_max, const int32_t * ntasks_dev, int nc,
                            const GemvDense * dense, float * dst, hipStream_t s);
 

@@ -32,7 +32,8 @@ EXPORTS = (
     "qmm_buffer_size", "qmm_buffer_base", "qmm_tensor_alloc_size", "qmm_tensor_nbytes", "qmm_type_block",
     "qmm_tensor_set", "qmm_tensor_get", "qmm_supports_op", "qmm_mul_mat", "qmm_mul_mat_id",
     "qmm_graph_compute", "qmm_dequantize", "qmm_quantize_act", "qmm_synchronize", "qmm_downgrades",
-    "qmm_last_path", "qmm_timer_begin", "qmm_timer_end", "qmm_buffer_copy",
+    "qmm_last_path", "qmm_timer_begin", "qmm_timer_end", "qmm_buffer_copy", "qmm_kernel_timing",
+    "qmm_kernel_time",
 )
 
 
@@ -93,6 +94,8 @@ def load() -> C.CDLL:
         L.qmm_timer_end.argtypes = [vp]
         L.qmm_timer_end.restype = C.c_float
         L.qmm_buffer_copy.argtypes = [vp, vp, sz, vp, sz, sz]
+        L.qmm_kernel_timing.argtypes = [vp, C.c_int]
+        L.qmm_kernel_time.argtypes = [vp, C.POINTER(C.c_double), C.POINTER(i64)]
         _lib = L
     return _lib
 
@@ -258,6 +261,15 @@ class Backend:
         if ms < 0:
             raise QmmError("timer_end failed")
         return ms
+
+    def kernel_timing(self, enable: bool):
+        self._check(self.L.qmm_kernel_timing(self.h, 1 if enable else 0), "kernel_timing")
+
+    def kernel_time(self) -> tuple[float, int]:
+        """(summed ms, launches) of the main kernels since kernel_timing(True)"""
+        ms, n = C.c_double(0), C.c_int64(0)
+        self._check(self.L.qmm_kernel_time(self.h, C.byref(ms), C.byref(n)), "kernel_time")
+        return ms.value, n.value
 
     def copy(self, dst: Buffer, dst_off: int, src: Buffer, src_off: int, size: int):
         self._check(self.L.qmm_buffer_copy(self.h, C.c_void_p(dst.ptr), dst_off, C.c_void_p(src.ptr), src_off, size),

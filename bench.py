@@ -1,0 +1,182 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized MUL_MAT hot path on one MI355X.
+
+Headline (`value`): Q4_K decode GEMV throughput in GB/s at N = 1 on the
+27B-class FFN gate/up shape (17408 x 5120), one step = one
+MUL_MAT (activation quantization + GEMV) over one of ~12 distinct weight
+copies (>= 2 x the 256 MB Infinity Cache), so the bytes come from HBM.
+Algorithmic bytes per step = weight block bytes + K*N*4 (x) + M*N*4 (dst).
+
+Also reported, on the same JSON line:
+  roofline      the GEMV kernel's own duration (HIP events around each launch
+                on the library's stream, a second pass of the same loop) ->
+                achieved GB/s against 8 TB/s, plus HBM traffic per launch
+                from profiles/ when the rocprofv3 PMC runs were committed
+  cpu_baseline  the CPU oracle (a C restatement of ggml-cpu's algorithm,
+                kind "port") on the same op, bounded to ~--cpu-seconds
+  secondary     Q4_0 4096x4096 at N = 512 (config 1) in TOPS vs the dense
+                int8 MFMA peak
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+MALL_BYTES = 256 << 20
+
+
+def weight_copies(be, qm, synth, qtype, M, K, seed, min_total=2 * MALL_BYTES):
+    raw = synth.weights(qtype, M, K, seed)
+    ncopy = max(2, -(-min_total // raw.nbytes))
+    first = be.new_tensor(qtype, (K, M))
+    be.set_tensor(first, raw)
+    ws = [first]
+    size = qm.alloc_size(qtype, (K, M))
+    for _ in range(ncopy - 1):
+        t = be.new_tensor(qtype, (K, M))
+        be.copy(t.buf, 0, first.buf, 0, size)
+        ws.append(t)
+    be.synchronize()
+    return raw, ws
+
+
+def run_mul_mat(be, ws, xt, yt, steps):
+    for i in range(steps):
+        be.mul_mat(ws[i % len(ws)], xt, yt)
+
+
+def time_op(be, ws, xt, yt, steps, warmup):
+    run_mul_mat(be, ws, xt, yt, warmup)
+    be.synchronize()
+    t0 = time.perf_counter()
+    be.timer_begin()
+    run_mul_mat(be, ws, xt, yt, steps)
+    dev_ms = be.timer_end()
+    wall = time.perf_counter() - t0
+    # second pass: the main kernel's own duration
+    be.kernel_timing(True)
+    run_mul_mat(be, ws, xt, yt, steps)
+    k_ms, n = be.kernel_time()
+    be.kernel_timing(False)
+    return wall, dev_ms, k_ms / max(n, 1)
+
+
+def profile_traffic(kernel_tag):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary, if any."""
+    p = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(p):
+        return None
+    try:
+        d = json.load(open(p))
+        return d.get(kernel_tag)
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(orc, qtype, raw, M, K, x, budget_s):
+    threads = min(os.cpu_count() or 1, 16)
+    nbytes = raw.nbytes + K * 4 + M * 4
+    orc.mul_mat(qtype, raw, M, K, x, threads=threads)     # warm
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        orc.mul_mat(qtype, raw, M, K, x, threads=threads)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or reps >= 2000:
+            break
+    return {"value": round(nbytes * reps / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"Q4_K {M}x{K} N=1 MUL_MAT x{reps} reps ({el:.1f} s) with the C oracle "
+                      f"(ggml-cpu's algorithm restated, scalar C, -O3 -mavx2)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--only", default="", help="profile one workload: q4k_gemv or q40_gemm")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for {args.gpus}); "
+              "MUL_MAT would shard by output rows with no reduction, see DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+
+    from arcint_amd import qmm, synth
+
+    be = qmm.Backend(0)
+    out = {}
+    M, K, N = 17408, 5120, 1
+    if args.only in ("", "q4k_gemv"):
+        raw, ws = weight_copies(be, qmm, synth, qmm.Q4_K, M, K, seed=0)
+        x = synth.activations(N, K, seed=1)
+        xt = be.new_tensor(qmm.F32, (K, N))
+        be.set_tensor(xt, x.view(np.uint8).ravel())
+        yt = be.new_tensor(qmm.F32, (M, N))
+        wall, dev_ms, k_ms = time_op(be, ws, xt, yt, args.steps, args.warmup)
+        path = be.last_path()
+        algo = raw.nbytes + K * N * 4 + M * N * 4
+        value = algo * args.steps / wall / 1e9
+        achieved = algo / (k_ms * 1e-3) / 1e9
+        traffic = profile_traffic("q4k_gemv")
+        out.update({
+            "metric": "Q4_K GEMV GB/s (% of 8 TB/s) at N=1; Q4_0 GEMM TOPS (% MFMA peak) at N=512",
+            "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(wall * 1e3 / args.steps, 5), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+            "config": {"workload": "Q4_K GEMV 17408x5120 N=1 (config 2 ffn gate/up), MUL_MAT incl. q8_K pre-pass",
+                       "weights": "Q4_K", "M": M, "K": K, "N": N, "weight_copies": len(ws),
+                       "rotated_bytes": int(len(ws) * raw.nbytes), "path": path,
+                       "device_ms_per_step": round(dev_ms / args.steps, 5)},
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                         "kernel": f"k_gemv<Q4_K,1>", "kernel_us": round(k_ms * 1e3, 3),
+                         "algorithmic_bytes": int(algo)},
+        })
+        if not args.no_cpu:
+            import oracle
+            out["cpu_baseline"] = cpu_baseline(oracle, qmm.Q4_K, raw, M, K, x, args.cpu_seconds)
+        for w in ws:
+            be.free_buffer(w.buf)
+
+    if not args.no_secondary and args.only in ("", "q40_gemm"):
+        M2, K2, N2 = 4096, 4096, 512
+        raw2, ws2 = weight_copies(be, qmm, synth, qmm.Q4_0, M2, K2, seed=2)
+        x2 = synth.activations(N2, K2, seed=3)
+        xt2 = be.new_tensor(qmm.F32, (K2, N2))
+        be.set_tensor(xt2, x2.view(np.uint8).ravel())
+        yt2 = be.new_tensor(qmm.F32, (M2, N2))
+        steps2 = max(5, args.steps // 10)
+        wall2, dev2, k2 = time_op(be, ws2, xt2, yt2, steps2, max(2, args.warmup // 4))
+        ops = 2.0 * M2 * N2 * K2
+        sec = {"workload": "Q4_0 GEMM 4096x4096x512 (config 1 attn)", "path": be.last_path(),
+               "tops": round(ops * steps2 / wall2 / 1e12, 3),
+               "kernel_tops": round(ops / (k2 * 1e-3) / 1e12, 3),
+               "frac_int8_peak": round(ops / (k2 * 1e-3) / 1e12 / INT8_PEAK_TOPS, 5),
+               "ms_per_op": round(wall2 * 1e3 / steps2, 4), "kernel_ms": round(k2, 4)}
+        if out:
+            out["secondary"] = sec
+        else:
+            out = {"metric": "Q4_0 GEMM TOPS at N=512", "value": sec["tops"], "unit": "TOPS", "secondary": sec}
+    be.close()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -168,6 +168,13 @@ const char * qmm_last_path(qmm_ctx * ctx);
 int    qmm_timer_begin(qmm_ctx * ctx);
 float  qmm_timer_end(qmm_ctx * ctx);
 
+/* Per-kernel device time of the main kernel of every op (the GEMV / GEMM,
+ * not the activation pre-pass): enable(1) clears and starts recording a HIP
+ * event pair around each such launch on the context's stream; read waits for
+ * the stream and returns the summed milliseconds and the launch count. */
+int    qmm_kernel_timing(qmm_ctx * ctx, int enable);
+int    qmm_kernel_time(qmm_ctx * ctx, double * total_ms, int64_t * launches);
+
 /* Copy between device buffers on the context's stream (harness plumbing). */
 int    qmm_buffer_copy(qmm_ctx * ctx, qmm_buffer * dst, size_t dst_off, const qmm_buffer * src, size_t src_off, size_t size);
 

@@ -208,10 +208,11 @@ def test_mul_mat_broadcast_and_strides(be, sc, orc):
     # a strided src1 view (every other column) and a padded dst
     xs = synth.activations(2 * N, K, seed=63)
     xst = sc.f32(xs)
+    w2 = sc.weights(qtype, raw[:rb], (K, M))
     view = qmm.Tensor(xst.buf, qmm.F32, (K, N), nb=(4, 8 * K, 8 * K * N, 8 * K * N))
     ypad = sc.empty_f32((M + 5, N))
     yview = qmm.Tensor(ypad.buf, qmm.F32, (M, N), nb=(4, 4 * (M + 5), 4 * (M + 5) * N, 4 * (M + 5) * N))
-    be.mul_mat(w, view, yview)
+    be.mul_mat(w2, view, yview)
     be.synchronize()
     got = be.get_f32(ypad).reshape(N, M + 5)[:, :M]
     ref = orc.mul_mat(qtype, raw[:rb], M, K, xs[0::2])
