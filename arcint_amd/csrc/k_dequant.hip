@@ -43,7 +43,7 @@ __global__ void k_deq_q4_K(WView w, int64_t nblk, float * __restrict__ y) {
     if (t >= nblk * 4) return;
     const int64_t i = t >> 2;
     const int c = (int)(t & 3);
-    const uint8_t * b = w.p[0] + i * 144;
+    const uint8_t * b = w.p[1] + i * 16;            // header {d, dmin, scales[12]}
     const float d = h2f(reinterpret_cast<const uint16_t *>(b)[0]);
     const float dmin = h2f(reinterpret_cast<const uint16_t *>(b)[1]);
     const uint8_t * s = b + 4;
@@ -55,7 +55,7 @@ __global__ void k_deq_q4_K(WView w, int64_t nblk, float * __restrict__ y) {
     }
     const float d1 = d * (float)sc[0], m1 = dmin * (float)m[0];
     const float d2 = d * (float)sc[1], m2 = dmin * (float)m[1];
-    const uint8_t * q = b + 16 + 32 * c;
+    const uint8_t * q = w.p[0] + i * 128 + 32 * c;
     float * o = y + i * 256 + 64 * c;
     for (int l = 0; l < 32; ++l) o[l] = d1 * (float)(q[l] & 0xF) - m1;
     for (int l = 0; l < 32; ++l) o[32 + l] = d2 * (float)(q[l] >> 4) - m2;

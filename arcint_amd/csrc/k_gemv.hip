@@ -4,17 +4,24 @@
 // kernel_mul_mv_q4_0_q8_1 (P02:6098-6220), kernel_mul_mv_iq4_xs_q8_1
 // (P01:3457-3553) and the MUL_MAT_ID matvec (P01:3923-3964), redesigned for
 // CDNA4 and for ggml-cpu's numerics instead of the reference's two-term q8_1:
-//  * activations are the vec_dot type's codes (q8_0 or q8_K, made on the
-//    device bit-exactly by k_quant.hip) staged per work-group in LDS, so the
-//    integer dot of every (sub-)block equals ggml-cpu's exactly and only the
-//    fp32 combine order differs;
-//  * each lane streams 16-byte units of the weight planes (one wave load =
-//    1 KB contiguous per row), unpacks nibbles / 6-bit codes / the IQ4
-//    codebook in VGPRs and reduces with v_dot4_i32_i8;
-//  * LPR lanes share one row (LPR = 64 for rows of >= 64 units), the partial
-//    sums are reduced across them with lane shuffles at the end.
+//  * activations are the vec_dot type's codes (q8_0 or q8_K, bit-exact with
+//    ggml-cpu's from_float) staged per work-group in LDS, so the integer dot
+//    of every (sub-)block equals ggml-cpu's exactly and only the fp32 combine
+//    order differs;
+//  * each lane streams 16-byte units of the weight planes (one wave load
+//    instruction = 64 contiguous 16-byte units), unpacks nibbles / 6-bit
+//    codes / the IQ4 codebook in VGPRs and reduces with v_dot4_i32_i8;
+//  * LPR lanes share one row (LPR chosen per shape so that few lanes idle),
+//    a wave covers RG = 64 / LPR rows at a time and walks row groups with a
+//    grid stride; the weight loads run D units ahead of the arithmetic in a
+//    register ring that crosses row boundaries, and the first D loads are in
+//    flight before the work-group quantizes x into LDS;
+//  * partial sums of a row are reduced across its LPR lanes with cross-lane
+//    adds once per row and written straight to dst (accumulated across K
+//    chunks when x does not fit LDS at once).
 // A task is up to NC activation columns against one weight matrix; dense
-// MUL_MAT derives its task from the grid, MUL_MAT_ID reads device-built tasks.
+// MUL_MAT derives its task from blockIdx.y, MUL_MAT_ID reads device-built
+// task lists.
 #include "qmm_device.h"
 
 #include <algorithm>
@@ -38,9 +45,9 @@ struct GemvParams {
     int64_t ne11, ne12, r2, r3, ne02, tpb;
     int64_t d_nb1, d_nb2, d_nb3; // dst strides in floats
     float * dst;
-    int kc;                      // weights per LDS chunk
+    int kc;                      // weights per LDS chunk (a multiple of 256, or K)
     int lpr_log2;                // lanes per row = 1 << lpr_log2
-    int riw;                     // row iterations per wave
+    int64_t ngroups;             // row groups of 64 / LPR rows
 };
 
 // activation chunk in LDS: NC columns of codes, then scales, then sums
@@ -115,6 +122,7 @@ template <> struct GV<QMM_TYPE_Q8_0> {
 };
 
 // ---- Q4_K: unit = 16 B of codes (part p of 8) + the 16 B block header -----
+// Planes: codes qs[128] per block, header {d, dmin, scales[12]} per block.
 // part p: chunk c = p/2, bytes 16h..16h+15 (h = p%2) of the chunk's 32 code
 // bytes: low nibbles are weights 64c+16h+[0,16) (sub-block 2c), high nibbles
 // 64c+32+16h+[0,16) (sub-block 2c+1).
@@ -122,9 +130,8 @@ template <> struct GV<QMM_TYPE_Q4_K> {
     static constexpr int BLK = 256, UPB = 8, BS = 256, SS = 16;
     struct W { uint4 q, h; };
     __device__ static void load(W & w, const WView & v, int64_t blk, int part) {
-        const uint8_t * b = v.p[0] + blk * 144;
-        w.h = ld16_nt(b);
-        w.q = ld16_nt(b + 16 + 16 * part);
+        w.q = ld16_nt(v.p[0] + blk * 128 + 16 * part);
+        w.h = ld16(v.p[1] + blk * 16);            // shared by the block's 8 lanes: keep it cached
     }
     template <int NC>
     __device__ static void dot(const W & w, int kb, int part, const XL<NC, BS, SS> & x, int nc, float * acc) {
@@ -171,9 +178,9 @@ template <> struct GV<QMM_TYPE_Q6_K> {
         w.qb = ld16_nt(v.p[0] + blk * 128 + 64 * n + 32 + l0);
         w.qh = ld16_nt(v.p[1] + blk * 64 + 32 * n + l0);
         const uint32_t * sp = reinterpret_cast<const uint32_t *>(v.p[2] + blk * 16 + 8 * n);
-        w.sc.x = ldg_nt(sp);
-        w.sc.y = ldg_nt(sp + 1);
-        w.d = ldg_nt(reinterpret_cast<const uint16_t *>(v.p[3]) + blk);
+        w.sc.x = sp[0];
+        w.sc.y = sp[1];
+        w.d = reinterpret_cast<const uint16_t *>(v.p[3])[blk];
     }
     __device__ static void codes(const W & w, int g, uint32_t o[4]) {
         const uint32_t m = 0x0F0F0F0Fu, mh = 0x30303030u;
@@ -225,8 +232,8 @@ template <> struct GV<QMM_TYPE_IQ4_XS> {
     __device__ static void load(W & w, const WView & v, int64_t blk, int ib) {
         w.q = ld16_nt(v.p[0] + blk * 128 + 16 * ib);
         const uint32_t * hp = reinterpret_cast<const uint32_t *>(v.p[1] + blk * 8);
-        w.h.x = ldg_nt(hp);
-        w.h.y = ldg_nt(hp + 1);
+        w.h.x = hp[0];
+        w.h.y = hp[1];
     }
     template <int NC>
     __device__ static void dot(const W & w, int kb, int ib, const XL<NC, BS, SS> & x, int nc, float * acc) {
@@ -254,49 +261,81 @@ template <> struct GV<QMM_TYPE_IQ4_XS> {
     }
 };
 
-// prefetch depth (items in flight per lane) by type
-template <int TYPE> constexpr int depth() { return TYPE == QMM_TYPE_Q6_K ? 3 : 4; }
+// weight units in flight per lane, by type (register budget: D * sizeof(W))
+template <int TYPE> constexpr int depth() {
+    return TYPE == QMM_TYPE_Q6_K ? 4 : (TYPE == QMM_TYPE_Q8_0 || TYPE == QMM_TYPE_Q4_K) ? 6 : 8;
+}
 
 // Quantize columns [0, nc) of the activation chunk [k0, k0 + kcur) into LDS
-// (codes, scales, sums), exactly as the stand-alone pre-pass does.
+// (codes, scales, sums), bit-identical to the stand-alone pre-pass.  The x
+// loads of QB items are issued together before any of them is used, so the
+// prologue pays about one L2 round trip per QB items rather than one each.
 template <int NC, int BS, int SS>
-__device__ void quantize_chunk(const GemvParams & p, const int64_t * s_col, int nc, int64_t k0, int kcur,
+__device__ void quantize_chunk(const GemvParams & p, const float * const * s_x, int nc, int64_t k0, int kcur,
                                uint8_t * lds) {
+    constexpr int QB = 4;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     int8_t * codes = reinterpret_cast<int8_t *>(lds);
     float * ds = reinterpret_cast<float *>(lds + (size_t)NC * p.kc);
     int16_t * ss = reinterpret_cast<int16_t *>(lds + (size_t)NC * p.kc + (size_t)NC * (p.kc / BS) * 4);
     if constexpr (BS == 256) {
-        const int nsb = kcur / 256;
-        for (int it = wave; it < nc * nsb; it += kWaves) {          // one wave per super-block
-            const int j = it / nsb, sb = it - j * nsb;
-            const float * x = f32_col(p.src, s_col[j]) + k0 + sb * 256 + 4 * lane;
-            float v[4] = { x[0], x[1], x[2], x[3] };
-            float d;
-            int bs;
-            const uint32_t q = quant_q8_K_wave(v, lane, &d, &bs);
-            *reinterpret_cast<uint32_t *>(codes + (size_t)j * p.kc + sb * 256 + 4 * lane) = q;
-            if ((lane & 3) == 0) ss[j * (p.kc / SS) + sb * 16 + (lane >> 2)] = (int16_t)bs;
-            if (lane == 0) ds[j * (p.kc / BS) + sb] = d;
+        // one wave per 256-weight super-block, 4 weights per lane
+        const int nsb = kcur / 256, total = nc * nsb;
+        for (int it0 = wave; it0 < total; it0 += kWaves * QB) {
+            float v[QB][4];
+#pragma unroll
+            for (int q = 0; q < QB; ++q) {
+                const int it = it0 + q * kWaves;
+                if (it < total) {
+                    const int j = it / nsb, sb = it - j * nsb;
+                    const float * x = s_x[j] + k0 + sb * 256 + 4 * lane;
+                    v[q][0] = x[0]; v[q][1] = x[1]; v[q][2] = x[2]; v[q][3] = x[3];
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < QB; ++q) {
+                const int it = it0 + q * kWaves;
+                if (it < total) {                                  // uniform per wave
+                    const int j = it / nsb, sb = it - j * nsb;
+                    float d;
+                    int bs;
+                    const uint32_t c = quant_q8_K_wave(v[q], lane, &d, &bs);
+                    *reinterpret_cast<uint32_t *>(codes + (size_t)j * p.kc + sb * 256 + 4 * lane) = c;
+                    if ((lane & 3) == 0) ss[j * (p.kc / SS) + sb * 16 + (lane >> 2)] = (int16_t)bs;
+                    if (lane == 0) ds[j * (p.kc / BS) + sb] = d;
+                }
+            }
         }
     } else {
-        const int nb = kcur / 32;                                   // 8 lanes per block
-        for (int it = tid >> 3; it < ((nc * nb + 7) & ~7); it += kThreads / 8) {
-            const bool live = it < nc * nb;
-            const int j = live ? it / nb : 0, b = live ? it - j * nb : 0, q4 = tid & 7;
-            float v[4] = { 0.f, 0.f, 0.f, 0.f };
-            if (live) {
-                const float * x = f32_col(p.src, s_col[j]) + k0 + b * 32 + 4 * q4;
-                v[0] = x[0]; v[1] = x[1]; v[2] = x[2]; v[3] = x[3];
+        // 8 lanes per 32-weight block, 4 weights per lane; the loop bounds are
+        // uniform over the work-group so every lane takes part in the
+        // 8-lane reductions
+        const int nb = kcur / 32, total = nc * nb, q4 = tid & 7;
+        for (int it0 = 0; it0 < total; it0 += (kThreads / 8) * QB) {
+            float v[QB][4];
+#pragma unroll
+            for (int q = 0; q < QB; ++q) {
+                const int it = it0 + q * (kThreads / 8) + (tid >> 3);
+                v[q][0] = v[q][1] = v[q][2] = v[q][3] = 0.0f;
+                if (it < total) {
+                    const int j = it / nb, b = it - j * nb;
+                    const float * x = s_x[j] + k0 + b * 32 + 4 * q4;
+                    v[q][0] = x[0]; v[q][1] = x[1]; v[q][2] = x[2]; v[q][3] = x[3];
+                }
             }
-            float d;
-            int sm;
-            const uint32_t q = quant_q8_0_lane(v, &d, &sm);
-            if (live) {
-                *reinterpret_cast<uint32_t *>(codes + (size_t)j * p.kc + b * 32 + 4 * q4) = q;
-                if (q4 == 0) {
-                    ds[j * (p.kc / BS) + b] = d;
-                    ss[j * (p.kc / SS) + b] = (int16_t)sm;
+#pragma unroll
+            for (int q = 0; q < QB; ++q) {
+                const int it = it0 + q * (kThreads / 8) + (tid >> 3);
+                float d;
+                int sm;
+                const uint32_t c = quant_q8_0_lane(v[q], &d, &sm);
+                if (it < total) {
+                    const int j = it / nb, b = it - j * nb;
+                    *reinterpret_cast<uint32_t *>(codes + (size_t)j * p.kc + b * 32 + 4 * q4) = c;
+                    if (q4 == 0) {
+                        ds[j * (p.kc / BS) + b] = d;
+                        ss[j * (p.kc / SS) + b] = (int16_t)sm;
+                    }
                 }
             }
         }
@@ -326,19 +365,26 @@ __device__ void stage_chunk(const GemvParams & p, const int64_t * s_col, int nc,
     }
 }
 
-// One work-group: rows [row0, row0 + 4 * riw * RG) of one task's matrix.
-// Each lane streams its items (row iteration ri, unit iteration i) with
-// depth() weight units in flight; at the end of every row the LPR lanes of
-// the row reduce their partial sums, which accumulate per row in LDS across
-// K chunks and are written once at the end.
-template <int TYPE, int NC>
+// One work-group: waves blockIdx.x * 4 + w walk row groups g, g + stride, ...
+// of one task's matrix.  Lane (rs, rl) handles row g * RG + rs and units
+// rl + LPR * i (i < UI) of it.  Items (g, i) are streamed through a D-deep
+// register ring: item t is used from buf[t % D], then buf[t % D] is refilled
+// with item t + D.  Every ring load is issued unconditionally (an item past
+// the end loads the matrix's first block and is not used), so the number of
+// loads in flight is static and each use waits only for its own load rather
+// than for all of them.  MULTI: x spans several LDS chunks and the partial
+// sums of later chunks are added to dst.
+template <int TYPE, int NC, bool MULTI>
 __global__ __launch_bounds__(kThreads) void k_gemv(GemvParams p) {
     using T = GV<TYPE>;
+    using W = typename T::W;
     constexpr int D = depth<TYPE>();
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ int64_t s_col[NC];      // activation column ids
-    __shared__ int64_t s_doff[NC];
+    __shared__ int64_t s_doff[NC];     // float offset of dst row 0 per column
+    __shared__ const float * s_x[NC];  // f32 activation columns (fused mode)
 
+    // task decode; every count here fits 32 bits, so no 64-bit divisions
     int mat, nc;
     if (p.tasks) {
         if (p.ntasks_dev && (int)blockIdx.y >= *p.ntasks_dev) return;
@@ -350,102 +396,101 @@ __global__ __launch_bounds__(kThreads) void k_gemv(GemvParams p) {
             s_doff[threadIdx.x] = t.dst_off[threadIdx.x];
         }
     } else {
-        const int64_t b = blockIdx.y / p.tpb, tt = blockIdx.y % p.tpb;
-        const int64_t i2 = b % p.ne12, i3 = b / p.ne12;
-        mat = (int)((i2 / p.r2) + (i3 / p.r3) * p.ne02);
-        const int64_t first = tt * NC;
+        const uint32_t y = blockIdx.y, tpb = (uint32_t)p.tpb, ne12 = (uint32_t)p.ne12;
+        const uint32_t b = y / tpb, tt = y - b * tpb;
+        const uint32_t i3 = b / ne12, i2 = b - i3 * ne12;
+        mat = (int)(i2 / (uint32_t)p.r2 + (i3 / (uint32_t)p.r3) * (uint32_t)p.ne02);
+        const int64_t first = (int64_t)tt * NC;
         nc = (int)((p.ne11 - first) < NC ? (p.ne11 - first) : NC);
         if (threadIdx.x < NC && (int)threadIdx.x < nc) {
             const int64_t i1 = first + threadIdx.x;
-            s_col[threadIdx.x] = b * p.ne11 + i1;
-            s_doff[threadIdx.x] = i1 * p.d_nb1 + i2 * p.d_nb2 + i3 * p.d_nb3;
+            s_col[threadIdx.x] = (int64_t)b * p.ne11 + i1;
+            s_doff[threadIdx.x] = i1 * p.d_nb1 + (int64_t)i2 * p.d_nb2 + (int64_t)i3 * p.d_nb3;
         }
     }
-    if (mat < 0 || nc <= 0) return;
+    if (mat < 0 || nc <= 0) return;    // uniform over the work-group
+    if (p.fused && threadIdx.x < NC && (int)threadIdx.x < nc) s_x[threadIdx.x] = f32_col(p.src, s_col[threadIdx.x]);
+    __syncthreads();                   // s_col, s_doff, s_x
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int lprl = p.lpr_log2, LPR = 1 << lprl, RG = 64 >> lprl;
     const int rl = lane & (LPR - 1), rs = lane >> lprl;
-    const int rows_wg = kWaves * p.riw * RG;
-    const int64_t row0 = (int64_t)blockIdx.x * rows_wg;
-    const int64_t bpr = p.w.bpr;
+    const int64_t g0 = (int64_t)blockIdx.x * kWaves + wave, gs = (int64_t)gridDim.x * kWaves;
+    const int64_t ngroups = p.ngroups, M = p.M, bpr = p.w.bpr;
+    const int64_t ngw = g0 < ngroups ? (int64_t)((uint32_t)(ngroups - 1 - g0) / (uint32_t)gs) + 1 : 0;   // row groups of this wave
+    const int64_t row_step = gs * RG, blk_step = row_step * bpr;
     const XL<NC, T::BS, T::SS> x{ lds, p.kc };
-    const size_t xbytes = (size_t)NC * p.kc + (size_t)NC * (p.kc / T::BS) * 4 + (size_t)NC * (p.kc / T::SS) * 2;
-    float * rowacc = reinterpret_cast<float *>(lds + ((xbytes + 15) & ~(size_t)15));   // [rows_wg][NC]
 
     for (int64_t k0 = 0; k0 < p.K; k0 += p.kc) {
         const int kcur = (int)((p.K - k0) < p.kc ? (p.K - k0) : p.kc);
-        __syncthreads();
-        if (p.fused) quantize_chunk<NC, T::BS, T::SS>(p, s_col, nc, k0, kcur, lds);
+        const int nunits = (kcur / T::BLK) * T::UPB;
+        const int UI = (nunits + LPR - 1) >> lprl;            // unit iterations per row
+        const int nitems = (int)(ngw * UI);
+        const int64_t blk0 = (int64_t)mat * M * bpr + k0 / T::BLK;   // (matrix, row 0, chunk start)
+
+        // load cursor: row lrow (block lblk of its unit 0), unit iteration li
+        int64_t lrow = g0 * RG + rs, lblk = blk0 + lrow * bpr;
+        int li = 0;
+        auto issue = [&](W & w) {
+            const int u = rl + (li << lprl);
+            const bool ok = lrow < M && u < nunits;
+            T::load(w, p.w, ok ? lblk + u / T::UPB : blk0, ok ? u % T::UPB : 0);
+            const bool wrap = ++li == UI;
+            li = wrap ? 0 : li;
+            lrow += wrap ? row_step : 0;
+            lblk += wrap ? blk_step : 0;
+        };
+        W buf[D];
+#pragma unroll
+        for (int j = 0; j < D; ++j) issue(buf[j]);
+
+        if (k0 > 0) __syncthreads();       // the previous chunk's LDS reads are done
+        if (p.fused) quantize_chunk<NC, T::BS, T::SS>(p, s_x, nc, k0, kcur, lds);
         else stage_chunk<NC, T::BS, T::SS>(p, s_col, nc, k0, kcur, lds);
         __syncthreads();
 
-        const int nunits = (kcur / T::BLK) * T::UPB;
-        const int upl = (nunits + LPR - 1) >> lprl;           // unit iterations per row
-        const int nitems = p.riw * upl;
-        const int64_t kblk0 = k0 / T::BLK;
-        auto item = [&](int t, int64_t & blk, int & u, int & rloc) -> bool {
-            const int ri = t / upl, i = t - ri * upl;
-            rloc = (wave * p.riw + ri) * RG + rs;
-            u = rl + (i << lprl);
-            const int64_t row = row0 + rloc;
-            blk = ((int64_t)mat * p.M + row) * bpr + kblk0 + u / T::UPB;
-            return row < p.M && u < nunits;
-        };
-        typename T::W buf[D];
-#pragma unroll
-        for (int j = 0; j < D; ++j) {
-            int64_t blk;
-            int u, rloc;
-            if (j < nitems && item(j, blk, u, rloc)) T::load(buf[j], p.w, blk, u % T::UPB);
-        }
+        int64_t crow = g0 * RG + rs;
+        int ci = 0;
         float acc[NC];
 #pragma unroll
         for (int j = 0; j < NC; ++j) acc[j] = 0.0f;
         for (int t0 = 0; t0 < nitems; t0 += D) {
 #pragma unroll
             for (int j = 0; j < D; ++j) {
-                const int t = t0 + j;
-                if (t < nitems) {
-                    const typename T::W cur = buf[j];
-                    int64_t blk;
-                    int u, rloc;
-                    if (t + D < nitems && item(t + D, blk, u, rloc)) T::load(buf[j], p.w, blk, u % T::UPB);
-                    const bool ok = item(t, blk, u, rloc);
-                    if (ok) T::template dot<NC>(cur, u / T::UPB, u % T::UPB, x, nc, acc);
-                    if ((t % upl) == upl - 1) {        // last unit iteration of a row (uniform)
+                if (t0 + j < nitems) {             // uniform per wave
+                    const int u = rl + (ci << lprl);
+                    if (crow < M && u < nunits) T::template dot<NC>(buf[j], u / T::UPB, u % T::UPB, x, nc, acc);
+                    if (++ci == UI) {              // the row is complete (uniform)
+                        ci = 0;
 #pragma unroll
                         for (int c = 0; c < NC; ++c) {
-                            const float v = group_sum(acc[c], LPR);
+                            const float v = group_sum(acc[c], lprl);
                             acc[c] = 0.0f;
-                            if (c < nc && rl == 0 && rloc < rows_wg) {
-                                float & r = rowacc[rloc * NC + c];
-                                r = (k0 == 0) ? v : r + v;
+                            if (c < nc && rl == 0 && crow < M) {
+                                float * o = p.dst + s_doff[c] + crow;
+                                if constexpr (MULTI) *o = (k0 == 0) ? v : *o + v;
+                                else *o = v;
                             }
                         }
+                        crow += row_step;
                     }
                 }
+                issue(buf[j]);
             }
         }
     }
-    __syncthreads();
-    for (int i = tid; i < rows_wg * nc; i += kThreads) {
-        const int c = i / rows_wg, r = i - c * rows_wg;
-        const int64_t row = row0 + r;
-        if (row < p.M) p.dst[s_doff[c] + row] = rowacc[r * NC + c];
-    }
 }
 
-template <int TYPE>
-hipError_t launch_t(const GemvParams & p, int nc, int64_t rows_per_wg, int64_t ntasks, size_t lds_bytes, hipStream_t s) {
-    const dim3 grid((unsigned)((p.M + rows_per_wg - 1) / rows_per_wg), (unsigned)ntasks);
+template <int TYPE, bool MULTI>
+hipError_t launch_t(const GemvParams & p, int nc, int64_t nwg, int64_t ntasks, size_t lds_bytes, hipStream_t s) {
+    const dim3 grid((unsigned)nwg, (unsigned)ntasks);
     switch (nc) {
 #define QMM_NC(N)                                                                                         \
     case N:                                                                                               \
         if (lds_bytes > 65536)                                                                            \
-            (void)hipFuncSetAttribute((const void *)k_gemv<TYPE, N>, hipFuncAttributeMaxDynamicSharedMemorySize, \
-                                      (int)lds_bytes);                                                    \
-        k_gemv<TYPE, N><<<grid, kThreads, lds_bytes, s>>>(p);                                             \
+            (void)hipFuncSetAttribute((const void *)k_gemv<TYPE, N, MULTI>,                               \
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);        \
+        k_gemv<TYPE, N, MULTI><<<grid, kThreads, lds_bytes, s>>>(p);                                      \
         break;
         QMM_NC(1) QMM_NC(2) QMM_NC(3) QMM_NC(4) QMM_NC(5) QMM_NC(6) QMM_NC(7) QMM_NC(8)
 #undef QMM_NC
@@ -471,13 +516,28 @@ int env_int(const char * name, int dflt) {
     return e ? atoi(e) : dflt;
 }
 
+// lanes per row: the widest (fewest rows per wave) that keeps >= 90 % of the
+// lanes busy on a row's units, else the one that idles the fewest lanes
+int pick_lpr_log2(int64_t units) {
+    int best = 6;
+    double best_eff = -1.0;
+    for (int l = 6; l >= 2; --l) {
+        const int64_t lpr = 1 << l;
+        const int64_t ui = (units + lpr - 1) / lpr;
+        const double eff = (double)units / (double)(ui * lpr);
+        if (eff >= 0.9) return l;
+        if (eff > best_eff + 1e-9) { best_eff = eff; best = l; }
+    }
+    return best;
+}
+
 }  // namespace
 
 hipError_t launch_gemv_any(int type, const WView & w, int64_t M, int64_t K, const ActBuf * a, const F32Cols * src,
                            const GemvTask * tasks, int ntasks_max, const int32_t * ntasks_dev, int nc,
                            const GemvDense * dense, float * dst, hipStream_t s) {
     const TypeShape ts = type_shape(type);
-    if (!ts.blk || nc < 1 || nc > kMaxTaskCols || K % ts.blk || (!a && !src)) return hipErrorInvalidValue;
+    if (!ts.blk || nc < 1 || nc > kMaxTaskCols || K % ts.blk || (!a && !src) || M <= 0) return hipErrorInvalidValue;
     GemvParams p{};
     p.w = w;
     p.M = M;
@@ -502,37 +562,36 @@ hipError_t launch_gemv_any(int type, const WView & w, int64_t M, int64_t K, cons
         ntasks = p.tpb * dense->ne12 * dense->ne13;
     }
     if (ntasks <= 0) return hipSuccess;
-    // lanes per row: enough to cover a row's units in one pass, at most a wave
-    const int64_t units = (K / ts.blk) * ts.upb;
-    int lprl = 0;
-    while ((1 << lprl) < units && lprl < 6) ++lprl;
-    p.lpr_log2 = lprl;
-    const int RG = 64 >> lprl;
-    // rows per wave: aim at ~1024 work-groups over all tasks
-    int riw = env_int("QMM_GEMV_RIW", 0);
-    if (riw <= 0) {
-        const int64_t target = std::max<int64_t>(1, 1024 / ntasks);
-        riw = (int)((M + (int64_t)kWaves * RG * target - 1) / ((int64_t)kWaves * RG * target));
-        riw = std::max(1, std::min(riw, 16));
-    }
-    p.riw = riw;
-    const int64_t rows_per_wg = (int64_t)kWaves * riw * RG;
-    // LDS chunk: up to 48 KB of activations per work-group
+    if (ntasks > 65535) return hipErrorInvalidValue;
+    // LDS chunk of x: up to ~40 KB per work-group (several work-groups per CU)
+    const int lds_budget = env_int("QMM_GEMV_LDS", 40960);
     const double per_k = 1.0 + 4.0 / ts.bs + 2.0 / ts.ss;
-    int64_t kc = (int64_t)(49152.0 / (nc * per_k));
+    int64_t kc = (int64_t)((double)lds_budget / (nc * per_k));
     kc = kc / 256 * 256;
     if (kc >= K || kc <= 0) kc = K;
     p.kc = (int)kc;
-    const size_t xbytes = (size_t)nc * kc + (size_t)nc * (kc / ts.bs) * 4 + (size_t)nc * (kc / ts.ss) * 2;
-    const size_t lds_bytes = ((xbytes + 15) & ~(size_t)15) + (size_t)rows_per_wg * nc * 4;
+    const int64_t units = (kc / ts.blk) * ts.upb;
+    const int lprl = env_int("QMM_GEMV_LPR", 0) > 0 ? std::min(6, std::max(0, env_int("QMM_GEMV_LPR", 0))) : pick_lpr_log2(units);
+    p.lpr_log2 = lprl;
+    const int RG = 64 >> lprl;
+    p.ngroups = (M + RG - 1) / RG;
+    // work-groups per task: ~target over all tasks, no more than row groups
+    const int64_t target = std::max(1, env_int("QMM_GEMV_WG", 1024));
+    int64_t nwg = std::max<int64_t>(1, target / ntasks);
+    nwg = std::min<int64_t>(nwg, (p.ngroups + kWaves - 1) / kWaves);
+    const size_t lds_bytes = (size_t)nc * kc + (size_t)nc * (kc / ts.bs) * 4 + (size_t)nc * (kc / ts.ss) * 2;
+    const bool multi = kc < K;
+#define QMM_T(TY) return multi ? launch_t<TY, true>(p, nc, nwg, ntasks, lds_bytes, s) \
+                               : launch_t<TY, false>(p, nc, nwg, ntasks, lds_bytes, s)
     switch (type) {
-        case QMM_TYPE_Q4_0:   return launch_t<QMM_TYPE_Q4_0>(p, nc, rows_per_wg, ntasks, lds_bytes, s);
-        case QMM_TYPE_Q8_0:   return launch_t<QMM_TYPE_Q8_0>(p, nc, rows_per_wg, ntasks, lds_bytes, s);
-        case QMM_TYPE_Q4_K:   return launch_t<QMM_TYPE_Q4_K>(p, nc, rows_per_wg, ntasks, lds_bytes, s);
-        case QMM_TYPE_Q6_K:   return launch_t<QMM_TYPE_Q6_K>(p, nc, rows_per_wg, ntasks, lds_bytes, s);
-        case QMM_TYPE_IQ4_XS: return launch_t<QMM_TYPE_IQ4_XS>(p, nc, rows_per_wg, ntasks, lds_bytes, s);
+        case QMM_TYPE_Q4_0:   QMM_T(QMM_TYPE_Q4_0);
+        case QMM_TYPE_Q8_0:   QMM_T(QMM_TYPE_Q8_0);
+        case QMM_TYPE_Q4_K:   QMM_T(QMM_TYPE_Q4_K);
+        case QMM_TYPE_Q6_K:   QMM_T(QMM_TYPE_Q6_K);
+        case QMM_TYPE_IQ4_XS: QMM_T(QMM_TYPE_IQ4_XS);
         default: return hipErrorInvalidValue;
     }
+#undef QMM_T
 }
 
 }  // namespace qmm

@@ -77,7 +77,7 @@ int fail(qmm_ctx * ctx, int code, const char * fmt, ...) {
 const TypeLayout kLayouts[] = {
     { QMM_TYPE_Q4_0, 32, 18, 2, { { 2, 16 }, { 0, 2 }, { 0, 0 }, { 0, 0 } } },
     { QMM_TYPE_Q8_0, 32, 34, 2, { { 2, 32 }, { 0, 2 }, { 0, 0 }, { 0, 0 } } },
-    { QMM_TYPE_Q4_K, 256, 144, 1, { { 0, 144 }, { 0, 0 }, { 0, 0 }, { 0, 0 } } },
+    { QMM_TYPE_Q4_K, 256, 144, 2, { { 16, 128 }, { 0, 16 }, { 0, 0 }, { 0, 0 } } },
     { QMM_TYPE_Q6_K, 256, 210, 4, { { 0, 128 }, { 128, 64 }, { 192, 16 }, { 208, 2 } } },
     { QMM_TYPE_IQ4_XS, 256, 136, 2, { { 8, 128 }, { 0, 8 }, { 0, 0 }, { 0, 0 } } },
 };

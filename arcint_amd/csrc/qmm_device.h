@@ -54,9 +54,25 @@ __device__ __forceinline__ uint4 ld16_nt(const uint8_t * p) {
 
 __device__ __forceinline__ uint4 ld16(const void * p) { return *reinterpret_cast<const uint4 *>(p); }
 
-// sum over groups of `width` consecutive lanes (width a power of two <= 64)
-__device__ __forceinline__ float group_sum(float v, int width) {
-    for (int o = width >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+// v + the value of lane sel(lane) of the same DPP row, by a DPP move
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+    const int o = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false);
+    return v + __builtin_bit_cast(float, o);
+}
+
+// Sum over groups of 2^log2w consecutive lanes (log2w <= 6); every lane of a
+// group receives the group's sum.  Within a 16-lane DPP row the butterfly
+// uses DPP moves (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror,
+// row_mirror: each pairs every lane with one of the other half of its group
+// of 2, 4, 8, 16); across rows it uses cross-lane permutes.
+__device__ __forceinline__ float group_sum(float v, int log2w) {
+    if (log2w >= 1) v = dpp_add<0xB1>(v);
+    if (log2w >= 2) v = dpp_add<0x4E>(v);
+    if (log2w >= 3) v = dpp_add<0x141>(v);
+    if (log2w >= 4) v = dpp_add<0x140>(v);
+    if (log2w >= 5) v += __shfl_xor(v, 16, 64);
+    if (log2w >= 6) v += __shfl_xor(v, 32, 64);
     return v;
 }
 
@@ -71,12 +87,50 @@ namespace qmm {
 // ---------------------------------------------------------------------------
 #pragma clang fp contract(off)
 
+// DPP lane moves used by the reductions below (all within one 16-lane row):
+// 0xB1 quad_perm [1,0,3,2] (lane ^ 1), 0x4E quad_perm [2,3,0,1] (lane ^ 2),
+// 0x141 row_half_mirror (lane i <-> 7 - i in each half row), 0x140
+// row_mirror (i <-> 15 - i).  After the ^1 and ^2 steps every lane holds its
+// quad's value, so a mirror step combines it with the other quad (half row)
+// or the other half row.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false); }
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) { return __builtin_bit_cast(float, dpp_i<CTRL>(__builtin_bit_cast(int, v))); }
+
+// max / sum over the 8 lanes of an aligned group (every lane gets the result)
+__device__ __forceinline__ float max8(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    return fmaxf(v, dpp_f<0x141>(v));
+}
+__device__ __forceinline__ int sum8(int v) {
+    v += dpp_i<0xB1>(v);
+    v += dpp_i<0x4E>(v);
+    return v + dpp_i<0x141>(v);
+}
+__device__ __forceinline__ int sum4(int v) {
+    v += dpp_i<0xB1>(v);
+    return v + dpp_i<0x4E>(v);
+}
+// max over the whole wave, uniform result (row reduction by DPP, then the
+// four row results read into scalars)
+__device__ __forceinline__ float wave_max(float v) {
+    v = max8(v);
+    v = fmaxf(v, dpp_f<0x140>(v));
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
 // q8_0 over 8 lanes (4 values each) of one 32-weight block; lane-group
-// aligned (lanes 8g..8g+7).  Returns this lane's four codes packed; *d and
-// *s (block scale, block code sum) are valid in every lane of the group.
+// aligned (lanes 8g..8g+7), all 64 lanes active.  Returns this lane's four
+// codes packed; *d and *s (block scale, block code sum) are valid in every
+// lane of the group.
 __device__ __forceinline__ uint32_t quant_q8_0_lane(const float v[4], float * d, int * s) {
-    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    for (int o = 1; o < 8; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    const float amax = max8(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
     const _Float16 dh = (_Float16)(amax / 127.f);
     const float mul = amax != 0.0f ? 127.f / amax : 0.0f;
     int q[4], sum = 0;
@@ -86,33 +140,30 @@ __device__ __forceinline__ uint32_t quant_q8_0_lane(const float v[4], float * d,
         q[i] = (int)r;
         sum += q[i];
     }
-    for (int o = 1; o < 8; o <<= 1) sum += __shfl_xor(sum, o, 64);
     *d = (float)dh;
-    *s = sum;
+    *s = sum8(sum);
     return (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) | ((uint32_t)(q[2] & 0xff) << 16) |
            ((uint32_t)(q[3] & 0xff) << 24);
 }
 
-// q8_K over a whole wave (4 values per lane, lane-major) of one 256-weight
-// super-block.  Returns this lane's codes; *d is the block scale (all lanes),
-// *bsum the sum of lanes 4b..4b+3's codes (valid in every lane of the quad).
+// q8_K over a whole wave (4 values per lane, element 4 * lane + i) of one
+// 256-weight super-block, all 64 lanes active.  mx is the first element of
+// largest |x|: the wave max of |x|, then the lowest lane holding it (ballot)
+// and that lane's first such element.  Returns this lane's codes; *d is the
+// block scale (all lanes), *bsum the sum of lanes 4b..4b+3's codes (valid in
+// every lane of the quad).
 __device__ __forceinline__ uint32_t quant_q8_K_wave(const float v[4], int lane, float * d, int * bsum) {
-    float ba = -1.0f;
-    int bi = 0;
-    for (int i = 0; i < 4; ++i) {
-        const float av = fabsf(v[i]);
-        if (av > ba) { ba = av; bi = 4 * lane + i; }
-    }
-    for (int o = 32; o > 0; o >>= 1) {
-        const float oa = __shfl_xor(ba, o, 64);
-        const int oi = __shfl_xor(bi, o, 64);
-        if (oa > ba || (oa == ba && oi < bi)) { ba = oa; bi = oi; }
-    }
-    const float pick = (bi & 3) == 0 ? v[0] : (bi & 3) == 1 ? v[1] : (bi & 3) == 2 ? v[2] : v[3];
-    const float mx = __shfl(pick, bi >> 2, 64);
+    (void)lane;
+    const float a0 = fabsf(v[0]), a1 = fabsf(v[1]), a2 = fabsf(v[2]), a3 = fabsf(v[3]);
+    const float amax = wave_max(fmaxf(fmaxf(a0, a1), fmaxf(a2, a3)));
+    const float first = a0 == amax ? v[0] : a1 == amax ? v[1] : a2 == amax ? v[2] : v[3];
+    const bool hit = a0 == amax || a1 == amax || a2 == amax || a3 == amax;
+    const uint64_t mask = __ballot(hit);
+    const int src = mask ? __builtin_ctzll(mask) : 0;
+    const float mx = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, first), src));
     int q[4] = { 0, 0, 0, 0 };
     float dv = 0.0f;
-    if (ba != 0.0f) {
+    if (amax != 0.0f) {
         const float iscale = -127.f / mx;
         for (int i = 0; i < 4; ++i) {
             const int r = (int)__builtin_rintf(iscale * v[i]);
@@ -120,21 +171,20 @@ __device__ __forceinline__ uint32_t quant_q8_K_wave(const float v[4], int lane, 
         }
         dv = 1.0f / iscale;
     }
-    int s = q[0] + q[1] + q[2] + q[3];
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
     *d = dv;
-    *bsum = s;
+    *bsum = sum4(q[0] + q[1] + q[2] + q[3]);
     return (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) | ((uint32_t)(q[2] & 0xff) << 16) |
            ((uint32_t)(q[3] & 0xff) << 24);
 }
 
 #pragma clang fp contract(fast)
 
-// f32 column c of an activation tensor (columns (i1, i2, i3), i1 fastest)
+// f32 column c of an activation tensor (columns (i1, i2, i3), i1 fastest);
+// column counts fit 32 bits, so the index split uses 32-bit divisions
 __device__ __forceinline__ const float * f32_col(const F32Cols & s, int64_t c) {
-    const int64_t i1 = c % s.ne1, r = c / s.ne1, i2 = r % s.ne2, i3 = r / s.ne2;
-    return reinterpret_cast<const float *>(s.base + i1 * s.nb1 + i2 * s.nb2 + i3 * s.nb3);
+    const uint32_t cc = (uint32_t)c, n1 = (uint32_t)s.ne1, n2 = (uint32_t)s.ne2;
+    const uint32_t r = cc / n1, i1 = cc - r * n1, i3 = r / n2, i2 = r - i3 * n2;
+    return reinterpret_cast<const float *>(s.base + (size_t)i1 * s.nb1 + (size_t)i2 * s.nb2 + (size_t)i3 * s.nb3);
 }
 
 }  // namespace qmm

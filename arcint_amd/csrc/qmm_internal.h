@@ -21,7 +21,7 @@ namespace qmm {
 // 128-bit loads:
 //   Q4_0   qs[16] | d[2]
 //   Q8_0   qs[32] | d[2]
-//   Q4_K   the 144-byte block itself (already 16-byte aligned)
+//   Q4_K   qs[128] | {d, dmin, scales[12]}[16]
 //   Q6_K   ql[128] | qh[64] | scales[16] | d[2]
 //   IQ4_XS qs[128] | {d, scales_h, scales_l[4]}[8]
 // ---------------------------------------------------------------------------
