@@ -16,7 +16,7 @@ namespace {
 #pragma clang fp contract(off)
 
 // 8 lanes per 32-weight block, 4 weights per lane
-__global__ void k_quant_q8_0(F32Cols src, int64_t K, int64_t ncols, ActBuf a, int want_h) {
+__global__ void k_quant_q8_0(F32Cols src, int64_t K, int64_t ncols, ActBuf a) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t kq = K / 4;
     const bool live = t < ncols * kq;              // groups of 8 lanes are all live or all dead
@@ -32,18 +32,16 @@ __global__ void k_quant_q8_0(F32Cols src, int64_t K, int64_t ncols, ActBuf a, in
     if (!live) return;
     const int64_t base = c * K + k;
     *reinterpret_cast<uint32_t *>(a.codes + base) = packed;
-    if (want_h) {
-        for (int i = 0; i < 4; ++i) a.hcodes[base + i] = (_Float16)(int8_t)(packed >> (8 * i));
-    }
     if ((t & 7) == 0) {
         const int64_t b = c * (K / 32) + k / 32;
         a.d[b] = d;
         a.sums[b] = (int16_t)s;
+        if (a.dT) a.dT[(k / 32) * a.ldT + c] = d;
     }
 }
 
 // one wave per 256-weight super-block, 4 weights per lane
-__global__ void k_quant_q8_K(F32Cols src, int64_t K, int64_t ncols, ActBuf a, int want_h) {
+__global__ void k_quant_q8_K(F32Cols src, int64_t K, int64_t ncols, ActBuf a) {
     const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
     const int lane = threadIdx.x & 63;
     const int64_t nsb = K / 256;
@@ -57,11 +55,11 @@ __global__ void k_quant_q8_K(F32Cols src, int64_t K, int64_t ncols, ActBuf a, in
     const uint32_t packed = quant_q8_K_wave(v, lane, &d, &s);
     const int64_t base = c * K + sb * 256 + 4 * lane;
     *reinterpret_cast<uint32_t *>(a.codes + base) = packed;
-    if (want_h) {
-        for (int i = 0; i < 4; ++i) a.hcodes[base + i] = (_Float16)(int8_t)(packed >> (8 * i));
-    }
     if ((lane & 3) == 0) a.sums[c * (K / 16) + sb * 16 + (lane >> 2)] = (int16_t)s;
-    if (lane == 0) a.d[c * nsb + sb] = d;
+    if (lane == 0) {
+        a.d[c * nsb + sb] = d;
+        if (a.dT) a.dT[sb * a.ldT + c] = d;
+    }
 }
 
 // ActBuf -> ggml block bytes, one thread per block
@@ -92,15 +90,15 @@ __global__ void k_act_blocks(ActBuf a, uint8_t * __restrict__ out) {
 
 }  // namespace
 
-hipError_t launch_quantize(const F32Cols & src, int64_t K, int64_t ncols, const ActBuf & a, bool want_h, hipStream_t s) {
+hipError_t launch_quantize(const F32Cols & src, int64_t K, int64_t ncols, const ActBuf & a, hipStream_t s) {
     if (ncols <= 0 || K <= 0) return hipSuccess;
     const int tpb = 256;
     if (a.vdt == QMM_TYPE_Q8_0) {
         const int64_t n = ncols * (K / 4);
-        k_quant_q8_0<<<dim3((unsigned)((n + tpb - 1) / tpb)), tpb, 0, s>>>(src, K, ncols, a, want_h ? 1 : 0);
+        k_quant_q8_0<<<dim3((unsigned)((n + tpb - 1) / tpb)), tpb, 0, s>>>(src, K, ncols, a);
     } else {
         const int64_t n = ncols * (K / 256) * 64;
-        k_quant_q8_K<<<dim3((unsigned)((n + tpb - 1) / tpb)), tpb, 0, s>>>(src, K, ncols, a, want_h ? 1 : 0);
+        k_quant_q8_K<<<dim3((unsigned)((n + tpb - 1) / tpb)), tpb, 0, s>>>(src, K, ncols, a);
     }
     return hipGetLastError();
 }

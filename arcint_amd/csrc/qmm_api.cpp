@@ -37,7 +37,7 @@ struct qmm_ctx {
         int64_t ne[4] = { 0, 0, 0, 0 };
         size_t nb[4] = { 0, 0, 0, 0 };
         int vdt = 0;
-        bool hcodes = false;
+        bool dT = false;
         uint64_t gen = 0;
         bool valid = false;
     } key;
@@ -121,15 +121,16 @@ WView weight_view(const qmm_tensor * t, int64_t rows_per_mat) {
     return w;
 }
 
-// activation scratch layout for ncols columns of K
-size_t act_bytes(int vdt, int64_t K, int64_t ncols, bool hcodes, size_t * o_h, size_t * o_d, size_t * o_s) {
+// activation scratch layout for ncols columns of K: codes, scales, sums and
+// (GEMM consumers) the scales again block-major with a row stride of ldT
+size_t act_bytes(int vdt, int64_t K, int64_t ncols, bool dT, int64_t ldT, size_t * o_d, size_t * o_s, size_t * o_t) {
     size_t off = align_up((size_t)(K * ncols), kPlaneAlign);
-    *o_h = off;
-    if (hcodes) off = align_up(off + (size_t)(K * ncols) * 2, kPlaneAlign);
     *o_d = off;
     off = align_up(off + (size_t)(ncols * (K / act_block(vdt))) * 4, kPlaneAlign);
     *o_s = off;
     off = align_up(off + (size_t)(ncols * (K / act_sum_block(vdt))) * 2, kPlaneAlign);
+    *o_t = off;
+    if (dT) off = align_up(off + (size_t)((K / act_block(vdt)) * ldT) * 4, kPlaneAlign);
     return off;
 }
 
@@ -161,36 +162,38 @@ F32Cols f32_cols(const qmm_tensor * t) {
 
 // Quantize src1 (all its columns) with the vec_dot type of `type`, reusing
 // the previous result inside one graph when src1 is the same tensor.
-int quantize_src1(qmm_ctx * ctx, int type, const qmm_tensor * src1, bool hcodes, ActBuf * out) {
+int quantize_src1(qmm_ctx * ctx, int type, const qmm_tensor * src1, bool dT, ActBuf * out) {
     const int vdt = vec_dot_type(type);
     const int64_t K = src1->ne[0], ncols = src1->ne[1] * src1->ne[2] * src1->ne[3];
     auto & k = ctx->key;
     if (ctx->in_graph && k.valid && k.gen == ctx->graph_gen && k.buf == src1->buffer && k.offs == src1->offs &&
-        k.vdt == vdt && (k.hcodes || !hcodes) && !memcmp(k.ne, src1->ne, sizeof(k.ne)) &&
+        k.vdt == vdt && (k.dT || !dT) && !memcmp(k.ne, src1->ne, sizeof(k.ne)) &&
         !memcmp(k.nb, src1->nb, sizeof(k.nb))) {
         *out = ctx->cached;
         return QMM_OK;
     }
-    size_t oh, od, os;
-    const size_t need = act_bytes(vdt, K, ncols, hcodes, &oh, &od, &os);
+    size_t od, os, ot;
+    const int64_t ldT = (ncols + 3) / 4 * 4 + 64;    // the GEMM reads up to 63 columns past the last
+    const size_t need = act_bytes(vdt, K, ncols, dT, ldT, &od, &os, &ot);
     int rc = ensure(ctx, &ctx->act, &ctx->act_cap, need);
     if (rc) return rc;
     uint8_t * b = (uint8_t *)ctx->act;
     ActBuf a;
     a.codes = (int8_t *)b;
-    a.hcodes = hcodes ? (_Float16 *)(b + oh) : nullptr;
     a.d = (float *)(b + od);
     a.sums = (int16_t *)(b + os);
+    a.dT = dT ? (float *)(b + ot) : nullptr;
+    a.ldT = ldT;
     a.K = K;
     a.ncols = ncols;
     a.vdt = vdt;
-    QMM_HIP(ctx, launch_quantize(f32_cols(src1), K, ncols, a, hcodes, ctx->stream));
+    QMM_HIP(ctx, launch_quantize(f32_cols(src1), K, ncols, a, ctx->stream));
     k.buf = src1->buffer;
     k.offs = src1->offs;
     memcpy(k.ne, src1->ne, sizeof(k.ne));
     memcpy(k.nb, src1->nb, sizeof(k.nb));
     k.vdt = vdt;
-    k.hcodes = hcodes;
+    k.dT = dT;
     k.gen = ctx->graph_gen;
     k.valid = true;
     ctx->cached = a;
@@ -421,6 +424,7 @@ static bool mul_mat_ok(const qmm_tensor * s0, const qmm_tensor * s1, const qmm_t
     if (!L) return why(reason, len, "src0 type is not Q4_0/Q8_0/Q4_K/Q6_K/IQ4_XS");
     if (s0->ne[0] % L->blck) return why(reason, len, "ne00 is not a multiple of the block size");
     if (!contiguous(s0)) return why(reason, len, "src0 is not contiguous");
+    if (s0->offs % kPlaneAlign) return why(reason, len, "src0 offset is not a multiple of 256");
     if (!check_f32(s1) || !check_f32(d)) return why(reason, len, "src1/dst must be f32 with nb[0] == 4");
     if (s1->ne[0] != s0->ne[0]) return why(reason, len, "src1 ne0 != src0 ne0");
     if (s1->ne[0] % 256 && vec_dot_type(s0->type) == QMM_TYPE_Q8_K) return why(reason, len, "K is not a multiple of 256");
@@ -440,6 +444,7 @@ static bool mul_mat_id_ok(const qmm_tensor * s0, const qmm_tensor * s1, const qm
     const TypeLayout * L = type_layout(s0->type);
     if (!L) return why(reason, len, "src0 type is not Q4_0/Q8_0/Q4_K/Q6_K/IQ4_XS");
     if (s0->ne[0] % L->blck || !contiguous(s0)) return why(reason, len, "src0 must be contiguous whole blocks");
+    if (s0->offs % kPlaneAlign) return why(reason, len, "src0 offset is not a multiple of 256");
     if (s0->ne[3] != 1) return why(reason, len, "src0 must be [K, M, n_as]");
     if (!check_f32(s1) || !check_f32(d)) return why(reason, len, "src1/dst must be f32 with nb[0] == 4");
     if (ids->type != QMM_TYPE_I32 || ids->nb[0] != 4) return why(reason, len, "ids must be i32");
@@ -465,11 +470,12 @@ int qmm_supports_op(qmm_ctx *, int32_t op, const qmm_tensor * src0, const qmm_te
 
 // ---- ops ---------------------------------------------------------------------
 
-// columns at or above which a 2-D batch goes to the MFMA GEMM
+// columns at or above which MUL_MAT goes to the MFMA GEMM (below: the GEMV,
+// one weight pass per 8 columns)
 static int64_t gemm_min_cols() {
     static int64_t v = [] {
         const char * e = getenv("QMM_GEMM_MIN_COLS");
-        return e ? std::max<int64_t>(1, atoll(e)) : (int64_t)1 << 40;
+        return e ? std::max<int64_t>(1, atoll(e)) : (int64_t)16;
     }();
     return v;
 }
@@ -500,6 +506,20 @@ int qmm_mul_mat(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1,
     dn.d_nb1 = (int64_t)(dst->nb[1] / 4);
     dn.d_nb2 = (int64_t)(dst->nb[2] / 4);
     dn.d_nb3 = (int64_t)(dst->nb[3] / 4);
+    if (use_gemm) {
+        GemmBatch bt;
+        bt.ne12 = dn.ne12;
+        bt.r2 = dn.r2;
+        bt.r3 = dn.r3;
+        bt.ne02 = dn.ne02;
+        bt.d_nb1 = dn.d_nb1;
+        bt.d_nb2 = dn.d_nb2;
+        bt.d_nb3 = dn.d_nb3;
+        ctx->path = "gemm-mfma";
+        if ((rc = ktime_mark(ctx, true))) return rc;
+        QMM_HIP(ctx, launch_gemm(src0->type, w, M, K, a, N, dn.ne12 * dn.ne13, bt, d, ctx->stream));
+        return ktime_mark(ctx, false);
+    }
     const int nc = (int)std::min<int64_t>(N, kMaxTaskCols);
     ctx->path = fused ? "gemv-fused" : "gemv-tasks";
     if (N > kMaxTaskCols) note_downgrade(ctx, "mul_mat: many columns on the GEMV");

@@ -45,7 +45,7 @@ static inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; 
 // ---------------------------------------------------------------------------
 // Quantized activations (the vec_dot type's from_float, done on the device).
 // For column c of ncols:
-//   codes  int8 [c][K]          (or fp16 codes [c][K] for the MFMA GEMM)
+//   codes  int8 [c][K]
 //   d      f32  [c][K/bs]       bs = 32 (q8_0) or 256 (q8_K); q8_0's d is
 //                               the fp16-rounded scale widened to f32
 //   sums   i16  [c][K/ss]       ss = 32 (q8_0: sum of the block's codes)
@@ -53,9 +53,10 @@ static inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; 
 // ---------------------------------------------------------------------------
 struct ActBuf {
     int8_t *   codes;
-    _Float16 * hcodes;     // non-null when fp16 codes were produced
     float *    d;
     int16_t *  sums;
+    float *    dT;         // non-null: the scales again, block-major: dT[b * ldT + c]
+    int64_t    ldT;        // >= ncols + 64 (the GEMM reads whole 64-column tiles)
     int64_t    K;
     int64_t    ncols;
     int        vdt;        // QMM_TYPE_Q8_0 or QMM_TYPE_Q8_K
@@ -96,7 +97,7 @@ struct GemvTask {
 // Launchers (defined in the .hip files); all enqueue on `s`.
 // ---------------------------------------------------------------------------
 hipError_t launch_dequant(int type, const WView & w, int64_t nblk, float * y, hipStream_t s);
-hipError_t launch_quantize(const F32Cols & src, int64_t K, int64_t ncols, const ActBuf & a, bool want_hcodes, hipStream_t s);
+hipError_t launch_quantize(const F32Cols & src, int64_t K, int64_t ncols, const ActBuf & a, hipStream_t s);
 // writes ggml block bytes (block_q8_0 / block_q8_K) of an ActBuf into `out` (device)
 hipError_t launch_act_to_blocks(const ActBuf & a, void * out, hipStream_t s);
 
@@ -116,10 +117,15 @@ hipError_t launch_gemv_any(int type, const WView & w, int64_t M, int64_t K, cons
                            const GemvTask * tasks, int ntasks_max, const int32_t * ntasks_dev, int nc,
                            const GemvDense * dense, float * dst, hipStream_t s);
 
-// dense GEMM: dst[n * ldd + m] = W(mat) * x(n) for n < N, m < M; activations
-// columns col0..col0+N-1 of `a` (fp16 codes)
-hipError_t launch_gemm(int type, const WView & w, int64_t mat, int64_t M, int64_t K, const ActBuf & a,
-                       int64_t col0, int64_t N, float * dst, int64_t ldd, hipStream_t s);
+// Prefill GEMM (int8 MFMA): for every batch b < nbatch, dst[doff(b) + n * d_nb1
+// + m] = W(mat(b)) row m . activation column col0(b) + n, for n < N, m < M.
+// Activations come from the pre-pass with block-major scales (a.dT).
+struct GemmBatch {
+    int64_t ne12, r2, r3, ne02;    // batch b = (i2, i3): mat = i2 / r2 + (i3 / r3) * ne02
+    int64_t d_nb1, d_nb2, d_nb3;   // dst strides in floats
+};
+hipError_t launch_gemm(int type, const WView & w, int64_t M, int64_t K, const ActBuf & a, int64_t N, int64_t nbatch,
+                       const GemmBatch & bt, float * dst, hipStream_t s);
 
 // MoE routing: builds GEMV tasks (one per expert and up to 8 pairs) from ids.
 struct RouteArgs {

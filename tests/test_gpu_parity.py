@@ -294,3 +294,54 @@ def test_full_size_gemv(be, sc, orc, qtype, M, K, N):
     say("full", qtype, M, K, N)
     got, ref = run_mul_mat(be, sc, orc, qtype, M, K, N, seed=91)
     assert rel_err(got, ref) <= TOL
+
+
+# ------------------------------------------------------------------ MFMA GEMM (N >= 16)
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("M,K,N", [(300, 1024, 16), (129, 2048, 37), (64, 512, 64), (500, 768, 130)])
+def test_mul_mat_gemm(be, sc, orc, qtype, M, K, N):
+    if K % 256 and qtype not in (qmm.Q4_0, qmm.Q8_0):
+        K = 1024
+    say("gemm", qtype, M, K, N)
+    got, ref = run_mul_mat(be, sc, orc, qtype, M, K, N, seed=57)
+    assert be.last_path() == "gemm-mfma"
+    assert rel_err(got, ref) <= TOL
+
+
+def test_mul_mat_gemm_broadcast_and_strides(be, sc, orc):
+    say("gemm-broadcast")
+    qtype, K, M, N = qmm.Q6_K, 512, 80, 21
+    raw = synth.weights(qtype, 2 * M, K, seed=64)
+    w = sc.weights(qtype, raw, (K, M, 2))
+    x = synth.activations(4 * N, K, seed=65).reshape(4, N, K)
+    y = sc.empty_f32((M, N, 4))
+    be.mul_mat(w, sc.f32(x), y)
+    be.synchronize()
+    assert be.last_path() == "gemm-mfma"
+    got = be.get_f32(y).reshape(4, N, M)
+    rb = synth.row_bytes(qtype, K) * M
+    for i2 in range(4):
+        ref = orc.mul_mat(qtype, raw[(i2 // 2) * rb:(i2 // 2 + 1) * rb], M, K, x[i2])
+        assert rel_err(got[i2], ref) <= TOL
+    ypad = sc.empty_f32((M + 3, N))
+    yview = qmm.Tensor(ypad.buf, qmm.F32, (M, N), nb=(4, 4 * (M + 3), 4 * (M + 3) * N, 4 * (M + 3) * N))
+    w2 = sc.weights(qtype, raw[:rb], (K, M))
+    be.mul_mat(w2, sc.f32(x[1]), yview)
+    be.synchronize()
+    got = be.get_f32(ypad).reshape(N, M + 3)[:, :M]
+    assert rel_err(got, orc.mul_mat(qtype, raw[:rb], M, K, x[1])) <= TOL
+
+
+GEMM_FULL = [
+    (qmm.Q4_0, 4096, 4096, 512), (qmm.Q4_0, 11008, 4096, 64), (qmm.Q4_0, 4096, 11008, 64),
+    (qmm.Q4_K, 17408, 5120, 64), (qmm.Q6_K, 5120, 17408, 64), (qmm.IQ4_XS, 4096, 14336, 32),
+    (qmm.Q8_0, 14336, 4096, 32),
+]
+
+
+@pytest.mark.parametrize("qtype,M,K,N", GEMM_FULL)
+def test_full_size_gemm(be, sc, orc, qtype, M, K, N):
+    say("gemm-full", qtype, M, K, N)
+    got, ref = run_mul_mat(be, sc, orc, qtype, M, K, N, seed=93)
+    assert be.last_path() == "gemm-mfma"
+    assert rel_err(got, ref) <= TOL
