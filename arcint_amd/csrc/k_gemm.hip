@@ -28,6 +28,8 @@
 // r < 4, of column l % 16.
 #include "qmm_device.h"
 
+#include <hip/hip_ext.h>
+
 #include <algorithm>
 #include <cstdlib>
 
@@ -40,8 +42,9 @@ constexpr int kThreads = 256;
 
 struct GemmParams {
     WView w;
-    int64_t M, K, N;
-    const int8_t * codes;   // activation codes [ncols][K]
+    int64_t M, K, N;    // M, K repeat w.M, w.K
+    const int8_t * codes;   // activation codes [ncols][ldk]
+    int64_t ldk;
     const float * dT;       // activation scales [K / BS][ldT]
     int64_t ldT;
     int64_t ntiles, tiles_n, chunk;
@@ -59,10 +62,11 @@ template <int TYPE> struct GW;
 template <> struct GW<QMM_TYPE_Q4_0> {
     static constexpr int BS = 32;
     struct R { uint2 q; uint32_t d; };
-    __device__ static void load(R & r, const WView & w, int64_t blk0, int kg, int g) {
-        const int64_t b = blk0 + kg;
-        r.q = *reinterpret_cast<const uint2 *>(w.p[0] + b * 16 + 8 * (g & 1));
-        r.d = reinterpret_cast<const uint16_t *>(w.p[1])[b];
+    __device__ static void load(R & r, const uint8_t * tb, int rr, size_t tgs, int kg, int g) {
+        const uint8_t * t = tb + (size_t)(kg >> 3) * tgs + rr * 16;
+        const int p = kg & 7;
+        r.q = *reinterpret_cast<const uint2 *>(t + p * kChunk + 8 * (g & 1));
+        r.d = *reinterpret_cast<const uint16_t *>(t + 8 * kChunk + 2 * p);
     }
     __device__ static long bop(const R & r, int g) {
         const int sh = 4 * (g >> 1);
@@ -76,10 +80,11 @@ template <> struct GW<QMM_TYPE_Q4_0> {
 template <> struct GW<QMM_TYPE_Q8_0> {
     static constexpr int BS = 32;
     struct R { uint2 q; uint32_t d; };
-    __device__ static void load(R & r, const WView & w, int64_t blk0, int kg, int g) {
-        const int64_t b = blk0 + kg;
-        r.q = *reinterpret_cast<const uint2 *>(w.p[0] + b * 32 + 8 * g);
-        r.d = reinterpret_cast<const uint16_t *>(w.p[1])[b];
+    __device__ static void load(R & r, const uint8_t * tb, int rr, size_t tgs, int kg, int g) {
+        const uint8_t * t = tb + (size_t)(kg >> 3) * tgs + rr * 16;
+        const int p = kg & 7;
+        r.q = *reinterpret_cast<const uint2 *>(t + (2 * p + (g >> 1)) * kChunk + 8 * (g & 1));
+        r.d = *reinterpret_cast<const uint16_t *>(t + 16 * kChunk + 2 * p);
     }
     __device__ static long bop(const R & r, int) { return (long)(((uint64_t)r.q.y << 32) | r.q.x); }
 };
@@ -89,11 +94,11 @@ template <> struct GW<QMM_TYPE_Q8_0> {
 template <> struct GW<QMM_TYPE_Q4_K> {
     static constexpr int BS = 256;
     struct R { uint2 q; uint4 h; };
-    __device__ static void load(R & r, const WView & w, int64_t blk0, int kg, int g) {
-        const int64_t sb = blk0 + (kg >> 3);
+    __device__ static void load(R & r, const uint8_t * tb, int rr, size_t tgs, int kg, int g) {
+        const uint8_t * t = tb + (size_t)(kg >> 3) * tgs + rr * 16;
         const int j = kg & 7;
-        r.q = *reinterpret_cast<const uint2 *>(w.p[0] + sb * 128 + 32 * (j >> 1) + 8 * g);
-        r.h = *reinterpret_cast<const uint4 *>(w.p[1] + sb * 16);
+        r.q = *reinterpret_cast<const uint2 *>(t + (2 * (j >> 1) + (g >> 1)) * kChunk + 8 * (g & 1));
+        r.h = *reinterpret_cast<const uint4 *>(t + 8 * kChunk);
     }
     __device__ static long bop(const R & r, int kg) {
         const int sh = 4 * (kg & 1);
@@ -118,11 +123,11 @@ template <> struct GW<QMM_TYPE_Q4_K> {
 template <> struct GW<QMM_TYPE_IQ4_XS> {
     static constexpr int BS = 256;
     struct R { uint2 q; uint2 h; };
-    __device__ static void load(R & r, const WView & w, int64_t blk0, int kg, int g) {
-        const int64_t sb = blk0 + (kg >> 3);
+    __device__ static void load(R & r, const uint8_t * tb, int rr, size_t tgs, int kg, int g) {
+        const uint8_t * t = tb + (size_t)(kg >> 3) * tgs;
         const int ib = kg & 7;
-        r.q = *reinterpret_cast<const uint2 *>(w.p[0] + sb * 128 + 16 * ib + 8 * (g & 1));
-        r.h = *reinterpret_cast<const uint2 *>(w.p[1] + sb * 8);
+        r.q = *reinterpret_cast<const uint2 *>(t + ib * kChunk + rr * 16 + 8 * (g & 1));
+        r.h = *reinterpret_cast<const uint2 *>(t + 8 * kChunk + rr * 8);
     }
     __device__ static long bop(const R & r, int g) {
         const int sh = 4 * (g >> 1);
@@ -140,13 +145,14 @@ template <> struct GW<QMM_TYPE_IQ4_XS> {
 template <> struct GW<QMM_TYPE_Q6_K> {
     static constexpr int BS = 256;
     struct R { uint2 ql, qh; uint4 sc; uint32_t d; };
-    __device__ static void load(R & r, const WView & w, int64_t blk0, int kg, int g) {
-        const int64_t sb = blk0 + (kg >> 3);
+    __device__ static void load(R & r, const uint8_t * tb, int rr, size_t tgs, int kg, int g) {
+        const uint8_t * t = tb + (size_t)(kg >> 3) * tgs;
         const int qi = kg & 7, n = qi >> 2, gq = qi & 3;
-        r.ql = *reinterpret_cast<const uint2 *>(w.p[0] + sb * 128 + 64 * n + 32 * (gq & 1) + 8 * g);
-        r.qh = *reinterpret_cast<const uint2 *>(w.p[1] + sb * 64 + 32 * n + 8 * g);
-        r.sc = *reinterpret_cast<const uint4 *>(w.p[2] + sb * 16);
-        r.d = reinterpret_cast<const uint16_t *>(w.p[3])[sb];
+        const uint8_t * tr = t + rr * 16;
+        r.ql = *reinterpret_cast<const uint2 *>(tr + (4 * n + 2 * (gq & 1) + (g >> 1)) * kChunk + 8 * (g & 1));
+        r.qh = *reinterpret_cast<const uint2 *>(tr + (8 + 2 * n + (g >> 1)) * kChunk + 8 * (g & 1));
+        r.sc = *reinterpret_cast<const uint4 *>(tr + 12 * kChunk);
+        r.d = *reinterpret_cast<const uint16_t *>(t + 13 * kChunk + rr * 2);
     }
     __device__ static long bop(const R & r, int kg) {
         const int gq = kg & 3, shl = 4 * (gq >> 1), shh = 2 * gq;
@@ -186,15 +192,18 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmParams p) {
 #pragma unroll
     for (int t = 0; t < GT; ++t) {
         const int64_t n = n0 + 16 * t + c16;
-        arow[t] = p.codes + (col0 + (n < N ? n : N - 1)) * K + 8 * g;
+        arow[t] = p.codes + (col0 + (n < N ? n : N - 1)) * p.ldk + 8 * g;
         dq[t] = col0 + n0 + 16 * t + 4 * g;               // < ncols + 61 <= ldT - 3 (64 columns of padding)
     }
-    int64_t wblk[GR];                                      // B operand: weight rows
+    const uint8_t * wtb[GR];                               // B operand: weight rows (tile base, row in tile)
+    int wrr[GR];
 #pragma unroll
     for (int s = 0; s < GR; ++s) {
-        const int64_t m = m0 + 16 * s + c16;
-        wblk[s] = (mat * M + (m < M ? m : M - 1)) * p.w.bpr;
+        const int64_t m0c = m0 + 16 * s + c16, m = m0c < M ? m0c : M - 1;
+        wtb[s] = tile_group(p.w, mat, m / kTileRows, 0);
+        wrr[s] = (int)(m % kTileRows);
     }
+    const size_t tgs = (size_t)p.w.tg;
 
     const int nk = (int)(K / 32);
     float out[GT][GR][4];
@@ -217,7 +226,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmParams p) {
 #pragma unroll
         for (int t = 0; t < GT; ++t) A[t] = *reinterpret_cast<const long *>(arow[t] + (int64_t)kg * 32);
 #pragma unroll
-        for (int s = 0; s < GR; ++s) T::load(W[s], p.w, wblk[s], kg, g);
+        for (int s = 0; s < GR; ++s) T::load(W[s], wtb[s], wrr[s], tgs, kg, g);
         const int64_t kb = (int64_t)kg * 32 / T::BS;
 #pragma unroll
         for (int t = 0; t < GT; ++t) {                     // 4 dwords: col0 need not be a multiple of 4
@@ -355,22 +364,25 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmParams p) {
 }
 
 template <int TYPE, int GT, int GR>
-hipError_t launch_t(GemmParams p, int64_t nbatch, hipStream_t s) {
+hipError_t launch_t(GemmParams p, int64_t nbatch, hipStream_t s, const KTime * kt) {
     const int64_t tiles_m = (p.M + 32 * GR - 1) / (32 * GR);
     p.tiles_n = (p.N + 32 * GT - 1) / (32 * GT);
     p.ntiles = tiles_m * p.tiles_n;
     p.chunk = (p.ntiles + 7) / 8;
     const int64_t grid = p.chunk * 8;
     if (grid > 0x7fffffff || nbatch > 65535) return hipErrorInvalidValue;
-    k_gemm<TYPE, GT, GR><<<dim3((unsigned)grid, (unsigned)nbatch), kThreads, 0, s>>>(p);
+    const dim3 g((unsigned)grid, (unsigned)nbatch);
+    if (kt) hipExtLaunchKernelGGL(k_gemm<TYPE, GT, GR>, g, dim3(kThreads), 0u, s, kt->start, kt->stop, 0, p);
+    else k_gemm<TYPE, GT, GR><<<g, kThreads, 0, s>>>(p);
     return hipGetLastError();
 }
 
 }  // namespace
 
-hipError_t launch_gemm(int type, const WView & w, int64_t M, int64_t K, const ActBuf & a, int64_t N, int64_t nbatch,
-                       const GemmBatch & bt, float * dst, hipStream_t s) {
-    if (!a.dT || a.ldT < N * nbatch + 64 || K % 32 || M <= 0 || N <= 0 || nbatch <= 0)
+hipError_t launch_gemm(int type, const WView & w, const ActBuf & a, int64_t N, int64_t nbatch,
+                       const GemmBatch & bt, float * dst, hipStream_t s, const KTime * kt) {
+    const int64_t M = w.M, K = w.K;
+    if (!a.dT || a.ldT < N * nbatch + 64 || K % 32 || M <= 0 || N <= 0 || nbatch <= 0 || a.K != K)
         return hipErrorInvalidValue;
     const bool kq = type == QMM_TYPE_Q4_K || type == QMM_TYPE_Q6_K || type == QMM_TYPE_IQ4_XS;
     if (kq && K % 256) return hipErrorInvalidValue;
@@ -380,16 +392,17 @@ hipError_t launch_gemm(int type, const WView & w, int64_t M, int64_t K, const Ac
     p.K = K;
     p.N = N;
     p.codes = a.codes;
+    p.ldk = a.ldk;
     p.dT = a.dT;
     p.ldT = a.ldT;
     p.bt = bt;
     p.dst = dst;
     switch (type) {
-        case QMM_TYPE_Q4_0:   return launch_t<QMM_TYPE_Q4_0, 2, 2>(p, nbatch, s);
-        case QMM_TYPE_Q8_0:   return launch_t<QMM_TYPE_Q8_0, 2, 2>(p, nbatch, s);
-        case QMM_TYPE_Q4_K:   return launch_t<QMM_TYPE_Q4_K, 2, 2>(p, nbatch, s);
-        case QMM_TYPE_Q6_K:   return launch_t<QMM_TYPE_Q6_K, 2, 2>(p, nbatch, s);
-        case QMM_TYPE_IQ4_XS: return launch_t<QMM_TYPE_IQ4_XS, 2, 2>(p, nbatch, s);
+        case QMM_TYPE_Q4_0:   return launch_t<QMM_TYPE_Q4_0, 2, 2>(p, nbatch, s, kt);
+        case QMM_TYPE_Q8_0:   return launch_t<QMM_TYPE_Q8_0, 2, 2>(p, nbatch, s, kt);
+        case QMM_TYPE_Q4_K:   return launch_t<QMM_TYPE_Q4_K, 2, 2>(p, nbatch, s, kt);
+        case QMM_TYPE_Q6_K:   return launch_t<QMM_TYPE_Q6_K, 2, 2>(p, nbatch, s, kt);
+        case QMM_TYPE_IQ4_XS: return launch_t<QMM_TYPE_IQ4_XS, 2, 2>(p, nbatch, s, kt);
         default: return hipErrorInvalidValue;
     }
 }

@@ -8,6 +8,10 @@
 //         bsums = sums of 16 codes; an all-zero block stays zero.
 // Divisions are IEEE (hipcc's default correctly-rounded f32 divide) and no
 // multiply is contracted, so every code and scale equals the CPU's.
+// Columns are written with a stride of ldk (K rounded up to 256); the padding
+// past K quantizes zeros.  The same launch can zero dst columns for a GEMV
+// that adds its K slices with atomics (work-groups past the quantization
+// ones do that).
 #include "qmm_device.h"
 
 namespace qmm {
@@ -15,14 +19,28 @@ namespace {
 
 #pragma clang fp contract(off)
 
+constexpr int kTpb = 256;
+
+__device__ void zero_cols(const ZeroJob & z, int64_t t) {
+    const int64_t n = z.M * z.ncols;
+    if (t >= n) return;
+    const int64_t c = t / z.M, m = t - c * z.M;
+    const int64_t r = c / z.ne1, i1 = c - r * z.ne1, i3 = r / z.ne2, i2 = r - i3 * z.ne2;
+    z.dst[i1 * z.nb1 + i2 * z.nb2 + i3 * z.nb3 + m] = 0.0f;
+}
+
 // 8 lanes per 32-weight block, 4 weights per lane
-__global__ void k_quant_q8_0(F32Cols src, int64_t K, int64_t ncols, ActBuf a) {
+__global__ void k_quant_q8_0(F32Cols src, int64_t K, int64_t ncols, ActBuf a, ZeroJob z, int64_t nqblk) {
+    if ((int64_t)blockIdx.x >= nqblk) {
+        zero_cols(z, ((int64_t)blockIdx.x - nqblk) * kTpb + threadIdx.x);
+        return;
+    }
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t kq = K / 4;
+    const int64_t kq = a.ldk / 4;
     const bool live = t < ncols * kq;              // groups of 8 lanes are all live or all dead
     const int64_t c = live ? t / kq : 0, k = live ? (t % kq) * 4 : 0;
     float v[4] = { 0.f, 0.f, 0.f, 0.f };
-    if (live) {
+    if (live && k < K) {
         const float * x = f32_col(src, c) + k;
         for (int i = 0; i < 4; ++i) v[i] = x[i];
     }
@@ -30,58 +48,65 @@ __global__ void k_quant_q8_0(F32Cols src, int64_t K, int64_t ncols, ActBuf a) {
     int s;
     const uint32_t packed = quant_q8_0_lane(v, &d, &s);
     if (!live) return;
-    const int64_t base = c * K + k;
-    *reinterpret_cast<uint32_t *>(a.codes + base) = packed;
+    *reinterpret_cast<uint32_t *>(a.codes + c * a.ldk + k) = packed;
     if ((t & 7) == 0) {
-        const int64_t b = c * (K / 32) + k / 32;
+        const int64_t b = c * (a.ldk / 32) + k / 32;
         a.d[b] = d;
         a.sums[b] = (int16_t)s;
-        if (a.dT) a.dT[(k / 32) * a.ldT + c] = d;
+        if (a.dT && k < K) a.dT[(k / 32) * a.ldT + c] = d;
     }
 }
 
 // one wave per 256-weight super-block, 4 weights per lane
-__global__ void k_quant_q8_K(F32Cols src, int64_t K, int64_t ncols, ActBuf a) {
+__global__ void k_quant_q8_K(F32Cols src, int64_t K, int64_t ncols, ActBuf a, ZeroJob z, int64_t nqblk) {
+    if ((int64_t)blockIdx.x >= nqblk) {
+        zero_cols(z, ((int64_t)blockIdx.x - nqblk) * kTpb + threadIdx.x);
+        return;
+    }
     const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
     const int lane = threadIdx.x & 63;
-    const int64_t nsb = K / 256;
+    const int64_t nsb = a.ldk / 256;
     if (wave >= ncols * nsb) return;               // whole waves only
     const int64_t c = wave / nsb, sb = wave % nsb;
-    const float * x = f32_col(src, c) + sb * 256 + 4 * lane;
-    float v[4];
-    for (int i = 0; i < 4; ++i) v[i] = x[i];
+    float v[4] = { 0.f, 0.f, 0.f, 0.f };
+    if (sb * 256 < K) {
+        const float * x = f32_col(src, c) + sb * 256 + 4 * lane;
+        for (int i = 0; i < 4; ++i) v[i] = x[i];
+    }
     float d;
     int s;
     const uint32_t packed = quant_q8_K_wave(v, lane, &d, &s);
-    const int64_t base = c * K + sb * 256 + 4 * lane;
-    *reinterpret_cast<uint32_t *>(a.codes + base) = packed;
-    if ((lane & 3) == 0) a.sums[c * (K / 16) + sb * 16 + (lane >> 2)] = (int16_t)s;
+    *reinterpret_cast<uint32_t *>(a.codes + c * a.ldk + sb * 256 + 4 * lane) = packed;
+    if ((lane & 3) == 0) a.sums[c * (a.ldk / 16) + sb * 16 + (lane >> 2)] = (int16_t)s;
     if (lane == 0) {
         a.d[c * nsb + sb] = d;
-        if (a.dT) a.dT[sb * a.ldT + c] = d;
+        if (a.dT && sb * 256 < K) a.dT[sb * a.ldT + c] = d;
     }
 }
 
 // ActBuf -> ggml block bytes, one thread per block
 __global__ void k_act_blocks(ActBuf a, uint8_t * __restrict__ out) {
     const int bs = act_block(a.vdt);
-    const int64_t nb = a.ncols * (a.K / bs);
+    const int64_t nbc = a.K / bs, nb = a.ncols * nbc;
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= nb) return;
-    const int8_t * codes = a.codes + i * bs;       // blocks of one column are contiguous
+    const int64_t c = i / nbc, b = i - c * nbc;
+    const int8_t * codes = a.codes + c * a.ldk + b * bs;
+    const float d = a.d[c * (a.ldk / bs) + b];
     if (a.vdt == QMM_TYPE_Q8_0) {
         uint8_t * o = out + i * 34;
-        const uint16_t h = __builtin_bit_cast(uint16_t, (_Float16)a.d[i]);
+        const uint16_t h = __builtin_bit_cast(uint16_t, (_Float16)d);
         o[0] = (uint8_t)(h & 0xff);
         o[1] = (uint8_t)(h >> 8);
         for (int j = 0; j < 32; ++j) o[2 + j] = (uint8_t)codes[j];
     } else {
         uint8_t * o = out + i * 292;
-        const uint32_t db = __builtin_bit_cast(uint32_t, a.d[i]);
+        const uint32_t db = __builtin_bit_cast(uint32_t, d);
         for (int j = 0; j < 4; ++j) o[j] = (uint8_t)(db >> (8 * j));
         for (int j = 0; j < 256; ++j) o[4 + j] = (uint8_t)codes[j];
+        const int16_t * sums = a.sums + c * (a.ldk / 16) + b * 16;
         for (int j = 0; j < 16; ++j) {
-            const uint16_t v = (uint16_t)a.sums[i * 16 + j];
+            const uint16_t v = (uint16_t)sums[j];
             o[260 + 2 * j] = (uint8_t)(v & 0xff);
             o[261 + 2 * j] = (uint8_t)(v >> 8);
         }
@@ -90,16 +115,18 @@ __global__ void k_act_blocks(ActBuf a, uint8_t * __restrict__ out) {
 
 }  // namespace
 
-hipError_t launch_quantize(const F32Cols & src, int64_t K, int64_t ncols, const ActBuf & a, hipStream_t s) {
-    if (ncols <= 0 || K <= 0) return hipSuccess;
-    const int tpb = 256;
-    if (a.vdt == QMM_TYPE_Q8_0) {
-        const int64_t n = ncols * (K / 4);
-        k_quant_q8_0<<<dim3((unsigned)((n + tpb - 1) / tpb)), tpb, 0, s>>>(src, K, ncols, a);
-    } else {
-        const int64_t n = ncols * (K / 256) * 64;
-        k_quant_q8_K<<<dim3((unsigned)((n + tpb - 1) / tpb)), tpb, 0, s>>>(src, K, ncols, a);
-    }
+hipError_t launch_quantize(const F32Cols & src, int64_t K, int64_t ncols, const ActBuf & a, const ZeroJob * z,
+                           hipStream_t s) {
+    if (K <= 0 || a.ldk % 256 || a.ldk < K) return hipErrorInvalidValue;
+    const ZeroJob zj = z ? *z : ZeroJob{};
+    const int64_t nzblk = z ? (zj.M * zj.ncols + kTpb - 1) / kTpb : 0;
+    int64_t nq = a.vdt == QMM_TYPE_Q8_0 ? ncols * (a.ldk / 4) : ncols * (a.ldk / 256) * 64;
+    const int64_t nqblk = ncols > 0 ? (nq + kTpb - 1) / kTpb : 0;
+    const int64_t grid = nqblk + nzblk;
+    if (grid <= 0) return hipSuccess;
+    if (grid > 0x7fffffff) return hipErrorInvalidValue;
+    if (a.vdt == QMM_TYPE_Q8_0) k_quant_q8_0<<<dim3((unsigned)grid), kTpb, 0, s>>>(src, K, ncols, a, zj, nqblk);
+    else k_quant_q8_K<<<dim3((unsigned)grid), kTpb, 0, s>>>(src, K, ncols, a, zj, nqblk);
     return hipGetLastError();
 }
 

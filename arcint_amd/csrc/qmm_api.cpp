@@ -1,5 +1,5 @@
 // qmm_api.cpp - the C ABI of libqmm (include/qmm.h): device context, buffers,
-// GGUF <-> planar repack, op validation and dispatch.  Host C++ calling HIP
+// GGUF <-> weight image repack, op validation and dispatch.  Host C++ calling HIP
 // directly; one in-order stream per context, like one ggml backend.
 #include <hip/hip_runtime.h>
 
@@ -11,6 +11,7 @@
 #include <vector>
 
 #include "qmm_internal.h"
+#include "qmm_layout.h"
 
 using namespace qmm;
 
@@ -74,14 +75,6 @@ int fail(qmm_ctx * ctx, int code, const char * fmt, ...) {
         if (e_ != hipSuccess) return fail((ctx), QMM_ERR_DEVICE, "%s: %s", #expr, hipGetErrorString(e_)); \
     } while (0)
 
-const TypeLayout kLayouts[] = {
-    { QMM_TYPE_Q4_0, 32, 18, 2, { { 2, 16 }, { 0, 2 }, { 0, 0 }, { 0, 0 } } },
-    { QMM_TYPE_Q8_0, 32, 34, 2, { { 2, 32 }, { 0, 2 }, { 0, 0 }, { 0, 0 } } },
-    { QMM_TYPE_Q4_K, 256, 144, 2, { { 16, 128 }, { 0, 16 }, { 0, 0 }, { 0, 0 } } },
-    { QMM_TYPE_Q6_K, 256, 210, 4, { { 0, 128 }, { 128, 64 }, { 192, 16 }, { 208, 2 } } },
-    { QMM_TYPE_IQ4_XS, 256, 136, 2, { { 8, 128 }, { 0, 8 }, { 0, 0 }, { 0, 0 } } },
-};
-
 bool is_quant(int type) { return type_layout(type) != nullptr; }
 
 size_t plain_elem(int type) {
@@ -108,29 +101,32 @@ bool contiguous(const qmm_tensor * t) {
     return true;
 }
 
-WView weight_view(const qmm_tensor * t, int64_t rows_per_mat) {
+WView weight_view(const qmm_tensor * t) {
     const TypeLayout & L = *type_layout(t->type);
-    const int64_t nblk = nelements(t->ne) / L.blck;
-    size_t off[4];
-    planes_alloc(L, nblk, off);
+    ImageShape sh;
+    image_shape(L, t->ne, &sh);
     WView w{};
-    const uint8_t * base = (const uint8_t *)t->buffer->ptr + t->offs;
-    for (int q = 0; q < 4; ++q) w.p[q] = q < L.nfields ? base + off[q] : nullptr;
-    w.bpr = t->ne[0] / L.blck;
-    w.rows_per_mat = rows_per_mat;
+    w.base = (const uint8_t *)t->buffer->ptr + t->offs;
+    w.M = sh.M;
+    w.K = sh.K;
+    w.bpr = sh.bpr;
+    w.G = sh.G;
+    w.ntiles = sh.ntiles;
+    w.tg = L.tg;
     return w;
 }
 
-// activation scratch layout for ncols columns of K: codes, scales, sums and
-// (GEMM consumers) the scales again block-major with a row stride of ldT
-size_t act_bytes(int vdt, int64_t K, int64_t ncols, bool dT, int64_t ldT, size_t * o_d, size_t * o_s, size_t * o_t) {
-    size_t off = align_up((size_t)(K * ncols), kPlaneAlign);
+// activation scratch layout for ncols columns of ldk (K rounded up to 256):
+// codes, scales, sums and (GEMM consumers) the scales again block-major with
+// a row stride of ldT
+size_t act_bytes(int vdt, int64_t ldk, int64_t ncols, bool dT, int64_t ldT, size_t * o_d, size_t * o_s, size_t * o_t) {
+    size_t off = align_up((size_t)(ldk * ncols), kPlaneAlign);
     *o_d = off;
-    off = align_up(off + (size_t)(ncols * (K / act_block(vdt))) * 4, kPlaneAlign);
+    off = align_up(off + (size_t)(ncols * (ldk / act_block(vdt))) * 4, kPlaneAlign);
     *o_s = off;
-    off = align_up(off + (size_t)(ncols * (K / act_sum_block(vdt))) * 2, kPlaneAlign);
+    off = align_up(off + (size_t)(ncols * (ldk / act_sum_block(vdt))) * 2, kPlaneAlign);
     *o_t = off;
-    if (dT) off = align_up(off + (size_t)((K / act_block(vdt)) * ldT) * 4, kPlaneAlign);
+    if (dT) off = align_up(off + (size_t)((ldk / act_block(vdt)) * ldT) * 4, kPlaneAlign);
     return off;
 }
 
@@ -160,21 +156,27 @@ F32Cols f32_cols(const qmm_tensor * t) {
     return c;
 }
 
+bool same_key(const qmm_ctx * ctx, int vdt, const qmm_tensor * src1, bool dT) {
+    const auto & k = ctx->key;
+    return k.valid && k.gen == ctx->graph_gen && k.buf == src1->buffer && k.offs == src1->offs && k.vdt == vdt &&
+           (k.dT || !dT) && !memcmp(k.ne, src1->ne, sizeof(k.ne)) && !memcmp(k.nb, src1->nb, sizeof(k.nb));
+}
+
 // Quantize src1 (all its columns) with the vec_dot type of `type`, reusing
 // the previous result inside one graph when src1 is the same tensor.
-int quantize_src1(qmm_ctx * ctx, int type, const qmm_tensor * src1, bool dT, ActBuf * out) {
+int quantize_src1(qmm_ctx * ctx, int type, const qmm_tensor * src1, bool dT, ActBuf * out, const ZeroJob * z = nullptr) {
     const int vdt = vec_dot_type(type);
     const int64_t K = src1->ne[0], ncols = src1->ne[1] * src1->ne[2] * src1->ne[3];
     auto & k = ctx->key;
-    if (ctx->in_graph && k.valid && k.gen == ctx->graph_gen && k.buf == src1->buffer && k.offs == src1->offs &&
-        k.vdt == vdt && (k.dT || !dT) && !memcmp(k.ne, src1->ne, sizeof(k.ne)) &&
-        !memcmp(k.nb, src1->nb, sizeof(k.nb))) {
+    if (ctx->in_graph && same_key(ctx, vdt, src1, dT)) {
         *out = ctx->cached;
+        if (z) QMM_HIP(ctx, launch_quantize(f32_cols(src1), K, 0, ctx->cached, z, ctx->stream));   // zeroing only
         return QMM_OK;
     }
     size_t od, os, ot;
+    const int64_t ldk = (K + 255) / 256 * 256;
     const int64_t ldT = (ncols + 3) / 4 * 4 + 64;    // the GEMM reads up to 63 columns past the last
-    const size_t need = act_bytes(vdt, K, ncols, dT, ldT, &od, &os, &ot);
+    const size_t need = act_bytes(vdt, ldk, ncols, dT, ldT, &od, &os, &ot);
     int rc = ensure(ctx, &ctx->act, &ctx->act_cap, need);
     if (rc) return rc;
     uint8_t * b = (uint8_t *)ctx->act;
@@ -185,9 +187,10 @@ int quantize_src1(qmm_ctx * ctx, int type, const qmm_tensor * src1, bool dT, Act
     a.dT = dT ? (float *)(b + ot) : nullptr;
     a.ldT = ldT;
     a.K = K;
+    a.ldk = ldk;
     a.ncols = ncols;
     a.vdt = vdt;
-    QMM_HIP(ctx, launch_quantize(f32_cols(src1), K, ncols, a, ctx->stream));
+    QMM_HIP(ctx, launch_quantize(f32_cols(src1), K, ncols, a, z, ctx->stream));
     k.buf = src1->buffer;
     k.offs = src1->offs;
     memcpy(k.ne, src1->ne, sizeof(k.ne));
@@ -216,18 +219,21 @@ bool check_f32(const qmm_tensor * t) {
     return t && t->buffer && t->type == QMM_TYPE_F32 && t->nb[0] == sizeof(float) && t->ne[0] > 0;
 }
 
-// event pair around the main kernel of an op when timing is on
-int ktime_mark(qmm_ctx * ctx, bool begin) {
+// event pair stamped by the main kernel of an op when timing is on (null otherwise)
+int ktime_pair(qmm_ctx * ctx, KTime * kt, const KTime ** out) {
+    *out = nullptr;
     if (!ctx->ktime) return QMM_OK;
-    if (begin && ctx->kev_used + 2 > ctx->kev.size()) {
+    if (ctx->kev_used + 2 > ctx->kev.size()) {
         for (int i = 0; i < 64; ++i) {
             hipEvent_t e;
             QMM_HIP(ctx, hipEventCreate(&e));
             ctx->kev.push_back(e);
         }
     }
-    QMM_HIP(ctx, hipEventRecord(ctx->kev[ctx->kev_used], ctx->stream));
-    ctx->kev_used++;
+    kt->start = ctx->kev[ctx->kev_used];
+    kt->stop = ctx->kev[ctx->kev_used + 1];
+    ctx->kev_used += 2;
+    *out = kt;
     return QMM_OK;
 }
 
@@ -237,28 +243,6 @@ void note_downgrade(qmm_ctx * ctx, const char * key) {
 }
 
 }  // namespace
-
-// ---------------------------------------------------------------------------
-namespace qmm {
-
-const TypeLayout * type_layout(int type) {
-    for (const auto & L : kLayouts)
-        if (L.type == type) return &L;
-    return nullptr;
-}
-
-size_t plane_bytes(const TypeLayout & L, int q, int64_t nblk) { return (size_t)L.f[q].size * (size_t)nblk; }
-
-size_t planes_alloc(const TypeLayout & L, int64_t nblk, size_t plane_off[4]) {
-    size_t off = 0;
-    for (int q = 0; q < 4; ++q) {
-        plane_off[q] = off;
-        if (q < L.nfields) off = align_up(off + plane_bytes(L, q, nblk), kPlaneAlign);
-    }
-    return off;
-}
-
-}  // namespace qmm
 
 // ---------------------------------------------------------------------------
 extern "C" {
@@ -344,9 +328,47 @@ size_t qmm_tensor_nbytes(int32_t type, const int64_t ne[4]) {
 size_t qmm_tensor_alloc_size(int32_t type, const int64_t ne[4]) {
     const TypeLayout * L = type_layout(type);
     if (!L) return qmm_tensor_nbytes(type, ne);
-    if (ne[0] % L->blck) return 0;
-    size_t off[4];
-    return planes_alloc(*L, nelements(ne) / L->blck, off);
+    ImageShape sh;
+    if (!image_shape(*L, ne, &sh)) return 0;
+    return sh.bytes;
+}
+
+// Quantized tensor IO: GGUF blocks [b0, b0 + nb) <-> the device image, staged
+// through host memory a run of whole tiles at a time.  A write that leaves
+// some row of a run untouched reads the run first (read-modify-write).
+static int quant_io(qmm_ctx * ctx, const TypeLayout & L, const ImageShape & sh, uint8_t * dev, uint8_t * host,
+                    int64_t b0, int64_t nb, bool write) {
+    if (nb <= 0) return QMM_OK;
+    const int64_t R0 = b0 / sh.bpr, R1 = (b0 + nb - 1) / sh.bpr + 1;
+    const int64_t Ta = tile_of_row(sh, R0), Tb = tile_of_row(sh, R1 - 1) + 1;
+    const size_t tile_bytes = (size_t)sh.G * (size_t)L.tg;
+    const int64_t run = std::max<int64_t>(1, (int64_t)((64u << 20) / tile_bytes));
+    std::vector<uint8_t> stage;
+    for (int64_t T0 = Ta; T0 < Tb; T0 += run) {
+        const int64_t T1 = std::min(Tb, T0 + run);
+        int64_t rowA, rowB, dummy;
+        tile_rows(sh, T0, &rowA, &dummy);
+        tile_rows(sh, T1 - 1, &dummy, &rowB);
+        const int64_t blkA = std::max(b0, rowA * sh.bpr), blkB = std::min(b0 + nb, rowB * sh.bpr);
+        const size_t bytes = (size_t)(T1 - T0) * tile_bytes;
+        uint8_t * d = dev + (size_t)T0 * tile_bytes;
+        stage.assign(bytes, 0);
+        const bool full = blkA == rowA * sh.bpr && blkB == rowB * sh.bpr;
+        if (!write || !full) {
+            QMM_HIP(ctx, hipMemcpyAsync(stage.data(), d, bytes, hipMemcpyDeviceToHost, ctx->stream));
+            QMM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        }
+        if (write) {
+            pack_blocks(L, sh, host + (size_t)(blkA - b0) * L.bytes, blkA, blkB - blkA, stage.data(), T0);
+            if (!full)
+                for (int64_t R = blkA / sh.bpr; R <= (blkB - 1) / sh.bpr; ++R) zero_row_padding(L, sh, R, stage.data(), T0);
+            QMM_HIP(ctx, hipMemcpyAsync(d, stage.data(), bytes, hipMemcpyHostToDevice, ctx->stream));
+            QMM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        } else {
+            unpack_blocks(L, sh, stage.data(), T0, blkA, blkB - blkA, host + (size_t)(blkA - b0) * L.bytes);
+        }
+    }
+    return QMM_OK;
 }
 
 static int tensor_io(qmm_ctx * ctx, const qmm_tensor * t, void * host, size_t offset, size_t size, bool write) {
@@ -362,36 +384,33 @@ static int tensor_io(qmm_ctx * ctx, const qmm_tensor * t, void * host, size_t of
     const TypeLayout * L = type_layout(t->type);
     if (L && (offset % L->bytes || size % L->bytes))
         return fail(ctx, QMM_ERR_INVALID, "tensor io: offset %zu / size %zu not whole %d-byte blocks", offset, size, L->bytes);
-    if (!L || L->nfields == 1) {   // the device bytes are the GGUF bytes
+    if (!L) {   // the device bytes are the plain bytes
         if (write) QMM_HIP(ctx, hipMemcpyAsync(dev + offset, host, size, hipMemcpyHostToDevice, ctx->stream));
         else QMM_HIP(ctx, hipMemcpyAsync(host, dev + offset, size, hipMemcpyDeviceToHost, ctx->stream));
         QMM_HIP(ctx, hipStreamSynchronize(ctx->stream));
         return QMM_OK;
     }
-    const int64_t nblk = nelements(t->ne) / L->blck, b0 = (int64_t)(offset / L->bytes), nb = (int64_t)(size / L->bytes);
-    size_t poff[4];
-    planes_alloc(*L, nblk, poff);
-    // staged in pieces so that large tensors do not need one huge host copy
-    const int64_t piece = 1 << 18;
-    std::vector<uint8_t> stage;
-    uint8_t * h = (uint8_t *)host;
-    for (int64_t s0 = 0; s0 < nb; s0 += piece) {
-        const int64_t n = std::min(piece, nb - s0);
-        for (int q = 0; q < L->nfields; ++q) {
-            const Field f = L->f[q];
-            stage.resize((size_t)(n * f.size));
-            uint8_t * pd = dev + poff[q] + (size_t)(b0 + s0) * f.size;
-            if (write) {
-                for (int64_t i = 0; i < n; ++i) memcpy(&stage[(size_t)(i * f.size)], h + (size_t)(s0 + i) * L->bytes + f.off, (size_t)f.size);
-                QMM_HIP(ctx, hipMemcpyAsync(pd, stage.data(), stage.size(), hipMemcpyHostToDevice, ctx->stream));
-                QMM_HIP(ctx, hipStreamSynchronize(ctx->stream));
-            } else {
-                QMM_HIP(ctx, hipMemcpyAsync(stage.data(), pd, stage.size(), hipMemcpyDeviceToHost, ctx->stream));
-                QMM_HIP(ctx, hipStreamSynchronize(ctx->stream));
-                for (int64_t i = 0; i < n; ++i) memcpy(h + (size_t)(s0 + i) * L->bytes + f.off, &stage[(size_t)(i * f.size)], (size_t)f.size);
-            }
-        }
-    }
+    ImageShape sh;
+    image_shape(*L, t->ne, &sh);
+    return quant_io(ctx, *L, sh, dev, (uint8_t *)host, (int64_t)(offset / L->bytes), (int64_t)(size / L->bytes), write);
+}
+
+int qmm_tensor_pack(int32_t type, const int64_t ne[4], const void * gguf, void * image, size_t image_size) {
+    const TypeLayout * L = type_layout(type);
+    ImageShape sh;
+    if (!L || !gguf || !image || !image_shape(*L, ne, &sh) || image_size < sh.bytes) return QMM_ERR_INVALID;
+    memset(image, 0, sh.bytes);
+    pack_blocks(*L, sh, (const uint8_t *)gguf, 0, sh.nmat * sh.M * sh.bpr, (uint8_t *)image, 0);
+    return QMM_OK;
+}
+
+int qmm_tensor_unpack(int32_t type, const int64_t ne[4], const void * image, void * gguf, size_t gguf_size) {
+    const TypeLayout * L = type_layout(type);
+    ImageShape sh;
+    if (!L || !gguf || !image || !image_shape(*L, ne, &sh)) return QMM_ERR_INVALID;
+    const int64_t nblk = sh.nmat * sh.M * sh.bpr;
+    if (gguf_size < (size_t)nblk * (size_t)L->bytes) return QMM_ERR_INVALID;
+    unpack_blocks(*L, sh, (const uint8_t *)image, 0, 0, nblk, (uint8_t *)gguf);
     return QMM_OK;
 }
 
@@ -480,21 +499,54 @@ static int64_t gemm_min_cols() {
     return v;
 }
 
+int qmm_describe_mul_mat(const qmm_tensor * src0, const qmm_tensor * src1, const qmm_tensor * dst, qmm_launch_info * out) {
+    if (!out) return QMM_ERR_INVALID;
+    memset(out, 0, sizeof(*out));
+    if (!src0 || !src1 || !dst) return QMM_ERR_INVALID;
+    qmm_tensor a = *src0, b = *src1, c = *dst;   // shapes only: any non-null buffer passes validation
+    qmm_buffer fake;
+    a.buffer = b.buffer = c.buffer = &fake;
+    char reason[160];
+    if (!mul_mat_ok(&a, &b, &c, reason, sizeof(reason))) return QMM_ERR_UNSUPPORTED;
+    const int64_t N = src1->ne[1];
+    const ImageShape sh = [&] { ImageShape t; image_shape(*type_layout(src0->type), src0->ne, &t); return t; }();
+    if (N >= gemm_min_cols()) {
+        snprintf(out->path, sizeof(out->path), "gemm-mfma");
+        out->threads = 256;
+        out->tasks = src1->ne[2] * src1->ne[3];
+        out->cols_per_task = (int32_t)std::min<int64_t>(N, INT32_MAX);
+        out->workgroups = ((sh.M + 63) / 64) * ((N + 63) / 64) * out->tasks;
+        return QMM_OK;
+    }
+    fake.ptr = nullptr;
+    fake.size = 0;
+    const WView w = weight_view(&a);
+    const int nc = (int)std::min<int64_t>(N, kMaxTaskCols);
+    const int64_t ntasks = (N + nc - 1) / nc * src1->ne[2] * src1->ne[3];
+    GemvPlan plan;
+    if (!gemv_plan(src0->type, w, nc, ntasks, true, &plan)) return QMM_ERR_UNSUPPORTED;
+    snprintf(out->path, sizeof(out->path), "gemv");
+    out->threads = 64 * plan.W;
+    out->cols_per_task = nc;
+    out->tasks = ntasks;
+    out->k_waves = plan.W;
+    out->k_slices = plan.KS;
+    out->groups_per_wave = plan.spw;
+    out->workgroups = ntasks * w.ntiles * plan.KS;
+    out->lds_bytes = plan.W > 1 ? (int64_t)plan.W * nc * 64 * 4 : 0;
+    return QMM_OK;
+}
+
 int qmm_mul_mat(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1, const qmm_tensor * dst) {
     if (!ctx) return QMM_ERR_INVALID;
     char reason[160];
     if (!mul_mat_ok(src0, src1, dst, reason, sizeof(reason))) return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat: %s", reason);
     QMM_HIP(ctx, hipSetDevice(ctx->device));
-    const int64_t K = src0->ne[0], M = src0->ne[1];
     const int64_t N = src1->ne[1];
     const bool use_gemm = N >= gemm_min_cols();
-    // up to 8 columns per batch: one task, the GEMV quantizes x in LDS itself
-    const bool fused = N <= kMaxTaskCols && !use_gemm;
     ActBuf a{};
     int rc;
-    if (!fused && (rc = quantize_src1(ctx, src0->type, src1, use_gemm, &a))) return rc;
-    const F32Cols xs = f32_cols(src1);
-    const WView w = weight_view(src0, M);
+    const WView w = weight_view(src0);
     float * d = (float *)((uint8_t *)dst->buffer->ptr + dst->offs);
     GemvDense dn;
     dn.ne11 = N;
@@ -507,6 +559,7 @@ int qmm_mul_mat(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1,
     dn.d_nb2 = (int64_t)(dst->nb[2] / 4);
     dn.d_nb3 = (int64_t)(dst->nb[3] / 4);
     if (use_gemm) {
+        if ((rc = quantize_src1(ctx, src0->type, src1, true, &a))) return rc;
         GemmBatch bt;
         bt.ne12 = dn.ne12;
         bt.r2 = dn.r2;
@@ -516,17 +569,26 @@ int qmm_mul_mat(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1,
         bt.d_nb2 = dn.d_nb2;
         bt.d_nb3 = dn.d_nb3;
         ctx->path = "gemm-mfma";
-        if ((rc = ktime_mark(ctx, true))) return rc;
-        QMM_HIP(ctx, launch_gemm(src0->type, w, M, K, a, N, dn.ne12 * dn.ne13, bt, d, ctx->stream));
-        return ktime_mark(ctx, false);
+        KTime kt;
+        const KTime * ktp;
+        if ((rc = ktime_pair(ctx, &kt, &ktp))) return rc;
+        QMM_HIP(ctx, launch_gemm(src0->type, w, a, N, dn.ne12 * dn.ne13, bt, d, ctx->stream, ktp));
+        return QMM_OK;
     }
+    // up to 8 columns per task against one weight pass
     const int nc = (int)std::min<int64_t>(N, kMaxTaskCols);
-    ctx->path = fused ? "gemv-fused" : "gemv-tasks";
+    const int64_t ntasks = (N + nc - 1) / nc * dn.ne12 * dn.ne13;
+    GemvPlan plan;
+    if (!gemv_plan(src0->type, w, nc, ntasks, true, &plan)) return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat: GEMV shape out of range");
+    ZeroJob z{ d, w.M, N * dn.ne12 * dn.ne13, N, dn.ne12, dn.d_nb1, dn.d_nb2, dn.d_nb3 };
+    if ((rc = quantize_src1(ctx, src0->type, src1, false, &a, plan.KS > 1 ? &z : nullptr))) return rc;
+    ctx->path = "gemv";
     if (N > kMaxTaskCols) note_downgrade(ctx, "mul_mat: many columns on the GEMV");
-    if ((rc = ktime_mark(ctx, true))) return rc;
-    QMM_HIP(ctx, launch_gemv_any(src0->type, w, M, K, fused ? nullptr : &a, &xs, nullptr, 0, nullptr, nc, &dn, d,
-                                 ctx->stream));
-    return ktime_mark(ctx, false);
+    KTime kt;
+    const KTime * ktp;
+    if ((rc = ktime_pair(ctx, &kt, &ktp))) return rc;
+    QMM_HIP(ctx, launch_gemv(src0->type, w, plan, a, nullptr, nullptr, &dn, d, ctx->stream, ktp));
+    return QMM_OK;
 }
 
 int qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1, const qmm_tensor * ids,
@@ -536,16 +598,18 @@ int qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * sr
     if (!mul_mat_id_ok(src0, src1, ids, dst, reason, sizeof(reason)))
         return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat_id: %s", reason);
     QMM_HIP(ctx, hipSetDevice(ctx->device));
-    const int64_t K = src0->ne[0], M = src0->ne[1], n_as = src0->ne[2];
+    const int64_t M = src0->ne[1], n_as = src0->ne[2];
     const int64_t n_used = ids->ne[0], T = ids->ne[1], ne11 = src1->ne[1];
-    // few tokens: each work-group quantizes its task's columns itself
-    const bool fused = T < 16;
     ActBuf a{};
-    int rc = QMM_OK;
-    if (!fused && (rc = quantize_src1(ctx, src0->type, src1, false, &a))) return rc;
-    const F32Cols xs = f32_cols(src1);
+    int rc;
+    if ((rc = quantize_src1(ctx, src0->type, src1, false, &a))) return rc;
     const int64_t npairs = n_used * T;
     const int64_t max_tasks = npairs / kMaxTaskCols + std::min(n_as, npairs) + 1;
+    const WView w = weight_view(src0);
+    const int nc = (int)std::min<int64_t>(kMaxTaskCols, npairs);
+    GemvPlan plan;
+    if (!gemv_plan(src0->type, w, nc, max_tasks, false, &plan))
+        return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat_id: GEMV shape out of range");
     const size_t o_tasks = align_up((size_t)npairs * 4, 256);
     const size_t o_cnt = align_up(o_tasks + (size_t)max_tasks * sizeof(GemvTask), 256);
     rc = ensure(ctx, &ctx->route, &ctx->route_cap, o_cnt + 256);
@@ -565,13 +629,12 @@ int qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * sr
     GemvTask * tasks = (GemvTask *)(rb + o_tasks);
     int32_t * ntasks = (int32_t *)(rb + o_cnt);
     QMM_HIP(ctx, launch_route(r, (int32_t *)rb, tasks, ntasks, d, M, ctx->stream));
-    const WView w = weight_view(src0, M);
-    const int nc = (int)std::min<int64_t>(kMaxTaskCols, T);
-    ctx->path = fused ? "gemv-id-fused" : "gemv-id";
-    if ((rc = ktime_mark(ctx, true))) return rc;
-    QMM_HIP(ctx, launch_gemv_any(src0->type, w, M, K, fused ? nullptr : &a, &xs, tasks, (int)max_tasks, ntasks, nc,
-                                 nullptr, d, ctx->stream));
-    return ktime_mark(ctx, false);
+    ctx->path = "gemv-id";
+    KTime kt;
+    const KTime * ktp;
+    if ((rc = ktime_pair(ctx, &kt, &ktp))) return rc;
+    QMM_HIP(ctx, launch_gemv(src0->type, w, plan, a, tasks, ntasks, nullptr, d, ctx->stream, ktp));
+    return QMM_OK;
 }
 
 int qmm_graph_compute(qmm_ctx * ctx, const qmm_node * nodes, int n_nodes) {
@@ -606,9 +669,9 @@ int qmm_dequantize(qmm_ctx * ctx, const qmm_tensor * src, const qmm_tensor * dst
     if (dst->type != QMM_TYPE_F32 || !contiguous(dst) || nelements(dst->ne) != nelements(src->ne))
         return fail(ctx, QMM_ERR_INVALID, "dequantize: dst must be contiguous f32 with as many elements");
     QMM_HIP(ctx, hipSetDevice(ctx->device));
-    const WView w = weight_view(src, src->ne[1]);
+    const WView w = weight_view(src);
     float * y = (float *)((uint8_t *)dst->buffer->ptr + dst->offs);
-    QMM_HIP(ctx, launch_dequant(src->type, w, nelements(src->ne) / L->blck, y, ctx->stream));
+    QMM_HIP(ctx, launch_dequant(src->type, w, src->ne[2] * src->ne[3], y, ctx->stream));
     return QMM_OK;
 }
 

@@ -11,44 +11,67 @@
 namespace qmm {
 
 // ---------------------------------------------------------------------------
-// Weight layout in HBM.
+// Weight image in HBM (the device layout behind qmm_tensor_set/get).
 //
-// A quantized tensor of nblk GGUF blocks is stored as up to four planes, one
-// per block field, each plane 256-byte aligned and holding that field of
-// every block in block order (block i = row * blocks_per_row + kb, rows of
-// all experts back to back).  The field split is chosen so that every plane
-// a decode kernel streams is 16-byte aligned per block, which gives each lane
-// 128-bit loads:
-//   Q4_0   qs[16] | d[2]
-//   Q8_0   qs[32] | d[2]
-//   Q4_K   qs[128] | {d, dmin, scales[12]}[16]
-//   Q6_K   ql[128] | qh[64] | scales[16] | d[2]
-//   IQ4_XS qs[128] | {d, scales_h, scales_l[4]}[8]
+// Rows of every matrix (expert / 2-D slice) are grouped in tiles of 64 rows
+// and the K axis in groups of 256 weights (8 GGUF blocks of Q4_0/Q8_0, one
+// super-block of the K-quants; a last partial group of Q4_0/Q8_0 is padded
+// with zero blocks).  The bytes of one (tile, group) - a "tile-group" - are
+// contiguous and consist of `nchunk` chunk planes of 64 x 16 bytes (row r of
+// the tile at byte 16 r of every plane) followed by an optional tail plane of
+// 64 x `tail` bytes.  A wave that gives lane r the row r reads one chunk
+// plane with a single fully coalesced 1 KB load.  Planes per tile-group:
+//   Q4_0    chunk p < 8: qs of block p | chunk 8: d of blocks 0..7 (fp16)
+//   Q8_0    chunks 2p, 2p+1: qs[0:16], qs[16:32] of block p | chunk 16: d[8]
+//   Q4_K    chunk c < 8: qs[16c:16c+16] | chunk 8: {d, dmin, scales[12]}
+//   Q6_K    chunk c < 8: ql[16c:+16] | chunks 8..11: qh[16c:+16] |
+//           chunk 12: scales[16] | tail (2 B): d
+//   IQ4_XS  chunk c < 8: qs[16c:+16] | tail (8 B): {d, scales_h, scales_l[4]}
+// Tile-groups are stored [matrix][tile][group]; rows past M in the last tile
+// and the padding blocks of a partial group are zero bytes.
 // ---------------------------------------------------------------------------
-struct Field { int off, size; };
-
-struct TypeLayout {
-    int type;
-    int blck;       // weights per block
-    int bytes;      // GGUF bytes per block
-    int nfields;
-    Field f[4];
-};
-
-const TypeLayout * type_layout(int type);   // nullptr for unknown types
-size_t plane_bytes(const TypeLayout & L, int q, int64_t nblk);
-size_t planes_alloc(const TypeLayout & L, int64_t nblk, size_t plane_off[4]);
-
+constexpr int kTileRows = 64;
+constexpr int kGroupW = 256;
+constexpr int kChunk = 1024;
 constexpr size_t kPlaneAlign = 256;
 static inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+struct TypeLayout {
+    int type;
+    int blck;     // weights per GGUF block
+    int bytes;    // GGUF bytes per block
+    int bpg;      // GGUF blocks per 256-weight group
+    int nchunk;   // chunk planes per tile-group
+    int tail;     // bytes per row of the tail plane (0: none)
+    int tg;       // bytes per tile-group = nchunk * 1024 + 64 * tail
+};
+
+const TypeLayout * type_layout(int type);   // nullptr for unknown types
+
+struct ImageShape {
+    int64_t K, M, nmat;   // row length, rows per matrix, matrices (ne2 * ne3)
+    int64_t bpr;          // GGUF blocks per row
+    int64_t G;            // 256-weight groups per row
+    int64_t ntiles;       // 64-row tiles per matrix
+    size_t bytes;         // image bytes (a multiple of 256)
+};
+// false when ne[0] is not a whole number of blocks
+bool image_shape(const TypeLayout & L, const int64_t ne[4], ImageShape * s);
+
+// One piece of a GGUF block placed in a tile-group: `size` bytes from byte
+// `src` of the block go to byte `dst` of the tile-group (row 0, block slot 0);
+// row r adds r * row_step, block slot p (Q4_0/Q8_0) adds p * slot_step.
+struct Piece { int src, size, dst, row_step, slot_step; };
+int block_pieces(const TypeLayout & L, Piece out[16]);
+
 // ---------------------------------------------------------------------------
 // Quantized activations (the vec_dot type's from_float, done on the device).
-// For column c of ncols:
-//   codes  int8 [c][K]
-//   d      f32  [c][K/bs]       bs = 32 (q8_0) or 256 (q8_K); q8_0's d is
+// Columns are padded to ldk = K rounded up to 256 (zero codes, zero scales,
+// zero sums past K).  For column c of ncols:
+//   codes  int8 [c][ldk]
+//   d      f32  [c][ldk/bs]     bs = 32 (q8_0) or 256 (q8_K); q8_0's d is
 //                               the fp16-rounded scale widened to f32
-//   sums   i16  [c][K/ss]       ss = 32 (q8_0: sum of the block's codes)
+//   sums   i16  [c][ldk/ss]     ss = 32 (q8_0: sum of the block's codes)
 //                               or 16 (q8_K: ggml's bsums)
 // ---------------------------------------------------------------------------
 struct ActBuf {
@@ -58,8 +81,18 @@ struct ActBuf {
     float *    dT;         // non-null: the scales again, block-major: dT[b * ldT + c]
     int64_t    ldT;        // >= ncols + 64 (the GEMM reads whole 64-column tiles)
     int64_t    K;
+    int64_t    ldk;        // K rounded up to 256
     int64_t    ncols;
     int        vdt;        // QMM_TYPE_Q8_0 or QMM_TYPE_Q8_K
+};
+
+// Zeroing of dst columns by the activation pre-pass (the GEMV then adds the
+// partial sums of its K slices with atomics): column c = (i1, i2, i3), i1
+// fastest, floats [0, M) at i1 * nb1 + i2 * nb2 + i3 * nb3 (float strides).
+struct ZeroJob {
+    float * dst;
+    int64_t M, ncols, ne1, ne2;
+    int64_t nb1, nb2, nb3;
 };
 
 __host__ __device__ static inline int act_block(int vdt) { return vdt == QMM_TYPE_Q8_0 ? 32 : 256; }
@@ -79,10 +112,19 @@ struct F32Cols {
 // Weight views handed to kernels
 // ---------------------------------------------------------------------------
 struct WView {
-    const uint8_t * p[4];      // planes
-    int64_t bpr;               // blocks per row
-    int64_t rows_per_mat;      // M (one expert / one 2-D slice)
+    const uint8_t * base;      // image of matrix 0
+    int64_t M;                 // rows per matrix
+    int64_t K;                 // weights per row
+    int64_t bpr;               // GGUF blocks per row
+    int64_t G;                 // groups per row
+    int64_t ntiles;            // tiles per matrix
+    int tg;                    // bytes per tile-group
 };
+
+// tile-group (mat, tile, g) of the image
+__host__ __device__ static inline const uint8_t * tile_group(const WView & w, int64_t mat, int64_t tile, int64_t g) {
+    return w.base + (size_t)(((mat * w.ntiles + tile) * w.G + g)) * (size_t)w.tg;
+}
 
 // A GEMV task: up to 8 columns against one weight matrix.
 constexpr int kMaxTaskCols = 8;
@@ -94,10 +136,16 @@ struct GemvTask {
 };
 
 // ---------------------------------------------------------------------------
-// Launchers (defined in the .hip files); all enqueue on `s`.
+// Launchers (defined in the .hip files); all enqueue on `s`.  A non-null
+// KTime has its events stamped with the main kernel's own start and end (the
+// dispatch itself, as a profiler sees it).
 // ---------------------------------------------------------------------------
-hipError_t launch_dequant(int type, const WView & w, int64_t nblk, float * y, hipStream_t s);
-hipError_t launch_quantize(const F32Cols & src, int64_t K, int64_t ncols, const ActBuf & a, hipStream_t s);
+struct KTime {
+    hipEvent_t start, stop;
+};
+hipError_t launch_dequant(int type, const WView & w, int64_t nmat, float * y, hipStream_t s);
+hipError_t launch_quantize(const F32Cols & src, int64_t K, int64_t ncols, const ActBuf & a, const ZeroJob * z,
+                           hipStream_t s);
 // writes ggml block bytes (block_q8_0 / block_q8_K) of an ActBuf into `out` (device)
 hipError_t launch_act_to_blocks(const ActBuf & a, void * out, hipStream_t s);
 
@@ -107,15 +155,23 @@ struct GemvDense {
     int64_t d_nb1, d_nb2, d_nb3;   // dst strides in floats
 };
 
-// GEMV: dst[dst_off + m] for m < M, rows of matrix `mat` of each task.
-// Activations come pre-quantized (`a`) or as f32 columns (`src`) that every
-// work-group quantizes into LDS itself (bit-identical to the pre-pass).
-// List mode (tasks != nullptr): `ntasks_dev` (optional) bounds the task list
-// on the device, ntasks_max sizes the grid.  Dense mode (tasks == nullptr):
-// tasks of up to nc columns are derived from `dense`.
-hipError_t launch_gemv_any(int type, const WView & w, int64_t M, int64_t K, const ActBuf * a, const F32Cols * src,
-                           const GemvTask * tasks, int ntasks_max, const int32_t * ntasks_dev, int nc,
-                           const GemvDense * dense, float * dst, hipStream_t s);
+// Launch shape of a GEMV (host): W waves per work-group and KS work-groups
+// per 64-row tile split K, spw groups of 256 weights per wave.  KS > 1 adds
+// partial sums to dst with atomics, so dst must be zeroed first.
+struct GemvPlan {
+    int nc;                        // columns per task (1..8)
+    int64_t ntasks;                // grid tasks (list mode: upper bound)
+    int W, KS, spw;
+};
+bool gemv_plan(int type, const WView & w, int nc, int64_t ntasks, bool allow_split, GemvPlan * plan);
+
+// GEMV: dst[dst_off + m] for m < M, rows of matrix `mat` of each task, from
+// the pre-pass activations `a` (ldk == 256 * groups).  List mode (tasks !=
+// nullptr): `ntasks_dev` (optional) bounds the task list on the device.
+// Dense mode (tasks == nullptr): tasks of up to nc columns from `dense`.
+hipError_t launch_gemv(int type, const WView & w, const GemvPlan & plan, const ActBuf & a, const GemvTask * tasks,
+                       const int32_t * ntasks_dev, const GemvDense * dense, float * dst, hipStream_t s,
+                       const KTime * kt = nullptr);
 
 // Prefill GEMM (int8 MFMA): for every batch b < nbatch, dst[doff(b) + n * d_nb1
 // + m] = W(mat(b)) row m . activation column col0(b) + n, for n < N, m < M.
@@ -124,8 +180,8 @@ struct GemmBatch {
     int64_t ne12, r2, r3, ne02;    // batch b = (i2, i3): mat = i2 / r2 + (i3 / r3) * ne02
     int64_t d_nb1, d_nb2, d_nb3;   // dst strides in floats
 };
-hipError_t launch_gemm(int type, const WView & w, int64_t M, int64_t K, const ActBuf & a, int64_t N, int64_t nbatch,
-                       const GemmBatch & bt, float * dst, hipStream_t s);
+hipError_t launch_gemm(int type, const WView & w, const ActBuf & a, int64_t N, int64_t nbatch,
+                       const GemmBatch & bt, float * dst, hipStream_t s, const KTime * kt = nullptr);
 
 // MoE routing: builds GEMV tasks (one per expert and up to 8 pairs) from ids.
 struct RouteArgs {
@@ -134,7 +190,7 @@ struct RouteArgs {
     int64_t n_used, T, ne11, n_as;
     int64_t dst_nb1, dst_nb2;   // float strides of dst dims 1 and 2
 };
-// scratch: counts [n_as], offsets [n_as], pairs [T*n_used]; tasks out
+// scratch: pairs [T*n_used]; tasks out
 hipError_t launch_route(const RouteArgs & r, int32_t * scratch, GemvTask * tasks, int32_t * ntasks,
                         float * dst, int64_t M, hipStream_t s);
 

@@ -33,7 +33,7 @@ EXPORTS = (
     "qmm_tensor_set", "qmm_tensor_get", "qmm_supports_op", "qmm_mul_mat", "qmm_mul_mat_id",
     "qmm_graph_compute", "qmm_dequantize", "qmm_quantize_act", "qmm_synchronize", "qmm_downgrades",
     "qmm_last_path", "qmm_timer_begin", "qmm_timer_end", "qmm_buffer_copy", "qmm_kernel_timing",
-    "qmm_kernel_time",
+    "qmm_kernel_time", "qmm_tensor_pack", "qmm_tensor_unpack", "qmm_describe_mul_mat",
 )
 
 
@@ -44,6 +44,12 @@ class QmmError(RuntimeError):
 class CTensor(C.Structure):
     _fields_ = [("type", C.c_int32), ("ne", C.c_int64 * 4), ("nb", C.c_size_t * 4),
                 ("buffer", C.c_void_p), ("offs", C.c_size_t)]
+
+
+class LaunchInfo(C.Structure):
+    _fields_ = [("path", C.c_char * 32), ("workgroups", C.c_int64), ("threads", C.c_int32),
+                ("cols_per_task", C.c_int32), ("tasks", C.c_int64), ("k_waves", C.c_int32),
+                ("k_slices", C.c_int32), ("groups_per_wave", C.c_int32), ("lds_bytes", C.c_int64)]
 
 
 class CNode(C.Structure):
@@ -96,6 +102,9 @@ def load() -> C.CDLL:
         L.qmm_buffer_copy.argtypes = [vp, vp, sz, vp, sz, sz]
         L.qmm_kernel_timing.argtypes = [vp, C.c_int]
         L.qmm_kernel_time.argtypes = [vp, C.POINTER(C.c_double), C.POINTER(i64)]
+        L.qmm_tensor_pack.argtypes = [i32, C.POINTER(i64), vp, vp, sz]
+        L.qmm_describe_mul_mat.argtypes = [T, T, T, C.POINTER(LaunchInfo)]
+        L.qmm_tensor_unpack.argtypes = [i32, C.POINTER(i64), vp, vp, sz]
         _lib = L
     return _lib
 
@@ -121,6 +130,37 @@ def nbytes(qtype: int, ne) -> int:
 def alloc_size(qtype: int, ne) -> int:
     arr = (C.c_int64 * 4)(*_ne4(ne))
     return load().qmm_tensor_alloc_size(qtype, arr)
+
+
+def describe_mul_mat(src0: "Tensor", src1: "Tensor", dst: "Tensor") -> dict:
+    """The launch qmm_mul_mat would make for these shapes (host only)."""
+    info = LaunchInfo()
+    rc = load().qmm_describe_mul_mat(C.byref(src0.c), C.byref(src1.c), C.byref(dst.c), C.byref(info))
+    if rc:
+        raise QmmError(f"qmm_describe_mul_mat: status {rc}")
+    return {f: (getattr(info, f).decode() if f == "path" else getattr(info, f)) for f, _ in LaunchInfo._fields_}
+
+
+def pack(qtype: int, ne, gguf: np.ndarray) -> np.ndarray:
+    """Device image of a whole tensor from its GGUF bytes (host only)."""
+    arr = (C.c_int64 * 4)(*_ne4(ne))
+    g = np.ascontiguousarray(gguf, np.uint8)
+    out = np.empty(alloc_size(qtype, ne), np.uint8)
+    rc = load().qmm_tensor_pack(qtype, arr, g.ctypes.data, out.ctypes.data, out.nbytes)
+    if rc:
+        raise QmmError(f"qmm_tensor_pack: status {rc}")
+    return out
+
+
+def unpack(qtype: int, ne, image: np.ndarray) -> np.ndarray:
+    """GGUF bytes of a whole tensor from its device image (host only)."""
+    arr = (C.c_int64 * 4)(*_ne4(ne))
+    im = np.ascontiguousarray(image, np.uint8)
+    out = np.empty(nbytes(qtype, ne), np.uint8)
+    rc = load().qmm_tensor_unpack(qtype, arr, im.ctypes.data, out.ctypes.data, out.nbytes)
+    if rc:
+        raise QmmError(f"qmm_tensor_unpack: status {rc}")
+    return out
 
 
 @dataclass

@@ -18,6 +18,10 @@
  *   qmm_tensor_set/get           buffer set_tensor / get_tensor: GGUF block
  *                                bytes in, device planes, exact bytes back
  *                                (P02:1556-1790)
+ *   qmm_tensor_pack/unpack       the same GGUF <-> device-image conversion on
+ *                                the host, for loaders that upload a prebuilt
+ *                                image (the role of the planar-layout header
+ *                                ggml-opencl-planes.h, 0116-...patch:17-159)
  *   qmm_supports_op              ggml_opencl_supports_op for MUL_MAT /
  *                                MUL_MAT_ID (P01:615-660)
  *   qmm_mul_mat                  ggml_cl_mul_mat (P01:1135-1160)
@@ -34,6 +38,9 @@
  *   qmm_last_error               the reason behind a failed status (the
  *                                reference aborts via GGML_ASSERT/CL_CHECK)
  *   qmm_downgrades               ggml_backend_opencl_downgrades() (0100-...patch:11-23)
+ *   qmm_describe_mul_mat         the path and launch shape a MUL_MAT would take,
+ *                                what GGML_OPENCL_FEWQ_LOG / _TRACE log per
+ *                                shape (docs/switches.md:189-190)
  *
  * Conventions (ggml's): a tensor is { type, ne[4], nb[4], data }.  For a
  * quantized type ne[0] is the row length in weights and must be a multiple
@@ -120,7 +127,8 @@ size_t qmm_buffer_size(const qmm_buffer * buf);
 /* device address of the buffer (for harnesses that share device memory) */
 void * qmm_buffer_base(const qmm_buffer * buf);
 
-/* bytes a contiguous tensor of this type and shape occupies on the device */
+/* bytes a contiguous tensor of this type and shape occupies on the device:
+ * rows in tiles of 64, the K axis in groups of 256 weights, zero padding */
 size_t qmm_tensor_alloc_size(int32_t type, const int64_t ne[4]);
 /* bytes of the GGUF layout (ggml_nbytes of a contiguous tensor) */
 size_t qmm_tensor_nbytes(int32_t type, const int64_t ne[4]);
@@ -132,6 +140,12 @@ int    qmm_type_block(int32_t type, size_t * block_bytes);
  * Both are synchronous with respect to the host buffer. */
 int    qmm_tensor_set(qmm_ctx * ctx, const qmm_tensor * t, const void * data, size_t offset, size_t size);
 int    qmm_tensor_get(qmm_ctx * ctx, const qmm_tensor * t, void * data, size_t offset, size_t size);
+/* Host only, no device: the device image (qmm_tensor_alloc_size bytes) of a
+ * whole contiguous quantized tensor from its GGUF bytes, and back.  Copying
+ * the image to the tensor's device address equals qmm_tensor_set of all of
+ * its bytes. */
+int    qmm_tensor_pack(int32_t type, const int64_t ne[4], const void * gguf, void * image, size_t image_size);
+int    qmm_tensor_unpack(int32_t type, const int64_t ne[4], const void * image, void * gguf, size_t gguf_size);
 
 /* ---- ops --------------------------------------------------------------- */
 /* 1 when the op is taken; otherwise 0 and, if reason != NULL, why. */
@@ -163,15 +177,32 @@ int64_t qmm_downgrades(qmm_ctx * ctx, char * buf, size_t buf_len);
 /* Name of the kernel path the last mul_mat / mul_mat_id took. */
 const char * qmm_last_path(qmm_ctx * ctx);
 
+/* The launch a qmm_mul_mat with these tensors would make (host only, no
+ * device, no buffers needed: only types and shapes are read). */
+typedef struct qmm_launch_info {
+    char    path[32];          /* "gemv" or "gemm-mfma" */
+    int64_t workgroups;
+    int32_t threads;           /* per work-group */
+    int32_t cols_per_task;     /* GEMV: activation columns per weight pass */
+    int64_t tasks;
+    int32_t k_waves;           /* GEMV: waves per work-group, splitting K */
+    int32_t k_slices;          /* GEMV: work-groups per 64-row tile, splitting K */
+    int32_t groups_per_wave;   /* GEMV: 256-weight groups per wave */
+    int64_t lds_bytes;         /* dynamic LDS per work-group */
+} qmm_launch_info;
+int    qmm_describe_mul_mat(const qmm_tensor * src0, const qmm_tensor * src1, const qmm_tensor * dst,
+                            qmm_launch_info * out);
+
 /* HIP events on the context's stream: begin records, end records and waits,
  * returning the elapsed milliseconds (device time between the two). */
 int    qmm_timer_begin(qmm_ctx * ctx);
 float  qmm_timer_end(qmm_ctx * ctx);
 
 /* Per-kernel device time of the main kernel of every op (the GEMV / GEMM,
- * not the activation pre-pass): enable(1) clears and starts recording a HIP
- * event pair around each such launch on the context's stream; read waits for
- * the stream and returns the summed milliseconds and the launch count. */
+ * not the activation pre-pass): enable(1) clears and starts stamping a HIP
+ * event pair with each such kernel's own start and end (the dispatch itself,
+ * as a profiler reports it); read waits for the stream and returns the summed
+ * milliseconds and the launch count. */
 int    qmm_kernel_timing(qmm_ctx * ctx, int enable);
 int    qmm_kernel_time(qmm_ctx * ctx, double * total_ms, int64_t * launches);
 

@@ -1,0 +1,233 @@
+"""The device weight image (host side, CPU only).
+
+* pack/unpack round trips for every type, ragged row counts, partial 256-weight
+  groups (Q4_0/Q8_0) and several matrices;
+* the placement of every GGUF byte, checked against an independent statement
+  of the layout (tile of 64 rows, group of 256 weights, 1 KB chunk planes);
+* a numpy emulation of the GEMV kernel's per-chunk arithmetic on the packed
+  image (which nibble meets which activation code, where each scale comes
+  from), compared with the CPU oracle's ggml-cpu dot products;
+* the GEMV launch plan: the waves cover the K axis, no work-group is left
+  without groups, and the LDS of the cross-wave sum is what the plan says.
+"""
+import numpy as np
+import pytest
+
+from arcint_amd import qmm, synth
+from conftest import rel_err
+
+TYPES = [qmm.Q4_0, qmm.Q8_0, qmm.Q4_K, qmm.Q6_K, qmm.IQ4_XS]
+# type -> (chunk planes, tail bytes per row)
+PLANES = {qmm.Q4_0: (9, 0), qmm.Q8_0: (17, 0), qmm.Q4_K: (9, 0), qmm.Q6_K: (13, 2), qmm.IQ4_XS: (8, 8)}
+
+
+def shapes(qtype):
+    blck, _ = synth.BLOCK[qtype]
+    out = [(256 * 2, 64, 1), (256 * 3, 130, 1), (512, 7, 3), (1024, 64, 2)]
+    if blck == 32:
+        out += [(32 * 11, 65, 1), (32 * 9, 3, 2)]          # partial last group
+    return out
+
+
+def tg_bytes(qtype):
+    nch, tail = PLANES[qtype]
+    return nch * 1024 + 64 * tail
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+def test_pack_unpack_roundtrip(qtype):
+    for K, M, E in shapes(qtype):
+        raw = synth.weights(qtype, M * E, K, seed=K + M)
+        img = qmm.pack(qtype, (K, M, E), raw)
+        assert img.nbytes == qmm.alloc_size(qtype, (K, M, E))
+        assert img.nbytes % 256 == 0
+        assert np.array_equal(qmm.unpack(qtype, (K, M, E), img), raw)
+
+
+def expected_pieces(qtype, p):
+    """(src offset in the block, size, chunk, byte in the chunk row, tail?) for block slot p"""
+    if qtype == qmm.Q4_0:
+        return [(2, 16, p, 0, False), (0, 2, 8, 2 * p, False)]
+    if qtype == qmm.Q8_0:
+        return [(2, 16, 2 * p, 0, False), (18, 16, 2 * p + 1, 0, False), (0, 2, 16, 2 * p, False)]
+    if qtype == qmm.Q4_K:
+        return [(16 + 16 * c, 16, c, 0, False) for c in range(8)] + [(0, 16, 8, 0, False)]
+    if qtype == qmm.Q6_K:
+        return ([(16 * c, 16, c, 0, False) for c in range(8)] + [(128 + 16 * c, 16, 8 + c, 0, False) for c in range(4)]
+                + [(192, 16, 12, 0, False), (208, 2, None, 0, True)])
+    return [(8 + 16 * c, 16, c, 0, False) for c in range(8)] + [(0, 8, None, 0, True)]
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+def test_pack_placement(qtype):
+    blck, bb = synth.BLOCK[qtype]
+    bpg = 256 // blck
+    nch, tail = PLANES[qtype]
+    tg = tg_bytes(qtype)
+    for K, M, E in shapes(qtype):
+        raw = synth.weights(qtype, M * E, K, seed=7 + K).reshape(E, M, K // blck, bb)
+        img = qmm.pack(qtype, (K, M, E), raw.ravel())
+        G, nt = -(-K // 256), -(-M // 64)
+        g = np.random.default_rng(K + M)
+        for _ in range(200):
+            e, m, kb = int(g.integers(E)), int(g.integers(M)), int(g.integers(K // blck))
+            t, r, grp, p = m // 64, m % 64, kb // bpg, kb % bpg
+            base = ((e * nt + t) * G + grp) * tg
+            for src, size, chunk, off, is_tail in expected_pieces(qtype, p):
+                at = base + (nch * 1024 + r * tail if is_tail else chunk * 1024 + r * 16 + off)
+                assert np.array_equal(img[at:at + size], raw[e, m, kb, src:src + size]), (e, m, kb, src)
+        # padding rows and padding blocks are zero
+        used = np.zeros(img.nbytes, bool)
+        for e in range(E):
+            for m in range(M):
+                t, r = m // 64, m % 64
+                for kb in range(K // blck):
+                    grp, p = kb // bpg, kb % bpg
+                    base = ((e * nt + t) * G + grp) * tg
+                    for src, size, chunk, off, is_tail in expected_pieces(qtype, p):
+                        at = base + (nch * 1024 + r * tail if is_tail else chunk * 1024 + r * 16 + off)
+                        used[at:at + size] = True
+        assert not img[~used].any()
+        assert used.sum() == raw.size
+
+
+# ---------------------------------------------------------------- kernel arithmetic on the image
+def image_planes(qtype, img, K, M):
+    """chunks [M, G, nchunk, 16] and tail [M, G, tail] of a single matrix"""
+    nch, tail = PLANES[qtype]
+    tg = tg_bytes(qtype)
+    G, nt = -(-K // 256), -(-M // 64)
+    a = img[:nt * G * tg].reshape(nt, G, tg)
+    ch = a[:, :, :nch * 1024].reshape(nt, G, nch, 64, 16).transpose(0, 3, 1, 2, 4).reshape(nt * 64, G, nch, 16)[:M]
+    tl = None
+    if tail:
+        tl = a[:, :, nch * 1024:nch * 1024 + 64 * tail].reshape(nt, G, 64, tail).transpose(0, 2, 1, 3)
+        tl = tl.reshape(nt * 64, G, tail)[:M]
+    return ch.astype(np.int64), tl
+
+
+def f16(lo, hi):
+    return (lo.astype(np.uint16) | (hi.astype(np.uint16) << 8)).view(np.float16).astype(np.float32)
+
+
+def q8_parts(orc, qtype, x):
+    """codes [K], d per block, sums per (16 or 32) from the oracle's quantizer"""
+    K = x.size
+    q = orc.quantize_act(qtype, x)
+    if orc.TYPES[qtype][2] == orc.Q8_0:
+        b = q.reshape(K // 32, 34)
+        return b[:, 2:].view(np.int8).astype(np.int64).ravel(), f16(b[:, 0], b[:, 1]), None
+    b = q.reshape(K // 256, 292)
+    d = b[:, :4].copy().view(np.float32).ravel()
+    codes = b[:, 4:260].copy().view(np.int8).astype(np.int64).ravel()
+    bsums = b[:, 260:].copy().view(np.int16).astype(np.int64).ravel()
+    return codes, d, bsums
+
+
+def emulate_gemv(qtype, img, K, M, codes, xd, bsums):
+    ch, tl = image_planes(qtype, img, K, M)
+    G = ch.shape[1]
+    Kp = G * 256
+    xc = np.zeros(Kp, np.int64)
+    xc[:K] = codes
+    xg = xc.reshape(G, 256)
+    acc = np.zeros(M, np.float64)
+    lo, hi = ch & 15, ch >> 4
+    if qtype in (qmm.Q4_0, qmm.Q8_0):
+        nb = K // 32
+        xdp = np.zeros(G * 8, np.float32)
+        xdp[:nb] = xd
+        xdp = xdp.reshape(G, 8)
+        for p in range(8):
+            dw = f16(ch[:, :, 16 if qtype == qmm.Q8_0 else 8, 2 * p], ch[:, :, 16 if qtype == qmm.Q8_0 else 8, 2 * p + 1])
+            xa, xb = xg[:, 32 * p:32 * p + 16], xg[:, 32 * p + 16:32 * p + 32]
+            if qtype == qmm.Q4_0:
+                s = (lo[:, :, p] * xa).sum(-1) + (hi[:, :, p] * xb).sum(-1) - 8 * (xa.sum(-1) + xb.sum(-1))
+            else:
+                w0 = ch[:, :, 2 * p].astype(np.uint8).view(np.int8).astype(np.int64)
+                w1 = ch[:, :, 2 * p + 1].astype(np.uint8).view(np.int8).astype(np.int64)
+                s = (w0 * xa).sum(-1) + (w1 * xb).sum(-1)
+            acc += (s * (dw * xdp[:, p])).sum(-1)
+        return acc
+    bs = bsums.reshape(G, 16)
+    if qtype == qmm.Q4_K:
+        h = ch[:, :, 8].astype(np.uint8)
+        d, dmin = f16(h[..., 0], h[..., 1]), f16(h[..., 2], h[..., 3])
+        w = h.view(np.uint32).astype(np.uint64)             # [M, G, 4] dwords
+        sc03, mn03 = w[..., 1] & 0x3f3f3f3f, w[..., 2] & 0x3f3f3f3f
+        sc47 = (w[..., 3] & 0x0f0f0f0f) | ((w[..., 1] >> 2) & 0x30303030)
+        mn47 = ((w[..., 3] >> 4) & 0x0f0f0f0f) | ((w[..., 2] >> 2) & 0x30303030)
+        sc = [((sc03 >> (8 * i)) & 255) for i in range(4)] + [((sc47 >> (8 * i)) & 255) for i in range(4)]
+        mn = [((mn03 >> (8 * i)) & 255) for i in range(4)] + [((mn47 >> (8 * i)) & 255) for i in range(4)]
+        isc = np.zeros(d.shape, np.int64)
+        for c in range(8):
+            jl, xo = 2 * (c // 2), 64 * (c // 2) + 16 * (c % 2)
+            sl = (lo[:, :, c] * xg[:, xo:xo + 16]).sum(-1)
+            sh = (hi[:, :, c] * xg[:, xo + 32:xo + 48]).sum(-1)
+            isc += sc[jl].astype(np.int64) * sl + sc[jl + 1].astype(np.int64) * sh
+        imn = sum(mn[i].astype(np.int64) * (bs[:, 2 * i] + bs[:, 2 * i + 1]) for i in range(8))
+        return (xd * (d * isc - dmin * imn)).sum(-1)
+    if qtype == qmm.Q6_K:
+        d = f16(tl[..., 0], tl[..., 1])
+        scs = ch[:, :, 12].astype(np.uint8).view(np.int8).astype(np.int64)
+        isum = np.zeros(d.shape, np.int64)
+        for n in range(2):
+            for lh in range(2):
+                qh = ch[:, :, 8 + 2 * n + lh]
+                for g in range(4):
+                    ql = ch[:, :, 4 * n + 2 * (g & 1) + lh]
+                    code = ((ql >> (0 if g < 2 else 4)) & 15) | (((qh >> (2 * g)) & 3) << 4)
+                    is_ = 8 * n + 2 * g + lh
+                    xo = 128 * n + 32 * g + 16 * lh
+                    s = (code * xg[:, xo:xo + 16]).sum(-1) - 32 * bs[:, is_]
+                    isum += scs[:, :, is_] * s
+        return ((d * xd) * isum).sum(-1)
+    # IQ4_XS
+    kv = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], np.int64)
+    dw = f16(tl[..., 0], tl[..., 1])
+    tl = tl.astype(np.int64)
+    shi = tl[..., 2] | (tl[..., 3] << 8)
+    slo = tl[..., 4] | (tl[..., 5] << 8) | (tl[..., 6] << 16) | (tl[..., 7] << 24)
+    isum = np.zeros(dw.shape, np.int64)
+    for ib in range(8):
+        ls = ((slo >> (4 * ib)) & 15) | (((shi >> (2 * ib)) & 3) << 4)
+        s = (kv[lo[:, :, ib]] * xg[:, 32 * ib:32 * ib + 16]).sum(-1) + (kv[hi[:, :, ib]] * xg[:, 32 * ib + 16:32 * ib + 32]).sum(-1)
+        isum += (ls - 32) * s
+    return ((dw * xd) * isum).sum(-1)
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+def test_gemv_arithmetic_on_image(orc, qtype):
+    blck, _ = synth.BLOCK[qtype]
+    for K, M in [(1024, 70), (512, 64)] + ([(32 * 13, 65)] if blck == 32 else []):
+        raw = synth.weights(qtype, M, K, seed=3 + K)
+        x = synth.activations(1, K, seed=4 + K)
+        img = qmm.pack(qtype, (K, M), raw)
+        codes, xd, bsums = q8_parts(orc, qtype, x[0])
+        got = emulate_gemv(qtype, img, K, M, codes, xd, bsums)
+        ref = orc.mul_mat(qtype, raw, M, K, x)[0]
+        assert rel_err(got, ref) <= 1e-5, qtype
+
+
+# ---------------------------------------------------------------- launch plan
+PLAN_SHAPES = [
+    (qmm.Q4_K, 5120, 17408, 1), (qmm.Q4_K, 5120, 17408, 4), (qmm.Q6_K, 17408, 5120, 1), (qmm.Q6_K, 5120, 151936, 1),
+    (qmm.Q4_0, 4096, 4096, 1), (qmm.Q4_0, 11008, 4096, 8), (qmm.Q8_0, 4096, 14336, 8), (qmm.IQ4_XS, 14336, 4096, 2),
+    (qmm.Q4_0, 352, 65, 3), (qmm.Q4_K, 256, 1, 1), (qmm.Q8_0, 32, 5, 8), (qmm.IQ4_XS, 512, 2048, 5),
+]
+
+
+@pytest.mark.parametrize("qtype,K,M,N", PLAN_SHAPES)
+def test_gemv_plan(qtype, K, M, N):
+    fake = qmm.Buffer(ptr=0x1000, size=1 << 44)
+    info = qmm.describe_mul_mat(qmm.Tensor(fake, qtype, (K, M)), qmm.Tensor(fake, qmm.F32, (K, N)),
+                                qmm.Tensor(fake, qmm.F32, (M, N)))
+    assert info["path"] == "gemv"
+    G, nt = -(-K // 256), -(-M // 64)
+    W, KS, spw, nc = info["k_waves"], info["k_slices"], info["groups_per_wave"], info["cols_per_task"]
+    assert 1 <= W <= 8 and KS >= 1 and spw >= 1 and info["threads"] == 64 * W
+    assert KS * W * spw >= G                             # the waves cover K
+    assert (KS - 1) * W * spw < G                        # no work-group without groups
+    assert info["tasks"] == -(-N // nc)
+    assert info["workgroups"] == info["tasks"] * nt * KS
+    assert info["lds_bytes"] == (W * nc * 64 * 4 if W > 1 else 0)
