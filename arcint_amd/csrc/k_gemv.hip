@@ -21,8 +21,10 @@
 //    device-scope fences, whose L2 write-backs would cost more than the whole
 //    product;
 //  * D stages of weight loads are in flight per wave in a register ring whose
-//    loads are unconditional (a stage past the end reloads the last one), so
-//    every wait is for a known load.
+//    loads are unconditional, so every wait is for a known load; a slot
+//    refilled past the last stage reads a small L2-resident sink buffer
+//    instead (re-reading real weights would go back to HBM: the weight loads
+//    are non-temporal).
 // A task is up to NC activation columns against one weight matrix; dense
 // MUL_MAT derives tasks from the work-group index, MUL_MAT_ID reads
 // device-built task lists.
@@ -48,6 +50,7 @@ struct GemvParams {
     int64_t ne11, ne12, r2, r3, ne02, tpb;
     int64_t d_nb1, d_nb2, d_nb3; // dst strides in floats
     float * dst;
+    const uint8_t * sink;        // >= kSinkBytes of readable memory for loads past the end
     int W;                       // waves per work-group
     int KS;                      // work-groups per tile (K slices); > 1: atomics into zeroed dst
     int spw;                     // groups per wave
@@ -371,9 +374,9 @@ __global__ __launch_bounds__(512) void k_gemv(GemvParams p) {
     }
     if (S > 0) {
         uint4 B[D][NL];
-        auto load_stage = [&](uint4 * b, int s) {
-            const int sc = s < S ? s : S - 1;
-            T::load(b, tbase + (size_t)(ga + sc / NST) * tgs, sc % NST, lane);
+        auto load_stage = [&](uint4 * b, int s) {             // past the end: the sink
+            const uint8_t * tg = s < S ? tbase + (size_t)(ga + s / NST) * tgs : p.sink;
+            T::load(b, tg, s < S ? s % NST : 0, lane);
         };
 #pragma unroll
         for (int i = 0; i < D; ++i) load_stage(B[i], i);
@@ -476,9 +479,9 @@ bool gemv_plan(int type, const WView & w, int nc, int64_t ntasks, bool allow_spl
 }
 
 hipError_t launch_gemv(int type, const WView & w, const GemvPlan & pl, const ActBuf & a, const GemvTask * tasks,
-                       const int32_t * ntasks_dev, const GemvDense * dense, float * dst, hipStream_t s,
-                       const KTime * kt) {
-    if ((!tasks && !dense) || pl.W < 1 || pl.W > 8 || pl.KS < 1 || pl.spw < 1 || a.ldk != w.G * 256 ||
+                       const int32_t * ntasks_dev, const GemvDense * dense, float * dst, const void * sink,
+                       hipStream_t s, const KTime * kt) {
+    if (!sink || (!tasks && !dense) || pl.W < 1 || pl.W > 8 || pl.KS < 1 || pl.spw < 1 || a.ldk != w.G * 256 ||
         a.vdt != vec_dot_type(type))
         return hipErrorInvalidValue;
     GemvParams p{};
@@ -490,6 +493,7 @@ hipError_t launch_gemv(int type, const WView & w, const GemvPlan & pl, const Act
     p.tasks = tasks;
     p.ntasks_dev = ntasks_dev;
     p.dst = dst;
+    p.sink = (const uint8_t *)sink;
     p.W = pl.W;
     p.KS = pl.KS;
     p.spw = pl.spw;

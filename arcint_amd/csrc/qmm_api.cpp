@@ -23,6 +23,7 @@ struct qmm_buffer {
 struct qmm_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
+    void * sink = nullptr;           // kSinkBytes of zeros the GEMV reads past the end of its pipeline
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     std::string err;
     std::string path = "none";
@@ -255,8 +256,10 @@ int qmm_ctx_create(int device, qmm_ctx ** out) {
     qmm_ctx * ctx = new qmm_ctx();
     ctx->device = device;
     if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess ||
-        hipEventCreate(&ctx->ev0) != hipSuccess || hipEventCreate(&ctx->ev1) != hipSuccess) {
-        delete ctx;
+        hipEventCreate(&ctx->ev0) != hipSuccess || hipEventCreate(&ctx->ev1) != hipSuccess ||
+        hipMalloc(&ctx->sink, kSinkBytes) != hipSuccess || hipMemsetAsync(ctx->sink, 0, kSinkBytes, ctx->stream) != hipSuccess ||
+        hipStreamSynchronize(ctx->stream) != hipSuccess) {
+        qmm_ctx_free(ctx);
         return QMM_ERR_DEVICE;
     }
     *out = ctx;
@@ -269,6 +272,7 @@ void qmm_ctx_free(qmm_ctx * ctx) {
     if (ctx->stream) hipStreamSynchronize(ctx->stream);
     if (ctx->act) hipFree(ctx->act);
     if (ctx->route) hipFree(ctx->route);
+    if (ctx->sink) hipFree(ctx->sink);
     for (hipEvent_t e : ctx->kev) (void)hipEventDestroy(e);
     if (ctx->ev0) hipEventDestroy(ctx->ev0);
     if (ctx->ev1) hipEventDestroy(ctx->ev1);
@@ -587,7 +591,7 @@ int qmm_mul_mat(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1,
     KTime kt;
     const KTime * ktp;
     if ((rc = ktime_pair(ctx, &kt, &ktp))) return rc;
-    QMM_HIP(ctx, launch_gemv(src0->type, w, plan, a, nullptr, nullptr, &dn, d, ctx->stream, ktp));
+    QMM_HIP(ctx, launch_gemv(src0->type, w, plan, a, nullptr, nullptr, &dn, d, ctx->sink, ctx->stream, ktp));
     return QMM_OK;
 }
 
@@ -633,7 +637,7 @@ int qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * sr
     KTime kt;
     const KTime * ktp;
     if ((rc = ktime_pair(ctx, &kt, &ktp))) return rc;
-    QMM_HIP(ctx, launch_gemv(src0->type, w, plan, a, tasks, ntasks, nullptr, d, ctx->stream, ktp));
+    QMM_HIP(ctx, launch_gemv(src0->type, w, plan, a, tasks, ntasks, nullptr, d, ctx->sink, ctx->stream, ktp));
     return QMM_OK;
 }
 

@@ -169,9 +169,12 @@ bool gemv_plan(int type, const WView & w, int nc, int64_t ntasks, bool allow_spl
 // the pre-pass activations `a` (ldk == 256 * groups).  List mode (tasks !=
 // nullptr): `ntasks_dev` (optional) bounds the task list on the device.
 // Dense mode (tasks == nullptr): tasks of up to nc columns from `dense`.
+// `sink`: kSinkBytes of device memory the kernel may read (not write) for
+// loads past the end of its pipeline.
+constexpr size_t kSinkBytes = 32768;
 hipError_t launch_gemv(int type, const WView & w, const GemvPlan & plan, const ActBuf & a, const GemvTask * tasks,
-                       const int32_t * ntasks_dev, const GemvDense * dense, float * dst, hipStream_t s,
-                       const KTime * kt = nullptr);
+                       const int32_t * ntasks_dev, const GemvDense * dense, float * dst, const void * sink,
+                       hipStream_t s, const KTime * kt = nullptr);
 
 // Prefill GEMM (int8 MFMA): for every batch b < nbatch, dst[doff(b) + n * d_nb1
 // + m] = W(mat(b)) row m . activation column col0(b) + n, for n < N, m < M.

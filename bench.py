@@ -79,14 +79,14 @@ def time_op(be, ws, xt, yt, steps, warmup):
 
 
 def profile_traffic(kernel_tag):
-    """HBM bytes per launch from the committed rocprofv3 PMC summary, if any."""
+    """HBM bytes per launch of a kernel from the committed rocprofv3 PMC runs
+    (FETCH_SIZE and WRITE_SIZE, each scaled by what the counter reads for the
+    runtime's copy kernel of known size), or None."""
     p = os.path.join(ROOT, "profiles", "traffic.json")
-    if not os.path.exists(p):
-        return None
     try:
         d = json.load(open(p))
-        return d.get(kernel_tag)
-    except (OSError, ValueError):
+        return d[kernel_tag]["traffic_bytes"]
+    except (OSError, ValueError, KeyError, TypeError):
         return None
 
 
