@@ -379,8 +379,22 @@ hipError_t launch_t(GemmParams p, int64_t nbatch, hipStream_t s, const KTime * k
 
 }  // namespace
 
+// QMM_GEMM_V1=1 keeps every type on the 16x16x32 kernel below
+bool gemm_uses_v2(int type) {
+    static const bool v1 = [] {
+        const char * e = getenv("QMM_GEMM_V1");
+        return e && atoi(e) != 0;
+    }();
+    return !v1 && gemm2_supported(type);
+}
+
+int gemm_kslices(int type, const WView & w, int64_t N, int64_t nbatch) {
+    return gemm_uses_v2(type) ? gemm2_kslices(w, N, nbatch) : 1;
+}
+
 hipError_t launch_gemm(int type, const WView & w, const ActBuf & a, int64_t N, int64_t nbatch,
                        const GemmBatch & bt, float * dst, hipStream_t s, const KTime * kt) {
+    if (gemm_uses_v2(type)) return launch_gemm2(type, w, a, N, nbatch, bt, dst, s, kt);
     const int64_t M = w.M, K = w.K;
     if (!a.dT || a.ldT < N * nbatch + 64 || K % 32 || M <= 0 || N <= 0 || nbatch <= 0 || a.K != K)
         return hipErrorInvalidValue;

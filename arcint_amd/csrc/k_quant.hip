@@ -53,7 +53,7 @@ __global__ void k_quant_q8_0(F32Cols src, int64_t K, int64_t ncols, ActBuf a, Ze
         const int64_t b = c * (a.ldk / 32) + k / 32;
         a.d[b] = d;
         a.sums[b] = (int16_t)s;
-        if (a.dT && k < K) a.dT[(k / 32) * a.ldT + c] = d;
+        if (a.dT) a.dT[(k / 32) * a.ldT + c] = d;            // padding blocks: d = 0
     }
 }
 
@@ -80,7 +80,7 @@ __global__ void k_quant_q8_K(F32Cols src, int64_t K, int64_t ncols, ActBuf a, Ze
     if ((lane & 3) == 0) a.sums[c * (a.ldk / 16) + sb * 16 + (lane >> 2)] = (int16_t)s;
     if (lane == 0) {
         a.d[c * nsb + sb] = d;
-        if (a.dT && sb * 256 < K) a.dT[sb * a.ldT + c] = d;
+        if (a.dT) a.dT[sb * a.ldT + c] = d;
     }
 }
 

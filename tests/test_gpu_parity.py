@@ -298,7 +298,8 @@ def test_full_size_gemv(be, sc, orc, qtype, M, K, N):
 
 # ------------------------------------------------------------------ MFMA GEMM (N >= 16)
 @pytest.mark.parametrize("qtype", TYPES)
-@pytest.mark.parametrize("M,K,N", [(300, 1024, 16), (129, 2048, 37), (64, 512, 64), (500, 768, 130)])
+@pytest.mark.parametrize("M,K,N", [(300, 1024, 16), (129, 2048, 37), (64, 512, 64), (500, 768, 130),
+                                   (200, 256, 40), (70, 800, 20), (1000, 512, 300)])
 def test_mul_mat_gemm(be, sc, orc, qtype, M, K, N):
     if K % 256 and qtype not in (qmm.Q4_0, qmm.Q8_0):
         K = 1024
@@ -308,9 +309,10 @@ def test_mul_mat_gemm(be, sc, orc, qtype, M, K, N):
     assert rel_err(got, ref) <= TOL
 
 
-def test_mul_mat_gemm_broadcast_and_strides(be, sc, orc):
-    say("gemm-broadcast")
-    qtype, K, M, N = qmm.Q6_K, 512, 80, 21
+@pytest.mark.parametrize("qtype", [qmm.Q6_K, qmm.Q4_K, qmm.Q4_0])
+def test_mul_mat_gemm_broadcast_and_strides(be, sc, orc, qtype):
+    say("gemm-broadcast", qtype)
+    K, M, N = 512, 80, 21
     raw = synth.weights(qtype, 2 * M, K, seed=64)
     w = sc.weights(qtype, raw, (K, M, 2))
     x = synth.activations(4 * N, K, seed=65).reshape(4, N, K)
