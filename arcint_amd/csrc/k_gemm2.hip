@@ -4,27 +4,31 @@
 // Role of the reference's int8 prefill GEMMs (kernel_mul_mm_kq2d_q4_0_i8,
 // P0099:377-455, and kernel_mul_mm_kq2d_q4_K_i8, P01:1919-2024), redesigned
 // for CDNA4 and for ggml-cpu's numerics:
-//  * a work-group owns 128 weight rows (two 64-row tiles of the weight image)
-//    x 128 activation columns and walks K in stages of 128 (half a group);
-//    per stage it stages in LDS the activation codes of its columns (a padded
-//    pitch spreads the rows over the banks), the stage's chunk planes of its
-//    two tiles (as laid out in HBM: the 16 bytes of a row are one MFMA
-//    operand) and the activation scales, double-buffered one stage ahead;
-//  * each of the 4 waves computes 64 rows x 64 columns as 2 x 2 MFMA tiles
-//    of 32 x 32, one 32-weight (sub-)block per MFMA.  Both operands place
-//    k in [16h, 16h + 16) of the block in lane half h, so the int32 result is
-//    the block's exact integer dot, as in ggml_vec_dot_*;
-//  * Q4_0: the weight operand is q - 8 (bytewise), and the float combine of
-//    every block, acc += (float)dot * (d_w * d_x), runs on the VALU as in
-//    ggml's vec_dot_q4_0_q8_0;
+//  * a work-group (8 waves) owns 128 weight rows (two 64-row tiles of the
+//    weight image) x BN activation columns (BN = 128 or 64) and walks K in
+//    stages of 128 (half a group).  Per stage it stages in LDS the activation
+//    codes of its columns (a padded pitch spreads the columns over the banks),
+//    its two tiles' weights unpacked into MFMA operands (once per work-group,
+//    not once per wave) and the scales; the data of a stage is fetched two
+//    stages ahead into registers and stored at the end of the stage before;
+//  * a wave computes 64 rows x 32 columns as 2 MFMA tiles of 32 x 32, one
+//    32-weight (sub-)block per MFMA.  Both operands place k in [16h, 16h + 16)
+//    of the block in lane half h, so the int32 result is the block's exact
+//    integer dot, as in ggml_vec_dot_*.  With BN = 64 two waves share each
+//    tile, one taking blocks 0 and 2 of every stage and the other blocks 1
+//    and 3, and their sums meet in LDS at the end (no atomics);
+//  * Q4_0: the weight operand is q - 8.  The MFMA adds the block's dot i to
+//    the bits of the float 12582912 (= 1.5 * 2^23), so fma(result, d_w,
+//    -12582912 d_w) is i * d_w rounded once (12582912 d_w is exact), and
+//    acc += d_x * that: two VALU ops per output and block;
 //  * Q4_K: the 6-bit sub-block scale sc = 8 sh + sl is folded into two int8
 //    operands q * sh and q * sl (a packed 16-bit multiply scales 4 codes at
-//    once; every product is < 128), and the min term is a third MFMA against
-//    the sub-block's min replicated (m * sum of the block's codes), so the
-//    whole super-block accumulates inside the MFMA in int32 and the float
-//    combine runs once per 256 weights;
+//    once; every product is < 128), so the scale part of a super-block
+//    accumulates inside the MFMA in int32.  The min term sum_j m_j bsum_j
+//    takes two MFMAs per super-block: the activation sub-block sums split as
+//    bsum = 64 bh + bl (bh in [-64, 63], bl in [0, 63]) against the 8 mins;
 //  * work-groups are numbered so that those sharing weight rows land on the
-//    same XCD; short matrices split K over KS work-groups that add their
+//    same XCD.  Small products split K over KS work-groups that add their
 //    partial sums to dst (zeroed by the activation pre-pass) atomically.
 // MFMA output layout: lane l holds D[8 (r/4) + 4 (l/32) + r%4][l % 32] in
 // accumulator register r.
@@ -40,16 +44,34 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
 
 constexpr int kT = 512;                  // threads per work-group (8 waves)
-constexpr int kBN = 128;                 // activation columns per work-group
 constexpr int kSK = 128;                 // k per stage
 constexpr int kAP = kSK + 16;            // LDS pitch of one column's codes
-constexpr int kAB = kBN * kAP;           // A stage bytes
-constexpr int kBB = 2 * 5 * kChunk;      // B stage bytes: 2 tiles x (4 code chunks + header)
-constexpr int kXB = 4 * kBN * 4;         // scale stage bytes (4 blocks x 128 columns, f32)
-constexpr int kStage = kAB + kBB + kXB;  // 30720
+constexpr int kMagic = 0x4B400000;       // float 12582912: its bits + i are the float 12582912 + i, |i| < 2^22
+
+// LDS stage layout (bytes):
+//   A  [col BN][kAP]                                 activation codes
+//   Q4_0  B  [tile 2][block 4][h 2][row 64] x 16 B    q - 8
+//         W  [tile 2][block 4][row 64] f32            d_w
+//         X  [block 4][col BN] f32                    d_x
+//   Q4_K  B  [tile 2][sub 4][h 2][hi/lo 2][row 64] x 16 B   q * sh, q * sl
+//         W  [tile 2][row 64] x 16 B                  the super-block's 8 mins, then 8 zero bytes
+//            [tile 2][row 64] float2                  (d, dmin)
+//         X  [col BN] f32                             d_x of the super-block
+//         S  [col BN] x 16 B                          bh[8], bl[8] of the super-block
+template <int TYPE, int BN> struct Lay {
+    static constexpr bool KQ = TYPE == QMM_TYPE_Q4_K;
+    static constexpr int A = BN * kAP;
+    static constexpr int B = KQ ? 2 * 4 * 2 * 2 * kChunk : 2 * 4 * 2 * kChunk;
+    static constexpr int W = KQ ? 2 * 64 * 16 + 2 * 64 * 8 : 2 * 4 * 64 * 4;
+    static constexpr int X = KQ ? BN * 4 : 4 * BN * 4;
+    static constexpr int S = KQ ? BN * 16 : 0;
+    static constexpr int oB = A, oW = oB + B, oX = oW + W, oS = oX + X;
+    static constexpr int stage = oS + S;
+};
 
 struct G2Params {
     WView w;
@@ -57,13 +79,23 @@ struct G2Params {
     int64_t ldk;
     const float * dT;                    // activation scales [block][ldT]
     int64_t ldT;
+    const int8_t * bsp;                  // q8_K: split sub-block sums [super-block][ldT] x 16 B
     int64_t N;                           // columns per batch
-    int64_t mt, nt;                      // work-group tiles along M (128 rows) and N (128 columns)
+    int64_t mt, nt;                      // work-group tiles along M (128 rows) and N (BN columns)
     int64_t chunk;                       // work-groups per XCD (numbering)
     int KS, spk;                         // K slices, stages per slice
     int64_t nst;                         // stages along K (2 per group)
     GemmBatch bt;
     float * dst;
+};
+
+// one stage of staged data in flight (per thread)
+struct StageRegs {
+    uint4 a[2];                          // activation codes: up to 2 units of 16 B
+    uint4 c;                             // weight code chunk (16 B of one row)
+    uint4 h;                             // that row's header (Q4_0: .x = the dword with the block's d)
+    uint4 s;                             // Q4_K: the column's split sub-block sums
+    float x;                             // one activation scale
 };
 
 __device__ __forceinline__ uint32_t v2_mul(uint32_t v, uint32_t s) {   // 4 bytes x s, no carries (products < 256)
@@ -72,195 +104,327 @@ __device__ __forceinline__ uint32_t v2_mul(uint32_t v, uint32_t s) {   // 4 byte
     return __builtin_bit_cast(uint32_t, a * b);
 }
 
-template <int TYPE>
-__global__ __launch_bounds__(kT) void k_gemm2(G2Params p) {
-    constexpr bool KQ = TYPE == QMM_TYPE_Q4_K;
-    constexpr int UQ = KQ ? 4 : 1;                                // Q4_0: one block's products live at a time
+__device__ __forceinline__ uint32_t q4_minus8(uint32_t nib) {   // 4 codes 0..15 (one per byte) -> q - 8 as int8
+    return (((nib | 0x80808080u) - 0x08080808u) ^ 0x80808080u);
+}
+
+// Q4_K sub-block j's 6-bit scale and min from the 12 scale bytes y|z|w
+// (get_scale_min_k4, P01:2164-2176)
+__device__ __forceinline__ void q4k_scale_min(int j, uint32_t y, uint32_t z, uint32_t w, uint32_t * sc, uint32_t * mn) {
+    const int b8 = 8 * (j & 3);
+    if (j < 4) {
+        *sc = (y >> b8) & 63;
+        *mn = (z >> b8) & 63;
+    } else {
+        *sc = ((w >> b8) & 0xF) | (((y >> b8) >> 6 & 3) << 4);
+        *mn = ((w >> b8) >> 4 & 0xF) | (((z >> b8) >> 6 & 3) << 4);
+    }
+}
+
+template <int TYPE, int BN>
+__global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per SIMD: one work-group per CU
+    using LY = Lay<TYPE, BN>;
+    constexpr bool KQ = LY::KQ;
+    constexpr int NWN = BN / 32;                                  // column groups of 32
+    constexpr int KSPLIT = 4 / NWN;                               // waves sharing a tile (BN 128: 1, 64: 2)
+    constexpr int NQ = 4 / KSPLIT;                                // blocks per stage and wave
+    constexpr int NA = BN / 64;                                   // 16-byte code units per thread and stage
+    constexpr int kStage = LY::stage;
     extern __shared__ __align__(16) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int64_t bid = blockIdx.x;
-    const int64_t L = (bid & 7) * p.chunk + (bid >> 3);
-    if (L >= p.mt * p.nt * p.KS) return;                          // uniform
-    const int64_t ntile = L % p.nt, rest = L / p.nt;
-    const int ks = (int)(rest % p.KS);
-    const int64_t mtile = rest / p.KS;
-    const int64_t bz = blockIdx.y;
-    const int64_t i2 = bz % p.bt.ne12, i3 = bz / p.bt.ne12;
+    const uint32_t bid = blockIdx.x;                              // grid < 2^31 (host check)
+    const uint32_t L = (bid & 7) * (uint32_t)p.chunk + (bid >> 3);
+    if (L >= (uint32_t)(p.mt * p.nt * p.KS)) return;              // uniform
+    const uint32_t ntile = L % (uint32_t)p.nt, rest = L / (uint32_t)p.nt;
+    const int ks = (int)(rest % (uint32_t)p.KS);
+    const int64_t mtile = rest / (uint32_t)p.KS;
+    const uint32_t bz = blockIdx.y;
+    const int64_t i2 = bz % (uint32_t)p.bt.ne12, i3 = bz / (uint32_t)p.bt.ne12;
     const int64_t mat = i2 / p.bt.r2 + (i3 / p.bt.r3) * p.bt.ne02;
     const int64_t col0 = bz * p.N;                                // first activation column of the batch
-    const int64_t n0 = ntile * kBN;
+    const int64_t n0 = (int64_t)ntile * BN;
     const int s0 = ks * p.spk;
-    const int s1 = (int)((s0 + p.spk) < p.nst ? (s0 + p.spk) : p.nst);
+    const int s1 = (int)((s0 + p.spk) < p.nst ? (s0 + p.spk) : p.nst);   // s1 - s0 is even
 
-    // ---- staging of one stage: global -> registers (fetch), registers -> LDS (store)
-    constexpr int kNA = kBN * kSK / 16 / kT;                      // 16-byte code units per thread
-    constexpr int kNB = (kBB / 16 + kT - 1) / kT;                 // 16-byte weight units per thread
-    uint4 ra[kNA], rb[kNB];
-    float4 rx;
-    auto fetch = [&](int s) {
-        const int64_t g = s >> 1, hh = s & 1;
+    // ---- staging addresses.  Thread tid stages code chunk cs = (tid / 64) % 4 of row tid % 64 of
+    // tile tid / 256 (and reads that row's header), NA 16-byte units of activation codes, one
+    // activation scale and (Q4_K) one column's sums.  Columns past N are clamped to N - 1: they are
+    // computed and never stored.
+    const int st_tile = tid >> 8, st_cs = (tid >> 6) & 3, st_row = tid & 63;
+    int64_t st_img = 2 * mtile + st_tile;
+    st_img = st_img < p.w.ntiles ? st_img : p.w.ntiles - 1;      // a missing second tile re-reads the first
+    const uint8_t * wbase = tile_group(p.w, mat, st_img, 0) + st_row * 16;
+    const int8_t * abase[NA];
 #pragma unroll
-        for (int q = 0; q < kNA; ++q) {                           // codes: 128 columns x 8 units
-            const int u = tid + kT * q, c = u >> 3, un = u & 7;
-            ra[q] = make_uint4(0, 0, 0, 0);
-            if (n0 + c < p.N) ra[q] = *reinterpret_cast<const uint4 *>(p.xc + (col0 + n0 + c) * p.ldk + s * kSK + un * 16);
+    for (int q = 0; q < NA; ++q) {
+        const int u = tid + kT * q;
+        const int64_t c = std::min<int64_t>(n0 + (u >> 3), p.N - 1);
+        abase[q] = p.xc + (col0 + c) * p.ldk + (u & 7) * 16;
+    }
+    const int x_blk = KQ ? 0 : (tid / BN) & 3;                    // Q4_0: 4 blocks x BN columns
+    const int64_t x_col = col0 + std::min<int64_t>(n0 + tid % BN, p.N - 1);
+    const float * xbase = p.dT + x_col;
+    const int8_t * sbase = KQ ? p.bsp + x_col * 16 : nullptr;
+    auto fetch = [&](int s) -> StageRegs {
+        StageRegs R;
+        const int g = s >> 1, hh = s & 1;
+#pragma unroll
+        for (int q = 0; q < NA; ++q) R.a[q] = *reinterpret_cast<const uint4 *>(abase[q] + s * kSK);
+        const uint8_t * tg = wbase + (size_t)g * p.w.tg;
+        R.c = ld16(tg + (4 * hh + st_cs) * kChunk);
+        if constexpr (KQ) {
+            R.h = ld16(tg + 8 * kChunk);
+            R.s = *reinterpret_cast<const uint4 *>(sbase + (int64_t)g * p.ldT * 16);
+        } else {
+            R.h.x = *reinterpret_cast<const uint32_t *>(tg + 8 * kChunk + 4 * (2 * hh + (st_cs >> 1)));
         }
+        R.x = xbase[(KQ ? (int64_t)g : (int64_t)s * 4 + x_blk) * p.ldT];
+        return R;
+    };
+    auto store = [&](const StageRegs R, int buf, int s) {
+        const int hh = s & 1;
+        uint8_t * A = lds + buf * kStage;
+        uint8_t * B = A + LY::oB;
+        uint8_t * W = A + LY::oW;
+        float * X = reinterpret_cast<float *>(A + LY::oX);
 #pragma unroll
-        for (int q = 0; q < kNB; ++q) {                           // weights: 2 tiles x 5 chunks x 64 rows
+        for (int q = 0; q < NA; ++q) {
             const int u = tid + kT * q;
-            rb[q] = make_uint4(0, 0, 0, 0);
-            if (u < kBB / 16) {
-                const int tt = u / 320, rem = u - tt * 320, cs = rem >> 6, r = rem & 63;
-                int64_t tile = 2 * mtile + tt;
-                tile = tile < p.w.ntiles ? tile : p.w.ntiles - 1;
-                const int c = cs < 4 ? 4 * (int)hh + cs : 8;
-                rb[q] = ld16_nt(tile_group(p.w, mat, tile, g) + c * kChunk + r * 16);
+            *reinterpret_cast<uint4 *>(A + (u >> 3) * kAP + (u & 7) * 16) = R.a[q];
+        }
+        const uint32_t e[4] = { R.c.x, R.c.y, R.c.z, R.c.w };
+        if constexpr (!KQ) {
+            // chunk 4 hh + cs is block cs of the stage: low nibbles k < 16, high nibbles k >= 16
+            uint4 lo, hi;
+            lo.x = q4_minus8(e[0] & 0x0F0F0F0Fu); hi.x = q4_minus8((e[0] >> 4) & 0x0F0F0F0Fu);
+            lo.y = q4_minus8(e[1] & 0x0F0F0F0Fu); hi.y = q4_minus8((e[1] >> 4) & 0x0F0F0F0Fu);
+            lo.z = q4_minus8(e[2] & 0x0F0F0F0Fu); hi.z = q4_minus8((e[2] >> 4) & 0x0F0F0F0Fu);
+            lo.w = q4_minus8(e[3] & 0x0F0F0F0Fu); hi.w = q4_minus8((e[3] >> 4) & 0x0F0F0F0Fu);
+            uint8_t * b = B + ((st_tile * 4 + st_cs) * 2) * kChunk + st_row * 16;
+            *reinterpret_cast<uint4 *>(b) = lo;
+            *reinterpret_cast<uint4 *>(b + kChunk) = hi;
+            // d of block cs of the stage (block 4 hh + cs of the group)
+            reinterpret_cast<float *>(W)[(st_tile * 4 + st_cs) * 64 + st_row] = h2f(R.h.x >> (16 * (st_cs & 1)));
+            if (tid < 4 * BN) X[tid] = R.x;                       // [block][col]
+        } else {
+            // chunk 4 hh + cs holds weights 16 h .. 16 h + 15 (h = cs % 2) of sub-blocks 4 hh + ql (low
+            // nibbles) and 4 hh + ql + 1 (high nibbles), ql = 2 (cs / 2)
+            const int h = st_cs & 1, ql = 2 * (st_cs >> 1);
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                uint32_t sc, mn;
+                q4k_scale_min(4 * hh + ql + t, R.h.y, R.h.z, R.h.w, &sc, &mn);
+                const uint32_t sh = sc >> 3, sl = sc & 7;
+                uint4 vh, vl;
+                const uint32_t m0 = (e[0] >> (4 * t)) & 0x0F0F0F0Fu, m1 = (e[1] >> (4 * t)) & 0x0F0F0F0Fu;
+                const uint32_t m2 = (e[2] >> (4 * t)) & 0x0F0F0F0Fu, m3 = (e[3] >> (4 * t)) & 0x0F0F0F0Fu;
+                vh.x = v2_mul(m0, sh); vl.x = v2_mul(m0, sl);
+                vh.y = v2_mul(m1, sh); vl.y = v2_mul(m1, sl);
+                vh.z = v2_mul(m2, sh); vl.z = v2_mul(m2, sl);
+                vh.w = v2_mul(m3, sh); vl.w = v2_mul(m3, sl);
+                uint8_t * b = B + (((st_tile * 4 + ql + t) * 2 + h) * 2) * kChunk + st_row * 16;
+                *reinterpret_cast<uint4 *>(b) = vh;
+                *reinterpret_cast<uint4 *>(b + kChunk) = vl;
+            }
+            {                                                     // mins 2 cs and 2 cs + 1 of the row (4 B: 2 mins, 2 zeros)
+                uint32_t sc, m0, m1;
+                q4k_scale_min(2 * st_cs, R.h.y, R.h.z, R.h.w, &sc, &m0);
+                q4k_scale_min(2 * st_cs + 1, R.h.y, R.h.z, R.h.w, &sc, &m1);
+                uint16_t * mw = reinterpret_cast<uint16_t *>(W + (st_tile * 64 + st_row) * 16);
+                mw[st_cs] = (uint16_t)(m0 | (m1 << 8));
+                mw[4 + st_cs] = 0;
+            }
+            if (st_cs == 0)                                       // d and dmin
+                reinterpret_cast<float2 *>(W + 2 * 64 * 16)[st_tile * 64 + st_row] = make_float2(h2f(R.h.x), h2f(R.h.x >> 16));
+            if (tid < BN) {
+                X[tid] = R.x;
+                *reinterpret_cast<uint4 *>(A + LY::oS + tid * 16) = R.s;
             }
         }
-        // scales: 4 blocks x 128 columns (q8_0) or 128 columns once per group (q8_K)
-        rx = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (tid < (KQ ? 32 : 128)) {
-            const int blk = KQ ? 0 : tid >> 5, c4 = (tid & 31) * 4;
-            const int64_t row = KQ ? g : (int64_t)s * 4 + blk;
-            const float * src = p.dT + row * p.ldT + col0 + n0 + c4;
-            if (n0 + c4 + 0 < p.N) rx.x = src[0];
-            if (n0 + c4 + 1 < p.N) rx.y = src[1];
-            if (n0 + c4 + 2 < p.N) rx.z = src[2];
-            if (n0 + c4 + 3 < p.N) rx.w = src[3];
-        }
-    };
-    auto store = [&](int buf) {
-        uint8_t * A = lds + buf * kStage;
-        uint8_t * B = A + kAB;
-        float * X = reinterpret_cast<float *>(B + kBB);
-#pragma unroll
-        for (int q = 0; q < kNA; ++q) {
-            const int u = tid + kT * q, c = u >> 3, un = u & 7;
-            *reinterpret_cast<uint4 *>(A + c * kAP + un * 16) = ra[q];
-        }
-#pragma unroll
-        for (int q = 0; q < kNB; ++q) {
-            const int u = tid + kT * q;
-            if (u < kBB / 16) *reinterpret_cast<uint4 *>(B + u * 16) = rb[q];
-        }
-        if (tid < (KQ ? 32 : 128)) *reinterpret_cast<float4 *>(X + tid * 4) = rx;
     };
 
-    // ---- per-wave tile: image tile wr (64 rows = 2 MFMA row tiles) x columns wn * 32 .. + 32
-    const int wr = wave & 1, wn = wave >> 1;
+    // ---- per-wave tile: image tile wr (64 rows = 2 MFMA row tiles) x columns wn * 32 .. + 32,
+    // blocks wk, wk + KSPLIT, ... of every stage
+    const int wr = wave & 1, wn = (wave >> 1) % NWN, wk = (wave >> 1) / NWN;
     const int h = lane >> 5, l32 = lane & 31;
-    float out[2][16];
-    v16i c1[2], c2[2], c3[2];
+    v16f out0 = v16f{}, out1 = v16f{};                            // row tiles 0 and 1
+    v16i c1[2], c2[2];
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) out[rt][r] = 0.0f;
         c1[rt] = v16i{};
         c2[rt] = v16i{};
-        c3[rt] = v16i{};
     }
+    v16i magic;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) magic[r] = kMagic;
 
-    if (s0 < s1) {
-        fetch(s0);
-        store(0);
-    }
-    __syncthreads();
-    for (int s = s0; s < s1; ++s) {                               // uniform over the work-group
-        const int buf = (s - s0) & 1;
-        if (s + 1 < s1) fetch(s + 1);
-        const uint8_t * A = lds + buf * kStage;
-        const uint8_t * B = A + kAB + wr * 5 * kChunk;            // this wave's image tile
-        const float * X = reinterpret_cast<const float *>(A + kAB + kBB);
-        const int hh = s & 1;
-        uint4 hdr[2];                                             // the lane's row headers (chunk 8)
+    // operands of one block (Q4_0) / sub-block (Q4_K); Q4_0 loads them from LDS one block ahead of
+    // the MFMAs that use them (two register sets)
+    struct Ops {
+        v4i a;                           // activation codes of this wave's 32 columns
+        v4i b[2][2];                     // [row tile][0: q - 8 (Q4_0) or q * sh (Q4_K), 1: q * sl]
+        float dw[2];                     // Q4_0: d_w of the lane's rows
+        float dx[16];                    // Q4_0: d_x of the lane's 16 columns
+    };
+    auto load_ops = [&](int buf, int q) -> Ops {
+        Ops o;
+        const uint8_t * A = lds + buf * kStage + (wn * 32 + l32) * kAP + 16 * h;
+        const uint8_t * B = lds + buf * kStage + LY::oB;
+        const uint8_t * W = lds + buf * kStage + LY::oW;
+        const float * X = reinterpret_cast<const float *>(lds + buf * kStage + LY::oX);
+        o.a = *reinterpret_cast<const v4i *>(A + q * 32);
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt) hdr[rt] = *reinterpret_cast<const uint4 *>(B + 4 * kChunk + (32 * rt + l32) * 16);
-#pragma unroll UQ
-        for (int q = 0; q < 4; ++q) {
-            const v4i a = *reinterpret_cast<const v4i *>(A + (wn * 32 + l32) * kAP + q * 32 + 16 * h);
+        for (int rt = 0; rt < 2; ++rt) {
+            const int row = 32 * rt + l32;
             if constexpr (!KQ) {
-                // Q4_0 block 4 hh + q: chunk slot q, low nibbles (k < 16) for h = 0, high for h = 1
-                float dx[16];
-#pragma unroll
-                for (int g4 = 0; g4 < 4; ++g4) {
-                    const float4 v = *reinterpret_cast<const float4 *>(X + q * kBN + wn * 32 + 8 * g4 + 4 * h);
-                    dx[4 * g4] = v.x; dx[4 * g4 + 1] = v.y; dx[4 * g4 + 2] = v.z; dx[4 * g4 + 3] = v.w;
-                }
-#pragma unroll
-                for (int rt = 0; rt < 2; ++rt) {
-                    const uint4 v = *reinterpret_cast<const uint4 *>(B + q * kChunk + (32 * rt + l32) * 16);
-                    const uint32_t e[4] = { v.x, v.y, v.z, v.w };
-                    uint32_t o[4];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const uint32_t nib = ((e[i] >> (4 * h)) & 0x0F0F0F0Fu) | 0x80808080u;
-                        o[i] = (nib - 0x08080808u) ^ 0x80808080u;   // q - 8, bytewise
-                    }
-                    const v4i bq = v4i{ (int)o[0], (int)o[1], (int)o[2], (int)o[3] };
-                    const int blk = 4 * hh + q;
-                    const uint32_t hw = blk < 2 ? hdr[rt].x : blk < 4 ? hdr[rt].y : blk < 6 ? hdr[rt].z : hdr[rt].w;
-                    const float dw = h2f(hw >> (16 * (blk & 1)));
-                    const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bq, v16i{}, 0, 0, 0);
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) out[rt][r] += (float)d[r] * (dw * dx[r]);
-                }
+                o.b[rt][0] = *reinterpret_cast<const v4i *>(B + ((wr * 4 + q) * 2 + h) * kChunk + row * 16);
+                o.dw[rt] = reinterpret_cast<const float *>(W)[(wr * 4 + q) * 64 + row];
             } else {
-                // Q4_K sub-block jj = 4 hh + q: chunk slot 2 (q / 2) + h, low nibbles for even q
-#pragma unroll
-                for (int rt = 0; rt < 2; ++rt) {
-                    const uint4 v = *reinterpret_cast<const uint4 *>(B + (2 * (q >> 1) + h) * kChunk + (32 * rt + l32) * 16);
-                    const int jj = 4 * hh + q, b8 = 8 * (jj & 3);
-                    uint32_t sc, mn;                              // get_scale_min_k4 (P01:2164-2176)
-                    if (jj < 4) {
-                        sc = (hdr[rt].y >> b8) & 63;
-                        mn = (hdr[rt].z >> b8) & 63;
-                    } else {
-                        sc = ((hdr[rt].w >> b8) & 0xF) | (((hdr[rt].y >> b8) >> 6 & 3) << 4);
-                        mn = ((hdr[rt].w >> b8) >> 4 & 0xF) | (((hdr[rt].z >> b8) >> 6 & 3) << 4);
-                    }
-                    const uint32_t sl = sc & 7u, sh = sc >> 3;
-                    const uint32_t e[4] = { v.x, v.y, v.z, v.w };
-                    uint32_t oh[4], ol[4];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const uint32_t nib = (e[i] >> (4 * (q & 1))) & 0x0F0F0F0Fu;
-                        oh[i] = v2_mul(nib, sh);
-                        ol[i] = v2_mul(nib, sl);
-                    }
-                    const v4i bh = v4i{ (int)oh[0], (int)oh[1], (int)oh[2], (int)oh[3] };
-                    const v4i bl = v4i{ (int)ol[0], (int)ol[1], (int)ol[2], (int)ol[3] };
-                    const int mrep = (int)(mn * 0x01010101u);
-                    const v4i bm = v4i{ mrep, mrep, mrep, mrep };
-                    c1[rt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bh, c1[rt], 0, 0, 0);
-                    c2[rt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bl, c2[rt], 0, 0, 0);
-                    c3[rt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bm, c3[rt], 0, 0, 0);
-                }
+                const uint8_t * b = B + (((wr * 4 + q) * 2 + h) * 2) * kChunk + row * 16;
+                o.b[rt][0] = *reinterpret_cast<const v4i *>(b);
+                o.b[rt][1] = *reinterpret_cast<const v4i *>(b + kChunk);
             }
         }
+        if constexpr (!KQ) {
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const float4 v = *reinterpret_cast<const float4 *>(X + q * BN + wn * 32 + 8 * g4 + 4 * h);
+                o.dx[4 * g4] = v.x; o.dx[4 * g4 + 1] = v.y; o.dx[4 * g4 + 2] = v.z; o.dx[4 * g4 + 3] = v.w;
+            }
+        }
+        return o;
+    };
+    auto mma = [&](const Ops o) {
+        if constexpr (!KQ) {
+            const v16i d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a, o.b[0][0], magic, 0, 0, 0);
+            const v16i d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a, o.b[1][0], magic, 0, 0, 0);
+            const float nm0 = -12582912.0f * o.dw[0], nm1 = -12582912.0f * o.dw[1];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int di = d0[r];                             // (bit_cast of a vector element reads element 0)
+                out0[r] = __builtin_fmaf(__builtin_fmaf(__builtin_bit_cast(float, di), o.dw[0], nm0), o.dx[r], out0[r]);
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int di = d1[r];
+                out1[r] = __builtin_fmaf(__builtin_fmaf(__builtin_bit_cast(float, di), o.dw[1], nm1), o.dx[r], out1[r]);
+            }
+            // keep this block's products from being deferred past later MFMAs (register pressure)
+            asm volatile("" : "+v"(out0), "+v"(out1));
+        } else {
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) {
+                c1[rt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a, o.b[rt][0], c1[rt], 0, 0, 0);
+                c2[rt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a, o.b[rt][1], c2[rt], 0, 0, 0);
+            }
+        }
+    };
+    auto compute = [&](int buf, int s) {
+        if constexpr (!KQ) {
+            Ops o0 = load_ops(buf, wk), o1;
+#pragma unroll
+            for (int i = 0; i < NQ; ++i) {
+                if (i + 1 < NQ) o1 = load_ops(buf, wk + (i + 1) * KSPLIT);
+                __builtin_amdgcn_sched_barrier(0);
+                mma(o0);
+                __builtin_amdgcn_sched_barrier(0);
+                o0 = o1;
+            }
+        } else {                                                  // (registers: no second operand set)
+#pragma unroll
+            for (int i = 0; i < NQ; ++i) mma(load_ops(buf, wk + i * KSPLIT));
+        }
         if constexpr (KQ) {
-            if (hh == 1) {                                        // end of the super-block (uniform)
+            if (s & 1) {                                          // end of the super-block (uniform)
+                const uint8_t * W = lds + buf * kStage + LY::oW;
+                const float * X = reinterpret_cast<const float *>(lds + buf * kStage + LY::oX);
+                const v4i sv = *reinterpret_cast<const v4i *>(lds + buf * kStage + LY::oS + (wn * 32 + l32) * 16);
                 float dx[16];
 #pragma unroll
                 for (int g4 = 0; g4 < 4; ++g4) {
                     const float4 v = *reinterpret_cast<const float4 *>(X + wn * 32 + 8 * g4 + 4 * h);
                     dx[4 * g4] = v.x; dx[4 * g4 + 1] = v.y; dx[4 * g4 + 2] = v.z; dx[4 * g4 + 3] = v.w;
                 }
+                // min term (one wave of the tile): k in [0, 8) of lane half 0 carries sub-blocks 0..7
+                const v4i zero = v4i{ 0, 0, 0, 0 };
+                const v4i ah = h ? zero : v4i{ sv.x, sv.y, 0, 0 };
+                const v4i al = h ? zero : v4i{ sv.z, sv.w, 0, 0 };
 #pragma unroll
                 for (int rt = 0; rt < 2; ++rt) {
-                    const float d = h2f(hdr[rt].x), dmin = h2f(hdr[rt].x >> 16);
+                    const int row = wr * 64 + 32 * rt + l32;
+                    const float2 dd = reinterpret_cast<const float2 *>(W + 2 * 64 * 16)[row];
+                    const v4i bmin = h ? zero : *reinterpret_cast<const v4i *>(W + row * 16);
+                    v16i mh = v16i{}, ml = v16i{};
+                    if (wk == 0) {
+                        mh = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, bmin, v16i{}, 0, 0, 0);
+                        ml = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, bmin, v16i{}, 0, 0, 0);
+                    }
+                    v16f & o = rt ? out1 : out0;
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         const int isc = 8 * c1[rt][r] + c2[rt][r];
-                        out[rt][r] += dx[r] * (d * (float)isc - dmin * (float)c3[rt][r]);
+                        const int imn = 64 * mh[r] + ml[r];
+                        o[r] += dx[r] * (dd.x * (float)isc - dd.y * (float)imn);
                     }
                     c1[rt] = v16i{};
                     c2[rt] = v16i{};
-                    c3[rt] = v16i{};
                 }
             }
         }
-        if (s + 1 < s1) store(buf ^ 1);                           // the other buffer was last read a stage ago
+    };
+
+    // ---- K loop.  Q4_0: stages in pairs; the data of a stage is fetched two stages before it is
+    // computed (two register sets) and stored to LDS during the stage before it (two LDS buffers).  Inside a
+    // stage, computing it and storing the next touch different buffers, so the order is free: waves
+    // 0-3 compute first and waves 4-7 (the second wave on each SIMD) store first, which keeps one wave
+    // per SIMD on the MFMAs while the other unpacks weights.  Fetches past the slice re-read its last
+    // stage (unconditional loads keep the wait counts static).
+    const bool store_first = wave >= 4;
+    if constexpr (!KQ) {
+        StageRegs R0 = fetch(s0), R1 = fetch(s0 + 1);
+        store(R0, 0, s0);
         __syncthreads();
+        for (int s = s0; s < s1; s += 2) {                        // uniform over the work-group
+            R0 = fetch(std::min(s + 2, s1 - 1));
+            if (store_first) store(R1, 1, s + 1);
+            compute(0, s);
+            if (!store_first) store(R1, 1, s + 1);
+            __syncthreads();
+            R1 = fetch(std::min(s + 3, s1 - 1));
+            if (store_first && s + 2 < s1) store(R0, 0, s + 2);
+            compute(1, s + 1);
+            if (!store_first && s + 2 < s1) store(R0, 0, s + 2);
+            __syncthreads();
+        }
+    } else {                                                      // Q4_K (registers): one stage ahead
+        StageRegs R = fetch(s0);
+        store(R, 0, s0);
+        __syncthreads();
+        for (int s = s0; s < s1; ++s) {
+            R = fetch(std::min(s + 1, s1 - 1));
+            compute((s - s0) & 1, s);
+            if (s + 1 < s1) store(R, (s - s0 + 1) & 1, s + 1);
+            __syncthreads();
+        }
+    }
+
+    // ---- the two waves of a tile (BN = 64) add their sums through LDS
+    if constexpr (KSPLIT == 2) {
+        float * red = reinterpret_cast<float *>(lds) + ((wr + 2 * wn) * 32) * 64 + lane;
+        if (wk == 1) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                red[r * 64] = out0[r];
+                red[(16 + r) * 64] = out1[r];
+            }
+        }
+        __syncthreads();
+        if (wk == 1) return;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            out0[r] += red[r * 64];
+            out1[r] += red[(16 + r) * 64];
+        }
     }
 
     // ---- store: lane holds row 32 rt + l32 of its image tile for 16 columns
@@ -269,66 +433,92 @@ __global__ __launch_bounds__(kT) void k_gemm2(G2Params p) {
     for (int rt = 0; rt < 2; ++rt) {
         const int64_t m = (2 * mtile + wr) * kTileRows + 32 * rt + l32;
         if (m >= p.w.M) continue;
+        const v16f v = rt ? out1 : out0;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int64_t n = n0 + wn * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
             if (n < p.N) {
                 float * o = dst + n * p.bt.d_nb1 + m;
-                if (p.KS == 1) *o = out[rt][r];
-                else atomicAdd(o, out[rt][r]);
+                const float x = v[r];
+                if (p.KS == 1) *o = x;
+                else atomicAdd(o, x);
             }
         }
     }
+}
+
+template <int TYPE, int BN>
+hipError_t launch_t(const G2Params & p, const dim3 & g, hipStream_t s, const KTime * kt) {
+    constexpr int lds = 2 * Lay<TYPE, BN>::stage;
+    static const hipError_t attr =
+        hipFuncSetAttribute((const void *)k_gemm2<TYPE, BN>, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (attr != hipSuccess) return attr;
+    if (kt) hipExtLaunchKernelGGL(k_gemm2<TYPE, BN>, g, dim3(kT), (uint32_t)lds, s, kt->start, kt->stop, 0, p);
+    else k_gemm2<TYPE, BN><<<g, kT, lds, s>>>(p);
+    return hipGetLastError();
+}
+
+// Launch shape: column tile BN, K slices KS and stages per slice spk.  The
+// 64-column tile (whose stages cost more than half of a 128-column stage:
+// the weight staging and the barrier do not shrink with it) is used only
+// when 128-column tiles cannot give every CU a work-group; K is split
+// (atomics, ~4x the cost of a store) only when even 64-column tiles leave
+// most of the chip idle.
+struct G2Shape {
+    int BN, KS, spk;
+    int64_t mt, nt;
+};
+G2Shape g2_shape(const WView & w, int64_t N, int64_t nbatch) {
+    static const int64_t cus = [] {
+        const char * e = getenv("QMM_GEMM_CUS");
+        return e ? std::max<int64_t>(1, atoll(e)) : (int64_t)256;
+    }();
+    G2Shape sh;
+    sh.mt = (w.M + 127) / 128;
+    const int64_t w128 = sh.mt * ((N + 127) / 128) * nbatch;
+    sh.BN = (N <= 64 || w128 < cus) ? 64 : 128;
+    sh.nt = (N + sh.BN - 1) / sh.BN;
+    const int64_t wgs = sh.mt * sh.nt * nbatch;
+    int64_t ks = 1;
+    if (wgs * 2 < cus) ks = std::min<int64_t>(w.G, cus / wgs);
+    const int64_t gps = (w.G + ks - 1) / ks;
+    sh.spk = (int)(2 * gps);
+    sh.KS = (int)((w.G + gps - 1) / gps);
+    return sh;
 }
 
 }  // namespace
 
 bool gemm2_supported(int type) { return type == QMM_TYPE_Q4_0 || type == QMM_TYPE_Q4_K; }
 
-// K split: enough work-groups to cover the chip (QMM_GEMM_WGS, default 512),
-// whole groups per slice
-static void g2_split(const WView & w, int64_t N, int64_t nbatch, int * KS, int * spk) {
-    static const int64_t target = [] {
-        const char * e = getenv("QMM_GEMM_WGS");
-        return e ? std::max<int64_t>(1, atoll(e)) : (int64_t)512;
-    }();
-    const int64_t wgs = ((w.M + 127) / 128) * ((N + kBN - 1) / kBN) * nbatch;
-    const int64_t ks = std::max<int64_t>(1, std::min<int64_t>(w.G, (target + wgs - 1) / wgs));
-    const int64_t gps = (w.G + ks - 1) / ks;
-    *spk = (int)(2 * gps);
-    *KS = (int)((w.G + gps - 1) / gps);
-}
-
-int gemm2_kslices(const WView & w, int64_t N, int64_t nbatch) {
-    int ks, spk;
-    g2_split(w, N, nbatch, &ks, &spk);
-    return ks;
-}
+int gemm2_kslices(const WView & w, int64_t N, int64_t nbatch) { return g2_shape(w, N, nbatch).KS; }
 
 void gemm2_shape(const WView & w, int64_t N, int64_t nbatch, int64_t * workgroups, int * threads, int * lds_bytes) {
-    int ks, spk;
-    g2_split(w, N, nbatch, &ks, &spk);
-    *workgroups = ((w.M + 127) / 128) * ((N + kBN - 1) / kBN) * ks * nbatch;
+    const G2Shape sh = g2_shape(w, N, nbatch);
+    *workgroups = sh.mt * sh.nt * sh.KS * nbatch;
     *threads = kT;
-    *lds_bytes = 2 * kStage;
+    *lds_bytes = 2 * (sh.BN == 64 ? Lay<QMM_TYPE_Q4_K, 64>::stage : Lay<QMM_TYPE_Q4_K, 128>::stage);
 }
 
 hipError_t launch_gemm2(int type, const WView & w, const ActBuf & a, int64_t N, int64_t nbatch, const GemmBatch & bt,
                         float * dst, hipStream_t s, const KTime * kt) {
     if (!gemm2_supported(type) || !a.dT || a.ldk != w.G * 256 || a.ldT < N * nbatch + 64 || N <= 0 || nbatch <= 0 ||
-        nbatch > 65535 || a.vdt != vec_dot_type(type))
+        nbatch > 65535 || a.vdt != vec_dot_type(type) || (type == QMM_TYPE_Q4_K && !a.bsp))
         return hipErrorInvalidValue;
+    const G2Shape sh = g2_shape(w, N, nbatch);
     G2Params p{};
     p.w = w;
     p.xc = a.codes;
     p.ldk = a.ldk;
     p.dT = a.dT;
     p.ldT = a.ldT;
+    p.bsp = a.bsp;
     p.N = N;
-    p.mt = (w.M + 127) / 128;
-    p.nt = (N + kBN - 1) / kBN;
+    p.mt = sh.mt;
+    p.nt = sh.nt;
     p.nst = 2 * w.G;
-    g2_split(w, N, nbatch, &p.KS, &p.spk);
+    p.KS = sh.KS;
+    p.spk = sh.spk;
     p.bt = bt;
     p.dst = dst;
     const int64_t total = p.mt * p.nt * p.KS;
@@ -336,15 +526,9 @@ hipError_t launch_gemm2(int type, const WView & w, const ActBuf & a, int64_t N, 
     const int64_t grid = p.chunk * 8;
     if (grid > 0x7fffffff) return hipErrorInvalidValue;
     const dim3 g((unsigned)grid, (unsigned)nbatch);
-    const size_t lds = 2 * (size_t)kStage;
-    if (type == QMM_TYPE_Q4_0) {
-        if (kt) hipExtLaunchKernelGGL(k_gemm2<QMM_TYPE_Q4_0>, g, dim3(kT), (uint32_t)lds, s, kt->start, kt->stop, 0, p);
-        else k_gemm2<QMM_TYPE_Q4_0><<<g, kT, lds, s>>>(p);
-    } else {
-        if (kt) hipExtLaunchKernelGGL(k_gemm2<QMM_TYPE_Q4_K>, g, dim3(kT), (uint32_t)lds, s, kt->start, kt->stop, 0, p);
-        else k_gemm2<QMM_TYPE_Q4_K><<<g, kT, lds, s>>>(p);
-    }
-    return hipGetLastError();
+    if (type == QMM_TYPE_Q4_0)
+        return sh.BN == 64 ? launch_t<QMM_TYPE_Q4_0, 64>(p, g, s, kt) : launch_t<QMM_TYPE_Q4_0, 128>(p, g, s, kt);
+    return sh.BN == 64 ? launch_t<QMM_TYPE_Q4_K, 64>(p, g, s, kt) : launch_t<QMM_TYPE_Q4_K, 128>(p, g, s, kt);
 }
 
 }  // namespace qmm

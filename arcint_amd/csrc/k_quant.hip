@@ -9,7 +9,9 @@
 // Divisions are IEEE (hipcc's default correctly-rounded f32 divide) and no
 // multiply is contracted, so every code and scale equals the CPU's.
 // Columns are written with a stride of ldk (K rounded up to 256); the padding
-// past K quantizes zeros.  The same launch can zero dst columns for a GEMV
+// past K quantizes zeros.  For a GEMM consumer the scales are written again
+// block-major (dT), and for q8_K the sub-block sums split into int8 halves
+// (bsp), the GEMM's operand for the Q4_K min term.  The same launch can zero dst columns for a GEMV
 // that adds its K slices with atomics (work-groups past the quantization
 // ones do that).
 #include "qmm_device.h"
@@ -78,6 +80,14 @@ __global__ void k_quant_q8_K(F32Cols src, int64_t K, int64_t ncols, ActBuf a, Ze
     const uint32_t packed = quant_q8_K_wave(v, lane, &d, &s);
     *reinterpret_cast<uint32_t *>(a.codes + c * a.ldk + sb * 256 + 4 * lane) = packed;
     if ((lane & 3) == 0) a.sums[c * (a.ldk / 16) + sb * 16 + (lane >> 2)] = (int16_t)s;
+    if (a.bsp) {                                   // sub-block sums (8 lanes = 32 codes) as 64 bh + bl
+        const int s32 = s + __shfl_xor(s, 4, 64);
+        if ((lane & 7) == 0) {
+            int8_t * o = a.bsp + (sb * a.ldT + c) * 16 + (lane >> 3);
+            o[0] = (int8_t)(s32 >> 6);
+            o[8] = (int8_t)(s32 & 63);
+        }
+    }
     if (lane == 0) {
         a.d[c * nsb + sb] = d;
         if (a.dT) a.dT[sb * a.ldT + c] = d;

@@ -120,7 +120,8 @@ WView weight_view(const qmm_tensor * t) {
 // activation scratch layout for ncols columns of ldk (K rounded up to 256):
 // codes, scales, sums and (GEMM consumers) the scales again block-major with
 // a row stride of ldT
-size_t act_bytes(int vdt, int64_t ldk, int64_t ncols, bool dT, int64_t ldT, size_t * o_d, size_t * o_s, size_t * o_t) {
+size_t act_bytes(int vdt, int64_t ldk, int64_t ncols, bool dT, int64_t ldT, size_t * o_d, size_t * o_s, size_t * o_t,
+                 size_t * o_b) {
     size_t off = align_up((size_t)(ldk * ncols), kPlaneAlign);
     *o_d = off;
     off = align_up(off + (size_t)(ncols * (ldk / act_block(vdt))) * 4, kPlaneAlign);
@@ -128,6 +129,8 @@ size_t act_bytes(int vdt, int64_t ldk, int64_t ncols, bool dT, int64_t ldT, size
     off = align_up(off + (size_t)(ncols * (ldk / act_sum_block(vdt))) * 2, kPlaneAlign);
     *o_t = off;
     if (dT) off = align_up(off + (size_t)((ldk / act_block(vdt)) * ldT) * 4, kPlaneAlign);
+    *o_b = off;
+    if (dT && vdt == QMM_TYPE_Q8_K) off = align_up(off + (size_t)((ldk / 256) * ldT) * 16, kPlaneAlign);
     return off;
 }
 
@@ -174,10 +177,10 @@ int quantize_src1(qmm_ctx * ctx, int type, const qmm_tensor * src1, bool dT, Act
         if (z) QMM_HIP(ctx, launch_quantize(f32_cols(src1), K, 0, ctx->cached, z, ctx->stream));   // zeroing only
         return QMM_OK;
     }
-    size_t od, os, ot;
+    size_t od, os, ot, ob;
     const int64_t ldk = (K + 255) / 256 * 256;
     const int64_t ldT = (ncols + 3) / 4 * 4 + 64;    // the GEMM reads up to 63 columns past the last
-    const size_t need = act_bytes(vdt, ldk, ncols, dT, ldT, &od, &os, &ot);
+    const size_t need = act_bytes(vdt, ldk, ncols, dT, ldT, &od, &os, &ot, &ob);
     int rc = ensure(ctx, &ctx->act, &ctx->act_cap, need);
     if (rc) return rc;
     uint8_t * b = (uint8_t *)ctx->act;
@@ -186,6 +189,7 @@ int quantize_src1(qmm_ctx * ctx, int type, const qmm_tensor * src1, bool dT, Act
     a.d = (float *)(b + od);
     a.sums = (int16_t *)(b + os);
     a.dT = dT ? (float *)(b + ot) : nullptr;
+    a.bsp = dT && vdt == QMM_TYPE_Q8_K ? (int8_t *)(b + ob) : nullptr;
     a.ldT = ldT;
     a.K = K;
     a.ldk = ldk;

@@ -79,6 +79,8 @@ struct ActBuf {
     float *    d;
     int16_t *  sums;
     float *    dT;         // non-null: the scales again, block-major: dT[b * ldT + c]
+    int8_t *   bsp;        // q8_K with dT: per super-block sb and column c, 16 bytes at (sb * ldT + c) * 16:
+                           // the 8 sub-block sums (32 codes each) split as 64 bh + bl, bh[8] then bl[8]
     int64_t    ldT;        // >= ncols + 64 (the GEMM reads whole 64-column tiles)
     int64_t    K;
     int64_t    ldk;        // K rounded up to 256

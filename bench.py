@@ -14,8 +14,9 @@ Also reported, on the same JSON line:
                 from profiles/ when the rocprofv3 PMC runs were committed
   cpu_baseline  the CPU oracle (a C restatement of ggml-cpu's algorithm,
                 kind "port") on the same op, bounded to ~--cpu-seconds
-  secondary     Q4_0 4096x4096 at N = 512 (config 1) in TOPS vs the dense
-                int8 MFMA peak
+  gemm          prefill MUL_MAT at N = 512: Q4_0 4096x4096 and 11008x4096
+                (config 1), Q4_K 17408x5120 (config 2), in TOPS vs the dense
+                int8 MFMA peak ("secondary" repeats the first)
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
@@ -106,6 +107,30 @@ def cpu_baseline(orc, qtype, raw, M, K, x, budget_s):
                       f"(ggml-cpu's algorithm restated in C, -O3 -mavx2; q8_K quantization included)"}
 
 
+def gemm_case(be, qmm, synth, qtype, M, K, N, name, args):
+    """One prefill MUL_MAT (activation pre-pass + GEMM) over rotated weight
+    copies: op TOPS (timed region), GEMM kernel TOPS (dispatch-stamped) and
+    its fraction of the dense int8 MFMA peak."""
+    raw, ws = weight_copies(be, qmm, synth, qtype, M, K, seed=2)
+    x = synth.activations(N, K, seed=3)
+    xt = be.new_tensor(qmm.F32, (K, N))
+    be.set_tensor(xt, x.view(np.uint8).ravel())
+    yt = be.new_tensor(qmm.F32, (M, N))
+    steps = max(5, args.steps // 10)
+    wall, dev, k = time_op(be, ws, xt, yt, steps, max(2, args.warmup // 4))
+    ops = 2.0 * M * N * K
+    sec = {"workload": name, "path": be.last_path(),
+           "tops": round(ops * steps / wall / 1e12, 3),
+           "kernel_tops": round(ops / (k * 1e-3) / 1e12, 3),
+           "frac_int8_peak": round(ops / (k * 1e-3) / 1e12 / INT8_PEAK_TOPS, 5),
+           "ms_per_op": round(wall * 1e3 / steps, 4), "kernel_ms": round(k, 4)}
+    for w in ws:
+        be.free_buffer(w.buf)
+    be.free_buffer(xt.buf)
+    be.free_buffer(yt.buf)
+    return sec
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -114,7 +139,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
-    ap.add_argument("--only", default="", help="profile one workload: q4k_gemv or q40_gemm")
+    ap.add_argument("--only", default="", help="profile one workload: q4k_gemv, q40_gemm or q4k_gemm")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -160,25 +185,20 @@ def main():
         for w in ws:
             be.free_buffer(w.buf)
 
-    if not args.no_secondary and args.only in ("", "q40_gemm"):
-        M2, K2, N2 = 4096, 4096, 512
-        raw2, ws2 = weight_copies(be, qmm, synth, qmm.Q4_0, M2, K2, seed=2)
-        x2 = synth.activations(N2, K2, seed=3)
-        xt2 = be.new_tensor(qmm.F32, (K2, N2))
-        be.set_tensor(xt2, x2.view(np.uint8).ravel())
-        yt2 = be.new_tensor(qmm.F32, (M2, N2))
-        steps2 = max(5, args.steps // 10)
-        wall2, dev2, k2 = time_op(be, ws2, xt2, yt2, steps2, max(2, args.warmup // 4))
-        ops = 2.0 * M2 * N2 * K2
-        sec = {"workload": "Q4_0 GEMM 4096x4096x512 (config 1 attn)", "path": be.last_path(),
-               "tops": round(ops * steps2 / wall2 / 1e12, 3),
-               "kernel_tops": round(ops / (k2 * 1e-3) / 1e12, 3),
-               "frac_int8_peak": round(ops / (k2 * 1e-3) / 1e12 / INT8_PEAK_TOPS, 5),
-               "ms_per_op": round(wall2 * 1e3 / steps2, 4), "kernel_ms": round(k2, 4)}
+    if not args.no_secondary and args.only in ("", "q40_gemm", "q4k_gemm"):
+        cases = [(qmm.Q4_0, 4096, 4096, 512, "Q4_0 GEMM 4096x4096x512 (config 1 attn)", "q40_gemm"),
+                 (qmm.Q4_0, 11008, 4096, 512, "Q4_0 GEMM 11008x4096x512 (config 1 ffn gate/up)", "q40_gemm"),
+                 (qmm.Q4_K, 17408, 5120, 512, "Q4_K GEMM 17408x5120x512 (config 2 ffn gate/up)", "q4k_gemm")]
+        secs = []
+        for qtype, M2, K2, N2, name, tag in cases:
+            if args.only and args.only != tag:
+                continue
+            secs.append(gemm_case(be, qmm, synth, qtype, M2, K2, N2, name, args))
         if out:
-            out["secondary"] = sec
+            out["secondary"] = secs[0]
+            out["gemm"] = secs
         else:
-            out = {"metric": "Q4_0 GEMM TOPS at N=512", "value": sec["tops"], "unit": "TOPS", "secondary": sec}
+            out = {"metric": "GEMM TOPS at N=512", "value": secs[0]["tops"], "unit": "TOPS", "gemm": secs}
     be.close()
     print(json.dumps(out), flush=True)
 
