@@ -107,7 +107,7 @@ def cpu_baseline(orc, qtype, raw, M, K, x, budget_s):
                       f"(ggml-cpu's algorithm restated in C, -O3 -mavx2; q8_K quantization included)"}
 
 
-def gemm_case(be, qmm, synth, qtype, M, K, N, name, args):
+def gemm_case(be, qmm, synth, qtype, M, K, N, name, args, traffic_tag):
     """One prefill MUL_MAT (activation pre-pass + GEMM) over rotated weight
     copies: op TOPS (timed region), GEMM kernel TOPS (dispatch-stamped) and
     its fraction of the dense int8 MFMA peak."""
@@ -123,7 +123,8 @@ def gemm_case(be, qmm, synth, qtype, M, K, N, name, args):
            "tops": round(ops * steps / wall / 1e12, 3),
            "kernel_tops": round(ops / (k * 1e-3) / 1e12, 3),
            "frac_int8_peak": round(ops / (k * 1e-3) / 1e12 / INT8_PEAK_TOPS, 5),
-           "ms_per_op": round(wall * 1e3 / steps, 4), "kernel_ms": round(k, 4)}
+           "ms_per_op": round(wall * 1e3 / steps, 4), "kernel_ms": round(k, 4),
+           "traffic": profile_traffic(traffic_tag)}
     for w in ws:
         be.free_buffer(w.buf)
     be.free_buffer(xt.buf)
@@ -186,14 +187,15 @@ def main():
             be.free_buffer(w.buf)
 
     if not args.no_secondary and args.only in ("", "q40_gemm", "q4k_gemm"):
-        cases = [(qmm.Q4_0, 4096, 4096, 512, "Q4_0 GEMM 4096x4096x512 (config 1 attn)", "q40_gemm"),
-                 (qmm.Q4_0, 11008, 4096, 512, "Q4_0 GEMM 11008x4096x512 (config 1 ffn gate/up)", "q40_gemm"),
-                 (qmm.Q4_K, 17408, 5120, 512, "Q4_K GEMM 17408x5120x512 (config 2 ffn gate/up)", "q4k_gemm")]
+        cases = [(qmm.Q4_0, 4096, 4096, 512, "Q4_0 GEMM 4096x4096x512 (config 1 attn)", "q40_gemm", "q40_gemm"),
+                 (qmm.Q4_0, 11008, 4096, 512, "Q4_0 GEMM 11008x4096x512 (config 1 ffn gate/up)", "q40_gemm",
+                  "q40_gemm_11008"),
+                 (qmm.Q4_K, 17408, 5120, 512, "Q4_K GEMM 17408x5120x512 (config 2 ffn gate/up)", "q4k_gemm", "q4k_gemm")]
         secs = []
-        for qtype, M2, K2, N2, name, tag in cases:
+        for qtype, M2, K2, N2, name, tag, ttag in cases:
             if args.only and args.only != tag:
                 continue
-            secs.append(gemm_case(be, qmm, synth, qtype, M2, K2, N2, name, args))
+            secs.append(gemm_case(be, qmm, synth, qtype, M2, K2, N2, name, args, ttag))
         if out:
             out["secondary"] = secs[0]
             out["gemm"] = secs
