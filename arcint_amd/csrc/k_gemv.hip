@@ -467,7 +467,9 @@ bool gemv_plan(int type, const WView & w, int nc, int64_t ntasks, bool allow_spl
     // (KS), which need dst zeroed before the launch
     const int64_t tiles = ntasks * w.ntiles;
     const int64_t target = std::max(1, env_int("QMM_GEMV_WAVES", 4096));
-    const int64_t wmax = std::min(8, std::max(1, env_int("QMM_GEMV_WMAX", 1)));
+    // without split K (task lists: dst rows are not zeroed first) the K split
+    // is all within the work-group, up to 8 waves
+    const int64_t wmax = std::min(8, std::max(1, env_int("QMM_GEMV_WMAX", allow_split ? 1 : 8)));
     int64_t kw = std::min<int64_t>(w.G, std::max<int64_t>(1, (target + tiles - 1) / tiles));
     if (!allow_split) kw = std::min(kw, wmax);
     int64_t spw = (w.G + kw - 1) / kw;

@@ -5,6 +5,8 @@
 // counts and scatters the pairs into per-expert tasks of up to kMaxTaskCols
 // activation columns, which the GEMV kernel then runs as "few columns against
 // one expert": every touched expert's weights are streamed once per task.
+// The expert counts are scanned in parallel (a wave scan by shuffles, then the
+// 16 wave totals): a serial scan by one thread over 512 experts took 24 us.
 // Pair (slot i, token t) reads activation column (i % ne11) + t * ne11 and
 // writes dst + t * nb2 + i * nb1 (P01:3916-3922); a negative or out-of-range
 // id writes a zero row (P02:98-103).
@@ -21,7 +23,7 @@ __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs r, int32_t * 
     extern __shared__ int32_t sm[];
     int32_t * cnt = sm;                 // [n_as] pair count, later the fill cursor
     int32_t * tstart = sm + r.n_as;     // [n_as] first task of each expert
-    __shared__ int32_t s_total;
+    __shared__ int32_t s_wsum[kRouteThreads / 64];
     const int tid = threadIdx.x;
     const int64_t npairs = r.n_used * r.T;
     for (int64_t e = tid; e < r.n_as; e += kRouteThreads) cnt[e] = 0;
@@ -33,14 +35,38 @@ __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs r, int32_t * 
         scratch[p] = e;
     }
     __syncthreads();
-    if (tid == 0) {   // serial scan over experts (n_as is small: hundreds to a few thousand)
-        int32_t acc = 0;
-        for (int64_t e = 0; e < r.n_as; ++e) {
-            tstart[e] = acc;
-            acc += (cnt[e] + kMaxTaskCols - 1) / kMaxTaskCols;
+    // exclusive scan of the experts' task counts: thread tid owns experts [tid per, tid per + per),
+    // a wave scan by shuffles, then the 16 wave totals through LDS
+    {
+        const int64_t per = (r.n_as + kRouteThreads - 1) / kRouteThreads, e0 = tid * per;
+        int32_t local = 0;
+        for (int64_t k = 0; k < per; ++k)
+            if (e0 + k < r.n_as) local += (cnt[e0 + k] + kMaxTaskCols - 1) / kMaxTaskCols;
+        const int lane = tid & 63, wave = tid >> 6;
+        int32_t x = local;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int32_t v = __shfl_up(x, d, 64);
+            if (lane >= d) x += v;
         }
-        s_total = acc;
-        *ntasks = acc;
+        if (lane == 63) s_wsum[wave] = x;
+        __syncthreads();
+        if (tid == 0) {
+            int32_t acc = 0;
+            for (int w = 0; w < kRouteThreads / 64; ++w) {
+                const int32_t t = s_wsum[w];
+                s_wsum[w] = acc;
+                acc += t;
+            }
+            *ntasks = acc;
+        }
+        __syncthreads();
+        int32_t excl = x - local + s_wsum[wave];
+        for (int64_t k = 0; k < per; ++k)
+            if (e0 + k < r.n_as) {
+                tstart[e0 + k] = excl;
+                excl += (cnt[e0 + k] + kMaxTaskCols - 1) / kMaxTaskCols;
+            }
     }
     __syncthreads();
     // task headers

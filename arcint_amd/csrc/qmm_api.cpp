@@ -270,17 +270,18 @@ int qmm_ctx_create(int device, qmm_ctx ** out) {
     return QMM_OK;
 }
 
+// teardown: errors here have no caller to go to (void API, as ggml's free)
 void qmm_ctx_free(qmm_ctx * ctx) {
     if (!ctx) return;
-    hipSetDevice(ctx->device);
-    if (ctx->stream) hipStreamSynchronize(ctx->stream);
-    if (ctx->act) hipFree(ctx->act);
-    if (ctx->route) hipFree(ctx->route);
-    if (ctx->sink) hipFree(ctx->sink);
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->act) (void)hipFree(ctx->act);
+    if (ctx->route) (void)hipFree(ctx->route);
+    if (ctx->sink) (void)hipFree(ctx->sink);
     for (hipEvent_t e : ctx->kev) (void)hipEventDestroy(e);
-    if (ctx->ev0) hipEventDestroy(ctx->ev0);
-    if (ctx->ev1) hipEventDestroy(ctx->ev1);
-    if (ctx->stream) hipStreamDestroy(ctx->stream);
+    if (ctx->ev0) (void)hipEventDestroy(ctx->ev0);
+    if (ctx->ev1) (void)hipEventDestroy(ctx->ev1);
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
 }
 
@@ -305,10 +306,10 @@ int qmm_buffer_alloc(qmm_ctx * ctx, size_t size, qmm_buffer ** out) {
 void qmm_buffer_free(qmm_ctx * ctx, qmm_buffer * buf) {
     if (!buf) return;
     if (ctx) {
-        hipStreamSynchronize(ctx->stream);
+        (void)hipStreamSynchronize(ctx->stream);
         if (ctx->key.buf == buf) ctx->key.valid = false;
     }
-    hipFree(buf->ptr);
+    (void)hipFree(buf->ptr);
     delete buf;
 }
 
@@ -715,7 +716,7 @@ int qmm_quantize_act(qmm_ctx * ctx, int32_t act_type, const qmm_tensor * src, vo
     hipError_t e = launch_act_to_blocks(a, tmp, ctx->stream);
     if (e == hipSuccess) e = hipMemcpyAsync(out, tmp, need, hipMemcpyDeviceToHost, ctx->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
-    hipFree(tmp);
+    (void)hipFree(tmp);                                   // the copy's error, if any, is the one reported
     if (e != hipSuccess) return fail(ctx, QMM_ERR_DEVICE, "quantize_act: %s", hipGetErrorString(e));
     return QMM_OK;
 }

@@ -17,6 +17,8 @@ Also reported, on the same JSON line:
   gemm          prefill MUL_MAT at N = 512: Q4_0 4096x4096 and 11008x4096
                 (config 1), Q4_K 17408x5120 (config 2), in TOPS vs the dense
                 int8 MFMA peak ("secondary" repeats the first)
+  moe           MUL_MAT_ID on config 3 (512 Q4_K experts, top-10) at T = 1,
+                4, 256 tokens: GB/s of the expert weights each step touches
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
@@ -132,6 +134,56 @@ def gemm_case(be, qmm, synth, qtype, M, K, N, name, args, traffic_tag):
     return sec
 
 
+def moe_case(be, qmm, synth, T, args):
+    """MUL_MAT_ID on config 3's expert gate/up: 512 Q4_K experts of 512 x 2048,
+    top-10 routing, T tokens sharing one activation column each (ne11 = 1).
+    One step = one MUL_MAT_ID (pre-pass, on-GPU routing, expert GEMV tasks)
+    with the next of 16 router id sets; GB/s counts the weight bytes of the
+    experts that step touches."""
+    E, n_used, M, K = 512, 10, 512, 2048
+    raw = synth.weights(qmm.Q4_K, E * M, K, seed=4)
+    w = be.new_tensor(qmm.Q4_K, (K, M, E))
+    be.set_tensor(w, raw)
+    ebytes = raw.nbytes // E
+    idsets, touched = [], []
+    for k in range(16):
+        ids = synth.moe_ids(T, E, n_used, seed=100 + k)
+        t = be.new_tensor(qmm.I32, (n_used, T))
+        be.set_tensor(t, ids.view(np.uint8).ravel())
+        idsets.append(t)
+        touched.append(len(np.unique(ids)) * ebytes)
+    x = synth.activations(T, K, seed=5)
+    xt = be.new_tensor(qmm.F32, (K, 1, T))
+    be.set_tensor(xt, x.view(np.uint8).ravel())
+    yt = be.new_tensor(qmm.F32, (M, n_used, T))
+    steps = max(16, args.steps // 2)
+    for i in range(16):
+        be.mul_mat_id(w, xt, idsets[i % 16], yt)
+    be.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        be.mul_mat_id(w, xt, idsets[i % 16], yt)
+    be.synchronize()
+    wall = time.perf_counter() - t0
+    be.kernel_timing(True)
+    for i in range(steps):
+        be.mul_mat_id(w, xt, idsets[i % 16], yt)
+    k_ms, n = be.kernel_time()
+    be.kernel_timing(False)
+    bytes_step = float(np.mean(touched))
+    us = wall * 1e6 / steps
+    k_us = k_ms / max(n, 1) * 1e3
+    out = {"workload": f"MUL_MAT_ID Q4_K 512 experts x (512 x 2048), top-10, T={T} (config 3 gate/up)",
+           "path": be.last_path(), "us_per_op": round(us, 3), "expert_bytes_touched": int(bytes_step),
+           "GBs": round(bytes_step / (us * 1e-6) / 1e9, 1), "kernel_us": round(k_us, 3),
+           "kernel_GBs": round(bytes_step / (k_us * 1e-6) / 1e9, 1)}
+    for t in idsets:
+        be.free_buffer(t.buf)
+    for t in (w, xt, yt):
+        be.free_buffer(t.buf)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -140,7 +192,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
-    ap.add_argument("--only", default="", help="profile one workload: q4k_gemv, q40_gemm or q4k_gemm")
+    ap.add_argument("--only", default="", help="profile one workload: q4k_gemv, q40_gemm, q4k_gemm or moe")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -201,6 +253,12 @@ def main():
             out["gemm"] = secs
         else:
             out = {"metric": "GEMM TOPS at N=512", "value": secs[0]["tops"], "unit": "TOPS", "gemm": secs}
+    if not args.no_secondary and args.only in ("", "moe"):
+        moe = [moe_case(be, qmm, synth, T, args) for T in (1, 4, 256)]
+        if out:
+            out["moe"] = moe
+        else:
+            out = {"metric": "MUL_MAT_ID GB/s", "value": moe[-1]["GBs"], "unit": "GB/s", "moe": moe}
     be.close()
     print(json.dumps(out), flush=True)
 
