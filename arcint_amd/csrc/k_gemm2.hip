@@ -1,4 +1,4 @@
-// k_gemm2.hip - prefill GEMM (N >= 16 columns) for Q4_0 and Q4_K on gfx950
+// k_gemm2.hip - prefill GEMM (N >= 16 columns) for Q4_0, Q8_0 and Q4_K on gfx950
 // v_mfma_i32_32x32x32_i8.
 //
 // Role of the reference's int8 prefill GEMMs (kernel_mul_mm_kq2d_q4_0_i8,
@@ -17,7 +17,7 @@
 //    integer dot, as in ggml_vec_dot_*.  With BN = 64 two waves share each
 //    tile, one taking blocks 0 and 2 of every stage and the other blocks 1
 //    and 3, and their sums meet in LDS at the end (no atomics);
-//  * Q4_0: the weight operand is q - 8.  The MFMA adds the block's dot i to
+//  * Q4_0 / Q8_0: the weight operand is q - 8 / q.  The MFMA adds the block's dot i to
 //    the bits of the float 12582912 (= 1.5 * 2^23), so fma(result, d_w,
 //    -12582912 d_w) is i * d_w rounded once (12582912 d_w is exact), and
 //    acc += d_x * that: two VALU ops per output and block;
@@ -125,6 +125,7 @@ template <int TYPE, int BN>
 __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per SIMD: one work-group per CU
     using LY = Lay<TYPE, BN>;
     constexpr bool KQ = LY::KQ;
+    constexpr bool Q8 = TYPE == QMM_TYPE_Q8_0;                    // Q4_0's path with plain int8 codes
     constexpr int NWN = BN / 32;                                  // column groups of 32
     constexpr int KSPLIT = 4 / NWN;                               // waves sharing a tile (BN 128: 1, 64: 2)
     constexpr int NQ = 4 / KSPLIT;                                // blocks per stage and wave
@@ -154,6 +155,17 @@ __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per 
     int64_t st_img = 2 * mtile + st_tile;
     st_img = st_img < p.w.ntiles ? st_img : p.w.ntiles - 1;      // a missing second tile re-reads the first
     const uint8_t * wbase = tile_group(p.w, mat, st_img, 0) + st_row * 16;
+    // Q8_0: thread tid stages chunk q8_ch = (tid / 64) % 8 of row tid % 64 of both tiles
+    const int q8_ch = (tid >> 6) & 7;
+    const uint8_t * wbase8[2];
+    if constexpr (Q8) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            int64_t img = 2 * mtile + t;
+            img = img < p.w.ntiles ? img : p.w.ntiles - 1;
+            wbase8[t] = tile_group(p.w, mat, img, 0) + st_row * 16;
+        }
+    }
     const int8_t * abase[NA];
 #pragma unroll
     for (int q = 0; q < NA; ++q) {
@@ -171,11 +183,22 @@ __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per 
 #pragma unroll
         for (int q = 0; q < NA; ++q) R.a[q] = *reinterpret_cast<const uint4 *>(abase[q] + s * kSK);
         const uint8_t * tg = wbase + (size_t)g * p.w.tg;
-        R.c = ld16(tg + (4 * hh + st_cs) * kChunk);
+        if constexpr (Q8) {
+            // chunks 8 hh .. 8 hh + 7 are blocks 4 hh .. 4 hh + 3 (two halves each); d of the group in chunk 16
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const uint8_t * tgt = wbase8[t] + (size_t)g * p.w.tg;
+                const uint4 v = ld16(tgt + (8 * hh + q8_ch) * kChunk);
+                const uint32_t dd = *reinterpret_cast<const uint32_t *>(tgt + 16 * kChunk + 8 * hh + 4 * (q8_ch >> 2));
+                if (t == 0) { R.c = v; R.h.x = dd; } else { R.s = v; R.h.y = dd; }
+            }
+        } else {
+            R.c = ld16(tg + (4 * hh + st_cs) * kChunk);
+        }
         if constexpr (KQ) {
             R.h = ld16(tg + 8 * kChunk);
             R.s = *reinterpret_cast<const uint4 *>(sbase + (int64_t)g * p.ldT * 16);
-        } else {
+        } else if constexpr (!Q8) {
             R.h.x = *reinterpret_cast<const uint32_t *>(tg + 8 * kChunk + 4 * (2 * hh + (st_cs >> 1)));
         }
         R.x = xbase[(KQ ? (int64_t)g : (int64_t)s * 4 + x_blk) * p.ldT];
@@ -193,7 +216,18 @@ __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per 
             *reinterpret_cast<uint4 *>(A + (u >> 3) * kAP + (u & 7) * 16) = R.a[q];
         }
         const uint32_t e[4] = { R.c.x, R.c.y, R.c.z, R.c.w };
-        if constexpr (!KQ) {
+        if constexpr (Q8) {
+            // chunk ch of the stage = half ch % 2 of block ch / 2: the layout of the B planes as is
+            *reinterpret_cast<uint4 *>(B + q8_ch * kChunk + st_row * 16) = R.c;
+            *reinterpret_cast<uint4 *>(B + (8 + q8_ch) * kChunk + st_row * 16) = R.s;
+            if ((q8_ch & 1) == 0) {                               // d of block ch / 2 of the stage
+                const int blk = q8_ch >> 1;
+                float * wd = reinterpret_cast<float *>(W) + blk * 64 + st_row;
+                wd[0] = h2f(R.h.x >> (16 * (blk & 1)));
+                wd[4 * 64] = h2f(R.h.y >> (16 * (blk & 1)));
+            }
+            if (tid < 4 * BN) X[tid] = R.x;                       // [block][col]
+        } else if constexpr (!KQ) {
             // chunk 4 hh + cs is block cs of the stage: low nibbles k < 16, high nibbles k >= 16
             uint4 lo, hi;
             lo.x = q4_minus8(e[0] & 0x0F0F0F0Fu); hi.x = q4_minus8((e[0] >> 4) & 0x0F0F0F0Fu);
@@ -489,7 +523,7 @@ G2Shape g2_shape(const WView & w, int64_t N, int64_t nbatch) {
 
 }  // namespace
 
-bool gemm2_supported(int type) { return type == QMM_TYPE_Q4_0 || type == QMM_TYPE_Q4_K; }
+bool gemm2_supported(int type) { return type == QMM_TYPE_Q4_0 || type == QMM_TYPE_Q8_0 || type == QMM_TYPE_Q4_K; }
 
 int gemm2_kslices(const WView & w, int64_t N, int64_t nbatch) { return g2_shape(w, N, nbatch).KS; }
 
@@ -528,6 +562,8 @@ hipError_t launch_gemm2(int type, const WView & w, const ActBuf & a, int64_t N, 
     const dim3 g((unsigned)grid, (unsigned)nbatch);
     if (type == QMM_TYPE_Q4_0)
         return sh.BN == 64 ? launch_t<QMM_TYPE_Q4_0, 64>(p, g, s, kt) : launch_t<QMM_TYPE_Q4_0, 128>(p, g, s, kt);
+    if (type == QMM_TYPE_Q8_0)
+        return sh.BN == 64 ? launch_t<QMM_TYPE_Q8_0, 64>(p, g, s, kt) : launch_t<QMM_TYPE_Q8_0, 128>(p, g, s, kt);
     return sh.BN == 64 ? launch_t<QMM_TYPE_Q4_K, 64>(p, g, s, kt) : launch_t<QMM_TYPE_Q4_K, 128>(p, g, s, kt);
 }
 

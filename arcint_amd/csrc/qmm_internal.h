@@ -190,7 +190,7 @@ hipError_t launch_gemm(int type, const WView & w, const ActBuf & a, int64_t N, i
 // K slices the GEMM splits this product into; above 1 the slices add their
 // partial sums to dst with atomics, so dst must be zeroed first.
 int gemm_kslices(int type, const WView & w, int64_t N, int64_t nbatch);
-// the 32x32x32 int8 MFMA GEMM (Q4_0, Q4_K), used by launch_gemm
+// the 32x32x32 int8 MFMA GEMM (Q4_0, Q8_0, Q4_K), used by launch_gemm
 bool gemm_uses_v2(int type);
 bool gemm2_supported(int type);
 int gemm2_kslices(const WView & w, int64_t N, int64_t nbatch);
