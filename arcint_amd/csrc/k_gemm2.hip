@@ -1,9 +1,10 @@
-// k_gemm2.hip - prefill GEMM (N >= 16 columns) for Q4_0, Q8_0 and Q4_K on gfx950
-// v_mfma_i32_32x32x32_i8.
+// k_gemm2.hip - prefill GEMM (N >= 16 columns) for the five weight types on
+// gfx950 v_mfma_i32_32x32x32_i8.
 //
-// Role of the reference's int8 prefill GEMMs (kernel_mul_mm_kq2d_q4_0_i8,
-// P0099:377-455, and kernel_mul_mm_kq2d_q4_K_i8, P01:1919-2024), redesigned
-// for CDNA4 and for ggml-cpu's numerics:
+// Role of the reference's prefill GEMMs (the int8 kernel_mul_mm_kq2d_q4_0_i8,
+// P0099:377-455, and kernel_mul_mm_kq2d_q4_K_i8, P01:1919-2024, and the fp16
+// tile kernels kernel_mul_mm_{q6_K,iq4_xs,q8_0}_f16, P01:2317-2406,
+// P02:4359-4384), redesigned for CDNA4 and for ggml-cpu's numerics:
 //  * a work-group (8 waves) owns 128 weight rows (two 64-row tiles of the
 //    weight image) x BN activation columns (BN = 128 or 64) and walks K in
 //    stages of 128 (half a group).  Per stage it stages in LDS the activation
@@ -27,6 +28,11 @@
 //    accumulates inside the MFMA in int32.  The min term sum_j m_j bsum_j
 //    takes two MFMAs per super-block: the activation sub-block sums split as
 //    bsum = 64 bh + bl (bh in [-64, 63], bl in [0, 63]) against the 8 mins;
+//  * IQ4_XS (codebook values, 6-bit scale per 32) and Q6_K (q - 32, int8
+//    scale per 16): the scaled weights do not fit int8, so each (sub-)block
+//    dot comes from a fresh MFMA and is multiplied by its integer scale into
+//    an int32 sum on the VALU (Q6_K: one MFMA per 16-weight half, the other
+//    half's operand zero); the float combine runs once per super-block;
 //  * work-groups are numbered so that those sharing weight rows land on the
 //    same XCD.  Small products split K over KS work-groups that add their
 //    partial sums to dst (zeroed by the activation pre-pass) atomically.
@@ -62,12 +68,18 @@ constexpr int kMagic = 0x4B400000;       // float 12582912: its bits + i are the
 //            [tile 2][row 64] float2                  (d, dmin)
 //         X  [col BN] f32                             d_x of the super-block
 //         S  [col BN] x 16 B                          bh[8], bl[8] of the super-block
+//   IQ4_XS, Q6_K (integer sub-block scales)
+//         B  [tile 2][block 4][h 2][row 64] x 16 B    codebook value / q - 32
+//         W  [tile 2][block 4][h 2][row 64] i32        ls - 32 (IQ4_XS: h = 0) / the 16-weight scale (Q6_K)
+//            [tile 2][row 64] f32                     d
+//         X  [col BN] f32                             d_x of the super-block
 template <int TYPE, int BN> struct Lay {
     static constexpr bool KQ = TYPE == QMM_TYPE_Q4_K;
+    static constexpr bool IS = TYPE == QMM_TYPE_IQ4_XS || TYPE == QMM_TYPE_Q6_K;
     static constexpr int A = BN * kAP;
     static constexpr int B = KQ ? 2 * 4 * 2 * 2 * kChunk : 2 * 4 * 2 * kChunk;
-    static constexpr int W = KQ ? 2 * 64 * 16 + 2 * 64 * 8 : 2 * 4 * 64 * 4;
-    static constexpr int X = KQ ? BN * 4 : 4 * BN * 4;
+    static constexpr int W = KQ ? 2 * 64 * 16 + 2 * 64 * 8 : IS ? 2 * 4 * 2 * 64 * 4 + 2 * 64 * 4 : 2 * 4 * 64 * 4;
+    static constexpr int X = (KQ || IS) ? BN * 4 : 4 * BN * 4;
     static constexpr int S = KQ ? BN * 16 : 0;
     static constexpr int oB = A, oW = oB + B, oX = oW + W, oS = oX + X;
     static constexpr int stage = oS + S;
@@ -126,6 +138,9 @@ __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per 
     using LY = Lay<TYPE, BN>;
     constexpr bool KQ = LY::KQ;
     constexpr bool Q8 = TYPE == QMM_TYPE_Q8_0;                    // Q4_0's path with plain int8 codes
+    constexpr bool IS = LY::IS;                                   // integer sub-block scales (IQ4_XS, Q6_K)
+    constexpr bool Q6 = TYPE == QMM_TYPE_Q6_K;
+    constexpr bool BF = !KQ && !IS;                               // a float scale per block (Q4_0, Q8_0)
     constexpr int NWN = BN / 32;                                  // column groups of 32
     constexpr int KSPLIT = 4 / NWN;                               // waves sharing a tile (BN 128: 1, 64: 2)
     constexpr int NQ = 4 / KSPLIT;                                // blocks per stage and wave
@@ -154,7 +169,8 @@ __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per 
     const int st_tile = tid >> 8, st_cs = (tid >> 6) & 3, st_row = tid & 63;
     int64_t st_img = 2 * mtile + st_tile;
     st_img = st_img < p.w.ntiles ? st_img : p.w.ntiles - 1;      // a missing second tile re-reads the first
-    const uint8_t * wbase = tile_group(p.w, mat, st_img, 0) + st_row * 16;
+    const uint8_t * tbase = tile_group(p.w, mat, st_img, 0);      // tile-group 0 of the staged tile
+    const uint8_t * wbase = tbase + st_row * 16;
     // Q8_0: thread tid stages chunk q8_ch = (tid / 64) % 8 of row tid % 64 of both tiles
     const int q8_ch = (tid >> 6) & 7;
     const uint8_t * wbase8[2];
@@ -173,7 +189,7 @@ __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per 
         const int64_t c = std::min<int64_t>(n0 + (u >> 3), p.N - 1);
         abase[q] = p.xc + (col0 + c) * p.ldk + (u & 7) * 16;
     }
-    const int x_blk = KQ ? 0 : (tid / BN) & 3;                    // Q4_0: 4 blocks x BN columns
+    const int x_blk = BF ? (tid / BN) & 3 : 0;                    // q8_0: 4 blocks x BN columns
     const int64_t x_col = col0 + std::min<int64_t>(n0 + tid % BN, p.N - 1);
     const float * xbase = p.dT + x_col;
     const int8_t * sbase = KQ ? p.bsp + x_col * 16 : nullptr;
@@ -198,10 +214,22 @@ __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per 
         if constexpr (KQ) {
             R.h = ld16(tg + 8 * kChunk);
             R.s = *reinterpret_cast<const uint4 *>(sbase + (int64_t)g * p.ldT * 16);
+        } else if constexpr (TYPE == QMM_TYPE_IQ4_XS) {
+            // the row's 8-byte header {d, scales_h, scales_l[4]} in the tail plane
+            const uint2 hd = *reinterpret_cast<const uint2 *>(tbase + (size_t)g * p.w.tg + 8 * kChunk + st_row * 8);
+            R.h.x = hd.x;
+            R.h.y = hd.y;
+        } else if constexpr (Q6) {
+            // qh chunk 8 + 2 hh + cs % 2, the stage's 8 scales, d in the tail plane
+            R.s = ld16(tg + (8 + 2 * hh + (st_cs & 1)) * kChunk);
+            const uint2 sc = *reinterpret_cast<const uint2 *>(tg + 12 * kChunk + 8 * hh);
+            R.h.x = sc.x;
+            R.h.y = sc.y;
+            R.h.z = *reinterpret_cast<const uint16_t *>(tbase + (size_t)g * p.w.tg + 13 * kChunk + st_row * 2);
         } else if constexpr (!Q8) {
             R.h.x = *reinterpret_cast<const uint32_t *>(tg + 8 * kChunk + 4 * (2 * hh + (st_cs >> 1)));
         }
-        R.x = xbase[(KQ ? (int64_t)g : (int64_t)s * 4 + x_blk) * p.ldT];
+        R.x = xbase[(BF ? (int64_t)s * 4 + x_blk : (int64_t)g) * p.ldT];
         return R;
     };
     auto store = [&](const StageRegs R, int buf, int s) {
@@ -227,6 +255,44 @@ __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per 
                 wd[4 * 64] = h2f(R.h.y >> (16 * (blk & 1)));
             }
             if (tid < 4 * BN) X[tid] = R.x;                       // [block][col]
+        } else if constexpr (TYPE == QMM_TYPE_IQ4_XS) {
+            // chunk 4 hh + cs is sub-block cs of the stage: low nibbles k < 16, high nibbles k >= 16,
+            // through the codebook; its scale ls - 32 (P01:3390-3398)
+            uint4 lo, hi;
+            lo.x = iq4_lookup(e[0] & 0x0F0F0F0Fu); hi.x = iq4_lookup((e[0] >> 4) & 0x0F0F0F0Fu);
+            lo.y = iq4_lookup(e[1] & 0x0F0F0F0Fu); hi.y = iq4_lookup((e[1] >> 4) & 0x0F0F0F0Fu);
+            lo.z = iq4_lookup(e[2] & 0x0F0F0F0Fu); hi.z = iq4_lookup((e[2] >> 4) & 0x0F0F0F0Fu);
+            lo.w = iq4_lookup(e[3] & 0x0F0F0F0Fu); hi.w = iq4_lookup((e[3] >> 4) & 0x0F0F0F0Fu);
+            uint8_t * b = B + ((st_tile * 4 + st_cs) * 2) * kChunk + st_row * 16;
+            *reinterpret_cast<uint4 *>(b) = lo;
+            *reinterpret_cast<uint4 *>(b + kChunk) = hi;
+            const int ib = 4 * hh + st_cs;
+            const int ls = (int)(((R.h.y >> (4 * ib)) & 0xFu) | ((((R.h.x >> 16) >> (2 * ib)) & 3u) << 4));
+            reinterpret_cast<int *>(W)[((st_tile * 4 + st_cs) * 2) * 64 + st_row] = ls - 32;
+            if (st_cs == 0) reinterpret_cast<float *>(W + 2 * 4 * 2 * 64 * 4)[st_tile * 64 + st_row] = h2f(R.h.x);
+            if (tid < BN) X[tid] = R.x;
+        } else if constexpr (Q6) {
+            // ql chunk 4 hh + cs: low nibbles of block cs / 2, high nibbles of block cs / 2 + 2, both half
+            // lh = cs % 2 (16 weights); qh bits 2 g .. 2 g + 1 of chunk 8 + 2 hh + lh; code - 32
+            const int lh = st_cs & 1, gl = st_cs >> 1;
+            const uint32_t qh[4] = { R.s.x, R.s.y, R.s.z, R.s.w };
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const int g = gl + 2 * t;
+                uint32_t v[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t c = ((e[i] >> (4 * t)) & 0x0F0F0F0Fu) | (((qh[i] >> (2 * g)) & 0x03030303u) << 4);
+                    v[i] = ((c | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+                }
+                *reinterpret_cast<uint4 *>(B + ((st_tile * 4 + g) * 2 + lh) * kChunk + st_row * 16) =
+                    make_uint4(v[0], v[1], v[2], v[3]);
+                const uint32_t scw = t ? R.h.y : R.h.x;           // scales 8 hh + 4 t .. + 3
+                reinterpret_cast<int *>(W)[((st_tile * 4 + g) * 2 + lh) * 64 + st_row] =
+                    (int)(int8_t)((scw >> (8 * st_cs)) & 0xffu);
+            }
+            if (st_cs == 0) reinterpret_cast<float *>(W + 2 * 4 * 2 * 64 * 4)[st_tile * 64 + st_row] = h2f(R.h.z);
+            if (tid < BN) X[tid] = R.x;
         } else if constexpr (!KQ) {
             // chunk 4 hh + cs is block cs of the stage: low nibbles k < 16, high nibbles k >= 16
             uint4 lo, hi;
@@ -297,8 +363,9 @@ __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per 
     struct Ops {
         v4i a;                           // activation codes of this wave's 32 columns
         v4i b[2][2];                     // [row tile][0: q - 8 (Q4_0) or q * sh (Q4_K), 1: q * sl]
-        float dw[2];                     // Q4_0: d_w of the lane's rows
-        float dx[16];                    // Q4_0: d_x of the lane's 16 columns
+        float dw[2];                     // Q4_0, Q8_0: d_w of the lane's rows
+        float dx[16];                    // Q4_0, Q8_0: d_x of the lane's 16 columns
+        int sc[2][2];                    // IQ4_XS, Q6_K: [row tile][16-weight half] integer scale
     };
     auto load_ops = [&](int buf, int q) -> Ops {
         Ops o;
@@ -310,16 +377,20 @@ __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per 
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt) {
             const int row = 32 * rt + l32;
-            if constexpr (!KQ) {
+            if constexpr (BF) {
                 o.b[rt][0] = *reinterpret_cast<const v4i *>(B + ((wr * 4 + q) * 2 + h) * kChunk + row * 16);
                 o.dw[rt] = reinterpret_cast<const float *>(W)[(wr * 4 + q) * 64 + row];
+            } else if constexpr (IS) {
+                o.b[rt][0] = *reinterpret_cast<const v4i *>(B + ((wr * 4 + q) * 2 + h) * kChunk + row * 16);
+                o.sc[rt][0] = reinterpret_cast<const int *>(W)[((wr * 4 + q) * 2) * 64 + row];
+                if constexpr (Q6) o.sc[rt][1] = reinterpret_cast<const int *>(W)[((wr * 4 + q) * 2 + 1) * 64 + row];
             } else {
                 const uint8_t * b = B + (((wr * 4 + q) * 2 + h) * 2) * kChunk + row * 16;
                 o.b[rt][0] = *reinterpret_cast<const v4i *>(b);
                 o.b[rt][1] = *reinterpret_cast<const v4i *>(b + kChunk);
             }
         }
-        if constexpr (!KQ) {
+        if constexpr (BF) {
 #pragma unroll
             for (int g4 = 0; g4 < 4; ++g4) {
                 const float4 v = *reinterpret_cast<const float4 *>(X + q * BN + wn * 32 + 8 * g4 + 4 * h);
@@ -329,7 +400,7 @@ __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per 
         return o;
     };
     auto mma = [&](const Ops o) {
-        if constexpr (!KQ) {
+        if constexpr (BF) {
             const v16i d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a, o.b[0][0], magic, 0, 0, 0);
             const v16i d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a, o.b[1][0], magic, 0, 0, 0);
             const float nm0 = -12582912.0f * o.dw[0], nm1 = -12582912.0f * o.dw[1];
@@ -345,6 +416,23 @@ __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per 
             }
             // keep this block's products from being deferred past later MFMAs (register pressure)
             asm volatile("" : "+v"(out0), "+v"(out1));
+        } else if constexpr (IS) {
+            // the (sub-)block dot from a fresh MFMA, times its integer scale into isum (c1).  Q6_K's
+            // scale changes every 16 weights: one MFMA per lane half, the other half's operand zero.
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) {
+                if constexpr (!Q6) {
+                    const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a, o.b[rt][0], v16i{}, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) c1[rt][r] += o.sc[rt][0] * d[r];
+                } else {
+                    const v4i zero = v4i{ 0, 0, 0, 0 };
+                    const v16i d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a, h ? zero : o.b[rt][0], v16i{}, 0, 0, 0);
+                    const v16i d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a, h ? o.b[rt][0] : zero, v16i{}, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) c1[rt][r] += o.sc[rt][0] * d0[r] + o.sc[rt][1] * d1[r];
+                }
+            }
         } else {
 #pragma unroll
             for (int rt = 0; rt < 2; ++rt) {
@@ -354,7 +442,7 @@ __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per 
         }
     };
     auto compute = [&](int buf, int s) {
-        if constexpr (!KQ) {
+        if constexpr (BF) {
             Ops o0 = load_ops(buf, wk), o1;
 #pragma unroll
             for (int i = 0; i < NQ; ++i) {
@@ -367,6 +455,29 @@ __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per 
         } else {                                                  // (registers: no second operand set)
 #pragma unroll
             for (int i = 0; i < NQ; ++i) mma(load_ops(buf, wk + i * KSPLIT));
+        }
+        if constexpr (IS) {
+            if (s & 1) {                                          // end of the super-block (uniform)
+                const float * X = reinterpret_cast<const float *>(lds + buf * kStage + LY::oX);
+                const float * Wd = reinterpret_cast<const float *>(lds + buf * kStage + LY::oW + 2 * 4 * 2 * 64 * 4);
+                float dx[16];
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4) {
+                    const float4 v = *reinterpret_cast<const float4 *>(X + wn * 32 + 8 * g4 + 4 * h);
+                    dx[4 * g4] = v.x; dx[4 * g4 + 1] = v.y; dx[4 * g4 + 2] = v.z; dx[4 * g4 + 3] = v.w;
+                }
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt) {
+                    const float d = Wd[wr * 64 + 32 * rt + l32];
+                    v16f & o = rt ? out1 : out0;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int is = c1[rt][r];
+                        o[r] = __builtin_fmaf(dx[r], d * (float)is, o[r]);
+                    }
+                    c1[rt] = v16i{};
+                }
+            }
         }
         if constexpr (KQ) {
             if (s & 1) {                                          // end of the super-block (uniform)
@@ -492,12 +603,13 @@ hipError_t launch_t(const G2Params & p, const dim3 & g, hipStream_t s, const KTi
     return hipGetLastError();
 }
 
-// Launch shape: column tile BN, K slices KS and stages per slice spk.  The
-// 64-column tile (whose stages cost more than half of a 128-column stage:
-// the weight staging and the barrier do not shrink with it) is used only
-// when 128-column tiles cannot give every CU a work-group; K is split
-// (atomics, ~4x the cost of a store) only when even 64-column tiles leave
-// most of the chip idle.
+// Launch shape: column tile BN, K slices KS and stages per slice spk, from a
+// cost model fitted to measurements on MI355X: a work-group stage costs ~2 us
+// at BN = 128 and 0.62 of that at BN = 64 (the weight staging and the barrier
+// do not shrink with the tile); work-groups run in rounds of one per CU; K
+// slices add their partial sums with float atomics (~480 adds per ns over the
+// chip), after the pre-pass zeroed dst.  Each candidate (BN, KS) is priced as
+// rounds x stages x stage cost + atomics and the cheapest is taken.
 struct G2Shape {
     int BN, KS, spk;
     int64_t mt, nt;
@@ -507,36 +619,52 @@ G2Shape g2_shape(const WView & w, int64_t N, int64_t nbatch) {
         const char * e = getenv("QMM_GEMM_CUS");
         return e ? std::max<int64_t>(1, atoll(e)) : (int64_t)256;
     }();
-    G2Shape sh;
-    sh.mt = (w.M + 127) / 128;
-    const int64_t w128 = sh.mt * ((N + 127) / 128) * nbatch;
-    sh.BN = (N <= 64 || w128 < cus) ? 64 : 128;
-    sh.nt = (N + sh.BN - 1) / sh.BN;
-    const int64_t wgs = sh.mt * sh.nt * nbatch;
-    int64_t ks = 1;
-    if (wgs * 2 < cus) ks = std::min<int64_t>(w.G, cus / wgs);
-    const int64_t gps = (w.G + ks - 1) / ks;
-    sh.spk = (int)(2 * gps);
-    sh.KS = (int)((w.G + gps - 1) / gps);
-    return sh;
+    G2Shape best{};
+    double best_us = 1e300;
+    const int64_t mt = (w.M + 127) / 128;
+    for (int bn : { 128, 64 }) {
+        const int64_t nt = (N + bn - 1) / bn;
+        int64_t prev_gps = -1;
+        for (int64_t ks = 1; ks <= std::min<int64_t>(w.G, 64); ++ks) {
+            const int64_t gps = (w.G + ks - 1) / ks;
+            if (gps == prev_gps) continue;                        // same split as a smaller ks
+            prev_gps = gps;
+            const int64_t kss = (w.G + gps - 1) / gps;
+            const int64_t wgs = mt * nt * nbatch * kss;
+            const double rounds = (double)((wgs + cus - 1) / cus);
+            double us = rounds * (double)(2 * gps) * 2.0 * (bn == 64 ? 0.62 : 1.0);
+            if (kss > 1) us += (double)w.M * (double)N * (double)nbatch * (double)kss / 480000.0;
+            if (us < best_us * 0.98) {                            // prefer the earlier (wider, unsplit) shape on ties
+                best_us = us;
+                best = G2Shape{ bn, (int)kss, (int)(2 * gps), mt, nt };
+            }
+        }
+    }
+    return best;
 }
 
 }  // namespace
 
-bool gemm2_supported(int type) { return type == QMM_TYPE_Q4_0 || type == QMM_TYPE_Q8_0 || type == QMM_TYPE_Q4_K; }
+int gemm_kslices(const WView & w, int64_t N, int64_t nbatch) { return g2_shape(w, N, nbatch).KS; }
 
-int gemm2_kslices(const WView & w, int64_t N, int64_t nbatch) { return g2_shape(w, N, nbatch).KS; }
-
-void gemm2_shape(const WView & w, int64_t N, int64_t nbatch, int64_t * workgroups, int * threads, int * lds_bytes) {
+void gemm_shape(int type, const WView & w, int64_t N, int64_t nbatch, int64_t * workgroups, int * threads,
+                int * lds_bytes) {
     const G2Shape sh = g2_shape(w, N, nbatch);
     *workgroups = sh.mt * sh.nt * sh.KS * nbatch;
     *threads = kT;
-    *lds_bytes = 2 * (sh.BN == 64 ? Lay<QMM_TYPE_Q4_K, 64>::stage : Lay<QMM_TYPE_Q4_K, 128>::stage);
+    int st;
+    switch (type) {
+        case QMM_TYPE_Q4_K: st = sh.BN == 64 ? Lay<QMM_TYPE_Q4_K, 64>::stage : Lay<QMM_TYPE_Q4_K, 128>::stage; break;
+        case QMM_TYPE_Q6_K:
+        case QMM_TYPE_IQ4_XS: st = sh.BN == 64 ? Lay<QMM_TYPE_Q6_K, 64>::stage : Lay<QMM_TYPE_Q6_K, 128>::stage; break;
+        default: st = sh.BN == 64 ? Lay<QMM_TYPE_Q4_0, 64>::stage : Lay<QMM_TYPE_Q4_0, 128>::stage; break;
+    }
+    *lds_bytes = 2 * st;
 }
 
-hipError_t launch_gemm2(int type, const WView & w, const ActBuf & a, int64_t N, int64_t nbatch, const GemmBatch & bt,
-                        float * dst, hipStream_t s, const KTime * kt) {
-    if (!gemm2_supported(type) || !a.dT || a.ldk != w.G * 256 || a.ldT < N * nbatch + 64 || N <= 0 || nbatch <= 0 ||
+hipError_t launch_gemm(int type, const WView & w, const ActBuf & a, int64_t N, int64_t nbatch, const GemmBatch & bt,
+                       float * dst, hipStream_t s, const KTime * kt) {
+    if (!a.dT || a.ldk != w.G * 256 || a.ldT < N * nbatch + 64 || N <= 0 || nbatch <= 0 ||
         nbatch > 65535 || a.vdt != vec_dot_type(type) || (type == QMM_TYPE_Q4_K && !a.bsp))
         return hipErrorInvalidValue;
     const G2Shape sh = g2_shape(w, N, nbatch);
@@ -564,7 +692,13 @@ hipError_t launch_gemm2(int type, const WView & w, const ActBuf & a, int64_t N, 
         return sh.BN == 64 ? launch_t<QMM_TYPE_Q4_0, 64>(p, g, s, kt) : launch_t<QMM_TYPE_Q4_0, 128>(p, g, s, kt);
     if (type == QMM_TYPE_Q8_0)
         return sh.BN == 64 ? launch_t<QMM_TYPE_Q8_0, 64>(p, g, s, kt) : launch_t<QMM_TYPE_Q8_0, 128>(p, g, s, kt);
-    return sh.BN == 64 ? launch_t<QMM_TYPE_Q4_K, 64>(p, g, s, kt) : launch_t<QMM_TYPE_Q4_K, 128>(p, g, s, kt);
+    if (type == QMM_TYPE_Q6_K)
+        return sh.BN == 64 ? launch_t<QMM_TYPE_Q6_K, 64>(p, g, s, kt) : launch_t<QMM_TYPE_Q6_K, 128>(p, g, s, kt);
+    if (type == QMM_TYPE_IQ4_XS)
+        return sh.BN == 64 ? launch_t<QMM_TYPE_IQ4_XS, 64>(p, g, s, kt) : launch_t<QMM_TYPE_IQ4_XS, 128>(p, g, s, kt);
+    if (type == QMM_TYPE_Q4_K)
+        return sh.BN == 64 ? launch_t<QMM_TYPE_Q4_K, 64>(p, g, s, kt) : launch_t<QMM_TYPE_Q4_K, 128>(p, g, s, kt);
+    return hipErrorInvalidValue;
 }
 
 }  // namespace qmm

@@ -521,21 +521,16 @@ int qmm_describe_mul_mat(const qmm_tensor * src0, const qmm_tensor * src1, const
     const ImageShape sh = [&] { ImageShape t; image_shape(*type_layout(src0->type), src0->ne, &t); return t; }();
     if (N >= gemm_min_cols()) {
         snprintf(out->path, sizeof(out->path), "gemm-mfma");
-        out->threads = 256;
         out->tasks = src1->ne[2] * src1->ne[3];
         out->cols_per_task = (int32_t)std::min<int64_t>(N, INT32_MAX);
-        out->workgroups = ((sh.M + 63) / 64) * ((N + 63) / 64) * out->tasks;
-        out->k_slices = 1;
         fake.ptr = nullptr;
         fake.size = 0;
         const WView w = weight_view(&a);
-        if (gemm_uses_v2(src0->type)) {
-            int threads, lds;
-            gemm2_shape(w, N, out->tasks, &out->workgroups, &threads, &lds);
-            out->threads = threads;
-            out->lds_bytes = lds;
-            out->k_slices = gemm_kslices(src0->type, w, N, out->tasks);
-        }
+        int threads, lds;
+        gemm_shape(src0->type, w, N, out->tasks, &out->workgroups, &threads, &lds);
+        out->threads = threads;
+        out->lds_bytes = lds;
+        out->k_slices = gemm_kslices(w, N, out->tasks);
         return QMM_OK;
     }
     fake.ptr = nullptr;
@@ -581,7 +576,7 @@ int qmm_mul_mat(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1,
     if (use_gemm) {
         const int64_t nbatch = dn.ne12 * dn.ne13;
         ZeroJob z{ d, w.M, N * nbatch, N, dn.ne12, dn.d_nb1, dn.d_nb2, dn.d_nb3 };
-        const bool split = gemm_kslices(src0->type, w, N, nbatch) > 1;
+        const bool split = gemm_kslices(w, N, nbatch) > 1;
         if ((rc = quantize_src1(ctx, src0->type, src1, true, &a, split ? &z : nullptr))) return rc;
         GemmBatch bt;
         bt.ne12 = dn.ne12;

@@ -178,9 +178,10 @@ hipError_t launch_gemv(int type, const WView & w, const GemvPlan & plan, const A
                        const int32_t * ntasks_dev, const GemvDense * dense, float * dst, const void * sink,
                        hipStream_t s, const KTime * kt = nullptr);
 
-// Prefill GEMM (int8 MFMA): for every batch b < nbatch, dst[doff(b) + n * d_nb1
-// + m] = W(mat(b)) row m . activation column col0(b) + n, for n < N, m < M.
-// Activations come from the pre-pass with block-major scales (a.dT).
+// Prefill GEMM (int8 MFMA, all five types): for every batch b < nbatch,
+// dst[doff(b) + n * d_nb1 + m] = W(mat(b)) row m . activation column
+// col0(b) + n, for n < N, m < M.  Activations come from the pre-pass with
+// block-major scales (a.dT) and, for q8_K, the split sub-block sums (a.bsp).
 struct GemmBatch {
     int64_t ne12, r2, r3, ne02;    // batch b = (i2, i3): mat = i2 / r2 + (i3 / r3) * ne02
     int64_t d_nb1, d_nb2, d_nb3;   // dst strides in floats
@@ -189,14 +190,10 @@ hipError_t launch_gemm(int type, const WView & w, const ActBuf & a, int64_t N, i
                        const GemmBatch & bt, float * dst, hipStream_t s, const KTime * kt = nullptr);
 // K slices the GEMM splits this product into; above 1 the slices add their
 // partial sums to dst with atomics, so dst must be zeroed first.
-int gemm_kslices(int type, const WView & w, int64_t N, int64_t nbatch);
-// the 32x32x32 int8 MFMA GEMM (Q4_0, Q8_0, Q4_K), used by launch_gemm
-bool gemm_uses_v2(int type);
-bool gemm2_supported(int type);
-int gemm2_kslices(const WView & w, int64_t N, int64_t nbatch);
-void gemm2_shape(const WView & w, int64_t N, int64_t nbatch, int64_t * workgroups, int * threads, int * lds_bytes);
-hipError_t launch_gemm2(int type, const WView & w, const ActBuf & a, int64_t N, int64_t nbatch, const GemmBatch & bt,
-                        float * dst, hipStream_t s, const KTime * kt);
+int gemm_kslices(const WView & w, int64_t N, int64_t nbatch);
+// launch shape of that GEMM (qmm_describe_mul_mat)
+void gemm_shape(int type, const WView & w, int64_t N, int64_t nbatch, int64_t * workgroups, int * threads,
+                int * lds_bytes);
 
 // MoE routing: builds GEMV tasks (one per expert and up to 8 pairs) from ids.
 struct RouteArgs {
