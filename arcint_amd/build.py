@@ -30,6 +30,10 @@ HIP_FLAGS = [
     f"-I{os.path.join(ROOT, 'include')}",
 ]
 
+# per-source extras: the few-column GEMV consumes its MFMA results on the VALU, so they are
+# written to VGPRs directly (no accumulation-register reads)
+FILE_FLAGS = {"k_gemv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
 
 def _run(cmd: list[str]) -> None:
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -50,7 +54,7 @@ def build_lib() -> str:
         o = os.path.join(BUILD, s + ".o")
         objs.append(o)
         lang = ["-x", "hip"]
-        jobs.append([HIPCC, *HIP_FLAGS, *lang, "-c", os.path.join(CSRC, s), "-o", o])
+        jobs.append([HIPCC, *HIP_FLAGS, *FILE_FLAGS.get(s, []), *lang, "-c", os.path.join(CSRC, s), "-o", o])
     with cf.ThreadPoolExecutor(max_workers=min(8, len(jobs))) as ex:
         list(ex.map(_run, jobs))
     tmp = LIB + ".tmp"

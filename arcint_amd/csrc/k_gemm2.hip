@@ -51,7 +51,6 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
-typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
 
 constexpr int kT = 512;                  // threads per work-group (8 waves)
 constexpr int kSK = 128;                 // k per stage
@@ -109,16 +108,6 @@ struct StageRegs {
     uint4 s;                             // Q4_K: the column's split sub-block sums
     float x;                             // one activation scale
 };
-
-__device__ __forceinline__ uint32_t v2_mul(uint32_t v, uint32_t s) {   // 4 bytes x s, no carries (products < 256)
-    const v2u16 a = __builtin_bit_cast(v2u16, v);
-    const v2u16 b = { (unsigned short)s, (unsigned short)s };
-    return __builtin_bit_cast(uint32_t, a * b);
-}
-
-__device__ __forceinline__ uint32_t q4_minus8(uint32_t nib) {   // 4 codes 0..15 (one per byte) -> q - 8 as int8
-    return (((nib | 0x80808080u) - 0x08080808u) ^ 0x80808080u);
-}
 
 // Q4_K sub-block j's 6-bit scale and min from the 12 scale bytes y|z|w
 // (get_scale_min_k4, P01:2164-2176)

@@ -43,6 +43,8 @@ struct GemvParams {
     const int8_t * xc;           // activation codes [col][ldk]
     const float * xd;            // scales [col][ldk / BS]
     const int16_t * xs;          // code sums [col][ldk / SS]
+    const int8_t * bsp;          // q8_K: split sub-block sums, 16 bytes at (super-block * ldT + col) * 16
+    int64_t ldT;
     int64_t ldk;
     const GemvTask * tasks;      // list mode when non-null
     const int32_t * ntasks_dev;
@@ -54,6 +56,8 @@ struct GemvParams {
     int W;                       // waves per work-group
     int KS;                      // work-groups per tile (K slices); > 1: atomics into zeroed dst
     int spw;                     // groups per wave
+    int nct;                     // dense mode: columns per task
+    int tw;                      // MFMA kernel: tiles per work-group (W / tw waves split K)
 };
 
 // wave-uniform (scalar) loads of the pre-quantized activations
@@ -433,6 +437,368 @@ __global__ __launch_bounds__(512) void k_gemv(GemvParams p) {
     }
 }
 
+// ---- few columns (3..8) on v_mfma_i32_32x32x32_i8 ---------------------------
+// A work-group is W waves on W consecutive 64-row tiles of one task's matrix
+// over one of KS K slices (KS > 1: atomics into zeroed dst).  The slice's
+// activation codes of the task's columns are staged once in LDS and shared by
+// the W waves; the weight stream is the same tiled image as k_gemv's (lane =
+// row), one stage ahead of the compute.  The dots run on the MFMA:
+// A = the task's activation columns (lane l: column l % 32, zeros past nc; k
+// half l / 32), B = two MFMAs per 32 weights, rows 0-31 and 32-63 of the tile.
+// A lane loads its own row's weights; v_permlane32_swap trades lanes 32-63 of
+// the lanes' k 0-15 for lanes 0-31 of their k 16-31, which is exactly the B
+// layout of rows 0-31 (first result) and of rows 32-63 (second).  Per-row
+// scales are applied after the MFMA on the integer results (Q4_K, IQ4_XS) or
+// in the float epilogue (Q4_0, Q8_0), swapped to the output lanes the same
+// way.  The output lane holds row l % 32 for columns 4 (l / 32) + r in
+// registers r < 4.  At N = 8 this is about a third of the VALU work of eight
+// v_dot4 per 32 weights and column.
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ void swap_halves(const uint4 & x, const uint4 & y, v4i & op0, v4i & op1) {
+    const auto a = __builtin_amdgcn_permlane32_swap(x.x, y.x, false, false);
+    const auto b = __builtin_amdgcn_permlane32_swap(x.y, y.y, false, false);
+    const auto c = __builtin_amdgcn_permlane32_swap(x.z, y.z, false, false);
+    const auto d = __builtin_amdgcn_permlane32_swap(x.w, y.w, false, false);
+    op0 = v4i{ (int)a[0], (int)b[0], (int)c[0], (int)d[0] };
+    op1 = v4i{ (int)a[1], (int)b[1], (int)c[1], (int)d[1] };
+}
+// a per-row value: rows 0-31 (r0) and rows 32-63 (r1) in the output lanes (row = lane % 32)
+__device__ __forceinline__ void swap_rows(uint32_t v, uint32_t & r0, uint32_t & r1) {
+    const auto a = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    r0 = a[0];
+    r1 = a[1];
+}
+__device__ __forceinline__ uint4 map4(const uint4 & q, uint32_t (*f)(uint32_t)) { return make_uint4(f(q.x), f(q.y), f(q.z), f(q.w)); }
+__device__ __forceinline__ uint4 nib(const uint4 & q, int sh) {
+    const uint32_t m = 0x0F0F0F0Fu;
+    return make_uint4((q.x >> sh) & m, (q.y >> sh) & m, (q.z >> sh) & m, (q.w >> sh) & m);
+}
+
+// Accumulators of the output lane: element 4 t + r = rows 32 t + l % 32, column 4 (l / 32) + r.
+// Each consume step ends with an empty asm on the whole vector: otherwise the compiler sinks
+// every block's consumption below all the MFMAs and keeps their 16-register results live.
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v8f __attribute__((ext_vector_type(8)));
+
+// acc[4 t + r] += s_t * e_t[r] for the output registers r < 4 of rows 0-31 (t = 0) and 32-63;
+// the products fit 24 bits (full-rate multiplies)
+__device__ __forceinline__ void scale_add(const v16i & e0, const v16i & e1, int s0, int s1, v8i & acc) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        acc[r] += __mul24(s0, e0[r]);
+        acc[4 + r] += __mul24(s1, e1[r]);
+    }
+    asm volatile("" : "+v"(acc));
+}
+// out[4 t + r] += (i * dw_t) * dx[r] with i read from the magic-biased result e_t[r]: the bits
+// of 12582912 + i, so fma(bits as float, dw, -12582912 dw) is i dw rounded once
+__device__ __forceinline__ void bf_epilogue(const v16i & e0, const v16i & e1, float dw0, float dw1, const float4 & dx4,
+                                            v8f & out) {
+    const float nm0 = -12582912.0f * dw0, nm1 = -12582912.0f * dw1;
+    const float dx[4] = { dx4.x, dx4.y, dx4.z, dx4.w };
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int i0 = e0[r], i1 = e1[r];
+        out[r] = __builtin_fmaf(__builtin_fmaf(__builtin_bit_cast(float, i0), dw0, nm0), dx[r], out[r]);
+        out[4 + r] = __builtin_fmaf(__builtin_fmaf(__builtin_bit_cast(float, i1), dw1, nm1), dx[r], out[4 + r]);
+    }
+    asm volatile("" : "+v"(out));
+}
+
+// One stage of the MFMA GEMV on the weights rw of the lane's row: A operands from the LDS
+// codes at xag (block b at 32 b), the output columns' scales at xdg (4 floats per block),
+// Q4_K split sums at xsg.  A scheduling barrier per block bounds the live MFMA results: the
+// K-quants issue block j's MFMAs before they consume block j - 1's, Q4_0 / Q8_0 (whose magic
+// accumulator input takes 16 more registers) consume each block's in its own group.
+template <int TYPE>
+__device__ __forceinline__ void mma_stage(const uint4 (&rw)[9], int st, const uint8_t * xag, const float * xdg,
+                                          const uint8_t * xsg, int h, const v16i & magic, v8f & out) {
+    constexpr bool KQ = TYPE == QMM_TYPE_Q4_K, IQ = TYPE == QMM_TYPE_IQ4_XS, Q8 = TYPE == QMM_TYPE_Q8_0;
+    constexpr bool BF = TYPE == QMM_TYPE_Q4_0 || Q8;
+    constexpr int NB = Q8 ? 4 : 8;                                // 32-weight blocks per stage
+    auto a_op = [&](int b) -> v4i { return *reinterpret_cast<const v4i *>(xag + 32 * (Q8 ? 4 * st + b : b)); };
+    auto dx_op = [&](int b) -> float4 { return *reinterpret_cast<const float4 *>(xdg + (Q8 ? 4 * st + b : b) * 8); };
+    uint4 as = make_uint4(0, 0, 0, 0);                            // Q4_K: split sums, lanes 0-15
+    if constexpr (KQ) {
+        const uint2 v = *reinterpret_cast<const uint2 *>(xsg);
+        as.x = v.x;
+        as.y = v.y;
+    }
+    if constexpr (BF) {
+        const uint32_t dw2[4] = { rw[8].x, rw[8].y, rw[8].z, rw[8].w };
+        v4i an = a_op(0);                                     // LDS reads one block ahead
+        float4 dn = dx_op(0);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int blk = Q8 ? 4 * st + b : b;                  // block of the group
+            uint32_t d0b, d1b;
+            swap_rows((dw2[blk >> 1] >> (16 * (blk & 1))) & 0xffffu, d0b, d1b);
+            const float dw0 = h2f(d0b), dw1 = h2f(d1b);
+            uint4 lo, hi;
+            if constexpr (Q8) {
+                lo = rw[2 * b];
+                hi = rw[2 * b + 1];
+            } else {
+                lo = map4(nib(rw[b], 0), q4_minus8);
+                hi = map4(nib(rw[b], 4), q4_minus8);
+            }
+            v4i op0, op1;
+            swap_halves(lo, hi, op0, op1);
+            const v4i av = an;
+            const float4 dxb = dn;
+            if (b + 1 < NB) {
+                an = a_op(b + 1);
+                dn = dx_op(b + 1);
+            }
+            const v16i e0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, op0, magic, 0, 0, 0);
+            const v16i e1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, op1, magic, 0, 0, 0);
+            bf_epilogue(e0, e1, dw0, dw1, dxb, out);          // consumed in its own block: the
+            __builtin_amdgcn_sched_barrier(0);                // SIMD's other waves cover the latency
+        }
+    } else if constexpr (KQ) {
+        // sub-block j: one MFMA per 32 rows on the raw nibbles, its 6-bit scale applied per
+        // row on the integer result; the min term sum_j m_j (64 bh_j + bl_j) is one MFMA
+        // with A rows 0-7 = bh of columns 0-7 and rows 8-15 = bl (k = j), B = the row's mins
+        const uint4 hd = rw[8];                               // d, dmin | scales[12]
+        const uint32_t sc03 = hd.y & 0x3f3f3f3fu, mn03 = hd.z & 0x3f3f3f3fu;
+        const uint32_t sc47 = (hd.w & 0x0f0f0f0fu) | ((hd.y >> 2) & 0x30303030u);
+        const uint32_t mn47 = ((hd.w >> 4) & 0x0f0f0f0fu) | ((hd.z >> 2) & 0x30303030u);
+        uint32_t scw[2][2], mnw[2][2];                        // [word][tile]
+        swap_rows(sc03, scw[0][0], scw[0][1]);
+        swap_rows(sc47, scw[1][0], scw[1][1]);
+        swap_rows(mn03, mnw[0][0], mnw[0][1]);
+        swap_rows(mn47, mnw[1][0], mnw[1][1]);
+        v8i isc = {};
+        v16i pe0, pe1;
+        int ps0 = 0, ps1 = 0;
+        v4i an = a_op(0);                                     // LDS reads one block ahead
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint4 lq = nib(rw[2 * (j >> 1)], 4 * (j & 1)), hq = nib(rw[2 * (j >> 1) + 1], 4 * (j & 1));
+            v4i op0, op1;
+            swap_halves(lq, hq, op0, op1);
+            const v4i av = an;
+            if (j + 1 < 8) an = a_op(j + 1);
+            const v16i e0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, op0, v16i{}, 0, 0, 0);
+            const v16i e1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, op1, v16i{}, 0, 0, 0);
+            if (j > 0) scale_add(pe0, pe1, ps0, ps1, isc);
+            __builtin_amdgcn_sched_barrier(0);
+            pe0 = e0;
+            pe1 = e1;
+            ps0 = (int)((scw[j >> 2][0] >> (8 * (j & 3))) & 0xffu);
+            ps1 = (int)((scw[j >> 2][1] >> (8 * (j & 3))) & 0xffu);
+        }
+        scale_add(pe0, pe1, ps0, ps1, isc);
+        const v4i bm0 = h ? v4i{} : v4i{ (int)mnw[0][0], (int)mnw[1][0], 0, 0 };
+        const v4i bm1 = h ? v4i{} : v4i{ (int)mnw[0][1], (int)mnw[1][1], 0, 0 };
+        const v4i asp = __builtin_bit_cast(v4i, as);
+        const v16i m0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(asp, bm0, v16i{}, 0, 0, 0);
+        const v16i m1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(asp, bm1, v16i{}, 0, 0, 0);
+        const float4 dx4 = dx_op(0);
+        const float dx0[4] = { dx4.x, dx4.y, dx4.z, dx4.w };
+        uint32_t dd0, dd1, dm0, dm1;
+        swap_rows(hd.x & 0xffffu, dd0, dd1);
+        swap_rows(hd.x >> 16, dm0, dm1);
+        const float d[2] = { h2f(dd0), h2f(dd1) }, dmin[2] = { h2f(dm0), h2f(dm1) };
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int imn0 = 64 * m0[r] + m0[4 + r], imn1 = 64 * m1[r] + m1[4 + r];
+            out[r] += dx0[r] * (d[0] * (float)isc[r] - dmin[0] * (float)imn0);
+            out[4 + r] += dx0[r] * (d[1] * (float)isc[4 + r] - dmin[1] * (float)imn1);
+        }
+    } else if constexpr (IQ) {
+        const uint32_t shi = rw[8].x >> 16, slo = rw[8].y;
+        v8i isum = {};
+        v16i pe0, pe1;
+        int ps0 = 0, ps1 = 0;
+        v4i an = a_op(0);                                     // LDS reads one block ahead
+#pragma unroll
+        for (int ib = 0; ib < 8; ++ib) {
+            v4i op0, op1;
+            swap_halves(map4(nib(rw[ib], 0), iq4_lookup), map4(nib(rw[ib], 4), iq4_lookup), op0, op1);
+            uint32_t s0, s1;
+            swap_rows(((slo >> (4 * ib)) & 0xFu) | (((shi >> (2 * ib)) & 3u) << 4), s0, s1);
+            const v4i av = an;
+            if (ib + 1 < 8) an = a_op(ib + 1);
+            const v16i e0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, op0, v16i{}, 0, 0, 0);
+            const v16i e1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, op1, v16i{}, 0, 0, 0);
+            if (ib > 0) scale_add(pe0, pe1, ps0, ps1, isum);
+            __builtin_amdgcn_sched_barrier(0);
+            pe0 = e0;
+            pe1 = e1;
+            ps0 = (int)s0 - 32;
+            ps1 = (int)s1 - 32;
+        }
+        scale_add(pe0, pe1, ps0, ps1, isum);
+        const float4 dx4 = dx_op(0);
+        const float dx0[4] = { dx4.x, dx4.y, dx4.z, dx4.w };
+        uint32_t dd0, dd1;
+        swap_rows(rw[8].x & 0xffffu, dd0, dd1);
+        const float d[2] = { h2f(dd0), h2f(dd1) };
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) out[4 * t + r] += dx0[r] * (d[t] * (float)isum[4 * t + r]);
+    }
+}
+
+// A work-group is TW tiles x WK waves: wave (tw, kw) = wave % TW, wave / TW streams tile
+// tb TW + tw over the groups [gw + kw spw, + spw) of the work-group's K range [gw, gw + WK spw)
+// (K slice ks of KS).  The K range's activations are staged once in LDS for all TW tiles, the
+// WK waves of a tile are added in LDS in a fixed order, and KS > 1 adds into zeroed dst with
+// atomics.  Weights stream through two register sets: stage s + 1 loads while s computes.
+template <int TYPE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_gemv_mma(GemvParams p) {
+    using T = GV<TYPE>;
+    constexpr int NL = T::NL, NST = T::NST;
+    static_assert(NL == 9, "mma_stage takes 9 weight registers");
+    constexpr bool KQ = TYPE == QMM_TYPE_Q4_K, Q8 = TYPE == QMM_TYPE_Q8_0;
+    constexpr bool BF = TYPE == QMM_TYPE_Q4_0 || Q8;             // a float scale per 32 weights
+    constexpr int BS = BF ? 32 : 256;                             // activation scale block
+    constexpr int NSB = BF ? 8 : 1;                               // activation scales per group
+    constexpr int kMagic = 0x4B400000;                            // float 12582912: its bits + i = 12582912 + i
+    // LDS: 256 zero bytes (the A operand of lanes without a column), [WK spw][8][kMmaColBytes]
+    // codes, for Q4_K [WK spw][8][16] split sums, then the activation scales [WK spw][NSB][8];
+    // after the stream, the waves' sums
+    extern __shared__ __align__(16) uint8_t xl[];
+    __shared__ int64_t s_col[kMaxTaskCols], s_doff[kMaxTaskCols];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int TW = p.tw, WK = p.W / p.tw;
+    const int tw = wave % TW, kw = wave / TW;
+    // work-group -> (task, tile block, K slice); these counts fit 32 bits
+    const uint32_t ntl = (uint32_t)p.w.ntiles, ntb = (ntl + (uint32_t)TW - 1) / (uint32_t)TW;
+    const uint32_t ks = blockIdx.x % (uint32_t)p.KS, rest = blockIdx.x / (uint32_t)p.KS;
+    const uint32_t tb = rest % ntb, task = rest / ntb;
+    int mat, nc;
+    if (p.tasks) {
+        if (p.ntasks_dev && (int)task >= *p.ntasks_dev) return;     // uniform
+        const GemvTask & t = p.tasks[task];
+        mat = t.mat;
+        nc = t.ncols < kMaxTaskCols ? t.ncols : kMaxTaskCols;
+        if (tid < nc) {
+            s_col[tid] = t.col[tid];
+            s_doff[tid] = t.dst_off[tid];
+        }
+    } else {
+        const uint32_t tpb = (uint32_t)p.tpb, ne12 = (uint32_t)p.ne12;
+        const uint32_t b = task / tpb, tt = task - b * tpb;
+        const uint32_t i3 = b / ne12, i2 = b - i3 * ne12;
+        mat = (int)(i2 / (uint32_t)p.r2 + (i3 / (uint32_t)p.r3) * (uint32_t)p.ne02);
+        const int64_t first = (int64_t)tt * p.nct;
+        nc = (int)((p.ne11 - first) < p.nct ? (p.ne11 - first) : p.nct);
+        if (tid < nc) {
+            const int64_t i1 = first + tid;
+            s_col[tid] = (int64_t)b * p.ne11 + i1;
+            s_doff[tid] = i1 * p.d_nb1 + (int64_t)i2 * p.d_nb2 + (int64_t)i3 * p.d_nb3;
+        }
+    }
+    if (mat < 0 || nc <= 0) return;                               // uniform
+    const int G = (int)p.w.G;
+    const int gw = (int)ks * WK * p.spw;                          // the work-group's groups [gw, gw + ngw)
+    const int ngw = gw + WK * p.spw < G ? WK * p.spw : G - gw;    // >= 1 (the plan leaves no empty slice)
+    const int ga = gw + kw * p.spw;                               // this wave's groups [ga, ga + nsw)
+    const int nsw = ga >= G ? 0 : (ga + p.spw < G ? p.spw : G - ga);
+    const uint32_t tile = tb * (uint32_t)TW + (uint32_t)tw;
+    const int S = tile < ntl ? nsw * NST : 0;                     // stages (uniform per wave)
+    const uint8_t * tbase = tile_group(p.w, mat, tile < ntl ? tile : 0, 0);
+    const size_t tgs = (size_t)p.w.tg;
+    auto load_stage = [&](uint4 (&b)[NL], int s) {                // past the last stage: the sink
+        const bool real = s < S;
+        T::load(b, real ? tbase + (size_t)(ga + s / NST) * tgs : p.sink, real ? s % NST : 0, lane);
+    };
+    // the first stage's weights are requested before the activations are staged
+    uint4 b0[NL], b1[NL];
+    if (S > 0) load_stage(b0, 0);
+    __syncthreads();                                              // s_col, s_doff
+    nc = __builtin_amdgcn_readfirstlane(nc);
+    // the work-group's activation codes, Q4_K split sums and scales into LDS (zeros for columns >= nc)
+    const int nthr = 64 * p.W;
+    uint8_t * const xcl = xl + kMmaZeroBytes;
+    if (tid < kMmaZeroBytes / 16) *reinterpret_cast<uint4 *>(xl + 16 * tid) = make_uint4(0, 0, 0, 0);
+    for (int i = tid; i < ngw * 8 * 16; i += nthr) {
+        const int g = i >> 7, c = (i >> 4) & 7, q = i & 15;
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (c < nc) v = *reinterpret_cast<const uint4 *>(p.xc + s_col[c] * p.ldk + (int64_t)(gw + g) * 256 + 16 * q);
+        *reinterpret_cast<uint4 *>(xcl + (g * 8 + c) * kMmaColBytes + 16 * q) = v;
+    }
+    const int per = WK * p.spw;                                   // groups the LDS holds
+    uint8_t * const xsl = xcl + per * 8 * kMmaColBytes;
+    if constexpr (KQ) {
+        for (int i = tid; i < ngw * 8; i += nthr) {
+            const int g = i >> 3, c = i & 7;
+            uint4 v = make_uint4(0, 0, 0, 0);
+            if (c < nc) v = *reinterpret_cast<const uint4 *>(p.bsp + ((int64_t)(gw + g) * p.ldT + s_col[c]) * 16);
+            *reinterpret_cast<uint4 *>(xsl + 16 * i) = v;
+        }
+    }
+    float * const xdl = reinterpret_cast<float *>(xsl + (KQ ? per * 8 * 16 : 0));
+    for (int i = tid; i < ngw * NSB * 8; i += nthr) {
+        const int c = i & 7, gb = i >> 3;                         // gb = group * NSB + block
+        xdl[i] = c < nc ? p.xd[s_col[c] * (p.ldk / BS) + (int64_t)gw * NSB + gb] : 0.0f;
+    }
+    __syncthreads();
+    const int h = lane >> 5, l32 = lane & 31;
+    // A operand: the lane's column l32 (zeros past nc), k half h.  Output columns 4 h + r, r < 4.
+    // Lanes without a column read the zero block (every offset stays inside its 256 bytes).
+    const bool a_live = l32 < nc;
+    const uint8_t * xar = a_live ? xcl + ((ga - gw) * 8 + l32) * kMmaColBytes + 16 * h : xl;
+    const int xas = a_live ? 8 * kMmaColBytes : 0;                // per group
+    // Q4_K min term: lane l < 16 brings bh (l < 8) or bl (8 <= l < 16) of column l % 8
+    const bool s_live = KQ && lane < 16;
+    const uint8_t * xsr = s_live ? xsl + ((ga - gw) * 8 + (lane & 7)) * 16 + 8 * ((lane >> 3) & 1) : xl;
+    const int xss = s_live ? 128 : 0;
+    // the scales of the lane's output columns 4 h .. 4 h + 3, per (group, block)
+    const float * xdr = xdl + (ga - gw) * NSB * 8 + 4 * h;
+    v8f out = {};
+    v16i magic;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) magic[r] = kMagic;
+    auto compute = [&](const uint4 (&b)[NL], int s) {
+        const int gl = s / NST;
+        mma_stage<TYPE>(b, s % NST, xar + gl * xas, xdr + gl * NSB * 8, xsr + gl * xss, h, magic, out);
+    };
+    for (int s = 0; s < S; s += 2) {                              // uniform
+        load_stage(b1, s + 1);
+        __builtin_amdgcn_sched_barrier(0);                        // the loads go out before the compute
+        compute(b0, s);
+        if (s + 1 >= S) break;
+        load_stage(b0, s + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(b1, s + 1);
+    }
+
+    // tile tw's WK waves are added in a fixed order (wave kw takes the elements e = kw, kw + WK,
+    // ... of the 8), then stored (KS == 1) or added (KS > 1)
+    const int64_t row0 = (int64_t)tile * kTileRows + l32;
+    auto store = [&](int e, float v) {
+        const int c = 4 * h + (e & 3);
+        const int64_t row = row0 + 32 * (e >> 2);
+        if (tile < ntl && c < nc && row < p.w.M) {
+            float * o = p.dst + s_doff[c] + row;
+            if (p.KS == 1) *o = v;
+            else atomicAdd(o, v);
+        }
+    };
+    if (WK == 1) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) store(e, out[e]);
+        return;
+    }
+    float * red = reinterpret_cast<float *>(xl);                  // [WK][TW][8][64], over the staged data
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < 8; ++e) red[((kw * TW + tw) * 8 + e) * 64 + lane] = out[e];
+    __syncthreads();
+    for (int e = kw; e < 8; e += WK) {
+        float v = 0.0f;
+        for (int k = 0; k < WK; ++k) v += red[((k * TW + tw) * 8 + e) * 64 + lane];
+        store(e, v);
+    }
+}
+
 template <int TYPE>
 hipError_t launch_t(const GemvParams & p, int nc, int64_t nwg, hipStream_t s, const KTime * kt) {
     const int threads = 64 * p.W;
@@ -458,14 +824,51 @@ int env_int(const char * name, int dflt) {
 
 }  // namespace
 
-bool gemv_plan(int type, const WView & w, int nc, int64_t ntasks, bool allow_split, GemvPlan * pl) {
+bool gemv_mma_supported(int type) {
+    return type == QMM_TYPE_Q4_0 || type == QMM_TYPE_Q8_0 || type == QMM_TYPE_Q4_K || type == QMM_TYPE_IQ4_XS;
+}
+
+bool gemv_plan(int type, const WView & w, int nc, int64_t ntasks, bool allow_split, bool want_mma, GemvPlan * pl) {
     if (!type_layout(type) || nc < 1 || nc > kMaxTaskCols || ntasks <= 0 || w.G <= 0 || w.ntiles <= 0) return false;
     pl->nc = nc;
     pl->ntasks = ntasks;
+    const int64_t tiles = ntasks * w.ntiles;
+    // MFMA kernel: about `target` waves, one per tile and K slice, W tiles per work-group; a
+    // slice stages at most kMmaMaxGroups groups of activations in LDS (task lists, which
+    // cannot split K, fall back to the v_dot4 kernel past that)
+    pl->mma = want_mma && gemv_mma_supported(type);
+    pl->tw = 1;
+    if (pl->mma) {
+        // MFMA kernel: about `target` waves in work-groups of TW tiles x WK waves; the WK waves
+        // of a tile split K and are added in LDS, which stages the work-group's activations
+        // (WK spw <= kMmaMaxGroups groups); the rest of the split is KS work-groups per tile
+        // (atomics).  Task lists cannot split K over work-groups and fall back to the v_dot4
+        // kernel past WK spw = G.
+        const int64_t target = std::max(1, env_int("QMM_GEMV_MMA_WAVES", 2048));
+        // (at most 4 waves per work-group: three 4-wave work-groups fill a CU at the kernel's
+        // occupancy of 3 waves per SIMD, 8-wave ones leave a third of it idle)
+        const int64_t TW = std::min<int64_t>(std::max(1, std::min(4, env_int("QMM_GEMV_MMA_TILES", 4))), w.ntiles);
+        const int64_t wkmax = std::max<int64_t>(1, std::min<int64_t>(env_int("QMM_GEMV_MMA_WK", 1), 4 / TW));
+        const int64_t kw = std::min<int64_t>(w.G, std::max<int64_t>(1, (target + tiles - 1) / tiles));
+        int64_t spw = (w.G + kw - 1) / kw;
+        int64_t WK = std::min<int64_t>((w.G + spw - 1) / spw, allow_split ? wkmax : 4 / TW);
+        spw = std::min<int64_t>(allow_split ? spw : (w.G + WK - 1) / WK, kMmaMaxGroups / WK);
+        int64_t KS = (w.G + spw * WK - 1) / (spw * WK);
+        WK = std::min<int64_t>(WK, ((w.G + KS - 1) / KS + spw - 1) / spw);   // balance the slices
+        KS = (w.G + spw * WK - 1) / (spw * WK);
+        if (KS == 1 || allow_split) {
+            pl->tw = (int)TW;
+            pl->W = (int)(TW * WK);
+            pl->KS = (int)KS;
+            pl->spw = (int)spw;
+            const int64_t nwg = gemv_workgroups(w, *pl);
+            return nwg > 0 && nwg < 0x7fffffff;
+        }
+        pl->mma = false;
+    }
     // waves: about `target` in all (each with at least one group), at most
     // wmax per work-group; the rest of the split goes to work-groups per tile
     // (KS), which need dst zeroed before the launch
-    const int64_t tiles = ntasks * w.ntiles;
     const int64_t target = std::max(1, env_int("QMM_GEMV_WAVES", 4096));
     // without split K (task lists: dst rows are not zeroed first) the K split
     // is all within the work-group, up to 8 waves
@@ -481,8 +884,24 @@ bool gemv_plan(int type, const WView & w, int nc, int64_t ntasks, bool allow_spl
     pl->W = (int)W;
     pl->KS = (int)KS;
     pl->spw = (int)spw;
-    const int64_t nwg = tiles * KS;
+    const int64_t nwg = gemv_workgroups(w, *pl);
     return nwg > 0 && nwg < 0x7fffffff;
+}
+
+int64_t gemv_workgroups(const WView & w, const GemvPlan & pl) {
+    const int64_t tw = pl.mma ? pl.tw : 1;
+    return pl.ntasks * ((w.ntiles + tw - 1) / tw) * pl.KS;
+}
+
+size_t gemv_lds_bytes(int type, const GemvPlan & pl) {
+    if (pl.mma) {
+        const size_t per_group = 8 * (kMmaColBytes + (type == QMM_TYPE_Q4_K ? 16 : 0)) +
+                                 8 * sizeof(float) * (type == QMM_TYPE_Q4_0 || type == QMM_TYPE_Q8_0 ? 8 : 1);
+        const size_t stage = kMmaZeroBytes + (size_t)(pl.W / pl.tw) * pl.spw * per_group;
+        const size_t red = pl.W > pl.tw ? (size_t)pl.W * 8 * 64 * sizeof(float) : 0;   // the K waves' sums
+        return std::max(stage, red);
+    }
+    return pl.W > 1 ? (size_t)pl.W * pl.nc * 64 * sizeof(float) : 0;
 }
 
 hipError_t launch_gemv(int type, const WView & w, const GemvPlan & pl, const ActBuf & a, const GemvTask * tasks,
@@ -496,6 +915,8 @@ hipError_t launch_gemv(int type, const WView & w, const GemvPlan & pl, const Act
     p.xc = a.codes;
     p.xd = a.d;
     p.xs = a.sums;
+    p.bsp = a.bsp;
+    p.ldT = a.ldT;
     p.ldk = a.ldk;
     p.tasks = tasks;
     p.ntasks_dev = ntasks_dev;
@@ -504,6 +925,8 @@ hipError_t launch_gemv(int type, const WView & w, const GemvPlan & pl, const Act
     p.W = pl.W;
     p.KS = pl.KS;
     p.spw = pl.spw;
+    p.nct = pl.nc;
+    p.tw = pl.tw;
     if (!tasks) {
         p.ne11 = dense->ne11;
         p.ne12 = dense->ne12;
@@ -516,7 +939,28 @@ hipError_t launch_gemv(int type, const WView & w, const GemvPlan & pl, const Act
         p.d_nb3 = dense->d_nb3;
         if (p.tpb * dense->ne12 * dense->ne13 != pl.ntasks) return hipErrorInvalidValue;
     }
-    const int64_t nwg = pl.ntasks * w.ntiles * pl.KS;
+    const int64_t nwg = gemv_workgroups(w, pl);
+    if (pl.mma) {
+        const int64_t per_wg = (int64_t)(pl.W / pl.tw) * pl.spw;
+        if (!gemv_mma_supported(type) || nwg >= 0x7fffffff || pl.W > 4 || pl.tw < 1 || pl.W % pl.tw ||
+            per_wg > kMmaMaxGroups ||
+            per_wg * pl.KS < w.G || per_wg * (pl.KS - 1) >= w.G || (type == QMM_TYPE_Q4_K && !a.bsp))
+            return hipErrorInvalidValue;
+        const uint32_t lds = (uint32_t)gemv_lds_bytes(type, pl);
+        const dim3 g((unsigned)nwg), b(64 * pl.W);
+#define QMM_MMA(T)                                                                                  \
+    if (kt) hipExtLaunchKernelGGL(k_gemv_mma<T>, g, b, lds, s, kt->start, kt->stop, 0, p);          \
+    else k_gemv_mma<T><<<g, b, lds, s>>>(p);                                                        \
+    return hipGetLastError();
+        switch (type) {
+            case QMM_TYPE_Q4_0: { QMM_MMA(QMM_TYPE_Q4_0) }
+            case QMM_TYPE_Q8_0: { QMM_MMA(QMM_TYPE_Q8_0) }
+            case QMM_TYPE_Q4_K: { QMM_MMA(QMM_TYPE_Q4_K) }
+            case QMM_TYPE_IQ4_XS: { QMM_MMA(QMM_TYPE_IQ4_XS) }
+            default: return hipErrorInvalidValue;
+        }
+#undef QMM_MMA
+    }
     switch (type) {
         case QMM_TYPE_Q4_0:   return launch_t<QMM_TYPE_Q4_0>(p, pl.nc, nwg, s, kt);
         case QMM_TYPE_Q8_0:   return launch_t<QMM_TYPE_Q8_0>(p, pl.nc, nwg, s, kt);

@@ -10,8 +10,9 @@
 // multiply is contracted, so every code and scale equals the CPU's.
 // Columns are written with a stride of ldk (K rounded up to 256); the padding
 // past K quantizes zeros.  For a GEMM consumer the scales are written again
-// block-major (dT), and for q8_K the sub-block sums split into int8 halves
-// (bsp), the GEMM's operand for the Q4_K min term.  The same launch can zero dst columns for a GEMV
+// block-major (dT); for q8_K the sub-block sums are also written split into
+// int8 halves (bsp), the int8 MFMA operand of the Q4_K min term in the GEMM
+// and the few-column GEMV.  The same launch can zero dst columns for a GEMV
 // that adds its K slices with atomics (work-groups past the quantization
 // ones do that).
 #include "qmm_device.h"

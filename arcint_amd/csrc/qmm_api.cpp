@@ -130,7 +130,7 @@ size_t act_bytes(int vdt, int64_t ldk, int64_t ncols, bool dT, int64_t ldT, size
     *o_t = off;
     if (dT) off = align_up(off + (size_t)((ldk / act_block(vdt)) * ldT) * 4, kPlaneAlign);
     *o_b = off;
-    if (dT && vdt == QMM_TYPE_Q8_K) off = align_up(off + (size_t)((ldk / 256) * ldT) * 16, kPlaneAlign);
+    if (vdt == QMM_TYPE_Q8_K) off = align_up(off + (size_t)((ldk / 256) * ldT) * 16, kPlaneAlign);
     return off;
 }
 
@@ -189,7 +189,7 @@ int quantize_src1(qmm_ctx * ctx, int type, const qmm_tensor * src1, bool dT, Act
     a.d = (float *)(b + od);
     a.sums = (int16_t *)(b + os);
     a.dT = dT ? (float *)(b + ot) : nullptr;
-    a.bsp = dT && vdt == QMM_TYPE_Q8_K ? (int8_t *)(b + ob) : nullptr;
+    a.bsp = vdt == QMM_TYPE_Q8_K ? (int8_t *)(b + ob) : nullptr;
     a.ldT = ldT;
     a.K = K;
     a.ldk = ldk;
@@ -508,6 +508,12 @@ static int64_t gemm_min_cols() {
     return v;
 }
 
+// few columns (this many and up to 8) on the MFMA GEMV; QMM_GEMV_MMA_MIN overrides
+static int gemv_mma_min_cols() {
+    const char * e = getenv("QMM_GEMV_MMA_MIN");
+    return e ? std::max(2, atoi(e)) : 3;
+}
+
 int qmm_describe_mul_mat(const qmm_tensor * src0, const qmm_tensor * src1, const qmm_tensor * dst, qmm_launch_info * out) {
     if (!out) return QMM_ERR_INVALID;
     memset(out, 0, sizeof(*out));
@@ -518,7 +524,6 @@ int qmm_describe_mul_mat(const qmm_tensor * src0, const qmm_tensor * src1, const
     char reason[160];
     if (!mul_mat_ok(&a, &b, &c, reason, sizeof(reason))) return QMM_ERR_UNSUPPORTED;
     const int64_t N = src1->ne[1];
-    const ImageShape sh = [&] { ImageShape t; image_shape(*type_layout(src0->type), src0->ne, &t); return t; }();
     if (N >= gemm_min_cols()) {
         snprintf(out->path, sizeof(out->path), "gemm-mfma");
         out->tasks = src1->ne[2] * src1->ne[3];
@@ -539,16 +544,17 @@ int qmm_describe_mul_mat(const qmm_tensor * src0, const qmm_tensor * src1, const
     const int nc = (int)std::min<int64_t>(N, kMaxTaskCols);
     const int64_t ntasks = (N + nc - 1) / nc * src1->ne[2] * src1->ne[3];
     GemvPlan plan;
-    if (!gemv_plan(src0->type, w, nc, ntasks, true, &plan)) return QMM_ERR_UNSUPPORTED;
-    snprintf(out->path, sizeof(out->path), "gemv");
+    if (!gemv_plan(src0->type, w, nc, ntasks, true, nc >= gemv_mma_min_cols(), &plan)) return QMM_ERR_UNSUPPORTED;
+    snprintf(out->path, sizeof(out->path), plan.mma ? "gemv-mfma" : "gemv");
     out->threads = 64 * plan.W;
     out->cols_per_task = nc;
     out->tasks = ntasks;
-    out->k_waves = plan.W;
+    out->k_waves = plan.mma ? plan.W / plan.tw : plan.W;
+    out->tiles_per_wg = plan.mma ? plan.tw : 1;
     out->k_slices = plan.KS;
     out->groups_per_wave = plan.spw;
-    out->workgroups = ntasks * w.ntiles * plan.KS;
-    out->lds_bytes = plan.W > 1 ? (int64_t)plan.W * nc * 64 * 4 : 0;
+    out->workgroups = gemv_workgroups(w, plan);
+    out->lds_bytes = (int64_t)gemv_lds_bytes(src0->type, plan);
     return QMM_OK;
 }
 
@@ -597,7 +603,8 @@ int qmm_mul_mat(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1,
     const int nc = (int)std::min<int64_t>(N, kMaxTaskCols);
     const int64_t ntasks = (N + nc - 1) / nc * dn.ne12 * dn.ne13;
     GemvPlan plan;
-    if (!gemv_plan(src0->type, w, nc, ntasks, true, &plan)) return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat: GEMV shape out of range");
+    if (!gemv_plan(src0->type, w, nc, ntasks, true, nc >= gemv_mma_min_cols(), &plan))
+        return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat: GEMV shape out of range");
     ZeroJob z{ d, w.M, N * dn.ne12 * dn.ne13, N, dn.ne12, dn.d_nb1, dn.d_nb2, dn.d_nb3 };
     if ((rc = quantize_src1(ctx, src0->type, src1, false, &a, plan.KS > 1 ? &z : nullptr))) return rc;
     ctx->path = "gemv";
@@ -626,7 +633,8 @@ int qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * sr
     const WView w = weight_view(src0);
     const int nc = (int)std::min<int64_t>(kMaxTaskCols, npairs);
     GemvPlan plan;
-    if (!gemv_plan(src0->type, w, nc, max_tasks, false, &plan))
+    // tasks carry 1..8 pairs each: the MFMA kernel pays off when experts average two or more
+    if (!gemv_plan(src0->type, w, nc, max_tasks, false, npairs >= 2 * n_as, &plan))
         return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat_id: GEMV shape out of range");
     const size_t o_tasks = align_up((size_t)npairs * 4, 256);
     const size_t o_cnt = align_up(o_tasks + (size_t)max_tasks * sizeof(GemvTask), 256);

@@ -37,6 +37,19 @@ __device__ __forceinline__ uint32_t iq4_lookup(uint32_t nib) {
     return perm(hi, lo, sel);
 }
 
+// four 4-bit codes 0..15 (one per byte) -> q - 8 as int8 (no borrow between bytes)
+__device__ __forceinline__ uint32_t q4_minus8(uint32_t nib) {
+    return (((nib | 0x80808080u) - 0x08080808u) ^ 0x80808080u);
+}
+
+// four bytes times s with a packed 16-bit multiply; every product must be < 256 (no carries)
+__device__ __forceinline__ uint32_t v2_mul(uint32_t v, uint32_t s) {
+    typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
+    const v2u16 a = __builtin_bit_cast(v2u16, v);
+    const v2u16 b = { (unsigned short)s, (unsigned short)s };
+    return __builtin_bit_cast(uint32_t, a * b);
+}
+
 template <typename T>
 __device__ __forceinline__ T ldg_nt(const T * p) {
     return __builtin_nontemporal_load(p);

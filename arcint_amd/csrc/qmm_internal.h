@@ -79,9 +79,9 @@ struct ActBuf {
     float *    d;
     int16_t *  sums;
     float *    dT;         // non-null: the scales again, block-major: dT[b * ldT + c]
-    int8_t *   bsp;        // q8_K with dT: per super-block sb and column c, 16 bytes at (sb * ldT + c) * 16:
+    int8_t *   bsp;        // q8_K: per super-block sb and column c, 16 bytes at (sb * ldT + c) * 16:
                            // the 8 sub-block sums (32 codes each) split as 64 bh + bl, bh[8] then bl[8]
-    int64_t    ldT;        // >= ncols + 64 (the GEMM reads whole 64-column tiles)
+    int64_t    ldT;        // >= ncols + 64 (the GEMM reads whole 64-column tiles); set also without dT
     int64_t    K;
     int64_t    ldk;        // K rounded up to 256
     int64_t    ncols;
@@ -160,12 +160,26 @@ struct GemvDense {
 // Launch shape of a GEMV (host): W waves per work-group and KS work-groups
 // per 64-row tile split K, spw groups of 256 weights per wave.  KS > 1 adds
 // partial sums to dst with atomics, so dst must be zeroed first.
+// v_dot4 kernel: a work-group is W waves splitting K on one tile (spw groups each), KS
+// work-groups per tile.  MFMA kernel (mma): a work-group is tw tiles x W / tw waves splitting
+// K; it stages its K range's activations in LDS (kMmaColBytes per column and group, at most
+// kMmaMaxGroups groups).
 struct GemvPlan {
     int nc;                        // columns per task (1..8)
     int64_t ntasks;                // grid tasks (list mode: upper bound)
     int W, KS, spw;
+    bool mma;                      // dots on the MFMA (few columns; Q4_0, Q8_0, Q4_K, IQ4_XS)
+    int tw;                        // mma: tiles per work-group, W / tw waves of each split K
 };
-bool gemv_plan(int type, const WView & w, int nc, int64_t ntasks, bool allow_split, GemvPlan * plan);
+constexpr int kMmaColBytes = 272;  // 256 codes + 16 bytes of padding (LDS banks)
+constexpr int kMmaZeroBytes = 256; // zeros ahead of the codes
+constexpr int kMmaMaxGroups = 24;
+// want_mma: use the MFMA kernel where the type allows it
+bool gemv_plan(int type, const WView & w, int nc, int64_t ntasks, bool allow_split, bool want_mma, GemvPlan * plan);
+int64_t gemv_workgroups(const WView & w, const GemvPlan & plan);
+size_t gemv_lds_bytes(int type, const GemvPlan & plan);
+// whether the few-column MFMA kernel handles this weight type
+bool gemv_mma_supported(int type);
 
 // GEMV: dst[dst_off + m] for m < M, rows of matrix `mat` of each task, from
 // the pre-pass activations `a` (ldk == 256 * groups).  List mode (tasks !=

@@ -49,7 +49,8 @@ class CTensor(C.Structure):
 class LaunchInfo(C.Structure):
     _fields_ = [("path", C.c_char * 32), ("workgroups", C.c_int64), ("threads", C.c_int32),
                 ("cols_per_task", C.c_int32), ("tasks", C.c_int64), ("k_waves", C.c_int32),
-                ("k_slices", C.c_int32), ("groups_per_wave", C.c_int32), ("lds_bytes", C.c_int64)]
+                ("k_slices", C.c_int32), ("groups_per_wave", C.c_int32), ("lds_bytes", C.c_int64),
+                ("tiles_per_wg", C.c_int32)]
 
 
 class CNode(C.Structure):

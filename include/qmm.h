@@ -180,7 +180,7 @@ const char * qmm_last_path(qmm_ctx * ctx);
 /* The launch a qmm_mul_mat with these tensors would make (host only, no
  * device, no buffers needed: only types and shapes are read). */
 typedef struct qmm_launch_info {
-    char    path[32];          /* "gemv" or "gemm-mfma" */
+    char    path[32];          /* "gemv", "gemv-mfma" (3..8 columns on the MFMA) or "gemm-mfma" */
     int64_t workgroups;
     int32_t threads;           /* per work-group */
     int32_t cols_per_task;     /* GEMV: activation columns per weight pass */
@@ -189,6 +189,8 @@ typedef struct qmm_launch_info {
     int32_t k_slices;          /* GEMV: work-groups per 64-row tile, splitting K */
     int32_t groups_per_wave;   /* GEMV: 256-weight groups per wave */
     int64_t lds_bytes;         /* dynamic LDS per work-group */
+    int32_t tiles_per_wg;      /* GEMV: 64-row tiles per work-group ("gemv-mfma": threads / 64 =
+                                  tiles_per_wg x k_waves) */
 } qmm_launch_info;
 int    qmm_describe_mul_mat(const qmm_tensor * src0, const qmm_tensor * src1, const qmm_tensor * dst,
                             qmm_launch_info * out);

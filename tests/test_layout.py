@@ -222,12 +222,26 @@ def test_gemv_plan(qtype, K, M, N):
     fake = qmm.Buffer(ptr=0x1000, size=1 << 44)
     info = qmm.describe_mul_mat(qmm.Tensor(fake, qtype, (K, M)), qmm.Tensor(fake, qmm.F32, (K, N)),
                                 qmm.Tensor(fake, qmm.F32, (M, N)))
-    assert info["path"] == "gemv"
+    # the MFMA kernel takes 3..8 columns of the types whose blocks it decodes
+    mma = N >= 3 and qtype in (qmm.Q4_0, qmm.Q8_0, qmm.Q4_K, qmm.IQ4_XS)
+    assert info["path"] == ("gemv-mfma" if mma else "gemv")
     G, nt = -(-K // 256), -(-M // 64)
     W, KS, spw, nc = info["k_waves"], info["k_slices"], info["groups_per_wave"], info["cols_per_task"]
-    assert 1 <= W <= 8 and KS >= 1 and spw >= 1 and info["threads"] == 64 * W
+    assert 1 <= W <= 8 and KS >= 1 and spw >= 1
     assert KS * W * spw >= G                             # the waves cover K
     assert (KS - 1) * W * spw < G                        # no work-group without groups
     assert info["tasks"] == -(-N // nc)
-    assert info["workgroups"] == info["tasks"] * nt * KS
-    assert info["lds_bytes"] == (W * nc * 64 * 4 if W > 1 else 0)
+    tw = info["tiles_per_wg"]
+    assert info["threads"] == 64 * W * tw
+    assert info["workgroups"] == info["tasks"] * -(-nt // tw) * KS
+    if mma:
+        # TW tiles x W waves splitting K; the K range's activations are staged in LDS: 256 zero
+        # bytes, then per column and group the codes (272 B), Q4_K split sums (16 B) and the
+        # scales (4 B per block); the W waves' sums reuse it
+        assert 1 <= tw <= 4 and W * tw <= 4 and W * spw <= 24
+        nsb = 8 if qtype in (qmm.Q4_0, qmm.Q8_0) else 1
+        stage = 256 + W * spw * 8 * (272 + (16 if qtype == qmm.Q4_K else 0) + 4 * nsb)
+        assert info["lds_bytes"] == max(stage, W * tw * 8 * 64 * 4 if W > 1 else 0)
+    else:
+        assert tw == 1
+        assert info["lds_bytes"] == (W * nc * 64 * 4 if W > 1 else 0)
