@@ -337,7 +337,7 @@ __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per 
     const int wr = wave & 1, wn = (wave >> 1) % NWN, wk = (wave >> 1) / NWN;
     const int h = lane >> 5, l32 = lane & 31;
     v16f out0 = v16f{}, out1 = v16f{};                            // row tiles 0 and 1
-    v16i c1[2], c2[2];
+    v16i c1[2], c2[2];                                            // Q4_K: set by each super-block's first MFMAs
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
         c1[rt] = v16i{};
@@ -388,7 +388,9 @@ __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per 
         }
         return o;
     };
-    auto mma = [&](const Ops o) {
+    // first: the super-block's first (sub-)block of this wave (Q4_K): its MFMAs start from an
+    // inline zero instead of cleared accumulators
+    auto mma = [&](const Ops o, bool first) {
         if constexpr (BF) {
             const v16i d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a, o.b[0][0], magic, 0, 0, 0);
             const v16i d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a, o.b[1][0], magic, 0, 0, 0);
@@ -422,6 +424,12 @@ __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per 
                     for (int r = 0; r < 16; ++r) c1[rt][r] += o.sc[rt][0] * d0[r] + o.sc[rt][1] * d1[r];
                 }
             }
+        } else if (first) {
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) {
+                c1[rt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a, o.b[rt][0], v16i{}, 0, 0, 0);
+                c2[rt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a, o.b[rt][1], v16i{}, 0, 0, 0);
+            }
         } else {
 #pragma unroll
             for (int rt = 0; rt < 2; ++rt) {
@@ -437,13 +445,17 @@ __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per 
             for (int i = 0; i < NQ; ++i) {
                 if (i + 1 < NQ) o1 = load_ops(buf, wk + (i + 1) * KSPLIT);
                 __builtin_amdgcn_sched_barrier(0);
-                mma(o0);
+                mma(o0, false);
                 __builtin_amdgcn_sched_barrier(0);
                 o0 = o1;
             }
+        } else if (KQ && (s & 1) == 0) {                          // uniform: a super-block starts
+            mma(load_ops(buf, wk), true);
+#pragma unroll
+            for (int i = 1; i < NQ; ++i) mma(load_ops(buf, wk + i * KSPLIT), false);
         } else {                                                  // (registers: no second operand set)
 #pragma unroll
-            for (int i = 0; i < NQ; ++i) mma(load_ops(buf, wk + i * KSPLIT));
+            for (int i = 0; i < NQ; ++i) mma(load_ops(buf, wk + i * KSPLIT), false);
         }
         if constexpr (IS) {
             if (s & 1) {                                          // end of the super-block (uniform)
@@ -488,8 +500,9 @@ __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per 
                     const int row = wr * 64 + 32 * rt + l32;
                     const float2 dd = reinterpret_cast<const float2 *>(W + 2 * 64 * 16)[row];
                     const v4i bmin = h ? zero : *reinterpret_cast<const v4i *>(W + row * 16);
+                    // (KSPLIT 2: the tile's second wave adds no min term; its sums meet wave 0's)
                     v16i mh = v16i{}, ml = v16i{};
-                    if (wk == 0) {
+                    if (KSPLIT == 1 || wk == 0) {
                         mh = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, bmin, v16i{}, 0, 0, 0);
                         ml = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, bmin, v16i{}, 0, 0, 0);
                     }
@@ -500,8 +513,6 @@ __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per 
                         const int imn = 64 * mh[r] + ml[r];
                         o[r] += dx[r] * (dd.x * (float)isc - dd.y * (float)imn);
                     }
-                    c1[rt] = v16i{};
-                    c2[rt] = v16i{};
                 }
             }
         }
