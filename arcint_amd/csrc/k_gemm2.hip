@@ -93,8 +93,10 @@ struct G2Params {
     const int8_t * bsp;                  // q8_K: split sub-block sums [super-block][ldT] x 16 B
     int64_t N;                           // columns per batch
     int64_t mt, nt;                      // work-group tiles along M (128 rows) and N (BN columns)
-    int64_t chunk;                       // work-groups per XCD (numbering)
-    int KS, spk;                         // K slices, stages per slice
+    int64_t P;                           // tiles computed whole (no K split), tile order
+    int KS, spk;                         // the other tiles: K slices of spk stages each
+    int64_t X;                           // work-groups numbered by XCD: all (P = 0) or the P whole tiles
+    int64_t chunk;                       // X / 8 rounded up
     int64_t nst;                         // stages along K (2 per group)
     GemmBatch bt;
     float * dst;
@@ -137,19 +139,27 @@ __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per 
     constexpr int kStage = LY::stage;
     extern __shared__ __align__(16) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // work-group -> tile (mtile-major) and K range.  The first P work-groups take tiles 0 .. P - 1
+    // whole, numbered so that those sharing weight rows run on one XCD (work-group b runs on XCD
+    // b % 8); the rest take the K slices of tiles P .. in plain order (spread over the XCDs) and add
+    // their sums into dst, zeroed from the first such tile's rows by the pre-pass.
     const uint32_t bid = blockIdx.x;                              // grid < 2^31 (host check)
-    const uint32_t L = (bid & 7) * (uint32_t)p.chunk + (bid >> 3);
-    if (L >= (uint32_t)(p.mt * p.nt * p.KS)) return;              // uniform
-    const uint32_t ntile = L % (uint32_t)p.nt, rest = L / (uint32_t)p.nt;
-    const int ks = (int)(rest % (uint32_t)p.KS);
-    const int64_t mtile = rest / (uint32_t)p.KS;
+    const uint32_t P = (uint32_t)p.P, X = (uint32_t)p.X, nx = 8 * (uint32_t)p.chunk;
+    const uint32_t total = P + (uint32_t)(p.mt * p.nt - p.P) * (uint32_t)p.KS;
+    const uint32_t L = bid < nx ? (bid & 7) * (uint32_t)p.chunk + (bid >> 3) : X + (bid - nx);
+    if (L >= total || (bid < nx && L >= X)) return;               // uniform
+    const uint32_t tile = L < P ? L : P + (L - P) / (uint32_t)p.KS;
+    const int ks = L < P ? 0 : (int)((L - P) % (uint32_t)p.KS);
+    const bool split = L >= P && p.KS > 1;                        // atomics into zeroed dst
+    const uint32_t ntile = tile % (uint32_t)p.nt;
+    const int64_t mtile = tile / (uint32_t)p.nt;
     const uint32_t bz = blockIdx.y;
     const int64_t i2 = bz % (uint32_t)p.bt.ne12, i3 = bz / (uint32_t)p.bt.ne12;
     const int64_t mat = i2 / p.bt.r2 + (i3 / p.bt.r3) * p.bt.ne02;
     const int64_t col0 = bz * p.N;                                // first activation column of the batch
     const int64_t n0 = (int64_t)ntile * BN;
-    const int s0 = ks * p.spk;
-    const int s1 = (int)((s0 + p.spk) < p.nst ? (s0 + p.spk) : p.nst);   // s1 - s0 is even
+    const int s0 = L < P ? 0 : ks * p.spk;
+    const int s1 = L < P ? (int)p.nst : (int)((s0 + p.spk) < p.nst ? (s0 + p.spk) : p.nst);   // s1 - s0 is even
 
     // ---- staging addresses.  Thread tid stages code chunk cs = (tid / 64) % 4 of row tid % 64 of
     // tile tid / 256 (and reads that row's header), NA 16-byte units of activation codes, one
@@ -585,7 +595,7 @@ __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per 
             if (n < p.N) {
                 float * o = dst + n * p.bt.d_nb1 + m;
                 const float x = v[r];
-                if (p.KS == 1) *o = x;
+                if (!split) *o = x;
                 else atomicAdd(o, x);
             }
         }
@@ -603,41 +613,65 @@ hipError_t launch_t(const G2Params & p, const dim3 & g, hipStream_t s, const KTi
     return hipGetLastError();
 }
 
-// Launch shape: column tile BN, K slices KS and stages per slice spk, from a
-// cost model fitted to measurements on MI355X: a work-group stage costs ~2 us
-// at BN = 128 and 0.62 of that at BN = 64 (the weight staging and the barrier
-// do not shrink with the tile); work-groups run in rounds of one per CU; K
+// Launch shape: column tile BN, and which tiles split K how, from a cost
+// model fitted to measurements on MI355X: a work-group stage costs ~2 us at
+// BN = 128 and 0.62 of that at BN = 64 (the weight staging and the barrier do
+// not shrink with the tile); work-groups run in rounds of one per CU; K
 // slices add their partial sums with float atomics (~480 adds per ns over the
-// chip), after the pre-pass zeroed dst.  Each candidate (BN, KS) is priced as
-// rounds x stages x stage cost + atomics and the cheapest is taken.
+// chip), into dst rows the pre-pass zeroed.  Two kinds of candidate, each
+// priced as rounds x stages x stage cost + atomics, the cheapest taken:
+//  * uniform: every tile in KS slices of spk stages;
+//  * tail (one batch): the tiles of the whole rounds (P, in whole rows of
+//    column tiles) unsplit, the rest in KS slices that fill the last round.
 struct G2Shape {
     int BN, KS, spk;
-    int64_t mt, nt;
+    int64_t mt, nt, P;
 };
 G2Shape g2_shape(const WView & w, int64_t N, int64_t nbatch) {
     static const int64_t cus = [] {
         const char * e = getenv("QMM_GEMM_CUS");
         return e ? std::max<int64_t>(1, atoll(e)) : (int64_t)256;
     }();
+    const char * te = getenv("QMM_GEMM_TAIL");
+    const bool tail_on = !te || atoi(te) != 0;
     G2Shape best{};
     double best_us = 1e300;
-    const int64_t mt = (w.M + 127) / 128;
+    const int64_t mt = (w.M + 127) / 128, nst = 2 * w.G;
+    auto consider = [&](double us, const G2Shape & sh) {
+        if (us < best_us * 0.98) {                                // prefer the earlier (wider, unsplit) shape on ties
+            best_us = us;
+            best = sh;
+        }
+    };
     for (int bn : { 128, 64 }) {
-        const int64_t nt = (N + bn - 1) / bn;
+        const double c = 2.0 * (bn == 64 ? 0.62 : 1.0);           // us per stage
+        const int64_t nt = (N + bn - 1) / bn, T = mt * nt;
         int64_t prev_gps = -1;
         for (int64_t ks = 1; ks <= std::min<int64_t>(w.G, 64); ++ks) {
             const int64_t gps = (w.G + ks - 1) / ks;
             if (gps == prev_gps) continue;                        // same split as a smaller ks
             prev_gps = gps;
             const int64_t kss = (w.G + gps - 1) / gps;
-            const int64_t wgs = mt * nt * nbatch * kss;
-            const double rounds = (double)((wgs + cus - 1) / cus);
-            double us = rounds * (double)(2 * gps) * 2.0 * (bn == 64 ? 0.62 : 1.0);
+            const int64_t wgs = T * nbatch * kss;
+            double us = (double)((wgs + cus - 1) / cus) * (double)(2 * gps) * c;
             if (kss > 1) us += (double)w.M * (double)N * (double)nbatch * (double)kss / 480000.0;
-            if (us < best_us * 0.98) {                            // prefer the earlier (wider, unsplit) shape on ties
-                best_us = us;
-                best = G2Shape{ bn, (int)kss, (int)(2 * gps), mt, nt };
-            }
+            consider(us, G2Shape{ bn, (int)kss, (int)(2 * gps), mt, nt, 0 });
+        }
+        if (!tail_on || nbatch != 1 || T <= cus) continue;
+        const int64_t R = T / cus, P = (R * cus / nt) * nt, tail = T - P;
+        if (P <= 0 || tail <= 0) continue;
+        prev_gps = -1;
+        for (int64_t ks = 2; ks <= std::min<int64_t>(w.G, 64); ++ks) {
+            const int64_t gps = (w.G + ks - 1) / ks;
+            if (gps == prev_gps) continue;
+            prev_gps = gps;
+            const int64_t kss = (w.G + gps - 1) / gps;
+            // slices first fill the slots the whole rounds leave free, then rounds of their own
+            const int64_t free_slots = (R * cus - P) * std::max<int64_t>(1, nst / (2 * gps));
+            const int64_t rest = std::max<int64_t>(0, tail * kss - free_slots);
+            double us = (double)R * (double)nst * c + (double)((rest + cus - 1) / cus) * (double)(2 * gps) * c;
+            us += (double)tail * (double)bn * 128.0 * (double)kss / 480000.0;
+            consider(us, G2Shape{ bn, (int)kss, (int)(2 * gps), mt, nt, P });
         }
     }
     return best;
@@ -647,10 +681,16 @@ G2Shape g2_shape(const WView & w, int64_t N, int64_t nbatch) {
 
 int gemm_kslices(const WView & w, int64_t N, int64_t nbatch) { return g2_shape(w, N, nbatch).KS; }
 
+int64_t gemm_zero_from(const WView & w, int64_t N, int64_t nbatch) {
+    const G2Shape sh = g2_shape(w, N, nbatch);
+    if (sh.KS == 1) return w.M;                                   // nothing adds into dst
+    return std::min<int64_t>(w.M, sh.P / sh.nt * 128);
+}
+
 void gemm_shape(int type, const WView & w, int64_t N, int64_t nbatch, int64_t * workgroups, int * threads,
                 int * lds_bytes) {
     const G2Shape sh = g2_shape(w, N, nbatch);
-    *workgroups = sh.mt * sh.nt * sh.KS * nbatch;
+    *workgroups = (sh.P + (sh.mt * sh.nt - sh.P) * sh.KS) * nbatch;
     *threads = kT;
     int st;
     switch (type) {
@@ -681,11 +721,13 @@ hipError_t launch_gemm(int type, const WView & w, const ActBuf & a, int64_t N, i
     p.nst = 2 * w.G;
     p.KS = sh.KS;
     p.spk = sh.spk;
+    p.P = sh.P;
     p.bt = bt;
     p.dst = dst;
-    const int64_t total = p.mt * p.nt * p.KS;
-    p.chunk = (total + 7) / 8;
-    const int64_t grid = p.chunk * 8;
+    const int64_t total = sh.P + (p.mt * p.nt - sh.P) * p.KS;
+    p.X = sh.P > 0 ? sh.P : total;
+    p.chunk = (p.X + 7) / 8;
+    const int64_t grid = 8 * p.chunk + (total - p.X);
     if (grid > 0x7fffffff) return hipErrorInvalidValue;
     const dim3 g((unsigned)grid, (unsigned)nbatch);
     if (type == QMM_TYPE_Q4_0)

@@ -25,9 +25,9 @@ namespace {
 constexpr int kTpb = 256;
 
 __device__ void zero_cols(const ZeroJob & z, int64_t t) {
-    const int64_t n = z.M * z.ncols;
+    const int64_t rows = z.M - z.m0, n = rows * z.ncols;
     if (t >= n) return;
-    const int64_t c = t / z.M, m = t - c * z.M;
+    const int64_t c = t / rows, m = z.m0 + (t - c * rows);
     const int64_t r = c / z.ne1, i1 = c - r * z.ne1, i3 = r / z.ne2, i2 = r - i3 * z.ne2;
     z.dst[i1 * z.nb1 + i2 * z.nb2 + i3 * z.nb3 + m] = 0.0f;
 }
@@ -130,7 +130,7 @@ hipError_t launch_quantize(const F32Cols & src, int64_t K, int64_t ncols, const 
                            hipStream_t s) {
     if (K <= 0 || a.ldk % 256 || a.ldk < K) return hipErrorInvalidValue;
     const ZeroJob zj = z ? *z : ZeroJob{};
-    const int64_t nzblk = z ? (zj.M * zj.ncols + kTpb - 1) / kTpb : 0;
+    const int64_t nzblk = z ? ((zj.M - zj.m0) * zj.ncols + kTpb - 1) / kTpb : 0;
     int64_t nq = a.vdt == QMM_TYPE_Q8_0 ? ncols * (a.ldk / 4) : ncols * (a.ldk / 256) * 64;
     const int64_t nqblk = ncols > 0 ? (nq + kTpb - 1) / kTpb : 0;
     const int64_t grid = nqblk + nzblk;

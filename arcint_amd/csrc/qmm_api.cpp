@@ -581,8 +581,10 @@ int qmm_mul_mat(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1,
     dn.d_nb3 = (int64_t)(dst->nb[3] / 4);
     if (use_gemm) {
         const int64_t nbatch = dn.ne12 * dn.ne13;
-        ZeroJob z{ d, w.M, N * nbatch, N, dn.ne12, dn.d_nb1, dn.d_nb2, dn.d_nb3 };
-        const bool split = gemm_kslices(w, N, nbatch) > 1;
+        // K slices add into dst rows from zero_from on (the pre-pass zeroes them)
+        const int64_t zero_from = gemm_zero_from(w, N, nbatch);
+        ZeroJob z{ d, w.M, N * nbatch, N, dn.ne12, dn.d_nb1, dn.d_nb2, dn.d_nb3, zero_from };
+        const bool split = zero_from < w.M;
         if ((rc = quantize_src1(ctx, src0->type, src1, true, &a, split ? &z : nullptr))) return rc;
         GemmBatch bt;
         bt.ne12 = dn.ne12;

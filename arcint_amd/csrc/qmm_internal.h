@@ -93,8 +93,9 @@ struct ActBuf {
 // fastest, floats [0, M) at i1 * nb1 + i2 * nb2 + i3 * nb3 (float strides).
 struct ZeroJob {
     float * dst;
-    int64_t M, ncols, ne1, ne2;
+    int64_t M, ncols, ne1, ne2;     // rows [m0, M) of each column
     int64_t nb1, nb2, nb3;
+    int64_t m0;                     // 0 unless set
 };
 
 __host__ __device__ static inline int act_block(int vdt) { return vdt == QMM_TYPE_Q8_0 ? 32 : 256; }
@@ -205,6 +206,9 @@ hipError_t launch_gemm(int type, const WView & w, const ActBuf & a, int64_t N, i
 // K slices the GEMM splits this product into; above 1 the slices add their
 // partial sums to dst with atomics, so dst must be zeroed first.
 int gemm_kslices(const WView & w, int64_t N, int64_t nbatch);
+// first dst row that K slices add into (the pre-pass zeroes rows [that, M) of every column;
+// M: no row)
+int64_t gemm_zero_from(const WView & w, int64_t N, int64_t nbatch);
 // launch shape of that GEMM (qmm_describe_mul_mat)
 void gemm_shape(int type, const WView & w, int64_t N, int64_t nbatch, int64_t * workgroups, int * threads,
                 int * lds_bytes);

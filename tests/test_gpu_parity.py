@@ -341,6 +341,23 @@ GEMM_FULL = [
 ]
 
 
+@pytest.mark.parametrize("qtype", [qmm.Q4_K, qmm.Q4_0])
+def test_gemm_tail_split(be, sc, orc, qtype):
+    # 66 row tiles x 4 column tiles = 264 > 256 work-groups: the first 256 tiles run whole and
+    # the last row of tiles (partial: 8384 = 65.5 x 128 rows) in K slices added into dst rows
+    # the pre-pass zeroed
+    M, K, N = 8384, 1024, 512
+    fake = qmm.Buffer(ptr=0x1000, size=1 << 44)
+    info = qmm.describe_mul_mat(qmm.Tensor(fake, qtype, (K, M)), qmm.Tensor(fake, qmm.F32, (K, N)),
+                                qmm.Tensor(fake, qmm.F32, (M, N)))
+    assert info["path"] == "gemm-mfma" and info["k_slices"] > 1
+    assert info["workgroups"] == 256 + 8 * info["k_slices"]
+    say("gemm-tail", qtype, M, K, N)
+    got, ref = run_mul_mat(be, sc, orc, qtype, M, K, N, seed=95)
+    assert be.last_path() == "gemm-mfma"
+    assert rel_err(got, ref) <= TOL
+
+
 @pytest.mark.parametrize("qtype,M,K,N", GEMM_FULL)
 def test_full_size_gemm(be, sc, orc, qtype, M, K, N):
     say("gemm-full", qtype, M, K, N)
