@@ -609,7 +609,7 @@ int qmm_mul_mat(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1,
         return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat: GEMV shape out of range");
     ZeroJob z{ d, w.M, N * dn.ne12 * dn.ne13, N, dn.ne12, dn.d_nb1, dn.d_nb2, dn.d_nb3 };
     if ((rc = quantize_src1(ctx, src0->type, src1, false, &a, plan.KS > 1 ? &z : nullptr))) return rc;
-    ctx->path = "gemv";
+    ctx->path = plan.mma ? "gemv-mfma" : "gemv";
     if (N > kMaxTaskCols) note_downgrade(ctx, "mul_mat: many columns on the GEMV");
     KTime kt;
     const KTime * ktp;
@@ -657,7 +657,7 @@ int qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * sr
     GemvTask * tasks = (GemvTask *)(rb + o_tasks);
     int32_t * ntasks = (int32_t *)(rb + o_cnt);
     QMM_HIP(ctx, launch_route(r, (int32_t *)rb, tasks, ntasks, d, M, ctx->stream));
-    ctx->path = "gemv-id";
+    ctx->path = plan.mma ? "gemv-id-mfma" : "gemv-id";
     KTime kt;
     const KTime * ktp;
     if ((rc = ktime_pair(ctx, &kt, &ktp))) return rc;

@@ -17,6 +17,10 @@ Also reported, on the same JSON line:
   gemm          prefill MUL_MAT at N = 512: Q4_0 4096x4096 and 11008x4096
                 (config 1), Q4_K 17408x5120 (config 2), in TOPS vs the dense
                 int8 MFMA peak ("secondary" repeats the first)
+  gemv          decode and few-column MUL_MAT: Q4_0 4096x4096 and Q6_K
+                5120x17408 at N = 1, Q4_K 17408x5120 at N = 4, IQ4_XS and Q8_0
+                14336x4096 at N = 2, 4, 8 (configs 0, 2, 4): GB/s and the
+                kernel's fraction of 8 TB/s
   moe           MUL_MAT_ID on config 3 (512 Q4_K experts, top-10) at T = 1,
                 4, 256 tokens: GB/s of the expert weights each step touches
 
@@ -134,6 +138,29 @@ def gemm_case(be, qmm, synth, qtype, M, K, N, name, args, traffic_tag):
     return sec
 
 
+def gemv_case(be, qmm, synth, qtype, M, K, N, name, args):
+    """One decode / few-column MUL_MAT (pre-pass + GEMV) over rotated weight
+    copies: GB/s of weight block bytes + activations + dst, for the op (timed
+    region) and for the GEMV kernel alone (dispatch-stamped)."""
+    raw, ws = weight_copies(be, qmm, synth, qtype, M, K, seed=6)
+    x = synth.activations(N, K, seed=7)
+    xt = be.new_tensor(qmm.F32, (K, N))
+    be.set_tensor(xt, x.view(np.uint8).ravel())
+    yt = be.new_tensor(qmm.F32, (M, N))
+    steps = max(20, args.steps // 2)
+    wall, dev, k = time_op(be, ws, xt, yt, steps, max(4, args.warmup // 2))
+    algo = raw.nbytes + K * N * 4 + M * N * 4
+    sec = {"workload": name, "path": be.last_path(), "N": N,
+           "GBs": round(algo * steps / wall / 1e9, 1), "us_per_op": round(wall * 1e6 / steps, 3),
+           "kernel_us": round(k * 1e3, 3), "kernel_GBs": round(algo / (k * 1e-3) / 1e9, 1),
+           "frac_hbm": round(algo / (k * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    for w in ws:
+        be.free_buffer(w.buf)
+    be.free_buffer(xt.buf)
+    be.free_buffer(yt.buf)
+    return sec
+
+
 def moe_case(be, qmm, synth, T, args):
     """MUL_MAT_ID on config 3's expert gate/up: 512 Q4_K experts of 512 x 2048,
     top-10 routing, T tokens sharing one activation column each (ne11 = 1).
@@ -192,7 +219,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
-    ap.add_argument("--only", default="", help="profile one workload: q4k_gemv, q40_gemm, q4k_gemm or moe")
+    ap.add_argument("--only", default="", help="profile one workload: q4k_gemv, q40_gemm, q4k_gemm, gemv or moe")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -253,6 +280,18 @@ def main():
             out["gemm"] = secs
         else:
             out = {"metric": "GEMM TOPS at N=512", "value": secs[0]["tops"], "unit": "TOPS", "gemm": secs}
+    if not args.no_secondary and args.only in ("", "gemv"):
+        gcases = [(qmm.Q4_0, 4096, 4096, 1, "Q4_0 GEMV 4096x4096 N=1 (config 0/1)"),
+                  (qmm.Q6_K, 5120, 17408, 1, "Q6_K GEMV 5120x17408 N=1 (config 2 ffn down)"),
+                  (qmm.Q4_K, 17408, 5120, 4, "Q4_K 17408x5120 N=4 (config 2)")]
+        for qt, nm in ((qmm.IQ4_XS, "IQ4_XS"), (qmm.Q8_0, "Q8_0")):
+            for n in (2, 4, 8):
+                gcases.append((qt, 14336, 4096, n, f"{nm} 14336x4096 N={n} (config 4)"))
+        gem = [gemv_case(be, qmm, synth, qt, M2, K2, N2, nm, args) for qt, M2, K2, N2, nm in gcases]
+        if out:
+            out["gemv"] = gem
+        else:
+            out = {"metric": "GEMV GB/s", "value": gem[0]["GBs"], "unit": "GB/s", "gemv": gem}
     if not args.no_secondary and args.only in ("", "moe"):
         moe = [moe_case(be, qmm, synth, T, args) for T in (1, 4, 256)]
         if out:

@@ -174,7 +174,10 @@ int    qmm_synchronize(qmm_ctx * ctx);
 /* Number of ops that took a slower path than their type promises (the
  * reference's DOWNGRADE keys); names of the last few in `buf`. */
 int64_t qmm_downgrades(qmm_ctx * ctx, char * buf, size_t buf_len);
-/* Name of the kernel path the last mul_mat / mul_mat_id took. */
+/* Name of the kernel path the last mul_mat / mul_mat_id took: "gemv" (v_dot4
+ * GEMV, 1..8 columns per weight pass), "gemv-mfma" (3..8 columns on the int8
+ * MFMA), "gemm-mfma" (prefill GEMM), "gemv-id" / "gemv-id-mfma" (MUL_MAT_ID
+ * expert tasks on either GEMV). */
 const char * qmm_last_path(qmm_ctx * ctx);
 
 /* The launch a qmm_mul_mat with these tensors would make (host only, no

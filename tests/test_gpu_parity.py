@@ -169,6 +169,9 @@ def test_mul_mat_gemv(be, sc, orc, qtype, N):
     M, K = 300, 2048
     say("gemv", qtype, M, K, N)
     got, ref = run_mul_mat(be, sc, orc, qtype, M, K, N, seed=51)
+    # 3..8 columns of the types the MFMA kernel decodes run on it
+    mma = N >= 3 and qtype != qmm.Q6_K
+    assert be.last_path() == ("gemv-mfma" if mma else "gemv")
     assert rel_err(got, ref) <= TOL
 
 
