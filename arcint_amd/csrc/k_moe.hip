@@ -1,4 +1,5 @@
-// k_moe.hip - MUL_MAT_ID routing on gfx950.
+// k_moe.hip - MUL_MAT_ID routing, the MoE router (softmax / top-k) and the
+// combine of the experts' outputs on gfx950.
 //
 // Role of the reference's kernel_moe_route_tiles (P01:2417-2444): one
 // work-group counts the (token, slot) pairs of every expert in LDS, scans the
@@ -97,7 +98,116 @@ __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs r, int32_t * 
     }
 }
 
+// ---- the router: softmax -> top-k -> normalized weights, one wave per token ----------
+// Role of the reference's kernel_topk_moe_softmax_norm (P09:899-1000), which replaces
+// llama.cpp's gating chain SOFT_MAX, ARGSORT (desc), VIEW, GET_ROWS, SUM_ROWS, CLAMP, DIV
+// (matched at P02:786-821).  Lane l holds the logits of experts l + 64 j, j < NPER.  The max
+// and the sum of exp(x - max) are wave reductions; each of the k rounds picks the largest
+// unselected exp(x - max) over the wave (ties: the lower expert) by DPP reductions.  The
+// weights are the picked exp(x - max) / sum, divided by their own sum clamped to [cmin, cmax].
+constexpr int kTopkWaves = 4;                   // tokens per work-group
+
+__device__ __forceinline__ float wave_sum_f(float v) {
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) v += __shfl_xor(v, d, 64);
+    return v;
+}
+
+template <int NPER>
+__global__ __launch_bounds__(64 * kTopkWaves) void k_topk(TopkArgs a) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t t = (int64_t)blockIdx.x * kTopkWaves + wave;
+    if (t >= a.n_tok) return;                                     // whole waves
+    const float * x = reinterpret_cast<const float *>(a.logits + t * a.nbl1);
+    float p[NPER];
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NPER; ++j) {
+        const int i = lane + 64 * j;
+        p[j] = i < a.n_expert ? x[i] : -INFINITY;
+        m = fmaxf(m, p[j]);
+    }
+    m = wave_max(m);
+    float sl = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NPER; ++j) {
+        const int i = lane + 64 * j;
+        p[j] = i < a.n_expert ? expf(p[j] - m) : -1.0f;          // -1: no expert (never picked)
+        if (i < a.n_expert) sl += p[j];
+    }
+    const float s = wave_sum_f(sl);
+    uint32_t sel = 0;                                             // bit j: p[j] picked
+    float wsum = 0.0f, my_w = 0.0f;
+    int my_id = 0;
+    for (int r = 0; r < a.k; ++r) {                               // uniform
+        float bv = -1.0f;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int j = 0; j < NPER; ++j) {
+            if (!(sel >> j & 1u) && p[j] > bv) {                  // j ascending: ties keep the lower expert
+                bv = p[j];
+                bi = lane + 64 * j;
+            }
+        }
+        // the wave's largest value (DPP row reductions, four readlanes), then the lowest expert
+        // among the lanes holding it
+        const float gv = wave_max(bv);
+        bi = wave_min_i(bv == gv ? bi : 0x7fffffff);
+        bv = gv;
+        const float wr = bv / s;
+        wsum += wr;
+        if (lane == r) {
+            my_w = wr;
+            my_id = bi;
+        }
+        if ((bi & 63) == lane && bi < a.n_expert) sel |= 1u << (bi >> 6);
+    }
+    if (lane < a.k) {
+        const float c = fminf(fmaxf(wsum, a.cmin), a.cmax);
+        reinterpret_cast<int32_t *>(a.ids + t * a.nbi1)[lane] = my_id;
+        reinterpret_cast<float *>(a.w + t * a.nbw1)[lane] = my_w / c;
+    }
+}
+
+// ---- the combine: dst[:, t] = sum_j w[j, t] experts[:, j, t] (+ shared[:, t] sigmoid(g[t]))
+// in llama.cpp's order: the products rounded, added slot by slot, then the gated shared
+// expert added (contraction off: ggml-cpu's MUL then ADDs round every product).
+__global__ __launch_bounds__(256) void k_combine(CombineArgs a) {
+#pragma clang fp contract(off)
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= a.M * a.T) return;
+    const int64_t t = idx / a.M, m = idx - t * a.M;
+    const char * e = a.experts + t * a.enb2 + m * 4;
+    const float * w = reinterpret_cast<const float *>(a.w + t * a.wnb1);
+    float y = reinterpret_cast<const float *>(e)[0] * w[0];
+    for (int j = 1; j < a.k; ++j) y = y + *reinterpret_cast<const float *>(e + j * a.enb1) * w[j];
+    if (a.shared) {
+        const float g = *reinterpret_cast<const float *>(a.gate + t * a.gnb1);
+        const float sg = 1.0f / (1.0f + expf(-g));
+        y = y + *reinterpret_cast<const float *>(a.shared + t * a.snb1 + m * 4) * sg;
+    }
+    *reinterpret_cast<float *>(a.dst + t * a.dnb1 + m * 4) = y;
+}
+
 }  // namespace
+
+hipError_t launch_topk(const TopkArgs & a, hipStream_t s) {
+    if (a.n_expert < 1 || a.n_expert > 1024 || a.k < 1 || a.k > 32 || a.k > a.n_expert || a.n_tok < 1) return hipErrorInvalidValue;
+    const dim3 g((unsigned)((a.n_tok + kTopkWaves - 1) / kTopkWaves)), b(64 * kTopkWaves);
+    const int nper = (a.n_expert + 63) / 64;
+    if (nper <= 1) k_topk<1><<<g, b, 0, s>>>(a);
+    else if (nper <= 2) k_topk<2><<<g, b, 0, s>>>(a);
+    else if (nper <= 4) k_topk<4><<<g, b, 0, s>>>(a);
+    else if (nper <= 8) k_topk<8><<<g, b, 0, s>>>(a);
+    else k_topk<16><<<g, b, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+hipError_t launch_combine(const CombineArgs & a, hipStream_t s) {
+    if (a.M < 1 || a.T < 1 || a.k < 1 || a.M * a.T >= ((int64_t)1 << 40)) return hipErrorInvalidValue;
+    k_combine<<<dim3((unsigned)((a.M * a.T + 255) / 256)), 256, 0, s>>>(a);
+    return hipGetLastError();
+}
 
 hipError_t launch_route(const RouteArgs & r, int32_t * scratch, GemvTask * tasks, int32_t * ntasks,
                         float * dst, int64_t M, hipStream_t s) {

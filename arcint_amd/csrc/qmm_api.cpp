@@ -665,6 +665,88 @@ int qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * sr
     return QMM_OK;
 }
 
+// the last byte a tensor view touches lies inside its buffer
+static bool span_ok(const qmm_tensor * t) {
+    size_t last = 0;
+    for (int i = 0; i < 4; ++i) {
+        if (t->ne[i] <= 0) return false;
+        last += (size_t)(t->ne[i] - 1) * t->nb[i];
+    }
+    return t->offs + last + t->nb[0] <= t->buffer->size;
+}
+
+int qmm_moe_topk(qmm_ctx * ctx, const qmm_tensor * logits, const qmm_tensor * ids, const qmm_tensor * weights,
+                 float cmin, float cmax) {
+    if (!ctx) return QMM_ERR_INVALID;
+    if (!check_f32(logits) || !check_f32(weights) || !ids || !ids->buffer || ids->type != QMM_TYPE_I32 || ids->nb[0] != 4)
+        return fail(ctx, QMM_ERR_INVALID, "moe_topk: logits / weights f32 and ids i32 with nb[0] == 4");
+    const int64_t n_expert = logits->ne[0], T = logits->ne[1], k = ids->ne[0];
+    if (logits->ne[2] != 1 || logits->ne[3] != 1 || ids->ne[1] != T || ids->ne[2] != 1 || ids->ne[3] != 1 ||
+        weights->ne[0] != k || weights->ne[1] != T || weights->ne[2] != 1 || weights->ne[3] != 1)
+        return fail(ctx, QMM_ERR_INVALID, "moe_topk: logits [n_expert, T], ids and weights [k, T]");
+    if (n_expert > 1024 || k < 1 || k > 32 || k > n_expert)
+        return fail(ctx, QMM_ERR_UNSUPPORTED, "moe_topk: n_expert <= 1024 and 1 <= k <= min(32, n_expert)");
+    if (!span_ok(logits) || !span_ok(ids) || !span_ok(weights) || logits->nb[1] % 4 || ids->nb[1] % 4 ||
+        weights->nb[1] % 4 || logits->offs % 4 || ids->offs % 4 || weights->offs % 4)
+        return fail(ctx, QMM_ERR_INVALID, "moe_topk: a view past its buffer or not 4-byte aligned");
+    if (!(cmin <= cmax) || !(cmax > 0.0f)) return fail(ctx, QMM_ERR_INVALID, "moe_topk: clamp range");
+    QMM_HIP(ctx, hipSetDevice(ctx->device));
+    TopkArgs a;
+    a.logits = (const char *)logits->buffer->ptr + logits->offs;
+    a.ids = (char *)ids->buffer->ptr + ids->offs;
+    a.w = (char *)weights->buffer->ptr + weights->offs;
+    a.nbl1 = (int64_t)logits->nb[1];
+    a.nbi1 = (int64_t)ids->nb[1];
+    a.nbw1 = (int64_t)weights->nb[1];
+    a.n_expert = (int)n_expert;
+    a.k = (int)k;
+    a.n_tok = T;
+    a.cmin = cmin;
+    a.cmax = cmax;
+    ctx->path = "moe-topk";
+    QMM_HIP(ctx, launch_topk(a, ctx->stream));
+    return QMM_OK;
+}
+
+int qmm_moe_combine(qmm_ctx * ctx, const qmm_tensor * experts, const qmm_tensor * weights, const qmm_tensor * shared,
+                    const qmm_tensor * gate, const qmm_tensor * dst) {
+    if (!ctx) return QMM_ERR_INVALID;
+    if (!check_f32(experts) || !check_f32(weights) || !check_f32(dst) || (shared && !check_f32(shared)) ||
+        (gate && !check_f32(gate)) || (!shared) != (!gate))
+        return fail(ctx, QMM_ERR_INVALID, "moe_combine: f32 tensors with nb[0] == 4; shared and gate together");
+    const int64_t M = experts->ne[0], k = experts->ne[1], T = experts->ne[2];
+    if (experts->ne[3] != 1 || weights->ne[0] != k || weights->ne[1] != T || weights->ne[2] != 1 || dst->ne[0] != M ||
+        dst->ne[1] != T || dst->ne[2] != 1 || (shared && (shared->ne[0] != M || shared->ne[1] != T || shared->ne[2] != 1)) ||
+        (gate && (gate->ne[0] != 1 || gate->ne[1] != T || gate->ne[2] != 1)))
+        return fail(ctx, QMM_ERR_INVALID, "moe_combine: experts [M, k, T], weights [k, T], shared and dst [M, T], gate [1, T]");
+    if (k < 1 || k > 64) return fail(ctx, QMM_ERR_UNSUPPORTED, "moe_combine: 1 <= k <= 64");
+    for (const qmm_tensor * t : { experts, weights, dst, shared, gate }) {
+        if (t && (!span_ok(t) || t->offs % 4 || t->nb[1] % 4 || t->nb[2] % 4))
+            return fail(ctx, QMM_ERR_INVALID, "moe_combine: a view past its buffer or not 4-byte aligned");
+    }
+    if (ranges_overlap(dst, experts) || ranges_overlap(dst, weights) || ranges_overlap(dst, shared) || ranges_overlap(dst, gate))
+        return fail(ctx, QMM_ERR_INVALID, "moe_combine: dst overlaps an input");
+    QMM_HIP(ctx, hipSetDevice(ctx->device));
+    CombineArgs a{};
+    a.experts = (const char *)experts->buffer->ptr + experts->offs;
+    a.w = (const char *)weights->buffer->ptr + weights->offs;
+    a.shared = shared ? (const char *)shared->buffer->ptr + shared->offs : nullptr;
+    a.gate = gate ? (const char *)gate->buffer->ptr + gate->offs : nullptr;
+    a.dst = (char *)dst->buffer->ptr + dst->offs;
+    a.M = M;
+    a.T = T;
+    a.k = (int)k;
+    a.enb1 = (int64_t)experts->nb[1];
+    a.enb2 = (int64_t)experts->nb[2];
+    a.wnb1 = (int64_t)weights->nb[1];
+    a.snb1 = shared ? (int64_t)shared->nb[1] : 0;
+    a.gnb1 = gate ? (int64_t)gate->nb[1] : 0;
+    a.dnb1 = (int64_t)dst->nb[1];
+    ctx->path = "moe-combine";
+    QMM_HIP(ctx, launch_combine(a, ctx->stream));
+    return QMM_OK;
+}
+
 int qmm_graph_compute(qmm_ctx * ctx, const qmm_node * nodes, int n_nodes) {
     if (!ctx || (!nodes && n_nodes)) return QMM_ERR_INVALID;
     ctx->graph_gen++;

@@ -220,6 +220,32 @@ struct RouteArgs {
     int64_t n_used, T, ne11, n_as;
     int64_t dst_nb1, dst_nb2;   // float strides of dst dims 1 and 2
 };
+// MoE router: for each token t (logits column, n_expert <= 1024 floats at logits + t nbl1),
+// ids [k] (i32 at ids + t nbi1) and weights [k] (f32 at w + t nbw1), k <= 32
+struct TopkArgs {
+    const char * logits;
+    char * ids;
+    char * w;
+    int64_t nbl1, nbi1, nbw1;   // bytes
+    int n_expert, k;
+    int64_t n_tok;
+    float cmin, cmax;
+};
+hipError_t launch_topk(const TopkArgs & a, hipStream_t s);
+// MoE combine: dst[m, t] = sum_j w[j, t] experts[m, j, t] (+ shared[m, t] sigmoid(gate[t]));
+// strides in bytes, elements along m contiguous
+struct CombineArgs {
+    const char * experts;
+    const char * w;
+    const char * shared;        // optional
+    const char * gate;          // with shared: one logit per token
+    char * dst;
+    int64_t M, T;
+    int k;
+    int64_t enb1, enb2, wnb1, snb1, gnb1, dnb1;
+};
+hipError_t launch_combine(const CombineArgs & a, hipStream_t s);
+
 // scratch: pairs [T*n_used]; tasks out
 hipError_t launch_route(const RouteArgs & r, int32_t * scratch, GemvTask * tasks, int32_t * ntasks,
                         float * dst, int64_t M, hipStream_t s);

@@ -33,7 +33,8 @@ EXPORTS = (
     "qmm_tensor_set", "qmm_tensor_get", "qmm_supports_op", "qmm_mul_mat", "qmm_mul_mat_id",
     "qmm_graph_compute", "qmm_dequantize", "qmm_quantize_act", "qmm_synchronize", "qmm_downgrades",
     "qmm_last_path", "qmm_timer_begin", "qmm_timer_end", "qmm_buffer_copy", "qmm_kernel_timing",
-    "qmm_kernel_time", "qmm_tensor_pack", "qmm_tensor_unpack", "qmm_describe_mul_mat",
+    "qmm_kernel_time", "qmm_tensor_pack", "qmm_tensor_unpack", "qmm_describe_mul_mat", "qmm_moe_topk",
+    "qmm_moe_combine",
 )
 
 
@@ -91,6 +92,8 @@ def load() -> C.CDLL:
         L.qmm_supports_op.argtypes = [vp, i32, T, T, T, T, C.c_char_p, sz]
         L.qmm_mul_mat.argtypes = [vp, T, T, T]
         L.qmm_mul_mat_id.argtypes = [vp, T, T, T, T]
+        L.qmm_moe_topk.argtypes = [vp, T, T, T, C.c_float, C.c_float]
+        L.qmm_moe_combine.argtypes = [vp, T, T, T, T, T]
         L.qmm_graph_compute.argtypes = [vp, C.POINTER(CNode), C.c_int]
         L.qmm_dequantize.argtypes = [vp, T, T]
         L.qmm_quantize_act.argtypes = [vp, i32, T, vp, sz]
@@ -265,6 +268,20 @@ class Backend:
     def mul_mat_id(self, src0: Tensor, src1: Tensor, ids: Tensor, dst: Tensor):
         self._check(self.L.qmm_mul_mat_id(self.h, C.byref(src0.c), C.byref(src1.c), C.byref(ids.c), C.byref(dst.c)),
                     "mul_mat_id")
+
+    def moe_topk(self, logits: Tensor, ids: Tensor, weights: Tensor, cmin: float = 6.103515625e-5,
+                 cmax: float = float("inf")):
+        """Router: softmax over each token's expert logits, top-k ids and their clamped-sum
+        normalized weights (cmin / cmax default to llama.cpp's clamp of the weight sum)."""
+        self._check(self.L.qmm_moe_topk(self.h, C.byref(logits.c), C.byref(ids.c), C.byref(weights.c), cmin, cmax),
+                    "moe_topk")
+
+    def moe_combine(self, experts: Tensor, weights: Tensor, dst: Tensor, shared: Tensor | None = None,
+                    gate: Tensor | None = None):
+        """dst[:, t] = sum_j weights[j, t] experts[:, j, t] (+ shared[:, t] sigmoid(gate[0, t]))."""
+        ref = lambda t: C.byref(t.c) if t is not None else None
+        self._check(self.L.qmm_moe_combine(self.h, C.byref(experts.c), C.byref(weights.c), ref(shared), ref(gate),
+                                           C.byref(dst.c)), "moe_combine")
 
     def graph_compute(self, nodes):
         """nodes: list of (op, src0, src1, ids_or_None, dst)."""

@@ -22,7 +22,8 @@ Also reported, on the same JSON line:
                 14336x4096 at N = 2, 4, 8 (configs 0, 2, 4): GB/s and the
                 kernel's fraction of 8 TB/s
   moe           MUL_MAT_ID on config 3 (512 Q4_K experts, top-10) at T = 1,
-                4, 256 tokens: GB/s of the expert weights each step touches
+                4, 256 tokens: GB/s of the expert weights each step touches; with
+                the router (softmax / top-10) and the combine (hidden 2048) per op
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
@@ -200,10 +201,32 @@ def moe_case(be, qmm, synth, T, args):
     bytes_step = float(np.mean(touched))
     us = wall * 1e6 / steps
     k_us = k_ms / max(n, 1) * 1e3
+    path = be.last_path()
+    # the router (softmax / top-10 over 512 logits per token) and the combine of the layer's
+    # down-projection outputs (hidden 2048, 10 slots) around it, device time per op
+    lg = be.new_tensor(qmm.F32, (E, T))
+    be.set_tensor(lg, synth.activations(T, E, seed=6).view(np.uint8).ravel())
+    rid = be.new_tensor(qmm.I32, (n_used, T))
+    rw = be.new_tensor(qmm.F32, (n_used, T))
+    ex = be.new_tensor(qmm.F32, (2048, n_used, T))
+    be.set_tensor(ex, synth.activations(n_used * T, 2048, seed=7).view(np.uint8).ravel())
+    yo = be.new_tensor(qmm.F32, (2048, T))
+    times = {}
+    for name, fn in (("router", lambda: be.moe_topk(lg, rid, rw)), ("combine", lambda: be.moe_combine(ex, rw, yo))):
+        for _ in range(10):
+            fn()
+        be.synchronize()
+        be.timer_begin()
+        for _ in range(steps):
+            fn()
+        times[name] = be.timer_end() * 1e3 / steps
     out = {"workload": f"MUL_MAT_ID Q4_K 512 experts x (512 x 2048), top-10, T={T} (config 3 gate/up)",
-           "path": be.last_path(), "us_per_op": round(us, 3), "expert_bytes_touched": int(bytes_step),
+           "path": path, "us_per_op": round(us, 3), "expert_bytes_touched": int(bytes_step),
            "GBs": round(bytes_step / (us * 1e-6) / 1e9, 1), "kernel_us": round(k_us, 3),
-           "kernel_GBs": round(bytes_step / (k_us * 1e-6) / 1e9, 1)}
+           "kernel_GBs": round(bytes_step / (k_us * 1e-6) / 1e9, 1),
+           "router_us": round(times["router"], 3), "combine_us": round(times["combine"], 3)}
+    for t in (lg, rid, rw, ex, yo):
+        be.free_buffer(t.buf)
     for t in idsets:
         be.free_buffer(t.buf)
     for t in (w, xt, yt):

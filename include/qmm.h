@@ -170,6 +170,28 @@ int    qmm_quantize_act(qmm_ctx * ctx, int32_t act_type, const qmm_tensor * src,
 
 int    qmm_synchronize(qmm_ctx * ctx);
 
+/* ---- MoE router and combine -------------------------------------------- */
+/* The router of a softmax-gated MoE layer in one kernel, replacing
+ * llama.cpp's SOFT_MAX, ARGSORT (desc), VIEW, GET_ROWS, SUM_ROWS, CLAMP, DIV,
+ * RESHAPE chain (the reference's fused kernel_topk_moe_softmax_norm,
+ * P09:899-1000, matched at P02:786-821): for every token t (column of
+ * logits [n_expert, T], f32), the softmax over its logits, the k largest
+ * probabilities in descending order (ties: the lower expert) into
+ * ids [k, T] (i32, the ids MUL_MAT_ID takes) and those probabilities divided
+ * by their sum clamped to [cmin, cmax] into weights [k, T] (f32).
+ * n_expert <= 1024, 1 <= k <= min(32, n_expert). */
+int    qmm_moe_topk(qmm_ctx * ctx, const qmm_tensor * logits, const qmm_tensor * ids, const qmm_tensor * weights,
+                    float cmin, float cmax);
+/* The experts' outputs combined (llama.cpp's build_moe_ffn: MUL by the
+ * weights, then the ADDs over the k slots, then the shared expert times the
+ * sigmoid of its gate): dst[:, t] = sum_j weights[j, t] experts[:, j, t]
+ * (+ shared[:, t] * sigmoid(gate[0, t])), each product rounded and the sums
+ * taken slot by slot in order.  experts [M, k, T] (the MUL_MAT_ID dst),
+ * weights [k, T], shared and dst [M, T], gate [1, T]; shared and gate both
+ * or neither (NULL). */
+int    qmm_moe_combine(qmm_ctx * ctx, const qmm_tensor * experts, const qmm_tensor * weights,
+                       const qmm_tensor * shared, const qmm_tensor * gate, const qmm_tensor * dst);
+
 /* ---- observability and timing ----------------------------------------- */
 /* Number of ops that took a slower path than their type promises (the
  * reference's DOWNGRADE keys); names of the last few in `buf`. */

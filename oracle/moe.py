@@ -1,0 +1,52 @@
+"""TEST INFRASTRUCTURE ONLY: CPU restatement of the MoE router and combine.
+
+The router is llama.cpp's softmax gating as the reference fuses it
+(kernel_topk_moe_softmax_norm, contrib/llama.cpp/patches/0000-09-moe-routing-gemm-tiles.patch
+lines 899-1000; the ggml op chain it replaces is matched at
+0000-02-lowbit-iq-types.patch lines 786-821): per token the softmax of its
+expert logits, the k largest probabilities in descending order with ties to the
+lower expert, and their probabilities divided by their sum clamped to
+[cmin, cmax].  Computed here in float64 (the GPU's float32 softmax agrees to
+~1e-7 relative).  The combine is build_moe_ffn's MUL by the weights, the ADDs
+over the k slots in slot order, then the shared expert times the sigmoid of its
+gate, each in float32 with no fused multiply-add (numpy rounds every
+operation).  Pinned by tests/test_oracle_moe.py against closed forms and brute
+force.  Only tests/ may import this module.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+
+def softmax(logits: np.ndarray) -> np.ndarray:
+    """row-wise softmax in float64 of logits [T, n_expert]"""
+    x = np.asarray(logits, np.float64)
+    e = np.exp(x - x.max(axis=1, keepdims=True))
+    return e / e.sum(axis=1, keepdims=True)
+
+
+def topk(logits: np.ndarray, k: int, cmin: float, cmax: float):
+    """ids [T, k] (int32) and weights [T, k] (float64) of the router."""
+    p = softmax(logits)
+    T, n = p.shape
+    # descending probability, ties to the lower expert: sort on (-p, expert)
+    order = np.lexsort((np.broadcast_to(np.arange(n), p.shape), -p), axis=1)
+    ids = order[:, :k].astype(np.int32)
+    w = np.take_along_axis(p, ids.astype(np.int64), axis=1)
+    s = np.clip(w.sum(axis=1, keepdims=True), cmin, cmax)
+    return ids, w / s
+
+
+def combine(experts: np.ndarray, weights: np.ndarray, shared: np.ndarray | None = None,
+            gate: np.ndarray | None = None) -> np.ndarray:
+    """experts [T, k, M], weights [T, k], shared [T, M], gate [T] -> [T, M] (float32)."""
+    e = np.asarray(experts, np.float32)
+    w = np.asarray(weights, np.float32)
+    y = e[:, 0, :] * w[:, 0:1]
+    for j in range(1, e.shape[1]):
+        y = y + e[:, j, :] * w[:, j:j + 1]
+    if shared is not None:
+        g = np.asarray(gate, np.float32)
+        sg = (np.float32(1.0) / (np.float32(1.0) + np.exp(-g.astype(np.float64)).astype(np.float32)))
+        y = y + np.asarray(shared, np.float32) * sg[:, None]
+    return y.astype(np.float32)

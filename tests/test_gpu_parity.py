@@ -367,3 +367,105 @@ def test_full_size_gemm(be, sc, orc, qtype, M, K, N):
     got, ref = run_mul_mat(be, sc, orc, qtype, M, K, N, seed=93)
     assert be.last_path() == "gemm-mfma"
     assert rel_err(got, ref) <= TOL
+
+
+# ------------------------------------------------------------------ MoE router and combine
+@pytest.mark.parametrize("n_expert,k", [(8, 2), (64, 8), (100, 10), (512, 10), (1024, 32), (32, 32)])
+@pytest.mark.parametrize("T", [1, 5, 37])
+def test_moe_topk(be, sc, orc, n_expert, k, T):
+    from oracle import moe
+    say("moe_topk", n_expert, k, T)
+    g = np.random.default_rng(n_expert * 7 + k * 3 + T)
+    logits = (g.standard_normal((T, n_expert)) * 3).astype(np.float32)
+    logits[0, : n_expert // 2] = logits[0, 0]                # one token with a run of equal logits
+    lt = sc.f32(logits)
+    ids = sc.i32(np.zeros((T, k), np.int32))
+    w = sc.empty_f32((k, T))
+    be.moe_topk(lt, ids, w)
+    be.synchronize()
+    got_ids = be.get_tensor(ids).view(np.int32).reshape(T, k)
+    got_w = be.get_f32(w).reshape(T, k)
+    ref_ids, ref_w = moe.topk(logits, k, 6.103515625e-5, np.inf)
+    assert np.array_equal(got_ids, ref_ids)
+    np.testing.assert_allclose(got_w, ref_w, rtol=2e-6, atol=1e-30)
+
+
+def test_moe_topk_clamp_and_views(be, sc, orc):
+    from oracle import moe
+    say("moe_topk_clamp")
+    T, n_expert, k = 6, 96, 4
+    g = np.random.default_rng(77)
+    logits = (g.standard_normal((T, n_expert)) * 5).astype(np.float32)
+    # logits as a view with padded rows, ids / weights into wider rows
+    pad = np.zeros((T, n_expert + 7), np.float32)
+    pad[:, :n_expert] = logits
+    lp = sc.f32(pad)
+    lv = qmm.Tensor(lp.buf, qmm.F32, (n_expert, T), nb=(4, 4 * (n_expert + 7), 4 * (n_expert + 7) * T,
+                                                           4 * (n_expert + 7) * T))
+    ib = sc.i32(np.zeros((T, k + 3), np.int32))
+    iv = qmm.Tensor(ib.buf, qmm.I32, (k, T), nb=(4, 4 * (k + 3), 4 * (k + 3) * T, 4 * (k + 3) * T))
+    wb = sc.empty_f32((k + 3, T))
+    wv = qmm.Tensor(wb.buf, qmm.F32, (k, T), nb=(4, 4 * (k + 3), 4 * (k + 3) * T, 4 * (k + 3) * T))
+    be.moe_topk(lv, iv, wv, 0.0, 0.5)
+    be.synchronize()
+    got_ids = be.get_tensor(ib).view(np.int32).reshape(T, k + 3)[:, :k]
+    got_w = be.get_f32(wb).reshape(T, k + 3)[:, :k]
+    ref_ids, ref_w = moe.topk(logits, k, 0.0, 0.5)
+    assert np.array_equal(got_ids, ref_ids)
+    np.testing.assert_allclose(got_w, ref_w, rtol=2e-6)
+    with pytest.raises(qmm.QmmError):                          # k above 32
+        be.moe_topk(sc.f32(logits), sc.i32(np.zeros((T, 33), np.int32)), sc.empty_f32((33, T)))
+
+
+@pytest.mark.parametrize("shared", [False, True])
+def test_moe_combine(be, sc, orc, shared):
+    from oracle import moe
+    say("moe_combine", shared)
+    T, k, M = 7, 10, 333
+    g = np.random.default_rng(11 + shared)
+    e = g.standard_normal((T, k, M)).astype(np.float32)
+    w = g.random((T, k)).astype(np.float32)
+    s = g.standard_normal((T, M)).astype(np.float32) if shared else None
+    gt = g.standard_normal(T).astype(np.float32) * 2 if shared else None
+    y = sc.empty_f32((M, T))
+    be.moe_combine(sc.f32(e), sc.f32(w), y, sc.f32(s) if shared else None,
+                   sc.f32(gt.reshape(T, 1)) if shared else None)
+    be.synchronize()
+    got = be.get_f32(y).reshape(T, M)
+    ref = moe.combine(e, w, s, gt)
+    if shared:                                                 # the sigmoid's expf may differ by an ulp
+        np.testing.assert_allclose(got, ref, rtol=1e-6, atol=1e-6)
+    else:                                                      # same products and order: bit-exact
+        assert np.array_equal(got, ref)
+
+
+def test_moe_layer_end_to_end(be, sc, orc):
+    """router -> MUL_MAT_ID (gate/up style, one activation column per token) -> combine,
+    against the oracle's router, per-expert products and combine"""
+    from oracle import moe
+    say("moe_layer")
+    E, k, T, K, M = 16, 4, 5, 512, 96
+    g = np.random.default_rng(123)
+    logits = (g.standard_normal((T, E)) * 2).astype(np.float32)
+    raw = synth.weights(qmm.Q4_K, E * M, K, seed=124)
+    x = synth.activations(T, K, seed=125)
+    w = sc.weights(qmm.Q4_K, raw, (K, M, E))
+    ids = sc.i32(np.zeros((T, k), np.int32))
+    wts = sc.empty_f32((k, T))
+    be.moe_topk(sc.f32(logits), ids, wts)
+    xt = sc.f32(x.reshape(T, 1, K))
+    ex = sc.empty_f32((M, k, T))
+    be.mul_mat_id(w, xt, ids, ex)
+    y = sc.empty_f32((M, T))
+    be.moe_combine(ex, wts, y)
+    be.synchronize()
+    got = be.get_f32(y).reshape(T, M)
+    ref_ids, ref_w = moe.topk(logits, k, 6.103515625e-5, np.inf)
+    rb = synth.row_bytes(qmm.Q4_K, K) * M
+    ref_e = np.zeros((T, k, M), np.float32)
+    for t in range(T):
+        for j in range(k):
+            e = int(ref_ids[t, j])
+            ref_e[t, j] = orc.mul_mat(qmm.Q4_K, raw[e * rb:(e + 1) * rb], M, K, x[t:t + 1])[0]
+    ref = moe.combine(ref_e, ref_w.astype(np.float32))
+    assert rel_err(got, ref) <= TOL
