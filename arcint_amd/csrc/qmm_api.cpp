@@ -102,19 +102,79 @@ bool contiguous(const qmm_tensor * t) {
     return true;
 }
 
-WView weight_view(const qmm_tensor * t) {
-    const TypeLayout & L = *type_layout(t->type);
-    ImageShape sh;
-    image_shape(L, t->ne, &sh);
-    WView w{};
-    w.base = (const uint8_t *)t->buffer->ptr + t->offs;
-    w.M = sh.M;
-    w.K = sh.K;
-    w.bpr = sh.bpr;
-    w.G = sh.G;
-    w.ntiles = sh.ntiles;
-    w.tg = L.tg;
-    return w;
+static bool why(char * reason, size_t len, const char * msg) {
+    if (reason && len) snprintf(reason, len, "%s", msg);
+    return false;
+}
+
+// the tensor that owns a quantized tensor's device image (ggml keeps view_src a non-view)
+static const qmm_tensor * base_of(const qmm_tensor * t) { return t->view_src ? t->view_src : t; }
+
+// ggml_nbytes: the bytes from a tensor's first to past its last element, strides as given
+static size_t view_nbytes(const qmm_tensor * t) {
+    size_t bb = 0;
+    const int bl = qmm_type_block(t->type, &bb);
+    if (!bl || t->ne[0] % bl) return 0;
+    size_t n = (size_t)(t->ne[0] / bl) * t->nb[0];
+    for (int i = 1; i < 4; ++i) {
+        if (t->ne[i] <= 0) return 0;
+        n += (size_t)(t->ne[i] - 1) * t->nb[i];
+    }
+    return n;
+}
+
+// the last byte a tensor view touches lies inside its buffer
+static bool span_ok(const qmm_tensor * t) {
+    size_t last = 0;
+    for (int i = 0; i < 4; ++i) {
+        if (t->ne[i] <= 0) return false;
+        last += (size_t)(t->ne[i] - 1) * t->nb[i];
+    }
+    return t->offs + last + t->nb[0] <= t->buffer->size;
+}
+
+// The device image the kernels read for a quantized tensor: its own, or the part of its
+// base's image a view covers.  A view is taken when its matrices are whole matrices of the
+// base (the reference's whole-slice rule, 0116-opencl-q3_K.patch:76-85) or, when every base
+// matrix is whole 64-row tiles, whole tiles of it: then its rows sit in the base image at a
+// tile boundary exactly as its own shape would lay them out.  `mem` also checks that the
+// image lies in its buffer (off for shape-only queries).
+static bool weight_image(const qmm_tensor * t, bool mem, WView * w, char * reason, size_t len) {
+    const TypeLayout * L = type_layout(t->type);
+    if (!L) return why(reason, len, "src0 type is not Q4_0/Q8_0/Q4_K/Q6_K/IQ4_XS");
+    if (t->ne[0] % L->blck) return why(reason, len, "ne00 is not a multiple of the block size");
+    if (!contiguous(t)) return why(reason, len, "src0 is not contiguous");
+    const qmm_tensor * b = base_of(t);
+    if (b != t && (b->view_src || b->type != t->type || b->ne[0] != t->ne[0] || !contiguous(b)))
+        return why(reason, len, "src0 view: its base is not a contiguous tensor of its type and row length");
+    ImageShape bs, vs;
+    if (!image_shape(*L, b->ne, &bs) || !image_shape(*L, t->ne, &vs)) return why(reason, len, "src0 shape");
+    if (b->offs % kPlaneAlign) return why(reason, len, "src0 offset is not a multiple of 256");
+    if (mem) {
+        if (!b->buffer) return why(reason, len, "src0 has no buffer");
+        if (b->offs > b->buffer->size || bs.bytes > b->buffer->size - b->offs)
+            return why(reason, len, "src0 image runs past its buffer");
+    }
+    const size_t row = (size_t)bs.bpr * (size_t)L->bytes, tile = (size_t)bs.G * (size_t)L->tg;
+    const size_t voff = b == t ? 0 : t->view_offs;
+    if (voff % row) return why(reason, len, "src0 view does not start on a row of its base");
+    const int64_t R0 = (int64_t)(voff / row), rows = t->ne[1] * t->ne[2] * t->ne[3];
+    if (R0 + rows > bs.M * bs.nmat) return why(reason, len, "src0 view runs past its base");
+    size_t at;
+    if (t->ne[1] == bs.M && R0 % bs.M == 0)
+        at = (size_t)(R0 / bs.M) * (size_t)bs.ntiles * tile;                       // whole matrices
+    else if (bs.M % kTileRows == 0 && t->ne[1] % kTileRows == 0 && R0 % kTileRows == 0)
+        at = (size_t)(R0 / kTileRows) * tile;                                      // whole tiles
+    else
+        return why(reason, len, "src0 view is not whole matrices or whole 64-row tiles of its base");
+    w->base = mem ? (const uint8_t *)b->buffer->ptr + b->offs + at : nullptr;
+    w->M = vs.M;
+    w->K = vs.K;
+    w->bpr = vs.bpr;
+    w->G = vs.G;
+    w->ntiles = vs.ntiles;
+    w->tg = L->tg;
+    return true;
 }
 
 // activation scratch layout for ncols columns of ldk (K rounded up to 256):
@@ -219,6 +279,8 @@ bool ranges_overlap(const qmm_tensor * a, const qmm_tensor * b) {
     const size_t a0 = a->offs, a1 = a->offs + span(a), b0 = b->offs, b1 = b->offs + span(b);
     return a0 < b1 && b0 < a1;
 }
+
+bool f32_shape(const qmm_tensor * t) { return t && t->type == QMM_TYPE_F32 && t->nb[0] == sizeof(float) && t->ne[0] > 0; }
 
 bool check_f32(const qmm_tensor * t) {
     return t && t->buffer && t->type == QMM_TYPE_F32 && t->nb[0] == sizeof(float) && t->ne[0] > 0;
@@ -380,28 +442,70 @@ static int quant_io(qmm_ctx * ctx, const TypeLayout & L, const ImageShape & sh, 
     return QMM_OK;
 }
 
+// GGUF bytes [lo, lo + size) of a quantized base: the whole blocks straight through quant_io,
+// a block that either end of the range cuts read first and patched (read-modify-write), the
+// reference's any-range rule (0116-opencl-q3_K.patch:113-133)
+static int quant_range_io(qmm_ctx * ctx, const TypeLayout & L, const ImageShape & sh, uint8_t * dev, uint8_t * host,
+                          size_t lo, size_t size, bool write) {
+    const size_t bb = (size_t)L.bytes, hi = lo + size;
+    if (lo % bb == 0 && hi % bb == 0)
+        return quant_io(ctx, L, sh, dev, host, (int64_t)(lo / bb), (int64_t)(size / bb), write);
+    std::vector<uint8_t> blk(bb);
+    // the end blocks of the range (one when it lies inside a block); those it covers in part
+    const int64_t first = (int64_t)(lo / bb), last = (int64_t)((hi - 1) / bb);
+    for (int64_t c = first; c <= last; c += std::max<int64_t>(1, last - first)) {
+        const size_t b0 = (size_t)c * bb, a = std::max(lo, b0), e = std::min(hi, b0 + bb);
+        if (a == b0 && e == b0 + bb) continue;              // whole: goes with the middle
+        int rc = quant_io(ctx, L, sh, dev, blk.data(), c, 1, false);
+        if (rc) return rc;
+        if (write) {
+            memcpy(blk.data() + (a - b0), host + (a - lo), e - a);
+            if ((rc = quant_io(ctx, L, sh, dev, blk.data(), c, 1, true))) return rc;
+        } else {
+            memcpy(host + (a - lo), blk.data() + (a - b0), e - a);
+        }
+    }
+    const size_t w0 = (lo + bb - 1) / bb, w1 = hi / bb;    // blocks wholly inside the range
+    if (w0 < w1) return quant_io(ctx, L, sh, dev, host + (w0 * bb - lo), (int64_t)w0, (int64_t)(w1 - w0), write);
+    return QMM_OK;
+}
+
+// set_tensor / get_tensor (P02:1556-1790): bytes [offset, offset + size) of the tensor as
+// ggml addresses them, data + offset, within ggml_nbytes.  A quantized view moves its base's
+// bytes at view_offs + offset; the base's shape lays them out (0116-opencl-q3_K.patch:56-59).
 static int tensor_io(qmm_ctx * ctx, const qmm_tensor * t, void * host, size_t offset, size_t size, bool write) {
-    if (!ctx || !t || !t->buffer || (!host && size)) return fail(ctx, QMM_ERR_INVALID, "tensor io: null argument");
+    if (!ctx || !t || (!host && size)) return fail(ctx, QMM_ERR_INVALID, "tensor io: null argument");
     QMM_HIP(ctx, hipSetDevice(ctx->device));
-    if (!contiguous(t)) return fail(ctx, QMM_ERR_INVALID, "tensor io: tensor is not contiguous");
-    const size_t total = qmm_tensor_nbytes(t->type, t->ne);
-    if (offset > total || size > total - offset) return fail(ctx, QMM_ERR_INVALID, "tensor io: range past the tensor");
-    const size_t alloc = qmm_tensor_alloc_size(t->type, t->ne);
-    if (t->offs + alloc > t->buffer->size) return fail(ctx, QMM_ERR_INVALID, "tensor io: tensor past its buffer");
-    uint8_t * dev = (uint8_t *)t->buffer->ptr + t->offs;
-    if (write) ctx->key.valid = false;
+    const size_t span = view_nbytes(t);
+    if (!span) return fail(ctx, QMM_ERR_INVALID, "tensor io: type %d / shape has no GGUF size", t->type);
+    if (offset > span || size > span - offset) return fail(ctx, QMM_ERR_INVALID, "tensor io: range past the tensor");
     const TypeLayout * L = type_layout(t->type);
-    if (L && (offset % L->bytes || size % L->bytes))
-        return fail(ctx, QMM_ERR_INVALID, "tensor io: offset %zu / size %zu not whole %d-byte blocks", offset, size, L->bytes);
+    const qmm_tensor * b = L ? base_of(t) : t;
+    if (!b->buffer) return fail(ctx, QMM_ERR_INVALID, "tensor io: no buffer");
+    if (write) ctx->key.valid = false;
     if (!L) {   // the device bytes are the plain bytes
-        if (write) QMM_HIP(ctx, hipMemcpyAsync(dev + offset, host, size, hipMemcpyHostToDevice, ctx->stream));
-        else QMM_HIP(ctx, hipMemcpyAsync(host, dev + offset, size, hipMemcpyDeviceToHost, ctx->stream));
+        if (t->offs > b->buffer->size || offset + size > b->buffer->size - t->offs)
+            return fail(ctx, QMM_ERR_INVALID, "tensor io: range past its buffer");
+        uint8_t * dev = (uint8_t *)b->buffer->ptr + t->offs + offset;
+        if (!size) return QMM_OK;
+        if (write) QMM_HIP(ctx, hipMemcpyAsync(dev, host, size, hipMemcpyHostToDevice, ctx->stream));
+        else QMM_HIP(ctx, hipMemcpyAsync(host, dev, size, hipMemcpyDeviceToHost, ctx->stream));
         QMM_HIP(ctx, hipStreamSynchronize(ctx->stream));
         return QMM_OK;
     }
+    if (b != t && (b->view_src || b->type != t->type))
+        return fail(ctx, QMM_ERR_INVALID, "tensor io: view_src is a view or of another type");
+    if (!contiguous(b)) return fail(ctx, QMM_ERR_INVALID, "tensor io: the base tensor is not contiguous");
+    const size_t total = qmm_tensor_nbytes(b->type, b->ne);
+    const size_t lo = (b == t ? 0 : t->view_offs) + offset;
+    if (lo > total || size > total - lo) return fail(ctx, QMM_ERR_INVALID, "tensor io: range past the view's base");
+    const size_t alloc = qmm_tensor_alloc_size(b->type, b->ne);
+    if (b->offs > b->buffer->size || alloc > b->buffer->size - b->offs)
+        return fail(ctx, QMM_ERR_INVALID, "tensor io: tensor past its buffer");
+    if (!size) return QMM_OK;
     ImageShape sh;
-    image_shape(*L, t->ne, &sh);
-    return quant_io(ctx, *L, sh, dev, (uint8_t *)host, (int64_t)(offset / L->bytes), (int64_t)(size / L->bytes), write);
+    image_shape(*L, b->ne, &sh);
+    return quant_range_io(ctx, *L, sh, (uint8_t *)b->buffer->ptr + b->offs, (uint8_t *)host, lo, size, write);
 }
 
 int qmm_tensor_pack(int32_t type, const int64_t ne[4], const void * gguf, void * image, size_t image_size) {
@@ -441,19 +545,14 @@ int qmm_buffer_copy(qmm_ctx * ctx, qmm_buffer * dst, size_t dst_off, const qmm_b
 
 // ---- validation ------------------------------------------------------------
 
-static bool why(char * reason, size_t len, const char * msg) {
-    if (reason && len) snprintf(reason, len, "%s", msg);
-    return false;
-}
-
-static bool mul_mat_ok(const qmm_tensor * s0, const qmm_tensor * s1, const qmm_tensor * d, char * reason, size_t len) {
-    if (!s0 || !s1 || !d || !s0->buffer || !s1->buffer || !d->buffer) return why(reason, len, "null tensor or buffer");
-    const TypeLayout * L = type_layout(s0->type);
-    if (!L) return why(reason, len, "src0 type is not Q4_0/Q8_0/Q4_K/Q6_K/IQ4_XS");
-    if (s0->ne[0] % L->blck) return why(reason, len, "ne00 is not a multiple of the block size");
-    if (!contiguous(s0)) return why(reason, len, "src0 is not contiguous");
-    if (s0->offs % kPlaneAlign) return why(reason, len, "src0 offset is not a multiple of 256");
-    if (!check_f32(s1) || !check_f32(d)) return why(reason, len, "src1/dst must be f32 with nb[0] == 4");
+// `mem`: also check that every operand lies inside its buffer (off for shape-only queries)
+static bool mul_mat_ok(const qmm_tensor * s0, const qmm_tensor * s1, const qmm_tensor * d, bool mem, WView * w,
+                       char * reason, size_t len) {
+    if (!s0 || !s1 || !d) return why(reason, len, "null tensor");
+    if (!weight_image(s0, mem, w, reason, len)) return false;
+    if (!f32_shape(s1) || !f32_shape(d)) return why(reason, len, "src1/dst must be f32 with nb[0] == 4");
+    if (mem && (!s1->buffer || !d->buffer)) return why(reason, len, "src1/dst has no buffer");
+    if (mem && (!span_ok(s1) || !span_ok(d))) return why(reason, len, "src1/dst runs past its buffer");
     if (s1->ne[0] != s0->ne[0]) return why(reason, len, "src1 ne0 != src0 ne0");
     if (s1->ne[0] % 256 && vec_dot_type(s0->type) == QMM_TYPE_Q8_K) return why(reason, len, "K is not a multiple of 256");
     if (s0->ne[2] <= 0 || s0->ne[3] <= 0 || s1->ne[2] % s0->ne[2] || s1->ne[3] % s0->ne[3])
@@ -466,16 +565,14 @@ static bool mul_mat_ok(const qmm_tensor * s0, const qmm_tensor * s1, const qmm_t
 }
 
 static bool mul_mat_id_ok(const qmm_tensor * s0, const qmm_tensor * s1, const qmm_tensor * ids, const qmm_tensor * d,
-                          char * reason, size_t len) {
-    if (!s0 || !s1 || !ids || !d || !s0->buffer || !s1->buffer || !ids->buffer || !d->buffer)
-        return why(reason, len, "null tensor or buffer");
-    const TypeLayout * L = type_layout(s0->type);
-    if (!L) return why(reason, len, "src0 type is not Q4_0/Q8_0/Q4_K/Q6_K/IQ4_XS");
-    if (s0->ne[0] % L->blck || !contiguous(s0)) return why(reason, len, "src0 must be contiguous whole blocks");
-    if (s0->offs % kPlaneAlign) return why(reason, len, "src0 offset is not a multiple of 256");
+                          bool mem, WView * w, char * reason, size_t len) {
+    if (!s0 || !s1 || !ids || !d) return why(reason, len, "null tensor");
+    if (!weight_image(s0, mem, w, reason, len)) return false;
     if (s0->ne[3] != 1) return why(reason, len, "src0 must be [K, M, n_as]");
-    if (!check_f32(s1) || !check_f32(d)) return why(reason, len, "src1/dst must be f32 with nb[0] == 4");
+    if (!f32_shape(s1) || !f32_shape(d)) return why(reason, len, "src1/dst must be f32 with nb[0] == 4");
     if (ids->type != QMM_TYPE_I32 || ids->nb[0] != 4) return why(reason, len, "ids must be i32");
+    if (mem && (!s1->buffer || !d->buffer || !ids->buffer)) return why(reason, len, "src1/ids/dst has no buffer");
+    if (mem && (!span_ok(s1) || !span_ok(d) || !span_ok(ids))) return why(reason, len, "src1/ids/dst runs past its buffer");
     if (s1->ne[0] != s0->ne[0]) return why(reason, len, "src1 ne0 != src0 ne0");
     if (s1->ne[0] % 256 && vec_dot_type(s0->type) == QMM_TYPE_Q8_K) return why(reason, len, "K is not a multiple of 256");
     const int64_t n_used = ids->ne[0], T = ids->ne[1];
@@ -488,10 +585,12 @@ static bool mul_mat_id_ok(const qmm_tensor * s0, const qmm_tensor * s1, const qm
     return true;
 }
 
+// shapes, types and views only: ggml's scheduler asks before the activations have memory
 int qmm_supports_op(qmm_ctx *, int32_t op, const qmm_tensor * src0, const qmm_tensor * src1, const qmm_tensor * ids,
                     const qmm_tensor * dst, char * reason, size_t reason_len) {
-    if (op == QMM_OP_MUL_MAT) return mul_mat_ok(src0, src1, dst, reason, reason_len) ? 1 : 0;
-    if (op == QMM_OP_MUL_MAT_ID) return mul_mat_id_ok(src0, src1, ids, dst, reason, reason_len) ? 1 : 0;
+    WView w;
+    if (op == QMM_OP_MUL_MAT) return mul_mat_ok(src0, src1, dst, false, &w, reason, reason_len) ? 1 : 0;
+    if (op == QMM_OP_MUL_MAT_ID) return mul_mat_id_ok(src0, src1, ids, dst, false, &w, reason, reason_len) ? 1 : 0;
     why(reason, reason_len, "op is not MUL_MAT or MUL_MAT_ID");
     return 0;
 }
@@ -518,19 +617,14 @@ int qmm_describe_mul_mat(const qmm_tensor * src0, const qmm_tensor * src1, const
     if (!out) return QMM_ERR_INVALID;
     memset(out, 0, sizeof(*out));
     if (!src0 || !src1 || !dst) return QMM_ERR_INVALID;
-    qmm_tensor a = *src0, b = *src1, c = *dst;   // shapes only: any non-null buffer passes validation
-    qmm_buffer fake;
-    a.buffer = b.buffer = c.buffer = &fake;
     char reason[160];
-    if (!mul_mat_ok(&a, &b, &c, reason, sizeof(reason))) return QMM_ERR_UNSUPPORTED;
+    WView w;   // shapes only: buffers are not looked at
+    if (!mul_mat_ok(src0, src1, dst, false, &w, reason, sizeof(reason))) return QMM_ERR_UNSUPPORTED;
     const int64_t N = src1->ne[1];
     if (N >= gemm_min_cols()) {
         snprintf(out->path, sizeof(out->path), "gemm-mfma");
         out->tasks = src1->ne[2] * src1->ne[3];
         out->cols_per_task = (int32_t)std::min<int64_t>(N, INT32_MAX);
-        fake.ptr = nullptr;
-        fake.size = 0;
-        const WView w = weight_view(&a);
         int threads, lds;
         gemm_shape(src0->type, w, N, out->tasks, &out->workgroups, &threads, &lds);
         out->threads = threads;
@@ -538,9 +632,6 @@ int qmm_describe_mul_mat(const qmm_tensor * src0, const qmm_tensor * src1, const
         out->k_slices = gemm_kslices(w, N, out->tasks);
         return QMM_OK;
     }
-    fake.ptr = nullptr;
-    fake.size = 0;
-    const WView w = weight_view(&a);
     const int nc = (int)std::min<int64_t>(N, kMaxTaskCols);
     const int64_t ntasks = (N + nc - 1) / nc * src1->ne[2] * src1->ne[3];
     GemvPlan plan;
@@ -561,13 +652,14 @@ int qmm_describe_mul_mat(const qmm_tensor * src0, const qmm_tensor * src1, const
 int qmm_mul_mat(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1, const qmm_tensor * dst) {
     if (!ctx) return QMM_ERR_INVALID;
     char reason[160];
-    if (!mul_mat_ok(src0, src1, dst, reason, sizeof(reason))) return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat: %s", reason);
+    WView w;
+    if (!mul_mat_ok(src0, src1, dst, true, &w, reason, sizeof(reason)))
+        return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat: %s", reason);
     QMM_HIP(ctx, hipSetDevice(ctx->device));
     const int64_t N = src1->ne[1];
     const bool use_gemm = N >= gemm_min_cols();
     ActBuf a{};
     int rc;
-    const WView w = weight_view(src0);
     float * d = (float *)((uint8_t *)dst->buffer->ptr + dst->offs);
     GemvDense dn;
     dn.ne11 = N;
@@ -622,7 +714,8 @@ int qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * sr
                    const qmm_tensor * dst) {
     if (!ctx) return QMM_ERR_INVALID;
     char reason[160];
-    if (!mul_mat_id_ok(src0, src1, ids, dst, reason, sizeof(reason)))
+    WView w;
+    if (!mul_mat_id_ok(src0, src1, ids, dst, true, &w, reason, sizeof(reason)))
         return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat_id: %s", reason);
     QMM_HIP(ctx, hipSetDevice(ctx->device));
     const int64_t M = src0->ne[1], n_as = src0->ne[2];
@@ -632,7 +725,6 @@ int qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * sr
     if ((rc = quantize_src1(ctx, src0->type, src1, false, &a))) return rc;
     const int64_t npairs = n_used * T;
     const int64_t max_tasks = npairs / kMaxTaskCols + std::min(n_as, npairs) + 1;
-    const WView w = weight_view(src0);
     const int nc = (int)std::min<int64_t>(kMaxTaskCols, npairs);
     GemvPlan plan;
     // tasks carry 1..8 pairs each: the MFMA kernel pays off when experts average two or more
@@ -663,16 +755,6 @@ int qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * sr
     if ((rc = ktime_pair(ctx, &kt, &ktp))) return rc;
     QMM_HIP(ctx, launch_gemv(src0->type, w, plan, a, tasks, ntasks, nullptr, d, ctx->sink, ctx->stream, ktp));
     return QMM_OK;
-}
-
-// the last byte a tensor view touches lies inside its buffer
-static bool span_ok(const qmm_tensor * t) {
-    size_t last = 0;
-    for (int i = 0; i < 4; ++i) {
-        if (t->ne[i] <= 0) return false;
-        last += (size_t)(t->ne[i] - 1) * t->nb[i];
-    }
-    return t->offs + last + t->nb[0] <= t->buffer->size;
 }
 
 int qmm_moe_topk(qmm_ctx * ctx, const qmm_tensor * logits, const qmm_tensor * ids, const qmm_tensor * weights,
@@ -773,13 +855,13 @@ int qmm_graph_compute(qmm_ctx * ctx, const qmm_node * nodes, int n_nodes) {
 }
 
 int qmm_dequantize(qmm_ctx * ctx, const qmm_tensor * src, const qmm_tensor * dst) {
-    if (!ctx || !src || !dst || !src->buffer || !dst->buffer) return fail(ctx, QMM_ERR_INVALID, "dequantize: null argument");
-    const TypeLayout * L = type_layout(src->type);
-    if (!L || src->ne[0] % L->blck || !contiguous(src)) return fail(ctx, QMM_ERR_UNSUPPORTED, "dequantize: unsupported source");
-    if (dst->type != QMM_TYPE_F32 || !contiguous(dst) || nelements(dst->ne) != nelements(src->ne))
-        return fail(ctx, QMM_ERR_INVALID, "dequantize: dst must be contiguous f32 with as many elements");
+    if (!ctx || !src || !dst || !dst->buffer) return fail(ctx, QMM_ERR_INVALID, "dequantize: null argument");
+    char reason[160];
+    WView w;
+    if (!weight_image(src, true, &w, reason, sizeof(reason))) return fail(ctx, QMM_ERR_UNSUPPORTED, "dequantize: %s", reason);
+    if (dst->type != QMM_TYPE_F32 || !contiguous(dst) || nelements(dst->ne) != nelements(src->ne) || !span_ok(dst))
+        return fail(ctx, QMM_ERR_INVALID, "dequantize: dst must be contiguous f32 with as many elements, in its buffer");
     QMM_HIP(ctx, hipSetDevice(ctx->device));
-    const WView w = weight_view(src);
     float * y = (float *)((uint8_t *)dst->buffer->ptr + dst->offs);
     QMM_HIP(ctx, launch_dequant(src->type, w, src->ne[2] * src->ne[3], y, ctx->stream));
     return QMM_OK;

@@ -43,8 +43,12 @@ class QmmError(RuntimeError):
 
 
 class CTensor(C.Structure):
-    _fields_ = [("type", C.c_int32), ("ne", C.c_int64 * 4), ("nb", C.c_size_t * 4),
-                ("buffer", C.c_void_p), ("offs", C.c_size_t)]
+    pass
+
+
+CTensor._fields_ = [("type", C.c_int32), ("ne", C.c_int64 * 4), ("nb", C.c_size_t * 4),
+                    ("buffer", C.c_void_p), ("offs", C.c_size_t), ("view_src", C.POINTER(CTensor)),
+                    ("view_offs", C.c_size_t)]
 
 
 class LaunchInfo(C.Structure):
@@ -174,9 +178,12 @@ class Buffer:
 
 
 class Tensor:
-    """A view {type, ne, nb, buffer, offs}; nb defaults to the contiguous strides."""
+    """A view {type, ne, nb, buffer, offs, view_src, view_offs}; nb defaults to the contiguous
+    strides.  Views of a tensor come from Tensor.view, as ggml_view_* / ggml_permute /
+    ggml_reshape make them."""
 
-    def __init__(self, buf: Buffer, qtype: int, ne, offs: int = 0, nb=None):
+    def __init__(self, buf: Buffer, qtype: int, ne, offs: int = 0, nb=None, view_src: "Tensor | None" = None,
+                 view_offs: int = 0):
         self.buf = buf
         self.type = qtype
         self.ne = _ne4(ne)
@@ -187,11 +194,23 @@ class Tensor:
             nb.append(nb[2] * self.ne[2])
         self.nb = tuple(int(v) for v in nb)
         self.offs = int(offs)
-        self.c = CTensor(qtype, (C.c_int64 * 4)(*self.ne), (C.c_size_t * 4)(*self.nb), buf.ptr, self.offs)
+        self.view_src = view_src          # kept alive: the C struct points at its struct
+        self.view_offs = int(view_offs)
+        self.c = CTensor(qtype, (C.c_int64 * 4)(*self.ne), (C.c_size_t * 4)(*self.nb), buf.ptr, self.offs,
+                         C.pointer(view_src.c) if view_src is not None else None, self.view_offs)
+
+    def view(self, ne, nb=None, offset: int = 0) -> "Tensor":
+        """ggml_view_4d: ne / nb (default contiguous) at byte `offset` of this tensor's layout;
+        its base is this tensor's base."""
+        base = self.view_src or self
+        voff = self.view_offs + int(offset)
+        return Tensor(self.buf, self.type, ne, self.offs + int(offset), nb, base, voff)
 
     @property
     def nbytes(self) -> int:
-        return nbytes(self.type, self.ne)
+        """ggml_nbytes: first to past the last element, with the tensor's strides"""
+        bl, _ = type_block(self.type)
+        return self.ne[0] // bl * self.nb[0] + sum((n - 1) * s for n, s in zip(self.ne[1:], self.nb[1:]))
 
 
 class Backend:

@@ -47,6 +47,12 @@
  * of the block size; nb[] are the strides of the GGUF byte layout.  The
  * device keeps quantized tensors in its own planar layout, so data of a
  * quantized tensor must be written and read through qmm_tensor_set/get.
+ * The ops take a quantized view as src0 when the base image holds its rows
+ * as whole matrices of the base (a slice of an expert stack; the reference's
+ * whole-slice rule, 0116-opencl-q3_K.patch:76-85) or, when the base's
+ * matrices are whole 64-row tiles, as whole tiles (a reshape [K, M*E] of
+ * [K, M, E], rows 64i.. of a matrix); qmm_supports_op says no, with the
+ * reason, for any other view.
  *   MUL_MAT:    src0 [K, M, ne02, ne03] quantized, src1 [K, N, ne12, ne13]
  *               f32, dst [M, N, ne12, ne13] f32; dst[m,n] = sum_k src0[k,m] *
  *               src1[k,n], src0 broadcast over dims 2 and 3 (ne12 % ne02 == 0).
@@ -98,13 +104,23 @@ enum qmm_status {
 typedef struct qmm_ctx    qmm_ctx;
 typedef struct qmm_buffer qmm_buffer;
 
-/* A non-owning view, like ggml_tensor: data lives at buffer + offs. */
+/* A non-owning view, like ggml_tensor: data lives at buffer + offs.
+ * view_src / view_offs are ggml_tensor's own fields: the tensor whose
+ * allocation this one views (never itself a view; NULL for a tensor that is
+ * its own allocation) and the byte offset of this view's first byte in
+ * view_src's GGUF layout.  A plain-typed (f32/f16/i32) tensor is addressed by
+ * its buffer + offs whatever view_src says.  A quantized view reads and
+ * writes its base's device image: its own buffer and offs are not used, and
+ * byte b of the view is byte view_offs + b of the base (the reference's rule,
+ * 0116-opencl-q3_K.patch:56-59 ggml_cl_lb_base and :113-133). */
 typedef struct qmm_tensor {
     int32_t      type;   /* enum qmm_type */
     int64_t      ne[4];
     size_t       nb[4];  /* byte strides of the logical (GGUF) layout */
     qmm_buffer * buffer;
     size_t       offs;
+    const struct qmm_tensor * view_src;
+    size_t       view_offs;
 } qmm_tensor;
 
 /* One node of an op graph (ggml_tensor's op + src[0..2]). */
@@ -135,9 +151,14 @@ size_t qmm_tensor_nbytes(int32_t type, const int64_t ne[4]);
 /* block size (weights per block) and block bytes of a type; 0 if unknown */
 int    qmm_type_block(int32_t type, size_t * block_bytes);
 
-/* Write / read `size` bytes at byte `offset` of the tensor's GGUF layout.
- * For quantized types offset and size must be multiples of the block bytes.
- * Both are synchronous with respect to the host buffer. */
+/* Write / read `size` bytes at byte `offset` of the tensor's GGUF layout
+ * (ggml_backend_tensor_set/get: the range lies inside ggml_nbytes of the
+ * tensor, strides notwithstanding).  Any byte range: a block that the range
+ * covers in part is read, patched and written back.  A quantized view goes
+ * through its base (view_src) at view_offs + offset, so every view of a
+ * weight - permuted, reshaped, a slice or rows of it - moves the bytes the
+ * base's layout puts there.  Both are synchronous with respect to the host
+ * buffer. */
 int    qmm_tensor_set(qmm_ctx * ctx, const qmm_tensor * t, const void * data, size_t offset, size_t size);
 int    qmm_tensor_get(qmm_ctx * ctx, const qmm_tensor * t, void * data, size_t offset, size_t size);
 /* Host only, no device: the device image (qmm_tensor_alloc_size bytes) of a

@@ -75,6 +75,56 @@ def test_supports_op_without_device():
     assert L.qmm_supports_op(None, qmm.OP_MUL_MAT_ID, C.byref(we.c), C.byref(xe3.c), C.byref(ids.c), C.byref(ye.c), buf, 128) == 0
 
 
+def test_supports_op_views_of_quantized_weights():
+    """a quantized view is taken where the base image holds its rows as whole matrices or whole
+    64-row tiles (the reference's whole-slice rule, 0116-opencl-q3_K.patch:76-85, widened to
+    tiles); anything else is refused with the reason"""
+    L = qmm.load()
+    fake = qmm.Buffer(ptr=0x1000, size=1 << 40)
+    buf = C.create_string_buffer(160)
+    K = 512
+    _, bb = qmm.type_block(qmm.Q4_K)
+    row = K // 256 * bb
+
+    def ok(w, n=3):
+        x, y = qmm.Tensor(fake, qmm.F32, (K, n, w.ne[2])), qmm.Tensor(fake, qmm.F32, (w.ne[1], n, w.ne[2]))
+        return L.qmm_supports_op(None, qmm.OP_MUL_MAT, C.byref(w.c), C.byref(x.c), None, C.byref(y.c), buf, 160) == 1
+
+    a = qmm.Tensor(fake, qmm.Q4_K, (K, 64, 3))
+    assert ok(a)
+    assert ok(a.view((K, 64), offset=2 * a.nb[2]))                 # slice 2
+    assert ok(a.view((K, 64, 2), offset=1 * a.nb[2]))              # slices 1..2
+    assert ok(a.view((K, 192)))                                    # reshape: whole tiles
+    assert not ok(a.view((K, 64), offset=5 * row)) and b"whole matrices" in buf.value   # rows 5..68
+    assert not ok(a.view((K, 32)))                                 # half a slice
+    assert not ok(a.view((K, 64), offset=row + 7)) and b"start on a row" in buf.value
+    assert not ok(a.view((K, 64, 2), offset=2 * a.nb[2])) and b"past its base" in buf.value
+    b = qmm.Tensor(fake, qmm.Q4_K, (K, 100, 3))
+    assert ok(b.view((K, 100), offset=b.nb[2]))
+    assert not ok(b.view((K, 300)))                                # 100-row matrices are not whole tiles
+    c = qmm.Tensor(fake, qmm.Q4_K, (K, 256))
+    assert ok(c.view((K, 128), offset=64 * row))                   # rows 64..191: whole tiles
+    assert not ok(c.view((K, 100), offset=64 * row))
+    # test-backend-ops' permuted weight: [K, 1, M] seen as [K, M]
+    p = qmm.Tensor(fake, qmm.Q4_K, (K, 1, 64))
+    assert not ok(p.view((K, 64), nb=(bb, p.nb[2], p.nb[2], 64 * p.nb[2])))
+    # MUL_MAT_ID on a run of experts of a stack
+    e = qmm.Tensor(fake, qmm.Q4_K, (K, 64, 8))
+    ev = e.view((K, 64, 4), offset=2 * e.nb[2])
+    xe, ids, ye = (qmm.Tensor(fake, qmm.F32, (K, 1, 5)), qmm.Tensor(fake, qmm.I32, (2, 5)),
+                   qmm.Tensor(fake, qmm.F32, (64, 2, 5)))
+    assert L.qmm_supports_op(None, qmm.OP_MUL_MAT_ID, C.byref(ev.c), C.byref(xe.c), C.byref(ids.c), C.byref(ye.c),
+                             buf, 160) == 1
+
+
+def test_view_nbytes_is_ggml_nbytes():
+    fake = qmm.Buffer(ptr=0x1000, size=1 << 40)
+    a = qmm.Tensor(fake, qmm.Q4_K, (512, 1, 64))
+    pv = a.view((512, 64), nb=(144, a.nb[2], a.nb[2], 64 * a.nb[2]))
+    assert pv.nbytes == a.nbytes == 64 * 288
+    assert a.view((512, 5), offset=70 * 288).nbytes == 5 * 288
+
+
 def test_no_device_is_an_error_not_a_fallback():
     try:
         be = qmm.Backend(0)

@@ -104,8 +104,186 @@ def test_set_get_roundtrip(be, sc, qtype):
     raw2[bb * 11:bb * 18] = part
     assert np.array_equal(be.get_tensor(w), raw2)
     assert np.array_equal(be.get_tensor(w, offset=bb * 5, size=bb * 20), raw2[bb * 5:bb * 25])
+    with pytest.raises(qmm.QmmError):                  # past the tensor's bytes
+        be.set_tensor(w, part[:bb + 1], offset=raw.size - bb)
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+def test_gguf_load_chunked(be, sc, orc, tmp_path, qtype):
+    """a GGUF tensor streamed into the device image in chunks of a few whole blocks (chunk
+    boundaries inside rows and across 64-row tiles) reads back as the file's bytes and
+    multiplies like the oracle"""
+    import gguf_writer
+    from arcint_amd import gguf
+    say("gguf_load", qtype)
+    blck, bb = synth.BLOCK[qtype]
+    M, K, N = 131, 1024, 5
+    raw = synth.weights(qtype, M, K, seed=61)
+    p = tmp_path / "w.gguf"
+    gguf_writer.write(p, [("general.architecture", gguf_writer.STRING, "test")],
+                      [("pad", (7,), qmm.F32, np.zeros(28, np.uint8)), ("blk.0.w", (K, M), qtype, raw)])
+    g = gguf.read(str(p))
+    w = gguf.load_tensor(be, g, "blk.0.w", chunk_bytes=7 * bb + 5)
+    sc.bufs.append(w.buf)
+    assert np.array_equal(be.get_tensor(w), raw)
+    x = synth.activations(N, K, 62)
+    xt = sc.f32(x)
+    y = sc.empty_f32((M, N))
+    be.mul_mat(w, xt, y)
+    be.synchronize()
+    assert rel_err(be.get_f32(y).reshape(N, M), orc.mul_mat(qtype, raw, M, K, x)) <= TOL
+
+
+# ------------------------------------------------------------------ views and partial ranges
+# The cases of the reference's tests/test_planes.cpp:106-286 (set_tensor / get_tensor of views
+# go through the base; any byte range is exact), on the device image.
+VK = 512
+
+
+def dequant_matches(be, sc, orc, qtype, t, raw):
+    """the device image of t decodes to the oracle's dequantization of raw (NaN where both are)"""
+    n = int(np.prod(t.ne))
+    y = sc.empty_f32(t.ne)
+    be.dequantize(t, y)
+    be.synchronize()
+    return np.array_equal(be.get_f32(y), orc.dequantize(qtype, raw, n), equal_nan=True)
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+def test_permuted_view_writes_through_its_base(be, sc, orc, qtype):
+    say("view_permuted", qtype)
+    M = 40
+    raw = synth.weights(qtype, M, VK, seed=71)
+    a = sc.weights(qtype, np.zeros_like(raw), (VK, 1, M))             # [K, 1, M]: M one-row matrices
+    ap = a.view((VK, M), nb=(a.nb[0], a.nb[2], a.nb[2], M * a.nb[2]))   # permute(0, 2, 1, 3)
+    assert ap.nbytes == a.nbytes
+    be.set_tensor(ap, raw)
+    assert np.array_equal(be.get_tensor(a), raw)
+    assert np.array_equal(be.get_tensor(ap), raw)
+    assert dequant_matches(be, sc, orc, qtype, a, raw)                # the image is the base's
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+def test_partial_range_is_read_modify_write(be, sc, orc, qtype):
+    say("partial_range", qtype)
+    M = 6
+    raw = synth.weights(qtype, M, VK, seed=72)
+    a = sc.weights(qtype, raw, (VK, M))
+    n = raw.size
+    g = np.random.default_rng(73)
+    exp = raw.copy()
+    for at, ln in [(n // 2 + 7, 300), (5, 3), (0, 1), (n - 1, 1), (n - 301, 301), (1, n - 2)]:
+        patch = g.integers(0, 256, ln, dtype=np.uint8)
+        be.set_tensor(a, patch, offset=at)
+        exp[at:at + ln] = patch
+        assert np.array_equal(be.get_tensor(a), exp), (at, ln)
+    assert np.array_equal(be.get_tensor(a, offset=41, size=123), exp[41:164])
+    assert np.array_equal(be.get_tensor(a, offset=n - 5, size=5), exp[n - 5:])
+    assert be.get_tensor(a, offset=7, size=0).size == 0
+    assert dequant_matches(be, sc, orc, qtype, a, exp)
     with pytest.raises(qmm.QmmError):
-        be.set_tensor(w, part[:bb - 1], offset=0)
+        be.set_tensor(a, exp[:10], offset=n - 9)                       # past the tensor
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+def test_reshape_of_a_3d_base_converts_by_the_base_slices(be, sc, orc, qtype):
+    say("view_reshape", qtype)
+    N, E = 64, 3
+    raw = synth.weights(qtype, N * E, VK, seed=74)
+    a = sc.weights(qtype, np.zeros_like(raw), (VK, N, E))
+    a2 = a.view((VK, N * E))                                          # ggml_reshape_2d
+    be.set_tensor(a2, raw)
+    rows = a.view((VK, 5), offset=70 * a.nb[1])                       # rows 70..74: slice 1
+    patch = synth.weights(qtype, 5, VK, seed=75)
+    be.set_tensor(rows, patch)
+    exp = raw.copy()
+    exp[70 * a.nb[1]:75 * a.nb[1]] = patch
+    assert np.array_equal(be.get_tensor(a), exp)
+    assert np.array_equal(be.get_tensor(rows), patch)
+    assert dequant_matches(be, sc, orc, qtype, a, exp)
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+def test_partial_range_across_a_slice_boundary_is_exact(be, sc, orc, qtype):
+    say("range_across_slices", qtype)
+    raw = synth.weights(qtype, 4 * 3, VK, seed=76)
+    a = sc.weights(qtype, raw, (VK, 4, 3))
+    sb = a.nb[2]
+    at, ln = sb - 37, sb + 100                                        # slice 0's tail .. slice 2's head
+    patch = np.random.default_rng(77).integers(0, 256, ln, dtype=np.uint8)
+    be.set_tensor(a, patch, offset=at)
+    exp = raw.copy()
+    exp[at:at + ln] = patch
+    assert np.array_equal(be.get_tensor(a), exp)
+    assert np.array_equal(be.get_tensor(a, offset=2 * sb - 40, size=80), exp[2 * sb - 40:2 * sb + 40])
+    # the same through a view of slice 1: its range is its base's at view_offs
+    s1 = a.view((VK, 4), offset=sb)
+    assert np.array_equal(be.get_tensor(s1, offset=3, size=sb - 6), exp[sb + 3:2 * sb - 3])
+    assert dequant_matches(be, sc, orc, qtype, a, exp)
+
+
+def mul_mat_of(be, sc, w, K, N, seed):
+    x = synth.activations(N * w.ne[2], K, seed)
+    xt = sc.f32(x.reshape(w.ne[2], N, K))
+    y = sc.empty_f32((w.ne[1], N, w.ne[2]))
+    be.mul_mat(w, xt, y)
+    be.synchronize()
+    return x, be.get_f32(y).reshape(w.ne[2], N, w.ne[1])
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("N", [1, 5, 20])
+def test_whole_slice_views_multiply_as_their_bytes(be, sc, orc, qtype, N):
+    """views the image addresses (a slice, a run of slices, a reshape over whole tiles, rows
+    64.. of a matrix) multiply like the oracle on the bytes they view"""
+    say("view_mul_mat", qtype, N)
+    blck, bb = synth.BLOCK[qtype]
+    row = VK // blck * bb
+    raw = synth.weights(qtype, 64 * 3, VK, seed=78)
+    a = sc.weights(qtype, raw, (VK, 64, 3))
+    big = synth.weights(qtype, 256, VK, seed=79)
+    c = sc.weights(qtype, big, (VK, 256))
+    cases = [(a.view((VK, 64), offset=2 * a.nb[2]), raw[2 * 64 * row:3 * 64 * row], 64),
+             (a.view((VK, 64, 2), offset=a.nb[2]), None, 64),
+             (a.view((VK, 192)), raw, 192),
+             (c.view((VK, 128), offset=64 * row), big[64 * row:192 * row], 128)]
+    for i, (v, vb, M) in enumerate(cases):
+        x, got = mul_mat_of(be, sc, v, VK, N, seed=80 + i)
+        if vb is not None:
+            ref = orc.mul_mat(qtype, vb, M, VK, x)
+            assert rel_err(got.reshape(N, M), ref) <= TOL, i
+        else:                                                         # two slices, each its own matrix
+            for j in range(2):
+                vb = raw[(1 + j) * 64 * row:(2 + j) * 64 * row]
+                ref = orc.mul_mat(qtype, vb, 64, VK, x[j * N:(j + 1) * N])
+                assert rel_err(got[j], ref) <= TOL, (i, j)
+    with pytest.raises(qmm.QmmError):                                 # rows 5..68: not whole tiles
+        mul_mat_of(be, sc, a.view((VK, 64), offset=5 * row), VK, N, seed=90)
+
+
+@pytest.mark.parametrize("qtype", [qmm.Q4_K, qmm.IQ4_XS])
+def test_mul_mat_id_on_a_run_of_experts(be, sc, orc, qtype):
+    say("view_mul_mat_id", qtype)
+    blck, bb = synth.BLOCK[qtype]
+    M, E, T, k = 64, 8, 6, 2
+    mat = M * VK // blck * bb
+    raw = synth.weights(qtype, M * E, VK, seed=91)
+    e = sc.weights(qtype, raw, (VK, M, E))
+    ev = e.view((VK, M, 4), offset=3 * e.nb[2])                       # experts 3..6 as 0..3
+    g = np.random.default_rng(92)
+    ids = np.stack([g.permutation(4)[:k] for _ in range(T)]).astype(np.int32)
+    x = synth.activations(T, VK, 93)
+    xt = sc.f32(x.reshape(T, 1, VK))
+    it = sc.i32(ids)
+    y = sc.empty_f32((M, k, T))
+    be.mul_mat_id(ev, xt, it, y)
+    be.synchronize()
+    got = be.get_f32(y).reshape(T, k, M)
+    for t in range(T):
+        for j in range(k):
+            xb = raw[(3 + ids[t, j]) * mat:(4 + ids[t, j]) * mat]
+            ref = orc.mul_mat(qtype, xb, M, VK, x[t:t + 1])
+            assert rel_err(got[t, j][None], ref) <= TOL, (t, j)
 
 
 # ------------------------------------------------------------------ bit-exact
