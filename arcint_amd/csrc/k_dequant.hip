@@ -4,7 +4,8 @@
 // Each thread expands one 32-weight group (one 64-weight chunk for Q4_K) of
 // one GGUF block in the evaluation order of ggml's dequantize_row_* (restated
 // in tools/mtp_fit.py:360-409; kernel forms at P02:2956-2984 (Q4_0),
-// P02:4359-4378 (Q8_0), P01:2199-2247 (Q4_K, Q6_K), P01:3390-3398 (IQ4_XS)).
+// P02:4359-4378 (Q8_0), P01:2199-2247 (Q4_K, Q6_K), P01:3390-3398 (IQ4_XS),
+// P01:3736-3750 (Q5_K's fifth bits), P01:3414-3455 (IQ4_NL)).
 // Every product here is exact in fp32 except the last multiply (Q6_K,
 // IQ4_XS) or the last subtract (Q4_K), so contraction is switched off to
 // keep that single rounding where ggml has it.
@@ -82,6 +83,53 @@ __global__ void k_deq_q4_K(WView w, int64_t nblk, float * __restrict__ y) {
     }
 }
 
+// Q5_K: Q4_K's chunk with the fifth bits of qh[l] (chunk 9 + l / 16): bit 2c for the low
+// nibble, 2c + 1 for the high one (ggml's dequantize_row_q5_K; the reference's decode of the
+// same fields, P01:3736-3750)
+__global__ void k_deq_q5_K(WView w, int64_t nblk, float * __restrict__ y) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nblk * 4) return;
+    const int64_t i = t >> 2;
+    const int c = (int)(t & 3);
+    int r, p;
+    const uint8_t * tg = block_tg(w, 1, i, &r, &p);
+    const uint8_t * b = tg + 8 * kChunk + r * 16;       // header {d, dmin, scales[12]}
+    const float d = h2f(reinterpret_cast<const uint16_t *>(b)[0]);
+    const float dmin = h2f(reinterpret_cast<const uint16_t *>(b)[1]);
+    const uint8_t * s = b + 4;
+    int sc[2], m[2];
+    for (int h = 0; h < 2; ++h) {
+        const int j = 2 * c + h;
+        if (j < 4) { sc[h] = s[j] & 63; m[h] = s[j + 4] & 63; }
+        else { sc[h] = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4); m[h] = (s[j + 4] >> 4) | ((s[j] >> 6) << 4); }
+    }
+    const float d1 = d * (float)sc[0], m1 = dmin * (float)m[0];
+    const float d2 = d * (float)sc[1], m2 = dmin * (float)m[1];
+    float * o = y + i * 256 + 64 * c;
+    for (int l = 0; l < 32; ++l) {
+        const uint8_t q = tg[(2 * c + (l >> 4)) * kChunk + r * 16 + (l & 15)];
+        const uint8_t qh = tg[(9 + (l >> 4)) * kChunk + r * 16 + (l & 15)];
+        o[l] = d1 * (float)((q & 0xF) | (((qh >> (2 * c)) & 1) << 4)) - m1;
+        o[32 + l] = d2 * (float)((q >> 4) | (((qh >> (2 * c + 1)) & 1) << 4)) - m2;
+    }
+}
+
+// IQ4_NL: Q4_0's placement, the codes through the codebook (ggml's dequantize_row_iq4_nl;
+// the reference's mv_iq4_nl, P01:3414-3455)
+__global__ void k_deq_iq4_nl(WView w, int64_t nblk, float * __restrict__ y) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblk) return;
+    int r, p;
+    const uint8_t * tg = block_tg(w, 8, i, &r, &p);
+    const uint8_t * qs = tg + p * kChunk + r * 16;
+    const float d = h2f(*reinterpret_cast<const uint16_t *>(tg + 8 * kChunk + r * 16 + 2 * p));
+    float * o = y + i * 32;
+    for (int j = 0; j < 16; ++j) {
+        o[j]      = d * (float)kKvalues[qs[j] & 0xF];
+        o[j + 16] = d * (float)kKvalues[qs[j] >> 4];
+    }
+}
+
 // thread = (block, 32-weight group 32g + l within half n)
 __global__ void k_deq_q6_K(WView w, int64_t nblk, float * __restrict__ y) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -137,6 +185,8 @@ hipError_t launch_dequant(int type, const WView & w, int64_t nmat, float * y, hi
         case QMM_TYPE_Q4_K:   k_deq_q4_K<<<grid(nblk * 4), tpb, 0, s>>>(w, nblk, y); break;
         case QMM_TYPE_Q6_K:   k_deq_q6_K<<<grid(nblk * 8), tpb, 0, s>>>(w, nblk, y); break;
         case QMM_TYPE_IQ4_XS: k_deq_iq4_xs<<<grid(nblk * 8), tpb, 0, s>>>(w, nblk, y); break;
+        case QMM_TYPE_Q5_K:   k_deq_q5_K<<<grid(nblk * 4), tpb, 0, s>>>(w, nblk, y); break;
+        case QMM_TYPE_IQ4_NL: k_deq_iq4_nl<<<grid(nblk), tpb, 0, s>>>(w, nblk, y); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

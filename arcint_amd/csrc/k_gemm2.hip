@@ -64,6 +64,8 @@ constexpr int kMagic = 0x4B400000;       // float 12582912: its bits + i are the
 //         X  [block 4][col BN] f32                    d_x
 //   Q4_K  B  [tile 2][sub 4][h 2][hi/lo 2][row 64] x 16 B   q * sh, q * sl
 //         W  [tile 2][row 64] x 16 B                  the super-block's 8 mins, then 8 zero bytes
+//   Q5_K  as Q4_K with (q - 16) * sh, (q - 16) * sl, and the 8 scales after the mins (the
+//         16 sum_j sc_j bsum_j that q - 16 takes off comes back from one more MFMA)
 //            [tile 2][row 64] float2                  (d, dmin)
 //         X  [col BN] f32                             d_x of the super-block
 //         S  [col BN] x 16 B                          bh[8], bl[8] of the super-block
@@ -73,7 +75,7 @@ constexpr int kMagic = 0x4B400000;       // float 12582912: its bits + i are the
 //            [tile 2][row 64] f32                     d
 //         X  [col BN] f32                             d_x of the super-block
 template <int TYPE, int BN> struct Lay {
-    static constexpr bool KQ = TYPE == QMM_TYPE_Q4_K;
+    static constexpr bool KQ = TYPE == QMM_TYPE_Q4_K || TYPE == QMM_TYPE_Q5_K;
     static constexpr bool IS = TYPE == QMM_TYPE_IQ4_XS || TYPE == QMM_TYPE_Q6_K;
     static constexpr int A = BN * kAP;
     static constexpr int B = KQ ? 2 * 4 * 2 * 2 * kChunk : 2 * 4 * 2 * kChunk;
@@ -108,6 +110,7 @@ struct StageRegs {
     uint4 c;                             // weight code chunk (16 B of one row)
     uint4 h;                             // that row's header (Q4_0: .x = the dword with the block's d)
     uint4 s;                             // Q4_K: the column's split sub-block sums
+    uint4 q5h;                           // Q5_K: the row's qh chunk (the fifth code bits)
     float x;                             // one activation scale
 };
 
@@ -131,7 +134,9 @@ __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per 
     constexpr bool Q8 = TYPE == QMM_TYPE_Q8_0;                    // Q4_0's path with plain int8 codes
     constexpr bool IS = LY::IS;                                   // integer sub-block scales (IQ4_XS, Q6_K)
     constexpr bool Q6 = TYPE == QMM_TYPE_Q6_K;
-    constexpr bool BF = !KQ && !IS;                               // a float scale per block (Q4_0, Q8_0)
+    constexpr bool Q5 = TYPE == QMM_TYPE_Q5_K;                    // Q4_K's path with 5-bit codes
+    constexpr bool NLQ = TYPE == QMM_TYPE_IQ4_NL;                 // Q4_0's path through the codebook
+    constexpr bool BF = !KQ && !IS;                               // a float scale per block (Q4_0, Q8_0, IQ4_NL)
     constexpr int NWN = BN / 32;                                  // column groups of 32
     constexpr int KSPLIT = 4 / NWN;                               // waves sharing a tile (BN 128: 1, 64: 2)
     constexpr int NQ = 4 / KSPLIT;                                // blocks per stage and wave
@@ -213,6 +218,7 @@ __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per 
         if constexpr (KQ) {
             R.h = ld16(tg + 8 * kChunk);
             R.s = *reinterpret_cast<const uint4 *>(sbase + (int64_t)g * p.ldT * 16);
+            if constexpr (Q5) R.q5h = ld16(tg + (9 + (st_cs & 1)) * kChunk);   // qh[16 (cs % 2) ..]
         } else if constexpr (TYPE == QMM_TYPE_IQ4_XS) {
             // the row's 8-byte header {d, scales_h, scales_l[4]} in the tail plane
             const uint2 hd = *reinterpret_cast<const uint2 *>(tbase + (size_t)g * p.w.tg + 8 * kChunk + st_row * 8);
@@ -294,11 +300,13 @@ __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per 
             if (tid < BN) X[tid] = R.x;
         } else if constexpr (!KQ) {
             // chunk 4 hh + cs is block cs of the stage: low nibbles k < 16, high nibbles k >= 16
+            // (IQ4_NL: the codebook value)
+            auto dec = [](uint32_t nib) { return NLQ ? iq4_lookup(nib) : q4_minus8(nib); };
             uint4 lo, hi;
-            lo.x = q4_minus8(e[0] & 0x0F0F0F0Fu); hi.x = q4_minus8((e[0] >> 4) & 0x0F0F0F0Fu);
-            lo.y = q4_minus8(e[1] & 0x0F0F0F0Fu); hi.y = q4_minus8((e[1] >> 4) & 0x0F0F0F0Fu);
-            lo.z = q4_minus8(e[2] & 0x0F0F0F0Fu); hi.z = q4_minus8((e[2] >> 4) & 0x0F0F0F0Fu);
-            lo.w = q4_minus8(e[3] & 0x0F0F0F0Fu); hi.w = q4_minus8((e[3] >> 4) & 0x0F0F0F0Fu);
+            lo.x = dec(e[0] & 0x0F0F0F0Fu); hi.x = dec((e[0] >> 4) & 0x0F0F0F0Fu);
+            lo.y = dec(e[1] & 0x0F0F0F0Fu); hi.y = dec((e[1] >> 4) & 0x0F0F0F0Fu);
+            lo.z = dec(e[2] & 0x0F0F0F0Fu); hi.z = dec((e[2] >> 4) & 0x0F0F0F0Fu);
+            lo.w = dec(e[3] & 0x0F0F0F0Fu); hi.w = dec((e[3] >> 4) & 0x0F0F0F0Fu);
             uint8_t * b = B + ((st_tile * 4 + st_cs) * 2) * kChunk + st_row * 16;
             *reinterpret_cast<uint4 *>(b) = lo;
             *reinterpret_cast<uint4 *>(b + kChunk) = hi;
@@ -321,6 +329,19 @@ __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per 
                 vh.y = v2_mul(m1, sh); vl.y = v2_mul(m1, sl);
                 vh.z = v2_mul(m2, sh); vl.z = v2_mul(m2, sl);
                 vh.w = v2_mul(m3, sh); vl.w = v2_mul(m3, sl);
+                if constexpr (Q5) {
+                    // (q - 16) s = q4 s - 16 s (1 - hb), hb = bit j of qh (j = the sub-block): q4 s < 128, so
+                    // the offset-binary subtract borrows nothing across bytes; the result is in [-112, 105]
+                    const int j = 4 * hh + ql + t;
+                    const uint32_t qh[4] = { R.q5h.x, R.q5h.y, R.q5h.z, R.q5h.w };
+                    uint32_t *ph[4] = { &vh.x, &vh.y, &vh.z, &vh.w }, *pl[4] = { &vl.x, &vl.y, &vl.z, &vl.w };
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const uint32_t nhb = (~qh[i] >> j) & 0x01010101u;
+                        *ph[i] = ((*ph[i] | 0x80808080u) - v2_mul(nhb, 16 * sh)) ^ 0x80808080u;
+                        *pl[i] = ((*pl[i] | 0x80808080u) - v2_mul(nhb, 16 * sl)) ^ 0x80808080u;
+                    }
+                }
                 uint8_t * b = B + (((st_tile * 4 + ql + t) * 2 + h) * 2) * kChunk + st_row * 16;
                 *reinterpret_cast<uint4 *>(b) = vh;
                 *reinterpret_cast<uint4 *>(b + kChunk) = vl;
@@ -331,7 +352,14 @@ __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per 
                 q4k_scale_min(2 * st_cs + 1, R.h.y, R.h.z, R.h.w, &sc, &m1);
                 uint16_t * mw = reinterpret_cast<uint16_t *>(W + (st_tile * 64 + st_row) * 16);
                 mw[st_cs] = (uint16_t)(m0 | (m1 << 8));
-                mw[4 + st_cs] = 0;
+                if constexpr (Q5) {                               // scales 2 cs, 2 cs + 1 after the mins
+                    uint32_t s0, s1, mm;
+                    q4k_scale_min(2 * st_cs, R.h.y, R.h.z, R.h.w, &s0, &mm);
+                    q4k_scale_min(2 * st_cs + 1, R.h.y, R.h.z, R.h.w, &s1, &mm);
+                    mw[4 + st_cs] = (uint16_t)(s0 | (s1 << 8));
+                } else {
+                    mw[4 + st_cs] = 0;
+                }
             }
             if (st_cs == 0)                                       // d and dmin
                 reinterpret_cast<float2 *>(W + 2 * 64 * 16)[st_tile * 64 + st_row] = make_float2(h2f(R.h.x), h2f(R.h.x >> 16));
@@ -511,15 +539,22 @@ __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per 
                     const float2 dd = reinterpret_cast<const float2 *>(W + 2 * 64 * 16)[row];
                     const v4i bmin = h ? zero : *reinterpret_cast<const v4i *>(W + row * 16);
                     // (KSPLIT 2: the tile's second wave adds no min term; its sums meet wave 0's)
-                    v16i mh = v16i{}, ml = v16i{};
+                    v16i mh = v16i{}, ml = v16i{}, sh = v16i{}, sl = v16i{};
                     if (KSPLIT == 1 || wk == 0) {
                         mh = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, bmin, v16i{}, 0, 0, 0);
                         ml = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, bmin, v16i{}, 0, 0, 0);
+                        if constexpr (Q5) {                       // sum_j sc_j bsum_j: k 8..15 of the row
+                            const v4i ash = h ? zero : v4i{ 0, 0, sv.x, sv.y };
+                            const v4i asl = h ? zero : v4i{ 0, 0, sv.z, sv.w };
+                            sh = __builtin_amdgcn_mfma_i32_32x32x32_i8(ash, bmin, v16i{}, 0, 0, 0);
+                            sl = __builtin_amdgcn_mfma_i32_32x32x32_i8(asl, bmin, v16i{}, 0, 0, 0);
+                        }
                     }
                     v16f & o = rt ? out1 : out0;
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
-                        const int isc = 8 * c1[rt][r] + c2[rt][r];
+                        int isc = 8 * c1[rt][r] + c2[rt][r];
+                        if constexpr (Q5) isc += 16 * (64 * sh[r] + sl[r]);
                         const int imn = 64 * mh[r] + ml[r];
                         o[r] += dx[r] * (dd.x * (float)isc - dd.y * (float)imn);
                     }
@@ -694,7 +729,8 @@ void gemm_shape(int type, const WView & w, int64_t N, int64_t nbatch, int64_t * 
     *threads = kT;
     int st;
     switch (type) {
-        case QMM_TYPE_Q4_K: st = sh.BN == 64 ? Lay<QMM_TYPE_Q4_K, 64>::stage : Lay<QMM_TYPE_Q4_K, 128>::stage; break;
+        case QMM_TYPE_Q4_K:
+        case QMM_TYPE_Q5_K: st = sh.BN == 64 ? Lay<QMM_TYPE_Q4_K, 64>::stage : Lay<QMM_TYPE_Q4_K, 128>::stage; break;
         case QMM_TYPE_Q6_K:
         case QMM_TYPE_IQ4_XS: st = sh.BN == 64 ? Lay<QMM_TYPE_Q6_K, 64>::stage : Lay<QMM_TYPE_Q6_K, 128>::stage; break;
         default: st = sh.BN == 64 ? Lay<QMM_TYPE_Q4_0, 64>::stage : Lay<QMM_TYPE_Q4_0, 128>::stage; break;
@@ -705,7 +741,7 @@ void gemm_shape(int type, const WView & w, int64_t N, int64_t nbatch, int64_t * 
 hipError_t launch_gemm(int type, const WView & w, const ActBuf & a, int64_t N, int64_t nbatch, const GemmBatch & bt,
                        float * dst, hipStream_t s, const KTime * kt) {
     if (!a.dT || a.ldk != w.G * 256 || a.ldT < N * nbatch + 64 || N <= 0 || nbatch <= 0 ||
-        nbatch > 65535 || a.vdt != vec_dot_type(type) || (type == QMM_TYPE_Q4_K && !a.bsp))
+        nbatch > 65535 || a.vdt != vec_dot_type(type) || ((type == QMM_TYPE_Q4_K || type == QMM_TYPE_Q5_K) && !a.bsp))
         return hipErrorInvalidValue;
     const G2Shape sh = g2_shape(w, N, nbatch);
     G2Params p{};
@@ -740,6 +776,10 @@ hipError_t launch_gemm(int type, const WView & w, const ActBuf & a, int64_t N, i
         return sh.BN == 64 ? launch_t<QMM_TYPE_IQ4_XS, 64>(p, g, s, kt) : launch_t<QMM_TYPE_IQ4_XS, 128>(p, g, s, kt);
     if (type == QMM_TYPE_Q4_K)
         return sh.BN == 64 ? launch_t<QMM_TYPE_Q4_K, 64>(p, g, s, kt) : launch_t<QMM_TYPE_Q4_K, 128>(p, g, s, kt);
+    if (type == QMM_TYPE_Q5_K)
+        return sh.BN == 64 ? launch_t<QMM_TYPE_Q5_K, 64>(p, g, s, kt) : launch_t<QMM_TYPE_Q5_K, 128>(p, g, s, kt);
+    if (type == QMM_TYPE_IQ4_NL)
+        return sh.BN == 64 ? launch_t<QMM_TYPE_IQ4_NL, 64>(p, g, s, kt) : launch_t<QMM_TYPE_IQ4_NL, 128>(p, g, s, kt);
     return hipErrorInvalidValue;
 }
 

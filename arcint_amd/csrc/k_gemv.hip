@@ -2,7 +2,8 @@
 //
 // Role of the reference's kernel_mul_mv_{q4_K,q6_K}_q8_1 (P01:3740-3921),
 // kernel_mul_mv_q4_0_q8_1 (P02:6098-6220), kernel_mul_mv_iq4_xs_q8_1
-// (P01:3457-3553), the Q8_0 matvec and the MUL_MAT_ID matvec
+// (P01:3457-3553), mv_q45_K's Q5_K and mv_iq4_nl (P01:3736-3800,
+// P01:3414-3455), the Q8_0 matvec and the MUL_MAT_ID matvec
 // (P01:3923-3964), redesigned for CDNA4 and for ggml-cpu's numerics instead
 // of the reference's two-term q8_1 activations:
 //  * lane r of a wave owns row r of a 64-row weight tile and walks groups of
@@ -299,6 +300,91 @@ template <> struct GV<QMM_TYPE_IQ4_XS> {
     }
 };
 
+// ---- IQ4_NL: Q4_0's stage (8 code chunks + the d chunk), the codes through the codebook
+template <> struct GV<QMM_TYPE_IQ4_NL> {
+    static constexpr int NST = 1, NL = 9, ND = 8, NS = 8;
+    __device__ static void load(uint4 * r, const uint8_t * tg, int st, int lane) { GV<QMM_TYPE_Q4_0>::load(r, tg, st, lane); }
+    template <int NC>
+    __device__ static void dot(const uint4 * r, int, const XG<NC> & x, int nc, float * acc, int *) {
+        const uint32_t dw2[4] = { r[8].x, r[8].y, r[8].z, r[8].w };
+        const uint32_t m = 0x0F0F0F0Fu;
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+            const uint4 q = r[p];
+            const uint32_t v0 = iq4_lookup(q.x & m), v1 = iq4_lookup(q.y & m), v2 = iq4_lookup(q.z & m), v3 = iq4_lookup(q.w & m);
+            const uint32_t u0 = iq4_lookup((q.x >> 4) & m), u1 = iq4_lookup((q.y >> 4) & m);
+            const uint32_t u2 = iq4_lookup((q.z >> 4) & m), u3 = iq4_lookup((q.w >> 4) & m);
+            const float dw = h2f(dw2[p >> 1] >> (16 * (p & 1)));
+#pragma unroll
+            for (int j = 0; j < NC; ++j) {
+                if (j < nc) {
+                    int s = dot16(v0, v1, v2, v3, sld4(x.c[j], 8 * p), 0);
+                    s = dot16(u0, u1, u2, u3, sld4(x.c[j], 8 * p + 4), s);
+                    acc[j] += (float)s * (dw * sldf(x.d[j], p));
+                }
+            }
+        }
+    }
+};
+
+// ---- Q5_K: Q4_K's stage plus the two qh chunks: byte i of qh chunk 9 + h holds the fifth bits
+// of position 16 h + i of all four 64-weight chunks (bit 2 cc low nibble, 2 cc + 1 high)
+template <> struct GV<QMM_TYPE_Q5_K> {
+    static constexpr int NST = 1, NL = 11, ND = 1, NS = 16;
+    __device__ static void load(uint4 * r, const uint8_t * tg, int, int lane) {
+        const uint8_t * p = tg + lane * 16;
+#pragma unroll
+        for (int c = 0; c < 11; ++c) r[c] = ld16_nt(p + c * kChunk);
+    }
+    template <int NC>
+    __device__ static void dot(const uint4 * r, int, const XG<NC> & x, int nc, float * acc, int *) {
+        const uint4 h = r[8];                              // d, dmin | scales[12]
+        const float d = h2f(h.x), dmin = h2f(h.x >> 16);
+        const uint32_t sc03 = h.y & 0x3f3f3f3fu, mn03 = h.z & 0x3f3f3f3fu;
+        const uint32_t sc47 = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
+        const uint32_t mn47 = ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u);
+        int sc[8], mn[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            sc[i] = (int)((sc03 >> (8 * i)) & 0xffu);
+            sc[4 + i] = (int)((sc47 >> (8 * i)) & 0xffu);
+            mn[i] = (int)((mn03 >> (8 * i)) & 0xffu);
+            mn[4 + i] = (int)((mn47 >> (8 * i)) & 0xffu);
+        }
+        int isc[NC];
+#pragma unroll
+        for (int j = 0; j < NC; ++j) isc[j] = 0;
+        const uint32_t m = 0x0F0F0F0Fu, b1 = 0x01010101u;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const uint4 q = r[c], qh = r[9 + (c & 1)];
+            const int bl = 2 * (c >> 1), bh = bl + 1;            // fifth-bit positions
+            const uint32_t l0 = (q.x & m) | (((qh.x >> bl) & b1) << 4), l1 = (q.y & m) | (((qh.y >> bl) & b1) << 4);
+            const uint32_t l2 = (q.z & m) | (((qh.z >> bl) & b1) << 4), l3 = (q.w & m) | (((qh.w >> bl) & b1) << 4);
+            const uint32_t h0 = ((q.x >> 4) & m) | (((qh.x >> bh) & b1) << 4), h1 = ((q.y >> 4) & m) | (((qh.y >> bh) & b1) << 4);
+            const uint32_t h2 = ((q.z >> 4) & m) | (((qh.z >> bh) & b1) << 4), h3 = ((q.w >> 4) & m) | (((qh.w >> bh) & b1) << 4);
+            const int jl = 2 * (c >> 1), xo = 16 * (c >> 1) + 4 * (c & 1);   // dwords
+#pragma unroll
+            for (int j = 0; j < NC; ++j) {
+                if (j < nc) {
+                    const int sl = dot16(l0, l1, l2, l3, sld4(x.c[j], xo), 0);
+                    const int sh = dot16(h0, h1, h2, h3, sld4(x.c[j], xo + 8), 0);
+                    isc[j] += sc[jl] * sl + sc[jl + 1] * sh;
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            if (j < nc) {
+                int imn = 0;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) imn += mn[i] * (slds16(x.s[j], 2 * i) + slds16(x.s[j], 2 * i + 1));
+                acc[j] += sldf(x.d[j], 0) * (d * (float)isc[j] - dmin * (float)imn);
+            }
+        }
+    }
+};
+
 // weight stages in flight per wave (register ring), by columns
 // Stages in flight per wave.  One (the next stage is loaded once the current
 // one is consumed; the other waves of the SIMD hide the latency) streams
@@ -516,7 +602,8 @@ template <int TYPE>
 __device__ __forceinline__ void mma_stage(const uint4 (&rw)[9], int st, const uint8_t * xag, const float * xdg,
                                           const uint8_t * xsg, int h, const v16i & magic, v8f & out) {
     constexpr bool KQ = TYPE == QMM_TYPE_Q4_K, IQ = TYPE == QMM_TYPE_IQ4_XS, Q8 = TYPE == QMM_TYPE_Q8_0;
-    constexpr bool BF = TYPE == QMM_TYPE_Q4_0 || Q8;
+    constexpr bool NLQ = TYPE == QMM_TYPE_IQ4_NL;                // Q4_0's blocks through the codebook
+    constexpr bool BF = TYPE == QMM_TYPE_Q4_0 || Q8 || NLQ;
     constexpr int NB = Q8 ? 4 : 8;                                // 32-weight blocks per stage
     auto a_op = [&](int b) -> v4i { return *reinterpret_cast<const v4i *>(xag + 32 * (Q8 ? 4 * st + b : b)); };
     auto dx_op = [&](int b) -> float4 { return *reinterpret_cast<const float4 *>(xdg + (Q8 ? 4 * st + b : b) * 8); };
@@ -540,6 +627,9 @@ __device__ __forceinline__ void mma_stage(const uint4 (&rw)[9], int st, const ui
             if constexpr (Q8) {
                 lo = rw[2 * b];
                 hi = rw[2 * b + 1];
+            } else if constexpr (NLQ) {
+                lo = map4(nib(rw[b], 0), iq4_lookup);
+                hi = map4(nib(rw[b], 4), iq4_lookup);
             } else {
                 lo = map4(nib(rw[b], 0), q4_minus8);
                 hi = map4(nib(rw[b], 4), q4_minus8);
@@ -655,7 +745,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     constexpr int NL = T::NL, NST = T::NST;
     static_assert(NL == 9, "mma_stage takes 9 weight registers");
     constexpr bool KQ = TYPE == QMM_TYPE_Q4_K, Q8 = TYPE == QMM_TYPE_Q8_0;
-    constexpr bool BF = TYPE == QMM_TYPE_Q4_0 || Q8;             // a float scale per 32 weights
+    constexpr bool BF = TYPE == QMM_TYPE_Q4_0 || Q8 || TYPE == QMM_TYPE_IQ4_NL;   // a float scale per 32 weights
     constexpr int BS = BF ? 32 : 256;                             // activation scale block
     constexpr int NSB = BF ? 8 : 1;                               // activation scales per group
     constexpr int kMagic = 0x4B400000;                            // float 12582912: its bits + i = 12582912 + i
@@ -825,7 +915,8 @@ int env_int(const char * name, int dflt) {
 }  // namespace
 
 bool gemv_mma_supported(int type) {
-    return type == QMM_TYPE_Q4_0 || type == QMM_TYPE_Q8_0 || type == QMM_TYPE_Q4_K || type == QMM_TYPE_IQ4_XS;
+    return type == QMM_TYPE_Q4_0 || type == QMM_TYPE_Q8_0 || type == QMM_TYPE_Q4_K || type == QMM_TYPE_IQ4_XS ||
+           type == QMM_TYPE_IQ4_NL;
 }
 
 bool gemv_plan(int type, const WView & w, int nc, int64_t ntasks, bool allow_split, bool want_mma, GemvPlan * pl) {
@@ -896,7 +987,7 @@ int64_t gemv_workgroups(const WView & w, const GemvPlan & pl) {
 size_t gemv_lds_bytes(int type, const GemvPlan & pl) {
     if (pl.mma) {
         const size_t per_group = 8 * (kMmaColBytes + (type == QMM_TYPE_Q4_K ? 16 : 0)) +
-                                 8 * sizeof(float) * (type == QMM_TYPE_Q4_0 || type == QMM_TYPE_Q8_0 ? 8 : 1);
+                                 8 * sizeof(float) * (vec_dot_type(type) == QMM_TYPE_Q8_0 ? 8 : 1);
         const size_t stage = kMmaZeroBytes + (size_t)(pl.W / pl.tw) * pl.spw * per_group;
         const size_t red = pl.W > pl.tw ? (size_t)pl.W * 8 * 64 * sizeof(float) : 0;   // the K waves' sums
         return std::max(stage, red);
@@ -957,6 +1048,7 @@ hipError_t launch_gemv(int type, const WView & w, const GemvPlan & pl, const Act
             case QMM_TYPE_Q8_0: { QMM_MMA(QMM_TYPE_Q8_0) }
             case QMM_TYPE_Q4_K: { QMM_MMA(QMM_TYPE_Q4_K) }
             case QMM_TYPE_IQ4_XS: { QMM_MMA(QMM_TYPE_IQ4_XS) }
+            case QMM_TYPE_IQ4_NL: { QMM_MMA(QMM_TYPE_IQ4_NL) }
             default: return hipErrorInvalidValue;
         }
 #undef QMM_MMA
@@ -967,6 +1059,8 @@ hipError_t launch_gemv(int type, const WView & w, const GemvPlan & pl, const Act
         case QMM_TYPE_Q4_K:   return launch_t<QMM_TYPE_Q4_K>(p, pl.nc, nwg, s, kt);
         case QMM_TYPE_Q6_K:   return launch_t<QMM_TYPE_Q6_K>(p, pl.nc, nwg, s, kt);
         case QMM_TYPE_IQ4_XS: return launch_t<QMM_TYPE_IQ4_XS>(p, pl.nc, nwg, s, kt);
+        case QMM_TYPE_Q5_K:   return launch_t<QMM_TYPE_Q5_K>(p, pl.nc, nwg, s, kt);
+        case QMM_TYPE_IQ4_NL: return launch_t<QMM_TYPE_IQ4_NL>(p, pl.nc, nwg, s, kt);
         default: return hipErrorInvalidValue;
     }
 }

@@ -141,7 +141,7 @@ static bool span_ok(const qmm_tensor * t) {
 // image lies in its buffer (off for shape-only queries).
 static bool weight_image(const qmm_tensor * t, bool mem, WView * w, char * reason, size_t len) {
     const TypeLayout * L = type_layout(t->type);
-    if (!L) return why(reason, len, "src0 type is not Q4_0/Q8_0/Q4_K/Q6_K/IQ4_XS");
+    if (!L) return why(reason, len, "src0 type is not Q4_0/Q8_0/Q4_K/Q5_K/Q6_K/IQ4_NL/IQ4_XS");
     if (t->ne[0] % L->blck) return why(reason, len, "ne00 is not a multiple of the block size");
     if (!contiguous(t)) return why(reason, len, "src0 is not contiguous");
     const qmm_tensor * b = base_of(t);

@@ -24,9 +24,11 @@ namespace qmm {
 //   Q4_0    chunk p < 8: qs of block p | chunk 8: d of blocks 0..7 (fp16)
 //   Q8_0    chunks 2p, 2p+1: qs[0:16], qs[16:32] of block p | chunk 16: d[8]
 //   Q4_K    chunk c < 8: qs[16c:16c+16] | chunk 8: {d, dmin, scales[12]}
+//   Q5_K    as Q4_K | chunks 9, 10: qh[0:16], qh[16:32]
 //   Q6_K    chunk c < 8: ql[16c:+16] | chunks 8..11: qh[16c:+16] |
 //           chunk 12: scales[16] | tail (2 B): d
 //   IQ4_XS  chunk c < 8: qs[16c:+16] | tail (8 B): {d, scales_h, scales_l[4]}
+//   IQ4_NL  as Q4_0 (the same block bytes; the codes index the codebook)
 // Tile-groups are stored [matrix][tile][group]; rows past M in the last tile
 // and the padding blocks of a partial group are zero bytes.
 // ---------------------------------------------------------------------------
@@ -101,7 +103,7 @@ struct ZeroJob {
 __host__ __device__ static inline int act_block(int vdt) { return vdt == QMM_TYPE_Q8_0 ? 32 : 256; }
 __host__ __device__ static inline int act_sum_block(int vdt) { return vdt == QMM_TYPE_Q8_0 ? 32 : 16; }
 __host__ __device__ static inline int vec_dot_type(int type) {
-    return (type == QMM_TYPE_Q4_0 || type == QMM_TYPE_Q8_0) ? QMM_TYPE_Q8_0 : QMM_TYPE_Q8_K;
+    return (type == QMM_TYPE_Q4_0 || type == QMM_TYPE_Q8_0 || type == QMM_TYPE_IQ4_NL) ? QMM_TYPE_Q8_0 : QMM_TYPE_Q8_K;
 }
 
 // f32 source columns: column c = (i1, i2, i3) with i1 fastest
@@ -169,7 +171,7 @@ struct GemvPlan {
     int nc;                        // columns per task (1..8)
     int64_t ntasks;                // grid tasks (list mode: upper bound)
     int W, KS, spw;
-    bool mma;                      // dots on the MFMA (few columns; Q4_0, Q8_0, Q4_K, IQ4_XS)
+    bool mma;                      // dots on the MFMA (few columns; Q4_0, Q8_0, Q4_K, IQ4_XS, IQ4_NL)
     int tw;                        // mma: tiles per work-group, W / tw waves of each split K
 };
 constexpr int kMmaColBytes = 272;  // 256 codes + 16 bytes of padding (LDS banks)

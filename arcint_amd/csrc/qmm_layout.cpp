@@ -19,6 +19,8 @@ const TypeLayout kLayouts[] = {
     { QMM_TYPE_Q4_K,   256, 144, 1, 9,  0, 9 * kChunk },
     { QMM_TYPE_Q6_K,   256, 210, 1, 13, 2, 13 * kChunk + 2 * kTileRows },
     { QMM_TYPE_IQ4_XS, 256, 136, 1, 8,  8, 8 * kChunk + 8 * kTileRows },
+    { QMM_TYPE_Q5_K,   256, 176, 1, 11, 0, 11 * kChunk },
+    { QMM_TYPE_IQ4_NL, 32,  18,  8, 9,  0, 9 * kChunk },
 };
 
 }  // namespace
@@ -46,6 +48,7 @@ int block_pieces(const TypeLayout & L, Piece out[16]) {
     int n = 0;
     switch (L.type) {
         case QMM_TYPE_Q4_0:
+        case QMM_TYPE_IQ4_NL:
             out[n++] = { 2, 16, 0, 16, kChunk };
             out[n++] = { 0, 2, 8 * kChunk, 16, 2 };
             break;
@@ -63,6 +66,12 @@ int block_pieces(const TypeLayout & L, Piece out[16]) {
             for (int c = 0; c < 4; ++c) out[n++] = { 128 + 16 * c, 16, (8 + c) * kChunk, 16, 0 };
             out[n++] = { 192, 16, 12 * kChunk, 16, 0 };
             out[n++] = { 208, 2, 13 * kChunk, 2, 0 };
+            break;
+        case QMM_TYPE_Q5_K:
+            for (int c = 0; c < 8; ++c) out[n++] = { 48 + 16 * c, 16, c * kChunk, 16, 0 };
+            out[n++] = { 0, 16, 8 * kChunk, 16, 0 };
+            out[n++] = { 16, 16, 9 * kChunk, 16, 0 };
+            out[n++] = { 32, 16, 10 * kChunk, 16, 0 };
             break;
         case QMM_TYPE_IQ4_XS:
             for (int c = 0; c < 8; ++c) out[n++] = { 8 + 16 * c, 16, c * kChunk, 16, 0 };

@@ -34,7 +34,9 @@ GGML_TYPES = {
     2: (32, 18),        # Q4_0
     8: (32, 34),        # Q8_0
     12: (256, 144),     # Q4_K
+    13: (256, 176),     # Q5_K
     14: (256, 210),     # Q6_K
+    20: (32, 18),       # IQ4_NL
     23: (256, 136),     # IQ4_XS
     24: (1, 1),         # I8
     25: (1, 2),         # I16

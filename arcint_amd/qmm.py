@@ -22,9 +22,9 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libqmm.so")
 
-F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, Q8_K, IQ4_XS, I32 = 0, 1, 2, 8, 12, 14, 15, 23, 26
+F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K, IQ4_NL, IQ4_XS, I32 = 0, 1, 2, 8, 12, 13, 14, 15, 20, 23, 26
 OP_MUL_MAT, OP_MUL_MAT_ID = 1, 2
-QUANT_TYPES = (Q4_0, Q8_0, Q4_K, Q6_K, IQ4_XS)
+QUANT_TYPES = (Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS)
 
 # every symbol include/qmm.h declares
 EXPORTS = (

@@ -6,6 +6,8 @@ Distributions follow the benchmark definition of the reference's configs:
   Q4_K    d, dmin = fp16(|N(0, 0.02)|), 12 scale bytes U{0..255}, code bytes U
   Q6_K    ql, qh U bytes, scales U{-128..127}, d = fp16(|N(0, 0.002)|)
   IQ4_XS  d = fp16(|N(0, 0.02)|), scales_h / scales_l / code bytes U
+  Q5_K    as Q4_K, with qh bytes U
+  IQ4_NL  as Q4_0 (the codes index the codebook)
   activations f32 N(0, 1); MoE ids = top-k of softmax(N(0, 1) logits)
 Scales are made from floats, so no fp16 NaN or Inf ever appears.  Each tensor
 takes its own numpy PCG64 stream (seed + a tensor index).
@@ -14,9 +16,10 @@ from __future__ import annotations
 
 import numpy as np
 
-Q4_0, Q8_0, Q4_K, Q6_K, Q8_K, IQ4_XS = 2, 8, 12, 14, 15, 23
-BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210), IQ4_XS: (256, 136)}
-NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K", IQ4_XS: "IQ4_XS"}
+Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K, IQ4_NL, IQ4_XS = 2, 8, 12, 13, 14, 15, 20, 23
+BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), IQ4_NL: (32, 18),
+         IQ4_XS: (256, 136)}
+NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", IQ4_NL: "IQ4_NL", IQ4_XS: "IQ4_XS"}
 BY_NAME = {v: k for k, v in NAMES.items()}
 
 
@@ -35,16 +38,16 @@ def weights(qtype: int, rows: int, k: int, seed: int) -> np.ndarray:
     nb = rows * (k // blck)
     g = rng(seed)
     b = np.empty((nb, nbytes), np.uint8)
-    if qtype == Q4_0:
+    if qtype in (Q4_0, IQ4_NL):
         b[:, 0:2] = _f16_bytes(np.abs(g.normal(0, 0.02, nb)).astype(np.float32))
         b[:, 2:] = g.integers(0, 256, (nb, 16), dtype=np.uint8)
     elif qtype == Q8_0:
         b[:, 0:2] = _f16_bytes(np.abs(g.normal(0, 0.02, nb)).astype(np.float32))
         b[:, 2:] = g.integers(-127, 128, (nb, 32), dtype=np.int8).view(np.uint8)
-    elif qtype == Q4_K:
+    elif qtype in (Q4_K, Q5_K):
         b[:, 0:2] = _f16_bytes(np.abs(g.normal(0, 0.02, nb)).astype(np.float32))
         b[:, 2:4] = _f16_bytes(np.abs(g.normal(0, 0.02, nb)).astype(np.float32))
-        b[:, 4:] = g.integers(0, 256, (nb, 140), dtype=np.uint8)
+        b[:, 4:] = g.integers(0, 256, (nb, nbytes - 4), dtype=np.uint8)
     elif qtype == Q6_K:
         b[:, 0:192] = g.integers(0, 256, (nb, 192), dtype=np.uint8)
         b[:, 192:208] = g.integers(-128, 128, (nb, 16), dtype=np.int8).view(np.uint8)

@@ -310,6 +310,10 @@ def main():
         for qt, nm in ((qmm.IQ4_XS, "IQ4_XS"), (qmm.Q8_0, "Q8_0")):
             for n in (2, 4, 8):
                 gcases.append((qt, 14336, 4096, n, f"{nm} 14336x4096 N={n} (config 4)"))
+        # the adjacent types on config shapes (no reference config quotes them)
+        gcases += [(qmm.Q5_K, 17408, 5120, 1, "Q5_K GEMV 17408x5120 N=1 (config 2 shape)"),
+                   (qmm.IQ4_NL, 14336, 4096, 1, "IQ4_NL GEMV 14336x4096 N=1 (config 4 shape)"),
+                   (qmm.IQ4_NL, 14336, 4096, 8, "IQ4_NL 14336x4096 N=8 (config 4 shape)")]
         gem = [gemv_case(be, qmm, synth, qt, M2, K2, N2, nm, args) for qt, M2, K2, N2, nm in gcases]
         if out:
             out["gemv"] = gem

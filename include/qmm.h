@@ -1,7 +1,8 @@
 /*
  * qmm.h - C ABI of libqmm, an MI355X (gfx950) implementation of ggml's
  * quantized matrix product: GGML_OP_MUL_MAT and GGML_OP_MUL_MAT_ID on GGUF
- * block-quant weights (Q4_0, Q8_0, Q4_K, Q6_K, IQ4_XS) with f32 activations.
+ * block-quant weights (Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS) with f32
+ * activations.
  *
  * The entry points mirror what a ggml backend exposes for this op, so that a
  * ggml backend adaptor (or a ctypes harness) can bind them with plain
@@ -30,7 +31,9 @@
  *                                list, graph_gen++ per call (P01:609-612);
  *                                activation dedup keyed per graph (P01:683-717)
  *   qmm_dequantize               dequantize_row_* of ggml (bit-exact gate;
- *                                tools/mtp_fit.py:338-409 restates them)
+ *                                tools/mtp_fit.py:338-409 restates them;
+ *                                Q5_K / IQ4_NL decode as P01:3736-3750 and
+ *                                P01:3414-3455)
  *   qmm_quantize_act             ggml-cpu's from_float for the vec_dot type
  *                                (quantize_row_q8_0 / quantize_row_q8_K,
  *                                restated at 0000-03-...patch:646-683)
@@ -80,8 +83,10 @@ enum qmm_type {
     QMM_TYPE_Q4_0   = 2,
     QMM_TYPE_Q8_0   = 8,
     QMM_TYPE_Q4_K   = 12,
+    QMM_TYPE_Q5_K   = 13,
     QMM_TYPE_Q6_K   = 14,
     QMM_TYPE_Q8_K   = 15,
+    QMM_TYPE_IQ4_NL = 20,
     QMM_TYPE_IQ4_XS = 23,
     QMM_TYPE_I32    = 26,
 };

@@ -1,7 +1,7 @@
 """TEST INFRASTRUCTURE ONLY: ctypes binding of the CPU oracle (liborc.so).
 
 The oracle restates ggml's CPU arithmetic for MUL_MAT / MUL_MAT_ID on
-Q4_0 / Q8_0 / Q4_K / Q6_K / IQ4_XS (see qmm_oracle.h for what pins each
+Q4_0 / Q8_0 / Q4_K / Q5_K / Q6_K / IQ4_NL / IQ4_XS (see qmm_oracle.h for what pins each
 function).  Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
 leg may import this package, and only as the checker or the timed CPU
 baseline; the product path never does.
@@ -16,11 +16,12 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB = os.path.join(_HERE, "liborc.so")
 
-Q4_0, Q8_0, Q4_K, Q6_K, Q8_K, IQ4_XS = 2, 8, 12, 14, 15, 23
+Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K, IQ4_NL, IQ4_XS = 2, 8, 12, 13, 14, 15, 20, 23
 # type -> (weights per block, bytes per block, vec_dot type)
-TYPES = {Q4_0: (32, 18, Q8_0), Q8_0: (32, 34, Q8_0), Q4_K: (256, 144, Q8_K),
-         Q6_K: (256, 210, Q8_K), IQ4_XS: (256, 136, Q8_K)}
-NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K", IQ4_XS: "IQ4_XS"}
+TYPES = {Q4_0: (32, 18, Q8_0), Q8_0: (32, 34, Q8_0), Q4_K: (256, 144, Q8_K), Q5_K: (256, 176, Q8_K),
+         Q6_K: (256, 210, Q8_K), IQ4_NL: (32, 18, Q8_0), IQ4_XS: (256, 136, Q8_K)}
+NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", IQ4_NL: "IQ4_NL",
+         IQ4_XS: "IQ4_XS"}
 
 _lib = None
 

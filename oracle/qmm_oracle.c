@@ -2,7 +2,7 @@
  * qmm_oracle.c - TEST INFRASTRUCTURE ONLY (see qmm_oracle.h).
  *
  * CPU restatement of ggml's arithmetic for MUL_MAT / MUL_MAT_ID on Q4_0,
- * Q8_0, Q4_K, Q6_K and IQ4_XS weights.  Each function names the reference
+ * Q8_0, Q4_K, Q5_K, Q6_K, IQ4_NL and IQ4_XS weights.  Each function names the reference
  * text it follows (paths relative to /root/reference; P01/P02/P03 =
  * contrib/llama.cpp/patches/0000-0{1,2,3}-*.patch).  Built with
  * -ffp-contract=off so that no multiply-add is fused behind our back.
@@ -20,6 +20,8 @@ _Static_assert(sizeof(orc_block_q8_0) == 34, "block_q8_0");
 _Static_assert(sizeof(orc_block_q4_K) == 144, "block_q4_K");
 _Static_assert(sizeof(orc_block_q6_K) == 210, "block_q6_K");
 _Static_assert(sizeof(orc_block_iq4_xs) == 136, "block_iq4_xs");
+_Static_assert(sizeof(orc_block_q5_K) == 176, "block_q5_K");
+_Static_assert(sizeof(orc_block_iq4_nl) == 18, "block_iq4_nl");
 _Static_assert(sizeof(orc_block_q8_K) == 292, "block_q8_K");
 
 /* ---- IEEE binary16 <-> binary32 (from the IEEE 754 encoding) ------------ */
@@ -71,6 +73,8 @@ int orc_type_info(int type, int * blck, int * bytes, int * vec_dot_type) {
         case ORC_Q4_K:   b = 256; s = 144; v = ORC_Q8_K; break;
         case ORC_Q6_K:   b = 256; s = 210; v = ORC_Q8_K; break;
         case ORC_IQ4_XS: b = 256; s = 136; v = ORC_Q8_K; break;
+        case ORC_Q5_K:   b = 256; s = 176; v = ORC_Q8_K; break;
+        case ORC_IQ4_NL: b = 32;  s = 18;  v = ORC_Q8_0; break;
         case ORC_Q8_K:   b = 256; s = 292; v = 0; break;
         default: return 0;
     }
@@ -168,6 +172,41 @@ static void dequant_iq4_xs(const orc_block_iq4_xs * x, float * y, int64_t nb) {
     }
 }
 
+/* Q5_K: Q4_K's d, dmin and 6-bit scales/mins with a fifth code bit per weight.  Chunk c of 64
+ * weights takes ql[32c + l] (low nibbles: weights 64c + l, high nibbles: 64c + 32 + l) and bits
+ * 2c (low) / 2c + 1 (high) of qh[l] (ggml's dequantize_row_q5_K; the reference's decode of the
+ * same fields, P01:3736-3750, mv_q45_K) */
+static void dequant_q5_K(const orc_block_q5_K * x, float * y, int64_t nb) {
+    for (int64_t i = 0; i < nb; ++i) {
+        const float d = orc_fp16_to_fp32(x[i].d), dmin = orc_fp16_to_fp32(x[i].dmin);
+        float * out = y + 256 * i;
+        for (int c = 0; c < 4; ++c) {
+            uint8_t sc, m;
+            scale_min_k4(2 * c, x[i].scales, &sc, &m);
+            const float d1 = d * (float)sc, m1 = dmin * (float)m;
+            scale_min_k4(2 * c + 1, x[i].scales, &sc, &m);
+            const float d2 = d * (float)sc, m2 = dmin * (float)m;
+            for (int l = 0; l < 32; ++l) {
+                const uint8_t q = x[i].qs[32 * c + l], h = x[i].qh[l];
+                out[64 * c + l]      = d1 * (float)((q & 0xF) + (((h >> (2 * c)) & 1) << 4)) - m1;
+                out[64 * c + 32 + l] = d2 * (float)((q >> 4) + (((h >> (2 * c + 1)) & 1) << 4)) - m2;
+            }
+        }
+    }
+}
+
+/* IQ4_NL: Q4_0's block (d, qs[16]) with the codes through the non-linear codebook instead of
+ * q - 8 (ggml's dequantize_row_iq4_nl; the reference's mv_iq4_nl, P01:3414-3455) */
+static void dequant_iq4_nl(const orc_block_iq4_nl * x, float * y, int64_t nb) {
+    for (int64_t i = 0; i < nb; ++i) {
+        const float d = orc_fp16_to_fp32(x[i].d);
+        for (int j = 0; j < 16; ++j) {
+            y[32 * i + j]      = d * (float)kvalues_iq4nl[x[i].qs[j] & 0xF];
+            y[32 * i + j + 16] = d * (float)kvalues_iq4nl[x[i].qs[j] >> 4];
+        }
+    }
+}
+
 void orc_dequantize_row(int type, const void * x, float * y, int64_t k) {
     int blck = 0;
     if (!orc_type_info(type, &blck, NULL, NULL)) return;
@@ -178,6 +217,8 @@ void orc_dequantize_row(int type, const void * x, float * y, int64_t k) {
         case ORC_Q4_K:   dequant_q4_K((const orc_block_q4_K *)x, y, nb); break;
         case ORC_Q6_K:   dequant_q6_K((const orc_block_q6_K *)x, y, nb); break;
         case ORC_IQ4_XS: dequant_iq4_xs((const orc_block_iq4_xs *)x, y, nb); break;
+        case ORC_Q5_K:   dequant_q5_K((const orc_block_q5_K *)x, y, nb); break;
+        case ORC_IQ4_NL: dequant_iq4_nl((const orc_block_iq4_nl *)x, y, nb); break;
         default: break;
     }
 }
@@ -327,6 +368,43 @@ static float dot_iq4_xs(int64_t nb, const orc_block_iq4_xs * x, const orc_block_
     return sumf;
 }
 
+/* Q4_K's combine with 5-bit codes (ggml's vec_dot_q5_K_q8_K, generic form) */
+static float dot_q5_K(int64_t nb, const orc_block_q5_K * x, const orc_block_q8_K * y) {
+    float sumf = 0.0f;
+    for (int64_t i = 0; i < nb; ++i) {
+        int sum_sc = 0, sum_m = 0;
+        for (int j = 0; j < 8; ++j) {
+            uint8_t sc, m;
+            scale_min_k4(j, x[i].scales, &sc, &m);
+            const uint8_t * q = x[i].qs + 32 * (j / 2);
+            const int8_t * a = y[i].qs + 32 * j;
+            const int shift = 4 * (j & 1);
+            int s = 0;
+            for (int l = 0; l < 32; ++l) s += (((q[l] >> shift) & 0xF) | (((x[i].qh[l] >> j) & 1) << 4)) * a[l];
+            sum_sc += sc * s;
+            sum_m += m * (y[i].bsums[2 * j] + y[i].bsums[2 * j + 1]);
+        }
+        const float d = orc_fp16_to_fp32(x[i].d) * y[i].d, dmin = orc_fp16_to_fp32(x[i].dmin) * y[i].d;
+        sumf += d * (float)sum_sc;
+        sumf -= dmin * (float)sum_m;
+    }
+    return sumf;
+}
+
+/* Q4_0's combine with codebook values (ggml's vec_dot_iq4_nl_q8_0) */
+static float dot_iq4_nl(int64_t nb, const orc_block_iq4_nl * x, const orc_block_q8_0 * y) {
+    float sumf = 0.0f;
+    for (int64_t i = 0; i < nb; ++i) {
+        int sumi = 0;
+        for (int j = 0; j < 16; ++j) {
+            sumi += kvalues_iq4nl[x[i].qs[j] & 0xF] * y[i].qs[j];
+            sumi += kvalues_iq4nl[x[i].qs[j] >> 4] * y[i].qs[j + 16];
+        }
+        sumf += (orc_fp16_to_fp32(y[i].d) * orc_fp16_to_fp32(x[i].d)) * (float)sumi;
+    }
+    return sumf;
+}
+
 float orc_vec_dot(int type, int64_t k, const void * w, const void * xq) {
     switch (type) {
         case ORC_Q4_0:   return dot_q4_0(k / 32, (const orc_block_q4_0 *)w, (const orc_block_q8_0 *)xq);
@@ -334,6 +412,8 @@ float orc_vec_dot(int type, int64_t k, const void * w, const void * xq) {
         case ORC_Q4_K:   return dot_q4_K(k / 256, (const orc_block_q4_K *)w, (const orc_block_q8_K *)xq);
         case ORC_Q6_K:   return dot_q6_K(k / 256, (const orc_block_q6_K *)w, (const orc_block_q8_K *)xq);
         case ORC_IQ4_XS: return dot_iq4_xs(k / 256, (const orc_block_iq4_xs *)w, (const orc_block_q8_K *)xq);
+        case ORC_Q5_K:   return dot_q5_K(k / 256, (const orc_block_q5_K *)w, (const orc_block_q8_K *)xq);
+        case ORC_IQ4_NL: return dot_iq4_nl(k / 32, (const orc_block_iq4_nl *)w, (const orc_block_q8_0 *)xq);
         default: return NAN;
     }
 }

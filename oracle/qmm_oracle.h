@@ -44,10 +44,13 @@ typedef struct { orc_half d; int8_t  qs[ORC_QK8_0]; } orc_block_q8_0;           
 typedef struct { orc_half d; orc_half dmin; uint8_t scales[12]; uint8_t qs[ORC_QK_K / 2]; } orc_block_q4_K; /* 144 */
 typedef struct { uint8_t ql[ORC_QK_K / 2]; uint8_t qh[ORC_QK_K / 4]; int8_t scales[ORC_QK_K / 16]; orc_half d; } orc_block_q6_K; /* 210 */
 typedef struct { orc_half d; uint16_t scales_h; uint8_t scales_l[ORC_QK_K / 64]; uint8_t qs[ORC_QK_K / 2]; } orc_block_iq4_xs; /* 136 */
+typedef struct { orc_half d; orc_half dmin; uint8_t scales[12]; uint8_t qh[ORC_QK_K / 8]; uint8_t qs[ORC_QK_K / 2]; } orc_block_q5_K; /* 176 */
+typedef struct { orc_half d; uint8_t qs[ORC_QK4_0 / 2]; } orc_block_iq4_nl;                /* 18  */
 typedef struct { float d; int8_t qs[ORC_QK_K]; int16_t bsums[ORC_QK_K / 16]; } orc_block_q8_K; /* 292 */
 
 /* type ids as ggml_type */
-enum { ORC_Q4_0 = 2, ORC_Q8_0 = 8, ORC_Q4_K = 12, ORC_Q6_K = 14, ORC_Q8_K = 15, ORC_IQ4_XS = 23 };
+enum { ORC_Q4_0 = 2, ORC_Q8_0 = 8, ORC_Q4_K = 12, ORC_Q5_K = 13, ORC_Q6_K = 14, ORC_Q8_K = 15, ORC_IQ4_NL = 20,
+       ORC_IQ4_XS = 23 };
 
 float    orc_fp16_to_fp32(orc_half h);
 orc_half orc_fp32_to_fp16(float f);          /* round to nearest even, like F16C imm 0 */
@@ -57,7 +60,7 @@ const int8_t * orc_kvalues_iq4nl(void);
 void orc_dequantize_row(int type, const void * x, float * y, int64_t k);
 void orc_quantize_row_q8_0(const float * x, void * y, int64_t k);
 void orc_quantize_row_q8_K(const float * x, void * y, int64_t k);
-/* from_float of the vec_dot type of `type` (q8_0 for Q4_0/Q8_0, q8_K else) */
+/* from_float of the vec_dot type of `type` (q8_0 for Q4_0/Q8_0/IQ4_NL, q8_K else) */
 void orc_quantize_act(int type, const float * x, void * y, int64_t k);
 size_t orc_act_row_size(int type, int64_t k);
 

@@ -16,7 +16,9 @@ from conftest import rel_err
 
 pytestmark = pytest.mark.gpu
 
-TYPES = [qmm.Q4_0, qmm.Q8_0, qmm.Q4_K, qmm.Q6_K, qmm.IQ4_XS]
+TYPES = [qmm.Q4_0, qmm.Q8_0, qmm.Q4_K, qmm.Q5_K, qmm.Q6_K, qmm.IQ4_NL, qmm.IQ4_XS]
+# the types whose 3..8-column products run on the MFMA GEMV
+MMA_TYPES = (qmm.Q4_0, qmm.Q8_0, qmm.Q4_K, qmm.IQ4_XS, qmm.IQ4_NL)
 TOL = 1e-3
 
 
@@ -83,7 +85,7 @@ def special_blocks(qtype, nblk, seed):
     doff = 208 if qtype == qmm.Q6_K else 0
     for i, bits in enumerate([0x0000, 0x8000, 0x0001, 0x7BFF, 0x03FF, 0xFBFF]):
         raw[i, doff:doff + 2] = np.frombuffer(np.uint16(bits).tobytes(), np.uint8)
-        if qtype == qmm.Q4_K:
+        if qtype in (qmm.Q4_K, qmm.Q5_K):
             raw[i, 2:4] = np.frombuffer(np.uint16(bits).tobytes(), np.uint8)
     return raw.ravel()
 
@@ -348,7 +350,7 @@ def test_mul_mat_gemv(be, sc, orc, qtype, N):
     say("gemv", qtype, M, K, N)
     got, ref = run_mul_mat(be, sc, orc, qtype, M, K, N, seed=51)
     # 3..8 columns of the types the MFMA kernel decodes run on it
-    mma = N >= 3 and qtype != qmm.Q6_K
+    mma = N >= 3 and qtype in MMA_TYPES
     assert be.last_path() == ("gemv-mfma" if mma else "gemv")
     assert rel_err(got, ref) <= TOL
 
@@ -359,6 +361,18 @@ def test_mul_mat_k_shapes(be, sc, orc, qtype, K):
     M, N = 129, 1
     say("gemv-k", qtype, M, K, N)
     got, ref = run_mul_mat(be, sc, orc, qtype, M, K, N, seed=52)
+    assert rel_err(got, ref) <= TOL
+
+
+@pytest.mark.parametrize("qtype", [qmm.Q4_0, qmm.Q8_0, qmm.IQ4_NL])
+@pytest.mark.parametrize("K", [640, 32 * 13])
+@pytest.mark.parametrize("N", [1, 5, 20])
+def test_mul_mat_k_not_whole_groups(be, sc, orc, qtype, K, N):
+    """32-weight block types with K not a multiple of 256 (the reference's IQ4_NL down
+    projections have K = 640, P01:3414-3416): the last group is zero-padded in the image"""
+    M = 200
+    say("k-partial", qtype, M, K, N)
+    got, ref = run_mul_mat(be, sc, orc, qtype, M, K, N, seed=53)
     assert rel_err(got, ref) <= TOL
 
 
@@ -466,6 +480,7 @@ FULL = [
     (qmm.Q4_0, 4096, 4096), (qmm.Q4_0, 11008, 4096), (qmm.Q4_0, 4096, 11008),
     (qmm.Q4_K, 17408, 5120), (qmm.Q6_K, 5120, 17408), (qmm.Q4_K, 12288, 5120),
     (qmm.IQ4_XS, 14336, 4096), (qmm.IQ4_XS, 4096, 14336), (qmm.Q8_0, 14336, 4096), (qmm.Q8_0, 4096, 14336),
+    (qmm.Q5_K, 17408, 5120), (qmm.Q5_K, 5120, 17408), (qmm.IQ4_NL, 14336, 4096), (qmm.IQ4_NL, 4096, 14336),
 ]
 
 
@@ -482,7 +497,7 @@ def test_full_size_gemv(be, sc, orc, qtype, M, K, N):
 @pytest.mark.parametrize("M,K,N", [(300, 1024, 16), (129, 2048, 37), (64, 512, 64), (500, 768, 130),
                                    (200, 256, 40), (70, 800, 20), (1000, 512, 300)])
 def test_mul_mat_gemm(be, sc, orc, qtype, M, K, N):
-    if K % 256 and qtype not in (qmm.Q4_0, qmm.Q8_0):
+    if K % 256 and qtype not in (qmm.Q4_0, qmm.Q8_0, qmm.IQ4_NL):
         K = 1024
     say("gemm", qtype, M, K, N)
     got, ref = run_mul_mat(be, sc, orc, qtype, M, K, N, seed=57)
@@ -490,7 +505,7 @@ def test_mul_mat_gemm(be, sc, orc, qtype, M, K, N):
     assert rel_err(got, ref) <= TOL
 
 
-@pytest.mark.parametrize("qtype", [qmm.Q6_K, qmm.Q4_K, qmm.Q4_0])
+@pytest.mark.parametrize("qtype", [qmm.Q6_K, qmm.Q4_K, qmm.Q5_K, qmm.Q4_0, qmm.IQ4_NL])
 def test_mul_mat_gemm_broadcast_and_strides(be, sc, orc, qtype):
     say("gemm-broadcast", qtype)
     K, M, N = 512, 80, 21
@@ -518,7 +533,7 @@ def test_mul_mat_gemm_broadcast_and_strides(be, sc, orc, qtype):
 GEMM_FULL = [
     (qmm.Q4_0, 4096, 4096, 512), (qmm.Q4_0, 11008, 4096, 64), (qmm.Q4_0, 4096, 11008, 64),
     (qmm.Q4_K, 17408, 5120, 64), (qmm.Q6_K, 5120, 17408, 64), (qmm.IQ4_XS, 4096, 14336, 32),
-    (qmm.Q8_0, 14336, 4096, 32),
+    (qmm.Q8_0, 14336, 4096, 32), (qmm.Q5_K, 17408, 5120, 64), (qmm.IQ4_NL, 4096, 14336, 32),
 ]
 
 

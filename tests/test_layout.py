@@ -16,9 +16,11 @@ import pytest
 from arcint_amd import qmm, synth
 from conftest import rel_err
 
-TYPES = [qmm.Q4_0, qmm.Q8_0, qmm.Q4_K, qmm.Q6_K, qmm.IQ4_XS]
+TYPES = [qmm.Q4_0, qmm.Q8_0, qmm.Q4_K, qmm.Q5_K, qmm.Q6_K, qmm.IQ4_NL, qmm.IQ4_XS]
 # type -> (chunk planes, tail bytes per row)
-PLANES = {qmm.Q4_0: (9, 0), qmm.Q8_0: (17, 0), qmm.Q4_K: (9, 0), qmm.Q6_K: (13, 2), qmm.IQ4_XS: (8, 8)}
+PLANES = {qmm.Q4_0: (9, 0), qmm.Q8_0: (17, 0), qmm.Q4_K: (9, 0), qmm.Q5_K: (11, 0), qmm.Q6_K: (13, 2),
+          qmm.IQ4_NL: (9, 0), qmm.IQ4_XS: (8, 8)}
+KV = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], np.int64)
 
 
 def shapes(qtype):
@@ -46,12 +48,15 @@ def test_pack_unpack_roundtrip(qtype):
 
 def expected_pieces(qtype, p):
     """(src offset in the block, size, chunk, byte in the chunk row, tail?) for block slot p"""
-    if qtype == qmm.Q4_0:
+    if qtype in (qmm.Q4_0, qmm.IQ4_NL):
         return [(2, 16, p, 0, False), (0, 2, 8, 2 * p, False)]
     if qtype == qmm.Q8_0:
         return [(2, 16, 2 * p, 0, False), (18, 16, 2 * p + 1, 0, False), (0, 2, 16, 2 * p, False)]
     if qtype == qmm.Q4_K:
         return [(16 + 16 * c, 16, c, 0, False) for c in range(8)] + [(0, 16, 8, 0, False)]
+    if qtype == qmm.Q5_K:   # d, dmin, scales[12] | qh[32] | qs[128]
+        return ([(48 + 16 * c, 16, c, 0, False) for c in range(8)] + [(0, 16, 8, 0, False)]
+                + [(16, 16, 9, 0, False), (32, 16, 10, 0, False)])
     if qtype == qmm.Q6_K:
         return ([(16 * c, 16, c, 0, False) for c in range(8)] + [(128 + 16 * c, 16, 8 + c, 0, False) for c in range(4)]
                 + [(192, 16, 12, 0, False), (208, 2, None, 0, True)])
@@ -133,7 +138,7 @@ def emulate_gemv(qtype, img, K, M, codes, xd, bsums):
     xg = xc.reshape(G, 256)
     acc = np.zeros(M, np.float64)
     lo, hi = ch & 15, ch >> 4
-    if qtype in (qmm.Q4_0, qmm.Q8_0):
+    if qtype in (qmm.Q4_0, qmm.Q8_0, qmm.IQ4_NL):
         nb = K // 32
         xdp = np.zeros(G * 8, np.float32)
         xdp[:nb] = xd
@@ -143,6 +148,8 @@ def emulate_gemv(qtype, img, K, M, codes, xd, bsums):
             xa, xb = xg[:, 32 * p:32 * p + 16], xg[:, 32 * p + 16:32 * p + 32]
             if qtype == qmm.Q4_0:
                 s = (lo[:, :, p] * xa).sum(-1) + (hi[:, :, p] * xb).sum(-1) - 8 * (xa.sum(-1) + xb.sum(-1))
+            elif qtype == qmm.IQ4_NL:
+                s = (KV[lo[:, :, p]] * xa).sum(-1) + (KV[hi[:, :, p]] * xb).sum(-1)
             else:
                 w0 = ch[:, :, 2 * p].astype(np.uint8).view(np.int8).astype(np.int64)
                 w1 = ch[:, :, 2 * p + 1].astype(np.uint8).view(np.int8).astype(np.int64)
@@ -150,7 +157,12 @@ def emulate_gemv(qtype, img, K, M, codes, xd, bsums):
             acc += (s * (dw * xdp[:, p])).sum(-1)
         return acc
     bs = bsums.reshape(G, 16)
-    if qtype == qmm.Q4_K:
+    if qtype in (qmm.Q4_K, qmm.Q5_K):
+        if qtype == qmm.Q5_K:   # fifth bits: byte 16 (c % 2) + i of qh, bit 2 (c // 2) (low) / + 1 (high)
+            for c in range(8):
+                qh = ch[:, :, 9 + (c & 1)]
+                lo[:, :, c] |= ((qh >> (2 * (c // 2))) & 1) << 4
+                hi[:, :, c] |= ((qh >> (2 * (c // 2) + 1)) & 1) << 4
         h = ch[:, :, 8].astype(np.uint8)
         d, dmin = f16(h[..., 0], h[..., 1]), f16(h[..., 2], h[..., 3])
         w = h.view(np.uint32).astype(np.uint64)             # [M, G, 4] dwords
@@ -214,6 +226,7 @@ PLAN_SHAPES = [
     (qmm.Q4_K, 5120, 17408, 1), (qmm.Q4_K, 5120, 17408, 4), (qmm.Q6_K, 17408, 5120, 1), (qmm.Q6_K, 5120, 151936, 1),
     (qmm.Q4_0, 4096, 4096, 1), (qmm.Q4_0, 11008, 4096, 8), (qmm.Q8_0, 4096, 14336, 8), (qmm.IQ4_XS, 14336, 4096, 2),
     (qmm.Q4_0, 352, 65, 3), (qmm.Q4_K, 256, 1, 1), (qmm.Q8_0, 32, 5, 8), (qmm.IQ4_XS, 512, 2048, 5),
+    (qmm.Q5_K, 5120, 17408, 1), (qmm.Q5_K, 4096, 4096, 6), (qmm.IQ4_NL, 640, 4096, 1), (qmm.IQ4_NL, 4096, 14336, 8),
 ]
 
 
@@ -223,7 +236,7 @@ def test_gemv_plan(qtype, K, M, N):
     info = qmm.describe_mul_mat(qmm.Tensor(fake, qtype, (K, M)), qmm.Tensor(fake, qmm.F32, (K, N)),
                                 qmm.Tensor(fake, qmm.F32, (M, N)))
     # the MFMA kernel takes 3..8 columns of the types whose blocks it decodes
-    mma = N >= 3 and qtype in (qmm.Q4_0, qmm.Q8_0, qmm.Q4_K, qmm.IQ4_XS)
+    mma = N >= 3 and qtype in (qmm.Q4_0, qmm.Q8_0, qmm.Q4_K, qmm.IQ4_XS, qmm.IQ4_NL)
     assert info["path"] == ("gemv-mfma" if mma else "gemv")
     G, nt = -(-K // 256), -(-M // 64)
     W, KS, spw, nc = info["k_waves"], info["k_slices"], info["groups_per_wave"], info["cols_per_task"]
@@ -239,7 +252,7 @@ def test_gemv_plan(qtype, K, M, N):
         # bytes, then per column and group the codes (272 B), Q4_K split sums (16 B) and the
         # scales (4 B per block); the W waves' sums reuse it
         assert 1 <= tw <= 4 and W * tw <= 4 and W * spw <= 24
-        nsb = 8 if qtype in (qmm.Q4_0, qmm.Q8_0) else 1
+        nsb = 8 if qtype in (qmm.Q4_0, qmm.Q8_0, qmm.IQ4_NL) else 1
         stage = 256 + W * spw * 8 * (272 + (16 if qtype == qmm.Q4_K else 0) + 4 * nsb)
         assert info["lds_bytes"] == max(stage, W * tw * 8 * 64 * 4 if W > 1 else 0)
     else:

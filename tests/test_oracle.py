@@ -163,25 +163,88 @@ def test_iq4_xs_scales_and_positions(orc):
             assert np.array_equal(y, exp), (ib, j)
 
 
-@pytest.mark.parametrize("qtype", [O.Q4_0, O.Q8_0])
+def test_iq4_nl_known_answer_and_equals_iq4_xs_at_unit_scales(orc):
+    # weight j (j < 16) = d * kv[low nibble of byte j], j + 16: d * kv[high nibble]
+    kv = orc.kvalues()
+    for v in (0x00, 0x98, 0xF0, 0x3C, 0xFF):
+        y = orc.dequantize(O.IQ4_NL, np.frombuffer(f16(0.5) + bytes([v] * 16), np.uint8), 32)
+        assert np.all(y[:16] == 0.5 * kv[v & 15]) and np.all(y[16:] == 0.5 * kv[v >> 4])
+    # an IQ4_XS super-block with every ls = 33 (scale ls - 32 = 1) is 8 IQ4_NL blocks of its d
+    g = np.random.default_rng(8)
+    for _ in range(20):
+        d = np.float16(abs(g.normal(0, 0.02)))
+        qs = g.integers(0, 256, 128, dtype=np.uint8)
+        xs = f16(d) + np.uint16(0b10_10_10_10_10_10_10_10).tobytes() + bytes([0x11] * 4) + qs.tobytes()
+        nl = b"".join(f16(d) + qs[16 * i:16 * i + 16].tobytes() for i in range(8))
+        assert np.array_equal(orc.dequantize(O.IQ4_XS, np.frombuffer(xs, np.uint8), 256),
+                              orc.dequantize(O.IQ4_NL, np.frombuffer(nl, np.uint8), 256))
+
+
+def _q5k_block(d, dmin, scales12, qh32, qs128):
+    return np.frombuffer(f16(d) + f16(dmin) + np.asarray(scales12, np.uint8).tobytes()
+                         + np.asarray(qh32, np.uint8).tobytes() + np.asarray(qs128, np.uint8).tobytes(), np.uint8)
+
+
+def test_q5_K_without_fifth_bits_is_q4_K(orc):
+    g = np.random.default_rng(9)
+    for _ in range(50):
+        d, dmin = np.float16(abs(g.normal(0, 0.02))), np.float16(abs(g.normal(0, 0.02)))
+        sc12, qs = g.integers(0, 256, 12), g.integers(0, 256, 128)
+        assert np.array_equal(orc.dequantize(O.Q5_K, _q5k_block(d, dmin, sc12, [0] * 32, qs), 256),
+                              orc.dequantize(O.Q4_K, _q4k_block(d, dmin, sc12, qs), 256))
+
+
+def test_q5_K_fifth_bit_positions(orc):
+    # qh[l] bit 2c adds 16 to weight 64c + l (low nibble), bit 2c + 1 to weight 64c + 32 + l
+    sc12 = [1, 1, 1, 1, 0, 0, 0, 0, 1, 1, 1, 1]   # every sub-block scale 1, min 0
+    for c in range(4):
+        for hi in (0, 1):
+            for l in (0, 13, 31):
+                qh = [0] * 32
+                qh[l] = 1 << (2 * c + hi)
+                y = orc.dequantize(O.Q5_K, _q5k_block(2.0, 3.0, sc12, qh, [0] * 128), 256)
+                assert list(np.nonzero(y)[0]) == [64 * c + 32 * hi + l]
+                assert y[64 * c + 32 * hi + l] == 2.0 * 16
+
+
+def test_q5_K_rounding_only_in_the_subtract(orc):
+    g = np.random.default_rng(10)
+    for _ in range(100):
+        d, dmin = np.float16(abs(g.normal(0, 0.02))), np.float16(abs(g.normal(0, 0.02)))
+        sc12, qh, qs = g.integers(0, 256, 12), g.integers(0, 256, 32), g.integers(0, 256, 128)
+        y = orc.dequantize(O.Q5_K, _q5k_block(d, dmin, sc12, qh, qs), 256)
+        y1 = orc.dequantize(O.Q4_K, _q4k_block(1.0, 1.0, sc12, [0x11] * 128), 256)
+        y0 = orc.dequantize(O.Q4_K, _q4k_block(1.0, 1.0, sc12, [0x00] * 128), 256)
+        for w in range(256):
+            c, r = divmod(w, 64)
+            hi, l = divmod(r, 32)
+            code = ((qs[32 * c + l] >> (4 * hi)) & 15) | (((qh[l] >> (2 * c + hi)) & 1) << 4)
+            m = -y0[w]
+            sc = y1[w] + m
+            d1 = np.float32(d) * np.float32(sc)           # exact
+            m1 = np.float32(dmin) * np.float32(m)         # exact
+            assert y[w] == np.float32(d1 * np.float32(code)) - m1   # d1 * code exact (22 bits)
+
+
+@pytest.mark.parametrize("qtype", [O.Q4_0, O.Q8_0, O.IQ4_NL])
 def test_q4_0_q8_0_values_are_exact_multiples_of_d(orc, qtype):
     from arcint_amd import synth
     raw = synth.weights(qtype, 64, 256, seed=5)
     y = orc.dequantize(qtype, raw, 64 * 256).reshape(-1, 32)
-    bs = 18 if qtype == O.Q4_0 else 34
+    bs = 34 if qtype == O.Q8_0 else 18
     d = raw.reshape(-1, bs)[:, :2].copy().view(np.float16).astype(np.float64)
     q = y.astype(np.float64) / d
     assert np.array_equal(q, np.round(q))
 
 
-@pytest.mark.parametrize("qtype", [O.Q4_0, O.Q8_0, O.Q4_K, O.Q6_K, O.IQ4_XS])
+@pytest.mark.parametrize("qtype", [O.Q4_0, O.Q8_0, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ4_NL, O.IQ4_XS])
 def test_dequant_special_scales(orc, qtype):
     from arcint_amd import synth
     blck, bs = O.TYPES[qtype][:2]
     raw = synth.weights(qtype, 1, blck, seed=1).copy()
     doff = 208 if qtype == O.Q6_K else 0
     raw[doff:doff + 2] = np.frombuffer(f16(0.0), np.uint8)
-    if qtype == O.Q4_K:
+    if qtype in (O.Q4_K, O.Q5_K):
         raw[2:4] = np.frombuffer(f16(0.0), np.uint8)
     assert np.all(orc.dequantize(qtype, raw, blck) == 0)
     raw[doff:doff + 2] = np.frombuffer(np.uint16(1).tobytes(), np.uint8)     # smallest subnormal d
@@ -249,7 +312,7 @@ def _deq_q8(qtype, xq, k):
     return (b[:, 4:260].view(np.int8).astype(np.float64) * b[:, 0:4].copy().view(np.float32).astype(np.float64)).ravel()
 
 
-@pytest.mark.parametrize("qtype", [O.Q4_0, O.Q8_0, O.Q4_K, O.Q6_K, O.IQ4_XS])
+@pytest.mark.parametrize("qtype", [O.Q4_0, O.Q8_0, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ4_NL, O.IQ4_XS])
 @pytest.mark.parametrize("k", [256, 512, 2048])
 def test_vec_dot_textbook_identity(orc, qtype, k):
     from arcint_amd import synth
