@@ -333,14 +333,14 @@ __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per 
                     // (q - 16) s = q4 s - 16 s (1 - hb), hb = bit j of qh (j = the sub-block): q4 s < 128, so
                     // the offset-binary subtract borrows nothing across bytes; the result is in [-112, 105]
                     const int j = 4 * hh + ql + t;
-                    const uint32_t qh[4] = { R.q5h.x, R.q5h.y, R.q5h.z, R.q5h.w };
-                    uint32_t *ph[4] = { &vh.x, &vh.y, &vh.z, &vh.w }, *pl[4] = { &vl.x, &vl.y, &vl.z, &vl.w };
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const uint32_t nhb = (~qh[i] >> j) & 0x01010101u;
-                        *ph[i] = ((*ph[i] | 0x80808080u) - v2_mul(nhb, 16 * sh)) ^ 0x80808080u;
-                        *pl[i] = ((*pl[i] | 0x80808080u) - v2_mul(nhb, 16 * sl)) ^ 0x80808080u;
-                    }
+                    auto fix = [&](uint32_t v, uint32_t qh, uint32_t s) {
+                        const uint32_t nhb = (~qh >> j) & 0x01010101u;
+                        return ((v | 0x80808080u) - v2_mul(nhb, 16 * s)) ^ 0x80808080u;
+                    };
+                    vh.x = fix(vh.x, R.q5h.x, sh); vl.x = fix(vl.x, R.q5h.x, sl);
+                    vh.y = fix(vh.y, R.q5h.y, sh); vl.y = fix(vl.y, R.q5h.y, sl);
+                    vh.z = fix(vh.z, R.q5h.z, sh); vl.z = fix(vl.z, R.q5h.z, sl);
+                    vh.w = fix(vh.w, R.q5h.w, sh); vl.w = fix(vl.w, R.q5h.w, sl);
                 }
                 uint8_t * b = B + (((st_tile * 4 + ql + t) * 2 + h) * 2) * kChunk + st_row * 16;
                 *reinterpret_cast<uint4 *>(b) = vh;
@@ -539,22 +539,29 @@ __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per 
                     const float2 dd = reinterpret_cast<const float2 *>(W + 2 * 64 * 16)[row];
                     const v4i bmin = h ? zero : *reinterpret_cast<const v4i *>(W + row * 16);
                     // (KSPLIT 2: the tile's second wave adds no min term; its sums meet wave 0's)
-                    v16i mh = v16i{}, ml = v16i{}, sh = v16i{}, sl = v16i{};
+                    v16i mh = v16i{}, ml = v16i{};
                     if (KSPLIT == 1 || wk == 0) {
-                        mh = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, bmin, v16i{}, 0, 0, 0);
-                        ml = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, bmin, v16i{}, 0, 0, 0);
-                        if constexpr (Q5) {                       // sum_j sc_j bsum_j: k 8..15 of the row
+                        if constexpr (Q5) {
+                            // sum_j sc_j bsum_j (k 8..15 of the row) times 16, into c2 (isc = 8 c1 + c2) one
+                            // MFMA result at a time
                             const v4i ash = h ? zero : v4i{ 0, 0, sv.x, sv.y };
                             const v4i asl = h ? zero : v4i{ 0, 0, sv.z, sv.w };
-                            sh = __builtin_amdgcn_mfma_i32_32x32x32_i8(ash, bmin, v16i{}, 0, 0, 0);
-                            sl = __builtin_amdgcn_mfma_i32_32x32x32_i8(asl, bmin, v16i{}, 0, 0, 0);
+                            const v16i sh = __builtin_amdgcn_mfma_i32_32x32x32_i8(ash, bmin, v16i{}, 0, 0, 0);
+#pragma unroll
+                            for (int r = 0; r < 16; ++r) c2[rt][r] += 1024 * sh[r];
+                            __builtin_amdgcn_sched_barrier(0);
+                            const v16i sl = __builtin_amdgcn_mfma_i32_32x32x32_i8(asl, bmin, v16i{}, 0, 0, 0);
+#pragma unroll
+                            for (int r = 0; r < 16; ++r) c2[rt][r] += 16 * sl[r];
+                            __builtin_amdgcn_sched_barrier(0);
                         }
+                        mh = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, bmin, v16i{}, 0, 0, 0);
+                        ml = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, bmin, v16i{}, 0, 0, 0);
                     }
                     v16f & o = rt ? out1 : out0;
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
-                        int isc = 8 * c1[rt][r] + c2[rt][r];
-                        if constexpr (Q5) isc += 16 * (64 * sh[r] + sl[r]);
+                        const int isc = 8 * c1[rt][r] + c2[rt][r];
                         const int imn = 64 * mh[r] + ml[r];
                         o[r] += dx[r] * (dd.x * (float)isc - dd.y * (float)imn);
                     }
@@ -662,7 +669,8 @@ struct G2Shape {
     int BN, KS, spk;
     int64_t mt, nt, P;
 };
-G2Shape g2_shape(const WView & w, int64_t N, int64_t nbatch) {
+// (Q5_K takes 64-column tiles only: at 128 its registers spill)
+G2Shape g2_shape(int type, const WView & w, int64_t N, int64_t nbatch) {
     static const int64_t cus = [] {
         const char * e = getenv("QMM_GEMM_CUS");
         return e ? std::max<int64_t>(1, atoll(e)) : (int64_t)256;
@@ -679,6 +687,7 @@ G2Shape g2_shape(const WView & w, int64_t N, int64_t nbatch) {
         }
     };
     for (int bn : { 128, 64 }) {
+        if (bn == 128 && type == QMM_TYPE_Q5_K) continue;
         const double c = 2.0 * (bn == 64 ? 0.62 : 1.0);           // us per stage
         const int64_t nt = (N + bn - 1) / bn, T = mt * nt;
         int64_t prev_gps = -1;
@@ -714,17 +723,17 @@ G2Shape g2_shape(const WView & w, int64_t N, int64_t nbatch) {
 
 }  // namespace
 
-int gemm_kslices(const WView & w, int64_t N, int64_t nbatch) { return g2_shape(w, N, nbatch).KS; }
+int gemm_kslices(int type, const WView & w, int64_t N, int64_t nbatch) { return g2_shape(type, w, N, nbatch).KS; }
 
-int64_t gemm_zero_from(const WView & w, int64_t N, int64_t nbatch) {
-    const G2Shape sh = g2_shape(w, N, nbatch);
+int64_t gemm_zero_from(int type, const WView & w, int64_t N, int64_t nbatch) {
+    const G2Shape sh = g2_shape(type, w, N, nbatch);
     if (sh.KS == 1) return w.M;                                   // nothing adds into dst
     return std::min<int64_t>(w.M, sh.P / sh.nt * 128);
 }
 
 void gemm_shape(int type, const WView & w, int64_t N, int64_t nbatch, int64_t * workgroups, int * threads,
                 int * lds_bytes) {
-    const G2Shape sh = g2_shape(w, N, nbatch);
+    const G2Shape sh = g2_shape(type, w, N, nbatch);
     *workgroups = (sh.P + (sh.mt * sh.nt - sh.P) * sh.KS) * nbatch;
     *threads = kT;
     int st;
@@ -743,7 +752,7 @@ hipError_t launch_gemm(int type, const WView & w, const ActBuf & a, int64_t N, i
     if (!a.dT || a.ldk != w.G * 256 || a.ldT < N * nbatch + 64 || N <= 0 || nbatch <= 0 ||
         nbatch > 65535 || a.vdt != vec_dot_type(type) || ((type == QMM_TYPE_Q4_K || type == QMM_TYPE_Q5_K) && !a.bsp))
         return hipErrorInvalidValue;
-    const G2Shape sh = g2_shape(w, N, nbatch);
+    const G2Shape sh = g2_shape(type, w, N, nbatch);
     G2Params p{};
     p.w = w;
     p.xc = a.codes;
@@ -777,7 +786,7 @@ hipError_t launch_gemm(int type, const WView & w, const ActBuf & a, int64_t N, i
     if (type == QMM_TYPE_Q4_K)
         return sh.BN == 64 ? launch_t<QMM_TYPE_Q4_K, 64>(p, g, s, kt) : launch_t<QMM_TYPE_Q4_K, 128>(p, g, s, kt);
     if (type == QMM_TYPE_Q5_K)
-        return sh.BN == 64 ? launch_t<QMM_TYPE_Q5_K, 64>(p, g, s, kt) : launch_t<QMM_TYPE_Q5_K, 128>(p, g, s, kt);
+        return launch_t<QMM_TYPE_Q5_K, 64>(p, g, s, kt);         // g2_shape takes BN = 64 only
     if (type == QMM_TYPE_IQ4_NL)
         return sh.BN == 64 ? launch_t<QMM_TYPE_IQ4_NL, 64>(p, g, s, kt) : launch_t<QMM_TYPE_IQ4_NL, 128>(p, g, s, kt);
     return hipErrorInvalidValue;

@@ -562,61 +562,72 @@ __device__ __forceinline__ uint4 nib(const uint4 & q, int sh) {
     return make_uint4((q.x >> sh) & m, (q.y >> sh) & m, (q.z >> sh) & m, (q.w >> sh) & m);
 }
 
-// Accumulators of the output lane: element 4 t + r = rows 32 t + l % 32, column 4 (l / 32) + r.
-// Each consume step ends with an empty asm on the whole vector: otherwise the compiler sinks
-// every block's consumption below all the MFMAs and keeps their 16-register results live.
-typedef int v8i __attribute__((ext_vector_type(8)));
-typedef float v8f __attribute__((ext_vector_type(8)));
+// Accumulators of the output lane.  A task has up to CM columns (8, 16 or 32: the MFMA's A
+// operand holds 32); NR = CM / 2 registers of each 32-row MFMA result carry them: register r
+// of lane l is column 8 (r / 4) + 4 (l / 32) + r % 4 of row l % 32.  Element NR t + r of the
+// accumulator is register r of row tile t (rows 32 t + l % 32).  Each consume step ends with
+// an empty asm on the whole vector: otherwise the compiler sinks every block's consumption
+// below all the MFMAs and keeps their 16-register results live.
+template <int N> using vNi = int __attribute__((ext_vector_type(N)));
+template <int N> using vNf = float __attribute__((ext_vector_type(N)));
 
-// acc[4 t + r] += s_t * e_t[r] for the output registers r < 4 of rows 0-31 (t = 0) and 32-63;
-// the products fit 24 bits (full-rate multiplies)
-__device__ __forceinline__ void scale_add(const v16i & e0, const v16i & e1, int s0, int s1, v8i & acc) {
+// column of accumulator register r (of a row tile) for lane half h
+__host__ __device__ constexpr int mma_col(int r, int h) { return 8 * (r / 4) + 4 * h + (r & 3); }
+
+// acc[NR t + r] += s_t * e_t[r]; the products fit 24 bits (full-rate multiplies)
+template <int NR>
+__device__ __forceinline__ void scale_add(const v16i & e0, const v16i & e1, int s0, int s1, vNi<2 * NR> & acc) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < NR; ++r) {
         acc[r] += __mul24(s0, e0[r]);
-        acc[4 + r] += __mul24(s1, e1[r]);
+        acc[NR + r] += __mul24(s1, e1[r]);
     }
     asm volatile("" : "+v"(acc));
 }
-// out[4 t + r] += (i * dw_t) * dx[r] with i read from the magic-biased result e_t[r]: the bits
+// out[NR t + r] += (i * dw_t) * dx[r] with i read from the magic-biased result e_t[r]: the bits
 // of 12582912 + i, so fma(bits as float, dw, -12582912 dw) is i dw rounded once
-__device__ __forceinline__ void bf_epilogue(const v16i & e0, const v16i & e1, float dw0, float dw1, const float4 & dx4,
-                                            v8f & out) {
+template <int NR>
+__device__ __forceinline__ void bf_epilogue(const v16i & e0, const v16i & e1, float dw0, float dw1, const float (&dx)[NR],
+                                            vNf<2 * NR> & out) {
     const float nm0 = -12582912.0f * dw0, nm1 = -12582912.0f * dw1;
-    const float dx[4] = { dx4.x, dx4.y, dx4.z, dx4.w };
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < NR; ++r) {
         const int i0 = e0[r], i1 = e1[r];
         out[r] = __builtin_fmaf(__builtin_fmaf(__builtin_bit_cast(float, i0), dw0, nm0), dx[r], out[r]);
-        out[4 + r] = __builtin_fmaf(__builtin_fmaf(__builtin_bit_cast(float, i1), dw1, nm1), dx[r], out[4 + r]);
+        out[NR + r] = __builtin_fmaf(__builtin_fmaf(__builtin_bit_cast(float, i1), dw1, nm1), dx[r], out[NR + r]);
     }
     asm volatile("" : "+v"(out));
 }
 
 // One stage of the MFMA GEMV on the weights rw of the lane's row: A operands from the LDS
-// codes at xag (block b at 32 b), the output columns' scales at xdg (4 floats per block),
-// Q4_K split sums at xsg.  A scheduling barrier per block bounds the live MFMA results: the
-// K-quants issue block j's MFMAs before they consume block j - 1's, Q4_0 / Q8_0 (whose magic
+// codes at xag (block b at 32 b), the scales of the lane's output columns at xdg (CM floats
+// per block, the lane's first at + 4 h), Q4_K split sums at xsg (bh[8], bl[8] of the lane's
+// column).  A scheduling barrier per block bounds the live MFMA results: the K-quants issue
+// block j's MFMAs before they consume block j - 1's, Q4_0 / Q8_0 / IQ4_NL (whose magic
 // accumulator input takes 16 more registers) consume each block's in its own group.
-template <int TYPE>
+template <int TYPE, int CM>
 __device__ __forceinline__ void mma_stage(const uint4 (&rw)[9], int st, const uint8_t * xag, const float * xdg,
-                                          const uint8_t * xsg, int h, const v16i & magic, v8f & out) {
+                                          const uint8_t * xsg, int h, const v16i & magic, vNf<CM> & out) {
+    constexpr int NR = CM / 2;
     constexpr bool KQ = TYPE == QMM_TYPE_Q4_K, IQ = TYPE == QMM_TYPE_IQ4_XS, Q8 = TYPE == QMM_TYPE_Q8_0;
     constexpr bool NLQ = TYPE == QMM_TYPE_IQ4_NL;                // Q4_0's blocks through the codebook
     constexpr bool BF = TYPE == QMM_TYPE_Q4_0 || Q8 || NLQ;
     constexpr int NB = Q8 ? 4 : 8;                                // 32-weight blocks per stage
     auto a_op = [&](int b) -> v4i { return *reinterpret_cast<const v4i *>(xag + 32 * (Q8 ? 4 * st + b : b)); };
-    auto dx_op = [&](int b) -> float4 { return *reinterpret_cast<const float4 *>(xdg + (Q8 ? 4 * st + b : b) * 8); };
-    uint4 as = make_uint4(0, 0, 0, 0);                            // Q4_K: split sums, lanes 0-15
-    if constexpr (KQ) {
-        const uint2 v = *reinterpret_cast<const uint2 *>(xsg);
-        as.x = v.x;
-        as.y = v.y;
-    }
+    // the lane's NR column scales of block b: quads at columns 8 q + 4 h
+    auto dx_op = [&](int b, float (&d)[NR]) {
+        const float * x = xdg + (Q8 ? 4 * st + b : b) * CM;
+#pragma unroll
+        for (int q = 0; q < NR / 4; ++q) {
+            const float4 v = *reinterpret_cast<const float4 *>(x + 8 * q);
+            d[4 * q] = v.x; d[4 * q + 1] = v.y; d[4 * q + 2] = v.z; d[4 * q + 3] = v.w;
+        }
+    };
     if constexpr (BF) {
         const uint32_t dw2[4] = { rw[8].x, rw[8].y, rw[8].z, rw[8].w };
         v4i an = a_op(0);                                     // LDS reads one block ahead
-        float4 dn = dx_op(0);
+        float dn[NR];
+        dx_op(0, dn);
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
             const int blk = Q8 ? 4 * st + b : b;                  // block of the group
@@ -637,20 +648,22 @@ __device__ __forceinline__ void mma_stage(const uint4 (&rw)[9], int st, const ui
             v4i op0, op1;
             swap_halves(lo, hi, op0, op1);
             const v4i av = an;
-            const float4 dxb = dn;
+            float dxb[NR];
+#pragma unroll
+            for (int r = 0; r < NR; ++r) dxb[r] = dn[r];
             if (b + 1 < NB) {
                 an = a_op(b + 1);
-                dn = dx_op(b + 1);
+                dx_op(b + 1, dn);
             }
             const v16i e0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, op0, magic, 0, 0, 0);
             const v16i e1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, op1, magic, 0, 0, 0);
-            bf_epilogue(e0, e1, dw0, dw1, dxb, out);          // consumed in its own block: the
+            bf_epilogue<NR>(e0, e1, dw0, dw1, dxb, out);      // consumed in its own block: the
             __builtin_amdgcn_sched_barrier(0);                // SIMD's other waves cover the latency
         }
     } else if constexpr (KQ) {
         // sub-block j: one MFMA per 32 rows on the raw nibbles, its 6-bit scale applied per
-        // row on the integer result; the min term sum_j m_j (64 bh_j + bl_j) is one MFMA
-        // with A rows 0-7 = bh of columns 0-7 and rows 8-15 = bl (k = j), B = the row's mins
+        // row on the integer result; the min term sum_j m_j (64 bh_j + bl_j) is two MFMAs with
+        // A = bh (then bl) of the lane's column at k = j and B = the row's mins
         const uint4 hd = rw[8];                               // d, dmin | scales[12]
         const uint32_t sc03 = hd.y & 0x3f3f3f3fu, mn03 = hd.z & 0x3f3f3f3fu;
         const uint32_t sc47 = (hd.w & 0x0f0f0f0fu) | ((hd.y >> 2) & 0x30303030u);
@@ -660,7 +673,7 @@ __device__ __forceinline__ void mma_stage(const uint4 (&rw)[9], int st, const ui
         swap_rows(sc47, scw[1][0], scw[1][1]);
         swap_rows(mn03, mnw[0][0], mnw[0][1]);
         swap_rows(mn47, mnw[1][0], mnw[1][1]);
-        v8i isc = {};
+        vNi<CM> isc = {};
         v16i pe0, pe1;
         int ps0 = 0, ps1 = 0;
         v4i an = a_op(0);                                     // LDS reads one block ahead
@@ -673,34 +686,38 @@ __device__ __forceinline__ void mma_stage(const uint4 (&rw)[9], int st, const ui
             if (j + 1 < 8) an = a_op(j + 1);
             const v16i e0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, op0, v16i{}, 0, 0, 0);
             const v16i e1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, op1, v16i{}, 0, 0, 0);
-            if (j > 0) scale_add(pe0, pe1, ps0, ps1, isc);
+            if (j > 0) scale_add<NR>(pe0, pe1, ps0, ps1, isc);
             __builtin_amdgcn_sched_barrier(0);
             pe0 = e0;
             pe1 = e1;
             ps0 = (int)((scw[j >> 2][0] >> (8 * (j & 3))) & 0xffu);
             ps1 = (int)((scw[j >> 2][1] >> (8 * (j & 3))) & 0xffu);
         }
-        scale_add(pe0, pe1, ps0, ps1, isc);
+        scale_add<NR>(pe0, pe1, ps0, ps1, isc);
+        const uint4 sp = *reinterpret_cast<const uint4 *>(xsg);   // zeros for lanes without a column
+        const v4i ah = h ? v4i{} : v4i{ (int)sp.x, (int)sp.y, 0, 0 };
+        const v4i al = h ? v4i{} : v4i{ (int)sp.z, (int)sp.w, 0, 0 };
         const v4i bm0 = h ? v4i{} : v4i{ (int)mnw[0][0], (int)mnw[1][0], 0, 0 };
         const v4i bm1 = h ? v4i{} : v4i{ (int)mnw[0][1], (int)mnw[1][1], 0, 0 };
-        const v4i asp = __builtin_bit_cast(v4i, as);
-        const v16i m0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(asp, bm0, v16i{}, 0, 0, 0);
-        const v16i m1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(asp, bm1, v16i{}, 0, 0, 0);
-        const float4 dx4 = dx_op(0);
-        const float dx0[4] = { dx4.x, dx4.y, dx4.z, dx4.w };
+        const v16i mh0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, bm0, v16i{}, 0, 0, 0);
+        const v16i ml0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, bm0, v16i{}, 0, 0, 0);
+        const v16i mh1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, bm1, v16i{}, 0, 0, 0);
+        const v16i ml1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, bm1, v16i{}, 0, 0, 0);
+        float dx0[NR];
+        dx_op(0, dx0);
         uint32_t dd0, dd1, dm0, dm1;
         swap_rows(hd.x & 0xffffu, dd0, dd1);
         swap_rows(hd.x >> 16, dm0, dm1);
         const float d[2] = { h2f(dd0), h2f(dd1) }, dmin[2] = { h2f(dm0), h2f(dm1) };
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int imn0 = 64 * m0[r] + m0[4 + r], imn1 = 64 * m1[r] + m1[4 + r];
+        for (int r = 0; r < NR; ++r) {
+            const int imn0 = 64 * mh0[r] + ml0[r], imn1 = 64 * mh1[r] + ml1[r];
             out[r] += dx0[r] * (d[0] * (float)isc[r] - dmin[0] * (float)imn0);
-            out[4 + r] += dx0[r] * (d[1] * (float)isc[4 + r] - dmin[1] * (float)imn1);
+            out[NR + r] += dx0[r] * (d[1] * (float)isc[NR + r] - dmin[1] * (float)imn1);
         }
     } else if constexpr (IQ) {
         const uint32_t shi = rw[8].x >> 16, slo = rw[8].y;
-        v8i isum = {};
+        vNi<CM> isum = {};
         v16i pe0, pe1;
         int ps0 = 0, ps1 = 0;
         v4i an = a_op(0);                                     // LDS reads one block ahead
@@ -714,46 +731,47 @@ __device__ __forceinline__ void mma_stage(const uint4 (&rw)[9], int st, const ui
             if (ib + 1 < 8) an = a_op(ib + 1);
             const v16i e0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, op0, v16i{}, 0, 0, 0);
             const v16i e1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, op1, v16i{}, 0, 0, 0);
-            if (ib > 0) scale_add(pe0, pe1, ps0, ps1, isum);
+            if (ib > 0) scale_add<NR>(pe0, pe1, ps0, ps1, isum);
             __builtin_amdgcn_sched_barrier(0);
             pe0 = e0;
             pe1 = e1;
             ps0 = (int)s0 - 32;
             ps1 = (int)s1 - 32;
         }
-        scale_add(pe0, pe1, ps0, ps1, isum);
-        const float4 dx4 = dx_op(0);
-        const float dx0[4] = { dx4.x, dx4.y, dx4.z, dx4.w };
+        scale_add<NR>(pe0, pe1, ps0, ps1, isum);
+        float dx0[NR];
+        dx_op(0, dx0);
         uint32_t dd0, dd1;
         swap_rows(rw[8].x & 0xffffu, dd0, dd1);
         const float d[2] = { h2f(dd0), h2f(dd1) };
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) out[4 * t + r] += dx0[r] * (d[t] * (float)isum[4 * t + r]);
+            for (int r = 0; r < NR; ++r) out[NR * t + r] += dx0[r] * (d[t] * (float)isum[NR * t + r]);
     }
 }
 
 // A work-group is TW tiles x WK waves: wave (tw, kw) = wave % TW, wave / TW streams tile
 // tb TW + tw over the groups [gw + kw spw, + spw) of the work-group's K range [gw, gw + WK spw)
-// (K slice ks of KS).  The K range's activations are staged once in LDS for all TW tiles, the
-// WK waves of a tile are added in LDS in a fixed order, and KS > 1 adds into zeroed dst with
-// atomics.  Weights stream through two register sets: stage s + 1 loads while s computes.
-template <int TYPE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_gemv_mma(GemvParams p) {
+// (K slice ks of KS).  The K range's activations (CM columns) are staged once in LDS for all TW
+// tiles, the WK waves of a tile are added in LDS in a fixed order, and KS > 1 adds into zeroed
+// dst with atomics.  Weights stream through two register sets: stage s + 1 loads while s
+// computes.
+template <int TYPE, int CM>
+__device__ __forceinline__ void gemv_mma_body(const GemvParams & p) {
     using T = GV<TYPE>;
-    constexpr int NL = T::NL, NST = T::NST;
+    constexpr int NL = T::NL, NST = T::NST, NR = CM / 2;
     static_assert(NL == 9, "mma_stage takes 9 weight registers");
     constexpr bool KQ = TYPE == QMM_TYPE_Q4_K, Q8 = TYPE == QMM_TYPE_Q8_0;
     constexpr bool BF = TYPE == QMM_TYPE_Q4_0 || Q8 || TYPE == QMM_TYPE_IQ4_NL;   // a float scale per 32 weights
     constexpr int BS = BF ? 32 : 256;                             // activation scale block
     constexpr int NSB = BF ? 8 : 1;                               // activation scales per group
     constexpr int kMagic = 0x4B400000;                            // float 12582912: its bits + i = 12582912 + i
-    // LDS: 256 zero bytes (the A operand of lanes without a column), [WK spw][8][kMmaColBytes]
-    // codes, for Q4_K [WK spw][8][16] split sums, then the activation scales [WK spw][NSB][8];
+    // LDS: 256 zero bytes (the A operand of lanes without a column), [WK spw][CM][kMmaColBytes]
+    // codes, for Q4_K [WK spw][CM][16] split sums, then the activation scales [WK spw][NSB][CM];
     // after the stream, the waves' sums
     extern __shared__ __align__(16) uint8_t xl[];
-    __shared__ int64_t s_col[kMaxTaskCols], s_doff[kMaxTaskCols];
+    __shared__ int64_t s_col[CM], s_doff[CM];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int TW = p.tw, WK = p.W / p.tw;
@@ -808,47 +826,47 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     const int nthr = 64 * p.W;
     uint8_t * const xcl = xl + kMmaZeroBytes;
     if (tid < kMmaZeroBytes / 16) *reinterpret_cast<uint4 *>(xl + 16 * tid) = make_uint4(0, 0, 0, 0);
-    for (int i = tid; i < ngw * 8 * 16; i += nthr) {
-        const int g = i >> 7, c = (i >> 4) & 7, q = i & 15;
+    for (int i = tid; i < ngw * CM * 16; i += nthr) {
+        const int q = i & 15, c = (i >> 4) % CM, g = (i >> 4) / CM;
         uint4 v = make_uint4(0, 0, 0, 0);
         if (c < nc) v = *reinterpret_cast<const uint4 *>(p.xc + s_col[c] * p.ldk + (int64_t)(gw + g) * 256 + 16 * q);
-        *reinterpret_cast<uint4 *>(xcl + (g * 8 + c) * kMmaColBytes + 16 * q) = v;
+        *reinterpret_cast<uint4 *>(xcl + (g * CM + c) * kMmaColBytes + 16 * q) = v;
     }
     const int per = WK * p.spw;                                   // groups the LDS holds
-    uint8_t * const xsl = xcl + per * 8 * kMmaColBytes;
+    uint8_t * const xsl = xcl + per * CM * kMmaColBytes;
     if constexpr (KQ) {
-        for (int i = tid; i < ngw * 8; i += nthr) {
-            const int g = i >> 3, c = i & 7;
+        for (int i = tid; i < ngw * CM; i += nthr) {
+            const int g = i / CM, c = i % CM;
             uint4 v = make_uint4(0, 0, 0, 0);
             if (c < nc) v = *reinterpret_cast<const uint4 *>(p.bsp + ((int64_t)(gw + g) * p.ldT + s_col[c]) * 16);
             *reinterpret_cast<uint4 *>(xsl + 16 * i) = v;
         }
     }
-    float * const xdl = reinterpret_cast<float *>(xsl + (KQ ? per * 8 * 16 : 0));
-    for (int i = tid; i < ngw * NSB * 8; i += nthr) {
-        const int c = i & 7, gb = i >> 3;                         // gb = group * NSB + block
+    float * const xdl = reinterpret_cast<float *>(xsl + (KQ ? per * CM * 16 : 0));
+    for (int i = tid; i < ngw * NSB * CM; i += nthr) {
+        const int c = i % CM, gb = i / CM;                        // gb = group * NSB + block
         xdl[i] = c < nc ? p.xd[s_col[c] * (p.ldk / BS) + (int64_t)gw * NSB + gb] : 0.0f;
     }
     __syncthreads();
     const int h = lane >> 5, l32 = lane & 31;
-    // A operand: the lane's column l32 (zeros past nc), k half h.  Output columns 4 h + r, r < 4.
-    // Lanes without a column read the zero block (every offset stays inside its 256 bytes).
+    // A operand: the lane's column l32 (zeros past nc), k half h.  Lanes without a column read
+    // the zero block (every offset stays inside its 256 bytes).
     const bool a_live = l32 < nc;
-    const uint8_t * xar = a_live ? xcl + ((ga - gw) * 8 + l32) * kMmaColBytes + 16 * h : xl;
-    const int xas = a_live ? 8 * kMmaColBytes : 0;                // per group
-    // Q4_K min term: lane l < 16 brings bh (l < 8) or bl (8 <= l < 16) of column l % 8
-    const bool s_live = KQ && lane < 16;
-    const uint8_t * xsr = s_live ? xsl + ((ga - gw) * 8 + (lane & 7)) * 16 + 8 * ((lane >> 3) & 1) : xl;
-    const int xss = s_live ? 128 : 0;
-    // the scales of the lane's output columns 4 h .. 4 h + 3, per (group, block)
-    const float * xdr = xdl + (ga - gw) * NSB * 8 + 4 * h;
-    v8f out = {};
+    const uint8_t * xar = a_live ? xcl + ((ga - gw) * CM + l32) * kMmaColBytes + 16 * h : xl;
+    const int xas = a_live ? CM * kMmaColBytes : 0;               // per group
+    // Q4_K min term: the split sums of the lane's column (lane half 0; zeros elsewhere)
+    const bool s_live = KQ && a_live && h == 0;
+    const uint8_t * xsr = s_live ? xsl + ((ga - gw) * CM + l32) * 16 : xl;
+    const int xss = s_live ? CM * 16 : 0;
+    // the scales of the lane's output columns (quads 8 q + 4 h), per (group, block)
+    const float * xdr = xdl + (ga - gw) * NSB * CM + 4 * h;
+    vNf<CM> out = {};
     v16i magic;
 #pragma unroll
     for (int r = 0; r < 16; ++r) magic[r] = kMagic;
     auto compute = [&](const uint4 (&b)[NL], int s) {
         const int gl = s / NST;
-        mma_stage<TYPE>(b, s % NST, xar + gl * xas, xdr + gl * NSB * 8, xsr + gl * xss, h, magic, out);
+        mma_stage<TYPE, CM>(b, s % NST, xar + gl * xas, xdr + gl * NSB * CM, xsr + gl * xss, h, magic, out);
     };
     for (int s = 0; s < S; s += 2) {                              // uniform
         load_stage(b1, s + 1);
@@ -861,11 +879,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     }
 
     // tile tw's WK waves are added in a fixed order (wave kw takes the elements e = kw, kw + WK,
-    // ... of the 8), then stored (KS == 1) or added (KS > 1)
+    // ... of the CM), then stored (KS == 1) or added (KS > 1)
     const int64_t row0 = (int64_t)tile * kTileRows + l32;
     auto store = [&](int e, float v) {
-        const int c = 4 * h + (e & 3);
-        const int64_t row = row0 + 32 * (e >> 2);
+        const int c = mma_col(e % NR, h);
+        const int64_t row = row0 + 32 * (e / NR);
         if (tile < ntl && c < nc && row < p.w.M) {
             float * o = p.dst + s_doff[c] + row;
             if (p.KS == 1) *o = v;
@@ -874,19 +892,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     };
     if (WK == 1) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) store(e, out[e]);
+        for (int e = 0; e < CM; ++e) store(e, out[e]);
         return;
     }
-    float * red = reinterpret_cast<float *>(xl);                  // [WK][TW][8][64], over the staged data
+    float * red = reinterpret_cast<float *>(xl);                  // [WK][TW][CM][64], over the staged data
     __syncthreads();
 #pragma unroll
-    for (int e = 0; e < 8; ++e) red[((kw * TW + tw) * 8 + e) * 64 + lane] = out[e];
+    for (int e = 0; e < CM; ++e) red[((kw * TW + tw) * CM + e) * 64 + lane] = out[e];
     __syncthreads();
-    for (int e = kw; e < 8; e += WK) {
+    for (int e = kw; e < CM; e += WK) {
         float v = 0.0f;
-        for (int k = 0; k < WK; ++k) v += red[((k * TW + tw) * 8 + e) * 64 + lane];
+        for (int k = 0; k < WK; ++k) v += red[((k * TW + tw) * CM + e) * 64 + lane];
         store(e, v);
     }
+}
+
+// 8 columns run three waves per SIMD; 16 and 32 (more accumulators: 16 spills 3 to 17
+// registers at three waves) two
+template <int TYPE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_gemv_mma(GemvParams p) {
+    gemv_mma_body<TYPE, 8>(p);
+}
+template <int TYPE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_gemv_mma16(GemvParams p) {
+    gemv_mma_body<TYPE, 16>(p);
+}
+template <int TYPE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_gemv_mma32(GemvParams p) {
+    gemv_mma_body<TYPE, 32>(p);
 }
 
 template <int TYPE>
@@ -920,7 +953,7 @@ bool gemv_mma_supported(int type) {
 }
 
 bool gemv_plan(int type, const WView & w, int nc, int64_t ntasks, bool allow_split, bool want_mma, GemvPlan * pl) {
-    if (!type_layout(type) || nc < 1 || nc > kMaxTaskCols || ntasks <= 0 || w.G <= 0 || w.ntiles <= 0) return false;
+    if (!type_layout(type) || nc < 1 || nc > kMmaMaxCols || ntasks <= 0 || w.G <= 0 || w.ntiles <= 0) return false;
     pl->nc = nc;
     pl->ntasks = ntasks;
     const int64_t tiles = ntasks * w.ntiles;
@@ -929,7 +962,11 @@ bool gemv_plan(int type, const WView & w, int nc, int64_t ntasks, bool allow_spl
     // cannot split K, fall back to the v_dot4 kernel past that)
     pl->mma = want_mma && gemv_mma_supported(type);
     pl->tw = 1;
+    pl->cm = 8;
+    if (nc < 1 || nc > (pl->mma ? kMmaMaxCols : kMaxTaskCols)) return false;
     if (pl->mma) {
+        pl->cm = nc <= 8 ? 8 : nc <= 16 ? 16 : 32;
+        const int64_t maxg = (int64_t)kMmaMaxGroups * 8 / pl->cm;   // the LDS stages cm columns per group
         // MFMA kernel: about `target` waves in work-groups of TW tiles x WK waves; the WK waves
         // of a tile split K and are added in LDS, which stages the work-group's activations
         // (WK spw <= kMmaMaxGroups groups); the rest of the split is KS work-groups per tile
@@ -943,7 +980,7 @@ bool gemv_plan(int type, const WView & w, int nc, int64_t ntasks, bool allow_spl
         const int64_t kw = std::min<int64_t>(w.G, std::max<int64_t>(1, (target + tiles - 1) / tiles));
         int64_t spw = (w.G + kw - 1) / kw;
         int64_t WK = std::min<int64_t>((w.G + spw - 1) / spw, allow_split ? wkmax : 4 / TW);
-        spw = std::min<int64_t>(allow_split ? spw : (w.G + WK - 1) / WK, kMmaMaxGroups / WK);
+        spw = std::min<int64_t>(allow_split ? spw : (w.G + WK - 1) / WK, std::max<int64_t>(1, maxg / WK));
         int64_t KS = (w.G + spw * WK - 1) / (spw * WK);
         WK = std::min<int64_t>(WK, ((w.G + KS - 1) / KS + spw - 1) / spw);   // balance the slices
         KS = (w.G + spw * WK - 1) / (spw * WK);
@@ -956,6 +993,8 @@ bool gemv_plan(int type, const WView & w, int nc, int64_t ntasks, bool allow_spl
             return nwg > 0 && nwg < 0x7fffffff;
         }
         pl->mma = false;
+        pl->cm = 8;
+        if (nc > kMaxTaskCols) return false;
     }
     // waves: about `target` in all (each with at least one group), at most
     // wmax per work-group; the rest of the split goes to work-groups per tile
@@ -986,10 +1025,11 @@ int64_t gemv_workgroups(const WView & w, const GemvPlan & pl) {
 
 size_t gemv_lds_bytes(int type, const GemvPlan & pl) {
     if (pl.mma) {
-        const size_t per_group = 8 * (kMmaColBytes + (type == QMM_TYPE_Q4_K ? 16 : 0)) +
-                                 8 * sizeof(float) * (vec_dot_type(type) == QMM_TYPE_Q8_0 ? 8 : 1);
+        const size_t cm = (size_t)pl.cm;
+        const size_t per_group = cm * (kMmaColBytes + (type == QMM_TYPE_Q4_K ? 16 : 0)) +
+                                 cm * sizeof(float) * (vec_dot_type(type) == QMM_TYPE_Q8_0 ? 8 : 1);
         const size_t stage = kMmaZeroBytes + (size_t)(pl.W / pl.tw) * pl.spw * per_group;
-        const size_t red = pl.W > pl.tw ? (size_t)pl.W * 8 * 64 * sizeof(float) : 0;   // the K waves' sums
+        const size_t red = pl.W > pl.tw ? (size_t)pl.W * cm * 64 * sizeof(float) : 0;   // the K waves' sums
         return std::max(stage, red);
     }
     return pl.W > 1 ? (size_t)pl.W * pl.nc * 64 * sizeof(float) : 0;
@@ -1034,15 +1074,20 @@ hipError_t launch_gemv(int type, const WView & w, const GemvPlan & pl, const Act
     if (pl.mma) {
         const int64_t per_wg = (int64_t)(pl.W / pl.tw) * pl.spw;
         if (!gemv_mma_supported(type) || nwg >= 0x7fffffff || pl.W > 4 || pl.tw < 1 || pl.W % pl.tw ||
-            per_wg > kMmaMaxGroups ||
+            (pl.cm != 8 && pl.cm != 16 && pl.cm != 32) || pl.nc > pl.cm || (tasks && pl.cm != 8) ||
+            per_wg > kMmaMaxGroups * 8 / pl.cm ||
             per_wg * pl.KS < w.G || per_wg * (pl.KS - 1) >= w.G || (type == QMM_TYPE_Q4_K && !a.bsp))
             return hipErrorInvalidValue;
         const uint32_t lds = (uint32_t)gemv_lds_bytes(type, pl);
         const dim3 g((unsigned)nwg), b(64 * pl.W);
-#define QMM_MMA(T)                                                                                  \
-    if (kt) hipExtLaunchKernelGGL(k_gemv_mma<T>, g, b, lds, s, kt->start, kt->stop, 0, p);          \
-    else k_gemv_mma<T><<<g, b, lds, s>>>(p);                                                        \
+#define QMM_MMA_K(K)                                                                                \
+    if (kt) hipExtLaunchKernelGGL(K, g, b, lds, s, kt->start, kt->stop, 0, p);                      \
+    else K<<<g, b, lds, s>>>(p);                                                                    \
     return hipGetLastError();
+#define QMM_MMA(T)                                                                                  \
+    if (pl.cm == 8) { QMM_MMA_K(k_gemv_mma<T>) }                                                    \
+    if (pl.cm == 16) { QMM_MMA_K(k_gemv_mma16<T>) }                                                 \
+    QMM_MMA_K(k_gemv_mma32<T>)
         switch (type) {
             case QMM_TYPE_Q4_0: { QMM_MMA(QMM_TYPE_Q4_0) }
             case QMM_TYPE_Q8_0: { QMM_MMA(QMM_TYPE_Q8_0) }
@@ -1052,7 +1097,9 @@ hipError_t launch_gemv(int type, const WView & w, const GemvPlan & pl, const Act
             default: return hipErrorInvalidValue;
         }
 #undef QMM_MMA
+#undef QMM_MMA_K
     }
+    if (pl.nc > kMaxTaskCols) return hipErrorInvalidValue;
     switch (type) {
         case QMM_TYPE_Q4_0:   return launch_t<QMM_TYPE_Q4_0>(p, pl.nc, nwg, s, kt);
         case QMM_TYPE_Q8_0:   return launch_t<QMM_TYPE_Q8_0>(p, pl.nc, nwg, s, kt);

@@ -597,20 +597,36 @@ int qmm_supports_op(qmm_ctx *, int32_t op, const qmm_tensor * src0, const qmm_te
 
 // ---- ops ---------------------------------------------------------------------
 
-// columns at or above which MUL_MAT goes to the MFMA GEMM (below: the GEMV,
-// one weight pass per 8 columns)
-static int64_t gemm_min_cols() {
-    static int64_t v = [] {
-        const char * e = getenv("QMM_GEMM_MIN_COLS");
-        return e ? std::max<int64_t>(1, atoll(e)) : (int64_t)16;
-    }();
-    return v;
-}
-
-// few columns (this many and up to 8) on the MFMA GEMV; QMM_GEMV_MMA_MIN overrides
+// few columns (this many and up to 32 per weight pass) on the MFMA GEMV; QMM_GEMV_MMA_MIN overrides
 static int gemv_mma_min_cols() {
     const char * e = getenv("QMM_GEMV_MMA_MIN");
     return e ? std::max(2, atoi(e)) : 3;
+}
+
+// columns at or above which MUL_MAT goes to the MFMA GEMM instead of the GEMV (32 columns per
+// weight pass on the MFMA GEMV, 8 on v_dot4).  Measured crossovers on MI355X (config shapes):
+// Q4_K's GEMV wins to ~100 columns (17408 x 5120: 69 us against 82 at 96), IQ4_XS's to 64,
+// Q4_0 / Q8_0 / IQ4_NL's to one pass (their GEMM keeps up from 33); the v_dot4 types switch
+// at 16.  QMM_GEMM_MIN_COLS overrides.
+static int64_t gemm_min_cols(int type) {
+    const char * e = getenv("QMM_GEMM_MIN_COLS");
+    if (e) return std::max<int64_t>(1, atoll(e));
+    switch (type) {
+        case QMM_TYPE_Q4_K:   return 128;
+        case QMM_TYPE_IQ4_XS: return 65;
+        case QMM_TYPE_Q4_0:
+        case QMM_TYPE_Q8_0:
+        case QMM_TYPE_IQ4_NL: return kMmaMaxCols + 1;
+        default:              return 16;
+    }
+}
+
+// columns per GEMV task: up to 32 on the MFMA kernel (the rows of its A operand), 8 on v_dot4,
+// spread evenly over the fewest weight passes
+static int gemv_task_cols(int type, int64_t N) {
+    const int64_t cap = gemv_mma_supported(type) && N >= gemv_mma_min_cols() ? kMmaMaxCols : kMaxTaskCols;
+    const int64_t passes = (N + cap - 1) / cap;
+    return (int)((N + passes - 1) / passes);
 }
 
 int qmm_describe_mul_mat(const qmm_tensor * src0, const qmm_tensor * src1, const qmm_tensor * dst, qmm_launch_info * out) {
@@ -621,7 +637,7 @@ int qmm_describe_mul_mat(const qmm_tensor * src0, const qmm_tensor * src1, const
     WView w;   // shapes only: buffers are not looked at
     if (!mul_mat_ok(src0, src1, dst, false, &w, reason, sizeof(reason))) return QMM_ERR_UNSUPPORTED;
     const int64_t N = src1->ne[1];
-    if (N >= gemm_min_cols()) {
+    if (N >= gemm_min_cols(src0->type)) {
         snprintf(out->path, sizeof(out->path), "gemm-mfma");
         out->tasks = src1->ne[2] * src1->ne[3];
         out->cols_per_task = (int32_t)std::min<int64_t>(N, INT32_MAX);
@@ -629,10 +645,10 @@ int qmm_describe_mul_mat(const qmm_tensor * src0, const qmm_tensor * src1, const
         gemm_shape(src0->type, w, N, out->tasks, &out->workgroups, &threads, &lds);
         out->threads = threads;
         out->lds_bytes = lds;
-        out->k_slices = gemm_kslices(w, N, out->tasks);
+        out->k_slices = gemm_kslices(src0->type, w, N, out->tasks);
         return QMM_OK;
     }
-    const int nc = (int)std::min<int64_t>(N, kMaxTaskCols);
+    const int nc = gemv_task_cols(src0->type, N);
     const int64_t ntasks = (N + nc - 1) / nc * src1->ne[2] * src1->ne[3];
     GemvPlan plan;
     if (!gemv_plan(src0->type, w, nc, ntasks, true, nc >= gemv_mma_min_cols(), &plan)) return QMM_ERR_UNSUPPORTED;
@@ -657,7 +673,7 @@ int qmm_mul_mat(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1,
         return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat: %s", reason);
     QMM_HIP(ctx, hipSetDevice(ctx->device));
     const int64_t N = src1->ne[1];
-    const bool use_gemm = N >= gemm_min_cols();
+    const bool use_gemm = N >= gemm_min_cols(src0->type);
     ActBuf a{};
     int rc;
     float * d = (float *)((uint8_t *)dst->buffer->ptr + dst->offs);
@@ -674,7 +690,7 @@ int qmm_mul_mat(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1,
     if (use_gemm) {
         const int64_t nbatch = dn.ne12 * dn.ne13;
         // K slices add into dst rows from zero_from on (the pre-pass zeroes them)
-        const int64_t zero_from = gemm_zero_from(w, N, nbatch);
+        const int64_t zero_from = gemm_zero_from(src0->type, w, N, nbatch);
         ZeroJob z{ d, w.M, N * nbatch, N, dn.ne12, dn.d_nb1, dn.d_nb2, dn.d_nb3, zero_from };
         const bool split = zero_from < w.M;
         if ((rc = quantize_src1(ctx, src0->type, src1, true, &a, split ? &z : nullptr))) return rc;
@@ -693,8 +709,8 @@ int qmm_mul_mat(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1,
         QMM_HIP(ctx, launch_gemm(src0->type, w, a, N, dn.ne12 * dn.ne13, bt, d, ctx->stream, ktp));
         return QMM_OK;
     }
-    // up to 8 columns per task against one weight pass
-    const int nc = (int)std::min<int64_t>(N, kMaxTaskCols);
+    // up to 8 (v_dot4) or 32 (MFMA) columns per task against one weight pass
+    const int nc = gemv_task_cols(src0->type, N);
     const int64_t ntasks = (N + nc - 1) / nc * dn.ne12 * dn.ne13;
     GemvPlan plan;
     if (!gemv_plan(src0->type, w, nc, ntasks, true, nc >= gemv_mma_min_cols(), &plan))
@@ -702,7 +718,7 @@ int qmm_mul_mat(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1,
     ZeroJob z{ d, w.M, N * dn.ne12 * dn.ne13, N, dn.ne12, dn.d_nb1, dn.d_nb2, dn.d_nb3 };
     if ((rc = quantize_src1(ctx, src0->type, src1, false, &a, plan.KS > 1 ? &z : nullptr))) return rc;
     ctx->path = plan.mma ? "gemv-mfma" : "gemv";
-    if (N > kMaxTaskCols) note_downgrade(ctx, "mul_mat: many columns on the GEMV");
+    if (N > nc) note_downgrade(ctx, "mul_mat: many columns on the GEMV");
     KTime kt;
     const KTime * ktp;
     if ((rc = ktime_pair(ctx, &kt, &ktp))) return rc;

@@ -168,15 +168,17 @@ struct GemvDense {
 // K; it stages its K range's activations in LDS (kMmaColBytes per column and group, at most
 // kMmaMaxGroups groups).
 struct GemvPlan {
-    int nc;                        // columns per task (1..8)
+    int nc;                        // columns per task (1..8; mma: 1..kMmaMaxCols)
     int64_t ntasks;                // grid tasks (list mode: upper bound)
     int W, KS, spw;
     bool mma;                      // dots on the MFMA (few columns; Q4_0, Q8_0, Q4_K, IQ4_XS, IQ4_NL)
     int tw;                        // mma: tiles per work-group, W / tw waves of each split K
+    int cm;                        // mma: the kernel's columns per task (8, 16 or 32) >= nc
 };
 constexpr int kMmaColBytes = 272;  // 256 codes + 16 bytes of padding (LDS banks)
 constexpr int kMmaZeroBytes = 256; // zeros ahead of the codes
-constexpr int kMmaMaxGroups = 24;
+constexpr int kMmaMaxGroups = 24;  // groups a work-group stages at 8 columns (8 / cm of it at cm)
+constexpr int kMmaMaxCols = 32;    // columns of one MFMA task (the A operand's 32 rows)
 // want_mma: use the MFMA kernel where the type allows it
 bool gemv_plan(int type, const WView & w, int nc, int64_t ntasks, bool allow_split, bool want_mma, GemvPlan * plan);
 int64_t gemv_workgroups(const WView & w, const GemvPlan & plan);
@@ -207,10 +209,10 @@ hipError_t launch_gemm(int type, const WView & w, const ActBuf & a, int64_t N, i
                        const GemmBatch & bt, float * dst, hipStream_t s, const KTime * kt = nullptr);
 // K slices the GEMM splits this product into; above 1 the slices add their
 // partial sums to dst with atomics, so dst must be zeroed first.
-int gemm_kslices(const WView & w, int64_t N, int64_t nbatch);
+int gemm_kslices(int type, const WView & w, int64_t N, int64_t nbatch);
 // first dst row that K slices add into (the pre-pass zeroes rows [that, M) of every column;
 // M: no row)
-int64_t gemm_zero_from(const WView & w, int64_t N, int64_t nbatch);
+int64_t gemm_zero_from(int type, const WView & w, int64_t N, int64_t nbatch);
 // launch shape of that GEMM (qmm_describe_mul_mat)
 void gemm_shape(int type, const WView & w, int64_t N, int64_t nbatch, int64_t * workgroups, int * threads,
                 int * lds_bytes);

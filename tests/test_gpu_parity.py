@@ -385,6 +385,38 @@ def test_mul_mat_many_columns(be, sc, orc, qtype, N):
     assert rel_err(got, ref) <= TOL
 
 
+@pytest.mark.parametrize("qtype", list(MMA_TYPES))
+@pytest.mark.parametrize("N", [9, 12, 16, 17, 24, 31, 32, 40, 64, 100])
+def test_mfma_gemv_wide_tasks(be, sc, orc, monkeypatch, qtype, N):
+    """the MFMA GEMV with 9..32 columns per weight pass (the 16- and 32-column kernels; 40 and
+    up in even passes), forced off the GEMM"""
+    monkeypatch.setenv("QMM_GEMM_MIN_COLS", "100000")
+    M, K = 300, 1024
+    say("gemv-wide", qtype, M, K, N)
+    got, ref = run_mul_mat(be, sc, orc, qtype, M, K, N, seed=54)
+    assert be.last_path() == "gemv-mfma"
+    assert rel_err(got, ref) <= TOL
+
+
+@pytest.mark.parametrize("qtype", [qmm.Q4_K, qmm.Q4_0])
+def test_mfma_gemv_wide_broadcast_and_strides(be, sc, orc, monkeypatch, qtype):
+    monkeypatch.setenv("QMM_GEMM_MIN_COLS", "100000")
+    say("gemv-wide-broadcast", qtype)
+    K, M, N = 512, 80, 21
+    raw = synth.weights(qtype, 2 * M, K, seed=66)
+    w = sc.weights(qtype, raw, (K, M, 2))
+    x = synth.activations(4 * N, K, seed=67).reshape(4, N, K)
+    ypad = sc.empty_f32((M + 5, N, 4))
+    yv = qmm.Tensor(ypad.buf, qmm.F32, (M, N, 4), nb=(4, 4 * (M + 5), 4 * (M + 5) * N, 4 * (M + 5) * N * 4))
+    be.mul_mat(w, sc.f32(x), yv)
+    be.synchronize()
+    assert be.last_path() == "gemv-mfma"
+    got = be.get_f32(ypad).reshape(4, N, M + 5)[:, :, :M]
+    rb = synth.row_bytes(qtype, K) * M
+    for i2 in range(4):
+        assert rel_err(got[i2], orc.mul_mat(qtype, raw[(i2 // 2) * rb:(i2 // 2 + 1) * rb], M, K, x[i2])) <= TOL
+
+
 def test_mul_mat_broadcast_and_strides(be, sc, orc):
     say("broadcast")
     qtype, K, M, N = qmm.Q4_K, 512, 64, 3
@@ -496,7 +528,8 @@ def test_full_size_gemv(be, sc, orc, qtype, M, K, N):
 @pytest.mark.parametrize("qtype", TYPES)
 @pytest.mark.parametrize("M,K,N", [(300, 1024, 16), (129, 2048, 37), (64, 512, 64), (500, 768, 130),
                                    (200, 256, 40), (70, 800, 20), (1000, 512, 300)])
-def test_mul_mat_gemm(be, sc, orc, qtype, M, K, N):
+def test_mul_mat_gemm(be, sc, orc, monkeypatch, qtype, M, K, N):
+    monkeypatch.setenv("QMM_GEMM_MIN_COLS", "16")                 # the GEMM from 16 columns, every type
     if K % 256 and qtype not in (qmm.Q4_0, qmm.Q8_0, qmm.IQ4_NL):
         K = 1024
     say("gemm", qtype, M, K, N)
@@ -506,7 +539,8 @@ def test_mul_mat_gemm(be, sc, orc, qtype, M, K, N):
 
 
 @pytest.mark.parametrize("qtype", [qmm.Q6_K, qmm.Q4_K, qmm.Q5_K, qmm.Q4_0, qmm.IQ4_NL])
-def test_mul_mat_gemm_broadcast_and_strides(be, sc, orc, qtype):
+def test_mul_mat_gemm_broadcast_and_strides(be, sc, orc, monkeypatch, qtype):
+    monkeypatch.setenv("QMM_GEMM_MIN_COLS", "16")
     say("gemm-broadcast", qtype)
     K, M, N = 512, 80, 21
     raw = synth.weights(qtype, 2 * M, K, seed=64)
@@ -555,7 +589,8 @@ def test_gemm_tail_split(be, sc, orc, qtype):
 
 
 @pytest.mark.parametrize("qtype,M,K,N", GEMM_FULL)
-def test_full_size_gemm(be, sc, orc, qtype, M, K, N):
+def test_full_size_gemm(be, sc, orc, monkeypatch, qtype, M, K, N):
+    monkeypatch.setenv("QMM_GEMM_MIN_COLS", "16")
     say("gemm-full", qtype, M, K, N)
     got, ref = run_mul_mat(be, sc, orc, qtype, M, K, N, seed=93)
     assert be.last_path() == "gemm-mfma"

@@ -227,6 +227,9 @@ PLAN_SHAPES = [
     (qmm.Q4_0, 4096, 4096, 1), (qmm.Q4_0, 11008, 4096, 8), (qmm.Q8_0, 4096, 14336, 8), (qmm.IQ4_XS, 14336, 4096, 2),
     (qmm.Q4_0, 352, 65, 3), (qmm.Q4_K, 256, 1, 1), (qmm.Q8_0, 32, 5, 8), (qmm.IQ4_XS, 512, 2048, 5),
     (qmm.Q5_K, 5120, 17408, 1), (qmm.Q5_K, 4096, 4096, 6), (qmm.IQ4_NL, 640, 4096, 1), (qmm.IQ4_NL, 4096, 14336, 8),
+    # wide MFMA tasks: 9..32 columns per weight pass, more in even passes
+    (qmm.Q4_K, 5120, 17408, 16), (qmm.Q4_K, 5120, 17408, 100), (qmm.Q4_0, 4096, 11008, 32), (qmm.Q8_0, 4096, 14336, 24),
+    (qmm.IQ4_XS, 4096, 14336, 40), (qmm.IQ4_NL, 4096, 4096, 9), (qmm.Q6_K, 17408, 5120, 12), (qmm.Q5_K, 5120, 4096, 9),
 ]
 
 
@@ -235,11 +238,14 @@ def test_gemv_plan(qtype, K, M, N):
     fake = qmm.Buffer(ptr=0x1000, size=1 << 44)
     info = qmm.describe_mul_mat(qmm.Tensor(fake, qtype, (K, M)), qmm.Tensor(fake, qmm.F32, (K, N)),
                                 qmm.Tensor(fake, qmm.F32, (M, N)))
-    # the MFMA kernel takes 3..8 columns of the types whose blocks it decodes
+    # the MFMA kernel takes 3 and more columns of the types whose blocks it decodes, up to 32 a
+    # weight pass; v_dot4 8; the columns spread evenly over the fewest passes
     mma = N >= 3 and qtype in (qmm.Q4_0, qmm.Q8_0, qmm.Q4_K, qmm.IQ4_XS, qmm.IQ4_NL)
     assert info["path"] == ("gemv-mfma" if mma else "gemv")
     G, nt = -(-K // 256), -(-M // 64)
     W, KS, spw, nc = info["k_waves"], info["k_slices"], info["groups_per_wave"], info["cols_per_task"]
+    cap = 32 if mma else 8
+    assert nc == -(-N // -(-N // cap))
     assert 1 <= W <= 8 and KS >= 1 and spw >= 1
     assert KS * W * spw >= G                             # the waves cover K
     assert (KS - 1) * W * spw < G                        # no work-group without groups
@@ -251,10 +257,12 @@ def test_gemv_plan(qtype, K, M, N):
         # TW tiles x W waves splitting K; the K range's activations are staged in LDS: 256 zero
         # bytes, then per column and group the codes (272 B), Q4_K split sums (16 B) and the
         # scales (4 B per block); the W waves' sums reuse it
-        assert 1 <= tw <= 4 and W * tw <= 4 and W * spw <= 24
+        # (cm = the kernel's columns: 8, 16 or 32; the LDS holds 24 x 8 / cm groups)
+        cm = 8 if nc <= 8 else 16 if nc <= 16 else 32
+        assert 1 <= tw <= 4 and W * tw <= 4 and W * spw <= 24 * 8 // cm
         nsb = 8 if qtype in (qmm.Q4_0, qmm.Q8_0, qmm.IQ4_NL) else 1
-        stage = 256 + W * spw * 8 * (272 + (16 if qtype == qmm.Q4_K else 0) + 4 * nsb)
-        assert info["lds_bytes"] == max(stage, W * tw * 8 * 64 * 4 if W > 1 else 0)
+        stage = 256 + W * spw * cm * (272 + (16 if qtype == qmm.Q4_K else 0) + 4 * nsb)
+        assert info["lds_bytes"] == max(stage, W * tw * cm * 64 * 4 if W > 1 else 0)
     else:
         assert tw == 1
         assert info["lds_bytes"] == (W * nc * 64 * 4 if W > 1 else 0)
