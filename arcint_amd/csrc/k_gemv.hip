@@ -54,12 +54,24 @@ struct GemvParams {
     int64_t d_nb1, d_nb2, d_nb3; // dst strides in floats
     float * dst;
     const uint8_t * sink;        // >= kSinkBytes of readable memory for loads past the end
+    const uint8_t * base2;       // dense mode: the image of matrix 1 (gate/up in one launch), or null
+    int64_t col_bs;              // dense mode: activation columns per batch
     int W;                       // waves per work-group
     int KS;                      // work-groups per tile (K slices); > 1: atomics into zeroed dst
     int spw;                     // groups per wave
     int nct;                     // dense mode: columns per task
     int tw;                      // MFMA kernel: tiles per work-group (W / tw waves split K)
 };
+
+// tile-group 0 of (matrix, tile): matrix 1 of a gate/up launch is a second image
+__device__ __forceinline__ const uint8_t * mat_tile(const GemvParams & p, int mat, uint32_t tile) {
+    if (p.base2 && mat == 1) {
+        WView w2 = p.w;
+        w2.base = p.base2;
+        return tile_group(w2, 0, tile, 0);
+    }
+    return tile_group(p.w, mat, tile, 0);
+}
 
 // wave-uniform (scalar) loads of the pre-quantized activations
 typedef const __attribute__((address_space(4))) uint32_t cu32;
@@ -431,7 +443,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvParams p) {
         nc = (int)((p.ne11 - first) < NC ? (p.ne11 - first) : NC);
         if (tid < nc) {
             const int64_t i1 = first + tid;
-            s_col[tid] = (int64_t)b * p.ne11 + i1;
+            s_col[tid] = (int64_t)b * p.col_bs + i1;
             s_doff[tid] = i1 * p.d_nb1 + (int64_t)i2 * p.d_nb2 + (int64_t)i3 * p.d_nb3;
         }
     }
@@ -443,7 +455,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvParams p) {
     const int ga = ((int)ks * p.W + wave) * p.spw;                // this wave's groups [ga, gb)
     const int gb = ga + p.spw < G ? ga + p.spw : G;
     const int S = ga < gb ? (gb - ga) * NST : 0;                  // stages (uniform)
-    const uint8_t * tbase = tile_group(p.w, mat, tile, 0);
+    const uint8_t * tbase = mat_tile(p, mat, tile);
     const size_t tgs = (size_t)p.w.tg;
 
     // per-column activation pointers at group 0 (uniform)
@@ -799,7 +811,7 @@ __device__ __forceinline__ void gemv_mma_body(const GemvParams & p) {
         nc = (int)((p.ne11 - first) < p.nct ? (p.ne11 - first) : p.nct);
         if (tid < nc) {
             const int64_t i1 = first + tid;
-            s_col[tid] = (int64_t)b * p.ne11 + i1;
+            s_col[tid] = (int64_t)b * p.col_bs + i1;
             s_doff[tid] = i1 * p.d_nb1 + (int64_t)i2 * p.d_nb2 + (int64_t)i3 * p.d_nb3;
         }
     }
@@ -811,7 +823,7 @@ __device__ __forceinline__ void gemv_mma_body(const GemvParams & p) {
     const int nsw = ga >= G ? 0 : (ga + p.spw < G ? p.spw : G - ga);
     const uint32_t tile = tb * (uint32_t)TW + (uint32_t)tw;
     const int S = tile < ntl ? nsw * NST : 0;                     // stages (uniform per wave)
-    const uint8_t * tbase = tile_group(p.w, mat, tile < ntl ? tile : 0, 0);
+    const uint8_t * tbase = mat_tile(p, mat, tile < ntl ? tile : 0);
     const size_t tgs = (size_t)p.w.tg;
     auto load_stage = [&](uint4 (&b)[NL], int s) {                // past the last stage: the sink
         const bool real = s < S;
@@ -1060,6 +1072,9 @@ hipError_t launch_gemv(int type, const WView & w, const GemvPlan & pl, const Act
     p.tw = pl.tw;
     if (!tasks) {
         p.ne11 = dense->ne11;
+        p.col_bs = dense->col_bs < 0 ? dense->ne11 : dense->col_bs;
+        p.base2 = dense->base2;
+        if (p.base2 && (dense->ne12 * dense->ne13 != 2 || dense->ne02 != 2 || dense->r2 != 1)) return hipErrorInvalidValue;
         p.ne12 = dense->ne12;
         p.r2 = dense->r2;
         p.r3 = dense->r3;

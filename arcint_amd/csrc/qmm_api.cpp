@@ -46,6 +46,8 @@ struct qmm_ctx {
     ActBuf cached{};
     // MoE route scratch: ids copy, tasks, task count
     void * route = nullptr;
+    size_t glu_cap = 0;
+    void * glu = nullptr;            // gate/up sums of qmm_mul_mat_glu
     size_t route_cap = 0;
     // downgrade counter (paths slower than the type promises)
     int64_t downgrades = 0;
@@ -339,6 +341,7 @@ void qmm_ctx_free(qmm_ctx * ctx) {
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->act) (void)hipFree(ctx->act);
     if (ctx->route) (void)hipFree(ctx->route);
+    if (ctx->glu) (void)hipFree(ctx->glu);
     if (ctx->sink) (void)hipFree(ctx->sink);
     for (hipEvent_t e : ctx->kev) (void)hipEventDestroy(e);
     if (ctx->ev0) (void)hipEventDestroy(ctx->ev0);
@@ -842,6 +845,100 @@ int qmm_moe_combine(qmm_ctx * ctx, const qmm_tensor * experts, const qmm_tensor 
     a.dnb1 = (int64_t)dst->nb[1];
     ctx->path = "moe-combine";
     QMM_HIP(ctx, launch_combine(a, ctx->stream));
+    return QMM_OK;
+}
+
+// MUL_MAT, MUL_MAT, GLU of an FFN (the chain the reference's fuse_mm_glu takes): the gate and up
+// sums go to a context scratch [2][batch][N][M], then the GLU kernel writes dst.  At GEMV widths
+// with one batch and one weight type a single GEMV launch streams both images (matrix 1 of the
+// launch is up's image, both read the same activation columns); otherwise two MUL_MATs share one
+// activation quantization.
+int qmm_mul_mat_glu(qmm_ctx * ctx, const qmm_tensor * gate, const qmm_tensor * up, const qmm_tensor * src1,
+                    const qmm_tensor * dst, int32_t glu_op) {
+    if (!ctx) return QMM_ERR_INVALID;
+    if (glu_op != QMM_GLU_REGLU && glu_op != QMM_GLU_GEGLU && glu_op != QMM_GLU_SWIGLU && glu_op != QMM_GLU_GEGLU_ERF &&
+        glu_op != QMM_GLU_GEGLU_QUICK)
+        return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat_glu: GLU op %d", glu_op);
+    char reason[160];
+    WView wg, wu;
+    if (!mul_mat_ok(gate, src1, dst, true, &wg, reason, sizeof(reason)))
+        return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat_glu: gate: %s", reason);
+    if (!mul_mat_ok(up, src1, dst, true, &wu, reason, sizeof(reason)))
+        return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat_glu: up: %s", reason);
+    if (memcmp(gate->ne, up->ne, sizeof(gate->ne))) return fail(ctx, QMM_ERR_INVALID, "mul_mat_glu: gate and up shapes differ");
+    QMM_HIP(ctx, hipSetDevice(ctx->device));
+    const int64_t M = gate->ne[1], N = src1->ne[1], ne12 = src1->ne[2], nb = src1->ne[2] * src1->ne[3];
+    const size_t half = (size_t)(M * N * nb);
+    int rc = ensure(ctx, &ctx->glu, &ctx->glu_cap, 2 * half * sizeof(float));
+    if (rc) return rc;
+    float * sg = (float *)ctx->glu, * su = sg + half;
+    const int type = gate->type;
+    const int nc = gemv_task_cols(type, N);
+    GemvPlan plan;
+    const bool fused = up->type == type && nb == 1 && N < gemm_min_cols(type) &&
+                       gemv_plan(type, wg, nc, (N + nc - 1) / nc * 2, true, nc >= gemv_mma_min_cols(), &plan);
+    if (fused) {
+        GemvDense dn;
+        dn.ne11 = N;
+        dn.ne12 = 2;                                              // batch 0: gate, 1: up
+        dn.ne13 = 1;
+        dn.r2 = dn.r3 = 1;
+        dn.ne02 = 2;
+        dn.d_nb1 = M;
+        dn.d_nb2 = M * N;
+        dn.d_nb3 = 2 * M * N;
+        dn.base2 = wu.base;
+        dn.col_bs = 0;                                            // both read src1's columns
+        ZeroJob z{ sg, M, 2 * N, N, 2, M, M * N, 2 * M * N, 0 };
+        ActBuf a{};
+        if ((rc = quantize_src1(ctx, type, src1, false, &a, plan.KS > 1 ? &z : nullptr))) return rc;
+        KTime kt;
+        const KTime * ktp;
+        if ((rc = ktime_pair(ctx, &kt, &ktp))) return rc;
+        QMM_HIP(ctx, launch_gemv(type, wg, plan, a, nullptr, nullptr, &dn, sg, ctx->sink, ctx->stream, ktp));
+        ctx->path = plan.mma ? "glu-fused-gemv-mfma" : "glu-fused-gemv";
+    } else {
+        qmm_buffer sb;
+        sb.ptr = ctx->glu;
+        sb.size = ctx->glu_cap;
+        qmm_tensor t[2];
+        for (int i = 0; i < 2; ++i) {
+            t[i] = qmm_tensor{};
+            t[i].type = QMM_TYPE_F32;
+            t[i].ne[0] = M;
+            t[i].ne[1] = N;
+            t[i].ne[2] = src1->ne[2];
+            t[i].ne[3] = src1->ne[3];
+            t[i].nb[0] = 4;
+            t[i].nb[1] = 4 * (size_t)M;
+            t[i].nb[2] = t[i].nb[1] * (size_t)N;
+            t[i].nb[3] = t[i].nb[2] * (size_t)src1->ne[2];
+            t[i].buffer = &sb;
+            t[i].offs = i * half * sizeof(float);
+        }
+        const bool outer = ctx->in_graph;                         // one quantization for both products
+        if (!outer) {
+            ctx->graph_gen++;
+            ctx->in_graph = true;
+        }
+        rc = qmm_mul_mat(ctx, gate, src1, &t[0]);
+        if (rc == QMM_OK) rc = qmm_mul_mat(ctx, up, src1, &t[1]);
+        if (!outer) ctx->in_graph = false;
+        if (rc) return rc;
+        ctx->path = "glu-" + ctx->path;
+    }
+    GluArgs g;
+    g.gate = sg;
+    g.up = su;
+    g.dst = (float *)((uint8_t *)dst->buffer->ptr + dst->offs);
+    g.M = M;
+    g.N = N;
+    g.nb = nb;
+    g.ne12 = ne12;
+    g.d_nb1 = (int64_t)(dst->nb[1] / 4);
+    g.d_nb2 = (int64_t)(dst->nb[2] / 4);
+    g.d_nb3 = (int64_t)(dst->nb[3] / 4);
+    QMM_HIP(ctx, launch_glu(glu_op, g, ctx->stream));
     return QMM_OK;
 }
 

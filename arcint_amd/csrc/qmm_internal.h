@@ -158,6 +158,10 @@ hipError_t launch_act_to_blocks(const ActBuf & a, void * out, hipStream_t s);
 struct GemvDense {
     int64_t ne11, ne12, ne13, r2, r3, ne02;
     int64_t d_nb1, d_nb2, d_nb3;   // dst strides in floats
+    // gate/up in one launch: matrix 1 is the image at base2 (same shape and type as matrix 0),
+    // and batch b reads activation columns b * col_bs + i1 (0: every batch the same columns)
+    const uint8_t * base2 = nullptr;
+    int64_t col_bs = -1;           // -1: ne11
 };
 
 // Launch shape of a GEMV (host): W waves per work-group and KS work-groups
@@ -249,6 +253,17 @@ struct CombineArgs {
     int64_t enb1, enb2, wnb1, snb1, gnb1, dnb1;
 };
 hipError_t launch_combine(const CombineArgs & a, hipStream_t s);
+
+// GLU of a gate/up pair: dst[m + n d_nb1 + i2 d_nb2 + i3 d_nb3] = act(gate[i]) * up[i], i over the
+// contiguous [nb][N][M] of gate and up (batch b = i2 + i3 ne12)
+struct GluArgs {
+    const float * gate;
+    const float * up;
+    float * dst;
+    int64_t M, N, nb, ne12;
+    int64_t d_nb1, d_nb2, d_nb3;   // floats
+};
+hipError_t launch_glu(int op, const GluArgs & a, hipStream_t s);
 
 // scratch: pairs [T*n_used]; tasks out
 hipError_t launch_route(const RouteArgs & r, int32_t * scratch, GemvTask * tasks, int32_t * ntasks,

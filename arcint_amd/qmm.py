@@ -24,6 +24,7 @@ LIB_PATH = os.path.join(_HERE, "libqmm.so")
 
 F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K, IQ4_NL, IQ4_XS, I32 = 0, 1, 2, 8, 12, 13, 14, 15, 20, 23, 26
 OP_MUL_MAT, OP_MUL_MAT_ID = 1, 2
+GLU_REGLU, GLU_GEGLU, GLU_SWIGLU, GLU_GEGLU_ERF, GLU_GEGLU_QUICK = 0, 1, 2, 4, 5
 QUANT_TYPES = (Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS)
 
 # every symbol include/qmm.h declares
@@ -34,7 +35,7 @@ EXPORTS = (
     "qmm_graph_compute", "qmm_dequantize", "qmm_quantize_act", "qmm_synchronize", "qmm_downgrades",
     "qmm_last_path", "qmm_timer_begin", "qmm_timer_end", "qmm_buffer_copy", "qmm_kernel_timing",
     "qmm_kernel_time", "qmm_tensor_pack", "qmm_tensor_unpack", "qmm_describe_mul_mat", "qmm_moe_topk",
-    "qmm_moe_combine",
+    "qmm_moe_combine", "qmm_mul_mat_glu",
 )
 
 
@@ -98,6 +99,7 @@ def load() -> C.CDLL:
         L.qmm_mul_mat_id.argtypes = [vp, T, T, T, T]
         L.qmm_moe_topk.argtypes = [vp, T, T, T, C.c_float, C.c_float]
         L.qmm_moe_combine.argtypes = [vp, T, T, T, T, T]
+        L.qmm_mul_mat_glu.argtypes = [vp, T, T, T, T, C.c_int32]
         L.qmm_graph_compute.argtypes = [vp, C.POINTER(CNode), C.c_int]
         L.qmm_dequantize.argtypes = [vp, T, T]
         L.qmm_quantize_act.argtypes = [vp, i32, T, vp, sz]
@@ -287,6 +289,11 @@ class Backend:
     def mul_mat_id(self, src0: Tensor, src1: Tensor, ids: Tensor, dst: Tensor):
         self._check(self.L.qmm_mul_mat_id(self.h, C.byref(src0.c), C.byref(src1.c), C.byref(ids.c), C.byref(dst.c)),
                     "mul_mat_id")
+
+    def mul_mat_glu(self, gate: Tensor, up: Tensor, src1: Tensor, dst: Tensor, op: int = GLU_SWIGLU):
+        """dst = act(gate x src1) * (up x src1): MUL_MAT, MUL_MAT and the split GLU in one call"""
+        self._check(self.L.qmm_mul_mat_glu(self.h, C.byref(gate.c), C.byref(up.c), C.byref(src1.c), C.byref(dst.c), op),
+                    "mul_mat_glu")
 
     def moe_topk(self, logits: Tensor, ids: Tensor, weights: Tensor, cmin: float = 6.103515625e-5,
                  cmax: float = float("inf")):

@@ -162,6 +162,50 @@ def gemv_case(be, qmm, synth, qtype, M, K, N, name, args):
     return sec
 
 
+def glu_case(be, qmm, synth, args):
+    """Config 2's FFN gate/up at decode (17408 x 5120 Q4_K each, N = 1) and its SwiGLU: the
+    fused call (one GEMV launch streams both images, then the GLU kernel) against the two
+    MUL_MATs alone (one graph: one activation quantization, two GEMV launches, no GLU).
+    GB/s counts both matrices' weight bytes."""
+    M, K, N = 17408, 5120, 1
+    _, wg = weight_copies(be, qmm, synth, qmm.Q4_K, M, K, seed=8)
+    _, wu = weight_copies(be, qmm, synth, qmm.Q4_K, M, K, seed=9)
+    x = synth.activations(N, K, seed=10)
+    xt = be.new_tensor(qmm.F32, (K, N))
+    be.set_tensor(xt, x.view(np.uint8).ravel())
+    yt = be.new_tensor(qmm.F32, (M, N))
+    yu = be.new_tensor(qmm.F32, (M, N))
+    steps = max(20, args.steps // 2)
+    nw = len(wg)
+
+    def run(n, fused):
+        for i in range(n):
+            g, u = wg[i % nw], wu[(i + 1) % nw]
+            if fused:
+                be.mul_mat_glu(g, u, xt, yt, qmm.GLU_SWIGLU)
+            else:
+                be.graph_compute([(qmm.OP_MUL_MAT, g, xt, None, yt), (qmm.OP_MUL_MAT, u, xt, None, yu)])
+
+    out = {"workload": "Q4_K FFN gate+up 2 x 17408x5120 N=1 + SwiGLU (config 2)"}
+    for fused in (True, False):
+        run(max(4, args.warmup // 2), fused)
+        be.synchronize()
+        t0 = time.perf_counter()
+        run(steps, fused)
+        be.synchronize()
+        out["fused_us" if fused else "two_gemv_us"] = round((time.perf_counter() - t0) * 1e6 / steps, 3)
+    run(1, True)
+    out["path"] = be.last_path()
+    wbytes = 2 * synth.row_bytes(qmm.Q4_K, K) * M
+    out["fused_GBs"] = round(wbytes / (out["fused_us"] * 1e-6) / 1e9, 1)
+    out["two_gemv_GBs"] = round(wbytes / (out["two_gemv_us"] * 1e-6) / 1e9, 1)
+    for w in wg + wu:
+        be.free_buffer(w.buf)
+    for t in (xt, yt, yu):
+        be.free_buffer(t.buf)
+    return out
+
+
 def moe_case(be, qmm, synth, T, args):
     """MUL_MAT_ID on config 3's expert gate/up: 512 Q4_K experts of 512 x 2048,
     top-10 routing, T tokens sharing one activation column each (ne11 = 1).
@@ -242,7 +286,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
-    ap.add_argument("--only", default="", help="profile one workload: q4k_gemv, q40_gemm, q4k_gemm, gemv or moe")
+    ap.add_argument("--only", default="", help="profile one workload: q4k_gemv, q40_gemm, q4k_gemm, gemv, glu or moe")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -319,6 +363,12 @@ def main():
             out["gemv"] = gem
         else:
             out = {"metric": "GEMV GB/s", "value": gem[0]["GBs"], "unit": "GB/s", "gemv": gem}
+    if not args.no_secondary and args.only in ("", "glu"):
+        g = glu_case(be, qmm, synth, args)
+        if out:
+            out["glu"] = g
+        else:
+            out = {"metric": "FFN gate+up GB/s", "value": g["fused_GBs"], "unit": "GB/s", "glu": g}
     if not args.no_secondary and args.only in ("", "moe"):
         moe = [moe_case(be, qmm, synth, T, args) for T in (1, 4, 256)]
         if out:

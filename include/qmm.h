@@ -98,6 +98,16 @@ enum qmm_op {
     QMM_OP_MUL_MAT_ID = 2,
 };
 
+/* GLU activations of qmm_mul_mat_glu: ggml's enum ggml_glu_op names (REGLU, GEGLU, SWIGLU,
+ * GEGLU_ERF, GEGLU_QUICK; SWIGLU_OAI is not taken) with values of this ABI */
+enum qmm_glu {
+    QMM_GLU_REGLU       = 0,
+    QMM_GLU_GEGLU       = 1,
+    QMM_GLU_SWIGLU      = 2,
+    QMM_GLU_GEGLU_ERF   = 4,
+    QMM_GLU_GEGLU_QUICK = 5,
+};
+
 enum qmm_status {
     QMM_OK            = 0,
     QMM_ERR_INVALID   = 1,   /* shape / type / stride precondition */
@@ -182,6 +192,15 @@ int    qmm_supports_op(qmm_ctx * ctx, int32_t op, const qmm_tensor * src0, const
 int    qmm_mul_mat(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1, const qmm_tensor * dst);
 int    qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1,
                       const qmm_tensor * ids, const qmm_tensor * dst);
+/* The FFN's gate/up pair and its GLU in one call: dst = act(gate x src1) * (up x src1), act =
+ * enum qmm_glu, gate and up quantized [K, M, ne02, ne03] of one shape, src1 / dst as MUL_MAT's.
+ * Replaces MUL_MAT, MUL_MAT, GLU (split form), the node chain the reference's fuse_mm_glu
+ * matches (P01:65; ggml-opencl.cpp:9836-9878 by the reference's audit,
+ * docs/campaigns/research-concept-mining/ipex-llm/audit.md:83-87).  One activation
+ * quantization serves both; at GEMV widths with one batch and one weight type both matrices
+ * stream in one launch.  Within MUL_MAT's tolerance of the unfused chain. */
+int    qmm_mul_mat_glu(qmm_ctx * ctx, const qmm_tensor * gate, const qmm_tensor * up, const qmm_tensor * src1,
+                       const qmm_tensor * dst, int32_t glu_op);
 /* Runs the nodes in order; bumps the graph generation first, so one
  * activation quantization serves every node of the graph that reads the same
  * src1 with the same vec_dot type. */

@@ -697,3 +697,76 @@ def test_moe_layer_end_to_end(be, sc, orc):
             ref_e[t, j] = orc.mul_mat(qmm.Q4_K, raw[e * rb:(e + 1) * rb], M, K, x[t:t + 1])[0]
     ref = moe.combine(ref_e, ref_w.astype(np.float32))
     assert rel_err(got, ref) <= TOL
+
+
+# ------------------------------------------------------------------ gate/up + GLU
+GLU_OPS = [qmm.GLU_REGLU, qmm.GLU_GEGLU, qmm.GLU_SWIGLU, qmm.GLU_GEGLU_ERF, qmm.GLU_GEGLU_QUICK]
+
+
+def glu_case(be, sc, orc, gtype, utype, M, K, N, op, seed, batches=(1, 1)):
+    from oracle import glu as G
+    b2, b3 = batches
+    rg, ru = synth.weights(gtype, M, K, seed), synth.weights(utype, M, K, seed + 1)
+    wg, wu = sc.weights(gtype, rg, (K, M)), sc.weights(utype, ru, (K, M))
+    x = synth.activations(N * b2 * b3, K, seed + 2)
+    xt = sc.f32(x.reshape(b3, b2, N, K))
+    y = sc.empty_f32((M, N, b2, b3))
+    be.mul_mat_glu(wg, wu, xt, y, op)
+    be.synchronize()
+    got = be.get_f32(y).reshape(b2 * b3 * N, M)
+    ref = G.glu(op, orc.mul_mat(gtype, rg, M, K, x), orc.mul_mat(utype, ru, M, K, x))
+    return got, ref
+
+
+@pytest.mark.parametrize("qtype", [qmm.Q4_K, qmm.Q4_0, qmm.Q6_K, qmm.Q5_K, qmm.IQ4_NL])
+@pytest.mark.parametrize("N", [1, 4, 20])
+def test_mul_mat_glu_fused(be, sc, orc, qtype, N):
+    """one GEMV launch over gate and up (both images, the same columns), then the GLU"""
+    M, K = 300, 1024
+    if N >= 16 and qtype in (qmm.Q6_K, qmm.Q5_K):
+        N = 12                                                        # their GEMM starts at 16
+    say("glu-fused", qtype, N)
+    got, ref = glu_case(be, sc, orc, qtype, qtype, M, K, N, qmm.GLU_SWIGLU, seed=101)
+    assert be.last_path().startswith("glu-fused-gemv")
+    assert rel_err(got, ref) <= TOL
+
+
+@pytest.mark.parametrize("op", GLU_OPS)
+def test_mul_mat_glu_ops(be, sc, orc, op):
+    say("glu-op", op)
+    got, ref = glu_case(be, sc, orc, qmm.Q4_K, qmm.Q4_K, 256, 512, 2, op, seed=111)
+    assert rel_err(got, ref) <= TOL
+
+
+def test_mul_mat_glu_split_paths(be, sc, orc):
+    """the unfused forms: mixed weight types, the GEMM (N >= the crossover), broadcast batches"""
+    say("glu-split mixed")
+    got, ref = glu_case(be, sc, orc, qmm.Q4_K, qmm.Q6_K, 200, 1024, 3, qmm.GLU_SWIGLU, seed=121)
+    assert be.last_path().startswith("glu-") and not be.last_path().startswith("glu-fused")
+    assert rel_err(got, ref) <= TOL
+    say("glu-split gemm")
+    got, ref = glu_case(be, sc, orc, qmm.Q4_0, qmm.Q4_0, 200, 1024, 40, qmm.GLU_GEGLU, seed=122)
+    assert be.last_path() == "glu-gemm-mfma"
+    assert rel_err(got, ref) <= TOL
+    say("glu-split batches")
+    got, ref = glu_case(be, sc, orc, qmm.Q4_K, qmm.Q4_K, 130, 512, 2, qmm.GLU_SWIGLU, seed=123, batches=(3, 2))
+    assert rel_err(got, ref) <= TOL
+
+
+def test_mul_mat_glu_full_size_decode(be, sc, orc):
+    """config 2's FFN gate/up (17408 x 5120 Q4_K) at N = 1"""
+    say("glu-full")
+    got, ref = glu_case(be, sc, orc, qmm.Q4_K, qmm.Q4_K, 17408, 5120, 1, qmm.GLU_SWIGLU, seed=131)
+    assert be.last_path() == "glu-fused-gemv"
+    assert rel_err(got, ref) <= TOL
+
+
+def test_mul_mat_glu_rejects(be, sc):
+    K, M = 512, 64
+    w1 = sc.weights(qmm.Q4_K, synth.weights(qmm.Q4_K, M, K, 1), (K, M))
+    w2 = sc.weights(qmm.Q4_K, synth.weights(qmm.Q4_K, 2 * M, K, 2), (K, 2 * M))
+    x, y = sc.f32(synth.activations(1, K, 3)), sc.empty_f32((M, 1))
+    with pytest.raises(qmm.QmmError):
+        be.mul_mat_glu(w1, w2, x, y, qmm.GLU_SWIGLU)                 # shapes differ
+    with pytest.raises(qmm.QmmError):
+        be.mul_mat_glu(w1, w1, x, y, 3)                              # SWIGLU_OAI is not taken
