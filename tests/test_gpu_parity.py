@@ -770,3 +770,25 @@ def test_mul_mat_glu_rejects(be, sc):
         be.mul_mat_glu(w1, w2, x, y, qmm.GLU_SWIGLU)                 # shapes differ
     with pytest.raises(qmm.QmmError):
         be.mul_mat_glu(w1, w1, x, y, 3)                              # SWIGLU_OAI is not taken
+
+
+# ------------------------------------------------------------------ permuted src1
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("nr", [4, 8, 12])
+def test_mul_mat_permuted_src1(be, sc, orc, qtype, nr):
+    """test-backend-ops' permuted src1 (the reference's review cases m = 256, n = 1, k = 2048,
+    nr = 4 / 8 / 12, per = [0, 2, 1, 3], contrib/llama.cpp/README.md:6864): src1 [K, 1, nr] is a
+    permutation of a contiguous [K, nr, 1], so nb1 = 4 K nr and nb2 = 4 K; the activation prep
+    must step columns by the strides, not by 4 K"""
+    M, K = 256, 2048
+    say("permuted-src1", qtype, nr)
+    raw = synth.weights(qtype, M, K, seed=141)
+    w = sc.weights(qtype, raw, (K, M))
+    x = synth.activations(nr, K, seed=142)                      # row i2: the activation of batch i2
+    base = sc.f32(x)                                            # contiguous [K, nr]
+    xp = qmm.Tensor(base.buf, qmm.F32, (K, 1, nr), nb=(4, 4 * K * nr, 4 * K, 4 * K * nr))
+    y = sc.empty_f32((M, 1, nr))
+    be.mul_mat(w, xp, y)
+    be.synchronize()
+    got = be.get_f32(y).reshape(nr, M)
+    assert rel_err(got, orc.mul_mat(qtype, raw, M, K, x)) <= TOL
