@@ -617,15 +617,21 @@ __device__ __forceinline__ void bf_epilogue(const v16i & e0, const v16i & e1, fl
 // column).  A scheduling barrier per block bounds the live MFMA results: the K-quants issue
 // block j's MFMAs before they consume block j - 1's, Q4_0 / Q8_0 / IQ4_NL (whose magic
 // accumulator input takes 16 more registers) consume each block's in its own group.
-template <int TYPE, int CM>
-__device__ __forceinline__ void mma_stage(const uint4 (&rw)[9], int st, const uint8_t * xag, const float * xdg,
-                                          const uint8_t * xsg, int h, const v16i & magic, vNf<CM> & out) {
+// Q6_K (two stages per group, `iacc` carrying the super-block's integer sum across them):
+// block g of half st is 32 weights whose k halves (lane halves after the swap) have their own
+// int8 scales, so each takes its own MFMA with the other half's operand zero.
+template <int TYPE, int CM, int NL>
+__device__ __forceinline__ void mma_stage(const uint4 (&rw)[NL], int st, const uint8_t * xag, const float * xdg,
+                                          const uint8_t * xsg, int h, const v16i & magic, vNf<CM> & out,
+                                          vNi<CM> & iacc) {
     constexpr int NR = CM / 2;
     constexpr bool KQ = TYPE == QMM_TYPE_Q4_K, IQ = TYPE == QMM_TYPE_IQ4_XS, Q8 = TYPE == QMM_TYPE_Q8_0;
     constexpr bool NLQ = TYPE == QMM_TYPE_IQ4_NL;                // Q4_0's blocks through the codebook
+    constexpr bool Q6 = TYPE == QMM_TYPE_Q6_K;
     constexpr bool BF = TYPE == QMM_TYPE_Q4_0 || Q8 || NLQ;
+    constexpr bool HALVES = Q8 || Q6;                             // a group takes two stages
     constexpr int NB = Q8 ? 4 : 8;                                // 32-weight blocks per stage
-    auto a_op = [&](int b) -> v4i { return *reinterpret_cast<const v4i *>(xag + 32 * (Q8 ? 4 * st + b : b)); };
+    auto a_op = [&](int b) -> v4i { return *reinterpret_cast<const v4i *>(xag + 32 * (HALVES ? 4 * st + b : b)); };
     // the lane's NR column scales of block b: quads at columns 8 q + 4 h
     auto dx_op = [&](int b, float (&d)[NR]) {
         const float * x = xdg + (Q8 ? 4 * st + b : b) * CM;
@@ -727,6 +733,56 @@ __device__ __forceinline__ void mma_stage(const uint4 (&rw)[9], int st, const ui
             out[r] += dx0[r] * (d[0] * (float)isc[r] - dmin[0] * (float)imn0);
             out[NR + r] += dx0[r] * (d[1] * (float)isc[NR + r] - dmin[1] * (float)imn1);
         }
+    } else if constexpr (Q6) {
+        // half st: ql chunks rw[0..3] (4 st + c), qh rw[4], rw[5] (lh = 0, 1), the 16 scales rw[6],
+        // d in rw[7].x.  Block g, half lh: codes from ql rw[2 (g & 1) + lh] (low nibble g < 2, high
+        // g >= 2) and bits 2g of qh rw[4 + lh], minus 32; scale index 8 st + 2 g + lh
+        if (st == 0) iacc = vNi<CM>{};
+        const uint32_t scw[4] = { rw[6].x, rw[6].y, rw[6].z, rw[6].w };
+        v4i an = a_op(0);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            uint4 half[2];
+#pragma unroll
+            for (int lh = 0; lh < 2; ++lh) {
+                const uint4 ql = rw[2 * (g & 1) + lh], qh = rw[4 + lh];
+                const int sh = g < 2 ? 0 : 4;
+                auto code = [&](uint32_t l, uint32_t hb) {
+                    const uint32_t c = ((l >> sh) & 0x0F0F0F0Fu) | (((hb >> (2 * g)) & 0x03030303u) << 4);
+                    return ((c | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+                };
+                half[lh] = make_uint4(code(ql.x, qh.x), code(ql.y, qh.y), code(ql.z, qh.z), code(ql.w, qh.w));
+            }
+            v4i op0, op1;
+            swap_halves(half[0], half[1], op0, op1);
+            // the row scales of halves lh = 0, 1 in the output lanes (rows 0-31: s?0, 32-63: s?1)
+            const int is0 = 8 * st + 2 * g, is1 = is0 + 1;
+            uint32_t a0, a1, b0, b1;
+            swap_rows((scw[is0 >> 2] >> (8 * (is0 & 3))) & 0xffu, a0, a1);
+            swap_rows((scw[is1 >> 2] >> (8 * (is1 & 3))) & 0xffu, b0, b1);
+            const v4i av = an;
+            if (g + 1 < 4) an = a_op(g + 1);
+            const v4i z = v4i{};
+            const v16i l0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, h ? z : op0, v16i{}, 0, 0, 0);
+            const v16i l1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, h ? z : op1, v16i{}, 0, 0, 0);
+            scale_add<NR>(l0, l1, (int)(int8_t)a0, (int)(int8_t)a1, iacc);
+            __builtin_amdgcn_sched_barrier(0);
+            const v16i u0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, h ? op0 : z, v16i{}, 0, 0, 0);
+            const v16i u1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, h ? op1 : z, v16i{}, 0, 0, 0);
+            scale_add<NR>(u0, u1, (int)(int8_t)b0, (int)(int8_t)b1, iacc);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (st == 1) {                                            // the super-block's float combine
+            float dx0[NR];
+            dx_op(0, dx0);
+            uint32_t dd0, dd1;
+            swap_rows(rw[7].x & 0xffffu, dd0, dd1);
+            const float d[2] = { h2f(dd0), h2f(dd1) };
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < NR; ++r) out[NR * t + r] += dx0[r] * (d[t] * (float)iacc[NR * t + r]);
+        }
     } else if constexpr (IQ) {
         const uint32_t shi = rw[8].x >> 16, slo = rw[8].y;
         vNi<CM> isum = {};
@@ -773,7 +829,6 @@ template <int TYPE, int CM>
 __device__ __forceinline__ void gemv_mma_body(const GemvParams & p) {
     using T = GV<TYPE>;
     constexpr int NL = T::NL, NST = T::NST, NR = CM / 2;
-    static_assert(NL == 9, "mma_stage takes 9 weight registers");
     constexpr bool KQ = TYPE == QMM_TYPE_Q4_K, Q8 = TYPE == QMM_TYPE_Q8_0;
     constexpr bool BF = TYPE == QMM_TYPE_Q4_0 || Q8 || TYPE == QMM_TYPE_IQ4_NL;   // a float scale per 32 weights
     constexpr int BS = BF ? 32 : 256;                             // activation scale block
@@ -873,12 +928,13 @@ __device__ __forceinline__ void gemv_mma_body(const GemvParams & p) {
     // the scales of the lane's output columns (quads 8 q + 4 h), per (group, block)
     const float * xdr = xdl + (ga - gw) * NSB * CM + 4 * h;
     vNf<CM> out = {};
+    vNi<CM> iacc = {};                                            // Q6_K: the super-block's integer sum
     v16i magic;
 #pragma unroll
     for (int r = 0; r < 16; ++r) magic[r] = kMagic;
     auto compute = [&](const uint4 (&b)[NL], int s) {
         const int gl = s / NST;
-        mma_stage<TYPE, CM>(b, s % NST, xar + gl * xas, xdr + gl * NSB * CM, xsr + gl * xss, h, magic, out);
+        mma_stage<TYPE, CM, NL>(b, s % NST, xar + gl * xas, xdr + gl * NSB * CM, xsr + gl * xss, h, magic, out, iacc);
     };
     for (int s = 0; s < S; s += 2) {                              // uniform
         load_stage(b1, s + 1);
@@ -961,7 +1017,7 @@ int env_int(const char * name, int dflt) {
 
 bool gemv_mma_supported(int type) {
     return type == QMM_TYPE_Q4_0 || type == QMM_TYPE_Q8_0 || type == QMM_TYPE_Q4_K || type == QMM_TYPE_IQ4_XS ||
-           type == QMM_TYPE_IQ4_NL;
+           type == QMM_TYPE_IQ4_NL || type == QMM_TYPE_Q6_K;
 }
 
 bool gemv_plan(int type, const WView & w, int nc, int64_t ntasks, bool allow_split, bool want_mma, GemvPlan * pl) {
@@ -1109,6 +1165,7 @@ hipError_t launch_gemv(int type, const WView & w, const GemvPlan & pl, const Act
             case QMM_TYPE_Q4_K: { QMM_MMA(QMM_TYPE_Q4_K) }
             case QMM_TYPE_IQ4_XS: { QMM_MMA(QMM_TYPE_IQ4_XS) }
             case QMM_TYPE_IQ4_NL: { QMM_MMA(QMM_TYPE_IQ4_NL) }
+            case QMM_TYPE_Q6_K: { QMM_MMA(QMM_TYPE_Q6_K) }
             default: return hipErrorInvalidValue;
         }
 #undef QMM_MMA

@@ -608,14 +608,15 @@ static int gemv_mma_min_cols() {
 
 // columns at or above which MUL_MAT goes to the MFMA GEMM instead of the GEMV (32 columns per
 // weight pass on the MFMA GEMV, 8 on v_dot4).  Measured crossovers on MI355X (config shapes):
-// Q4_K's GEMV wins to ~100 columns (17408 x 5120: 69 us against 82 at 96), IQ4_XS's to 64,
-// Q4_0 / Q8_0 / IQ4_NL's to one pass (their GEMM keeps up from 33); the v_dot4 types switch
-// at 16.  QMM_GEMM_MIN_COLS overrides.
+// Q4_K's GEMV wins to ~100 columns (17408 x 5120: 69 us against 82 at 96), Q6_K's too (5120 x
+// 17408: 80 against 94 at 96), IQ4_XS's to 64, Q4_0 / Q8_0 / IQ4_NL's to one pass (their GEMM
+// keeps up from 33); Q5_K (v_dot4 only) switches at 16.  QMM_GEMM_MIN_COLS overrides.
 static int64_t gemm_min_cols(int type) {
     const char * e = getenv("QMM_GEMM_MIN_COLS");
     if (e) return std::max<int64_t>(1, atoll(e));
     switch (type) {
         case QMM_TYPE_Q4_K:   return 128;
+        case QMM_TYPE_Q6_K:   return 97;
         case QMM_TYPE_IQ4_XS: return 65;
         case QMM_TYPE_Q4_0:
         case QMM_TYPE_Q8_0:

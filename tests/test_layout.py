@@ -240,7 +240,7 @@ def test_gemv_plan(qtype, K, M, N):
                                 qmm.Tensor(fake, qmm.F32, (M, N)))
     # the MFMA kernel takes 3 and more columns of the types whose blocks it decodes, up to 32 a
     # weight pass; v_dot4 8; the columns spread evenly over the fewest passes
-    mma = N >= 3 and qtype in (qmm.Q4_0, qmm.Q8_0, qmm.Q4_K, qmm.IQ4_XS, qmm.IQ4_NL)
+    mma = N >= 3 and qtype in (qmm.Q4_0, qmm.Q8_0, qmm.Q4_K, qmm.IQ4_XS, qmm.IQ4_NL, qmm.Q6_K)
     assert info["path"] == ("gemv-mfma" if mma else "gemv")
     G, nt = -(-K // 256), -(-M // 64)
     W, KS, spw, nc = info["k_waves"], info["k_slices"], info["groups_per_wave"], info["cols_per_task"]
