@@ -430,6 +430,12 @@ __global__ __launch_bounds__(512) void k_gemv(GemvParams p) {
         const GemvTask & t = p.tasks[task];
         mat = t.mat;
         nc = t.ncols < NC ? t.ncols : NC;
+        if (mat < 0) {                                            // pairs of invalid ids: zero rows
+            const int64_t row = (int64_t)tile * kTileRows + lane;
+            if (ks == 0 && wave == 0 && row < p.w.M)
+                for (int j = 0; j < nc; ++j) p.dst[t.dst_off[j] + row] = 0.0f;
+            return;                                               // uniform
+        }
         if (tid < nc) {
             s_col[tid] = t.col[tid];
             s_doff[tid] = t.dst_off[tid];
@@ -853,6 +859,13 @@ __device__ __forceinline__ void gemv_mma_body(const GemvParams & p) {
         const GemvTask & t = p.tasks[task];
         mat = t.mat;
         nc = t.ncols < kMaxTaskCols ? t.ncols : kMaxTaskCols;
+        if (mat < 0) {                                            // pairs of invalid ids: zero rows
+            const uint32_t ztile = tb * (uint32_t)TW + (uint32_t)tw;
+            const int64_t row = (int64_t)ztile * kTileRows + lane;
+            if (ks == 0 && kw == 0 && ztile < ntl && row < p.w.M)
+                for (int j = 0; j < nc; ++j) p.dst[t.dst_off[j] + row] = 0.0f;
+            return;                                               // uniform
+        }
         if (tid < nc) {
             s_col[tid] = t.col[tid];
             s_doff[tid] = t.dst_off[tid];

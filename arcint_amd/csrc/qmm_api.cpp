@@ -46,9 +46,17 @@ struct qmm_ctx {
     ActBuf cached{};
     // MoE route scratch: ids copy, tasks, task count
     void * route = nullptr;
+    size_t route_cap = 0;
+    // the route in the scratch, reused inside one graph by products with the same ids, ne11,
+    // dst strides and expert count (the reference's route cache, P01:1267-1269)
+    struct RouteKey {
+        qmm_tensor ids{};
+        int64_t ne11 = 0, n_as = 0, dnb1 = 0, dnb2 = 0;
+        uint64_t gen = 0;
+        bool valid = false;
+    } rkey;
     size_t glu_cap = 0;
     void * glu = nullptr;            // gate/up sums of qmm_mul_mat_glu
-    size_t route_cap = 0;
     // downgrade counter (paths slower than the type promises)
     int64_t downgrades = 0;
     std::string downgrade_names;
@@ -485,7 +493,7 @@ static int tensor_io(qmm_ctx * ctx, const qmm_tensor * t, void * host, size_t of
     const TypeLayout * L = type_layout(t->type);
     const qmm_tensor * b = L ? base_of(t) : t;
     if (!b->buffer) return fail(ctx, QMM_ERR_INVALID, "tensor io: no buffer");
-    if (write) ctx->key.valid = false;
+    if (write) ctx->key.valid = ctx->rkey.valid = false;
     if (!L) {   // the device bytes are the plain bytes
         if (t->offs > b->buffer->size || offset + size > b->buffer->size - t->offs)
             return fail(ctx, QMM_ERR_INVALID, "tensor io: range past its buffer");
@@ -738,13 +746,14 @@ int qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * sr
     if (!mul_mat_id_ok(src0, src1, ids, dst, true, &w, reason, sizeof(reason)))
         return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat_id: %s", reason);
     QMM_HIP(ctx, hipSetDevice(ctx->device));
-    const int64_t M = src0->ne[1], n_as = src0->ne[2];
+    const int64_t n_as = src0->ne[2];
     const int64_t n_used = ids->ne[0], T = ids->ne[1], ne11 = src1->ne[1];
     ActBuf a{};
     int rc;
     if ((rc = quantize_src1(ctx, src0->type, src1, false, &a))) return rc;
     const int64_t npairs = n_used * T;
-    const int64_t max_tasks = npairs / kMaxTaskCols + std::min(n_as, npairs) + 1;
+    // (one more bucket: the pairs of invalid ids)
+    const int64_t max_tasks = npairs / kMaxTaskCols + std::min(n_as + 1, npairs) + 1;
     const int nc = (int)std::min<int64_t>(kMaxTaskCols, npairs);
     GemvPlan plan;
     // tasks carry 1..8 pairs each: the MFMA kernel pays off when experts average two or more
@@ -768,7 +777,21 @@ int qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * sr
     float * d = (float *)((uint8_t *)dst->buffer->ptr + dst->offs);
     GemvTask * tasks = (GemvTask *)(rb + o_tasks);
     int32_t * ntasks = (int32_t *)(rb + o_cnt);
-    QMM_HIP(ctx, launch_route(r, (int32_t *)rb, tasks, ntasks, d, M, ctx->stream));
+    auto & rk = ctx->rkey;
+    const bool hit = ctx->in_graph && rk.valid && rk.gen == ctx->graph_gen && rk.ids.buffer == ids->buffer &&
+                     rk.ids.offs == ids->offs && !memcmp(rk.ids.ne, ids->ne, sizeof(ids->ne)) &&
+                     !memcmp(rk.ids.nb, ids->nb, sizeof(ids->nb)) && rk.ne11 == ne11 && rk.n_as == n_as &&
+                     rk.dnb1 == r.dst_nb1 && rk.dnb2 == r.dst_nb2;
+    if (!hit) {
+        QMM_HIP(ctx, launch_route(r, (int32_t *)rb, tasks, ntasks, ctx->stream));
+        rk.ids = *ids;
+        rk.ne11 = ne11;
+        rk.n_as = n_as;
+        rk.dnb1 = r.dst_nb1;
+        rk.dnb2 = r.dst_nb2;
+        rk.gen = ctx->graph_gen;
+        rk.valid = ctx->in_graph;
+    }
     ctx->path = plan.mma ? "gemv-id-mfma" : "gemv-id";
     KTime kt;
     const KTime * ktp;
@@ -963,6 +986,7 @@ int qmm_graph_compute(qmm_ctx * ctx, const qmm_node * nodes, int n_nodes) {
             memcpy(src.nb, ctx->key.nb, sizeof(src.nb));
             if (ranges_overlap(&src, n.dst)) ctx->key.valid = false;
         }
+        if (ctx->rkey.valid && ranges_overlap(&ctx->rkey.ids, n.dst)) ctx->rkey.valid = false;
     }
     ctx->in_graph = false;
     return rc;

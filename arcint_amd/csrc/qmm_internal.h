@@ -266,7 +266,7 @@ struct GluArgs {
 hipError_t launch_glu(int op, const GluArgs & a, hipStream_t s);
 
 // scratch: pairs [T*n_used]; tasks out
-hipError_t launch_route(const RouteArgs & r, int32_t * scratch, GemvTask * tasks, int32_t * ntasks,
-                        float * dst, int64_t M, hipStream_t s);
+// tasks of mat = -1 carry pairs of invalid ids: the GEMV writes their dst rows as zeros
+hipError_t launch_route(const RouteArgs & r, int32_t * scratch, GemvTask * tasks, int32_t * ntasks, hipStream_t s);
 
 }  // namespace qmm

@@ -792,3 +792,56 @@ def test_mul_mat_permuted_src1(be, sc, orc, qtype, nr):
     be.synchronize()
     got = be.get_f32(y).reshape(nr, M)
     assert rel_err(got, orc.mul_mat(qtype, raw, M, K, x)) <= TOL
+
+
+# ------------------------------------------------------------------ MoE: invalid ids, the route cache
+@pytest.mark.parametrize("qtype", [qmm.Q4_K, qmm.Q4_0])
+@pytest.mark.parametrize("T", [1, 6, 40])
+def test_mul_mat_id_invalid_ids_write_zero_rows(be, sc, orc, qtype, T):
+    """negative and out-of-range ids (P02:98-103) write zero rows over whatever dst held, on the
+    v_dot4 and (T = 40: 160 pairs on 16 experts) MFMA task paths"""
+    E, n_used, M, K = 16, 4, 130, 512
+    say("mul_mat_id-invalid", qtype, T)
+    raw = synth.weights(qtype, E * M, K, seed=151)
+    ids = synth.moe_ids(T, E, n_used, seed=152)
+    ids[0, 1] = -1
+    if T > 1:
+        ids[1, 0] = E                                             # out of range
+        ids[T - 1, :] = [-7, E + 3, -1, E]                        # a whole token of invalid ids
+    x = synth.activations(T, K, seed=153).reshape(T, 1, K)
+    w = sc.weights(qtype, raw, (K, M, E))
+    y = sc.f32(np.full((T, n_used, M), 7.0, np.float32))          # dst holds non-zeros
+    be.mul_mat_id(w, sc.f32(x), sc.i32(ids), y)
+    be.synchronize()
+    got = be.get_f32(y).reshape(T, n_used, M)
+    ref = orc.mul_mat_id(qtype, raw, M, K, E, x, ids)
+    bad = (ids < 0) | (ids >= E)
+    assert (got[bad] == 0).all()
+    assert rel_err(got[~bad], ref[~bad]) <= TOL
+
+
+def test_graph_route_shared_by_gate_and_up(be, sc, orc):
+    """gate and up MUL_MAT_IDs with the same ids in one graph reuse one route (the second
+    launches no routing); the down projection (ne11 = n_used) routes again"""
+    E, n_used, M, K, T = 32, 4, 64, 512, 9
+    say("graph-route-cache")
+    rg, ru = synth.weights(qmm.Q4_K, E * M, K, 161), synth.weights(qmm.Q4_K, E * M, K, 162)
+    rd = synth.weights(qmm.Q4_K, E * K, M * 4, 163)               # down: [4M, K, E] (K' = 4 M)
+    ids = synth.moe_ids(T, E, n_used, seed=164)
+    ids[2, 1] = -1
+    wg, wu = sc.weights(qmm.Q4_K, rg, (K, M, E)), sc.weights(qmm.Q4_K, ru, (K, M, E))
+    wd = sc.weights(qmm.Q4_K, rd, (4 * M, K, E))
+    x = synth.activations(T, K, seed=165).reshape(T, 1, K)
+    xd = synth.activations(T * n_used, 4 * M, seed=166).reshape(T, n_used, 4 * M)
+    xt, xdt, it = sc.f32(x), sc.f32(xd), sc.i32(ids)
+    yg, yu = sc.f32(np.full((T, n_used, M), 3.0, np.float32)), sc.f32(np.full((T, n_used, M), 3.0, np.float32))
+    yd = sc.f32(np.full((T, n_used, K), 3.0, np.float32))
+    be.graph_compute([(qmm.OP_MUL_MAT_ID, wg, xt, it, yg), (qmm.OP_MUL_MAT_ID, wu, xt, it, yu),
+                      (qmm.OP_MUL_MAT_ID, wd, xdt, it, yd)])
+    be.synchronize()
+    bad = ids < 0
+    for y, raw, xx, m, k in ((yg, rg, x, M, K), (yu, ru, x, M, K), (yd, rd, xd, K, 4 * M)):
+        got = be.get_f32(y).reshape(T, n_used, m)
+        ref = orc.mul_mat_id(qmm.Q4_K, raw, m, k, E, xx, ids)
+        assert (got[bad] == 0).all()
+        assert rel_err(got[~bad], ref[~bad]) <= TOL
