@@ -54,8 +54,10 @@ struct GemvParams {
     int64_t d_nb1, d_nb2, d_nb3; // dst strides in floats
     float * dst;
     const uint8_t * sink;        // >= kSinkBytes of readable memory for loads past the end
-    const uint8_t * base2;       // dense mode: the image of matrix 1 (gate/up in one launch), or null
+    const uint8_t * base2;       // gate/up in one launch: the second image (dense: matrix 1; lists:
+                                 // the task list runs twice, the second time on this stack), or null
     int64_t col_bs;              // dense mode: activation columns per batch
+    int64_t up_doff;             // lists with base2: floats added to the second pass's dst offsets
     int W;                       // waves per work-group
     int KS;                      // work-groups per tile (K slices); > 1: atomics into zeroed dst
     int spw;                     // groups per wave
@@ -63,12 +65,12 @@ struct GemvParams {
     int tw;                      // MFMA kernel: tiles per work-group (W / tw waves split K)
 };
 
-// tile-group 0 of (matrix, tile): matrix 1 of a gate/up launch is a second image
-__device__ __forceinline__ const uint8_t * mat_tile(const GemvParams & p, int mat, uint32_t tile) {
-    if (p.base2 && mat == 1) {
+// tile-group 0 of (matrix, tile) of the first image, or (sec) of the second
+__device__ __forceinline__ const uint8_t * mat_tile(const GemvParams & p, int mat, uint32_t tile, bool sec) {
+    if (sec) {
         WView w2 = p.w;
         w2.base = p.base2;
-        return tile_group(w2, 0, tile, 0);
+        return tile_group(w2, mat, tile, 0);
     }
     return tile_group(p.w, mat, tile, 0);
 }
@@ -425,26 +427,37 @@ __global__ __launch_bounds__(512) void k_gemv(GemvParams p) {
     const uint32_t ks = blockIdx.x % (uint32_t)p.KS, rest = blockIdx.x / (uint32_t)p.KS;
     const uint32_t tile = rest % ntl, task = rest / ntl;
     int mat, nc;
+    bool sec = false;                  // the second image (gate/up in one launch)
     if (p.tasks) {
-        if (p.ntasks_dev && (int)task >= *p.ntasks_dev) return;     // uniform
-        const GemvTask & t = p.tasks[task];
+        uint32_t tk = task;
+        if (p.base2 && p.ntasks_dev && (int)tk >= *p.ntasks_dev) {  // the second pass over the list
+            tk -= (uint32_t)*p.ntasks_dev;
+            sec = true;
+        }
+        if (p.ntasks_dev && (int)tk >= *p.ntasks_dev) return;     // uniform
+        const GemvTask & t = p.tasks[tk];
+        const int64_t dadd = sec ? p.up_doff : 0;
         mat = t.mat;
         nc = t.ncols < NC ? t.ncols : NC;
         if (mat < 0) {                                            // pairs of invalid ids: zero rows
             const int64_t row = (int64_t)tile * kTileRows + lane;
             if (ks == 0 && wave == 0 && row < p.w.M)
-                for (int j = 0; j < nc; ++j) p.dst[t.dst_off[j] + row] = 0.0f;
+                for (int j = 0; j < nc; ++j) p.dst[t.dst_off[j] + dadd + row] = 0.0f;
             return;                                               // uniform
         }
         if (tid < nc) {
             s_col[tid] = t.col[tid];
-            s_doff[tid] = t.dst_off[tid];
+            s_doff[tid] = t.dst_off[tid] + dadd;
         }
     } else {
         const uint32_t tpb = (uint32_t)p.tpb, ne12 = (uint32_t)p.ne12;
         const uint32_t b = task / tpb, tt = task - b * tpb;
         const uint32_t i3 = b / ne12, i2 = b - i3 * ne12;
         mat = (int)(i2 / (uint32_t)p.r2 + (i3 / (uint32_t)p.r3) * (uint32_t)p.ne02);
+        if (p.base2 && mat == 1) {                                // gate/up in one launch
+            mat = 0;
+            sec = true;
+        }
         const int64_t first = (int64_t)tt * NC;
         nc = (int)((p.ne11 - first) < NC ? (p.ne11 - first) : NC);
         if (tid < nc) {
@@ -461,7 +474,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvParams p) {
     const int ga = ((int)ks * p.W + wave) * p.spw;                // this wave's groups [ga, gb)
     const int gb = ga + p.spw < G ? ga + p.spw : G;
     const int S = ga < gb ? (gb - ga) * NST : 0;                  // stages (uniform)
-    const uint8_t * tbase = mat_tile(p, mat, tile);
+    const uint8_t * tbase = mat_tile(p, mat, tile, sec);
     const size_t tgs = (size_t)p.w.tg;
 
     // per-column activation pointers at group 0 (uniform)
@@ -854,27 +867,38 @@ __device__ __forceinline__ void gemv_mma_body(const GemvParams & p) {
     const uint32_t ks = blockIdx.x % (uint32_t)p.KS, rest = blockIdx.x / (uint32_t)p.KS;
     const uint32_t tb = rest % ntb, task = rest / ntb;
     int mat, nc;
+    bool sec = false;                  // the second image (gate/up in one launch)
     if (p.tasks) {
-        if (p.ntasks_dev && (int)task >= *p.ntasks_dev) return;     // uniform
-        const GemvTask & t = p.tasks[task];
+        uint32_t tk = task;
+        if (p.base2 && p.ntasks_dev && (int)tk >= *p.ntasks_dev) {  // the second pass over the list
+            tk -= (uint32_t)*p.ntasks_dev;
+            sec = true;
+        }
+        if (p.ntasks_dev && (int)tk >= *p.ntasks_dev) return;     // uniform
+        const GemvTask & t = p.tasks[tk];
+        const int64_t dadd = sec ? p.up_doff : 0;
         mat = t.mat;
         nc = t.ncols < kMaxTaskCols ? t.ncols : kMaxTaskCols;
         if (mat < 0) {                                            // pairs of invalid ids: zero rows
             const uint32_t ztile = tb * (uint32_t)TW + (uint32_t)tw;
             const int64_t row = (int64_t)ztile * kTileRows + lane;
             if (ks == 0 && kw == 0 && ztile < ntl && row < p.w.M)
-                for (int j = 0; j < nc; ++j) p.dst[t.dst_off[j] + row] = 0.0f;
+                for (int j = 0; j < nc; ++j) p.dst[t.dst_off[j] + dadd + row] = 0.0f;
             return;                                               // uniform
         }
         if (tid < nc) {
             s_col[tid] = t.col[tid];
-            s_doff[tid] = t.dst_off[tid];
+            s_doff[tid] = t.dst_off[tid] + dadd;
         }
     } else {
         const uint32_t tpb = (uint32_t)p.tpb, ne12 = (uint32_t)p.ne12;
         const uint32_t b = task / tpb, tt = task - b * tpb;
         const uint32_t i3 = b / ne12, i2 = b - i3 * ne12;
         mat = (int)(i2 / (uint32_t)p.r2 + (i3 / (uint32_t)p.r3) * (uint32_t)p.ne02);
+        if (p.base2 && mat == 1) {                                // gate/up in one launch
+            mat = 0;
+            sec = true;
+        }
         const int64_t first = (int64_t)tt * p.nct;
         nc = (int)((p.ne11 - first) < p.nct ? (p.ne11 - first) : p.nct);
         if (tid < nc) {
@@ -891,7 +915,7 @@ __device__ __forceinline__ void gemv_mma_body(const GemvParams & p) {
     const int nsw = ga >= G ? 0 : (ga + p.spw < G ? p.spw : G - ga);
     const uint32_t tile = tb * (uint32_t)TW + (uint32_t)tw;
     const int S = tile < ntl ? nsw * NST : 0;                     // stages (uniform per wave)
-    const uint8_t * tbase = mat_tile(p, mat, tile < ntl ? tile : 0);
+    const uint8_t * tbase = mat_tile(p, mat, tile < ntl ? tile : 0, sec);
     const size_t tgs = (size_t)p.w.tg;
     auto load_stage = [&](uint4 (&b)[NL], int s) {                // past the last stage: the sink
         const bool real = s < S;
@@ -1118,7 +1142,7 @@ size_t gemv_lds_bytes(int type, const GemvPlan & pl) {
 
 hipError_t launch_gemv(int type, const WView & w, const GemvPlan & pl, const ActBuf & a, const GemvTask * tasks,
                        const int32_t * ntasks_dev, const GemvDense * dense, float * dst, const void * sink,
-                       hipStream_t s, const KTime * kt) {
+                       hipStream_t s, const KTime * kt, const GemvPair * pair) {
     if (!sink || (!tasks && !dense) || pl.W < 1 || pl.W > 8 || pl.KS < 1 || pl.spw < 1 || a.ldk != w.G * 256 ||
         a.vdt != vec_dot_type(type))
         return hipErrorInvalidValue;
@@ -1139,6 +1163,11 @@ hipError_t launch_gemv(int type, const WView & w, const GemvPlan & pl, const Act
     p.spw = pl.spw;
     p.nct = pl.nc;
     p.tw = pl.tw;
+    if (pair) {
+        if (!tasks || !ntasks_dev || !pair->base2) return hipErrorInvalidValue;
+        p.base2 = pair->base2;
+        p.up_doff = pair->up_doff;
+    }
     if (!tasks) {
         p.ne11 = dense->ne11;
         p.col_bs = dense->col_bs < 0 ? dense->ne11 : dense->col_bs;

@@ -738,6 +738,51 @@ int qmm_mul_mat(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1,
     return QMM_OK;
 }
 
+// The expert tasks of ids into the route scratch (reused inside a graph when ids, ne11, the
+// dst strides and the expert count are those of the route already there): pair (i, t) reads
+// activation column (i % ne11) + t ne11 and writes dst floats t dnb2 + i dnb1
+static int route_tasks(qmm_ctx * ctx, const qmm_tensor * ids, int64_t ne11, int64_t n_as, int64_t dnb1, int64_t dnb2,
+                       int64_t max_tasks, GemvTask ** tasks, int32_t ** ntasks) {
+    const int64_t n_used = ids->ne[0], T = ids->ne[1], npairs = n_used * T;
+    const size_t o_tasks = align_up((size_t)npairs * 4, 256);
+    const size_t o_cnt = align_up(o_tasks + (size_t)max_tasks * sizeof(GemvTask), 256);
+    int rc = ensure(ctx, &ctx->route, &ctx->route_cap, o_cnt + 256);
+    if (rc) return rc;
+    uint8_t * rb = (uint8_t *)ctx->route;
+    *tasks = (GemvTask *)(rb + o_tasks);
+    *ntasks = (int32_t *)(rb + o_cnt);
+    auto & rk = ctx->rkey;
+    const bool hit = ctx->in_graph && rk.valid && rk.gen == ctx->graph_gen && rk.ids.buffer == ids->buffer &&
+                     rk.ids.offs == ids->offs && !memcmp(rk.ids.ne, ids->ne, sizeof(ids->ne)) &&
+                     !memcmp(rk.ids.nb, ids->nb, sizeof(ids->nb)) && rk.ne11 == ne11 && rk.n_as == n_as &&
+                     rk.dnb1 == dnb1 && rk.dnb2 == dnb2;
+    if (hit) return QMM_OK;
+    RouteArgs r;
+    r.ids = (const int32_t *)((const uint8_t *)ids->buffer->ptr + ids->offs);
+    r.ids_nb0 = ids->nb[0];
+    r.ids_nb1 = ids->nb[1];
+    r.n_used = n_used;
+    r.T = T;
+    r.ne11 = ne11;
+    r.n_as = n_as;
+    r.dst_nb1 = dnb1;
+    r.dst_nb2 = dnb2;
+    QMM_HIP(ctx, launch_route(r, (int32_t *)rb, *tasks, *ntasks, ctx->stream));
+    rk.ids = *ids;
+    rk.ne11 = ne11;
+    rk.n_as = n_as;
+    rk.dnb1 = dnb1;
+    rk.dnb2 = dnb2;
+    rk.gen = ctx->graph_gen;
+    rk.valid = ctx->in_graph;
+    return QMM_OK;
+}
+
+// tasks of one route: (token, slot) pairs of one expert, 1..8 per task, plus the invalid bucket
+static int64_t route_max_tasks(int64_t npairs, int64_t n_as) {
+    return npairs / kMaxTaskCols + std::min(n_as + 1, npairs) + 1;
+}
+
 int qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1, const qmm_tensor * ids,
                    const qmm_tensor * dst) {
     if (!ctx) return QMM_ERR_INVALID;
@@ -747,56 +792,84 @@ int qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * sr
         return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat_id: %s", reason);
     QMM_HIP(ctx, hipSetDevice(ctx->device));
     const int64_t n_as = src0->ne[2];
-    const int64_t n_used = ids->ne[0], T = ids->ne[1], ne11 = src1->ne[1];
+    const int64_t npairs = ids->ne[0] * ids->ne[1];
     ActBuf a{};
     int rc;
     if ((rc = quantize_src1(ctx, src0->type, src1, false, &a))) return rc;
-    const int64_t npairs = n_used * T;
-    // (one more bucket: the pairs of invalid ids)
-    const int64_t max_tasks = npairs / kMaxTaskCols + std::min(n_as + 1, npairs) + 1;
+    const int64_t max_tasks = route_max_tasks(npairs, n_as);
     const int nc = (int)std::min<int64_t>(kMaxTaskCols, npairs);
     GemvPlan plan;
     // tasks carry 1..8 pairs each: the MFMA kernel pays off when experts average two or more
     if (!gemv_plan(src0->type, w, nc, max_tasks, false, npairs >= 2 * n_as, &plan))
         return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat_id: GEMV shape out of range");
-    const size_t o_tasks = align_up((size_t)npairs * 4, 256);
-    const size_t o_cnt = align_up(o_tasks + (size_t)max_tasks * sizeof(GemvTask), 256);
-    rc = ensure(ctx, &ctx->route, &ctx->route_cap, o_cnt + 256);
-    if (rc) return rc;
-    uint8_t * rb = (uint8_t *)ctx->route;
-    RouteArgs r;
-    r.ids = (const int32_t *)((const uint8_t *)ids->buffer->ptr + ids->offs);
-    r.ids_nb0 = ids->nb[0];
-    r.ids_nb1 = ids->nb[1];
-    r.n_used = n_used;
-    r.T = T;
-    r.ne11 = ne11;
-    r.n_as = n_as;
-    r.dst_nb1 = (int64_t)(dst->nb[1] / 4);
-    r.dst_nb2 = (int64_t)(dst->nb[2] / 4);
+    GemvTask * tasks;
+    int32_t * ntasks;
+    if ((rc = route_tasks(ctx, ids, src1->ne[1], n_as, (int64_t)(dst->nb[1] / 4), (int64_t)(dst->nb[2] / 4), max_tasks,
+                          &tasks, &ntasks)))
+        return rc;
     float * d = (float *)((uint8_t *)dst->buffer->ptr + dst->offs);
-    GemvTask * tasks = (GemvTask *)(rb + o_tasks);
-    int32_t * ntasks = (int32_t *)(rb + o_cnt);
-    auto & rk = ctx->rkey;
-    const bool hit = ctx->in_graph && rk.valid && rk.gen == ctx->graph_gen && rk.ids.buffer == ids->buffer &&
-                     rk.ids.offs == ids->offs && !memcmp(rk.ids.ne, ids->ne, sizeof(ids->ne)) &&
-                     !memcmp(rk.ids.nb, ids->nb, sizeof(ids->nb)) && rk.ne11 == ne11 && rk.n_as == n_as &&
-                     rk.dnb1 == r.dst_nb1 && rk.dnb2 == r.dst_nb2;
-    if (!hit) {
-        QMM_HIP(ctx, launch_route(r, (int32_t *)rb, tasks, ntasks, ctx->stream));
-        rk.ids = *ids;
-        rk.ne11 = ne11;
-        rk.n_as = n_as;
-        rk.dnb1 = r.dst_nb1;
-        rk.dnb2 = r.dst_nb2;
-        rk.gen = ctx->graph_gen;
-        rk.valid = ctx->in_graph;
-    }
     ctx->path = plan.mma ? "gemv-id-mfma" : "gemv-id";
     KTime kt;
     const KTime * ktp;
     if ((rc = ktime_pair(ctx, &kt, &ktp))) return rc;
     QMM_HIP(ctx, launch_gemv(src0->type, w, plan, a, tasks, ntasks, nullptr, d, ctx->sink, ctx->stream, ktp));
+    return QMM_OK;
+}
+
+// MUL_MAT_ID (gate experts), MUL_MAT_ID (up experts) and the GLU, the MoE form of
+// qmm_mul_mat_glu (the reference's MUL_MAT_ID + GLU fuse; its audit,
+// docs/campaigns/research-concept-mining/ipex-llm/audit.md:83-87): one activation
+// quantization, one route, one GEMV launch that runs the task list over the gate stack and
+// again over the up stack into a scratch [2][T][n_used][M], then the GLU writes dst.
+int qmm_mul_mat_id_glu(qmm_ctx * ctx, const qmm_tensor * gate, const qmm_tensor * up, const qmm_tensor * src1,
+                       const qmm_tensor * ids, const qmm_tensor * dst, int32_t glu_op) {
+    if (!ctx) return QMM_ERR_INVALID;
+    if (glu_op != QMM_GLU_REGLU && glu_op != QMM_GLU_GEGLU && glu_op != QMM_GLU_SWIGLU && glu_op != QMM_GLU_GEGLU_ERF &&
+        glu_op != QMM_GLU_GEGLU_QUICK)
+        return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat_id_glu: GLU op %d", glu_op);
+    char reason[160];
+    WView wg, wu;
+    if (!mul_mat_id_ok(gate, src1, ids, dst, true, &wg, reason, sizeof(reason)))
+        return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat_id_glu: gate: %s", reason);
+    if (!mul_mat_id_ok(up, src1, ids, dst, true, &wu, reason, sizeof(reason)))
+        return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat_id_glu: up: %s", reason);
+    if (up->type != gate->type || memcmp(gate->ne, up->ne, sizeof(gate->ne)))
+        return fail(ctx, QMM_ERR_INVALID, "mul_mat_id_glu: gate and up must be one type and shape");
+    QMM_HIP(ctx, hipSetDevice(ctx->device));
+    const int64_t M = gate->ne[1], n_as = gate->ne[2], n_used = ids->ne[0], T = ids->ne[1], npairs = n_used * T;
+    const size_t half = (size_t)(M * npairs);
+    int rc = ensure(ctx, &ctx->glu, &ctx->glu_cap, 2 * half * sizeof(float));
+    if (rc) return rc;
+    float * sg = (float *)ctx->glu;
+    ActBuf a{};
+    if ((rc = quantize_src1(ctx, gate->type, src1, false, &a))) return rc;
+    const int64_t max_tasks = route_max_tasks(npairs, n_as);
+    const int nc = (int)std::min<int64_t>(kMaxTaskCols, npairs);
+    GemvPlan plan;
+    if (!gemv_plan(gate->type, wg, nc, 2 * max_tasks, false, npairs >= 2 * n_as, &plan))
+        return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat_id_glu: GEMV shape out of range");
+    GemvTask * tasks;
+    int32_t * ntasks;
+    // the scratch halves are contiguous [T][n_used][M]
+    if ((rc = route_tasks(ctx, ids, src1->ne[1], n_as, M, M * n_used, max_tasks, &tasks, &ntasks))) return rc;
+    GemvPair pair{ wu.base, (int64_t)half };
+    ctx->path = plan.mma ? "glu-gemv-id-mfma" : "glu-gemv-id";
+    KTime kt;
+    const KTime * ktp;
+    if ((rc = ktime_pair(ctx, &kt, &ktp))) return rc;
+    QMM_HIP(ctx, launch_gemv(gate->type, wg, plan, a, tasks, ntasks, nullptr, sg, ctx->sink, ctx->stream, ktp, &pair));
+    GluArgs g;
+    g.gate = sg;
+    g.up = sg + half;
+    g.dst = (float *)((uint8_t *)dst->buffer->ptr + dst->offs);
+    g.M = M;
+    g.N = n_used;
+    g.nb = T;
+    g.ne12 = T;
+    g.d_nb1 = (int64_t)(dst->nb[1] / 4);
+    g.d_nb2 = (int64_t)(dst->nb[2] / 4);
+    g.d_nb3 = 0;
+    QMM_HIP(ctx, launch_glu(glu_op, g, ctx->stream));
     return QMM_OK;
 }
 

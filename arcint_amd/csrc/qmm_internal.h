@@ -197,9 +197,15 @@ bool gemv_mma_supported(int type);
 // `sink`: kSinkBytes of device memory the kernel may read (not write) for
 // loads past the end of its pipeline.
 constexpr size_t kSinkBytes = 32768;
+// pair (task lists only): the list runs a second time on the image at pair->base2 (an expert
+// stack of w's shape), its dst offsets plus pair->up_doff floats; plan.ntasks counts both passes
+struct GemvPair {
+    const uint8_t * base2;
+    int64_t up_doff;
+};
 hipError_t launch_gemv(int type, const WView & w, const GemvPlan & plan, const ActBuf & a, const GemvTask * tasks,
                        const int32_t * ntasks_dev, const GemvDense * dense, float * dst, const void * sink,
-                       hipStream_t s, const KTime * kt = nullptr);
+                       hipStream_t s, const KTime * kt = nullptr, const GemvPair * pair = nullptr);
 
 // Prefill GEMM (int8 MFMA, all five types): for every batch b < nbatch,
 // dst[doff(b) + n * d_nb1 + m] = W(mat(b)) row m . activation column

@@ -35,7 +35,7 @@ EXPORTS = (
     "qmm_graph_compute", "qmm_dequantize", "qmm_quantize_act", "qmm_synchronize", "qmm_downgrades",
     "qmm_last_path", "qmm_timer_begin", "qmm_timer_end", "qmm_buffer_copy", "qmm_kernel_timing",
     "qmm_kernel_time", "qmm_tensor_pack", "qmm_tensor_unpack", "qmm_describe_mul_mat", "qmm_moe_topk",
-    "qmm_moe_combine", "qmm_mul_mat_glu",
+    "qmm_moe_combine", "qmm_mul_mat_glu", "qmm_mul_mat_id_glu",
 )
 
 
@@ -100,6 +100,7 @@ def load() -> C.CDLL:
         L.qmm_moe_topk.argtypes = [vp, T, T, T, C.c_float, C.c_float]
         L.qmm_moe_combine.argtypes = [vp, T, T, T, T, T]
         L.qmm_mul_mat_glu.argtypes = [vp, T, T, T, T, C.c_int32]
+        L.qmm_mul_mat_id_glu.argtypes = [vp, T, T, T, T, T, C.c_int32]
         L.qmm_graph_compute.argtypes = [vp, C.POINTER(CNode), C.c_int]
         L.qmm_dequantize.argtypes = [vp, T, T]
         L.qmm_quantize_act.argtypes = [vp, i32, T, vp, sz]
@@ -294,6 +295,11 @@ class Backend:
         """dst = act(gate x src1) * (up x src1): MUL_MAT, MUL_MAT and the split GLU in one call"""
         self._check(self.L.qmm_mul_mat_glu(self.h, C.byref(gate.c), C.byref(up.c), C.byref(src1.c), C.byref(dst.c), op),
                     "mul_mat_glu")
+
+    def mul_mat_id_glu(self, gate: Tensor, up: Tensor, src1: Tensor, ids: Tensor, dst: Tensor, op: int = GLU_SWIGLU):
+        """dst = act(gate_experts x src1) * (up_experts x src1), routed by ids"""
+        self._check(self.L.qmm_mul_mat_id_glu(self.h, C.byref(gate.c), C.byref(up.c), C.byref(src1.c), C.byref(ids.c),
+                                              C.byref(dst.c), op), "mul_mat_id_glu")
 
     def moe_topk(self, logits: Tensor, ids: Tensor, weights: Tensor, cmin: float = 6.103515625e-5,
                  cmax: float = float("inf")):

@@ -255,8 +255,19 @@ def moe_case(be, qmm, synth, T, args):
     ex = be.new_tensor(qmm.F32, (2048, n_used, T))
     be.set_tensor(ex, synth.activations(n_used * T, 2048, seed=7).view(np.uint8).ravel())
     yo = be.new_tensor(qmm.F32, (2048, T))
+    # the layer's gate and up stacks with the SwiGLU in one call (one route, one GEMV launch)
+    wu = be.new_tensor(qmm.Q4_K, (K, M, E))
+    be.copy(wu.buf, 0, w.buf, 0, qmm.alloc_size(qmm.Q4_K, (K, M, E)))
+    yg = be.new_tensor(qmm.F32, (M, n_used, T))
+    state = {"i": 0}
+
+    def glu():
+        be.mul_mat_id_glu(w, wu, xt, idsets[state["i"] % 16], yg, qmm.GLU_SWIGLU)
+        state["i"] += 1
+
     times = {}
-    for name, fn in (("router", lambda: be.moe_topk(lg, rid, rw)), ("combine", lambda: be.moe_combine(ex, rw, yo))):
+    for name, fn in (("router", lambda: be.moe_topk(lg, rid, rw)), ("combine", lambda: be.moe_combine(ex, rw, yo)),
+                     ("gate_up_glu", glu)):
         for _ in range(10):
             fn()
         be.synchronize()
@@ -268,8 +279,9 @@ def moe_case(be, qmm, synth, T, args):
            "path": path, "us_per_op": round(us, 3), "expert_bytes_touched": int(bytes_step),
            "GBs": round(bytes_step / (us * 1e-6) / 1e9, 1), "kernel_us": round(k_us, 3),
            "kernel_GBs": round(bytes_step / (k_us * 1e-6) / 1e9, 1),
-           "router_us": round(times["router"], 3), "combine_us": round(times["combine"], 3)}
-    for t in (lg, rid, rw, ex, yo):
+           "router_us": round(times["router"], 3), "combine_us": round(times["combine"], 3),
+           "gate_up_glu_us": round(times["gate_up_glu"], 3)}
+    for t in (lg, rid, rw, ex, yo, wu, yg):
         be.free_buffer(t.buf)
     for t in idsets:
         be.free_buffer(t.buf)

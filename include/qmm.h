@@ -201,6 +201,13 @@ int    qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor *
  * stream in one launch.  Within MUL_MAT's tolerance of the unfused chain. */
 int    qmm_mul_mat_glu(qmm_ctx * ctx, const qmm_tensor * gate, const qmm_tensor * up, const qmm_tensor * src1,
                        const qmm_tensor * dst, int32_t glu_op);
+/* The MoE form: dst = act(MUL_MAT_ID(gate, src1, ids)) * MUL_MAT_ID(up, src1, ids), gate and
+ * up expert stacks [K, M, n_as] of one type and shape, src1 / ids / dst as qmm_mul_mat_id's.
+ * Replaces MUL_MAT_ID, MUL_MAT_ID, GLU (the reference's MUL_MAT_ID / GLU fuse, by its audit
+ * docs/campaigns/research-concept-mining/ipex-llm/audit.md:83-87): one quantization, one
+ * route, one GEMV launch over both stacks.  Invalid ids give zero rows. */
+int    qmm_mul_mat_id_glu(qmm_ctx * ctx, const qmm_tensor * gate, const qmm_tensor * up, const qmm_tensor * src1,
+                          const qmm_tensor * ids, const qmm_tensor * dst, int32_t glu_op);
 /* Runs the nodes in order; bumps the graph generation first, so one
  * activation quantization serves every node of the graph that reads the same
  * src1 with the same vec_dot type. */

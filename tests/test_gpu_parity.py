@@ -845,3 +845,46 @@ def test_graph_route_shared_by_gate_and_up(be, sc, orc):
         ref = orc.mul_mat_id(qmm.Q4_K, raw, m, k, E, xx, ids)
         assert (got[bad] == 0).all()
         assert rel_err(got[~bad], ref[~bad]) <= TOL
+
+
+@pytest.mark.parametrize("qtype", [qmm.Q4_K, qmm.Q4_0, qmm.Q6_K])
+@pytest.mark.parametrize("T", [1, 4, 40])
+def test_mul_mat_id_glu(be, sc, orc, qtype, T):
+    """MUL_MAT_ID gate, MUL_MAT_ID up and the GLU in one call (one route, one GEMV launch over
+    both stacks); invalid ids give zero rows"""
+    from oracle import glu as G
+    E, n_used, M, K = 16, 4, 130, 512
+    say("mul_mat_id_glu", qtype, T)
+    rg, ru = synth.weights(qtype, E * M, K, seed=171), synth.weights(qtype, E * M, K, seed=172)
+    ids = synth.moe_ids(T, E, n_used, seed=173)
+    ids[0, 2] = -1
+    if T > 1:
+        ids[1, 0] = E + 2
+    x = synth.activations(T, K, seed=174).reshape(T, 1, K)
+    wg, wu = sc.weights(qtype, rg, (K, M, E)), sc.weights(qtype, ru, (K, M, E))
+    y = sc.f32(np.full((T, n_used, M), 5.0, np.float32))
+    be.mul_mat_id_glu(wg, wu, sc.f32(x), sc.i32(ids), y, qmm.GLU_SWIGLU)
+    be.synchronize()
+    assert be.last_path().startswith("glu-gemv-id")
+    got = be.get_f32(y).reshape(T, n_used, M)
+    ref = G.glu(qmm.GLU_SWIGLU, orc.mul_mat_id(qtype, rg, M, K, E, x, ids), orc.mul_mat_id(qtype, ru, M, K, E, x, ids))
+    bad = (ids < 0) | (ids >= E)
+    assert (got[bad] == 0).all()
+    assert rel_err(got[~bad], ref[~bad]) <= TOL
+
+
+def test_mul_mat_id_glu_per_slot_src1(be, sc, orc):
+    """src1 [K, n_used, T] (one row per slot) and GEGLU"""
+    from oracle import glu as G
+    E, n_used, M, K, T = 8, 3, 64, 256, 5
+    say("mul_mat_id_glu ne11=n_used")
+    rg, ru = synth.weights(qmm.Q4_K, E * M, K, seed=181), synth.weights(qmm.Q4_K, E * M, K, seed=182)
+    ids = synth.moe_ids(T, E, n_used, seed=183)
+    x = synth.activations(T * n_used, K, seed=184).reshape(T, n_used, K)
+    wg, wu = sc.weights(qmm.Q4_K, rg, (K, M, E)), sc.weights(qmm.Q4_K, ru, (K, M, E))
+    y = sc.empty_f32((M, n_used, T))
+    be.mul_mat_id_glu(wg, wu, sc.f32(x), sc.i32(ids), y, qmm.GLU_GEGLU)
+    be.synchronize()
+    got = be.get_f32(y).reshape(T, n_used, M)
+    ref = G.glu(qmm.GLU_GEGLU, orc.mul_mat_id(qmm.Q4_K, rg, M, K, E, x, ids), orc.mul_mat_id(qmm.Q4_K, ru, M, K, E, x, ids))
+    assert rel_err(got, ref) <= TOL
