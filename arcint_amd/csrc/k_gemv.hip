@@ -58,6 +58,8 @@ struct GemvParams {
                                  // the task list runs twice, the second time on this stack), or null
     int64_t col_bs;              // dense mode: activation columns per batch
     int64_t up_doff;             // lists with base2: floats added to the second pass's dst offsets
+    int glu;                     // lists with base2, >= 0: each work-group streams the gate tile (w)
+                                 // and the up tile (base2) and stores act(gate) * up (enum qmm_glu)
     int W;                       // waves per work-group
     int KS;                      // work-groups per tile (K slices); > 1: atomics into zeroed dst
     int spw;                     // groups per wave
@@ -430,7 +432,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvParams p) {
     bool sec = false;                  // the second image (gate/up in one launch)
     if (p.tasks) {
         uint32_t tk = task;
-        if (p.base2 && p.ntasks_dev && (int)tk >= *p.ntasks_dev) {  // the second pass over the list
+        if (p.base2 && p.glu < 0 && p.ntasks_dev && (int)tk >= *p.ntasks_dev) {  // the second pass over the list
             tk -= (uint32_t)*p.ntasks_dev;
             sec = true;
         }
@@ -491,17 +493,19 @@ __global__ __launch_bounds__(512) void k_gemv(GemvParams p) {
         xs0[j] = p.xs + cu * (p.ldk / (256 / NS));
     }
 
-    float acc[NC];
+    float acc[NC], accu[NC];
     int st_state[NC];
+    // the wave's groups of one image into a[] (gate/up with GLU: the gate tile, then the up tile)
+    auto stream = [&](const uint8_t * tb, float (&a)[NC]) {
 #pragma unroll
-    for (int j = 0; j < NC; ++j) {
-        acc[j] = 0.0f;
-        st_state[j] = 0;
-    }
-    if (S > 0) {
+        for (int j = 0; j < NC; ++j) {
+            a[j] = 0.0f;
+            st_state[j] = 0;
+        }
+        if (S <= 0) return;
         uint4 B[D][NL];
         auto load_stage = [&](uint4 * b, int s) {             // past the end: the sink
-            const uint8_t * tg = s < S ? tbase + (size_t)(ga + s / NST) * tgs : p.sink;
+            const uint8_t * tg = s < S ? tb + (size_t)(ga + s / NST) * tgs : p.sink;
             T::load(b, tg, s < S ? s % NST : 0, lane);
         };
 #pragma unroll
@@ -518,30 +522,43 @@ __global__ __launch_bounds__(512) void k_gemv(GemvParams p) {
                         x.d[j] = xd0[j] + (int64_t)g * ND;
                         x.s[j] = xs0[j] + (int64_t)g * NS;
                     }
-                    T::template dot<NC>(B[i], (s + i) % NST, x, nc, acc, st_state);
+                    T::template dot<NC>(B[i], (s + i) % NST, x, nc, a, st_state);
                 }
                 load_stage(B[i], s + i + D);
             }
         }
-    }
+    };
+    const bool glu = p.glu >= 0;                                  // uniform (lists only)
+    stream(tbase, acc);
+    if (glu) stream(mat_tile(p, mat, tile, true), accu);
 
-    // add the W waves in a fixed order
+    // add the W waves in a fixed order (with the GLU: both sums, then act(gate) * up)
     const int64_t row = (int64_t)tile * kTileRows + lane;
     float tot[NC];
     if (p.W > 1) {
+        const int NV = glu ? 2 * NC : NC;
 #pragma unroll
-        for (int j = 0; j < NC; ++j) red[(wave * NC + j) * 64 + lane] = acc[j];
+        for (int j = 0; j < NC; ++j) red[(wave * NV + j) * 64 + lane] = acc[j];
+        if (glu) {
+#pragma unroll
+            for (int j = 0; j < NC; ++j) red[(wave * NV + NC + j) * 64 + lane] = accu[j];
+        }
         __syncthreads();
         if (wave != 0) return;
 #pragma unroll
         for (int j = 0; j < NC; ++j) {
             float v = red[j * 64 + lane];
-            for (int w = 1; w < p.W; ++w) v += red[(w * NC + j) * 64 + lane];
+            for (int w = 1; w < p.W; ++w) v += red[(w * NV + j) * 64 + lane];
+            if (glu) {
+                float u = red[(NC + j) * 64 + lane];
+                for (int w = 1; w < p.W; ++w) u += red[(w * NV + NC + j) * 64 + lane];
+                v = glu_apply(p.glu, v, u);
+            }
             tot[j] = v;
         }
     } else {
 #pragma unroll
-        for (int j = 0; j < NC; ++j) tot[j] = acc[j];
+        for (int j = 0; j < NC; ++j) tot[j] = glu ? glu_apply(p.glu, acc[j], accu[j]) : acc[j];
     }
     if (row >= p.w.M) return;
 #pragma unroll
@@ -870,7 +887,7 @@ __device__ __forceinline__ void gemv_mma_body(const GemvParams & p) {
     bool sec = false;                  // the second image (gate/up in one launch)
     if (p.tasks) {
         uint32_t tk = task;
-        if (p.base2 && p.ntasks_dev && (int)tk >= *p.ntasks_dev) {  // the second pass over the list
+        if (p.base2 && p.glu < 0 && p.ntasks_dev && (int)tk >= *p.ntasks_dev) {  // the second pass over the list
             tk -= (uint32_t)*p.ntasks_dev;
             sec = true;
         }
@@ -915,8 +932,9 @@ __device__ __forceinline__ void gemv_mma_body(const GemvParams & p) {
     const int nsw = ga >= G ? 0 : (ga + p.spw < G ? p.spw : G - ga);
     const uint32_t tile = tb * (uint32_t)TW + (uint32_t)tw;
     const int S = tile < ntl ? nsw * NST : 0;                     // stages (uniform per wave)
-    const uint8_t * tbase = mat_tile(p, mat, tile < ntl ? tile : 0, sec);
+    const uint8_t * tbase = mat_tile(p, mat, tile < ntl ? tile : 0, sec);   // the up tile after the gate (GLU)
     const size_t tgs = (size_t)p.w.tg;
+    const bool glu = CM == 8 && p.glu >= 0;                       // uniform (lists: 8-column tasks only)
     auto load_stage = [&](uint4 (&b)[NL], int s) {                // past the last stage: the sink
         const bool real = s < S;
         T::load(b, real ? tbase + (size_t)(ga + s / NST) * tgs : p.sink, real ? s % NST : 0, lane);
@@ -973,14 +991,27 @@ __device__ __forceinline__ void gemv_mma_body(const GemvParams & p) {
         const int gl = s / NST;
         mma_stage<TYPE, CM, NL>(b, s % NST, xar + gl * xas, xdr + gl * NSB * CM, xsr + gl * xss, h, magic, out, iacc);
     };
-    for (int s = 0; s < S; s += 2) {                              // uniform
-        load_stage(b1, s + 1);
-        __builtin_amdgcn_sched_barrier(0);                        // the loads go out before the compute
-        compute(b0, s);
-        if (s + 1 >= S) break;
-        load_stage(b0, s + 2);
-        __builtin_amdgcn_sched_barrier(0);
-        compute(b1, s + 1);
+    auto run = [&]() {
+        for (int s = 0; s < S; s += 2) {                          // uniform
+            load_stage(b1, s + 1);
+            __builtin_amdgcn_sched_barrier(0);                    // the loads go out before the compute
+            compute(b0, s);
+            if (s + 1 >= S) break;
+            load_stage(b0, s + 2);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(b1, s + 1);
+        }
+    };
+    run();
+    vNf<CM> outu = {};
+    if (glu) {                                                    // the up tile against the same activations
+        const vNf<CM> outg = out;
+        out = vNf<CM>{};
+        tbase = mat_tile(p, mat, tile < ntl ? tile : 0, true);
+        if (S > 0) load_stage(b0, 0);
+        run();
+        outu = out;
+        out = outg;
     }
 
     // tile tw's WK waves are added in a fixed order (wave kw takes the elements e = kw, kw + WK,
@@ -997,17 +1028,27 @@ __device__ __forceinline__ void gemv_mma_body(const GemvParams & p) {
     };
     if (WK == 1) {
 #pragma unroll
-        for (int e = 0; e < CM; ++e) store(e, out[e]);
+        for (int e = 0; e < CM; ++e) store(e, glu ? glu_apply(p.glu, out[e], outu[e]) : out[e]);
         return;
     }
-    float * red = reinterpret_cast<float *>(xl);                  // [WK][TW][CM][64], over the staged data
+    // [WK][TW][NV][64] over the staged data (NV = CM, with the GLU 2 CM: gate, then up)
+    const int NV = glu ? 2 * CM : CM;
+    float * red = reinterpret_cast<float *>(xl);
     __syncthreads();
 #pragma unroll
-    for (int e = 0; e < CM; ++e) red[((kw * TW + tw) * CM + e) * 64 + lane] = out[e];
+    for (int e = 0; e < CM; ++e) red[((kw * TW + tw) * NV + e) * 64 + lane] = out[e];
+    if (glu) {
+#pragma unroll
+        for (int e = 0; e < CM; ++e) red[((kw * TW + tw) * NV + CM + e) * 64 + lane] = outu[e];
+    }
     __syncthreads();
     for (int e = kw; e < CM; e += WK) {
-        float v = 0.0f;
-        for (int k = 0; k < WK; ++k) v += red[((k * TW + tw) * CM + e) * 64 + lane];
+        float v = 0.0f, u = 0.0f;
+        for (int k = 0; k < WK; ++k) v += red[((k * TW + tw) * NV + e) * 64 + lane];
+        if (glu) {
+            for (int k = 0; k < WK; ++k) u += red[((k * TW + tw) * NV + CM + e) * 64 + lane];
+            v = glu_apply(p.glu, v, u);
+        }
         store(e, v);
     }
 }
@@ -1030,7 +1071,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 template <int TYPE>
 hipError_t launch_t(const GemvParams & p, int nc, int64_t nwg, hipStream_t s, const KTime * kt) {
     const int threads = 64 * p.W;
-    const size_t lds = p.W > 1 ? (size_t)p.W * nc * 64 * sizeof(float) : 0;
+    const size_t lds = p.W > 1 ? (size_t)p.W * nc * 64 * sizeof(float) * (p.glu >= 0 ? 2 : 1) : 0;
     switch (nc) {
 #define QMM_NC(N)                                                                                  \
     case N:                                                                                        \
@@ -1163,10 +1204,12 @@ hipError_t launch_gemv(int type, const WView & w, const GemvPlan & pl, const Act
     p.spw = pl.spw;
     p.nct = pl.nc;
     p.tw = pl.tw;
+    p.glu = -1;
     if (pair) {
-        if (!tasks || !ntasks_dev || !pair->base2) return hipErrorInvalidValue;
+        if (!tasks || !ntasks_dev || !pair->base2 || pair->glu > QMM_GLU_GEGLU_QUICK) return hipErrorInvalidValue;
         p.base2 = pair->base2;
         p.up_doff = pair->up_doff;
+        p.glu = pair->glu;
     }
     if (!tasks) {
         p.ne11 = dense->ne11;
@@ -1191,7 +1234,9 @@ hipError_t launch_gemv(int type, const WView & w, const GemvPlan & pl, const Act
             per_wg > kMmaMaxGroups * 8 / pl.cm ||
             per_wg * pl.KS < w.G || per_wg * (pl.KS - 1) >= w.G || (type == QMM_TYPE_Q4_K && !a.bsp))
             return hipErrorInvalidValue;
-        const uint32_t lds = (uint32_t)gemv_lds_bytes(type, pl);
+        uint32_t lds = (uint32_t)gemv_lds_bytes(type, pl);
+        if (p.glu >= 0 && pl.W > pl.tw)                          // the K waves' sums of gate and up
+            lds = std::max<uint32_t>(lds, (uint32_t)pl.W * (uint32_t)pl.cm * 64 * 4 * 2);
         const dim3 g((unsigned)nwg), b(64 * pl.W);
 #define QMM_MMA_K(K)                                                                                \
     if (kt) hipExtLaunchKernelGGL(K, g, b, lds, s, kt->start, kt->stop, 0, p);                      \

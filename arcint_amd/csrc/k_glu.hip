@@ -17,20 +17,6 @@ namespace {
 
 #pragma clang fp contract(off)
 
-__device__ __forceinline__ float glu_act(int op, float x) {
-    switch (op) {
-        case QMM_GLU_REGLU: return x > 0.0f ? x : 0.0f;
-        case QMM_GLU_GEGLU: {
-            const float k0 = 0.79788456080286535587989211986876f, k1 = 0.044715f;
-            return 0.5f * x * (1.0f + tanhf(k0 * x * (1.0f + k1 * x * x)));
-        }
-        case QMM_GLU_SWIGLU: return x / (1.0f + expf(-x));
-        case QMM_GLU_GEGLU_ERF: return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440084436210484f));
-        case QMM_GLU_GEGLU_QUICK: return x * (1.0f / (1.0f + expf(-1.702f * x)));
-        default: return 0.0f;
-    }
-}
-
 // grid: x over the rows in 256-row blocks, y over the columns of all batches (col = c + N b):
 // no division per element
 template <int OP>

@@ -819,8 +819,13 @@ int qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * sr
 // MUL_MAT_ID (gate experts), MUL_MAT_ID (up experts) and the GLU, the MoE form of
 // qmm_mul_mat_glu (the reference's MUL_MAT_ID + GLU fuse; its audit,
 // docs/campaigns/research-concept-mining/ipex-llm/audit.md:83-87): one activation
-// quantization, one route, one GEMV launch that runs the task list over the gate stack and
-// again over the up stack into a scratch [2][T][n_used][M], then the GLU writes dst.
+// quantization, one route, one GEMV launch over both stacks.  With enough tasks to fill the
+// chip, each work-group streams its tile of the gate stack, then of the up stack, against the
+// same activations and stores act(gate) * up (task lists never split K over work-groups, so
+// each holds whole sums): no scratch and no GLU launch.  With few (decode), the list runs once
+// on each stack in parallel into a scratch [2][T][n_used][M] and the GLU kernel writes dst:
+// twice the work-groups for a latency-bound launch (config 3 at T = 1: 17.2 against 22.4 us
+// per call, at T = 256 127 against 123).
 int qmm_mul_mat_id_glu(qmm_ctx * ctx, const qmm_tensor * gate, const qmm_tensor * up, const qmm_tensor * src1,
                        const qmm_tensor * ids, const qmm_tensor * dst, int32_t glu_op) {
     if (!ctx) return QMM_ERR_INVALID;
@@ -837,31 +842,39 @@ int qmm_mul_mat_id_glu(qmm_ctx * ctx, const qmm_tensor * gate, const qmm_tensor 
         return fail(ctx, QMM_ERR_INVALID, "mul_mat_id_glu: gate and up must be one type and shape");
     QMM_HIP(ctx, hipSetDevice(ctx->device));
     const int64_t M = gate->ne[1], n_as = gate->ne[2], n_used = ids->ne[0], T = ids->ne[1], npairs = n_used * T;
-    const size_t half = (size_t)(M * npairs);
-    int rc = ensure(ctx, &ctx->glu, &ctx->glu_cap, 2 * half * sizeof(float));
-    if (rc) return rc;
-    float * sg = (float *)ctx->glu;
     ActBuf a{};
+    int rc;
     if ((rc = quantize_src1(ctx, gate->type, src1, false, &a))) return rc;
     const int64_t max_tasks = route_max_tasks(npairs, n_as);
     const int nc = (int)std::min<int64_t>(kMaxTaskCols, npairs);
+    const bool in_wg = max_tasks * wg.ntiles >= 1024;             // enough work-groups to fill the chip
     GemvPlan plan;
-    if (!gemv_plan(gate->type, wg, nc, 2 * max_tasks, false, npairs >= 2 * n_as, &plan))
+    if (!gemv_plan(gate->type, wg, nc, in_wg ? max_tasks : 2 * max_tasks, false, npairs >= 2 * n_as, &plan))
         return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat_id_glu: GEMV shape out of range");
+    const size_t half = (size_t)(M * npairs);
+    float * sg = nullptr;
+    if (!in_wg) {
+        if ((rc = ensure(ctx, &ctx->glu, &ctx->glu_cap, 2 * half * sizeof(float)))) return rc;
+        sg = (float *)ctx->glu;
+    }
     GemvTask * tasks;
     int32_t * ntasks;
-    // the scratch halves are contiguous [T][n_used][M]
-    if ((rc = route_tasks(ctx, ids, src1->ne[1], n_as, M, M * n_used, max_tasks, &tasks, &ntasks))) return rc;
-    GemvPair pair{ wu.base, (int64_t)half };
+    // in_wg: the dst's strides; else the scratch halves, contiguous [T][n_used][M]
+    const int64_t dnb1 = in_wg ? (int64_t)(dst->nb[1] / 4) : M, dnb2 = in_wg ? (int64_t)(dst->nb[2] / 4) : M * n_used;
+    if ((rc = route_tasks(ctx, ids, src1->ne[1], n_as, dnb1, dnb2, max_tasks, &tasks, &ntasks))) return rc;
+    GemvPair pair{ wu.base, in_wg ? 0 : (int64_t)half, in_wg ? glu_op : -1 };
+    float * d = (float *)((uint8_t *)dst->buffer->ptr + dst->offs);
     ctx->path = plan.mma ? "glu-gemv-id-mfma" : "glu-gemv-id";
     KTime kt;
     const KTime * ktp;
     if ((rc = ktime_pair(ctx, &kt, &ktp))) return rc;
-    QMM_HIP(ctx, launch_gemv(gate->type, wg, plan, a, tasks, ntasks, nullptr, sg, ctx->sink, ctx->stream, ktp, &pair));
+    QMM_HIP(ctx, launch_gemv(gate->type, wg, plan, a, tasks, ntasks, nullptr, in_wg ? d : sg, ctx->sink, ctx->stream, ktp,
+                             &pair));
+    if (in_wg) return QMM_OK;
     GluArgs g;
     g.gate = sg;
     g.up = sg + half;
-    g.dst = (float *)((uint8_t *)dst->buffer->ptr + dst->offs);
+    g.dst = d;
     g.M = M;
     g.N = n_used;
     g.nb = T;

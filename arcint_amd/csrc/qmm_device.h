@@ -37,6 +37,26 @@ __device__ __forceinline__ uint32_t iq4_lookup(uint32_t nib) {
     return perm(hi, lo, sel);
 }
 
+// The GLU activations of ggml's split GLU (ggml-cpu vec.h scalar forms), fp32 with the device
+// library's expf / tanhf / erff; glu_apply(op, x, g) = act(x) * g, REGLU as x > 0 ? x g : 0
+__device__ __forceinline__ float glu_act(int op, float x) {
+    switch (op) {
+        case QMM_GLU_REGLU: return x > 0.0f ? x : 0.0f;
+        case QMM_GLU_GEGLU: {
+            const float k0 = 0.79788456080286535587989211986876f, k1 = 0.044715f;
+            return 0.5f * x * (1.0f + tanhf(k0 * x * (1.0f + k1 * x * x)));
+        }
+        case QMM_GLU_SWIGLU: return x / (1.0f + expf(-x));
+        case QMM_GLU_GEGLU_ERF: return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440084436210484f));
+        case QMM_GLU_GEGLU_QUICK: return x * (1.0f / (1.0f + expf(-1.702f * x)));
+        default: return 0.0f;
+    }
+}
+
+__device__ __forceinline__ float glu_apply(int op, float x, float g) {
+    return op == QMM_GLU_REGLU ? (x > 0.0f ? x * g : 0.0f) : glu_act(op, x) * g;
+}
+
 // four 4-bit codes 0..15 (one per byte) -> q - 8 as int8 (no borrow between bytes)
 __device__ __forceinline__ uint32_t q4_minus8(uint32_t nib) {
     return (((nib | 0x80808080u) - 0x08080808u) ^ 0x80808080u);

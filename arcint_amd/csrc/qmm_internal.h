@@ -197,11 +197,14 @@ bool gemv_mma_supported(int type);
 // `sink`: kSinkBytes of device memory the kernel may read (not write) for
 // loads past the end of its pipeline.
 constexpr size_t kSinkBytes = 32768;
-// pair (task lists only): the list runs a second time on the image at pair->base2 (an expert
-// stack of w's shape), its dst offsets plus pair->up_doff floats; plan.ntasks counts both passes
+// pair (task lists only), a second expert stack of w's shape at pair->base2: with glu < 0 the
+// list runs a second time on it, its dst offsets plus up_doff floats (plan.ntasks counts both
+// passes); with glu >= 0 (enum qmm_glu) each work-group streams its tile of both stacks and
+// stores act(gate) * up
 struct GemvPair {
     const uint8_t * base2;
     int64_t up_doff;
+    int glu = -1;
 };
 hipError_t launch_gemv(int type, const WView & w, const GemvPlan & plan, const ActBuf & a, const GemvTask * tasks,
                        const int32_t * ntasks_dev, const GemvDense * dense, float * dst, const void * sink,

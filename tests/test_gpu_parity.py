@@ -848,12 +848,14 @@ def test_graph_route_shared_by_gate_and_up(be, sc, orc):
 
 
 @pytest.mark.parametrize("qtype", [qmm.Q4_K, qmm.Q4_0, qmm.Q6_K])
-@pytest.mark.parametrize("T", [1, 4, 40])
-def test_mul_mat_id_glu(be, sc, orc, qtype, T):
+@pytest.mark.parametrize("T,E", [(1, 16), (4, 16), (40, 16), (300, 64), (40, 512)])
+def test_mul_mat_id_glu(be, sc, orc, qtype, T, E):
     """MUL_MAT_ID gate, MUL_MAT_ID up and the GLU in one call (one route, one GEMV launch over
-    both stacks); invalid ids give zero rows"""
+    both stacks: the two-pass form into a scratch plus the GLU kernel at few tasks, the
+    in-work-group GLU at many - T = 300 on 64 experts and T = 40 on 512 pass the 1024
+    work-group mark); invalid ids give zero rows"""
     from oracle import glu as G
-    E, n_used, M, K = 16, 4, 130, 512
+    n_used, M, K = 4, 130, 512
     say("mul_mat_id_glu", qtype, T)
     rg, ru = synth.weights(qtype, E * M, K, seed=171), synth.weights(qtype, E * M, K, seed=172)
     ids = synth.moe_ids(T, E, n_used, seed=173)
