@@ -365,7 +365,9 @@ def main():
                   (qmm.Q4_K, 17408, 5120, 4, "Q4_K 17408x5120 N=4 (config 2)"),
                   (qmm.Q4_K, 17408, 5120, 16, "Q4_K 17408x5120 N=16 (config 2, 16-column MFMA task)"),
                   (qmm.Q4_K, 17408, 5120, 32, "Q4_K 17408x5120 N=32 (config 2, 32-column MFMA task)"),
-                  (qmm.Q6_K, 5120, 17408, 8, "Q6_K 5120x17408 N=8 (config 2 ffn down, MFMA)")]
+                  (qmm.Q6_K, 5120, 17408, 8, "Q6_K 5120x17408 N=8 (config 2 ffn down, MFMA)"),
+                  (qmm.Q6_K, 151936, 5120, 1, "Q6_K GEMV 151936x5120 N=1 (config 2 output head)"),
+                  (qmm.Q6_K, 151936, 5120, 4, "Q6_K 151936x5120 N=4 (config 2 output head, MTP verify width)")]
         for qt, nm in ((qmm.IQ4_XS, "IQ4_XS"), (qmm.Q8_0, "Q8_0")):
             for n in (2, 4, 8):
                 gcases.append((qt, 14336, 4096, n, f"{nm} 14336x4096 N={n} (config 4)"))
