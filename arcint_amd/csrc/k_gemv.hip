@@ -418,9 +418,8 @@ __global__ __launch_bounds__(512) void k_gemv(GemvParams p) {
     using T = GV<TYPE>;
     constexpr int NL = T::NL, NST = T::NST, ND = T::ND, NS = T::NS;
     constexpr int D = ring_depth<NC>();
+    static_assert(NC <= kMaxTaskCols, "a task holds kMaxTaskCols columns");
     extern __shared__ __align__(16) float red[];       // [W][NC][64]
-    __shared__ int64_t s_col[NC];      // activation column ids
-    __shared__ int64_t s_doff[NC];     // float offset of dst row 0 per column
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -430,13 +429,17 @@ __global__ __launch_bounds__(512) void k_gemv(GemvParams p) {
     const uint32_t tile = rest % ntl, task = rest / ntl;
     int mat, nc;
     bool sec = false;                  // the second image (gate/up in one launch)
+    // per column: activation column id and float offset of dst row 0, uniform
+    // registers (no LDS copy and barrier ahead of the first weight load)
+    int64_t colv[NC], doffv[NC];
     if (p.tasks) {
+        const int ntk = p.ntasks_dev ? *p.ntasks_dev : 0x7fffffff;   // one load of the task count
         uint32_t tk = task;
-        if (p.base2 && p.glu < 0 && p.ntasks_dev && (int)tk >= *p.ntasks_dev) {  // the second pass over the list
-            tk -= (uint32_t)*p.ntasks_dev;
+        if (p.base2 && p.glu < 0 && (int)tk >= ntk) {             // the second pass over the list
+            tk -= (uint32_t)ntk;
             sec = true;
         }
-        if (p.ntasks_dev && (int)tk >= *p.ntasks_dev) return;     // uniform
+        if ((int)tk >= ntk) return;                               // uniform
         const GemvTask & t = p.tasks[tk];
         const int64_t dadd = sec ? p.up_doff : 0;
         mat = t.mat;
@@ -447,9 +450,10 @@ __global__ __launch_bounds__(512) void k_gemv(GemvParams p) {
                 for (int j = 0; j < nc; ++j) p.dst[t.dst_off[j] + dadd + row] = 0.0f;
             return;                                               // uniform
         }
-        if (tid < nc) {
-            s_col[tid] = t.col[tid];
-            s_doff[tid] = t.dst_off[tid] + dadd;
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {                            // col[] / dst_off[] hold kMaxTaskCols >= NC
+            colv[j] = j < nc ? t.col[j] : t.col[0];
+            doffv[j] = (j < nc ? t.dst_off[j] : 0) + dadd;
         }
     } else {
         const uint32_t tpb = (uint32_t)p.tpb, ne12 = (uint32_t)p.ne12;
@@ -462,14 +466,14 @@ __global__ __launch_bounds__(512) void k_gemv(GemvParams p) {
         }
         const int64_t first = (int64_t)tt * NC;
         nc = (int)((p.ne11 - first) < NC ? (p.ne11 - first) : NC);
-        if (tid < nc) {
-            const int64_t i1 = first + tid;
-            s_col[tid] = (int64_t)b * p.col_bs + i1;
-            s_doff[tid] = i1 * p.d_nb1 + (int64_t)i2 * p.d_nb2 + (int64_t)i3 * p.d_nb3;
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            const int64_t i1 = first + (j < nc ? j : 0);
+            colv[j] = (int64_t)b * p.col_bs + i1;
+            doffv[j] = i1 * p.d_nb1 + (int64_t)i2 * p.d_nb2 + (int64_t)i3 * p.d_nb3;
         }
     }
     if (mat < 0 || nc <= 0) return;    // uniform over the work-group
-    __syncthreads();                   // s_col, s_doff
     nc = __builtin_amdgcn_readfirstlane(nc);
 
     const int G = (int)p.w.G;
@@ -485,7 +489,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvParams p) {
     const int16_t * xs0[NC];
 #pragma unroll
     for (int j = 0; j < NC; ++j) {
-        const int64_t col = j < nc ? s_col[j] : s_col[0];
+        const int64_t col = colv[j];
         const int64_t cu = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(col >> 32)) << 32) |
                                      (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)col));
         xc0[j] = p.xc + cu * p.ldk;
@@ -564,7 +568,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvParams p) {
 #pragma unroll
     for (int j = 0; j < NC; ++j) {
         if (j < nc) {
-            float * o = p.dst + s_doff[j] + row;
+            float * o = p.dst + doffv[j] + row;
             if (p.KS == 1) *o = tot[j];
             else atomicAdd(o, tot[j]);
         }
