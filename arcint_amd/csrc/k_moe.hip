@@ -20,13 +20,13 @@ namespace {
 
 constexpr int kRouteThreads = 1024;
 
-__global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs r, int32_t * __restrict__ scratch,
-                                                         GemvTask * __restrict__ tasks, int32_t * __restrict__ ntasks) {
-    extern __shared__ int32_t sm[];
+// one work-group of kRouteThreads; sm = [2 (n_as + 1)] ints of LDS, s_wsum = [kRouteThreads / 64]
+__device__ __forceinline__ void route_body(const RouteArgs & r, int32_t * __restrict__ scratch,
+                                           GemvTask * __restrict__ tasks, int32_t * __restrict__ ntasks,
+                                           int32_t * sm, int32_t * s_wsum) {
     const int64_t nbk = r.n_as + 1;     // buckets: the experts, then the invalid ids
     int32_t * cnt = sm;                 // [nbk] pair count, later the fill cursor
     int32_t * tstart = sm + nbk;        // [nbk] first task of each bucket
-    __shared__ int32_t s_wsum[kRouteThreads / 64];
     const int tid = threadIdx.x;
     const int64_t npairs = r.n_used * r.T;
     for (int64_t e = tid; e < nbk; e += kRouteThreads) cnt[e] = 0;
@@ -94,6 +94,33 @@ __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs r, int32_t * 
         T.col[slot % kMaxTaskCols] = b < r.n_as ? (int32_t)((i % r.ne11) + t * r.ne11) : 0;
         T.dst_off[slot % kMaxTaskCols] = t * r.dst_nb2 + i * r.dst_nb1;
     }
+}
+
+__global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs r, int32_t * __restrict__ scratch,
+                                                         GemvTask * __restrict__ tasks, int32_t * __restrict__ ntasks) {
+    extern __shared__ int32_t sm[];
+    __shared__ int32_t s_wsum[kRouteThreads / 64];
+    route_body(r, scratch, tasks, ntasks, sm, s_wsum);
+}
+
+// MUL_MAT_ID's two independent preparations in one launch: work-group 0 routes, the others
+// quantize the activations (the q8_0 or q8_K pass of the quantization launch, no dst
+// zeroing).  At decode both are a few microseconds of latency each; side by side the GEMV
+// waits for the longer one instead of their sum.
+template <int VDT>
+__global__ __launch_bounds__(kRouteThreads) void k_quant_route(F32Cols src, int64_t K, int64_t ncols, ActBuf a,
+                                                               RouteArgs r, int32_t * __restrict__ scratch,
+                                                               GemvTask * __restrict__ tasks,
+                                                               int32_t * __restrict__ ntasks) {
+    extern __shared__ int32_t sm[];
+    __shared__ int32_t s_wsum[kRouteThreads / 64];
+    if (blockIdx.x == 0) {                                        // uniform
+        route_body(r, scratch, tasks, ntasks, sm, s_wsum);
+        return;
+    }
+    const int64_t t = (int64_t)(blockIdx.x - 1) * kRouteThreads + threadIdx.x;
+    if (VDT == QMM_TYPE_Q8_0) quant_q8_0_at(src, K, ncols, a, t);
+    else quant_q8_K_at(src, K, ncols, a, t);
 }
 
 // ---- the router: softmax -> top-k -> normalized weights, one wave per token ----------
@@ -211,6 +238,20 @@ hipError_t launch_route(const RouteArgs & r, int32_t * scratch, GemvTask * tasks
     const size_t lds = (size_t)(r.n_as + 1) * 2 * sizeof(int32_t);
     if (lds > 64 * 1024) return hipErrorInvalidValue;
     k_route<<<1, kRouteThreads, lds, s>>>(r, scratch, tasks, ntasks);
+    return hipGetLastError();
+}
+
+hipError_t launch_quant_route(const F32Cols & src, int64_t K, int64_t ncols, const ActBuf & a, const RouteArgs & r,
+                              int32_t * scratch, GemvTask * tasks, int32_t * ntasks, hipStream_t s) {
+    const size_t lds = (size_t)(r.n_as + 1) * 2 * sizeof(int32_t);
+    if (lds > 64 * 1024 || K <= 0 || ncols < 0 || a.ldk % 256 || a.ldk < K) return hipErrorInvalidValue;
+    const int64_t nq = a.vdt == QMM_TYPE_Q8_0 ? ncols * (a.ldk / 4) : ncols * (a.ldk / 256) * 64;
+    const int64_t grid = 1 + (nq + kRouteThreads - 1) / kRouteThreads;
+    if (grid > 0x7fffffff) return hipErrorInvalidValue;
+    if (a.vdt == QMM_TYPE_Q8_0)
+        k_quant_route<QMM_TYPE_Q8_0><<<dim3((unsigned)grid), kRouteThreads, lds, s>>>(src, K, ncols, a, r, scratch, tasks, ntasks);
+    else
+        k_quant_route<QMM_TYPE_Q8_K><<<dim3((unsigned)grid), kRouteThreads, lds, s>>>(src, K, ncols, a, r, scratch, tasks, ntasks);
     return hipGetLastError();
 }
 

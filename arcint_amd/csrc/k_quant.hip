@@ -38,26 +38,7 @@ __global__ void k_quant_q8_0(F32Cols src, int64_t K, int64_t ncols, ActBuf a, Ze
         zero_cols(z, ((int64_t)blockIdx.x - nqblk) * kTpb + threadIdx.x);
         return;
     }
-    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t kq = a.ldk / 4;
-    const bool live = t < ncols * kq;              // groups of 8 lanes are all live or all dead
-    const int64_t c = live ? t / kq : 0, k = live ? (t % kq) * 4 : 0;
-    float v[4] = { 0.f, 0.f, 0.f, 0.f };
-    if (live && k < K) {
-        const float * x = f32_col(src, c) + k;
-        for (int i = 0; i < 4; ++i) v[i] = x[i];
-    }
-    float d;
-    int s;
-    const uint32_t packed = quant_q8_0_lane(v, &d, &s);
-    if (!live) return;
-    *reinterpret_cast<uint32_t *>(a.codes + c * a.ldk + k) = packed;
-    if ((t & 7) == 0) {
-        const int64_t b = c * (a.ldk / 32) + k / 32;
-        a.d[b] = d;
-        a.sums[b] = (int16_t)s;
-        if (a.dT) a.dT[(k / 32) * a.ldT + c] = d;            // padding blocks: d = 0
-    }
+    quant_q8_0_at(src, K, ncols, a, (int64_t)blockIdx.x * blockDim.x + threadIdx.x);
 }
 
 // one wave per 256-weight super-block, 4 weights per lane
@@ -66,33 +47,7 @@ __global__ void k_quant_q8_K(F32Cols src, int64_t K, int64_t ncols, ActBuf a, Ze
         zero_cols(z, ((int64_t)blockIdx.x - nqblk) * kTpb + threadIdx.x);
         return;
     }
-    const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-    const int lane = threadIdx.x & 63;
-    const int64_t nsb = a.ldk / 256;
-    if (wave >= ncols * nsb) return;               // whole waves only
-    const int64_t c = wave / nsb, sb = wave % nsb;
-    float v[4] = { 0.f, 0.f, 0.f, 0.f };
-    if (sb * 256 < K) {
-        const float * x = f32_col(src, c) + sb * 256 + 4 * lane;
-        for (int i = 0; i < 4; ++i) v[i] = x[i];
-    }
-    float d;
-    int s;
-    const uint32_t packed = quant_q8_K_wave(v, lane, &d, &s);
-    *reinterpret_cast<uint32_t *>(a.codes + c * a.ldk + sb * 256 + 4 * lane) = packed;
-    if ((lane & 3) == 0) a.sums[c * (a.ldk / 16) + sb * 16 + (lane >> 2)] = (int16_t)s;
-    if (a.bsp) {                                   // sub-block sums (8 lanes = 32 codes) as 64 bh + bl
-        const int s32 = s + __shfl_xor(s, 4, 64);
-        if ((lane & 7) == 0) {
-            int8_t * o = a.bsp + (sb * a.ldT + c) * 16 + (lane >> 3);
-            o[0] = (int8_t)(s32 >> 6);
-            o[8] = (int8_t)(s32 & 63);
-        }
-    }
-    if (lane == 0) {
-        a.d[c * nsb + sb] = d;
-        if (a.dT) a.dT[sb * a.ldT + c] = d;
-    }
+    quant_q8_K_at(src, K, ncols, a, (int64_t)blockIdx.x * blockDim.x + threadIdx.x);
 }
 
 // ActBuf -> ggml block bytes, one thread per block

@@ -238,13 +238,26 @@ bool same_key(const qmm_ctx * ctx, int vdt, const qmm_tensor * src1, bool dT) {
 
 // Quantize src1 (all its columns) with the vec_dot type of `type`, reusing
 // the previous result inside one graph when src1 is the same tensor.
-int quantize_src1(qmm_ctx * ctx, int type, const qmm_tensor * src1, bool dT, ActBuf * out, const ZeroJob * z = nullptr) {
+// a MUL_MAT_ID route whose launch joins the activation quantization's (the two are independent)
+struct PendingRoute {
+    RouteArgs r;
+    int32_t * scratch;
+    GemvTask * tasks;
+    int32_t * ntasks;
+};
+
+// quantize src1 for the vec_dot type of `type` (skipped when this graph already did); with
+// pr, the route runs in the same launch (or alone when the quantization is skipped)
+int quantize_src1(qmm_ctx * ctx, int type, const qmm_tensor * src1, bool dT, ActBuf * out, const ZeroJob * z = nullptr,
+                  const PendingRoute * pr = nullptr) {
     const int vdt = vec_dot_type(type);
     const int64_t K = src1->ne[0], ncols = src1->ne[1] * src1->ne[2] * src1->ne[3];
     auto & k = ctx->key;
+    if (pr && z) return fail(ctx, QMM_ERR_INVALID, "internal: a route launch with dst zeroing");
     if (ctx->in_graph && same_key(ctx, vdt, src1, dT)) {
         *out = ctx->cached;
         if (z) QMM_HIP(ctx, launch_quantize(f32_cols(src1), K, 0, ctx->cached, z, ctx->stream));   // zeroing only
+        if (pr) QMM_HIP(ctx, launch_route(pr->r, pr->scratch, pr->tasks, pr->ntasks, ctx->stream));
         return QMM_OK;
     }
     size_t od, os, ot, ob;
@@ -265,7 +278,8 @@ int quantize_src1(qmm_ctx * ctx, int type, const qmm_tensor * src1, bool dT, Act
     a.ldk = ldk;
     a.ncols = ncols;
     a.vdt = vdt;
-    QMM_HIP(ctx, launch_quantize(f32_cols(src1), K, ncols, a, z, ctx->stream));
+    if (pr) QMM_HIP(ctx, launch_quant_route(f32_cols(src1), K, ncols, a, pr->r, pr->scratch, pr->tasks, pr->ntasks, ctx->stream));
+    else QMM_HIP(ctx, launch_quantize(f32_cols(src1), K, ncols, a, z, ctx->stream));
     k.buf = src1->buffer;
     k.offs = src1->offs;
     memcpy(k.ne, src1->ne, sizeof(k.ne));
@@ -741,8 +755,11 @@ int qmm_mul_mat(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1,
 // The expert tasks of ids into the route scratch (reused inside a graph when ids, ne11, the
 // dst strides and the expert count are those of the route already there): pair (i, t) reads
 // activation column (i % ne11) + t ne11 and writes dst floats t dnb2 + i dnb1
+// with defer, a route that has to run is handed back (*pending) for the quantization launch
 static int route_tasks(qmm_ctx * ctx, const qmm_tensor * ids, int64_t ne11, int64_t n_as, int64_t dnb1, int64_t dnb2,
-                       int64_t max_tasks, GemvTask ** tasks, int32_t ** ntasks) {
+                       int64_t max_tasks, GemvTask ** tasks, int32_t ** ntasks, PendingRoute * defer = nullptr,
+                       bool * pending = nullptr) {
+    if (pending) *pending = false;
     const int64_t n_used = ids->ne[0], T = ids->ne[1], npairs = n_used * T;
     const size_t o_tasks = align_up((size_t)npairs * 4, 256);
     const size_t o_cnt = align_up(o_tasks + (size_t)max_tasks * sizeof(GemvTask), 256);
@@ -767,7 +784,12 @@ static int route_tasks(qmm_ctx * ctx, const qmm_tensor * ids, int64_t ne11, int6
     r.n_as = n_as;
     r.dst_nb1 = dnb1;
     r.dst_nb2 = dnb2;
-    QMM_HIP(ctx, launch_route(r, (int32_t *)rb, *tasks, *ntasks, ctx->stream));
+    if (defer) {
+        *defer = PendingRoute{ r, (int32_t *)rb, *tasks, *ntasks };
+        *pending = true;
+    } else {
+        QMM_HIP(ctx, launch_route(r, (int32_t *)rb, *tasks, *ntasks, ctx->stream));
+    }
     rk.ids = *ids;
     rk.ne11 = ne11;
     rk.n_as = n_as;
@@ -795,7 +817,6 @@ int qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * sr
     const int64_t npairs = ids->ne[0] * ids->ne[1];
     ActBuf a{};
     int rc;
-    if ((rc = quantize_src1(ctx, src0->type, src1, false, &a))) return rc;
     const int64_t max_tasks = route_max_tasks(npairs, n_as);
     const int nc = (int)std::min<int64_t>(kMaxTaskCols, npairs);
     GemvPlan plan;
@@ -804,9 +825,15 @@ int qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * sr
         return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat_id: GEMV shape out of range");
     GemvTask * tasks;
     int32_t * ntasks;
+    PendingRoute pr;
+    bool pending;
     if ((rc = route_tasks(ctx, ids, src1->ne[1], n_as, (int64_t)(dst->nb[1] / 4), (int64_t)(dst->nb[2] / 4), max_tasks,
-                          &tasks, &ntasks)))
+                          &tasks, &ntasks, &pr, &pending)))
         return rc;
+    if ((rc = quantize_src1(ctx, src0->type, src1, false, &a, nullptr, pending ? &pr : nullptr))) {
+        ctx->rkey.valid = false;                                  // the route may not have run
+        return rc;
+    }
     float * d = (float *)((uint8_t *)dst->buffer->ptr + dst->offs);
     ctx->path = plan.mma ? "gemv-id-mfma" : "gemv-id";
     KTime kt;
@@ -844,7 +871,6 @@ int qmm_mul_mat_id_glu(qmm_ctx * ctx, const qmm_tensor * gate, const qmm_tensor 
     const int64_t M = gate->ne[1], n_as = gate->ne[2], n_used = ids->ne[0], T = ids->ne[1], npairs = n_used * T;
     ActBuf a{};
     int rc;
-    if ((rc = quantize_src1(ctx, gate->type, src1, false, &a))) return rc;
     const int64_t max_tasks = route_max_tasks(npairs, n_as);
     const int nc = (int)std::min<int64_t>(kMaxTaskCols, npairs);
     const bool in_wg = max_tasks * wg.ntiles >= 1024;             // enough work-groups to fill the chip
@@ -861,7 +887,13 @@ int qmm_mul_mat_id_glu(qmm_ctx * ctx, const qmm_tensor * gate, const qmm_tensor 
     int32_t * ntasks;
     // in_wg: the dst's strides; else the scratch halves, contiguous [T][n_used][M]
     const int64_t dnb1 = in_wg ? (int64_t)(dst->nb[1] / 4) : M, dnb2 = in_wg ? (int64_t)(dst->nb[2] / 4) : M * n_used;
-    if ((rc = route_tasks(ctx, ids, src1->ne[1], n_as, dnb1, dnb2, max_tasks, &tasks, &ntasks))) return rc;
+    PendingRoute pr;
+    bool pending;
+    if ((rc = route_tasks(ctx, ids, src1->ne[1], n_as, dnb1, dnb2, max_tasks, &tasks, &ntasks, &pr, &pending))) return rc;
+    if ((rc = quantize_src1(ctx, gate->type, src1, false, &a, nullptr, pending ? &pr : nullptr))) {
+        ctx->rkey.valid = false;                                  // the route may not have run
+        return rc;
+    }
     GemvPair pair{ wu.base, in_wg ? 0 : (int64_t)half, in_wg ? glu_op : -1 };
     float * d = (float *)((uint8_t *)dst->buffer->ptr + dst->offs);
     ctx->path = plan.mma ? "glu-gemv-id-mfma" : "glu-gemv-id";

@@ -230,4 +230,65 @@ __device__ __forceinline__ const float * f32_col(const F32Cols & s, int64_t c) {
     return reinterpret_cast<const float *>(s.base + (size_t)i1 * s.nb1 + (size_t)i2 * s.nb2 + (size_t)i3 * s.nb3);
 }
 
+// Activation quantization bodies, shared by the quantization launch and the
+// MoE launch that also routes.  t = the thread's index over the quantization
+// threads (whole waves; a block of threads is a multiple of 64).
+#pragma clang fp contract(off)
+
+// q8_0: 8 lanes per 32-weight block, 4 weights per lane
+__device__ __forceinline__ void quant_q8_0_at(const F32Cols & src, int64_t K, int64_t ncols, const ActBuf & a, int64_t t) {
+    const int64_t kq = a.ldk / 4;
+    const bool live = t < ncols * kq;              // groups of 8 lanes are all live or all dead
+    const int64_t c = live ? t / kq : 0, k = live ? (t % kq) * 4 : 0;
+    float v[4] = { 0.f, 0.f, 0.f, 0.f };
+    if (live && k < K) {
+        const float * x = f32_col(src, c) + k;
+        for (int i = 0; i < 4; ++i) v[i] = x[i];
+    }
+    float d;
+    int s;
+    const uint32_t packed = quant_q8_0_lane(v, &d, &s);
+    if (!live) return;
+    *reinterpret_cast<uint32_t *>(a.codes + c * a.ldk + k) = packed;
+    if ((t & 7) == 0) {
+        const int64_t b = c * (a.ldk / 32) + k / 32;
+        a.d[b] = d;
+        a.sums[b] = (int16_t)s;
+        if (a.dT) a.dT[(k / 32) * a.ldT + c] = d;            // padding blocks: d = 0
+    }
+}
+
+// q8_K: one wave per 256-weight super-block, 4 weights per lane
+__device__ __forceinline__ void quant_q8_K_at(const F32Cols & src, int64_t K, int64_t ncols, const ActBuf & a, int64_t t) {
+    const int64_t wave = t >> 6;
+    const int lane = (int)(t & 63);
+    const int64_t nsb = a.ldk / 256;
+    if (wave >= ncols * nsb) return;               // whole waves only
+    const int64_t c = wave / nsb, sb = wave % nsb;
+    float v[4] = { 0.f, 0.f, 0.f, 0.f };
+    if (sb * 256 < K) {
+        const float * x = f32_col(src, c) + sb * 256 + 4 * lane;
+        for (int i = 0; i < 4; ++i) v[i] = x[i];
+    }
+    float d;
+    int s;
+    const uint32_t packed = quant_q8_K_wave(v, lane, &d, &s);
+    *reinterpret_cast<uint32_t *>(a.codes + c * a.ldk + sb * 256 + 4 * lane) = packed;
+    if ((lane & 3) == 0) a.sums[c * (a.ldk / 16) + sb * 16 + (lane >> 2)] = (int16_t)s;
+    if (a.bsp) {                                   // sub-block sums (8 lanes = 32 codes) as 64 bh + bl
+        const int s32 = s + __shfl_xor(s, 4, 64);
+        if ((lane & 7) == 0) {
+            int8_t * o = a.bsp + (sb * a.ldT + c) * 16 + (lane >> 3);
+            o[0] = (int8_t)(s32 >> 6);
+            o[8] = (int8_t)(s32 & 63);
+        }
+    }
+    if (lane == 0) {
+        a.d[c * nsb + sb] = d;
+        if (a.dT) a.dT[sb * a.ldT + c] = d;
+    }
+}
+
+#pragma clang fp contract(fast)
+
 }  // namespace qmm

@@ -277,5 +277,8 @@ hipError_t launch_glu(int op, const GluArgs & a, hipStream_t s);
 // scratch: pairs [T*n_used]; tasks out
 // tasks of mat = -1 carry pairs of invalid ids: the GEMV writes their dst rows as zeros
 hipError_t launch_route(const RouteArgs & r, int32_t * scratch, GemvTask * tasks, int32_t * ntasks, hipStream_t s);
+// the route and the activation quantization (no dst zeroing) in one launch
+hipError_t launch_quant_route(const F32Cols & src, int64_t K, int64_t ncols, const ActBuf & a, const RouteArgs & r,
+                              int32_t * scratch, GemvTask * tasks, int32_t * ntasks, hipStream_t s);
 
 }  // namespace qmm
