@@ -473,6 +473,25 @@ def test_mul_mat_id(be, sc, orc, qtype, T, bcast):
         assert not got[1, 2].any()
 
 
+@pytest.mark.parametrize("T", [1024, 1100])
+def test_mul_mat_id_many_pairs(be, sc, orc, T):
+    """4096 and 4400 (token, slot) pairs: a route over several pairs per route thread, about
+    275 pairs per expert in tasks of 8, one invalid id"""
+    qtype, E, n_used, M, K = qmm.Q4_K, 16, 4, 64, 256
+    say("mul_mat_id many pairs", T)
+    raw = synth.weights(qtype, E * M, K, seed=77)
+    ids = synth.moe_ids(T, E, n_used, seed=78)
+    ids[T - 1, 3] = -1
+    x = synth.activations(T, K, seed=79).reshape(T, 1, K)
+    w = sc.weights(qtype, raw, (K, M, E))
+    y = sc.empty_f32((M, n_used, T))
+    be.mul_mat_id(w, sc.f32(x), sc.i32(ids), y)
+    be.synchronize()
+    got = be.get_f32(y).reshape(T, n_used, M)
+    assert rel_err(got, orc.mul_mat_id(qtype, raw, M, K, E, x, ids)) <= TOL
+    assert not got[T - 1, 3].any()
+
+
 def test_mul_mat_id_all_tokens_one_expert(be, sc, orc):
     # more than 8 pairs on one expert: several tasks per expert
     qtype, E, n_used, M, K, T = qmm.Q4_K, 4, 2, 64, 256, 40
