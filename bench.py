@@ -369,8 +369,10 @@ def main():
                   (qmm.Q6_K, 151936, 5120, 1, "Q6_K GEMV 151936x5120 N=1 (config 2 output head)"),
                   (qmm.Q6_K, 151936, 5120, 4, "Q6_K 151936x5120 N=4 (config 2 output head, MTP verify width)")]
         for qt, nm in ((qmm.IQ4_XS, "IQ4_XS"), (qmm.Q8_0, "Q8_0")):
-            for n in (2, 4, 8):
+            for n in (1, 2, 4, 8):
                 gcases.append((qt, 14336, 4096, n, f"{nm} 14336x4096 N={n} (config 4)"))
+            for n in (1, 8):
+                gcases.append((qt, 4096, 14336, n, f"{nm} 4096x14336 N={n} (config 4)"))
         # the adjacent types on config shapes (no reference config quotes them)
         gcases += [(qmm.Q5_K, 17408, 5120, 1, "Q5_K GEMV 17408x5120 N=1 (config 2 shape)"),
                    (qmm.IQ4_NL, 14336, 4096, 1, "IQ4_NL GEMV 14336x4096 N=1 (config 4 shape)"),
