@@ -1122,7 +1122,13 @@ bool gemv_plan(int type, const WView & w, int nc, int64_t ntasks, bool allow_spl
         // (WK spw <= kMmaMaxGroups groups); the rest of the split is KS work-groups per tile
         // (atomics).  Task lists cannot split K over work-groups and fall back to the v_dot4
         // kernel past WK spw = G.
-        const int64_t target = std::max(1, env_int("QMM_GEMV_MMA_WAVES", 2048));
+        // by (tile, group) pairs (sweeps on the config shapes: 3584 pairs ran best at 1024
+        // waves, 5440 at 2048, the 151936-row head's 47480 at 4096, 10 % under its time at
+        // 2048); targets between these split the groups unevenly (3584 pairs at 1433 waves:
+        // slices of 3, 3, 3, 3, 3, 1 groups, slower than either neighbour)
+        const int64_t pairs = tiles * w.G;
+        const int64_t tgw = pairs < 4096 ? 1024 : pairs < 16384 ? 2048 : 4096;
+        const int64_t target = std::max(1, env_int("QMM_GEMV_MMA_WAVES", (int)tgw));
         // (at most 4 waves per work-group: three 4-wave work-groups fill a CU at the kernel's
         // occupancy of 3 waves per SIMD, 8-wave ones leave a third of it idle)
         const int64_t TW = std::min<int64_t>(std::max(1, std::min(4, env_int("QMM_GEMV_MMA_TILES", 4))), w.ntiles);
