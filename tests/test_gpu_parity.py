@@ -866,6 +866,31 @@ def test_graph_route_shared_by_gate_and_up(be, sc, orc):
         assert rel_err(got[~bad], ref[~bad]) <= TOL
 
 
+@pytest.mark.parametrize("qtype", [qmm.Q4_K, qmm.Q4_0])
+def test_graph_shared_src1_new_ids(be, sc, orc, qtype):
+    """MUL_MAT_IDs in one graph on the same src1 with other ids: the activations are quantized
+    once (route and quantization in one launch), the later nodes route alone"""
+    E, n_used, M, K, T = 16, 3, 64, 512, 7
+    say("graph-src1-new-ids", qtype)
+    raws = [synth.weights(qtype, E * M, K, 191 + i) for i in range(3)]
+    idss = [synth.moe_ids(T, E, n_used, seed=194 + i) for i in range(2)]
+    idss[1][3, 0] = -1
+    ws = [sc.weights(qtype, r, (K, M, E)) for r in raws]
+    x = synth.activations(T, K, seed=196).reshape(T, 1, K)
+    xt = sc.f32(x)
+    its = [sc.i32(i) for i in idss]
+    ys = [sc.f32(np.full((T, n_used, M), 3.0, np.float32)) for _ in range(3)]
+    order = [(0, 0), (1, 1), (2, 0)]                             # weights, ids: back to the first ids
+    be.graph_compute([(qmm.OP_MUL_MAT_ID, ws[w], xt, its[i], ys[n]) for n, (w, i) in enumerate(order)])
+    be.synchronize()
+    for n, (w, i) in enumerate(order):
+        got = be.get_f32(ys[n]).reshape(T, n_used, M)
+        ref = orc.mul_mat_id(qtype, raws[w], M, K, E, x, idss[i])
+        bad = idss[i] < 0
+        assert (got[bad] == 0).all()
+        assert rel_err(got[~bad], ref[~bad]) <= TOL, n
+
+
 @pytest.mark.parametrize("qtype", [qmm.Q4_K, qmm.Q4_0, qmm.Q6_K])
 @pytest.mark.parametrize("T,E", [(1, 16), (4, 16), (40, 16), (300, 64), (40, 512)])
 def test_mul_mat_id_glu(be, sc, orc, qtype, T, E):
