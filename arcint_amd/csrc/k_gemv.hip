@@ -102,6 +102,7 @@ template <int TYPE> struct GV;
 // ---- Q4_0: one stage per group: 8 code chunks (block p = chunk p) + d chunk
 template <> struct GV<QMM_TYPE_Q4_0> {
     static constexpr int NST = 1, NL = 9, ND = 8, NS = 8;
+    static constexpr int kReadEnd = 8 * kChunk + kTileRows * 16;         // chunks 0..8, 16 B a lane
     __device__ static void load(uint4 * r, const uint8_t * tg, int, int lane) {
         const uint8_t * p = tg + lane * 16;
 #pragma unroll
@@ -133,6 +134,7 @@ template <> struct GV<QMM_TYPE_Q4_0> {
 // ---- Q8_0: two stages per group: blocks 4st..4st+3 (chunks 8st..8st+7) + d
 template <> struct GV<QMM_TYPE_Q8_0> {
     static constexpr int NST = 2, NL = 9, ND = 8, NS = 8;
+    static constexpr int kReadEnd = 16 * kChunk + kTileRows * 16;        // chunks 0..15 and 16
     __device__ static void load(uint4 * r, const uint8_t * tg, int st, int lane) {
         const uint8_t * p = tg + lane * 16;
 #pragma unroll
@@ -165,6 +167,7 @@ template <> struct GV<QMM_TYPE_Q8_0> {
 // sub-block 2(c/2), high nibbles the same + 32 of sub-block 2(c/2) + 1.
 template <> struct GV<QMM_TYPE_Q4_K> {
     static constexpr int NST = 1, NL = 9, ND = 1, NS = 16;
+    static constexpr int kReadEnd = 8 * kChunk + kTileRows * 16;         // chunks 0..8
     __device__ static void load(uint4 * r, const uint8_t * tg, int, int lane) {
         const uint8_t * p = tg + lane * 16;
 #pragma unroll
@@ -224,6 +227,7 @@ template <> struct GV<QMM_TYPE_Q4_K> {
 // sum index 8n + 2g + lh.
 template <> struct GV<QMM_TYPE_Q6_K> {
     static constexpr int NST = 2, NL = 8, ND = 1, NS = 16;
+    static constexpr int kReadEnd = 13 * kChunk + kTileRows * 2;         // chunks 0..12, then d (2 B a lane)
     __device__ static void load(uint4 * r, const uint8_t * tg, int st, int lane) {
         const uint8_t * p = tg + lane * 16;
 #pragma unroll
@@ -278,6 +282,7 @@ template <> struct GV<QMM_TYPE_Q6_K> {
 // + the 8-byte header {d, scales_h, scales_l[4]} of the tail plane
 template <> struct GV<QMM_TYPE_IQ4_XS> {
     static constexpr int NST = 1, NL = 9, ND = 1, NS = 16;
+    static constexpr int kReadEnd = 8 * kChunk + kTileRows * 8;          // chunks 0..7, then the 8 B header
     __device__ static void load(uint4 * r, const uint8_t * tg, int, int lane) {
         const uint8_t * p = tg + lane * 16;
 #pragma unroll
@@ -319,6 +324,7 @@ template <> struct GV<QMM_TYPE_IQ4_XS> {
 // ---- IQ4_NL: Q4_0's stage (8 code chunks + the d chunk), the codes through the codebook
 template <> struct GV<QMM_TYPE_IQ4_NL> {
     static constexpr int NST = 1, NL = 9, ND = 8, NS = 8;
+    static constexpr int kReadEnd = GV<QMM_TYPE_Q4_0>::kReadEnd;
     __device__ static void load(uint4 * r, const uint8_t * tg, int st, int lane) { GV<QMM_TYPE_Q4_0>::load(r, tg, st, lane); }
     template <int NC>
     __device__ static void dot(const uint4 * r, int, const XG<NC> & x, int nc, float * acc, int *) {
@@ -347,6 +353,7 @@ template <> struct GV<QMM_TYPE_IQ4_NL> {
 // of position 16 h + i of all four 64-weight chunks (bit 2 cc low nibble, 2 cc + 1 high)
 template <> struct GV<QMM_TYPE_Q5_K> {
     static constexpr int NST = 1, NL = 11, ND = 1, NS = 16;
+    static constexpr int kReadEnd = 10 * kChunk + kTileRows * 16;        // chunks 0..10
     __device__ static void load(uint4 * r, const uint8_t * tg, int, int lane) {
         const uint8_t * p = tg + lane * 16;
 #pragma unroll
@@ -409,6 +416,44 @@ template <> struct GV<QMM_TYPE_Q5_K> {
 // at depth 3.
 template <int NC> constexpr int ring_depth() { return 1; }
 
+// ---- index math of the two GEMV kernels, shared with the host replay of their loads --------
+// (gemv_extent below walks every work-group, wave and stage of a plan with these functions)
+// work-group b of a launch of n units (tiles or tile blocks) per task and KS K slices
+struct WgPos { uint32_t ks, unit, task; };
+__host__ __device__ __forceinline__ WgPos wg_pos(uint32_t b, uint32_t KS, uint32_t n) {
+    const uint32_t rest = b / KS;
+    return WgPos{ b % KS, rest % n, rest / n };
+}
+// dense task -> batch b = i2 + i3 ne12, column tile tt of the batch, and the weight matrix
+struct DenseTask { uint32_t b, tt, i2, i3; int mat; };
+__host__ __device__ __forceinline__ DenseTask dense_task(uint32_t task, uint32_t tpb, uint32_t ne12, uint32_t r2,
+                                                         uint32_t r3, uint32_t ne02) {
+    DenseTask d;
+    d.b = task / tpb;
+    d.tt = task - d.b * tpb;
+    d.i3 = d.b / ne12;
+    d.i2 = d.b - d.i3 * ne12;
+    d.mat = (int)(d.i2 / r2 + (d.i3 / r3) * ne02);
+    return d;
+}
+// v_dot4 kernel: wave `wave` of K slice ks streams S stages from group ga on (S = 0: none)
+__host__ __device__ __forceinline__ void dot4_stages(int ks, int W, int wave, int spw, int G, int nst, int & ga, int & S) {
+    ga = (ks * W + wave) * spw;
+    const int gb = ga + spw < G ? ga + spw : G;
+    S = ga < gb ? (gb - ga) * nst : 0;
+}
+// MFMA kernel: the work-group of K slice ks stages the activations of groups [gw, gw + ngw); its
+// K wave kw streams groups [ga, ga + nsw)
+__host__ __device__ __forceinline__ void mma_groups(int ks, int WK, int kw, int spw, int G, int & gw, int & ngw, int & ga,
+                                                    int & nsw) {
+    gw = ks * WK * spw;
+    ngw = gw + WK * spw < G ? WK * spw : G - gw;
+    ga = gw + kw * spw;
+    nsw = ga >= G ? 0 : (ga + spw < G ? spw : G - ga);
+}
+// the group whose tile-group stage s of a wave starting at group ga loads (s < S)
+__host__ __device__ __forceinline__ int stage_group(int ga, int s, int nst) { return ga + s / nst; }
+
 // One work-group: W waves on one 64-row tile of one task's matrix and one of
 // the tile's KS K slices; wave w takes groups [(ks W + w) spw, + spw).  Lane r
 // owns row r.  At the end the W waves are added in LDS in a fixed order and
@@ -424,9 +469,11 @@ __global__ __launch_bounds__(512) void k_gemv(GemvParams p) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     // work-group -> (task, tile, K slice); these counts fit 32 bits
+    static_assert(T::kReadEnd <= tile_group_bytes(TYPE) && tile_group_bytes(TYPE) <= (int)kSinkBytes,
+                  "a stage reads inside one tile-group, which fits in the sink");
     const uint32_t ntl = (uint32_t)p.w.ntiles;
-    const uint32_t ks = blockIdx.x % (uint32_t)p.KS, rest = blockIdx.x / (uint32_t)p.KS;
-    const uint32_t tile = rest % ntl, task = rest / ntl;
+    const WgPos wp = wg_pos(blockIdx.x, (uint32_t)p.KS, ntl);
+    const uint32_t ks = wp.ks, tile = wp.unit, task = wp.task;
     int mat, nc;
     bool sec = false;                  // the second image (gate/up in one launch)
     // per column: activation column id and float offset of dst row 0, uniform
@@ -456,30 +503,28 @@ __global__ __launch_bounds__(512) void k_gemv(GemvParams p) {
             doffv[j] = (j < nc ? t.dst_off[j] : 0) + dadd;
         }
     } else {
-        const uint32_t tpb = (uint32_t)p.tpb, ne12 = (uint32_t)p.ne12;
-        const uint32_t b = task / tpb, tt = task - b * tpb;
-        const uint32_t i3 = b / ne12, i2 = b - i3 * ne12;
-        mat = (int)(i2 / (uint32_t)p.r2 + (i3 / (uint32_t)p.r3) * (uint32_t)p.ne02);
+        const DenseTask dt = dense_task(task, (uint32_t)p.tpb, (uint32_t)p.ne12, (uint32_t)p.r2, (uint32_t)p.r3,
+                                        (uint32_t)p.ne02);
+        mat = dt.mat;
         if (p.base2 && mat == 1) {                                // gate/up in one launch
             mat = 0;
             sec = true;
         }
-        const int64_t first = (int64_t)tt * NC;
+        const int64_t first = (int64_t)dt.tt * NC;
         nc = (int)((p.ne11 - first) < NC ? (p.ne11 - first) : NC);
 #pragma unroll
         for (int j = 0; j < NC; ++j) {
             const int64_t i1 = first + (j < nc ? j : 0);
-            colv[j] = (int64_t)b * p.col_bs + i1;
-            doffv[j] = i1 * p.d_nb1 + (int64_t)i2 * p.d_nb2 + (int64_t)i3 * p.d_nb3;
+            colv[j] = (int64_t)dt.b * p.col_bs + i1;
+            doffv[j] = i1 * p.d_nb1 + (int64_t)dt.i2 * p.d_nb2 + (int64_t)dt.i3 * p.d_nb3;
         }
     }
     if (mat < 0 || nc <= 0) return;    // uniform over the work-group
     nc = __builtin_amdgcn_readfirstlane(nc);
 
     const int G = (int)p.w.G;
-    const int ga = ((int)ks * p.W + wave) * p.spw;                // this wave's groups [ga, gb)
-    const int gb = ga + p.spw < G ? ga + p.spw : G;
-    const int S = ga < gb ? (gb - ga) * NST : 0;                  // stages (uniform)
+    int ga, S;                                                    // this wave's first group, its stages (uniform)
+    dot4_stages((int)ks, p.W, wave, p.spw, G, NST, ga, S);
     const uint8_t * tbase = mat_tile(p, mat, tile, sec);
     const size_t tgs = (size_t)p.w.tg;
 
@@ -509,7 +554,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvParams p) {
         if (S <= 0) return;
         uint4 B[D][NL];
         auto load_stage = [&](uint4 * b, int s) {             // past the end: the sink
-            const uint8_t * tg = s < S ? tb + (size_t)(ga + s / NST) * tgs : p.sink;
+            const uint8_t * tg = s < S ? tb + (size_t)stage_group(ga, s, NST) * tgs : p.sink;
             T::load(b, tg, s < S ? s % NST : 0, lane);
         };
 #pragma unroll
@@ -518,7 +563,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvParams p) {
 #pragma unroll
             for (int i = 0; i < D; ++i) {
                 if (s + i < S) {                                  // uniform
-                    const int g = ga + (s + i) / NST;
+                    const int g = stage_group(ga, s + i, NST);
                     XG<NC> x;
 #pragma unroll
                     for (int j = 0; j < NC; ++j) {
@@ -884,9 +929,11 @@ __device__ __forceinline__ void gemv_mma_body(const GemvParams & p) {
     const int TW = p.tw, WK = p.W / p.tw;
     const int tw = wave % TW, kw = wave / TW;
     // work-group -> (task, tile block, K slice); these counts fit 32 bits
+    static_assert(T::kReadEnd <= tile_group_bytes(TYPE) && tile_group_bytes(TYPE) <= (int)kSinkBytes,
+                  "a stage reads inside one tile-group, which fits in the sink");
     const uint32_t ntl = (uint32_t)p.w.ntiles, ntb = (ntl + (uint32_t)TW - 1) / (uint32_t)TW;
-    const uint32_t ks = blockIdx.x % (uint32_t)p.KS, rest = blockIdx.x / (uint32_t)p.KS;
-    const uint32_t tb = rest % ntb, task = rest / ntb;
+    const WgPos wp = wg_pos(blockIdx.x, (uint32_t)p.KS, ntb);
+    const uint32_t ks = wp.ks, tb = wp.unit, task = wp.task;
     int mat, nc;
     bool sec = false;                  // the second image (gate/up in one launch)
     if (p.tasks) {
@@ -912,28 +959,27 @@ __device__ __forceinline__ void gemv_mma_body(const GemvParams & p) {
             s_doff[tid] = t.dst_off[tid] + dadd;
         }
     } else {
-        const uint32_t tpb = (uint32_t)p.tpb, ne12 = (uint32_t)p.ne12;
-        const uint32_t b = task / tpb, tt = task - b * tpb;
-        const uint32_t i3 = b / ne12, i2 = b - i3 * ne12;
-        mat = (int)(i2 / (uint32_t)p.r2 + (i3 / (uint32_t)p.r3) * (uint32_t)p.ne02);
+        const DenseTask dt = dense_task(task, (uint32_t)p.tpb, (uint32_t)p.ne12, (uint32_t)p.r2, (uint32_t)p.r3,
+                                        (uint32_t)p.ne02);
+        mat = dt.mat;
         if (p.base2 && mat == 1) {                                // gate/up in one launch
             mat = 0;
             sec = true;
         }
-        const int64_t first = (int64_t)tt * p.nct;
+        const int64_t first = (int64_t)dt.tt * p.nct;
         nc = (int)((p.ne11 - first) < p.nct ? (p.ne11 - first) : p.nct);
         if (tid < nc) {
             const int64_t i1 = first + tid;
-            s_col[tid] = (int64_t)b * p.col_bs + i1;
-            s_doff[tid] = i1 * p.d_nb1 + (int64_t)i2 * p.d_nb2 + (int64_t)i3 * p.d_nb3;
+            s_col[tid] = (int64_t)dt.b * p.col_bs + i1;
+            s_doff[tid] = i1 * p.d_nb1 + (int64_t)dt.i2 * p.d_nb2 + (int64_t)dt.i3 * p.d_nb3;
         }
     }
     if (mat < 0 || nc <= 0) return;                               // uniform
     const int G = (int)p.w.G;
-    const int gw = (int)ks * WK * p.spw;                          // the work-group's groups [gw, gw + ngw)
-    const int ngw = gw + WK * p.spw < G ? WK * p.spw : G - gw;    // >= 1 (the plan leaves no empty slice)
-    const int ga = gw + kw * p.spw;                               // this wave's groups [ga, ga + nsw)
-    const int nsw = ga >= G ? 0 : (ga + p.spw < G ? p.spw : G - ga);
+    // the work-group's groups [gw, gw + ngw) (ngw >= 1: the plan leaves no empty slice), this
+    // wave's [ga, ga + nsw)
+    int gw, ngw, ga, nsw;
+    mma_groups((int)ks, WK, kw, p.spw, G, gw, ngw, ga, nsw);
     const uint32_t tile = tb * (uint32_t)TW + (uint32_t)tw;
     const int S = tile < ntl ? nsw * NST : 0;                     // stages (uniform per wave)
     const uint8_t * tbase = mat_tile(p, mat, tile < ntl ? tile : 0, sec);   // the up tile after the gate (GLU)
@@ -941,7 +987,7 @@ __device__ __forceinline__ void gemv_mma_body(const GemvParams & p) {
     const bool glu = CM == 8 && p.glu >= 0;                       // uniform (lists: 8-column tasks only)
     auto load_stage = [&](uint4 (&b)[NL], int s) {                // past the last stage: the sink
         const bool real = s < S;
-        T::load(b, real ? tbase + (size_t)(ga + s / NST) * tgs : p.sink, real ? s % NST : 0, lane);
+        T::load(b, real ? tbase + (size_t)stage_group(ga, s, NST) * tgs : p.sink, real ? s % NST : 0, lane);
     };
     // the first stage's weights are requested before the activations are staged
     uint4 b0[NL], b1[NL];
@@ -1189,6 +1235,80 @@ size_t gemv_lds_bytes(int type, const GemvPlan & pl) {
         return std::max(stage, red);
     }
     return pl.W > 1 ? (size_t)pl.W * pl.nc * 64 * sizeof(float) : 0;
+}
+
+namespace {
+template <int TYPE> constexpr int read_end_of() { return GV<TYPE>::kReadEnd; }
+template <int TYPE> constexpr int nst_of() { return GV<TYPE>::NST; }
+// (read extent of a stage from its tile-group base, stages per group) of a type; false if unknown
+bool stage_shape(int type, int * read_end, int * nst) {
+    switch (type) {
+#define QMM_SS(T) case T: *read_end = read_end_of<T>(); *nst = nst_of<T>(); return true;
+        QMM_SS(QMM_TYPE_Q4_0) QMM_SS(QMM_TYPE_Q8_0) QMM_SS(QMM_TYPE_Q4_K) QMM_SS(QMM_TYPE_Q5_K)
+        QMM_SS(QMM_TYPE_Q6_K) QMM_SS(QMM_TYPE_IQ4_XS) QMM_SS(QMM_TYPE_IQ4_NL)
+#undef QMM_SS
+        default: return false;
+    }
+}
+}  // namespace
+
+// The loads a GEMV launch makes, replayed on the host with the kernels' own index functions
+// (wg_pos, dense_task, dot4_stages / mma_groups, stage_group): every work-group and wave, its
+// stages 0 .. S - 1 from the image and the one stage S that the ring loads past its end from
+// the sink (both kernels keep one stage in flight, so stage S is loaded and never consumed).
+bool gemv_extent(int type, const WView & w, const GemvPlan & pl, const GemvDense * dense, int64_t nmat, int list_mat,
+                 GemvExtent * e) {
+    int rend, nst;
+    if (!e || !stage_shape(type, &rend, &nst) || w.tg != tile_group_bytes(type)) return false;
+    *e = GemvExtent{};
+    e->image_bytes = (int64_t)nmat * w.ntiles * w.G * w.tg;
+    e->real_lo = INT64_MAX;
+    e->read_end = rend;
+    const int64_t nwg = gemv_workgroups(w, pl);
+    const int G = (int)w.G;
+    const uint32_t ntl = (uint32_t)w.ntiles, TW = pl.mma ? (uint32_t)pl.tw : 1u, ntb = (ntl + TW - 1) / TW;
+    const int64_t tpb = dense ? (dense->ne11 + pl.nc - 1) / pl.nc : 0;
+    auto wave_loads = [&](int mat, uint32_t tile, int ga, int S) {
+        if (S <= 0) return;
+        for (int s = 0; s < S; ++s) {
+            const int g = stage_group(ga, s, nst);
+            const int64_t off = ((mat * (int64_t)w.ntiles + tile) * w.G + g) * w.tg;
+            if (mat < 0 || mat >= nmat || tile >= ntl || g < 0 || g >= G || off < 0 || off + rend > e->image_bytes) e->bad++;
+            e->real_lo = std::min(e->real_lo, off);
+            e->real_hi = std::max(e->real_hi, off + rend);
+            e->real_loads++;
+        }
+        e->sink_hi = std::max<int64_t>(e->sink_hi, rend);         // stage S: the sink, at its base
+        e->sink_loads++;
+        if (rend > (int64_t)kSinkBytes) e->bad++;
+    };
+    for (int64_t b = 0; b < nwg; ++b) {
+        const WgPos wp = wg_pos((uint32_t)b, (uint32_t)pl.KS, pl.mma ? ntb : ntl);
+        int mat = list_mat;
+        if (dense) {
+            mat = dense_task(wp.task, (uint32_t)tpb, (uint32_t)dense->ne12, (uint32_t)dense->r2, (uint32_t)dense->r3,
+                             (uint32_t)dense->ne02).mat;
+            if (dense->base2 && mat == 1) mat = 0;                // the second image has the first's shape
+        }
+        if (pl.mma) {
+            const int WK = pl.W / pl.tw;
+            for (int wave = 0; wave < pl.W; ++wave) {
+                int gw, ngw, ga, nsw;
+                mma_groups((int)wp.ks, WK, wave / pl.tw, pl.spw, G, gw, ngw, ga, nsw);
+                if (ngw < 1 || gw + ngw > G || ngw > WK * pl.spw) e->bad++;   // activation groups staged in LDS
+                const uint32_t tile = wp.unit * TW + (uint32_t)(wave % pl.tw);
+                wave_loads(mat, tile, ga, tile < ntl ? nsw * nst : 0);
+            }
+        } else {
+            for (int wave = 0; wave < pl.W; ++wave) {
+                int ga, S;
+                dot4_stages((int)wp.ks, pl.W, wave, pl.spw, G, nst, ga, S);
+                wave_loads(mat, wp.unit, ga, S);
+            }
+        }
+    }
+    if (!e->real_loads) e->real_lo = 0;
+    return true;
 }
 
 hipError_t launch_gemv(int type, const WView & w, const GemvPlan & pl, const ActBuf & a, const GemvTask * tasks,

@@ -1084,6 +1084,56 @@ int qmm_mul_mat_glu(qmm_ctx * ctx, const qmm_tensor * gate, const qmm_tensor * u
     return QMM_OK;
 }
 
+// Self-check for the tests (declared in qmm_internal.h, not part of the op ABI): the weight
+// loads the GEMV launch of a qmm_mul_mat (id_n_used == 0: src0 of shape ne0, src1 [K, N,
+// nbatch]) or of a qmm_mul_mat_id (id_n_used > 0: N tokens of id_n_used ids over ne0[2]
+// experts, every task on the first and on the last expert) would make, planned as those entry
+// points plan them and replayed on the host by gemv_extent.  out[8] = image bytes, lowest
+// first byte, highest end byte, highest sink end, real loads, sink loads, bad loads, the
+// stage's read extent.  No device is touched.  QMM_ERR_UNSUPPORTED when the product would run
+// on the GEMM instead.
+int qmm_internal_gemv_extent(int32_t type, const int64_t ne0[4], int64_t N, int64_t nbatch, int64_t id_n_used,
+                             int64_t out[8]) {
+    const TypeLayout * L = type_layout(type);
+    ImageShape sh;
+    if (!L || !out || N < 1 || nbatch < 1 || id_n_used < 0 || !image_shape(*L, ne0, &sh)) return QMM_ERR_INVALID;
+    WView w{ nullptr, sh.M, sh.K, sh.bpr, sh.G, sh.ntiles, L->tg };
+    GemvPlan plan;
+    GemvExtent e[2];
+    if (id_n_used == 0) {
+        if (N >= gemm_min_cols(type)) return QMM_ERR_UNSUPPORTED;
+        const int nc = gemv_task_cols(type, N);
+        const int64_t ntasks = (N + nc - 1) / nc * nbatch;
+        if (!gemv_plan(type, w, nc, ntasks, true, nc >= gemv_mma_min_cols(), &plan)) return QMM_ERR_UNSUPPORTED;
+        GemvDense dn;
+        dn.ne11 = N;
+        dn.ne12 = nbatch;
+        dn.ne13 = 1;
+        dn.r2 = nbatch / sh.nmat;
+        dn.r3 = 1;
+        dn.ne02 = sh.nmat;
+        if (sh.nmat < 1 || nbatch % sh.nmat) return QMM_ERR_INVALID;
+        if (!gemv_extent(type, w, plan, &dn, sh.nmat, 0, &e[0])) return QMM_ERR_INVALID;
+        e[1] = e[0];
+    } else {
+        const int64_t n_as = sh.nmat, npairs = id_n_used * N;
+        const int64_t max_tasks = route_max_tasks(npairs, n_as);
+        const int nc = (int)std::min<int64_t>(kMaxTaskCols, npairs);
+        if (!gemv_plan(type, w, nc, max_tasks, false, npairs >= 2 * n_as, &plan)) return QMM_ERR_UNSUPPORTED;
+        for (int i = 0; i < 2; ++i)
+            if (!gemv_extent(type, w, plan, nullptr, n_as, i ? (int)(n_as - 1) : 0, &e[i])) return QMM_ERR_INVALID;
+    }
+    out[0] = e[0].image_bytes;
+    out[1] = std::min(e[0].real_lo, e[1].real_lo);
+    out[2] = std::max(e[0].real_hi, e[1].real_hi);
+    out[3] = std::max(e[0].sink_hi, e[1].sink_hi);
+    out[4] = e[0].real_loads;
+    out[5] = e[0].sink_loads;
+    out[6] = e[0].bad + e[1].bad;
+    out[7] = e[0].read_end;
+    return QMM_OK;
+}
+
 int qmm_graph_compute(qmm_ctx * ctx, const qmm_node * nodes, int n_nodes) {
     if (!ctx || (!nodes && n_nodes)) return QMM_ERR_INVALID;
     ctx->graph_gen++;

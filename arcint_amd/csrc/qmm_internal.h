@@ -38,6 +38,27 @@ constexpr int kChunk = 1024;
 constexpr size_t kPlaneAlign = 256;
 static inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+// bytes of one tile-group: chunk planes * 1 KB + 64 rows * tail bytes (0: not a weight type)
+__host__ __device__ constexpr int tile_group_bytes(int type) {
+    return type == QMM_TYPE_Q4_0 || type == QMM_TYPE_IQ4_NL ? 9 * kChunk
+         : type == QMM_TYPE_Q8_0                          ? 17 * kChunk
+         : type == QMM_TYPE_Q4_K                          ? 9 * kChunk
+         : type == QMM_TYPE_Q5_K                          ? 11 * kChunk
+         : type == QMM_TYPE_Q6_K                          ? 13 * kChunk + 2 * kTileRows
+         : type == QMM_TYPE_IQ4_XS                        ? 8 * kChunk + 8 * kTileRows
+                                                          : 0;
+}
+
+// The GEMV kernels keep their weight loads unconditional: a stage past the end of a wave's
+// range reads this many bytes of zeros (the context's sink) instead of weights.  A stage reads
+// at most one tile-group from its base, so every type's tile-group must fit in the sink.
+constexpr size_t kSinkBytes = 32768;
+static_assert(tile_group_bytes(QMM_TYPE_Q4_0) <= (int)kSinkBytes && tile_group_bytes(QMM_TYPE_Q8_0) <= (int)kSinkBytes &&
+                  tile_group_bytes(QMM_TYPE_Q4_K) <= (int)kSinkBytes && tile_group_bytes(QMM_TYPE_Q5_K) <= (int)kSinkBytes &&
+                  tile_group_bytes(QMM_TYPE_Q6_K) <= (int)kSinkBytes && tile_group_bytes(QMM_TYPE_IQ4_XS) <= (int)kSinkBytes &&
+                  tile_group_bytes(QMM_TYPE_IQ4_NL) <= (int)kSinkBytes,
+              "a stage load past the end reads one tile-group's extent of the sink");
+
 struct TypeLayout {
     int type;
     int blck;     // weights per GGUF block
@@ -186,6 +207,19 @@ constexpr int kMmaMaxCols = 32;    // columns of one MFMA task (the A operand's 
 // want_mma: use the MFMA kernel where the type allows it
 bool gemv_plan(int type, const WView & w, int nc, int64_t ntasks, bool allow_split, bool want_mma, GemvPlan * plan);
 int64_t gemv_workgroups(const WView & w, const GemvPlan & plan);
+// The weight loads of a GEMV launch, replayed on the host (no device) with the kernels' own
+// index functions: byte ranges relative to the image base of `nmat` matrices, and of the sink.
+// Task lists take matrix list_mat for every task (dense launches derive it from `dense`).
+struct GemvExtent {
+    int64_t image_bytes;        // bytes of the nmat matrices' tile-groups
+    int64_t real_lo, real_hi;   // lowest first byte / highest end of a load from the image
+    int64_t sink_hi;            // highest end of a load from the sink (<= kSinkBytes)
+    int64_t real_loads, sink_loads;
+    int64_t read_end;           // bytes a stage reads from its tile-group base
+    int64_t bad;                // loads outside the image or the sink, groups outside [0, G)
+};
+bool gemv_extent(int type, const WView & w, const GemvPlan & plan, const GemvDense * dense, int64_t nmat, int list_mat,
+                 GemvExtent * e);
 size_t gemv_lds_bytes(int type, const GemvPlan & plan);
 // whether the few-column MFMA kernel handles this weight type
 bool gemv_mma_supported(int type);
@@ -196,7 +230,6 @@ bool gemv_mma_supported(int type);
 // Dense mode (tasks == nullptr): tasks of up to nc columns from `dense`.
 // `sink`: kSinkBytes of device memory the kernel may read (not write) for
 // loads past the end of its pipeline.
-constexpr size_t kSinkBytes = 32768;
 // pair (task lists only), a second expert stack of w's shape at pair->base2: with glu < 0 the
 // list runs a second time on it, its dst offsets plus up_doff floats (plan.ntasks counts both
 // passes); with glu >= 0 (enum qmm_glu) each work-group streams its tile of both stacks and
@@ -282,3 +315,8 @@ hipError_t launch_quant_route(const F32Cols & src, int64_t K, int64_t ncols, con
                               int32_t * scratch, GemvTask * tasks, int32_t * ntasks, hipStream_t s);
 
 }  // namespace qmm
+
+// Self-check for the tests, exported from libqmm but not part of the op ABI (include/qmm.h):
+// the GEMV weight loads of a MUL_MAT / MUL_MAT_ID shape replayed on the host (qmm_api.cpp).
+extern "C" int qmm_internal_gemv_extent(int32_t type, const int64_t ne0[4], int64_t N, int64_t nbatch,
+                                        int64_t id_n_used, int64_t out[8]);

@@ -13,15 +13,20 @@ namespace qmm {
 namespace {
 
 // type, blck, bytes, bpg, nchunk, tail, tg
-const TypeLayout kLayouts[] = {
-    { QMM_TYPE_Q4_0,   32,  18,  8, 9,  0, 9 * kChunk },
-    { QMM_TYPE_Q8_0,   32,  34,  8, 17, 0, 17 * kChunk },
-    { QMM_TYPE_Q4_K,   256, 144, 1, 9,  0, 9 * kChunk },
-    { QMM_TYPE_Q6_K,   256, 210, 1, 13, 2, 13 * kChunk + 2 * kTileRows },
-    { QMM_TYPE_IQ4_XS, 256, 136, 1, 8,  8, 8 * kChunk + 8 * kTileRows },
-    { QMM_TYPE_Q5_K,   256, 176, 1, 11, 0, 11 * kChunk },
-    { QMM_TYPE_IQ4_NL, 32,  18,  8, 9,  0, 9 * kChunk },
+constexpr TypeLayout kLayouts[] = {
+    { QMM_TYPE_Q4_0,   32,  18,  8, 9,  0, tile_group_bytes(QMM_TYPE_Q4_0) },
+    { QMM_TYPE_Q8_0,   32,  34,  8, 17, 0, tile_group_bytes(QMM_TYPE_Q8_0) },
+    { QMM_TYPE_Q4_K,   256, 144, 1, 9,  0, tile_group_bytes(QMM_TYPE_Q4_K) },
+    { QMM_TYPE_Q6_K,   256, 210, 1, 13, 2, tile_group_bytes(QMM_TYPE_Q6_K) },
+    { QMM_TYPE_IQ4_XS, 256, 136, 1, 8,  8, tile_group_bytes(QMM_TYPE_IQ4_XS) },
+    { QMM_TYPE_Q5_K,   256, 176, 1, 11, 0, tile_group_bytes(QMM_TYPE_Q5_K) },
+    { QMM_TYPE_IQ4_NL, 32,  18,  8, 9,  0, tile_group_bytes(QMM_TYPE_IQ4_NL) },
 };
+// the planes fill the tile-group exactly
+constexpr bool planes_fill(const TypeLayout & L) { return L.nchunk * kChunk + kTileRows * L.tail == L.tg; }
+static_assert(planes_fill(kLayouts[0]) && planes_fill(kLayouts[1]) && planes_fill(kLayouts[2]) && planes_fill(kLayouts[3]) &&
+                  planes_fill(kLayouts[4]) && planes_fill(kLayouts[5]) && planes_fill(kLayouts[6]),
+              "chunk planes + tail plane = tile-group bytes");
 
 }  // namespace
 

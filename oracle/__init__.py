@@ -25,6 +25,10 @@ NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", I
 
 _lib = None
 
+# worker threads of mul_mat / mul_mat_id when the caller names none: the host share of a
+# one-GPU box is 16 cores, whatever os.cpu_count() reports there
+DEFAULT_THREADS = max(1, min(16, os.cpu_count() or 1))
+
 
 def lib() -> C.CDLL:
     global _lib
@@ -105,7 +109,7 @@ def mul_mat(qtype: int, w: np.ndarray, M: int, K: int, x: np.ndarray, threads: i
     x = np.ascontiguousarray(x, np.float32)
     N = x.shape[0]
     out = np.empty((N, M), np.float32)
-    lib().orc_mul_mat(qtype, w.ctypes.data, M, K, _f32p(x), N, _f32p(out), threads)
+    lib().orc_mul_mat(qtype, w.ctypes.data, M, K, _f32p(x), N, _f32p(out), threads or DEFAULT_THREADS)
     return out
 
 
@@ -119,5 +123,5 @@ def mul_mat_id(qtype: int, w: np.ndarray, M: int, K: int, E: int, x: np.ndarray,
     n_used = ids.shape[1]
     out = np.empty((T, n_used, M), np.float32)
     lib().orc_mul_mat_id(qtype, w.ctypes.data, M, K, E, _f32p(x), ne11,
-                         ids.ctypes.data_as(C.POINTER(C.c_int32)), n_used, T, _f32p(out), threads)
+                         ids.ctypes.data_as(C.POINTER(C.c_int32)), n_used, T, _f32p(out), threads or DEFAULT_THREADS)
     return out

@@ -1,0 +1,266 @@
+"""GPU parity at the BASELINE configs' own sizes, through the default dispatch (no environment
+override of the path choice), against the CPU oracle on the same seeded inputs.
+
+  C1  Q4_0 at Llama-2-7B layer shapes: 4096x4096, 11008x4096, 4096x11008 at N = 1 and 512
+  C2  the 27B-class layer: Q4_K 17408x5120 (gate/up), Q6_K 5120x17408 (down), the Q6_K
+      151936x5120 output head, the Q4_K attention shapes (q 12288x5120, k/v 1024x5120,
+      o 5120x6144) at N = 1, 4 and 512
+  C3  the MoE layer: 512 Q4_K experts, hidden 2048, expert FFN 512, top-10 routing plus one
+      shared expert, T = 1, 4 and 256: gate/up MUL_MAT_ID (src1 ne11 = 1), down MUL_MAT_ID
+      (ne11 = n_used), gate/up + SwiGLU in one call, and the chain router -> gate/up + GLU ->
+      down -> combine with the sigmoid-gated shared expert
+  C4  IQ4_XS and Q8_0 at 14336x4096 and 4096x14336, N = 1, 2, 4, 8
+
+Bar: max relative error <= 1e-3 with the denominator floored at 5 % of the output rms
+(conftest.rel_err); every case also prints the unfloored maximum, how many outputs pass 1e-3
+unfloored and the largest |ref| among them, so the floor's reading is visible per case.
+Each case prints its name before it touches the GPU."""
+import sys
+
+import numpy as np
+import pytest
+
+from arcint_amd import qmm, synth
+from conftest import err_report, rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+def check(got, ref, name):
+    r = err_report(got, ref)
+    print(f"[err] {name}: floored {r['floored']:.3g} unfloored {r['unfloored']:.3g} "
+          f"({r['n_over_1e-3']} of {r['n']} over 1e-3 unfloored, |ref| <= {r['max_abs_ref_over_rms']:.2g} rms there; "
+          f"max |err| {r['max_abs_err_over_rms']:.2g} rms)", flush=True)
+    assert r["floored"] <= TOL, (name, r)
+
+
+@pytest.fixture(scope="module")
+def be():
+    b = qmm.Backend(0)
+    yield b
+    b.close()
+
+
+class Weights:
+    """Device weights of one shape, made once per module and shared by its N cases."""
+
+    def __init__(self, be):
+        self.be = be
+        self.cache = {}
+
+    def get(self, qtype, M, K, seed, ne=None):
+        key = (qtype, M, K, seed, ne)
+        if key not in self.cache:
+            raw = synth.weights(qtype, M, K, seed)
+            t = self.be.new_tensor(qtype, ne or (K, M))
+            self.be.set_tensor(t, raw)
+            self.cache[key] = (raw, t)
+        return self.cache[key]
+
+    def close(self):
+        for _, t in self.cache.values():
+            self.be.free_buffer(t.buf)
+
+
+@pytest.fixture(scope="module")
+def wc(be):
+    w = Weights(be)
+    yield w
+    w.close()
+
+
+def f32(be, arr, bufs):
+    arr = np.ascontiguousarray(arr, np.float32)
+    t = be.new_tensor(qmm.F32, tuple(reversed(arr.shape)))
+    be.set_tensor(t, arr.view(np.uint8).ravel())
+    bufs.append(t.buf)
+    return t
+
+
+def i32(be, arr, bufs):
+    arr = np.ascontiguousarray(arr, np.int32)
+    t = be.new_tensor(qmm.I32, tuple(reversed(arr.shape)))
+    be.set_tensor(t, arr.view(np.uint8).ravel())
+    bufs.append(t.buf)
+    return t
+
+
+def empty(be, ne, bufs):
+    t = be.new_tensor(qmm.F32, ne)
+    bufs.append(t.buf)
+    return t
+
+
+@pytest.fixture
+def bufs(be):
+    out = []
+    yield out
+    for b in out:
+        be.free_buffer(b)
+
+
+def mul_mat_case(be, wc, orc, bufs, qtype, M, K, N, seed):
+    raw, w = wc.get(qtype, M, K, seed)
+    x = synth.activations(N, K, seed + 1000 + N)
+    y = empty(be, (M, N), bufs)
+    be.mul_mat(w, f32(be, x, bufs), y)
+    be.synchronize()
+    path = be.last_path()
+    got = be.get_f32(y).reshape(N, M)
+    ref = orc.mul_mat(qtype, raw, M, K, x)
+    return got, ref, path
+
+
+C1 = [(qmm.Q4_0, 4096, 4096), (qmm.Q4_0, 11008, 4096), (qmm.Q4_0, 4096, 11008)]
+C2 = [(qmm.Q4_K, 17408, 5120), (qmm.Q6_K, 5120, 17408), (qmm.Q6_K, 151936, 5120),
+      (qmm.Q4_K, 12288, 5120), (qmm.Q4_K, 1024, 5120), (qmm.Q4_K, 5120, 6144)]
+C4 = [(qmm.IQ4_XS, 14336, 4096), (qmm.IQ4_XS, 4096, 14336), (qmm.Q8_0, 14336, 4096), (qmm.Q8_0, 4096, 14336)]
+
+
+@pytest.mark.parametrize("qtype,M,K", C1)
+@pytest.mark.parametrize("N", [1, 512])
+def test_c1_llama2_q4_0(be, wc, orc, bufs, qtype, M, K, N):
+    name = f"C1 {synth.NAMES[qtype]} {M}x{K} N={N}"
+    say(name)
+    got, ref, path = mul_mat_case(be, wc, orc, bufs, qtype, M, K, N, seed=7)
+    assert path == ("gemm-mfma" if N == 512 else "gemv"), path
+    check(got, ref, name)
+
+
+@pytest.mark.parametrize("qtype,M,K", C2)
+@pytest.mark.parametrize("N", [1, 4, 512])
+def test_c2_27b_layer(be, wc, orc, bufs, qtype, M, K, N):
+    name = f"C2 {synth.NAMES[qtype]} {M}x{K} N={N}"
+    say(name)
+    got, ref, path = mul_mat_case(be, wc, orc, bufs, qtype, M, K, N, seed=11)
+    assert path == {1: "gemv", 4: "gemv-mfma", 512: "gemm-mfma"}[N], path
+    check(got, ref, name)
+
+
+@pytest.mark.parametrize("qtype,M,K", C4)
+@pytest.mark.parametrize("N", [1, 2, 4, 8])
+def test_c4_iquant_q8_0_decode(be, wc, orc, bufs, qtype, M, K, N):
+    name = f"C4 {synth.NAMES[qtype]} {M}x{K} N={N}"
+    say(name)
+    got, ref, path = mul_mat_case(be, wc, orc, bufs, qtype, M, K, N, seed=13)
+    assert path == ("gemv" if N <= 2 else "gemv-mfma"), path
+    check(got, ref, name)
+
+
+# ------------------------------------------------------------------ C3: the MoE layer
+E, N_USED, HID, FFN = 512, 10, 2048, 512
+
+
+@pytest.fixture(scope="module")
+def moe_w(wc):
+    """gate and up stacks [HID, FFN, E], the down stack [FFN, HID, E], the shared expert's
+    gate / up [HID, FFN] and down [FFN, HID], all Q4_K"""
+    q = qmm.Q4_K
+    return {"gate": wc.get(q, E * FFN, HID, 201, (HID, FFN, E)), "up": wc.get(q, E * FFN, HID, 202, (HID, FFN, E)),
+            "down": wc.get(q, E * HID, FFN, 203, (FFN, HID, E)),
+            "sgate": wc.get(q, FFN, HID, 204), "sup": wc.get(q, FFN, HID, 205), "sdown": wc.get(q, HID, FFN, 206)}
+
+
+def router_ids(T, seed):
+    """top-10 of softmax(N(0, 1)) over 512 experts per token, as the config defines"""
+    return synth.moe_ids(T, E, N_USED, seed)
+
+
+@pytest.mark.parametrize("T", [1, 4, 256])
+def test_c3_gate_up_mul_mat_id(be, orc, bufs, moe_w, T):
+    name = f"C3 gate/up MUL_MAT_ID T={T}"
+    say(name)
+    raw, w = moe_w["gate"]
+    ids = router_ids(T, 300 + T)
+    x = synth.activations(T, HID, 310 + T).reshape(T, 1, HID)
+    y = empty(be, (FFN, N_USED, T), bufs)
+    be.mul_mat_id(w, f32(be, x, bufs), i32(be, ids, bufs), y)
+    be.synchronize()
+    got = be.get_f32(y).reshape(T, N_USED, FFN)
+    check(got, orc.mul_mat_id(qmm.Q4_K, raw, FFN, HID, E, x, ids), name)
+
+
+@pytest.mark.parametrize("T", [1, 4, 256])
+def test_c3_down_mul_mat_id(be, orc, bufs, moe_w, T):
+    """the down projection: src1 [FFN, n_used, T], one activation row per (slot, token)"""
+    name = f"C3 down MUL_MAT_ID T={T}"
+    say(name)
+    raw, w = moe_w["down"]
+    ids = router_ids(T, 320 + T)
+    x = synth.activations(T * N_USED, FFN, 330 + T).reshape(T, N_USED, FFN)
+    y = empty(be, (HID, N_USED, T), bufs)
+    be.mul_mat_id(w, f32(be, x, bufs), i32(be, ids, bufs), y)
+    be.synchronize()
+    got = be.get_f32(y).reshape(T, N_USED, HID)
+    check(got, orc.mul_mat_id(qmm.Q4_K, raw, HID, FFN, E, x, ids), name)
+
+
+@pytest.mark.parametrize("T", [1, 4, 256])
+def test_c3_layer_chain(be, orc, bufs, moe_w, T):
+    """router (softmax, top-10, clamped-sum weights) -> gate/up + SwiGLU (one call) -> down
+    (ne11 = n_used) -> combine with the shared expert (gate/up + SwiGLU, down, sigmoid gate):
+    each stage against the oracle on the GPU's own inputs to it, and the whole chain against
+    the oracle's chain"""
+    from oracle import glu as G
+    from oracle import moe
+    say(f"C3 layer chain T={T}")
+    g = np.random.default_rng(340 + T)
+    logits = g.standard_normal((T, E)).astype(np.float32)
+    x = synth.activations(T, HID, 350 + T)
+    sgl = g.standard_normal((T, 1)).astype(np.float32)          # the shared expert's gate logit
+    rg, wg = moe_w["gate"]
+    ru, wu = moe_w["up"]
+    rd, wd = moe_w["down"]
+    rsg, wsg = moe_w["sgate"]
+    rsu, wsu = moe_w["sup"]
+    rsd, wsd = moe_w["sdown"]
+    lt, xt = f32(be, logits, bufs), f32(be, x.reshape(T, 1, HID), bufs)
+    ids = i32(be, np.zeros((T, N_USED), np.int32), bufs)
+    wts = empty(be, (N_USED, T), bufs)
+    h = empty(be, (FFN, N_USED, T), bufs)
+    ex = empty(be, (HID, N_USED, T), bufs)
+    xs = f32(be, x, bufs)
+    hs = empty(be, (FFN, T), bufs)
+    ys = empty(be, (HID, T), bufs)
+    out = empty(be, (HID, T), bufs)
+    be.moe_topk(lt, ids, wts)
+    be.mul_mat_id_glu(wg, wu, xt, ids, h, qmm.GLU_SWIGLU)
+    hv = qmm.Tensor(h.buf, qmm.F32, (FFN, N_USED, T))            # the GLU output as down's src1
+    be.mul_mat_id(wd, hv, ids, ex)
+    be.mul_mat_glu(wsg, wsu, xs, hs, qmm.GLU_SWIGLU)
+    be.mul_mat(wsd, hs, ys)
+    be.moe_combine(ex, wts, out, ys, f32(be, sgl, bufs))
+    be.synchronize()
+    got_ids = be.get_tensor(ids).view(np.int32).reshape(T, N_USED)
+    got_w = be.get_f32(wts).reshape(T, N_USED)
+    got_h = be.get_f32(h).reshape(T, N_USED, FFN)
+    got_ex = be.get_f32(ex).reshape(T, N_USED, HID)
+    got_hs = be.get_f32(hs).reshape(T, FFN)
+    got_ys = be.get_f32(ys).reshape(T, HID)
+    got = be.get_f32(out).reshape(T, HID)
+    # stage by stage, each on the GPU's inputs to it
+    ref_ids, ref_w = moe.topk(logits, N_USED, 6.103515625e-5, np.inf)
+    assert np.array_equal(got_ids, ref_ids)
+    np.testing.assert_allclose(got_w, ref_w, rtol=2e-6, atol=1e-30)
+    xr = x.reshape(T, 1, HID)
+    ref_h = G.glu(qmm.GLU_SWIGLU, orc.mul_mat_id(qmm.Q4_K, rg, FFN, HID, E, xr, ref_ids),
+                  orc.mul_mat_id(qmm.Q4_K, ru, FFN, HID, E, xr, ref_ids))
+    check(got_h, ref_h, f"C3 T={T} gate/up + SwiGLU")
+    ref_ex = orc.mul_mat_id(qmm.Q4_K, rd, HID, FFN, E, got_h, ref_ids)
+    check(got_ex, ref_ex, f"C3 T={T} down")
+    ref_hs = G.glu(qmm.GLU_SWIGLU, orc.mul_mat(qmm.Q4_K, rsg, FFN, HID, x), orc.mul_mat(qmm.Q4_K, rsu, FFN, HID, x))
+    check(got_hs, ref_hs, f"C3 T={T} shared gate/up + SwiGLU")
+    ref_ys = orc.mul_mat(qmm.Q4_K, rsd, HID, FFN, got_hs)
+    check(got_ys, ref_ys, f"C3 T={T} shared down")
+    check(got, moe.combine(got_ex, got_w, got_ys, sgl[:, 0]), f"C3 T={T} combine")
+    # the whole chain on the oracle's own intermediates
+    ref_ex2 = orc.mul_mat_id(qmm.Q4_K, rd, HID, FFN, E, ref_h.astype(np.float32), ref_ids)
+    ref_ys2 = orc.mul_mat(qmm.Q4_K, rsd, HID, FFN, ref_hs.astype(np.float32))
+    check(got, moe.combine(ref_ex2, ref_w.astype(np.float32), ref_ys2, sgl[:, 0]), f"C3 T={T} layer end to end")

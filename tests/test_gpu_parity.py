@@ -329,6 +329,23 @@ def test_quantize_act_bit_exact(be, sc, orc, act):
     assert np.array_equal(got, ref)
 
 
+def test_quantize_act_exact_ties(be, sc):
+    """exact .5 ties under each quantizer's scale round half to even on the GPU: q8_K with a
+    first max-|x| of -127 (iscale 1), q8_0 with amax 63.5 (multiplier 2, d = fp16 0.5)"""
+    from test_oracle import q8k_tie_block
+    say("quantize_act ties")
+    x, want = q8k_tie_block()
+    b = be.quantize_act(qmm.Q8_K, sc.f32(x[None, :]))
+    assert b[0:4].view(np.float32)[0] == np.float32(1.0)
+    assert np.array_equal(b[4:260].view(np.int8), want)
+    # q8_0: values k / 2 + 1 / 4 scale by 2 to k + 1 / 2
+    k = np.arange(31) - 15
+    x0 = np.concatenate([[63.5], k / 2.0 + 0.25]).astype(np.float32)
+    b0 = be.quantize_act(qmm.Q8_0, sc.f32(x0[None, :]))
+    assert b0[0:2].view(np.float16)[0] == np.float16(0.5)
+    assert np.array_equal(b0[2:34].view(np.int8), np.concatenate([[127], np.where(k % 2 == 0, k, k + 1)]).astype(np.int8))
+
+
 # ------------------------------------------------------------------ MUL_MAT
 def run_mul_mat(be, sc, orc, qtype, M, K, N, seed):
     raw = synth.weights(qtype, M, K, seed)

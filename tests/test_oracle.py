@@ -302,6 +302,25 @@ def test_q8_K_sign_of_first_max_and_bsums(orc):
     assert not z.any()
 
 
+def q8k_tie_block():
+    """A q8_K block whose first max-|x| element is -127, so iscale = -127 / -127 = 1 exactly
+    and every other element n + 1/2 (n in [-100, 99]) lands on an exact tie; with the codes
+    round-half-even gives: n when n is even, n + 1 when n is odd (half away from zero would
+    give n + 1 for n >= 0 and n for n < 0)."""
+    n = (np.arange(255) % 200) - 100
+    x = np.concatenate([[-127.0], n + 0.5]).astype(np.float32)
+    want = np.concatenate([[-127], np.where(n % 2 == 0, n, n + 1)]).astype(np.int8)
+    return x, want
+
+
+def test_q8_K_exact_ties_round_half_even(orc):
+    x, want = q8k_tie_block()
+    d, qs, bs = _q8k_fields(orc.quantize_q8_K(x))
+    assert d == np.float32(1.0)
+    assert np.array_equal(qs, want)
+    assert np.array_equal(bs, want.astype(np.int32).reshape(16, 16).sum(1))
+
+
 # ---------------------------------------------------------------- dots
 def _deq_q8(qtype, xq, k):
     """dequantized activations (q * d) in fp64 from the block bytes"""
