@@ -9,10 +9,13 @@
 // The expert counts are scanned in parallel (a wave scan by shuffles, then the
 // 16 wave totals): a serial scan by one thread over 512 experts took 24 us.
 // Pair (slot i, token t) reads activation column (i % ne11) + t * ne11 and
-// writes dst + t * nb2 + i * nb1 (P01:3916-3922); a negative or out-of-range
-// id writes a zero row (P02:98-103): such pairs go to one more bucket whose
-// tasks (mat = -1) the GEMV turns into zero rows, so the route writes no dst
-// and one route serves every product that shares the ids.
+// writes dst + t * nb2 + i * nb1 (P01:3916-3922).  A negative id writes a zero
+// row (the reference's expert-cache rule, P02:98-103); an id at or past n_as,
+// which ggml-cpu asserts on (P02:105), also writes a zero row - nothing reads
+// outside the stack - and sets the context's error flag, which
+// qmm_synchronize reports.  Such pairs go to one more bucket whose tasks
+// (mat = -1) the GEMV turns into zero rows, so the route writes no dst and one
+// route serves every product that shares the ids.
 #include "qmm_device.h"
 
 namespace qmm {
@@ -35,6 +38,7 @@ __device__ __forceinline__ void route_body(const RouteArgs & r, int32_t * __rest
         const int64_t t = p / r.n_used, i = p % r.n_used;
         const int32_t e = *reinterpret_cast<const int32_t *>(reinterpret_cast<const char *>(r.ids) + t * r.ids_nb1 + i * r.ids_nb0);
         const int32_t b = (e >= 0 && e < r.n_as) ? e : (int32_t)r.n_as;
+        if (e >= r.n_as) *r.bad_id = 1;
         atomicAdd(&cnt[b], 1);
         scratch[p] = b;
     }
@@ -123,14 +127,41 @@ __global__ __launch_bounds__(kRouteThreads) void k_quant_route(F32Cols src, int6
     else quant_q8_K_at(src, K, ncols, a, t);
 }
 
-// ---- the router: softmax -> top-k -> normalized weights, one wave per token ----------
-// Role of the reference's kernel_topk_moe_softmax_norm (P09:899-1000), which replaces
-// llama.cpp's gating chain SOFT_MAX, ARGSORT (desc), VIEW, GET_ROWS, SUM_ROWS, CLAMP, DIV
-// (matched at P02:786-821).  Lane l holds the logits of experts l + 64 j, j < NPER.  The max
-// and the sum of exp(x - max) are wave reductions; each of the k rounds picks the largest
-// unselected exp(x - max) over the wave (ties: the lower expert) by DPP reductions.  The
-// weights are the picked exp(x - max) / sum, divided by their own sum clamped to [cmin, cmax].
-constexpr int kTopkWaves = 4;                   // tokens per work-group
+// ---- the router: softmax -> top-k -> normalized weights ------------------------------------
+// Role of the reference's fused router (kernel_topk_moe_softmax_norm, P09:899-1000), which
+// replaces llama.cpp's gating chain SOFT_MAX, ARGSORT (desc), VIEW, GET_ROWS, SUM_ROWS, CLAMP,
+// DIV (matched at P02:786-821); the selection here is a threshold search, not repeated arg-max
+// rounds.  One wave per token (a one-wave work-group); lane l holds the logits of the NPER
+// consecutive experts [l NPER, (l + 1) NPER).  Softmax is monotone, so the winners are the k
+// largest logits, equal logits ordered by expert (the order of the probabilities, which the
+// float32 exp could otherwise merge into ties):
+//  1. each logit becomes an order-preserving 32-bit key; padding lanes get key 0, below every
+//     real key;
+//  2. the k-th largest key tau is found most-significant bit first: 32 steps, each counting the
+//     keys at or above a candidate with one ballot per register (the count is uniform);
+//  3. every key above tau wins, and of the keys equal to tau the lowest experts, counted in
+//     expert order by an exclusive scan of the lanes' tie counts, until there are k;
+//  4. the k winners go to LDS at the offsets of a scan of the lanes' win counts, and each of
+//     the first k lanes counts the winners ahead of its own (larger key, or equal key and lower
+//     expert): its rank in the output.
+// Weights: exp(x - max) / sum over all experts (a wave sum), divided by the winners' sum, taken
+// in rank order and clamped to [cmin, cmax].
+
+// a float's bits as an unsigned key with the float's order (-0 as +0: equal floats, equal keys)
+__device__ __forceinline__ uint32_t order_key(float x) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, x == 0.0f ? 0.0f : x);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// the sum over lanes 0 .. lane of v (inclusive), by shuffles
+__device__ __forceinline__ int lane_scan(int v, int lane) {
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int u = __shfl_up(v, d, 64);
+        if (lane >= d) v += u;
+    }
+    return v;
+}
 
 __device__ __forceinline__ float wave_sum_f(float v) {
 #pragma unroll
@@ -138,59 +169,88 @@ __device__ __forceinline__ float wave_sum_f(float v) {
     return v;
 }
 
+// number of register values of the wave with pred true (uniform)
+template <int NPER, typename F>
+__device__ __forceinline__ int wave_count(F pred) {
+    int c = 0;
+#pragma unroll
+    for (int j = 0; j < NPER; ++j) c += __popcll(__ballot(pred(j)));
+    return c;
+}
+
 template <int NPER>
-__global__ __launch_bounds__(64 * kTopkWaves) void k_topk(TopkArgs a) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int64_t t = (int64_t)blockIdx.x * kTopkWaves + wave;
-    if (t >= a.n_tok) return;                                     // whole waves
+__global__ __launch_bounds__(64) void k_topk(TopkArgs a) {
+    __shared__ uint32_t win_key[32];
+    __shared__ int win_exp[32];
+    __shared__ float win_p[32], ranked_p[32];
+    const int lane = threadIdx.x;
+    const int64_t t = blockIdx.x;
     const float * x = reinterpret_cast<const float *>(a.logits + t * a.nbl1);
-    float p[NPER];
-    float m = -INFINITY;
+    const int e0 = lane * NPER, k = a.k;
+    float v[NPER];
+    uint32_t key[NPER];
+    float mx = -INFINITY;
 #pragma unroll
     for (int j = 0; j < NPER; ++j) {
-        const int i = lane + 64 * j;
-        p[j] = i < a.n_expert ? x[i] : -INFINITY;
-        m = fmaxf(m, p[j]);
+        const bool live = e0 + j < a.n_expert;
+        v[j] = live ? x[e0 + j] : -INFINITY;
+        key[j] = live ? order_key(v[j]) : 0u;
+        mx = fmaxf(mx, v[j]);
     }
-    m = wave_max(m);
-    float sl = 0.0f;
+    const float m = wave_max(mx);
+    float part = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NPER; ++j)
+        if (e0 + j < a.n_expert) part += expf(v[j] - m);
+    const float S = wave_sum_f(part);
+    // 2. tau: the largest key with at least k keys at or above it
+    uint32_t tau = 0;
+    for (int b = 31; b >= 0; --b) {
+        const uint32_t cand = tau | (1u << b);
+        if (wave_count<NPER>([&](int j) { return key[j] >= cand; }) >= k) tau = cand;
+    }
+    // 3. winners: keys above tau, then ties at tau in expert order
+    const int need = k - wave_count<NPER>([&](int j) { return key[j] > tau; });   // >= 1
+    int ties = 0;
+#pragma unroll
+    for (int j = 0; j < NPER; ++j) ties += key[j] == tau;
+    int tie_rank = lane_scan(ties, lane) - ties;                  // ties at lower experts
+    bool win[NPER];
+    int nwin = 0;
 #pragma unroll
     for (int j = 0; j < NPER; ++j) {
-        const int i = lane + 64 * j;
-        p[j] = i < a.n_expert ? expf(p[j] - m) : -1.0f;          // -1: no expert (never picked)
-        if (i < a.n_expert) sl += p[j];
+        win[j] = key[j] > tau;
+        if (key[j] == tau) win[j] = tie_rank++ < need;
+        nwin += win[j];
     }
-    const float s = wave_sum_f(sl);
-    uint32_t sel = 0;                                             // bit j: p[j] picked
-    float wsum = 0.0f, my_w = 0.0f;
-    int my_id = 0;
-    for (int r = 0; r < a.k; ++r) {                               // uniform
-        float bv = -1.0f;
-        int bi = 0x7fffffff;
+    // 4. compaction into LDS, then each winner's rank
+    int slot = lane_scan(nwin, lane) - nwin;
 #pragma unroll
-        for (int j = 0; j < NPER; ++j) {
-            if (!(sel >> j & 1u) && p[j] > bv) {                  // j ascending: ties keep the lower expert
-                bv = p[j];
-                bi = lane + 64 * j;
-            }
+    for (int j = 0; j < NPER; ++j) {
+        if (win[j]) {
+            win_key[slot] = key[j];
+            win_exp[slot] = e0 + j;
+            win_p[slot] = expf(v[j] - m) / S;
+            ++slot;
         }
-        // the wave's largest value (DPP row reductions, four readlanes), then the lowest expert
-        // among the lanes holding it
-        const float gv = wave_max(bv);
-        bi = wave_min_i(bv == gv ? bi : 0x7fffffff);
-        bv = gv;
-        const float wr = bv / s;
-        wsum += wr;
-        if (lane == r) {
-            my_w = wr;
-            my_id = bi;
-        }
-        if ((bi & 63) == lane && bi < a.n_expert) sel |= 1u << (bi >> 6);
     }
-    if (lane < a.k) {
+    __syncthreads();
+    int rank = 0, my_exp = 0;
+    float my_p = 0.0f;
+    if (lane < k) {
+        const uint32_t ku = win_key[lane];
+        my_exp = win_exp[lane];
+        my_p = win_p[lane];
+        for (int i = 0; i < k; ++i) rank += win_key[i] > ku || (win_key[i] == ku && win_exp[i] < my_exp);
+        ranked_p[rank] = my_p;
+    }
+    __syncthreads();
+    float wsum = 0.0f;
+    for (int i = 0; i < k; ++i) wsum += ranked_p[i];              // uniform, in rank order
+    if (lane < k) {
         const float c = fminf(fmaxf(wsum, a.cmin), a.cmax);
-        reinterpret_cast<int32_t *>(a.ids + t * a.nbi1)[lane] = my_id;
-        reinterpret_cast<float *>(a.w + t * a.nbw1)[lane] = my_w / c;
+        reinterpret_cast<int32_t *>(a.ids + t * a.nbi1)[rank] = my_exp;
+        reinterpret_cast<float *>(a.w + t * a.nbw1)[rank] = my_p / c;
     }
 }
 
@@ -218,7 +278,8 @@ __global__ __launch_bounds__(256) void k_combine(CombineArgs a) {
 
 hipError_t launch_topk(const TopkArgs & a, hipStream_t s) {
     if (a.n_expert < 1 || a.n_expert > 1024 || a.k < 1 || a.k > 32 || a.k > a.n_expert || a.n_tok < 1) return hipErrorInvalidValue;
-    const dim3 g((unsigned)((a.n_tok + kTopkWaves - 1) / kTopkWaves)), b(64 * kTopkWaves);
+    if (a.n_tok > 0x7fffffff) return hipErrorInvalidValue;
+    const dim3 g((unsigned)a.n_tok), b(64);                       // one wave per token
     const int nper = (a.n_expert + 63) / 64;
     if (nper <= 1) k_topk<1><<<g, b, 0, s>>>(a);
     else if (nper <= 2) k_topk<2><<<g, b, 0, s>>>(a);

@@ -24,6 +24,8 @@ struct qmm_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
     void * sink = nullptr;           // kSinkBytes of zeros the GEMV reads past the end of its pipeline
+    int32_t * dflags = nullptr;      // device error flags: [0] an id >= n_as was routed
+    int32_t * hflags = nullptr;      // pinned host copy, read by qmm_synchronize
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     std::string err;
     std::string path = "none";
@@ -57,9 +59,16 @@ struct qmm_ctx {
     } rkey;
     size_t glu_cap = 0;
     void * glu = nullptr;            // gate/up sums of qmm_mul_mat_glu
-    // downgrade counter (paths slower than the type promises)
-    int64_t downgrades = 0;
-    std::string downgrade_names;
+    // downgrades: ops that took a slower path than their weight type promises, counted per key
+    // in fixed storage (recording one allocates nothing); keys past the table count as "other"
+    struct Downgrade {
+        char key[112];
+        int64_t count;
+    };
+    static constexpr int kMaxDowngradeKeys = 48;
+    Downgrade dg[kMaxDowngradeKeys];
+    int n_dg = 0;
+    int64_t dg_other = 0;
     // main-kernel timing (qmm_kernel_timing)
     bool ktime = false;
     std::vector<hipEvent_t> kev;   // pairs
@@ -248,13 +257,20 @@ struct PendingRoute {
 
 // quantize src1 for the vec_dot type of `type` (skipped when this graph already did); with
 // pr, the route runs in the same launch (or alone when the quantization is skipped)
+// Device memory the activations go to instead of the context's scratch: nothing is allocated
+// and the graph's activation cache is neither read nor written.
+struct FixedAct {
+    uint8_t * base;
+    size_t cap;
+};
+
 int quantize_src1(qmm_ctx * ctx, int type, const qmm_tensor * src1, bool dT, ActBuf * out, const ZeroJob * z = nullptr,
-                  const PendingRoute * pr = nullptr) {
+                  const PendingRoute * pr = nullptr, const FixedAct * fixed = nullptr) {
     const int vdt = vec_dot_type(type);
     const int64_t K = src1->ne[0], ncols = src1->ne[1] * src1->ne[2] * src1->ne[3];
     auto & k = ctx->key;
     if (pr && z) return fail(ctx, QMM_ERR_INVALID, "internal: a route launch with dst zeroing");
-    if (ctx->in_graph && same_key(ctx, vdt, src1, dT)) {
+    if (!fixed && ctx->in_graph && same_key(ctx, vdt, src1, dT)) {
         *out = ctx->cached;
         if (z) QMM_HIP(ctx, launch_quantize(f32_cols(src1), K, 0, ctx->cached, z, ctx->stream));   // zeroing only
         if (pr) QMM_HIP(ctx, launch_route(pr->r, pr->scratch, pr->tasks, pr->ntasks, ctx->stream));
@@ -264,9 +280,14 @@ int quantize_src1(qmm_ctx * ctx, int type, const qmm_tensor * src1, bool dT, Act
     const int64_t ldk = (K + 255) / 256 * 256;
     const int64_t ldT = (ncols + 3) / 4 * 4 + 64;    // the GEMM reads up to 63 columns past the last
     const size_t need = act_bytes(vdt, ldk, ncols, dT, ldT, &od, &os, &ot, &ob);
-    int rc = ensure(ctx, &ctx->act, &ctx->act_cap, need);
-    if (rc) return rc;
-    uint8_t * b = (uint8_t *)ctx->act;
+    if (fixed && need > fixed->cap)
+        return fail(ctx, QMM_ERR_NOMEM, "the activations of src1 [%lld, %lld] need %zu bytes of scratch; at most %zu",
+                    (long long)K, (long long)ncols, need, fixed->cap);
+    if (!fixed) {
+        const int rc = ensure(ctx, &ctx->act, &ctx->act_cap, need);
+        if (rc) return rc;
+    }
+    uint8_t * b = fixed ? fixed->base : (uint8_t *)ctx->act;
     ActBuf a;
     a.codes = (int8_t *)b;
     a.d = (float *)(b + od);
@@ -280,6 +301,8 @@ int quantize_src1(qmm_ctx * ctx, int type, const qmm_tensor * src1, bool dT, Act
     a.vdt = vdt;
     if (pr) QMM_HIP(ctx, launch_quant_route(f32_cols(src1), K, ncols, a, pr->r, pr->scratch, pr->tasks, pr->ntasks, ctx->stream));
     else QMM_HIP(ctx, launch_quantize(f32_cols(src1), K, ncols, a, z, ctx->stream));
+    *out = a;
+    if (fixed) return QMM_OK;
     k.buf = src1->buffer;
     k.offs = src1->offs;
     memcpy(k.ne, src1->ne, sizeof(k.ne));
@@ -289,7 +312,6 @@ int quantize_src1(qmm_ctx * ctx, int type, const qmm_tensor * src1, bool dT, Act
     k.gen = ctx->graph_gen;
     k.valid = true;
     ctx->cached = a;
-    *out = a;
     return QMM_OK;
 }
 
@@ -328,9 +350,47 @@ int ktime_pair(qmm_ctx * ctx, KTime * kt, const KTime ** out) {
     return QMM_OK;
 }
 
-void note_downgrade(qmm_ctx * ctx, const char * key) {
-    ctx->downgrades++;
-    ctx->downgrade_names = key;
+const char * type_name(int type) {
+    switch (type) {
+        case QMM_TYPE_Q4_0: return "Q4_0";
+        case QMM_TYPE_Q8_0: return "Q8_0";
+        case QMM_TYPE_Q4_K: return "Q4_K";
+        case QMM_TYPE_Q5_K: return "Q5_K";
+        case QMM_TYPE_Q6_K: return "Q6_K";
+        case QMM_TYPE_IQ4_NL: return "IQ4_NL";
+        case QMM_TYPE_IQ4_XS: return "IQ4_XS";
+        case QMM_TYPE_F32: return "F32";
+        case QMM_TYPE_F16: return "F16";
+        default: return "?";
+    }
+}
+
+// column counts in the buckets the downgrade keys use (a key holds no per-request value)
+const char * cols_bucket(int64_t n) {
+    return n <= 1 ? "1" : n <= 8 ? "2-8" : n <= 16 ? "9-16" : n <= 32 ? "17-32" : n <= 128 ? "33-128" : "129+";
+}
+
+// one downgrade under a key (the reference's ggml_cl_downgrade, 0100-...patch:44-66): counted per
+// key; the first of a key is logged to stderr when QMM_DOWNGRADE_LOG is set
+void note_downgrade(qmm_ctx * ctx, const char * fmt, ...) {
+    char key[sizeof(ctx->dg[0].key)];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(key, sizeof(key), fmt, ap);
+    va_end(ap);
+    for (int i = 0; i < ctx->n_dg; ++i) {
+        if (!strcmp(ctx->dg[i].key, key)) {
+            ctx->dg[i].count++;
+            return;
+        }
+    }
+    if (ctx->n_dg == qmm_ctx::kMaxDowngradeKeys) {
+        ctx->dg_other++;
+        return;
+    }
+    memcpy(ctx->dg[ctx->n_dg].key, key, sizeof(key));
+    ctx->dg[ctx->n_dg++].count = 1;
+    if (getenv("QMM_DOWNGRADE_LOG")) fprintf(stderr, "DOWNGRADE src=qmm %s\n", key);
 }
 
 }  // namespace
@@ -348,6 +408,8 @@ int qmm_ctx_create(int device, qmm_ctx ** out) {
     if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess ||
         hipEventCreate(&ctx->ev0) != hipSuccess || hipEventCreate(&ctx->ev1) != hipSuccess ||
         hipMalloc(&ctx->sink, kSinkBytes) != hipSuccess || hipMemsetAsync(ctx->sink, 0, kSinkBytes, ctx->stream) != hipSuccess ||
+        hipMalloc(&ctx->dflags, 256) != hipSuccess || hipMemsetAsync(ctx->dflags, 0, 256, ctx->stream) != hipSuccess ||
+        hipHostMalloc(&ctx->hflags, 256, hipHostMallocDefault) != hipSuccess ||
         hipStreamSynchronize(ctx->stream) != hipSuccess) {
         qmm_ctx_free(ctx);
         return QMM_ERR_DEVICE;
@@ -365,6 +427,8 @@ void qmm_ctx_free(qmm_ctx * ctx) {
     if (ctx->route) (void)hipFree(ctx->route);
     if (ctx->glu) (void)hipFree(ctx->glu);
     if (ctx->sink) (void)hipFree(ctx->sink);
+    if (ctx->dflags) (void)hipFree(ctx->dflags);
+    if (ctx->hflags) (void)hipHostFree(ctx->hflags);
     for (hipEvent_t e : ctx->kev) (void)hipEventDestroy(e);
     if (ctx->ev0) (void)hipEventDestroy(ctx->ev0);
     if (ctx->ev1) (void)hipEventDestroy(ctx->ev1);
@@ -691,13 +755,11 @@ int qmm_describe_mul_mat(const qmm_tensor * src0, const qmm_tensor * src1, const
     return QMM_OK;
 }
 
-int qmm_mul_mat(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1, const qmm_tensor * dst) {
-    if (!ctx) return QMM_ERR_INVALID;
-    char reason[160];
-    WView w;
-    if (!mul_mat_ok(src0, src1, dst, true, &w, reason, sizeof(reason)))
-        return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat: %s", reason);
-    QMM_HIP(ctx, hipSetDevice(ctx->device));
+// The MUL_MAT after validation: the activation pre-pass, then the GEMV or the GEMM.  With
+// `fixed` the activations go to that memory (nothing is allocated, no graph dedup, no kernel
+// timing events); otherwise to the context's scratch.
+static int mul_mat_launch(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1, const qmm_tensor * dst,
+                          const WView & w, const FixedAct * fixed) {
     const int64_t N = src1->ne[1];
     const bool use_gemm = N >= gemm_min_cols(src0->type);
     ActBuf a{};
@@ -713,13 +775,15 @@ int qmm_mul_mat(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1,
     dn.d_nb1 = (int64_t)(dst->nb[1] / 4);
     dn.d_nb2 = (int64_t)(dst->nb[2] / 4);
     dn.d_nb3 = (int64_t)(dst->nb[3] / 4);
+    KTime kt;
+    const KTime * ktp = nullptr;
     if (use_gemm) {
         const int64_t nbatch = dn.ne12 * dn.ne13;
         // K slices add into dst rows from zero_from on (the pre-pass zeroes them)
         const int64_t zero_from = gemm_zero_from(src0->type, w, N, nbatch);
         ZeroJob z{ d, w.M, N * nbatch, N, dn.ne12, dn.d_nb1, dn.d_nb2, dn.d_nb3, zero_from };
         const bool split = zero_from < w.M;
-        if ((rc = quantize_src1(ctx, src0->type, src1, true, &a, split ? &z : nullptr))) return rc;
+        if ((rc = quantize_src1(ctx, src0->type, src1, true, &a, split ? &z : nullptr, nullptr, fixed))) return rc;
         GemmBatch bt;
         bt.ne12 = dn.ne12;
         bt.r2 = dn.r2;
@@ -729,9 +793,7 @@ int qmm_mul_mat(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1,
         bt.d_nb2 = dn.d_nb2;
         bt.d_nb3 = dn.d_nb3;
         ctx->path = "gemm-mfma";
-        KTime kt;
-        const KTime * ktp;
-        if ((rc = ktime_pair(ctx, &kt, &ktp))) return rc;
+        if (!fixed && (rc = ktime_pair(ctx, &kt, &ktp))) return rc;
         QMM_HIP(ctx, launch_gemm(src0->type, w, a, N, dn.ne12 * dn.ne13, bt, d, ctx->stream, ktp));
         return QMM_OK;
     }
@@ -739,17 +801,31 @@ int qmm_mul_mat(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1,
     const int nc = gemv_task_cols(src0->type, N);
     const int64_t ntasks = (N + nc - 1) / nc * dn.ne12 * dn.ne13;
     GemvPlan plan;
-    if (!gemv_plan(src0->type, w, nc, ntasks, true, nc >= gemv_mma_min_cols(), &plan))
+    const bool want_mma = nc >= gemv_mma_min_cols();
+    if (!gemv_plan(src0->type, w, nc, ntasks, true, want_mma, &plan))
         return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat: GEMV shape out of range");
     ZeroJob z{ d, w.M, N * dn.ne12 * dn.ne13, N, dn.ne12, dn.d_nb1, dn.d_nb2, dn.d_nb3 };
-    if ((rc = quantize_src1(ctx, src0->type, src1, false, &a, plan.KS > 1 ? &z : nullptr))) return rc;
+    if ((rc = quantize_src1(ctx, src0->type, src1, false, &a, plan.KS > 1 ? &z : nullptr, nullptr, fixed))) return rc;
     ctx->path = plan.mma ? "gemv-mfma" : "gemv";
-    if (N > nc) note_downgrade(ctx, "mul_mat: many columns on the GEMV");
-    KTime kt;
-    const KTime * ktp;
-    if ((rc = ktime_pair(ctx, &kt, &ktp))) return rc;
+    if (N > nc)
+        note_downgrade(ctx, "op=MUL_MAT type=%s k=%lld cols=%s path=%s reason=several-weight-passes", type_name(src0->type),
+                       (long long)w.K, cols_bucket(N), plan.mma ? "gemv-mfma" : "gemv");
+    if (want_mma && !plan.mma)
+        note_downgrade(ctx, "op=MUL_MAT type=%s k=%lld cols=%s path=gemv reason=no-mfma-gemv", type_name(src0->type),
+                       (long long)w.K, cols_bucket(N));
+    if (!fixed && (rc = ktime_pair(ctx, &kt, &ktp))) return rc;
     QMM_HIP(ctx, launch_gemv(src0->type, w, plan, a, nullptr, nullptr, &dn, d, ctx->sink, ctx->stream, ktp));
     return QMM_OK;
+}
+
+int qmm_mul_mat(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1, const qmm_tensor * dst) {
+    if (!ctx) return QMM_ERR_INVALID;
+    char reason[160];
+    WView w;
+    if (!mul_mat_ok(src0, src1, dst, true, &w, reason, sizeof(reason)))
+        return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat: %s", reason);
+    QMM_HIP(ctx, hipSetDevice(ctx->device));
+    return mul_mat_launch(ctx, src0, src1, dst, w, nullptr);
 }
 
 // The expert tasks of ids into the route scratch (reused inside a graph when ids, ne11, the
@@ -784,6 +860,7 @@ static int route_tasks(qmm_ctx * ctx, const qmm_tensor * ids, int64_t ne11, int6
     r.n_as = n_as;
     r.dst_nb1 = dnb1;
     r.dst_nb2 = dnb2;
+    r.bad_id = ctx->dflags;
     if (defer) {
         *defer = PendingRoute{ r, (int32_t *)rb, *tasks, *ntasks };
         *pending = true;
@@ -1196,16 +1273,38 @@ int qmm_quantize_act(qmm_ctx * ctx, int32_t act_type, const qmm_tensor * src, vo
     return QMM_OK;
 }
 
+// Waits for the stream, then reports what the kernels flagged since the last call: MUL_MAT_ID
+// ids at or past n_as (their rows were written as zeros; ggml-cpu asserts on them, P02:105).
 int qmm_synchronize(qmm_ctx * ctx) {
     if (!ctx) return QMM_ERR_INVALID;
+    QMM_HIP(ctx, hipMemcpyAsync(ctx->hflags, ctx->dflags, sizeof(int32_t), hipMemcpyDeviceToHost, ctx->stream));
     QMM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (ctx->hflags[0]) {
+        ctx->hflags[0] = 0;
+        QMM_HIP(ctx, hipMemsetAsync(ctx->dflags, 0, sizeof(int32_t), ctx->stream));
+        QMM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        return fail(ctx, QMM_ERR_INVALID, "mul_mat_id: ids at or past the expert count were routed (their rows were "
+                                          "written as zeros; ggml-cpu asserts on such ids)");
+    }
     return QMM_OK;
 }
 
 int64_t qmm_downgrades(qmm_ctx * ctx, char * buf, size_t buf_len) {
     if (!ctx) return -1;
-    if (buf && buf_len) snprintf(buf, buf_len, "%s", ctx->downgrade_names.c_str());
-    return ctx->downgrades;
+    int64_t total = ctx->dg_other;
+    size_t at = 0;
+    if (buf && buf_len) buf[0] = 0;
+    auto line = [&](const char * key, int64_t n) {
+        if (!buf || at + 1 >= buf_len) return;
+        const int w = snprintf(buf + at, buf_len - at, "src=qmm %s\t%lld\n", key, (long long)n);
+        if (w > 0) at = std::min(buf_len - 1, at + (size_t)w);
+    };
+    for (int i = 0; i < ctx->n_dg; ++i) {
+        line(ctx->dg[i].key, ctx->dg[i].count);
+        total += ctx->dg[i].count;
+    }
+    if (ctx->dg_other) line("other", ctx->dg_other);
+    return total;
 }
 
 int qmm_kernel_timing(qmm_ctx * ctx, int enable) {

@@ -157,17 +157,6 @@ __device__ __forceinline__ float wave_max(float v) {
     const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
     return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
-// min over the whole wave (ints), uniform result, the same way
-__device__ __forceinline__ int wave_min_i(int v) {
-    v = min(v, dpp_i<0xB1>(v));
-    v = min(v, dpp_i<0x4E>(v));
-    v = min(v, dpp_i<0x141>(v));
-    v = min(v, dpp_i<0x140>(v));
-    const int r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
-    const int r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
-    return min(min(r0, r1), min(r2, r3));
-}
-
 // q8_0 over 8 lanes (4 values each) of one 32-weight block; lane-group
 // aligned (lanes 8g..8g+7), all 64 lanes active.  Returns this lane's four
 // codes packed; *d and *s (block scale, block code sum) are valid in every

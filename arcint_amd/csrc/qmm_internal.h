@@ -269,6 +269,7 @@ struct RouteArgs {
     size_t ids_nb0, ids_nb1;
     int64_t n_used, T, ne11, n_as;
     int64_t dst_nb1, dst_nb2;   // float strides of dst dims 1 and 2
+    int32_t * bad_id;           // set to 1 (a plain store) when an id is >= n_as
 };
 // MoE router: for each token t (logits column, n_expert <= 1024 floats at logits + t nbl1),
 // ids [k] (i32 at ids + t nbi1) and weights [k] (f32 at w + t nbw1), k <= 32

@@ -1,31 +1,37 @@
 """GGUF reader: the header, metadata and tensor table of a (possibly split) GGUF file, tensor
 bytes read through a memory map, and a loader that streams a tensor into a libqmm buffer.
 
-Format as the reference reads it (tools/mtp_fit.py:270-335, read_gguf_header /
-find_gguf_tensor): "GGUF", version (>= 2), tensor count and metadata count (u64), the
-metadata as (string key, u32 type, value) with strings as u64 length + UTF-8 bytes and
-arrays as (u32 element type, u64 count, elements); then per tensor its name, u32 dimension
-count, u64 dims (ne0 first), u32 ggml type and u64 offset relative to the data section,
-which starts at the next multiple of `general.alignment` (32 by default).  A split model
-(`name-00001-of-0000N.gguf`) keeps each tensor in one of its shards.
+The GGUF container (version 2 and 3, little-endian), as llama.cpp's gguf writer lays it out:
 
-The loader hands GGUF block bytes to qmm_tensor_set in chunks of whole blocks (the library
-repacks them into its device image); bytes never pass through a whole-file copy in host
-memory.
+    "GGUF" | u32 version | u64 tensor count | u64 metadata count
+    metadata:     string key | u32 value type | value
+    tensor infos: string name | u32 n_dims | u64 ne[n_dims] (ne0 first) | u32 ggml type |
+                  u64 offset into the data section
+    data section: starts at the first multiple of general.alignment (default 32) past the
+                  tensor infos; every tensor offset is a multiple of it
+
+A string is a u64 byte count and UTF-8 bytes; an array value is a u32 element type, a u64
+count and the elements.  The reference reads the same container (tools/mtp_fit.py:270-335).
+A model split by llama.cpp's gguf-split is named <prefix>-00001-of-0000N.gguf ... -0000N-of-
+0000N.gguf; every shard holds its own header and tensors and carries split.count and split.no.
+
+The whole file is mapped, never read: the header is decoded from the map at a moving offset,
+and a tensor's bytes are copied out of the map only for the range asked for.  The loader hands
+GGUF block bytes to qmm_tensor_set in chunks of whole blocks (the library repacks them into its
+device image).
 """
 from __future__ import annotations
 
 import os
-import re
-import struct
 from dataclasses import dataclass, field
 
 import numpy as np
 
 GGUF_MAGIC = b"GGUF"
-# metadata value types
-_FIXED = {0: "<B", 1: "<b", 2: "<H", 3: "<h", 4: "<I", 5: "<i", 6: "<f", 7: "<?", 10: "<Q", 11: "<q", 12: "<d"}
-T_STRING, T_ARRAY = 8, 9
+# metadata value type -> numpy dtype (little-endian); 8 is a string, 9 an array
+_VALUE_DTYPES = {0: "<u1", 1: "<i1", 2: "<u2", 3: "<i2", 4: "<u4", 5: "<i4", 6: "<f4", 7: "?",
+                 10: "<u8", 11: "<i8", 12: "<f8"}
+VT_STRING, VT_ARRAY = 8, 9
 
 # ggml types: (elements per block, bytes per block) for the types a GGUF file of this path holds
 GGML_TYPES = {
@@ -55,7 +61,7 @@ class GGUFTensor:
     ne: tuple            # ne0 first, as ggml
     type: int
     offset: int          # absolute byte offset in its file
-    nbytes: int
+    nbytes: int          # -1 for a ggml type this reader does not size
     path: str
 
 
@@ -78,10 +84,13 @@ class GGUF:
         size = t.nbytes - start if size is None else size
         if start < 0 or size < 0 or start + size > t.nbytes:
             raise GGUFError(f"{name}: range [{start}, {start + size}) outside its {t.nbytes} bytes")
-        mm = np.memmap(t.path, dtype=np.uint8, mode="r", offset=t.offset + start, shape=(size,)) if size else None
-        out = np.array(mm, copy=True) if size else np.zeros(0, np.uint8)
-        del mm
-        return out
+        if size == 0:
+            return np.zeros(0, np.uint8)
+        view = np.memmap(t.path, dtype=np.uint8, mode="r", offset=t.offset + start, shape=(size,))
+        try:
+            return np.array(view)
+        finally:
+            del view
 
 
 def tensor_nbytes(ggml_type: int, ne) -> int:
@@ -90,104 +99,124 @@ def tensor_nbytes(ggml_type: int, ne) -> int:
     blck, bb = GGML_TYPES[ggml_type]
     if ne[0] % blck:
         raise GGUFError(f"ne0 = {ne[0]} is not a whole number of {blck}-element blocks")
-    n = ne[0] // blck
-    for d in ne[1:]:
-        n *= d
-    return int(n * bb)
+    return int(np.prod(ne, dtype=np.int64)) // blck * bb
 
 
-class _Reader:
-    def __init__(self, f):
-        self.f = f
+class _Cursor:
+    """Little-endian GGUF fields decoded from a mapped file at a moving byte offset."""
 
-    def take(self, n: int) -> bytes:
-        b = self.f.read(n)
-        if len(b) != n:
-            raise GGUFError("truncated GGUF file")
-        return b
+    def __init__(self, buf: np.ndarray, path: str):
+        self.buf, self.at, self.path = buf, 0, path
 
-    def u32(self) -> int:
-        return struct.unpack("<I", self.take(4))[0]
+    def _span(self, n: int) -> int:
+        at = self.at
+        if n < 0 or at + n > self.buf.size:
+            raise GGUFError(f"{self.path}: the header runs past the end of the file (byte {at} + {n})")
+        self.at = at + n
+        return at
 
-    def u64(self) -> int:
-        return struct.unpack("<Q", self.take(8))[0]
+    def items(self, dtype, count: int) -> np.ndarray:
+        dt = np.dtype(dtype)
+        at = self._span(dt.itemsize * count)
+        return self.buf[at:at + dt.itemsize * count].view(dt).copy()
 
-    def string(self) -> str:
-        return self.take(self.u64()).decode("utf-8", "replace")
+    def one(self, dtype):
+        return self.items(dtype, 1)[0].item()
 
-    def value(self, t: int):
-        if t in _FIXED:
-            fmt = _FIXED[t]
-            return struct.unpack(fmt, self.take(struct.calcsize(fmt)))[0]
-        if t == T_STRING:
-            return self.string()
-        if t == T_ARRAY:
-            et, n = self.u32(), self.u64()
-            if et in _FIXED:                                      # numeric arrays in one read
-                fmt = _FIXED[et]
-                dt = np.dtype(fmt.replace("?", "b1"))
-                return np.frombuffer(self.take(dt.itemsize * n), dtype=dt).copy()
-            return [self.value(et) for _ in range(n)]
-        raise GGUFError(f"GGUF metadata value type {t}")
+    def text(self) -> str:
+        n = self.one("<u8")
+        at = self._span(n)
+        return bytes(self.buf[at:at + n]).decode("utf-8", "replace")
+
+    def value(self, vtype: int):
+        dt = _VALUE_DTYPES.get(vtype)
+        if dt is not None:
+            return self.one(dt)
+        if vtype == VT_STRING:
+            return self.text()
+        if vtype == VT_ARRAY:
+            etype, count = self.one("<u4"), self.one("<u8")
+            edt = _VALUE_DTYPES.get(etype)
+            if edt is not None:                                   # a numeric array: one slice of the map
+                return self.items(edt, count)
+            return [self.value(etype) for _ in range(count)]
+        raise GGUFError(f"{self.path}: metadata value type {vtype} at byte {self.at - 4}")
 
 
-def _read_one(path: str) -> GGUF:
-    with open(path, "rb") as f:
-        if f.read(4) != GGUF_MAGIC:
+def _parse(path: str) -> GGUF:
+    """One GGUF file: metadata and the tensor table with absolute offsets."""
+    size = os.path.getsize(path)
+    if size < 24:
+        raise GGUFError(f"{path}: {size} bytes is shorter than a GGUF header")
+    buf = np.memmap(path, dtype=np.uint8, mode="r")
+    try:
+        if bytes(buf[:4]) != GGUF_MAGIC:
             raise GGUFError(f"{path}: not a GGUF file")
-        r = _Reader(f)
-        version = r.u32()
-        if version < 2:
-            raise GGUFError(f"{path}: GGUF version {version} (counts of version 1 are 32-bit; not read)")
-        n_tensors, n_kv = r.u64(), r.u64()
-        g = GGUF(path=path, version=version)
+        cur = _Cursor(buf, path)
+        cur.at = 4
+        version = cur.one("<u4")
+        if version not in (2, 3):
+            raise GGUFError(f"{path}: GGUF version {version} (version 1's counts are 32-bit; not read)")
+        n_tensors, n_kv = cur.one("<u8"), cur.one("<u8")
+        out = GGUF(path=path, version=version)
         for _ in range(n_kv):
-            key = r.string()
-            g.kv[key] = r.value(r.u32())
-        g.alignment = int(g.kv.get("general.alignment", 32))
-        if g.alignment <= 0 or g.alignment & (g.alignment - 1):
-            raise GGUFError(f"{path}: general.alignment {g.alignment} is not a power of two")
-        infos = []
+            key = cur.text()
+            out.kv[key] = cur.value(cur.one("<u4"))
+        align = int(out.kv.get("general.alignment", 32))
+        if align <= 0 or align & (align - 1):
+            raise GGUFError(f"{path}: general.alignment {align} is not a power of two")
+        out.alignment = align
+        table = []
         for _ in range(n_tensors):
-            name = r.string()
-            nd = r.u32()
-            if nd > 4:
-                raise GGUFError(f"{path}: tensor {name!r} has {nd} dimensions")
-            dims = tuple(r.u64() for _ in range(nd))
-            ty, off = r.u32(), r.u64()
-            infos.append((name, dims, ty, off))
-        pos = f.tell()
-        data = (pos + g.alignment - 1) // g.alignment * g.alignment
-        size = os.fstat(f.fileno()).st_size
-    for name, dims, ty, off in infos:
-        ne = tuple(dims) + (1,) * (4 - len(dims))
-        nbytes = tensor_nbytes(ty, ne) if ty in GGML_TYPES else -1
-        if off % g.alignment:
-            raise GGUFError(f"{path}: tensor {name!r} offset {off} is not aligned to {g.alignment}")
-        if nbytes >= 0 and data + off + nbytes > size:
+            name = cur.text()
+            n_dims = cur.one("<u4")
+            if not 1 <= n_dims <= 4:
+                raise GGUFError(f"{path}: tensor {name!r} has {n_dims} dimensions")
+            ne = tuple(int(d) for d in cur.items("<u8", n_dims))
+            table.append((name, ne + (1,) * (4 - n_dims), cur.one("<u4"), cur.one("<u8")))
+        data_start = -(-cur.at // align) * align
+    finally:
+        del buf
+    for name, ne, gtype, rel in table:
+        if rel % align:
+            raise GGUFError(f"{path}: tensor {name!r} offset {rel} is not a multiple of {align}")
+        nbytes = tensor_nbytes(gtype, ne) if gtype in GGML_TYPES else -1
+        if nbytes > 0 and data_start + rel + nbytes > size:
             raise GGUFError(f"{path}: tensor {name!r} runs past the end of the file")
-        if name in g.tensors:
+        if name in out.tensors:
             raise GGUFError(f"{path}: tensor {name!r} appears twice")
-        g.tensors[name] = GGUFTensor(name, ne, ty, data + off, nbytes, path)
-    return g
+        out.tensors[name] = GGUFTensor(name, ne, gtype, data_start + rel, nbytes, path)
+    return out
+
+
+def shard_paths(first: str, count: int) -> list[str]:
+    """The file names gguf-split gives the `count` shards of a model whose first shard is
+    `first` (<prefix>-00001-of-NNNNN.gguf)."""
+    stem, dot, ext = first.rpartition(".")
+    head, of, total = stem.rpartition("-of-")
+    prefix, dash, index = head.rpartition("-")
+    if not (dot and of and dash) or index != "00001" or not total.isdigit() or int(total) != count:
+        raise GGUFError(f"{first}: split.count is {count} but the name is not <prefix>-00001-of-{count:05d}.{ext}")
+    return [f"{prefix}-{i:05d}-of-{total}.{ext}" for i in range(1, count + 1)]
 
 
 def read(path: str) -> GGUF:
     """Header, metadata and tensor table of a GGUF file; for the first shard of a split model
-    (`-00001-of-0000N`) the other shards' tensors are added (metadata from the first)."""
-    g = _read_one(path)
-    n = int(g.kv.get("split.count", 1))
-    m = re.search(r"-00001-of-(\d+)", path)
-    if n > 1 and m:
-        for k in range(2, n + 1):
-            shard = path[:m.start()] + "-%05d-of-%s" % (k, m.group(1)) + path[m.end():]
-            if not os.path.exists(shard):
-                raise GGUFError(f"{path}: shard {shard} is missing")
-            s = _read_one(shard)
-            for name, t in s.tensors.items():
-                if name in g.tensors:
-                    raise GGUFError(f"{shard}: tensor {name!r} is also in another shard")
-                g.tensors[name] = t
+    the other shards' tensors are added (the metadata is the first shard's)."""
+    g = _parse(path)
+    count = int(g.kv.get("split.count", 1))
+    if count <= 1:
+        return g
+    for no, shard in enumerate(shard_paths(path, count)[1:], start=1):
+        if not os.path.exists(shard):
+            raise GGUFError(f"{path}: shard {shard} is missing")
+        part = _parse(shard)
+        if int(part.kv.get("split.no", no)) != no:
+            raise GGUFError(f"{shard}: split.no is {part.kv['split.no']}, its name says {no}")
+        for name, t in part.tensors.items():
+            if name in g.tensors:
+                raise GGUFError(f"{shard}: tensor {name!r} is also in another shard")
+            g.tensors[name] = t
     return g
 
 
@@ -199,9 +228,8 @@ def load_tensor(be, g: GGUF, name: str, chunk_bytes: int = 64 << 20):
     if t.nbytes < 0:
         raise GGUFError(f"{name}: ggml type {t.type} has no size here")
     dst = be.new_tensor(t.type, t.ne)
-    blck, bb = GGML_TYPES[t.type]
+    bb = GGML_TYPES[t.type][1]
     step = max(bb, chunk_bytes // bb * bb)
     for start in range(0, t.nbytes, step):
-        size = min(step, t.nbytes - start)
-        be.set_tensor(dst, g.read(name, start, size), offset=start)
+        be.set_tensor(dst, g.read(name, start, min(step, t.nbytes - start)), offset=start)
     return dst

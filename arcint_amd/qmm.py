@@ -335,10 +335,15 @@ class Backend:
     def synchronize(self):
         self._check(self.L.qmm_synchronize(self.h), "synchronize")
 
-    def downgrades(self) -> tuple[int, str]:
-        buf = C.create_string_buffer(256)
-        n = self.L.qmm_downgrades(self.h, buf, 256)
-        return int(n), buf.value.decode()
+    def downgrades(self) -> tuple[int, dict]:
+        """(total count, {key: count}) of the ops that took a slower path than their type promises"""
+        buf = C.create_string_buffer(1 << 14)
+        n = self.L.qmm_downgrades(self.h, buf, len(buf))
+        keys = {}
+        for line in buf.value.decode().splitlines():
+            k, _, c = line.rpartition("\t")
+            keys[k] = int(c)
+        return int(n), keys
 
     def last_path(self) -> str:
         return self.L.qmm_last_path(self.h).decode()

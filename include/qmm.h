@@ -245,8 +245,11 @@ int    qmm_moe_combine(qmm_ctx * ctx, const qmm_tensor * experts, const qmm_tens
                        const qmm_tensor * shared, const qmm_tensor * gate, const qmm_tensor * dst);
 
 /* ---- observability and timing ----------------------------------------- */
-/* Number of ops that took a slower path than their type promises (the
- * reference's DOWNGRADE keys); names of the last few in `buf`. */
+/* Ops that took a slower path than their weight type promises (the reference's DOWNGRADE keys,
+ * ggml_backend_opencl_downgrades, 0100-...patch:19-22 and :67-80): `buf` (NUL-terminated,
+ * truncated to buf_len) gets one "src=qmm <key>\t<count>\n" line per key, the key naming the
+ * op, weight type, K, a column bucket, the path taken and the reason ("op=MUL_MAT type=Q5_K
+ * k=5120 cols=2-8 path=gemv reason=no-mfma-gemv"); returns the total count over all keys. */
 int64_t qmm_downgrades(qmm_ctx * ctx, char * buf, size_t buf_len);
 /* Name of the kernel path the last mul_mat / mul_mat_id took: "gemv" (v_dot4
  * GEMV, 1..8 columns per weight pass), "gemv-mfma" (3..8 columns on the int8

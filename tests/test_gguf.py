@@ -94,3 +94,21 @@ def test_rejects_malformed_files(tmp_path):
     p.write_bytes(bytes(b))
     with pytest.raises(gguf.GGUFError):
         gguf.read(str(p))
+
+
+def test_split_numbering_checked(tmp_path):
+    """each shard's split.no must match its name, and a split model is opened by its first
+    shard, named <prefix>-00001-of-NNNNN.gguf"""
+    t = [(f"w{i}", (256, 2), 12, W.random_block_bytes(12, (256, 2), seed=60 + i)) for i in range(2)]
+    base = str(tmp_path / "m")
+    W.write(base + "-00001-of-00002.gguf", [("split.count", W.U16, 2), ("split.no", W.U16, 0)], t[:1])
+    W.write(base + "-00002-of-00002.gguf", [("split.count", W.U16, 2), ("split.no", W.U16, 1)], t[1:])
+    g = gguf.read(base + "-00001-of-00002.gguf")
+    assert sorted(g.tensors) == ["w0", "w1"]
+    assert gguf.shard_paths(base + "-00001-of-00002.gguf", 2)[1] == base + "-00002-of-00002.gguf"
+    W.write(base + "-00002-of-00002.gguf", [("split.count", W.U16, 2), ("split.no", W.U16, 0)], t[1:])
+    with pytest.raises(gguf.GGUFError):
+        gguf.read(base + "-00001-of-00002.gguf")
+    W.write(str(tmp_path / "solo.gguf"), [("split.count", W.U16, 2)], t[:1])
+    with pytest.raises(gguf.GGUFError):
+        gguf.read(str(tmp_path / "solo.gguf"))

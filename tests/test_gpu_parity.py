@@ -834,8 +834,10 @@ def test_mul_mat_permuted_src1(be, sc, orc, qtype, nr):
 @pytest.mark.parametrize("qtype", [qmm.Q4_K, qmm.Q4_0])
 @pytest.mark.parametrize("T", [1, 6, 40])
 def test_mul_mat_id_invalid_ids_write_zero_rows(be, sc, orc, qtype, T):
-    """negative and out-of-range ids (P02:98-103) write zero rows over whatever dst held, on the
-    v_dot4 and (T = 40: 160 pairs on 16 experts) MFMA task paths"""
+    """negative ids (the reference's rule, P02:98-103) write zero rows over whatever dst held, on
+    the v_dot4 and (T = 40: 160 pairs on 16 experts) MFMA task paths; ids at or past the expert
+    count, which ggml-cpu asserts on (P02:105), write zero rows too and make the next
+    synchronize report the error (once)"""
     E, n_used, M, K = 16, 4, 130, 512
     say("mul_mat_id-invalid", qtype, T)
     raw = synth.weights(qtype, E * M, K, seed=151)
@@ -848,6 +850,9 @@ def test_mul_mat_id_invalid_ids_write_zero_rows(be, sc, orc, qtype, T):
     w = sc.weights(qtype, raw, (K, M, E))
     y = sc.f32(np.full((T, n_used, M), 7.0, np.float32))          # dst holds non-zeros
     be.mul_mat_id(w, sc.f32(x), sc.i32(ids), y)
+    if T > 1:
+        with pytest.raises(qmm.QmmError, match="past the expert count"):
+            be.synchronize()
     be.synchronize()
     got = be.get_f32(y).reshape(T, n_used, M)
     ref = orc.mul_mat_id(qtype, raw, M, K, E, x, ids)
@@ -927,6 +932,9 @@ def test_mul_mat_id_glu(be, sc, orc, qtype, T, E):
     wg, wu = sc.weights(qtype, rg, (K, M, E)), sc.weights(qtype, ru, (K, M, E))
     y = sc.f32(np.full((T, n_used, M), 5.0, np.float32))
     be.mul_mat_id_glu(wg, wu, sc.f32(x), sc.i32(ids), y, qmm.GLU_SWIGLU)
+    if T > 1:                                                     # the id E + 2 is reported
+        with pytest.raises(qmm.QmmError, match="past the expert count"):
+            be.synchronize()
     be.synchronize()
     assert be.last_path().startswith("glu-gemv-id")
     got = be.get_f32(y).reshape(T, n_used, M)
@@ -951,3 +959,32 @@ def test_mul_mat_id_glu_per_slot_src1(be, sc, orc):
     got = be.get_f32(y).reshape(T, n_used, M)
     ref = G.glu(qmm.GLU_GEGLU, orc.mul_mat_id(qmm.Q4_K, rg, M, K, E, x, ids), orc.mul_mat_id(qmm.Q4_K, ru, M, K, E, x, ids))
     assert rel_err(got, ref) <= TOL
+
+
+def test_downgrade_keys(sc, orc):
+    """the downgrade export counts per key: Q5_K at 4 columns runs on the v_dot4 GEMV (no MFMA
+    form), Q4_K at 40 columns takes two weight passes on the MFMA GEMV; a product on its
+    promised path adds nothing"""
+    say("downgrades")
+    with qmm.Backend(0) as b2:
+        bufs = []
+
+        def run(qtype, M, K, N):
+            w = b2.new_tensor(qtype, (K, M))
+            b2.set_tensor(w, synth.weights(qtype, M, K, 1))
+            x = b2.new_tensor(qmm.F32, (K, N))
+            b2.set_tensor(x, synth.activations(N, K, 2).view(np.uint8).ravel())
+            y = b2.new_tensor(qmm.F32, (M, N))
+            b2.mul_mat(w, x, y)
+            bufs.extend([w, x, y])
+
+        run(qmm.Q4_K, 128, 512, 1)
+        assert b2.downgrades() == (0, {})
+        run(qmm.Q5_K, 128, 512, 4)
+        run(qmm.Q5_K, 128, 512, 5)
+        run(qmm.Q4_K, 128, 512, 40)
+        b2.synchronize()
+        n, keys = b2.downgrades()
+        assert keys == {"src=qmm op=MUL_MAT type=Q5_K k=512 cols=2-8 path=gemv reason=no-mfma-gemv": 2,
+                        "src=qmm op=MUL_MAT type=Q4_K k=512 cols=33-128 path=gemv-mfma reason=several-weight-passes": 1}
+        assert n == 3
