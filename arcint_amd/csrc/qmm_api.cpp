@@ -7,6 +7,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -14,6 +15,12 @@
 #include "qmm_layout.h"
 
 using namespace qmm;
+
+// The activation scratch of qmm_mul_mat_noalloc: a file-scope device array, one copy on every
+// GPU the library runs on, held until the process ends.  Host code never uses the array's name
+// as an address (on the host it is only a stand-in): it uses the per-device address that
+// hipGetSymbolAddress returns at context creation (scratch_address below).
+static __device__ __align__(256) uint8_t scratch[QMM_NOALLOC_SCRATCH_BYTES];
 
 struct qmm_buffer {
     void * ptr = nullptr;
@@ -69,6 +76,9 @@ struct qmm_ctx {
     Downgrade dg[kMaxDowngradeKeys];
     int n_dg = 0;
     int64_t dg_other = 0;
+    // the activation scratch of qmm_mul_mat_noalloc on this context's device (a __device__
+    // array of this file; its address comes from hipGetSymbolAddress at context creation)
+    uint8_t * fixed_scratch = nullptr;
     // main-kernel timing (qmm_kernel_timing)
     bool ktime = false;
     std::vector<hipEvent_t> kev;   // pairs
@@ -393,6 +403,25 @@ void note_downgrade(qmm_ctx * ctx, const char * fmt, ...) {
     if (getenv("QMM_DOWNGRADE_LOG")) fprintf(stderr, "DOWNGRADE src=qmm %s\n", key);
 }
 
+// the device address of `scratch` on `device`, which must be current: looked up once per
+// device and kept (every context on that device shares the array)
+std::mutex g_scratch_mu;
+constexpr int kMaxDevices = 64;
+uint8_t * g_scratch_ptr[kMaxDevices] = {};
+
+hipError_t scratch_address(int device, uint8_t ** out) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    if (!g_scratch_ptr[device]) {
+        void * p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        g_scratch_ptr[device] = (uint8_t *)p;
+    }
+    *out = g_scratch_ptr[device];
+    return hipSuccess;
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -410,7 +439,7 @@ int qmm_ctx_create(int device, qmm_ctx ** out) {
         hipMalloc(&ctx->sink, kSinkBytes) != hipSuccess || hipMemsetAsync(ctx->sink, 0, kSinkBytes, ctx->stream) != hipSuccess ||
         hipMalloc(&ctx->dflags, 256) != hipSuccess || hipMemsetAsync(ctx->dflags, 0, 256, ctx->stream) != hipSuccess ||
         hipHostMalloc(&ctx->hflags, 256, hipHostMallocDefault) != hipSuccess ||
-        hipStreamSynchronize(ctx->stream) != hipSuccess) {
+        hipStreamSynchronize(ctx->stream) != hipSuccess || scratch_address(device, &ctx->fixed_scratch) != hipSuccess) {
         qmm_ctx_free(ctx);
         return QMM_ERR_DEVICE;
     }
@@ -826,6 +855,18 @@ int qmm_mul_mat(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1,
         return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat: %s", reason);
     QMM_HIP(ctx, hipSetDevice(ctx->device));
     return mul_mat_launch(ctx, src0, src1, dst, w, nullptr);
+}
+
+int qmm_mul_mat_noalloc(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1, const qmm_tensor * dst) {
+    if (!ctx) return QMM_ERR_INVALID;
+    char reason[160];
+    WView w;
+    if (!mul_mat_ok(src0, src1, dst, true, &w, reason, sizeof(reason)))
+        return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat_noalloc: %s", reason);
+    if (!ctx->fixed_scratch) return fail(ctx, QMM_ERR_DEVICE, "mul_mat_noalloc: the device scratch has no address");
+    QMM_HIP(ctx, hipSetDevice(ctx->device));
+    const FixedAct fixed{ ctx->fixed_scratch, QMM_NOALLOC_SCRATCH_BYTES };
+    return mul_mat_launch(ctx, src0, src1, dst, w, &fixed);
 }
 
 // The expert tasks of ids into the route scratch (reused inside a graph when ids, ne11, the

@@ -35,8 +35,9 @@ EXPORTS = (
     "qmm_graph_compute", "qmm_dequantize", "qmm_quantize_act", "qmm_synchronize", "qmm_downgrades",
     "qmm_last_path", "qmm_timer_begin", "qmm_timer_end", "qmm_buffer_copy", "qmm_kernel_timing",
     "qmm_kernel_time", "qmm_tensor_pack", "qmm_tensor_unpack", "qmm_describe_mul_mat", "qmm_moe_topk",
-    "qmm_moe_combine", "qmm_mul_mat_glu", "qmm_mul_mat_id_glu",
+    "qmm_moe_combine", "qmm_mul_mat_glu", "qmm_mul_mat_id_glu", "qmm_mul_mat_noalloc",
 )
+NOALLOC_SCRATCH_BYTES = 16 << 20     # QMM_NOALLOC_SCRATCH_BYTES
 
 
 class QmmError(RuntimeError):
@@ -97,6 +98,7 @@ def load() -> C.CDLL:
         L.qmm_supports_op.argtypes = [vp, i32, T, T, T, T, C.c_char_p, sz]
         L.qmm_mul_mat.argtypes = [vp, T, T, T]
         L.qmm_mul_mat_id.argtypes = [vp, T, T, T, T]
+        L.qmm_mul_mat_noalloc.argtypes = [vp, T, T, T]
         L.qmm_moe_topk.argtypes = [vp, T, T, T, C.c_float, C.c_float]
         L.qmm_moe_combine.argtypes = [vp, T, T, T, T, T]
         L.qmm_mul_mat_glu.argtypes = [vp, T, T, T, T, C.c_int32]
@@ -286,6 +288,11 @@ class Backend:
 
     def mul_mat(self, src0: Tensor, src1: Tensor, dst: Tensor):
         self._check(self.L.qmm_mul_mat(self.h, C.byref(src0.c), C.byref(src1.c), C.byref(dst.c)), "mul_mat")
+
+    def mul_mat_noalloc(self, src0: Tensor, src1: Tensor, dst: Tensor):
+        """qmm_mul_mat with the activations in the library's per-device array: allocates nothing"""
+        self._check(self.L.qmm_mul_mat_noalloc(self.h, C.byref(src0.c), C.byref(src1.c), C.byref(dst.c)),
+                    "mul_mat_noalloc")
 
     def mul_mat_id(self, src0: Tensor, src1: Tensor, ids: Tensor, dst: Tensor):
         self._check(self.L.qmm_mul_mat_id(self.h, C.byref(src0.c), C.byref(src1.c), C.byref(ids.c), C.byref(dst.c)),

@@ -27,6 +27,8 @@
  *                                MUL_MAT_ID (P01:615-660)
  *   qmm_mul_mat                  ggml_cl_mul_mat (P01:1135-1160)
  *   qmm_mul_mat_id               ggml_cl_mul_mat_id (P01:1316-1325)
+ *   qmm_mul_mat_noalloc          no counterpart in the reference: qmm_mul_mat for
+ *                                callers that cannot allocate device memory
  *   qmm_graph_compute            ggml_backend_opencl_graph_compute over a node
  *                                list, graph_gen++ per call (P01:609-612);
  *                                activation dedup keyed per graph (P01:683-717)
@@ -208,6 +210,19 @@ int    qmm_mul_mat_glu(qmm_ctx * ctx, const qmm_tensor * gate, const qmm_tensor 
  * route, one GEMV launch over both stacks.  Invalid ids give zero rows. */
 int    qmm_mul_mat_id_glu(qmm_ctx * ctx, const qmm_tensor * gate, const qmm_tensor * up, const qmm_tensor * src1,
                           const qmm_tensor * ids, const qmm_tensor * dst, int32_t glu_op);
+/* qmm_mul_mat with nothing allocated: no reference counterpart; for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Same operands, kernels and results as qmm_mul_mat; the activation
+ * quantization goes to a device array of QMM_NOALLOC_SCRATCH_BYTES that the library holds on
+ * every GPU it runs on until the process ends (its address is looked up when a context is
+ * created) instead of the context's scratch, and no graph dedup or kernel timing applies.
+ * Fails with QMM_ERR_NOMEM, before launching anything, when src1's quantized activations need
+ * more than that: about K * N * 1.2 bytes (K rounded up to 256; 16 MiB holds 512 columns at
+ * K = 17408).  Every call on one GPU shares the array, which keeps the last call's contents:
+ * calls that overlap on one GPU (contexts with different streams) race; calls on one context
+ * are ordered by its stream. */
+#define QMM_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+int    qmm_mul_mat_noalloc(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1, const qmm_tensor * dst);
 /* Runs the nodes in order; bumps the graph generation first, so one
  * activation quantization serves every node of the graph that reads the same
  * src1 with the same vec_dot type. */
