@@ -85,12 +85,19 @@ __device__ __forceinline__ float sldf(const void * p, int i) { return __builtin_
 // int16 number i of an int16 array (4-byte aligned)
 __device__ __forceinline__ int slds16(const void * p, int i) { return (int)(int16_t)(sld(p, i >> 1) >> (16 * (i & 1))); }
 
-// one group (256 weights) of the activation columns of a task
-template <int NC>
+// One group (256 weights) of the activation columns of a task, and how the stage dots read it:
+// c4 = four code dwords from dword i, df = scale i, s16 = code sum i.  XG reads the pre-pass's
+// codes in global memory with scalar loads (uniform over the wave); XL (the fused kernel) reads
+// the wave's own quantization in LDS, a broadcast read.
+template <int N>
 struct XG {
-    const int8_t * c[NC];        // codes of the group
-    const float * d[NC];         // its scales
-    const int16_t * s[NC];       // its code sums
+    static constexpr int NC = N;
+    const int8_t * c[N];         // codes of the group
+    const float * d[N];          // its scales
+    const int16_t * s[N];        // its code sums
+    __device__ static uint4 c4(const int8_t * p, int i) { return sld4(p, i); }
+    __device__ static float df(const float * p, int i) { return sldf(p, i); }
+    __device__ static int s16(const int16_t * p, int i) { return slds16(p, i); }
 };
 
 __device__ __forceinline__ int dot16(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3, const uint4 & a, int acc) {
@@ -108,8 +115,9 @@ template <> struct GV<QMM_TYPE_Q4_0> {
 #pragma unroll
         for (int c = 0; c < 9; ++c) r[c] = ld16_nt(p + c * kChunk);
     }
-    template <int NC>
-    __device__ static void dot(const uint4 * r, int, const XG<NC> & x, int nc, float * acc, int *) {
+    template <class X>
+    __device__ static void dot(const uint4 * r, int, const X & x, int nc, float * acc, int *) {
+        constexpr int NC = X::NC;
         const uint32_t dw2[4] = { r[8].x, r[8].y, r[8].z, r[8].w };
         const uint32_t m = 0x0F0F0F0Fu;
 #pragma unroll
@@ -121,10 +129,10 @@ template <> struct GV<QMM_TYPE_Q4_0> {
 #pragma unroll
             for (int j = 0; j < NC; ++j) {
                 if (j < nc) {
-                    int s = dot16(l0, l1, l2, l3, sld4(x.c[j], 8 * p), 0);
-                    s = dot16(h0, h1, h2, h3, sld4(x.c[j], 8 * p + 4), s);
-                    s -= 8 * slds16(x.s[j], p);                // codes are q, the weight is q - 8
-                    acc[j] += (float)s * (dw * sldf(x.d[j], p));
+                    int s = dot16(l0, l1, l2, l3, X::c4(x.c[j], 8 * p), 0);
+                    s = dot16(h0, h1, h2, h3, X::c4(x.c[j], 8 * p + 4), s);
+                    s -= 8 * X::s16(x.s[j], p);                // codes are q, the weight is q - 8
+                    acc[j] += (float)s * (dw * X::df(x.d[j], p));
                 }
             }
         }
@@ -141,8 +149,9 @@ template <> struct GV<QMM_TYPE_Q8_0> {
         for (int c = 0; c < 8; ++c) r[c] = ld16_nt(p + (8 * st + c) * kChunk);
         r[8] = ld16(p + 16 * kChunk);                     // both stages: keep it cached
     }
-    template <int NC>
-    __device__ static void dot(const uint4 * r, int st, const XG<NC> & x, int nc, float * acc, int *) {
+    template <class X>
+    __device__ static void dot(const uint4 * r, int st, const X & x, int nc, float * acc, int *) {
+        constexpr int NC = X::NC;
         const uint32_t dw2[4] = { r[8].x, r[8].y, r[8].z, r[8].w };
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) {
@@ -153,9 +162,9 @@ template <> struct GV<QMM_TYPE_Q8_0> {
 #pragma unroll
             for (int j = 0; j < NC; ++j) {
                 if (j < nc) {
-                    int s = dot16(q0.x, q0.y, q0.z, q0.w, sld4(x.c[j], 8 * p), 0);
-                    s = dot16(q1.x, q1.y, q1.z, q1.w, sld4(x.c[j], 8 * p + 4), s);
-                    acc[j] += (float)s * (dw * sldf(x.d[j], p));
+                    int s = dot16(q0.x, q0.y, q0.z, q0.w, X::c4(x.c[j], 8 * p), 0);
+                    s = dot16(q1.x, q1.y, q1.z, q1.w, X::c4(x.c[j], 8 * p + 4), s);
+                    acc[j] += (float)s * (dw * X::df(x.d[j], p));
                 }
             }
         }
@@ -173,8 +182,9 @@ template <> struct GV<QMM_TYPE_Q4_K> {
 #pragma unroll
         for (int c = 0; c < 9; ++c) r[c] = ld16_nt(p + c * kChunk);
     }
-    template <int NC>
-    __device__ static void dot(const uint4 * r, int, const XG<NC> & x, int nc, float * acc, int *) {
+    template <class X>
+    __device__ static void dot(const uint4 * r, int, const X & x, int nc, float * acc, int *) {
+        constexpr int NC = X::NC;
         const uint4 h = r[8];                              // d, dmin | scales[12]
         const float d = h2f(h.x), dmin = h2f(h.x >> 16);
         // 6-bit scales / mins (get_scale_min_k4, P01:2164-2176), one per byte
@@ -202,8 +212,8 @@ template <> struct GV<QMM_TYPE_Q4_K> {
 #pragma unroll
             for (int j = 0; j < NC; ++j) {
                 if (j < nc) {
-                    const int sl = dot16(l0, l1, l2, l3, sld4(x.c[j], xo), 0);
-                    const int sh = dot16(h0, h1, h2, h3, sld4(x.c[j], xo + 8), 0);
+                    const int sl = dot16(l0, l1, l2, l3, X::c4(x.c[j], xo), 0);
+                    const int sh = dot16(h0, h1, h2, h3, X::c4(x.c[j], xo + 8), 0);
                     isc[j] += sc[jl] * sl + sc[jl + 1] * sh;
                 }
             }
@@ -213,8 +223,8 @@ template <> struct GV<QMM_TYPE_Q4_K> {
             if (j < nc) {
                 int imn = 0;
 #pragma unroll
-                for (int i = 0; i < 8; ++i) imn += mn[i] * (slds16(x.s[j], 2 * i) + slds16(x.s[j], 2 * i + 1));
-                acc[j] += sldf(x.d[j], 0) * (d * (float)isc[j] - dmin * (float)imn);
+                for (int i = 0; i < 8; ++i) imn += mn[i] * (X::s16(x.s[j], 2 * i) + X::s16(x.s[j], 2 * i + 1));
+                acc[j] += X::df(x.d[j], 0) * (d * (float)isc[j] - dmin * (float)imn);
             }
         }
     }
@@ -237,8 +247,9 @@ template <> struct GV<QMM_TYPE_Q6_K> {
         r[6] = ld16(p + 12 * kChunk);                      // both stages: keep it cached
         r[7].x = *reinterpret_cast<const uint16_t *>(tg + 13 * kChunk + lane * 2);
     }
-    template <int NC>
-    __device__ static void dot(const uint4 * r, int st, const XG<NC> & x, int nc, float * acc, int * isum) {
+    template <class X>
+    __device__ static void dot(const uint4 * r, int st, const X & x, int nc, float * acc, int * isum) {
+        constexpr int NC = X::NC;
         if (st == 0) {
 #pragma unroll
             for (int j = 0; j < NC; ++j) isum[j] = 0;
@@ -262,8 +273,8 @@ template <> struct GV<QMM_TYPE_Q6_K> {
 #pragma unroll
                 for (int j = 0; j < NC; ++j) {
                     if (j < nc) {
-                        int s = dot16(c0, c1, c2, c3, sld4(x.c[j], xo), 0);
-                        s -= 32 * slds16(x.s[j], is);           // codes are q, the weight q - 32
+                        int s = dot16(c0, c1, c2, c3, X::c4(x.c[j], xo), 0);
+                        s -= 32 * X::s16(x.s[j], is);           // codes are q, the weight q - 32
                         isum[j] += sc * s;
                     }
                 }
@@ -273,7 +284,7 @@ template <> struct GV<QMM_TYPE_Q6_K> {
             const float d = h2f(r[7].x);
 #pragma unroll
             for (int j = 0; j < NC; ++j)
-                if (j < nc) acc[j] += (d * sldf(x.d[j], 0)) * (float)isum[j];
+                if (j < nc) acc[j] += (d * X::df(x.d[j], 0)) * (float)isum[j];
         }
     }
 };
@@ -291,8 +302,9 @@ template <> struct GV<QMM_TYPE_IQ4_XS> {
         r[8].x = h.x;
         r[8].y = h.y;
     }
-    template <int NC>
-    __device__ static void dot(const uint4 * r, int, const XG<NC> & x, int nc, float * acc, int *) {
+    template <class X>
+    __device__ static void dot(const uint4 * r, int, const X & x, int nc, float * acc, int *) {
+        constexpr int NC = X::NC;
         const float dw = h2f(r[8].x);
         const uint32_t shi = r[8].x >> 16, slo = r[8].y;
         int isum[NC];
@@ -309,15 +321,15 @@ template <> struct GV<QMM_TYPE_IQ4_XS> {
 #pragma unroll
             for (int j = 0; j < NC; ++j) {
                 if (j < nc) {
-                    int s = dot16(v0, v1, v2, v3, sld4(x.c[j], 8 * ib), 0);
-                    s = dot16(u0, u1, u2, u3, sld4(x.c[j], 8 * ib + 4), s);
+                    int s = dot16(v0, v1, v2, v3, X::c4(x.c[j], 8 * ib), 0);
+                    s = dot16(u0, u1, u2, u3, X::c4(x.c[j], 8 * ib + 4), s);
                     isum[j] += ls * s;
                 }
             }
         }
 #pragma unroll
         for (int j = 0; j < NC; ++j)
-            if (j < nc) acc[j] += (dw * sldf(x.d[j], 0)) * (float)isum[j];
+            if (j < nc) acc[j] += (dw * X::df(x.d[j], 0)) * (float)isum[j];
     }
 };
 
@@ -326,8 +338,9 @@ template <> struct GV<QMM_TYPE_IQ4_NL> {
     static constexpr int NST = 1, NL = 9, ND = 8, NS = 8;
     static constexpr int kReadEnd = GV<QMM_TYPE_Q4_0>::kReadEnd;
     __device__ static void load(uint4 * r, const uint8_t * tg, int st, int lane) { GV<QMM_TYPE_Q4_0>::load(r, tg, st, lane); }
-    template <int NC>
-    __device__ static void dot(const uint4 * r, int, const XG<NC> & x, int nc, float * acc, int *) {
+    template <class X>
+    __device__ static void dot(const uint4 * r, int, const X & x, int nc, float * acc, int *) {
+        constexpr int NC = X::NC;
         const uint32_t dw2[4] = { r[8].x, r[8].y, r[8].z, r[8].w };
         const uint32_t m = 0x0F0F0F0Fu;
 #pragma unroll
@@ -340,9 +353,9 @@ template <> struct GV<QMM_TYPE_IQ4_NL> {
 #pragma unroll
             for (int j = 0; j < NC; ++j) {
                 if (j < nc) {
-                    int s = dot16(v0, v1, v2, v3, sld4(x.c[j], 8 * p), 0);
-                    s = dot16(u0, u1, u2, u3, sld4(x.c[j], 8 * p + 4), s);
-                    acc[j] += (float)s * (dw * sldf(x.d[j], p));
+                    int s = dot16(v0, v1, v2, v3, X::c4(x.c[j], 8 * p), 0);
+                    s = dot16(u0, u1, u2, u3, X::c4(x.c[j], 8 * p + 4), s);
+                    acc[j] += (float)s * (dw * X::df(x.d[j], p));
                 }
             }
         }
@@ -359,8 +372,9 @@ template <> struct GV<QMM_TYPE_Q5_K> {
 #pragma unroll
         for (int c = 0; c < 11; ++c) r[c] = ld16_nt(p + c * kChunk);
     }
-    template <int NC>
-    __device__ static void dot(const uint4 * r, int, const XG<NC> & x, int nc, float * acc, int *) {
+    template <class X>
+    __device__ static void dot(const uint4 * r, int, const X & x, int nc, float * acc, int *) {
+        constexpr int NC = X::NC;
         const uint4 h = r[8];                              // d, dmin | scales[12]
         const float d = h2f(h.x), dmin = h2f(h.x >> 16);
         const uint32_t sc03 = h.y & 0x3f3f3f3fu, mn03 = h.z & 0x3f3f3f3fu;
@@ -390,8 +404,8 @@ template <> struct GV<QMM_TYPE_Q5_K> {
 #pragma unroll
             for (int j = 0; j < NC; ++j) {
                 if (j < nc) {
-                    const int sl = dot16(l0, l1, l2, l3, sld4(x.c[j], xo), 0);
-                    const int sh = dot16(h0, h1, h2, h3, sld4(x.c[j], xo + 8), 0);
+                    const int sl = dot16(l0, l1, l2, l3, X::c4(x.c[j], xo), 0);
+                    const int sh = dot16(h0, h1, h2, h3, X::c4(x.c[j], xo + 8), 0);
                     isc[j] += sc[jl] * sl + sc[jl + 1] * sh;
                 }
             }
@@ -401,8 +415,8 @@ template <> struct GV<QMM_TYPE_Q5_K> {
             if (j < nc) {
                 int imn = 0;
 #pragma unroll
-                for (int i = 0; i < 8; ++i) imn += mn[i] * (slds16(x.s[j], 2 * i) + slds16(x.s[j], 2 * i + 1));
-                acc[j] += sldf(x.d[j], 0) * (d * (float)isc[j] - dmin * (float)imn);
+                for (int i = 0; i < 8; ++i) imn += mn[i] * (X::s16(x.s[j], 2 * i) + X::s16(x.s[j], 2 * i + 1));
+                acc[j] += X::df(x.d[j], 0) * (d * (float)isc[j] - dmin * (float)imn);
             }
         }
     }
@@ -571,7 +585,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvParams p) {
                         x.d[j] = xd0[j] + (int64_t)g * ND;
                         x.s[j] = xs0[j] + (int64_t)g * NS;
                     }
-                    T::template dot<NC>(B[i], (s + i) % NST, x, nc, a, st_state);
+                    T::dot(B[i], (s + i) % NST, x, nc, a, st_state);
                 }
                 load_stage(B[i], s + i + D);
             }
@@ -1141,7 +1155,304 @@ int env_int(const char * name, int dflt) {
     return e ? atoi(e) : dflt;
 }
 
+// ---- the v_dot4 GEMV with its own activation quantization (one launch per op) -------------
+// k_gemv needs the pre-pass: a launch that quantizes src1 (and zeroes dst for its K slices'
+// atomics) ahead of it.  At decode that launch and its kernel boundary are a fifth of the op.
+// Here every wave quantizes the groups it streams itself, with the pre-pass's own quantizers
+// (so the codes equal ggml-cpu's), into its own LDS slots, after its first weight stage is on
+// its way; K is split only among the waves of a work-group and added in LDS, so every output
+// is stored once and nothing has to be zeroed first.  The same kernel takes:
+//  * dense MUL_MAT at 1 or 2 columns per task;
+//  * MUL_MAT_ID at small batches with no route: task p is the (token, slot) pair p and reads its
+//    expert id itself (the reference's per-pair matvec below 16 tokens, P01:1189-1192 and
+//    P01:1222-1248); a negative id writes a zero row, an id past the stack too and sets the
+//    error flag;
+//  * either of them for a gate/up pair with its GLU: the work-group streams the gate tile, then
+//    the up tile against the same quantized activations, and stores act(gate) * up.
+constexpr int kFqSlot = 320;   // one (group, column): 256 codes, 8 f32 scales at 256, 16 i16 sums at 288
+constexpr int kFqMaxWaves = 16;
+
+template <int N>
+struct XL {
+    static constexpr int NC = N;
+    const int8_t * c[N];
+    const float * d[N];
+    const int16_t * s[N];
+    __device__ static uint4 c4(const int8_t * p, int i) { return *reinterpret_cast<const uint4 *>(p + 4 * i); }
+    __device__ static float df(const float * p, int i) { return p[i]; }
+    __device__ static int s16(const int16_t * p, int i) { return p[i]; }
+};
+
+struct FqParams {
+    WView w;
+    F32Cols x;
+    int64_t K;
+    // dense tasks (ids == null): as k_gemv's
+    int64_t ne11, ne12, r2, r3, ne02, tpb, col_bs;
+    int64_t d_nb1, d_nb2, d_nb3;
+    // MUL_MAT_ID pairs: pair p = t n_used + i, its id at t ids_nb1 + i ids_nb0 (bytes), its
+    // activation column (i % ne11i) + t ne11i, its dst floats t dnb2 + i dnb1
+    const char * ids;
+    int64_t ids_nb0, ids_nb1, n_used, ne11i, n_as, dnb1, dnb2;
+    int32_t * bad_id;
+    float * dst;
+    const uint8_t * sink;
+    const uint8_t * base2;       // glu >= 0: the up image, w's shape
+    int glu;
+    int W, spw;
+};
+
+// group g of activation column col, quantized by one wave into a slot (the pre-pass's quantizers)
+template <int VDT>
+__device__ __forceinline__ void quant_slot(const F32Cols & xs, int64_t K, int64_t col, int g, uint8_t * slot, int lane) {
+    float v[4] = { 0.f, 0.f, 0.f, 0.f };
+    const int64_t k = (int64_t)g * 256 + 4 * lane;                // K is whole 32-blocks (q8_0) or 256-blocks
+    if (k < K) {
+        const float * x = f32_col(xs, col) + k;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = x[i];
+    }
+    float d;
+    int s;
+    if constexpr (VDT == QMM_TYPE_Q8_K) {
+        const uint32_t q = quant_q8_K_wave(v, lane, &d, &s);
+        reinterpret_cast<uint32_t *>(slot)[lane] = q;
+        if ((lane & 3) == 0) reinterpret_cast<int16_t *>(slot + 288)[lane >> 2] = (int16_t)s;
+        if (lane == 0) reinterpret_cast<float *>(slot + 256)[0] = d;
+    } else {
+        const uint32_t q = quant_q8_0_lane(v, &d, &s);
+        reinterpret_cast<uint32_t *>(slot)[lane] = q;
+        if ((lane & 7) == 0) {
+            reinterpret_cast<float *>(slot + 256)[lane >> 3] = d;
+            reinterpret_cast<int16_t *>(slot + 288)[lane >> 3] = (int16_t)s;
+        }
+    }
+}
+
+// A work-group is W waves on one 64-row tile of one task, wave w streaming groups
+// [w spw, w spw + spw) (dot4_stages with one K slice).  LDS: the waves' slots [W][spw][NC], then,
+// after the stream, the waves' sums [W][NV][64].
+template <int TYPE, int NC>
+__global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
+    using T = GV<TYPE>;
+    constexpr int NL = T::NL, NST = T::NST;
+    constexpr int VDT = (TYPE == QMM_TYPE_Q4_0 || TYPE == QMM_TYPE_Q8_0 || TYPE == QMM_TYPE_IQ4_NL) ? QMM_TYPE_Q8_0
+                                                                                                     : QMM_TYPE_Q8_K;
+    static_assert(T::kReadEnd <= tile_group_bytes(TYPE) && tile_group_bytes(TYPE) <= (int)kSinkBytes,
+                  "a stage reads inside one tile-group, which fits in the sink");
+    extern __shared__ __align__(16) uint8_t sm[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t ntl = (uint32_t)p.w.ntiles;
+    const WgPos wp = wg_pos(blockIdx.x, 1u, ntl);
+    const uint32_t tile = wp.unit, task = wp.task;
+    int mat, nc;
+    int64_t colv[NC], doffv[NC];
+    if (p.ids) {
+        const int64_t t = (int64_t)task / p.n_used, i = (int64_t)task - t * p.n_used;
+        const int32_t e = *reinterpret_cast<const int32_t *>(p.ids + t * p.ids_nb1 + i * p.ids_nb0);
+        const int64_t doff = t * p.dnb2 + i * p.dnb1;
+        if (e < 0 || e >= p.n_as) {                                // uniform: a zero row
+            if (wave == 0) {
+                const int64_t row = (int64_t)tile * kTileRows + lane;
+                if (row < p.w.M) p.dst[doff + row] = 0.0f;
+                if (e >= p.n_as && tile == 0 && lane == 0) *p.bad_id = 1;
+            }
+            return;
+        }
+        mat = e;
+        nc = 1;
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            colv[j] = (i % p.ne11i) + t * p.ne11i;
+            doffv[j] = doff;
+        }
+    } else {
+        const DenseTask dt = dense_task(task, (uint32_t)p.tpb, (uint32_t)p.ne12, (uint32_t)p.r2, (uint32_t)p.r3,
+                                        (uint32_t)p.ne02);
+        mat = dt.mat;
+        const int64_t first = (int64_t)dt.tt * NC;
+        nc = (int)((p.ne11 - first) < NC ? (p.ne11 - first) : NC);
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            const int64_t i1 = first + (j < nc ? j : 0);
+            colv[j] = (int64_t)dt.b * p.col_bs + i1;
+            doffv[j] = i1 * p.d_nb1 + (int64_t)dt.i2 * p.d_nb2 + (int64_t)dt.i3 * p.d_nb3;
+        }
+    }
+    nc = __builtin_amdgcn_readfirstlane(nc);
+    const int G = (int)p.w.G;
+    int ga, S;
+    dot4_stages(0, p.W, wave, p.spw, G, NST, ga, S);
+    const bool glu = p.glu >= 0;                                  // uniform
+    const int ST = glu ? 2 * S : S;                               // gate stages, then up stages
+    const uint8_t * tbg = tile_group(p.w, mat, tile, 0);
+    WView w2 = p.w;
+    w2.base = p.base2;
+    const uint8_t * tbu = glu ? tile_group(w2, mat, tile, 0) : tbg;
+    const size_t tgs = (size_t)p.w.tg;
+    uint4 B[NL];
+    auto load_stage = [&](int s) {                                // past the last stage: the sink
+        const uint8_t * tg = p.sink;
+        int st = 0;
+        if (s < ST) {
+            const int sl = s < S ? s : s - S;
+            tg = (s < S ? tbg : tbu) + (size_t)stage_group(ga, sl, NST) * tgs;
+            st = sl % NST;
+        }
+        T::load(B, tg, st, lane);
+    };
+    if (ST > 0) load_stage(0);                                    // the weights go out first
+    // the wave's groups of its columns into its slots [group][column]
+    uint8_t * const slots = sm + (size_t)wave * p.spw * NC * kFqSlot;
+    for (int gi = 0; gi * NST < S; ++gi) {                        // uniform
+#pragma unroll
+        for (int j = 0; j < NC; ++j)
+            if (j < nc) quant_slot<VDT>(p.x, p.K, colv[j], ga + gi, slots + (gi * NC + j) * kFqSlot, lane);
+    }
+    __builtin_amdgcn_wave_barrier();
+    float acc[NC], accu[NC];
+    int st_state[NC];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+        acc[j] = 0.0f;
+        accu[j] = 0.0f;
+        st_state[j] = 0;
+    }
+    for (int s = 0; s < ST; ++s) {                                // uniform
+        const int sl = s < S ? s : s - S, gi = sl / NST;
+        XL<NC> x;
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            const uint8_t * sj = slots + (gi * NC + j) * kFqSlot;
+            x.c[j] = reinterpret_cast<const int8_t *>(sj);
+            x.d[j] = reinterpret_cast<const float *>(sj + 256);
+            x.s[j] = reinterpret_cast<const int16_t *>(sj + 288);
+        }
+        if (s < S) T::dot(B, sl % NST, x, nc, acc, st_state);
+        else T::dot(B, sl % NST, x, nc, accu, st_state);
+        load_stage(s + 1);
+    }
+    // the W waves added in a fixed order (with the GLU both sums, then act(gate) * up)
+    const int64_t row = (int64_t)tile * kTileRows + lane;
+    float tot[NC];
+    if (p.W > 1) {
+        const int NV = glu ? 2 * NC : NC;
+        float * red = reinterpret_cast<float *>(sm);
+        __syncthreads();                                          // every wave is done with the slots
+#pragma unroll
+        for (int j = 0; j < NC; ++j) red[(wave * NV + j) * 64 + lane] = acc[j];
+        if (glu) {
+#pragma unroll
+            for (int j = 0; j < NC; ++j) red[(wave * NV + NC + j) * 64 + lane] = accu[j];
+        }
+        __syncthreads();
+        if (wave != 0) return;
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            float v = red[j * 64 + lane];
+            for (int ww = 1; ww < p.W; ++ww) v += red[(ww * NV + j) * 64 + lane];
+            if (glu) {
+                float u = red[(NC + j) * 64 + lane];
+                for (int ww = 1; ww < p.W; ++ww) u += red[(ww * NV + NC + j) * 64 + lane];
+                v = glu_apply(p.glu, v, u);
+            }
+            tot[j] = v;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < NC; ++j) tot[j] = glu ? glu_apply(p.glu, acc[j], accu[j]) : acc[j];
+    }
+    if (row >= p.w.M) return;
+#pragma unroll
+    for (int j = 0; j < NC; ++j)
+        if (j < nc) p.dst[doffv[j] + row] = tot[j];
+}
+
 }  // namespace
+
+bool gemv_fused_plan(int type, const WView & w, int nc, int64_t ntasks, int target, FusedPlan * pl) {
+    if (!type_layout(type) || nc < 1 || nc > 2 || ntasks <= 0 || w.G <= 0 || w.ntiles <= 0) return false;
+    const int64_t tiles = ntasks * w.ntiles;
+    int64_t W = std::min<int64_t>(std::min<int64_t>(kFqMaxWaves, w.G), std::max<int64_t>(1, (target + tiles - 1) / tiles));
+    const int64_t spw = (w.G + W - 1) / W;
+    W = (w.G + spw - 1) / spw;                                    // no wave without groups
+    pl->nc = nc;
+    pl->ntasks = ntasks;
+    pl->W = (int)W;
+    pl->spw = (int)spw;
+    pl->lds = std::max<int64_t>(W * spw * nc * kFqSlot, W * 2 * nc * 64 * 4);
+    return pl->lds <= 64 * 1024 && tiles < 0x7fffffff;
+}
+
+int gemv_fused_waves_target() { return std::max(1, env_int("QMM_GEMV_FQ_WAVES", 4096)); }
+
+hipError_t launch_gemv_fused(int type, const WView & w, const FusedPlan & pl, const FusedGemv & f, float * dst,
+                             const void * sink, hipStream_t s, const KTime * kt) {
+    if (!sink || !dst || pl.W < 1 || pl.W > kFqMaxWaves || pl.spw < 1 || pl.nc < 1 || pl.nc > 2 ||
+        (int64_t)pl.W * pl.spw < w.G || (int64_t)(pl.W - 1) * pl.spw >= w.G || f.K != w.K ||
+        (f.ids && (pl.nc != 1 || f.n_used < 1 || pl.ntasks != f.n_used * f.T || !f.bad_id)) ||
+        (f.glu > QMM_GLU_GEGLU_QUICK) || (f.glu >= 0 && !f.base2))
+        return hipErrorInvalidValue;
+    FqParams p{};
+    p.w = w;
+    p.x = f.x;
+    p.K = f.K;
+    p.dst = dst;
+    p.sink = (const uint8_t *)sink;
+    p.base2 = f.base2;
+    p.glu = f.glu;
+    p.W = pl.W;
+    p.spw = pl.spw;
+    if (f.ids) {
+        p.ids = f.ids;
+        p.ids_nb0 = f.ids_nb0;
+        p.ids_nb1 = f.ids_nb1;
+        p.n_used = f.n_used;
+        p.ne11i = f.ne11;
+        p.n_as = f.n_as;
+        p.dnb1 = f.dnb1;
+        p.dnb2 = f.dnb2;
+        p.bad_id = f.bad_id;
+    } else {
+        const GemvDense & d = f.dense;
+        p.ne11 = d.ne11;
+        p.ne12 = d.ne12;
+        p.r2 = d.r2;
+        p.r3 = d.r3;
+        p.ne02 = d.ne02;
+        p.col_bs = d.col_bs < 0 ? d.ne11 : d.col_bs;
+        p.tpb = (d.ne11 + pl.nc - 1) / pl.nc;
+        p.d_nb1 = d.d_nb1;
+        p.d_nb2 = d.d_nb2;
+        p.d_nb3 = d.d_nb3;
+        if (p.tpb * d.ne12 * d.ne13 != pl.ntasks) return hipErrorInvalidValue;
+    }
+    const int64_t nwg = pl.ntasks * w.ntiles;
+    if (nwg <= 0 || nwg >= 0x7fffffff) return hipErrorInvalidValue;
+    const dim3 g((unsigned)nwg), b(64 * pl.W);
+    const uint32_t lds = (uint32_t)pl.lds;
+#define QMM_FQ_K(...)                                                                              \
+    if (kt) hipExtLaunchKernelGGL(__VA_ARGS__, g, b, lds, s, kt->start, kt->stop, 0, p);            \
+    else __VA_ARGS__<<<g, b, lds, s>>>(p);                                                          \
+    return hipGetLastError();
+#define QMM_FQ(T)                                                                                   \
+    if (pl.nc == 1) { QMM_FQ_K(k_gemv_fq<T, 1>) }                                                   \
+    QMM_FQ_K(k_gemv_fq<T, 2>)
+    switch (type) {
+        case QMM_TYPE_Q4_0: { QMM_FQ(QMM_TYPE_Q4_0) }
+        case QMM_TYPE_Q8_0: { QMM_FQ(QMM_TYPE_Q8_0) }
+        case QMM_TYPE_Q4_K: { QMM_FQ(QMM_TYPE_Q4_K) }
+        case QMM_TYPE_Q5_K: { QMM_FQ(QMM_TYPE_Q5_K) }
+        case QMM_TYPE_Q6_K: { QMM_FQ(QMM_TYPE_Q6_K) }
+        case QMM_TYPE_IQ4_XS: { QMM_FQ(QMM_TYPE_IQ4_XS) }
+        case QMM_TYPE_IQ4_NL: { QMM_FQ(QMM_TYPE_IQ4_NL) }
+        default: return hipErrorInvalidValue;
+    }
+#undef QMM_FQ
+#undef QMM_FQ_K
+}
+
 
 bool gemv_mma_supported(int type) {
     return type == QMM_TYPE_Q4_0 || type == QMM_TYPE_Q8_0 || type == QMM_TYPE_Q4_K || type == QMM_TYPE_IQ4_XS ||

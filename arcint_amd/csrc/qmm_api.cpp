@@ -748,6 +748,40 @@ static int gemv_task_cols(int type, int64_t N) {
     return (int)((N + passes - 1) / passes);
 }
 
+// The fused-quantization GEMV (k_gemv_fq, no pre-pass launch).  MUL_MAT_ID of few tokens takes
+// it (its pairs need no route launch: 13.3 -> 6.0 us per op at config 3's T = 1).  Dense
+// products do not by default: with K split only among the waves of a work-group the chip runs
+// unbalanced (17408 x 5120 Q4_K: 272 work-groups of 10 waves on 256 CUs, kernel 15.8 us against
+// the split-K kernel's 12.7 us, whose pre-pass costs the op 0.8 us); QMM_GEMV_FQ_MIN_WAVES = n
+// takes it for 1-2 columns when its work-groups give the chip n waves or more.
+// QMM_GEMV_FUSED=0 switches the kernel off everywhere.
+static bool fused_on() {
+    const char * e = getenv("QMM_GEMV_FUSED");
+    return !e || atoi(e) != 0;
+}
+static int64_t fused_min_waves() {
+    const char * e = getenv("QMM_GEMV_FQ_MIN_WAVES");
+    return e ? atoll(e) : INT64_MAX;
+}
+// MUL_MAT_ID below this many tokens reads its ids per (slot, token) pair in the GEMV (no route;
+// the reference's per-pair matvec below 16 tokens, P01:1189-1192); QMM_MOE_DIRECT_T overrides
+static int64_t moe_direct_tokens() {
+    const char * e = getenv("QMM_MOE_DIRECT_T");
+    return e ? atoll(e) : 16;
+}
+
+// whether a dense product of N columns in nbatch batches takes the fused GEMV, and its plan
+static bool fused_dense_plan(int type, const WView & w, int64_t N, int64_t nbatch, FusedPlan * fp) {
+    if (!fused_on() || N > 2 || N < 1) return false;
+    if (!gemv_fused_plan(type, w, (int)N, nbatch, gemv_fused_waves_target(), fp)) return false;
+    return fp->ntasks * w.ntiles * fp->W >= fused_min_waves();
+}
+// whether a MUL_MAT_ID of T tokens with n_used ids each takes the fused GEMV's pairs, and its plan
+static bool fused_id_plan(int type, const WView & w, int64_t n_used, int64_t T, FusedPlan * fp) {
+    if (!fused_on() || T >= moe_direct_tokens()) return false;
+    return gemv_fused_plan(type, w, 1, n_used * T, gemv_fused_waves_target(), fp);
+}
+
 int qmm_describe_mul_mat(const qmm_tensor * src0, const qmm_tensor * src1, const qmm_tensor * dst, qmm_launch_info * out) {
     if (!out) return QMM_ERR_INVALID;
     memset(out, 0, sizeof(*out));
@@ -767,6 +801,20 @@ int qmm_describe_mul_mat(const qmm_tensor * src0, const qmm_tensor * src1, const
         out->k_slices = gemm_kslices(src0->type, w, N, out->tasks);
         return QMM_OK;
     }
+    FusedPlan fp;
+    if (fused_dense_plan(src0->type, w, N, src1->ne[2] * src1->ne[3], &fp)) {
+        snprintf(out->path, sizeof(out->path), "gemv-fq");
+        out->threads = 64 * fp.W;
+        out->cols_per_task = fp.nc;
+        out->tasks = fp.ntasks;
+        out->k_waves = fp.W;
+        out->tiles_per_wg = 1;
+        out->k_slices = 1;
+        out->groups_per_wave = fp.spw;
+        out->workgroups = fp.ntasks * w.ntiles;
+        out->lds_bytes = fp.lds;
+        return QMM_OK;
+    }
     const int nc = gemv_task_cols(src0->type, N);
     const int64_t ntasks = (N + nc - 1) / nc * src1->ne[2] * src1->ne[3];
     GemvPlan plan;
@@ -782,6 +830,56 @@ int qmm_describe_mul_mat(const qmm_tensor * src0, const qmm_tensor * src1, const
     out->workgroups = gemv_workgroups(w, plan);
     out->lds_bytes = (int64_t)gemv_lds_bytes(src0->type, plan);
     return QMM_OK;
+}
+
+// a dense fused launch when the shape suits it (false: not taken, nothing enqueued)
+static bool try_fused_dense(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1, const WView & w,
+                            const GemvDense & dn, float * d, const uint8_t * up_base, int glu, int * rc) {
+    FusedPlan fp;
+    if (!fused_dense_plan(src0->type, w, src1->ne[1], dn.ne12 * dn.ne13, &fp)) return false;
+    FusedGemv f{};
+    f.x = f32_cols(src1);
+    f.K = src1->ne[0];
+    f.dense = dn;
+    f.base2 = up_base;
+    f.glu = glu;
+    KTime kt;
+    const KTime * ktp = nullptr;
+    if ((*rc = ktime_pair(ctx, &kt, &ktp))) return true;
+    const hipError_t e = launch_gemv_fused(src0->type, w, fp, f, d, ctx->sink, ctx->stream, ktp);
+    *rc = e == hipSuccess ? QMM_OK : fail(ctx, QMM_ERR_DEVICE, "launch_gemv_fused: %s", hipGetErrorString(e));
+    return true;
+}
+
+// MUL_MAT_ID of few tokens with no route: the fused GEMV reads each (slot, token) pair's id
+// itself (false: not taken, nothing enqueued)
+static bool try_fused_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1, const qmm_tensor * ids,
+                         const qmm_tensor * dst, const WView & w, const uint8_t * up_base, int glu, int * rc) {
+    const int64_t n_used = ids->ne[0], T = ids->ne[1];
+    FusedPlan fp;
+    if (!fused_id_plan(src0->type, w, n_used, T, &fp)) return false;
+    FusedGemv f{};
+    f.x = f32_cols(src1);
+    f.K = src1->ne[0];
+    f.ids = (const char *)ids->buffer->ptr + ids->offs;
+    f.ids_nb0 = (int64_t)ids->nb[0];
+    f.ids_nb1 = (int64_t)ids->nb[1];
+    f.n_used = n_used;
+    f.T = T;
+    f.ne11 = src1->ne[1];
+    f.n_as = src0->ne[2];
+    f.dnb1 = (int64_t)(dst->nb[1] / 4);
+    f.dnb2 = (int64_t)(dst->nb[2] / 4);
+    f.bad_id = ctx->dflags;
+    f.base2 = up_base;
+    f.glu = glu;
+    KTime kt;
+    const KTime * ktp = nullptr;
+    if ((*rc = ktime_pair(ctx, &kt, &ktp))) return true;
+    float * d = (float *)((uint8_t *)dst->buffer->ptr + dst->offs);
+    const hipError_t e = launch_gemv_fused(src0->type, w, fp, f, d, ctx->sink, ctx->stream, ktp);
+    *rc = e == hipSuccess ? QMM_OK : fail(ctx, QMM_ERR_DEVICE, "launch_gemv_fused: %s", hipGetErrorString(e));
+    return true;
 }
 
 // The MUL_MAT after validation: the activation pre-pass, then the GEMV or the GEMM.  With
@@ -825,6 +923,10 @@ static int mul_mat_launch(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tens
         if (!fixed && (rc = ktime_pair(ctx, &kt, &ktp))) return rc;
         QMM_HIP(ctx, launch_gemm(src0->type, w, a, N, dn.ne12 * dn.ne13, bt, d, ctx->stream, ktp));
         return QMM_OK;
+    }
+    if (try_fused_dense(ctx, src0, src1, w, dn, d, nullptr, -1, &rc)) {
+        ctx->path = "gemv-fq";
+        return rc;
     }
     // up to 8 (v_dot4) or 32 (MFMA) columns per task against one weight pass
     const int nc = gemv_task_cols(src0->type, N);
@@ -935,6 +1037,10 @@ int qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * sr
     const int64_t npairs = ids->ne[0] * ids->ne[1];
     ActBuf a{};
     int rc;
+    if (try_fused_id(ctx, src0, src1, ids, dst, w, nullptr, -1, &rc)) {
+        ctx->path = "gemv-id-fq";
+        return rc;
+    }
     const int64_t max_tasks = route_max_tasks(npairs, n_as);
     const int nc = (int)std::min<int64_t>(kMaxTaskCols, npairs);
     GemvPlan plan;
@@ -989,6 +1095,10 @@ int qmm_mul_mat_id_glu(qmm_ctx * ctx, const qmm_tensor * gate, const qmm_tensor 
     const int64_t M = gate->ne[1], n_as = gate->ne[2], n_used = ids->ne[0], T = ids->ne[1], npairs = n_used * T;
     ActBuf a{};
     int rc;
+    if (try_fused_id(ctx, gate, src1, ids, dst, wg, wu.base, glu_op, &rc)) {
+        ctx->path = "glu-gemv-id-fq";
+        return rc;
+    }
     const int64_t max_tasks = route_max_tasks(npairs, n_as);
     const int nc = (int)std::min<int64_t>(kMaxTaskCols, npairs);
     const bool in_wg = max_tasks * wg.ntiles >= 1024;             // enough work-groups to fill the chip
@@ -1127,6 +1237,23 @@ int qmm_mul_mat_glu(qmm_ctx * ctx, const qmm_tensor * gate, const qmm_tensor * u
         return fail(ctx, QMM_ERR_UNSUPPORTED, "mul_mat_glu: up: %s", reason);
     if (memcmp(gate->ne, up->ne, sizeof(gate->ne))) return fail(ctx, QMM_ERR_INVALID, "mul_mat_glu: gate and up shapes differ");
     QMM_HIP(ctx, hipSetDevice(ctx->device));
+    if (up->type == gate->type) {                                 // one fused launch: gate, up and the GLU
+        GemvDense dn;
+        dn.ne11 = src1->ne[1];
+        dn.ne12 = src1->ne[2];
+        dn.ne13 = src1->ne[3];
+        dn.r2 = src1->ne[2] / gate->ne[2];
+        dn.r3 = src1->ne[3] / gate->ne[3];
+        dn.ne02 = gate->ne[2];
+        dn.d_nb1 = (int64_t)(dst->nb[1] / 4);
+        dn.d_nb2 = (int64_t)(dst->nb[2] / 4);
+        dn.d_nb3 = (int64_t)(dst->nb[3] / 4);
+        int frc;
+        if (try_fused_dense(ctx, gate, src1, wg, dn, (float *)((uint8_t *)dst->buffer->ptr + dst->offs), wu.base, glu_op, &frc)) {
+            ctx->path = "glu-fused-gemv-fq";
+            return frc;
+        }
+    }
     const int64_t M = gate->ne[1], N = src1->ne[1], ne12 = src1->ne[2], nb = src1->ne[2] * src1->ne[3];
     const size_t half = (size_t)(M * N * nb);
     int rc = ensure(ctx, &ctx->glu, &ctx->glu_cap, 2 * half * sizeof(float));
@@ -1218,11 +1345,25 @@ int qmm_internal_gemv_extent(int32_t type, const int64_t ne0[4], int64_t N, int6
     WView w{ nullptr, sh.M, sh.K, sh.bpr, sh.G, sh.ntiles, L->tg };
     GemvPlan plan;
     GemvExtent e[2];
+    FusedPlan fp;
+    // the fused kernel's loads are k_gemv's with one K slice: replayed through the same plan shape
+    auto as_plan = [&](const FusedPlan & f) {
+        plan = GemvPlan{};
+        plan.nc = f.nc;
+        plan.ntasks = f.ntasks;
+        plan.W = f.W;
+        plan.KS = 1;
+        plan.spw = f.spw;
+        plan.mma = false;
+        plan.tw = 1;
+        plan.cm = 8;
+    };
     if (id_n_used == 0) {
         if (N >= gemm_min_cols(type)) return QMM_ERR_UNSUPPORTED;
         const int nc = gemv_task_cols(type, N);
         const int64_t ntasks = (N + nc - 1) / nc * nbatch;
-        if (!gemv_plan(type, w, nc, ntasks, true, nc >= gemv_mma_min_cols(), &plan)) return QMM_ERR_UNSUPPORTED;
+        if (fused_dense_plan(type, w, N, nbatch, &fp)) as_plan(fp);
+        else if (!gemv_plan(type, w, nc, ntasks, true, nc >= gemv_mma_min_cols(), &plan)) return QMM_ERR_UNSUPPORTED;
         GemvDense dn;
         dn.ne11 = N;
         dn.ne12 = nbatch;
@@ -1237,7 +1378,8 @@ int qmm_internal_gemv_extent(int32_t type, const int64_t ne0[4], int64_t N, int6
         const int64_t n_as = sh.nmat, npairs = id_n_used * N;
         const int64_t max_tasks = route_max_tasks(npairs, n_as);
         const int nc = (int)std::min<int64_t>(kMaxTaskCols, npairs);
-        if (!gemv_plan(type, w, nc, max_tasks, false, npairs >= 2 * n_as, &plan)) return QMM_ERR_UNSUPPORTED;
+        if (fused_id_plan(type, w, id_n_used, N, &fp)) as_plan(fp);
+        else if (!gemv_plan(type, w, nc, max_tasks, false, npairs >= 2 * n_as, &plan)) return QMM_ERR_UNSUPPORTED;
         for (int i = 0; i < 2; ++i)
             if (!gemv_extent(type, w, plan, nullptr, n_as, i ? (int)(n_as - 1) : 0, &e[i])) return QMM_ERR_INVALID;
     }

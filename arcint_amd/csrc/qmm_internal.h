@@ -243,6 +243,33 @@ hipError_t launch_gemv(int type, const WView & w, const GemvPlan & plan, const A
                        const int32_t * ntasks_dev, const GemvDense * dense, float * dst, const void * sink,
                        hipStream_t s, const KTime * kt = nullptr, const GemvPair * pair = nullptr);
 
+// The v_dot4 GEMV with its own activation quantization (k_gemv_fq): no pre-pass, K split only
+// among the W waves of a work-group (at most 16), every output stored once.  nc = columns per
+// task (1 or 2).  Dense tasks as GemvDense; with ids, task p is the MUL_MAT_ID pair p = t n_used
+// + i (nc = 1).  glu >= 0: the work-group streams w (gate) then base2 (up) and stores
+// act(gate) * up.
+struct FusedGemv {
+    F32Cols x;                  // src1's f32 columns
+    int64_t K;
+    GemvDense dense;            // dense tasks (ids == nullptr)
+    const char * ids;           // MUL_MAT_ID: i32 ids, pair (i, t) at t ids_nb1 + i ids_nb0 bytes
+    int64_t ids_nb0, ids_nb1, n_used, T, ne11, n_as;
+    int64_t dnb1, dnb2;         // dst floats of pair (i, t): t dnb2 + i dnb1
+    int32_t * bad_id;           // set when an id is >= n_as
+    const uint8_t * base2;      // glu >= 0: the up image
+    int glu;
+};
+struct FusedPlan {
+    int nc, W, spw;
+    int64_t ntasks;
+    int64_t lds;
+};
+// about `target` waves over ntasks x tiles work-groups; false when the K range does not fit
+bool gemv_fused_plan(int type, const WView & w, int nc, int64_t ntasks, int target, FusedPlan * plan);
+int gemv_fused_waves_target();
+hipError_t launch_gemv_fused(int type, const WView & w, const FusedPlan & plan, const FusedGemv & f, float * dst,
+                             const void * sink, hipStream_t s, const KTime * kt = nullptr);
+
 // Prefill GEMM (int8 MFMA, all five types): for every batch b < nbatch,
 // dst[doff(b) + n * d_nb1 + m] = W(mat(b)) row m . activation column
 // col0(b) + n, for n < N, m < M.  Activations come from the pre-pass with

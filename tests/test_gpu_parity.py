@@ -793,7 +793,7 @@ def test_mul_mat_glu_full_size_decode(be, sc, orc):
     """config 2's FFN gate/up (17408 x 5120 Q4_K) at N = 1"""
     say("glu-full")
     got, ref = glu_case(be, sc, orc, qmm.Q4_K, qmm.Q4_K, 17408, 5120, 1, qmm.GLU_SWIGLU, seed=131)
-    assert be.last_path() == "glu-fused-gemv"
+    assert be.last_path().startswith("glu-fused-gemv")
     assert rel_err(got, ref) <= TOL
 
 
@@ -988,3 +988,130 @@ def test_downgrade_keys(sc, orc):
         assert keys == {"src=qmm op=MUL_MAT type=Q5_K k=512 cols=2-8 path=gemv reason=no-mfma-gemv": 2,
                         "src=qmm op=MUL_MAT type=Q4_K k=512 cols=33-128 path=gemv-mfma reason=several-weight-passes": 1}
         assert n == 3
+
+
+
+# ------------------------------------------------------------------ the fused-quantization GEMV
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("N", [1, 2])
+@pytest.mark.parametrize("M,K", [(300, 2048), (1, 256), (65, 5120), (63, 768), (130, 4352)])
+def test_fused_gemv(be, sc, orc, monkeypatch, qtype, N, M, K):
+    """k_gemv_fq (each wave quantizes its own groups; K split only inside the work-group) on
+    every type, forced onto small shapes; K = 4352 takes 17 groups, more than the work-group's 16
+    waves"""
+    monkeypatch.setenv("QMM_GEMV_FQ_MIN_WAVES", "1")
+    say("fused", qtype, M, K, N)
+    got, ref = run_mul_mat(be, sc, orc, qtype, M, K, N, seed=201)
+    assert be.last_path() == "gemv-fq"
+    assert rel_err(got, ref) <= TOL
+
+
+@pytest.mark.parametrize("qtype", [qmm.Q4_0, qmm.Q8_0, qmm.IQ4_NL])
+@pytest.mark.parametrize("K", [640, 416])
+def test_fused_gemv_partial_group(be, sc, orc, monkeypatch, qtype, K):
+    monkeypatch.setenv("QMM_GEMV_FQ_MIN_WAVES", "1")
+    say("fused partial group", qtype, K)
+    got, ref = run_mul_mat(be, sc, orc, qtype, 200, K, 2, seed=202)
+    assert be.last_path() == "gemv-fq"
+    assert rel_err(got, ref) <= TOL
+
+
+@pytest.mark.parametrize("qtype", [qmm.Q4_K, qmm.Q4_0, qmm.Q6_K])
+def test_fused_gemv_broadcast_strides_and_split_path(be, sc, orc, monkeypatch, qtype):
+    """broadcast batches, a strided src1 view and a padded dst on the fused kernel; the same
+    product on the pre-pass path (QMM_GEMV_FUSED=0) agrees"""
+    monkeypatch.setenv("QMM_GEMV_FQ_MIN_WAVES", "1")
+    say("fused broadcast", qtype)
+    K, M, N = 512, 80, 2
+    raw = synth.weights(qtype, 2 * M, K, seed=203)
+    w = sc.weights(qtype, raw, (K, M, 2))
+    x = synth.activations(8 * N, K, seed=204).reshape(4, 2 * N, K)        # every other column used
+    xt = sc.f32(x)
+    xv = qmm.Tensor(xt.buf, qmm.F32, (K, N, 4), nb=(4, 8 * K, 8 * K * N, 8 * K * N * 4))
+    ypad = sc.empty_f32((M + 5, N, 4))
+    yv = qmm.Tensor(ypad.buf, qmm.F32, (M, N, 4), nb=(4, 4 * (M + 5), 4 * (M + 5) * N, 4 * (M + 5) * N * 4))
+    be.mul_mat(w, xv, yv)
+    be.synchronize()
+    assert be.last_path() == "gemv-fq"
+    got = be.get_f32(ypad).reshape(4, N, M + 5)[:, :, :M].copy()
+    rb = synth.row_bytes(qtype, K) * M
+    for i2 in range(4):
+        assert rel_err(got[i2], orc.mul_mat(qtype, raw[(i2 // 2) * rb:(i2 // 2 + 1) * rb], M, K, x[i2, 0::2])) <= TOL
+    monkeypatch.setenv("QMM_GEMV_FUSED", "0")
+    be.mul_mat(w, xv, yv)
+    be.synchronize()
+    assert be.last_path() == "gemv"
+    assert rel_err(be.get_f32(ypad).reshape(4, N, M + 5)[:, :, :M], got) <= TOL
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("T", [1, 4, 15])
+@pytest.mark.parametrize("bcast", [True, False])
+def test_mul_mat_id_direct(be, sc, orc, qtype, T, bcast):
+    """MUL_MAT_ID below 16 tokens: each (slot, token) pair reads its expert id in the fused GEMV
+    (no route launch); a negative id writes a zero row, an id past the stack too and is reported
+    by synchronize"""
+    E, n_used, M, K = 16, 4, 96, 512
+    say("mul_mat_id direct", qtype, T, bcast)
+    raw = synth.weights(qtype, E * M, K, seed=205)
+    ids = synth.moe_ids(T, E, n_used, seed=206)
+    ids[0, 1] = -1
+    if T > 1:
+        ids[T - 1, 3] = E + 1
+    ne11 = 1 if bcast else n_used
+    x = synth.activations(T * ne11, K, seed=207).reshape(T, ne11, K)
+    w = sc.weights(qtype, raw, (K, M, E))
+    y = sc.f32(np.full((T, n_used, M), 9.0, np.float32))
+    be.mul_mat_id(w, sc.f32(x), sc.i32(ids), y)
+    assert be.last_path() == "gemv-id-fq"
+    if T > 1:
+        with pytest.raises(qmm.QmmError, match="past the expert count"):
+            be.synchronize()
+    be.synchronize()
+    got = be.get_f32(y).reshape(T, n_used, M)
+    bad = (ids < 0) | (ids >= E)
+    assert (got[bad] == 0).all()
+    assert rel_err(got[~bad], orc.mul_mat_id(qtype, raw, M, K, E, x, ids)[~bad]) <= TOL
+
+
+@pytest.mark.parametrize("qtype", [qmm.Q4_K, qmm.Q4_0, qmm.Q6_K])
+@pytest.mark.parametrize("T", [1, 4, 19])
+def test_mul_mat_id_route_and_direct_agree(be, sc, orc, monkeypatch, qtype, T):
+    """the same MUL_MAT_ID on the route (QMM_MOE_DIRECT_T=0) and on the pairs
+    (QMM_MOE_DIRECT_T=1000), gate/up + GLU included"""
+    from oracle import glu as G
+    E, n_used, M, K = 32, 6, 130, 512
+    say("mul_mat_id route vs direct", qtype, T)
+    rg, ru = synth.weights(qtype, E * M, K, seed=208), synth.weights(qtype, E * M, K, seed=209)
+    ids = synth.moe_ids(T, E, n_used, seed=210)
+    x = synth.activations(T, K, seed=211).reshape(T, 1, K)
+    wg, wu = sc.weights(qtype, rg, (K, M, E)), sc.weights(qtype, ru, (K, M, E))
+    xt, it = sc.f32(x), sc.i32(ids)
+    outs = {}
+    for direct in ("0", "1000"):
+        monkeypatch.setenv("QMM_MOE_DIRECT_T", direct)
+        y, yg = sc.empty_f32((M, n_used, T)), sc.empty_f32((M, n_used, T))
+        be.mul_mat_id(wg, xt, it, y)
+        p1 = be.last_path()
+        be.mul_mat_id_glu(wg, wu, xt, it, yg, qmm.GLU_SWIGLU)
+        p2 = be.last_path()
+        be.synchronize()
+        assert (p1 == "gemv-id-fq") == (direct != "0") and (p2 == "glu-gemv-id-fq") == (direct != "0"), (p1, p2)
+        outs[direct] = (be.get_f32(y).reshape(T, n_used, M), be.get_f32(yg).reshape(T, n_used, M))
+    ref = orc.mul_mat_id(qtype, rg, M, K, E, x, ids)
+    refg = G.glu(qmm.GLU_SWIGLU, ref, orc.mul_mat_id(qtype, ru, M, K, E, x, ids))
+    for direct, (a, b) in outs.items():
+        assert rel_err(a, ref) <= TOL, direct
+        assert rel_err(b, refg) <= TOL, direct
+
+
+@pytest.mark.parametrize("op", GLU_OPS)
+@pytest.mark.parametrize("qtype", [qmm.Q4_K, qmm.Q5_K, qmm.IQ4_NL])
+def test_mul_mat_glu_fused_kernel(be, sc, orc, monkeypatch, op, qtype):
+    """gate/up + GLU on the fused kernel: each work-group streams the gate tile, then the up tile,
+    and stores act(gate) * up"""
+    monkeypatch.setenv("QMM_GEMV_FQ_MIN_WAVES", "1")
+    say("glu fused kernel", op, qtype)
+    got, ref = glu_case(be, sc, orc, qtype, qtype, 200, 1024, 2, op, seed=212, batches=(2, 1))
+    assert be.last_path() == "glu-fused-gemv-fq"
+    assert rel_err(got, ref) <= TOL

@@ -241,8 +241,18 @@ def test_gemv_plan(qtype, K, M, N):
     # the MFMA kernel takes 3 and more columns of the types whose blocks it decodes, up to 32 a
     # weight pass; v_dot4 8; the columns spread evenly over the fewest passes
     mma = N >= 3 and qtype in (qmm.Q4_0, qmm.Q8_0, qmm.Q4_K, qmm.IQ4_XS, qmm.IQ4_NL, qmm.Q6_K)
-    assert info["path"] == ("gemv-mfma" if mma else "gemv")
     G, nt = -(-K // 256), -(-M // 64)
+    if info["path"] == "gemv-fq":
+        # the fused-quantization kernel: 1-2 columns, one work-group per 64-row tile and task, K
+        # split among its (up to 16) waves only, enough waves to fill the chip; LDS holds each
+        # wave's quantized groups (320 B per group and column), then the waves' sums
+        W, spw, nc = info["k_waves"], info["groups_per_wave"], info["cols_per_task"]
+        assert N <= 2 and nc == N and info["k_slices"] == 1 and info["tasks"] == 1
+        assert 1 <= W <= 16 and W * spw >= G and (W - 1) * spw < G
+        assert info["workgroups"] == nt and info["threads"] == 64 * W
+        assert info["lds_bytes"] == max(W * spw * nc * 320, W * 2 * nc * 64 * 4)
+        return
+    assert info["path"] == ("gemv-mfma" if mma else "gemv")
     W, KS, spw, nc = info["k_waves"], info["k_slices"], info["groups_per_wave"], info["cols_per_task"]
     cap = 32 if mma else 8
     assert nc == -(-N // -(-N // cap))
