@@ -130,20 +130,20 @@ __global__ __launch_bounds__(kRouteThreads) void k_quant_route(F32Cols src, int6
 // ---- the router: softmax -> top-k -> normalized weights ------------------------------------
 // Role of the reference's fused router (kernel_topk_moe_softmax_norm, P09:899-1000), which
 // replaces llama.cpp's gating chain SOFT_MAX, ARGSORT (desc), VIEW, GET_ROWS, SUM_ROWS, CLAMP,
-// DIV (matched at P02:786-821); the selection here is a threshold search, not repeated arg-max
+// DIV (matched at P02:786-821); the selection here is a filter and a count, not repeated arg-max
 // rounds.  One wave per token (a one-wave work-group); lane l holds the logits of the NPER
 // consecutive experts [l NPER, (l + 1) NPER).  Softmax is monotone, so the winners are the k
 // largest logits, equal logits ordered by expert (the order of the probabilities, which the
 // float32 exp could otherwise merge into ties):
-//  1. each logit becomes an order-preserving 32-bit key; padding lanes get key 0, below every
-//     real key;
-//  2. the k-th largest key tau is found most-significant bit first: 32 steps, each counting the
-//     keys at or above a candidate with one ballot per register (the count is uniform);
-//  3. every key above tau wins, and of the keys equal to tau the lowest experts, counted in
-//     expert order by an exclusive scan of the lanes' tie counts, until there are k;
-//  4. the k winners go to LDS at the offsets of a scan of the lanes' win counts, and each of
-//     the first k lanes counts the winners ahead of its own (larger key, or equal key and lower
-//     expert): its rank in the output.
+//  1. each logit becomes an order-preserving 32-bit key; padding gets key 0, below every real
+//     key;
+//  2. the filter: tau0 = the k-th largest of the 64 lanes' largest keys, found most-significant
+//     bit first (32 steps of one ballot).  The lanes holding the k largest maxima hold k keys
+//     >= tau0, so every winner is >= tau0;
+//  3. the candidates (keys >= tau0; usually a few more than k) go to LDS at the offsets of a
+//     scan of the lanes' counts, in expert order;
+//  4. each candidate counts the candidates ahead of it (larger key, or equal key and lower
+//     expert): those with fewer than k ahead win, at that rank.
 // Weights: exp(x - max) / sum over all experts (a wave sum), divided by the winners' sum, taken
 // in rank order and clamped to [cmin, cmax].
 
@@ -169,20 +169,13 @@ __device__ __forceinline__ float wave_sum_f(float v) {
     return v;
 }
 
-// number of register values of the wave with pred true (uniform)
-template <int NPER, typename F>
-__device__ __forceinline__ int wave_count(F pred) {
-    int c = 0;
-#pragma unroll
-    for (int j = 0; j < NPER; ++j) c += __popcll(__ballot(pred(j)));
-    return c;
-}
+constexpr int kTopkMaxExperts = 1024;
 
 template <int NPER>
 __global__ __launch_bounds__(64) void k_topk(TopkArgs a) {
-    __shared__ uint32_t win_key[32];
-    __shared__ int win_exp[32];
-    __shared__ float win_p[32], ranked_p[32];
+    __shared__ uint32_t cand_key[kTopkMaxExperts];
+    __shared__ int cand_exp[kTopkMaxExperts];
+    __shared__ float ranked_p[32];
     const int lane = threadIdx.x;
     const int64_t t = blockIdx.x;
     const float * x = reinterpret_cast<const float *>(a.logits + t * a.nbl1);
@@ -190,12 +183,14 @@ __global__ __launch_bounds__(64) void k_topk(TopkArgs a) {
     float v[NPER];
     uint32_t key[NPER];
     float mx = -INFINITY;
+    uint32_t kmax = 0;
 #pragma unroll
     for (int j = 0; j < NPER; ++j) {
         const bool live = e0 + j < a.n_expert;
         v[j] = live ? x[e0 + j] : -INFINITY;
         key[j] = live ? order_key(v[j]) : 0u;
         mx = fmaxf(mx, v[j]);
+        kmax = key[j] > kmax ? key[j] : kmax;
     }
     const float m = wave_max(mx);
     float part = 0.0f;
@@ -203,54 +198,53 @@ __global__ __launch_bounds__(64) void k_topk(TopkArgs a) {
     for (int j = 0; j < NPER; ++j)
         if (e0 + j < a.n_expert) part += expf(v[j] - m);
     const float S = wave_sum_f(part);
-    // 2. tau: the largest key with at least k keys at or above it
-    uint32_t tau = 0;
+    // 2. tau0: the largest value with at least k lane maxima at or above it
+    uint32_t tau0 = 0;
     for (int b = 31; b >= 0; --b) {
-        const uint32_t cand = tau | (1u << b);
-        if (wave_count<NPER>([&](int j) { return key[j] >= cand; }) >= k) tau = cand;
+        const uint32_t c = tau0 | (1u << b);
+        if (__popcll(__ballot(kmax >= c)) >= k) tau0 = c;
     }
-    // 3. winners: keys above tau, then ties at tau in expert order
-    const int need = k - wave_count<NPER>([&](int j) { return key[j] > tau; });   // >= 1
-    int ties = 0;
+    // 3. the candidates into LDS, in expert order
+    int nc = 0;
 #pragma unroll
-    for (int j = 0; j < NPER; ++j) ties += key[j] == tau;
-    int tie_rank = lane_scan(ties, lane) - ties;                  // ties at lower experts
-    bool win[NPER];
-    int nwin = 0;
+    for (int j = 0; j < NPER; ++j) nc += key[j] >= tau0;
+    int slot = lane_scan(nc, lane) - nc;
+    const int ncand = __shfl(slot + nc, 63, 64);
 #pragma unroll
     for (int j = 0; j < NPER; ++j) {
-        win[j] = key[j] > tau;
-        if (key[j] == tau) win[j] = tie_rank++ < need;
-        nwin += win[j];
-    }
-    // 4. compaction into LDS, then each winner's rank
-    int slot = lane_scan(nwin, lane) - nwin;
-#pragma unroll
-    for (int j = 0; j < NPER; ++j) {
-        if (win[j]) {
-            win_key[slot] = key[j];
-            win_exp[slot] = e0 + j;
-            win_p[slot] = expf(v[j] - m) / S;
+        if (key[j] >= tau0) {
+            cand_key[slot] = key[j];
+            cand_exp[slot] = e0 + j;
             ++slot;
         }
     }
     __syncthreads();
-    int rank = 0, my_exp = 0;
-    float my_p = 0.0f;
-    if (lane < k) {
-        const uint32_t ku = win_key[lane];
-        my_exp = win_exp[lane];
-        my_p = win_p[lane];
-        for (int i = 0; i < k; ++i) rank += win_key[i] > ku || (win_key[i] == ku && win_exp[i] < my_exp);
-        ranked_p[rank] = my_p;
+    // 4. each candidate's rank; the first k are the winners (their probabilities summed in
+    // rank order below)
+    int my_rank[kTopkMaxExperts / 64], my_exp[kTopkMaxExperts / 64];
+    float my_p[kTopkMaxExperts / 64];
+    int nmine = 0;
+    for (int c = lane; c < ncand; c += 64) {
+        const uint32_t ku = cand_key[c];
+        const int ke = cand_exp[c];
+        int r = 0;
+        for (int i = 0; i < ncand && r < k; ++i) r += cand_key[i] > ku || (cand_key[i] == ku && cand_exp[i] < ke);
+        if (r < k) {
+            const float p = expf(x[ke] - m) / S;
+            ranked_p[r] = p;
+            my_rank[nmine] = r;
+            my_exp[nmine] = ke;
+            my_p[nmine] = p;
+            ++nmine;
+        }
     }
     __syncthreads();
     float wsum = 0.0f;
-    for (int i = 0; i < k; ++i) wsum += ranked_p[i];              // uniform, in rank order
-    if (lane < k) {
-        const float c = fminf(fmaxf(wsum, a.cmin), a.cmax);
-        reinterpret_cast<int32_t *>(a.ids + t * a.nbi1)[rank] = my_exp;
-        reinterpret_cast<float *>(a.w + t * a.nbw1)[rank] = my_p / c;
+    for (int i = 0; i < k; ++i) wsum += ranked_p[i];               // uniform, in rank order
+    const float cl = fminf(fmaxf(wsum, a.cmin), a.cmax);
+    for (int q = 0; q < nmine; ++q) {
+        reinterpret_cast<int32_t *>(a.ids + t * a.nbi1)[my_rank[q]] = my_exp[q];
+        reinterpret_cast<float *>(a.w + t * a.nbw1)[my_rank[q]] = my_p[q] / cl;
     }
 }
 

@@ -81,6 +81,8 @@ struct qmm_ctx {
     uint8_t * fixed_scratch = nullptr;
     // main-kernel timing (qmm_kernel_timing)
     bool ktime = false;
+    bool ktime_markers = false;    // event records around the launch instead of dispatch stamps
+    hipEvent_t ktime_stop = nullptr;   // marker mode: the stop event of the launch just made
     std::vector<hipEvent_t> kev;   // pairs
     size_t kev_used = 0;
 };
@@ -356,7 +358,22 @@ int ktime_pair(qmm_ctx * ctx, KTime * kt, const KTime ** out) {
     kt->start = ctx->kev[ctx->kev_used];
     kt->stop = ctx->kev[ctx->kev_used + 1];
     ctx->kev_used += 2;
+    if (ctx->ktime_markers) {                                     // the caller launches next
+        QMM_HIP(ctx, hipEventRecord(kt->start, ctx->stream));
+        ctx->ktime_stop = kt->stop;
+        return QMM_OK;
+    }
     *out = kt;
+    return QMM_OK;
+}
+
+// after the main kernel's launch: in marker mode, the stop event
+int ktime_done(qmm_ctx * ctx) {
+    if (ctx->ktime_stop) {
+        const hipEvent_t e = ctx->ktime_stop;
+        ctx->ktime_stop = nullptr;
+        QMM_HIP(ctx, hipEventRecord(e, ctx->stream));
+    }
     return QMM_OK;
 }
 
@@ -770,10 +787,22 @@ static int64_t moe_direct_tokens() {
     return e ? atoll(e) : 16;
 }
 
+// Small dense products are the exception: at most 8 groups along K (one per wave) and 512
+// tile-groups in all, the op is launch latency and one launch beats two (config 3's shared
+// expert, N = 1: gate + up + SwiGLU 512 x 2048 9.1 -> 6.4 us, down 2048 x 512 6.8 -> 4.4 us;
+// at 16 groups the fused kernel lost, Q4_0 2048 x 4096 7.5 against 6.5 us).
+// QMM_GEMV_FQ_SMALL_TG sets the tile-group bound (0: never).
+static int64_t fused_small_tgroups() {
+    const char * e = getenv("QMM_GEMV_FQ_SMALL_TG");
+    return e ? atoll(e) : 512;
+}
+
 // whether a dense product of N columns in nbatch batches takes the fused GEMV, and its plan
 static bool fused_dense_plan(int type, const WView & w, int64_t N, int64_t nbatch, FusedPlan * fp) {
     if (!fused_on() || N > 2 || N < 1) return false;
     if (!gemv_fused_plan(type, w, (int)N, nbatch, gemv_fused_waves_target(), fp)) return false;
+    const int64_t tgroups = fp->ntasks * w.ntiles * w.G;
+    if (w.G <= 8 && tgroups <= fused_small_tgroups()) return true;
     return fp->ntasks * w.ntiles * fp->W >= fused_min_waves();
 }
 // whether a MUL_MAT_ID of T tokens with n_used ids each takes the fused GEMV's pairs, and its plan
@@ -847,7 +876,7 @@ static bool try_fused_dense(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_te
     const KTime * ktp = nullptr;
     if ((*rc = ktime_pair(ctx, &kt, &ktp))) return true;
     const hipError_t e = launch_gemv_fused(src0->type, w, fp, f, d, ctx->sink, ctx->stream, ktp);
-    *rc = e == hipSuccess ? QMM_OK : fail(ctx, QMM_ERR_DEVICE, "launch_gemv_fused: %s", hipGetErrorString(e));
+    *rc = e == hipSuccess ? ktime_done(ctx) : fail(ctx, QMM_ERR_DEVICE, "launch_gemv_fused: %s", hipGetErrorString(e));
     return true;
 }
 
@@ -878,7 +907,7 @@ static bool try_fused_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tenso
     if ((*rc = ktime_pair(ctx, &kt, &ktp))) return true;
     float * d = (float *)((uint8_t *)dst->buffer->ptr + dst->offs);
     const hipError_t e = launch_gemv_fused(src0->type, w, fp, f, d, ctx->sink, ctx->stream, ktp);
-    *rc = e == hipSuccess ? QMM_OK : fail(ctx, QMM_ERR_DEVICE, "launch_gemv_fused: %s", hipGetErrorString(e));
+    *rc = e == hipSuccess ? ktime_done(ctx) : fail(ctx, QMM_ERR_DEVICE, "launch_gemv_fused: %s", hipGetErrorString(e));
     return true;
 }
 
@@ -922,7 +951,7 @@ static int mul_mat_launch(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tens
         ctx->path = "gemm-mfma";
         if (!fixed && (rc = ktime_pair(ctx, &kt, &ktp))) return rc;
         QMM_HIP(ctx, launch_gemm(src0->type, w, a, N, dn.ne12 * dn.ne13, bt, d, ctx->stream, ktp));
-        return QMM_OK;
+        return ktime_done(ctx);
     }
     if (try_fused_dense(ctx, src0, src1, w, dn, d, nullptr, -1, &rc)) {
         ctx->path = "gemv-fq";
@@ -946,7 +975,7 @@ static int mul_mat_launch(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tens
                        (long long)w.K, cols_bucket(N));
     if (!fixed && (rc = ktime_pair(ctx, &kt, &ktp))) return rc;
     QMM_HIP(ctx, launch_gemv(src0->type, w, plan, a, nullptr, nullptr, &dn, d, ctx->sink, ctx->stream, ktp));
-    return QMM_OK;
+    return ktime_done(ctx);
 }
 
 int qmm_mul_mat(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1, const qmm_tensor * dst) {
@@ -1064,7 +1093,7 @@ int qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * sr
     const KTime * ktp;
     if ((rc = ktime_pair(ctx, &kt, &ktp))) return rc;
     QMM_HIP(ctx, launch_gemv(src0->type, w, plan, a, tasks, ntasks, nullptr, d, ctx->sink, ctx->stream, ktp));
-    return QMM_OK;
+    return ktime_done(ctx);
 }
 
 // MUL_MAT_ID (gate experts), MUL_MAT_ID (up experts) and the GLU, the MoE form of
@@ -1130,6 +1159,7 @@ int qmm_mul_mat_id_glu(qmm_ctx * ctx, const qmm_tensor * gate, const qmm_tensor 
     if ((rc = ktime_pair(ctx, &kt, &ktp))) return rc;
     QMM_HIP(ctx, launch_gemv(gate->type, wg, plan, a, tasks, ntasks, nullptr, in_wg ? d : sg, ctx->sink, ctx->stream, ktp,
                              &pair));
+    if ((rc = ktime_done(ctx))) return rc;
     if (in_wg) return QMM_OK;
     GluArgs g;
     g.gate = sg;
@@ -1283,6 +1313,7 @@ int qmm_mul_mat_glu(qmm_ctx * ctx, const qmm_tensor * gate, const qmm_tensor * u
         const KTime * ktp;
         if ((rc = ktime_pair(ctx, &kt, &ktp))) return rc;
         QMM_HIP(ctx, launch_gemv(type, wg, plan, a, nullptr, nullptr, &dn, sg, ctx->sink, ctx->stream, ktp));
+        if ((rc = ktime_done(ctx))) return rc;
         ctx->path = plan.mma ? "glu-fused-gemv-mfma" : "glu-fused-gemv";
     } else {
         qmm_buffer sb;
@@ -1491,11 +1522,25 @@ int64_t qmm_downgrades(qmm_ctx * ctx, char * buf, size_t buf_len) {
 }
 
 int qmm_kernel_timing(qmm_ctx * ctx, int enable) {
-    if (!ctx) return QMM_ERR_INVALID;
+    if (!ctx || enable < 0 || enable > 2) return QMM_ERR_INVALID;
     QMM_HIP(ctx, hipStreamSynchronize(ctx->stream));
     ctx->ktime = enable != 0;
+    ctx->ktime_markers = enable == 2;
+    ctx->ktime_stop = nullptr;
     ctx->kev_used = 0;
     return QMM_OK;
+}
+
+int64_t qmm_kernel_times(qmm_ctx * ctx, double * ms, int64_t cap) {
+    if (!ctx || (cap > 0 && !ms)) return -1;
+    if (hipStreamSynchronize(ctx->stream) != hipSuccess) return -1;
+    const int64_t n = (int64_t)(ctx->kev_used / 2);
+    for (int64_t i = 0; i < n && i < cap; ++i) {
+        float t = 0.0f;
+        if (hipEventElapsedTime(&t, ctx->kev[2 * i], ctx->kev[2 * i + 1]) != hipSuccess) return -1;
+        ms[i] = t;
+    }
+    return n;
 }
 
 int qmm_kernel_time(qmm_ctx * ctx, double * total_ms, int64_t * launches) {

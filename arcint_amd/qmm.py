@@ -35,7 +35,7 @@ EXPORTS = (
     "qmm_graph_compute", "qmm_dequantize", "qmm_quantize_act", "qmm_synchronize", "qmm_downgrades",
     "qmm_last_path", "qmm_timer_begin", "qmm_timer_end", "qmm_buffer_copy", "qmm_kernel_timing",
     "qmm_kernel_time", "qmm_tensor_pack", "qmm_tensor_unpack", "qmm_describe_mul_mat", "qmm_moe_topk",
-    "qmm_moe_combine", "qmm_mul_mat_glu", "qmm_mul_mat_id_glu", "qmm_mul_mat_noalloc",
+    "qmm_moe_combine", "qmm_mul_mat_glu", "qmm_mul_mat_id_glu", "qmm_mul_mat_noalloc", "qmm_kernel_times",
 )
 NOALLOC_SCRATCH_BYTES = 16 << 20     # QMM_NOALLOC_SCRATCH_BYTES
 
@@ -115,6 +115,8 @@ def load() -> C.CDLL:
         L.qmm_buffer_copy.argtypes = [vp, vp, sz, vp, sz, sz]
         L.qmm_kernel_timing.argtypes = [vp, C.c_int]
         L.qmm_kernel_time.argtypes = [vp, C.POINTER(C.c_double), C.POINTER(i64)]
+        L.qmm_kernel_times.argtypes = [vp, C.POINTER(C.c_double), i64]
+        L.qmm_kernel_times.restype = i64
         L.qmm_tensor_pack.argtypes = [i32, C.POINTER(i64), vp, vp, sz]
         L.qmm_describe_mul_mat.argtypes = [T, T, T, C.POINTER(LaunchInfo)]
         L.qmm_tensor_unpack.argtypes = [i32, C.POINTER(i64), vp, vp, sz]
@@ -364,8 +366,20 @@ class Backend:
             raise QmmError("timer_end failed")
         return ms
 
-    def kernel_timing(self, enable: bool):
-        self._check(self.L.qmm_kernel_timing(self.h, 1 if enable else 0), "kernel_timing")
+    def kernel_timing(self, enable, markers: bool = False):
+        """start (enable) or stop stamping the ops' main kernels: dispatch stamps, or with
+        markers event records on the stream around each launch"""
+        self._check(self.L.qmm_kernel_timing(self.h, (2 if markers else 1) if enable else 0), "kernel_timing")
+
+    def kernel_times(self) -> np.ndarray:
+        """milliseconds of each main-kernel launch since kernel_timing(True)"""
+        n = self.L.qmm_kernel_times(self.h, None, 0)
+        if n < 0:
+            raise QmmError("kernel_times failed")
+        out = np.zeros(max(n, 1), np.float64)
+        if self.L.qmm_kernel_times(self.h, out.ctypes.data_as(C.POINTER(C.c_double)), n) != n:
+            raise QmmError("kernel_times failed")
+        return out[:n]
 
     def kernel_time(self) -> tuple[float, int]:
         """(summed ms, launches) of the main kernels since kernel_timing(True)"""

@@ -8,22 +8,26 @@ copies (>= 2 x the 256 MB Infinity Cache), so the bytes come from HBM.
 Algorithmic bytes per step = weight block bytes + K*N*4 (x) + M*N*4 (dst).
 
 Also reported, on the same JSON line:
-  roofline      the GEMV kernel's own duration (HIP events around each launch
-                on the library's stream, a second pass of the same loop) ->
-                achieved GB/s against 8 TB/s, plus HBM traffic per launch
-                from profiles/ when the rocprofv3 PMC runs were committed
+  roofline      the GEMV kernel's own duration: the median over the timed
+                region's launches of a HIP event pair stamped by each
+                dispatch on the library's stream (a second pass of the same
+                loop), cross-checked by event records placed on the stream
+                around each launch -> achieved GB/s against 8 TB/s; HBM
+                traffic per launch from the committed rocprofv3 PMC runs
   cpu_baseline  the CPU oracle (a C restatement of ggml-cpu's algorithm,
-                kind "port") on the same op, bounded to ~--cpu-seconds
+                kind "port") on the same op on the cores this process may use
+                (at most 16, the host share of a one-GPU box), median of its
+                reps, with nproc and a single-thread figure
   gemm          prefill MUL_MAT at N = 512: Q4_0 4096x4096 and 11008x4096
                 (config 1), Q4_K 17408x5120 (config 2), in TOPS vs the dense
                 int8 MFMA peak ("secondary" repeats the first)
-  gemv          decode and few-column MUL_MAT: Q4_0 4096x4096 and Q6_K
-                5120x17408 at N = 1, Q4_K 17408x5120 at N = 4, IQ4_XS and Q8_0
-                14336x4096 at N = 2, 4, 8 (configs 0, 2, 4): GB/s and the
-                kernel's fraction of 8 TB/s
-  moe           MUL_MAT_ID on config 3 (512 Q4_K experts, top-10) at T = 1,
-                4, 256 tokens: GB/s of the expert weights each step touches; with
-                the router (softmax / top-10) and the combine (hidden 2048) per op
+  gemv          decode and few-column MUL_MAT of configs 0, 2 and 4: GB/s and
+                the kernel's fraction of 8 TB/s
+  moe           config 3's whole MoE layer at T = 1, 4, 256 tokens (router,
+                gate + up + SwiGLU over 512 Q4_K experts, down, the shared
+                expert, the combine), rotated over two layers' expert stacks
+                (1.8 GB): GB/s of the expert weights each step touches, against
+                the layer's HBM roofline, and each op's own time
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
@@ -65,13 +69,24 @@ def run_mul_mat(be, ws, xt, yt, steps):
         be.mul_mat(ws[i % len(ws)], xt, yt)
 
 
+def kernel_medians(be, fn, steps):
+    """Median main-kernel duration (ms) of `steps` calls of fn(i): stamped by each dispatch,
+    then placed as event records on the stream around each launch (two more passes)."""
+    out = []
+    for markers in (False, True):
+        be.kernel_timing(True, markers=markers)
+        for i in range(steps):
+            fn(i)
+        t = be.kernel_times()
+        be.kernel_timing(False)
+        out.append(float(np.median(t)) if t.size else float("nan"))
+    return out
+
+
 def time_op(be, ws, xt, yt, steps, warmup):
-    """Timed region: `steps` ops between a stream synchronize on both sides,
-    uninstrumented (value).  Then the same `steps` ops again with every main
-    kernel (GEMV / GEMM) stamping a HIP event pair with its own dispatch start
-    and end on the library's stream: the kernel's average duration for the
-    roofline (stamping every launch slows the host side, so it stays out of
-    the timed region)."""
+    """Timed region: `steps` ops between a stream synchronize on both sides, uninstrumented
+    (value).  Then the kernel's own median duration from two more passes (stamping every
+    launch slows the host side, so it stays out of the timed region)."""
     run_mul_mat(be, ws, xt, yt, warmup)
     be.synchronize()
     t0 = time.perf_counter()
@@ -79,11 +94,14 @@ def time_op(be, ws, xt, yt, steps, warmup):
     run_mul_mat(be, ws, xt, yt, steps)
     dev_ms = be.timer_end()
     wall = time.perf_counter() - t0
-    be.kernel_timing(True)
-    run_mul_mat(be, ws, xt, yt, steps)
-    k_ms, n = be.kernel_time()
-    be.kernel_timing(False)
-    return wall, dev_ms, k_ms / max(n, 1)
+    k_disp, k_mark = kernel_medians(be, lambda i: be.mul_mat(ws[i % len(ws)], xt, yt), steps)
+    return wall, dev_ms, k_disp, k_mark
+
+
+def kernel_ms(k_disp, k_mark, op_ms):
+    """The kernel time a roofline uses: the dispatch stamps, unless they exceed the op's own
+    time per step (then the stream markers, which bound it from above)"""
+    return k_disp if k_disp <= op_ms else k_mark
 
 
 def profile_traffic(kernel_tag):
@@ -99,38 +117,52 @@ def profile_traffic(kernel_tag):
 
 
 def cpu_baseline(orc, qtype, raw, M, K, x, budget_s):
-    threads = min(os.cpu_count() or 1, 16)
+    """The oracle on the cores this process may use (at most 16) and on one core: median GB/s
+    of its reps (at least 5, about budget_s seconds in all)."""
+    nproc = os.cpu_count() or 1
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else nproc
+    threads = max(1, min(16, avail))
     nbytes = raw.nbytes + K * 4 + M * 4
-    orc.mul_mat(qtype, raw, M, K, x, threads=threads)     # warm
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        orc.mul_mat(qtype, raw, M, K, x, threads=threads)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s:
-            break
-    return {"value": round(nbytes * reps / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"Q4_K {M}x{K} N=1 MUL_MAT x{reps} reps ({el:.1f} s, {threads} threads) with the C oracle "
-                      f"(ggml-cpu's algorithm restated in C, -O3 -mavx2; q8_K quantization included)"}
+
+    def reps(nthreads, budget, at_least):
+        orc.mul_mat(qtype, raw, M, K, x, threads=nthreads)    # warm
+        times = []
+        while len(times) < at_least or sum(times) < budget:
+            t0 = time.perf_counter()
+            orc.mul_mat(qtype, raw, M, K, x, threads=nthreads)
+            times.append(time.perf_counter() - t0)
+        return times
+
+    tm = reps(threads, 0.8 * budget_s, 5)
+    t1 = reps(1, 0.2 * budget_s, 5)
+    med, med1 = float(np.median(tm)), float(np.median(t1))
+    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "nproc": nproc, "cores_available": avail,
+            "single_thread": {"value": round(nbytes / med1 / 1e9, 3), "unit": "GB/s", "cores": 1, "reps": len(t1)},
+            "sample": f"Q4_K {M}x{K} N=1 MUL_MAT, median of {len(tm)} reps ({sum(tm):.1f} s) on {threads} threads "
+                      f"(nproc {nproc}, {avail} available to the process) with the C oracle (ggml-cpu's algorithm "
+                      f"restated in C, -O3 -mavx2; q8_K quantization included); single thread: median of {len(t1)} reps"}
 
 
 def gemm_case(be, qmm, synth, qtype, M, K, N, name, args, traffic_tag):
     """One prefill MUL_MAT (activation pre-pass + GEMM) over rotated weight
-    copies: op TOPS (timed region), GEMM kernel TOPS (dispatch-stamped) and
-    its fraction of the dense int8 MFMA peak."""
+    copies: op TOPS (timed region), GEMM kernel TOPS (median dispatch-stamped
+    duration) and its fraction of the dense int8 MFMA peak."""
     raw, ws = weight_copies(be, qmm, synth, qtype, M, K, seed=2)
     x = synth.activations(N, K, seed=3)
     xt = be.new_tensor(qmm.F32, (K, N))
     be.set_tensor(xt, x.view(np.uint8).ravel())
     yt = be.new_tensor(qmm.F32, (M, N))
-    steps = max(5, args.steps // 10)
-    wall, dev, k = time_op(be, ws, xt, yt, steps, max(2, args.warmup // 4))
+    steps = max(20, args.steps // 10)
+    wall, dev, kd, km = time_op(be, ws, xt, yt, steps, max(2, args.warmup // 4))
+    op_ms = wall * 1e3 / steps
+    k = kernel_ms(kd, km, op_ms)
     ops = 2.0 * M * N * K
     sec = {"workload": name, "path": be.last_path(),
            "tops": round(ops * steps / wall / 1e12, 3),
            "kernel_tops": round(ops / (k * 1e-3) / 1e12, 3),
            "frac_int8_peak": round(ops / (k * 1e-3) / 1e12 / INT8_PEAK_TOPS, 5),
-           "ms_per_op": round(wall * 1e3 / steps, 4), "kernel_ms": round(k, 4),
+           "ms_per_op": round(op_ms, 4), "kernel_ms": round(k, 4), "kernel_ms_markers": round(km, 4),
            "traffic": profile_traffic(traffic_tag)}
     for w in ws:
         be.free_buffer(w.buf)
@@ -142,18 +174,21 @@ def gemm_case(be, qmm, synth, qtype, M, K, N, name, args, traffic_tag):
 def gemv_case(be, qmm, synth, qtype, M, K, N, name, args):
     """One decode / few-column MUL_MAT (pre-pass + GEMV) over rotated weight
     copies: GB/s of weight block bytes + activations + dst, for the op (timed
-    region) and for the GEMV kernel alone (dispatch-stamped)."""
+    region) and for the GEMV kernel alone (median dispatch-stamped duration)."""
     raw, ws = weight_copies(be, qmm, synth, qtype, M, K, seed=6)
     x = synth.activations(N, K, seed=7)
     xt = be.new_tensor(qmm.F32, (K, N))
     be.set_tensor(xt, x.view(np.uint8).ravel())
     yt = be.new_tensor(qmm.F32, (M, N))
     steps = max(20, args.steps // 2)
-    wall, dev, k = time_op(be, ws, xt, yt, steps, max(4, args.warmup // 2))
+    wall, dev, kd, km = time_op(be, ws, xt, yt, steps, max(4, args.warmup // 2))
+    us = wall * 1e6 / steps
+    k = kernel_ms(kd, km, us * 1e-3)
     algo = raw.nbytes + K * N * 4 + M * N * 4
     sec = {"workload": name, "path": be.last_path(), "N": N,
-           "GBs": round(algo * steps / wall / 1e9, 1), "us_per_op": round(wall * 1e6 / steps, 3),
-           "kernel_us": round(k * 1e3, 3), "kernel_GBs": round(algo / (k * 1e-3) / 1e9, 1),
+           "GBs": round(algo * steps / wall / 1e9, 1), "us_per_op": round(us, 3),
+           "kernel_us": round(k * 1e3, 3), "kernel_us_markers": round(km * 1e3, 3),
+           "kernel_GBs": round(algo / (k * 1e-3) / 1e9, 1),
            "frac_hbm": round(algo / (k * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     for w in ws:
         be.free_buffer(w.buf)
@@ -206,88 +241,144 @@ def glu_case(be, qmm, synth, args):
     return out
 
 
-def moe_case(be, qmm, synth, T, args):
-    """MUL_MAT_ID on config 3's expert gate/up: 512 Q4_K experts of 512 x 2048,
-    top-10 routing, T tokens sharing one activation column each (ne11 = 1).
-    One step = one MUL_MAT_ID (pre-pass, on-GPU routing, expert GEMV tasks)
-    with the next of 16 router id sets; GB/s counts the weight bytes of the
-    experts that step touches."""
-    E, n_used, M, K = 512, 10, 512, 2048
-    raw = synth.weights(qmm.Q4_K, E * M, K, seed=4)
-    w = be.new_tensor(qmm.Q4_K, (K, M, E))
-    be.set_tensor(w, raw)
-    ebytes = raw.nbytes // E
-    idsets, touched = [], []
-    for k in range(16):
-        ids = synth.moe_ids(T, E, n_used, seed=100 + k)
-        t = be.new_tensor(qmm.I32, (n_used, T))
-        be.set_tensor(t, ids.view(np.uint8).ravel())
-        idsets.append(t)
-        touched.append(len(np.unique(ids)) * ebytes)
-    x = synth.activations(T, K, seed=5)
-    xt = be.new_tensor(qmm.F32, (K, 1, T))
-    be.set_tensor(xt, x.view(np.uint8).ravel())
-    yt = be.new_tensor(qmm.F32, (M, n_used, T))
-    steps = max(16, args.steps // 2)
-    for i in range(16):
-        be.mul_mat_id(w, xt, idsets[i % 16], yt)
-    be.synchronize()
-    t0 = time.perf_counter()
-    for i in range(steps):
-        be.mul_mat_id(w, xt, idsets[i % 16], yt)
-    be.synchronize()
-    wall = time.perf_counter() - t0
-    be.kernel_timing(True)
-    for i in range(steps):
-        be.mul_mat_id(w, xt, idsets[i % 16], yt)
-    k_ms, n = be.kernel_time()
-    be.kernel_timing(False)
-    bytes_step = float(np.mean(touched))
-    us = wall * 1e6 / steps
-    k_us = k_ms / max(n, 1) * 1e3
-    path = be.last_path()
-    # the router (softmax / top-10 over 512 logits per token) and the combine of the layer's
-    # down-projection outputs (hidden 2048, 10 slots) around it, device time per op
-    lg = be.new_tensor(qmm.F32, (E, T))
-    be.set_tensor(lg, synth.activations(T, E, seed=6).view(np.uint8).ravel())
-    rid = be.new_tensor(qmm.I32, (n_used, T))
-    rw = be.new_tensor(qmm.F32, (n_used, T))
-    ex = be.new_tensor(qmm.F32, (2048, n_used, T))
-    be.set_tensor(ex, synth.activations(n_used * T, 2048, seed=7).view(np.uint8).ravel())
-    yo = be.new_tensor(qmm.F32, (2048, T))
-    # the layer's gate and up stacks with the SwiGLU in one call (one route, one GEMV launch)
-    wu = be.new_tensor(qmm.Q4_K, (K, M, E))
-    be.copy(wu.buf, 0, w.buf, 0, qmm.alloc_size(qmm.Q4_K, (K, M, E)))
-    yg = be.new_tensor(qmm.F32, (M, n_used, T))
-    state = {"i": 0}
+class MoeLayers:
+    """Config 3's MoE layer, `nl` copies: per layer the gate and up expert stacks [2048, 512, 512]
+    and the down stack [512, 2048, 512] in Q4_K (906 MB), the shared expert's gate / up
+    [2048, 512] and down [512, 2048], and the buffers of one layer's chain.  The layers' stacks
+    hold the same bytes (device copies of one seeded stack per shape)."""
+    E, K_USED, HID, FFN = 512, 10, 2048, 512
 
-    def glu():
-        be.mul_mat_id_glu(w, wu, xt, idsets[state["i"] % 16], yg, qmm.GLU_SWIGLU)
-        state["i"] += 1
-
-    times = {}
-    for name, fn in (("router", lambda: be.moe_topk(lg, rid, rw)), ("combine", lambda: be.moe_combine(ex, rw, yo)),
-                     ("gate_up_glu", glu)):
-        for _ in range(10):
-            fn()
+    def __init__(self, be, qmm, synth, nl):
+        self.be, self.qmm, self.nl = be, qmm, nl
+        E, HID, FFN = self.E, self.HID, self.FFN
+        q = qmm.Q4_K
+        self.ebytes = synth.row_bytes(q, HID) * FFN                # one expert matrix: 589,824 B
+        self.bufs = []
+        proto = {}
+        for name, (rows, k, ne, seed) in {"gate": (E * FFN, HID, (HID, FFN, E), 11), "down": (E * HID, FFN, (FFN, HID, E), 13),
+                                          "sgate": (FFN, HID, (HID, FFN), 14), "sdown": (HID, FFN, (FFN, HID), 16)}.items():
+            t = be.new_tensor(q, ne)
+            be.set_tensor(t, synth.weights(q, rows, k, seed))
+            proto[name] = t
+        self.layers = []
+        for _ in range(nl):
+            L = {}
+            for name, src in (("gate", "gate"), ("up", "gate"), ("down", "down"), ("sgate", "sgate"), ("sup", "sgate"),
+                              ("sdown", "sdown")):
+                t = be.new_tensor(q, proto[src].ne)
+                be.copy(t.buf, 0, proto[src].buf, 0, qmm.alloc_size(q, proto[src].ne))
+                L[name] = t
+                self.bufs.append(t.buf)
+            self.layers.append(L)
+        for t in proto.values():
+            be.free_buffer(t.buf)
         be.synchronize()
-        be.timer_begin()
-        for _ in range(steps):
-            fn()
-        times[name] = be.timer_end() * 1e3 / steps
-    out = {"workload": f"MUL_MAT_ID Q4_K 512 experts x (512 x 2048), top-10, T={T} (config 3 gate/up)",
-           "path": path, "us_per_op": round(us, 3), "expert_bytes_touched": int(bytes_step),
-           "GBs": round(bytes_step / (us * 1e-6) / 1e9, 1), "kernel_us": round(k_us, 3),
-           "kernel_GBs": round(bytes_step / (k_us * 1e-6) / 1e9, 1),
-           "router_us": round(times["router"], 3), "combine_us": round(times["combine"], 3),
-           "gate_up_glu_us": round(times["gate_up_glu"], 3)}
-    for t in (lg, rid, rw, ex, yo, wu, yg):
-        be.free_buffer(t.buf)
-    for t in idsets:
-        be.free_buffer(t.buf)
-    for t in (w, xt, yt):
-        be.free_buffer(t.buf)
-    return out
+
+    def close(self):
+        for b in self.bufs:
+            self.be.free_buffer(b)
+
+
+def moe_case(be, qmm, synth, layers, T, args):
+    """Config 3's whole MoE layer at T tokens, one step = one layer: the router (softmax /
+    top-10 over 512 logits per token), gate + up + SwiGLU over the routed experts (one call),
+    the down projection (src1 [512, 10, T]), the shared expert's gate + up + SwiGLU and down,
+    and the combine with the sigmoid-gated shared expert.  Steps alternate between the layers
+    and take the next of 32 router-logit sets, so the stacks (1.8 GB) rotate through HBM.  GB/s
+    counts the expert weights each step touches (distinct routed experts x 3 matrices + the
+    shared expert), the bytes BASELINE.md's C3 row quotes."""
+    qm = qmm
+    be_ = be
+    E, k, HID, FFN = layers.E, layers.K_USED, layers.HID, layers.FFN
+    g = np.random.default_rng(1000 + T)
+    nlog = 32
+    logits = [g.standard_normal((T, E)).astype(np.float32) for _ in range(nlog)]
+    lts = []
+    touched = []
+    for lg in logits:
+        t = be_.new_tensor(qm.F32, (E, T))
+        be_.set_tensor(t, lg.view(np.uint8).ravel())
+        lts.append(t)
+        top = np.argpartition(-lg, k - 1, axis=1)[:, :k]          # the k largest logits of each token
+        touched.append((len(np.unique(top)) * 3 + 3) * layers.ebytes)
+    x = synth.activations(T, HID, seed=5)
+    xt = be_.new_tensor(qm.F32, (HID, 1, T))
+    be_.set_tensor(xt, x.view(np.uint8).ravel())
+    x2 = qm.Tensor(xt.buf, qm.F32, (HID, T))
+    sgl = be_.new_tensor(qm.F32, (1, T))
+    be_.set_tensor(sgl, g.standard_normal(T).astype(np.float32).view(np.uint8))
+    ids = be_.new_tensor(qm.I32, (k, T))
+    wts = be_.new_tensor(qm.F32, (k, T))
+    h = be_.new_tensor(qm.F32, (FFN, k, T))
+    ex = be_.new_tensor(qm.F32, (HID, k, T))
+    hs = be_.new_tensor(qm.F32, (FFN, T))
+    ys = be_.new_tensor(qm.F32, (HID, T))
+    out = be_.new_tensor(qm.F32, (HID, T))
+    tmp = [lts, [xt, sgl, ids, wts, h, ex, hs, ys, out]]
+    nl = len(layers.layers)
+
+    def router(i):
+        be_.moe_topk(lts[i % nlog], ids, wts)
+
+    def gate_up(i):
+        L = layers.layers[i % nl]
+        be_.mul_mat_id_glu(L["gate"], L["up"], xt, ids, h, qm.GLU_SWIGLU)
+
+    def down(i):
+        be_.mul_mat_id(layers.layers[i % nl]["down"], h, ids, ex)
+
+    def shared(i):
+        L = layers.layers[i % nl]
+        be_.mul_mat_glu(L["sgate"], L["sup"], x2, hs, qm.GLU_SWIGLU)
+        be_.mul_mat(L["sdown"], hs, ys)
+
+    def combine(i):
+        be_.moe_combine(ex, wts, out, ys, sgl)
+
+    def layer(i):
+        router(i)
+        gate_up(i)
+        down(i)
+        shared(i)
+        combine(i)
+
+    steps = max(32, args.steps // 2)
+    for i in range(16):
+        layer(i)
+    be_.synchronize()
+    t0 = time.perf_counter()
+    be_.timer_begin()
+    for i in range(steps):
+        layer(i)
+    dev_ms = be_.timer_end()
+    wall = time.perf_counter() - t0
+    paths = {}
+    for name, fn in (("gate_up_glu", gate_up), ("down", down)):
+        layer(0)
+        fn(0)
+        paths[name] = be_.last_path()
+    times = {}
+    for name, fn in (("router", router), ("gate_up_glu", gate_up), ("down", down), ("shared", shared),
+                     ("combine", combine)):
+        for i in range(8):
+            layer(i)
+        be_.synchronize()
+        be_.timer_begin()
+        for i in range(steps):
+            fn(i)
+        times[name] = be_.timer_end() * 1e3 / steps
+    bytes_step = float(np.mean([touched[i % nlog] for i in range(steps)]))
+    us = dev_ms * 1e3 / steps
+    res = {"workload": f"config 3 MoE layer, T={T}: router + gate/up/SwiGLU (512 Q4_K experts, top-10) + down + "
+                       f"shared expert + combine, {nl} layers rotated",
+           "T": T, "us_per_layer": round(us, 3), "wall_us_per_layer": round(wall * 1e6 / steps, 3),
+           "weight_bytes_touched": int(bytes_step), "GBs": round(bytes_step / (us * 1e-6) / 1e9, 1),
+           "frac_hbm": round(bytes_step / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+           "roofline_us": round(bytes_step / (HBM_PEAK_GBS * 1e9) * 1e6, 3),
+           "op_us": {n: round(v, 3) for n, v in times.items()}, "paths": paths}
+    for t in tmp[0] + tmp[1]:
+        be_.free_buffer(t.buf)
+    return res
 
 
 def main():
@@ -318,10 +409,11 @@ def main():
         xt = be.new_tensor(qmm.F32, (K, N))
         be.set_tensor(xt, x.view(np.uint8).ravel())
         yt = be.new_tensor(qmm.F32, (M, N))
-        wall, dev_ms, k_ms = time_op(be, ws, xt, yt, args.steps, args.warmup)
+        wall, dev_ms, kd, km = time_op(be, ws, xt, yt, args.steps, args.warmup)
         path = be.last_path()
         algo = raw.nbytes + K * N * 4 + M * N * 4
         value = algo * args.steps / wall / 1e9
+        k_ms = kernel_ms(kd, km, wall * 1e3 / args.steps)
         achieved = algo / (k_ms * 1e-3) / 1e9
         traffic = profile_traffic("q4k_gemv")
         out.update({
@@ -335,7 +427,11 @@ def main():
                        "device_ms_per_step": round(dev_ms / args.steps, 5)},
             "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                         "traffic_source": "profiles/traffic.json: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of this "
+                                           "kernel (profiles/k_gemv_q4k_17408x5120_n1.md), scaled by the copy kernel's "
+                                           "counts; not measured in this run",
                          "kernel": "k_gemv<12, 1> (Q4_K, 1 column)", "kernel_us": round(k_ms * 1e3, 3),
+                         "kernel_us_markers": round(km * 1e3, 3), "kernel_us_stat": f"median of {args.steps} launches",
                          "algorithmic_bytes": int(algo)},
         })
         if not args.no_cpu:
@@ -389,11 +485,13 @@ def main():
         else:
             out = {"metric": "FFN gate+up GB/s", "value": g["fused_GBs"], "unit": "GB/s", "glu": g}
     if not args.no_secondary and args.only in ("", "moe"):
-        moe = [moe_case(be, qmm, synth, T, args) for T in (1, 4, 256)]
+        layers = MoeLayers(be, qmm, synth, 2)
+        moe = [moe_case(be, qmm, synth, layers, T, args) for T in (1, 4, 256)]
+        layers.close()
         if out:
             out["moe"] = moe
         else:
-            out = {"metric": "MUL_MAT_ID GB/s", "value": moe[-1]["GBs"], "unit": "GB/s", "moe": moe}
+            out = {"metric": "MoE layer GB/s", "value": moe[0]["GBs"], "unit": "GB/s", "moe": moe}
     be.close()
     print(json.dumps(out), flush=True)
 

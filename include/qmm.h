@@ -296,12 +296,17 @@ int    qmm_timer_begin(qmm_ctx * ctx);
 float  qmm_timer_end(qmm_ctx * ctx);
 
 /* Per-kernel device time of the main kernel of every op (the GEMV / GEMM,
- * not the activation pre-pass): enable(1) clears and starts stamping a HIP
+ * not the activation pre-pass): enable = 1 clears and starts stamping a HIP
  * event pair with each such kernel's own start and end (the dispatch itself,
- * as a profiler reports it); read waits for the stream and returns the summed
- * milliseconds and the launch count. */
+ * as a profiler reports it); enable = 2 instead records the pair on the
+ * stream right before and right after the launch (the start completes with
+ * the work queued ahead of the kernel); 0 stops.  qmm_kernel_time waits for
+ * the stream and returns the summed milliseconds and the launch count;
+ * qmm_kernel_times writes each launch's milliseconds (at most cap) and
+ * returns the launch count, -1 on error. */
 int    qmm_kernel_timing(qmm_ctx * ctx, int enable);
 int    qmm_kernel_time(qmm_ctx * ctx, double * total_ms, int64_t * launches);
+int64_t qmm_kernel_times(qmm_ctx * ctx, double * ms, int64_t cap);
 
 /* Copy between device buffers on the context's stream (harness plumbing). */
 int    qmm_buffer_copy(qmm_ctx * ctx, qmm_buffer * dst, size_t dst_off, const qmm_buffer * src, size_t src_off, size_t size);

@@ -260,7 +260,16 @@ def test_c3_layer_chain(be, orc, bufs, moe_w, T):
     ref_ys = orc.mul_mat(qmm.Q4_K, rsd, HID, FFN, got_hs)
     check(got_ys, ref_ys, f"C3 T={T} shared down")
     check(got, moe.combine(got_ex, got_w, got_ys, sgl[:, 0]), f"C3 T={T} combine")
-    # the whole chain on the oracle's own intermediates
+    # The whole chain on the oracle's own intermediates.  The per-product bar above does not
+    # apply here: each intermediate is quantized to q8 again before the next product, and an
+    # intermediate that differs at the 1e-7 level (float32 GLU against the oracle's float64,
+    # split-K atomics' add order) can flip a code there, which moves an output by about one
+    # code's share of a sum over K = 512: ~1e-3 of the output rms.  The bar is 1e-2 of the rms
+    # (a wrong expert, weight or slot moves outputs by the whole rms).
     ref_ex2 = orc.mul_mat_id(qmm.Q4_K, rd, HID, FFN, E, ref_h.astype(np.float32), ref_ids)
     ref_ys2 = orc.mul_mat(qmm.Q4_K, rsd, HID, FFN, ref_hs.astype(np.float32))
-    check(got, moe.combine(ref_ex2, ref_w.astype(np.float32), ref_ys2, sgl[:, 0]), f"C3 T={T} layer end to end")
+    ref = moe.combine(ref_ex2, ref_w.astype(np.float32), ref_ys2, sgl[:, 0])
+    r = err_report(got, ref)
+    print(f"[err] C3 T={T} layer end to end: max |err| {r['max_abs_err_over_rms']:.2g} rms "
+          f"(floored relative {r['floored']:.3g})", flush=True)
+    assert r["max_abs_err_over_rms"] <= 1e-2, r

@@ -362,7 +362,10 @@ def run_mul_mat(be, sc, orc, qtype, M, K, N, seed):
 
 @pytest.mark.parametrize("qtype", TYPES)
 @pytest.mark.parametrize("N", [1, 2, 3, 4, 5, 8])
-def test_mul_mat_gemv(be, sc, orc, qtype, N):
+def test_mul_mat_gemv(be, sc, orc, monkeypatch, qtype, N):
+    """the pre-pass GEMV kernels (the fused one, which small 1-2 column products take by
+    default, has its own tests)"""
+    monkeypatch.setenv("QMM_GEMV_FQ_SMALL_TG", "0")
     M, K = 300, 2048
     say("gemv", qtype, M, K, N)
     got, ref = run_mul_mat(be, sc, orc, qtype, M, K, N, seed=51)
