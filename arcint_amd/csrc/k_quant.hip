@@ -50,6 +50,32 @@ __global__ void k_quant_q8_K(F32Cols src, int64_t K, int64_t ncols, ActBuf a, Ze
     quant_q8_K_at(src, K, ncols, a, (int64_t)blockIdx.x * blockDim.x + threadIdx.x);
 }
 
+// q8_0 into the streaming GEMM's tiled layout: 8 lanes per 32-weight block, 4 weights per
+// lane, over every column of every tile (columns past N of a batch quantize zeros, which gives
+// zero codes and a zero scale)
+__global__ void k_quant_tiled_q8_0(F32Cols src, int64_t K, TiledAct ta, int64_t nthreads) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const bool live = t < nthreads;                // whole waves are live or dead
+    const int64_t kq = ta.nblk * 8;                // threads per column
+    const int64_t cp = live ? t / kq : 0, k = live ? (t - cp * kq) * 4 : 0;
+    const int64_t tile = cp >> 5, b = tile / ta.ntb;
+    const int i = (int)(cp & 31);
+    const int64_t n = (tile - b * ta.ntb) * 32 + i;
+    float v[4] = { 0.f, 0.f, 0.f, 0.f };
+    if (live && n < ta.N && k < K) {
+        const float * x = f32_col(src, b * ta.N + n) + k;
+        for (int j = 0; j < 4; ++j) v[j] = x[j];
+    }
+    float d;
+    int s;
+    const uint32_t packed = quant_q8_0_lane(v, &d, &s);
+    if (!live) return;
+    const int64_t blk = tile * ta.nblk + (k >> 5);
+    const int o = (int)(k & 31);
+    *reinterpret_cast<uint32_t *>(ta.A + ((blk * 64 + (o >> 4) * 32 + i) << 4) + (o & 15)) = packed;
+    if ((t & 7) == 0) ta.D[blk * 32 + tiled_pos(i)] = d;
+}
+
 // ActBuf -> ggml block bytes, one thread per block
 __global__ void k_act_blocks(ActBuf a, uint8_t * __restrict__ out) {
     const int bs = act_block(a.vdt);
@@ -93,6 +119,17 @@ hipError_t launch_quantize(const F32Cols & src, int64_t K, int64_t ncols, const 
     if (grid > 0x7fffffff) return hipErrorInvalidValue;
     if (a.vdt == QMM_TYPE_Q8_0) k_quant_q8_0<<<dim3((unsigned)grid), kTpb, 0, s>>>(src, K, ncols, a, zj, nqblk);
     else k_quant_q8_K<<<dim3((unsigned)grid), kTpb, 0, s>>>(src, K, ncols, a, zj, nqblk);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_tiled(const F32Cols & src, int64_t K, const TiledAct & t, hipStream_t s) {
+    if (K <= 0 || t.nblk * 32 < K || t.nblk % 8 || t.ntb <= 0 || t.ntiles <= 0 || t.ntiles % t.ntb || t.N <= 0 ||
+        t.N > 32 * t.ntb)
+        return hipErrorInvalidValue;
+    const int64_t n = t.ntiles * 32 * t.nblk * 8;    // a multiple of 64: whole waves
+    const int64_t grid = (n + kTpb - 1) / kTpb;
+    if (grid > 0x7fffffff) return hipErrorInvalidValue;
+    k_quant_tiled_q8_0<<<dim3((unsigned)grid), kTpb, 0, s>>>(src, K, t, n);
     return hipGetLastError();
 }
 

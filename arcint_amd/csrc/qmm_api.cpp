@@ -49,10 +49,12 @@ struct qmm_ctx {
         size_t nb[4] = { 0, 0, 0, 0 };
         int vdt = 0;
         bool dT = false;
+        bool tiled = false;          // the streaming GEMM's tiled layout (cached_tiled)
         uint64_t gen = 0;
         bool valid = false;
     } key;
     ActBuf cached{};
+    TiledAct cached_tiled{};
     // MoE route scratch: ids copy, tasks, task count
     void * route = nullptr;
     size_t route_cap = 0;
@@ -251,10 +253,11 @@ F32Cols f32_cols(const qmm_tensor * t) {
     return c;
 }
 
-bool same_key(const qmm_ctx * ctx, int vdt, const qmm_tensor * src1, bool dT) {
+bool same_key(const qmm_ctx * ctx, int vdt, const qmm_tensor * src1, bool dT, bool tiled) {
     const auto & k = ctx->key;
     return k.valid && k.gen == ctx->graph_gen && k.buf == src1->buffer && k.offs == src1->offs && k.vdt == vdt &&
-           (k.dT || !dT) && !memcmp(k.ne, src1->ne, sizeof(k.ne)) && !memcmp(k.nb, src1->nb, sizeof(k.nb));
+           k.tiled == tiled && (k.dT || !dT) && !memcmp(k.ne, src1->ne, sizeof(k.ne)) &&
+           !memcmp(k.nb, src1->nb, sizeof(k.nb));
 }
 
 // Quantize src1 (all its columns) with the vec_dot type of `type`, reusing
@@ -282,7 +285,7 @@ int quantize_src1(qmm_ctx * ctx, int type, const qmm_tensor * src1, bool dT, Act
     const int64_t K = src1->ne[0], ncols = src1->ne[1] * src1->ne[2] * src1->ne[3];
     auto & k = ctx->key;
     if (pr && z) return fail(ctx, QMM_ERR_INVALID, "internal: a route launch with dst zeroing");
-    if (!fixed && ctx->in_graph && same_key(ctx, vdt, src1, dT)) {
+    if (!fixed && ctx->in_graph && same_key(ctx, vdt, src1, dT, false)) {
         *out = ctx->cached;
         if (z) QMM_HIP(ctx, launch_quantize(f32_cols(src1), K, 0, ctx->cached, z, ctx->stream));   // zeroing only
         if (pr) QMM_HIP(ctx, launch_route(pr->r, pr->scratch, pr->tasks, pr->ntasks, ctx->stream));
@@ -321,9 +324,52 @@ int quantize_src1(qmm_ctx * ctx, int type, const qmm_tensor * src1, bool dT, Act
     memcpy(k.nb, src1->nb, sizeof(k.nb));
     k.vdt = vdt;
     k.dT = dT;
+    k.tiled = false;
     k.gen = ctx->graph_gen;
     k.valid = true;
     ctx->cached = a;
+    return QMM_OK;
+}
+
+// Quantize src1 (q8_0) into the streaming GEMM's tiled layout for weights of G groups per row,
+// reusing the previous result inside one graph when src1 is the same tensor.
+int quantize_src1_tiled(qmm_ctx * ctx, const qmm_tensor * src1, int64_t G, TiledAct * out,
+                        const FixedAct * fixed = nullptr) {
+    const int64_t K = src1->ne[0], N = src1->ne[1], nbatch = src1->ne[2] * src1->ne[3];
+    auto & k = ctx->key;
+    if (!fixed && ctx->in_graph && same_key(ctx, QMM_TYPE_Q8_0, src1, false, true) && ctx->cached_tiled.nblk == G * 8) {
+        *out = ctx->cached_tiled;
+        return QMM_OK;
+    }
+    TiledAct t;
+    t.nblk = G * 8;
+    t.ntb = (N + 31) / 32;
+    t.ntiles = t.ntb * nbatch;
+    t.N = N;
+    const size_t oa = tiled_a_bytes(t.ntiles, t.nblk), need = oa + tiled_d_bytes(t.ntiles, t.nblk);
+    if (fixed && need > fixed->cap)
+        return fail(ctx, QMM_ERR_NOMEM, "the activations of src1 [%lld, %lld] need %zu bytes of scratch; at most %zu",
+                    (long long)K, (long long)(N * nbatch), need, fixed->cap);
+    if (!fixed) {
+        const int rc = ensure(ctx, &ctx->act, &ctx->act_cap, need);
+        if (rc) return rc;
+    }
+    uint8_t * b = fixed ? fixed->base : (uint8_t *)ctx->act;
+    t.A = (int8_t *)b;
+    t.D = (float *)(b + oa);
+    QMM_HIP(ctx, launch_quantize_tiled(f32_cols(src1), K, t, ctx->stream));
+    *out = t;
+    if (fixed) return QMM_OK;
+    k.buf = src1->buffer;
+    k.offs = src1->offs;
+    memcpy(k.ne, src1->ne, sizeof(k.ne));
+    memcpy(k.nb, src1->nb, sizeof(k.nb));
+    k.vdt = QMM_TYPE_Q8_0;
+    k.dT = false;
+    k.tiled = true;
+    k.gen = ctx->graph_gen;
+    k.valid = true;
+    ctx->cached_tiled = t;
     return QMM_OK;
 }
 
@@ -819,6 +865,20 @@ int qmm_describe_mul_mat(const qmm_tensor * src0, const qmm_tensor * src1, const
     WView w;   // shapes only: buffers are not looked at
     if (!mul_mat_ok(src0, src1, dst, false, &w, reason, sizeof(reason))) return QMM_ERR_UNSUPPORTED;
     const int64_t N = src1->ne[1];
+    G3Shape g3;
+    if (N >= gemm_min_cols(src0->type) && gemm3_shape(src0->type, w, N, src1->ne[2] * src1->ne[3], &g3)) {
+        snprintf(out->path, sizeof(out->path), "gemm-stream");
+        out->tasks = src1->ne[2] * src1->ne[3];
+        out->cols_per_task = 32 * g3.C;
+        out->workgroups = g3.workgroups;
+        out->threads = g3.threads;
+        out->lds_bytes = g3.lds;
+        out->k_slices = g3.KS;
+        out->k_waves = g3.KS;
+        out->tiles_per_wg = g3.U;
+        out->groups_per_wave = (int32_t)((int64_t)g3.sps * g3.SB / 8);
+        return QMM_OK;
+    }
     if (N >= gemm_min_cols(src0->type)) {
         snprintf(out->path, sizeof(out->path), "gemm-mfma");
         out->tasks = src1->ne[2] * src1->ne[3];
@@ -933,6 +993,23 @@ static int mul_mat_launch(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tens
     dn.d_nb3 = (int64_t)(dst->nb[3] / 4);
     KTime kt;
     const KTime * ktp = nullptr;
+    if (use_gemm && gemm3_supported(src0->type)) {           // weights streamed per wave, dst written once
+        const int64_t nbatch = dn.ne12 * dn.ne13;
+        TiledAct ta;
+        if ((rc = quantize_src1_tiled(ctx, src1, w.G, &ta, fixed))) return rc;
+        GemmBatch bt;
+        bt.ne12 = dn.ne12;
+        bt.r2 = dn.r2;
+        bt.r3 = dn.r3;
+        bt.ne02 = dn.ne02;
+        bt.d_nb1 = dn.d_nb1;
+        bt.d_nb2 = dn.d_nb2;
+        bt.d_nb3 = dn.d_nb3;
+        ctx->path = "gemm-stream";
+        if (!fixed && (rc = ktime_pair(ctx, &kt, &ktp))) return rc;
+        QMM_HIP(ctx, launch_gemm3(src0->type, w, ta, nbatch, bt, d, ctx->stream, ktp));
+        return ktime_done(ctx);
+    }
     if (use_gemm) {
         const int64_t nbatch = dn.ne12 * dn.ne13;
         // K slices add into dst rows from zero_from on (the pre-pass zeroes them)

@@ -280,6 +280,50 @@ struct GemmBatch {
 };
 hipError_t launch_gemm(int type, const WView & w, const ActBuf & a, int64_t N, int64_t nbatch,
                        const GemmBatch & bt, float * dst, hipStream_t s, const KTime * kt = nullptr);
+// ---------------------------------------------------------------------------
+// Tiled activations of the streaming GEMM (k_gemm3), written by its pre-pass.
+// The columns of each batch go in tiles of 32: column n of batch b is column
+// n % 32 of tile b * ntb + n / 32 (ntb = ceil(N / 32)); columns past N in a
+// batch's last tile hold zeros.  For tile t and 32-weight block k < nblk:
+//   A  int8 [t][k][64][16]  the v_mfma_i32_32x32x32_i8 A operand: the 16
+//      bytes of lane (i, h) are codes 16 h .. 16 h + 15 of the block in
+//      column i (i = lane % 32, h = lane / 32)
+//   D  f32 [t][k][32]       the q8_0 block scales (fp16-rounded, as ggml-cpu
+//      keeps them) in the MFMA's output order: entry 16 h + r is column
+//      8 (r / 4) + 4 h + r % 4, the column that register r of lane half h
+//      holds
+// ---------------------------------------------------------------------------
+struct TiledAct {
+    int8_t * A;
+    float * D;
+    int64_t nblk;      // 32-weight blocks per column (ldk / 32)
+    int64_t ntb;       // tiles per batch
+    int64_t ntiles;    // tiles of all batches
+    int64_t N;         // columns per batch
+};
+__host__ __device__ constexpr int tiled_pos(int i) { return 16 * ((i >> 2) & 1) + 4 * (i >> 3) + (i & 3); }
+// bytes of the two arrays for ntiles tiles of nblk blocks (each a multiple of 256)
+__host__ __device__ inline size_t tiled_a_bytes(int64_t ntiles, int64_t nblk) { return (size_t)(ntiles * nblk) * 1024; }
+__host__ __device__ inline size_t tiled_d_bytes(int64_t ntiles, int64_t nblk) { return (size_t)(ntiles * nblk) * 128; }
+// q8_0 quantization of the f32 columns into the tiled layout (ggml-cpu's from_float numerics)
+hipError_t launch_quantize_tiled(const F32Cols & src, int64_t K, const TiledAct & t, hipStream_t s);
+
+// Streaming GEMM for the types whose scale is one float per 32-weight block
+// (Q4_0, Q8_0, IQ4_NL): every weight batch b < nbatch, dst[doff(b) + n d_nb1
+// + m] = W(mat(b)) row m . column n of batch b, n < N, m < M.  Each output is
+// written once (no atomics, no zeroing of dst).
+bool gemm3_supported(int type);
+struct G3Shape {
+    int C, U, KS, SB;              // column tiles per wave, row tiles (64) per work-group, K slices, blocks per stage
+    int64_t mbn, nbn;              // work-group blocks along M and N per batch
+    int sps, nst;                  // stages per K slice, stages along K
+    int threads, lds;
+    int64_t workgroups;            // all batches
+};
+bool gemm3_shape(int type, const WView & w, int64_t N, int64_t nbatch, G3Shape * sh);
+hipError_t launch_gemm3(int type, const WView & w, const TiledAct & a, int64_t nbatch, const GemmBatch & bt,
+                        float * dst, hipStream_t s, const KTime * kt = nullptr);
+
 // K slices the GEMM splits this product into; above 1 the slices add their
 // partial sums to dst with atomics, so dst must be zeroed first.
 int gemm_kslices(int type, const WView & w, int64_t N, int64_t nbatch);

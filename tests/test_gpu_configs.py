@@ -130,7 +130,7 @@ def test_c1_llama2_q4_0(be, wc, orc, bufs, qtype, M, K, N):
     name = f"C1 {synth.NAMES[qtype]} {M}x{K} N={N}"
     say(name)
     got, ref, path = mul_mat_case(be, wc, orc, bufs, qtype, M, K, N, seed=7)
-    assert path in (("gemm-mfma",) if N == 512 else ("gemv", "gemv-fq")), path
+    assert path in (("gemm-stream",) if N == 512 else ("gemv", "gemv-fq")), path
     check(got, ref, name)
 
 

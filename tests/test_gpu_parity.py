@@ -20,6 +20,12 @@ TYPES = [qmm.Q4_0, qmm.Q8_0, qmm.Q4_K, qmm.Q5_K, qmm.Q6_K, qmm.IQ4_NL, qmm.IQ4_X
 # the types whose 3..8-column products run on the MFMA GEMV
 MMA_TYPES = (qmm.Q4_0, qmm.Q8_0, qmm.Q4_K, qmm.IQ4_XS, qmm.IQ4_NL, qmm.Q6_K)
 TOL = 1e-3
+# the types whose GEMM streams weights per wave (one float scale per 32-weight block)
+STREAM_TYPES = (qmm.Q4_0, qmm.Q8_0, qmm.IQ4_NL)
+
+
+def gemm_path(qtype):
+    return "gemm-stream" if qtype in STREAM_TYPES else "gemm-mfma"
 
 
 def say(*a):
@@ -573,7 +579,7 @@ def test_mul_mat_gemm(be, sc, orc, monkeypatch, qtype, M, K, N):
         K = 1024
     say("gemm", qtype, M, K, N)
     got, ref = run_mul_mat(be, sc, orc, qtype, M, K, N, seed=57)
-    assert be.last_path() == "gemm-mfma"
+    assert be.last_path() == gemm_path(qtype)
     assert rel_err(got, ref) <= TOL
 
 
@@ -588,7 +594,7 @@ def test_mul_mat_gemm_broadcast_and_strides(be, sc, orc, monkeypatch, qtype):
     y = sc.empty_f32((M, N, 4))
     be.mul_mat(w, sc.f32(x), y)
     be.synchronize()
-    assert be.last_path() == "gemm-mfma"
+    assert be.last_path() == gemm_path(qtype)
     got = be.get_f32(y).reshape(4, N, M)
     rb = synth.row_bytes(qtype, K) * M
     for i2 in range(4):
@@ -610,7 +616,7 @@ GEMM_FULL = [
 ]
 
 
-@pytest.mark.parametrize("qtype", [qmm.Q4_K, qmm.Q4_0])
+@pytest.mark.parametrize("qtype", [qmm.Q4_K, qmm.Q6_K])
 def test_gemm_tail_split(be, sc, orc, qtype):
     # 66 row tiles x 4 column tiles = 264 > 256 work-groups: the first 256 tiles run whole and
     # the last row of tiles (partial: 8384 = 65.5 x 128 rows) in K slices added into dst rows
@@ -632,8 +638,37 @@ def test_full_size_gemm(be, sc, orc, monkeypatch, qtype, M, K, N):
     monkeypatch.setenv("QMM_GEMM_MIN_COLS", "16")
     say("gemm-full", qtype, M, K, N)
     got, ref = run_mul_mat(be, sc, orc, qtype, M, K, N, seed=93)
-    assert be.last_path() == "gemm-mfma"
+    assert be.last_path() == gemm_path(qtype)
     assert rel_err(got, ref) <= TOL
+
+
+# streaming GEMM launch shapes: K slices per work-group KS (1..3) forced, on ragged shapes (N
+# not a multiple of 32, a work-group's last row tiles missing, K not a multiple of 256 or of a
+# stage, batches with broadcast weights)
+@pytest.mark.parametrize("qtype", STREAM_TYPES)
+@pytest.mark.parametrize("KS", [1, 2, 3])
+def test_gemm_stream_shapes(be, sc, orc, monkeypatch, qtype, KS):
+    monkeypatch.setenv("QMM_GEMM3_KS", str(KS))
+    for (M, K, N, seed) in [(200, 800, 33, 301), (64, 2048, 100, 302), (130, 512, 64, 303), (448, 1280, 161, 304),
+                            (700, 4352, 40, 307)]:
+        say("gemm-stream", qtype, KS, M, K, N)
+        got, ref = run_mul_mat(be, sc, orc, qtype, M, K, N, seed=seed)
+        assert be.last_path() == "gemm-stream"
+        assert rel_err(got, ref) <= TOL, (M, K, N)
+    say("gemm-stream batches", qtype, KS)
+    K, M, N = 768, 96, 45
+    raw = synth.weights(qtype, 2 * M, K, seed=305)
+    w = sc.weights(qtype, raw, (K, M, 2))
+    x = synth.activations(4 * N, K, seed=306).reshape(4, N, K)
+    y = sc.empty_f32((M, N, 4))
+    be.mul_mat(w, sc.f32(x), y)
+    be.synchronize()
+    assert be.last_path() == "gemm-stream"
+    got = be.get_f32(y).reshape(4, N, M)
+    rb = synth.row_bytes(qtype, K) * M
+    for i2 in range(4):
+        ref = orc.mul_mat(qtype, raw[(i2 // 2) * rb:(i2 // 2 + 1) * rb], M, K, x[i2])
+        assert rel_err(got[i2], ref) <= TOL
 
 
 # ------------------------------------------------------------------ MoE router and combine
@@ -785,7 +820,7 @@ def test_mul_mat_glu_split_paths(be, sc, orc):
     assert rel_err(got, ref) <= TOL
     say("glu-split gemm")
     got, ref = glu_case(be, sc, orc, qmm.Q4_0, qmm.Q4_0, 200, 1024, 40, qmm.GLU_GEGLU, seed=122)
-    assert be.last_path() == "glu-gemm-mfma"
+    assert be.last_path() == "glu-gemm-stream"
     assert rel_err(got, ref) <= TOL
     say("glu-split batches")
     got, ref = glu_case(be, sc, orc, qmm.Q4_K, qmm.Q4_K, 130, 512, 2, qmm.GLU_SWIGLU, seed=123, batches=(3, 2))

@@ -276,3 +276,30 @@ def test_gemv_plan(qtype, K, M, N):
     else:
         assert tw == 1
         assert info["lds_bytes"] == (W * nc * 64 * 4 if W > 1 else 0)
+
+
+# the streaming GEMM (types with one float scale per 32-weight block): a wave per (64-row tile,
+# 32-column tile, K slice), work-groups of 4 row tiles x KS K slices (KS = 1 when 4-wave groups
+# fill the chip, else 3), numbered 8 per XCD round; LDS: two stages of 16 blocks (8 for Q8_0) of
+# A operands (1 KB) and f32 scales (128 B) per K slice, or the K slices' sums if larger
+GEMM3_SHAPES = [(qmm.Q4_0, 4096, 4096, 512), (qmm.Q4_0, 11008, 4096, 512), (qmm.Q4_0, 4096, 11008, 512),
+                (qmm.Q8_0, 4096, 14336, 64), (qmm.IQ4_NL, 800, 130, 33), (qmm.Q4_0, 4096, 4096, 100)]
+
+
+@pytest.mark.parametrize("qtype,K,M,N", GEMM3_SHAPES)
+def test_gemm_stream_plan(qtype, K, M, N):
+    fake = qmm.Buffer(ptr=0x1000, size=1 << 44)
+    info = qmm.describe_mul_mat(qmm.Tensor(fake, qtype, (K, M)), qmm.Tensor(fake, qmm.F32, (K, N)),
+                                qmm.Tensor(fake, qmm.F32, (M, N)))
+    assert info["path"] == "gemm-stream"
+    KS = info["k_slices"]
+    G, nt, ntb = -(-K // 256), -(-M // 64), -(-N // 32)
+    units = -(-nt // 4) * ntb
+    SB = 8 if qtype == qmm.Q8_0 else 16
+    nst = -(-8 * G // SB)
+    assert info["cols_per_task"] == 32 and info["tiles_per_wg"] == 4
+    ks = min(1 if units * 4 >= 2048 else 3, nst)
+    assert KS == -(-nst // -(-nst // ks))                 # slices of ceil(nst / ks) stages, none empty
+    assert info["threads"] == 64 * 4 * KS
+    assert info["workgroups"] == 8 * -(-units // 8)
+    assert info["lds_bytes"] == max(KS * 2 * SB * 1152, (KS - 1) * 4 * 32 * 64 * 4) <= 160 * 1024
