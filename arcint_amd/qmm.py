@@ -20,7 +20,8 @@ from dataclasses import dataclass
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libqmm.so")
+# QMM_LIB names another build of the same library (the sanitizer and mutation builds of the tests)
+LIB_PATH = os.environ.get("QMM_LIB") or os.path.join(_HERE, "libqmm.so")
 
 F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K, IQ4_NL, IQ4_XS, I32 = 0, 1, 2, 8, 12, 13, 14, 15, 20, 23, 26
 OP_MUL_MAT, OP_MUL_MAT_ID = 1, 2

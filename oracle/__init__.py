@@ -14,7 +14,7 @@ import os
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB = os.path.join(_HERE, "liborc.so")
+_LIB = os.environ.get("QMM_ORACLE_LIB") or os.path.join(_HERE, "liborc.so")   # (the sanitizer build: tests/sanitize.sh)
 
 Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K, IQ4_NL, IQ4_XS = 2, 8, 12, 13, 14, 15, 20, 23
 # type -> (weights per block, bytes per block, vec_dot type)
