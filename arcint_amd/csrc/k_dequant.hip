@@ -69,7 +69,7 @@ __global__ void k_deq_q4_K(WView w, int64_t nblk, float * __restrict__ y) {
     const uint8_t * s = b + 4;
     int sc[2], m[2];
     for (int h = 0; h < 2; ++h) {
-        const int j = 2 * c + h;
+        const int j = (2 * c + h) ^ (QMM_RED == 1);           // (mutation 1, Q4_K: the neighbouring sub-block's scale)
         if (j < 4) { sc[h] = s[j] & 63; m[h] = s[j + 4] & 63; }
         else { sc[h] = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4); m[h] = (s[j + 4] >> 4) | ((s[j] >> 6) << 4); }
     }

@@ -320,7 +320,7 @@ __global__ __launch_bounds__(kT, 2) void k_gemm2(G2Params p) {   // 2 waves per 
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
                 uint32_t sc, mn;
-                q4k_scale_min(4 * hh + ql + t, R.h.y, R.h.z, R.h.w, &sc, &mn);
+                q4k_scale_min((4 * hh + ql + t) ^ (QMM_RED == 5), R.h.y, R.h.z, R.h.w, &sc, &mn);   // (mutation 5)
                 const uint32_t sh = sc >> 3, sl = sc & 7;
                 uint4 vh, vl;
                 const uint32_t m0 = (e[0] >> (4 * t)) & 0x0F0F0F0Fu, m1 = (e[1] >> (4 * t)) & 0x0F0F0F0Fu;

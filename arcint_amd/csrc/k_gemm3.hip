@@ -252,6 +252,7 @@ __global__ __launch_bounds__(64 * kU * kMaxKS) void k_gemm3(G3Params p) {
             wload(wb, kb + kRing);                            // the slot's next block
             float dw0 = h2f(d0b), dw1 = h2f(d1b);
             asm volatile("" : "+v"(dw0), "+v"(dw1));          // f32 operands (no fp16 source folding)
+            if (QMM_RED == 6) dw1 = dw0;                      // (mutation 6: rows 32-63 take rows 0-31's scale)
             const float nm0 = -12582912.0f * dw0, nm1 = -12582912.0f * dw1;
             const Act & c = x;
             // (one MFMA result at a time: the SIMD's other waves cover its latency)

@@ -128,7 +128,7 @@ template <> struct GV<QMM_TYPE_Q4_0> {
             const float dw = h2f(dw2[p >> 1] >> (16 * (p & 1)));
 #pragma unroll
             for (int j = 0; j < NC; ++j) {
-                if (j < nc) {
+                if (j < nc && !(QMM_RED == 3 && p == 7)) {      // (mutation 3: the group's last block dropped)
                     int s = dot16(l0, l1, l2, l3, X::c4(x.c[j], 8 * p), 0);
                     s = dot16(h0, h1, h2, h3, X::c4(x.c[j], 8 * p + 4), s);
                     s -= 8 * X::s16(x.s[j], p);                // codes are q, the weight is q - 8
@@ -700,7 +700,7 @@ __device__ __forceinline__ void scale_add(const v16i & e0, const v16i & e1, int 
 template <int NR>
 __device__ __forceinline__ void bf_epilogue(const v16i & e0, const v16i & e1, float dw0, float dw1, const float (&dx)[NR],
                                             vNf<2 * NR> & out) {
-    const float nm0 = -12582912.0f * dw0, nm1 = -12582912.0f * dw1;
+    const float nm0 = -12582912.0f * dw0, nm1 = -12582912.0f * (QMM_RED == 4 ? dw0 : dw1);   // (mutation 4)
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
         const int i0 = e0[r], i1 = e1[r];
@@ -1260,7 +1260,7 @@ __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
             }
             return;
         }
-        mat = e;
+        mat = QMM_RED == 8 ? (int)((e + 1) % p.n_as) : e;      // (mutation 8: the next expert)
         nc = 1;
 #pragma unroll
         for (int j = 0; j < NC; ++j) {

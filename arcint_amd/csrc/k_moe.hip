@@ -83,7 +83,7 @@ __device__ __forceinline__ void route_body(const RouteArgs & r, int32_t * __rest
         const int32_t nt = (c + kMaxTaskCols - 1) / kMaxTaskCols;
         for (int32_t k = 0; k < nt; ++k) {
             GemvTask & T = tasks[tstart[e] + k];
-            T.mat = e < r.n_as ? (int32_t)e : -1;
+            T.mat = e < r.n_as ? (int32_t)(QMM_RED == 7 ? (e + 1) % r.n_as : e) : -1;   // (mutation 7: next expert)
             T.ncols = (c - k * kMaxTaskCols) < kMaxTaskCols ? (c - k * kMaxTaskCols) : kMaxTaskCols;
         }
     }

@@ -50,30 +50,50 @@ __global__ void k_quant_q8_K(F32Cols src, int64_t K, int64_t ncols, ActBuf a, Ze
     quant_q8_K_at(src, K, ncols, a, (int64_t)blockIdx.x * blockDim.x + threadIdx.x);
 }
 
-// q8_0 into the streaming GEMM's tiled layout: 8 lanes per 32-weight block, 4 weights per
-// lane, over every column of every tile (columns past N of a batch quantize zeros, which gives
-// zero codes and a zero scale)
-__global__ void k_quant_tiled_q8_0(F32Cols src, int64_t K, TiledAct ta, int64_t nthreads) {
-    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const bool live = t < nthreads;                // whole waves are live or dead
-    const int64_t kq = ta.nblk * 8;                // threads per column
-    const int64_t cp = live ? t / kq : 0, k = live ? (t - cp * kq) * 4 : 0;
-    const int64_t tile = cp >> 5, b = tile / ta.ntb;
-    const int i = (int)(cp & 31);
-    const int64_t n = (tile - b * ta.ntb) * 32 + i;
-    float v[4] = { 0.f, 0.f, 0.f, 0.f };
-    if (live && n < ta.N && k < K) {
-        const float * x = f32_col(src, b * ta.N + n) + k;
-        for (int j = 0; j < 4; ++j) v[j] = x[j];
+// q8_0 into the streaming GEMM's tiled layout: one wave per (tile, 32-weight block), lane
+// (i, h) quantizes k 16 h .. 16 h + 15 of the block in column i of the tile (columns past N
+// of a batch quantize zeros: zero codes and a zero scale).  The block's |x| maximum meets the
+// other half's through v_permlane32_swap; the scale and the codes follow quant_q8_0_lane's
+// arithmetic step for step (the same bits).  Each lane writes its 16 codes as one chunk, so a
+// wave writes the block's 1 KB A operand in one piece.
+__global__ __launch_bounds__(256) void k_quant_tiled_q8_0(F32Cols src, int64_t K, TiledAct ta, int64_t nwaves) {
+    const int64_t w = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
+    if (w >= nwaves) return;                       // whole waves
+    const int lane = threadIdx.x & 63, i = lane & 31, h = lane >> 5;
+    const int64_t tile = w / ta.nblk, blk = w - tile * ta.nblk, b = tile / ta.ntb;
+    const int64_t n = (tile - b * ta.ntb) * 32 + i, k0 = blk * 32 + 16 * h;
+    float v[16];
+    if (n < ta.N && k0 < K) {
+        const float * x = f32_col(src, b * ta.N + n) + k0;   // (column strides are only 4-byte aligned)
+#pragma unroll
+        for (int q = 0; q < 16; ++q) v[q] = x[q];
+    } else {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) v[q] = 0.0f;
     }
-    float d;
-    int s;
-    const uint32_t packed = quant_q8_0_lane(v, &d, &s);
-    if (!live) return;
-    const int64_t blk = tile * ta.nblk + (k >> 5);
-    const int o = (int)(k & 31);
-    *reinterpret_cast<uint32_t *>(ta.A + ((blk * 64 + (o >> 4) * 32 + i) << 4) + (o & 15)) = packed;
-    if ((t & 7) == 0) ta.D[blk * 32 + tiled_pos(i)] = d;
+    float m = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) m = fmaxf(m, fabsf(v[q]));
+    const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, m), __builtin_bit_cast(uint32_t, m),
+                                                     false, false);
+    const float amax = fmaxf(m, __builtin_bit_cast(float, h ? sw[0] : sw[1]));
+    const _Float16 dh = (_Float16)(amax / 127.f);
+    const float mul = amax != 0.0f ? 127.f / amax : 0.0f;
+    uint32_t c[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float r = __builtin_rintf(v[4 * q + e] * mul);
+            r = fminf(fmaxf(r, -128.f), 127.f);
+            word |= ((uint32_t)(int)r & 0xffu) << (8 * e);
+        }
+        c[q] = word;
+    }
+    const int64_t t = tile * ta.nblk + blk;
+    *reinterpret_cast<uint4 *>(ta.A + (t * 64 + lane) * 16) = make_uint4(c[0], c[1], c[2], c[3]);
+    if (h == 0) ta.D[t * 32 + tiled_pos(i)] = (float)dh;
 }
 
 // ActBuf -> ggml block bytes, one thread per block
@@ -124,12 +144,11 @@ hipError_t launch_quantize(const F32Cols & src, int64_t K, int64_t ncols, const 
 
 hipError_t launch_quantize_tiled(const F32Cols & src, int64_t K, const TiledAct & t, hipStream_t s) {
     if (K <= 0 || t.nblk * 32 < K || t.nblk % 8 || t.ntb <= 0 || t.ntiles <= 0 || t.ntiles % t.ntb || t.N <= 0 ||
-        t.N > 32 * t.ntb)
+        t.N > 32 * t.ntb || K % 32)
         return hipErrorInvalidValue;
-    const int64_t n = t.ntiles * 32 * t.nblk * 8;    // a multiple of 64: whole waves
-    const int64_t grid = (n + kTpb - 1) / kTpb;
+    const int64_t nw = t.ntiles * t.nblk, grid = (nw + 3) / 4;
     if (grid > 0x7fffffff) return hipErrorInvalidValue;
-    k_quant_tiled_q8_0<<<dim3((unsigned)grid), kTpb, 0, s>>>(src, K, t, n);
+    k_quant_tiled_q8_0<<<dim3((unsigned)grid), 256, 0, s>>>(src, K, t, nw);
     return hipGetLastError();
 }
 

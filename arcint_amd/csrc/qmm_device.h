@@ -167,7 +167,7 @@ __device__ __forceinline__ uint32_t quant_q8_0_lane(const float v[4], float * d,
     const float mul = amax != 0.0f ? 127.f / amax : 0.0f;
     int q[4], sum = 0;
     for (int i = 0; i < 4; ++i) {
-        float r = __builtin_rintf(v[i] * mul);
+        float r = QMM_RED == 2 ? roundf(v[i] * mul) : __builtin_rintf(v[i] * mul);   // (mutation 2: ties away)
         r = fminf(fmaxf(r, -128.f), 127.f);
         q[i] = (int)r;
         sum += q[i];

@@ -8,6 +8,14 @@
 
 #include "../../include/qmm.h"
 
+// QMM_RED = k plants known mistake k in one kernel family (a mutation build of the tests,
+// arcint_amd.build --red k, never the product: the product build leaves it 0); the GPU parity
+// suite must fail against every k (tests/red/run_red.py).  1 dequant, 2 q8_0 quantizer,
+// 3 v_dot4 GEMV, 4 MFMA GEMV, 5 Q4_K GEMM, 6 streaming GEMM, 7 MoE route, 8 fused MoE GEMV.
+#ifndef QMM_RED
+#define QMM_RED 0
+#endif
+
 namespace qmm {
 
 // ---------------------------------------------------------------------------
