@@ -319,6 +319,252 @@ __global__ __launch_bounds__(64 * kU * kMaxKS) void k_gemm3(G3Params p) {
     }
 }
 
+// ---- Q4_K ------------------------------------------------------------------------------------
+// Role of the reference's K-quant integer GEMM (P01:1919-2024: an integer dot per sub-block, its
+// 6-bit scale applied to the dot, the min term once per super-block), on q8_K activations.
+//  * a wave owns 32 rows (one half of a 64-row image tile) x 64 columns (two column tiles) over
+//    one K slice: lane (j, h) loads chunk plane 2c + h of row j, whose low nibbles are k
+//    16 h .. 16 h + 15 of sub-block 2c and whose high nibbles are those of sub-block 2c + 1, which
+//    is the MFMA's B operand for row j as it lies (no lane exchange), and the output lane (j, h)
+//    holds row j, so the lane's own header gives its row's scales;
+//  * sub-block s of both column tiles: two MFMAs on the raw nibbles (0..15), each int32 result
+//    multiplied by the row's 6-bit scale into the super-block's integer sum (v_mad_i32_i24);
+//  * the min term sum_j m_j bsum_j is two MFMAs per column tile and super-block: A = the
+//    columns' split sums bh (then bl, bsum = 64 bh + bl) at k = j, B = the row's 8 mins; the
+//    second one starts from 64 * first + the bits of 12582912.0f, so its result read as a float
+//    is 12582912 + the exact min sum (|sum| < 2^22) and one FMA takes dmin times it;
+//  * per super-block and output: out += dx * (d * isc - dmin * imn);
+//  * activations (the super-block's A operands of both tiles, split sums and scales: 18 KB) go
+//    from the pre-pass layout into LDS by buffer loads that write LDS directly (no registers), one
+//    super-block ahead; the U row-half waves of a K slice share them, one barrier per super-block;
+//  * the weights stream through registers one super-block ahead: a chunk is reloaded with the
+//    next super-block's as soon as its two sub-blocks are done.
+constexpr int kKQStage = 18 * 1024;           // A [2 tiles][8 sub-blocks][1 KB], S [2][32][16], D [2][32] f32 (1 KB slot)
+constexpr int kKQMaxWaves = 12;
+// every wave stages ceil(18 / U) units of 1 KB per super-block, the same count on every wave and
+// every iteration (so the barrier waits for exactly these loads, not the weight loads issued
+// after them); units past 18 read nothing (out of range) into a 1 KB slot after the stages
+__host__ __device__ constexpr int kq_units(int U) { return (18 + U - 1) / U; }
+// s_waitcnt immediate (gfx9 encoding): vmcnt 5 (bits 3:0, 15:14), expcnt and lgkmcnt not waited on
+constexpr int kVmcnt5 = 5 | (0x7 << 4) | (0xF << 8);
+
+struct KQParams {
+    WView w;
+    const int8_t * tA;
+    const float * tD;
+    const int8_t * tS;
+    int64_t nsb;                         // super-blocks per column (the weights' groups)
+    int64_t ntb;                         // column tiles per batch
+    int64_t N;                           // columns per batch
+    int64_t mbn, nbn;                    // work-group blocks per batch: U row halves along M, column pairs along N
+    int64_t total, chunk;                // mbn * nbn, ceil(total / 8)
+    int U, KS, sps;                      // row-half waves per K slice, K slices, super-blocks per slice
+    GemmBatch bt;
+    float * dst;
+};
+
+// 16 bytes per lane from a buffer into LDS at lds + 16 lane (lds wave-uniform)
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t * lds, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16, (int)voff, (int)soff,
+                                             0, 0);
+}
+
+template <int U>
+__global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q4k(KQParams p) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, j32 = lane & 31;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int u = wave % U, ks = wave / U;
+
+    const uint32_t L = (blockIdx.x & 7) * (uint32_t)p.chunk + (blockIdx.x >> 3);
+    if (L >= (uint32_t)p.total) return;                       // uniform over the work-group
+    const uint32_t mb = L / (uint32_t)p.nbn, nb = L - mb * (uint32_t)p.nbn;
+    const uint32_t bz = blockIdx.y;
+    const uint32_t i2 = bz % (uint32_t)p.bt.ne12, i3 = bz / (uint32_t)p.bt.ne12;
+    const int64_t mat = (int64_t)(i2 / (uint32_t)p.bt.r2) + (int64_t)(i3 / (uint32_t)p.bt.r3) * p.bt.ne02;
+    const int64_t rh_raw = (int64_t)mb * U + u;               // the wave's row half
+    const bool row_ok = rh_raw < 2 * p.w.ntiles;              // a missing row half computes a copy, stores nothing
+    const int64_t rh = row_ok ? rh_raw : 2 * p.w.ntiles - 1;
+    const int64_t mtile = rh >> 1;
+    const int t = (int)(rh & 1);
+    const int64_t ct0 = (int64_t)bz * p.ntb + 2 * (int64_t)nb; // the pair's first column tile
+    const int64_t nct = std::min<int64_t>(2, p.ntb - 2 * (int64_t)nb);
+    const int nsb = (int)p.nsb;
+    const int s0 = ks * p.sps;
+    const int s1 = std::min(s0 + p.sps, nsb);                 // (every slice has super-blocks)
+
+    const __amdgpu_buffer_rsrc_t wbuf = buffer_rsrc(tile_group(p.w, mat, mtile, 0), (uint32_t)(p.w.G * p.w.tg));
+    // the pair's activations; a pair with one tile reads zeros for the second (past the range)
+    const __amdgpu_buffer_rsrc_t abuf = buffer_rsrc(p.tA + ct0 * p.nsb * 8192, (uint32_t)(nct * p.nsb * 8192));
+    const __amdgpu_buffer_rsrc_t sbuf = buffer_rsrc(p.tS + ct0 * p.nsb * 512, (uint32_t)(nct * p.nsb * 512));
+    const __amdgpu_buffer_rsrc_t dbuf = buffer_rsrc(p.tD + ct0 * p.nsb * 32, (uint32_t)(nct * p.nsb * 128));
+    const uint32_t lane16 = (uint32_t)lane * 16;
+
+    // ---- staging of super-block s into buffer b of the slice: 18 units of 1 KB (A: tile
+    // unit / 8, sub-block unit % 8; S; D, lanes 16.. reading zeros into the slot's padding),
+    // wave u taking units u, u + U, ...
+    constexpr int NU = kq_units(U);
+    const uint32_t a_stride = (uint32_t)p.nsb * 8192, s_stride = (uint32_t)p.nsb * 512, d_stride = (uint32_t)p.nsb * 128;
+    const uint32_t s_lane = (uint32_t)(lane >> 5) * s_stride + (uint32_t)j32 * 16;
+    const uint32_t d_lane = lane < 16 ? (uint32_t)(lane >> 3) * d_stride + (uint32_t)(lane & 7) * 16 : 0x7ff00000u;
+    uint8_t * const dump = lds + 2 * p.KS * kKQStage;
+    auto stage = [&](int s, int b) {
+        uint8_t * S = lds + (ks * 2 + b) * kKQStage;
+#pragma unroll
+        for (int i = 0; i < NU; ++i) {
+            const int unit = u + i * U;                       // wave-uniform
+            if (unit < 16)
+                dma16(abuf, S + unit * 1024, lane16 + (uint32_t)(unit >> 3) * a_stride + (uint32_t)(unit & 7) * 1024,
+                      (uint32_t)s * 8192);
+            else if (unit == 16)
+                dma16(sbuf, S + 16 * 1024, s_lane, (uint32_t)s * 512);
+            else if (unit == 17)
+                dma16(dbuf, S + 17 * 1024, d_lane, (uint32_t)s * 128);
+            else
+                dma16(dbuf, dump, 0x7ff00000u, 0);            // (nothing: keeps the count)
+        }
+    };
+
+    // ---- weights of the lane's row (32 t + j32): chunk planes 2c + h, and the header plane
+    const uint32_t row16 = (uint32_t)(32 * t + j32) * 16, wl = row16 + (uint32_t)h * kChunk;
+    const uint32_t tgs = (uint32_t)p.w.tg;
+    uint4 ch[4], hd;
+
+    v16f out0 = v16f{}, out1 = v16f{};                       // column tiles 0 and 1 of the pair
+    auto compute = [&](int b, int s) {
+        const uint8_t * S = lds + (ks * 2 + b) * kKQStage;
+        // the row's 6-bit scales and mins (get_scale_min_k4, P01:2164-2176), four per word
+        const uint32_t sc03 = hd.y & 0x3f3f3f3fu, mn03 = hd.z & 0x3f3f3f3fu;
+        const uint32_t sc47 = (hd.w & 0x0f0f0f0fu) | ((hd.y >> 2) & 0x30303030u);
+        const uint32_t mn47 = ((hd.w >> 4) & 0x0f0f0f0fu) | ((hd.z >> 2) & 0x30303030u);
+        const uint32_t dd = hd.x;
+        const uint32_t sn = (uint32_t)std::min(s + 1, s1 - 1) * tgs;   // the next super-block (clamped)
+        hd = bld16(wbuf, row16, sn + 8 * kChunk);
+        v16i isc0 = v16i{}, isc1 = v16i{};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint4 q = ch[j >> 1];
+            const int sh = 4 * (j & 1);
+            const v4i bop = v4i{ (int)((q.x >> sh) & 0x0F0F0F0Fu), (int)((q.y >> sh) & 0x0F0F0F0Fu),
+                                 (int)((q.z >> sh) & 0x0F0F0F0Fu), (int)((q.w >> sh) & 0x0F0F0F0Fu) };
+            if (j & 1) ch[j >> 1] = bld16(wbuf, wl, sn + 2 * (j >> 1) * kChunk);
+            const v4i a0 = *reinterpret_cast<const v4i *>(S + j * 1024 + lane16);
+            const v4i a1 = *reinterpret_cast<const v4i *>(S + 8192 + j * 1024 + lane16);
+            const v16i e0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bop, v16i{}, 0, 0, 0);
+            const v16i e1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bop, v16i{}, 0, 0, 0);
+            const int js = j ^ (QMM_RED == 5);                // (mutation 5: neighbouring scales swapped)
+            const int sj = (int)(((js < 4 ? sc03 : sc47) >> (8 * (js & 3))) & 0xffu);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                isc0[r] += __mul24(sj, e0[r]);
+                isc1[r] += __mul24(sj, e1[r]);
+            }
+            asm volatile("" : "+v"(isc0), "+v"(isc1));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // min term, then the float combine of each column tile
+        float d = h2f(dd & 0xffffu), dmin = h2f(dd >> 16);
+        asm volatile("" : "+v"(d), "+v"(dmin));               // f32 operands (no fp16 source folding)
+        const float nmag = 12582912.0f * dmin;                // exact: fp16 dmin times 3 * 2^22
+        const v4i bm = h ? v4i{} : v4i{ (int)mn03, (int)mn47, 0, 0 };
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const uint4 sp = *reinterpret_cast<const uint4 *>(S + 16384 + c * 512 + j32 * 16);
+            const v4i ah = h ? v4i{} : v4i{ (int)sp.x, (int)sp.y, 0, 0 };
+            const v4i al = h ? v4i{} : v4i{ (int)sp.z, (int)sp.w, 0, 0 };
+            v16i mh = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, bm, v16i{}, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mh[r] = mh[r] * 64 + kMagic;
+            const v16i ml = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, bm, mh, 0, 0, 0);
+            float dx[16];
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const float4 v = *reinterpret_cast<const float4 *>(S + 17408 + c * 128 + h * 64 + 16 * q4);
+                dx[4 * q4] = v.x;
+                dx[4 * q4 + 1] = v.y;
+                dx[4 * q4 + 2] = v.z;
+                dx[4 * q4 + 3] = v.w;
+            }
+            v16f & o = c ? out1 : out0;
+            const v16i & is = c ? isc1 : isc0;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                // (the element goes through a scalar: clang's __builtin_bit_cast of an ext-vector
+                // element reads element 0)
+                const int iml = ml[r];
+                const float wv = __builtin_fmaf(__builtin_bit_cast(float, iml), -dmin, nmag);   // -dmin * imn
+                const float v = __builtin_fmaf((float)is[r], d, wv);
+                o[r] = __builtin_fmaf(v, dx[r], o[r]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // ---- K loop: super-block s + 1 goes into LDS while s is computed (its buffer was last read
+    // before the previous barrier); the barrier's wait covers only these LDS loads, which are
+    // issued before the iteration's weight loads
+    stage(s0, 0);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) ch[c] = bld16(wbuf, wl, (uint32_t)s0 * tgs + 2 * c * kChunk);
+    hd = bld16(wbuf, row16, (uint32_t)s0 * tgs + 8 * kChunk);
+    __syncthreads();
+    for (int it = 0; it < p.sps; ++it) {                      // uniform over the work-group
+        const int s = s0 + it;
+        stage(std::min(s + 1, s1 - 1), (it + 1) & 1);         // (past the slice: a copy nobody reads)
+        __builtin_amdgcn_sched_barrier(0);                    // the LDS loads go out before the weight loads
+        if (s < s1) {
+            compute(it & 1, s);
+        } else {                                              // a slice shorter than sps: the same loads as
+#pragma unroll                                                // compute's (unused), so that every path
+            for (int c = 0; c < 4; ++c)                       // leaves them outstanding at the barrier
+                ch[c] = bld16(wbuf, wl, (uint32_t)(s1 - 1) * tgs + 2 * c * kChunk);
+            hd = bld16(wbuf, row16, (uint32_t)(s1 - 1) * tgs + 8 * kChunk);
+        }
+        // this wave's LDS loads are complete once at most the 5 weight loads issued after them
+        // are outstanding (vmcnt(5)); the barrier then publishes them to the other waves
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(kVmcnt5);
+        __syncthreads();
+    }
+
+    // ---- K slices 1.. add their sums into slice 0's through LDS (fixed order), slice 0 stores
+    if (p.KS > 1) {
+        float * red = reinterpret_cast<float *>(lds);
+        if (ks > 0) {
+            float * o = red + ((size_t)((ks - 1) * U + u) * 32) * 64 + lane;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                o[r * 64] = out0[r];
+                o[(16 + r) * 64] = out1[r];
+            }
+        }
+        __syncthreads();
+        if (ks > 0) return;
+        for (int k = 1; k < p.KS; ++k) {
+            const float * o = red + ((size_t)((k - 1) * U + u) * 32) * 64 + lane;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                out0[r] += o[r * 64];
+                out1[r] += o[(16 + r) * 64];
+            }
+        }
+    }
+    if (!row_ok) return;
+    const int64_t m = mtile * kTileRows + 32 * t + j32;
+    if (m >= p.w.M) return;
+    float * dst = p.dst + (int64_t)i2 * p.bt.d_nb2 + (int64_t)i3 * p.bt.d_nb3 + m;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        const int64_t n0 = (2 * (int64_t)nb + c) * 32;
+        const v16f & v = c ? out1 : out0;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int64_t n = n0 + 8 * (r >> 2) + 4 * h + (r & 3);
+            if (n < p.N) __builtin_nontemporal_store(v[r], dst + n * p.bt.d_nb1);
+        }
+    }
+}
+
 template <int TYPE>
 hipError_t launch_t(const G3Params & p, const G3Shape & sh, const dim3 & g, hipStream_t s, const KTime * kt) {
     static const hipError_t attr =
@@ -330,6 +576,17 @@ hipError_t launch_t(const G3Params & p, const G3Shape & sh, const dim3 & g, hipS
     return hipGetLastError();
 }
 
+template <int U>
+hipError_t launch_kq(const KQParams & q, const G3Shape & sh, const dim3 & g, const dim3 & b, hipStream_t s,
+                     const KTime * kt) {
+    static const hipError_t attr =
+        hipFuncSetAttribute((const void *)k_gemm3_q4k<U>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (attr != hipSuccess) return attr;
+    if (kt) hipExtLaunchKernelGGL(k_gemm3_q4k<U>, g, b, (uint32_t)sh.lds, s, kt->start, kt->stop, 0, q);
+    else k_gemm3_q4k<U><<<g, b, sh.lds, s>>>(q);
+    return hipGetLastError();
+}
+
 int env_int3(const char * name, int dflt) {
     const char * e = getenv(name);
     return e ? atoi(e) : dflt;
@@ -338,17 +595,63 @@ int env_int3(const char * name, int dflt) {
 }  // namespace
 
 bool gemm3_supported(int type) {
-    static const bool on = env_int3("QMM_GEMM3", 1) != 0;
-    return on && (type == QMM_TYPE_Q4_0 || type == QMM_TYPE_Q8_0 || type == QMM_TYPE_IQ4_NL);
+    if (env_int3("QMM_GEMM3", 1) == 0) return false;          // (read per call: tests switch them)
+    return type == QMM_TYPE_Q4_0 || type == QMM_TYPE_Q8_0 || type == QMM_TYPE_IQ4_NL ||
+           (type == QMM_TYPE_Q4_K && env_int3("QMM_GEMM3_Q4K", 1) != 0);
 }
+
+namespace {
+// Q4_K launch shape: U row-half waves per K slice x KS slices, chosen by rounds of work-groups
+// on the chip x super-blocks per slice: 12-wave work-groups fill a CU alone (3 waves per SIMD),
+// whole rounds; 4-wave ones go three to a CU and a partial last round costs its fraction (the
+// CUs take the next small group as one finishes; measured on 17408 x 5120 x 512: 4-wave groups
+// 141 us, (6, 2) 145 us, (12, 1) 155 us).  Ties go to the earlier (larger U) candidate.
+bool kq_shape(const WView & w, int64_t N, int64_t nbatch, G3Shape * sh) {
+    struct Cand { int U, KS, per_cu; };
+    static const Cand cands[] = { { 12, 1, 1 }, { 6, 2, 1 }, { 4, 3, 1 }, { 3, 4, 1 }, { 4, 1, 3 }, { 2, 2, 3 } };
+    const int64_t nrh = 2 * w.ntiles, ncp = ((N + 31) / 32 + 1) / 2, G = w.G;
+    const int cus = 256;
+    int64_t best = -1;
+    const int forced = env_int3("QMM_GEMM3_KQ", -1);           // index into cands (tuning)
+    for (int i = 0; i < (int)(sizeof(cands) / sizeof(cands[0])); ++i) {
+        if (forced >= 0 && i != forced) continue;
+        const Cand & c = cands[i];
+        const int64_t sps = (G + c.KS - 1) / c.KS, KS = (G + sps - 1) / sps;
+        const int64_t mbn = (nrh + c.U - 1) / c.U, nwg = mbn * ncp * nbatch;
+        const int64_t slots = (int64_t)cus * c.per_cu;
+        // (in 1/64 rounds)
+        const int64_t rounds = c.per_cu > 1 ? std::max<int64_t>(64, (nwg * 64 + slots - 1) / slots)
+                                            : 64 * ((nwg + slots - 1) / slots);
+        const int64_t cost = rounds * sps;
+        if (best >= 0 && cost >= best) continue;
+        best = cost;
+        sh->U = c.U;
+        sh->KS = (int)KS;
+        sh->sps = (int)sps;
+        sh->mbn = mbn;
+    }
+    if (best < 0) return false;
+    sh->C = 2;
+    sh->R = 32;
+    sh->SB = 8;
+    sh->nbn = ncp;
+    sh->nst = (int)G;
+    sh->threads = 64 * sh->U * sh->KS;
+    sh->lds = std::max(sh->KS * 2 * kKQStage + (18 % sh->U ? 1024 : 0), (sh->KS - 1) * sh->U * 32 * 64 * 4);
+    sh->workgroups = 8 * ((sh->mbn * ncp + 7) / 8) * nbatch;
+    return sh->mbn * ncp < 0x7fffffff && sh->lds <= 160 * 1024 && sh->threads <= 64 * kKQMaxWaves;
+}
+}  // namespace
 
 // Launch shape: C column tiles per wave (2 shares each weight unpack between two column tiles,
 // at twice the accumulators), kU row tiles per work-group, and K slices so that the waves come
 // to about `target` (3 per SIMD).
 bool gemm3_shape(int type, const WView & w, int64_t N, int64_t nbatch, G3Shape * sh) {
     if (!gemm3_supported(type) || N <= 0 || nbatch <= 0 || nbatch > 65535 || w.G <= 0 || w.ntiles <= 0) return false;
+    if (type == QMM_TYPE_Q4_K) return kq_shape(w, N, nbatch, sh);
     const int64_t ntb = (N + 31) / 32;
     sh->C = 1;
+    sh->R = 64;
     sh->U = kU;
     sh->SB = stage_blocks(type);
     sh->mbn = (w.ntiles + kU - 1) / kU;
@@ -374,8 +677,37 @@ hipError_t launch_gemm3(int type, const WView & w, const TiledAct & a, int64_t n
                         float * dst, hipStream_t s, const KTime * kt) {
     G3Shape sh;
     if (!gemm3_shape(type, w, a.N, nbatch, &sh) || !a.A || !a.D || a.nblk != w.G * 8 || a.ntb != (a.N + 31) / 32 ||
-        a.ntiles != a.ntb * nbatch)
+        a.ntiles != a.ntb * nbatch || a.vdt != vec_dot_type(type))
         return hipErrorInvalidValue;
+    if (type == QMM_TYPE_Q4_K) {
+        if (!a.S) return hipErrorInvalidValue;
+        KQParams q{};
+        q.w = w;
+        q.tA = a.A;
+        q.tD = a.D;
+        q.tS = a.S;
+        q.nsb = w.G;
+        q.ntb = a.ntb;
+        q.N = a.N;
+        q.mbn = sh.mbn;
+        q.nbn = sh.nbn;
+        q.total = sh.mbn * sh.nbn;
+        q.chunk = (q.total + 7) / 8;
+        q.U = sh.U;
+        q.KS = sh.KS;
+        q.sps = sh.sps;
+        q.bt = bt;
+        q.dst = dst;
+        const dim3 g((unsigned)(8 * q.chunk), (unsigned)nbatch), b(sh.threads);
+        switch (sh.U) {
+            case 12: return launch_kq<12>(q, sh, g, b, s, kt);
+            case 6: return launch_kq<6>(q, sh, g, b, s, kt);
+            case 4: return launch_kq<4>(q, sh, g, b, s, kt);
+            case 3: return launch_kq<3>(q, sh, g, b, s, kt);
+            case 2: return launch_kq<2>(q, sh, g, b, s, kt);
+            default: return hipErrorInvalidValue;
+        }
+    }
     G3Params p{};
     p.w = w;
     p.tA = a.A;

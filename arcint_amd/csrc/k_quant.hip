@@ -96,6 +96,107 @@ __global__ __launch_bounds__(256) void k_quant_tiled_q8_0(F32Cols src, int64_t K
     if (h == 0) ta.D[t * 32 + tiled_pos(i)] = (float)dh;
 }
 
+// q8_K into the tiled layout: one work-group of 8 waves per (tile, 256-weight super-block),
+// wave w the super-block's sub-block w; lane (i, h) holds k 16 h .. 16 h + 15 of it in column
+// i of the tile (columns past N of a batch quantize zeros).  quantize_row_q8_K_ref's scale
+// source is the first element of the largest |x| (a strictly larger |x| replaces it, scanning
+// k upwards): each lane finds its own first maximum, the two lane halves of a wave (k ranges
+// 16 h + [0, 16) of the same sub-block) and then the 8 waves (sub-blocks in k order, through
+// LDS) keep the earlier one on ties.  iscale, the codes and d follow quant_q8_K_wave's
+// arithmetic step for step.  Writes: the codes as the 1 KB A operand of block sb * 8 + w, the
+// super-block's d into D in output order, and each sub-block's code sum split as 64 bh + bl
+// into S (column i: bh[8], then bl[8]).
+__global__ __launch_bounds__(512) void k_quant_tiled_q8_K(F32Cols src, int64_t K, TiledAct ta, int64_t nsb) {
+    __shared__ float s_amax[8][32], s_mx[8][32];
+    __shared__ int8_t s_split[32][16];
+    const int64_t job = blockIdx.x;                  // (tile, super-block)
+    const int64_t tile = job / nsb, sb = job - tile * nsb, b = tile / ta.ntb;
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, i = lane & 31, h = lane >> 5;
+    const int64_t n = (tile - b * ta.ntb) * 32 + i, k0 = sb * 256 + 32 * w + 16 * h;
+    float v[16];
+    if (n < ta.N && k0 < K) {
+        const float * x = f32_col(src, b * ta.N + n) + k0;   // (column strides are only 4-byte aligned)
+#pragma unroll
+        for (int q = 0; q < 16; ++q) v[q] = x[q];
+    } else {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) v[q] = 0.0f;
+    }
+    float am = 0.0f, mx = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        const float a = fabsf(v[q]);
+        if (a > am) {
+            am = a;
+            mx = v[q];
+        }
+    }
+    // the other lane half of the same column (h = 0 holds the lower k)
+    const auto sa = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, am), __builtin_bit_cast(uint32_t, am),
+                                                     false, false);
+    const auto sm = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, mx), __builtin_bit_cast(uint32_t, mx),
+                                                     false, false);
+    const float oam = __builtin_bit_cast(float, h ? sa[0] : sa[1]), omx = __builtin_bit_cast(float, h ? sm[0] : sm[1]);
+    float wam, wmx;                                  // the sub-block's first maximum
+    if (h == 0) {
+        wam = oam > am ? oam : am;
+        wmx = oam > am ? omx : mx;
+    } else {
+        wam = am > oam ? am : oam;
+        wmx = am > oam ? mx : omx;
+    }
+    if (h == 0) {
+        s_amax[w][i] = wam;
+        s_mx[w][i] = wmx;
+    }
+    __syncthreads();
+    float amax = s_amax[0][i], m = s_mx[0][i];
+#pragma unroll
+    for (int u = 1; u < 8; ++u) {
+        const float a = s_amax[u][i];
+        if (a > amax) {
+            amax = a;
+            m = s_mx[u][i];
+        }
+    }
+    int c[16];
+    float dv = 0.0f;
+    if (amax != 0.0f) {
+        const float iscale = -127.f / m;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const int r = (int)__builtin_rintf(iscale * v[q]);
+            c[q] = r > 127 ? 127 : r;
+        }
+        dv = 1.0f / iscale;
+    } else {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) c[q] = 0;
+    }
+    uint32_t word[4];
+    int s16 = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        word[q] = (uint32_t)(c[4 * q] & 0xff) | ((uint32_t)(c[4 * q + 1] & 0xff) << 8) |
+                  ((uint32_t)(c[4 * q + 2] & 0xff) << 16) | ((uint32_t)(c[4 * q + 3] & 0xff) << 24);
+        s16 += c[4 * q] + c[4 * q + 1] + c[4 * q + 2] + c[4 * q + 3];
+    }
+    const int64_t blk = tile * ta.nblk + sb * 8 + w;
+    *reinterpret_cast<uint4 *>(ta.A + (blk * 64 + lane) * 16) = make_uint4(word[0], word[1], word[2], word[3]);
+    const auto ss = __builtin_amdgcn_permlane32_swap((uint32_t)s16, (uint32_t)s16, false, false);
+    const int s32 = s16 + (int)(h ? ss[0] : ss[1]);
+    if (h == 0) {
+        s_split[i][w] = (int8_t)(s32 >> 6);
+        s_split[i][8 + w] = (int8_t)(s32 & 63);
+    }
+    __syncthreads();
+    if (w == 0 && h == 0) {
+        const int64_t t = tile * (ta.nblk / 8) + sb;
+        *reinterpret_cast<uint4 *>(ta.S + (t * 32 + i) * 16) = *reinterpret_cast<const uint4 *>(&s_split[i][0]);
+        ta.D[t * 32 + tiled_pos(i)] = dv;
+    }
+}
+
 // ActBuf -> ggml block bytes, one thread per block
 __global__ void k_act_blocks(ActBuf a, uint8_t * __restrict__ out) {
     const int bs = act_block(a.vdt);
@@ -146,6 +247,14 @@ hipError_t launch_quantize_tiled(const F32Cols & src, int64_t K, const TiledAct 
     if (K <= 0 || t.nblk * 32 < K || t.nblk % 8 || t.ntb <= 0 || t.ntiles <= 0 || t.ntiles % t.ntb || t.N <= 0 ||
         t.N > 32 * t.ntb || K % 32)
         return hipErrorInvalidValue;
+    if (t.vdt == QMM_TYPE_Q8_K) {
+        if (K % 256 || !t.S) return hipErrorInvalidValue;
+        const int64_t nsb = t.nblk / 8, grid = t.ntiles * nsb;
+        if (grid > 0x7fffffff) return hipErrorInvalidValue;
+        k_quant_tiled_q8_K<<<dim3((unsigned)grid), 512, 0, s>>>(src, K, t, nsb);
+        return hipGetLastError();
+    }
+    if (t.vdt != QMM_TYPE_Q8_0) return hipErrorInvalidValue;
     const int64_t nw = t.ntiles * t.nblk, grid = (nw + 3) / 4;
     if (grid > 0x7fffffff) return hipErrorInvalidValue;
     k_quant_tiled_q8_0<<<dim3((unsigned)grid), 256, 0, s>>>(src, K, t, nw);

@@ -331,13 +331,15 @@ int quantize_src1(qmm_ctx * ctx, int type, const qmm_tensor * src1, bool dT, Act
     return QMM_OK;
 }
 
-// Quantize src1 (q8_0) into the streaming GEMM's tiled layout for weights of G groups per row,
-// reusing the previous result inside one graph when src1 is the same tensor.
-int quantize_src1_tiled(qmm_ctx * ctx, const qmm_tensor * src1, int64_t G, TiledAct * out,
+// Quantize src1 (the vec_dot type of `type`: q8_0, or q8_K for Q4_K) into the streaming GEMM's
+// tiled layout for weights of G groups per row, reusing the previous result inside one graph
+// when src1 is the same tensor.
+int quantize_src1_tiled(qmm_ctx * ctx, int type, const qmm_tensor * src1, int64_t G, TiledAct * out,
                         const FixedAct * fixed = nullptr) {
     const int64_t K = src1->ne[0], N = src1->ne[1], nbatch = src1->ne[2] * src1->ne[3];
+    const int vdt = vec_dot_type(type);
     auto & k = ctx->key;
-    if (!fixed && ctx->in_graph && same_key(ctx, QMM_TYPE_Q8_0, src1, false, true) && ctx->cached_tiled.nblk == G * 8) {
+    if (!fixed && ctx->in_graph && same_key(ctx, vdt, src1, false, true) && ctx->cached_tiled.nblk == G * 8) {
         *out = ctx->cached_tiled;
         return QMM_OK;
     }
@@ -346,7 +348,12 @@ int quantize_src1_tiled(qmm_ctx * ctx, const qmm_tensor * src1, int64_t G, Tiled
     t.ntb = (N + 31) / 32;
     t.ntiles = t.ntb * nbatch;
     t.N = N;
-    const size_t oa = tiled_a_bytes(t.ntiles, t.nblk), need = oa + tiled_d_bytes(t.ntiles, t.nblk);
+    t.vdt = vdt;
+    // q8_K: one scale per 8 blocks, and the split sub-block sums
+    const bool kq = vdt == QMM_TYPE_Q8_K;
+    const size_t oa = tiled_a_bytes(t.ntiles, t.nblk);
+    const size_t od = tiled_d_bytes(t.ntiles, kq ? t.nblk / 8 : t.nblk);
+    const size_t need = oa + od + (kq ? tiled_s_bytes(t.ntiles, t.nblk) : 0);
     if (fixed && need > fixed->cap)
         return fail(ctx, QMM_ERR_NOMEM, "the activations of src1 [%lld, %lld] need %zu bytes of scratch; at most %zu",
                     (long long)K, (long long)(N * nbatch), need, fixed->cap);
@@ -357,6 +364,7 @@ int quantize_src1_tiled(qmm_ctx * ctx, const qmm_tensor * src1, int64_t G, Tiled
     uint8_t * b = fixed ? fixed->base : (uint8_t *)ctx->act;
     t.A = (int8_t *)b;
     t.D = (float *)(b + oa);
+    t.S = kq ? (int8_t *)(b + oa + od) : nullptr;
     QMM_HIP(ctx, launch_quantize_tiled(f32_cols(src1), K, t, ctx->stream));
     *out = t;
     if (fixed) return QMM_OK;
@@ -364,7 +372,7 @@ int quantize_src1_tiled(qmm_ctx * ctx, const qmm_tensor * src1, int64_t G, Tiled
     k.offs = src1->offs;
     memcpy(k.ne, src1->ne, sizeof(k.ne));
     memcpy(k.nb, src1->nb, sizeof(k.nb));
-    k.vdt = QMM_TYPE_Q8_0;
+    k.vdt = vdt;
     k.dT = false;
     k.tiled = true;
     k.gen = ctx->graph_gen;
@@ -875,7 +883,7 @@ int qmm_describe_mul_mat(const qmm_tensor * src0, const qmm_tensor * src1, const
         out->lds_bytes = g3.lds;
         out->k_slices = g3.KS;
         out->k_waves = g3.KS;
-        out->tiles_per_wg = g3.U;
+        out->tiles_per_wg = g3.U * g3.R / 64;
         out->groups_per_wave = (int32_t)((int64_t)g3.sps * g3.SB / 8);
         return QMM_OK;
     }
@@ -996,7 +1004,7 @@ static int mul_mat_launch(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tens
     if (use_gemm && gemm3_supported(src0->type)) {           // weights streamed per wave, dst written once
         const int64_t nbatch = dn.ne12 * dn.ne13;
         TiledAct ta;
-        if ((rc = quantize_src1_tiled(ctx, src1, w.G, &ta, fixed))) return rc;
+        if ((rc = quantize_src1_tiled(ctx, src0->type, src1, w.G, &ta, fixed))) return rc;
         GemmBatch bt;
         bt.ne12 = dn.ne12;
         bt.r2 = dn.r2;
@@ -1445,6 +1453,25 @@ int qmm_mul_mat_glu(qmm_ctx * ctx, const qmm_tensor * gate, const qmm_tensor * u
 // first byte, highest end byte, highest sink end, real loads, sink loads, bad loads, the
 // stage's read extent.  No device is touched.  QMM_ERR_UNSUPPORTED when the product would run
 // on the GEMM instead.
+int64_t qmm_internal_quantize_tiled(qmm_ctx * ctx, const qmm_tensor * src1, int32_t type, void * out, int64_t cap) {
+    if (!ctx || !src1 || !out || src1->type != QMM_TYPE_F32 || !type_layout(type)) return 0;
+    const int64_t K = src1->ne[0], bk = vec_dot_type(type) == QMM_TYPE_Q8_K ? 256 : 32;
+    if (K <= 0 || K % bk) return 0;
+    ctx->key.valid = false;                                   // a fresh quantization
+    TiledAct t;
+    if (quantize_src1_tiled(ctx, type, src1, (K + 255) / 256, &t)) return 0;
+    const bool kq = t.vdt == QMM_TYPE_Q8_K;
+    const size_t a = tiled_a_bytes(t.ntiles, t.nblk), d = tiled_d_bytes(t.ntiles, kq ? t.nblk / 8 : t.nblk);
+    const size_t sb = kq ? tiled_s_bytes(t.ntiles, t.nblk) : 0;
+    if ((int64_t)(a + d + sb) > cap) return 0;
+    uint8_t * o = (uint8_t *)out;
+    hipError_t e = hipMemcpyAsync(o, t.A, a, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(o + a, t.D, d, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess && kq) e = hipMemcpyAsync(o + a + d, t.S, sb, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    return e == hipSuccess ? (int64_t)(a + d + sb) : 0;
+}
+
 int qmm_internal_gemv_extent(int32_t type, const int64_t ne0[4], int64_t N, int64_t nbatch, int64_t id_n_used,
                              int64_t out[8]) {
     const TypeLayout * L = type_layout(type);

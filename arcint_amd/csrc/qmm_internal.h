@@ -301,28 +301,39 @@ hipError_t launch_gemm(int type, const WView & w, const ActBuf & a, int64_t N, i
 //      8 (r / 4) + 4 h + r % 4, the column that register r of lane half h
 //      holds
 // ---------------------------------------------------------------------------
+//   q8_K (the K-quant GEMM) keeps A as above (a 32-weight block is a sub-block) and per
+//   256-weight super-block sb of tile t:
+//   D  f32 [t][sb][32]      the super-block scale d in the same output order
+//   S  int8 [t][sb][32][16] column i's 8 sub-block code sums split as 64 bh + bl: bh[8],
+//      then bl[8] (the A operand of the Q4_K min term)
+// ---------------------------------------------------------------------------
 struct TiledAct {
     int8_t * A;
     float * D;
+    int8_t * S;        // q8_K only
     int64_t nblk;      // 32-weight blocks per column (ldk / 32)
     int64_t ntb;       // tiles per batch
     int64_t ntiles;    // tiles of all batches
     int64_t N;         // columns per batch
+    int vdt;           // QMM_TYPE_Q8_0 or QMM_TYPE_Q8_K
 };
 __host__ __device__ constexpr int tiled_pos(int i) { return 16 * ((i >> 2) & 1) + 4 * (i >> 3) + (i & 3); }
 // bytes of the two arrays for ntiles tiles of nblk blocks (each a multiple of 256)
 __host__ __device__ inline size_t tiled_a_bytes(int64_t ntiles, int64_t nblk) { return (size_t)(ntiles * nblk) * 1024; }
 __host__ __device__ inline size_t tiled_d_bytes(int64_t ntiles, int64_t nblk) { return (size_t)(ntiles * nblk) * 128; }
-// q8_0 quantization of the f32 columns into the tiled layout (ggml-cpu's from_float numerics)
+__host__ __device__ inline size_t tiled_s_bytes(int64_t ntiles, int64_t nblk) { return (size_t)(ntiles * nblk) * 64; }
+// quantization of the f32 columns into the tiled layout (t.vdt: q8_0 or q8_K, ggml-cpu's
+// from_float numerics)
 hipError_t launch_quantize_tiled(const F32Cols & src, int64_t K, const TiledAct & t, hipStream_t s);
 
-// Streaming GEMM for the types whose scale is one float per 32-weight block
-// (Q4_0, Q8_0, IQ4_NL): every weight batch b < nbatch, dst[doff(b) + n d_nb1
-// + m] = W(mat(b)) row m . column n of batch b, n < N, m < M.  Each output is
-// written once (no atomics, no zeroing of dst).
+// Streaming GEMM for Q4_0, Q8_0, IQ4_NL (q8_0 activations) and Q4_K (q8_K): for
+// every weight batch b < nbatch, dst[doff(b) + n d_nb1 + m] = W(mat(b)) row m .
+// column n of batch b, n < N, m < M.  Each output is written once (no atomics,
+// no zeroing of dst).
 bool gemm3_supported(int type);
 struct G3Shape {
-    int C, U, KS, SB;              // column tiles per wave, row tiles (64) per work-group, K slices, blocks per stage
+    int C, U, KS, SB;              // column tiles per wave, row-unit waves per K slice, K slices, blocks per stage
+    int R;                         // rows per wave (64: Q4_0 / Q8_0 / IQ4_NL, 32: Q4_K)
     int64_t mbn, nbn;              // work-group blocks along M and N per batch
     int sps, nst;                  // stages per K slice, stages along K
     int threads, lds;
@@ -400,3 +411,8 @@ hipError_t launch_quant_route(const F32Cols & src, int64_t K, int64_t ncols, con
 // the GEMV weight loads of a MUL_MAT / MUL_MAT_ID shape replayed on the host (qmm_api.cpp).
 extern "C" int qmm_internal_gemv_extent(int32_t type, const int64_t ne0[4], int64_t N, int64_t nbatch,
                                         int64_t id_n_used, int64_t out[8]);
+// The streaming GEMM's activation pre-pass for weights of `type` (q8_0 or q8_K tiles) over the
+// f32 tensor src1, copied to host `out`: A, then D, then S (q8_K), as the kernel reads them.
+// Returns the byte count written (0 on error; `cap` too small is an error).
+extern "C" int64_t qmm_internal_quantize_tiled(struct qmm_ctx * ctx, const struct qmm_tensor * src1, int32_t type,
+                                               void * out, int64_t cap);

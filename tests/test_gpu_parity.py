@@ -21,7 +21,7 @@ TYPES = [qmm.Q4_0, qmm.Q8_0, qmm.Q4_K, qmm.Q5_K, qmm.Q6_K, qmm.IQ4_NL, qmm.IQ4_X
 MMA_TYPES = (qmm.Q4_0, qmm.Q8_0, qmm.Q4_K, qmm.IQ4_XS, qmm.IQ4_NL, qmm.Q6_K)
 TOL = 1e-3
 # the types whose GEMM streams weights per wave (one float scale per 32-weight block)
-STREAM_TYPES = (qmm.Q4_0, qmm.Q8_0, qmm.IQ4_NL)
+STREAM_TYPES = (qmm.Q4_0, qmm.Q8_0, qmm.IQ4_NL, qmm.Q4_K)
 
 
 def gemm_path(qtype):
@@ -352,6 +352,69 @@ def test_quantize_act_exact_ties(be, sc):
     assert np.array_equal(b0[2:34].view(np.int8), np.concatenate([[127], np.where(k % 2 == 0, k, k + 1)]).astype(np.int8))
 
 
+def tiled_expected(orc, vdt, x, ntb):
+    """The streaming GEMM's tiled activations from the oracle's quantization of x [N, K]: A
+    [tile][32-weight block][lane half h][column i][16 codes], D [tile][scale block][32] f32 in
+    MFMA output order (column i at 16 ((i >> 2) & 1) + 4 (i >> 3) + (i & 3)), and for q8_K S
+    [tile][super-block][column][bh[8], bl[8]] with each sub-block sum = 64 bh + bl."""
+    N, K = x.shape
+    nblk = K // 32
+    codes = np.zeros((ntb * 32, K), np.int8)
+    if vdt == qmm.Q8_K:
+        nsb = K // 256
+        q = orc.quantize_q8_K(x).reshape(N, nsb, 292)
+        d = np.zeros((ntb * 32, nsb), np.float32)
+        d[:N] = q[:, :, 0:4].copy().view(np.float32)[:, :, 0]
+        codes[:N] = q[:, :, 4:260].view(np.int8).reshape(N, K)
+        bs = np.zeros((ntb * 32, nsb, 8), np.int64)
+        bs[:N] = q[:, :, 260:292].copy().view(np.int16).reshape(N, nsb, 8, 2).sum(-1)
+    else:
+        nsb = nblk
+        q = orc.quantize_q8_0(x).reshape(N, nblk, 34)
+        d = np.zeros((ntb * 32, nblk), np.float32)
+        d[:N] = q[:, :, 0:2].copy().view(np.float16)[:, :, 0].astype(np.float32)
+        codes[:N] = q[:, :, 2:34].view(np.int8).reshape(N, K)
+    A = codes.reshape(ntb, 32, nblk, 2, 16).transpose(0, 2, 3, 1, 4)
+    pos = np.array([16 * ((i >> 2) & 1) + 4 * (i >> 3) + (i & 3) for i in range(32)])
+    D = np.zeros((ntb, nsb, 32), np.float32)
+    D[:, :, pos] = d.reshape(ntb, 32, nsb).transpose(0, 2, 1)
+    parts = [A.ravel().view(np.uint8), D.ravel().view(np.uint8)]
+    if vdt == qmm.Q8_K:
+        bsr = bs.reshape(ntb, 32, nsb, 8).transpose(0, 2, 1, 3)
+        S = np.concatenate([bsr >> 6, bsr & 63], -1).astype(np.int8)
+        parts.append(S.ravel().view(np.uint8))
+    return np.concatenate(parts)
+
+
+@pytest.mark.parametrize("qtype", [qmm.Q4_0, qmm.Q4_K])
+@pytest.mark.parametrize("N,K", [(1, 256), (33, 512), (64, 2048), (100, 768)])
+def test_quantize_tiled(be, sc, orc, qtype, N, K):
+    """the streaming GEMM's tiled pre-pass is the oracle's quantization, laid out as the kernel
+    reads it (columns past N zero)"""
+    import ctypes as C
+    say("quantize_tiled", qtype, N, K)
+    x = synth.activations(N, K, seed=N + K)
+    x[0, 7] = -3 * np.abs(x[0]).max()                          # a negative first maximum
+    if N > 3:
+        x[3, :] = 0.0                                          # an all-zero column
+    ntb = -(-N // 32)
+    want = tiled_expected(orc, qmm.Q8_K if qtype == qmm.Q4_K else qmm.Q8_0, x, ntb)
+    L = qmm.load()
+    f = L.qmm_internal_quantize_tiled
+    f.argtypes = [C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_int64]
+    f.restype = C.c_int64
+    out = np.zeros(want.size + 64, np.uint8)
+    xt = sc.f32(x)
+    n = f(be.h, C.byref(xt.c), qtype, out.ctypes.data, out.size)
+    assert n == want.size
+    got = out[:n]
+    nA = ntb * (K // 32) * 1024
+    assert np.array_equal(got[:nA], want[:nA]), "codes"
+    nD = ntb * (K // (256 if qtype == qmm.Q4_K else 32)) * 128
+    assert np.array_equal(got[nA:nA + nD], want[nA:nA + nD]), "scales"
+    assert np.array_equal(got[nA + nD:], want[nA + nD:]), "split sums"
+
+
 # ------------------------------------------------------------------ MUL_MAT
 def run_mul_mat(be, sc, orc, qtype, M, K, N, seed):
     raw = synth.weights(qtype, M, K, seed)
@@ -617,10 +680,11 @@ GEMM_FULL = [
 
 
 @pytest.mark.parametrize("qtype", [qmm.Q4_K, qmm.Q6_K])
-def test_gemm_tail_split(be, sc, orc, qtype):
+def test_gemm_tail_split(be, sc, orc, monkeypatch, qtype):
     # 66 row tiles x 4 column tiles = 264 > 256 work-groups: the first 256 tiles run whole and
     # the last row of tiles (partial: 8384 = 65.5 x 128 rows) in K slices added into dst rows
-    # the pre-pass zeroed
+    # the pre-pass zeroed (Q4_K on this kernel when the streaming one is switched off)
+    monkeypatch.setenv("QMM_GEMM3_Q4K", "0")
     M, K, N = 8384, 1024, 512
     fake = qmm.Buffer(ptr=0x1000, size=1 << 44)
     info = qmm.describe_mul_mat(qmm.Tensor(fake, qtype, (K, M)), qmm.Tensor(fake, qmm.F32, (K, N)),
@@ -645,7 +709,7 @@ def test_full_size_gemm(be, sc, orc, monkeypatch, qtype, M, K, N):
 # streaming GEMM launch shapes: K slices per work-group KS (1..3) forced, on ragged shapes (N
 # not a multiple of 32, a work-group's last row tiles missing, K not a multiple of 256 or of a
 # stage, batches with broadcast weights)
-@pytest.mark.parametrize("qtype", STREAM_TYPES)
+@pytest.mark.parametrize("qtype", [qmm.Q4_0, qmm.Q8_0, qmm.IQ4_NL])
 @pytest.mark.parametrize("KS", [1, 2, 3])
 def test_gemm_stream_shapes(be, sc, orc, monkeypatch, qtype, KS):
     monkeypatch.setenv("QMM_GEMM3_KS", str(KS))
@@ -660,6 +724,37 @@ def test_gemm_stream_shapes(be, sc, orc, monkeypatch, qtype, KS):
     raw = synth.weights(qtype, 2 * M, K, seed=305)
     w = sc.weights(qtype, raw, (K, M, 2))
     x = synth.activations(4 * N, K, seed=306).reshape(4, N, K)
+    y = sc.empty_f32((M, N, 4))
+    be.mul_mat(w, sc.f32(x), y)
+    be.synchronize()
+    assert be.last_path() == "gemm-stream"
+    got = be.get_f32(y).reshape(4, N, M)
+    rb = synth.row_bytes(qtype, K) * M
+    for i2 in range(4):
+        ref = orc.mul_mat(qtype, raw[(i2 // 2) * rb:(i2 // 2 + 1) * rb], M, K, x[i2])
+        assert rel_err(got[i2], ref) <= TOL
+
+
+# Q4_K streaming GEMM: each launch shape (row-half waves U x K slices KS, forced by index) on
+# ragged shapes: rows not a whole number of 32-row halves or of a work-group's U, column tiles
+# not a whole number of pairs (N = 80: 3 tiles), K slices of unequal length (G = 17 over 3 or
+# 4 slices), a single super-block, batches with broadcast weights
+@pytest.mark.parametrize("shape", range(6))
+def test_gemm_stream_q4k_shapes(be, sc, orc, monkeypatch, shape):
+    monkeypatch.setenv("QMM_GEMM3_KQ", str(shape))
+    monkeypatch.setenv("QMM_GEMM_MIN_COLS", "16")
+    qtype = qmm.Q4_K
+    for (M, K, N, seed) in [(200, 768, 33, 311), (64, 2048, 100, 312), (130, 256, 64, 313), (448, 1280, 161, 314),
+                            (330, 4352, 80, 317), (1000, 1024, 128, 318)]:
+        say("gemm-stream q4k", shape, M, K, N)
+        got, ref = run_mul_mat(be, sc, orc, qtype, M, K, N, seed=seed)
+        assert be.last_path() == "gemm-stream"
+        assert rel_err(got, ref) <= TOL, (M, K, N)
+    say("gemm-stream q4k batches", shape)
+    K, M, N = 512, 96, 45
+    raw = synth.weights(qtype, 2 * M, K, seed=315)
+    w = sc.weights(qtype, raw, (K, M, 2))
+    x = synth.activations(4 * N, K, seed=316).reshape(4, N, K)
     y = sc.empty_f32((M, N, 4))
     be.mul_mat(w, sc.f32(x), y)
     be.synchronize()

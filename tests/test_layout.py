@@ -10,6 +10,8 @@
 * the GEMV launch plan: the waves cover the K axis, no work-group is left
   without groups, and the LDS of the cross-wave sum is what the plan says.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -303,3 +305,44 @@ def test_gemm_stream_plan(qtype, K, M, N):
     assert info["threads"] == 64 * 4 * KS
     assert info["workgroups"] == 8 * -(-units // 8)
     assert info["lds_bytes"] == max(KS * 2 * SB * 1152, (KS - 1) * 4 * 32 * 64 * 4) <= 160 * 1024
+
+
+# Q4_K on the streaming GEMM: a wave per (32-row half of a tile, pair of 32-column tiles, K
+# slice); U row-half waves per K slice share the staged activations, KS slices per work-group.
+# (U, KS) minimizes rounds of work-groups on 256 CUs (12-wave groups: one per CU, whole rounds;
+# 4-wave: three per CU, a partial last round counted as its fraction) times super-blocks per
+# slice, ties to the earlier candidate; LDS: two 18 KB stages per slice (+ a 1 KB slot when 18
+# units do not divide over U), or the slices' sums if larger
+KQ_CANDS = [(12, 1, 1), (6, 2, 1), (4, 3, 1), (3, 4, 1), (4, 1, 3), (2, 2, 3)]
+GEMM3_KQ_SHAPES = [(5120, 17408, 512), (5120, 12288, 512), (5120, 1024, 512), (6144, 5120, 512),
+                   (4096, 4096, 128), (256, 130, 33)]
+
+
+@pytest.mark.parametrize("K,M,N", GEMM3_KQ_SHAPES)
+def test_gemm_stream_q4k_plan(K, M, N):
+    fake = qmm.Buffer(ptr=0x1000, size=1 << 44)
+    os.environ["QMM_GEMM_MIN_COLS"] = "16"
+    try:
+        info = qmm.describe_mul_mat(qmm.Tensor(fake, qmm.Q4_K, (K, M)), qmm.Tensor(fake, qmm.F32, (K, N)),
+                                    qmm.Tensor(fake, qmm.F32, (M, N)))
+    finally:
+        del os.environ["QMM_GEMM_MIN_COLS"]
+    assert info["path"] == "gemm-stream"
+    G, nrh, ncp = K // 256, 2 * -(-M // 64), -(-(-(-N // 32)) // 2)
+    best = None
+    for U, ks, per_cu in KQ_CANDS:
+        sps = -(-G // ks)
+        mbn = -(-nrh // U)
+        slots = 256 * per_cu
+        nwg = mbn * ncp
+        rounds = max(64, -(-(nwg * 64) // slots)) if per_cu > 1 else 64 * -(-nwg // slots)
+        cost = rounds * sps
+        if best is None or cost < best[0]:
+            best = (cost, U, -(-G // sps), sps, mbn)
+    _, U, KS, sps, mbn = best
+    assert info["k_slices"] == KS and info["cols_per_task"] == 64
+    assert info["threads"] == 64 * U * KS
+    assert info["workgroups"] == 8 * -(-(mbn * ncp) // 8)
+    assert info["groups_per_wave"] == sps
+    lds = max(KS * 2 * 18 * 1024 + (1024 if 18 % U else 0), (KS - 1) * U * 32 * 64 * 4)
+    assert info["lds_bytes"] == lds <= 160 * 1024
