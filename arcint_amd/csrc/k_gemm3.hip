@@ -327,8 +327,12 @@ __global__ __launch_bounds__(64 * kU * kMaxKS) void k_gemm3(G3Params p) {
 //    16 h .. 16 h + 15 of sub-block 2c and whose high nibbles are those of sub-block 2c + 1, which
 //    is the MFMA's B operand for row j as it lies (no lane exchange), and the output lane (j, h)
 //    holds row j, so the lane's own header gives its row's scales;
-//  * sub-block s of both column tiles: two MFMAs on the raw nibbles (0..15), each int32 result
-//    multiplied by the row's 6-bit scale into the super-block's integer sum (v_mad_i32_i24);
+//  * the 6-bit sub-block scale goes into the B operand: sc = 8 sh + sl with 3-bit halves, so
+//    q sh and q sl (<= 105) are int8 (one packed 16-bit multiply per dword: a byte times s <= 7
+//    carries nothing into the next), and four MFMA chains per sub-block (sh and sl, two column
+//    tiles) accumulate the super-block's sums in place; isc = 8 sum_sh + sum_sl at the end.  The
+//    VALU never waits for an MFMA result inside the super-block (a per-row multiply-add on each
+//    sub-block's int32 result cost 256 VALU instructions per super-block and wave, 47 % of it);
 //  * the min term sum_j m_j bsum_j is two MFMAs per column tile and super-block: A = the
 //    columns' split sums bh (then bl, bsum = 64 bh + bl) at k = j, B = the row's 8 mins; the
 //    second one starts from 64 * first + the bits of 12582912.0f, so its result read as a float
@@ -361,7 +365,27 @@ struct KQParams {
     int U, KS, sps;                      // row-half waves per K slice, K slices, super-blocks per slice
     GemmBatch bt;
     float * dst;
+    // grouped MoE mode: work-group column pair nb is unit nb of the route (nbn = the units'
+    // upper bound, *nunits the count), its activations gathered from the route's quantization
+    const GemmUnit * units;
+    const int32_t * nunits;
+    const int8_t * codes;                // [column][ldk]
+    const float * dcol;                  // [column][nsb]
+    const int8_t * bsp;                  // [super-block][ldT][16]
+    int64_t ldk, ldT, ncols;
 };
+
+// the two 16-bit halves of v times those of s (v_pk_mul_lo_u16)
+__device__ __forceinline__ uint32_t mul_u16x2(uint32_t v, uint32_t s) {
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, v) * __builtin_bit_cast(u16x2, s));
+}
+
+// 4 bytes per lane from a buffer into LDS at lds + 4 lane (lds wave-uniform)
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, uint8_t * lds, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 4, (int)voff, (int)soff,
+                                             0, 0);
+}
 
 // 16 bytes per lane from a buffer into LDS at lds + 16 lane (lds wave-uniform)
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t * lds, uint32_t voff, uint32_t soff) {
@@ -369,7 +393,7 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t * lds, u
                                              0, 0);
 }
 
-template <int U>
+template <int U, bool GATHER>
 __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q4k(KQParams p) {
     extern __shared__ __align__(16) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, j32 = lane & 31;
@@ -381,7 +405,13 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q4k(KQParams p) {
     const uint32_t mb = L / (uint32_t)p.nbn, nb = L - mb * (uint32_t)p.nbn;
     const uint32_t bz = blockIdx.y;
     const uint32_t i2 = bz % (uint32_t)p.bt.ne12, i3 = bz / (uint32_t)p.bt.ne12;
-    const int64_t mat = (int64_t)(i2 / (uint32_t)p.bt.r2) + (int64_t)(i3 / (uint32_t)p.bt.r3) * p.bt.ne02;
+    int64_t mat = (int64_t)(i2 / (uint32_t)p.bt.r2) + (int64_t)(i3 / (uint32_t)p.bt.r3) * p.bt.ne02;
+    int ncu = 64;                                             // grouped mode: the unit's columns
+    if constexpr (GATHER) {
+        if ((int32_t)nb >= __builtin_amdgcn_readfirstlane(*p.nunits)) return;   // uniform: past the route's units
+        mat = __builtin_amdgcn_readfirstlane(p.units[nb].mat);
+        ncu = __builtin_amdgcn_readfirstlane(p.units[nb].ncols);
+    }
     const int64_t rh_raw = (int64_t)mb * U + u;               // the wave's row half
     const bool row_ok = rh_raw < 2 * p.w.ntiles;              // a missing row half computes a copy, stores nothing
     const int64_t rh = row_ok ? rh_raw : 2 * p.w.ntiles - 1;
@@ -393,35 +423,87 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q4k(KQParams p) {
     const int s0 = ks * p.sps;
     const int s1 = std::min(s0 + p.sps, nsb);                 // (every slice has super-blocks)
 
+    if (GATHER && mat < 0) {                                  // invalid ids: zero rows (uniform)
+        const int64_t m = mtile * kTileRows + 32 * t + j32;
+        if (!row_ok || m >= p.w.M || ks > 0) return;
+        for (int n = h; n < ncu; n += 2) p.dst[p.units[nb].dst_off[n] + m] = 0.0f;
+        return;
+    }
+
     const __amdgpu_buffer_rsrc_t wbuf = buffer_rsrc(tile_group(p.w, mat, mtile, 0), (uint32_t)(p.w.G * p.w.tg));
-    // the pair's activations; a pair with one tile reads zeros for the second (past the range)
-    const __amdgpu_buffer_rsrc_t abuf = buffer_rsrc(p.tA + ct0 * p.nsb * 8192, (uint32_t)(nct * p.nsb * 8192));
-    const __amdgpu_buffer_rsrc_t sbuf = buffer_rsrc(p.tS + ct0 * p.nsb * 512, (uint32_t)(nct * p.nsb * 512));
-    const __amdgpu_buffer_rsrc_t dbuf = buffer_rsrc(p.tD + ct0 * p.nsb * 32, (uint32_t)(nct * p.nsb * 128));
+    // the pair's activations; a pair with one tile reads zeros for the second (past the range);
+    // grouped mode: the whole quantization, each lane at its own column (zeros past the unit)
+    const __amdgpu_buffer_rsrc_t abuf = GATHER ? buffer_rsrc(p.codes, (uint32_t)(p.ncols * p.ldk))
+                                               : buffer_rsrc(p.tA + ct0 * p.nsb * 8192, (uint32_t)(nct * p.nsb * 8192));
+    const __amdgpu_buffer_rsrc_t sbuf = GATHER ? buffer_rsrc(p.bsp, (uint32_t)(p.nsb * p.ldT * 16))
+                                               : buffer_rsrc(p.tS + ct0 * p.nsb * 512, (uint32_t)(nct * p.nsb * 512));
+    const __amdgpu_buffer_rsrc_t dbuf = GATHER ? buffer_rsrc(p.dcol, (uint32_t)(p.ncols * p.nsb * 4))
+                                               : buffer_rsrc(p.tD + ct0 * p.nsb * 32, (uint32_t)(nct * p.nsb * 128));
     const uint32_t lane16 = (uint32_t)lane * 16;
+    // grouped mode: the activation column of lane (j32, h) in tile c (both lane halves share it),
+    // and the column of lane `lane` for the S and D gathers (tile lane / 32); kOut past the unit
+    constexpr uint32_t kOut = 0x7ff00000u;
+    uint32_t gcol[2] = { 0, 0 }, gsd = 0;
+    if constexpr (GATHER) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const int slot = 32 * c + j32;
+            gcol[c] = slot < ncu ? (uint32_t)p.units[nb].col[slot] : kOut;
+        }
+        gsd = (lane >> 5) ? gcol[1] : gcol[0];
+    }
 
     // ---- staging of super-block s into buffer b of the slice: 18 units of 1 KB (A: tile
     // unit / 8, sub-block unit % 8; S; D, lanes 16.. reading zeros into the slot's padding),
     // wave u taking units u, u + U, ...
     constexpr int NU = kq_units(U);
     const uint32_t a_stride = (uint32_t)p.nsb * 8192, s_stride = (uint32_t)p.nsb * 512, d_stride = (uint32_t)p.nsb * 128;
-    const uint32_t s_lane = (uint32_t)(lane >> 5) * s_stride + (uint32_t)j32 * 16;
-    const uint32_t d_lane = lane < 16 ? (uint32_t)(lane >> 3) * d_stride + (uint32_t)(lane & 7) * 16 : 0x7ff00000u;
+    uint32_t s_lane = (uint32_t)(lane >> 5) * s_stride + (uint32_t)j32 * 16;
+    uint32_t d_lane = lane < 16 ? (uint32_t)(lane >> 3) * d_stride + (uint32_t)(lane & 7) * 16 : kOut;
+    // Grouped mode, A: unit (c, g) holds columns 4g..4g+3 of tile c whole (the super-block's 256
+    // code bytes of each, 16 lanes per column: a few whole lines per load instead of 32 pieces);
+    // in LDS column i of tile c sits at c 8192 + 256 i with its 16-byte chunk q at slot
+    // q ^ (i & 15), so the MFMA operand reads (chunk 2 j + h of column i for lane (i, h)) hit
+    // 16 different slots per 16 lanes: no bank conflicts.  avo[k]: lane offset of this wave's
+    // k-th A unit.  S: the column's 16 bytes; D: its 4.
+    uint32_t avo[NU];
+#pragma unroll
+    for (int k = 0; k < NU; ++k) avo[k] = 0;
+    if constexpr (GATHER) {
+#pragma unroll
+        for (int k = 0; k < NU; ++k) {
+            const int unit = u + k * U;
+            if (unit < 16) {
+                const int ci = 4 * (unit & 7) + (lane >> 4);  // column of the tile
+                const int slot = 32 * (unit >> 3) + ci;
+                const uint32_t col = slot < ncu ? (uint32_t)p.units[nb].col[slot] : kOut;
+                const uint32_t q = (uint32_t)((lane & 15) ^ (ci & 15));
+                avo[k] = col == kOut ? kOut : col * (uint32_t)p.ldk + 16 * q;
+            }
+        }
+        s_lane = gsd == kOut ? kOut : gsd * 16;
+        d_lane = gsd == kOut ? kOut : gsd * (uint32_t)p.nsb * 4;
+    }
     uint8_t * const dump = lds + 2 * p.KS * kKQStage;
     auto stage = [&](int s, int b) {
         uint8_t * S = lds + (ks * 2 + b) * kKQStage;
 #pragma unroll
         for (int i = 0; i < NU; ++i) {
             const int unit = u + i * U;                       // wave-uniform
-            if (unit < 16)
-                dma16(abuf, S + unit * 1024, lane16 + (uint32_t)(unit >> 3) * a_stride + (uint32_t)(unit & 7) * 1024,
-                      (uint32_t)s * 8192);
-            else if (unit == 16)
-                dma16(sbuf, S + 16 * 1024, s_lane, (uint32_t)s * 512);
-            else if (unit == 17)
-                dma16(dbuf, S + 17 * 1024, d_lane, (uint32_t)s * 128);
-            else
-                dma16(dbuf, dump, 0x7ff00000u, 0);            // (nothing: keeps the count)
+            if (unit < 16) {
+                if (GATHER)
+                    dma16(abuf, S + unit * 1024, avo[i], (uint32_t)s * 256);
+                else
+                    dma16(abuf, S + unit * 1024, lane16 + (uint32_t)(unit >> 3) * a_stride + (uint32_t)(unit & 7) * 1024,
+                          (uint32_t)s * 8192);
+            } else if (unit == 16) {
+                dma16(sbuf, S + 16 * 1024, s_lane, GATHER ? (uint32_t)(s * p.ldT * 16) : (uint32_t)s * 512);
+            } else if (unit == 17) {
+                if (GATHER) dma4(dbuf, S + 17 * 1024, d_lane, (uint32_t)s * 4);   // [tile][32] f32 in column order
+                else dma16(dbuf, S + 17 * 1024, d_lane, (uint32_t)s * 128);
+            } else {
+                dma16(dbuf, dump, kOut, 0);                   // (nothing: keeps the count)
+            }
         }
     };
 
@@ -440,27 +522,41 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q4k(KQParams p) {
         const uint32_t dd = hd.x;
         const uint32_t sn = (uint32_t)std::min(s + 1, s1 - 1) * tgs;   // the next super-block (clamped)
         hd = bld16(wbuf, row16, sn + 8 * kChunk);
-        v16i isc0 = v16i{}, isc1 = v16i{};
+        const uint32_t sh03 = (sc03 >> 3) & 0x07070707u, sl03 = sc03 & 0x07070707u;
+        const uint32_t sh47 = (sc47 >> 3) & 0x07070707u, sl47 = sc47 & 0x07070707u;
+        v16i acc[4];                                          // [sh, sl] x [tile 0, tile 1]
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const uint4 q = ch[j >> 1];
-            const int sh = 4 * (j & 1);
-            const v4i bop = v4i{ (int)((q.x >> sh) & 0x0F0F0F0Fu), (int)((q.y >> sh) & 0x0F0F0F0Fu),
-                                 (int)((q.z >> sh) & 0x0F0F0F0Fu), (int)((q.w >> sh) & 0x0F0F0F0Fu) };
+            const int nsh = 4 * (j & 1);
+            const uint32_t n0 = (q.x >> nsh) & 0x0F0F0F0Fu, n1 = (q.y >> nsh) & 0x0F0F0F0Fu;
+            const uint32_t n2 = (q.z >> nsh) & 0x0F0F0F0Fu, n3 = (q.w >> nsh) & 0x0F0F0F0Fu;
             if (j & 1) ch[j >> 1] = bld16(wbuf, wl, sn + 2 * (j >> 1) * kChunk);
-            const v4i a0 = *reinterpret_cast<const v4i *>(S + j * 1024 + lane16);
-            const v4i a1 = *reinterpret_cast<const v4i *>(S + 8192 + j * 1024 + lane16);
-            const v16i e0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bop, v16i{}, 0, 0, 0);
-            const v16i e1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bop, v16i{}, 0, 0, 0);
+            // (grouped mode: chunk 2 j + h of column j32 at its swizzled slot)
+            const uint32_t aoff = GATHER ? (uint32_t)j32 * 256 + 16 * (uint32_t)((2 * j + h) ^ (j32 & 15))
+                                         : (uint32_t)(j * 1024) + lane16;
+            const v4i a0 = *reinterpret_cast<const v4i *>(S + aoff);
+            const v4i a1 = *reinterpret_cast<const v4i *>(S + 8192 + aoff);
             const int js = j ^ (QMM_RED == 5);                // (mutation 5: neighbouring scales swapped)
-            const int sj = (int)(((js < 4 ? sc03 : sc47) >> (8 * (js & 3))) & 0xffu);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                isc0[r] += __mul24(sj, e0[r]);
-                isc1[r] += __mul24(sj, e1[r]);
-            }
-            asm volatile("" : "+v"(isc0), "+v"(isc1));
+            // the sub-block's sh and sl in both 16-bit halves (bytes 1 and 3 zero)
+            const uint32_t sel = 0x0c000c00u | (uint32_t)(js & 3) * 0x00010001u;
+            const uint32_t mh = __builtin_amdgcn_perm(js < 4 ? sh03 : sh47, js < 4 ? sh03 : sh47, sel);
+            const uint32_t ml = __builtin_amdgcn_perm(js < 4 ? sl03 : sl47, js < 4 ? sl03 : sl47, sel);
+            const v4i bh = v4i{ (int)mul_u16x2(n0, mh), (int)mul_u16x2(n1, mh), (int)mul_u16x2(n2, mh),
+                                (int)mul_u16x2(n3, mh) };
+            const v4i bl = v4i{ (int)mul_u16x2(n0, ml), (int)mul_u16x2(n1, ml), (int)mul_u16x2(n2, ml),
+                                (int)mul_u16x2(n3, ml) };
+            acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bh, j ? acc[0] : v16i{}, 0, 0, 0);
+            acc[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bh, j ? acc[1] : v16i{}, 0, 0, 0);
+            acc[2] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bl, j ? acc[2] : v16i{}, 0, 0, 0);
+            acc[3] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bl, j ? acc[3] : v16i{}, 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
+        }
+        // isc = 8 sum_sh + sum_sl, in place (frees the sl sums before the min term)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            acc[0][r] = (acc[0][r] << 3) + acc[2][r];
+            acc[1][r] = (acc[1][r] << 3) + acc[3][r];
         }
         // min term, then the float combine of each column tile
         float d = h2f(dd & 0xffffu), dmin = h2f(dd >> 16);
@@ -479,21 +575,24 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q4k(KQParams p) {
             float dx[16];
 #pragma unroll
             for (int q4 = 0; q4 < 4; ++q4) {
-                const float4 v = *reinterpret_cast<const float4 *>(S + 17408 + c * 128 + h * 64 + 16 * q4);
+                // (output order: register r of half h is column 8 (r / 4) + 4 h + r % 4; the
+                // grouped mode's scales lie in column order)
+                const int off = GATHER ? 4 * (8 * q4 + 4 * h) : h * 64 + 16 * q4;
+                const float4 v = *reinterpret_cast<const float4 *>(S + 17408 + c * 128 + off);
                 dx[4 * q4] = v.x;
                 dx[4 * q4 + 1] = v.y;
                 dx[4 * q4 + 2] = v.z;
                 dx[4 * q4 + 3] = v.w;
             }
             v16f & o = c ? out1 : out0;
-            const v16i & is = c ? isc1 : isc0;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 // (the element goes through a scalar: clang's __builtin_bit_cast of an ext-vector
                 // element reads element 0)
                 const int iml = ml[r];
+                const int isc = acc[c][r];
                 const float wv = __builtin_fmaf(__builtin_bit_cast(float, iml), -dmin, nmag);   // -dmin * imn
-                const float v = __builtin_fmaf((float)is[r], d, wv);
+                const float v = __builtin_fmaf((float)isc, d, wv);
                 o[r] = __builtin_fmaf(v, dx[r], o[r]);
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -552,6 +651,18 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q4k(KQParams p) {
     if (!row_ok) return;
     const int64_t m = mtile * kTileRows + 32 * t + j32;
     if (m >= p.w.M) return;
+    if constexpr (GATHER) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const v16f & v = c ? out1 : out0;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int slot = 32 * c + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (slot < ncu) __builtin_nontemporal_store(v[r], p.dst + p.units[nb].dst_off[slot] + m);
+            }
+        }
+        return;
+    }
     float * dst = p.dst + (int64_t)i2 * p.bt.d_nb2 + (int64_t)i3 * p.bt.d_nb3 + m;
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
@@ -576,15 +687,28 @@ hipError_t launch_t(const G3Params & p, const G3Shape & sh, const dim3 & g, hipS
     return hipGetLastError();
 }
 
-template <int U>
+template <int U, bool GATHER>
 hipError_t launch_kq(const KQParams & q, const G3Shape & sh, const dim3 & g, const dim3 & b, hipStream_t s,
                      const KTime * kt) {
-    static const hipError_t attr =
-        hipFuncSetAttribute((const void *)k_gemm3_q4k<U>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    static const hipError_t attr = hipFuncSetAttribute((const void *)k_gemm3_q4k<U, GATHER>,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (attr != hipSuccess) return attr;
-    if (kt) hipExtLaunchKernelGGL(k_gemm3_q4k<U>, g, b, (uint32_t)sh.lds, s, kt->start, kt->stop, 0, q);
-    else k_gemm3_q4k<U><<<g, b, sh.lds, s>>>(q);
+    if (kt) hipExtLaunchKernelGGL(k_gemm3_q4k<U, GATHER>, g, b, (uint32_t)sh.lds, s, kt->start, kt->stop, 0, q);
+    else k_gemm3_q4k<U, GATHER><<<g, b, sh.lds, s>>>(q);
     return hipGetLastError();
+}
+
+template <bool GATHER>
+hipError_t launch_kq_u(const KQParams & q, const G3Shape & sh, const dim3 & g, const dim3 & b, hipStream_t s,
+                       const KTime * kt) {
+    switch (sh.U) {
+        case 12: return launch_kq<12, GATHER>(q, sh, g, b, s, kt);
+        case 6: return launch_kq<6, GATHER>(q, sh, g, b, s, kt);
+        case 4: return launch_kq<4, GATHER>(q, sh, g, b, s, kt);
+        case 3: return launch_kq<3, GATHER>(q, sh, g, b, s, kt);
+        case 2: return launch_kq<2, GATHER>(q, sh, g, b, s, kt);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 int env_int3(const char * name, int dflt) {
@@ -606,10 +730,11 @@ namespace {
 // whole rounds; 4-wave ones go three to a CU and a partial last round costs its fraction (the
 // CUs take the next small group as one finishes; measured on 17408 x 5120 x 512: 4-wave groups
 // 141 us, (6, 2) 145 us, (12, 1) 155 us).  Ties go to the earlier (larger U) candidate.
-bool kq_shape(const WView & w, int64_t N, int64_t nbatch, G3Shape * sh) {
+// ncp = column pairs (grouped mode: route units) per batch
+bool kq_shape_ncp(const WView & w, int64_t ncp, int64_t nbatch, G3Shape * sh) {
     struct Cand { int U, KS, per_cu; };
     static const Cand cands[] = { { 12, 1, 1 }, { 6, 2, 1 }, { 4, 3, 1 }, { 3, 4, 1 }, { 4, 1, 3 }, { 2, 2, 3 } };
-    const int64_t nrh = 2 * w.ntiles, ncp = ((N + 31) / 32 + 1) / 2, G = w.G;
+    const int64_t nrh = 2 * w.ntiles, G = w.G;
     const int cus = 256;
     int64_t best = -1;
     const int forced = env_int3("QMM_GEMM3_KQ", -1);           // index into cands (tuning)
@@ -641,7 +766,48 @@ bool kq_shape(const WView & w, int64_t N, int64_t nbatch, G3Shape * sh) {
     sh->workgroups = 8 * ((sh->mbn * ncp + 7) / 8) * nbatch;
     return sh->mbn * ncp < 0x7fffffff && sh->lds <= 160 * 1024 && sh->threads <= 64 * kKQMaxWaves;
 }
+bool kq_shape(const WView & w, int64_t N, int64_t nbatch, G3Shape * sh) {
+    return kq_shape_ncp(w, ((N + 31) / 32 + 1) / 2, nbatch, sh);
+}
 }  // namespace
+
+bool gemm3_id_supported(int type) { return type == QMM_TYPE_Q4_K && gemm3_supported(type); }
+
+bool gemm3_id_shape(const WView & w, int64_t max_units, G3Shape * sh) {
+    return gemm3_id_supported(QMM_TYPE_Q4_K) && max_units > 0 && w.G > 0 && w.ntiles > 0 &&
+           kq_shape_ncp(w, max_units, 1, sh);
+}
+
+hipError_t launch_gemm3_id(int type, const WView & w, const ActBuf & a, const GemmUnit * units, const int32_t * nunits,
+                           int64_t max_units, float * dst, hipStream_t s, const KTime * kt) {
+    G3Shape sh;
+    if (!gemm3_id_supported(type) || a.vdt != QMM_TYPE_Q8_K || !a.bsp || !units || !nunits || a.ldk != w.G * 256 ||
+        !gemm3_id_shape(w, max_units, &sh) || a.ncols * a.ldk >= ((int64_t)1 << 31) ||
+        w.G * a.ldT * 16 >= ((int64_t)1 << 31) || a.ldT < a.ncols)
+        return hipErrorInvalidValue;
+    KQParams q{};
+    q.w = w;
+    q.nsb = w.G;
+    q.mbn = sh.mbn;
+    q.nbn = max_units;
+    q.total = sh.mbn * max_units;
+    q.chunk = (q.total + 7) / 8;
+    q.U = sh.U;
+    q.KS = sh.KS;
+    q.sps = sh.sps;
+    q.bt = GemmBatch{ 1, 1, 1, 0, 0, 0, 0 };                 // (one batch: mat comes from the unit)
+    q.dst = dst;
+    q.units = units;
+    q.nunits = nunits;
+    q.codes = a.codes;
+    q.dcol = a.d;
+    q.bsp = a.bsp;
+    q.ldk = a.ldk;
+    q.ldT = a.ldT;
+    q.ncols = a.ncols;
+    const dim3 g((unsigned)(8 * q.chunk), 1u), b(sh.threads);
+    return launch_kq_u<true>(q, sh, g, b, s, kt);
+}
 
 // Launch shape: C column tiles per wave (2 shares each weight unpack between two column tiles,
 // at twice the accumulators), kU row tiles per work-group, and K slices so that the waves come
@@ -699,14 +865,7 @@ hipError_t launch_gemm3(int type, const WView & w, const TiledAct & a, int64_t n
         q.bt = bt;
         q.dst = dst;
         const dim3 g((unsigned)(8 * q.chunk), (unsigned)nbatch), b(sh.threads);
-        switch (sh.U) {
-            case 12: return launch_kq<12>(q, sh, g, b, s, kt);
-            case 6: return launch_kq<6>(q, sh, g, b, s, kt);
-            case 4: return launch_kq<4>(q, sh, g, b, s, kt);
-            case 3: return launch_kq<3>(q, sh, g, b, s, kt);
-            case 2: return launch_kq<2>(q, sh, g, b, s, kt);
-            default: return hipErrorInvalidValue;
-        }
+        return launch_kq_u<false>(q, sh, g, b, s, kt);
     }
     G3Params p{};
     p.w = w;

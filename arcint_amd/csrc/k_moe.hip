@@ -23,9 +23,11 @@ namespace {
 
 constexpr int kRouteThreads = 1024;
 
-// one work-group of kRouteThreads; sm = [2 (n_as + 1)] ints of LDS, s_wsum = [kRouteThreads / 64]
+// one work-group of kRouteThreads; sm = [2 (n_as + 1)] ints of LDS, s_wsum = [kRouteThreads / 64];
+// tasks of up to TC pairs (GEMV tasks: 8, the grouped GEMM's units: 64)
+template <int TC>
 __device__ __forceinline__ void route_body(const RouteArgs & r, int32_t * __restrict__ scratch,
-                                           GemvTask * __restrict__ tasks, int32_t * __restrict__ ntasks,
+                                           TaskOf<TC> * __restrict__ tasks, int32_t * __restrict__ ntasks,
                                            int32_t * sm, int32_t * s_wsum) {
     const int64_t nbk = r.n_as + 1;     // buckets: the experts, then the invalid ids
     int32_t * cnt = sm;                 // [nbk] pair count, later the fill cursor
@@ -49,7 +51,7 @@ __device__ __forceinline__ void route_body(const RouteArgs & r, int32_t * __rest
         const int64_t per = (nbk + kRouteThreads - 1) / kRouteThreads, e0 = tid * per;
         int32_t local = 0;
         for (int64_t k = 0; k < per; ++k)
-            if (e0 + k < nbk) local += (cnt[e0 + k] + kMaxTaskCols - 1) / kMaxTaskCols;
+            if (e0 + k < nbk) local += (cnt[e0 + k] + TC - 1) / TC;
         const int lane = tid & 63, wave = tid >> 6;
         int32_t x = local;
 #pragma unroll
@@ -73,18 +75,18 @@ __device__ __forceinline__ void route_body(const RouteArgs & r, int32_t * __rest
         for (int64_t k = 0; k < per; ++k)
             if (e0 + k < nbk) {
                 tstart[e0 + k] = excl;
-                excl += (cnt[e0 + k] + kMaxTaskCols - 1) / kMaxTaskCols;
+                excl += (cnt[e0 + k] + TC - 1) / TC;
             }
     }
     __syncthreads();
     // task headers (the invalid bucket's tasks: mat = -1, zero rows)
     for (int64_t e = tid; e < nbk; e += kRouteThreads) {
         const int32_t c = cnt[e];
-        const int32_t nt = (c + kMaxTaskCols - 1) / kMaxTaskCols;
+        const int32_t nt = (c + TC - 1) / TC;
         for (int32_t k = 0; k < nt; ++k) {
-            GemvTask & T = tasks[tstart[e] + k];
+            TaskOf<TC> & T = tasks[tstart[e] + k];
             T.mat = e < r.n_as ? (int32_t)(QMM_RED == 7 ? (e + 1) % r.n_as : e) : -1;   // (mutation 7: next expert)
-            T.ncols = (c - k * kMaxTaskCols) < kMaxTaskCols ? (c - k * kMaxTaskCols) : kMaxTaskCols;
+            T.ncols = (c - k * TC) < TC ? (c - k * TC) : TC;
         }
     }
     __syncthreads();
@@ -94,32 +96,33 @@ __device__ __forceinline__ void route_body(const RouteArgs & r, int32_t * __rest
         const int32_t b = scratch[p];
         const int64_t t = p / r.n_used, i = p % r.n_used;
         const int32_t slot = atomicAdd(&cnt[b], 1);
-        GemvTask & T = tasks[tstart[b] + slot / kMaxTaskCols];
-        T.col[slot % kMaxTaskCols] = b < r.n_as ? (int32_t)((i % r.ne11) + t * r.ne11) : 0;
-        T.dst_off[slot % kMaxTaskCols] = t * r.dst_nb2 + i * r.dst_nb1;
+        TaskOf<TC> & T = tasks[tstart[b] + slot / TC];
+        T.col[slot % TC] = b < r.n_as ? (int32_t)((i % r.ne11) + t * r.ne11) : 0;
+        T.dst_off[slot % TC] = t * r.dst_nb2 + i * r.dst_nb1;
     }
 }
 
+template <int TC>
 __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs r, int32_t * __restrict__ scratch,
-                                                         GemvTask * __restrict__ tasks, int32_t * __restrict__ ntasks) {
+                                                         TaskOf<TC> * __restrict__ tasks, int32_t * __restrict__ ntasks) {
     extern __shared__ int32_t sm[];
     __shared__ int32_t s_wsum[kRouteThreads / 64];
-    route_body(r, scratch, tasks, ntasks, sm, s_wsum);
+    route_body<TC>(r, scratch, tasks, ntasks, sm, s_wsum);
 }
 
 // MUL_MAT_ID's two independent preparations in one launch: work-group 0 routes, the others
 // quantize the activations (the q8_0 or q8_K pass of the quantization launch, no dst
 // zeroing).  At decode both are a few microseconds of latency each; side by side the GEMV
 // waits for the longer one instead of their sum.
-template <int VDT>
+template <int VDT, int TC>
 __global__ __launch_bounds__(kRouteThreads) void k_quant_route(F32Cols src, int64_t K, int64_t ncols, ActBuf a,
                                                                RouteArgs r, int32_t * __restrict__ scratch,
-                                                               GemvTask * __restrict__ tasks,
+                                                               TaskOf<TC> * __restrict__ tasks,
                                                                int32_t * __restrict__ ntasks) {
     extern __shared__ int32_t sm[];
     __shared__ int32_t s_wsum[kRouteThreads / 64];
     if (blockIdx.x == 0) {                                        // uniform
-        route_body(r, scratch, tasks, ntasks, sm, s_wsum);
+        route_body<TC>(r, scratch, tasks, ntasks, sm, s_wsum);
         return;
     }
     const int64_t t = (int64_t)(blockIdx.x - 1) * kRouteThreads + threadIdx.x;
@@ -289,25 +292,46 @@ hipError_t launch_combine(const CombineArgs & a, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_route(const RouteArgs & r, int32_t * scratch, GemvTask * tasks, int32_t * ntasks, hipStream_t s) {
+namespace {
+template <int TC>
+hipError_t route_t(const RouteArgs & r, int32_t * scratch, TaskOf<TC> * tasks, int32_t * ntasks, hipStream_t s) {
     const size_t lds = (size_t)(r.n_as + 1) * 2 * sizeof(int32_t);
     if (lds > 64 * 1024) return hipErrorInvalidValue;
-    k_route<<<1, kRouteThreads, lds, s>>>(r, scratch, tasks, ntasks);
+    k_route<TC><<<1, kRouteThreads, lds, s>>>(r, scratch, tasks, ntasks);
     return hipGetLastError();
 }
 
-hipError_t launch_quant_route(const F32Cols & src, int64_t K, int64_t ncols, const ActBuf & a, const RouteArgs & r,
-                              int32_t * scratch, GemvTask * tasks, int32_t * ntasks, hipStream_t s) {
+template <int TC>
+hipError_t quant_route_t(const F32Cols & src, int64_t K, int64_t ncols, const ActBuf & a, const RouteArgs & r,
+                         int32_t * scratch, TaskOf<TC> * tasks, int32_t * ntasks, hipStream_t s) {
     const size_t lds = (size_t)(r.n_as + 1) * 2 * sizeof(int32_t);
     if (lds > 64 * 1024 || K <= 0 || ncols < 0 || a.ldk % 256 || a.ldk < K) return hipErrorInvalidValue;
     const int64_t nq = a.vdt == QMM_TYPE_Q8_0 ? ncols * (a.ldk / 4) : ncols * (a.ldk / 256) * 64;
     const int64_t grid = 1 + (nq + kRouteThreads - 1) / kRouteThreads;
     if (grid > 0x7fffffff) return hipErrorInvalidValue;
     if (a.vdt == QMM_TYPE_Q8_0)
-        k_quant_route<QMM_TYPE_Q8_0><<<dim3((unsigned)grid), kRouteThreads, lds, s>>>(src, K, ncols, a, r, scratch, tasks, ntasks);
+        k_quant_route<QMM_TYPE_Q8_0, TC><<<dim3((unsigned)grid), kRouteThreads, lds, s>>>(src, K, ncols, a, r, scratch,
+                                                                                          tasks, ntasks);
     else
-        k_quant_route<QMM_TYPE_Q8_K><<<dim3((unsigned)grid), kRouteThreads, lds, s>>>(src, K, ncols, a, r, scratch, tasks, ntasks);
+        k_quant_route<QMM_TYPE_Q8_K, TC><<<dim3((unsigned)grid), kRouteThreads, lds, s>>>(src, K, ncols, a, r, scratch,
+                                                                                          tasks, ntasks);
     return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_route(const RouteArgs & r, int32_t * scratch, GemvTask * tasks, int32_t * ntasks, hipStream_t s) {
+    return route_t(r, scratch, tasks, ntasks, s);
+}
+hipError_t launch_route(const RouteArgs & r, int32_t * scratch, GemmUnit * units, int32_t * nunits, hipStream_t s) {
+    return route_t(r, scratch, units, nunits, s);
+}
+hipError_t launch_quant_route(const F32Cols & src, int64_t K, int64_t ncols, const ActBuf & a, const RouteArgs & r,
+                              int32_t * scratch, GemvTask * tasks, int32_t * ntasks, hipStream_t s) {
+    return quant_route_t(src, K, ncols, a, r, scratch, tasks, ntasks, s);
+}
+hipError_t launch_quant_route(const F32Cols & src, int64_t K, int64_t ncols, const ActBuf & a, const RouteArgs & r,
+                              int32_t * scratch, GemmUnit * units, int32_t * nunits, hipStream_t s) {
+    return quant_route_t(src, K, ncols, a, r, scratch, units, nunits, s);
 }
 
 }  // namespace qmm

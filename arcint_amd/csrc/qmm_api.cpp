@@ -266,8 +266,9 @@ bool same_key(const qmm_ctx * ctx, int vdt, const qmm_tensor * src1, bool dT, bo
 struct PendingRoute {
     RouteArgs r;
     int32_t * scratch;
-    GemvTask * tasks;
+    GemvTask * tasks;              // GEMV tasks, or
     int32_t * ntasks;
+    GemmUnit * units = nullptr;    // the grouped GEMM's 64-column units (then tasks is unused)
 };
 
 // quantize src1 for the vec_dot type of `type` (skipped when this graph already did); with
@@ -288,7 +289,8 @@ int quantize_src1(qmm_ctx * ctx, int type, const qmm_tensor * src1, bool dT, Act
     if (!fixed && ctx->in_graph && same_key(ctx, vdt, src1, dT, false)) {
         *out = ctx->cached;
         if (z) QMM_HIP(ctx, launch_quantize(f32_cols(src1), K, 0, ctx->cached, z, ctx->stream));   // zeroing only
-        if (pr) QMM_HIP(ctx, launch_route(pr->r, pr->scratch, pr->tasks, pr->ntasks, ctx->stream));
+        if (pr && pr->units) QMM_HIP(ctx, launch_route(pr->r, pr->scratch, pr->units, pr->ntasks, ctx->stream));
+        else if (pr) QMM_HIP(ctx, launch_route(pr->r, pr->scratch, pr->tasks, pr->ntasks, ctx->stream));
         return QMM_OK;
     }
     size_t od, os, ot, ob;
@@ -314,7 +316,10 @@ int quantize_src1(qmm_ctx * ctx, int type, const qmm_tensor * src1, bool dT, Act
     a.ldk = ldk;
     a.ncols = ncols;
     a.vdt = vdt;
-    if (pr) QMM_HIP(ctx, launch_quant_route(f32_cols(src1), K, ncols, a, pr->r, pr->scratch, pr->tasks, pr->ntasks, ctx->stream));
+    if (pr && pr->units)
+        QMM_HIP(ctx, launch_quant_route(f32_cols(src1), K, ncols, a, pr->r, pr->scratch, pr->units, pr->ntasks, ctx->stream));
+    else if (pr)
+        QMM_HIP(ctx, launch_quant_route(f32_cols(src1), K, ncols, a, pr->r, pr->scratch, pr->tasks, pr->ntasks, ctx->stream));
     else QMM_HIP(ctx, launch_quantize(f32_cols(src1), K, ncols, a, z, ctx->stream));
     *out = a;
     if (fixed) return QMM_OK;
@@ -1139,6 +1144,52 @@ static int64_t route_max_tasks(int64_t npairs, int64_t n_as) {
     return npairs / kMaxTaskCols + std::min(n_as + 1, npairs) + 1;
 }
 
+// The grouped GEMM's route: units of up to 64 pairs of one expert (the invalid ids' bucket
+// last), written into the route scratch by the quantization launch (pr).  The GEMV route
+// cached there for this graph is gone after this.
+static int64_t route_max_units(int64_t npairs, int64_t n_as) {
+    return npairs / kUnitCols + std::min(n_as + 1, npairs) + 1;
+}
+static int route_units(qmm_ctx * ctx, const qmm_tensor * ids, int64_t ne11, int64_t n_as, int64_t dnb1, int64_t dnb2,
+                       int64_t max_units, GemmUnit ** units, int32_t ** nunits, PendingRoute * pr) {
+    const int64_t n_used = ids->ne[0], T = ids->ne[1], npairs = n_used * T;
+    const size_t o_units = align_up((size_t)npairs * 4, 256);
+    const size_t o_cnt = align_up(o_units + (size_t)max_units * sizeof(GemmUnit), 256);
+    int rc = ensure(ctx, &ctx->route, &ctx->route_cap, o_cnt + 256);
+    if (rc) return rc;
+    ctx->rkey.valid = false;
+    uint8_t * rb = (uint8_t *)ctx->route;
+    *units = (GemmUnit *)(rb + o_units);
+    *nunits = (int32_t *)(rb + o_cnt);
+    RouteArgs r;
+    r.ids = (const int32_t *)((const uint8_t *)ids->buffer->ptr + ids->offs);
+    r.ids_nb0 = ids->nb[0];
+    r.ids_nb1 = ids->nb[1];
+    r.n_used = n_used;
+    r.T = T;
+    r.ne11 = ne11;
+    r.n_as = n_as;
+    r.dst_nb1 = dnb1;
+    r.dst_nb2 = dnb2;
+    r.bad_id = ctx->dflags;
+    *pr = PendingRoute{ r, (int32_t *)rb, nullptr, *nunits, *units };
+    return QMM_OK;
+}
+
+// MUL_MAT_ID on the grouped GEMM when the experts average this many pairs or more
+// (QMM_MOE_GEMM_MIN overrides; 0 switches it off)
+static int64_t moe_gemm_min_pairs() {
+    const char * e = getenv("QMM_MOE_GEMM_MIN");
+    return e ? atoll(e) : 32;
+}
+static bool use_moe_gemm(int type, const WView & w, int64_t npairs, int64_t n_as) {
+    const int64_t mn = moe_gemm_min_pairs();
+    G3Shape sh;
+    // (K >= 1024: with fewer super-blocks per wave the GEMV tasks win, measured on 2048 x 512)
+    return mn > 0 && npairs >= mn * n_as && w.G >= 4 && gemm3_id_supported(type) &&
+           gemm3_id_shape(w, route_max_units(npairs, n_as), &sh);
+}
+
 int qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1, const qmm_tensor * ids,
                    const qmm_tensor * dst) {
     if (!ctx) return QMM_ERR_INVALID;
@@ -1154,6 +1205,23 @@ int qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * sr
     if (try_fused_id(ctx, src0, src1, ids, dst, w, nullptr, -1, &rc)) {
         ctx->path = "gemv-id-fq";
         return rc;
+    }
+    float * dptr = (float *)((uint8_t *)dst->buffer->ptr + dst->offs);
+    if (use_moe_gemm(src0->type, w, npairs, n_as)) {
+        const int64_t max_units = route_max_units(npairs, n_as);
+        GemmUnit * units;
+        int32_t * nunits;
+        PendingRoute pr;
+        if ((rc = route_units(ctx, ids, src1->ne[1], n_as, (int64_t)(dst->nb[1] / 4), (int64_t)(dst->nb[2] / 4),
+                              max_units, &units, &nunits, &pr)))
+            return rc;
+        if ((rc = quantize_src1(ctx, src0->type, src1, false, &a, nullptr, &pr))) return rc;
+        ctx->path = "gemm-id-stream";
+        KTime kt;
+        const KTime * ktp;
+        if ((rc = ktime_pair(ctx, &kt, &ktp))) return rc;
+        QMM_HIP(ctx, launch_gemm3_id(src0->type, w, a, units, nunits, max_units, dptr, ctx->stream, ktp));
+        return ktime_done(ctx);
     }
     const int64_t max_tasks = route_max_tasks(npairs, n_as);
     const int nc = (int)std::min<int64_t>(kMaxTaskCols, npairs);

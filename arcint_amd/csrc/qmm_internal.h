@@ -160,14 +160,18 @@ __host__ __device__ static inline const uint8_t * tile_group(const WView & w, in
     return w.base + (size_t)(((mat * w.ntiles + tile) * w.G + g)) * (size_t)w.tg;
 }
 
-// A GEMV task: up to 8 columns against one weight matrix.
-constexpr int kMaxTaskCols = 8;
-struct GemvTask {
-    int32_t mat;                   // weight matrix (expert / slice) index; <0: skip
+// A routed task: up to TC columns against one weight matrix.  GEMV tasks carry up to 8; the
+// grouped MoE GEMM's units 64 (one 64-column wave job of the streaming Q4_K GEMM).
+template <int TC> struct TaskOf {
+    int32_t mat;                   // weight matrix (expert / slice) index; <0: zero rows
     int32_t ncols;
-    int32_t col[kMaxTaskCols];     // activation column ids
-    int64_t dst_off[kMaxTaskCols]; // float offset of dst row 0 for that column
+    int32_t col[TC];               // activation column ids
+    int64_t dst_off[TC];           // float offset of dst row 0 for that column
 };
+constexpr int kMaxTaskCols = 8;
+constexpr int kUnitCols = 64;
+using GemvTask = TaskOf<kMaxTaskCols>;
+using GemmUnit = TaskOf<kUnitCols>;
 
 // ---------------------------------------------------------------------------
 // Launchers (defined in the .hip files); all enqueue on `s`.  A non-null
@@ -340,6 +344,13 @@ struct G3Shape {
     int64_t workgroups;            // all batches
 };
 bool gemm3_shape(int type, const WView & w, int64_t N, int64_t nbatch, G3Shape * sh);
+// Grouped MoE GEMM (MUL_MAT_ID with many pairs per expert): the route's 64-column units
+// (*nunits of at most max_units) of one expert each, activations gathered from the route's q8_K
+// quantization a; unit pairs with mat < 0 get zero rows.  Q4_K only.
+bool gemm3_id_supported(int type);
+bool gemm3_id_shape(const WView & w, int64_t max_units, G3Shape * sh);
+hipError_t launch_gemm3_id(int type, const WView & w, const ActBuf & a, const GemmUnit * units, const int32_t * nunits,
+                           int64_t max_units, float * dst, hipStream_t s, const KTime * kt = nullptr);
 hipError_t launch_gemm3(int type, const WView & w, const TiledAct & a, int64_t nbatch, const GemmBatch & bt,
                         float * dst, hipStream_t s, const KTime * kt = nullptr);
 
@@ -401,9 +412,12 @@ hipError_t launch_glu(int op, const GluArgs & a, hipStream_t s);
 // scratch: pairs [T*n_used]; tasks out
 // tasks of mat = -1 carry pairs of invalid ids: the GEMV writes their dst rows as zeros
 hipError_t launch_route(const RouteArgs & r, int32_t * scratch, GemvTask * tasks, int32_t * ntasks, hipStream_t s);
+hipError_t launch_route(const RouteArgs & r, int32_t * scratch, GemmUnit * units, int32_t * nunits, hipStream_t s);
 // the route and the activation quantization (no dst zeroing) in one launch
 hipError_t launch_quant_route(const F32Cols & src, int64_t K, int64_t ncols, const ActBuf & a, const RouteArgs & r,
                               int32_t * scratch, GemvTask * tasks, int32_t * ntasks, hipStream_t s);
+hipError_t launch_quant_route(const F32Cols & src, int64_t K, int64_t ncols, const ActBuf & a, const RouteArgs & r,
+                              int32_t * scratch, GemmUnit * units, int32_t * nunits, hipStream_t s);
 
 }  // namespace qmm
 

@@ -581,6 +581,55 @@ def test_mul_mat_id_many_pairs(be, sc, orc, T):
     assert not got[T - 1, 3].any()
 
 
+@pytest.mark.parametrize("bcast", [True, False])
+def test_mul_mat_id_grouped_gemm(be, sc, orc, monkeypatch, bcast):
+    """MUL_MAT_ID on the grouped GEMM (experts averaging >= 32 pairs): 64-column units of one
+    expert, activations gathered from the route's quantization; ragged: 100 rows, 3 of 8
+    experts without pairs, pair counts not a multiple of 64, negative ids (zero rows)"""
+    qtype, E, n_used, M, K, T = qmm.Q4_K, 8, 3, 100, 1280, 300
+    say("mul_mat_id grouped gemm", bcast)
+    raw = synth.weights(qtype, E * M, K, seed=81)
+    g = np.random.default_rng(82)
+    ids = np.stack([g.choice([0, 2, 4, 5, 6], size=n_used, replace=False) for _ in range(T)]).astype(np.int32)
+    ids[7, 1] = -1
+    ids[11, 0] = -1
+    ne11 = 1 if bcast else n_used
+    x = synth.activations(T * ne11, K, seed=83).reshape(T, ne11, K)
+    w = sc.weights(qtype, raw, (K, M, E))
+    y = sc.empty_f32((M, n_used, T))
+    be.mul_mat_id(w, sc.f32(x), sc.i32(ids), y)
+    be.synchronize()
+    assert be.last_path() == "gemm-id-stream"
+    got = be.get_f32(y).reshape(T, n_used, M)
+    assert rel_err(got, orc.mul_mat_id(qtype, raw, M, K, E, x, ids)) <= TOL
+    assert not got[7, 1].any() and not got[11, 0].any()
+    # the same op on the GEMV tasks agrees
+    monkeypatch.setenv("QMM_MOE_GEMM_MIN", "0")
+    y2 = sc.empty_f32((M, n_used, T))
+    be.mul_mat_id(w, sc.f32(x), sc.i32(ids), y2)
+    be.synchronize()
+    assert be.last_path() != "gemm-id-stream"
+    assert rel_err(got, be.get_f32(y2).reshape(T, n_used, M)) <= TOL
+
+
+@pytest.mark.parametrize("T", [1024])
+def test_mul_mat_id_grouped_gemm_config3_shape(be, sc, orc, T):
+    """config 3's expert shape (Q4_K 512 x 2048 gate/up, ne11 = 1) with 16 experts, top-10:
+    640 pairs per expert on the grouped GEMM"""
+    qtype, E, n_used, M, K = qmm.Q4_K, 16, 10, 512, 2048
+    say("mul_mat_id grouped gemm config3 shape", T)
+    raw = synth.weights(qtype, E * M, K, seed=84)
+    ids = synth.moe_ids(T, E, n_used, seed=85)
+    x = synth.activations(T, K, seed=86).reshape(T, 1, K)
+    w = sc.weights(qtype, raw, (K, M, E))
+    y = sc.empty_f32((M, n_used, T))
+    be.mul_mat_id(w, sc.f32(x), sc.i32(ids), y)
+    be.synchronize()
+    assert be.last_path() == "gemm-id-stream"
+    got = be.get_f32(y).reshape(T, n_used, M)
+    assert rel_err(got, orc.mul_mat_id(qtype, raw, M, K, E, x, ids)) <= TOL
+
+
 def test_mul_mat_id_all_tokens_one_expert(be, sc, orc):
     # more than 8 pairs on one expert: several tasks per expert
     qtype, E, n_used, M, K, T = qmm.Q4_K, 4, 2, 64, 256, 40
