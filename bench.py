@@ -28,6 +28,9 @@ Also reported, on the same JSON line:
                 expert, the combine), rotated over two layers' expert stacks
                 (1.8 GB): GB/s of the expert weights each step touches, against
                 the layer's HBM roofline, and each op's own time
+  moe_grouped   MUL_MAT_ID with many tokens per expert (16 experts x 1024 tokens
+                top-10, 128 experts x 512 tokens top-8; Q4_K 512x2048): op and
+                kernel time, TOPS against the int8 peak
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
@@ -241,6 +244,50 @@ def glu_case(be, qmm, synth, args):
     return out
 
 
+def moe_grouped_case(be, qmm, synth, E, n_used, M, K, T, name, args):
+    """MUL_MAT_ID with many tokens per expert (Q4_K experts [K, M, E], src1 [K, 1, T], top-n_used
+    of softmaxed random logits): one step = one op over one of several copies of the stack
+    (>= 2 x the MALL).  TOPS = 2 x pairs x M x K over the main kernel's median; GB/s counts the
+    touched expert bytes, the f32 activations and dst over the op's own time."""
+    raw, ws = weight_copies(be, qmm, synth, qmm.Q4_K, M * E, K, seed=21)
+    ws = [qmm.Tensor(w.buf, qmm.Q4_K, (K, M, E)) for w in ws]
+    ids = synth.moe_ids(T, E, n_used, seed=22)
+    x = synth.activations(T, K, seed=23)
+    xt = be.new_tensor(qmm.F32, (K, 1, T))
+    be.set_tensor(xt, x.view(np.uint8).ravel())
+    it = be.new_tensor(qmm.I32, (n_used, T))
+    be.set_tensor(it, ids.view(np.uint8).ravel())
+    yt = be.new_tensor(qmm.F32, (M, n_used, T))
+    steps = max(10, args.steps // 4)
+    for i in range(args.warmup):
+        be.mul_mat_id(ws[i % len(ws)], xt, it, yt)
+    be.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        be.mul_mat_id(ws[i % len(ws)], xt, it, yt)
+    be.synchronize()
+    op_s = (time.perf_counter() - t0) / steps
+    path = be.last_path()
+    be.kernel_timing(True)
+    for i in range(steps):
+        be.mul_mat_id(ws[i % len(ws)], xt, it, yt)
+    be.synchronize()
+    kt = be.kernel_times()
+    be.kernel_timing(False)
+    k_ms = float(np.median(kt)) if kt.size else float("nan")
+    ops = 2.0 * T * n_used * M * K
+    touched = len(np.unique(ids)) * synth.row_bytes(qmm.Q4_K, K) * M
+    moved = touched + T * K * 4 + T * n_used * M * 4
+    for w in ws:
+        be.free_buffer(w.buf)
+    for t in (xt, it, yt):
+        be.free_buffer(t.buf)
+    return {"workload": name, "path": path, "experts": E, "tokens": T, "n_used": n_used, "M": M, "K": K,
+            "op_us": round(op_s * 1e6, 2), "kernel_us": round(k_ms * 1e3, 2),
+            "kernel_tops": round(ops / (k_ms * 1e-3) / 1e12, 1), "frac_int8_peak": round(ops / (k_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
+            "GBs": round(moved / op_s / 1e9, 1)}
+
+
 class MoeLayers:
     """Config 3's MoE layer, `nl` copies: per layer the gate and up expert stacks [2048, 512, 512]
     and the down stack [512, 2048, 512] in Q4_K (906 MB), the shared expert's gate / up
@@ -389,7 +436,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
-    ap.add_argument("--only", default="", help="profile one workload: q4k_gemv, q40_gemm, q4k_gemm, gemv, glu or moe")
+    ap.add_argument("--only", default="", help="profile one workload: q4k_gemv, q40_gemm, q4k_gemm, gemv, glu, moe or "
+                                                 "moe_grouped")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -492,6 +540,15 @@ def main():
             out["moe"] = moe
         else:
             out = {"metric": "MoE layer GB/s", "value": moe[0]["GBs"], "unit": "GB/s", "moe": moe}
+    if not args.no_secondary and args.only in ("", "moe", "moe_grouped"):
+        mg = [moe_grouped_case(be, qmm, synth, 16, 10, 512, 2048, 1024,
+                               "MUL_MAT_ID 16 Q4_K experts 512x2048, 1024 tokens top-10 (640 pairs per expert)", args),
+              moe_grouped_case(be, qmm, synth, 128, 8, 512, 2048, 512,
+                               "MUL_MAT_ID 128 Q4_K experts 512x2048, 512 tokens top-8 (32 pairs per expert)", args)]
+        if out:
+            out["moe_grouped"] = mg
+        else:
+            out = {"metric": "grouped MUL_MAT_ID TOPS", "value": mg[0]["kernel_tops"], "unit": "TOPS", "moe_grouped": mg}
     be.close()
     print(json.dumps(out), flush=True)
 
