@@ -816,6 +816,18 @@ static int64_t gemm_min_cols(int type) {
     }
 }
 
+// MUL_MAT on the GEMM: from gemm_min_cols, unless the streaming GEMM's launch would not give
+// every SIMD a wave (rows x column units x K slices < 1024): then the GEMV's tasks, which split
+// K over work-groups, win (config 3's shared expert, Q4_K 512 x 2048 at N = 256: 42.8 us on
+// the GEMM in 24 work-groups, 30.4 on the GEMV).  QMM_GEMM_MIN_COLS, when set, decides alone.
+static bool use_gemm_for(int type, const WView & w, int64_t N, int64_t nbatch) {
+    if (N < gemm_min_cols(type)) return false;
+    if (getenv("QMM_GEMM_MIN_COLS")) return true;
+    G3Shape sh;
+    if (!gemm3_shape(type, w, N, nbatch, &sh)) return true;      // (the shared-tile GEMM)
+    return sh.mbn * sh.nbn * nbatch * sh.U * sh.KS >= 1024;
+}
+
 // columns per GEMV task: up to 32 on the MFMA kernel (the rows of its A operand), 8 on v_dot4,
 // spread evenly over the fewest weight passes
 static int gemv_task_cols(int type, int64_t N) {
@@ -879,7 +891,8 @@ int qmm_describe_mul_mat(const qmm_tensor * src0, const qmm_tensor * src1, const
     if (!mul_mat_ok(src0, src1, dst, false, &w, reason, sizeof(reason))) return QMM_ERR_UNSUPPORTED;
     const int64_t N = src1->ne[1];
     G3Shape g3;
-    if (N >= gemm_min_cols(src0->type) && gemm3_shape(src0->type, w, N, src1->ne[2] * src1->ne[3], &g3)) {
+    const bool gemm = use_gemm_for(src0->type, w, N, src1->ne[2] * src1->ne[3]);
+    if (gemm && gemm3_shape(src0->type, w, N, src1->ne[2] * src1->ne[3], &g3)) {
         snprintf(out->path, sizeof(out->path), "gemm-stream");
         out->tasks = src1->ne[2] * src1->ne[3];
         out->cols_per_task = 32 * g3.C;
@@ -892,7 +905,7 @@ int qmm_describe_mul_mat(const qmm_tensor * src0, const qmm_tensor * src1, const
         out->groups_per_wave = (int32_t)((int64_t)g3.sps * g3.SB / 8);
         return QMM_OK;
     }
-    if (N >= gemm_min_cols(src0->type)) {
+    if (gemm) {
         snprintf(out->path, sizeof(out->path), "gemm-mfma");
         out->tasks = src1->ne[2] * src1->ne[3];
         out->cols_per_task = (int32_t)std::min<int64_t>(N, INT32_MAX);
@@ -990,7 +1003,7 @@ static bool try_fused_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tenso
 static int mul_mat_launch(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1, const qmm_tensor * dst,
                           const WView & w, const FixedAct * fixed) {
     const int64_t N = src1->ne[1];
-    const bool use_gemm = N >= gemm_min_cols(src0->type);
+    const bool use_gemm = use_gemm_for(src0->type, w, N, src1->ne[2] * src1->ne[3]);
     ActBuf a{};
     int rc;
     float * d = (float *)((uint8_t *)dst->buffer->ptr + dst->offs);
@@ -1445,7 +1458,7 @@ int qmm_mul_mat_glu(qmm_ctx * ctx, const qmm_tensor * gate, const qmm_tensor * u
     const int type = gate->type;
     const int nc = gemv_task_cols(type, N);
     GemvPlan plan;
-    const bool fused = up->type == type && nb == 1 && N < gemm_min_cols(type) &&
+    const bool fused = up->type == type && nb == 1 && !use_gemm_for(type, wg, N, nb) &&
                        gemv_plan(type, wg, nc, (N + nc - 1) / nc * 2, true, nc >= gemv_mma_min_cols(), &plan);
     if (fused) {
         GemvDense dn;
@@ -1562,7 +1575,7 @@ int qmm_internal_gemv_extent(int32_t type, const int64_t ne0[4], int64_t N, int6
         plan.cm = 8;
     };
     if (id_n_used == 0) {
-        if (N >= gemm_min_cols(type)) return QMM_ERR_UNSUPPORTED;
+        if (use_gemm_for(type, w, N, nbatch)) return QMM_ERR_UNSUPPORTED;
         const int nc = gemv_task_cols(type, N);
         const int64_t ntasks = (N + nc - 1) / nc * nbatch;
         if (fused_dense_plan(type, w, N, nbatch, &fp)) as_plan(fp);

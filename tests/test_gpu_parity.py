@@ -762,6 +762,7 @@ def test_full_size_gemm(be, sc, orc, monkeypatch, qtype, M, K, N):
 @pytest.mark.parametrize("KS", [1, 2, 3])
 def test_gemm_stream_shapes(be, sc, orc, monkeypatch, qtype, KS):
     monkeypatch.setenv("QMM_GEMM3_KS", str(KS))
+    monkeypatch.setenv("QMM_GEMM_MIN_COLS", "16")                 # (small shapes: the GEMM regardless)
     for (M, K, N, seed) in [(200, 800, 33, 301), (64, 2048, 100, 302), (130, 512, 64, 303), (448, 1280, 161, 304),
                             (700, 4352, 40, 307)]:
         say("gemm-stream", qtype, KS, M, K, N)
@@ -956,15 +957,18 @@ def test_mul_mat_glu_ops(be, sc, orc, op):
     assert rel_err(got, ref) <= TOL
 
 
-def test_mul_mat_glu_split_paths(be, sc, orc):
-    """the unfused forms: mixed weight types, the GEMM (N >= the crossover), broadcast batches"""
+def test_mul_mat_glu_split_paths(be, sc, orc, monkeypatch):
+    """the unfused forms: mixed weight types, the GEMM (forced on this small shape), broadcast
+    batches"""
     say("glu-split mixed")
     got, ref = glu_case(be, sc, orc, qmm.Q4_K, qmm.Q6_K, 200, 1024, 3, qmm.GLU_SWIGLU, seed=121)
     assert be.last_path().startswith("glu-") and not be.last_path().startswith("glu-fused")
     assert rel_err(got, ref) <= TOL
     say("glu-split gemm")
-    got, ref = glu_case(be, sc, orc, qmm.Q4_0, qmm.Q4_0, 200, 1024, 40, qmm.GLU_GEGLU, seed=122)
-    assert be.last_path() == "glu-gemm-stream"
+    with monkeypatch.context() as mp:
+        mp.setenv("QMM_GEMM_MIN_COLS", "33")
+        got, ref = glu_case(be, sc, orc, qmm.Q4_0, qmm.Q4_0, 200, 1024, 40, qmm.GLU_GEGLU, seed=122)
+        assert be.last_path() == "glu-gemm-stream"
     assert rel_err(got, ref) <= TOL
     say("glu-split batches")
     got, ref = glu_case(be, sc, orc, qmm.Q4_K, qmm.Q4_K, 130, 512, 2, qmm.GLU_SWIGLU, seed=123, batches=(3, 2))

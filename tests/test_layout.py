@@ -289,7 +289,8 @@ GEMM3_SHAPES = [(qmm.Q4_0, 4096, 4096, 512), (qmm.Q4_0, 11008, 4096, 512), (qmm.
 
 
 @pytest.mark.parametrize("qtype,K,M,N", GEMM3_SHAPES)
-def test_gemm_stream_plan(qtype, K, M, N):
+def test_gemm_stream_plan(qtype, K, M, N, monkeypatch):
+    monkeypatch.setenv("QMM_GEMM_MIN_COLS", "16")                 # (small shapes: the GEMM regardless)
     fake = qmm.Buffer(ptr=0x1000, size=1 << 44)
     info = qmm.describe_mul_mat(qmm.Tensor(fake, qtype, (K, M)), qmm.Tensor(fake, qmm.F32, (K, N)),
                                 qmm.Tensor(fake, qmm.F32, (M, N)))
@@ -313,6 +314,18 @@ def test_gemm_stream_plan(qtype, K, M, N):
 # 4-wave: three per CU, a partial last round counted as its fraction) times super-blocks per
 # slice, ties to the earlier candidate; LDS: two 18 KB stages per slice (+ a 1 KB slot when 18
 # units do not divide over U), or the slices' sums if larger
+# past the column crossover the GEMM is taken when its launch gives every SIMD a wave (row units x
+# column units x K slices >= 1024), else the GEMV's split-K tasks
+@pytest.mark.parametrize("qtype,K,M,N,path", [(qmm.Q4_K, 2048, 512, 256, "gemv-mfma"), (qmm.Q4_K, 5120, 17408, 512, "gemm-stream"),
+                                              (qmm.Q4_K, 5120, 1024, 512, "gemm-stream"), (qmm.Q4_0, 4096, 4096, 100, "gemv-mfma"),
+                                              (qmm.Q4_0, 4096, 4096, 512, "gemm-stream"), (qmm.Q6_K, 17408, 5120, 512, "gemm-mfma")])
+def test_gemm_fill_rule(qtype, K, M, N, path):
+    fake = qmm.Buffer(ptr=0x1000, size=1 << 44)
+    info = qmm.describe_mul_mat(qmm.Tensor(fake, qtype, (K, M)), qmm.Tensor(fake, qmm.F32, (K, N)),
+                                qmm.Tensor(fake, qmm.F32, (M, N)))
+    assert info["path"] == path
+
+
 KQ_CANDS = [(12, 1, 1), (6, 2, 1), (4, 3, 1), (3, 4, 1), (4, 1, 3), (2, 2, 3)]
 GEMM3_KQ_SHAPES = [(5120, 17408, 512), (5120, 12288, 512), (5120, 1024, 512), (6144, 5120, 512),
                    (4096, 4096, 128), (256, 130, 33)]
