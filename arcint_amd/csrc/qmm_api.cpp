@@ -87,18 +87,37 @@ struct qmm_ctx {
     hipEvent_t ktime_stop = nullptr;   // marker mode: the stop event of the launch just made
     std::vector<hipEvent_t> kev;   // pairs
     size_t kev_used = 0;
+    // HIP-graph capture of the stream (qmm_capture_begin/end): ops allocate nothing and record
+    // no timing events meanwhile; a failure while capturing makes qmm_capture_end fail
+    bool capturing = false;
+    bool capture_failed = false;
+    int capture_code = 0;          // the first failure while capturing, and its reason
+    std::string capture_err;
+};
+
+// an instantiated capture (qmm_capture_end)
+struct qmm_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    int device = 0;
 };
 
 namespace {
 
 int fail(qmm_ctx * ctx, int code, const char * fmt, ...) {
     if (ctx) {
+        const bool first_in_capture = ctx->capturing && !ctx->capture_failed;
         char buf[512];
         va_list ap;
         va_start(ap, fmt);
         vsnprintf(buf, sizeof(buf), fmt, ap);
         va_end(ap);
         ctx->err = buf;
+        if (first_in_capture) {
+            ctx->capture_failed = true;
+            ctx->capture_code = code;
+            ctx->capture_err = buf;
+        }
     }
     return code;
 }
@@ -229,6 +248,9 @@ size_t act_bytes(int vdt, int64_t ldk, int64_t ncols, bool dT, int64_t ldT, size
 
 int ensure(qmm_ctx * ctx, void ** p, size_t * cap, size_t need) {
     if (need <= *cap) return QMM_OK;
+    if (ctx->capturing)
+        return fail(ctx, QMM_ERR_NOMEM, "capture: the op needs %zu bytes of scratch and the context has %zu; run it "
+                                        "once outside a capture first", need, *cap);
     if (*p) {
         QMM_HIP(ctx, hipStreamSynchronize(ctx->stream));
         QMM_HIP(ctx, hipFree(*p));
@@ -406,7 +428,7 @@ bool check_f32(const qmm_tensor * t) {
 // event pair stamped by the main kernel of an op when timing is on (null otherwise)
 int ktime_pair(qmm_ctx * ctx, KTime * kt, const KTime ** out) {
     *out = nullptr;
-    if (!ctx->ktime) return QMM_OK;
+    if (!ctx->ktime || ctx->capturing) return QMM_OK;
     if (ctx->kev_used + 2 > ctx->kev.size()) {
         for (int i = 0; i < 64; ++i) {
             hipEvent_t e;
@@ -527,6 +549,12 @@ int qmm_ctx_create(int device, qmm_ctx ** out) {
 void qmm_ctx_free(qmm_ctx * ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
+    if (ctx->capturing) {                            // a capture left open: end it, drop its graph
+        hipGraph_t g = nullptr;
+        (void)hipStreamEndCapture(ctx->stream, &g);
+        if (g) (void)hipGraphDestroy(g);
+        ctx->capturing = false;
+    }
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->act) (void)hipFree(ctx->act);
     if (ctx->route) (void)hipFree(ctx->route);
@@ -561,6 +589,10 @@ int qmm_buffer_alloc(qmm_ctx * ctx, size_t size, qmm_buffer ** out) {
 
 void qmm_buffer_free(qmm_ctx * ctx, qmm_buffer * buf) {
     if (!buf) return;
+    if (ctx && ctx->capturing) {                      // (it synchronizes the stream: refused, buffer kept)
+        (void)fail(ctx, QMM_ERR_INVALID, "buffer_free: not while capturing (it synchronizes the stream)");
+        return;
+    }
     if (ctx) {
         (void)hipStreamSynchronize(ctx->stream);
         if (ctx->key.buf == buf) ctx->key.valid = false;
@@ -722,10 +754,12 @@ int qmm_tensor_unpack(int32_t type, const int64_t ne[4], const void * image, voi
 }
 
 int qmm_tensor_set(qmm_ctx * ctx, const qmm_tensor * t, const void * data, size_t offset, size_t size) {
+    if (ctx && ctx->capturing) return fail(ctx, QMM_ERR_INVALID, "tensor_set: not while capturing (it synchronizes the stream)");
     return tensor_io(ctx, t, const_cast<void *>(data), offset, size, true);
 }
 
 int qmm_tensor_get(qmm_ctx * ctx, const qmm_tensor * t, void * data, size_t offset, size_t size) {
+    if (ctx && ctx->capturing) return fail(ctx, QMM_ERR_INVALID, "tensor_get: not while capturing (it synchronizes the stream)");
     return tensor_io(ctx, t, data, offset, size, false);
 }
 
@@ -1650,6 +1684,7 @@ int qmm_dequantize(qmm_ctx * ctx, const qmm_tensor * src, const qmm_tensor * dst
 }
 
 int qmm_quantize_act(qmm_ctx * ctx, int32_t act_type, const qmm_tensor * src, void * out, size_t out_size) {
+    if (ctx && ctx->capturing) return fail(ctx, QMM_ERR_INVALID, "quantize_act: not while capturing (it synchronizes the stream)");
     if (!ctx || !check_f32(src) || !out) return fail(ctx, QMM_ERR_INVALID, "quantize_act: bad argument");
     if (act_type != QMM_TYPE_Q8_0 && act_type != QMM_TYPE_Q8_K) return fail(ctx, QMM_ERR_INVALID, "quantize_act: type");
     const int bs = act_block(act_type), bb = act_type == QMM_TYPE_Q8_0 ? 34 : 292;
@@ -1675,6 +1710,7 @@ int qmm_quantize_act(qmm_ctx * ctx, int32_t act_type, const qmm_tensor * src, vo
 // Waits for the stream, then reports what the kernels flagged since the last call: MUL_MAT_ID
 // ids at or past n_as (their rows were written as zeros; ggml-cpu asserts on them, P02:105).
 int qmm_synchronize(qmm_ctx * ctx) {
+    if (ctx && ctx->capturing) return fail(ctx, QMM_ERR_INVALID, "synchronize: not while capturing (it synchronizes the stream)");
     if (!ctx) return QMM_ERR_INVALID;
     QMM_HIP(ctx, hipMemcpyAsync(ctx->hflags, ctx->dflags, sizeof(int32_t), hipMemcpyDeviceToHost, ctx->stream));
     QMM_HIP(ctx, hipStreamSynchronize(ctx->stream));
@@ -1707,6 +1743,7 @@ int64_t qmm_downgrades(qmm_ctx * ctx, char * buf, size_t buf_len) {
 }
 
 int qmm_kernel_timing(qmm_ctx * ctx, int enable) {
+    if (ctx && ctx->capturing) return fail(ctx, QMM_ERR_INVALID, "kernel_timing: not while capturing (it synchronizes the stream)");
     if (!ctx || enable < 0 || enable > 2) return QMM_ERR_INVALID;
     QMM_HIP(ctx, hipStreamSynchronize(ctx->stream));
     ctx->ktime = enable != 0;
@@ -1729,6 +1766,7 @@ int64_t qmm_kernel_times(qmm_ctx * ctx, double * ms, int64_t cap) {
 }
 
 int qmm_kernel_time(qmm_ctx * ctx, double * total_ms, int64_t * launches) {
+    if (ctx && ctx->capturing) return fail(ctx, QMM_ERR_INVALID, "kernel_time: not while capturing (it synchronizes the stream)");
     if (!ctx || !total_ms || !launches) return QMM_ERR_INVALID;
     QMM_HIP(ctx, hipStreamSynchronize(ctx->stream));
     double t = 0.0;
@@ -1742,6 +1780,64 @@ int qmm_kernel_time(qmm_ctx * ctx, double * total_ms, int64_t * launches) {
     return QMM_OK;
 }
 
+int qmm_capture_begin(qmm_ctx * ctx) {
+    if (!ctx) return QMM_ERR_INVALID;
+    if (ctx->capturing) return fail(ctx, QMM_ERR_INVALID, "capture_begin: already capturing");
+    QMM_HIP(ctx, hipSetDevice(ctx->device));
+    ctx->ktime_stop = nullptr;
+    QMM_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    ctx->capturing = true;
+    ctx->capture_failed = false;
+    return QMM_OK;
+}
+
+int qmm_capture_end(qmm_ctx * ctx, qmm_graph ** out) {
+    if (!ctx || !out) return QMM_ERR_INVALID;
+    *out = nullptr;
+    if (!ctx->capturing) return fail(ctx, QMM_ERR_INVALID, "capture_end: not capturing");
+    const bool failed = ctx->capture_failed;
+    ctx->capturing = false;
+    ctx->capture_failed = false;
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(ctx->stream, &g);      // ends it whatever happened meanwhile
+    if (e != hipSuccess || failed) {
+        if (g) (void)hipGraphDestroy(g);
+        if (failed) {                                              // the first failure's status and reason
+            const std::string why = ctx->capture_err;
+            return fail(ctx, ctx->capture_code, "capture_end: an op failed while capturing: %s", why.c_str());
+        }
+        return fail(ctx, QMM_ERR_DEVICE, "hipStreamEndCapture: %s", hipGetErrorString(e));
+    }
+    qmm_graph * r = new qmm_graph();
+    r->graph = g;
+    r->device = ctx->device;
+    const hipError_t ei = hipGraphInstantiate(&r->exec, g, nullptr, nullptr, 0);
+    if (ei != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        delete r;
+        return fail(ctx, QMM_ERR_DEVICE, "hipGraphInstantiate: %s", hipGetErrorString(ei));
+    }
+    *out = r;
+    return QMM_OK;
+}
+
+int qmm_graph_launch(qmm_ctx * ctx, const qmm_graph * graph) {
+    if (!ctx || !graph) return QMM_ERR_INVALID;
+    if (ctx->capturing) return fail(ctx, QMM_ERR_INVALID, "graph_launch: not while capturing");
+    if (graph->device != ctx->device) return fail(ctx, QMM_ERR_INVALID, "graph_launch: the graph is of another device");
+    QMM_HIP(ctx, hipSetDevice(ctx->device));
+    QMM_HIP(ctx, hipGraphLaunch(graph->exec, ctx->stream));
+    return QMM_OK;
+}
+
+void qmm_graph_free(qmm_graph * graph) {
+    if (!graph) return;
+    (void)hipSetDevice(graph->device);
+    if (graph->exec) (void)hipGraphExecDestroy(graph->exec);
+    if (graph->graph) (void)hipGraphDestroy(graph->graph);
+    delete graph;
+}
+
 int qmm_timer_begin(qmm_ctx * ctx) {
     if (!ctx) return QMM_ERR_INVALID;
     QMM_HIP(ctx, hipEventRecord(ctx->ev0, ctx->stream));
@@ -1749,7 +1845,7 @@ int qmm_timer_begin(qmm_ctx * ctx) {
 }
 
 float qmm_timer_end(qmm_ctx * ctx) {
-    if (!ctx) return -1.0f;
+    if (!ctx || ctx->capturing) return -1.0f;
     if (hipEventRecord(ctx->ev1, ctx->stream) != hipSuccess || hipEventSynchronize(ctx->ev1) != hipSuccess) return -1.0f;
     float ms = -1.0f;
     if (hipEventElapsedTime(&ms, ctx->ev0, ctx->ev1) != hipSuccess) return -1.0f;

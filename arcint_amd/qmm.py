@@ -37,6 +37,7 @@ EXPORTS = (
     "qmm_last_path", "qmm_timer_begin", "qmm_timer_end", "qmm_buffer_copy", "qmm_kernel_timing",
     "qmm_kernel_time", "qmm_tensor_pack", "qmm_tensor_unpack", "qmm_describe_mul_mat", "qmm_moe_topk",
     "qmm_moe_combine", "qmm_mul_mat_glu", "qmm_mul_mat_id_glu", "qmm_mul_mat_noalloc", "qmm_kernel_times",
+    "qmm_capture_begin", "qmm_capture_end", "qmm_graph_launch", "qmm_graph_free",
 )
 NOALLOC_SCRATCH_BYTES = 16 << 20     # QMM_NOALLOC_SCRATCH_BYTES
 
@@ -121,6 +122,10 @@ def load() -> C.CDLL:
         L.qmm_tensor_pack.argtypes = [i32, C.POINTER(i64), vp, vp, sz]
         L.qmm_describe_mul_mat.argtypes = [T, T, T, C.POINTER(LaunchInfo)]
         L.qmm_tensor_unpack.argtypes = [i32, C.POINTER(i64), vp, vp, sz]
+        L.qmm_capture_begin.argtypes = [vp]
+        L.qmm_capture_end.argtypes = [vp, C.POINTER(vp)]
+        L.qmm_graph_launch.argtypes = [vp, vp]
+        L.qmm_graph_free.argtypes = [vp]
         _lib = L
     return _lib
 
@@ -219,6 +224,19 @@ class Tensor:
         """ggml_nbytes: first to past the last element, with the tensor's strides"""
         bl, _ = type_block(self.type)
         return self.ne[0] // bl * self.nb[0] + sum((n - 1) * s for n, s in zip(self.ne[1:], self.nb[1:]))
+
+
+class Graph:
+    """An instantiated capture (qmm_capture_end); free() it before its Backend closes."""
+
+    def __init__(self, L, h):
+        self.L = L
+        self.h = h
+
+    def free(self):
+        if self.h:
+            self.L.qmm_graph_free(self.h)
+            self.h = None
 
 
 class Backend:
@@ -331,6 +349,19 @@ class Backend:
         for i, (op, s0, s1, ids, d) in enumerate(nodes):
             arr[i] = CNode(op, C.pointer(s0.c), C.pointer(s1.c), C.pointer(ids.c) if ids else None, C.pointer(d.c))
         self._check(self.L.qmm_graph_compute(self.h, arr, len(nodes)), "graph_compute")
+
+    def capture_begin(self):
+        """start recording the ops of this context's stream into a HIP graph (qmm_capture_begin)"""
+        self._check(self.L.qmm_capture_begin(self.h), "capture_begin")
+
+    def capture_end(self) -> "Graph":
+        """end the recording; the instantiated graph (qmm_capture_end: raises if an op failed)"""
+        g = C.c_void_p()
+        self._check(self.L.qmm_capture_end(self.h, C.byref(g)), "capture_end")
+        return Graph(self.L, g)
+
+    def graph_launch(self, g: "Graph"):
+        self._check(self.L.qmm_graph_launch(self.h, g.h), "graph_launch")
 
     def dequantize(self, src: Tensor, dst: Tensor):
         self._check(self.L.qmm_dequantize(self.h, C.byref(src.c), C.byref(dst.c)), "dequantize")

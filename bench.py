@@ -101,6 +101,33 @@ def time_op(be, ws, xt, yt, steps, warmup):
     return wall, dev_ms, k_disp, k_mark
 
 
+def graph_replay_us(be, fns, steps, warmup):
+    """The same ops replayed from one HIP graph (qmm_capture_begin/end, qmm_graph_launch): the
+    callables in fns run once eagerly (which sizes the scratch), then are captured in order into
+    one graph, which is replayed (steps / len(fns) launches, at least one) between stream
+    synchronizes; microseconds per callable.  The kernels and buffers are the eager ones; only
+    the launches differ.  (One graph per op loses on this ROCm: a hipGraphLaunch costs ~18 us of
+    host time; a graph of many ops amortizes it.)"""
+    for fn in fns:
+        fn()
+    be.synchronize()
+    be.capture_begin()
+    for fn in fns:
+        fn()
+    g = be.capture_end()
+    try:
+        for _ in range(max(1, warmup // len(fns))):
+            be.graph_launch(g)
+        be.synchronize()
+        reps = max(1, steps // len(fns))
+        be.timer_begin()
+        for _ in range(reps):
+            be.graph_launch(g)
+        return be.timer_end() * 1e3 / (reps * len(fns))
+    finally:
+        g.free()
+
+
 def kernel_ms(k_disp, k_mark, op_ms):
     """The kernel time a roofline uses: the dispatch stamps, unless they exceed the op's own
     time per step (then the stream markers, which bound it from above)"""
@@ -416,13 +443,18 @@ def moe_case(be, qmm, synth, layers, T, args):
         times[name] = be_.timer_end() * 1e3 / steps
     bytes_step = float(np.mean([touched[i % nlog] for i in range(steps)]))
     us = dev_ms * 1e3 / steps
+    # the layer from one HIP graph holding the eager rotation's first nlog steps (layer copies and
+    # logits sets in turn), so the replays touch the same experts and stacks as the eager steps
+    g_us = graph_replay_us(be_, [lambda i=i: layer(i) for i in range(nlog)], steps, 16)
     res = {"workload": f"config 3 MoE layer, T={T}: router + gate/up/SwiGLU (512 Q4_K experts, top-10) + down + "
                        f"shared expert + combine, {nl} layers rotated",
            "T": T, "us_per_layer": round(us, 3), "wall_us_per_layer": round(wall * 1e6 / steps, 3),
            "weight_bytes_touched": int(bytes_step), "GBs": round(bytes_step / (us * 1e-6) / 1e9, 1),
            "frac_hbm": round(bytes_step / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
            "roofline_us": round(bytes_step / (HBM_PEAK_GBS * 1e9) * 1e6, 3),
-           "op_us": {n: round(v, 3) for n, v in times.items()}, "paths": paths}
+           "op_us": {n: round(v, 3) for n, v in times.items()}, "paths": paths,
+           "us_per_layer_graph": round(g_us, 3),
+           "GBs_graph": round(bytes_step / (g_us * 1e-6) / 1e9, 1)}
     for t in tmp[0] + tmp[1]:
         be_.free_buffer(t.buf)
     return res
@@ -482,6 +514,13 @@ def main():
                          "kernel_us_markers": round(km * 1e3, 3), "kernel_us_stat": f"median of {args.steps} launches",
                          "algorithmic_bytes": int(algo)},
         })
+        # the same ops from one HIP graph: four passes over the weight copies (the value above is
+        # the eager op)
+        g_us = graph_replay_us(be, [lambda w=w: be.mul_mat(w, xt, yt) for w in ws * 4], args.steps, args.warmup)
+        out["graph"] = {"us_per_op": round(g_us, 3), "GBs": round(algo / (g_us * 1e-6) / 1e9, 1),
+                        "frac_hbm": round(algo / (g_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                        "note": f"{4 * len(ws)} MUL_MATs (q8_K pre-pass + GEMV, the weight copies in turn) captured "
+                                "in one HIP graph and replayed (qmm_graph_launch); value is the eager op"}
         if not args.no_cpu:
             import oracle
             out["cpu_baseline"] = cpu_baseline(oracle, qmm.Q4_K, raw, M, K, x, args.cpu_seconds)

@@ -32,6 +32,10 @@
  *   qmm_graph_compute            ggml_backend_opencl_graph_compute over a node
  *                                list, graph_gen++ per call (P01:609-612);
  *                                activation dedup keyed per graph (P01:683-717)
+ *   qmm_capture_begin/end,       no counterpart in the reference (OpenCL has no
+ *   qmm_graph_launch/free        graph replay): HIP-graph capture and replay of
+ *                                the ops on the context's stream, for decode
+ *                                loops bound by launch latency
  *   qmm_dequantize               dequantize_row_* of ggml (bit-exact gate;
  *                                tools/mtp_fit.py:338-409 restates them;
  *                                Q5_K / IQ4_NL decode as P01:3736-3750 and
@@ -227,6 +231,26 @@ int    qmm_mul_mat_noalloc(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_ten
  * activation quantization serves every node of the graph that reads the same
  * src1 with the same vec_dot type. */
 int    qmm_graph_compute(qmm_ctx * ctx, const qmm_node * nodes, int n_nodes);
+
+/* HIP-graph capture and replay: no reference counterpart (the reference's OpenCL backend
+ * launches every op on its queue); for callers whose decode steps are bound by launch latency,
+ * the role CUDA graphs play in ggml-cuda's decode path.  qmm_capture_begin starts capturing
+ * the context's stream; every op up to qmm_capture_end is recorded, not run.  While capturing
+ * an op allocates nothing: it fails with QMM_ERR_NOMEM when the context's scratch is too small
+ * for it (run the same ops once outside a capture first), records no kernel-timing events, and
+ * counts its downgrades once.  The ops that synchronize (tensor set/get, qmm_synchronize,
+ * qmm_quantize_act, buffer free) must not be called while capturing.  qmm_capture_end ends the
+ * capture and, if every captured op succeeded, returns the instantiated graph; the stream is
+ * usable again either way.  qmm_graph_launch replays it on the context's stream: the same
+ * kernels on the same buffers (the data in them may change between launches).  The graph uses
+ * the context's scratch: replays are ordered with the context's other work by its stream, and
+ * an op run outside the graph may leave the scratch holding other activations, which the next
+ * replay overwrites before it reads them.  Free the graph before its context. */
+typedef struct qmm_graph qmm_graph;
+int    qmm_capture_begin(qmm_ctx * ctx);
+int    qmm_capture_end(qmm_ctx * ctx, qmm_graph ** out);
+int    qmm_graph_launch(qmm_ctx * ctx, const qmm_graph * graph);
+void   qmm_graph_free(qmm_graph * graph);
 
 /* dst (f32, contiguous, ne = src ne) = dequantize_row_<type>(src) */
 int    qmm_dequantize(qmm_ctx * ctx, const qmm_tensor * src, const qmm_tensor * dst);
