@@ -65,6 +65,8 @@ struct GemvParams {
     int spw;                     // groups per wave
     int nct;                     // dense mode: columns per task
     int tw;                      // MFMA kernel: tiles per work-group (W / tw waves split K)
+    int task0;                   // v_dot4 kernel: the grid is (KS, tiles, tasks from task0), blockIdx
+                                 // is the position (launches of at most 65535 tasks each)
 };
 
 // tile-group 0 of (matrix, tile) of the first image, or (sec) of the second
@@ -485,9 +487,9 @@ __global__ __launch_bounds__(512) void k_gemv(GemvParams p) {
     // work-group -> (task, tile, K slice); these counts fit 32 bits
     static_assert(T::kReadEnd <= tile_group_bytes(TYPE) && tile_group_bytes(TYPE) <= (int)kSinkBytes,
                   "a stage reads inside one tile-group, which fits in the sink");
-    const uint32_t ntl = (uint32_t)p.w.ntiles;
-    const WgPos wp = wg_pos(blockIdx.x, (uint32_t)p.KS, ntl);
-    const uint32_t ks = wp.ks, tile = wp.unit, task = wp.task;
+    // the grid's dimensions are the position (work-group ks + KS (tile + ntl task) of wg_pos's
+    // numbering): no divisions and no branch ahead of the first weight load
+    const uint32_t ks = blockIdx.x, tile = blockIdx.y, task = blockIdx.z + (uint32_t)p.task0;
     int mat, nc;
     bool sec = false;                  // the second image (gate/up in one launch)
     // per column: activation column id and float offset of dst row 0, uniform
@@ -517,8 +519,11 @@ __global__ __launch_bounds__(512) void k_gemv(GemvParams p) {
             doffv[j] = (j < nc ? t.dst_off[j] : 0) + dadd;
         }
     } else {
-        const DenseTask dt = dense_task(task, (uint32_t)p.tpb, (uint32_t)p.ne12, (uint32_t)p.r2, (uint32_t)p.r3,
-                                        (uint32_t)p.ne02);
+        // (task 0 is batch 0, column tile 0 and matrix 0 whatever the divisors: the one task of a
+        // single-batch decode product takes no divisions)
+        const DenseTask dt = task == 0 ? DenseTask{ 0, 0, 0, 0, 0 }
+                                       : dense_task(task, (uint32_t)p.tpb, (uint32_t)p.ne12, (uint32_t)p.r2,
+                                                    (uint32_t)p.r3, (uint32_t)p.ne02);
         mat = dt.mat;
         if (p.base2 && mat == 1) {                                // gate/up in one launch
             mat = 0;
@@ -1133,21 +1138,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 }
 
 template <int TYPE>
-hipError_t launch_t(const GemvParams & p, int nc, int64_t nwg, hipStream_t s, const KTime * kt) {
-    const int threads = 64 * p.W;
-    const size_t lds = p.W > 1 ? (size_t)p.W * nc * 64 * sizeof(float) * (p.glu >= 0 ? 2 : 1) : 0;
-    switch (nc) {
+hipError_t launch_t(const GemvParams & p0, int nc, int64_t nwg, hipStream_t s, const KTime * kt) {
+    const int threads = 64 * p0.W;
+    const size_t lds = p0.W > 1 ? (size_t)p0.W * nc * 64 * sizeof(float) * (p0.glu >= 0 ? 2 : 1) : 0;
+    GemvParams p = p0;
+    const int64_t per_task = (int64_t)p.KS * p.w.ntiles, ntasks = nwg / per_task;
+    if (ntasks * per_task != nwg || p.w.ntiles > 65535) return hipErrorInvalidValue;
+    // grid (KS, tiles, tasks): one launch per 65535 tasks (kernel timing stamps the first)
+    for (int64_t t0 = 0; t0 < ntasks; t0 += 65535) {
+        p.task0 = (int)t0;
+        const dim3 g((unsigned)p.KS, (unsigned)p.w.ntiles, (unsigned)std::min<int64_t>(65535, ntasks - t0));
+        const KTime * k = t0 == 0 ? kt : nullptr;
+        switch (nc) {
 #define QMM_NC(N)                                                                                  \
     case N:                                                                                        \
-        if (kt) hipExtLaunchKernelGGL(k_gemv<TYPE, N>, dim3((unsigned)nwg), dim3(threads), (uint32_t)lds, s, \
-                                      kt->start, kt->stop, 0, p);                                  \
-        else k_gemv<TYPE, N><<<dim3((unsigned)nwg), threads, lds, s>>>(p);                         \
+        if (k) hipExtLaunchKernelGGL(k_gemv<TYPE, N>, g, dim3(threads), (uint32_t)lds, s, k->start, k->stop, 0, p); \
+        else k_gemv<TYPE, N><<<g, threads, lds, s>>>(p);                                           \
         break;
-        QMM_NC(1) QMM_NC(2) QMM_NC(3) QMM_NC(4) QMM_NC(5) QMM_NC(6) QMM_NC(7) QMM_NC(8)
+            QMM_NC(1) QMM_NC(2) QMM_NC(3) QMM_NC(4) QMM_NC(5) QMM_NC(6) QMM_NC(7) QMM_NC(8)
 #undef QMM_NC
-        default: return hipErrorInvalidValue;
+            default: return hipErrorInvalidValue;
+        }
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
     }
-    return hipGetLastError();
+    return hipSuccess;
 }
 
 int env_int(const char * name, int dflt) {
