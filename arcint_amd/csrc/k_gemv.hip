@@ -65,7 +65,7 @@ struct GemvParams {
     int spw;                     // groups per wave
     int nct;                     // dense mode: columns per task
     int tw;                      // MFMA kernel: tiles per work-group (W / tw waves split K)
-    int task0;                   // v_dot4 kernel: the grid is (KS, tiles, tasks from task0), blockIdx
+    int task0;                   // the grid is (KS, tiles or tile blocks, tasks from task0), blockIdx
                                  // is the position (launches of at most 65535 tasks each)
 };
 
@@ -950,9 +950,9 @@ __device__ __forceinline__ void gemv_mma_body(const GemvParams & p) {
     // work-group -> (task, tile block, K slice); these counts fit 32 bits
     static_assert(T::kReadEnd <= tile_group_bytes(TYPE) && tile_group_bytes(TYPE) <= (int)kSinkBytes,
                   "a stage reads inside one tile-group, which fits in the sink");
-    const uint32_t ntl = (uint32_t)p.w.ntiles, ntb = (ntl + (uint32_t)TW - 1) / (uint32_t)TW;
-    const WgPos wp = wg_pos(blockIdx.x, (uint32_t)p.KS, ntb);
-    const uint32_t ks = wp.ks, tb = wp.unit, task = wp.task;
+    const uint32_t ntl = (uint32_t)p.w.ntiles;
+    // the grid (KS, tile blocks, tasks) is the position, as in k_gemv
+    const uint32_t ks = blockIdx.x, tb = blockIdx.y, task = blockIdx.z + (uint32_t)p.task0;
     int mat, nc;
     bool sec = false;                  // the second image (gate/up in one launch)
     if (p.tasks) {
@@ -978,8 +978,9 @@ __device__ __forceinline__ void gemv_mma_body(const GemvParams & p) {
             s_doff[tid] = t.dst_off[tid] + dadd;
         }
     } else {
-        const DenseTask dt = dense_task(task, (uint32_t)p.tpb, (uint32_t)p.ne12, (uint32_t)p.r2, (uint32_t)p.r3,
-                                        (uint32_t)p.ne02);
+        const DenseTask dt = task == 0 ? DenseTask{ 0, 0, 0, 0, 0 }
+                                       : dense_task(task, (uint32_t)p.tpb, (uint32_t)p.ne12, (uint32_t)p.r2,
+                                                    (uint32_t)p.r3, (uint32_t)p.ne02);
         mat = dt.mat;
         if (p.base2 && mat == 1) {                                // gate/up in one launch
             mat = 0;
@@ -1258,13 +1259,13 @@ __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
     extern __shared__ __align__(16) uint8_t sm[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t ntl = (uint32_t)p.w.ntiles;
-    const WgPos wp = wg_pos(blockIdx.x, 1u, ntl);
-    const uint32_t tile = wp.unit, task = wp.task;
+    // the grid is the position: (tiles, slots, tokens) for MUL_MAT_ID pairs, pair p = t n_used + i;
+    // (tiles, tasks, 1) for dense products
+    const uint32_t tile = blockIdx.x, task = blockIdx.y;
     int mat, nc;
     int64_t colv[NC], doffv[NC];
     if (p.ids) {
-        const int64_t t = (int64_t)task / p.n_used, i = (int64_t)task - t * p.n_used;
+        const int64_t t = blockIdx.z, i = blockIdx.y;
         const int32_t e = *reinterpret_cast<const int32_t *>(p.ids + t * p.ids_nb1 + i * p.ids_nb0);
         const int64_t doff = t * p.dnb2 + i * p.dnb1;
         if (e < 0 || e >= p.n_as) {                                // uniform: a zero row
@@ -1283,8 +1284,9 @@ __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
             doffv[j] = doff;
         }
     } else {
-        const DenseTask dt = dense_task(task, (uint32_t)p.tpb, (uint32_t)p.ne12, (uint32_t)p.r2, (uint32_t)p.r3,
-                                        (uint32_t)p.ne02);
+        const DenseTask dt = task == 0 ? DenseTask{ 0, 0, 0, 0, 0 }
+                                       : dense_task(task, (uint32_t)p.tpb, (uint32_t)p.ne12, (uint32_t)p.r2,
+                                                    (uint32_t)p.r3, (uint32_t)p.ne02);
         mat = dt.mat;
         const int64_t first = (int64_t)dt.tt * NC;
         nc = (int)((p.ne11 - first) < NC ? (p.ne11 - first) : NC);
@@ -1387,7 +1389,9 @@ __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
 }  // namespace
 
 bool gemv_fused_plan(int type, const WView & w, int nc, int64_t ntasks, int target, FusedPlan * pl) {
-    if (!type_layout(type) || nc < 1 || nc > 2 || ntasks <= 0 || w.G <= 0 || w.ntiles <= 0) return false;
+    // (the launch's grid takes the tasks, or a MUL_MAT_ID's slots and tokens, as a dimension)
+    if (!type_layout(type) || nc < 1 || nc > 2 || ntasks <= 0 || ntasks > 65535 || w.G <= 0 || w.ntiles <= 0)
+        return false;
     const int64_t tiles = ntasks * w.ntiles;
     int64_t W = std::min<int64_t>(std::min<int64_t>(kFqMaxWaves, w.G), std::max<int64_t>(1, (target + tiles - 1) / tiles));
     const int64_t spw = (w.G + W - 1) / W;
@@ -1445,7 +1449,11 @@ hipError_t launch_gemv_fused(int type, const WView & w, const FusedPlan & pl, co
     }
     const int64_t nwg = pl.ntasks * w.ntiles;
     if (nwg <= 0 || nwg >= 0x7fffffff) return hipErrorInvalidValue;
-    const dim3 g((unsigned)nwg), b(64 * pl.W);
+    const dim3 g = f.ids ? dim3((unsigned)w.ntiles, (unsigned)f.n_used, (unsigned)f.T)
+                         : dim3((unsigned)w.ntiles, (unsigned)pl.ntasks, 1u);
+    if (w.ntiles > 0x7fffffff || (f.ids ? f.n_used > 65535 || f.T > 65535 : pl.ntasks > 65535))
+        return hipErrorInvalidValue;
+    const dim3 b(64 * pl.W);
     const uint32_t lds = (uint32_t)pl.lds;
 #define QMM_FQ_K(...)                                                                              \
     if (kt) hipExtLaunchKernelGGL(__VA_ARGS__, g, b, lds, s, kt->start, kt->stop, 0, p);            \
@@ -1693,11 +1701,20 @@ hipError_t launch_gemv(int type, const WView & w, const GemvPlan & pl, const Act
         uint32_t lds = (uint32_t)gemv_lds_bytes(type, pl);
         if (p.glu >= 0 && pl.W > pl.tw)                          // the K waves' sums of gate and up
             lds = std::max<uint32_t>(lds, (uint32_t)pl.W * (uint32_t)pl.cm * 64 * 4 * 2);
-        const dim3 g((unsigned)nwg), b(64 * pl.W);
+        // grid (KS, tile blocks, tasks): one launch per 65535 tasks (kernel timing stamps the first)
+        const int64_t ntb = (w.ntiles + pl.tw - 1) / pl.tw, per_task = (int64_t)pl.KS * ntb, ntasks = nwg / per_task;
+        if (ntasks * per_task != nwg || ntb > 65535) return hipErrorInvalidValue;
+        const dim3 b(64 * pl.W);
 #define QMM_MMA_K(K)                                                                                \
-    if (kt) hipExtLaunchKernelGGL(K, g, b, lds, s, kt->start, kt->stop, 0, p);                      \
-    else K<<<g, b, lds, s>>>(p);                                                                    \
-    return hipGetLastError();
+    for (int64_t t0 = 0; t0 < ntasks; t0 += 65535) {                                                \
+        p.task0 = (int)t0;                                                                          \
+        const dim3 g((unsigned)pl.KS, (unsigned)ntb, (unsigned)std::min<int64_t>(65535, ntasks - t0)); \
+        if (kt && t0 == 0) hipExtLaunchKernelGGL(K, g, b, lds, s, kt->start, kt->stop, 0, p);      \
+        else K<<<g, b, lds, s>>>(p);                                                                \
+        const hipError_t e_ = hipGetLastError();                                                    \
+        if (e_ != hipSuccess) return e_;                                                            \
+    }                                                                                               \
+    return hipSuccess;
 #define QMM_MMA(T)                                                                                  \
     if (pl.cm == 8) { QMM_MMA_K(k_gemv_mma<T>) }                                                    \
     if (pl.cm == 16) { QMM_MMA_K(k_gemv_mma16<T>) }                                                 \
