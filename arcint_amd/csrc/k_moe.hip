@@ -18,6 +18,8 @@
 // route serves every product that shares the ids.
 #include "qmm_device.h"
 
+#include <algorithm>
+
 namespace qmm {
 namespace {
 
@@ -254,11 +256,11 @@ __global__ __launch_bounds__(64) void k_topk(TopkArgs a) {
 // ---- the combine: dst[:, t] = sum_j w[j, t] experts[:, j, t] (+ shared[:, t] sigmoid(g[t]))
 // in llama.cpp's order: the products rounded, added slot by slot, then the gated shared
 // expert added (contraction off: ggml-cpu's MUL then ADDs round every product).
-__global__ __launch_bounds__(256) void k_combine(CombineArgs a) {
+// grid (ceil(M / 256), tokens from t0): the position without a division
+__global__ __launch_bounds__(256) void k_combine(CombineArgs a, int64_t t0) {
 #pragma clang fp contract(off)
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= a.M * a.T) return;
-    const int64_t t = idx / a.M, m = idx - t * a.M;
+    const int64_t m = (int64_t)blockIdx.x * 256 + threadIdx.x, t = t0 + blockIdx.y;
+    if (m >= a.M) return;
     const char * e = a.experts + t * a.enb2 + m * 4;
     const float * w = reinterpret_cast<const float *>(a.w + t * a.wnb1);
     float y = reinterpret_cast<const float *>(e)[0] * w[0];
@@ -287,9 +289,14 @@ hipError_t launch_topk(const TopkArgs & a, hipStream_t s) {
 }
 
 hipError_t launch_combine(const CombineArgs & a, hipStream_t s) {
-    if (a.M < 1 || a.T < 1 || a.k < 1 || a.M * a.T >= ((int64_t)1 << 40)) return hipErrorInvalidValue;
-    k_combine<<<dim3((unsigned)((a.M * a.T + 255) / 256)), 256, 0, s>>>(a);
-    return hipGetLastError();
+    if (a.M < 1 || a.T < 1 || a.k < 1 || a.M * a.T >= ((int64_t)1 << 40) || (a.M + 255) / 256 > 0x7fffffff)
+        return hipErrorInvalidValue;
+    for (int64_t t0 = 0; t0 < a.T; t0 += 65535) {              // (grid y: at most 65535 tokens a launch)
+        k_combine<<<dim3((unsigned)((a.M + 255) / 256), (unsigned)std::min<int64_t>(65535, a.T - t0)), 256, 0, s>>>(a, t0);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 namespace {

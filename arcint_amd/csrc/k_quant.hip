@@ -27,8 +27,9 @@ constexpr int kTpb = 256;
 __device__ void zero_cols(const ZeroJob & z, int64_t t) {
     const int64_t rows = z.M - z.m0, n = rows * z.ncols;
     if (t >= n) return;
-    const int64_t c = t / rows, m = z.m0 + (t - c * rows);
-    const int64_t r = c / z.ne1, i1 = c - r * z.ne1, i3 = r / z.ne2, i2 = r - i3 * z.ne2;
+    int64_t mr, i1, i2;
+    const int64_t c = qdiv(t, rows, mr), m = z.m0 + mr;
+    const int64_t r = qdiv(c, z.ne1, i1), i3 = qdiv(r, z.ne2, i2);
     z.dst[i1 * z.nb1 + i2 * z.nb2 + i3 * z.nb3 + m] = 0.0f;
 }
 
@@ -60,8 +61,9 @@ __global__ __launch_bounds__(256) void k_quant_tiled_q8_0(F32Cols src, int64_t K
     const int64_t w = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
     if (w >= nwaves) return;                       // whole waves
     const int lane = threadIdx.x & 63, i = lane & 31, h = lane >> 5;
-    const int64_t tile = w / ta.nblk, blk = w - tile * ta.nblk, b = tile / ta.ntb;
-    const int64_t n = (tile - b * ta.ntb) * 32 + i, k0 = blk * 32 + 16 * h;
+    int64_t blk, tt;
+    const int64_t tile = qdiv(w, ta.nblk, blk), b = qdiv(tile, ta.ntb, tt);
+    const int64_t n = tt * 32 + i, k0 = blk * 32 + 16 * h;
     float v[16];
     if (n < ta.N && k0 < K) {
         const float * x = f32_col(src, b * ta.N + n) + k0;   // (column strides are only 4-byte aligned)
@@ -110,9 +112,10 @@ __global__ __launch_bounds__(512) void k_quant_tiled_q8_K(F32Cols src, int64_t K
     __shared__ float s_amax[8][32], s_mx[8][32];
     __shared__ int8_t s_split[32][16];
     const int64_t job = blockIdx.x;                  // (tile, super-block)
-    const int64_t tile = job / nsb, sb = job - tile * nsb, b = tile / ta.ntb;
+    int64_t sb, tt;
+    const int64_t tile = qdiv(job, nsb, sb), b = qdiv(tile, ta.ntb, tt);
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, i = lane & 31, h = lane >> 5;
-    const int64_t n = (tile - b * ta.ntb) * 32 + i, k0 = sb * 256 + 32 * w + 16 * h;
+    const int64_t n = tt * 32 + i, k0 = sb * 256 + 32 * w + 16 * h;
     float v[16];
     if (n < ta.N && k0 < K) {
         const float * x = f32_col(src, b * ta.N + n) + k0;   // (column strides are only 4-byte aligned)

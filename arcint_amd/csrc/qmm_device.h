@@ -224,11 +224,26 @@ __device__ __forceinline__ const float * f32_col(const F32Cols & s, int64_t c) {
 // threads (whole waves; a block of threads is a multiple of 64).
 #pragma clang fp contract(off)
 
+// a / b (and a % b in r) for a, b >= 0: 32-bit when both fit, as they do for every realistic
+// shape (a 64-bit division is a long instruction sequence ahead of a latency-bound kernel's
+// first memory access)
+__device__ __forceinline__ int64_t qdiv(int64_t a, int64_t b, int64_t & r) {
+    if (((uint64_t)a | (uint64_t)b) < 0x80000000ull) {
+        const uint32_t q = (uint32_t)a / (uint32_t)b;
+        r = (int64_t)((uint32_t)a - q * (uint32_t)b);
+        return (int64_t)q;
+    }
+    const int64_t q = a / b;
+    r = a - q * b;
+    return q;
+}
+
 // q8_0: 8 lanes per 32-weight block, 4 weights per lane
 __device__ __forceinline__ void quant_q8_0_at(const F32Cols & src, int64_t K, int64_t ncols, const ActBuf & a, int64_t t) {
     const int64_t kq = a.ldk / 4;
     const bool live = t < ncols * kq;              // groups of 8 lanes are all live or all dead
-    const int64_t c = live ? t / kq : 0, k = live ? (t % kq) * 4 : 0;
+    int64_t kr = 0;
+    const int64_t c = live ? qdiv(t, kq, kr) : 0, k = live ? kr * 4 : 0;
     float v[4] = { 0.f, 0.f, 0.f, 0.f };
     if (live && k < K) {
         const float * x = f32_col(src, c) + k;
@@ -253,7 +268,8 @@ __device__ __forceinline__ void quant_q8_K_at(const F32Cols & src, int64_t K, in
     const int lane = (int)(t & 63);
     const int64_t nsb = a.ldk / 256;
     if (wave >= ncols * nsb) return;               // whole waves only
-    const int64_t c = wave / nsb, sb = wave % nsb;
+    int64_t sb;
+    const int64_t c = qdiv(wave, nsb, sb);
     float v[4] = { 0.f, 0.f, 0.f, 0.f };
     if (sb * 256 < K) {
         const float * x = f32_col(src, c) + sb * 256 + 4 * lane;
