@@ -1176,9 +1176,13 @@ int env_int(const char * name, int dflt) {
 // atomics) ahead of it.  At decode that launch and its kernel boundary are a fifth of the op.
 // Here every wave quantizes the groups it streams itself, with the pre-pass's own quantizers
 // (so the codes equal ggml-cpu's), into its own LDS slots, after its first weight stage is on
-// its way; K is split only among the waves of a work-group and added in LDS, so every output
-// is stored once and nothing has to be zeroed first.  The same kernel takes:
-//  * dense MUL_MAT at 1 or 2 columns per task;
+// its way; K is split among the waves of a work-group and added in LDS, so every output is
+// stored once and nothing has to be zeroed first.  A dense product may also split K over KS
+// work-groups per tile (one tile per work-group puts 272 work-groups of config 2's 17408-row
+// matrices on 256 CUs, 16 of which then stream twice): the work-groups' sums meet in a
+// pairwise tree of exchanges (tree_add) and the last arrival stores the row.  The same kernel
+// takes:
+//  * dense MUL_MAT at 1 or 2 columns per task, K split over KS >= 1 work-groups (no GLU);
 //  * MUL_MAT_ID at small batches with no route: task p is the (token, slot) pair p and reads its
 //    expert id itself (the reference's per-pair matvec below 16 tokens, P01:1189-1192 and
 //    P01:1222-1248); a negative id writes a zero row, an id past the stack too and sets the
@@ -1216,18 +1220,62 @@ struct FqParams {
     const uint8_t * base2;       // glu >= 0: the up image, w's shape
     int glu;
     int W, spw;
+    int KS;                      // dense: work-groups per tile along K (grid z)
+    uint32_t * tree;             // KS > 1: slots [task][tile][2 KS nodes][NC][64], each kTreeEmpty
 };
 
-// group g of activation column col, quantized by one wave into a slot (the pre-pass's quantizers)
-template <int VDT>
-__device__ __forceinline__ void quant_slot(const F32Cols & xs, int64_t K, int64_t col, int g, uint8_t * slot, int lane) {
-    float v[4] = { 0.f, 0.f, 0.f, 0.f };
-    const int64_t k = (int64_t)g * 256 + 4 * lane;                // K is whole 32-blocks (q8_0) or 256-blocks
-    if (k < K) {
-        const float * x = f32_col(xs, col) + k;
+// The K slices of a tile add their sums v[j] (column j, this lane's row) up a pairwise tree
+// in slot memory: at a level of n nodes, node i meets node i ^ 1 in slot (i / 2) of the
+// level (an odd last node moves up alone).  Each meeting is one exchange: the first arrival
+// leaves its sum in the slot and is done; the second takes it, adds it to its own (the
+// sum of the two is the same whichever arrives first) and puts the slot back to kTreeEmpty.
+// The last arrival at the root holds the row's total: alive[j] stays true for that lane
+// only.  Every slot is reached by exactly two exchanges, so the protocol needs no ordering
+// between different slots, and the launch ends with every slot empty again.
+template <int NC>
+__device__ __forceinline__ void tree_add(uint32_t * nodes, int ks, int KS, int nc, float (&v)[NC], bool (&alive)[NC],
+                                         int lane) {
+    uint32_t i = (uint32_t)ks, n = (uint32_t)KS, off = 0;
+    while (n > 1) {                                               // uniform
+        if ((i ^ 1u) < n) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = x[i];
+            for (int j = 0; j < NC; ++j) {
+                if (j < nc && alive[j]) {
+                    uint32_t * s = nodes + ((size_t)(off + (i >> 1)) * NC + j) * 64 + lane;
+                    const uint32_t o = __hip_atomic_exchange(s, __float_as_uint(v[j]), __ATOMIC_RELAXED,
+                                                             __HIP_MEMORY_SCOPE_AGENT);
+                    if (o == kTreeEmpty) {
+                        alive[j] = false;
+                    } else {
+                        v[j] += __uint_as_float(o);
+                        __hip_atomic_store(s, kTreeEmpty, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
+                }
+            }
+        }
+        off += (n + 1) >> 1;
+        i >>= 1;
+        n = (n + 1) >> 1;
     }
+}
+
+// this lane's 4 activations of group g of column col (zeros past K; the loads stay inside the
+// column and take no branch, so the waits that follow can count them)
+__device__ __forceinline__ void load_x4(const F32Cols & xs, int64_t K, int64_t col, int g, int lane, float (&v)[4]) {
+    const int64_t k = (int64_t)g * 256 + 4 * lane;                // K is whole 32-blocks (q8_0) or 256-blocks
+    const bool in = k < K;
+    const float * x = f32_col(xs, col) + (in ? k : 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float t = x[i];
+        v[i] = in ? t : 0.f;
+    }
+}
+
+// group g of activation column col, quantized by one wave into a slot (the pre-pass's quantizers)
+// from the lanes' 4 values each (load_x4)
+template <int VDT>
+__device__ __forceinline__ void quant_slot(float (&v)[4], uint8_t * slot, int lane) {
     float d;
     int s;
     if constexpr (VDT == QMM_TYPE_Q8_K) {
@@ -1260,8 +1308,9 @@ __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     // the grid is the position: (tiles, slots, tokens) for MUL_MAT_ID pairs, pair p = t n_used + i;
-    // (tiles, tasks, 1) for dense products
+    // (tiles, tasks, K slices) for dense products
     const uint32_t tile = blockIdx.x, task = blockIdx.y;
+    const int ks = p.ids ? 0 : (int)blockIdx.z;
     int mat, nc;
     int64_t colv[NC], doffv[NC];
     if (p.ids) {
@@ -1300,7 +1349,7 @@ __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
     nc = __builtin_amdgcn_readfirstlane(nc);
     const int G = (int)p.w.G;
     int ga, S;
-    dot4_stages(0, p.W, wave, p.spw, G, NST, ga, S);
+    dot4_stages(ks, p.W, wave, p.spw, G, NST, ga, S);
     const bool glu = p.glu >= 0;                                  // uniform
     const int ST = glu ? 2 * S : S;                               // gate stages, then up stages
     const uint8_t * tbg = tile_group(p.w, mat, tile, 0);
@@ -1319,13 +1368,24 @@ __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
         }
         T::load(B, tg, st, lane);
     };
-    if (ST > 0) load_stage(0);                                    // the weights go out first
+    // the first group's activations are requested ahead of the weights: behind the weight
+    // stream in the memory queues they would arrive with its end and hold every dot back
+    // (both unconditional: colv[j] is a column of src1 for every j, a wave without groups reads
+    // zeros and the sink)
+    float xv[NC][4];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) load_x4(p.x, p.K, colv[j], ga, lane, xv[j]);
+    load_stage(0);
     // the wave's groups of its columns into its slots [group][column]
     uint8_t * const slots = sm + (size_t)wave * p.spw * NC * kFqSlot;
     for (int gi = 0; gi * NST < S; ++gi) {                        // uniform
 #pragma unroll
-        for (int j = 0; j < NC; ++j)
-            if (j < nc) quant_slot<VDT>(p.x, p.K, colv[j], ga + gi, slots + (gi * NC + j) * kFqSlot, lane);
+        for (int j = 0; j < NC; ++j) {
+            if (j < nc) {
+                if (gi > 0) load_x4(p.x, p.K, colv[j], ga + gi, lane, xv[j]);
+                quant_slot<VDT>(xv[j], slots + (gi * NC + j) * kFqSlot, lane);
+            }
+        }
     }
     __builtin_amdgcn_wave_barrier();
     float acc[NC], accu[NC];
@@ -1380,10 +1440,16 @@ __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
 #pragma unroll
         for (int j = 0; j < NC; ++j) tot[j] = glu ? glu_apply(p.glu, acc[j], accu[j]) : acc[j];
     }
+    bool alive[NC];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) alive[j] = true;
+    if (p.KS > 1)                                                 // uniform (dense, no GLU)
+        tree_add<NC>(p.tree + ((size_t)task * (size_t)p.w.ntiles + tile) * (2 * (size_t)p.KS * NC * 64), ks, p.KS, nc,
+                     tot, alive, lane);
     if (row >= p.w.M) return;
 #pragma unroll
     for (int j = 0; j < NC; ++j)
-        if (j < nc) p.dst[doffv[j] + row] = tot[j];
+        if (j < nc && alive[j]) p.dst[doffv[j] + row] = tot[j];
 }
 
 }  // namespace
@@ -1400,16 +1466,39 @@ bool gemv_fused_plan(int type, const WView & w, int nc, int64_t ntasks, int targ
     pl->ntasks = ntasks;
     pl->W = (int)W;
     pl->spw = (int)spw;
+    pl->KS = 1;
     pl->lds = std::max<int64_t>(W * spw * nc * kFqSlot, W * 2 * nc * 64 * 4);
     return pl->lds <= 64 * 1024 && tiles < 0x7fffffff;
+}
+
+bool gemv_fused_split_plan(int type, const WView & w, int nc, int64_t ntasks, int W, int spw, FusedPlan * pl) {
+    if (!type_layout(type) || nc < 1 || nc > 2 || ntasks <= 0 || ntasks > 65535 || w.G <= 0 || w.ntiles <= 0 ||
+        W < 1 || W > kFqMaxWaves || spw < 1)
+        return false;
+    const int64_t per_wg = (int64_t)W * spw;
+    const int64_t KS = (w.G + per_wg - 1) / per_wg;               // the last slice may have idle waves
+    if (KS < 2 || KS > 65535) return false;
+    pl->nc = nc;
+    pl->ntasks = ntasks;
+    pl->W = W;
+    pl->spw = spw;
+    pl->KS = (int)KS;
+    pl->lds = std::max<int64_t>(per_wg * nc * kFqSlot, (int64_t)W * 2 * nc * 64 * 4);
+    return pl->lds <= 64 * 1024 && ntasks * w.ntiles < 0x7fffffff;
+}
+
+int64_t gemv_fused_tree_words(const WView & w, const FusedPlan & pl) {
+    return pl.KS > 1 ? pl.ntasks * w.ntiles * 2 * pl.KS * pl.nc * 64 : 0;
 }
 
 int gemv_fused_waves_target() { return std::max(1, env_int("QMM_GEMV_FQ_WAVES", 4096)); }
 
 hipError_t launch_gemv_fused(int type, const WView & w, const FusedPlan & pl, const FusedGemv & f, float * dst,
                              const void * sink, hipStream_t s, const KTime * kt) {
-    if (!sink || !dst || pl.W < 1 || pl.W > kFqMaxWaves || pl.spw < 1 || pl.nc < 1 || pl.nc > 2 ||
-        (int64_t)pl.W * pl.spw < w.G || (int64_t)(pl.W - 1) * pl.spw >= w.G || f.K != w.K ||
+    if (!sink || !dst || pl.W < 1 || pl.W > kFqMaxWaves || pl.spw < 1 || pl.nc < 1 || pl.nc > 2 || pl.KS < 1 ||
+        pl.KS > 65535 || (int64_t)pl.KS * pl.W * pl.spw < w.G ||
+        (pl.KS == 1 ? (int64_t)(pl.W - 1) * pl.spw >= w.G : (int64_t)(pl.KS - 1) * pl.W * pl.spw >= w.G) ||
+        (pl.KS > 1 && (f.ids || f.glu >= 0 || !f.tree)) || f.K != w.K ||
         (f.ids && (pl.nc != 1 || f.n_used < 1 || pl.ntasks != f.n_used * f.T || !f.bad_id)) ||
         (f.glu > QMM_GLU_GEGLU_QUICK) || (f.glu >= 0 && !f.base2))
         return hipErrorInvalidValue;
@@ -1423,6 +1512,8 @@ hipError_t launch_gemv_fused(int type, const WView & w, const FusedPlan & pl, co
     p.glu = f.glu;
     p.W = pl.W;
     p.spw = pl.spw;
+    p.KS = pl.KS;
+    p.tree = f.tree;
     if (f.ids) {
         p.ids = f.ids;
         p.ids_nb0 = f.ids_nb0;
@@ -1450,7 +1541,7 @@ hipError_t launch_gemv_fused(int type, const WView & w, const FusedPlan & pl, co
     const int64_t nwg = pl.ntasks * w.ntiles;
     if (nwg <= 0 || nwg >= 0x7fffffff) return hipErrorInvalidValue;
     const dim3 g = f.ids ? dim3((unsigned)w.ntiles, (unsigned)f.n_used, (unsigned)f.T)
-                         : dim3((unsigned)w.ntiles, (unsigned)pl.ntasks, 1u);
+                         : dim3((unsigned)w.ntiles, (unsigned)pl.ntasks, (unsigned)pl.KS);
     if (w.ntiles > 0x7fffffff || (f.ids ? f.n_used > 65535 || f.T > 65535 : pl.ntasks > 65535))
         return hipErrorInvalidValue;
     const dim3 b(64 * pl.W);

@@ -68,6 +68,10 @@ struct qmm_ctx {
     } rkey;
     size_t glu_cap = 0;
     void * glu = nullptr;            // gate/up sums of qmm_mul_mat_glu
+    // the slots of the fused GEMV's K-slice tree: filled with kTreeEmpty when allocated, and
+    // every launch leaves them so
+    uint32_t * tree = nullptr;
+    size_t tree_words = 0;
     // downgrades: ops that took a slower path than their weight type promises, counted per key
     // in fixed storage (recording one allocates nothing); keys past the table count as "other"
     struct Downgrade {
@@ -261,6 +265,26 @@ int ensure(qmm_ctx * ctx, void ** p, size_t * cap, size_t need) {
     size_t sz = std::max(need, (size_t)(*cap * 3 / 2));
     QMM_HIP(ctx, hipMalloc(p, sz));
     *cap = sz;
+    return QMM_OK;
+}
+
+// tree slots for a split fused GEMV: grown outside captures only, each new allocation filled
+// with kTreeEmpty on the stream ahead of its first use
+int ensure_tree(qmm_ctx * ctx, size_t words) {
+    if (words <= ctx->tree_words) return QMM_OK;
+    if (ctx->capturing)
+        return fail(ctx, QMM_ERR_NOMEM, "capture: the op needs %zu words of tree slots and the context has %zu; run "
+                                        "it once outside a capture first", words, ctx->tree_words);
+    if (ctx->tree) {
+        QMM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        QMM_HIP(ctx, hipFree(ctx->tree));
+        ctx->tree = nullptr;
+        ctx->tree_words = 0;
+    }
+    const size_t n = std::max(words, ctx->tree_words * 3 / 2);
+    QMM_HIP(ctx, hipMalloc((void **)&ctx->tree, n * 4));
+    QMM_HIP(ctx, hipMemsetD32Async((hipDeviceptr_t)ctx->tree, (int)kTreeEmpty, n, ctx->stream));
+    ctx->tree_words = n;
     return QMM_OK;
 }
 
@@ -559,6 +583,7 @@ void qmm_ctx_free(qmm_ctx * ctx) {
     if (ctx->act) (void)hipFree(ctx->act);
     if (ctx->route) (void)hipFree(ctx->route);
     if (ctx->glu) (void)hipFree(ctx->glu);
+    if (ctx->tree) (void)hipFree(ctx->tree);
     if (ctx->sink) (void)hipFree(ctx->sink);
     if (ctx->dflags) (void)hipFree(ctx->dflags);
     if (ctx->hflags) (void)hipHostFree(ctx->hflags);
@@ -902,13 +927,37 @@ static int64_t fused_small_tgroups() {
     return e ? atoll(e) : 512;
 }
 
-// whether a dense product of N columns in nbatch batches takes the fused GEMV, and its plan
-static bool fused_dense_plan(int type, const WView & w, int64_t N, int64_t nbatch, FusedPlan * fp) {
+// Dense products of 1-2 columns may also split K over work-groups of the fused kernel (its
+// K-slice tree): one launch instead of the pre-pass and the GEMV, which wins where the image is
+// small enough for the pre-pass to be a large part of the op (Q4_0 4096 x 4096, 9.4 MB, N = 1:
+// 7.0-8.9 -> 6.2-6.3 us) and loses on larger ones, where the wave's own quantization costs more
+// than the launch it saves (Q4_K 17408 x 5120: 12.5 -> 13.9 us; Q6_K 5120 x 17408 16.5 -> 18.1;
+// Q8_0 14336 x 4096 14.3 -> 15.5).  Taken up to QMM_GEMV_FQS_MAX_KB of one matrix's image
+// (16 MiB); QMM_GEMV_FQS = 0 never, = 1 at any size; work-groups of QMM_GEMV_FQS_W waves (4,
+// the best of 1, 2, 4, 5 and 10 on config 2's Q4_K) with QMM_GEMV_FQS_SPW groups each (1).
+static int env_or(const char * name, int dflt) {
+    const char * e = getenv(name);
+    return e ? atoi(e) : dflt;
+}
+static bool fused_split_for(const WView & w) {
+    const int mode = env_or("QMM_GEMV_FQS", -1);
+    if (mode == 0) return false;
+    if (mode > 0) return true;
+    const int64_t image = w.ntiles * w.G * (int64_t)w.tg;
+    return image <= (int64_t)env_or("QMM_GEMV_FQS_MAX_KB", 16384) * 1024;
+}
+
+// whether a dense product of N columns in nbatch batches takes the fused GEMV, and its plan;
+// split: K may be split over work-groups (not for a GLU, nor where nothing may be allocated)
+static bool fused_dense_plan(int type, const WView & w, int64_t N, int64_t nbatch, FusedPlan * fp, bool split) {
     if (!fused_on() || N > 2 || N < 1) return false;
-    if (!gemv_fused_plan(type, w, (int)N, nbatch, gemv_fused_waves_target(), fp)) return false;
-    const int64_t tgroups = fp->ntasks * w.ntiles * w.G;
-    if (w.G <= 8 && tgroups <= fused_small_tgroups()) return true;
-    return fp->ntasks * w.ntiles * fp->W >= fused_min_waves();
+    if (gemv_fused_plan(type, w, (int)N, nbatch, gemv_fused_waves_target(), fp)) {
+        const int64_t tgroups = fp->ntasks * w.ntiles * w.G;
+        if (w.G <= 8 && tgroups <= fused_small_tgroups()) return true;
+        if (fp->ntasks * w.ntiles * fp->W >= fused_min_waves()) return true;
+    }
+    return split && fused_split_for(w) &&
+           gemv_fused_split_plan(type, w, (int)N, nbatch, env_or("QMM_GEMV_FQS_W", 4), env_or("QMM_GEMV_FQS_SPW", 1), fp);
 }
 // whether a MUL_MAT_ID of T tokens with n_used ids each takes the fused GEMV's pairs, and its plan
 static bool fused_id_plan(int type, const WView & w, int64_t n_used, int64_t T, FusedPlan * fp) {
@@ -951,16 +1000,16 @@ int qmm_describe_mul_mat(const qmm_tensor * src0, const qmm_tensor * src1, const
         return QMM_OK;
     }
     FusedPlan fp;
-    if (fused_dense_plan(src0->type, w, N, src1->ne[2] * src1->ne[3], &fp)) {
+    if (fused_dense_plan(src0->type, w, N, src1->ne[2] * src1->ne[3], &fp, true)) {
         snprintf(out->path, sizeof(out->path), "gemv-fq");
         out->threads = 64 * fp.W;
         out->cols_per_task = fp.nc;
         out->tasks = fp.ntasks;
         out->k_waves = fp.W;
         out->tiles_per_wg = 1;
-        out->k_slices = 1;
+        out->k_slices = fp.KS;
         out->groups_per_wave = fp.spw;
-        out->workgroups = fp.ntasks * w.ntiles;
+        out->workgroups = fp.ntasks * w.ntiles * fp.KS;
         out->lds_bytes = fp.lds;
         return QMM_OK;
     }
@@ -983,10 +1032,14 @@ int qmm_describe_mul_mat(const qmm_tensor * src0, const qmm_tensor * src1, const
 
 // a dense fused launch when the shape suits it (false: not taken, nothing enqueued)
 static bool try_fused_dense(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1, const WView & w,
-                            const GemvDense & dn, float * d, const uint8_t * up_base, int glu, int * rc) {
+                            const GemvDense & dn, float * d, const uint8_t * up_base, int glu, bool noalloc, int * rc) {
     FusedPlan fp;
-    if (!fused_dense_plan(src0->type, w, src1->ne[1], dn.ne12 * dn.ne13, &fp)) return false;
+    if (!fused_dense_plan(src0->type, w, src1->ne[1], dn.ne12 * dn.ne13, &fp, glu < 0 && !noalloc)) return false;
     FusedGemv f{};
+    if (fp.KS > 1) {
+        if ((*rc = ensure_tree(ctx, (size_t)gemv_fused_tree_words(w, fp)))) return true;
+        f.tree = ctx->tree;
+    }
     f.x = f32_cols(src1);
     f.K = src1->ne[0];
     f.dense = dn;
@@ -1090,7 +1143,7 @@ static int mul_mat_launch(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tens
         QMM_HIP(ctx, launch_gemm(src0->type, w, a, N, dn.ne12 * dn.ne13, bt, d, ctx->stream, ktp));
         return ktime_done(ctx);
     }
-    if (try_fused_dense(ctx, src0, src1, w, dn, d, nullptr, -1, &rc)) {
+    if (try_fused_dense(ctx, src0, src1, w, dn, d, nullptr, -1, fixed != nullptr, &rc)) {
         ctx->path = "gemv-fq";
         return rc;
     }
@@ -1479,7 +1532,7 @@ int qmm_mul_mat_glu(qmm_ctx * ctx, const qmm_tensor * gate, const qmm_tensor * u
         dn.d_nb2 = (int64_t)(dst->nb[2] / 4);
         dn.d_nb3 = (int64_t)(dst->nb[3] / 4);
         int frc;
-        if (try_fused_dense(ctx, gate, src1, wg, dn, (float *)((uint8_t *)dst->buffer->ptr + dst->offs), wu.base, glu_op, &frc)) {
+        if (try_fused_dense(ctx, gate, src1, wg, dn, (float *)((uint8_t *)dst->buffer->ptr + dst->offs), wu.base, glu_op, false, &frc)) {
             ctx->path = "glu-fused-gemv-fq";
             return frc;
         }
@@ -1602,7 +1655,7 @@ int qmm_internal_gemv_extent(int32_t type, const int64_t ne0[4], int64_t N, int6
         plan.nc = f.nc;
         plan.ntasks = f.ntasks;
         plan.W = f.W;
-        plan.KS = 1;
+        plan.KS = f.KS;
         plan.spw = f.spw;
         plan.mma = false;
         plan.tw = 1;
@@ -1612,7 +1665,7 @@ int qmm_internal_gemv_extent(int32_t type, const int64_t ne0[4], int64_t N, int6
         if (use_gemm_for(type, w, N, nbatch)) return QMM_ERR_UNSUPPORTED;
         const int nc = gemv_task_cols(type, N);
         const int64_t ntasks = (N + nc - 1) / nc * nbatch;
-        if (fused_dense_plan(type, w, N, nbatch, &fp)) as_plan(fp);
+        if (fused_dense_plan(type, w, N, nbatch, &fp, true)) as_plan(fp);
         else if (!gemv_plan(type, w, nc, ntasks, true, nc >= gemv_mma_min_cols(), &plan)) return QMM_ERR_UNSUPPORTED;
         GemvDense dn;
         dn.ne11 = N;

@@ -255,11 +255,12 @@ hipError_t launch_gemv(int type, const WView & w, const GemvPlan & plan, const A
                        const int32_t * ntasks_dev, const GemvDense * dense, float * dst, const void * sink,
                        hipStream_t s, const KTime * kt = nullptr, const GemvPair * pair = nullptr);
 
-// The v_dot4 GEMV with its own activation quantization (k_gemv_fq): no pre-pass, K split only
-// among the W waves of a work-group (at most 16), every output stored once.  nc = columns per
-// task (1 or 2).  Dense tasks as GemvDense; with ids, task p is the MUL_MAT_ID pair p = t n_used
-// + i (nc = 1).  glu >= 0: the work-group streams w (gate) then base2 (up) and stores
-// act(gate) * up.
+// The v_dot4 GEMV with its own activation quantization (k_gemv_fq): no pre-pass, K split
+// among the W waves of a work-group (at most 16) and, for dense products without a GLU, over
+// KS work-groups per tile whose sums meet in a tree of exchanges (tree slots below); every
+// output is stored once.  nc = columns per task (1 or 2).  Dense tasks as GemvDense; with ids,
+// task p is the MUL_MAT_ID pair p = t n_used + i (nc = 1).  glu >= 0: the work-group streams w
+// (gate) then base2 (up) and stores act(gate) * up.
 struct FusedGemv {
     F32Cols x;                  // src1's f32 columns
     int64_t K;
@@ -270,14 +271,25 @@ struct FusedGemv {
     int32_t * bad_id;           // set when an id is >= n_as
     const uint8_t * base2;      // glu >= 0: the up image
     int glu;
+    uint32_t * tree;            // KS > 1: gemv_fused_tree_words words, each kTreeEmpty
 };
 struct FusedPlan {
     int nc, W, spw;
+    int KS = 1;                 // work-groups per tile along K (dense, no GLU)
     int64_t ntasks;
     int64_t lds;
 };
+// The slots of the K-slice tree hold this between launches: a signaling NaN, which no float
+// arithmetic produces, so a slot holds either it or one work-group's sum.  A launch leaves
+// every slot it touched at this value again.
+constexpr uint32_t kTreeEmpty = 0x7F800001u;
 // about `target` waves over ntasks x tiles work-groups; false when the K range does not fit
 bool gemv_fused_plan(int type, const WView & w, int nc, int64_t ntasks, int target, FusedPlan * plan);
+// dense products split along K: work-groups of W waves with spw groups per wave, KS =
+// ceil(G / (W spw)) >= 2 of them per tile; false when that gives one slice or does not fit
+bool gemv_fused_split_plan(int type, const WView & w, int nc, int64_t ntasks, int W, int spw, FusedPlan * plan);
+// tree slots (32-bit words) a split plan needs
+int64_t gemv_fused_tree_words(const WView & w, const FusedPlan & plan);
 int gemv_fused_waves_target();
 hipError_t launch_gemv_fused(int type, const WView & w, const FusedPlan & plan, const FusedGemv & f, float * dst,
                              const void * sink, hipStream_t s, const KTime * kt = nullptr);

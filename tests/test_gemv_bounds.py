@@ -104,3 +104,23 @@ def test_sink_covers_every_stage_extent():
         e = extent(qtype, (256, 64), 1)
         assert e["read_end"] <= SINK_BYTES
         assert e["read_end"] * ((64 + 63) // 64) * 1 <= e["image_bytes"]
+
+
+@pytest.mark.parametrize("qtype,M,K", SHAPES)
+def test_fused_split_loads_in_bounds(monkeypatch, qtype, M, K):
+    """the fused kernel with K split over work-groups (forced at every size, 1 and 4 waves a
+    work-group): its loads stay inside the image and the sink, every tile-group once"""
+    monkeypatch.setenv("QMM_GEMV_FQS", "1")
+    fake = qmm.Buffer(ptr=0x1000, size=1 << 44)
+    for W in ("1", "4"):
+        monkeypatch.setenv("QMM_GEMV_FQS_W", W)
+        for N in (1, 2):
+            ne0 = (K, M)
+            e = extent(qtype, ne0, N)
+            info = qmm.describe_mul_mat(qmm.Tensor(fake, qtype, ne0), qmm.Tensor(fake, qmm.F32, (K, N)),
+                                        qmm.Tensor(fake, qmm.F32, (M, N)))
+            assert info["path"] == "gemv-fq", info
+            nt, G = tiles_groups(ne0)
+            check(e, info["tasks"] * nt * G)
+            if G > int(W):
+                assert info["k_slices"] == -(-G // int(W)) or info["k_slices"] == 1, info

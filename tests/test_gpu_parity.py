@@ -435,6 +435,7 @@ def test_mul_mat_gemv(be, sc, orc, monkeypatch, qtype, N):
     """the pre-pass GEMV kernels (the fused one, which small 1-2 column products take by
     default, has its own tests)"""
     monkeypatch.setenv("QMM_GEMV_FQ_SMALL_TG", "0")
+    monkeypatch.setenv("QMM_GEMV_FQS", "0")
     M, K = 300, 2048
     say("gemv", qtype, M, K, N)
     got, ref = run_mul_mat(be, sc, orc, qtype, M, K, N, seed=51)
@@ -1228,6 +1229,57 @@ def test_fused_gemv_broadcast_strides_and_split_path(be, sc, orc, monkeypatch, q
     be.synchronize()
     assert be.last_path() == "gemv"
     assert rel_err(be.get_f32(ypad).reshape(4, N, M + 5)[:, :, :M], got) <= TOL
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("M,K,N,W", [(300, 2048, 1, 4), (130, 5120, 2, 3), (65, 4352, 1, 1), (64, 768, 2, 2),
+                                     (1, 768, 1, 1)])
+def test_fused_gemv_split(be, sc, orc, monkeypatch, qtype, M, K, N, W):
+    """K split over work-groups of the fused kernel, their sums met in the exchange tree: KS = 2;
+    20 groups over 7 slices of 3 waves (an odd KS, an idle last wave); 17 one-group slices; 3
+    groups over 2 slices of 2 waves; a one-row matrix.  Twice on the same weights with new
+    activations: the tree's slots are empty again after every launch"""
+    monkeypatch.setenv("QMM_GEMV_FQS", "1")
+    monkeypatch.setenv("QMM_GEMV_FQS_W", str(W))
+    monkeypatch.setenv("QMM_GEMV_FQ_SMALL_TG", "0")
+    say("fused split", qtype, M, K, N, W)
+    raw = synth.weights(qtype, M, K, seed=211)
+    w = sc.weights(qtype, raw, (K, M))
+    xt, y = sc.f32(np.zeros((N, K), np.float32)), sc.empty_f32((M, N))
+    G = -(-K // 256)
+    for seed in (212, 213):
+        x = synth.activations(N, K, seed=seed)
+        be.set_tensor(xt, x.view(np.uint8).ravel())
+        be.mul_mat(w, xt, y)
+        be.synchronize()
+        assert be.last_path() == "gemv-fq"
+        assert qmm.describe_mul_mat(w, xt, y)["k_slices"] == -(-G // W)
+        assert rel_err(be.get_f32(y).reshape(N, M), orc.mul_mat(qtype, raw, M, K, x)) <= TOL, seed
+
+
+@pytest.mark.parametrize("qtype", [qmm.Q4_K, qmm.Q4_0, qmm.Q6_K])
+def test_fused_gemv_split_broadcast(be, sc, orc, monkeypatch, qtype):
+    """the K-split fused kernel over broadcast batches with a strided src1 view and a padded dst
+    (each batch's tiles meet in their own tree slots)"""
+    monkeypatch.setenv("QMM_GEMV_FQS", "1")
+    monkeypatch.setenv("QMM_GEMV_FQS_W", "1")
+    monkeypatch.setenv("QMM_GEMV_FQ_SMALL_TG", "0")
+    say("fused split broadcast", qtype)
+    K, M, N = 512, 80, 2
+    raw = synth.weights(qtype, 2 * M, K, seed=214)
+    w = sc.weights(qtype, raw, (K, M, 2))
+    x = synth.activations(8 * N, K, seed=215).reshape(4, 2 * N, K)
+    xt = sc.f32(x)
+    xv = qmm.Tensor(xt.buf, qmm.F32, (K, N, 4), nb=(4, 8 * K, 8 * K * N, 8 * K * N * 4))
+    ypad = sc.empty_f32((M + 5, N, 4))
+    yv = qmm.Tensor(ypad.buf, qmm.F32, (M, N, 4), nb=(4, 4 * (M + 5), 4 * (M + 5) * N, 4 * (M + 5) * N * 4))
+    be.mul_mat(w, xv, yv)
+    be.synchronize()
+    assert be.last_path() == "gemv-fq"
+    got = be.get_f32(ypad).reshape(4, N, M + 5)[:, :, :M]
+    rb = synth.row_bytes(qtype, K) * M
+    for i2 in range(4):
+        assert rel_err(got[i2], orc.mul_mat(qtype, raw[(i2 // 2) * rb:(i2 // 2 + 1) * rb], M, K, x[i2, 0::2])) <= TOL
 
 
 @pytest.mark.parametrize("qtype", TYPES)

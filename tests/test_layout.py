@@ -245,13 +245,20 @@ def test_gemv_plan(qtype, K, M, N):
     mma = N >= 3 and qtype in (qmm.Q4_0, qmm.Q8_0, qmm.Q4_K, qmm.IQ4_XS, qmm.IQ4_NL, qmm.Q6_K)
     G, nt = -(-K // 256), -(-M // 64)
     if info["path"] == "gemv-fq":
-        # the fused-quantization kernel: 1-2 columns, one work-group per 64-row tile and task, K
-        # split among its (up to 16) waves only, enough waves to fill the chip; LDS holds each
+        # the fused-quantization kernel: 1-2 columns, work-groups of up to 16 waves per 64-row
+        # tile and task; K split among the waves and, for a small image (at most 16 MiB), over
+        # KS work-groups of 4 waves with one group each (the K-slice tree); LDS holds each
         # wave's quantized groups (320 B per group and column), then the waves' sums
-        W, spw, nc = info["k_waves"], info["groups_per_wave"], info["cols_per_task"]
-        assert N <= 2 and nc == N and info["k_slices"] == 1 and info["tasks"] == 1
-        assert 1 <= W <= 16 and W * spw >= G and (W - 1) * spw < G
-        assert info["workgroups"] == nt and info["threads"] == 64 * W
+        W, spw, nc, KS = info["k_waves"], info["groups_per_wave"], info["cols_per_task"], info["k_slices"]
+        assert N <= 2 and nc == N and info["tasks"] == 1
+        assert 1 <= W <= 16 and KS * W * spw >= G and (KS - 1) * W * spw < G
+        if KS == 1:
+            assert (W - 1) * spw < G
+        else:
+            image = nt * G * {qmm.Q4_0: 18, qmm.Q8_0: 34, qmm.Q4_K: 144, qmm.Q5_K: 176, qmm.Q6_K: 210,
+                              qmm.IQ4_XS: 136, qmm.IQ4_NL: 18}[qtype] * (8 if qtype in (qmm.Q4_0, qmm.Q8_0, qmm.IQ4_NL) else 1) * 64
+            assert image <= 16 << 20 and W == 4 and spw == 1
+        assert info["workgroups"] == nt * KS and info["threads"] == 64 * W
         assert info["lds_bytes"] == max(W * spw * nc * 320, W * 2 * nc * 64 * 4)
         return
     assert info["path"] == ("gemv-mfma" if mma else "gemv")
