@@ -21,11 +21,12 @@
 //    sums are added to dst (zeroed by the pre-pass) with float atomics - no
 //    device-scope fences, whose L2 write-backs would cost more than the whole
 //    product;
-//  * D stages of weight loads are in flight per wave in a register ring whose
-//    loads are unconditional, so every wait is for a known load; a slot
-//    refilled past the last stage reads a small L2-resident sink buffer
-//    instead (re-reading real weights would go back to HBM: the weight loads
-//    are non-temporal).
+//  * one stage of weight loads is in flight per wave (the v_dot4 kernels load
+//    nothing past their last stage); the MFMA kernel's two-buffer ring loads
+//    unconditionally, so every wait is for a known load, and a buffer refilled
+//    past the last stage reads a small L2-resident sink buffer instead
+//    (re-reading real weights would go back to HBM: the weight loads are
+//    non-temporal).
 // A task is up to NC activation columns against one weight matrix; dense
 // MUL_MAT derives tasks from the work-group index, MUL_MAT_ID reads
 // device-built task lists.
@@ -592,7 +593,10 @@ __global__ __launch_bounds__(512) void k_gemv(GemvParams p) {
                     }
                     T::dot(B[i], (s + i) % NST, x, nc, a, st_state);
                 }
-                load_stage(B[i], s + i + D);
+                // (no stage past the last: with one stage in flight nothing else is outstanding
+                // here, and 5440 waves re-reading one stage of the sink at their end cost the
+                // chip ~50 MB of L2 reads at once)
+                if (s + i + D < S) load_stage(B[i], s + i + D);
             }
         }
     };
@@ -1408,7 +1412,7 @@ __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
         }
         if (s < S) T::dot(B, sl % NST, x, nc, acc, st_state);
         else T::dot(B, sl % NST, x, nc, accu, st_state);
-        load_stage(s + 1);
+        if (s + 1 < ST) load_stage(s + 1);                        // (nothing past the last stage)
     }
     // the W waves added in a fixed order (with the GLU both sums, then act(gate) * up)
     const int64_t row = (int64_t)tile * kTileRows + lane;
@@ -1682,8 +1686,10 @@ bool stage_shape(int type, int * read_end, int * nst) {
 
 // The loads a GEMV launch makes, replayed on the host with the kernels' own index functions
 // (wg_pos, dense_task, dot4_stages / mma_groups, stage_group): every work-group and wave, its
-// stages 0 .. S - 1 from the image and the one stage S that the ring loads past its end from
-// the sink (both kernels keep one stage in flight, so stage S is loaded and never consumed).
+// stages 0 .. S - 1 from the image and, for the MFMA kernel, the one stage S that its
+// two-buffer ring loads past its end from the sink (loaded and never consumed).  The v_dot4
+// kernels load no stage past their last; a wave of the fused kernel without groups (the last
+// K slice of a split plan) loads one stage of the sink, which is not counted here.
 bool gemv_extent(int type, const WView & w, const GemvPlan & pl, const GemvDense * dense, int64_t nmat, int list_mat,
                  GemvExtent * e) {
     int rend, nst;
@@ -1706,8 +1712,10 @@ bool gemv_extent(int type, const WView & w, const GemvPlan & pl, const GemvDense
             e->real_hi = std::max(e->real_hi, off + rend);
             e->real_loads++;
         }
-        e->sink_hi = std::max<int64_t>(e->sink_hi, rend);         // stage S: the sink, at its base
-        e->sink_loads++;
+        if (pl.mma) {                                             // stage S: the sink, at its base
+            e->sink_hi = std::max<int64_t>(e->sink_hi, rend);
+            e->sink_loads++;
+        }
         if (rend > (int64_t)kSinkBytes) e->bad++;
     };
     for (int64_t b = 0; b < nwg; ++b) {

@@ -928,21 +928,24 @@ static int64_t fused_small_tgroups() {
 }
 
 // Dense products of 1-2 columns may also split K over work-groups of the fused kernel (its
-// K-slice tree): one launch instead of the pre-pass and the GEMV, which wins where the image is
-// small enough for the pre-pass to be a large part of the op (Q4_0 4096 x 4096, 9.4 MB, N = 1:
-// 7.0-8.9 -> 6.2-6.3 us) and loses on larger ones, where the wave's own quantization costs more
-// than the launch it saves (Q4_K 17408 x 5120: 12.5 -> 13.9 us; Q6_K 5120 x 17408 16.5 -> 18.1;
-// Q8_0 14336 x 4096 14.3 -> 15.5).  Taken up to QMM_GEMV_FQS_MAX_KB of one matrix's image
-// (16 MiB); QMM_GEMV_FQS = 0 never, = 1 at any size; work-groups of QMM_GEMV_FQS_W waves (4,
-// the best of 1, 2, 4, 5 and 10 on config 2's Q4_K) with QMM_GEMV_FQS_SPW groups each (1).
+// K-slice tree): one launch instead of the pre-pass and the GEMV.  Measured per op (bench,
+// one box): one column of every type but Q6_K gains (config 2's Q4_K 17408 x 5120 12.6 ->
+// 11.6 us, Q5_K 14.7 -> 13.8, config 4's Q8_0 14.3 -> 13.9, Q4_0 4096 x 4096 7.0-8.9 -> 6.0; the
+// IQ4 types within 1 %); Q6_K (two stages a group) loses 2-3 % (16.4 -> 16.8 us, the output head
+// 100.0 -> 101.9) and so do two columns on large images (Q8_0 14336 x 4096 15.3 -> 15.7, IQ4_XS
+// 13.0-13.5 -> 14.2).  So: one column of any type but Q6_K, and 1-2 columns of any type for
+// images up to QMM_GEMV_FQS_MAX_KB (16 MiB) of one matrix; QMM_GEMV_FQS = 0 never, = 1 always;
+// work-groups of QMM_GEMV_FQS_W waves (4: 11.6 us on the Q4_K against 12.2-12.3 at 2, 5 and 8)
+// with QMM_GEMV_FQS_SPW groups each (1).
 static int env_or(const char * name, int dflt) {
     const char * e = getenv(name);
     return e ? atoi(e) : dflt;
 }
-static bool fused_split_for(const WView & w) {
+static bool fused_split_for(int type, const WView & w, int64_t N) {
     const int mode = env_or("QMM_GEMV_FQS", -1);
     if (mode == 0) return false;
     if (mode > 0) return true;
+    if (N == 1 && type != QMM_TYPE_Q6_K) return true;
     const int64_t image = w.ntiles * w.G * (int64_t)w.tg;
     return image <= (int64_t)env_or("QMM_GEMV_FQS_MAX_KB", 16384) * 1024;
 }
@@ -956,7 +959,7 @@ static bool fused_dense_plan(int type, const WView & w, int64_t N, int64_t nbatc
         if (w.G <= 8 && tgroups <= fused_small_tgroups()) return true;
         if (fp->ntasks * w.ntiles * fp->W >= fused_min_waves()) return true;
     }
-    return split && fused_split_for(w) &&
+    return split && fused_split_for(type, w, N) &&
            gemv_fused_split_plan(type, w, (int)N, nbatch, env_or("QMM_GEMV_FQS_W", 4), env_or("QMM_GEMV_FQS_SPW", 1), fp);
 }
 // whether a MUL_MAT_ID of T tokens with n_used ids each takes the fused GEMV's pairs, and its plan

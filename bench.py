@@ -495,22 +495,30 @@ def main():
         value = algo * args.steps / wall / 1e9
         k_ms = kernel_ms(kd, km, wall * 1e3 / args.steps)
         achieved = algo / (k_ms * 1e-3) / 1e9
-        traffic = profile_traffic("q4k_gemv")
+        # one launch (the fused kernel quantizes its own activations, K over 4-wave work-groups)
+        # or the q8_K pre-pass and the GEMV
+        fused = path == "gemv-fq"
+        tag = "q4k_gemv_fq" if fused else "q4k_gemv"
+        prof = "profiles/k_gemv_fq_q4k_17408x5120_n1.md" if fused else "profiles/k_gemv_q4k_17408x5120_n1.md"
+        kname = ("k_gemv_fq<12, 1> (Q4_K, 1 column, K split over 4-wave work-groups, activations quantized "
+                 "in the kernel)" if fused else "k_gemv<12, 1> (Q4_K, 1 column)")
+        op_desc = "MUL_MAT in one launch" if fused else "MUL_MAT incl. q8_K pre-pass"
+        traffic = profile_traffic(tag)
         out.update({
             "metric": "Q4_K GEMV GB/s (% of 8 TB/s) at N=1; Q4_0 GEMM TOPS (% MFMA peak) at N=512",
             "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": round(wall * 1e3 / args.steps, 5), "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": "int8", "data": "synthetic",
-            "config": {"workload": "Q4_K GEMV 17408x5120 N=1 (config 2 ffn gate/up), MUL_MAT incl. q8_K pre-pass",
+            "config": {"workload": f"Q4_K GEMV 17408x5120 N=1 (config 2 ffn gate/up), {op_desc}",
                        "weights": "Q4_K", "M": M, "K": K, "N": N, "weight_copies": len(ws),
                        "rotated_bytes": int(len(ws) * raw.nbytes), "path": path,
                        "device_ms_per_step": round(dev_ms / args.steps, 5)},
             "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                         "traffic_source": "profiles/traffic.json: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of this "
-                                           "kernel (profiles/k_gemv_q4k_17408x5120_n1.md), scaled by the copy kernel's "
-                                           "counts; not measured in this run",
-                         "kernel": "k_gemv<12, 1> (Q4_K, 1 column)", "kernel_us": round(k_ms * 1e3, 3),
+                         "traffic_source": f"profiles/traffic.json: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of this "
+                                           f"kernel ({prof}), scaled by the copy kernel's counts; not measured in "
+                                           "this run",
+                         "kernel": kname, "kernel_us": round(k_ms * 1e3, 3),
                          "kernel_us_markers": round(km * 1e3, 3), "kernel_us_stat": f"median of {args.steps} launches",
                          "algorithmic_bytes": int(algo)},
         })
@@ -519,8 +527,9 @@ def main():
         g_us = graph_replay_us(be, [lambda w=w: be.mul_mat(w, xt, yt) for w in ws * 4], args.steps, args.warmup)
         out["graph"] = {"us_per_op": round(g_us, 3), "GBs": round(algo / (g_us * 1e-6) / 1e9, 1),
                         "frac_hbm": round(algo / (g_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                        "note": f"{4 * len(ws)} MUL_MATs (q8_K pre-pass + GEMV, the weight copies in turn) captured "
-                                "in one HIP graph and replayed (qmm_graph_launch); value is the eager op"}
+                        "note": f"{4 * len(ws)} MUL_MATs ({'one launch each' if fused else 'q8_K pre-pass + GEMV'}, "
+                                "the weight copies in turn) captured in one HIP graph and replayed (qmm_graph_launch); "
+                                "value is the eager op"}
         if not args.no_cpu:
             import oracle
             out["cpu_baseline"] = cpu_baseline(oracle, qmm.Q4_K, raw, M, K, x, args.cpu_seconds)

@@ -4,10 +4,11 @@ sink, at every config shape and column count that runs on the GEMV.
 The library replays a launch's loads on the host (qmm_internal_gemv_extent, declared in
 arcint_amd/csrc/qmm_internal.h): it plans the launch as qmm_mul_mat / qmm_mul_mat_id do and
 walks every work-group, wave and stage with the kernels' own index functions, including the
-one stage per wave that the register ring loads past its last one (from the sink).  Checked
-here: no load outside [0, image bytes) of the matrices it may address, none past the sink,
-every (task, tile, group) of the product loaded exactly once (the plan covers K and the rows
-with no gap or overlap), and one sink load per wave that streams anything."""
+one stage per wave that the MFMA kernel's register ring loads past its last one (from the
+sink; the v_dot4 kernels load none).  Checked here: no load outside [0, image bytes) of the
+matrices it may address, none past the sink, every (task, tile, group) of the product loaded
+exactly once (the plan covers K and the rows with no gap or overlap), and at most one sink
+load per wave that streams anything."""
 import ctypes as C
 
 import numpy as np
@@ -52,7 +53,7 @@ def check(e, tasks_times_tiles_groups=None):
     assert e["bad"] == 0, e
     assert 0 <= e["real_lo"] and e["real_hi"] <= e["image_bytes"], e
     assert e["sink_hi"] <= SINK_BYTES, e
-    assert e["sink_loads"] >= 1 and e["real_loads"] >= e["sink_loads"], e
+    assert e["real_loads"] >= 1 and e["real_loads"] >= e["sink_loads"], e
     if tasks_times_tiles_groups:
         nst, r = divmod(e["real_loads"], tasks_times_tiles_groups)
         assert r == 0 and nst in (1, 2), (e, tasks_times_tiles_groups)
