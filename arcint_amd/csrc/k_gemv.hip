@@ -24,9 +24,9 @@
 //  * one stage of weight loads is in flight per wave (the v_dot4 kernels load
 //    nothing past their last stage); the MFMA kernel's two-buffer ring loads
 //    unconditionally, so every wait is for a known load, and a buffer refilled
-//    past the last stage reads a small L2-resident sink buffer instead
-//    (re-reading real weights would go back to HBM: the weight loads are
-//    non-temporal).
+//    past the last stage reads a small L2-resident sink buffer instead, all
+//    lanes at one address (re-reading real weights would go back to HBM: the
+//    weight loads are non-temporal).
 // A task is up to NC activation columns against one weight matrix; dense
 // MUL_MAT derives tasks from the work-group index, MUL_MAT_ID reads
 // device-built task lists.
@@ -1009,9 +1009,11 @@ __device__ __forceinline__ void gemv_mma_body(const GemvParams & p) {
     const uint8_t * tbase = mat_tile(p, mat, tile < ntl ? tile : 0, sec);   // the up tile after the gate (GLU)
     const size_t tgs = (size_t)p.w.tg;
     const bool glu = CM == 8 && p.glu >= 0;                       // uniform (lists: 8-column tasks only)
-    auto load_stage = [&](uint4 (&b)[NL], int s) {                // past the last stage: the sink
+    // past the last stage: the sink, every lane at lane 0's address (one line per load
+    // instruction instead of 16; the loads stay unconditional, so every wait counts both buffers)
+    auto load_stage = [&](uint4 (&b)[NL], int s) {
         const bool real = s < S;
-        T::load(b, real ? tbase + (size_t)stage_group(ga, s, NST) * tgs : p.sink, real ? s % NST : 0, lane);
+        T::load(b, real ? tbase + (size_t)stage_group(ga, s, NST) * tgs : p.sink, real ? s % NST : 0, real ? lane : 0);
     };
     // the first stage's weights are requested before the activations are staged
     uint4 b0[NL], b1[NL];
