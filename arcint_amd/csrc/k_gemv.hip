@@ -1188,7 +1188,7 @@ int env_int(const char * name, int dflt) {
 // matrices on 256 CUs, 16 of which then stream twice): the work-groups' sums meet in a
 // pairwise tree of exchanges (tree_add) and the last arrival stores the row.  The same kernel
 // takes:
-//  * dense MUL_MAT at 1 or 2 columns per task, K split over KS >= 1 work-groups (no GLU);
+//  * dense MUL_MAT at 1 or 2 columns per task, K split over KS >= 1 work-groups;
 //  * MUL_MAT_ID at small batches with no route: task p is the (token, slot) pair p and reads its
 //    expert id itself (the reference's per-pair matvec below 16 tokens, P01:1189-1192 and
 //    P01:1222-1248); a negative id writes a zero row, an id past the stack too and sets the
@@ -1227,7 +1227,7 @@ struct FqParams {
     int glu;
     int W, spw;
     int KS;                      // dense: work-groups per tile along K (grid z)
-    uint32_t * tree;             // KS > 1: slots [task][tile][2 KS nodes][NC][64], each kTreeEmpty
+    uint32_t * tree;             // KS > 1: slots [task][tile][2 KS nodes][NC][64] (64-bit pairs with the GLU)
 };
 
 // The K slices of a tile add their sums v[j] (column j, this lane's row) up a pairwise tree
@@ -1255,6 +1255,39 @@ __device__ __forceinline__ void tree_add(uint32_t * nodes, int ks, int KS, int n
                     } else {
                         v[j] += __uint_as_float(o);
                         __hip_atomic_store(s, kTreeEmpty, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
+                }
+            }
+        }
+        off += (n + 1) >> 1;
+        i >>= 1;
+        n = (n + 1) >> 1;
+    }
+}
+
+// The same tree for a gate sum a[j] and an up sum b[j] (the GLU applied at the root): the pair
+// travels as one 64-bit exchange (gate in the low word), so both meet the same partner at every
+// node and the root holds both totals.  A gate sum is never the sentinel, so the low word says
+// whether the slot was empty.
+template <int NC>
+__device__ __forceinline__ void tree_add_pairs(uint64_t * nodes, int ks, int KS, int nc, float (&a)[NC], float (&b)[NC],
+                                               bool (&alive)[NC], int lane) {
+    constexpr uint64_t kEmpty2 = ((uint64_t)kTreeEmpty << 32) | kTreeEmpty;
+    uint32_t i = (uint32_t)ks, n = (uint32_t)KS, off = 0;
+    while (n > 1) {                                               // uniform
+        if ((i ^ 1u) < n) {
+#pragma unroll
+            for (int j = 0; j < NC; ++j) {
+                if (j < nc && alive[j]) {
+                    uint64_t * s = nodes + ((size_t)(off + (i >> 1)) * NC + j) * 64 + lane;
+                    const uint64_t mine = (uint64_t)__float_as_uint(a[j]) | ((uint64_t)__float_as_uint(b[j]) << 32);
+                    const uint64_t o = __hip_atomic_exchange(s, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if ((uint32_t)o == kTreeEmpty) {
+                        alive[j] = false;
+                    } else {
+                        a[j] += __uint_as_float((uint32_t)o);
+                        b[j] += __uint_as_float((uint32_t)(o >> 32));
+                        __hip_atomic_store(s, kEmpty2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     }
                 }
             }
@@ -1416,9 +1449,10 @@ __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
         else T::dot(B, sl % NST, x, nc, accu, st_state);
         if (s + 1 < ST) load_stage(s + 1);                        // (nothing past the last stage)
     }
-    // the W waves added in a fixed order (with the GLU both sums, then act(gate) * up)
+    // the W waves added in a fixed order: the gate (or only) sums tot[], with the GLU the up sums
+    // totu[]; act(gate) * up once the K slices have met
     const int64_t row = (int64_t)tile * kTileRows + lane;
-    float tot[NC];
+    float tot[NC], totu[NC];
     if (p.W > 1) {
         const int NV = glu ? 2 * NC : NC;
         float * red = reinterpret_cast<float *>(sm);
@@ -1433,29 +1467,34 @@ __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
         if (wave != 0) return;
 #pragma unroll
         for (int j = 0; j < NC; ++j) {
-            float v = red[j * 64 + lane];
+            float v = red[j * 64 + lane], u = 0.0f;
             for (int ww = 1; ww < p.W; ++ww) v += red[(ww * NV + j) * 64 + lane];
             if (glu) {
-                float u = red[(NC + j) * 64 + lane];
+                u = red[(NC + j) * 64 + lane];
                 for (int ww = 1; ww < p.W; ++ww) u += red[(ww * NV + NC + j) * 64 + lane];
-                v = glu_apply(p.glu, v, u);
             }
             tot[j] = v;
+            totu[j] = u;
         }
     } else {
 #pragma unroll
-        for (int j = 0; j < NC; ++j) tot[j] = glu ? glu_apply(p.glu, acc[j], accu[j]) : acc[j];
+        for (int j = 0; j < NC; ++j) {
+            tot[j] = acc[j];
+            totu[j] = accu[j];
+        }
     }
     bool alive[NC];
 #pragma unroll
     for (int j = 0; j < NC; ++j) alive[j] = true;
-    if (p.KS > 1)                                                 // uniform (dense, no GLU)
-        tree_add<NC>(p.tree + ((size_t)task * (size_t)p.w.ntiles + tile) * (2 * (size_t)p.KS * NC * 64), ks, p.KS, nc,
-                     tot, alive, lane);
+    if (p.KS > 1) {                                               // uniform (dense)
+        uint32_t * nodes = p.tree + ((size_t)task * (size_t)p.w.ntiles + tile) * (2 * (size_t)p.KS * NC * 64) * (glu ? 2 : 1);
+        if (glu) tree_add_pairs<NC>(reinterpret_cast<uint64_t *>(nodes), ks, p.KS, nc, tot, totu, alive, lane);
+        else tree_add<NC>(nodes, ks, p.KS, nc, tot, alive, lane);
+    }
     if (row >= p.w.M) return;
 #pragma unroll
     for (int j = 0; j < NC; ++j)
-        if (j < nc && alive[j]) p.dst[doffv[j] + row] = tot[j];
+        if (j < nc && alive[j]) p.dst[doffv[j] + row] = glu ? glu_apply(p.glu, tot[j], totu[j]) : tot[j];
 }
 
 }  // namespace
@@ -1493,8 +1532,8 @@ bool gemv_fused_split_plan(int type, const WView & w, int nc, int64_t ntasks, in
     return pl->lds <= 64 * 1024 && ntasks * w.ntiles < 0x7fffffff;
 }
 
-int64_t gemv_fused_tree_words(const WView & w, const FusedPlan & pl) {
-    return pl.KS > 1 ? pl.ntasks * w.ntiles * 2 * pl.KS * pl.nc * 64 : 0;
+int64_t gemv_fused_tree_words(const WView & w, const FusedPlan & pl, bool glu) {
+    return pl.KS > 1 ? pl.ntasks * w.ntiles * 2 * pl.KS * pl.nc * 64 * (glu ? 2 : 1) : 0;
 }
 
 int gemv_fused_waves_target() { return std::max(1, env_int("QMM_GEMV_FQ_WAVES", 4096)); }
@@ -1504,7 +1543,7 @@ hipError_t launch_gemv_fused(int type, const WView & w, const FusedPlan & pl, co
     if (!sink || !dst || pl.W < 1 || pl.W > kFqMaxWaves || pl.spw < 1 || pl.nc < 1 || pl.nc > 2 || pl.KS < 1 ||
         pl.KS > 65535 || (int64_t)pl.KS * pl.W * pl.spw < w.G ||
         (pl.KS == 1 ? (int64_t)(pl.W - 1) * pl.spw >= w.G : (int64_t)(pl.KS - 1) * pl.W * pl.spw >= w.G) ||
-        (pl.KS > 1 && (f.ids || f.glu >= 0 || !f.tree)) || f.K != w.K ||
+        (pl.KS > 1 && (f.ids || !f.tree || ((uintptr_t)f.tree & 7))) || f.K != w.K ||
         (f.ids && (pl.nc != 1 || f.n_used < 1 || pl.ntasks != f.n_used * f.T || !f.bad_id)) ||
         (f.glu > QMM_GLU_GEGLU_QUICK) || (f.glu >= 0 && !f.base2))
         return hipErrorInvalidValue;

@@ -951,7 +951,7 @@ static bool fused_split_for(int type, const WView & w, int64_t N) {
 }
 
 // whether a dense product of N columns in nbatch batches takes the fused GEMV, and its plan;
-// split: K may be split over work-groups (not for a GLU, nor where nothing may be allocated)
+// split: K may be split over work-groups (not where nothing may be allocated)
 static bool fused_dense_plan(int type, const WView & w, int64_t N, int64_t nbatch, FusedPlan * fp, bool split) {
     if (!fused_on() || N > 2 || N < 1) return false;
     if (gemv_fused_plan(type, w, (int)N, nbatch, gemv_fused_waves_target(), fp)) {
@@ -1037,10 +1037,10 @@ int qmm_describe_mul_mat(const qmm_tensor * src0, const qmm_tensor * src1, const
 static bool try_fused_dense(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1, const WView & w,
                             const GemvDense & dn, float * d, const uint8_t * up_base, int glu, bool noalloc, int * rc) {
     FusedPlan fp;
-    if (!fused_dense_plan(src0->type, w, src1->ne[1], dn.ne12 * dn.ne13, &fp, glu < 0 && !noalloc)) return false;
+    if (!fused_dense_plan(src0->type, w, src1->ne[1], dn.ne12 * dn.ne13, &fp, !noalloc)) return false;
     FusedGemv f{};
     if (fp.KS > 1) {
-        if ((*rc = ensure_tree(ctx, (size_t)gemv_fused_tree_words(w, fp)))) return true;
+        if ((*rc = ensure_tree(ctx, (size_t)gemv_fused_tree_words(w, fp, glu >= 0)))) return true;
         f.tree = ctx->tree;
     }
     f.x = f32_cols(src1);

@@ -256,8 +256,8 @@ hipError_t launch_gemv(int type, const WView & w, const GemvPlan & plan, const A
                        hipStream_t s, const KTime * kt = nullptr, const GemvPair * pair = nullptr);
 
 // The v_dot4 GEMV with its own activation quantization (k_gemv_fq): no pre-pass, K split
-// among the W waves of a work-group (at most 16) and, for dense products without a GLU, over
-// KS work-groups per tile whose sums meet in a tree of exchanges (tree slots below); every
+// among the W waves of a work-group (at most 16) and, for dense products, over KS
+// work-groups per tile whose sums meet in a tree of exchanges (tree slots below); every
 // output is stored once.  nc = columns per task (1 or 2).  Dense tasks as GemvDense; with ids,
 // task p is the MUL_MAT_ID pair p = t n_used + i (nc = 1).  glu >= 0: the work-group streams w
 // (gate) then base2 (up) and stores act(gate) * up.
@@ -275,7 +275,7 @@ struct FusedGemv {
 };
 struct FusedPlan {
     int nc, W, spw;
-    int KS = 1;                 // work-groups per tile along K (dense, no GLU)
+    int KS = 1;                 // work-groups per tile along K (dense)
     int64_t ntasks;
     int64_t lds;
 };
@@ -288,8 +288,8 @@ bool gemv_fused_plan(int type, const WView & w, int nc, int64_t ntasks, int targ
 // dense products split along K: work-groups of W waves with spw groups per wave, KS =
 // ceil(G / (W spw)) >= 2 of them per tile; false when that gives one slice or does not fit
 bool gemv_fused_split_plan(int type, const WView & w, int nc, int64_t ntasks, int W, int spw, FusedPlan * plan);
-// tree slots (32-bit words) a split plan needs
-int64_t gemv_fused_tree_words(const WView & w, const FusedPlan & plan);
+// tree slots (32-bit words) a split plan needs (glu: gate and up sums travel as one 64-bit pair)
+int64_t gemv_fused_tree_words(const WView & w, const FusedPlan & plan, bool glu);
 int gemv_fused_waves_target();
 hipError_t launch_gemv_fused(int type, const WView & w, const FusedPlan & plan, const FusedGemv & f, float * dst,
                              const void * sink, hipStream_t s, const KTime * kt = nullptr);

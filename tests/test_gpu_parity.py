@@ -976,6 +976,35 @@ def test_mul_mat_glu_split_paths(be, sc, orc, monkeypatch):
     assert rel_err(got, ref) <= TOL
 
 
+@pytest.mark.parametrize("qtype", [qmm.Q4_K, qmm.Q4_0, qmm.Q6_K, qmm.IQ4_XS, qmm.Q8_0])
+@pytest.mark.parametrize("N,W", [(1, 4), (2, 3), (1, 1)])
+def test_mul_mat_glu_split_tree(be, sc, orc, monkeypatch, qtype, N, W):
+    """gate/up + GLU in one launch with K split over work-groups: each slice streams its gate and
+    up groups, the slices' (gate, up) pairs meet in the exchange tree as one 64-bit exchange and
+    the last arrival applies the GLU (K = 5120: 20 groups, slices of 4, 3 and 1 groups); two
+    calls in a row on one context (the slots empty again after each)"""
+    monkeypatch.setenv("QMM_GEMV_FQS", "1")
+    monkeypatch.setenv("QMM_GEMV_FQS_W", str(W))
+    monkeypatch.setenv("QMM_GEMV_FQ_SMALL_TG", "0")
+    for seed in (141, 151):
+        say("glu split tree", qtype, N, W, seed)
+        got, ref = glu_case(be, sc, orc, qtype, qtype, 130, 5120, N, qmm.GLU_SWIGLU, seed=seed)
+        assert be.last_path() == "glu-fused-gemv-fq"
+        assert rel_err(got, ref) <= TOL, seed
+
+
+@pytest.mark.parametrize("op", GLU_OPS)
+def test_mul_mat_glu_split_tree_ops_batches(be, sc, orc, monkeypatch, op):
+    """every GLU applied at the tree's root, over broadcast batches"""
+    monkeypatch.setenv("QMM_GEMV_FQS", "1")
+    monkeypatch.setenv("QMM_GEMV_FQS_W", "2")
+    monkeypatch.setenv("QMM_GEMV_FQ_SMALL_TG", "0")
+    say("glu split tree op", op)
+    got, ref = glu_case(be, sc, orc, qmm.Q4_K, qmm.Q4_K, 200, 1536, 2, op, seed=161, batches=(3, 2))
+    assert be.last_path() == "glu-fused-gemv-fq"
+    assert rel_err(got, ref) <= TOL
+
+
 def test_mul_mat_glu_full_size_decode(be, sc, orc):
     """config 2's FFN gate/up (17408 x 5120 Q4_K) at N = 1"""
     say("glu-full")
