@@ -953,7 +953,14 @@ static bool fused_split_for(int type, const WView & w, int64_t N) {
 // whether a dense product of N columns in nbatch batches takes the fused GEMV, and its plan;
 // split: K may be split over work-groups (not where nothing may be allocated)
 static bool fused_dense_plan(int type, const WView & w, int64_t N, int64_t nbatch, FusedPlan * fp, bool split) {
-    if (!fused_on() || N > 2 || N < 1) return false;
+    if (!fused_on() || N < 1) return false;
+    if (N > 2) {
+        // 3-16 columns as 2-column tasks, on small products only (the bound above), where the
+        // launches are the op: config 3's shared expert at T = 4 (Q4_K 512 x 2048 gate + up +
+        // SwiGLU, 2048 x 512 down) ran as pre-pass + MFMA GEMV (+ GLU kernel), five launches
+        if (N > 16 || !gemv_fused_plan(type, w, 2, (N + 1) / 2 * nbatch, gemv_fused_waves_target(), fp)) return false;
+        return w.G <= 8 && fp->ntasks * w.ntiles * w.G <= fused_small_tgroups();
+    }
     if (gemv_fused_plan(type, w, (int)N, nbatch, gemv_fused_waves_target(), fp)) {
         const int64_t tgroups = fp->ntasks * w.ntiles * w.G;
         if (w.G <= 8 && tgroups <= fused_small_tgroups()) return true;

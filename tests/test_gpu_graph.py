@@ -191,12 +191,12 @@ def test_graph_replay_mul_mat(be, orc, bufs, qtype, M, K, N):
 
 
 def test_capture_refuses_allocation(orc):
-    """a fresh context has no scratch: the captured op (three columns: the pre-pass's
-    activations go to the scratch) fails, capture_end reports it, and the stream runs the same
-    op eagerly afterwards"""
+    """a fresh context has no scratch: the captured op (three columns over 16 groups along K:
+    the pre-pass path, whose activations go to the scratch) fails, capture_end reports it, and
+    the stream runs the same op eagerly afterwards"""
     say("graph capture needs scratch")
     with qmm.Backend(0) as b:
-        qtype, M, K, N = qmm.Q4_K, 256, 1024, 3
+        qtype, M, K, N = qmm.Q4_K, 256, 4096, 3
         raw = synth.weights(qtype, M, K, 820)
         x = synth.activations(N, K, 821)
         w = b.new_tensor(qtype, (K, M))

@@ -479,8 +479,10 @@ def test_mul_mat_many_columns(be, sc, orc, qtype, N):
 @pytest.mark.parametrize("N", [9, 12, 16, 17, 24, 31, 32, 40, 64, 100])
 def test_mfma_gemv_wide_tasks(be, sc, orc, monkeypatch, qtype, N):
     """the MFMA GEMV with 9..32 columns per weight pass (the 16- and 32-column kernels; 40 and
-    up in even passes), forced off the GEMM"""
+    up in even passes), forced off the GEMM and off the fused kernel (which takes small products
+    to 16 columns)"""
     monkeypatch.setenv("QMM_GEMM_MIN_COLS", "100000")
+    monkeypatch.setenv("QMM_GEMV_FQ_SMALL_TG", "0")
     M, K = 300, 1024
     say("gemv-wide", qtype, M, K, N)
     got, ref = run_mul_mat(be, sc, orc, qtype, M, K, N, seed=54)
@@ -491,6 +493,7 @@ def test_mfma_gemv_wide_tasks(be, sc, orc, monkeypatch, qtype, N):
 @pytest.mark.parametrize("qtype", [qmm.Q4_K, qmm.Q4_0])
 def test_mfma_gemv_wide_broadcast_and_strides(be, sc, orc, monkeypatch, qtype):
     monkeypatch.setenv("QMM_GEMM_MIN_COLS", "100000")
+    monkeypatch.setenv("QMM_GEMV_FQ_SMALL_TG", "0")
     say("gemv-wide-broadcast", qtype)
     K, M, N = 512, 80, 21
     raw = synth.weights(qtype, 2 * M, K, seed=66)
@@ -1177,10 +1180,13 @@ def test_mul_mat_id_glu_per_slot_src1(be, sc, orc):
     assert rel_err(got, ref) <= TOL
 
 
-def test_downgrade_keys(sc, orc):
+def test_downgrade_keys(sc, orc, monkeypatch):
     """the downgrade export counts per key: Q5_K at 4 columns runs on the v_dot4 GEMV (no MFMA
     form), Q4_K at 40 columns takes two weight passes on the MFMA GEMV; a product on its
-    promised path adds nothing"""
+    promised path adds nothing (the fused kernel, which takes these small products at 1-16
+    columns, switched off)"""
+    monkeypatch.setenv("QMM_GEMV_FQ_SMALL_TG", "0")
+    monkeypatch.setenv("QMM_GEMV_FQS", "0")
     say("downgrades")
     with qmm.Backend(0) as b2:
         bufs = []
@@ -1284,6 +1290,37 @@ def test_fused_gemv_split(be, sc, orc, monkeypatch, qtype, M, K, N, W):
         assert be.last_path() == "gemv-fq"
         assert qmm.describe_mul_mat(w, xt, y)["k_slices"] == -(-G // W)
         assert rel_err(be.get_f32(y).reshape(N, M), orc.mul_mat(qtype, raw, M, K, x)) <= TOL, seed
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("N", [3, 5, 8, 12])
+def test_fused_gemv_small_many_columns(be, sc, orc, qtype, N):
+    """small products (8 groups along K, 5 tiles) of 3-16 columns take the fused kernel as
+    2-column tasks (one launch instead of the pre-pass and the MFMA GEMV; Q5_K's GEMM, which
+    MUL_MAT picks first, starts at 16 columns)"""
+    say("fused small many columns", qtype, N)
+    got, ref = run_mul_mat(be, sc, orc, qtype, 300, 2048, N, seed=221)
+    assert be.last_path() == "gemv-fq"
+    assert rel_err(got, ref) <= TOL
+
+
+def test_fused_gemv_small_many_columns_batches(be, sc, orc):
+    """5 columns (2-column tasks, the last with one) over broadcast batches: two matrices, four
+    batches"""
+    say("fused small many columns batches")
+    qtype, K, M, N = qmm.Q4_K, 512, 80, 5
+    raw = synth.weights(qtype, 2 * M, K, seed=222)
+    w = sc.weights(qtype, raw, (K, M, 2))
+    x = synth.activations(4 * N, K, seed=223).reshape(4, N, K)
+    xt = sc.f32(x)
+    y = sc.empty_f32((M, N, 4))
+    be.mul_mat(w, xt, y)
+    be.synchronize()
+    assert be.last_path() == "gemv-fq"
+    got = be.get_f32(y).reshape(4, N, M)
+    rb = synth.row_bytes(qtype, K) * M
+    for i2 in range(4):
+        assert rel_err(got[i2], orc.mul_mat(qtype, raw[(i2 // 2) * rb:(i2 // 2 + 1) * rb], M, K, x[i2])) <= TOL
 
 
 @pytest.mark.parametrize("qtype", [qmm.Q4_K, qmm.Q4_0, qmm.Q6_K])

@@ -251,7 +251,10 @@ def test_gemv_plan(qtype, K, M, N):
         # (the K-slice tree); LDS holds each wave's quantized groups (320 B per group and
         # column), then the waves' sums
         W, spw, nc, KS = info["k_waves"], info["groups_per_wave"], info["cols_per_task"], info["k_slices"]
-        assert N <= 2 and nc == N and info["tasks"] == 1
+        # (3-16 columns as 2-column tasks on small products: at most 8 groups, 512 tile-groups)
+        assert nc == min(N, 2) and info["tasks"] == -(-N // 2) and N <= 16
+        if N > 2:
+            assert G <= 8 and info["tasks"] * nt * G <= 512 and KS == 1
         assert 1 <= W <= 16 and KS * W * spw >= G and (KS - 1) * W * spw < G
         if KS == 1:
             assert (W - 1) * spw < G
@@ -260,7 +263,7 @@ def test_gemv_plan(qtype, K, M, N):
                               qmm.IQ4_XS: 136, qmm.IQ4_NL: 18}[qtype] * (8 if qtype in (qmm.Q4_0, qmm.Q8_0, qmm.IQ4_NL) else 1) * 64
             assert (N == 1 and qtype != qmm.Q6_K) or image <= 16 << 20
             assert W == 4 and spw == 1
-        assert info["workgroups"] == nt * KS and info["threads"] == 64 * W
+        assert info["workgroups"] == info["tasks"] * nt * KS and info["threads"] == 64 * W
         assert info["lds_bytes"] == max(W * spw * nc * 320, W * 2 * nc * 64 * 4)
         return
     assert info["path"] == ("gemv-mfma" if mma else "gemv")
