@@ -95,6 +95,9 @@ struct qmm_ctx {
     // no timing events meanwhile; a failure while capturing makes qmm_capture_end fail
     bool capturing = false;
     bool capture_failed = false;
+    // bumped whenever a scratch buffer the kernels read is freed for a larger one: a graph
+    // captured before then points at freed memory and is refused (qmm_graph_launch)
+    uint64_t scratch_gen = 0;
     int capture_code = 0;          // the first failure while capturing, and its reason
     std::string capture_err;
 };
@@ -104,6 +107,8 @@ struct qmm_graph {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     int device = 0;
+    const qmm_ctx * ctx = nullptr;   // the context captured from, and its scratch generation then
+    uint64_t scratch_gen = 0;
 };
 
 namespace {
@@ -261,6 +266,7 @@ int ensure(qmm_ctx * ctx, void ** p, size_t * cap, size_t need) {
         *p = nullptr;
         *cap = 0;
         ctx->key.valid = false;
+        ctx->scratch_gen++;
     }
     size_t sz = std::max(need, (size_t)(*cap * 3 / 2));
     QMM_HIP(ctx, hipMalloc(p, sz));
@@ -280,6 +286,7 @@ int ensure_tree(qmm_ctx * ctx, size_t words) {
         QMM_HIP(ctx, hipFree(ctx->tree));
         ctx->tree = nullptr;
         ctx->tree_words = 0;
+        ctx->scratch_gen++;
     }
     const size_t n = std::max(words, ctx->tree_words * 3 / 2);
     QMM_HIP(ctx, hipMalloc((void **)&ctx->tree, n * 4));
@@ -1874,6 +1881,8 @@ int qmm_capture_end(qmm_ctx * ctx, qmm_graph ** out) {
     qmm_graph * r = new qmm_graph();
     r->graph = g;
     r->device = ctx->device;
+    r->ctx = ctx;
+    r->scratch_gen = ctx->scratch_gen;
     const hipError_t ei = hipGraphInstantiate(&r->exec, g, nullptr, nullptr, 0);
     if (ei != hipSuccess) {
         (void)hipGraphDestroy(g);
@@ -1888,6 +1897,10 @@ int qmm_graph_launch(qmm_ctx * ctx, const qmm_graph * graph) {
     if (!ctx || !graph) return QMM_ERR_INVALID;
     if (ctx->capturing) return fail(ctx, QMM_ERR_INVALID, "graph_launch: not while capturing");
     if (graph->device != ctx->device) return fail(ctx, QMM_ERR_INVALID, "graph_launch: the graph is of another device");
+    if (graph->ctx != ctx) return fail(ctx, QMM_ERR_INVALID, "graph_launch: the graph was captured on another context");
+    if (graph->scratch_gen != ctx->scratch_gen)
+        return fail(ctx, QMM_ERR_INVALID, "graph_launch: an op outside the graph grew the context's scratch after the "
+                                          "capture, so the graph's buffers are gone; capture again");
     QMM_HIP(ctx, hipSetDevice(ctx->device));
     QMM_HIP(ctx, hipGraphLaunch(graph->exec, ctx->stream));
     return QMM_OK;

@@ -245,7 +245,10 @@ int    qmm_graph_compute(qmm_ctx * ctx, const qmm_node * nodes, int n_nodes);
  * kernels on the same buffers (the data in them may change between launches).  The graph uses
  * the context's scratch: replays are ordered with the context's other work by its stream, and
  * an op run outside the graph may leave the scratch holding other activations, which the next
- * replay overwrites before it reads them.  Free the graph before its context. */
+ * replay overwrites before it reads them.  An op outside the graph that needs more scratch than
+ * the context has replaces the scratch: the graphs captured before then are refused by
+ * qmm_graph_launch (QMM_ERR_INVALID; capture again), as is a graph launched on a context other
+ * than its own.  Free the graph before its context. */
 typedef struct qmm_graph qmm_graph;
 int    qmm_capture_begin(qmm_ctx * ctx);
 int    qmm_capture_end(qmm_ctx * ctx, qmm_graph ** out);

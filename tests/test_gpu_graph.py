@@ -219,3 +219,57 @@ def test_capture_refuses_allocation(orc):
         assert rel_err(b.get_f32(y).reshape(N, M), orc.mul_mat(qtype, raw, M, K, x)) <= TOL
         for t in (w, xt, y):
             b.free_buffer(t.buf)
+
+
+def test_graph_refused_after_scratch_grows(be, orc):
+    """an op outside a graph that needs more scratch than the context has replaces it: the graph
+    captured before then is refused (its buffers are gone) and a new capture runs; a graph is
+    refused on another context too"""
+    say("graph refused after the scratch grows")
+    with qmm.Backend(0) as b:
+        qtype, M = qmm.Q4_K, 256
+        ts = []
+
+        def product(K, N, seed):
+            raw = synth.weights(qtype, M, K, seed)
+            x = synth.activations(N, K, seed + 1)
+            w = b.new_tensor(qtype, (K, M))
+            b.set_tensor(w, raw)
+            xt = b.new_tensor(qmm.F32, (K, N))
+            b.set_tensor(xt, x.view(np.uint8).ravel())
+            y = b.new_tensor(qmm.F32, (M, N))
+            ts.extend([w, xt, y])
+            return raw, x, w, xt, y
+
+        # 16 groups along K, 3 columns: the pre-pass path (activations in the scratch)
+        raw, x, w, xt, y = product(4096, 3, 830)
+        b.mul_mat(w, xt, y)
+        b.synchronize()
+        b.capture_begin()
+        b.mul_mat(w, xt, y)
+        g = b.capture_end()
+        try:
+            b.graph_launch(g)
+            b.synchronize()
+            assert rel_err(b.get_f32(y).reshape(3, M), orc.mul_mat(qtype, raw, M, 4096, x)) <= TOL
+            with pytest.raises(qmm.QmmError, match="another context"):
+                be.graph_launch(g)
+            rb, xb, wb, xtb, yb = product(16384, 8, 840)          # more activations: the scratch grows
+            b.mul_mat(wb, xtb, yb)
+            b.synchronize()
+            assert rel_err(b.get_f32(yb).reshape(8, M), orc.mul_mat(qtype, rb, M, 16384, xb)) <= TOL
+            with pytest.raises(qmm.QmmError, match="capture again"):
+                b.graph_launch(g)
+        finally:
+            g.free()
+        b.capture_begin()
+        b.mul_mat(w, xt, y)
+        g2 = b.capture_end()
+        try:
+            b.graph_launch(g2)
+            b.synchronize()
+            assert rel_err(b.get_f32(y).reshape(3, M), orc.mul_mat(qtype, raw, M, 4096, x)) <= TOL
+        finally:
+            g2.free()
+        for t in ts:
+            b.free_buffer(t.buf)
