@@ -942,8 +942,9 @@ static int64_t fused_small_tgroups() {
 // 100.0 -> 101.9) and so do two columns on large images (Q8_0 14336 x 4096 15.3 -> 15.7, IQ4_XS
 // 13.0-13.5 -> 14.2).  So: one column of any type but Q6_K, and 1-2 columns of any type for
 // images up to QMM_GEMV_FQS_MAX_KB (16 MiB) of one matrix; QMM_GEMV_FQS = 0 never, = 1 always;
-// work-groups of QMM_GEMV_FQS_W waves (4: 11.6 us on the Q4_K against 12.2-12.3 at 2, 5 and 8)
-// with QMM_GEMV_FQS_SPW groups each (1).
+// work-groups of QMM_GEMV_FQS_W waves with QMM_GEMV_FQS_SPW groups each (1): 4 waves (Q4_K 11.6
+// us against 12.2-12.3 at 2, 5 and 8; Q5_K 14.1-14.2 against 15.7 at 8), 8 for Q8_0, whose
+// 17 KB tile-groups run 2.5 % faster so (13.2 against 13.5 us on 14336 x 4096).
 static int env_or(const char * name, int dflt) {
     const char * e = getenv(name);
     return e ? atoi(e) : dflt;
@@ -974,7 +975,8 @@ static bool fused_dense_plan(int type, const WView & w, int64_t N, int64_t nbatc
         if (fp->ntasks * w.ntiles * fp->W >= fused_min_waves()) return true;
     }
     return split && fused_split_for(type, w, N) &&
-           gemv_fused_split_plan(type, w, (int)N, nbatch, env_or("QMM_GEMV_FQS_W", 4), env_or("QMM_GEMV_FQS_SPW", 1), fp);
+           gemv_fused_split_plan(type, w, (int)N, nbatch, env_or("QMM_GEMV_FQS_W", type == QMM_TYPE_Q8_0 ? 8 : 4),
+                                 env_or("QMM_GEMV_FQS_SPW", 1), fp);
 }
 // whether a MUL_MAT_ID of T tokens with n_used ids each takes the fused GEMV's pairs, and its plan
 static bool fused_id_plan(int type, const WView & w, int64_t n_used, int64_t T, FusedPlan * fp) {

@@ -247,7 +247,8 @@ def test_gemv_plan(qtype, K, M, N):
     if info["path"] == "gemv-fq":
         # the fused-quantization kernel: 1-2 columns, work-groups of up to 16 waves per 64-row
         # tile and task; K split among the waves and, for one column of any type but Q6_K or
-        # a small image (at most 16 MiB), over KS work-groups of 4 waves with one group each
+        # a small image (at most 16 MiB), over KS work-groups of 4 waves (8 for Q8_0) with one
+        # group each
         # (the K-slice tree); LDS holds each wave's quantized groups (320 B per group and
         # column), then the waves' sums
         W, spw, nc, KS = info["k_waves"], info["groups_per_wave"], info["cols_per_task"], info["k_slices"]
@@ -262,7 +263,7 @@ def test_gemv_plan(qtype, K, M, N):
             image = nt * G * {qmm.Q4_0: 18, qmm.Q8_0: 34, qmm.Q4_K: 144, qmm.Q5_K: 176, qmm.Q6_K: 210,
                               qmm.IQ4_XS: 136, qmm.IQ4_NL: 18}[qtype] * (8 if qtype in (qmm.Q4_0, qmm.Q8_0, qmm.IQ4_NL) else 1) * 64
             assert (N == 1 and qtype != qmm.Q6_K) or image <= 16 << 20
-            assert W == 4 and spw == 1
+            assert W == (8 if qtype == qmm.Q8_0 else 4) and spw == 1
         assert info["workgroups"] == info["tasks"] * nt * KS and info["threads"] == 64 * W
         assert info["lds_bytes"] == max(W * spw * nc * 320, W * 2 * nc * 64 * 4)
         return
