@@ -137,11 +137,12 @@ __global__ __launch_bounds__(kRouteThreads) void k_quant_route(F32Cols src, int6
 // replaces llama.cpp's gating chain SOFT_MAX, ARGSORT (desc), VIEW, GET_ROWS, SUM_ROWS, CLAMP,
 // DIV (matched at P02:786-821); the selection here is a filter and a count, not repeated arg-max
 // rounds.  One wave per token (a one-wave work-group); lane l holds the logits of the NPER
-// consecutive experts [l NPER, (l + 1) NPER).  Softmax is monotone, so the winners are the k
-// largest logits, equal logits ordered by expert (the order of the probabilities, which the
-// float32 exp could otherwise merge into ties):
-//  1. each logit becomes an order-preserving 32-bit key; padding gets key 0, below every real
-//     key;
+// consecutive experts [l NPER, (l + 1) NPER).  The order is the reference's: the float32 values
+// e = exp(x - max) it ranks (P09:935-966), equal values to the lower expert, so two distinct
+// logits whose float32 exp is equal tie (as ggml's SOFT_MAX -> ARGSORT ranks float32
+// probabilities):
+//  1. each e becomes a 32-bit key, its bits + 1 (e >= 0, so the bits are in e's order; an exp
+//     that underflows to 0 still ranks above the padding); padding gets key 0;
 //  2. the filter: tau0 = the k-th largest of the 64 lanes' largest keys, found most-significant
 //     bit first (32 steps of one ballot).  The lanes holding the k largest maxima hold k keys
 //     >= tau0, so every winner is >= tau0;
@@ -152,11 +153,6 @@ __global__ __launch_bounds__(kRouteThreads) void k_quant_route(F32Cols src, int6
 // Weights: exp(x - max) / sum over all experts (a wave sum), divided by the winners' sum, taken
 // in rank order and clamped to [cmin, cmax].
 
-// a float's bits as an unsigned key with the float's order (-0 as +0: equal floats, equal keys)
-__device__ __forceinline__ uint32_t order_key(float x) {
-    const uint32_t b = __builtin_bit_cast(uint32_t, x == 0.0f ? 0.0f : x);
-    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
 
 // the sum over lanes 0 .. lane of v (inclusive), by shuffles
 __device__ __forceinline__ int lane_scan(int v, int lane) {
@@ -188,20 +184,22 @@ __global__ __launch_bounds__(64) void k_topk(TopkArgs a) {
     float v[NPER];
     uint32_t key[NPER];
     float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NPER; ++j) {
+        v[j] = e0 + j < a.n_expert ? x[e0 + j] : -INFINITY;
+        mx = fmaxf(mx, v[j]);
+    }
+    const float m = wave_max(mx);
+    float part = 0.0f;
     uint32_t kmax = 0;
 #pragma unroll
     for (int j = 0; j < NPER; ++j) {
         const bool live = e0 + j < a.n_expert;
-        v[j] = live ? x[e0 + j] : -INFINITY;
-        key[j] = live ? order_key(v[j]) : 0u;
-        mx = fmaxf(mx, v[j]);
+        const float e = live ? expf(v[j] - m) : 0.0f;
+        part += e;
+        key[j] = live ? __builtin_bit_cast(uint32_t, e) + 1u : 0u;
         kmax = key[j] > kmax ? key[j] : kmax;
     }
-    const float m = wave_max(mx);
-    float part = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NPER; ++j)
-        if (e0 + j < a.n_expert) part += expf(v[j] - m);
     const float S = wave_sum_f(part);
     // 2. tau0: the largest value with at least k lane maxima at or above it
     uint32_t tau0 = 0;

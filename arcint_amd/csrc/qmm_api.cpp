@@ -1069,7 +1069,8 @@ static bool try_fused_dense(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_te
     f.glu = glu;
     KTime kt;
     const KTime * ktp = nullptr;
-    if ((*rc = ktime_pair(ctx, &kt, &ktp))) return true;
+    // (the allocation-free entry point records no timing events)
+    if (!noalloc && (*rc = ktime_pair(ctx, &kt, &ktp))) return true;
     const hipError_t e = launch_gemv_fused(src0->type, w, fp, f, d, ctx->sink, ctx->stream, ktp);
     *rc = e == hipSuccess ? ktime_done(ctx) : fail(ctx, QMM_ERR_DEVICE, "launch_gemv_fused: %s", hipGetErrorString(e));
     return true;
@@ -1128,7 +1129,10 @@ static int mul_mat_launch(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tens
     dn.d_nb3 = (int64_t)(dst->nb[3] / 4);
     KTime kt;
     const KTime * ktp = nullptr;
-    if (use_gemm && gemm3_supported(src0->type)) {           // weights streamed per wave, dst written once
+    G3Shape g3;
+    // weights streamed per wave, dst written once (the shape check is qmm_describe_mul_mat's, so
+    // a shape the streaming kernel declines runs on the shared-tile GEMM below, as described)
+    if (use_gemm && gemm3_shape(src0->type, w, N, dn.ne12 * dn.ne13, &g3)) {
         const int64_t nbatch = dn.ne12 * dn.ne13;
         TiledAct ta;
         if ((rc = quantize_src1_tiled(ctx, src0->type, src1, w.G, &ta, fixed))) return rc;

@@ -216,7 +216,10 @@ int    qmm_mul_mat_id_glu(qmm_ctx * ctx, const qmm_tensor * gate, const qmm_tens
                           const qmm_tensor * ids, const qmm_tensor * dst, int32_t glu_op);
 /* qmm_mul_mat with nothing allocated: no reference counterpart; for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
- * forbid hipMalloc).  Same operands, kernels and results as qmm_mul_mat; the activation
+ * forbid hipMalloc).  Same operands as qmm_mul_mat and the same results within MUL_MAT's
+ * tolerance, on the same kernels except that it never takes the K-split one-launch GEMV
+ * ("gemv-fq" with work-groups meeting in the exchange tree, whose slots the context allocates):
+ * such products run the activation pre-pass and the GEMV instead; the activation
  * quantization goes to a device array of QMM_NOALLOC_SCRATCH_BYTES that the library holds on
  * every GPU it runs on until the process ends (its address is looked up when a context is
  * created) instead of the context's scratch, and no graph dedup or kernel timing applies.
@@ -293,16 +296,24 @@ int    qmm_moe_combine(qmm_ctx * ctx, const qmm_tensor * experts, const qmm_tens
  * op, weight type, K, a column bucket, the path taken and the reason ("op=MUL_MAT type=Q5_K
  * k=5120 cols=2-8 path=gemv reason=no-mfma-gemv"); returns the total count over all keys. */
 int64_t qmm_downgrades(qmm_ctx * ctx, char * buf, size_t buf_len);
-/* Name of the kernel path the last mul_mat / mul_mat_id took: "gemv" (v_dot4
- * GEMV, 1..8 columns per weight pass), "gemv-mfma" (3..8 columns on the int8
- * MFMA), "gemm-mfma" (prefill GEMM), "gemv-id" / "gemv-id-mfma" (MUL_MAT_ID
- * expert tasks on either GEMV). */
+/* Name of the kernel path the last op took.  MUL_MAT: "gemv" (activation pre-pass + v_dot4
+ * GEMV, 1..8 columns per weight pass), "gemv-mfma" (pre-pass + the few-column int8 MFMA GEMV,
+ * up to 32 columns per weight pass), "gemv-fq" (one launch: the GEMV quantizes its own
+ * activations, K split over work-groups met in an exchange tree), "gemm-stream" (tiled pre-pass
+ * + the streaming int8 MFMA GEMM), "gemm-mfma" (pre-pass + the shared-tile int8 MFMA GEMM).
+ * MUL_MAT_ID: "gemv-id-fq" (one launch, each (slot, token) pair read from ids), "gemv-id" /
+ * "gemv-id-mfma" (route + expert tasks on either GEMV), "gemm-id-stream" (route + the grouped
+ * streaming GEMM).  qmm_mul_mat_glu: "glu-fused-gemv-fq", "glu-fused-gemv", "glu-fused-gemv-mfma"
+ * (gate and up in one launch) or "glu-" + the MUL_MAT path (two products and a GLU kernel).
+ * qmm_mul_mat_id_glu: "glu-gemv-id-fq", "glu-gemv-id", "glu-gemv-id-mfma".  The router and the
+ * combine: "moe-topk", "moe-combine". */
 const char * qmm_last_path(qmm_ctx * ctx);
 
 /* The launch a qmm_mul_mat with these tensors would make (host only, no
  * device, no buffers needed: only types and shapes are read). */
 typedef struct qmm_launch_info {
-    char    path[32];          /* "gemv", "gemv-mfma" (3..8 columns on the MFMA) or "gemm-mfma" */
+    char    path[32];          /* as qmm_last_path: "gemv", "gemv-mfma", "gemv-fq", "gemm-stream" or
+                                  "gemm-mfma" */
     int64_t workgroups;
     int32_t threads;           /* per work-group */
     int32_t cols_per_task;     /* GEMV: activation columns per weight pass */

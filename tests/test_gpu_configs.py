@@ -15,6 +15,8 @@ Bar: max relative error <= 1e-3 with the denominator floored at 5 % of the outpu
 (conftest.rel_err); every case also prints the unfloored maximum, how many outputs pass 1e-3
 unfloored and the largest |ref| among them, so the floor's reading is visible per case.
 Each case prints its name before it touches the GPU."""
+import json
+import os
 import sys
 
 import numpy as np
@@ -33,11 +35,17 @@ def say(*a):
     sys.stdout.flush()
 
 
-def check(got, ref, name):
+def check(got, ref, name, path=None):
+    """The bar (floored) asserted; the unfloored figures printed and, with QMM_PARITY_LOG set to a
+    file, appended to it as one JSON line per case (the committed parity table is built from it)."""
     r = err_report(got, ref)
     print(f"[err] {name}: floored {r['floored']:.3g} unfloored {r['unfloored']:.3g} "
           f"({r['n_over_1e-3']} of {r['n']} over 1e-3 unfloored, |ref| <= {r['max_abs_ref_over_rms']:.2g} rms there; "
           f"max |err| {r['max_abs_err_over_rms']:.2g} rms)", flush=True)
+    log = os.environ.get("QMM_PARITY_LOG")
+    if log:
+        with open(log, "a") as f:
+            f.write(json.dumps({"case": name, "path": path, **r}) + "\n")
     assert r["floored"] <= TOL, (name, r)
 
 
@@ -131,7 +139,7 @@ def test_c1_llama2_q4_0(be, wc, orc, bufs, qtype, M, K, N):
     say(name)
     got, ref, path = mul_mat_case(be, wc, orc, bufs, qtype, M, K, N, seed=7)
     assert path in (("gemm-stream",) if N == 512 else ("gemv", "gemv-fq")), path
-    check(got, ref, name)
+    check(got, ref, name, path)
 
 
 @pytest.mark.parametrize("qtype,M,K", C2)
@@ -142,7 +150,7 @@ def test_c2_27b_layer(be, wc, orc, bufs, qtype, M, K, N):
     got, ref, path = mul_mat_case(be, wc, orc, bufs, qtype, M, K, N, seed=11)
     gemm = "gemm-stream" if qtype == qmm.Q4_K else "gemm-mfma"
     assert path in {1: ("gemv", "gemv-fq"), 4: ("gemv-mfma",), 512: (gemm,)}[N], path
-    check(got, ref, name)
+    check(got, ref, name, path)
 
 
 @pytest.mark.parametrize("qtype,M,K", C4)
@@ -152,7 +160,7 @@ def test_c4_iquant_q8_0_decode(be, wc, orc, bufs, qtype, M, K, N):
     say(name)
     got, ref, path = mul_mat_case(be, wc, orc, bufs, qtype, M, K, N, seed=13)
     assert path in (("gemv", "gemv-fq") if N <= 2 else ("gemv-mfma",)), path
-    check(got, ref, name)
+    check(got, ref, name, path)
 
 
 # ------------------------------------------------------------------ C3: the MoE layer
@@ -185,7 +193,7 @@ def test_c3_gate_up_mul_mat_id(be, orc, bufs, moe_w, T):
     be.mul_mat_id(w, f32(be, x, bufs), i32(be, ids, bufs), y)
     be.synchronize()
     got = be.get_f32(y).reshape(T, N_USED, FFN)
-    check(got, orc.mul_mat_id(qmm.Q4_K, raw, FFN, HID, E, x, ids), name)
+    check(got, orc.mul_mat_id(qmm.Q4_K, raw, FFN, HID, E, x, ids), name, be.last_path())
 
 
 @pytest.mark.parametrize("T", [1, 4, 256])
@@ -200,7 +208,7 @@ def test_c3_down_mul_mat_id(be, orc, bufs, moe_w, T):
     be.mul_mat_id(w, f32(be, x, bufs), i32(be, ids, bufs), y)
     be.synchronize()
     got = be.get_f32(y).reshape(T, N_USED, HID)
-    check(got, orc.mul_mat_id(qmm.Q4_K, raw, HID, FFN, E, x, ids), name)
+    check(got, orc.mul_mat_id(qmm.Q4_K, raw, HID, FFN, E, x, ids), name, be.last_path())
 
 
 @pytest.mark.parametrize("T", [1, 4, 256])

@@ -31,6 +31,16 @@ def test_gelu_forms():
     np.testing.assert_allclose(G.act(G.GEGLU_QUICK, X), G.act(G.SWIGLU, 1.702 * X) / 1.702, rtol=1e-12, atol=1e-300)
 
 
+def test_tanh_gelu_against_torch():
+    """the tanh form against torch's gelu(approximate='tanh') in float64: a wrong cubic
+    coefficient or constant moves it by far more than 1e-12"""
+    torch = pytest.importorskip("torch")
+    ref = torch.nn.functional.gelu(torch.from_numpy(X), approximate="tanh").numpy()
+    np.testing.assert_allclose(G.act(G.GEGLU, X), ref, rtol=1e-12, atol=1e-15)
+    e = torch.nn.functional.gelu(torch.from_numpy(X)).numpy()
+    np.testing.assert_allclose(G.act(G.GEGLU_ERF, X), e, rtol=1e-12, atol=1e-15)
+
+
 def test_reglu_and_the_product():
     assert list(G.act(G.REGLU, np.array([-2.0, 0.0, 3.5]))) == [0.0, 0.0, 3.5]
     g = np.random.default_rng(1).standard_normal(50)

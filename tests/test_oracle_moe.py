@@ -35,6 +35,22 @@ def test_topk_matches_brute_force(n, k):
         np.testing.assert_allclose(w[t], sel / sel.sum(), rtol=1e-12)
 
 
+def test_float32_exp_ties_go_to_the_lower_expert():
+    """Distinct logits whose float32 exp(x - max) is equal tie, and the lower expert wins (the
+    reference ranks the float32 exp values, and ggml's SOFT_MAX -> ARGSORT the float32
+    probabilities).  exp(-1e-8) and exp(-2e-8) are within half an ulp of 1 (ulp 2^-24 below 1),
+    so every correctly rounded exp returns 1.0f for them, as for the maximum itself."""
+    assert np.exp(np.float32(-1e-8)) == np.float32(1.0) and np.exp(np.float32(-2e-8)) == np.float32(1.0)
+    logits = np.full((1, 400), -3.0, np.float32)
+    logits[0, 300] = 0.0                                  # the maximum, at a high index
+    logits[0, 7] = -2e-8
+    logits[0, 5] = -1e-8
+    logits[0, 9] = -0.5
+    ids, w = moe.topk(logits, 4, 0.0, np.inf)
+    assert list(ids[0]) == [5, 7, 300, 9]                  # logit order would be 300, 5, 7, 9
+    np.testing.assert_allclose(w[0, :3], w[0, 0], rtol=1e-7)
+
+
 def test_uniform_logits_pick_the_lowest_experts_with_equal_weights():
     ids, w = moe.topk(np.full((3, 40), 1.25), 6, 6.103515625e-5, np.inf)
     assert (ids == np.arange(6)).all()

@@ -1,8 +1,16 @@
 """qmm_mul_mat_noalloc (activations in the library's per-device array, nothing allocated)
-against qmm_mul_mat on the same operands, through the C ABI, and against the CPU oracle: the GEMM
-and both GEMV kernels, two and more calls in a row with the later ones smaller (the array keeps
-the last call's contents), and a product whose activations need more than the array holds
-(refused before anything runs)."""
+against qmm_mul_mat on the same operands, through the C ABI, and against the CPU oracle, two and
+more calls in a row with the later ones smaller (the array keeps the last call's contents).  Each
+kernel path the entry point can take on the array is pinned by the path it reports:
+  gemm-stream  the streaming GEMM (tiled pre-pass into the array)
+  gemm-mfma    the shared-tile GEMM (a type the streaming kernel does not take, and QMM_GEMM3=0)
+  gemv-mfma    pre-pass + the few-column MFMA GEMV
+  gemv         pre-pass + the v_dot4 GEMV: a large one-column product, which qmm_mul_mat runs as
+               the K-split one-launch GEMV (its exchange-tree slots are allocated, so the
+               allocation-free entry point takes the pre-pass path), and QMM_GEMV_FUSED=0
+  gemv-fq      the one-launch GEMV of small products (no scratch at all)
+plus a product whose activations need more than the array holds (refused before anything runs)
+and a call with kernel timing on (the entry point records no timing events)."""
 import sys
 
 import numpy as np
@@ -57,6 +65,64 @@ def test_noalloc_matches_mul_mat(be, orc, seq):
         b = be.get_f32(yb).reshape(N, M)
         assert rel_err(b, a) <= TOL, (i, path)
         assert rel_err(b, orc.mul_mat(qtype, raw, M, K, x)) <= TOL, (i, path)
+        for t in (w, xt, ya, yb):
+            be.free_buffer(t.buf)
+
+
+@pytest.mark.parametrize("case", [
+    # (type, M, K, N, environment, the path qmm_mul_mat_noalloc must report)
+    (qmm.Q4_K, 17408, 5120, 1, {}, "gemv"),
+    (qmm.Q4_K, 17408, 5120, 1, {"QMM_GEMV_FUSED": "0"}, "gemv"),
+    (qmm.Q5_K, 1024, 2048, 64, {}, "gemm-mfma"),
+    (qmm.Q4_0, 2048, 4096, 512, {"QMM_GEMM3": "0"}, "gemm-mfma"),
+    (qmm.Q4_0, 2048, 4096, 512, {}, "gemm-stream"),
+    (qmm.Q8_0, 4096, 4096, 24, {}, "gemv-mfma"),
+    (qmm.IQ4_XS, 256, 512, 2, {}, "gemv-fq"),
+    (qmm.Q6_K, 128, 256, 1, {}, "gemv-fq"),
+])
+def test_noalloc_paths(be, orc, monkeypatch, case):
+    qtype, M, K, N, env, want = case
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    say("noalloc path", synth.NAMES[qtype], M, K, N, env, want)
+    raw, x, w, xt, ya, yb = product(be, qtype, M, K, N, seed=700 + M % 97)
+    be.mul_mat_noalloc(w, xt, yb)
+    be.synchronize()
+    assert be.last_path() == want
+    be.mul_mat(w, xt, ya)
+    be.synchronize()
+    b = be.get_f32(yb).reshape(N, M)
+    assert rel_err(b, be.get_f32(ya).reshape(N, M)) <= TOL
+    assert rel_err(b, orc.mul_mat(qtype, raw, M, K, x)) <= TOL
+    # a second, smaller call on the same array
+    xs = qmm.Tensor(xt.buf, qmm.F32, (K, 1))
+    ys = qmm.Tensor(yb.buf, qmm.F32, (M, 1))
+    be.mul_mat_noalloc(w, xs, ys)
+    be.synchronize()
+    assert rel_err(be.get_f32(yb)[:M], orc.mul_mat(qtype, raw, M, K, x[:1])) <= TOL
+    for t in (w, xt, ya, yb):
+        be.free_buffer(t.buf)
+
+
+def test_noalloc_records_no_timing(be, orc):
+    """With kernel timing on, qmm_mul_mat stamps one event pair per op and the allocation-free
+    entry point none, on every path (one-launch GEMV, pre-pass GEMV, GEMM)"""
+    say("noalloc timing")
+    cases = [(qmm.IQ4_XS, 256, 512, 2), (qmm.Q4_K, 2048, 4096, 1), (qmm.Q4_0, 2048, 4096, 512)]
+    made = [(q, M, K, N, *product(be, q, M, K, N, seed=800 + i)) for i, (q, M, K, N) in enumerate(cases)]
+    be.kernel_timing(1)
+    try:
+        for q, M, K, N, raw, x, w, xt, ya, yb in made:
+            be.mul_mat_noalloc(w, xt, yb)
+        be.synchronize()
+        assert be.kernel_time()[1] == 0
+        for q, M, K, N, raw, x, w, xt, ya, yb in made:
+            be.mul_mat(w, xt, ya)
+        assert be.kernel_time()[1] == len(made)
+    finally:
+        be.kernel_timing(0)
+    for q, M, K, N, raw, x, w, xt, ya, yb in made:
+        assert rel_err(be.get_f32(yb).reshape(N, M), orc.mul_mat(q, raw, M, K, x)) <= TOL
         for t in (w, xt, ya, yb):
             be.free_buffer(t.buf)
 
