@@ -525,6 +525,17 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q4k(KQParams p) {
         const uint32_t sh03 = (sc03 >> 3) & 0x07070707u, sl03 = sc03 & 0x07070707u;
         const uint32_t sh47 = (sc47 >> 3) & 0x07070707u, sl47 = sc47 & 0x07070707u;
         v16i acc[4];                                          // [sh, sl] x [tile 0, tile 1]
+        // the A operands of sub-block j of both column tiles, read one sub-block ahead (the LDS
+        // latency runs under the previous sub-block's MFMAs)
+        auto aread = [&](int j, v4i & x0, v4i & x1) {
+            // (grouped mode: chunk 2 j + h of column j32 at its swizzled slot)
+            const uint32_t aoff = GATHER ? (uint32_t)j32 * 256 + 16 * (uint32_t)((2 * j + h) ^ (j32 & 15))
+                                         : (uint32_t)(j * 1024) + lane16;
+            x0 = *reinterpret_cast<const v4i *>(S + aoff);
+            x1 = *reinterpret_cast<const v4i *>(S + 8192 + aoff);
+        };
+        v4i na0, na1;
+        aread(0, na0, na1);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const uint4 q = ch[j >> 1];
@@ -532,11 +543,8 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q4k(KQParams p) {
             const uint32_t n0 = (q.x >> nsh) & 0x0F0F0F0Fu, n1 = (q.y >> nsh) & 0x0F0F0F0Fu;
             const uint32_t n2 = (q.z >> nsh) & 0x0F0F0F0Fu, n3 = (q.w >> nsh) & 0x0F0F0F0Fu;
             if (j & 1) ch[j >> 1] = bld16(wbuf, wl, sn + 2 * (j >> 1) * kChunk);
-            // (grouped mode: chunk 2 j + h of column j32 at its swizzled slot)
-            const uint32_t aoff = GATHER ? (uint32_t)j32 * 256 + 16 * (uint32_t)((2 * j + h) ^ (j32 & 15))
-                                         : (uint32_t)(j * 1024) + lane16;
-            const v4i a0 = *reinterpret_cast<const v4i *>(S + aoff);
-            const v4i a1 = *reinterpret_cast<const v4i *>(S + 8192 + aoff);
+            const v4i a0 = na0, a1 = na1;
+            if (j < 7) aread(j + 1, na0, na1);
             const int js = j ^ (QMM_RED == 5);                // (mutation 5: neighbouring scales swapped)
             // the sub-block's sh and sl in both 16-bit halves (bytes 1 and 3 zero)
             const uint32_t sel = 0x0c000c00u | (uint32_t)(js & 3) * 0x00010001u;
@@ -546,23 +554,25 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q4k(KQParams p) {
                                 (int)mul_u16x2(n3, mh) };
             const v4i bl = v4i{ (int)mul_u16x2(n0, ml), (int)mul_u16x2(n1, ml), (int)mul_u16x2(n2, ml),
                                 (int)mul_u16x2(n3, ml) };
+            // (the last sub-block issues tile 0's two chains first: its combine below waits for
+            // them only)
             acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bh, j ? acc[0] : v16i{}, 0, 0, 0);
+            if (j == 7) acc[2] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bl, acc[2], 0, 0, 0);
             acc[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bh, j ? acc[1] : v16i{}, 0, 0, 0);
-            acc[2] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bl, j ? acc[2] : v16i{}, 0, 0, 0);
+            if (j < 7) acc[2] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bl, j ? acc[2] : v16i{}, 0, 0, 0);
             acc[3] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bl, j ? acc[3] : v16i{}, 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
         }
-        // isc = 8 sum_sh + sum_sl, in place (frees the sl sums before the min term)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            acc[0][r] = (acc[0][r] << 3) + acc[2][r];
-            acc[1][r] = (acc[1][r] << 3) + acc[3][r];
-        }
-        // min term, then the float combine of each column tile
+        // min term sum_j m_j bsum_j of each column tile: A = the columns' split sums bh (then bl,
+        // bsum = 64 bh + bl) at k = j, B = the row's 8 mins; the second MFMA starts from 64 * first
+        // + the bits of 12582912.0f, so its result read as a float is 12582912 + imn exactly
+        // (|imn| < 2^22).  Each tile's isc = 8 sum_sh + sum_sl (in place) runs under its first
+        // min MFMA, and tile 1's min term under tile 0's second.
         float d = h2f(dd & 0xffffu), dmin = h2f(dd >> 16);
         asm volatile("" : "+v"(d), "+v"(dmin));               // f32 operands (no fp16 source folding)
         const float nmag = 12582912.0f * dmin;                // exact: fp16 dmin times 3 * 2^22
         const v4i bm = h ? v4i{} : v4i{ (int)mn03, (int)mn47, 0, 0 };
+        v16i mlt[2];
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             const uint4 sp = *reinterpret_cast<const uint4 *>(S + 16384 + c * 512 + j32 * 16);
@@ -570,8 +580,15 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q4k(KQParams p) {
             const v4i al = h ? v4i{} : v4i{ (int)sp.z, (int)sp.w, 0, 0 };
             v16i mh = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, bm, v16i{}, 0, 0, 0);
 #pragma unroll
+            for (int r = 0; r < 16; ++r) acc[c][r] = (acc[c][r] << 3) + acc[2 + c][r];
+#pragma unroll
             for (int r = 0; r < 16; ++r) mh[r] = mh[r] * 64 + kMagic;
-            const v16i ml = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, bm, mh, 0, 0, 0);
+            mlt[c] = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, bm, mh, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // the float combine of each column tile
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
             float dx[16];
 #pragma unroll
             for (int q4 = 0; q4 < 4; ++q4) {
@@ -589,7 +606,7 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q4k(KQParams p) {
             for (int r = 0; r < 16; ++r) {
                 // (the element goes through a scalar: clang's __builtin_bit_cast of an ext-vector
                 // element reads element 0)
-                const int iml = ml[r];
+                const int iml = mlt[c][r];
                 const int isc = acc[c][r];
                 const float wv = __builtin_fmaf(__builtin_bit_cast(float, iml), -dmin, nmag);   // -dmin * imn
                 const float v = __builtin_fmaf((float)isc, d, wv);

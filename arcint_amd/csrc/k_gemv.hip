@@ -1194,7 +1194,11 @@ int env_int(const char * name, int dflt) {
 //    P01:1222-1248); a negative id writes a zero row, an id past the stack too and sets the
 //    error flag;
 //  * either of them for a gate/up pair with its GLU: the work-group streams the gate tile, then
-//    the up tile against the same quantized activations, and stores act(gate) * up.
+//    the up tile against the same quantized activations, and stores act(gate) * up;
+//  * a MoE FFN block's two products (qmm_moe_ffn): pairs may add a shared-expert slot (slot
+//    n_used of every token, its own images, no id), and the down product combines: each pair's
+//    row is scaled by its router weight (the shared slot's by the sigmoid of its gate logit),
+//    the token's slots meet in the exchange tree, and the root stores the token's output row.
 constexpr int kFqSlot = 320;   // one (group, column): 256 codes, 8 f32 scales at 256, 16 i16 sums at 288
 constexpr int kFqMaxWaves = 16;
 
@@ -1227,7 +1231,20 @@ struct FqParams {
     int glu;
     int W, spw;
     int KS;                      // dense: work-groups per tile along K (grid z)
-    uint32_t * tree;             // KS > 1: slots [task][tile][2 KS nodes][NC][64] (64-bit pairs with the GLU)
+    uint32_t * tree;             // KS > 1: slots [task][tile][2 KS nodes][NC][64] (64-bit pairs with the GLU);
+                                 // combine: [token][tile][2 slots nodes][64]
+    // MoE FFN: a shared-expert slot after the n_used routed ones (its images: the gate / only
+    // matrix and the up one, w's shape); combine: slot i of token t weighted by
+    // cw[t cw_nb1 + i cw_nb0] (the shared slot by sigmoid(sl[t sl_nb1]), 1 without sl), the
+    // token's row stored at dst + t d_nb1
+    int n_shared;
+    const uint8_t * sh_base;
+    const uint8_t * sh_base2;
+    int comb;
+    const float * cw;
+    int64_t cw_nb0, cw_nb1;
+    const float * sl;
+    int64_t sl_nb1;
 };
 
 // The K slices of a tile add their sums v[j] (column j, this lane's row) up a pairwise tree
@@ -1352,19 +1369,24 @@ __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
     const int ks = p.ids ? 0 : (int)blockIdx.z;
     int mat, nc;
     int64_t colv[NC], doffv[NC];
+    bool shared = false, skip = false;
     if (p.ids) {
         const int64_t t = blockIdx.z, i = blockIdx.y;
-        const int32_t e = *reinterpret_cast<const int32_t *>(p.ids + t * p.ids_nb1 + i * p.ids_nb0);
+        shared = i >= p.n_used;                                   // uniform: the shared expert's slot
+        const int32_t e = shared ? 0 : *reinterpret_cast<const int32_t *>(p.ids + t * p.ids_nb1 + i * p.ids_nb0);
         const int64_t doff = t * p.dnb2 + i * p.dnb1;
         if (e < 0 || e >= p.n_as) {                                // uniform: a zero row
-            if (wave == 0) {
-                const int64_t row = (int64_t)tile * kTileRows + lane;
-                if (row < p.w.M) p.dst[doff + row] = 0.0f;
-                if (e >= p.n_as && tile == 0 && lane == 0) *p.bad_id = 1;
+            if (wave == 0 && e >= p.n_as && tile == 0 && lane == 0) *p.bad_id = 1;
+            if (!p.comb) {
+                if (wave == 0) {
+                    const int64_t row = (int64_t)tile * kTileRows + lane;
+                    if (row < p.w.M) p.dst[doff + row] = 0.0f;
+                }
+                return;
             }
-            return;
+            skip = true;                                          // (combine: the slot still meets the others)
         }
-        mat = QMM_RED == 8 ? (int)((e + 1) % p.n_as) : e;      // (mutation 8: the next expert)
+        mat = skip || shared ? 0 : QMM_RED == 8 ? (int)((e + 1) % p.n_as) : e;   // (mutation 8: the next expert)
         nc = 1;
 #pragma unroll
         for (int j = 0; j < NC; ++j) {
@@ -1389,11 +1411,13 @@ __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
     const int G = (int)p.w.G;
     int ga, S;
     dot4_stages(ks, p.W, wave, p.spw, G, NST, ga, S);
+    if (skip) S = 0;                                              // (a zero row: no stages, no groups)
     const bool glu = p.glu >= 0;                                  // uniform
     const int ST = glu ? 2 * S : S;                               // gate stages, then up stages
-    const uint8_t * tbg = tile_group(p.w, mat, tile, 0);
-    WView w2 = p.w;
-    w2.base = p.base2;
+    WView w1 = p.w, w2 = p.w;
+    if (shared) w1.base = p.sh_base;
+    w2.base = shared ? p.sh_base2 : p.base2;
+    const uint8_t * tbg = tile_group(w1, mat, tile, 0);
     const uint8_t * tbu = glu ? tile_group(w2, mat, tile, 0) : tbg;
     const size_t tgs = (size_t)p.w.tg;
     uint4 B[NL];
@@ -1491,6 +1515,22 @@ __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
         if (glu) tree_add_pairs<NC>(reinterpret_cast<uint64_t *>(nodes), ks, p.KS, nc, tot, totu, alive, lane);
         else tree_add<NC>(nodes, ks, p.KS, nc, tot, alive, lane);
     }
+    if (p.comb) {                                                 // uniform (MoE down, one column)
+        // the slot's row times its weight (each product rounded, as the graph's MUL), then the
+        // token's slots added in the tree; every slot of every tile takes part, so each node
+        // sees its two exchanges and the launch leaves the slots empty
+        const int64_t t = blockIdx.z, i = blockIdx.y, nsl = p.n_used + p.n_shared;
+        float wgt;
+        if (!shared) wgt = p.cw[t * p.cw_nb1 + i * p.cw_nb0];
+        else wgt = p.sl ? 1.0f / (1.0f + expf(-p.sl[t * p.sl_nb1])) : 1.0f;
+#pragma unroll
+        for (int j = 0; j < NC; ++j) tot[j] = __fmul_rn(tot[j], wgt);
+        uint32_t * nodes = p.tree + ((size_t)t * (size_t)p.w.ntiles + tile) * (2 * (size_t)nsl * 64);
+        tree_add<NC>(nodes, (int)i, (int)nsl, 1, tot, alive, lane);
+        if (row >= p.w.M || !alive[0]) return;
+        p.dst[t * p.d_nb1 + row] = tot[0];
+        return;
+    }
     if (row >= p.w.M) return;
 #pragma unroll
     for (int j = 0; j < NC; ++j)
@@ -1544,7 +1584,10 @@ hipError_t launch_gemv_fused(int type, const WView & w, const FusedPlan & pl, co
         pl.KS > 65535 || (int64_t)pl.KS * pl.W * pl.spw < w.G ||
         (pl.KS == 1 ? (int64_t)(pl.W - 1) * pl.spw >= w.G : (int64_t)(pl.KS - 1) * pl.W * pl.spw >= w.G) ||
         (pl.KS > 1 && (f.ids || !f.tree || ((uintptr_t)f.tree & 7))) || f.K != w.K ||
-        (f.ids && (pl.nc != 1 || f.n_used < 1 || pl.ntasks != f.n_used * f.T || !f.bad_id)) ||
+        (f.ids && (pl.nc != 1 || f.n_used < 1 || f.n_shared < 0 || f.n_shared > 1 ||
+                   pl.ntasks != (f.n_used + f.n_shared) * f.T || !f.bad_id)) ||
+        (!f.ids && (f.n_shared || f.comb)) || (f.n_shared && (!f.sh_base || (f.glu >= 0 && !f.sh_base2))) ||
+        (f.comb && (pl.KS != 1 || !f.tree || !f.cw || f.glu >= 0 || (f.n_used + f.n_shared) * f.T * w.ntiles > 0x7fffffff)) ||
         (f.glu > QMM_GLU_GEGLU_QUICK) || (f.glu >= 0 && !f.base2))
         return hipErrorInvalidValue;
     FqParams p{};
@@ -1569,6 +1612,16 @@ hipError_t launch_gemv_fused(int type, const WView & w, const FusedPlan & pl, co
         p.dnb1 = f.dnb1;
         p.dnb2 = f.dnb2;
         p.bad_id = f.bad_id;
+        p.n_shared = f.n_shared;
+        p.sh_base = f.sh_base;
+        p.sh_base2 = f.sh_base2;
+        p.comb = f.comb;
+        p.cw = f.cw;
+        p.cw_nb0 = f.cw_nb0;
+        p.cw_nb1 = f.cw_nb1;
+        p.sl = f.sl;
+        p.sl_nb1 = f.sl_nb1;
+        p.d_nb1 = f.d_nb1;
     } else {
         const GemvDense & d = f.dense;
         p.ne11 = d.ne11;
@@ -1585,9 +1638,9 @@ hipError_t launch_gemv_fused(int type, const WView & w, const FusedPlan & pl, co
     }
     const int64_t nwg = pl.ntasks * w.ntiles;
     if (nwg <= 0 || nwg >= 0x7fffffff) return hipErrorInvalidValue;
-    const dim3 g = f.ids ? dim3((unsigned)w.ntiles, (unsigned)f.n_used, (unsigned)f.T)
+    const dim3 g = f.ids ? dim3((unsigned)w.ntiles, (unsigned)(f.n_used + f.n_shared), (unsigned)f.T)
                          : dim3((unsigned)w.ntiles, (unsigned)pl.ntasks, (unsigned)pl.KS);
-    if (w.ntiles > 0x7fffffff || (f.ids ? f.n_used > 65535 || f.T > 65535 : pl.ntasks > 65535))
+    if (w.ntiles > 0x7fffffff || (f.ids ? f.n_used + f.n_shared > 65535 || f.T > 65535 : pl.ntasks > 65535))
         return hipErrorInvalidValue;
     const dim3 b(64 * pl.W);
     const uint32_t lds = (uint32_t)pl.lds;

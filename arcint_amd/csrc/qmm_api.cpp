@@ -1527,6 +1527,147 @@ int qmm_moe_combine(qmm_ctx * ctx, const qmm_tensor * experts, const qmm_tensor 
     return QMM_OK;
 }
 
+// A MoE FFN block after its router in two launches of the fused GEMV (decode token counts):
+//  1. every (slot, token) pair's gate and up rows and their GLU, the shared expert as one more
+//     slot of every token, into a context scratch h [T][slots][M];
+//  2. every pair's down rows from its h column, times its router weight (the shared slot's by
+//     the sigmoid of its gate logit), the token's slots added in the exchange tree, the root
+//     storing dst's row.
+// Replaces MUL_MAT_ID gate, MUL_MAT_ID up, GLU, MUL_MAT_ID down, MUL by the weights, the ADDs
+// over the slots and the shared expert's MUL_MATs, GLU, sigmoid and ADD: five dependent launches
+// of the op-by-op chain (the router stays qmm_moe_topk).  The slot sums are taken in the tree's
+// pairwise order instead of slot by slot.
+static bool glu_op_ok(int32_t op) {
+    return op == QMM_GLU_REGLU || op == QMM_GLU_GEGLU || op == QMM_GLU_SWIGLU || op == QMM_GLU_GEGLU_ERF ||
+           op == QMM_GLU_GEGLU_QUICK;
+}
+
+int qmm_moe_ffn(qmm_ctx * ctx, const qmm_tensor * gate, const qmm_tensor * up, const qmm_tensor * down,
+                const qmm_tensor * x, const qmm_tensor * ids, const qmm_tensor * weights, const qmm_tensor * sgate,
+                const qmm_tensor * sup, const qmm_tensor * sdown, const qmm_tensor * slogit, int32_t glu_op,
+                const qmm_tensor * dst) {
+    if (!ctx) return QMM_ERR_INVALID;
+    if (!glu_op_ok(glu_op)) return fail(ctx, QMM_ERR_UNSUPPORTED, "moe_ffn: GLU op %d", glu_op);
+    if (!gate || !up || !down || !x || !ids || !weights || !dst) return fail(ctx, QMM_ERR_INVALID, "moe_ffn: null tensor");
+    const bool sh = sgate || sup || sdown;
+    if (sh && !(sgate && sup && sdown))
+        return fail(ctx, QMM_ERR_INVALID, "moe_ffn: the shared expert's gate, up and down: all or none");
+    if (slogit && !sh) return fail(ctx, QMM_ERR_INVALID, "moe_ffn: a shared gate logit without a shared expert");
+    char reason[160];
+    WView wg, wu, wd, wsg{}, wsu{}, wsd{};
+    if (!weight_image(gate, true, &wg, reason, sizeof(reason)) || !weight_image(up, true, &wu, reason, sizeof(reason)) ||
+        !weight_image(down, true, &wd, reason, sizeof(reason)))
+        return fail(ctx, QMM_ERR_UNSUPPORTED, "moe_ffn: experts: %s", reason);
+    const int type = gate->type;
+    if (up->type != type || down->type != type || memcmp(gate->ne, up->ne, sizeof(gate->ne)) || gate->ne[3] != 1 ||
+        down->ne[3] != 1)
+        return fail(ctx, QMM_ERR_UNSUPPORTED, "moe_ffn: gate, up and down experts of one type, gate and up of one shape");
+    const int64_t HID = gate->ne[0], M = gate->ne[1], n_as = gate->ne[2], OUT = down->ne[1];
+    if (down->ne[0] != M || down->ne[2] != n_as)
+        return fail(ctx, QMM_ERR_INVALID, "moe_ffn: down experts must be [M, n_out, n_as] with gate's M and n_as");
+    if (n_as > 8192) return fail(ctx, QMM_ERR_UNSUPPORTED, "moe_ffn: more than 8192 experts");
+    if ((HID % 256 || M % 256) && vec_dot_type(type) == QMM_TYPE_Q8_K)
+        return fail(ctx, QMM_ERR_UNSUPPORTED, "moe_ffn: K is not a multiple of 256");
+    if (sh) {
+        if (!weight_image(sgate, true, &wsg, reason, sizeof(reason)) || !weight_image(sup, true, &wsu, reason, sizeof(reason)) ||
+            !weight_image(sdown, true, &wsd, reason, sizeof(reason)))
+            return fail(ctx, QMM_ERR_UNSUPPORTED, "moe_ffn: shared expert: %s", reason);
+        if (sgate->type != type || sup->type != type || sdown->type != type || sgate->ne[0] != HID ||
+            sgate->ne[1] != M || sgate->ne[2] != 1 || sgate->ne[3] != 1 || memcmp(sgate->ne, sup->ne, sizeof(sgate->ne)) ||
+            sdown->ne[0] != M || sdown->ne[1] != OUT || sdown->ne[2] != 1 || sdown->ne[3] != 1)
+            return fail(ctx, QMM_ERR_UNSUPPORTED,
+                        "moe_ffn: the shared expert must have the routed experts' type and matrix shapes (run the ops "
+                        "one by one)");
+    }
+    const int64_t n_used = ids->ne[0], T = ids->ne[1];
+    if (ids->type != QMM_TYPE_I32 || ids->nb[0] != 4 || !ids->buffer || ids->ne[2] != 1 || ids->ne[3] != 1 ||
+        !span_ok(ids) || ids->nb[1] % 4 || ids->offs % 4)
+        return fail(ctx, QMM_ERR_INVALID, "moe_ffn: ids must be i32 [n_used, T] with nb[0] == 4");
+    if (!check_f32(weights) || weights->ne[0] != n_used || weights->ne[1] != T || weights->ne[2] != 1 ||
+        weights->ne[3] != 1 || !span_ok(weights) || weights->nb[1] % 4 || weights->offs % 4)
+        return fail(ctx, QMM_ERR_INVALID, "moe_ffn: weights must be f32 [n_used, T]");
+    // x: [HID, T] or [HID, 1, T]; dst: [n_out, T] or [n_out, 1, T] (token t's row at t dnb floats)
+    const bool xt2 = x->ne[1] == T && x->ne[2] == 1, dt2 = dst->ne[1] == T && dst->ne[2] == 1;
+    if (!check_f32(x) || x->ne[0] != HID || !(xt2 || (x->ne[1] == 1 && x->ne[2] == T)) || x->ne[3] != 1 ||
+        !span_ok(x) || x->nb[1] % 4 || x->nb[2] % 4 || x->offs % 4)
+        return fail(ctx, QMM_ERR_INVALID, "moe_ffn: x must be f32 [K, T] or [K, 1, T] with K the experts' ne0");
+    if (!check_f32(dst) || dst->ne[0] != OUT || !(dt2 || (dst->ne[1] == 1 && dst->ne[2] == T)) || dst->ne[3] != 1 ||
+        !span_ok(dst) || dst->nb[1] % 4 || dst->nb[2] % 4 || dst->offs % 4)
+        return fail(ctx, QMM_ERR_INVALID, "moe_ffn: dst must be f32 [n_out, T] or [n_out, 1, T]");
+    if (slogit && (!check_f32(slogit) || slogit->ne[0] != 1 || slogit->ne[1] != T || slogit->ne[2] != 1 ||
+                   slogit->ne[3] != 1 || !span_ok(slogit) || slogit->nb[1] % 4 || slogit->offs % 4))
+        return fail(ctx, QMM_ERR_INVALID, "moe_ffn: the shared gate logit must be f32 [1, T]");
+    const int64_t nsl = n_used + (sh ? 1 : 0);
+    if (!fused_on() || T >= moe_direct_tokens())
+        return fail(ctx, QMM_ERR_UNSUPPORTED, "moe_ffn: %lld tokens: the fused block takes fewer than %lld (run the "
+                                              "ops one by one)", (long long)T, (long long)moe_direct_tokens());
+    FusedPlan p1, p2;
+    if (!gemv_fused_plan(type, wg, 1, nsl * T, gemv_fused_waves_target(), &p1) ||
+        !gemv_fused_plan(type, wd, 1, nsl * T, gemv_fused_waves_target(), &p2) || nsl > 65535 ||
+        nsl * T * wd.ntiles >= 0x7fffffff)
+        return fail(ctx, QMM_ERR_UNSUPPORTED, "moe_ffn: fused GEMV shape out of range");
+    QMM_HIP(ctx, hipSetDevice(ctx->device));
+    int rc;
+    const size_t hbytes = (size_t)(M * nsl * T) * sizeof(float);
+    if ((rc = ensure(ctx, &ctx->glu, &ctx->glu_cap, hbytes))) return rc;
+    if ((rc = ensure_tree(ctx, (size_t)(T * wd.ntiles * 2 * nsl * 64)))) return rc;
+    float * h = (float *)ctx->glu;
+    const char * idp = (const char *)ids->buffer->ptr + ids->offs;
+
+    FusedGemv f1{};
+    f1.x = f32_cols(x);
+    f1.K = HID;
+    f1.ids = idp;
+    f1.ids_nb0 = 4;
+    f1.ids_nb1 = (int64_t)ids->nb[1];
+    f1.n_used = n_used;
+    f1.T = T;
+    f1.ne11 = 1;
+    f1.n_as = n_as;
+    f1.dnb1 = M;
+    f1.dnb2 = M * nsl;
+    f1.bad_id = ctx->dflags;
+    f1.base2 = wu.base;
+    f1.glu = glu_op;
+    f1.n_shared = sh ? 1 : 0;
+    f1.sh_base = wsg.base;
+    f1.sh_base2 = wsu.base;
+    hipError_t e = launch_gemv_fused(type, wg, p1, f1, h, ctx->sink, ctx->stream, nullptr);
+    if (e != hipSuccess) return fail(ctx, QMM_ERR_DEVICE, "moe_ffn: gate/up launch: %s", hipGetErrorString(e));
+
+    FusedGemv f2{};
+    f2.x.base = (const char *)h;                                  // h column i + t nsl
+    f2.x.ne1 = nsl * T;
+    f2.x.ne2 = 1;
+    f2.x.nb1 = (size_t)M * sizeof(float);
+    f2.x.nb2 = f2.x.nb3 = (size_t)(M * nsl * T) * sizeof(float);
+    f2.K = M;
+    f2.ids = idp;
+    f2.ids_nb0 = 4;
+    f2.ids_nb1 = (int64_t)ids->nb[1];
+    f2.n_used = n_used;
+    f2.T = T;
+    f2.ne11 = nsl;
+    f2.n_as = n_as;
+    f2.bad_id = ctx->dflags;
+    f2.glu = -1;
+    f2.tree = ctx->tree;
+    f2.n_shared = sh ? 1 : 0;
+    f2.sh_base = wsd.base;
+    f2.comb = 1;
+    f2.cw = (const float *)((const char *)weights->buffer->ptr + weights->offs);
+    f2.cw_nb0 = 1;
+    f2.cw_nb1 = (int64_t)(weights->nb[1] / 4);
+    f2.sl = slogit ? (const float *)((const char *)slogit->buffer->ptr + slogit->offs) : nullptr;
+    f2.sl_nb1 = slogit ? (int64_t)(slogit->nb[1] / 4) : 0;
+    f2.d_nb1 = (int64_t)((dt2 ? dst->nb[1] : dst->nb[2]) / 4);
+    float * d = (float *)((uint8_t *)dst->buffer->ptr + dst->offs);
+    e = launch_gemv_fused(type, wd, p2, f2, d, ctx->sink, ctx->stream, nullptr);
+    if (e != hipSuccess) return fail(ctx, QMM_ERR_DEVICE, "moe_ffn: down/combine launch: %s", hipGetErrorString(e));
+    ctx->path = "moe-ffn-fq";
+    return QMM_OK;
+}
+
 // MUL_MAT, MUL_MAT, GLU of an FFN (the chain the reference's fuse_mm_glu takes): the gate and up
 // sums go to a context scratch [2][batch][N][M], then the GLU kernel writes dst.  At GEMV widths
 // with one batch and one weight type a single GEMV launch streams both images (matrix 1 of the

@@ -271,7 +271,20 @@ struct FusedGemv {
     int32_t * bad_id;           // set when an id is >= n_as
     const uint8_t * base2;      // glu >= 0: the up image
     int glu;
-    uint32_t * tree;            // KS > 1: gemv_fused_tree_words words, each kTreeEmpty
+    uint32_t * tree;            // KS > 1: gemv_fused_tree_words words, each kTreeEmpty; combine:
+                                // T x ntiles x 2 (n_used + n_shared) x 64 words
+    // MoE FFN (ids != nullptr): a shared-expert slot n_used of every token (n_shared = 1) with
+    // images sh_base (gate / only matrix) and sh_base2 (up) of w's shape; comb: pair (i, t)'s row
+    // times cw[t cw_nb1 + i cw_nb0] (the shared slot: sigmoid(sl[t sl_nb1]), 1 without sl), the
+    // token's slots added in the tree and stored at dst + t d_nb1
+    int n_shared;
+    const uint8_t * sh_base;
+    const uint8_t * sh_base2;
+    int comb;
+    const float * cw;
+    int64_t cw_nb0, cw_nb1;
+    const float * sl;
+    int64_t sl_nb1, d_nb1;
 };
 struct FusedPlan {
     int nc, W, spw;

@@ -37,7 +37,7 @@ EXPORTS = (
     "qmm_last_path", "qmm_timer_begin", "qmm_timer_end", "qmm_buffer_copy", "qmm_kernel_timing",
     "qmm_kernel_time", "qmm_tensor_pack", "qmm_tensor_unpack", "qmm_describe_mul_mat", "qmm_moe_topk",
     "qmm_moe_combine", "qmm_mul_mat_glu", "qmm_mul_mat_id_glu", "qmm_mul_mat_noalloc", "qmm_kernel_times",
-    "qmm_capture_begin", "qmm_capture_end", "qmm_graph_launch", "qmm_graph_free",
+    "qmm_capture_begin", "qmm_capture_end", "qmm_graph_launch", "qmm_graph_free", "qmm_moe_ffn",
 )
 NOALLOC_SCRATCH_BYTES = 16 << 20     # QMM_NOALLOC_SCRATCH_BYTES
 
@@ -103,6 +103,7 @@ def load() -> C.CDLL:
         L.qmm_mul_mat_noalloc.argtypes = [vp, T, T, T]
         L.qmm_moe_topk.argtypes = [vp, T, T, T, C.c_float, C.c_float]
         L.qmm_moe_combine.argtypes = [vp, T, T, T, T, T]
+        L.qmm_moe_ffn.argtypes = [vp, T, T, T, T, T, T, T, T, T, T, C.c_int32, T]
         L.qmm_mul_mat_glu.argtypes = [vp, T, T, T, T, C.c_int32]
         L.qmm_mul_mat_id_glu.argtypes = [vp, T, T, T, T, T, C.c_int32]
         L.qmm_graph_compute.argtypes = [vp, C.POINTER(CNode), C.c_int]
@@ -342,6 +343,17 @@ class Backend:
         ref = lambda t: C.byref(t.c) if t is not None else None
         self._check(self.L.qmm_moe_combine(self.h, C.byref(experts.c), C.byref(weights.c), ref(shared), ref(gate),
                                            C.byref(dst.c)), "moe_combine")
+
+    def moe_ffn(self, gate: Tensor, up: Tensor, down: Tensor, x: Tensor, ids: Tensor, weights: Tensor, dst: Tensor,
+                shared: tuple | None = None, shared_logit: Tensor | None = None, op: int = GLU_SWIGLU):
+        """A MoE FFN block after its router in two launches: dst[:, t] = sum_j weights[j, t]
+        down[ids[j, t]] glu(gate[ids[j, t]] x_t, up[ids[j, t]] x_t) (+ sigmoid(shared_logit[0, t])
+        sdown glu(sgate x_t, sup x_t) with shared = (sgate, sup, sdown))."""
+        ref = lambda t: C.byref(t.c) if t is not None else None
+        sg, su, sd = shared if shared is not None else (None, None, None)
+        self._check(self.L.qmm_moe_ffn(self.h, C.byref(gate.c), C.byref(up.c), C.byref(down.c), C.byref(x.c),
+                                       C.byref(ids.c), C.byref(weights.c), ref(sg), ref(su), ref(sd), ref(shared_logit),
+                                       op, C.byref(dst.c)), "moe_ffn")
 
     def graph_compute(self, nodes):
         """nodes: list of (op, src0, src1, ids_or_None, dst)."""

@@ -446,6 +446,41 @@ def moe_case(be, qmm, synth, layers, T, args):
     # the layer from one HIP graph holding the eager rotation's first nlog steps (layer copies and
     # logits sets in turn), so the replays touch the same experts and stacks as the eager steps
     g_us = graph_replay_us(be_, [lambda i=i: layer(i) for i in range(nlog)], steps, 16)
+    # the same layer with the expert products, the shared expert and the combine in one call
+    # (qmm_moe_ffn: two launches) after the router, where it takes the token count
+    def layer_fused(i):
+        L = layers.layers[i % nl]
+        router(i)
+        be_.moe_ffn(L["gate"], L["up"], L["down"], xt, ids, wts, out, shared=(L["sgate"], L["sup"], L["sdown"]),
+                    shared_logit=sgl)
+
+    fused = None
+    try:
+        layer_fused(0)
+    except qm.QmmError:                                          # (more tokens than the fused block takes)
+        pass
+    else:
+        fpath = be_.last_path()
+        for i in range(16):
+            layer_fused(i)
+        be_.synchronize()
+        be_.timer_begin()
+        for i in range(steps):
+            layer_fused(i)
+        f_us = be_.timer_end() * 1e3 / steps
+        be_.timer_begin()
+        for i in range(steps):
+            be_.moe_ffn(layers.layers[i % nl]["gate"], layers.layers[i % nl]["up"], layers.layers[i % nl]["down"], xt,
+                        ids, wts, out, shared=(layers.layers[i % nl]["sgate"], layers.layers[i % nl]["sup"],
+                                               layers.layers[i % nl]["sdown"]), shared_logit=sgl)
+        ffn_us = be_.timer_end() * 1e3 / steps
+        fg_us = graph_replay_us(be_, [lambda i=i: layer_fused(i) for i in range(nlog)], steps, 16)
+        fused = {"us_per_layer": round(f_us, 3), "GBs": round(bytes_step / (f_us * 1e-6) / 1e9, 1),
+                 "frac_hbm": round(bytes_step / (f_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                 "op_us": {"router": round(times["router"], 3), "moe_ffn": round(ffn_us, 3)}, "path": fpath,
+                 "us_per_layer_graph": round(fg_us, 3),
+                 "note": "router (qmm_moe_topk) + qmm_moe_ffn: gate/up + SwiGLU of the routed pairs and the shared "
+                         "expert in one launch, down + router weights + sigmoid-gated shared + slot sum in a second"}
     res = {"workload": f"config 3 MoE layer, T={T}: router + gate/up/SwiGLU (512 Q4_K experts, top-10) + down + "
                        f"shared expert + combine, {nl} layers rotated",
            "T": T, "us_per_layer": round(us, 3), "wall_us_per_layer": round(wall * 1e6 / steps, 3),
@@ -454,7 +489,8 @@ def moe_case(be, qmm, synth, layers, T, args):
            "roofline_us": round(bytes_step / (HBM_PEAK_GBS * 1e9) * 1e6, 3),
            "op_us": {n: round(v, 3) for n, v in times.items()}, "paths": paths,
            "us_per_layer_graph": round(g_us, 3),
-           "GBs_graph": round(bytes_step / (g_us * 1e-6) / 1e9, 1)}
+           "GBs_graph": round(bytes_step / (g_us * 1e-6) / 1e9, 1),
+           "fused": fused}
     for t in tmp[0] + tmp[1]:
         be_.free_buffer(t.buf)
     return res

@@ -288,6 +288,29 @@ int    qmm_moe_topk(qmm_ctx * ctx, const qmm_tensor * logits, const qmm_tensor *
  * or neither (NULL). */
 int    qmm_moe_combine(qmm_ctx * ctx, const qmm_tensor * experts, const qmm_tensor * weights,
                        const qmm_tensor * shared, const qmm_tensor * gate, const qmm_tensor * dst);
+/* A MoE FFN block after its router in two launches: llama.cpp's build_moe_ffn from the expert
+ * products on (MUL_MAT_ID gate and up, the GLU, MUL_MAT_ID down, MUL by the weights, the ADDs
+ * over the slots) with an optional shared expert (its gate and up MUL_MATs, GLU, down MUL_MAT,
+ * times the sigmoid of its gate logit, added last), the chain the reference runs node by node
+ * (gate/up/down MUL_MAT_IDs at P01:1189-1248 with the GLU of fuse_mm_glu, the weights' MUL and
+ * ADDs on its element-wise kernels) and that qmm_mul_mat_id_glu, qmm_mul_mat_id, qmm_mul_mat_glu,
+ * qmm_mul_mat and qmm_moe_combine run as five dependent launches:
+ *   dst[:, t] = sum_j weights[j, t] down[ids[j, t]] glu(gate[ids[j, t]] x_t, up[ids[j, t]] x_t)
+ *               (+ sigmoid(shared_logit[0, t]) shared_down glu(shared_gate x_t, shared_up x_t))
+ * with each weight product rounded and the slots' sum taken in a pairwise tree (not slot by
+ * slot: equal to qmm_moe_combine's to float rounding).  gate and up experts [K, M, n_as], down
+ * [M, n_out, n_as], one type; x f32 [K, T] or [K, 1, T]; ids i32 and weights f32 [n_used, T]
+ * (qmm_moe_topk's); the shared expert all three of shared_gate / shared_up [K, M] and
+ * shared_down [M, n_out] of the experts' type, or none; shared_logit f32 [1, T] or NULL (the
+ * shared expert unweighted); dst f32 [n_out, T] or [n_out, 1, T].  A negative id adds nothing,
+ * an id >= n_as adds nothing and raises QMM_ERR_INVALID at the next qmm_synchronize.  Returns
+ * QMM_ERR_UNSUPPORTED (nothing enqueued) at 16 tokens or more (QMM_MOE_DIRECT_T) or when the
+ * shared expert's type or shapes differ from the experts': then run the ops one by one. */
+int    qmm_moe_ffn(qmm_ctx * ctx, const qmm_tensor * gate_exps, const qmm_tensor * up_exps,
+                   const qmm_tensor * down_exps, const qmm_tensor * x, const qmm_tensor * ids,
+                   const qmm_tensor * weights, const qmm_tensor * shared_gate, const qmm_tensor * shared_up,
+                   const qmm_tensor * shared_down, const qmm_tensor * shared_logit, int32_t glu_op,
+                   const qmm_tensor * dst);
 
 /* ---- observability and timing ----------------------------------------- */
 /* Ops that took a slower path than their weight type promises (the reference's DOWNGRADE keys,
@@ -306,7 +329,7 @@ int64_t qmm_downgrades(qmm_ctx * ctx, char * buf, size_t buf_len);
  * streaming GEMM).  qmm_mul_mat_glu: "glu-fused-gemv-fq", "glu-fused-gemv", "glu-fused-gemv-mfma"
  * (gate and up in one launch) or "glu-" + the MUL_MAT path (two products and a GLU kernel).
  * qmm_mul_mat_id_glu: "glu-gemv-id-fq", "glu-gemv-id", "glu-gemv-id-mfma".  The router and the
- * combine: "moe-topk", "moe-combine". */
+ * combine: "moe-topk", "moe-combine"; qmm_moe_ffn: "moe-ffn-fq". */
 const char * qmm_last_path(qmm_ctx * ctx);
 
 /* The launch a qmm_mul_mat with these tensors would make (host only, no

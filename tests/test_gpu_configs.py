@@ -282,3 +282,123 @@ def test_c3_layer_chain(be, orc, bufs, moe_w, T):
     print(f"[err] C3 T={T} layer end to end: max |err| {r['max_abs_err_over_rms']:.2g} rms "
           f"(floored relative {r['floored']:.3g})", flush=True)
     assert r["max_abs_err_over_rms"] <= 1e-2, r
+
+
+# ------------------------------------------------------------------ C3: the fused MoE FFN block
+def c3_chain_inputs(be, bufs, T, seed):
+    g = np.random.default_rng(seed)
+    logits = g.standard_normal((T, E)).astype(np.float32)
+    x = synth.activations(T, HID, seed + 1)
+    sgl = g.standard_normal((T, 1)).astype(np.float32)
+    ids = i32(be, np.zeros((T, N_USED), np.int32), bufs)
+    wts = empty(be, (N_USED, T), bufs)
+    be.moe_topk(f32(be, logits, bufs), ids, wts)
+    return x, sgl, ids, wts
+
+
+@pytest.mark.parametrize("T", [1, 4, 15])
+def test_c3_moe_ffn_routed_against_op_chain(be, bufs, moe_w, T):
+    """qmm_moe_ffn without a shared expert against the op-by-op chain on the GPU
+    (mul_mat_id_glu -> mul_mat_id -> moe_combine) on the same router output: the same per-pair
+    kernels and plans produce the same expert rows, so the two differ only in the order the
+    weighted slots are added (pairwise tree against slot by slot), float rounding of a 10-term sum"""
+    name = f"C3 moe_ffn routed T={T}"
+    say(name)
+    x, _, ids, wts = c3_chain_inputs(be, bufs, T, 400 + T)
+    xt = f32(be, x.reshape(T, 1, HID), bufs)
+    h = empty(be, (FFN, N_USED, T), bufs)
+    ex = empty(be, (HID, N_USED, T), bufs)
+    ref_t = empty(be, (HID, T), bufs)
+    out = empty(be, (HID, T), bufs)
+    (_, wg), (_, wu), (_, wd) = moe_w["gate"], moe_w["up"], moe_w["down"]
+    be.mul_mat_id_glu(wg, wu, xt, ids, h, qmm.GLU_SWIGLU)
+    be.mul_mat_id(wd, qmm.Tensor(h.buf, qmm.F32, (FFN, N_USED, T)), ids, ex)
+    be.moe_combine(ex, wts, ref_t)
+    be.moe_ffn(wg, wu, wd, xt, ids, wts, out)
+    assert be.last_path() == "moe-ffn-fq"
+    be.synchronize()
+    got, ref = be.get_f32(out).reshape(T, HID), be.get_f32(ref_t).reshape(T, HID)
+    r = err_report(got, ref)
+    print(f"[err] {name}: floored {r['floored']:.3g}, max |err| {r['max_abs_err_over_rms']:.2g} rms", flush=True)
+    assert r["floored"] <= 1e-5, r
+
+
+@pytest.mark.parametrize("T", [1, 4, 15])
+@pytest.mark.parametrize("x3", [False, True])
+def test_c3_moe_ffn_with_shared_expert(be, orc, bufs, moe_w, T, x3):
+    """qmm_moe_ffn with the sigmoid-gated shared expert (x as [K, T] or [K, 1, T], dst [n_out, T])
+    against the oracle's whole chain on its own intermediates, the bar of test_c3_layer_chain's
+    end-to-end check (each intermediate quantized again before the next product: 1e-2 of the rms,
+    a wrong expert, weight, slot or shared gate moves outputs by the whole rms)"""
+    from oracle import glu as G
+    from oracle import moe
+    name = f"C3 moe_ffn with shared T={T} x3={x3}"
+    say(name)
+    x, sgl, ids, wts = c3_chain_inputs(be, bufs, T, 420 + T)
+    xt = f32(be, x.reshape(T, 1, HID) if x3 else x, bufs)
+    out = empty(be, (HID, T), bufs)
+    sh = tuple(moe_w[k][1] for k in ("sgate", "sup", "sdown"))
+    be.moe_ffn(moe_w["gate"][1], moe_w["up"][1], moe_w["down"][1], xt, ids, wts, out, shared=sh,
+               shared_logit=f32(be, sgl, bufs))
+    be.synchronize()
+    got = be.get_f32(out).reshape(T, HID)
+    got_ids = be.get_tensor(ids).view(np.int32).reshape(T, N_USED)
+    got_w = be.get_f32(wts).reshape(T, N_USED)
+    rg, ru, rd = moe_w["gate"][0], moe_w["up"][0], moe_w["down"][0]
+    rsg, rsu, rsd = moe_w["sgate"][0], moe_w["sup"][0], moe_w["sdown"][0]
+    xr = x.reshape(T, 1, HID)
+    ref_h = G.glu(qmm.GLU_SWIGLU, orc.mul_mat_id(qmm.Q4_K, rg, FFN, HID, E, xr, got_ids),
+                  orc.mul_mat_id(qmm.Q4_K, ru, FFN, HID, E, xr, got_ids))
+    ref_ex = orc.mul_mat_id(qmm.Q4_K, rd, HID, FFN, E, ref_h.astype(np.float32), got_ids)
+    ref_hs = G.glu(qmm.GLU_SWIGLU, orc.mul_mat(qmm.Q4_K, rsg, FFN, HID, x), orc.mul_mat(qmm.Q4_K, rsu, FFN, HID, x))
+    ref_ys = orc.mul_mat(qmm.Q4_K, rsd, HID, FFN, ref_hs.astype(np.float32))
+    ref = moe.combine(ref_ex, got_w, ref_ys, sgl[:, 0])
+    r = err_report(got, ref)
+    print(f"[err] {name}: max |err| {r['max_abs_err_over_rms']:.2g} rms (floored relative {r['floored']:.3g})",
+          flush=True)
+    assert r["max_abs_err_over_rms"] <= 1e-2, r
+    # the shared expert unweighted (no logit): its rows enter with weight 1
+    out1 = empty(be, (HID, T), bufs)
+    be.moe_ffn(moe_w["gate"][1], moe_w["up"][1], moe_w["down"][1], xt, ids, wts, out1, shared=sh)
+    be.synchronize()
+    r1 = err_report(be.get_f32(out1).reshape(T, HID), moe.combine(ref_ex, got_w, ref_ys, np.full(T, np.inf)))
+    assert r1["max_abs_err_over_rms"] <= 1e-2, r1
+
+
+def test_c3_moe_ffn_bad_ids_and_limits(be, bufs, moe_w):
+    """a negative id adds nothing (the other slots still meet in the tree: a following call
+    finds every tree slot empty again), an id >= n_as adds nothing and raises at synchronize, and
+    16 tokens are refused with nothing enqueued"""
+    T = 3
+    say("C3 moe_ffn bad ids")
+    x, _, ids, wts = c3_chain_inputs(be, bufs, T, 440)
+    xt = f32(be, x, bufs)
+    (_, wg), (_, wu), (_, wd) = moe_w["gate"], moe_w["up"], moe_w["down"]
+    idn = be.get_tensor(ids).view(np.int32).reshape(T, N_USED).copy()
+    wn = be.get_f32(wts).reshape(T, N_USED).copy()
+    out_ok = empty(be, (HID, T), bufs)
+    be.moe_ffn(wg, wu, wd, xt, ids, wts, out_ok)
+    bad = idn.copy()
+    bad[0, 3] = -1
+    bad[2, 0] = -7
+    wz = wn.copy()
+    wz[0, 3] = 0.0
+    wz[2, 0] = 0.0
+    out_neg, out_zero = empty(be, (HID, T), bufs), empty(be, (HID, T), bufs)
+    be.moe_ffn(wg, wu, wd, xt, i32(be, bad, bufs), wts, out_neg)
+    be.moe_ffn(wg, wu, wd, xt, ids, f32(be, wz, bufs), out_zero)
+    be.synchronize()
+    got_neg, got_zero = be.get_f32(out_neg).reshape(T, HID), be.get_f32(out_zero).reshape(T, HID)
+    r = err_report(got_neg, got_zero)
+    assert r["floored"] <= 1e-5, r                     # a dropped slot is a zero-weighted one
+    assert np.array_equal(be.get_f32(out_ok).reshape(T, HID)[1], got_neg[1])   # token 1 untouched
+    over = idn.copy()
+    over[1, 2] = E
+    be.moe_ffn(wg, wu, wd, xt, i32(be, over, bufs), wts, empty(be, (HID, T), bufs))
+    with pytest.raises(qmm.QmmError):
+        be.synchronize()
+    T16 = 16
+    x16 = f32(be, synth.activations(T16, HID, 441), bufs)
+    with pytest.raises(qmm.QmmError):
+        be.moe_ffn(wg, wu, wd, x16, i32(be, np.zeros((T16, N_USED), np.int32), bufs), empty(be, (N_USED, T16), bufs),
+                   empty(be, (HID, T16), bufs))
