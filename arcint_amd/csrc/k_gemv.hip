@@ -1198,7 +1198,9 @@ int env_int(const char * name, int dflt) {
 //  * a MoE FFN block's two products (qmm_moe_ffn): pairs may add a shared-expert slot (slot
 //    n_used of every token, its own images, no id), and the down product combines: each pair's
 //    row is scaled by its router weight (the shared slot's by the sigmoid of its gate logit),
-//    the token's slots meet in the exchange tree, and the root stores the token's output row.
+//    the token's slots meet in the exchange tree, and the root stores the token's output row;
+//    the gate/up launch may rank the tokens' router logits itself (ROUTE: the work-group's first
+//    wave runs topk_wave before the weight stream, whose addresses need the expert).
 constexpr int kFqSlot = 320;   // one (group, column): 256 codes, 8 f32 scales at 256, 16 i16 sums at 288
 constexpr int kFqMaxWaves = 16;
 
@@ -1245,6 +1247,16 @@ struct FqParams {
     int64_t cw_nb0, cw_nb1;
     const float * sl;
     int64_t sl_nb1;
+    // MoE FFN with its router (the ROUTE kernel): the first wave of every work-group ranks its
+    // token's logits (lg + t lg_nb1, n_expert of them) and takes its slot's expert from the
+    // ranking; the work-groups of tile 0, slot 0 store the token's ids and weights (ids + t
+    // ids_nb1 bytes, wout + t wout_nb1 floats) for the down launch
+    const float * lg;
+    int64_t lg_nb1;
+    int n_expert;
+    float cmin, cmax;
+    float * wout;
+    int64_t wout_nb1;
 };
 
 // The K slices of a tile add their sums v[j] (column j, this lane's row) up a pairwise tree
@@ -1352,7 +1364,7 @@ __device__ __forceinline__ void quant_slot(float (&v)[4], uint8_t * slot, int la
 // A work-group is W waves on one 64-row tile of one task, wave w streaming groups
 // [w spw, w spw + spw) (dot4_stages with one K slice).  LDS: the waves' slots [W][spw][NC], then,
 // after the stream, the waves' sums [W][NV][64].
-template <int TYPE, int NC>
+template <int TYPE, int NC, bool ROUTE = false>
 __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
     using T = GV<TYPE>;
     constexpr int NL = T::NL, NST = T::NST;
@@ -1373,7 +1385,25 @@ __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
     if (p.ids) {
         const int64_t t = blockIdx.z, i = blockIdx.y;
         shared = i >= p.n_used;                                   // uniform: the shared expert's slot
-        const int32_t e = shared ? 0 : *reinterpret_cast<const int32_t *>(p.ids + t * p.ids_nb1 + i * p.ids_nb0);
+        int32_t e = 0;
+        if constexpr (ROUTE) {
+            __shared__ uint32_t r_key[1024];
+            __shared__ int r_exp[1024];
+            __shared__ float r_p[32];
+            __shared__ int32_t r_id[32];
+            __shared__ float r_w[32];
+            if (wave == 0)
+                topk_wave_any(p.lg + t * p.lg_nb1, p.n_expert, (int)p.n_used, p.cmin, p.cmax, lane, r_key, r_exp, r_p,
+                              r_id, r_w);
+            __syncthreads();
+            if (!shared) e = r_id[i];
+            if (tile == 0 && i == 0 && wave == 0 && lane < p.n_used) {
+                reinterpret_cast<int32_t *>(const_cast<char *>(p.ids) + t * p.ids_nb1)[lane] = r_id[lane];
+                p.wout[t * p.wout_nb1 + lane] = r_w[lane];
+            }
+        } else if (!shared) {
+            e = *reinterpret_cast<const int32_t *>(p.ids + t * p.ids_nb1 + i * p.ids_nb0);
+        }
         const int64_t doff = t * p.dnb2 + i * p.dnb1;
         if (e < 0 || e >= p.n_as) {                                // uniform: a zero row
             if (wave == 0 && e >= p.n_as && tile == 0 && lane == 0) *p.bad_id = 1;
@@ -1588,6 +1618,8 @@ hipError_t launch_gemv_fused(int type, const WView & w, const FusedPlan & pl, co
                    pl.ntasks != (f.n_used + f.n_shared) * f.T || !f.bad_id)) ||
         (!f.ids && (f.n_shared || f.comb)) || (f.n_shared && (!f.sh_base || (f.glu >= 0 && !f.sh_base2))) ||
         (f.comb && (pl.KS != 1 || !f.tree || !f.cw || f.glu >= 0 || (f.n_used + f.n_shared) * f.T * w.ntiles > 0x7fffffff)) ||
+        (f.lg && (!f.ids || f.comb || !f.wout || f.n_expert < 1 || f.n_expert > 1024 || f.n_used > 32 ||
+                  f.n_used > f.n_expert || f.ids_nb0 != 4 || f.n_as != f.n_expert)) ||
         (f.glu > QMM_GLU_GEGLU_QUICK) || (f.glu >= 0 && !f.base2))
         return hipErrorInvalidValue;
     FqParams p{};
@@ -1622,6 +1654,13 @@ hipError_t launch_gemv_fused(int type, const WView & w, const FusedPlan & pl, co
         p.sl = f.sl;
         p.sl_nb1 = f.sl_nb1;
         p.d_nb1 = f.d_nb1;
+        p.lg = f.lg;
+        p.lg_nb1 = f.lg_nb1;
+        p.n_expert = f.n_expert;
+        p.cmin = f.cmin;
+        p.cmax = f.cmax;
+        p.wout = f.wout;
+        p.wout_nb1 = f.wout_nb1;
     } else {
         const GemvDense & d = f.dense;
         p.ne11 = d.ne11;
@@ -1649,6 +1688,7 @@ hipError_t launch_gemv_fused(int type, const WView & w, const FusedPlan & pl, co
     else __VA_ARGS__<<<g, b, lds, s>>>(p);                                                          \
     return hipGetLastError();
 #define QMM_FQ(T)                                                                                   \
+    if (f.lg) { QMM_FQ_K(k_gemv_fq<T, 1, true>) }                                                   \
     if (pl.nc == 1) { QMM_FQ_K(k_gemv_fq<T, 1>) }                                                   \
     QMM_FQ_K(k_gemv_fq<T, 2>)
     switch (type) {

@@ -133,43 +133,9 @@ __global__ __launch_bounds__(kRouteThreads) void k_quant_route(F32Cols src, int6
 }
 
 // ---- the router: softmax -> top-k -> normalized weights ------------------------------------
-// Role of the reference's fused router (kernel_topk_moe_softmax_norm, P09:899-1000), which
-// replaces llama.cpp's gating chain SOFT_MAX, ARGSORT (desc), VIEW, GET_ROWS, SUM_ROWS, CLAMP,
-// DIV (matched at P02:786-821); the selection here is a filter and a count, not repeated arg-max
-// rounds.  One wave per token (a one-wave work-group); lane l holds the logits of the NPER
-// consecutive experts [l NPER, (l + 1) NPER).  The order is the reference's: the float32 values
-// e = exp(x - max) it ranks (P09:935-966), equal values to the lower expert, so two distinct
-// logits whose float32 exp is equal tie (as ggml's SOFT_MAX -> ARGSORT ranks float32
-// probabilities):
-//  1. each e becomes a 32-bit key, its bits + 1 (e >= 0, so the bits are in e's order; an exp
-//     that underflows to 0 still ranks above the padding); padding gets key 0;
-//  2. the filter: tau0 = the k-th largest of the 64 lanes' largest keys, found most-significant
-//     bit first (32 steps of one ballot).  The lanes holding the k largest maxima hold k keys
-//     >= tau0, so every winner is >= tau0;
-//  3. the candidates (keys >= tau0; usually a few more than k) go to LDS at the offsets of a
-//     scan of the lanes' counts, in expert order;
-//  4. each candidate counts the candidates ahead of it (larger key, or equal key and lower
-//     expert): those with fewer than k ahead win, at that rank.
-// Weights: exp(x - max) / sum over all experts (a wave sum), divided by the winners' sum, taken
-// in rank order and clamped to [cmin, cmax].
-
-
-// the sum over lanes 0 .. lane of v (inclusive), by shuffles
-__device__ __forceinline__ int lane_scan(int v, int lane) {
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const int u = __shfl_up(v, d, 64);
-        if (lane >= d) v += u;
-    }
-    return v;
-}
-
-__device__ __forceinline__ float wave_sum_f(float v) {
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) v += __shfl_xor(v, d, 64);
-    return v;
-}
-
+// One wave per token (a one-wave work-group) runs topk_wave (qmm_device.h: the role of the
+// reference's fused router, P09:899-1000); the fused MoE FFN's gate/up launch runs the same
+// function in each work-group's first wave.
 constexpr int kTopkMaxExperts = 1024;
 
 template <int NPER>
@@ -177,78 +143,10 @@ __global__ __launch_bounds__(64) void k_topk(TopkArgs a) {
     __shared__ uint32_t cand_key[kTopkMaxExperts];
     __shared__ int cand_exp[kTopkMaxExperts];
     __shared__ float ranked_p[32];
-    const int lane = threadIdx.x;
     const int64_t t = blockIdx.x;
-    const float * x = reinterpret_cast<const float *>(a.logits + t * a.nbl1);
-    const int e0 = lane * NPER, k = a.k;
-    float v[NPER];
-    uint32_t key[NPER];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < NPER; ++j) {
-        v[j] = e0 + j < a.n_expert ? x[e0 + j] : -INFINITY;
-        mx = fmaxf(mx, v[j]);
-    }
-    const float m = wave_max(mx);
-    float part = 0.0f;
-    uint32_t kmax = 0;
-#pragma unroll
-    for (int j = 0; j < NPER; ++j) {
-        const bool live = e0 + j < a.n_expert;
-        const float e = live ? expf(v[j] - m) : 0.0f;
-        part += e;
-        key[j] = live ? __builtin_bit_cast(uint32_t, e) + 1u : 0u;
-        kmax = key[j] > kmax ? key[j] : kmax;
-    }
-    const float S = wave_sum_f(part);
-    // 2. tau0: the largest value with at least k lane maxima at or above it
-    uint32_t tau0 = 0;
-    for (int b = 31; b >= 0; --b) {
-        const uint32_t c = tau0 | (1u << b);
-        if (__popcll(__ballot(kmax >= c)) >= k) tau0 = c;
-    }
-    // 3. the candidates into LDS, in expert order
-    int nc = 0;
-#pragma unroll
-    for (int j = 0; j < NPER; ++j) nc += key[j] >= tau0;
-    int slot = lane_scan(nc, lane) - nc;
-    const int ncand = __shfl(slot + nc, 63, 64);
-#pragma unroll
-    for (int j = 0; j < NPER; ++j) {
-        if (key[j] >= tau0) {
-            cand_key[slot] = key[j];
-            cand_exp[slot] = e0 + j;
-            ++slot;
-        }
-    }
-    __syncthreads();
-    // 4. each candidate's rank; the first k are the winners (their probabilities summed in
-    // rank order below)
-    int my_rank[kTopkMaxExperts / 64], my_exp[kTopkMaxExperts / 64];
-    float my_p[kTopkMaxExperts / 64];
-    int nmine = 0;
-    for (int c = lane; c < ncand; c += 64) {
-        const uint32_t ku = cand_key[c];
-        const int ke = cand_exp[c];
-        int r = 0;
-        for (int i = 0; i < ncand && r < k; ++i) r += cand_key[i] > ku || (cand_key[i] == ku && cand_exp[i] < ke);
-        if (r < k) {
-            const float p = expf(x[ke] - m) / S;
-            ranked_p[r] = p;
-            my_rank[nmine] = r;
-            my_exp[nmine] = ke;
-            my_p[nmine] = p;
-            ++nmine;
-        }
-    }
-    __syncthreads();
-    float wsum = 0.0f;
-    for (int i = 0; i < k; ++i) wsum += ranked_p[i];               // uniform, in rank order
-    const float cl = fminf(fmaxf(wsum, a.cmin), a.cmax);
-    for (int q = 0; q < nmine; ++q) {
-        reinterpret_cast<int32_t *>(a.ids + t * a.nbi1)[my_rank[q]] = my_exp[q];
-        reinterpret_cast<float *>(a.w + t * a.nbw1)[my_rank[q]] = my_p[q] / cl;
-    }
+    topk_wave<NPER>(reinterpret_cast<const float *>(a.logits + t * a.nbl1), a.n_expert, a.k, a.cmin, a.cmax,
+                    (int)threadIdx.x, cand_key, cand_exp, ranked_p, reinterpret_cast<int32_t *>(a.ids + t * a.nbi1),
+                    reinterpret_cast<float *>(a.w + t * a.nbw1));
 }
 
 // ---- the combine: dst[:, t] = sum_j w[j, t] experts[:, j, t] (+ shared[:, t] sigmoid(g[t]))

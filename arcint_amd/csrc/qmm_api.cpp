@@ -1527,26 +1527,30 @@ int qmm_moe_combine(qmm_ctx * ctx, const qmm_tensor * experts, const qmm_tensor 
     return QMM_OK;
 }
 
-// A MoE FFN block after its router in two launches of the fused GEMV (decode token counts):
+// A MoE FFN block in two launches of the fused GEMV (decode token counts):
 //  1. every (slot, token) pair's gate and up rows and their GLU, the shared expert as one more
-//     slot of every token, into a context scratch h [T][slots][M];
+//     slot of every token, into a context scratch h [T][slots][M] (with the router's logits:
+//     every work-group first ranks its token, and tile 0 of slot 0 stores the ids and weights);
 //  2. every pair's down rows from its h column, times its router weight (the shared slot's by
 //     the sigmoid of its gate logit), the token's slots added in the exchange tree, the root
 //     storing dst's row.
 // Replaces MUL_MAT_ID gate, MUL_MAT_ID up, GLU, MUL_MAT_ID down, MUL by the weights, the ADDs
 // over the slots and the shared expert's MUL_MATs, GLU, sigmoid and ADD: five dependent launches
-// of the op-by-op chain (the router stays qmm_moe_topk).  The slot sums are taken in the tree's
-// pairwise order instead of slot by slot.
+// of the op-by-op chain, six with the router.  The slot sums are taken in the tree's pairwise
+// order instead of slot by slot.
 static bool glu_op_ok(int32_t op) {
     return op == QMM_GLU_REGLU || op == QMM_GLU_GEGLU || op == QMM_GLU_SWIGLU || op == QMM_GLU_GEGLU_ERF ||
            op == QMM_GLU_GEGLU_QUICK;
 }
 
-int qmm_moe_ffn(qmm_ctx * ctx, const qmm_tensor * gate, const qmm_tensor * up, const qmm_tensor * down,
-                const qmm_tensor * x, const qmm_tensor * ids, const qmm_tensor * weights, const qmm_tensor * sgate,
-                const qmm_tensor * sup, const qmm_tensor * sdown, const qmm_tensor * slogit, int32_t glu_op,
-                const qmm_tensor * dst) {
+int qmm_moe_ffn(qmm_ctx * ctx, const qmm_moe_ffn_args * args) {
     if (!ctx) return QMM_ERR_INVALID;
+    if (!args) return fail(ctx, QMM_ERR_INVALID, "moe_ffn: null args");
+    const qmm_tensor *gate = args->gate_exps, *up = args->up_exps, *down = args->down_exps, *x = args->x;
+    const qmm_tensor *ids = args->ids, *weights = args->weights, *dst = args->dst, *logits = args->logits;
+    const qmm_tensor *sgate = args->shared_gate, *sup = args->shared_up, *sdown = args->shared_down;
+    const qmm_tensor * slogit = args->shared_logit;
+    const int32_t glu_op = args->glu_op;
     if (!glu_op_ok(glu_op)) return fail(ctx, QMM_ERR_UNSUPPORTED, "moe_ffn: GLU op %d", glu_op);
     if (!gate || !up || !down || !x || !ids || !weights || !dst) return fail(ctx, QMM_ERR_INVALID, "moe_ffn: null tensor");
     const bool sh = sgate || sup || sdown;
@@ -1597,6 +1601,13 @@ int qmm_moe_ffn(qmm_ctx * ctx, const qmm_tensor * gate, const qmm_tensor * up, c
     if (slogit && (!check_f32(slogit) || slogit->ne[0] != 1 || slogit->ne[1] != T || slogit->ne[2] != 1 ||
                    slogit->ne[3] != 1 || !span_ok(slogit) || slogit->nb[1] % 4 || slogit->offs % 4))
         return fail(ctx, QMM_ERR_INVALID, "moe_ffn: the shared gate logit must be f32 [1, T]");
+    if (logits) {
+        if (!check_f32(logits) || logits->ne[0] != n_as || logits->ne[1] != T || logits->ne[2] != 1 ||
+            logits->ne[3] != 1 || !span_ok(logits) || logits->nb[1] % 4 || logits->offs % 4)
+            return fail(ctx, QMM_ERR_INVALID, "moe_ffn: router logits must be f32 [n_as, T]");
+        if (n_as > 1024 || n_used < 1 || n_used > 32 || n_used > n_as)
+            return fail(ctx, QMM_ERR_UNSUPPORTED, "moe_ffn: the router takes n_as <= 1024 and 1 <= n_used <= min(32, n_as)");
+    }
     const int64_t nsl = n_used + (sh ? 1 : 0);
     if (!fused_on() || T >= moe_direct_tokens())
         return fail(ctx, QMM_ERR_UNSUPPORTED, "moe_ffn: %lld tokens: the fused block takes fewer than %lld (run the "
@@ -1632,6 +1643,15 @@ int qmm_moe_ffn(qmm_ctx * ctx, const qmm_tensor * gate, const qmm_tensor * up, c
     f1.n_shared = sh ? 1 : 0;
     f1.sh_base = wsg.base;
     f1.sh_base2 = wsu.base;
+    if (logits) {
+        f1.lg = (const float *)((const char *)logits->buffer->ptr + logits->offs);
+        f1.lg_nb1 = (int64_t)(logits->nb[1] / 4);
+        f1.n_expert = (int)n_as;
+        f1.cmin = args->cmin;
+        f1.cmax = args->cmax;
+        f1.wout = (float *)((char *)weights->buffer->ptr + weights->offs);
+        f1.wout_nb1 = (int64_t)(weights->nb[1] / 4);
+    }
     hipError_t e = launch_gemv_fused(type, wg, p1, f1, h, ctx->sink, ctx->stream, nullptr);
     if (e != hipSuccess) return fail(ctx, QMM_ERR_DEVICE, "moe_ffn: gate/up launch: %s", hipGetErrorString(e));
 

@@ -296,4 +296,163 @@ __device__ __forceinline__ void quant_q8_K_at(const F32Cols & src, int64_t K, in
 
 #pragma clang fp contract(fast)
 
+
+// ---- the MoE router of one token, run by one wave -----------------------------------------
+// Role of the reference's fused router (kernel_topk_moe_softmax_norm, P09:899-1000), which
+// replaces llama.cpp's gating chain SOFT_MAX, ARGSORT (desc), VIEW, GET_ROWS, SUM_ROWS, CLAMP,
+// DIV (matched at P02:786-821); the selection here is a filter and a count, not repeated arg-max
+// rounds.  Lane l holds the logits of the NPER consecutive experts [l NPER, (l + 1) NPER).  The
+// order is the reference's: the float32 values e = exp(x - max) it ranks (P09:935-966), equal
+// values to the lower expert, so two distinct logits whose float32 exp is equal tie (as ggml's
+// SOFT_MAX -> ARGSORT ranks float32 probabilities):
+//  1. each e becomes a 32-bit key, its bits + 1 (e >= 0, so the bits are in e's order; an exp
+//     that underflows to 0 still ranks above the padding); padding gets key 0;
+//  2. the filter: tau0 = the k-th largest of the 64 lanes' largest keys, found most-significant
+//     bit first (32 steps of one ballot).  The lanes holding the k largest maxima hold k keys
+//     >= tau0, so every winner is >= tau0;
+//  3. the candidates (keys >= tau0; usually a few more than k) go to LDS at the offsets of a
+//     scan of the lanes' counts, in expert order;
+//  4. each candidate counts the candidates ahead of it (larger key, or equal key and lower
+//     expert): those with fewer than k ahead win, at that rank.
+// Weights: exp(x - max) / sum over all experts (a wave sum), divided by the winners' sum, taken
+// in rank order and clamped to [cmin, cmax].  Only the calling wave takes part (its LDS traffic
+// is ordered by wave-scope fences, no work-group barrier): cand_key / cand_exp hold n_expert
+// entries, ranked_p 32; the winners go to rid[r] (expert) and rw[r] (weight), r < k.
+
+// the sum over lanes 0 .. lane of v (inclusive), by shuffles
+__device__ __forceinline__ int lane_scan(int v, int lane) {
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int u = __shfl_up(v, d, 64);
+        if (lane >= d) v += u;
+    }
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum_f(float v) {
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) v += __shfl_xor(v, d, 64);
+    return v;
+}
+
+// the wave's LDS writes before this are seen by its loads after it
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int NPER>
+__device__ __forceinline__ void topk_wave(const float * x, int n_expert, int k, float cmin, float cmax, int lane,
+                                          uint32_t * cand_key, int * cand_exp, float * ranked_p, int32_t * rid,
+                                          float * rw) {
+    const int e0 = lane * NPER;
+    float v[NPER];
+    uint32_t key[NPER];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NPER; ++j) {
+        v[j] = e0 + j < n_expert ? x[e0 + j] : -INFINITY;
+        mx = fmaxf(mx, v[j]);
+    }
+    const float m = wave_max(mx);
+    float part = 0.0f;
+    uint32_t kmax = 0;
+#pragma unroll
+    for (int j = 0; j < NPER; ++j) {
+        const bool live = e0 + j < n_expert;
+        const float e = live ? expf(v[j] - m) : 0.0f;
+        part += e;
+        key[j] = live ? __builtin_bit_cast(uint32_t, e) + 1u : 0u;
+        kmax = key[j] > kmax ? key[j] : kmax;
+    }
+    const float S = wave_sum_f(part);
+    // 2. tau0: the largest value with at least k lane maxima at or above it
+    uint32_t tau0 = 0;
+    for (int b = 31; b >= 0; --b) {
+        const uint32_t c = tau0 | (1u << b);
+        if (__popcll(__ballot(kmax >= c)) >= k) tau0 = c;
+    }
+    // 3. the candidates into LDS, in expert order
+    int nc = 0;
+#pragma unroll
+    for (int j = 0; j < NPER; ++j) nc += key[j] >= tau0;
+    int slot = lane_scan(nc, lane) - nc;
+    const int ncand = __shfl(slot + nc, 63, 64);
+#pragma unroll
+    for (int j = 0; j < NPER; ++j) {
+        if (key[j] >= tau0) {
+            cand_key[slot] = key[j];
+            cand_exp[slot] = e0 + j;
+            ++slot;
+        }
+    }
+    wave_lds_sync();
+    // 4. each candidate's rank; the first k are the winners (their probabilities summed in
+    // rank order).  A winner's probability is its e / S: e is its key less one, as bits.
+    if (ncand <= 64) {                                            // uniform: one candidate per lane
+        // (the candidates broadcast from registers by readlane: no LDS round trip per compare)
+        const uint32_t ck = lane < ncand ? cand_key[lane] : 0u;
+        const int ce = lane < ncand ? cand_exp[lane] : 0;
+        int r = 0;
+        for (int i = 0; i < ncand; ++i) {                         // uniform
+            const uint32_t ki = (uint32_t)__builtin_amdgcn_readlane((int)ck, i);
+            const int ei = __builtin_amdgcn_readlane(ce, i);
+            r += ki > ck || (ki == ck && ei < ce);
+        }
+        const bool win = lane < ncand && r < k;
+        const float pr = win ? __builtin_bit_cast(float, ck - 1u) / S : 0.0f;
+        float wsum = 0.0f;
+        for (int i = 0; i < k; ++i) {                             // uniform, in rank order
+            const uint64_t at = __ballot(win && r == i);
+            wsum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pr),
+                                                                        at ? (int)__builtin_ctzll(at) : 0));
+        }
+        const float cl = fminf(fmaxf(wsum, cmin), cmax);
+        if (win) {
+            rid[r] = ce;
+            rw[r] = pr / cl;
+        }
+        return;
+    }
+    constexpr int kMaxMine = 1024 / 64;
+    int my_rank[kMaxMine], my_exp[kMaxMine];
+    float my_p[kMaxMine];
+    int nmine = 0;
+    for (int c = lane; c < ncand; c += 64) {
+        const uint32_t ku = cand_key[c];
+        const int ke = cand_exp[c];
+        int r = 0;
+        for (int i = 0; i < ncand && r < k; ++i) r += cand_key[i] > ku || (cand_key[i] == ku && cand_exp[i] < ke);
+        if (r < k) {
+            const float p = __builtin_bit_cast(float, ku - 1u) / S;
+            ranked_p[r] = p;
+            my_rank[nmine] = r;
+            my_exp[nmine] = ke;
+            my_p[nmine] = p;
+            ++nmine;
+        }
+    }
+    wave_lds_sync();
+    float wsum = 0.0f;
+    for (int i = 0; i < k; ++i) wsum += ranked_p[i];               // uniform, in rank order
+    const float cl = fminf(fmaxf(wsum, cmin), cmax);
+    for (int q = 0; q < nmine; ++q) {
+        rid[my_rank[q]] = my_exp[q];
+        rw[my_rank[q]] = my_p[q] / cl;
+    }
+}
+
+// topk_wave for any n_expert <= 1024 (lanes hold ceil(n_expert / 64) rounded up to a power of 2)
+__device__ __forceinline__ void topk_wave_any(const float * x, int n_expert, int k, float cmin, float cmax, int lane,
+                                              uint32_t * cand_key, int * cand_exp, float * ranked_p, int32_t * rid,
+                                              float * rw) {
+    const int nper = (n_expert + 63) / 64;
+    if (nper <= 1) topk_wave<1>(x, n_expert, k, cmin, cmax, lane, cand_key, cand_exp, ranked_p, rid, rw);
+    else if (nper <= 2) topk_wave<2>(x, n_expert, k, cmin, cmax, lane, cand_key, cand_exp, ranked_p, rid, rw);
+    else if (nper <= 4) topk_wave<4>(x, n_expert, k, cmin, cmax, lane, cand_key, cand_exp, ranked_p, rid, rw);
+    else if (nper <= 8) topk_wave<8>(x, n_expert, k, cmin, cmax, lane, cand_key, cand_exp, ranked_p, rid, rw);
+    else topk_wave<16>(x, n_expert, k, cmin, cmax, lane, cand_key, cand_exp, ranked_p, rid, rw);
+}
+
 }  // namespace qmm

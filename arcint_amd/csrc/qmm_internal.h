@@ -285,6 +285,15 @@ struct FusedGemv {
     int64_t cw_nb0, cw_nb1;
     const float * sl;
     int64_t sl_nb1, d_nb1;
+    // gate/up with the router (lg != nullptr): every work-group's first wave ranks token t's
+    // logits lg + t lg_nb1 (n_expert of them, top n_used, weight sum clamped to [cmin, cmax]);
+    // the ids go to `ids` (written, ids_nb0 == 4) and the weights to wout + t wout_nb1
+    const float * lg;
+    int64_t lg_nb1;
+    int n_expert;
+    float cmin, cmax;
+    float * wout;
+    int64_t wout_nb1;
 };
 struct FusedPlan {
     int nc, W, spw;

@@ -67,6 +67,17 @@ class CNode(C.Structure):
                 ("ids", C.POINTER(CTensor)), ("dst", C.POINTER(CTensor))]
 
 
+# qmm_moe_ffn_args, field for field
+_TP = C.POINTER(CTensor)
+
+
+class CMoeFfn(C.Structure):
+    _fields_ = [("gate_exps", _TP), ("up_exps", _TP), ("down_exps", _TP), ("x", _TP), ("logits", _TP),
+                ("cmin", C.c_float), ("cmax", C.c_float), ("ids", _TP), ("weights", _TP), ("shared_gate", _TP),
+                ("shared_up", _TP), ("shared_down", _TP), ("shared_logit", _TP), ("glu_op", C.c_int32),
+                ("dst", _TP)]
+
+
 _lib = None
 
 
@@ -103,7 +114,7 @@ def load() -> C.CDLL:
         L.qmm_mul_mat_noalloc.argtypes = [vp, T, T, T]
         L.qmm_moe_topk.argtypes = [vp, T, T, T, C.c_float, C.c_float]
         L.qmm_moe_combine.argtypes = [vp, T, T, T, T, T]
-        L.qmm_moe_ffn.argtypes = [vp, T, T, T, T, T, T, T, T, T, T, C.c_int32, T]
+        L.qmm_moe_ffn.argtypes = [vp, C.POINTER(CMoeFfn)]
         L.qmm_mul_mat_glu.argtypes = [vp, T, T, T, T, C.c_int32]
         L.qmm_mul_mat_id_glu.argtypes = [vp, T, T, T, T, T, C.c_int32]
         L.qmm_graph_compute.argtypes = [vp, C.POINTER(CNode), C.c_int]
@@ -345,15 +356,17 @@ class Backend:
                                            C.byref(dst.c)), "moe_combine")
 
     def moe_ffn(self, gate: Tensor, up: Tensor, down: Tensor, x: Tensor, ids: Tensor, weights: Tensor, dst: Tensor,
-                shared: tuple | None = None, shared_logit: Tensor | None = None, op: int = GLU_SWIGLU):
-        """A MoE FFN block after its router in two launches: dst[:, t] = sum_j weights[j, t]
-        down[ids[j, t]] glu(gate[ids[j, t]] x_t, up[ids[j, t]] x_t) (+ sigmoid(shared_logit[0, t])
-        sdown glu(sgate x_t, sup x_t) with shared = (sgate, sup, sdown))."""
-        ref = lambda t: C.byref(t.c) if t is not None else None
+                shared: tuple | None = None, shared_logit: Tensor | None = None, op: int = GLU_SWIGLU,
+                logits: Tensor | None = None, cmin: float = 6.103515625e-5, cmax: float = float("inf")):
+        """A MoE FFN block in two launches: dst[:, t] = sum_j weights[j, t] down[ids[j, t]]
+        glu(gate[ids[j, t]] x_t, up[ids[j, t]] x_t) (+ sigmoid(shared_logit[0, t]) sdown glu(sgate x_t,
+        sup x_t) with shared = (sgate, sup, sdown)).  With logits the router runs inside and ids /
+        weights are written (moe_topk's values)."""
+        ptr = lambda t: C.pointer(t.c) if t is not None else None
         sg, su, sd = shared if shared is not None else (None, None, None)
-        self._check(self.L.qmm_moe_ffn(self.h, C.byref(gate.c), C.byref(up.c), C.byref(down.c), C.byref(x.c),
-                                       C.byref(ids.c), C.byref(weights.c), ref(sg), ref(su), ref(sd), ref(shared_logit),
-                                       op, C.byref(dst.c)), "moe_ffn")
+        a = CMoeFfn(ptr(gate), ptr(up), ptr(down), ptr(x), ptr(logits), cmin, cmax, ptr(ids), ptr(weights), ptr(sg),
+                    ptr(su), ptr(sd), ptr(shared_logit), op, ptr(dst))
+        self._check(self.L.qmm_moe_ffn(self.h, C.byref(a)), "moe_ffn")
 
     def graph_compute(self, nodes):
         """nodes: list of (op, src0, src1, ids_or_None, dst)."""

@@ -132,3 +132,23 @@ def test_no_device_is_an_error_not_a_fallback():
         return                      # no device: the product refuses instead of falling back
     be.close()
     pytest.skip("a device is present")
+
+
+def test_moe_ffn_args_layout():
+    """qmm_moe_ffn_args as the C compiler lays it out (gcc on the header) equals the binding's
+    ctypes structure, field by field"""
+    import shutil
+    import subprocess
+    import tempfile
+    if not shutil.which("gcc"):
+        pytest.skip("no gcc")
+    fields = [f for f, _ in qmm.CMoeFfn._fields_]
+    body = "".join(f'printf("%zu\\n", offsetof(qmm_moe_ffn_args, {f}));' for f in fields)
+    src = ('#include "qmm.h"\n#include <stddef.h>\n#include <stdio.h>\n'
+           f'int main(void) {{ printf("%zu\\n", sizeof(qmm_moe_ffn_args)); {body} return 0; }}\n')
+    with tempfile.TemporaryDirectory() as d:
+        c, exe = os.path.join(d, "l.c"), os.path.join(d, "l")
+        open(c, "w").write(src)
+        subprocess.run(["gcc", "-I" + os.path.join(ROOT, "include"), c, "-o", exe], check=True)
+        got = [int(v) for v in subprocess.run([exe], capture_output=True, text=True, check=True).stdout.split()]
+    assert got == [C.sizeof(qmm.CMoeFfn)] + [getattr(qmm.CMoeFfn, f).offset for f in fields]

@@ -402,3 +402,29 @@ def test_c3_moe_ffn_bad_ids_and_limits(be, bufs, moe_w):
     with pytest.raises(qmm.QmmError):
         be.moe_ffn(wg, wu, wd, x16, i32(be, np.zeros((T16, N_USED), np.int32), bufs), empty(be, (N_USED, T16), bufs),
                    empty(be, (HID, T16), bufs))
+
+
+@pytest.mark.parametrize("T", [1, 4, 15])
+def test_c3_moe_ffn_router_inside(be, bufs, moe_w, T):
+    """qmm_moe_ffn given the router's logits: the ids and weights it writes equal qmm_moe_topk's
+    bit for bit (the same one-wave ranking, run by every work-group of the gate/up launch), and its
+    output equals the call given those ids and weights, bit for bit"""
+    name = f"C3 moe_ffn router inside T={T}"
+    say(name)
+    g = np.random.default_rng(460 + T)
+    logits = f32(be, g.standard_normal((T, E)).astype(np.float32), bufs)
+    x = f32(be, synth.activations(T, HID, 461 + T), bufs)
+    sgl = f32(be, g.standard_normal((T, 1)).astype(np.float32), bufs)
+    sh = tuple(moe_w[k][1] for k in ("sgate", "sup", "sdown"))
+    (_, wg), (_, wu), (_, wd) = moe_w["gate"], moe_w["up"], moe_w["down"]
+    ids_a, w_a = i32(be, np.zeros((T, N_USED), np.int32), bufs), empty(be, (N_USED, T), bufs)
+    ids_b, w_b = i32(be, np.zeros((T, N_USED), np.int32), bufs), empty(be, (N_USED, T), bufs)
+    out_a, out_b = empty(be, (HID, T), bufs), empty(be, (HID, T), bufs)
+    be.moe_topk(logits, ids_a, w_a)
+    be.moe_ffn(wg, wu, wd, x, ids_a, w_a, out_a, shared=sh, shared_logit=sgl)
+    be.moe_ffn(wg, wu, wd, x, ids_b, w_b, out_b, shared=sh, shared_logit=sgl, logits=logits)
+    assert be.last_path() == "moe-ffn-fq"
+    be.synchronize()
+    assert np.array_equal(be.get_tensor(ids_a).view(np.int32), be.get_tensor(ids_b).view(np.int32))
+    assert np.array_equal(be.get_f32(w_a).view(np.uint32), be.get_f32(w_b).view(np.uint32))
+    assert np.array_equal(be.get_f32(out_a).view(np.uint32), be.get_f32(out_b).view(np.uint32))
