@@ -1450,8 +1450,10 @@ __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
     const uint8_t * tbg = tile_group(w1, mat, tile, 0);
     const uint8_t * tbu = glu ? tile_group(w2, mat, tile, 0) : tbg;
     const size_t tgs = (size_t)p.w.tg;
-    uint4 B[NL];
-    auto load_stage = [&](int s) {                                // past the last stage: the sink
+    // Two-stage types (Q6_K, Q8_0): both stages of a group are requested together (B, then B1),
+    // so a wave of one group waits for one weight round trip, not two.
+    uint4 B[NL], B1[NL];
+    auto load_into = [&](uint4 (&dst)[NL], int s) {               // past the last stage: the sink
         const uint8_t * tg = p.sink;
         int st = 0;
         if (s < ST) {
@@ -1459,7 +1461,11 @@ __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
             tg = (s < S ? tbg : tbu) + (size_t)stage_group(ga, sl, NST) * tgs;
             st = sl % NST;
         }
-        T::load(B, tg, st, lane);
+        T::load(dst, tg, st, lane);
+    };
+    auto load_stage = [&](int s) {
+        load_into(B, s);
+        if constexpr (NST == 2) load_into(B1, s + 1);
     };
     // the first group's activations are requested ahead of the weights: behind the weight
     // stream in the memory queues they would arrive with its end and hold every dot back
@@ -1499,9 +1505,21 @@ __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
             x.d[j] = reinterpret_cast<const float *>(sj + 256);
             x.s[j] = reinterpret_cast<const int16_t *>(sj + 288);
         }
-        if (s < S) T::dot(B, sl % NST, x, nc, acc, st_state);
-        else T::dot(B, sl % NST, x, nc, accu, st_state);
-        if (s + 1 < ST) load_stage(s + 1);                        // (nothing past the last stage)
+        if constexpr (NST == 2) {                                 // (ST is even: whole groups)
+            if (s < S) {
+                T::dot(B, 0, x, nc, acc, st_state);
+                T::dot(B1, 1, x, nc, acc, st_state);
+            } else {
+                T::dot(B, 0, x, nc, accu, st_state);
+                T::dot(B1, 1, x, nc, accu, st_state);
+            }
+            ++s;
+            if (s + 1 < ST) load_stage(s + 1);                    // (nothing past the last stage)
+        } else {
+            if (s < S) T::dot(B, sl % NST, x, nc, acc, st_state);
+            else T::dot(B, sl % NST, x, nc, accu, st_state);
+            if (s + 1 < ST) load_stage(s + 1);                    // (nothing past the last stage)
+        }
     }
     // the W waves added in a fixed order: the gate (or only) sums tot[], with the GLU the up sums
     // totu[]; act(gate) * up once the K slices have met

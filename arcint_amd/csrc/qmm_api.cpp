@@ -936,13 +936,14 @@ static int64_t fused_small_tgroups() {
 
 // Dense products of 1-2 columns may also split K over work-groups of the fused kernel (its
 // K-slice tree): one launch instead of the pre-pass and the GEMV.  Measured per op (bench,
-// one box): one column of every type but Q6_K gains (config 2's Q4_K 17408 x 5120 12.6 ->
+// one box): one column of every type gains or ties (config 2's Q4_K 17408 x 5120 12.6 ->
 // 11.6 us, Q5_K 14.7 -> 13.8, config 4's Q8_0 14.3 -> 13.9, Q4_0 4096 x 4096 7.0-8.9 -> 6.0; the
-// IQ4 types within 1 %); Q6_K (two stages a group) loses 2-3 % (16.4 -> 16.8 us, the output head
-// 100.0 -> 101.9) and so do two columns on large images (Q8_0 14336 x 4096 15.3 -> 15.7, IQ4_XS
-// 13.0-13.5 -> 14.2; with 8 waves a work-group Q8_0 gains at two columns too, 15.5 -> 14.8 us,
-// while IQ4_XS ties and Q4_K loses 2-3 %).  So: one column of any type but Q6_K, two of Q8_0,
-// and 1-2 columns of any type for images up to QMM_GEMV_FQS_MAX_KB (16 MiB) of one matrix;
+// IQ4 types within 1 %; Q6_K, two stages a group requested together, 16.6 -> 16.4 us and the
+// output head 99.9 -> 99.2); two columns on large images lose (Q6_K 5120 x 17408 18.8 -> 20.3,
+// Q8_0 14336 x 4096 15.3 -> 15.7, IQ4_XS 13.0-13.5 -> 14.2; with 8 waves a work-group Q8_0 gains
+// at two columns too, 15.5 -> 14.8 us, while IQ4_XS ties and Q4_K loses 2-3 %).  So: one column
+// of any type, two of Q8_0, and 1-2 columns of any type for images up to QMM_GEMV_FQS_MAX_KB
+// (16 MiB) of one matrix;
 // QMM_GEMV_FQS = 0 never, = 1 always;
 // work-groups of QMM_GEMV_FQS_W waves with QMM_GEMV_FQS_SPW groups each (1): 4 waves (Q4_K 11.6
 // us against 12.2-12.3 at 2, 5 and 8; Q5_K 14.1-14.2 against 15.7 at 8), 8 for Q8_0, whose
@@ -955,7 +956,7 @@ static bool fused_split_for(int type, const WView & w, int64_t N) {
     const int mode = env_or("QMM_GEMV_FQS", -1);
     if (mode == 0) return false;
     if (mode > 0) return true;
-    if (N == 1 && type != QMM_TYPE_Q6_K) return true;
+    if (N == 1) return true;
     if (N == 2 && type == QMM_TYPE_Q8_0) return true;            // (14336 x 4096: 15.5 -> 14.8 us)
     const int64_t image = w.ntiles * w.G * (int64_t)w.tg;
     return image <= (int64_t)env_or("QMM_GEMV_FQS_MAX_KB", 16384) * 1024;
