@@ -1,39 +1,33 @@
-// k_gemm3.hip - prefill GEMM for the block types with one float scale per 32 weights (Q4_0,
-// Q8_0, IQ4_NL) on gfx950 v_mfma_i32_32x32x32_i8, weights streamed by each wave.
+// k_gemm3.hip - the streaming prefill GEMMs on gfx950 v_mfma_i32_32x32x32_i8: Q4_K
+// (k_gemm3_q4k, also the grouped MoE GEMM) and the block types with one float scale per 32
+// weights, Q4_0, Q8_0 and IQ4_NL (k_gemm3_blk), weights streamed by each wave.
 //
-// Role of the reference's int8 prefill GEMM (kernel_mul_mm_kq2d_q4_0_i8, P0099:377-455) and
-// its fp16 tile kernel for Q8_0 (P02:4359-4384), redesigned for CDNA4 and for ggml-cpu's
-// numerics.  ggml's dot for these types is sum_b d_x(b) d_w(b) I_b, a scale per 32-weight
-// block on both sides, so every output takes a float multiply-add per block on top of the
-// block's integer dot I_b: two VALU instructions per output and block, 32 per 32x32x32 MFMA.
-// The VALU, not the MFMA, bounds this GEMM, so the design keeps the SIMDs' VALU issuing:
-//  * a wave owns one 64-row tile of the weight image x one column tile of 32 over one K slice
-//    and streams its weights itself: lane l loads row l's 16 bytes of a block (one coalesced
-//    1 KB buffer load of the image's chunk plane), unpacks them in registers and trades
-//    halves with v_permlane32_swap into the B operands of rows 0-31 and rows 32-63;
+// Role of the reference's int8 prefill GEMMs (kernel_mul_mm_kq2d_q4_0_i8, P0099:377-455;
+// kernel_mul_mm_kq2d_q4_K_i8, P01:1919-2024) and its fp16 tile kernel for Q8_0
+// (P02:4359-4384), redesigned for CDNA4 and for ggml-cpu's numerics.  Both kernels share one
+// frame:
+//  * a wave owns 32 rows (one half of a 64-row image tile) x 64 columns (two column tiles)
+//    over one K slice and streams its rows' weights itself; lane (j, h) supplies row j's k
+//    16 h .. 16 h + 15 of every 32 weights as the MFMA's B operand, and the output lane (j, h)
+//    holds row j, so the lane's own row scales apply with no lane exchanges;
 //  * the activations come from the pre-pass in MFMA A-operand order (1 KB per column tile and
-//    block) with their scales as f32 in MFMA output order; the kU waves of a work-group that
-//    share a K slice (different row tiles, same columns) stage them in LDS once, a stage of
-//    blocks ahead, one barrier per stage;
-//  * Q4_0 codes are unpacked into the high nibble of each byte after flipping bit 3: the int8
-//    byte (q ^ 8) << 4 is 16 (q - 8), with no borrow handling; the sums carry the factor 16,
-//    taken off exactly (a power of two) at the store;
-//  * the MFMA's C input is the bits of the float 12582912 (1.5 * 2^23), so its int32 result
-//    read as a float is 12582912 + I exactly; fma(that, d_w, -12582912 d_w) is I d_w rounded
-//    once and fma(., d_x, acc) accumulates it: two plain f32 FMAs per output and block (on
-//    gfx950 an fp16 source operand, v_fma_mix, halves the FMA issue rate);
-//  * three waves per SIMD (at most 168 registers): work-groups of kU = 4 waves when the tiles
-//    fill the chip, three of them per CU, else work-groups of 3 K slices x kU (12 waves, one
-//    per CU: a work-group's waves go to the CU's SIMDs in turn, so 8-wave groups would leave
-//    room for one group only and 2 waves per SIMD);
-//  * the K slices of a row tile are waves of one work-group: slices 1.. add their sums into LDS
+//    32 weights) with their scales in MFMA output order; the U row-half waves of a K slice
+//    (different rows, same columns) share a stage in LDS (256 weights of both column tiles,
+//    18 KB), loaded by buffer loads that write LDS directly, one stage ahead, one barrier per
+//    stage;
+//  * three waves per SIMD (at most 168 registers): work-groups of 12 waves (U x KS) fill a CU
+//    alone, 4-wave ones go three to a CU (shapes chosen by rounds of work-groups on the chip);
+//  * the K slices of a row half are waves of one work-group: slices 1.. add their sums into LDS
 //    at the end and slice 0 stores, so dst is written once (non-temporal), with no atomics and
 //    no zeroing;
 //  * every load goes through a buffer resource: the wave-uniform address math stays on the
-//    SALU, and reads past a resource's range (the last stage of a row whose groups are not a
-//    whole number of stages) return zeros;
+//    SALU, and reads past a resource's range return zeros;
 //  * work-groups that share weight rows are numbered onto one XCD (work-group b runs on XCD
 //    b % 8), so a row tile's weights come from HBM once and from that XCD's L2 after.
+// ggml's dot for the block types is sum_b d_x(b) d_w(b) I_b, a scale per 32-weight block on both
+// sides, so every output takes a float multiply-add per block on top of the block's integer dot:
+// two VALU instructions per output and block, 32 per MFMA, which bound that GEMM (the VALU, not
+// the MFMA); Q4_K's scales fold into the int8 operands and its float combine runs once per 256.
 // MFMA layouts (i = lane % 32, h = lane / 32): A operand lane (i, h) = column i, k 16 h..+15;
 // B operand lane (j, h) = row j, k 16 h..+15; result register r of lane (j, h) = column
 // 8 (r / 4) + 4 h + r % 4 of row j.
@@ -52,47 +46,6 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int kMagic = 0x4B400000;       // float 12582912: its bits + i are the float 12582912 + i, |i| < 2^22
-constexpr int kU = 4;                    // row tiles per work-group: the waves sharing a K slice's staging
-constexpr int kMaxKS = 3;                // K slices per work-group (12 waves: 3 per SIMD)
-constexpr int kRing = 2;                 // weight blocks in flight per wave
-// blocks per stage: two groups, one for Q8_0 (its two code chunks per block take the registers);
-// a stage in LDS holds the A operands of its blocks (1 KB each), then their f32 scales (128 B)
-__host__ __device__ constexpr int stage_blocks(int type) { return type == QMM_TYPE_Q8_0 ? 8 : 16; }
-__host__ __device__ constexpr int stage_bytes(int type) { return stage_blocks(type) * (1024 + 128); }
-
-struct G3Params {
-    WView w;
-    const int8_t * tA;
-    const float * tD;
-    int64_t nblk;                        // blocks per activation column
-    int64_t ntb;                         // column tiles per batch
-    int64_t N;                           // columns per batch
-    int64_t mbn, nbn;                    // work-group blocks per batch along M (kU row tiles) and N (C column tiles)
-    int64_t total;                       // mbn * nbn
-    int64_t chunk;                       // ceil(total / 8): logical work-groups per XCD
-    int KS, sps, nst;                    // K slices, stages per slice, stages along K (kSB blocks each)
-    GemmBatch bt;
-    float * dst;
-};
-
-// lo (k 0..15) and hi (k 16..31) of the lane's own row -> B operands of rows 0-31 (op0) and
-// rows 32-63 (op1): lanes 32-63 trade their lo for lanes 0-31's hi
-__device__ __forceinline__ void swap_halves(const uint4 & lo, const uint4 & hi, v4i & op0, v4i & op1) {
-    const auto a = __builtin_amdgcn_permlane32_swap(lo.x, hi.x, false, false);
-    const auto b = __builtin_amdgcn_permlane32_swap(lo.y, hi.y, false, false);
-    const auto c = __builtin_amdgcn_permlane32_swap(lo.z, hi.z, false, false);
-    const auto d = __builtin_amdgcn_permlane32_swap(lo.w, hi.w, false, false);
-    op0 = v4i{ (int)a[0], (int)b[0], (int)c[0], (int)d[0] };
-    op1 = v4i{ (int)a[1], (int)b[1], (int)c[1], (int)d[1] };
-}
-
-// a per-row value of the lane's own row -> that of row lane % 32 (r0) and row 32 + lane % 32 (r1)
-__device__ __forceinline__ void swap_rows(uint32_t v, uint32_t & r0, uint32_t & r1) {
-    const auto a = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-    r0 = a[0];
-    r1 = a[1];
-}
-
 // Buffer loads: a wave-uniform resource (base and byte size in scalar registers), a 32-bit lane
 // offset and a scalar block offset, so the per-load address math stays on the SALU; reads past
 // the size return zeros.  (Word 3 is the gfx9 raw-buffer format.)
@@ -110,213 +63,6 @@ __device__ __forceinline__ uint4 bld16(__amdgpu_buffer_rsrc_t r, uint32_t voff, 
 }
 __device__ __forceinline__ uint32_t bld4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
-}
-
-// one weight block of the lane's row in flight
-template <int TYPE> struct WBlk {
-    uint4 c[TYPE == QMM_TYPE_Q8_0 ? 2 : 1];   // codes: Q8_0 qs[0:16], qs[16:32]; else the 16 bytes of qs
-    uint32_t d;                               // the dword of the d plane holding the block's fp16 scale
-};
-
-template <int TYPE>
-__global__ __launch_bounds__(64 * kU * kMaxKS) void k_gemm3(G3Params p) {
-    constexpr bool Q8 = TYPE == QMM_TYPE_Q8_0;
-    constexpr bool NLQ = TYPE == QMM_TYPE_IQ4_NL;
-    constexpr int kDch = Q8 ? 16 : 8;                         // chunk plane of the block scales
-    constexpr int kSB = stage_blocks(TYPE), kSA = kSB * 1024, kStage = stage_bytes(TYPE);
-    static_assert(kSB % kRing == 0 && kSB % kU == 0, "ring slots repeat every stage; A blocks spread over the waves");
-    extern __shared__ __align__(16) uint8_t lds[];
-    const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int u = wave % kU, ks = wave / kU;
-
-    const uint32_t L = (blockIdx.x & 7) * (uint32_t)p.chunk + (blockIdx.x >> 3);
-    if (L >= (uint32_t)p.total) return;                       // uniform over the work-group
-    const uint32_t mb = L / (uint32_t)p.nbn, nb = L - mb * (uint32_t)p.nbn;
-    const uint32_t bz = blockIdx.y;
-    const uint32_t i2 = bz % (uint32_t)p.bt.ne12, i3 = bz / (uint32_t)p.bt.ne12;
-    const int64_t mat = (int64_t)(i2 / (uint32_t)p.bt.r2) + (int64_t)(i3 / (uint32_t)p.bt.r3) * p.bt.ne02;
-    const int64_t mt_raw = (int64_t)mb * kU + u;
-    const bool row_ok = mt_raw < p.w.ntiles;                  // a missing tile computes a copy, stores nothing
-    const int64_t mtile = row_ok ? mt_raw : p.w.ntiles - 1;
-    const int64_t ctile = (int64_t)bz * p.ntb + nb;           // the work-group's column tile
-    // this slice's stages [s0, s1); every slice runs sps iterations (the barriers are work-group
-    // wide), the idle ones past s1 only staging (clamped) and waiting
-    const int s0 = ks * p.sps;
-    const int s1 = std::min(s0 + p.sps, p.nst);
-    const int slast = s1 - 1;                                 // (every slice has stages: KS = ceil(nst / sps))
-    const int kb_last = s1 * kSB - 1;                         // (blocks past the row read zeros: buffer ranges)
-
-    // ---- buffer resources (wave-uniform): the tile's weight row, the column tile's A operands
-    // (1 KB per block) and f32 scales (128 B per block)
-    const __amdgpu_buffer_rsrc_t wbuf = buffer_rsrc(tile_group(p.w, mat, mtile, 0), (uint32_t)(p.w.G * p.w.tg));
-    const __amdgpu_buffer_rsrc_t abuf = buffer_rsrc(p.tA + ctile * p.nblk * 1024, (uint32_t)(p.nblk * 1024));
-    const __amdgpu_buffer_rsrc_t dbuf = buffer_rsrc(p.tD + ctile * p.nblk * 32, (uint32_t)(p.nblk * 128));
-    const uint32_t lane16 = (uint32_t)lane * 16;
-    const uint32_t tgs = (uint32_t)p.w.tg;
-
-    // ---- staging: the kU waves of a slice copy a stage (kSB blocks of A and scales) into LDS,
-    // wave u the A operands of blocks u, u + kU, ... and 16-byte units u * 16 + lane (lane < 16)
-    // of the scales
-    constexpr int kNA = kSB / kU;
-    uint4 ra[kNA], rd = make_uint4(0, 0, 0, 0);
-    const bool dlane = lane < kSB * 8 / kU;
-    auto fetch = [&](int st) {
-        st = std::min(st, slast);
-#pragma unroll
-        for (int j = 0; j < kNA; ++j) ra[j] = bld16(abuf, lane16, (uint32_t)(st * kSB + u + kU * j) * 1024);
-        if (dlane) rd = bld16(dbuf, (uint32_t)(u * (kSB * 8 / kU) + lane) * 16, (uint32_t)st * kSB * 128);
-    };
-    auto store = [&](int buf) {
-        uint8_t * S = lds + (ks * 2 + buf) * kStage;
-#pragma unroll
-        for (int j = 0; j < kNA; ++j) *reinterpret_cast<uint4 *>(S + (u + kU * j) * 1024 + lane16) = ra[j];
-        if (dlane) *reinterpret_cast<uint4 *>(S + kSA + (u * (kSB * 8 / kU) + lane) * 16) = rd;
-    };
-
-    // ---- weight ring: block kb of the K axis, clamped to the slice's last block
-    WBlk<TYPE> ring[kRing];
-    auto wload = [&](WBlk<TYPE> & r, int kb) {
-        kb = std::min(kb, kb_last);
-        const uint32_t pl = (uint32_t)kb & 7, tg = (uint32_t)(kb >> 3) * tgs;   // uniform
-        r.c[0] = bld16(wbuf, lane16, tg + pl * (Q8 ? 2 : 1) * kChunk);
-        if constexpr (Q8) r.c[1] = bld16(wbuf, lane16, tg + (2 * pl + 1) * kChunk);
-        r.d = bld4(wbuf, lane16, tg + kDch * kChunk + 4 * (pl >> 1));
-    };
-
-    v16f acc0 = v16f{}, acc1 = v16f{};                       // rows lane % 32 and 32 + lane % 32
-    v16i magic;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) magic[r] = kMagic;
-    struct Act {
-        v4i a;                                                // A operand
-        float dx[16];                                         // scales of the lane's 16 result columns
-    };
-    auto aread = [&](Act & x, const uint8_t * S, int j) {     // block j of a stage in LDS
-        x.a = *reinterpret_cast<const v4i *>(S + j * 1024 + lane16);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const float4 v = *reinterpret_cast<const float4 *>(S + kSA + j * 128 + h * 64 + 16 * q);
-            x.dx[4 * q] = v.x;
-            x.dx[4 * q + 1] = v.y;
-            x.dx[4 * q + 2] = v.z;
-            x.dx[4 * q + 3] = v.w;
-        }
-    };
-    // acc += (I d_w rounded once) d_x for the 16 results of one MFMA: the 16 products first (in the
-    // result's registers), then the 16 accumulations, so no VALU instruction waits on the one just
-    // before it; plain f32 FMAs (an fp16 source operand halves their issue rate)
-    auto consume = [&](v16f & acc, const v16i & e, float dw, float nm, const float (&dx)[16]) {
-        v16f tv;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int iv = e[r];
-            tv[r] = __builtin_fmaf(__builtin_bit_cast(float, iv), dw, nm);
-        }
-        asm volatile("" : "+v"(tv));
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[r] = __builtin_fmaf(tv[r], dx[r], acc[r]);
-    };
-    auto compute = [&](int buf, int st) {
-        const uint8_t * S = lds + (ks * 2 + buf) * kStage;
-        Act x;
-#pragma unroll
-        for (int j = 0; j < kSB; ++j) {
-            const int kb = st * kSB + j;
-            aread(x, S, j);                                   // (the SIMD's other waves cover the LDS latency)
-            WBlk<TYPE> & wb = ring[j % kRing];
-            // block kb's weights of the lane's row -> B operands of rows 0-31 and 32-63, and d_w of the
-            // output rows lane % 32 and 32 + lane % 32
-            uint4 lo, hi;
-            if constexpr (Q8) {
-                lo = wb.c[0];
-                hi = wb.c[1];
-            } else if constexpr (NLQ) {
-                const uint4 q = wb.c[0];
-                lo = make_uint4(iq4_lookup(q.x & 0x0F0F0F0Fu), iq4_lookup(q.y & 0x0F0F0F0Fu),
-                                iq4_lookup(q.z & 0x0F0F0F0Fu), iq4_lookup(q.w & 0x0F0F0F0Fu));
-                hi = make_uint4(iq4_lookup((q.x >> 4) & 0x0F0F0F0Fu), iq4_lookup((q.y >> 4) & 0x0F0F0F0Fu),
-                                iq4_lookup((q.z >> 4) & 0x0F0F0F0Fu), iq4_lookup((q.w >> 4) & 0x0F0F0F0Fu));
-            } else {
-                // (q ^ 8) in the high nibble: the int8 byte is 16 (q - 8)
-                const uint32_t x0 = wb.c[0].x ^ 0x88888888u, x1 = wb.c[0].y ^ 0x88888888u;
-                const uint32_t x2 = wb.c[0].z ^ 0x88888888u, x3 = wb.c[0].w ^ 0x88888888u;
-                lo = make_uint4((x0 << 4) & 0xF0F0F0F0u, (x1 << 4) & 0xF0F0F0F0u, (x2 << 4) & 0xF0F0F0F0u,
-                                (x3 << 4) & 0xF0F0F0F0u);
-                hi = make_uint4(x0 & 0xF0F0F0F0u, x1 & 0xF0F0F0F0u, x2 & 0xF0F0F0F0u, x3 & 0xF0F0F0F0u);
-            }
-            v4i op0, op1;
-            swap_halves(lo, hi, op0, op1);
-            uint32_t d0b, d1b;
-            swap_rows(wb.d >> (16 * (kb & 1)), d0b, d1b);
-            wload(wb, kb + kRing);                            // the slot's next block
-            float dw0 = h2f(d0b), dw1 = h2f(d1b);
-            asm volatile("" : "+v"(dw0), "+v"(dw1));          // f32 operands (no fp16 source folding)
-            if (QMM_RED == 6) dw1 = dw0;                      // (mutation 6: rows 32-63 take rows 0-31's scale)
-            const float nm0 = -12582912.0f * dw0, nm1 = -12582912.0f * dw1;
-            const Act & c = x;
-            // (one MFMA result at a time: the SIMD's other waves cover its latency)
-            const v16i e0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(c.a, op0, magic, 0, 0, 0);
-            consume(acc0, e0, dw0, nm0, c.dx);
-            __builtin_amdgcn_sched_barrier(0);
-            const v16i e1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(c.a, op1, magic, 0, 0, 0);
-            consume(acc1, e1, dw1, nm1, c.dx);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    };
-
-    // ---- K loop: stage s + 1 is in registers while s is computed; it goes to the other buffer,
-    // whose stage s - 1 every wave finished before the last barrier
-#pragma unroll
-    for (int i = 0; i < kRing; ++i) wload(ring[i], s0 * kSB + i);
-    fetch(s0);
-    store(0);
-    fetch(s0 + 1);
-    __syncthreads();
-    for (int it = 0; it < p.sps; ++it) {                      // uniform over the work-group
-        if (s0 + it < s1) compute(it & 1, s0 + it);
-        if (it + 1 < p.sps) store((it + 1) & 1);
-        if (it + 2 < p.sps) fetch(s0 + it + 2);
-        __syncthreads();
-    }
-
-    // ---- K slices 1.. add their sums into slice 0's through LDS (fixed order), slice 0 stores
-    if (p.KS > 1) {
-        float * red = reinterpret_cast<float *>(lds);
-        if (ks > 0) {
-            float * o = red + ((size_t)((ks - 1) * kU + u) * 32) * 64 + lane;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                o[r * 64] = acc0[r];
-                o[(16 + r) * 64] = acc1[r];
-            }
-        }
-        __syncthreads();
-        if (ks > 0) return;
-        for (int k = 1; k < p.KS; ++k) {
-            const float * o = red + ((size_t)((k - 1) * kU + u) * 32) * 64 + lane;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                acc0[r] += o[r * 64];
-                acc1[r] += o[(16 + r) * 64];
-            }
-        }
-    }
-    if (!row_ok) return;
-    const float scale = (TYPE == QMM_TYPE_Q4_0) ? 0.0625f : 1.0f;   // Q4_0 codes carried 16 (q - 8)
-    float * dst = p.dst + (int64_t)i2 * p.bt.d_nb2 + (int64_t)i3 * p.bt.d_nb3;
-    const int64_t n0 = (int64_t)nb * 32;
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        const int64_t m = mtile * kTileRows + 32 * t + (lane & 31);
-        if (m >= p.w.M) continue;
-        const v16f & v = t ? acc1 : acc0;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int64_t n = n0 + 8 * (r >> 2) + 4 * h + (r & 3);
-            if (n < p.N) __builtin_nontemporal_store(v[r] * scale, dst + n * p.bt.d_nb1 + m);
-        }
-    }
 }
 
 // ---- Q4_K ------------------------------------------------------------------------------------
@@ -349,8 +95,10 @@ constexpr int kKQMaxWaves = 12;
 // every iteration (so the barrier waits for exactly these loads, not the weight loads issued
 // after them); units past 18 read nothing (out of range) into a 1 KB slot after the stages
 __host__ __device__ constexpr int kq_units(int U) { return (18 + U - 1) / U; }
-// s_waitcnt immediate (gfx9 encoding): vmcnt 5 (bits 3:0, 15:14), expcnt and lgkmcnt not waited on
+// s_waitcnt immediates (gfx9 encoding): vmcnt 5 / 9 (bits 3:0, 15:14), expcnt and lgkmcnt not
+// waited on
 constexpr int kVmcnt5 = 5 | (0x7 << 4) | (0xF << 8);
+constexpr int kVmcnt9 = 9 | (0x7 << 4) | (0xF << 8);
 
 struct KQParams {
     WView w;
@@ -693,15 +441,216 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q4k(KQParams p) {
     }
 }
 
-template <int TYPE>
-hipError_t launch_t(const G3Params & p, const G3Shape & sh, const dim3 & g, hipStream_t s, const KTime * kt) {
-    static const hipError_t attr =
-        hipFuncSetAttribute((const void *)k_gemm3<TYPE>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    if (attr != hipSuccess) return attr;
-    const dim3 b(sh.threads);
-    if (kt) hipExtLaunchKernelGGL(k_gemm3<TYPE>, g, b, (uint32_t)sh.lds, s, kt->start, kt->stop, 0, p);
-    else k_gemm3<TYPE><<<g, b, sh.lds, s>>>(p);
-    return hipGetLastError();
+// ---- Q4_0, Q8_0, IQ4_NL: the streaming form with 32-row x 64-column waves -----------------
+// The block types on the Q4_K kernel's frame: a wave owns 32 rows (one half of a 64-row image
+// tile) x 64 columns (two column tiles) over one K slice, the U row-half waves of a K slice
+// share a stage of activations in LDS (one 256-weight group: both tiles' A operands, 16 KB, and
+// their f32 scales, 2 KB, by buffer loads that write LDS directly), one barrier per group.
+//  * lane (j, h) supplies row j's k 16 h .. 16 h + 15 of every block as the MFMA's B operand,
+//    and the output lane (j, h) holds row j: the lane's own row scale d_w applies, no lane
+//    exchanges.  Q4_0 / IQ4_NL: the lane loads the row's 16 bytes of the block and takes the low
+//    (h = 0) or high (h = 1) nibbles; Q8_0: the lane loads the row's code plane h of the block;
+//  * one weight unpack feeds the MFMAs of both column tiles (the 64 x 32 form unpacks once per
+//    column tile and trades lane halves with v_permlane32_swap): ~75 VALU per 2 MFMAs, against
+//    ~91, of which 64 are ggml's float combine (two FMAs per output and block);
+//  * Q4_0 codes enter as (q ^ 8) << 4 = 16 (q - 8) (no borrow handling), the sums carrying the
+//    factor 16 taken off exactly at the store;
+//  * the MFMA's C input is the bits of 12582912.0f: its result read as a float is 12582912 + I
+//    exactly, fma(that, d_w, -12582912 d_w) is I d_w rounded once and fma(., d_x, acc)
+//    accumulates it (ggml's per-block combine);
+//  * the lane's weights stream one group ahead: a block's chunk is reloaded with the next
+//    group's as soon as its MFMAs are issued.
+template <int TYPE, int U>
+__global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_blk(KQParams p) {
+    constexpr bool Q8 = TYPE == QMM_TYPE_Q8_0;
+    constexpr bool NLQ = TYPE == QMM_TYPE_IQ4_NL;
+    constexpr int kDch = Q8 ? 16 : 8;                         // chunk plane of the block scales
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, j32 = lane & 31;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int u = wave % U, ks = wave / U;
+
+    const uint32_t L = (blockIdx.x & 7) * (uint32_t)p.chunk + (blockIdx.x >> 3);
+    if (L >= (uint32_t)p.total) return;                       // uniform over the work-group
+    const uint32_t mb = L / (uint32_t)p.nbn, nb = L - mb * (uint32_t)p.nbn;
+    const uint32_t bz = blockIdx.y;
+    const uint32_t i2 = bz % (uint32_t)p.bt.ne12, i3 = bz / (uint32_t)p.bt.ne12;
+    const int64_t mat = (int64_t)(i2 / (uint32_t)p.bt.r2) + (int64_t)(i3 / (uint32_t)p.bt.r3) * p.bt.ne02;
+    const int64_t rh_raw = (int64_t)mb * U + u;               // the wave's row half
+    const bool row_ok = rh_raw < 2 * p.w.ntiles;              // a missing row half computes a copy, stores nothing
+    const int64_t rh = row_ok ? rh_raw : 2 * p.w.ntiles - 1;
+    const int64_t mtile = rh >> 1;
+    const int t = (int)(rh & 1);
+    const int64_t ct0 = (int64_t)bz * p.ntb + 2 * (int64_t)nb; // the pair's first column tile
+    const int64_t nct = std::min<int64_t>(2, p.ntb - 2 * (int64_t)nb);
+    const int ng = (int)p.nsb;                                // groups (256 weights) along K
+    const int s0 = ks * p.sps;
+    const int s1 = std::min(s0 + p.sps, ng);                  // (every slice has groups)
+    const int64_t nblk = 8 * p.nsb;                           // blocks per activation column
+
+    const __amdgpu_buffer_rsrc_t wbuf = buffer_rsrc(tile_group(p.w, mat, mtile, 0), (uint32_t)(p.w.G * p.w.tg));
+    // the pair's activations; a pair with one tile reads zeros for the second (past the range)
+    const __amdgpu_buffer_rsrc_t abuf = buffer_rsrc(p.tA + ct0 * nblk * 1024, (uint32_t)(nct * nblk * 1024));
+    const __amdgpu_buffer_rsrc_t dbuf = buffer_rsrc(p.tD + ct0 * nblk * 32, (uint32_t)(nct * nblk * 128));
+    const uint32_t lane16 = (uint32_t)lane * 16;
+
+    // ---- staging of group s into buffer b of the slice: 18 units of 1 KB (A: tile unit / 8,
+    // block unit % 8; the scales of tile unit - 16), wave u taking units u, u + U, ...
+    constexpr int NU = kq_units(U);
+    constexpr uint32_t kOut = 0x7ff00000u;
+    const uint32_t a_stride = (uint32_t)(nblk * 1024), d_stride = (uint32_t)(nblk * 128);
+    uint8_t * const dump = lds + 2 * p.KS * kKQStage;
+    auto stage = [&](int s, int b) {
+        uint8_t * S = lds + (ks * 2 + b) * kKQStage;
+#pragma unroll
+        for (int i = 0; i < NU; ++i) {
+            const int unit = u + i * U;                       // wave-uniform
+            if (unit < 16)
+                dma16(abuf, S + unit * 1024, lane16 + (uint32_t)(unit >> 3) * a_stride + (uint32_t)(unit & 7) * 1024,
+                      (uint32_t)s * 8192);
+            else if (unit < 18)
+                dma16(dbuf, S + unit * 1024, lane16 + (uint32_t)(unit - 16) * d_stride, (uint32_t)s * 1024);
+            else
+                dma16(dbuf, dump, kOut, 0);                   // (nothing: keeps the count)
+        }
+    };
+
+    // ---- weights of the lane's row (32 t + j32): per block the row's 16 bytes (Q8_0: its code
+    // plane h), and the row's 8 block scales
+    const uint32_t row16 = (uint32_t)(32 * t + j32) * 16;
+    const uint32_t tgs = (uint32_t)p.w.tg;
+    auto wplane = [&](int jb) -> uint32_t { return (uint32_t)(Q8 ? 2 * jb + h : jb) * kChunk; };
+    uint4 wq[8], wd;
+
+    v16f out0 = v16f{}, out1 = v16f{};                       // column tiles 0 and 1 of the pair
+    v16i magic;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) magic[r] = kMagic;
+    // acc += (I d_w rounded once) d_x for the 16 results of one MFMA (the products first, then
+    // the accumulations: no VALU instruction waits on the one before it)
+    auto consume = [&](v16f & acc, const v16i & e, float dw, float nm, const uint8_t * D) {
+        float dx[16];
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+            // (output order: register r of half h is column 8 (r / 4) + 4 h + r % 4)
+            const float4 v = *reinterpret_cast<const float4 *>(D + h * 64 + 16 * q4);
+            dx[4 * q4] = v.x;
+            dx[4 * q4 + 1] = v.y;
+            dx[4 * q4 + 2] = v.z;
+            dx[4 * q4 + 3] = v.w;
+        }
+        v16f tv;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int iv = e[r];
+            tv[r] = __builtin_fmaf(__builtin_bit_cast(float, iv), dw, nm);
+        }
+        asm volatile("" : "+v"(tv));
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] = __builtin_fmaf(tv[r], dx[r], acc[r]);
+    };
+    const uint32_t nshift = (uint32_t)(4 - 4 * h);            // Q4_0: the lane half's nibble to the high nibble
+    auto compute = [&](int b, int s) {
+        const uint8_t * S = lds + (ks * 2 + b) * kKQStage;
+        const uint4 dd = wd;
+        const uint32_t sn = (uint32_t)std::min(s + 1, s1 - 1) * tgs;   // the next group (clamped)
+        wd = bld16(wbuf, row16, sn + kDch * kChunk);
+#pragma unroll
+        for (int jb = 0; jb < 8; ++jb) {
+            const uint4 x = wq[jb];
+            v4i bop;
+            if constexpr (Q8) {
+                bop = v4i{ (int)x.x, (int)x.y, (int)x.z, (int)x.w };
+            } else if constexpr (NLQ) {
+                const uint32_t sh = 4u * (uint32_t)h;
+                bop = v4i{ (int)iq4_lookup((x.x >> sh) & 0x0F0F0F0Fu), (int)iq4_lookup((x.y >> sh) & 0x0F0F0F0Fu),
+                           (int)iq4_lookup((x.z >> sh) & 0x0F0F0F0Fu), (int)iq4_lookup((x.w >> sh) & 0x0F0F0F0Fu) };
+            } else {
+                // (q ^ 8) in the high nibble: the int8 byte is 16 (q - 8)
+                bop = v4i{ (int)(((x.x << nshift) & 0xF0F0F0F0u) ^ 0x80808080u),
+                           (int)(((x.y << nshift) & 0xF0F0F0F0u) ^ 0x80808080u),
+                           (int)(((x.z << nshift) & 0xF0F0F0F0u) ^ 0x80808080u),
+                           (int)(((x.w << nshift) & 0xF0F0F0F0u) ^ 0x80808080u) };
+            }
+            const uint32_t dword = jb < 2 ? dd.x : jb < 4 ? dd.y : jb < 6 ? dd.z : dd.w;
+            float dw = h2f((dword >> (16 * (jb & 1))) & 0xffffu);
+            asm volatile("" : "+v"(dw));                      // f32 operands (no fp16 source folding)
+            const float nm = -12582912.0f * dw;
+            const v4i a0 = *reinterpret_cast<const v4i *>(S + jb * 1024 + lane16);
+            const v4i a1 = *reinterpret_cast<const v4i *>(S + 8192 + jb * 1024 + lane16);
+            const v16i e0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bop, magic, 0, 0, 0);
+            const v16i e1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bop, magic, 0, 0, 0);
+            wq[jb] = bld16(wbuf, row16, sn + wplane(jb));     // the slot's next group (its registers free)
+            consume(out0, e0, dw, nm, S + 16384 + jb * 128);
+            consume(out1, e1, dw, nm, S + 17408 + jb * 128);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // ---- K loop: group s + 1 goes into LDS while s is computed (its buffer was last read before
+    // the previous barrier); the barrier's wait covers only these LDS loads, which are issued
+    // before the iteration's weight loads (9 per lane)
+    stage(s0, 0);
+#pragma unroll
+    for (int jb = 0; jb < 8; ++jb) wq[jb] = bld16(wbuf, row16, (uint32_t)s0 * tgs + wplane(jb));
+    wd = bld16(wbuf, row16, (uint32_t)s0 * tgs + kDch * kChunk);
+    __syncthreads();
+    for (int it = 0; it < p.sps; ++it) {                      // uniform over the work-group
+        const int s = s0 + it;
+        stage(std::min(s + 1, s1 - 1), (it + 1) & 1);         // (past the slice: a copy nobody reads)
+        __builtin_amdgcn_sched_barrier(0);                    // the LDS loads go out before the weight loads
+        if (s < s1) {
+            compute(it & 1, s);
+        } else {                                              // a slice shorter than sps: the same loads as
+#pragma unroll                                                // compute's (unused), so that every path
+            for (int jb = 0; jb < 8; ++jb)                    // leaves them outstanding at the barrier
+                wq[jb] = bld16(wbuf, row16, (uint32_t)(s1 - 1) * tgs + wplane(jb));
+            wd = bld16(wbuf, row16, (uint32_t)(s1 - 1) * tgs + kDch * kChunk);
+        }
+        // this wave's LDS loads are complete once at most the 9 weight loads issued after them
+        // are outstanding (vmcnt(9)); the barrier then publishes them to the other waves
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(kVmcnt9);
+        __syncthreads();
+    }
+
+    // ---- K slices 1.. add their sums into slice 0's through LDS (fixed order), slice 0 stores
+    if (p.KS > 1) {
+        float * red = reinterpret_cast<float *>(lds);
+        if (ks > 0) {
+            float * o = red + ((size_t)((ks - 1) * U + u) * 32) * 64 + lane;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                o[r * 64] = out0[r];
+                o[(16 + r) * 64] = out1[r];
+            }
+        }
+        __syncthreads();
+        if (ks > 0) return;
+        for (int k = 1; k < p.KS; ++k) {
+            const float * o = red + ((size_t)((k - 1) * U + u) * 32) * 64 + lane;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                out0[r] += o[r * 64];
+                out1[r] += o[(16 + r) * 64];
+            }
+        }
+    }
+    if (!row_ok) return;
+    const int64_t m = mtile * kTileRows + 32 * t + j32;
+    if (m >= p.w.M) return;
+    const float scale = (TYPE == QMM_TYPE_Q4_0) ? 0.0625f : 1.0f;   // Q4_0 codes carried 16 (q - 8)
+    float * dst = p.dst + (int64_t)i2 * p.bt.d_nb2 + (int64_t)i3 * p.bt.d_nb3 + m;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        const int64_t n0 = (2 * (int64_t)nb + c) * 32;
+        const v16f & v = c ? out1 : out0;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int64_t n = n0 + 8 * (r >> 2) + 4 * h + (r & 3);
+            if (n < p.N) __builtin_nontemporal_store(v[r] * scale, dst + n * p.bt.d_nb1);
+        }
+    }
 }
 
 template <int U, bool GATHER>
@@ -713,6 +662,30 @@ hipError_t launch_kq(const KQParams & q, const G3Shape & sh, const dim3 & g, con
     if (kt) hipExtLaunchKernelGGL(k_gemm3_q4k<U, GATHER>, g, b, (uint32_t)sh.lds, s, kt->start, kt->stop, 0, q);
     else k_gemm3_q4k<U, GATHER><<<g, b, sh.lds, s>>>(q);
     return hipGetLastError();
+}
+
+template <int TYPE, int U>
+hipError_t launch_blk(const KQParams & q, const G3Shape & sh, const dim3 & g, const dim3 & b, hipStream_t s,
+                      const KTime * kt) {
+    static const hipError_t attr = hipFuncSetAttribute((const void *)k_gemm3_blk<TYPE, U>,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (attr != hipSuccess) return attr;
+    if (kt) hipExtLaunchKernelGGL(k_gemm3_blk<TYPE, U>, g, b, (uint32_t)sh.lds, s, kt->start, kt->stop, 0, q);
+    else k_gemm3_blk<TYPE, U><<<g, b, sh.lds, s>>>(q);
+    return hipGetLastError();
+}
+
+template <int TYPE>
+hipError_t launch_blk_u(const KQParams & q, const G3Shape & sh, const dim3 & g, const dim3 & b, hipStream_t s,
+                        const KTime * kt) {
+    switch (sh.U) {
+        case 12: return launch_blk<TYPE, 12>(q, sh, g, b, s, kt);
+        case 6: return launch_blk<TYPE, 6>(q, sh, g, b, s, kt);
+        case 4: return launch_blk<TYPE, 4>(q, sh, g, b, s, kt);
+        case 3: return launch_blk<TYPE, 3>(q, sh, g, b, s, kt);
+        case 2: return launch_blk<TYPE, 2>(q, sh, g, b, s, kt);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 template <bool GATHER>
@@ -748,7 +721,7 @@ namespace {
 // CUs take the next small group as one finishes; measured on 17408 x 5120 x 512: 4-wave groups
 // 141 us, (6, 2) 145 us, (12, 1) 155 us).  Ties go to the earlier (larger U) candidate.
 // ncp = column pairs (grouped mode: route units) per batch
-bool kq_shape_ncp(const WView & w, int64_t ncp, int64_t nbatch, G3Shape * sh) {
+bool kq_shape_ncp(const WView & w, int64_t ncp, int64_t nbatch, G3Shape * sh, bool blk) {
     struct Cand { int U, KS, per_cu; };
     static const Cand cands[] = { { 12, 1, 1 }, { 6, 2, 1 }, { 4, 3, 1 }, { 3, 4, 1 }, { 4, 1, 3 }, { 2, 2, 3 } };
     const int64_t nrh = 2 * w.ntiles, G = w.G;
@@ -758,6 +731,9 @@ bool kq_shape_ncp(const WView & w, int64_t ncp, int64_t nbatch, G3Shape * sh) {
     for (int i = 0; i < (int)(sizeof(cands) / sizeof(cands[0])); ++i) {
         if (forced >= 0 && i != forced) continue;
         const Cand & c = cands[i];
+        // (the block types: two waves per stage share too little of their 2 KB of activations per
+        // block; 11008 x 4096 x 512 measured 97 us at (2, 2) against 76 at (12, 1) and (4, 1, 3))
+        if (blk && c.U == 2 && forced < 0) continue;
         const int64_t sps = (G + c.KS - 1) / c.KS, KS = (G + sps - 1) / sps;
         const int64_t mbn = (nrh + c.U - 1) / c.U, nwg = mbn * ncp * nbatch;
         const int64_t slots = (int64_t)cus * c.per_cu;
@@ -783,8 +759,8 @@ bool kq_shape_ncp(const WView & w, int64_t ncp, int64_t nbatch, G3Shape * sh) {
     sh->workgroups = 8 * ((sh->mbn * ncp + 7) / 8) * nbatch;
     return sh->mbn * ncp < 0x7fffffff && sh->lds <= 160 * 1024 && sh->threads <= 64 * kKQMaxWaves;
 }
-bool kq_shape(const WView & w, int64_t N, int64_t nbatch, G3Shape * sh) {
-    return kq_shape_ncp(w, ((N + 31) / 32 + 1) / 2, nbatch, sh);
+bool kq_shape(const WView & w, int64_t N, int64_t nbatch, G3Shape * sh, bool blk) {
+    return kq_shape_ncp(w, ((N + 31) / 32 + 1) / 2, nbatch, sh, blk);
 }
 }  // namespace
 
@@ -792,7 +768,7 @@ bool gemm3_id_supported(int type) { return type == QMM_TYPE_Q4_K && gemm3_suppor
 
 bool gemm3_id_shape(const WView & w, int64_t max_units, G3Shape * sh) {
     return gemm3_id_supported(QMM_TYPE_Q4_K) && max_units > 0 && w.G > 0 && w.ntiles > 0 &&
-           kq_shape_ncp(w, max_units, 1, sh);
+           kq_shape_ncp(w, max_units, 1, sh, false);
 }
 
 hipError_t launch_gemm3_id(int type, const WView & w, const ActBuf & a, const GemmUnit * units, const int32_t * nunits,
@@ -826,34 +802,10 @@ hipError_t launch_gemm3_id(int type, const WView & w, const ActBuf & a, const Ge
     return launch_kq_u<true>(q, sh, g, b, s, kt);
 }
 
-// Launch shape: C column tiles per wave (2 shares each weight unpack between two column tiles,
-// at twice the accumulators), kU row tiles per work-group, and K slices so that the waves come
-// to about `target` (3 per SIMD).
+// Launch shape of both kernels (kq_shape): U row-half waves per K slice x KS slices.
 bool gemm3_shape(int type, const WView & w, int64_t N, int64_t nbatch, G3Shape * sh) {
     if (!gemm3_supported(type) || N <= 0 || nbatch <= 0 || nbatch > 65535 || w.G <= 0 || w.ntiles <= 0) return false;
-    if (type == QMM_TYPE_Q4_K) return kq_shape(w, N, nbatch, sh);
-    const int64_t ntb = (N + 31) / 32;
-    sh->C = 1;
-    sh->R = 64;
-    sh->U = kU;
-    sh->SB = stage_blocks(type);
-    sh->mbn = (w.ntiles + kU - 1) / kU;
-    sh->nbn = ntb;
-    sh->nst = (int)((w.G * 8 + sh->SB - 1) / sh->SB);
-    // Work-groups of kU waves (one per SIMD, three per CU) when that fills the chip, else of 3 K
-    // slices (12 waves: three per SIMD in one work-group); the waves of a work-group are spread
-    // over the CU's SIMDs in turn, so 8-wave groups would leave room for one group only.
-    const int64_t units = sh->mbn * sh->nbn * nbatch;             // work-groups of one K slice
-    int ks = units * kU >= 2048 ? 1 : kMaxKS;
-    const int ksenv = env_int3("QMM_GEMM3_KS", 0);
-    if (ksenv >= 1 && ksenv <= kMaxKS) ks = ksenv;
-    ks = std::min(ks, sh->nst);
-    sh->sps = (sh->nst + ks - 1) / ks;
-    sh->KS = (sh->nst + sh->sps - 1) / sh->sps;                   // no slice without stages
-    sh->threads = 64 * kU * sh->KS;
-    sh->lds = std::max(sh->KS * 2 * stage_bytes(type), (sh->KS - 1) * kU * 32 * 64 * 4);
-    sh->workgroups = 8 * ((units / nbatch + 7) / 8) * nbatch;
-    return units / nbatch < 0x7fffffff && sh->lds <= 160 * 1024;
+    return kq_shape(w, N, nbatch, sh, type != QMM_TYPE_Q4_K);
 }
 
 hipError_t launch_gemm3(int type, const WView & w, const TiledAct & a, int64_t nbatch, const GemmBatch & bt,
@@ -862,49 +814,30 @@ hipError_t launch_gemm3(int type, const WView & w, const TiledAct & a, int64_t n
     if (!gemm3_shape(type, w, a.N, nbatch, &sh) || !a.A || !a.D || a.nblk != w.G * 8 || a.ntb != (a.N + 31) / 32 ||
         a.ntiles != a.ntb * nbatch || a.vdt != vec_dot_type(type))
         return hipErrorInvalidValue;
-    if (type == QMM_TYPE_Q4_K) {
-        if (!a.S) return hipErrorInvalidValue;
-        KQParams q{};
-        q.w = w;
-        q.tA = a.A;
-        q.tD = a.D;
-        q.tS = a.S;
-        q.nsb = w.G;
-        q.ntb = a.ntb;
-        q.N = a.N;
-        q.mbn = sh.mbn;
-        q.nbn = sh.nbn;
-        q.total = sh.mbn * sh.nbn;
-        q.chunk = (q.total + 7) / 8;
-        q.U = sh.U;
-        q.KS = sh.KS;
-        q.sps = sh.sps;
-        q.bt = bt;
-        q.dst = dst;
-        const dim3 g((unsigned)(8 * q.chunk), (unsigned)nbatch), b(sh.threads);
-        return launch_kq_u<false>(q, sh, g, b, s, kt);
-    }
-    G3Params p{};
-    p.w = w;
-    p.tA = a.A;
-    p.tD = a.D;
-    p.nblk = a.nblk;
-    p.ntb = a.ntb;
-    p.N = a.N;
-    p.mbn = sh.mbn;
-    p.nbn = sh.nbn;
-    p.total = sh.mbn * sh.nbn;
-    p.chunk = (p.total + 7) / 8;
-    p.KS = sh.KS;
-    p.sps = sh.sps;
-    p.nst = sh.nst;
-    p.bt = bt;
-    p.dst = dst;
-    const dim3 g((unsigned)(8 * p.chunk), (unsigned)nbatch);
+    if (type == QMM_TYPE_Q4_K && !a.S) return hipErrorInvalidValue;
+    KQParams q{};
+    q.w = w;
+    q.tA = a.A;
+    q.tD = a.D;
+    q.tS = a.S;
+    q.nsb = w.G;
+    q.ntb = a.ntb;
+    q.N = a.N;
+    q.mbn = sh.mbn;
+    q.nbn = sh.nbn;
+    q.total = sh.mbn * sh.nbn;
+    q.chunk = (q.total + 7) / 8;
+    q.U = sh.U;
+    q.KS = sh.KS;
+    q.sps = sh.sps;
+    q.bt = bt;
+    q.dst = dst;
+    const dim3 g((unsigned)(8 * q.chunk), (unsigned)nbatch), b(sh.threads);
     switch (type) {
-        case QMM_TYPE_Q4_0: return launch_t<QMM_TYPE_Q4_0>(p, sh, g, s, kt);
-        case QMM_TYPE_Q8_0: return launch_t<QMM_TYPE_Q8_0>(p, sh, g, s, kt);
-        case QMM_TYPE_IQ4_NL: return launch_t<QMM_TYPE_IQ4_NL>(p, sh, g, s, kt);
+        case QMM_TYPE_Q4_K: return launch_kq_u<false>(q, sh, g, b, s, kt);
+        case QMM_TYPE_Q4_0: return launch_blk_u<QMM_TYPE_Q4_0>(q, sh, g, b, s, kt);
+        case QMM_TYPE_Q8_0: return launch_blk_u<QMM_TYPE_Q8_0>(q, sh, g, b, s, kt);
+        case QMM_TYPE_IQ4_NL: return launch_blk_u<QMM_TYPE_IQ4_NL>(q, sh, g, b, s, kt);
         default: return hipErrorInvalidValue;
     }
 }

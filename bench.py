@@ -524,8 +524,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
-    ap.add_argument("--only", default="", help="profile one workload: q4k_gemv, q40_gemm, q4k_gemm, gemv, glu, moe or "
-                                                 "moe_grouped")
+    ap.add_argument("--only", default="", help="profile one workload: q4k_gemv, q40_gemm, q4k_gemm, q6k_gemm, gemv, glu, "
+                                                 "moe or moe_grouped")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -592,11 +592,16 @@ def main():
         for w in ws:
             be.free_buffer(w.buf)
 
-    if not args.no_secondary and args.only in ("", "q40_gemm", "q4k_gemm"):
+    if not args.no_secondary and args.only in ("", "q40_gemm", "q4k_gemm", "q6k_gemm"):
         cases = [(qmm.Q4_0, 4096, 4096, 512, "Q4_0 GEMM 4096x4096x512 (config 1 attn)", "q40_gemm", "q40_gemm"),
                  (qmm.Q4_0, 11008, 4096, 512, "Q4_0 GEMM 11008x4096x512 (config 1 ffn gate/up)", "q40_gemm",
                   "q40_gemm_11008"),
-                 (qmm.Q4_K, 17408, 5120, 512, "Q4_K GEMM 17408x5120x512 (config 2 ffn gate/up)", "q4k_gemm", "q4k_gemm")]
+                 (qmm.Q4_K, 17408, 5120, 512, "Q4_K GEMM 17408x5120x512 (config 2 ffn gate/up)", "q4k_gemm", "q4k_gemm"),
+                 (qmm.Q4_0, 4096, 11008, 512, "Q4_0 GEMM 4096x11008x512 (config 1 ffn down)", "q40_gemm",
+                  "q40_gemm_down"),
+                 (qmm.Q6_K, 5120, 17408, 512, "Q6_K GEMM 5120x17408x512 (config 2 ffn down)", "q6k_gemm", "q6k_gemm"),
+                 (qmm.Q6_K, 151936, 5120, 512, "Q6_K GEMM 151936x5120x512 (config 2 output head)", "q6k_gemm",
+                  "q6k_gemm_head")]
         secs = []
         for qtype, M2, K2, N2, name, tag, ttag in cases:
             if args.only and args.only != tag:

@@ -759,13 +759,14 @@ def test_full_size_gemm(be, sc, orc, monkeypatch, qtype, M, K, N):
     assert rel_err(got, ref) <= TOL
 
 
-# streaming GEMM launch shapes: K slices per work-group KS (1..3) forced, on ragged shapes (N
-# not a multiple of 32, a work-group's last row tiles missing, K not a multiple of 256 or of a
-# stage, batches with broadcast weights)
+# streaming GEMM of the block types: each launch shape (row-half waves U x K slices KS, forced
+# by index) on ragged shapes (N not a multiple of 32 or of a column pair, a work-group's last
+# row halves missing, K not a multiple of 256, K slices of unequal length: G = 17 over 3 or 4
+# slices), batches with broadcast weights
 @pytest.mark.parametrize("qtype", [qmm.Q4_0, qmm.Q8_0, qmm.IQ4_NL])
-@pytest.mark.parametrize("KS", [1, 2, 3])
+@pytest.mark.parametrize("KS", range(6))
 def test_gemm_stream_shapes(be, sc, orc, monkeypatch, qtype, KS):
-    monkeypatch.setenv("QMM_GEMM3_KS", str(KS))
+    monkeypatch.setenv("QMM_GEMM3_KQ", str(KS))
     monkeypatch.setenv("QMM_GEMM_MIN_COLS", "16")                 # (small shapes: the GEMM regardless)
     for (M, K, N, seed) in [(200, 800, 33, 301), (64, 2048, 100, 302), (130, 512, 64, 303), (448, 1280, 161, 304),
                             (700, 4352, 40, 307)]:

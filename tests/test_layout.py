@@ -262,7 +262,7 @@ def test_gemv_plan(qtype, K, M, N):
         else:
             image = nt * G * {qmm.Q4_0: 18, qmm.Q8_0: 34, qmm.Q4_K: 144, qmm.Q5_K: 176, qmm.Q6_K: 210,
                               qmm.IQ4_XS: 136, qmm.IQ4_NL: 18}[qtype] * (8 if qtype in (qmm.Q4_0, qmm.Q8_0, qmm.IQ4_NL) else 1) * 64
-            assert (N == 1 and qtype != qmm.Q6_K) or (N == 2 and qtype == qmm.Q8_0) or image <= 16 << 20
+            assert N == 1 or (N == 2 and qtype == qmm.Q8_0) or image <= 16 << 20
             assert W == (8 if qtype == qmm.Q8_0 else 4) and spw == 1
         assert info["workgroups"] == info["tasks"] * nt * KS and info["threads"] == 64 * W
         assert info["lds_bytes"] == max(W * spw * nc * 320, W * 2 * nc * 64 * 4)
@@ -293,10 +293,9 @@ def test_gemv_plan(qtype, K, M, N):
         assert info["lds_bytes"] == (W * nc * 64 * 4 if W > 1 else 0)
 
 
-# the streaming GEMM (types with one float scale per 32-weight block): a wave per (64-row tile,
-# 32-column tile, K slice), work-groups of 4 row tiles x KS K slices (KS = 1 when 4-wave groups
-# fill the chip, else 3), numbered 8 per XCD round; LDS: two stages of 16 blocks (8 for Q8_0) of
-# A operands (1 KB) and f32 scales (128 B) per K slice, or the K slices' sums if larger
+# the streaming GEMM of the block types (one float scale per 32 weights) has Q4_K's frame (the
+# plan rule below: test_gemm_stream_q4k_plan), without the candidate of two row-half waves per
+# K slice, whose stages are shared by too few waves
 GEMM3_SHAPES = [(qmm.Q4_0, 4096, 4096, 512), (qmm.Q4_0, 11008, 4096, 512), (qmm.Q4_0, 4096, 11008, 512),
                 (qmm.Q8_0, 4096, 14336, 64), (qmm.IQ4_NL, 800, 130, 33), (qmm.Q4_0, 4096, 4096, 100)]
 
@@ -308,17 +307,7 @@ def test_gemm_stream_plan(qtype, K, M, N, monkeypatch):
     info = qmm.describe_mul_mat(qmm.Tensor(fake, qtype, (K, M)), qmm.Tensor(fake, qmm.F32, (K, N)),
                                 qmm.Tensor(fake, qmm.F32, (M, N)))
     assert info["path"] == "gemm-stream"
-    KS = info["k_slices"]
-    G, nt, ntb = -(-K // 256), -(-M // 64), -(-N // 32)
-    units = -(-nt // 4) * ntb
-    SB = 8 if qtype == qmm.Q8_0 else 16
-    nst = -(-8 * G // SB)
-    assert info["cols_per_task"] == 32 and info["tiles_per_wg"] == 4
-    ks = min(1 if units * 4 >= 2048 else 3, nst)
-    assert KS == -(-nst // -(-nst // ks))                 # slices of ceil(nst / ks) stages, none empty
-    assert info["threads"] == 64 * 4 * KS
-    assert info["workgroups"] == 8 * -(-units // 8)
-    assert info["lds_bytes"] == max(KS * 2 * SB * 1152, (KS - 1) * 4 * 32 * 64 * 4) <= 160 * 1024
+    check_kq_plan(info, -(-K // 256), M, N, [c for c in KQ_CANDS if c[0] != 2])
 
 
 # Q4_K on the streaming GEMM: a wave per (32-row half of a tile, pair of 32-column tiles, K
@@ -330,7 +319,8 @@ def test_gemm_stream_plan(qtype, K, M, N, monkeypatch):
 # past the column crossover the GEMM is taken when its launch gives every SIMD a wave (row units x
 # column units x K slices >= 1024), else the GEMV's split-K tasks
 @pytest.mark.parametrize("qtype,K,M,N,path", [(qmm.Q4_K, 2048, 512, 256, "gemv-mfma"), (qmm.Q4_K, 5120, 17408, 512, "gemm-stream"),
-                                              (qmm.Q4_K, 5120, 1024, 512, "gemm-stream"), (qmm.Q4_0, 4096, 4096, 100, "gemv-mfma"),
+                                              (qmm.Q4_K, 5120, 1024, 512, "gemm-stream"), (qmm.Q4_0, 4096, 4096, 64, "gemv-mfma"),
+                                              (qmm.Q4_0, 4096, 4096, 128, "gemm-stream"),
                                               (qmm.Q4_0, 4096, 4096, 512, "gemm-stream"), (qmm.Q6_K, 17408, 5120, 512, "gemm-mfma")])
 def test_gemm_fill_rule(qtype, K, M, N, path):
     fake = qmm.Buffer(ptr=0x1000, size=1 << 44)
@@ -344,19 +334,13 @@ GEMM3_KQ_SHAPES = [(5120, 17408, 512), (5120, 12288, 512), (5120, 1024, 512), (6
                    (4096, 4096, 128), (256, 130, 33)]
 
 
-@pytest.mark.parametrize("K,M,N", GEMM3_KQ_SHAPES)
-def test_gemm_stream_q4k_plan(K, M, N):
-    fake = qmm.Buffer(ptr=0x1000, size=1 << 44)
-    os.environ["QMM_GEMM_MIN_COLS"] = "16"
-    try:
-        info = qmm.describe_mul_mat(qmm.Tensor(fake, qmm.Q4_K, (K, M)), qmm.Tensor(fake, qmm.F32, (K, N)),
-                                    qmm.Tensor(fake, qmm.F32, (M, N)))
-    finally:
-        del os.environ["QMM_GEMM_MIN_COLS"]
-    assert info["path"] == "gemm-stream"
-    G, nrh, ncp = K // 256, 2 * -(-M // 64), -(-(-(-N // 32)) // 2)
+def check_kq_plan(info, G, M, N, cands):
+    """the streaming GEMMs' launch plan: (U, KS) minimizes rounds of work-groups on 256 CUs (12-wave
+    groups: one per CU, whole rounds; 4-wave: three per CU, a partial last round counted as its
+    fraction) times groups per slice, ties to the earlier candidate"""
+    nrh, ncp = 2 * -(-M // 64), -(-(-(-N // 32)) // 2)
     best = None
-    for U, ks, per_cu in KQ_CANDS:
+    for U, ks, per_cu in cands:
         sps = -(-G // ks)
         mbn = -(-nrh // U)
         slots = 256 * per_cu
@@ -372,3 +356,16 @@ def test_gemm_stream_q4k_plan(K, M, N):
     assert info["groups_per_wave"] == sps
     lds = max(KS * 2 * 18 * 1024 + (1024 if 18 % U else 0), (KS - 1) * U * 32 * 64 * 4)
     assert info["lds_bytes"] == lds <= 160 * 1024
+
+
+@pytest.mark.parametrize("K,M,N", GEMM3_KQ_SHAPES)
+def test_gemm_stream_q4k_plan(K, M, N):
+    fake = qmm.Buffer(ptr=0x1000, size=1 << 44)
+    os.environ["QMM_GEMM_MIN_COLS"] = "16"
+    try:
+        info = qmm.describe_mul_mat(qmm.Tensor(fake, qmm.Q4_K, (K, M)), qmm.Tensor(fake, qmm.F32, (K, N)),
+                                    qmm.Tensor(fake, qmm.F32, (M, N)))
+    finally:
+        del os.environ["QMM_GEMM_MIN_COLS"]
+    assert info["path"] == "gemm-stream"
+    check_kq_plan(info, K // 256, M, N, KQ_CANDS)
