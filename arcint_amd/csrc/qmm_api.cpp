@@ -1166,6 +1166,10 @@ static int mul_mat_launch(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tens
         bt.d_nb2 = dn.d_nb2;
         bt.d_nb3 = dn.d_nb3;
         ctx->path = "gemm-mfma";
+        // (Q5_K / Q6_K / IQ4_XS have no streaming kernel: their integer sub-block scales do not fold
+        // into int8 operands, so each scale is a VALU multiply-add per output)
+        note_downgrade(ctx, "op=MUL_MAT type=%s k=%lld cols=%s path=gemm-mfma reason=no-streaming-gemm",
+                       type_name(src0->type), (long long)w.K, cols_bucket(N));
         if (!fixed && (rc = ktime_pair(ctx, &kt, &ktp))) return rc;
         QMM_HIP(ctx, launch_gemm(src0->type, w, a, N, dn.ne12 * dn.ne13, bt, d, ctx->stream, ktp));
         return ktime_done(ctx);
@@ -1317,6 +1321,22 @@ static bool use_moe_gemm(int type, const WView & w, int64_t npairs, int64_t n_as
            gemm3_id_shape(w, route_max_units(npairs, n_as), &sh);
 }
 
+// The route-task path's known costs, as downgrade keys: an expert with more pairs than a task
+// takes (8) streams its weights once per task; past the grouped GEMM's pair threshold the type
+// has no grouped kernel (only Q4_K does) or K is below its 1024
+static void note_moe_downgrades(qmm_ctx * ctx, const char * op, int type, const WView & w, int64_t npairs, int64_t n_as,
+                                const char * path) {
+    if (npairs > (int64_t)kMaxTaskCols * n_as)
+        note_downgrade(ctx, "op=%s type=%s k=%lld pairs/expert=%s path=%s reason=expert-weights-per-8-pair-task", op,
+                       type_name(type), (long long)w.K, cols_bucket((npairs + n_as - 1) / n_as), path);
+    const int64_t mn = moe_gemm_min_pairs();
+    if (mn > 0 && npairs >= mn * n_as)
+        note_downgrade(ctx, "op=%s type=%s k=%lld pairs/expert=%s path=%s reason=%s", op, type_name(type),
+                       (long long)w.K, cols_bucket((npairs + n_as - 1) / n_as), path,
+                       !gemm3_id_supported(type) ? "no-grouped-gemm-for-type" : w.G < 4 ? "grouped-gemm-needs-k-1024"
+                                                                                    : "grouped-gemm-shape");
+}
+
 int qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * src1, const qmm_tensor * ids,
                    const qmm_tensor * dst) {
     if (!ctx) return QMM_ERR_INVALID;
@@ -1369,6 +1389,7 @@ int qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * sr
     }
     float * d = (float *)((uint8_t *)dst->buffer->ptr + dst->offs);
     ctx->path = plan.mma ? "gemv-id-mfma" : "gemv-id";
+    note_moe_downgrades(ctx, "MUL_MAT_ID", src0->type, w, npairs, n_as, ctx->path.c_str());
     KTime kt;
     const KTime * ktp;
     if ((rc = ktime_pair(ctx, &kt, &ktp))) return rc;
@@ -1434,6 +1455,7 @@ int qmm_mul_mat_id_glu(qmm_ctx * ctx, const qmm_tensor * gate, const qmm_tensor 
     GemvPair pair{ wu.base, in_wg ? 0 : (int64_t)half, in_wg ? glu_op : -1 };
     float * d = (float *)((uint8_t *)dst->buffer->ptr + dst->offs);
     ctx->path = plan.mma ? "glu-gemv-id-mfma" : "glu-gemv-id";
+    note_moe_downgrades(ctx, "MUL_MAT_ID+GLU", gate->type, wg, npairs, n_as, ctx->path.c_str());
     KTime kt;
     const KTime * ktp;
     if ((rc = ktime_pair(ctx, &kt, &ktp))) return rc;

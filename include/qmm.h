@@ -50,6 +50,15 @@
  *   qmm_describe_mul_mat         the path and launch shape a MUL_MAT would take,
  *                                what GGML_OPENCL_FEWQ_LOG / _TRACE log per
  *                                shape (docs/switches.md:189-190)
+ *   qmm_mul_mat_glu,             the reference's fuse_mm_glu chains (MUL_MAT /
+ *   qmm_mul_mat_id_glu           MUL_MAT_ID gate and up, then GLU)
+ *   qmm_moe_topk                 kernel_topk_moe_softmax_norm (P09:899-1000)
+ *   qmm_moe_combine              the weights' MUL and the slot ADDs of
+ *                                llama.cpp's build_moe_ffn
+ *   qmm_moe_ffn                  no one call in the reference: the router,
+ *                                expert products, GLU, down and combine of a
+ *                                MoE FFN block (with a shared expert) in two
+ *                                launches, for an adaptor that matches the chain
  *
  * Conventions (ggml's): a tensor is { type, ne[4], nb[4], data }.  For a
  * quantized type ne[0] is the row length in weights and must be a multiple

@@ -1211,6 +1211,30 @@ def test_downgrade_keys(sc, orc, monkeypatch):
         assert keys == {"src=qmm op=MUL_MAT type=Q5_K k=512 cols=2-8 path=gemv reason=no-mfma-gemv": 2,
                         "src=qmm op=MUL_MAT type=Q4_K k=512 cols=33-128 path=gemv-mfma reason=several-weight-passes": 1}
         assert n == 3
+        # the shared-tile GEMM of a type without a streaming kernel
+        run(qmm.Q6_K, 128, 512, 512)
+        b2.synchronize()
+        n, keys = b2.downgrades()
+        assert keys["src=qmm op=MUL_MAT type=Q6_K k=512 cols=129+ path=gemm-mfma reason=no-streaming-gemm"] == 1
+        # MUL_MAT_ID on route tasks: 16 experts, 80 tokens x 8 used = 40 pairs an expert (each expert's
+        # weights stream once per 8-pair task); Q6_K has no grouped GEMM past its 32-pair threshold
+        E, T, k, M, K = 16, 80, 8, 64, 512
+        w = b2.new_tensor(qmm.Q6_K, (K, M, E))
+        b2.set_tensor(w, synth.weights(qmm.Q6_K, M * E, K, 3))
+        x = b2.new_tensor(qmm.F32, (K, 1, T))
+        b2.set_tensor(x, synth.activations(T, K, 4).view(np.uint8).ravel())
+        ids = b2.new_tensor(qmm.I32, (k, T))
+        b2.set_tensor(ids, synth.moe_ids(T, E, k, 5).view(np.uint8).ravel())
+        y = b2.new_tensor(qmm.F32, (M, k, T))
+        b2.mul_mat_id(w, x, ids, y)
+        bufs.extend([w, x, ids, y])
+        b2.synchronize()
+        n, keys = b2.downgrades()
+        path = b2.last_path()
+        assert keys[f"src=qmm op=MUL_MAT_ID type=Q6_K k=512 pairs/expert=33-128 path={path} "
+                    "reason=expert-weights-per-8-pair-task"] == 1
+        assert keys[f"src=qmm op=MUL_MAT_ID type=Q6_K k=512 pairs/expert=33-128 path={path} "
+                    "reason=no-grouped-gemm-for-type"] == 1
 
 
 
