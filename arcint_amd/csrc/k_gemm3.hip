@@ -109,8 +109,13 @@ struct KQParams {
     int64_t ntb;                         // column tiles per batch
     int64_t N;                           // columns per batch
     int64_t mbn, nbn;                    // work-group blocks per batch: U row halves along M, column pairs along N
-    int64_t total, chunk;                // mbn * nbn, ceil(total / 8)
+    int64_t total;                       // mbn * nbn
     int U, KS, sps;                      // row-half waves per K slice, K slices, super-blocks per slice
+    // blocks [0, full) whole, by 8 fchunk work-groups; the rest as ts pieces of pk super-blocks,
+    // by 8 tchunk more, which meet in tree (tslots slots per output of a block's wave)
+    int64_t full, fchunk, tchunk;
+    int ts, pk, tslots;
+    uint32_t * tree;
     GemmBatch bt;
     float * dst;
     // grouped MoE mode: work-group column pair nb is unit nb of the route (nbn = the units'
@@ -122,6 +127,64 @@ struct KQParams {
     const int8_t * bsp;                  // [super-block][ldT][16]
     int64_t ldk, ldT, ncols;
 };
+
+// The work-group's block L and K piece (-1: the whole K) from its index bx.  Blocks [0, full)
+// come first, whole, XCD x (bx % 8) taking blocks x fchunk .. (x + 1) fchunk - 1, so the column
+// pairs of one row block (neighbours in L) share their weight rows in one L2; then the tail's
+// pieces e = ts (L - full) + i the same way.  false: no work (past the last block or piece).
+__device__ __forceinline__ bool kq_block(const KQParams & p, uint32_t bx, uint32_t & L, int & piece) {
+    const uint32_t fw = 8u * (uint32_t)p.fchunk;
+    if (bx < fw) {
+        L = (bx & 7) * (uint32_t)p.fchunk + (bx >> 3);
+        piece = -1;
+        return L < (uint32_t)p.full;
+    }
+    const uint32_t q = bx - fw, e = (q & 7) * (uint32_t)p.tchunk + (q >> 3);
+    L = (uint32_t)p.full + e / (uint32_t)p.ts;
+    piece = (int)(e % (uint32_t)p.ts);
+    return e < (uint32_t)(p.total - p.full) * (uint32_t)p.ts;
+}
+
+// The ts pieces of a tail block add a wave's 32 sums per lane (out0, out1) up a pairwise tree of
+// exchanges in slot memory, as the split GEMV's K slices do: at a level of n nodes, node i meets
+// node i ^ 1 in slot i / 2 of the level (an odd last node moves up alone); the first arrival
+// leaves its value and drops it, the second adds it to its own (a + b = b + a: the same sum
+// whichever arrives first) and puts the slot back to kTreeEmpty.  Returns the mask of values
+// this lane still holds at the root (to be stored); every slot ends empty.  nodes: the wave's
+// slots, [slot][32 values][64 lanes].
+__device__ __forceinline__ uint32_t kq_meet(uint32_t * nodes, int piece, int ts, v16f & out0, v16f & out1,
+                                            int lane) {
+    uint32_t live = 0xffffffffu;
+    uint32_t i = (uint32_t)piece, n = (uint32_t)ts, off = 0;
+    while (n > 1) {                                               // uniform
+        if ((i ^ 1u) < n) {
+            uint32_t * sl = nodes + (size_t)(off + (i >> 1)) * 2048 + lane;
+            uint32_t o[32];
+#pragma unroll
+            for (int r = 0; r < 32; ++r) {
+                const float v = r < 16 ? out0[r] : out1[r - 16];
+                o[r] = (live >> r) & 1u ? __hip_atomic_exchange(sl + r * 64, __float_as_uint(v), __ATOMIC_RELAXED,
+                                                                __HIP_MEMORY_SCOPE_AGENT)
+                                        : kTreeEmpty;
+            }
+#pragma unroll
+            for (int r = 0; r < 32; ++r) {
+                if (!((live >> r) & 1u)) continue;
+                if (o[r] == kTreeEmpty) {
+                    live &= ~(1u << r);
+                } else {
+                    if (r < 16) out0[r] += __uint_as_float(o[r]);
+                    else out1[r - 16] += __uint_as_float(o[r]);
+                    __hip_atomic_store(sl + r * 64, kTreeEmpty, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+        }
+        off += (n + 1) >> 1;
+        i >>= 1;
+        n = (n + 1) >> 1;
+    }
+    return live;
+}
 
 // the two 16-bit halves of v times those of s (v_pk_mul_lo_u16)
 __device__ __forceinline__ uint32_t mul_u16x2(uint32_t v, uint32_t s) {
@@ -148,8 +211,9 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q4k(KQParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int u = wave % U, ks = wave / U;
 
-    const uint32_t L = (blockIdx.x & 7) * (uint32_t)p.chunk + (blockIdx.x >> 3);
-    if (L >= (uint32_t)p.total) return;                       // uniform over the work-group
+    uint32_t L;
+    int piece;
+    if (!kq_block(p, blockIdx.x, L, piece)) return;           // uniform over the work-group
     const uint32_t mb = L / (uint32_t)p.nbn, nb = L - mb * (uint32_t)p.nbn;
     const uint32_t bz = blockIdx.y;
     const uint32_t i2 = bz % (uint32_t)p.bt.ne12, i3 = bz / (uint32_t)p.bt.ne12;
@@ -168,8 +232,11 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q4k(KQParams p) {
     const int64_t ct0 = (int64_t)bz * p.ntb + 2 * (int64_t)nb; // the pair's first column tile
     const int64_t nct = std::min<int64_t>(2, p.ntb - 2 * (int64_t)nb);
     const int nsb = (int)p.nsb;
-    const int s0 = ks * p.sps;
-    const int s1 = std::min(s0 + p.sps, nsb);                 // (every slice has super-blocks)
+    // the work-group's super-blocks [kb, ke): all, or its piece's
+    const int kb = piece >= 0 ? piece * p.pk : 0, ke = piece >= 0 ? std::min(kb + p.pk, nsb) : nsb;
+    const int sps = piece >= 0 ? p.pk : p.sps;                // (pieces: one K slice)
+    const int s0 = kb + ks * sps;
+    const int s1 = std::min(s0 + sps, ke);                    // (every slice has super-blocks)
 
     if (GATHER && mat < 0) {                                  // invalid ids: zero rows (uniform)
         const int64_t m = mtile * kTileRows + 32 * t + j32;
@@ -372,7 +439,7 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q4k(KQParams p) {
     for (int c = 0; c < 4; ++c) ch[c] = bld16(wbuf, wl, (uint32_t)s0 * tgs + 2 * c * kChunk);
     hd = bld16(wbuf, row16, (uint32_t)s0 * tgs + 8 * kChunk);
     __syncthreads();
-    for (int it = 0; it < p.sps; ++it) {                      // uniform over the work-group
+    for (int it = 0; it < sps; ++it) {                        // uniform over the work-group
         const int s = s0 + it;
         stage(std::min(s + 1, s1 - 1), (it + 1) & 1);         // (past the slice: a copy nobody reads)
         __builtin_amdgcn_sched_barrier(0);                    // the LDS loads go out before the weight loads
@@ -428,6 +495,10 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q4k(KQParams p) {
         }
         return;
     }
+    // a tail piece: the block's pieces meet first, the holder of a sum stores it
+    const uint32_t live = piece >= 0 ? kq_meet(p.tree + ((size_t)(L - p.full) * U + u) * (size_t)p.tslots * 2048, piece,
+                                               p.ts, out0, out1, lane)
+                                     : 0xffffffffu;
     float * dst = p.dst + (int64_t)i2 * p.bt.d_nb2 + (int64_t)i3 * p.bt.d_nb3 + m;
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
@@ -436,7 +507,7 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q4k(KQParams p) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int64_t n = n0 + 8 * (r >> 2) + 4 * h + (r & 3);
-            if (n < p.N) __builtin_nontemporal_store(v[r], dst + n * p.bt.d_nb1);
+            if (n < p.N && ((live >> (16 * c + r)) & 1u)) __builtin_nontemporal_store(v[r], dst + n * p.bt.d_nb1);
         }
     }
 }
@@ -470,8 +541,9 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_blk(KQParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int u = wave % U, ks = wave / U;
 
-    const uint32_t L = (blockIdx.x & 7) * (uint32_t)p.chunk + (blockIdx.x >> 3);
-    if (L >= (uint32_t)p.total) return;                       // uniform over the work-group
+    uint32_t L;
+    int piece;
+    if (!kq_block(p, blockIdx.x, L, piece)) return;           // uniform over the work-group
     const uint32_t mb = L / (uint32_t)p.nbn, nb = L - mb * (uint32_t)p.nbn;
     const uint32_t bz = blockIdx.y;
     const uint32_t i2 = bz % (uint32_t)p.bt.ne12, i3 = bz / (uint32_t)p.bt.ne12;
@@ -484,8 +556,11 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_blk(KQParams p) {
     const int64_t ct0 = (int64_t)bz * p.ntb + 2 * (int64_t)nb; // the pair's first column tile
     const int64_t nct = std::min<int64_t>(2, p.ntb - 2 * (int64_t)nb);
     const int ng = (int)p.nsb;                                // groups (256 weights) along K
-    const int s0 = ks * p.sps;
-    const int s1 = std::min(s0 + p.sps, ng);                  // (every slice has groups)
+    // the work-group's groups [kb, ke): all, or its piece's
+    const int kb = piece >= 0 ? piece * p.pk : 0, ke = piece >= 0 ? std::min(kb + p.pk, ng) : ng;
+    const int sps = piece >= 0 ? p.pk : p.sps;                // (pieces: one K slice)
+    const int s0 = kb + ks * sps;
+    const int s1 = std::min(s0 + sps, ke);                    // (every slice has groups)
     const int64_t nblk = 8 * p.nsb;                           // blocks per activation column
 
     const __amdgpu_buffer_rsrc_t wbuf = buffer_rsrc(tile_group(p.w, mat, mtile, 0), (uint32_t)(p.w.G * p.w.tg));
@@ -595,7 +670,7 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_blk(KQParams p) {
     for (int jb = 0; jb < 8; ++jb) wq[jb] = bld16(wbuf, row16, (uint32_t)s0 * tgs + wplane(jb));
     wd = bld16(wbuf, row16, (uint32_t)s0 * tgs + kDch * kChunk);
     __syncthreads();
-    for (int it = 0; it < p.sps; ++it) {                      // uniform over the work-group
+    for (int it = 0; it < sps; ++it) {                        // uniform over the work-group
         const int s = s0 + it;
         stage(std::min(s + 1, s1 - 1), (it + 1) & 1);         // (past the slice: a copy nobody reads)
         __builtin_amdgcn_sched_barrier(0);                    // the LDS loads go out before the weight loads
@@ -640,6 +715,10 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_blk(KQParams p) {
     const int64_t m = mtile * kTileRows + 32 * t + j32;
     if (m >= p.w.M) return;
     const float scale = (TYPE == QMM_TYPE_Q4_0) ? 0.0625f : 1.0f;   // Q4_0 codes carried 16 (q - 8)
+    // a tail piece: the block's pieces meet first, the holder of a sum stores it
+    const uint32_t live = piece >= 0 ? kq_meet(p.tree + ((size_t)(L - p.full) * U + u) * (size_t)p.tslots * 2048, piece,
+                                               p.ts, out0, out1, lane)
+                                     : 0xffffffffu;
     float * dst = p.dst + (int64_t)i2 * p.bt.d_nb2 + (int64_t)i3 * p.bt.d_nb3 + m;
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
@@ -648,7 +727,7 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_blk(KQParams p) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int64_t n = n0 + 8 * (r >> 2) + 4 * h + (r & 3);
-            if (n < p.N) __builtin_nontemporal_store(v[r] * scale, dst + n * p.bt.d_nb1);
+            if (n < p.N && ((live >> (16 * c + r)) & 1u)) __builtin_nontemporal_store(v[r] * scale, dst + n * p.bt.d_nb1);
         }
     }
 }
@@ -721,7 +800,7 @@ namespace {
 // CUs take the next small group as one finishes; measured on 17408 x 5120 x 512: 4-wave groups
 // 141 us, (6, 2) 145 us, (12, 1) 155 us).  Ties go to the earlier (larger U) candidate.
 // ncp = column pairs (grouped mode: route units) per batch
-bool kq_shape_ncp(const WView & w, int64_t ncp, int64_t nbatch, G3Shape * sh, bool blk) {
+bool kq_shape_ncp(const WView & w, int64_t ncp, int64_t nbatch, G3Shape * sh, bool blk, bool tail) {
     struct Cand { int U, KS, per_cu; };
     static const Cand cands[] = { { 12, 1, 1 }, { 6, 2, 1 }, { 4, 3, 1 }, { 3, 4, 1 }, { 4, 1, 3 }, { 2, 2, 3 } };
     const int64_t nrh = 2 * w.ntiles, G = w.G;
@@ -756,11 +835,45 @@ bool kq_shape_ncp(const WView & w, int64_t ncp, int64_t nbatch, G3Shape * sh, bo
     sh->nst = (int)G;
     sh->threads = 64 * sh->U * sh->KS;
     sh->lds = std::max(sh->KS * 2 * kKQStage + (18 % sh->U ? 1024 : 0), (sh->KS - 1) * sh->U * 32 * 64 * 4);
-    sh->workgroups = 8 * ((sh->mbn * ncp + 7) / 8) * nbatch;
+    // The last partial round (one K slice, one batch) when it holds at most one block per CU:
+    // its blocks run as ts pieces along K on the CUs that it would leave idle.  ts minimizes the
+    // pieces' load per CU, ceil(tail ts / CUs) / ts blocks, below the one block; at least two
+    // stages a piece, ties to fewer pieces.  (Measured at N = 512: IQ4_NL 14336 x 4096, 896
+    // blocks of 4 waves = 768 + 128, 124 -> 108 us in halves; Q4_K 17408 x 5120, 768 + 320,
+    // whose tail already puts two blocks on 64 CUs, 128-140 -> 132-148 us in pieces: not split.)
+    const int64_t nwg = sh->mbn * ncp;
+    sh->full = nwg;
+    sh->ts = 1;
+    sh->pk = (int)G;
+    sh->tslots = 0;
+    const int tail_env = env_int3("QMM_GEMM3_TAIL", 1);       // 0: whole blocks, 2..4: that many pieces (tuning)
+    if (tail && nbatch == 1 && sh->KS == 1 && tail_env != 0) {
+        const int64_t slots = (int64_t)cus * (kKQMaxWaves / sh->U);   // (work-groups of U waves a CU holds)
+        const int64_t full = nwg / slots * slots, rest = nwg - full;
+        int64_t bn = 1, bd = 1;                                 // best load bn / bd (1: whole blocks)
+        for (int ts = 2; ts <= 4 && rest > 0 && (rest <= cus || tail_env > 1); ++ts) {
+            const int64_t pk = (G + ts - 1) / ts;
+            if (pk < 2 || (ts - 1) * pk >= G || (tail_env > 1 && ts != tail_env)) continue;
+            const int64_t r = (rest * ts + cus - 1) / cus;
+            if (r * bd < bn * ts || tail_env > 1) {
+                bn = r;
+                bd = ts;
+            }
+        }
+        if (bd > 1) {
+            sh->full = full;
+            sh->ts = (int)bd;
+            sh->pk = (int)((G + bd - 1) / bd);
+            sh->tslots = bd == 2 ? 1 : 3;                       // (pairs, then the pair of pairs)
+        }
+    }
+    sh->fchunk = (sh->full + 7) / 8;
+    sh->tchunk = ((nwg - sh->full) * sh->ts + 7) / 8;
+    sh->workgroups = 8 * (sh->fchunk + sh->tchunk) * nbatch;
     return sh->mbn * ncp < 0x7fffffff && sh->lds <= 160 * 1024 && sh->threads <= 64 * kKQMaxWaves;
 }
 bool kq_shape(const WView & w, int64_t N, int64_t nbatch, G3Shape * sh, bool blk) {
-    return kq_shape_ncp(w, ((N + 31) / 32 + 1) / 2, nbatch, sh, blk);
+    return kq_shape_ncp(w, ((N + 31) / 32 + 1) / 2, nbatch, sh, blk, true);
 }
 }  // namespace
 
@@ -768,7 +881,7 @@ bool gemm3_id_supported(int type) { return type == QMM_TYPE_Q4_K && gemm3_suppor
 
 bool gemm3_id_shape(const WView & w, int64_t max_units, G3Shape * sh) {
     return gemm3_id_supported(QMM_TYPE_Q4_K) && max_units > 0 && w.G > 0 && w.ntiles > 0 &&
-           kq_shape_ncp(w, max_units, 1, sh, false);
+           kq_shape_ncp(w, max_units, 1, sh, false, false);
 }
 
 hipError_t launch_gemm3_id(int type, const WView & w, const ActBuf & a, const GemmUnit * units, const int32_t * nunits,
@@ -784,7 +897,9 @@ hipError_t launch_gemm3_id(int type, const WView & w, const ActBuf & a, const Ge
     q.mbn = sh.mbn;
     q.nbn = max_units;
     q.total = sh.mbn * max_units;
-    q.chunk = (q.total + 7) / 8;
+    q.full = q.total;
+    q.fchunk = (q.total + 7) / 8;
+    q.ts = 1;
     q.U = sh.U;
     q.KS = sh.KS;
     q.sps = sh.sps;
@@ -798,7 +913,7 @@ hipError_t launch_gemm3_id(int type, const WView & w, const ActBuf & a, const Ge
     q.ldk = a.ldk;
     q.ldT = a.ldT;
     q.ncols = a.ncols;
-    const dim3 g((unsigned)(8 * q.chunk), 1u), b(sh.threads);
+    const dim3 g((unsigned)(8 * q.fchunk), 1u), b(sh.threads);
     return launch_kq_u<true>(q, sh, g, b, s, kt);
 }
 
@@ -808,8 +923,12 @@ bool gemm3_shape(int type, const WView & w, int64_t N, int64_t nbatch, G3Shape *
     return kq_shape(w, N, nbatch, sh, type != QMM_TYPE_Q4_K);
 }
 
+size_t gemm3_tree_words(const G3Shape & sh) {
+    return sh.ts > 1 ? (size_t)(sh.mbn * sh.nbn - sh.full) * (size_t)sh.U * (size_t)sh.tslots * 2048 : 0;
+}
+
 hipError_t launch_gemm3(int type, const WView & w, const TiledAct & a, int64_t nbatch, const GemmBatch & bt,
-                        float * dst, hipStream_t s, const KTime * kt) {
+                        float * dst, hipStream_t s, const KTime * kt, uint32_t * tree) {
     G3Shape sh;
     if (!gemm3_shape(type, w, a.N, nbatch, &sh) || !a.A || !a.D || a.nblk != w.G * 8 || a.ntb != (a.N + 31) / 32 ||
         a.ntiles != a.ntb * nbatch || a.vdt != vec_dot_type(type))
@@ -826,13 +945,25 @@ hipError_t launch_gemm3(int type, const WView & w, const TiledAct & a, int64_t n
     q.mbn = sh.mbn;
     q.nbn = sh.nbn;
     q.total = sh.mbn * sh.nbn;
-    q.chunk = (q.total + 7) / 8;
     q.U = sh.U;
     q.KS = sh.KS;
     q.sps = sh.sps;
     q.bt = bt;
     q.dst = dst;
-    const dim3 g((unsigned)(8 * q.chunk), (unsigned)nbatch), b(sh.threads);
+    if (sh.ts > 1 && tree) {                                  // the tail in pieces
+        q.full = sh.full;
+        q.fchunk = sh.fchunk;
+        q.tchunk = sh.tchunk;
+        q.ts = sh.ts;
+        q.pk = sh.pk;
+        q.tslots = sh.tslots;
+        q.tree = tree;
+    } else {
+        q.full = q.total;
+        q.fchunk = (q.total + 7) / 8;
+        q.ts = 1;
+    }
+    const dim3 g((unsigned)(8 * (q.fchunk + q.tchunk)), (unsigned)nbatch), b(sh.threads);
     switch (type) {
         case QMM_TYPE_Q4_K: return launch_kq_u<false>(q, sh, g, b, s, kt);
         case QMM_TYPE_Q4_0: return launch_blk_u<QMM_TYPE_Q4_0>(q, sh, g, b, s, kt);

@@ -1382,9 +1382,31 @@ __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
     int mat, nc;
     int64_t colv[NC], doffv[NC];
     bool shared = false, skip = false;
+    const int G = (int)p.w.G;
+    int ga, S;
+    dot4_stages(ks, p.W, wave, p.spw, G, NST, ga, S);
+    // the wave's activation groups, quantized into its slots [group][column]
+    float xv[NC][4];
+    uint8_t * const slots = sm + (size_t)wave * p.spw * NC * kFqSlot;
+    bool xq = false;                                              // the slots are filled
+    auto quantize = [&]() {
+        for (int gi = 0; gi * NST < S; ++gi) {                    // uniform
+#pragma unroll
+            for (int j = 0; j < NC; ++j) {
+                if (j < nc) {
+                    if (gi > 0) load_x4(p.x, p.K, colv[j], ga + gi, lane, xv[j]);
+                    quant_slot<VDT>(xv[j], slots + (gi * NC + j) * kFqSlot, lane);
+                }
+            }
+        }
+        xq = true;
+    };
     if (p.ids) {
         const int64_t t = blockIdx.z, i = blockIdx.y;
         shared = i >= p.n_used;                                   // uniform: the shared expert's slot
+        nc = 1;
+#pragma unroll
+        for (int j = 0; j < NC; ++j) colv[j] = (i % p.ne11i) + t * p.ne11i;
         int32_t e = 0;
         if constexpr (ROUTE) {
             __shared__ uint32_t r_key[1024];
@@ -1392,9 +1414,15 @@ __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
             __shared__ float r_p[32];
             __shared__ int32_t r_id[32];
             __shared__ float r_w[32];
+            // the activations do not depend on the route: every wave requests its first group
+            // before the ranking, and the waves that do not rank quantize theirs meanwhile
+#pragma unroll
+            for (int j = 0; j < NC; ++j) load_x4(p.x, p.K, colv[j], ga, lane, xv[j]);
             if (wave == 0)
                 topk_wave_any(p.lg + t * p.lg_nb1, p.n_expert, (int)p.n_used, p.cmin, p.cmax, lane, r_key, r_exp, r_p,
                               r_id, r_w);
+            else
+                quantize();
             __syncthreads();
             if (!shared) e = r_id[i];
             if (tile == 0 && i == 0 && wave == 0 && lane < p.n_used) {
@@ -1417,12 +1445,8 @@ __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
             skip = true;                                          // (combine: the slot still meets the others)
         }
         mat = skip || shared ? 0 : QMM_RED == 8 ? (int)((e + 1) % p.n_as) : e;   // (mutation 8: the next expert)
-        nc = 1;
 #pragma unroll
-        for (int j = 0; j < NC; ++j) {
-            colv[j] = (i % p.ne11i) + t * p.ne11i;
-            doffv[j] = doff;
-        }
+        for (int j = 0; j < NC; ++j) doffv[j] = doff;
     } else {
         const DenseTask dt = task == 0 ? DenseTask{ 0, 0, 0, 0, 0 }
                                        : dense_task(task, (uint32_t)p.tpb, (uint32_t)p.ne12, (uint32_t)p.r2,
@@ -1438,9 +1462,6 @@ __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
         }
     }
     nc = __builtin_amdgcn_readfirstlane(nc);
-    const int G = (int)p.w.G;
-    int ga, S;
-    dot4_stages(ks, p.W, wave, p.spw, G, NST, ga, S);
     if (skip) S = 0;                                              // (a zero row: no stages, no groups)
     const bool glu = p.glu >= 0;                                  // uniform
     const int ST = glu ? 2 * S : S;                               // gate stages, then up stages
@@ -1470,22 +1491,13 @@ __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
     // the first group's activations are requested ahead of the weights: behind the weight
     // stream in the memory queues they would arrive with its end and hold every dot back
     // (both unconditional: colv[j] is a column of src1 for every j, a wave without groups reads
-    // zeros and the sink)
-    float xv[NC][4];
+    // zeros and the sink; with a route they were requested before the ranking)
+    if (!ROUTE) {
 #pragma unroll
-    for (int j = 0; j < NC; ++j) load_x4(p.x, p.K, colv[j], ga, lane, xv[j]);
-    load_stage(0);
-    // the wave's groups of its columns into its slots [group][column]
-    uint8_t * const slots = sm + (size_t)wave * p.spw * NC * kFqSlot;
-    for (int gi = 0; gi * NST < S; ++gi) {                        // uniform
-#pragma unroll
-        for (int j = 0; j < NC; ++j) {
-            if (j < nc) {
-                if (gi > 0) load_x4(p.x, p.K, colv[j], ga + gi, lane, xv[j]);
-                quant_slot<VDT>(xv[j], slots + (gi * NC + j) * kFqSlot, lane);
-            }
-        }
+        for (int j = 0; j < NC; ++j) load_x4(p.x, p.K, colv[j], ga, lane, xv[j]);
     }
+    load_stage(0);
+    if (!xq) quantize();
     __builtin_amdgcn_wave_barrier();
     float acc[NC], accu[NC];
     int st_state[NC];

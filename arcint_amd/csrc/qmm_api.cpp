@@ -1146,8 +1146,16 @@ static int mul_mat_launch(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tens
         bt.d_nb2 = dn.d_nb2;
         bt.d_nb3 = dn.d_nb3;
         ctx->path = "gemm-stream";
+        // the last partial round's blocks in K pieces meeting in tree slots (grown outside
+        // captures only; without them, and in qmm_mul_mat_noalloc, the blocks run whole)
+        uint32_t * tree = nullptr;
+        const size_t tw = gemm3_tree_words(g3);
+        if (tw && !fixed) {
+            if (!ctx->capturing && (rc = ensure_tree(ctx, tw))) return rc;
+            if (ctx->tree_words >= tw) tree = ctx->tree;
+        }
         if (!fixed && (rc = ktime_pair(ctx, &kt, &ktp))) return rc;
-        QMM_HIP(ctx, launch_gemm3(src0->type, w, ta, nbatch, bt, d, ctx->stream, ktp));
+        QMM_HIP(ctx, launch_gemm3(src0->type, w, ta, nbatch, bt, d, ctx->stream, ktp, tree));
         return ktime_done(ctx);
     }
     if (use_gemm) {

@@ -307,11 +307,11 @@ __device__ __forceinline__ void quant_q8_K_at(const F32Cols & src, int64_t K, in
 // SOFT_MAX -> ARGSORT ranks float32 probabilities):
 //  1. each e becomes a 32-bit key, its bits + 1 (e >= 0, so the bits are in e's order; an exp
 //     that underflows to 0 still ranks above the padding); padding gets key 0;
-//  2. the filter: tau0 = the k-th largest of the 64 lanes' largest keys, found most-significant
-//     bit first (32 steps of one ballot).  The lanes holding the k largest maxima hold k keys
-//     >= tau0, so every winner is >= tau0;
-//  3. the candidates (keys >= tau0; usually a few more than k) go to LDS at the offsets of a
-//     scan of the lanes' counts, in expert order;
+//  2. the filter: tau0 = the k-th largest of the 64 lanes' largest keys with its low 14 bits
+//     cleared, found most-significant bit first (16 steps of one ballot).  The lanes holding the
+//     k largest maxima hold k keys >= tau0, so every winner is >= tau0;
+//  3. the candidates (keys >= tau0; usually a few more than k) go to LDS, each lane's at the
+//     places a ballot per held key gives it;
 //  4. each candidate counts the candidates ahead of it (larger key, or equal key and lower
 //     expert): those with fewer than k ahead win, at that rank.
 // Weights: exp(x - max) / sum over all experts (a wave sum), divided by the winners' sum, taken
@@ -319,20 +319,18 @@ __device__ __forceinline__ void quant_q8_K_at(const F32Cols & src, int64_t K, in
 // is ordered by wave-scope fences, no work-group barrier): cand_key / cand_exp hold n_expert
 // entries, ranked_p 32; the winners go to rid[r] (expert) and rw[r] (weight), r < k.
 
-// the sum over lanes 0 .. lane of v (inclusive), by shuffles
-__device__ __forceinline__ int lane_scan(int v, int lane) {
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const int u = __shfl_up(v, d, 64);
-        if (lane >= d) v += u;
-    }
-    return v;
-}
-
 __device__ __forceinline__ float wave_sum_f(float v) {
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) v += __shfl_xor(v, d, 64);
-    return v;
+    // rows by DPP (every lane of a row ends with the row's sum: a + b and b + a are the same
+    // float), then the four row sums in a fixed order
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x141>(v);
+    v += dpp_f<0x140>(v);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return (r0 + r1) + (r2 + r3);
 }
 
 // the wave's LDS writes before this are seen by its loads after it
@@ -367,25 +365,28 @@ __device__ __forceinline__ void topk_wave(const float * x, int n_expert, int k, 
         kmax = key[j] > kmax ? key[j] : kmax;
     }
     const float S = wave_sum_f(part);
-    // 2. tau0: the largest value with at least k lane maxima at or above it
+    // 2. tau0: the largest value of the key's bits 29..14 (lower bits zero) with at least k lane
+    // maxima at or above it (keys are <= bits(1.0f) + 1 < 2^30): the k-th largest lane maximum
+    // with its low bits cleared, so every winner is still >= tau0
     uint32_t tau0 = 0;
-    for (int b = 31; b >= 0; --b) {
+#pragma unroll
+    for (int b = 29; b >= 14; --b) {
         const uint32_t c = tau0 | (1u << b);
         if (__popcll(__ballot(kmax >= c)) >= k) tau0 = c;
     }
-    // 3. the candidates into LDS, in expert order
-    int nc = 0;
-#pragma unroll
-    for (int j = 0; j < NPER; ++j) nc += key[j] >= tau0;
-    int slot = lane_scan(nc, lane) - nc;
-    const int ncand = __shfl(slot + nc, 63, 64);
+    // 3. the candidates into LDS: per j, a ballot gives each lane its place among the lanes
+    // holding one (the order of the candidates does not matter to the ranking below)
+    int ncand = 0;
 #pragma unroll
     for (int j = 0; j < NPER; ++j) {
+        const uint64_t m = __ballot(key[j] >= tau0);
         if (key[j] >= tau0) {
+            const int slot = ncand + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                                    __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
             cand_key[slot] = key[j];
             cand_exp[slot] = e0 + j;
-            ++slot;
         }
+        ncand += __popcll(m);
     }
     wave_lds_sync();
     // 4. each candidate's rank; the first k are the winners (their probabilities summed in

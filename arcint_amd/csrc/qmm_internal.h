@@ -376,8 +376,16 @@ struct G3Shape {
     int sps, nst;                  // stages per K slice, stages along K
     int threads, lds;
     int64_t workgroups;            // all batches
+    // the last partial round: blocks [full, mbn nbn) run as ts work-groups each, piece i over
+    // stages [i pk, (i + 1) pk) (the pieces meet in tree slots: tslots per output and block);
+    // ts = 1: every block whole
+    int64_t full;
+    int ts, pk, tslots;
+    int64_t fchunk, tchunk;        // per XCD: whole blocks, tail pieces
 };
 bool gemm3_shape(int type, const WView & w, int64_t N, int64_t nbatch, G3Shape * sh);
+// tree words the tail pieces of that launch meet in (0: no pieces)
+size_t gemm3_tree_words(const G3Shape & sh);
 // Grouped MoE GEMM (MUL_MAT_ID with many pairs per expert): the route's 64-column units
 // (*nunits of at most max_units) of one expert each, activations gathered from the route's q8_K
 // quantization a; unit pairs with mat < 0 get zero rows.  Q4_K only.
@@ -385,8 +393,10 @@ bool gemm3_id_supported(int type);
 bool gemm3_id_shape(const WView & w, int64_t max_units, G3Shape * sh);
 hipError_t launch_gemm3_id(int type, const WView & w, const ActBuf & a, const GemmUnit * units, const int32_t * nunits,
                            int64_t max_units, float * dst, hipStream_t s, const KTime * kt = nullptr);
+// tree: gemm3_tree_words(shape) words of tree slots, each kTreeEmpty (left so), or nullptr: then
+// the tail blocks run whole
 hipError_t launch_gemm3(int type, const WView & w, const TiledAct & a, int64_t nbatch, const GemmBatch & bt,
-                        float * dst, hipStream_t s, const KTime * kt = nullptr);
+                        float * dst, hipStream_t s, const KTime * kt = nullptr, uint32_t * tree = nullptr);
 
 // K slices the GEMM splits this product into; above 1 the slices add their
 // partial sums to dst with atomics, so dst must be zeroed first.

@@ -790,6 +790,33 @@ def test_gemm_stream_shapes(be, sc, orc, monkeypatch, qtype, KS):
         assert rel_err(got[i2], ref) <= TOL
 
 
+# the last partial round of a one-slice launch in K pieces that meet in tree slots: 2, 3 and 4
+# pieces (G = 4, 5 and 17 over the forced 4-wave shape, whose 768 slots the few blocks leave
+# mostly empty), against the oracle, the same bits on a second call (every slot is left empty,
+# and a + b = b + a whichever piece arrives first) and within rounding of whole blocks
+# (QMM_GEMM3_TAIL=0)
+@pytest.mark.parametrize("qtype", [qmm.Q4_K, qmm.Q4_0, qmm.IQ4_NL])
+def test_gemm_tail_pieces(be, sc, orc, monkeypatch, qtype):
+    monkeypatch.setenv("QMM_GEMM3_KQ", "4")
+    monkeypatch.setenv("QMM_GEMM_MIN_COLS", "16")
+    fake = qmm.Buffer(ptr=0x1000, size=1 << 44)
+    for (M, K, N, ts, seed) in [(200, 1024, 33, 2, 321), (448, 1280, 161, 3, 322), (700, 4352, 40, 4, 323)]:
+        say("gemm-tail", qtype, M, K, N, ts)
+        info = qmm.describe_mul_mat(qmm.Tensor(fake, qtype, (K, M)), qmm.Tensor(fake, qmm.F32, (K, N)),
+                                    qmm.Tensor(fake, qmm.F32, (M, N)))
+        nwg = -(-(2 * -(-M // 64)) // 4) * -(-(-(-N // 32)) // 2)
+        assert info["workgroups"] == 8 * -(-(nwg * ts) // 8), (info, nwg, ts)
+        got, ref = run_mul_mat(be, sc, orc, qtype, M, K, N, seed=seed)
+        assert be.last_path() == "gemm-stream"
+        assert rel_err(got, ref) <= TOL, (M, K, N)
+        again, _ = run_mul_mat(be, sc, orc, qtype, M, K, N, seed=seed)
+        assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+        monkeypatch.setenv("QMM_GEMM3_TAIL", "0")
+        whole, _ = run_mul_mat(be, sc, orc, qtype, M, K, N, seed=seed)
+        monkeypatch.delenv("QMM_GEMM3_TAIL")
+        assert rel_err(got, whole) <= 1e-4                       # (the same float sums in another order)
+
+
 # Q4_K streaming GEMM: each launch shape (row-half waves U x K slices KS, forced by index) on
 # ragged shapes: rows not a whole number of 32-row halves or of a work-group's U, column tiles
 # not a whole number of pairs (N = 80: 3 tiles), K slices of unequal length (G = 17 over 3 or

@@ -334,10 +334,32 @@ GEMM3_KQ_SHAPES = [(5120, 17408, 512), (5120, 12288, 512), (5120, 1024, 512), (6
                    (4096, 4096, 128), (256, 130, 33)]
 
 
+def kq_tail(nwg, U, KS, G):
+    """the last partial round of a one-slice launch in K pieces when it holds at most one block
+    per CU: (whole blocks, pieces per tail block); ts in 2..4 minimizes the load per CU
+    ceil(tail ts / 256) / ts below 1, at least two stages a piece and the last piece not empty,
+    ties to fewer pieces"""
+    if KS != 1:
+        return nwg, 1
+    slots = 256 * (12 // U)
+    full = nwg // slots * slots
+    rest = nwg - full
+    best = (1, 1)                                                 # load per CU: num / den
+    for ts in range(2, 5):
+        pk = -(-G // ts)
+        if rest == 0 or rest > 256 or pk < 2 or (ts - 1) * pk >= G:
+            continue
+        r = -(-(rest * ts) // 256)
+        if r * best[1] < best[0] * ts:
+            best = (r, ts)
+    return (full, best[1]) if best[1] > 1 else (nwg, 1)
+
+
 def check_kq_plan(info, G, M, N, cands):
     """the streaming GEMMs' launch plan: (U, KS) minimizes rounds of work-groups on 256 CUs (12-wave
     groups: one per CU, whole rounds; 4-wave: three per CU, a partial last round counted as its
-    fraction) times groups per slice, ties to the earlier candidate"""
+    fraction) times groups per slice, ties to the earlier candidate; a one-slice launch runs its
+    last partial round's blocks in K pieces (kq_tail)"""
     nrh, ncp = 2 * -(-M // 64), -(-(-(-N // 32)) // 2)
     best = None
     for U, ks, per_cu in cands:
@@ -352,7 +374,8 @@ def check_kq_plan(info, G, M, N, cands):
     _, U, KS, sps, mbn = best
     assert info["k_slices"] == KS and info["cols_per_task"] == 64
     assert info["threads"] == 64 * U * KS
-    assert info["workgroups"] == 8 * -(-(mbn * ncp) // 8)
+    full, ts = kq_tail(mbn * ncp, U, KS, G)
+    assert info["workgroups"] == 8 * -(-full // 8) + 8 * -(-((mbn * ncp - full) * ts) // 8)
     assert info["groups_per_wave"] == sps
     lds = max(KS * 2 * 18 * 1024 + (1024 if 18 % U else 0), (KS - 1) * U * 32 * 64 * 4)
     assert info["lds_bytes"] == lds <= 160 * 1024
@@ -369,3 +392,18 @@ def test_gemm_stream_q4k_plan(K, M, N):
         del os.environ["QMM_GEMM_MIN_COLS"]
     assert info["path"] == "gemm-stream"
     check_kq_plan(info, K // 256, M, N, KQ_CANDS)
+
+
+# IQ4_NL 14336 x 4096 x 512: 896 blocks of 4 row-half waves, three a CU; the 768 of the first round
+# run whole, the other 128 as two K halves each (1024 work-groups); QMM_GEMM3_TAIL=0: whole
+# blocks.  Q4_K 17408 x 5120 x 512 (1088 blocks, a tail of 320: two on some CUs) is not split.
+@pytest.mark.parametrize("qtype,K,M,tail,wgs", [(qmm.IQ4_NL, 4096, 14336, "1", 768 + 2 * 128),
+                                                (qmm.IQ4_NL, 4096, 14336, "0", 896),
+                                                (qmm.Q4_K, 5120, 17408, "1", 1088)])
+def test_gemm_tail_split_plan(qtype, K, M, tail, wgs, monkeypatch):
+    monkeypatch.setenv("QMM_GEMM3_TAIL", tail)
+    fake = qmm.Buffer(ptr=0x1000, size=1 << 44)
+    info = qmm.describe_mul_mat(qmm.Tensor(fake, qtype, (K, M)), qmm.Tensor(fake, qmm.F32, (K, 512)),
+                                qmm.Tensor(fake, qmm.F32, (M, 512)))
+    assert info["path"] == "gemm-stream" and info["threads"] == 256 and info["k_slices"] == 1
+    assert info["workgroups"] == wgs
