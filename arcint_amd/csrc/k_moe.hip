@@ -24,6 +24,7 @@ namespace qmm {
 namespace {
 
 constexpr int kRouteThreads = 1024;
+constexpr int kHeld = 16;               // pairs a route thread keeps in registers (16384 in all)
 
 // one work-group of kRouteThreads; sm = [2 (n_as + 1)] ints of LDS, s_wsum = [kRouteThreads / 64];
 // tasks of up to TC pairs (GEMV tasks: 8, the grouped GEMM's units: 64)
@@ -37,12 +38,38 @@ __device__ __forceinline__ void route_body(const RouteArgs & r, int32_t * __rest
     const int tid = threadIdx.x;
     const int64_t npairs = r.n_used * r.T;
     for (int64_t e = tid; e < nbk; e += kRouteThreads) cnt[e] = 0;
+    // a thread's first kHeld pairs p = tid + j kRouteThreads: every id requested before any is
+    // used (one memory round trip, not one per pair), their buckets kept for the scatter; pairs
+    // past them (more than kHeld kRouteThreads) go through scratch
+    int32_t held[kHeld];
+    // pair p = t n_used + i in 32 bits (the launcher keeps n_used T below 2^31): a 64-bit division
+    // per pair is a long instruction sequence, and one work-group runs every pair
+    const uint32_t nu = (uint32_t)r.n_used, n11 = (uint32_t)r.ne11;
+    auto pair_id = [&](int64_t p) {
+        const uint32_t t = (uint32_t)p / nu, i = (uint32_t)p - t * nu;
+        return *reinterpret_cast<const int32_t *>(reinterpret_cast<const char *>(r.ids) + (size_t)t * r.ids_nb1 +
+                                                  (size_t)i * r.ids_nb0);
+    };
+#pragma unroll
+    for (int j = 0; j < kHeld; ++j) {
+        const int64_t p = tid + (int64_t)j * kRouteThreads;
+        held[j] = p < npairs ? pair_id(p) : 0;
+    }
     __syncthreads();
-    for (int64_t p = tid; p < npairs; p += kRouteThreads) {
-        const int64_t t = p / r.n_used, i = p % r.n_used;
-        const int32_t e = *reinterpret_cast<const int32_t *>(reinterpret_cast<const char *>(r.ids) + t * r.ids_nb1 + i * r.ids_nb0);
-        const int32_t b = (e >= 0 && e < r.n_as) ? e : (int32_t)r.n_as;
+    auto bucket = [&](int32_t e) {
         if (e >= r.n_as) *r.bad_id = 1;
+        return (e >= 0 && e < r.n_as) ? e : (int32_t)r.n_as;
+    };
+#pragma unroll
+    for (int j = 0; j < kHeld; ++j) {
+        const int64_t p = tid + (int64_t)j * kRouteThreads;
+        if (p < npairs) {
+            held[j] = bucket(held[j]);
+            atomicAdd(&cnt[held[j]], 1);
+        }
+    }
+    for (int64_t p = tid + (int64_t)kHeld * kRouteThreads; p < npairs; p += kRouteThreads) {
+        const int32_t b = bucket(pair_id(p));
         atomicAdd(&cnt[b], 1);
         scratch[p] = b;
     }
@@ -94,14 +121,20 @@ __device__ __forceinline__ void route_body(const RouteArgs & r, int32_t * __rest
     __syncthreads();
     for (int64_t e = tid; e < nbk; e += kRouteThreads) cnt[e] = 0;
     __syncthreads();
-    for (int64_t p = tid; p < npairs; p += kRouteThreads) {
-        const int32_t b = scratch[p];
-        const int64_t t = p / r.n_used, i = p % r.n_used;
-        const int32_t slot = atomicAdd(&cnt[b], 1);
-        TaskOf<TC> & T = tasks[tstart[b] + slot / TC];
-        T.col[slot % TC] = b < r.n_as ? (int32_t)((i % r.ne11) + t * r.ne11) : 0;
-        T.dst_off[slot % TC] = t * r.dst_nb2 + i * r.dst_nb1;
+    // the task slot q of pair p (of bucket b): its column and dst offset
+    auto write = [&](int64_t q, int64_t p, bool valid) {
+        const uint32_t t = (uint32_t)p / nu, i = (uint32_t)p - t * nu;
+        TaskOf<TC> & T = tasks[q / TC];
+        T.col[q % TC] = valid ? (int32_t)((n11 == nu ? i : i % n11) + t * n11) : 0;
+        T.dst_off[q % TC] = (int64_t)t * r.dst_nb2 + (int64_t)i * r.dst_nb1;
+    };
+    auto place = [&](int64_t p, int32_t b) { write((int64_t)tstart[b] * TC + atomicAdd(&cnt[b], 1), p, b < r.n_as); };
+#pragma unroll
+    for (int j = 0; j < kHeld; ++j) {
+        const int64_t p = tid + (int64_t)j * kRouteThreads;
+        if (p < npairs) place(p, held[j]);
     }
+    for (int64_t p = tid + (int64_t)kHeld * kRouteThreads; p < npairs; p += kRouteThreads) place(p, scratch[p]);
 }
 
 template <int TC>
@@ -199,7 +232,7 @@ namespace {
 template <int TC>
 hipError_t route_t(const RouteArgs & r, int32_t * scratch, TaskOf<TC> * tasks, int32_t * ntasks, hipStream_t s) {
     const size_t lds = (size_t)(r.n_as + 1) * 2 * sizeof(int32_t);
-    if (lds > 64 * 1024) return hipErrorInvalidValue;
+    if (lds > 64 * 1024 || r.n_used * r.T >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
     k_route<TC><<<1, kRouteThreads, lds, s>>>(r, scratch, tasks, ntasks);
     return hipGetLastError();
 }
@@ -208,7 +241,8 @@ template <int TC>
 hipError_t quant_route_t(const F32Cols & src, int64_t K, int64_t ncols, const ActBuf & a, const RouteArgs & r,
                          int32_t * scratch, TaskOf<TC> * tasks, int32_t * ntasks, hipStream_t s) {
     const size_t lds = (size_t)(r.n_as + 1) * 2 * sizeof(int32_t);
-    if (lds > 64 * 1024 || K <= 0 || ncols < 0 || a.ldk % 256 || a.ldk < K) return hipErrorInvalidValue;
+    if (lds > 64 * 1024 || r.n_used * r.T >= ((int64_t)1 << 31) || K <= 0 || ncols < 0 || a.ldk % 256 || a.ldk < K)
+        return hipErrorInvalidValue;
     const int64_t nq = a.vdt == QMM_TYPE_Q8_0 ? ncols * (a.ldk / 4) : ncols * (a.ldk / 256) * 64;
     const int64_t grid = 1 + (nq + kRouteThreads - 1) / kRouteThreads;
     if (grid > 0x7fffffff) return hipErrorInvalidValue;
