@@ -1238,7 +1238,8 @@ struct FqParams {
     // MoE FFN: a shared-expert slot after the n_used routed ones (its images: the gate / only
     // matrix and the up one, w's shape); combine: slot i of token t weighted by
     // cw[t cw_nb1 + i cw_nb0] (the shared slot by sigmoid(sl[t sl_nb1]), 1 without sl), the
-    // token's row stored at dst + t d_nb1
+    // token's row stored at dst + t d_nb1 (comb 1: the slots meet in the tree; comb 2: wave i
+    // of the tile's work-group is slot i, the rows added in slot order through LDS)
     int n_shared;
     const uint8_t * sh_base;
     const uint8_t * sh_base2;
@@ -1383,8 +1384,10 @@ __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
     int64_t colv[NC], doffv[NC];
     bool shared = false, skip = false;
     const int G = (int)p.w.G;
+    // combine mode 2 (MoE down, slots as waves): wave w is slot w of the token over the whole K
+    const bool slotw = p.comb == 2;                               // uniform
     int ga, S;
-    dot4_stages(ks, p.W, wave, p.spw, G, NST, ga, S);
+    dot4_stages(ks, slotw ? 1 : p.W, slotw ? 0 : wave, p.spw, G, NST, ga, S);
     // the wave's activation groups, quantized into its slots [group][column]
     float xv[NC][4];
     uint8_t * const slots = sm + (size_t)wave * p.spw * NC * kFqSlot;
@@ -1402,8 +1405,8 @@ __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
         xq = true;
     };
     if (p.ids) {
-        const int64_t t = blockIdx.z, i = blockIdx.y;
-        shared = i >= p.n_used;                                   // uniform: the shared expert's slot
+        const int64_t t = blockIdx.z, i = slotw ? wave : blockIdx.y;
+        shared = i >= p.n_used;                                   // uniform (over the wave): the shared expert's slot
         nc = 1;
 #pragma unroll
         for (int j = 0; j < NC; ++j) colv[j] = (i % p.ne11i) + t * p.ne11i;
@@ -1434,7 +1437,7 @@ __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
         }
         const int64_t doff = t * p.dnb2 + i * p.dnb1;
         if (e < 0 || e >= p.n_as) {                                // uniform: a zero row
-            if (wave == 0 && e >= p.n_as && tile == 0 && lane == 0) *p.bad_id = 1;
+            if ((slotw || wave == 0) && e >= p.n_as && tile == 0 && lane == 0) *p.bad_id = 1;
             if (!p.comb) {
                 if (wave == 0) {
                     const int64_t row = (int64_t)tile * kTileRows + lane;
@@ -1533,9 +1536,28 @@ __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
             if (s + 1 < ST) load_stage(s + 1);                    // (nothing past the last stage)
         }
     }
+    const int64_t row = (int64_t)tile * kTileRows + lane;
+    if (slotw) {                                                  // uniform (MoE down, one column)
+        // each slot's row times its weight (rounded, as the graph's MUL), then the token's rows
+        // added slot by slot, the routed ones in order and the gated shared expert last: the
+        // graph's chain of ADDs
+        const int64_t t = blockIdx.z;
+        const int nsl = (int)(p.n_used + p.n_shared);
+        float wgt;
+        if (!shared) wgt = p.cw[t * p.cw_nb1 + (int64_t)wave * p.cw_nb0];
+        else wgt = p.sl ? 1.0f / (1.0f + expf(-p.sl[t * p.sl_nb1])) : 1.0f;
+        float * red = reinterpret_cast<float *>(sm);
+        __syncthreads();                                          // every wave is done with its slots
+        red[wave * 64 + lane] = __fmul_rn(acc[0], wgt);
+        __syncthreads();
+        if (wave != 0 || row >= p.w.M) return;
+        float v = red[lane];
+        for (int ww = 1; ww < nsl; ++ww) v = __fadd_rn(v, red[ww * 64 + lane]);
+        p.dst[t * p.d_nb1 + row] = v;
+        return;
+    }
     // the W waves added in a fixed order: the gate (or only) sums tot[], with the GLU the up sums
     // totu[]; act(gate) * up once the K slices have met
-    const int64_t row = (int64_t)tile * kTileRows + lane;
     float tot[NC], totu[NC];
     if (p.W > 1) {
         const int NV = glu ? 2 * NC : NC;
@@ -1632,6 +1654,18 @@ bool gemv_fused_split_plan(int type, const WView & w, int nc, int64_t ntasks, in
     return pl->lds <= 64 * 1024 && ntasks * w.ntiles < 0x7fffffff;
 }
 
+bool gemv_fused_slot_plan(int type, const WView & w, int64_t nslots, int64_t T, FusedPlan * pl) {
+    if (!type_layout(type) || nslots < 1 || nslots > kFqMaxWaves || T < 1 || T > 65535 || w.G <= 0 || w.ntiles <= 0)
+        return false;
+    pl->nc = 1;
+    pl->ntasks = nslots * T;
+    pl->W = (int)nslots;
+    pl->spw = (int)w.G;
+    pl->KS = 1;
+    pl->lds = std::max<int64_t>(nslots * w.G * kFqSlot, nslots * 64 * 4);
+    return pl->lds <= 64 * 1024 && T * w.ntiles < 0x7fffffff;
+}
+
 int64_t gemv_fused_tree_words(const WView & w, const FusedPlan & pl, bool glu) {
     return pl.KS > 1 ? pl.ntasks * w.ntiles * 2 * pl.KS * pl.nc * 64 * (glu ? 2 : 1) : 0;
 }
@@ -1642,12 +1676,14 @@ hipError_t launch_gemv_fused(int type, const WView & w, const FusedPlan & pl, co
                              const void * sink, hipStream_t s, const KTime * kt) {
     if (!sink || !dst || pl.W < 1 || pl.W > kFqMaxWaves || pl.spw < 1 || pl.nc < 1 || pl.nc > 2 || pl.KS < 1 ||
         pl.KS > 65535 || (int64_t)pl.KS * pl.W * pl.spw < w.G ||
-        (pl.KS == 1 ? (int64_t)(pl.W - 1) * pl.spw >= w.G : (int64_t)(pl.KS - 1) * pl.W * pl.spw >= w.G) ||
+        (f.comb == 2 ? pl.KS != 1 || pl.spw < w.G || pl.W != f.n_used + f.n_shared
+                     : pl.KS == 1 ? (int64_t)(pl.W - 1) * pl.spw >= w.G : (int64_t)(pl.KS - 1) * pl.W * pl.spw >= w.G) ||
         (pl.KS > 1 && (f.ids || !f.tree || ((uintptr_t)f.tree & 7))) || f.K != w.K ||
         (f.ids && (pl.nc != 1 || f.n_used < 1 || f.n_shared < 0 || f.n_shared > 1 ||
                    pl.ntasks != (f.n_used + f.n_shared) * f.T || !f.bad_id)) ||
         (!f.ids && (f.n_shared || f.comb)) || (f.n_shared && (!f.sh_base || (f.glu >= 0 && !f.sh_base2))) ||
-        (f.comb && (pl.KS != 1 || !f.tree || !f.cw || f.glu >= 0 || (f.n_used + f.n_shared) * f.T * w.ntiles > 0x7fffffff)) ||
+        (f.comb && (pl.KS != 1 || (f.comb == 1 && !f.tree) || f.comb > 2 || !f.cw || f.glu >= 0 ||
+                    (f.n_used + f.n_shared) * f.T * w.ntiles > 0x7fffffff)) ||
         (f.lg && (!f.ids || f.comb || !f.wout || f.n_expert < 1 || f.n_expert > 1024 || f.n_used > 32 ||
                   f.n_used > f.n_expert || f.ids_nb0 != 4 || f.n_as != f.n_expert)) ||
         (f.glu > QMM_GLU_GEGLU_QUICK) || (f.glu >= 0 && !f.base2))
@@ -1707,7 +1743,7 @@ hipError_t launch_gemv_fused(int type, const WView & w, const FusedPlan & pl, co
     }
     const int64_t nwg = pl.ntasks * w.ntiles;
     if (nwg <= 0 || nwg >= 0x7fffffff) return hipErrorInvalidValue;
-    const dim3 g = f.ids ? dim3((unsigned)w.ntiles, (unsigned)(f.n_used + f.n_shared), (unsigned)f.T)
+    const dim3 g = f.ids ? dim3((unsigned)w.ntiles, f.comb == 2 ? 1u : (unsigned)(f.n_used + f.n_shared), (unsigned)f.T)
                          : dim3((unsigned)w.ntiles, (unsigned)pl.ntasks, (unsigned)pl.KS);
     if (w.ntiles > 0x7fffffff || (f.ids ? f.n_used + f.n_shared > 65535 || f.T > 65535 : pl.ntasks > 65535))
         return hipErrorInvalidValue;

@@ -1648,11 +1648,19 @@ int qmm_moe_ffn(qmm_ctx * ctx, const qmm_moe_ffn_args * args) {
         !gemv_fused_plan(type, wd, 1, nsl * T, gemv_fused_waves_target(), &p2) || nsl > 65535 ||
         nsl * T * wd.ntiles >= 0x7fffffff)
         return fail(ctx, QMM_ERR_UNSUPPORTED, "moe_ffn: fused GEMV shape out of range");
+    // the down launch: once its (tile, token) work-groups fill the CUs, a work-group per (tile,
+    // token) whose waves are the token's slots, each over the whole K, their rows added in slot
+    // order through LDS (the graph's ADD order, no tree); fewer tokens: one work-group per (tile,
+    // slot, token), spreading the slots over more CUs, the slots meeting in the tree (config 3
+    // layer: T = 1 17.6 against 20.0 us, T = 4 even, T = 8 35.2 against 33.4-34.3, T = 15 58.5
+    // against 56.4).  QMM_MOE_SLOTW: 0 the tree, 1 the slot waves when they fit (tests).
+    const char * sw = getenv("QMM_MOE_SLOTW");
+    const bool slotw = (sw ? atoi(sw) != 0 : T * wd.ntiles >= 256) && gemv_fused_slot_plan(type, wd, nsl, T, &p2);
     QMM_HIP(ctx, hipSetDevice(ctx->device));
     int rc;
     const size_t hbytes = (size_t)(M * nsl * T) * sizeof(float);
     if ((rc = ensure(ctx, &ctx->glu, &ctx->glu_cap, hbytes))) return rc;
-    if ((rc = ensure_tree(ctx, (size_t)(T * wd.ntiles * 2 * nsl * 64)))) return rc;
+    if (!slotw && (rc = ensure_tree(ctx, (size_t)(T * wd.ntiles * 2 * nsl * 64)))) return rc;
     float * h = (float *)ctx->glu;
     const char * idp = (const char *)ids->buffer->ptr + ids->offs;
 
@@ -1705,7 +1713,7 @@ int qmm_moe_ffn(qmm_ctx * ctx, const qmm_moe_ffn_args * args) {
     f2.tree = ctx->tree;
     f2.n_shared = sh ? 1 : 0;
     f2.sh_base = wsd.base;
-    f2.comb = 1;
+    f2.comb = slotw ? 2 : 1;
     f2.cw = (const float *)((const char *)weights->buffer->ptr + weights->offs);
     f2.cw_nb0 = 1;
     f2.cw_nb1 = (int64_t)(weights->nb[1] / 4);

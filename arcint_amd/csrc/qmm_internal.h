@@ -276,7 +276,9 @@ struct FusedGemv {
     // MoE FFN (ids != nullptr): a shared-expert slot n_used of every token (n_shared = 1) with
     // images sh_base (gate / only matrix) and sh_base2 (up) of w's shape; comb: pair (i, t)'s row
     // times cw[t cw_nb1 + i cw_nb0] (the shared slot: sigmoid(sl[t sl_nb1]), 1 without sl), the
-    // token's slots added in the tree and stored at dst + t d_nb1
+    // token's slots added and stored at dst + t d_nb1: comb 1 in the tree (grid: tiles x slots x
+    // tokens), comb 2 in slot order through LDS (grid: tiles x 1 x tokens, one wave per slot over
+    // the whole K: plan W = slots, spw >= G)
     int n_shared;
     const uint8_t * sh_base;
     const uint8_t * sh_base2;
@@ -310,6 +312,9 @@ bool gemv_fused_plan(int type, const WView & w, int nc, int64_t ntasks, int targ
 // dense products split along K: work-groups of W waves with spw groups per wave, KS =
 // ceil(G / (W spw)) >= 2 of them per tile; false when that gives one slice or does not fit
 bool gemv_fused_split_plan(int type, const WView & w, int nc, int64_t ntasks, int W, int spw, FusedPlan * plan);
+// MoE down with the combine in slot order (comb 2): a work-group per (tile, token) of nslots waves,
+// each over the whole K; false when the slots exceed a work-group's waves or the LDS
+bool gemv_fused_slot_plan(int type, const WView & w, int64_t nslots, int64_t T, FusedPlan * plan);
 // tree slots (32-bit words) a split plan needs (glu: gate and up sums travel as one 64-bit pair)
 int64_t gemv_fused_tree_words(const WView & w, const FusedPlan & plan, bool glu);
 int gemv_fused_waves_target();

@@ -297,12 +297,15 @@ def c3_chain_inputs(be, bufs, T, seed):
 
 
 @pytest.mark.parametrize("T", [1, 4, 15])
-def test_c3_moe_ffn_routed_against_op_chain(be, bufs, moe_w, T):
+@pytest.mark.parametrize("slotw", ["1", "0"])
+def test_c3_moe_ffn_routed_against_op_chain(be, bufs, moe_w, monkeypatch, T, slotw):
     """qmm_moe_ffn without a shared expert against the op-by-op chain on the GPU
-    (mul_mat_id_glu -> mul_mat_id -> moe_combine) on the same router output: the same per-pair
-    kernels and plans produce the same expert rows, so the two differ only in the order the
-    weighted slots are added (pairwise tree against slot by slot), float rounding of a 10-term sum"""
-    name = f"C3 moe_ffn routed T={T}"
+    (mul_mat_id_glu -> mul_mat_id -> moe_combine) on the same router output.  The down launch
+    with one wave per slot (QMM_MOE_SLOTW=1, the default) adds the weighted rows slot by slot as
+    moe_combine does, its rows summing K's two groups in one wave instead of two; the tree form
+    (QMM_MOE_SLOTW=0) adds them pairwise: float rounding of a 10-term sum either way"""
+    monkeypatch.setenv("QMM_MOE_SLOTW", slotw)
+    name = f"C3 moe_ffn routed T={T} slotw={slotw}"
     say(name)
     x, _, ids, wts = c3_chain_inputs(be, bufs, T, 400 + T)
     xt = f32(be, x.reshape(T, 1, HID), bufs)
@@ -365,12 +368,14 @@ def test_c3_moe_ffn_with_shared_expert(be, orc, bufs, moe_w, T, x3):
     assert r1["max_abs_err_over_rms"] <= 1e-2, r1
 
 
-def test_c3_moe_ffn_bad_ids_and_limits(be, bufs, moe_w):
-    """a negative id adds nothing (the other slots still meet in the tree: a following call
-    finds every tree slot empty again), an id >= n_as adds nothing and raises at synchronize, and
-    16 tokens are refused with nothing enqueued"""
+@pytest.mark.parametrize("slotw", ["1", "0"])
+def test_c3_moe_ffn_bad_ids_and_limits(be, bufs, moe_w, monkeypatch, slotw):
+    """a negative id adds nothing (the other slots still meet, in slot order or in the tree: a
+    following call finds every tree slot empty again), an id >= n_as adds nothing and raises at
+    synchronize, and 16 tokens are refused with nothing enqueued"""
+    monkeypatch.setenv("QMM_MOE_SLOTW", slotw)
     T = 3
-    say("C3 moe_ffn bad ids")
+    say(f"C3 moe_ffn bad ids slotw={slotw}")
     x, _, ids, wts = c3_chain_inputs(be, bufs, T, 440)
     xt = f32(be, x, bufs)
     (_, wg), (_, wu), (_, wd) = moe_w["gate"], moe_w["up"], moe_w["down"]
