@@ -869,6 +869,28 @@ def test_moe_topk(be, sc, orc, n_expert, k, T):
     np.testing.assert_allclose(got_w, ref_w, rtol=2e-6, atol=1e-30)
 
 
+def test_moe_topk_float32_exp_ties(be, sc, orc):
+    """the router ranks the float32 values exp(x - max): logits -1e-8 and -2e-8 (experts 5 and 7)
+    have the maximum's exp, 1.0f, so the three tie and go in expert order, ahead of the maximum
+    (expert 300); logit order would put 300 first (the oracle's own case, test_oracle_moe.py)"""
+    from oracle import moe
+    say("moe_topk float32 exp ties")
+    logits = np.full((2, 400), -3.0, np.float32)
+    logits[:, 300] = 0.0
+    logits[:, 7] = -2e-8
+    logits[:, 5] = -1e-8
+    logits[:, 9] = -0.5
+    ids = sc.i32(np.zeros((2, 4), np.int32))
+    w = sc.empty_f32((4, 2))
+    be.moe_topk(sc.f32(logits), ids, w, 0.0, float("inf"))
+    be.synchronize()
+    got_ids = be.get_tensor(ids).view(np.int32).reshape(2, 4)
+    ref_ids, ref_w = moe.topk(logits, 4, 0.0, np.inf)
+    assert [list(r) for r in ref_ids] == [[5, 7, 300, 9]] * 2
+    assert np.array_equal(got_ids, ref_ids)
+    np.testing.assert_allclose(be.get_f32(w).reshape(2, 4), ref_w, rtol=2e-6)
+
+
 def test_moe_topk_clamp_and_views(be, sc, orc):
     from oracle import moe
     say("moe_topk_clamp")
