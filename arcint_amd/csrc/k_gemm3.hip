@@ -241,7 +241,7 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q4k(KQParams p) {
     if (GATHER && mat < 0) {                                  // invalid ids: zero rows (uniform)
         const int64_t m = mtile * kTileRows + 32 * t + j32;
         if (!row_ok || m >= p.w.M || ks > 0) return;
-        for (int n = h; n < ncu; n += 2) p.dst[p.units[nb].dst_off[n] + m] = 0.0f;
+        for (int n = h; n < ncu; n += 2) p.dst[p.units[nb].c[n].dst_off + m] = 0.0f;
         return;
     }
 
@@ -263,7 +263,7 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q4k(KQParams p) {
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             const int slot = 32 * c + j32;
-            gcol[c] = slot < ncu ? (uint32_t)p.units[nb].col[slot] : kOut;
+            gcol[c] = slot < ncu ? (uint32_t)p.units[nb].c[slot].col : kOut;
         }
         gsd = (lane >> 5) ? gcol[1] : gcol[0];
     }
@@ -291,7 +291,7 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q4k(KQParams p) {
             if (unit < 16) {
                 const int ci = 4 * (unit & 7) + (lane >> 4);  // column of the tile
                 const int slot = 32 * (unit >> 3) + ci;
-                const uint32_t col = slot < ncu ? (uint32_t)p.units[nb].col[slot] : kOut;
+                const uint32_t col = slot < ncu ? (uint32_t)p.units[nb].c[slot].col : kOut;
                 const uint32_t q = (uint32_t)((lane & 15) ^ (ci & 15));
                 avo[k] = col == kOut ? kOut : col * (uint32_t)p.ldk + 16 * q;
             }
@@ -490,7 +490,7 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q4k(KQParams p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int slot = 32 * c + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (slot < ncu) __builtin_nontemporal_store(v[r], p.dst + p.units[nb].dst_off[slot] + m);
+                if (slot < ncu) __builtin_nontemporal_store(v[r], p.dst + p.units[nb].c[slot].dst_off + m);
             }
         }
         return;

@@ -511,13 +511,13 @@ __global__ __launch_bounds__(512) void k_gemv(GemvParams p) {
         if (mat < 0) {                                            // pairs of invalid ids: zero rows
             const int64_t row = (int64_t)tile * kTileRows + lane;
             if (ks == 0 && wave == 0 && row < p.w.M)
-                for (int j = 0; j < nc; ++j) p.dst[t.dst_off[j] + dadd + row] = 0.0f;
+                for (int j = 0; j < nc; ++j) p.dst[t.c[j].dst_off + dadd + row] = 0.0f;
             return;                                               // uniform
         }
 #pragma unroll
-        for (int j = 0; j < NC; ++j) {                            // col[] / dst_off[] hold kMaxTaskCols >= NC
-            colv[j] = j < nc ? t.col[j] : t.col[0];
-            doffv[j] = (j < nc ? t.dst_off[j] : 0) + dadd;
+        for (int j = 0; j < NC; ++j) {                            // c[] holds kMaxTaskCols >= NC
+            colv[j] = j < nc ? t.c[j].col : t.c[0].col;
+            doffv[j] = (j < nc ? t.c[j].dst_off : 0) + dadd;
         }
     } else {
         // (task 0 is batch 0, column tile 0 and matrix 0 whatever the divisors: the one task of a
@@ -974,12 +974,12 @@ __device__ __forceinline__ void gemv_mma_body(const GemvParams & p) {
             const uint32_t ztile = tb * (uint32_t)TW + (uint32_t)tw;
             const int64_t row = (int64_t)ztile * kTileRows + lane;
             if (ks == 0 && kw == 0 && ztile < ntl && row < p.w.M)
-                for (int j = 0; j < nc; ++j) p.dst[t.dst_off[j] + dadd + row] = 0.0f;
+                for (int j = 0; j < nc; ++j) p.dst[t.c[j].dst_off + dadd + row] = 0.0f;
             return;                                               // uniform
         }
         if (tid < nc) {
-            s_col[tid] = t.col[tid];
-            s_doff[tid] = t.dst_off[tid] + dadd;
+            s_col[tid] = t.c[tid].col;
+            s_doff[tid] = t.c[tid].dst_off + dadd;
         }
     } else {
         const DenseTask dt = task == 0 ? DenseTask{ 0, 0, 0, 0, 0 }

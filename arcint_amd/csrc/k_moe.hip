@@ -45,15 +45,34 @@ __device__ __forceinline__ void route_body(const RouteArgs & r, int32_t * __rest
     // pair p = t n_used + i in 32 bits (the launcher keeps n_used T below 2^31): a 64-bit division
     // per pair is a long instruction sequence, and one work-group runs every pair
     const uint32_t nu = (uint32_t)r.n_used, n11 = (uint32_t)r.ne11;
-    auto pair_id = [&](int64_t p) {
-        const uint32_t t = (uint32_t)p / nu, i = (uint32_t)p - t * nu;
+    auto id_at = [&](uint32_t t, uint32_t i) {
         return *reinterpret_cast<const int32_t *>(reinterpret_cast<const char *>(r.ids) + (size_t)t * r.ids_nb1 +
                                                   (size_t)i * r.ids_nb0);
     };
+    auto pair_id = [&](int64_t p) {
+        const uint32_t t = (uint32_t)p / nu;
+        return id_at(t, (uint32_t)p - t * nu);
+    };
+    // the held pairs' (t, i) by steps: p grows by kRouteThreads, i.e. t by dq and i by dr (one
+    // division per thread instead of one per pair)
+    const uint32_t dq = (uint32_t)kRouteThreads / nu, dr = (uint32_t)kRouteThreads - dq * nu;
+    const uint32_t t0 = (uint32_t)tid / nu, i0 = (uint32_t)tid - t0 * nu;
+    auto step = [&](uint32_t & t, uint32_t & i) {
+        i += dr;
+        t += dq;
+        if (i >= nu) {
+            i -= nu;
+            ++t;
+        }
+    };
+    {
+        uint32_t t = t0, i = i0;
 #pragma unroll
-    for (int j = 0; j < kHeld; ++j) {
-        const int64_t p = tid + (int64_t)j * kRouteThreads;
-        held[j] = p < npairs ? pair_id(p) : 0;
+        for (int j = 0; j < kHeld; ++j) {
+            const int64_t p = tid + (int64_t)j * kRouteThreads;
+            held[j] = p < npairs ? id_at(t, i) : 0;
+            step(t, i);
+        }
     }
     __syncthreads();
     auto bucket = [&](int32_t e) {
@@ -122,19 +141,29 @@ __device__ __forceinline__ void route_body(const RouteArgs & r, int32_t * __rest
     for (int64_t e = tid; e < nbk; e += kRouteThreads) cnt[e] = 0;
     __syncthreads();
     // the task slot q of pair p (of bucket b): its column and dst offset
-    auto write = [&](int64_t q, int64_t p, bool valid) {
-        const uint32_t t = (uint32_t)p / nu, i = (uint32_t)p - t * nu;
-        TaskOf<TC> & T = tasks[q / TC];
-        T.col[q % TC] = valid ? (int32_t)((n11 == nu ? i : i % n11) + t * n11) : 0;
-        T.dst_off[q % TC] = (int64_t)t * r.dst_nb2 + (int64_t)i * r.dst_nb1;
+    auto write = [&](int64_t q, uint32_t t, uint32_t i, bool valid) {
+        TaskCol c;
+        c.col = valid ? (int32_t)((n11 == nu ? i : i % n11) + t * n11) : 0;
+        c.pad = 0;
+        c.dst_off = (int64_t)t * r.dst_nb2 + (int64_t)i * r.dst_nb1;
+        tasks[q / TC].c[q % TC] = c;                              // (one 16-byte store)
     };
-    auto place = [&](int64_t p, int32_t b) { write((int64_t)tstart[b] * TC + atomicAdd(&cnt[b], 1), p, b < r.n_as); };
+    auto place = [&](uint32_t t, uint32_t i, int32_t b) {
+        write((int64_t)tstart[b] * TC + atomicAdd(&cnt[b], 1), t, i, b < r.n_as);
+    };
+    {
+        uint32_t t = t0, i = i0;
 #pragma unroll
-    for (int j = 0; j < kHeld; ++j) {
-        const int64_t p = tid + (int64_t)j * kRouteThreads;
-        if (p < npairs) place(p, held[j]);
+        for (int j = 0; j < kHeld; ++j) {
+            const int64_t p = tid + (int64_t)j * kRouteThreads;
+            if (p < npairs) place(t, i, held[j]);
+            step(t, i);
+        }
     }
-    for (int64_t p = tid + (int64_t)kHeld * kRouteThreads; p < npairs; p += kRouteThreads) place(p, scratch[p]);
+    for (int64_t p = tid + (int64_t)kHeld * kRouteThreads; p < npairs; p += kRouteThreads) {
+        const uint32_t t = (uint32_t)p / nu;
+        place(t, (uint32_t)p - t * nu, scratch[p]);
+    }
 }
 
 template <int TC>

@@ -162,11 +162,18 @@ __host__ __device__ static inline const uint8_t * tile_group(const WView & w, in
 
 // A routed task: up to TC columns against one weight matrix.  GEMV tasks carry up to 8; the
 // grouped MoE GEMM's units 64 (one 64-column wave job of the streaming Q4_K GEMM).
+// A column's activation id and dst offset lie together, so the route writes each pair with one
+// 16-byte store (it scatters every pair of a MUL_MAT_ID from one work-group, and its time goes to
+// those stores).
+struct TaskCol {
+    int32_t col;                   // activation column id
+    int32_t pad;
+    int64_t dst_off;               // float offset of dst row 0 for that column
+};
 template <int TC> struct TaskOf {
     int32_t mat;                   // weight matrix (expert / slice) index; <0: zero rows
     int32_t ncols;
-    int32_t col[TC];               // activation column ids
-    int64_t dst_off[TC];           // float offset of dst row 0 for that column
+    TaskCol c[TC];
 };
 constexpr int kMaxTaskCols = 8;
 constexpr int kUnitCols = 64;
