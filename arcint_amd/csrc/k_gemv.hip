@@ -68,10 +68,18 @@ struct GemvParams {
     int tw;                      // MFMA kernel: tiles per work-group (W / tw waves split K)
     int task0;                   // the grid is (KS, tiles or tile blocks, tasks from task0), blockIdx
                                  // is the position (launches of at most 65535 tasks each)
+    int sh_mat;                  // lists: tasks of this matrix read the shared expert's images
+    const uint8_t * sh_base;     // (its first image and, for base2's, its second); -1: none
+    const uint8_t * sh_base2;
 };
 
 // tile-group 0 of (matrix, tile) of the first image, or (sec) of the second
 __device__ __forceinline__ const uint8_t * mat_tile(const GemvParams & p, int mat, uint32_t tile, bool sec) {
+    if (mat == p.sh_mat) {                                        // (uniform) the shared expert
+        WView ws = p.w;
+        ws.base = sec ? p.sh_base2 : p.sh_base;
+        return tile_group(ws, 0, tile, 0);
+    }
     if (sec) {
         WView w2 = p.w;
         w2.base = p.base2;
@@ -1971,11 +1979,17 @@ hipError_t launch_gemv(int type, const WView & w, const GemvPlan & pl, const Act
     p.nct = pl.nc;
     p.tw = pl.tw;
     p.glu = -1;
+    p.sh_mat = -1;
     if (pair) {
-        if (!tasks || !ntasks_dev || !pair->base2 || pair->glu > QMM_GLU_GEGLU_QUICK) return hipErrorInvalidValue;
+        if (!tasks || !ntasks_dev || pair->glu > QMM_GLU_GEGLU_QUICK || (pair->glu >= 0 && !pair->base2) ||
+            (pair->sh_mat >= 0 && (!pair->sh_base || (pair->base2 && !pair->sh_base2))))
+            return hipErrorInvalidValue;
         p.base2 = pair->base2;
         p.up_doff = pair->up_doff;
         p.glu = pair->glu;
+        p.sh_mat = pair->sh_mat;
+        p.sh_base = pair->sh_base;
+        p.sh_base2 = pair->sh_base2;
     }
     if (!tasks) {
         p.ne11 = dense->ne11;

@@ -32,11 +32,12 @@ template <int TC>
 __device__ __forceinline__ void route_body(const RouteArgs & r, int32_t * __restrict__ scratch,
                                            TaskOf<TC> * __restrict__ tasks, int32_t * __restrict__ ntasks,
                                            int32_t * sm, int32_t * s_wsum) {
-    const int64_t nbk = r.n_as + 1;     // buckets: the experts, then the invalid ids
+    const int64_t nbk = r.n_as + 1 + r.shared;   // buckets: the experts, [the shared expert,] the invalid ids
+    const int32_t inv = (int32_t)(r.n_as + r.shared);
     int32_t * cnt = sm;                 // [nbk] pair count, later the fill cursor
     int32_t * tstart = sm + nbk;        // [nbk] first task of each bucket
     const int tid = threadIdx.x;
-    const int64_t npairs = r.n_used * r.T;
+    const int64_t npairs = (r.n_used + r.shared) * r.T;
     for (int64_t e = tid; e < nbk; e += kRouteThreads) cnt[e] = 0;
     // a thread's first kHeld pairs p = tid + j kRouteThreads: every id requested before any is
     // used (one memory round trip, not one per pair), their buckets kept for the scatter; pairs
@@ -44,8 +45,10 @@ __device__ __forceinline__ void route_body(const RouteArgs & r, int32_t * __rest
     int32_t held[kHeld];
     // pair p = t n_used + i in 32 bits (the launcher keeps n_used T below 2^31): a 64-bit division
     // per pair is a long instruction sequence, and one work-group runs every pair
-    const uint32_t nu = (uint32_t)r.n_used, n11 = (uint32_t)r.ne11;
+    const uint32_t nu = (uint32_t)(r.n_used + r.shared), n11 = (uint32_t)r.ne11;
+    constexpr int32_t kSharedId = -2147483647 - 1;                // (slot n_used with the shared expert: no id)
     auto id_at = [&](uint32_t t, uint32_t i) {
+        if (r.shared && i == (uint32_t)r.n_used) return kSharedId;
         return *reinterpret_cast<const int32_t *>(reinterpret_cast<const char *>(r.ids) + (size_t)t * r.ids_nb1 +
                                                   (size_t)i * r.ids_nb0);
     };
@@ -76,8 +79,9 @@ __device__ __forceinline__ void route_body(const RouteArgs & r, int32_t * __rest
     }
     __syncthreads();
     auto bucket = [&](int32_t e) {
+        if (e == kSharedId) return (int32_t)r.n_as;
         if (e >= r.n_as) *r.bad_id = 1;
-        return (e >= 0 && e < r.n_as) ? e : (int32_t)r.n_as;
+        return (e >= 0 && e < r.n_as) ? e : inv;
     };
 #pragma unroll
     for (int j = 0; j < kHeld; ++j) {
@@ -133,7 +137,7 @@ __device__ __forceinline__ void route_body(const RouteArgs & r, int32_t * __rest
         const int32_t nt = (c + TC - 1) / TC;
         for (int32_t k = 0; k < nt; ++k) {
             TaskOf<TC> & T = tasks[tstart[e] + k];
-            T.mat = e < r.n_as ? (int32_t)(QMM_RED == 7 ? (e + 1) % r.n_as : e) : -1;   // (mutation 7: next expert)
+            T.mat = e < r.n_as ? (int32_t)(QMM_RED == 7 ? (e + 1) % r.n_as : e) : e < inv ? (int32_t)e : -1;   // (mutation 7: next expert)
             T.ncols = (c - k * TC) < TC ? (c - k * TC) : TC;
         }
     }
@@ -149,7 +153,7 @@ __device__ __forceinline__ void route_body(const RouteArgs & r, int32_t * __rest
         tasks[q / TC].c[q % TC] = c;                              // (one 16-byte store)
     };
     auto place = [&](uint32_t t, uint32_t i, int32_t b) {
-        write((int64_t)tstart[b] * TC + atomicAdd(&cnt[b], 1), t, i, b < r.n_as);
+        write((int64_t)tstart[b] * TC + atomicAdd(&cnt[b], 1), t, i, b != inv);
     };
     {
         uint32_t t = t0, i = i0;
@@ -223,10 +227,11 @@ __global__ __launch_bounds__(256) void k_combine(CombineArgs a, int64_t t0) {
     const float * w = reinterpret_cast<const float *>(a.w + t * a.wnb1);
     float y = reinterpret_cast<const float *>(e)[0] * w[0];
     for (int j = 1; j < a.k; ++j) y = y + *reinterpret_cast<const float *>(e + j * a.enb1) * w[j];
-    if (a.shared) {
-        const float g = *reinterpret_cast<const float *>(a.gate + t * a.gnb1);
-        const float sg = 1.0f / (1.0f + expf(-g));
-        y = y + *reinterpret_cast<const float *>(a.shared + t * a.snb1 + m * 4) * sg;
+    if (a.shared) {                                               // (no gate logit: the shared row unweighted)
+        float sg = 1.0f;
+        if (a.gate) sg = 1.0f / (1.0f + expf(-*reinterpret_cast<const float *>(a.gate + t * a.gnb1)));
+        y = y + (a.gate ? *reinterpret_cast<const float *>(a.shared + t * a.snb1 + m * 4) * sg
+                        : *reinterpret_cast<const float *>(a.shared + t * a.snb1 + m * 4));
     }
     *reinterpret_cast<float *>(a.dst + t * a.dnb1 + m * 4) = y;
 }
@@ -260,8 +265,9 @@ hipError_t launch_combine(const CombineArgs & a, hipStream_t s) {
 namespace {
 template <int TC>
 hipError_t route_t(const RouteArgs & r, int32_t * scratch, TaskOf<TC> * tasks, int32_t * ntasks, hipStream_t s) {
-    const size_t lds = (size_t)(r.n_as + 1) * 2 * sizeof(int32_t);
-    if (lds > 64 * 1024 || r.n_used * r.T >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
+    const size_t lds = (size_t)(r.n_as + 1 + r.shared) * 2 * sizeof(int32_t);
+    if (lds > 64 * 1024 || (r.n_used + r.shared) * r.T >= ((int64_t)1 << 31) || r.shared < 0 || r.shared > 1)
+        return hipErrorInvalidValue;
     k_route<TC><<<1, kRouteThreads, lds, s>>>(r, scratch, tasks, ntasks);
     return hipGetLastError();
 }
@@ -269,8 +275,9 @@ hipError_t route_t(const RouteArgs & r, int32_t * scratch, TaskOf<TC> * tasks, i
 template <int TC>
 hipError_t quant_route_t(const F32Cols & src, int64_t K, int64_t ncols, const ActBuf & a, const RouteArgs & r,
                          int32_t * scratch, TaskOf<TC> * tasks, int32_t * ntasks, hipStream_t s) {
-    const size_t lds = (size_t)(r.n_as + 1) * 2 * sizeof(int32_t);
-    if (lds > 64 * 1024 || r.n_used * r.T >= ((int64_t)1 << 31) || K <= 0 || ncols < 0 || a.ldk % 256 || a.ldk < K)
+    const size_t lds = (size_t)(r.n_as + 1 + r.shared) * 2 * sizeof(int32_t);
+    if (lds > 64 * 1024 || (r.n_used + r.shared) * r.T >= ((int64_t)1 << 31) || r.shared < 0 || r.shared > 1 || K <= 0 ||
+        ncols < 0 || a.ldk % 256 || a.ldk < K)
         return hipErrorInvalidValue;
     const int64_t nq = a.vdt == QMM_TYPE_Q8_0 ? ncols * (a.ldk / 4) : ncols * (a.ldk / 256) * 64;
     const int64_t grid = 1 + (nq + kRouteThreads - 1) / kRouteThreads;

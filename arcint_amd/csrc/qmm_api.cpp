@@ -63,6 +63,7 @@ struct qmm_ctx {
     struct RouteKey {
         qmm_tensor ids{};
         int64_t ne11 = 0, n_as = 0, dnb1 = 0, dnb2 = 0;
+        int shared = 0;
         uint64_t gen = 0;
         bool valid = false;
     } rkey;
@@ -1233,11 +1234,12 @@ int qmm_mul_mat_noalloc(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor
 // dst strides and the expert count are those of the route already there): pair (i, t) reads
 // activation column (i % ne11) + t ne11 and writes dst floats t dnb2 + i dnb1
 // with defer, a route that has to run is handed back (*pending) for the quantization launch
+// (shared: every token has one more slot, n_used, holding the shared expert: tasks of matrix n_as)
 static int route_tasks(qmm_ctx * ctx, const qmm_tensor * ids, int64_t ne11, int64_t n_as, int64_t dnb1, int64_t dnb2,
                        int64_t max_tasks, GemvTask ** tasks, int32_t ** ntasks, PendingRoute * defer = nullptr,
-                       bool * pending = nullptr) {
+                       bool * pending = nullptr, int shared = 0) {
     if (pending) *pending = false;
-    const int64_t n_used = ids->ne[0], T = ids->ne[1], npairs = n_used * T;
+    const int64_t n_used = ids->ne[0], T = ids->ne[1], npairs = (n_used + shared) * T;
     const size_t o_tasks = align_up((size_t)npairs * 4, 256);
     const size_t o_cnt = align_up(o_tasks + (size_t)max_tasks * sizeof(GemvTask), 256);
     int rc = ensure(ctx, &ctx->route, &ctx->route_cap, o_cnt + 256);
@@ -1249,7 +1251,7 @@ static int route_tasks(qmm_ctx * ctx, const qmm_tensor * ids, int64_t ne11, int6
     const bool hit = ctx->in_graph && rk.valid && rk.gen == ctx->graph_gen && rk.ids.buffer == ids->buffer &&
                      rk.ids.offs == ids->offs && !memcmp(rk.ids.ne, ids->ne, sizeof(ids->ne)) &&
                      !memcmp(rk.ids.nb, ids->nb, sizeof(ids->nb)) && rk.ne11 == ne11 && rk.n_as == n_as &&
-                     rk.dnb1 == dnb1 && rk.dnb2 == dnb2;
+                     rk.dnb1 == dnb1 && rk.dnb2 == dnb2 && rk.shared == shared;
     if (hit) return QMM_OK;
     RouteArgs r;
     r.ids = (const int32_t *)((const uint8_t *)ids->buffer->ptr + ids->offs);
@@ -1262,6 +1264,7 @@ static int route_tasks(qmm_ctx * ctx, const qmm_tensor * ids, int64_t ne11, int6
     r.dst_nb1 = dnb1;
     r.dst_nb2 = dnb2;
     r.bad_id = ctx->dflags;
+    r.shared = shared;
     if (defer) {
         *defer = PendingRoute{ r, (int32_t *)rb, *tasks, *ntasks };
         *pending = true;
@@ -1273,14 +1276,16 @@ static int route_tasks(qmm_ctx * ctx, const qmm_tensor * ids, int64_t ne11, int6
     rk.n_as = n_as;
     rk.dnb1 = dnb1;
     rk.dnb2 = dnb2;
+    rk.shared = shared;
     rk.gen = ctx->graph_gen;
     rk.valid = ctx->in_graph;
     return QMM_OK;
 }
 
 // tasks of one route: (token, slot) pairs of one expert, 1..8 per task, plus the invalid bucket
-static int64_t route_max_tasks(int64_t npairs, int64_t n_as) {
-    return npairs / kMaxTaskCols + std::min(n_as + 1, npairs) + 1;
+// (and with the shared expert's slot, its bucket)
+static int64_t route_max_tasks(int64_t npairs, int64_t n_as, int shared = 0) {
+    return npairs / kMaxTaskCols + std::min(n_as + 1 + shared, npairs) + 1;
 }
 
 // The grouped GEMM's route: units of up to 64 pairs of one expert (the invalid ids' bucket
@@ -1574,6 +1579,127 @@ static bool glu_op_ok(int32_t op) {
            op == QMM_GLU_GEGLU_QUICK;
 }
 
+// The MoE FFN block at 16 tokens or more: the router (when given logits), then one route and
+// activation quantization, the gate/up + GLU products over the route's tasks, the down
+// product's route and quantization, its products, and the combine - with the shared expert as
+// one more slot of every token in both routes (bucket n_as: tasks of matrix n_as read its
+// images), so it streams inside the routed launches on their quantization instead of running
+// as its own five launches.  h [M][slots][T] and the expert rows [OUT][slots][T] live in the
+// context's scratch.
+static int moe_ffn_route(qmm_ctx * ctx, const qmm_moe_ffn_args * args, int type, const WView & wg, const WView & wu,
+                         const WView & wd, const WView & wsg, const WView & wsu, const WView & wsd, int64_t HID, int64_t M,
+                         int64_t OUT, int64_t n_as, int64_t n_used, int64_t T, bool sh, bool xt2, bool dt2) {
+    const qmm_tensor *x = args->x, *ids = args->ids, *weights = args->weights, *dst = args->dst;
+    const int shared = sh ? 1 : 0;
+    const int64_t nsl = n_used + shared, npairs = nsl * T;
+    int rc;
+    // experts averaging the grouped GEMM's pair count stream faster through the ops' grouped
+    // GEMM than through 8-column tasks: decline, nothing enqueued
+    if (use_moe_gemm(type, wg, n_used * T, n_as) || use_moe_gemm(type, wd, n_used * T, n_as))
+        return fail(ctx, QMM_ERR_UNSUPPORTED, "moe_ffn: the experts' pairs take the grouped GEMM: run the ops");
+    const int64_t max_tasks = route_max_tasks(npairs, n_as, shared);
+    const int nc = (int)std::min<int64_t>(kMaxTaskCols, npairs);
+    const bool in_wg = max_tasks * wg.ntiles >= 1024;             // as qmm_mul_mat_id_glu
+    GemvPlan p1, p2;
+    if (!gemv_plan(type, wg, nc, in_wg ? max_tasks : 2 * max_tasks, false, npairs >= 2 * n_as, &p1) ||
+        !gemv_plan(type, wd, nc, max_tasks, false, npairs >= 2 * n_as, &p2))
+        return fail(ctx, QMM_ERR_UNSUPPORTED, "moe_ffn: GEMV shape out of range");
+    if (args->logits) {
+        if ((rc = qmm_moe_topk(ctx, args->logits, ids, weights, args->cmin, args->cmax))) return rc;
+    }
+    // scratch: h, then the expert rows, then (the few-work-group form) the gate and up halves
+    const size_t hb = (size_t)(M * npairs), eb = (size_t)(OUT * npairs);
+    if ((rc = ensure(ctx, &ctx->glu, &ctx->glu_cap, (hb + eb + (in_wg ? 0 : 2 * hb)) * sizeof(float)))) return rc;
+    float * h = (float *)ctx->glu, * ex = h + hb, * sg = ex + eb;
+    qmm_buffer scratch{ ctx->glu, ctx->glu_cap };
+    // x as MUL_MAT_ID's src1 [HID, 1, T]
+    qmm_tensor xs = *x;
+    xs.ne[0] = HID;
+    xs.ne[1] = 1;
+    xs.ne[2] = T;
+    xs.ne[3] = 1;
+    xs.nb[2] = xt2 ? x->nb[1] : x->nb[2];
+    xs.nb[3] = xs.nb[2] * (size_t)T;
+    // gate/up + GLU into h
+    GemvTask * tasks;
+    int32_t * ntasks;
+    PendingRoute pr;
+    bool pending;
+    ActBuf a{};
+    if ((rc = route_tasks(ctx, ids, 1, n_as, M, M * nsl, max_tasks, &tasks, &ntasks, &pr, &pending, shared))) return rc;
+    if ((rc = quantize_src1(ctx, type, &xs, false, &a, nullptr, pending ? &pr : nullptr))) {
+        ctx->rkey.valid = false;
+        return rc;
+    }
+    GemvPair gp;
+    gp.base2 = wu.base;
+    gp.up_doff = in_wg ? 0 : (int64_t)hb;
+    gp.glu = in_wg ? args->glu_op : -1;
+    gp.sh_mat = sh ? (int32_t)n_as : -1;
+    gp.sh_base = wsg.base;
+    gp.sh_base2 = wsu.base;
+    QMM_HIP(ctx, launch_gemv(type, wg, p1, a, tasks, ntasks, nullptr, in_wg ? h : sg, ctx->sink, ctx->stream, nullptr, &gp));
+    if (!in_wg) {
+        GluArgs g;
+        g.gate = sg;
+        g.up = sg + hb;
+        g.dst = h;
+        g.M = M;
+        g.N = nsl;
+        g.nb = T;
+        g.ne12 = T;
+        g.d_nb1 = M;
+        g.d_nb2 = M * nsl;
+        g.d_nb3 = 0;
+        QMM_HIP(ctx, launch_glu(args->glu_op, g, ctx->stream));
+    }
+    // down over h [M, slots, T] into the expert rows [OUT, slots, T]
+    qmm_tensor hs{};
+    hs.type = QMM_TYPE_F32;
+    hs.buffer = &scratch;
+    hs.offs = 0;
+    hs.ne[0] = M;
+    hs.ne[1] = nsl;
+    hs.ne[2] = T;
+    hs.ne[3] = 1;
+    hs.nb[0] = 4;
+    hs.nb[1] = (size_t)M * 4;
+    hs.nb[2] = (size_t)(M * nsl) * 4;
+    hs.nb[3] = hs.nb[2] * (size_t)T;
+    ActBuf a2{};
+    if ((rc = route_tasks(ctx, ids, nsl, n_as, OUT, OUT * nsl, max_tasks, &tasks, &ntasks, &pr, &pending, shared))) return rc;
+    rc = quantize_src1(ctx, type, &hs, false, &a2, nullptr, pending ? &pr : nullptr);
+    ctx->key.valid = false;                                       // (h's buffer is this call's own)
+    ctx->rkey.valid = false;
+    if (rc) return rc;
+    GemvPair dp;
+    dp.base2 = nullptr;
+    dp.up_doff = 0;
+    dp.glu = -1;
+    dp.sh_mat = sh ? (int32_t)n_as : -1;
+    dp.sh_base = wsd.base;
+    QMM_HIP(ctx, launch_gemv(type, wd, p2, a2, tasks, ntasks, nullptr, ex, ctx->sink, ctx->stream, nullptr, &dp));
+    // the routed rows times their weights in slot order, then the (gated) shared row
+    CombineArgs c{};
+    c.experts = (const char *)ex;
+    c.w = (const char *)weights->buffer->ptr + weights->offs;
+    c.shared = sh ? (const char *)(ex + n_used * OUT) : nullptr;
+    c.gate = args->shared_logit ? (const char *)args->shared_logit->buffer->ptr + args->shared_logit->offs : nullptr;
+    c.dst = (char *)dst->buffer->ptr + dst->offs;
+    c.M = OUT;
+    c.T = T;
+    c.k = (int)n_used;
+    c.enb1 = OUT * 4;
+    c.enb2 = OUT * nsl * 4;
+    c.wnb1 = (int64_t)weights->nb[1];
+    c.snb1 = OUT * nsl * 4;
+    c.gnb1 = args->shared_logit ? (int64_t)args->shared_logit->nb[1] : 0;
+    c.dnb1 = (int64_t)(dt2 ? dst->nb[1] : dst->nb[2]);
+    QMM_HIP(ctx, launch_combine(c, ctx->stream));
+    ctx->path = "moe-ffn-route";
+    return QMM_OK;
+}
+
 int qmm_moe_ffn(qmm_ctx * ctx, const qmm_moe_ffn_args * args) {
     if (!ctx) return QMM_ERR_INVALID;
     if (!args) return fail(ctx, QMM_ERR_INVALID, "moe_ffn: null args");
@@ -1640,9 +1766,11 @@ int qmm_moe_ffn(qmm_ctx * ctx, const qmm_moe_ffn_args * args) {
             return fail(ctx, QMM_ERR_UNSUPPORTED, "moe_ffn: the router takes n_as <= 1024 and 1 <= n_used <= min(32, n_as)");
     }
     const int64_t nsl = n_used + (sh ? 1 : 0);
-    if (!fused_on() || T >= moe_direct_tokens())
-        return fail(ctx, QMM_ERR_UNSUPPORTED, "moe_ffn: %lld tokens: the fused block takes fewer than %lld (run the "
-                                              "ops one by one)", (long long)T, (long long)moe_direct_tokens());
+    if (n_used > 64) return fail(ctx, QMM_ERR_UNSUPPORTED, "moe_ffn: more than 64 slots a token");
+    if (!fused_on() || T >= moe_direct_tokens()) {
+        QMM_HIP(ctx, hipSetDevice(ctx->device));
+        return moe_ffn_route(ctx, args, type, wg, wu, wd, wsg, wsu, wsd, HID, M, OUT, n_as, n_used, T, sh, xt2, dt2);
+    }
     FusedPlan p1, p2;
     if (!gemv_fused_plan(type, wg, 1, nsl * T, gemv_fused_waves_target(), &p1) ||
         !gemv_fused_plan(type, wd, 1, nsl * T, gemv_fused_waves_target(), &p2) || nsl > 65535 ||

@@ -257,6 +257,11 @@ struct GemvPair {
     const uint8_t * base2;
     int64_t up_doff;
     int glu = -1;
+    // list mode: tasks of matrix sh_mat read the shared expert's images instead (sh_base, and
+    // sh_base2 for base2's); -1: none
+    int32_t sh_mat = -1;
+    const uint8_t * sh_base = nullptr;
+    const uint8_t * sh_base2 = nullptr;
 };
 hipError_t launch_gemv(int type, const WView & w, const GemvPlan & plan, const ActBuf & a, const GemvTask * tasks,
                        const int32_t * ntasks_dev, const GemvDense * dense, float * dst, const void * sink,
@@ -427,6 +432,9 @@ struct RouteArgs {
     int64_t n_used, T, ne11, n_as;
     int64_t dst_nb1, dst_nb2;   // float strides of dst dims 1 and 2
     int32_t * bad_id;           // set to 1 (a plain store) when an id is >= n_as
+    int32_t shared = 0;         // 1: every token has one more slot, n_used, holding the shared
+                                // expert (no id read): its pairs go to bucket n_as, tasks of
+                                // matrix n_as; the invalid ids' bucket moves to n_as + 1
 };
 // MoE router: for each token t (logits column, n_expert <= 1024 floats at logits + t nbl1),
 // ids [k] (i32 at ids + t nbi1) and weights [k] (f32 at w + t nbw1), k <= 32

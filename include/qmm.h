@@ -297,10 +297,11 @@ int    qmm_moe_topk(qmm_ctx * ctx, const qmm_tensor * logits, const qmm_tensor *
  * or neither (NULL). */
 int    qmm_moe_combine(qmm_ctx * ctx, const qmm_tensor * experts, const qmm_tensor * weights,
                        const qmm_tensor * shared, const qmm_tensor * gate, const qmm_tensor * dst);
-/* A MoE FFN block in two launches: llama.cpp's build_moe_ffn from the router's logits (or its
- * ids and weights) on: the router (SOFT_MAX, ARGSORT, GET_ROWS, SUM_ROWS, CLAMP, DIV, as
- * qmm_moe_topk), MUL_MAT_ID gate and up, the GLU, MUL_MAT_ID down, MUL by the weights, the ADDs
- * over the slots, with an optional shared expert (its gate and up MUL_MATs, GLU, down MUL_MAT,
+/* A MoE FFN block in two launches (below 16 tokens; from 16, five after the router's):
+ * llama.cpp's build_moe_ffn from the router's logits (or its ids and weights) on: the router
+ * (SOFT_MAX, ARGSORT, GET_ROWS, SUM_ROWS, CLAMP, DIV, as qmm_moe_topk), MUL_MAT_ID gate and
+ * up, the GLU, MUL_MAT_ID down, MUL by the weights, the ADDs over the slots, with an optional
+ * shared expert (its gate and up MUL_MATs, GLU, down MUL_MAT,
  * times the sigmoid of its gate logit, added last) - the chain the reference runs node by node
  * (its fused router kernel_topk_moe_softmax_norm P09:899-1000, the gate/up/down MUL_MAT_IDs at
  * P01:1189-1248 with the GLU of fuse_mm_glu, the weights' MUL and ADDs on its element-wise
@@ -308,19 +309,23 @@ int    qmm_moe_combine(qmm_ctx * ctx, const qmm_tensor * experts, const qmm_tens
  * qmm_mul_mat and qmm_moe_combine run as six dependent launches:
  *   dst[:, t] = sum_j weights[j, t] down[ids[j, t]] glu(gate[ids[j, t]] x_t, up[ids[j, t]] x_t)
  *               (+ sigmoid(shared_logit[0, t]) shared_down glu(shared_gate x_t, shared_up x_t))
- * with each weight product rounded and the slots' sum taken in a pairwise tree (not slot by
- * slot: equal to qmm_moe_combine's to float rounding).  With logits (f32 [n_as, T]) the ids and
+ * with each weight product rounded and the slots added in slot order, the shared row last (the
+ * graph's ADD order), or, when the down launch has fewer than 256 (tile, token) work-groups, in a
+ * pairwise tree (equal to qmm_moe_combine's to float rounding).  With logits (f32 [n_as, T]) the ids and
  * weights are outputs, written with qmm_moe_topk's values (cmin / cmax clamp the winners' weight
  * sum; n_as <= 1024, n_used <= 32); without, they are inputs.  gate and up experts [K, M, n_as],
  * down [M, n_out, n_as], one type; x f32 [K, T] or [K, 1, T]; ids i32 and weights f32
  * [n_used, T]; the shared expert all three of shared_gate / shared_up [K, M] and shared_down
  * [M, n_out] of the experts' type, or none; shared_logit f32 [1, T] or NULL (the shared expert
  * unweighted); dst f32 [n_out, T] or [n_out, 1, T].  A negative id adds nothing, an id >= n_as
- * adds nothing and raises QMM_ERR_INVALID at the next qmm_synchronize.  Returns
- * QMM_ERR_UNSUPPORTED (nothing enqueued) at 16 tokens or more (QMM_MOE_DIRECT_T) or when the
- * shared expert's type or shapes differ from the experts': then run the ops one by one.  The
- * reference has no one call for the block: a ggml backend adaptor matches the node chain (from
- * the router's SOFT_MAX to the last ADD) and makes this call in its place. */
+ * adds nothing and raises QMM_ERR_INVALID at the next qmm_synchronize.  From 16 tokens
+ * (QMM_MOE_DIRECT_T) the block runs as routes: the router, then gate/up + GLU and down as expert
+ * tasks with the shared expert one more slot of every token, then the combine in slot order
+ * (qmm_moe_combine's sums).  Returns QMM_ERR_UNSUPPORTED (nothing enqueued) when the shared
+ * expert's type or shapes differ from the experts', or when the experts average the pair count
+ * from which MUL_MAT_ID takes the grouped GEMM (QMM_MOE_GEMM_MIN): then run the ops one by one.
+ * The reference has no one call for the block: a ggml backend adaptor matches the node chain
+ * (from the router's SOFT_MAX to the last ADD) and makes this call in its place. */
 typedef struct qmm_moe_ffn_args {
     const qmm_tensor * gate_exps;      /* [K, M, n_as] */
     const qmm_tensor * up_exps;        /* [K, M, n_as] */
@@ -356,7 +361,7 @@ int64_t qmm_downgrades(qmm_ctx * ctx, char * buf, size_t buf_len);
  * streaming GEMM).  qmm_mul_mat_glu: "glu-fused-gemv-fq", "glu-fused-gemv", "glu-fused-gemv-mfma"
  * (gate and up in one launch) or "glu-" + the MUL_MAT path (two products and a GLU kernel).
  * qmm_mul_mat_id_glu: "glu-gemv-id-fq", "glu-gemv-id", "glu-gemv-id-mfma".  The router and the
- * combine: "moe-topk", "moe-combine"; qmm_moe_ffn: "moe-ffn-fq". */
+ * combine: "moe-topk", "moe-combine"; qmm_moe_ffn: "moe-ffn-fq" (below 16 tokens), "moe-ffn-route". */
 const char * qmm_last_path(qmm_ctx * ctx);
 
 /* The launch a qmm_mul_mat with these tensors would make (host only, no

@@ -402,11 +402,139 @@ def test_c3_moe_ffn_bad_ids_and_limits(be, bufs, moe_w, monkeypatch, slotw):
     be.moe_ffn(wg, wu, wd, xt, i32(be, over, bufs), wts, empty(be, (HID, T), bufs))
     with pytest.raises(qmm.QmmError):
         be.synchronize()
-    T16 = 16
-    x16 = f32(be, synth.activations(T16, HID, 441), bufs)
+
+
+# ------------------------------------------------------------------ C3: the block from 16 tokens
+@pytest.mark.parametrize("T", [16, 64, 256])
+@pytest.mark.parametrize("shared", [True, False])
+def test_c3_moe_ffn_route_form(be, bufs, moe_w, T, shared):
+    """qmm_moe_ffn from 16 tokens: the route form (the shared expert as one more slot of every token
+    in both routes, its pairs streaming in the routed launches) against the op-by-op chain on the
+    GPU on the same router output (mul_mat_id_glu, mul_mat_id, and for the shared expert
+    mul_mat_glu and mul_mat, then moe_combine).  The routed rows come from the same kernels (bar:
+    float rounding, 1e-5 floored).  The shared expert's come from the routed GEMV's 8-column tasks
+    instead of the dense product's kernels: its GLU rows differ at the 1e-7 level, which can flip a
+    q8 code when they are quantized for the down product and move an output by about one code's
+    share of a 512-term sum (~1e-3 of the output rms; test_c3_layer_chain's note), so with the
+    shared expert the bar is 2e-3 of the rms (a wrong expert, slot or weight moves outputs by the
+    whole rms)"""
+    name = f"C3 moe_ffn route form T={T} shared={shared}"
+    say(name)
+    x, sgl, ids, wts = c3_chain_inputs(be, bufs, T, 500 + T)
+    xt = f32(be, x.reshape(T, 1, HID), bufs)
+    x2 = qmm.Tensor(xt.buf, qmm.F32, (HID, T))
+    sg = f32(be, sgl, bufs)
+    (_, wg), (_, wu), (_, wd) = moe_w["gate"], moe_w["up"], moe_w["down"]
+    h = empty(be, (FFN, N_USED, T), bufs)
+    ex = empty(be, (HID, N_USED, T), bufs)
+    ref_t = empty(be, (HID, T), bufs)
+    be.mul_mat_id_glu(wg, wu, xt, ids, h, qmm.GLU_SWIGLU)
+    be.mul_mat_id(wd, qmm.Tensor(h.buf, qmm.F32, (FFN, N_USED, T)), ids, ex)
+    sh = None
+    if shared:
+        sh = tuple(moe_w[k][1] for k in ("sgate", "sup", "sdown"))
+        hs = empty(be, (FFN, T), bufs)
+        ys = empty(be, (HID, T), bufs)
+        be.mul_mat_glu(sh[0], sh[1], x2, hs, qmm.GLU_SWIGLU)
+        be.mul_mat(sh[2], hs, ys)
+        be.moe_combine(ex, wts, ref_t, ys, sg)
+    else:
+        be.moe_combine(ex, wts, ref_t)
+    out = empty(be, (HID, T), bufs)
+    be.moe_ffn(wg, wu, wd, xt, ids, wts, out, shared=sh, shared_logit=sg if shared else None)
+    assert be.last_path() == "moe-ffn-route"
+    be.synchronize()
+    r = err_report(be.get_f32(out).reshape(T, HID), be.get_f32(ref_t).reshape(T, HID))
+    print(f"[err] {name}: floored {r['floored']:.3g}, max |err| {r['max_abs_err_over_rms']:.2g} rms", flush=True)
+    if shared:
+        assert r["max_abs_err_over_rms"] <= 2e-3, r
+    else:
+        assert r["floored"] <= 1e-5, r
+    # again (the route scratch and the activation cache are this call's own), and the shared expert
+    # without its gate logit (its row added unweighted)
+    out2 = empty(be, (HID, T), bufs)
+    be.moe_ffn(wg, wu, wd, x2, ids, wts, out2, shared=sh, shared_logit=sg if shared else None)
+    be.synchronize()
+    assert np.array_equal(be.get_f32(out).view(np.uint32), be.get_f32(out2).view(np.uint32))
+    if shared:
+        ys_h = be.get_f32(ys).reshape(T, HID)
+        out3 = empty(be, (HID, T), bufs)
+        be.moe_ffn(wg, wu, wd, xt, ids, wts, out3, shared=sh)
+        ref3 = empty(be, (HID, T), bufs)
+        be.moe_combine(ex, wts, ref3)
+        be.synchronize()
+        r3 = err_report(be.get_f32(out3).reshape(T, HID), be.get_f32(ref3).reshape(T, HID) + ys_h)
+        assert r3["max_abs_err_over_rms"] <= 2e-3, r3
+
+
+@pytest.mark.parametrize("T", [16, 100])
+def test_c3_moe_ffn_route_form_router_and_ids(be, bufs, moe_w, T):
+    """the route form given the router's logits writes qmm_moe_topk's ids and weights bit for bit
+    and the output of the call given them; a negative id adds nothing (equal to a zero weight), an
+    id >= n_as adds nothing and raises at synchronize"""
+    say(f"C3 moe_ffn route form router T={T}")
+    g = np.random.default_rng(520 + T)
+    logits = f32(be, g.standard_normal((T, E)).astype(np.float32), bufs)
+    x = f32(be, synth.activations(T, HID, 521 + T), bufs)
+    sgl = f32(be, g.standard_normal((T, 1)).astype(np.float32), bufs)
+    sh = tuple(moe_w[k][1] for k in ("sgate", "sup", "sdown"))
+    (_, wg), (_, wu), (_, wd) = moe_w["gate"], moe_w["up"], moe_w["down"]
+    ids_a, w_a = i32(be, np.zeros((T, N_USED), np.int32), bufs), empty(be, (N_USED, T), bufs)
+    ids_b, w_b = i32(be, np.zeros((T, N_USED), np.int32), bufs), empty(be, (N_USED, T), bufs)
+    out_a, out_b = empty(be, (HID, T), bufs), empty(be, (HID, T), bufs)
+    be.moe_topk(logits, ids_a, w_a)
+    be.moe_ffn(wg, wu, wd, x, ids_a, w_a, out_a, shared=sh, shared_logit=sgl)
+    be.moe_ffn(wg, wu, wd, x, ids_b, w_b, out_b, shared=sh, shared_logit=sgl, logits=logits)
+    assert be.last_path() == "moe-ffn-route"
+    be.synchronize()
+    assert np.array_equal(be.get_tensor(ids_a).view(np.int32), be.get_tensor(ids_b).view(np.int32))
+    assert np.array_equal(be.get_f32(w_a).view(np.uint32), be.get_f32(w_b).view(np.uint32))
+    assert np.array_equal(be.get_f32(out_a).view(np.uint32), be.get_f32(out_b).view(np.uint32))
+    idn = be.get_tensor(ids_a).view(np.int32).reshape(T, N_USED).copy()
+    wn = be.get_f32(w_a).reshape(T, N_USED).copy()
+    bad, wz = idn.copy(), wn.copy()
+    bad[0, 3] = -1
+    wz[0, 3] = 0.0
+    out_neg, out_zero = empty(be, (HID, T), bufs), empty(be, (HID, T), bufs)
+    be.moe_ffn(wg, wu, wd, x, i32(be, bad, bufs), w_a, out_neg, shared=sh, shared_logit=sgl)
+    be.moe_ffn(wg, wu, wd, x, ids_a, f32(be, wz, bufs), out_zero, shared=sh, shared_logit=sgl)
+    be.synchronize()
+    r = err_report(be.get_f32(out_neg).reshape(T, HID), be.get_f32(out_zero).reshape(T, HID))
+    assert r["floored"] <= 1e-5, r
+    over = idn.copy()
+    over[1, 2] = E
+    be.moe_ffn(wg, wu, wd, x, i32(be, over, bufs), w_a, empty(be, (HID, T), bufs), shared=sh, shared_logit=sgl)
     with pytest.raises(qmm.QmmError):
-        be.moe_ffn(wg, wu, wd, x16, i32(be, np.zeros((T16, N_USED), np.int32), bufs), empty(be, (N_USED, T16), bufs),
-                   empty(be, (HID, T16), bufs))
+        be.synchronize()
+
+
+def test_c3_moe_ffn_declines_grouped_gemm_sizes(be, bufs, moe_w, monkeypatch):
+    """when the experts average the grouped GEMM's pair count (QMM_MOE_GEMM_MIN, lowered here to
+    2 so that 256 tokens x 10 slots over 512 experts reach it) the block declines before any
+    launch: QMM_ERR_UNSUPPORTED, the router not run (ids and weights unwritten), dst untouched,
+    so that the adaptor runs the ops and MUL_MAT_ID takes the grouped GEMM"""
+    monkeypatch.setenv("QMM_MOE_GEMM_MIN", "2")
+    T = 256
+    say(f"C3 moe_ffn declines T={T} at QMM_MOE_GEMM_MIN=2")
+    g = np.random.default_rng(530)
+    logits = f32(be, g.standard_normal((T, E)).astype(np.float32), bufs)
+    x = f32(be, synth.activations(T, HID, 531), bufs)
+    (_, wg), (_, wu), (_, wd) = moe_w["gate"], moe_w["up"], moe_w["down"]
+    ids0 = np.full((T, N_USED), 7, np.int32)
+    w0 = np.full((T, N_USED), 0.25, np.float32)
+    d0 = np.full((T, HID), 3.0, np.float32)
+    ids, wts, out = i32(be, ids0, bufs), f32(be, w0, bufs), f32(be, d0, bufs)
+    with pytest.raises(qmm.QmmError, match="grouped GEMM"):
+        be.moe_ffn(wg, wu, wd, x, ids, wts, out, logits=logits)
+    be.synchronize()
+    assert np.array_equal(be.get_tensor(ids).view(np.int32).reshape(T, N_USED), ids0)
+    assert np.array_equal(be.get_f32(wts).reshape(T, N_USED), w0)
+    assert np.array_equal(be.get_f32(out).reshape(T, HID), d0)
+    # the same call at the default threshold runs the route form
+    monkeypatch.delenv("QMM_MOE_GEMM_MIN")
+    be.moe_ffn(wg, wu, wd, x, ids, wts, out, logits=logits)
+    assert be.last_path() == "moe-ffn-route"
+    be.synchronize()
 
 
 @pytest.mark.parametrize("T", [1, 4, 15])
