@@ -126,6 +126,12 @@ struct KQParams {
     const float * dcol;                  // [column][nsb]
     const int8_t * bsp;                  // [super-block][ldT][16]
     int64_t ldk, ldT, ncols;
+    // grouped mode with a GLU (glu >= 0): this launch is the up product, gsrc the gate product's
+    // rows at the same offsets; stores act(gate) * up.  dspan: floats of dst (and gsrc) the
+    // stores may reach, below 2^30
+    const float * gsrc;
+    int glu;
+    int64_t dspan;
 };
 
 // The work-group's block L and K piece (-1: the whole K) from its index bx.  Blocks [0, full)
@@ -184,6 +190,13 @@ __device__ __forceinline__ uint32_t kq_meet(uint32_t * nodes, int piece, int ts,
         n = (n + 1) >> 1;
     }
     return live;
+}
+
+// v[i] = act(g[i]) * v[i] for one GLU op, as the split GLU computes it (glu_apply)
+template <int OP>
+__device__ __forceinline__ void glu_rows(const float (&g)[32], float (&v)[32]) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) v[i] = glu_apply(OP, g[i], v[i]);
 }
 
 // the two 16-bit halves of v times those of s (v_pk_mul_lo_u16)
@@ -484,15 +497,39 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q4k(KQParams p) {
     const int64_t m = mtile * kTileRows + 32 * t + j32;
     if (m >= p.w.M) return;
     if constexpr (GATHER) {
+        // every destination offset (and gate value) is requested before the first store, and no
+        // load or store sits in a branch: through buffer resources over dst's span an offset past
+        // it (kNoStore: a slot past the unit) reads zero and drops its store.  (Conditional
+        // accesses, and loads after stores to dst that might alias them, made each of the 32
+        // stores wait for a memory round trip.)
+        constexpr uint32_t kNoStore = 0xffffffffu;
+        const uint32_t span4 = (uint32_t)(p.dspan * 4);
+        const __amdgpu_buffer_rsrc_t dres = buffer_rsrc(p.dst, span4);
+        uint32_t off[32];
+        float val[32];
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-            const v16f & v = c ? out1 : out0;
+        for (int i = 0; i < 32; ++i) {
+            const int slot = 32 * (i >> 4) + 8 * ((i & 15) >> 2) + 4 * h + (i & 3);   // < 64: in the unit
+            const int64_t o = p.units[nb].c[slot].dst_off + m;
+            off[i] = slot < ncu ? 4u * (uint32_t)o : kNoStore;
+            val[i] = i < 16 ? out0[i] : out1[i - 16];
+        }
+        if (p.glu >= 0) {                                         // uniform
+            const __amdgpu_buffer_rsrc_t gres = buffer_rsrc(p.gsrc, span4);
+            float gv[32];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int slot = 32 * c + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (slot < ncu) __builtin_nontemporal_store(v[r], p.dst + p.units[nb].c[slot].dst_off + m);
+            for (int i = 0; i < 32; ++i) gv[i] = __uint_as_float(bld4(gres, off[i], 0));
+            // one branch for the op, then straight-line code over the values
+            switch (p.glu) {
+                case QMM_GLU_REGLU: glu_rows<QMM_GLU_REGLU>(gv, val); break;
+                case QMM_GLU_GEGLU: glu_rows<QMM_GLU_GEGLU>(gv, val); break;
+                case QMM_GLU_SWIGLU: glu_rows<QMM_GLU_SWIGLU>(gv, val); break;
+                case QMM_GLU_GEGLU_ERF: glu_rows<QMM_GLU_GEGLU_ERF>(gv, val); break;
+                default: glu_rows<QMM_GLU_GEGLU_QUICK>(gv, val); break;
             }
         }
+#pragma unroll
+        for (int i = 0; i < 32; ++i) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val[i]), dres, (int)off[i], 0, 0);
         return;
     }
     // a tail piece: the block's pieces meet first, the holder of a sum stores it
@@ -885,9 +922,14 @@ bool gemm3_id_shape(const WView & w, int64_t max_units, G3Shape * sh) {
 }
 
 hipError_t launch_gemm3_id(int type, const WView & w, const ActBuf & a, const GemmUnit * units, const int32_t * nunits,
-                           int64_t max_units, float * dst, hipStream_t s, const KTime * kt) {
+                           int64_t max_units, float * dst, int64_t dst_span, hipStream_t s, const KTime * kt,
+                           const float * gsrc, int glu) {
     G3Shape sh;
     if (!gemm3_id_supported(type) || a.vdt != QMM_TYPE_Q8_K || !a.bsp || !units || !nunits || a.ldk != w.G * 256 ||
+        dst_span <= 0 || dst_span >= ((int64_t)1 << 30) ||
+        (glu >= 0) != (gsrc != nullptr) ||
+        (glu != -1 && glu != QMM_GLU_REGLU && glu != QMM_GLU_GEGLU && glu != QMM_GLU_SWIGLU &&
+         glu != QMM_GLU_GEGLU_ERF && glu != QMM_GLU_GEGLU_QUICK) ||
         !gemm3_id_shape(w, max_units, &sh) || a.ncols * a.ldk >= ((int64_t)1 << 31) ||
         w.G * a.ldT * 16 >= ((int64_t)1 << 31) || a.ldT < a.ncols)
         return hipErrorInvalidValue;
@@ -913,6 +955,9 @@ hipError_t launch_gemm3_id(int type, const WView & w, const ActBuf & a, const Ge
     q.ldk = a.ldk;
     q.ldT = a.ldT;
     q.ncols = a.ncols;
+    q.gsrc = gsrc;
+    q.glu = glu;
+    q.dspan = dst_span;
     const dim3 g((unsigned)(8 * q.fchunk), 1u), b(sh.threads);
     return launch_kq_u<true>(q, sh, g, b, s, kt);
 }

@@ -1326,6 +1326,13 @@ static int64_t moe_gemm_min_pairs() {
     const char * e = getenv("QMM_MOE_GEMM_MIN");
     return e ? atoll(e) : 32;
 }
+// floats from a MUL_MAT_ID dst's first element to one past its last (the grouped GEMM stores
+// through 32-bit byte offsets: it takes spans below 2^30 floats)
+static int64_t id_dst_span(const qmm_tensor * dst) {
+    return (dst->ne[1] - 1) * (int64_t)(dst->nb[1] / 4) + (dst->ne[2] - 1) * (int64_t)(dst->nb[2] / 4) +
+           (dst->ne[3] - 1) * (int64_t)(dst->nb[3] / 4) + dst->ne[0];
+}
+constexpr int64_t kMaxIdSpan = ((int64_t)1 << 30) - 1;
 static bool use_moe_gemm(int type, const WView & w, int64_t npairs, int64_t n_as) {
     const int64_t mn = moe_gemm_min_pairs();
     G3Shape sh;
@@ -1367,7 +1374,7 @@ int qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * sr
         return rc;
     }
     float * dptr = (float *)((uint8_t *)dst->buffer->ptr + dst->offs);
-    if (use_moe_gemm(src0->type, w, npairs, n_as)) {
+    if (use_moe_gemm(src0->type, w, npairs, n_as) && id_dst_span(dst) <= kMaxIdSpan) {
         const int64_t max_units = route_max_units(npairs, n_as);
         GemmUnit * units;
         int32_t * nunits;
@@ -1380,7 +1387,7 @@ int qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * sr
         KTime kt;
         const KTime * ktp;
         if ((rc = ktime_pair(ctx, &kt, &ktp))) return rc;
-        QMM_HIP(ctx, launch_gemm3_id(src0->type, w, a, units, nunits, max_units, dptr, ctx->stream, ktp));
+        QMM_HIP(ctx, launch_gemm3_id(src0->type, w, a, units, nunits, max_units, dptr, id_dst_span(dst), ctx->stream, ktp));
         return ktime_done(ctx);
     }
     const int64_t max_tasks = route_max_tasks(npairs, n_as);
@@ -1441,6 +1448,25 @@ int qmm_mul_mat_id_glu(qmm_ctx * ctx, const qmm_tensor * gate, const qmm_tensor 
     if (try_fused_id(ctx, gate, src1, ids, dst, wg, wu.base, glu_op, &rc)) {
         ctx->path = "glu-gemv-id-fq";
         return rc;
+    }
+    if (use_moe_gemm(gate->type, wg, npairs, n_as) && id_dst_span(dst) <= kMaxIdSpan) {
+        // the grouped GEMM: one route and quantization for both products; gate into the scratch
+        // at dst's offsets, then up with act(gate) * up applied at its stores
+        const int64_t dnb1 = (int64_t)(dst->nb[1] / 4), dnb2 = (int64_t)(dst->nb[2] / 4);
+        const int64_t span = id_dst_span(dst);
+        if ((rc = ensure(ctx, &ctx->glu, &ctx->glu_cap, (size_t)span * sizeof(float)))) return rc;
+        const int64_t max_units = route_max_units(npairs, n_as);
+        GemmUnit * units;
+        int32_t * nunits;
+        PendingRoute pr;
+        if ((rc = route_units(ctx, ids, src1->ne[1], n_as, dnb1, dnb2, max_units, &units, &nunits, &pr))) return rc;
+        if ((rc = quantize_src1(ctx, gate->type, src1, false, &a, nullptr, &pr))) return rc;
+        float * g = (float *)ctx->glu;
+        float * d = (float *)((uint8_t *)dst->buffer->ptr + dst->offs);
+        QMM_HIP(ctx, launch_gemm3_id(gate->type, wg, a, units, nunits, max_units, g, span, ctx->stream));
+        QMM_HIP(ctx, launch_gemm3_id(up->type, wu, a, units, nunits, max_units, d, span, ctx->stream, nullptr, g, glu_op));
+        ctx->path = "glu-gemm-id-stream";
+        return QMM_OK;
     }
     const int64_t max_tasks = route_max_tasks(npairs, n_as);
     const int nc = (int)std::min<int64_t>(kMaxTaskCols, npairs);

@@ -30,7 +30,8 @@ Also reported, on the same JSON line:
                 the layer's HBM roofline, and each op's own time
   moe_grouped   MUL_MAT_ID with many tokens per expert (16 experts x 1024 tokens
                 top-10, 128 experts x 512 tokens top-8; Q4_K 512x2048): op and
-                kernel time, TOPS against the int8 peak
+                kernel time, TOPS against the int8 peak; and gate + up + SwiGLU
+                in one call at 16 x 1024 against the same op on GEMV tasks
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
@@ -271,7 +272,38 @@ def glu_case(be, qmm, synth, args):
     return out
 
 
-def moe_grouped_case(be, qmm, synth, E, n_used, M, K, T, name, args):
+def moe_grouped_glu(be, qmm, synth, ws, xt, it, yt, ids, E, n_used, M, K, T, name, args, steps):
+    """MUL_MAT_ID gate + up + SwiGLU in one call (qmm_mul_mat_id_glu), gate and up two of the
+    rotated stacks: the op's time on its default path (the grouped GEMM past 32 pairs per expert)
+    and on the 8-pair GEMV tasks (QMM_MOE_GEMM_MIN=0); TOPS = 2 products x 2 x pairs x M x K over
+    the op's time."""
+    def run(n):
+        t0 = time.perf_counter()
+        for i in range(n):
+            be.mul_mat_id_glu(ws[i % len(ws)], ws[(i + 1) % len(ws)], xt, it, yt, qmm.GLU_SWIGLU)
+        be.synchronize()
+        return (time.perf_counter() - t0) / max(n, 1)
+    run(args.warmup)
+    op_s = run(steps)
+    path = be.last_path()
+    os.environ["QMM_MOE_GEMM_MIN"] = "0"
+    try:
+        run(args.warmup)
+        tasks_s = run(steps)
+        tasks_path = be.last_path()
+    finally:
+        del os.environ["QMM_MOE_GEMM_MIN"]
+    ops = 2.0 * 2.0 * T * n_used * M * K
+    for w in ws:
+        be.free_buffer(w.buf)
+    for t in (xt, it, yt):
+        be.free_buffer(t.buf)
+    return {"workload": name, "path": path, "experts": E, "tokens": T, "n_used": n_used, "M": M, "K": K,
+            "op_us": round(op_s * 1e6, 2), "op_tops": round(ops / op_s / 1e12, 1),
+            "gemv_tasks_op_us": round(tasks_s * 1e6, 2), "gemv_tasks_path": tasks_path}
+
+
+def moe_grouped_case(be, qmm, synth, E, n_used, M, K, T, name, args, glu=False):
     """MUL_MAT_ID with many tokens per expert (Q4_K experts [K, M, E], src1 [K, 1, T], top-n_used
     of softmaxed random logits): one step = one op over one of several copies of the stack
     (>= 2 x the MALL).  TOPS = 2 x pairs x M x K over the main kernel's median; GB/s counts the
@@ -286,6 +318,8 @@ def moe_grouped_case(be, qmm, synth, E, n_used, M, K, T, name, args):
     be.set_tensor(it, ids.view(np.uint8).ravel())
     yt = be.new_tensor(qmm.F32, (M, n_used, T))
     steps = max(10, args.steps // 4)
+    if glu:
+        return moe_grouped_glu(be, qmm, synth, ws, xt, it, yt, ids, E, n_used, M, K, T, name, args, steps)
     for i in range(args.warmup):
         be.mul_mat_id(ws[i % len(ws)], xt, it, yt)
     be.synchronize()
@@ -653,7 +687,10 @@ def main():
         mg = [moe_grouped_case(be, qmm, synth, 16, 10, 512, 2048, 1024,
                                "MUL_MAT_ID 16 Q4_K experts 512x2048, 1024 tokens top-10 (640 pairs per expert)", args),
               moe_grouped_case(be, qmm, synth, 128, 8, 512, 2048, 512,
-                               "MUL_MAT_ID 128 Q4_K experts 512x2048, 512 tokens top-8 (32 pairs per expert)", args)]
+                               "MUL_MAT_ID 128 Q4_K experts 512x2048, 512 tokens top-8 (32 pairs per expert)", args),
+              moe_grouped_case(be, qmm, synth, 16, 10, 512, 2048, 1024,
+                               "MUL_MAT_ID gate + up + SwiGLU, 16 Q4_K experts 512x2048, 1024 tokens top-10", args,
+                               glu=True)]
         if out:
             out["moe_grouped"] = mg
         else:

@@ -220,7 +220,9 @@ int    qmm_mul_mat_glu(qmm_ctx * ctx, const qmm_tensor * gate, const qmm_tensor 
  * up expert stacks [K, M, n_as] of one type and shape, src1 / ids / dst as qmm_mul_mat_id's.
  * Replaces MUL_MAT_ID, MUL_MAT_ID, GLU (the reference's MUL_MAT_ID / GLU fuse, by its audit
  * docs/campaigns/research-concept-mining/ipex-llm/audit.md:83-87): one quantization, one
- * route, one GEMV launch over both stacks.  Invalid ids give zero rows. */
+ * route, one GEMV launch over both stacks; experts averaging the grouped GEMM's pair count
+ * (QMM_MOE_GEMM_MIN) take it twice, the GLU applied at the up product's stores.  Invalid ids
+ * give zero rows. */
 int    qmm_mul_mat_id_glu(qmm_ctx * ctx, const qmm_tensor * gate, const qmm_tensor * up, const qmm_tensor * src1,
                           const qmm_tensor * ids, const qmm_tensor * dst, int32_t glu_op);
 /* qmm_mul_mat with nothing allocated: no reference counterpart; for callers that cannot
@@ -360,8 +362,10 @@ int64_t qmm_downgrades(qmm_ctx * ctx, char * buf, size_t buf_len);
  * "gemv-id-mfma" (route + expert tasks on either GEMV), "gemm-id-stream" (route + the grouped
  * streaming GEMM).  qmm_mul_mat_glu: "glu-fused-gemv-fq", "glu-fused-gemv", "glu-fused-gemv-mfma"
  * (gate and up in one launch) or "glu-" + the MUL_MAT path (two products and a GLU kernel).
- * qmm_mul_mat_id_glu: "glu-gemv-id-fq", "glu-gemv-id", "glu-gemv-id-mfma".  The router and the
- * combine: "moe-topk", "moe-combine"; qmm_moe_ffn: "moe-ffn-fq" (below 16 tokens), "moe-ffn-route". */
+ * qmm_mul_mat_id_glu: "glu-gemv-id-fq", "glu-gemv-id", "glu-gemv-id-mfma", "glu-gemm-id-stream"
+ * (route + the grouped GEMM for gate, then for up with the GLU at its stores).  The router and
+ * the combine: "moe-topk", "moe-combine"; qmm_moe_ffn: "moe-ffn-fq" (below 16 tokens),
+ * "moe-ffn-route". */
 const char * qmm_last_path(qmm_ctx * ctx);
 
 /* The launch a qmm_mul_mat with these tensors would make (host only, no

@@ -1230,6 +1230,48 @@ def test_mul_mat_id_glu_per_slot_src1(be, sc, orc):
     assert rel_err(got, ref) <= TOL
 
 
+@pytest.mark.parametrize("op,bcast", [(qmm.GLU_SWIGLU, True), (qmm.GLU_GEGLU, False), (qmm.GLU_REGLU, True)])
+def test_mul_mat_id_glu_grouped_gemm(be, sc, orc, monkeypatch, op, bcast):
+    """MUL_MAT_ID gate + up + GLU on the grouped GEMM (experts averaging >= 32 pairs): one route
+    and quantization, the gate product into a scratch at dst's offsets, the up product storing
+    act(gate) * up; ragged (100 rows, 3 of 8 experts without pairs, pair counts not a multiple of
+    64), negative ids give zero rows, an id past the expert count is reported; the same op on the
+    GEMV tasks agrees"""
+    from oracle import glu as G
+    qtype, E, n_used, M, K, T = qmm.Q4_K, 8, 3, 100, 1280, 300
+    say("mul_mat_id_glu grouped gemm", op, bcast)
+    rg, ru = synth.weights(qtype, E * M, K, seed=191), synth.weights(qtype, E * M, K, seed=192)
+    g = np.random.default_rng(193)
+    ids = np.stack([g.choice([0, 2, 4, 5, 6], size=n_used, replace=False) for _ in range(T)]).astype(np.int32)
+    ids[7, 1] = -1
+    ids[11, 0] = -1
+    ne11 = 1 if bcast else n_used
+    x = synth.activations(T * ne11, K, seed=194).reshape(T, ne11, K)
+    wg, wu = sc.weights(qtype, rg, (K, M, E)), sc.weights(qtype, ru, (K, M, E))
+    y = sc.f32(np.full((T, n_used, M), 5.0, np.float32))
+    be.mul_mat_id_glu(wg, wu, sc.f32(x), sc.i32(ids), y, op)
+    be.synchronize()
+    assert be.last_path() == "glu-gemm-id-stream"
+    got = be.get_f32(y).reshape(T, n_used, M)
+    ref = G.glu(op, orc.mul_mat_id(qtype, rg, M, K, E, x, ids), orc.mul_mat_id(qtype, ru, M, K, E, x, ids))
+    assert not got[7, 1].any() and not got[11, 0].any()
+    bad = ids < 0
+    assert rel_err(got[~bad], ref[~bad]) <= TOL
+    monkeypatch.setenv("QMM_MOE_GEMM_MIN", "0")
+    y2 = sc.empty_f32((M, n_used, T))
+    be.mul_mat_id_glu(wg, wu, sc.f32(x), sc.i32(ids), y2, op)
+    be.synchronize()
+    assert be.last_path().startswith("glu-gemv-id")
+    assert rel_err(got, be.get_f32(y2).reshape(T, n_used, M)) <= TOL
+    monkeypatch.delenv("QMM_MOE_GEMM_MIN")
+    over = ids.copy()
+    over[5, 2] = E + 1
+    be.mul_mat_id_glu(wg, wu, sc.f32(x), sc.i32(over), sc.empty_f32((M, n_used, T)), op)
+    assert be.last_path() == "glu-gemm-id-stream"
+    with pytest.raises(qmm.QmmError, match="past the expert count"):
+        be.synchronize()
+
+
 def test_downgrade_keys(sc, orc, monkeypatch):
     """the downgrade export counts per key: Q5_K at 4 columns runs on the v_dot4 GEMV (no MFMA
     form), Q4_K at 40 columns takes two weight passes on the MFMA GEMV; a product on its
