@@ -95,9 +95,10 @@ constexpr int kKQMaxWaves = 12;
 // every iteration (so the barrier waits for exactly these loads, not the weight loads issued
 // after them); units past 18 read nothing (out of range) into a 1 KB slot after the stages
 __host__ __device__ constexpr int kq_units(int U) { return (18 + U - 1) / U; }
-// s_waitcnt immediates (gfx9 encoding): vmcnt 5 / 9 (bits 3:0, 15:14), expcnt and lgkmcnt not
+// s_waitcnt immediates (gfx9 encoding): vmcnt 5 / 8 / 9 (bits 3:0, 15:14), expcnt and lgkmcnt not
 // waited on
 constexpr int kVmcnt5 = 5 | (0x7 << 4) | (0xF << 8);
+constexpr int kVmcnt8 = 8 | (0x7 << 4) | (0xF << 8);
 constexpr int kVmcnt9 = 9 | (0x7 << 4) | (0xF << 8);
 
 struct KQParams {
@@ -549,6 +550,236 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q4k(KQParams p) {
     }
 }
 
+// ---- Q6_K ------------------------------------------------------------------------------------
+// Role of the reference's Q6_K prefill GEMM (kernel_mul_mm_kq2d_q6_K, P01:1776-1860: fp16 DPAS on
+// 1024 + code halves), on int8 MFMAs and ggml-cpu's numerics (q6_K x q8_K: an exact integer dot
+// per 16-weight group times its int8 scale, summed per super-block, then d_w d_x).  The frame is
+// k_gemm3_q4k's (32 rows x 64 columns per wave, q8_K activations staged in LDS one super-block
+// ahead, weights streamed by each wave, K slices met in LDS, the tail in K pieces).
+//  * The scaled weight sc (q - 32) takes 13 bits, so the scale stays out of the operand.  Lane
+//    (j, h)'s 16 weights of sub-block s (32 weights) are exactly one scale group, 2 s + h, so an
+//    MFMA whose B operand is the lane's codes with the other lane half's masked to zero gives that
+//    group's integer dot for the 32 x 32 outputs, and one v_mad_i32_i24 per output adds it times
+//    the output lane's own row scale: 4 MFMAs (2 groups x 2 column tiles) and 64 multiply-adds
+//    per sub-block and wave.
+//  * Codes: weight k = 128 n + 32 s + l of the super-block is ql[64 n + 32 (s & 1) + l] (low
+//    nibble for s < 2, high for s >= 2) with qh[32 n + l] bits 2 s, 2 s + 1 above it; lane half
+//    h holds l in [16 h, 16 h + 16): ql chunk plane 4 n + 2 (s & 1) + h, qh plane 8 + 2 n + h.
+//    q - 32 per byte without borrows: (q + 0x60) ^ 0x80 (q + 0x60 <= 0x9f).
+//  * Per super-block and output: out += dx (d isum) (ggml's d_w d_x times the integer sum).
+template <int U>
+__global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q6k(KQParams p) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, j32 = lane & 31;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int u = wave % U, ks = wave / U;
+
+    uint32_t L;
+    int piece;
+    if (!kq_block(p, blockIdx.x, L, piece)) return;           // uniform over the work-group
+    const uint32_t mb = L / (uint32_t)p.nbn, nb = L - mb * (uint32_t)p.nbn;
+    const uint32_t bz = blockIdx.y;
+    const uint32_t i2 = bz % (uint32_t)p.bt.ne12, i3 = bz / (uint32_t)p.bt.ne12;
+    const int64_t mat = (int64_t)(i2 / (uint32_t)p.bt.r2) + (int64_t)(i3 / (uint32_t)p.bt.r3) * p.bt.ne02;
+    const int64_t rh_raw = (int64_t)mb * U + u;               // the wave's row half
+    const bool row_ok = rh_raw < 2 * p.w.ntiles;              // a missing row half computes a copy, stores nothing
+    const int64_t rh = row_ok ? rh_raw : 2 * p.w.ntiles - 1;
+    const int64_t mtile = rh >> 1;
+    const int t = (int)(rh & 1);
+    const int64_t ct0 = (int64_t)bz * p.ntb + 2 * (int64_t)nb; // the pair's first column tile
+    const int64_t nct = std::min<int64_t>(2, p.ntb - 2 * (int64_t)nb);
+    const int nsb = (int)p.nsb;
+    const int kb = piece >= 0 ? piece * p.pk : 0, ke = piece >= 0 ? std::min(kb + p.pk, nsb) : nsb;
+    const int sps = piece >= 0 ? p.pk : p.sps;                // (pieces: one K slice)
+    const int s0 = kb + ks * sps;
+    const int s1 = std::min(s0 + sps, ke);                    // (every slice has super-blocks)
+
+    const __amdgpu_buffer_rsrc_t wbuf = buffer_rsrc(tile_group(p.w, mat, mtile, 0), (uint32_t)(p.w.G * p.w.tg));
+    const __amdgpu_buffer_rsrc_t abuf = buffer_rsrc(p.tA + ct0 * p.nsb * 8192, (uint32_t)(nct * p.nsb * 8192));
+    const __amdgpu_buffer_rsrc_t dbuf = buffer_rsrc(p.tD + ct0 * p.nsb * 32, (uint32_t)(nct * p.nsb * 128));
+    const uint32_t lane16 = (uint32_t)lane * 16;
+
+    // ---- staging: k_gemm3_q4k's 18 units of 1 KB per super-block (A of both tiles; unit 16, the
+    // split sums Q4_K takes, reads nothing here (an offset past the range: zeros into its slot) but
+    // keeps every wave's load count; the scales)
+    constexpr int NU = kq_units(U);
+    constexpr uint32_t kOut = 0x7ff00000u;
+    const uint32_t a_stride = (uint32_t)p.nsb * 8192, d_stride = (uint32_t)p.nsb * 128;
+    const uint32_t d_lane = lane < 16 ? (uint32_t)(lane >> 3) * d_stride + (uint32_t)(lane & 7) * 16 : kOut;
+    uint8_t * const dump = lds + 2 * p.KS * kKQStage;
+    auto stage = [&](int s, int b) {
+        uint8_t * S = lds + (ks * 2 + b) * kKQStage;
+#pragma unroll
+        for (int i = 0; i < NU; ++i) {
+            const int unit = u + i * U;                       // wave-uniform
+            if (unit < 16)
+                dma16(abuf, S + unit * 1024, lane16 + (uint32_t)(unit >> 3) * a_stride + (uint32_t)(unit & 7) * 1024,
+                      (uint32_t)s * 8192);
+            else if (unit == 16)
+                dma16(dbuf, S + 16 * 1024, kOut, 0);
+            else if (unit == 17)
+                dma16(dbuf, S + 17 * 1024, d_lane, (uint32_t)s * 128);
+            else
+                dma16(dbuf, dump, kOut, 0);                   // (nothing: keeps the count)
+        }
+    };
+
+    // ---- weights of the lane's row (32 t + j32): ql planes 4 n + 2 c + h (c = s & 1), qh planes
+    // 8 + 2 n + h, the 16 scales (plane 12), d (the tail's 2 bytes, in the row pair's dword)
+    const uint32_t row = (uint32_t)(32 * t + j32), row16 = row * 16;
+    const uint32_t tgs = (uint32_t)p.w.tg;
+    auto plane = [&](int pl) { return row16 + (uint32_t)(pl + h) * kChunk; };   // (pl: the h = 0 plane)
+    const uint32_t d_off = 13u * kChunk + (row & ~1u) * 2;
+    uint4 ql[4], qh[2], sc;                                   // ql[2 n + c]
+    uint32_t dw;
+    auto wload = [&](uint32_t sb) {
+#pragma unroll
+        for (int n = 0; n < 2; ++n) {
+#pragma unroll
+            for (int c = 0; c < 2; ++c) ql[2 * n + c] = bld16(wbuf, plane(4 * n + 2 * c), sb);
+            qh[n] = bld16(wbuf, plane(8 + 2 * n), sb);
+        }
+        sc = bld16(wbuf, row16 + 12 * kChunk, sb);
+        dw = bld4(wbuf, d_off, sb);
+    };
+    const uint32_t m0 = h ? 0u : 0xffffffffu, m1 = ~m0;      // group 2 s (lanes h = 0), 2 s + 1 (h = 1)
+
+    v16f out0 = v16f{}, out1 = v16f{};                       // column tiles 0 and 1 of the pair
+    auto compute = [&](int b, int s) {
+        const uint8_t * S = lds + (ks * 2 + b) * kKQStage;
+        // each plane is reloaded with the next super-block's as soon as its last sub-block has
+        // used it (8 loads in all: the barrier's wait counts them)
+        const uint32_t sn = (uint32_t)std::min(s + 1, s1 - 1) * tgs;
+        const uint32_t cdw = dw;
+        v16i is0 = v16i{}, is1 = v16i{};                      // the super-block's integer sums
+        v4i na0 = *reinterpret_cast<const v4i *>(S + lane16), na1 = *reinterpret_cast<const v4i *>(S + 8192 + lane16);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int n = j >> 2, sj = j & 3;
+            const uint4 q = ql[2 * n + (sj & 1)], hb = qh[n];
+            auto code = [&](uint32_t lo, uint32_t hi) {
+                const uint32_t nib = (sj < 2 ? lo : lo >> 4) & 0x0F0F0F0Fu;
+                const uint32_t hp = (sj == 0 ? hi << 4 : sj == 1 ? hi << 2 : sj == 2 ? hi : hi >> 2) & 0x30303030u;
+                return (nib + hp + 0x60606060u) ^ 0x80808080u;  // q - 32 per byte
+            };
+            const uint32_t w0 = code(q.x, hb.x), w1 = code(q.y, hb.y), w2 = code(q.z, hb.z), w3 = code(q.w, hb.w);
+            const v4i b0 = v4i{ (int)(w0 & m0), (int)(w1 & m0), (int)(w2 & m0), (int)(w3 & m0) };
+            const v4i b1 = v4i{ (int)(w0 & m1), (int)(w1 & m1), (int)(w2 & m1), (int)(w3 & m1) };
+            const v4i a0 = na0, a1 = na1;
+            if (j < 7) {
+                na0 = *reinterpret_cast<const v4i *>(S + (j + 1) * 1024 + lane16);
+                na1 = *reinterpret_cast<const v4i *>(S + 8192 + (j + 1) * 1024 + lane16);
+            }
+            // the scales of groups 2 j and 2 j + 1 of the lane's row (bytes 2 j, 2 j + 1 of plane 12)
+            const uint32_t sw = (j >> 1) == 0 ? sc.x : (j >> 1) == 1 ? sc.y : (j >> 1) == 2 ? sc.z : sc.w;
+            const int sc0 = __builtin_amdgcn_sbfe((int)sw, 16 * (j & 1), 8);
+            const int sc1 = __builtin_amdgcn_sbfe((int)sw, 16 * (j & 1) + 8, 8);
+            if (sj >= 2) ql[2 * n + (sj & 1)] = bld16(wbuf, plane(4 * n + 2 * (sj & 1)), sn);   // (its last use)
+            if (sj == 3) qh[n] = bld16(wbuf, plane(8 + 2 * n), sn);
+            if (j == 7) {
+                sc = bld16(wbuf, row16 + 12 * kChunk, sn);
+                dw = bld4(wbuf, d_off, sn);
+            }
+            const v16i p00 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, v16i{}, 0, 0, 0);
+            const v16i p10 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b0, v16i{}, 0, 0, 0);
+            // (the sums are made opaque after each group: otherwise the compiler reassociates them
+            // across the sub-blocks, keeps every MFMA result for one sum at the end and spills)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) is0[r] = __mul24(sc0, p00[r]) + is0[r];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) is1[r] = __mul24(sc0, p10[r]) + is1[r];
+            asm volatile("" : "+v"(is0), "+v"(is1));
+            const v16i p01 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b1, v16i{}, 0, 0, 0);
+            const v16i p11 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, v16i{}, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) is0[r] = __mul24(sc1, p01[r]) + is0[r];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) is1[r] = __mul24(sc1, p11[r]) + is1[r];
+            asm volatile("" : "+v"(is0), "+v"(is1));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // the float combine of each column tile: out += dx (d isum)
+        float d = h2f(cdw >> (16 * (row & 1)));
+        asm volatile("" : "+v"(d));                           // f32 operand (no fp16 source folding)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            float dx[16];
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const float4 v = *reinterpret_cast<const float4 *>(S + 17408 + c * 128 + h * 64 + 16 * q4);
+                dx[4 * q4] = v.x;
+                dx[4 * q4 + 1] = v.y;
+                dx[4 * q4 + 2] = v.z;
+                dx[4 * q4 + 3] = v.w;
+            }
+            v16f & o = c ? out1 : out0;
+            const v16i & is = c ? is1 : is0;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int iv = is[r];
+                o[r] = __builtin_fmaf((float)iv * d, dx[r], o[r]);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // ---- K loop (k_gemm3_q4k's): super-block s + 1 goes into LDS while s is computed; the
+    // barrier's wait covers only these LDS loads, issued before the iteration's 8 weight loads
+    stage(s0, 0);
+    wload((uint32_t)s0 * tgs);
+    __syncthreads();
+    for (int it = 0; it < sps; ++it) {                        // uniform over the work-group
+        const int s = s0 + it;
+        stage(std::min(s + 1, s1 - 1), (it + 1) & 1);         // (past the slice: a copy nobody reads)
+        __builtin_amdgcn_sched_barrier(0);
+        if (s < s1) compute(it & 1, s);
+        else wload((uint32_t)(s1 - 1) * tgs);                 // (the same loads, unused: the wait below counts them)
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(kVmcnt8);
+        __syncthreads();
+    }
+
+    // ---- K slices 1.. add their sums into slice 0's through LDS (fixed order), slice 0 stores
+    if (p.KS > 1) {
+        float * red = reinterpret_cast<float *>(lds);
+        if (ks > 0) {
+            float * o = red + ((size_t)((ks - 1) * U + u) * 32) * 64 + lane;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                o[r * 64] = out0[r];
+                o[(16 + r) * 64] = out1[r];
+            }
+        }
+        __syncthreads();
+        if (ks > 0) return;
+        for (int k = 1; k < p.KS; ++k) {
+            const float * o = red + ((size_t)((k - 1) * U + u) * 32) * 64 + lane;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                out0[r] += o[r * 64];
+                out1[r] += o[(16 + r) * 64];
+            }
+        }
+    }
+    if (!row_ok) return;
+    const int64_t m = mtile * kTileRows + 32 * t + j32;
+    if (m >= p.w.M) return;
+    const uint32_t live = piece >= 0 ? kq_meet(p.tree + ((size_t)(L - p.full) * U + u) * (size_t)p.tslots * 2048, piece,
+                                               p.ts, out0, out1, lane)
+                                     : 0xffffffffu;
+    float * dst = p.dst + (int64_t)i2 * p.bt.d_nb2 + (int64_t)i3 * p.bt.d_nb3 + m;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        const int64_t n0 = (2 * (int64_t)nb + c) * 32;
+        const v16f & v = c ? out1 : out0;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int64_t n = n0 + 8 * (r >> 2) + 4 * h + (r & 3);
+            if (n < p.N && ((live >> (16 * c + r)) & 1u)) __builtin_nontemporal_store(v[r], dst + n * p.bt.d_nb1);
+        }
+    }
+}
+
 // ---- Q4_0, Q8_0, IQ4_NL: the streaming form with 32-row x 64-column waves -----------------
 // The block types on the Q4_K kernel's frame: a wave owns 32 rows (one half of a 64-row image
 // tile) x 64 columns (two column tiles) over one K slice, the U row-half waves of a K slice
@@ -780,6 +1011,29 @@ hipError_t launch_kq(const KQParams & q, const G3Shape & sh, const dim3 & g, con
     return hipGetLastError();
 }
 
+template <int U>
+hipError_t launch_q6k(const KQParams & q, const G3Shape & sh, const dim3 & g, const dim3 & b, hipStream_t s,
+                      const KTime * kt) {
+    static const hipError_t attr = hipFuncSetAttribute((const void *)k_gemm3_q6k<U>,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (attr != hipSuccess) return attr;
+    if (kt) hipExtLaunchKernelGGL(k_gemm3_q6k<U>, g, b, (uint32_t)sh.lds, s, kt->start, kt->stop, 0, q);
+    else k_gemm3_q6k<U><<<g, b, sh.lds, s>>>(q);
+    return hipGetLastError();
+}
+
+hipError_t launch_q6k_u(const KQParams & q, const G3Shape & sh, const dim3 & g, const dim3 & b, hipStream_t s,
+                        const KTime * kt) {
+    switch (sh.U) {
+        case 12: return launch_q6k<12>(q, sh, g, b, s, kt);
+        case 6: return launch_q6k<6>(q, sh, g, b, s, kt);
+        case 4: return launch_q6k<4>(q, sh, g, b, s, kt);
+        case 3: return launch_q6k<3>(q, sh, g, b, s, kt);
+        case 2: return launch_q6k<2>(q, sh, g, b, s, kt);
+        default: return hipErrorInvalidValue;
+    }
+}
+
 template <int TYPE, int U>
 hipError_t launch_blk(const KQParams & q, const G3Shape & sh, const dim3 & g, const dim3 & b, hipStream_t s,
                       const KTime * kt) {
@@ -827,7 +1081,8 @@ int env_int3(const char * name, int dflt) {
 bool gemm3_supported(int type) {
     if (env_int3("QMM_GEMM3", 1) == 0) return false;          // (read per call: tests switch them)
     return type == QMM_TYPE_Q4_0 || type == QMM_TYPE_Q8_0 || type == QMM_TYPE_IQ4_NL ||
-           (type == QMM_TYPE_Q4_K && env_int3("QMM_GEMM3_Q4K", 1) != 0);
+           (type == QMM_TYPE_Q4_K && env_int3("QMM_GEMM3_Q4K", 1) != 0) ||
+           (type == QMM_TYPE_Q6_K && env_int3("QMM_GEMM3_Q6K", 1) != 0);
 }
 
 namespace {
@@ -856,7 +1111,10 @@ bool kq_shape_ncp(const WView & w, int64_t ncp, int64_t nbatch, G3Shape * sh, bo
         // (in 1/64 rounds)
         const int64_t rounds = c.per_cu > 1 ? std::max<int64_t>(64, (nwg * 64 + slots - 1) / slots)
                                             : 64 * ((nwg + slots - 1) / slots);
-        const int64_t cost = rounds * sps;
+        // (dense launches: two row-half waves share a stage of activations, half the sharing of
+        // four, a cost the rounds do not count: U = 2 pays 1/16 more.  Q6_K 151936 x 5120 x 512 tied
+        // (2, 2, 3) with (4, 1, 3) to rounding and measured 1.50 against 1.33 ms)
+        const int64_t cost = tail && c.U == 2 ? rounds * sps * 17 / 16 : rounds * sps;
         if (best >= 0 && cost >= best) continue;
         best = cost;
         sh->U = c.U;
@@ -965,7 +1223,7 @@ hipError_t launch_gemm3_id(int type, const WView & w, const ActBuf & a, const Ge
 // Launch shape of both kernels (kq_shape): U row-half waves per K slice x KS slices.
 bool gemm3_shape(int type, const WView & w, int64_t N, int64_t nbatch, G3Shape * sh) {
     if (!gemm3_supported(type) || N <= 0 || nbatch <= 0 || nbatch > 65535 || w.G <= 0 || w.ntiles <= 0) return false;
-    return kq_shape(w, N, nbatch, sh, type != QMM_TYPE_Q4_K);
+    return kq_shape(w, N, nbatch, sh, type != QMM_TYPE_Q4_K && type != QMM_TYPE_Q6_K);
 }
 
 size_t gemm3_tree_words(const G3Shape & sh) {
@@ -1011,6 +1269,7 @@ hipError_t launch_gemm3(int type, const WView & w, const TiledAct & a, int64_t n
     const dim3 g((unsigned)(8 * (q.fchunk + q.tchunk)), (unsigned)nbatch), b(sh.threads);
     switch (type) {
         case QMM_TYPE_Q4_K: return launch_kq_u<false>(q, sh, g, b, s, kt);
+        case QMM_TYPE_Q6_K: return launch_q6k_u(q, sh, g, b, s, kt);
         case QMM_TYPE_Q4_0: return launch_blk_u<QMM_TYPE_Q4_0>(q, sh, g, b, s, kt);
         case QMM_TYPE_Q8_0: return launch_blk_u<QMM_TYPE_Q8_0>(q, sh, g, b, s, kt);
         case QMM_TYPE_IQ4_NL: return launch_blk_u<QMM_TYPE_IQ4_NL>(q, sh, g, b, s, kt);

@@ -148,7 +148,7 @@ def test_c2_27b_layer(be, wc, orc, bufs, qtype, M, K, N):
     name = f"C2 {synth.NAMES[qtype]} {M}x{K} N={N}"
     say(name)
     got, ref, path = mul_mat_case(be, wc, orc, bufs, qtype, M, K, N, seed=11)
-    gemm = "gemm-stream" if qtype == qmm.Q4_K else "gemm-mfma"
+    gemm = "gemm-stream" if qtype in (qmm.Q4_K, qmm.Q6_K) else "gemm-mfma"
     assert path in {1: ("gemv", "gemv-fq"), 4: ("gemv-mfma",), 512: (gemm,)}[N], path
     check(got, ref, name, path)
 

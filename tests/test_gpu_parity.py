@@ -21,7 +21,7 @@ TYPES = [qmm.Q4_0, qmm.Q8_0, qmm.Q4_K, qmm.Q5_K, qmm.Q6_K, qmm.IQ4_NL, qmm.IQ4_X
 MMA_TYPES = (qmm.Q4_0, qmm.Q8_0, qmm.Q4_K, qmm.IQ4_XS, qmm.IQ4_NL, qmm.Q6_K)
 TOL = 1e-3
 # the types whose GEMM streams weights per wave (one float scale per 32-weight block)
-STREAM_TYPES = (qmm.Q4_0, qmm.Q8_0, qmm.IQ4_NL, qmm.Q4_K)
+STREAM_TYPES = (qmm.Q4_0, qmm.Q8_0, qmm.IQ4_NL, qmm.Q4_K, qmm.Q6_K)
 
 
 def gemm_path(qtype):
@@ -736,8 +736,9 @@ GEMM_FULL = [
 def test_gemm_tail_split(be, sc, orc, monkeypatch, qtype):
     # 66 row tiles x 4 column tiles = 264 > 256 work-groups: the first 256 tiles run whole and
     # the last row of tiles (partial: 8384 = 65.5 x 128 rows) in K slices added into dst rows
-    # the pre-pass zeroed (Q4_K on this kernel when the streaming one is switched off)
+    # the pre-pass zeroed (Q4_K and Q6_K on this kernel when the streaming ones are switched off)
     monkeypatch.setenv("QMM_GEMM3_Q4K", "0")
+    monkeypatch.setenv("QMM_GEMM3_Q6K", "0")
     M, K, N = 8384, 1024, 512
     fake = qmm.Buffer(ptr=0x1000, size=1 << 44)
     info = qmm.describe_mul_mat(qmm.Tensor(fake, qtype, (K, M)), qmm.Tensor(fake, qmm.F32, (K, N)),
@@ -1302,11 +1303,13 @@ def test_downgrade_keys(sc, orc, monkeypatch):
         assert keys == {"src=qmm op=MUL_MAT type=Q5_K k=512 cols=2-8 path=gemv reason=no-mfma-gemv": 2,
                         "src=qmm op=MUL_MAT type=Q4_K k=512 cols=33-128 path=gemv-mfma reason=several-weight-passes": 1}
         assert n == 3
-        # the shared-tile GEMM of a type without a streaming kernel
+        # the shared-tile GEMM of a type without a streaming kernel; Q6_K has one (no key)
+        run(qmm.Q5_K, 128, 512, 512)
         run(qmm.Q6_K, 128, 512, 512)
         b2.synchronize()
         n, keys = b2.downgrades()
-        assert keys["src=qmm op=MUL_MAT type=Q6_K k=512 cols=129+ path=gemm-mfma reason=no-streaming-gemm"] == 1
+        assert keys["src=qmm op=MUL_MAT type=Q5_K k=512 cols=129+ path=gemm-mfma reason=no-streaming-gemm"] == 1
+        assert not any("type=Q6_K" in k and "no-streaming-gemm" in k for k in keys), keys
         # MUL_MAT_ID on route tasks: 16 experts, 80 tokens x 8 used = 40 pairs an expert (each expert's
         # weights stream once per 8-pair task); Q6_K has no grouped GEMM past its 32-pair threshold
         E, T, k, M, K = 16, 80, 8, 64, 512

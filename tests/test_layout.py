@@ -321,7 +321,7 @@ def test_gemm_stream_plan(qtype, K, M, N, monkeypatch):
 @pytest.mark.parametrize("qtype,K,M,N,path", [(qmm.Q4_K, 2048, 512, 256, "gemv-mfma"), (qmm.Q4_K, 5120, 17408, 512, "gemm-stream"),
                                               (qmm.Q4_K, 5120, 1024, 512, "gemm-stream"), (qmm.Q4_0, 4096, 4096, 64, "gemv-mfma"),
                                               (qmm.Q4_0, 4096, 4096, 128, "gemm-stream"),
-                                              (qmm.Q4_0, 4096, 4096, 512, "gemm-stream"), (qmm.Q6_K, 17408, 5120, 512, "gemm-mfma")])
+                                              (qmm.Q4_0, 4096, 4096, 512, "gemm-stream"), (qmm.Q6_K, 17408, 5120, 512, "gemm-stream")])
 def test_gemm_fill_rule(qtype, K, M, N, path):
     fake = qmm.Buffer(ptr=0x1000, size=1 << 44)
     info = qmm.describe_mul_mat(qmm.Tensor(fake, qtype, (K, M)), qmm.Tensor(fake, qmm.F32, (K, N)),
@@ -331,7 +331,7 @@ def test_gemm_fill_rule(qtype, K, M, N, path):
 
 KQ_CANDS = [(12, 1, 1), (6, 2, 1), (4, 3, 1), (3, 4, 1), (4, 1, 3), (2, 2, 3)]
 GEMM3_KQ_SHAPES = [(5120, 17408, 512), (5120, 12288, 512), (5120, 1024, 512), (6144, 5120, 512),
-                   (4096, 4096, 128), (256, 130, 33)]
+                   (4096, 4096, 128), (256, 130, 33), (17408, 5120, 512), (5120, 151936, 512)]
 
 
 def kq_tail(nwg, U, KS, G):
@@ -358,8 +358,9 @@ def kq_tail(nwg, U, KS, G):
 def check_kq_plan(info, G, M, N, cands):
     """the streaming GEMMs' launch plan: (U, KS) minimizes rounds of work-groups on 256 CUs (12-wave
     groups: one per CU, whole rounds; 4-wave: three per CU, a partial last round counted as its
-    fraction) times groups per slice, ties to the earlier candidate; a one-slice launch runs its
-    last partial round's blocks in K pieces (kq_tail)"""
+    fraction) times groups per slice, U = 2 paying 1/16 more (its stage shared by two waves), ties
+    to the earlier candidate; a one-slice launch runs its last partial round's blocks in K pieces
+    (kq_tail)"""
     nrh, ncp = 2 * -(-M // 64), -(-(-(-N // 32)) // 2)
     best = None
     for U, ks, per_cu in cands:
@@ -368,7 +369,7 @@ def check_kq_plan(info, G, M, N, cands):
         slots = 256 * per_cu
         nwg = mbn * ncp
         rounds = max(64, -(-(nwg * 64) // slots)) if per_cu > 1 else 64 * -(-nwg // slots)
-        cost = rounds * sps
+        cost = rounds * sps * 17 // 16 if U == 2 else rounds * sps     # (dense: two waves share a stage)
         if best is None or cost < best[0]:
             best = (cost, U, -(-G // sps), sps, mbn)
     _, U, KS, sps, mbn = best
@@ -381,12 +382,13 @@ def check_kq_plan(info, G, M, N, cands):
     assert info["lds_bytes"] == lds <= 160 * 1024
 
 
+@pytest.mark.parametrize("qtype", [qmm.Q4_K, qmm.Q6_K])
 @pytest.mark.parametrize("K,M,N", GEMM3_KQ_SHAPES)
-def test_gemm_stream_q4k_plan(K, M, N):
+def test_gemm_stream_kquant_plan(qtype, K, M, N):
     fake = qmm.Buffer(ptr=0x1000, size=1 << 44)
     os.environ["QMM_GEMM_MIN_COLS"] = "16"
     try:
-        info = qmm.describe_mul_mat(qmm.Tensor(fake, qmm.Q4_K, (K, M)), qmm.Tensor(fake, qmm.F32, (K, N)),
+        info = qmm.describe_mul_mat(qmm.Tensor(fake, qtype, (K, M)), qmm.Tensor(fake, qmm.F32, (K, N)),
                                     qmm.Tensor(fake, qmm.F32, (M, N)))
     finally:
         del os.environ["QMM_GEMM_MIN_COLS"]
