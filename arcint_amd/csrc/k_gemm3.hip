@@ -780,6 +780,279 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q6k(KQParams p) {
     }
 }
 
+// ---- IQ4_XS and Q5_K: one integer scale per 32-weight sub-block ----------------------------
+// Role of the reference's Q5_K and IQ4_XS prefill GEMMs (kernel_mul_mm_kq2d_q5_K, P01:1734-1775;
+// kernel_mul_mm_iq4_xs_f16 over deq_iq4_xs, P01:2288-2310 and P01:2505-2507), on int8 MFMAs and
+// ggml-cpu's numerics (an exact integer dot per sub-block times its integer scale; Q5_K's min
+// term per super-block), on k_gemm3_q6k's frame.
+//  * A sub-block's 32 weights share one scale (IQ4_XS: ls - 32, ls the 6-bit scale; Q5_K: the
+//    6-bit sc), whose product with a code does not fit an int8 operand.  Both lane halves carry
+//    sub-block j (lane (j, h): k 16 h .. 16 h + 15), so one MFMA per column tile gives its integer
+//    dot for 32 x 32 outputs and a v_mad_i32_i24 per output adds it times the row's scale: 2 MFMAs
+//    and 32 multiply-adds per sub-block and wave.
+//  * IQ4_XS: chunk plane j holds sub-block j's 16 code bytes (low nibbles k 0..15, high 16..31),
+//    lane h takes nibble h through the codebook; the tail's 8 bytes per row: d, scales_h,
+//    scales_l[4] (ls = scales_l nibble j | scales_h bits 2 j, 2 j + 1 above it).
+//  * Q5_K: Q4_K's planes (2 c + h: sub-blocks 2 c, 2 c + 1 in the nibbles) and header, the qh
+//    planes 9 + h (bit j of byte l: the fifth bit of weight l of sub-block j); codes 0..31; the
+//    min term as k_gemm3_q4k's (two MFMAs per column tile over the split sums and the mins).
+//  * Per super-block and output: out += dx (d isum) (IQ4_XS), dx (d isum - dmin imn) (Q5_K).
+template <int TYPE, int U>
+__global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_sbs(KQParams p) {
+    constexpr bool Q5 = TYPE == QMM_TYPE_Q5_K;
+    constexpr int kVm = Q5 ? (6 | (0x7 << 4) | (0xF << 8)) : (10 | (0x7 << 4) | (0xF << 8));   // weight loads a super-block
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, j32 = lane & 31;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int u = wave % U, ks = wave / U;
+
+    uint32_t L;
+    int piece;
+    if (!kq_block(p, blockIdx.x, L, piece)) return;           // uniform over the work-group
+    const uint32_t mb = L / (uint32_t)p.nbn, nb = L - mb * (uint32_t)p.nbn;
+    const uint32_t bz = blockIdx.y;
+    const uint32_t i2 = bz % (uint32_t)p.bt.ne12, i3 = bz / (uint32_t)p.bt.ne12;
+    const int64_t mat = (int64_t)(i2 / (uint32_t)p.bt.r2) + (int64_t)(i3 / (uint32_t)p.bt.r3) * p.bt.ne02;
+    const int64_t rh_raw = (int64_t)mb * U + u;               // the wave's row half
+    const bool row_ok = rh_raw < 2 * p.w.ntiles;              // a missing row half computes a copy, stores nothing
+    const int64_t rh = row_ok ? rh_raw : 2 * p.w.ntiles - 1;
+    const int64_t mtile = rh >> 1;
+    const int t = (int)(rh & 1);
+    const int64_t ct0 = (int64_t)bz * p.ntb + 2 * (int64_t)nb; // the pair's first column tile
+    const int64_t nct = std::min<int64_t>(2, p.ntb - 2 * (int64_t)nb);
+    const int nsb = (int)p.nsb;
+    const int kb = piece >= 0 ? piece * p.pk : 0, ke = piece >= 0 ? std::min(kb + p.pk, nsb) : nsb;
+    const int sps = piece >= 0 ? p.pk : p.sps;                // (pieces: one K slice)
+    const int s0 = kb + ks * sps;
+    const int s1 = std::min(s0 + sps, ke);                    // (every slice has super-blocks)
+
+    const __amdgpu_buffer_rsrc_t wbuf = buffer_rsrc(tile_group(p.w, mat, mtile, 0), (uint32_t)(p.w.G * p.w.tg));
+    const __amdgpu_buffer_rsrc_t abuf = buffer_rsrc(p.tA + ct0 * p.nsb * 8192, (uint32_t)(nct * p.nsb * 8192));
+    const __amdgpu_buffer_rsrc_t sbuf = buffer_rsrc(p.tS + ct0 * p.nsb * 512, (uint32_t)(nct * p.nsb * 512));
+    const __amdgpu_buffer_rsrc_t dbuf = buffer_rsrc(p.tD + ct0 * p.nsb * 32, (uint32_t)(nct * p.nsb * 128));
+    const uint32_t lane16 = (uint32_t)lane * 16;
+
+    // ---- staging: k_gemm3_q4k's 18 units of 1 KB per super-block (the split sums read by Q5_K's
+    // min term; IQ4_XS reads nothing into their slot but keeps every wave's load count)
+    constexpr int NU = kq_units(U);
+    constexpr uint32_t kOut = 0x7ff00000u;
+    const uint32_t a_stride = (uint32_t)p.nsb * 8192, s_stride = (uint32_t)p.nsb * 512, d_stride = (uint32_t)p.nsb * 128;
+    const uint32_t s_lane = Q5 ? (uint32_t)(lane >> 5) * s_stride + (uint32_t)j32 * 16 : kOut;
+    const uint32_t d_lane = lane < 16 ? (uint32_t)(lane >> 3) * d_stride + (uint32_t)(lane & 7) * 16 : kOut;
+    uint8_t * const dump = lds + 2 * p.KS * kKQStage;
+    auto stage = [&](int s, int b) {
+        uint8_t * S = lds + (ks * 2 + b) * kKQStage;
+#pragma unroll
+        for (int i = 0; i < NU; ++i) {
+            const int unit = u + i * U;                       // wave-uniform
+            if (unit < 16)
+                dma16(abuf, S + unit * 1024, lane16 + (uint32_t)(unit >> 3) * a_stride + (uint32_t)(unit & 7) * 1024,
+                      (uint32_t)s * 8192);
+            else if (unit == 16)
+                dma16(Q5 ? sbuf : dbuf, S + 16 * 1024, s_lane, Q5 ? (uint32_t)s * 512 : 0u);
+            else if (unit == 17)
+                dma16(dbuf, S + 17 * 1024, d_lane, (uint32_t)s * 128);
+            else
+                dma16(dbuf, dump, kOut, 0);                   // (nothing: keeps the count)
+        }
+    };
+
+    // ---- weights of the lane's row (32 t + j32)
+    const uint32_t row = (uint32_t)(32 * t + j32), row16 = row * 16;
+    const uint32_t tgs = (uint32_t)p.w.tg;
+    // IQ4_XS: planes j (8), the tail's two dwords; Q5_K: planes 2 c + h (4), the header, qh plane 9 + h
+    constexpr int NP = Q5 ? 4 : 8;
+    uint4 pl[NP], hd;                                         // (hd: Q5_K's header, IQ4_XS's tail in .x, .y)
+    uint4 qh = uint4{ 0, 0, 0, 0 };
+    auto pl_off = [&](int c) { return Q5 ? row16 + (uint32_t)(2 * c + h) * kChunk : row16 + (uint32_t)c * kChunk; };
+    const uint32_t tail = 8u * kChunk + row * 8;
+    auto hload = [&](uint32_t sb) {
+        if constexpr (Q5) {
+            hd = bld16(wbuf, row16 + 8 * kChunk, sb);
+            qh = bld16(wbuf, row16 + (uint32_t)(9 + h) * kChunk, sb);
+        } else {
+            hd.x = bld4(wbuf, tail, sb);
+            hd.y = bld4(wbuf, tail + 4, sb);
+        }
+    };
+    const uint32_t nsh = 4u * (uint32_t)h;                    // IQ4_XS: the lane half's nibble
+
+    v16f out0 = v16f{}, out1 = v16f{};                       // column tiles 0 and 1 of the pair
+    auto compute = [&](int b, int s) {
+        const uint8_t * S = lds + (ks * 2 + b) * kKQStage;
+        const uint32_t sn = (uint32_t)std::min(s + 1, s1 - 1) * tgs;   // the next super-block (clamped)
+        // the row's scales (and Q5_K's mins and fifth bits) from this super-block's header, whose
+        // registers are reloaded with the next one's at once
+        const uint4 chd = hd, cqh = qh;
+        hload(sn);
+        uint32_t sc03, sc47, mn03 = 0, mn47 = 0;
+        if constexpr (Q5) {
+            sc03 = chd.y & 0x3f3f3f3fu;
+            mn03 = chd.z & 0x3f3f3f3fu;
+            sc47 = (chd.w & 0x0f0f0f0fu) | ((chd.y >> 2) & 0x30303030u);
+            mn47 = ((chd.w >> 4) & 0x0f0f0f0fu) | ((chd.z >> 2) & 0x30303030u);
+        } else {
+            sc03 = chd.y;                                     // scales_l (nibble j = bits 4 j)
+            sc47 = chd.x >> 16;                               // scales_h (bits 2 j, 2 j + 1)
+        }
+        v16i is0 = v16i{}, is1 = v16i{};                      // the super-block's integer sums
+        v4i na0 = *reinterpret_cast<const v4i *>(S + lane16), na1 = *reinterpret_cast<const v4i *>(S + 8192 + lane16);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            v4i bop;
+            if constexpr (Q5) {
+                const uint4 q = pl[j >> 1];
+                const uint32_t ns = 4u * (uint32_t)(j & 1);
+                auto code = [&](uint32_t w, uint32_t hb) {
+                    const uint32_t fifth = (j <= 4 ? hb << (4 - j) : hb >> (j - 4)) & 0x10101010u;
+                    return ((w >> ns) & 0x0F0F0F0Fu) | fifth;
+                };
+                bop = v4i{ (int)code(q.x, cqh.x), (int)code(q.y, cqh.y), (int)code(q.z, cqh.z), (int)code(q.w, cqh.w) };
+                if (j & 1) pl[j >> 1] = bld16(wbuf, pl_off(j >> 1), sn);   // (its last sub-block)
+            } else {
+                const uint4 q = pl[j];
+                bop = v4i{ (int)iq4_lookup((q.x >> nsh) & 0x0F0F0F0Fu), (int)iq4_lookup((q.y >> nsh) & 0x0F0F0F0Fu),
+                           (int)iq4_lookup((q.z >> nsh) & 0x0F0F0F0Fu), (int)iq4_lookup((q.w >> nsh) & 0x0F0F0F0Fu) };
+                pl[j] = bld16(wbuf, pl_off(j), sn);
+            }
+            const v4i a0 = na0, a1 = na1;
+            if (j < 7) {
+                na0 = *reinterpret_cast<const v4i *>(S + (j + 1) * 1024 + lane16);
+                na1 = *reinterpret_cast<const v4i *>(S + 8192 + (j + 1) * 1024 + lane16);
+            }
+            int sc;
+            if constexpr (Q5) {
+                sc = (int)__builtin_amdgcn_ubfe(j < 4 ? sc03 : sc47, 8 * (j & 3), 8);
+            } else {
+                sc = (int)(__builtin_amdgcn_ubfe(sc03, 4 * j, 4) | (__builtin_amdgcn_ubfe(sc47, 2 * j, 2) << 4)) - 32;
+            }
+            const v16i p0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bop, v16i{}, 0, 0, 0);
+            const v16i p1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bop, v16i{}, 0, 0, 0);
+            // (the sums are made opaque after each sub-block: the compiler would otherwise
+            // reassociate them across the sub-blocks and keep every MFMA result)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) is0[r] = __mul24(sc, p0[r]) + is0[r];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) is1[r] = __mul24(sc, p1[r]) + is1[r];
+            asm volatile("" : "+v"(is0), "+v"(is1));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // the float combine of each column tile
+        float d, dmin = 0.0f;
+        if constexpr (Q5) {
+            d = h2f(chd.x & 0xffffu);
+            dmin = h2f(chd.x >> 16);
+        } else {
+            d = h2f(chd.x & 0xffffu);
+        }
+        asm volatile("" : "+v"(d), "+v"(dmin));               // f32 operands (no fp16 source folding)
+        v16i mlt[2];
+        if constexpr (Q5) {
+            // Q5_K's min term (k_gemm3_q4k's): A = the columns' split sums bh, then bl, at k = j, B
+            // = the row's 8 mins; the second MFMA starts from 64 * first + the bits of 12582912.0f
+            const v4i bm = h ? v4i{} : v4i{ (int)mn03, (int)mn47, 0, 0 };
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                const uint4 sp = *reinterpret_cast<const uint4 *>(S + 16384 + c * 512 + j32 * 16);
+                const v4i ah = h ? v4i{} : v4i{ (int)sp.x, (int)sp.y, 0, 0 };
+                const v4i al = h ? v4i{} : v4i{ (int)sp.z, (int)sp.w, 0, 0 };
+                v16i mh = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, bm, v16i{}, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mh[r] = mh[r] * 64 + kMagic;
+                mlt[c] = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, bm, mh, 0, 0, 0);
+            }
+        }
+        const float nmag = 12582912.0f * dmin;                // exact: fp16 dmin times 3 * 2^22
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            float dx[16];
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const float4 v = *reinterpret_cast<const float4 *>(S + 17408 + c * 128 + h * 64 + 16 * q4);
+                dx[4 * q4] = v.x;
+                dx[4 * q4 + 1] = v.y;
+                dx[4 * q4 + 2] = v.z;
+                dx[4 * q4 + 3] = v.w;
+            }
+            v16f & o = c ? out1 : out0;
+            const v16i & is = c ? is1 : is0;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int iv = is[r];
+                if constexpr (Q5) {
+                    const int iml = mlt[c][r];
+                    const float wv = __builtin_fmaf(__builtin_bit_cast(float, iml), -dmin, nmag);   // -dmin * imn
+                    o[r] = __builtin_fmaf(__builtin_fmaf((float)iv, d, wv), dx[r], o[r]);
+                } else {
+                    o[r] = __builtin_fmaf((float)iv * d, dx[r], o[r]);
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // ---- K loop (k_gemm3_q4k's): super-block s + 1 goes into LDS while s is computed; the
+    // barrier's wait covers only these LDS loads, issued before the iteration's weight loads
+    auto wload_all = [&](uint32_t sb) {
+#pragma unroll
+        for (int c = 0; c < NP; ++c) pl[c] = bld16(wbuf, pl_off(c), sb);
+        hload(sb);
+    };
+    stage(s0, 0);
+    wload_all((uint32_t)s0 * tgs);
+    __syncthreads();
+    for (int it = 0; it < sps; ++it) {                        // uniform over the work-group
+        const int s = s0 + it;
+        stage(std::min(s + 1, s1 - 1), (it + 1) & 1);         // (past the slice: a copy nobody reads)
+        __builtin_amdgcn_sched_barrier(0);
+        if (s < s1) compute(it & 1, s);
+        else wload_all((uint32_t)(s1 - 1) * tgs);             // (the same loads, unused: the wait below counts them)
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(kVm);
+        __syncthreads();
+    }
+
+    // ---- K slices 1.. add their sums into slice 0's through LDS (fixed order), slice 0 stores
+    if (p.KS > 1) {
+        float * red = reinterpret_cast<float *>(lds);
+        if (ks > 0) {
+            float * o = red + ((size_t)((ks - 1) * U + u) * 32) * 64 + lane;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                o[r * 64] = out0[r];
+                o[(16 + r) * 64] = out1[r];
+            }
+        }
+        __syncthreads();
+        if (ks > 0) return;
+        for (int k = 1; k < p.KS; ++k) {
+            const float * o = red + ((size_t)((k - 1) * U + u) * 32) * 64 + lane;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                out0[r] += o[r * 64];
+                out1[r] += o[(16 + r) * 64];
+            }
+        }
+    }
+    if (!row_ok) return;
+    const int64_t m = mtile * kTileRows + 32 * t + j32;
+    if (m >= p.w.M) return;
+    const uint32_t live = piece >= 0 ? kq_meet(p.tree + ((size_t)(L - p.full) * U + u) * (size_t)p.tslots * 2048, piece,
+                                               p.ts, out0, out1, lane)
+                                     : 0xffffffffu;
+    float * dst = p.dst + (int64_t)i2 * p.bt.d_nb2 + (int64_t)i3 * p.bt.d_nb3 + m;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        const int64_t n0 = (2 * (int64_t)nb + c) * 32;
+        const v16f & v = c ? out1 : out0;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int64_t n = n0 + 8 * (r >> 2) + 4 * h + (r & 3);
+            if (n < p.N && ((live >> (16 * c + r)) & 1u)) __builtin_nontemporal_store(v[r], dst + n * p.bt.d_nb1);
+        }
+    }
+}
+
 // ---- Q4_0, Q8_0, IQ4_NL: the streaming form with 32-row x 64-column waves -----------------
 // The block types on the Q4_K kernel's frame: a wave owns 32 rows (one half of a 64-row image
 // tile) x 64 columns (two column tiles) over one K slice, the U row-half waves of a K slice
@@ -1022,6 +1295,30 @@ hipError_t launch_q6k(const KQParams & q, const G3Shape & sh, const dim3 & g, co
     return hipGetLastError();
 }
 
+template <int TYPE, int U>
+hipError_t launch_sbs(const KQParams & q, const G3Shape & sh, const dim3 & g, const dim3 & b, hipStream_t s,
+                      const KTime * kt) {
+    static const hipError_t attr = hipFuncSetAttribute((const void *)k_gemm3_sbs<TYPE, U>,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (attr != hipSuccess) return attr;
+    if (kt) hipExtLaunchKernelGGL(k_gemm3_sbs<TYPE, U>, g, b, (uint32_t)sh.lds, s, kt->start, kt->stop, 0, q);
+    else k_gemm3_sbs<TYPE, U><<<g, b, sh.lds, s>>>(q);
+    return hipGetLastError();
+}
+
+template <int TYPE>
+hipError_t launch_sbs_u(const KQParams & q, const G3Shape & sh, const dim3 & g, const dim3 & b, hipStream_t s,
+                        const KTime * kt) {
+    switch (sh.U) {
+        case 12: return launch_sbs<TYPE, 12>(q, sh, g, b, s, kt);
+        case 6: return launch_sbs<TYPE, 6>(q, sh, g, b, s, kt);
+        case 4: return launch_sbs<TYPE, 4>(q, sh, g, b, s, kt);
+        case 3: return launch_sbs<TYPE, 3>(q, sh, g, b, s, kt);
+        case 2: return launch_sbs<TYPE, 2>(q, sh, g, b, s, kt);
+        default: return hipErrorInvalidValue;
+    }
+}
+
 hipError_t launch_q6k_u(const KQParams & q, const G3Shape & sh, const dim3 & g, const dim3 & b, hipStream_t s,
                         const KTime * kt) {
     switch (sh.U) {
@@ -1082,7 +1379,8 @@ bool gemm3_supported(int type) {
     if (env_int3("QMM_GEMM3", 1) == 0) return false;          // (read per call: tests switch them)
     return type == QMM_TYPE_Q4_0 || type == QMM_TYPE_Q8_0 || type == QMM_TYPE_IQ4_NL ||
            (type == QMM_TYPE_Q4_K && env_int3("QMM_GEMM3_Q4K", 1) != 0) ||
-           (type == QMM_TYPE_Q6_K && env_int3("QMM_GEMM3_Q6K", 1) != 0);
+           (type == QMM_TYPE_Q6_K && env_int3("QMM_GEMM3_Q6K", 1) != 0) ||
+           ((type == QMM_TYPE_Q5_K || type == QMM_TYPE_IQ4_XS) && env_int3("QMM_GEMM3_SBS", 1) != 0);
 }
 
 namespace {
@@ -1223,7 +1521,9 @@ hipError_t launch_gemm3_id(int type, const WView & w, const ActBuf & a, const Ge
 // Launch shape of both kernels (kq_shape): U row-half waves per K slice x KS slices.
 bool gemm3_shape(int type, const WView & w, int64_t N, int64_t nbatch, G3Shape * sh) {
     if (!gemm3_supported(type) || N <= 0 || nbatch <= 0 || nbatch > 65535 || w.G <= 0 || w.ntiles <= 0) return false;
-    return kq_shape(w, N, nbatch, sh, type != QMM_TYPE_Q4_K && type != QMM_TYPE_Q6_K);
+    // (the K-quant frame's launch rule for the super-block types; the block types' for the rest)
+    const bool kframe = type == QMM_TYPE_Q4_K || type == QMM_TYPE_Q6_K || type == QMM_TYPE_Q5_K || type == QMM_TYPE_IQ4_XS;
+    return kq_shape(w, N, nbatch, sh, !kframe);
 }
 
 size_t gemm3_tree_words(const G3Shape & sh) {
@@ -1236,7 +1536,7 @@ hipError_t launch_gemm3(int type, const WView & w, const TiledAct & a, int64_t n
     if (!gemm3_shape(type, w, a.N, nbatch, &sh) || !a.A || !a.D || a.nblk != w.G * 8 || a.ntb != (a.N + 31) / 32 ||
         a.ntiles != a.ntb * nbatch || a.vdt != vec_dot_type(type))
         return hipErrorInvalidValue;
-    if (type == QMM_TYPE_Q4_K && !a.S) return hipErrorInvalidValue;
+    if ((type == QMM_TYPE_Q4_K || type == QMM_TYPE_Q5_K) && !a.S) return hipErrorInvalidValue;
     KQParams q{};
     q.w = w;
     q.tA = a.A;
@@ -1270,6 +1570,8 @@ hipError_t launch_gemm3(int type, const WView & w, const TiledAct & a, int64_t n
     switch (type) {
         case QMM_TYPE_Q4_K: return launch_kq_u<false>(q, sh, g, b, s, kt);
         case QMM_TYPE_Q6_K: return launch_q6k_u(q, sh, g, b, s, kt);
+        case QMM_TYPE_Q5_K: return launch_sbs_u<QMM_TYPE_Q5_K>(q, sh, g, b, s, kt);
+        case QMM_TYPE_IQ4_XS: return launch_sbs_u<QMM_TYPE_IQ4_XS>(q, sh, g, b, s, kt);
         case QMM_TYPE_Q4_0: return launch_blk_u<QMM_TYPE_Q4_0>(q, sh, g, b, s, kt);
         case QMM_TYPE_Q8_0: return launch_blk_u<QMM_TYPE_Q8_0>(q, sh, g, b, s, kt);
         case QMM_TYPE_IQ4_NL: return launch_blk_u<QMM_TYPE_IQ4_NL>(q, sh, g, b, s, kt);

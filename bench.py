@@ -18,9 +18,11 @@ Also reported, on the same JSON line:
                 kind "port") on the same op on the cores this process may use
                 (at most 16, the host share of a one-GPU box), median of its
                 reps, with nproc and a single-thread figure
-  gemm          prefill MUL_MAT at N = 512: Q4_0 4096x4096 and 11008x4096
-                (config 1), Q4_K 17408x5120 (config 2), in TOPS vs the dense
-                int8 MFMA peak ("secondary" repeats the first)
+  gemm          prefill MUL_MAT at N = 512: Q4_0 4096x4096, 11008x4096 and
+                4096x11008 (config 1), Q4_K 17408x5120, Q6_K 5120x17408 and the
+                Q6_K 151936x5120 head (config 2), in TOPS vs the dense int8
+                MFMA peak ("secondary" repeats the first); --only adj_gemm:
+                IQ4_XS 14336x4096 and Q5_K 17408x5120 at N = 512
   gemv          decode and few-column MUL_MAT of configs 0, 2 and 4: GB/s and
                 the kernel's fraction of 8 TB/s
   moe           config 3's whole MoE layer at T = 1, 4, 256 tokens (router,
@@ -558,7 +560,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
-    ap.add_argument("--only", default="", help="profile one workload: q4k_gemv, q40_gemm, q4k_gemm, q6k_gemm, gemv, glu, "
+    ap.add_argument("--only", default="", help="profile one workload: q4k_gemv, q40_gemm, q4k_gemm, q6k_gemm, adj_gemm, gemv, glu, "
                                                  "moe or moe_grouped")
     args = ap.parse_args()
 
@@ -626,7 +628,7 @@ def main():
         for w in ws:
             be.free_buffer(w.buf)
 
-    if not args.no_secondary and args.only in ("", "q40_gemm", "q4k_gemm", "q6k_gemm"):
+    if not args.no_secondary and args.only in ("", "q40_gemm", "q4k_gemm", "q6k_gemm", "adj_gemm"):
         cases = [(qmm.Q4_0, 4096, 4096, 512, "Q4_0 GEMM 4096x4096x512 (config 1 attn)", "q40_gemm", "q40_gemm"),
                  (qmm.Q4_0, 11008, 4096, 512, "Q4_0 GEMM 11008x4096x512 (config 1 ffn gate/up)", "q40_gemm",
                   "q40_gemm_11008"),
@@ -635,10 +637,13 @@ def main():
                   "q40_gemm_down"),
                  (qmm.Q6_K, 5120, 17408, 512, "Q6_K GEMM 5120x17408x512 (config 2 ffn down)", "q6k_gemm", "q6k_gemm"),
                  (qmm.Q6_K, 151936, 5120, 512, "Q6_K GEMM 151936x5120x512 (config 2 output head)", "q6k_gemm",
-                  "q6k_gemm_head")]
+                  "q6k_gemm_head"),
+                 # (the adjacent types at config shapes: --only adj_gemm, not in the default run)
+                 (qmm.IQ4_XS, 14336, 4096, 512, "IQ4_XS GEMM 14336x4096x512 (config 4 shape)", "adj_gemm", "iq4xs_gemm"),
+                 (qmm.Q5_K, 17408, 5120, 512, "Q5_K GEMM 17408x5120x512 (config 2 shape)", "adj_gemm", "q5k_gemm")]
         secs = []
         for qtype, M2, K2, N2, name, tag, ttag in cases:
-            if args.only and args.only != tag:
+            if (args.only and args.only != tag) or (not args.only and tag == "adj_gemm"):
                 continue
             secs.append(gemm_case(be, qmm, synth, qtype, M2, K2, N2, name, args, ttag))
         if out:

@@ -21,7 +21,7 @@ TYPES = [qmm.Q4_0, qmm.Q8_0, qmm.Q4_K, qmm.Q5_K, qmm.Q6_K, qmm.IQ4_NL, qmm.IQ4_X
 MMA_TYPES = (qmm.Q4_0, qmm.Q8_0, qmm.Q4_K, qmm.IQ4_XS, qmm.IQ4_NL, qmm.Q6_K)
 TOL = 1e-3
 # the types whose GEMM streams weights per wave (one float scale per 32-weight block)
-STREAM_TYPES = (qmm.Q4_0, qmm.Q8_0, qmm.IQ4_NL, qmm.Q4_K, qmm.Q6_K)
+STREAM_TYPES = (qmm.Q4_0, qmm.Q8_0, qmm.IQ4_NL, qmm.Q4_K, qmm.Q6_K, qmm.Q5_K, qmm.IQ4_XS)
 
 
 def gemm_path(qtype):
@@ -1303,8 +1303,11 @@ def test_downgrade_keys(sc, orc, monkeypatch):
         assert keys == {"src=qmm op=MUL_MAT type=Q5_K k=512 cols=2-8 path=gemv reason=no-mfma-gemv": 2,
                         "src=qmm op=MUL_MAT type=Q4_K k=512 cols=33-128 path=gemv-mfma reason=several-weight-passes": 1}
         assert n == 3
-        # the shared-tile GEMM of a type without a streaming kernel; Q6_K has one (no key)
+        # the shared-tile GEMM when the streaming one is switched off (QMM_GEMM3_SBS=0 for Q5_K);
+        # Q6_K streams (no key)
+        monkeypatch.setenv("QMM_GEMM3_SBS", "0")
         run(qmm.Q5_K, 128, 512, 512)
+        monkeypatch.delenv("QMM_GEMM3_SBS")
         run(qmm.Q6_K, 128, 512, 512)
         b2.synchronize()
         n, keys = b2.downgrades()

@@ -382,7 +382,7 @@ def check_kq_plan(info, G, M, N, cands):
     assert info["lds_bytes"] == lds <= 160 * 1024
 
 
-@pytest.mark.parametrize("qtype", [qmm.Q4_K, qmm.Q6_K])
+@pytest.mark.parametrize("qtype", [qmm.Q4_K, qmm.Q6_K, qmm.Q5_K, qmm.IQ4_XS])
 @pytest.mark.parametrize("K,M,N", GEMM3_KQ_SHAPES)
 def test_gemm_stream_kquant_plan(qtype, K, M, N):
     fake = qmm.Buffer(ptr=0x1000, size=1 << 44)

@@ -3,7 +3,7 @@ against qmm_mul_mat on the same operands, through the C ABI, and against the CPU
 more calls in a row with the later ones smaller (the array keeps the last call's contents).  Each
 kernel path the entry point can take on the array is pinned by the path it reports:
   gemm-stream  the streaming GEMM (tiled pre-pass into the array)
-  gemm-mfma    the shared-tile GEMM (a type the streaming kernel does not take, and QMM_GEMM3=0)
+  gemm-mfma    the shared-tile GEMM (the streaming kernels switched off: QMM_GEMM3_SBS=0, QMM_GEMM3=0)
   gemv-mfma    pre-pass + the few-column MFMA GEMV
   gemv         pre-pass + the v_dot4 GEMV: a large one-column product, which qmm_mul_mat runs as
                the K-split one-launch GEMV (its exchange-tree slots are allocated, so the
@@ -73,9 +73,10 @@ def test_noalloc_matches_mul_mat(be, orc, seq):
     # (type, M, K, N, environment, the path qmm_mul_mat_noalloc must report)
     (qmm.Q4_K, 17408, 5120, 1, {}, "gemv"),
     (qmm.Q4_K, 17408, 5120, 1, {"QMM_GEMV_FUSED": "0"}, "gemv"),
-    (qmm.Q5_K, 1024, 2048, 64, {}, "gemm-mfma"),
+    (qmm.Q5_K, 1024, 2048, 64, {"QMM_GEMM3_SBS": "0"}, "gemm-mfma"),
     (qmm.Q4_0, 2048, 4096, 512, {"QMM_GEMM3": "0"}, "gemm-mfma"),
     (qmm.Q4_0, 2048, 4096, 512, {}, "gemm-stream"),
+    (qmm.Q6_K, 4096, 2048, 512, {}, "gemm-stream"),
     (qmm.Q8_0, 4096, 4096, 24, {}, "gemv-mfma"),
     (qmm.IQ4_XS, 256, 512, 2, {}, "gemv-fq"),
     (qmm.Q6_K, 128, 256, 1, {}, "gemv-fq"),
