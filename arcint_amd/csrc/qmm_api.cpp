@@ -1175,8 +1175,8 @@ static int mul_mat_launch(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tens
         bt.d_nb2 = dn.d_nb2;
         bt.d_nb3 = dn.d_nb3;
         ctx->path = "gemm-mfma";
-        // (Q5_K / IQ4_XS have no streaming kernel: their integer sub-block scales do not fold into
-        // int8 operands, so each scale is a VALU multiply-add per output)
+        // (every type streams unless the streaming kernels are switched off: QMM_GEMM3=0, or
+        // QMM_GEMM3_Q4K / _Q6K / _SBS per type)
         note_downgrade(ctx, "op=MUL_MAT type=%s k=%lld cols=%s path=gemm-mfma reason=no-streaming-gemm",
                        type_name(src0->type), (long long)w.K, cols_bucket(N));
         if (!fixed && (rc = ktime_pair(ctx, &kt, &ktp))) return rc;
