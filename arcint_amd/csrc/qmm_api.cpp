@@ -864,35 +864,39 @@ static int gemv_mma_min_cols() {
     return e ? std::max(2, atoi(e)) : 3;
 }
 
-// columns at or above which MUL_MAT goes to the MFMA GEMM instead of the GEMV (32 columns per
-// weight pass on the MFMA GEMV, 8 on v_dot4).  Measured crossovers on MI355X (config shapes):
-// Q4_K's GEMV wins to ~100 columns (17408 x 5120: 69 us against 82 at 96), Q6_K's too (5120 x
-// 17408: 80 against 94 at 96), IQ4_XS's to 64, Q4_0 / Q8_0 / IQ4_NL's to one pass (their GEMM
-// keeps up from 33); Q5_K (v_dot4 only) switches at 16.  QMM_GEMM_MIN_COLS overrides.
+// columns at or above which MUL_MAT may go to the GEMM instead of the GEMV (32 columns per
+// weight pass on the MFMA GEMV, 8 on v_dot4): within one MFMA GEMV pass the GEMV won every
+// measured shape (Q4_K 17408 x 5120 at 24-32: 25-29 against 30 us); past it use_gemm_for
+// weighs the launch.  QMM_GEMM_MIN_COLS overrides.
 static int64_t gemm_min_cols(int type) {
     const char * e = getenv("QMM_GEMM_MIN_COLS");
     if (e) return std::max<int64_t>(1, atoll(e));
-    switch (type) {
-        case QMM_TYPE_Q4_K:   return 128;
-        case QMM_TYPE_Q6_K:   return 97;
-        case QMM_TYPE_IQ4_XS: return 65;
-        case QMM_TYPE_Q4_0:
-        case QMM_TYPE_Q8_0:
-        case QMM_TYPE_IQ4_NL: return kMmaMaxCols + 1;
-        default:              return 16;
-    }
+    // (past one pass of the few-column MFMA GEMV; Q5_K, which has no MFMA GEMV, from 16: its
+    // v_dot4 GEMV takes 8 columns a pass; use_gemm_for decides from there)
+    return gemv_mma_supported(type) ? kMmaMaxCols + 1 : 16;
 }
 
-// MUL_MAT on the GEMM: from gemm_min_cols, unless the streaming GEMM's launch would not give
-// every SIMD a wave (rows x column units x K slices < 1024): then the GEMV's tasks, which split
-// K over work-groups, win (config 3's shared expert, Q4_K 512 x 2048 at N = 256: 42.8 us on
-// the GEMM in 24 work-groups, 30.4 on the GEMV).  QMM_GEMM_MIN_COLS, when set, decides alone.
+// MUL_MAT on the GEMM: from gemm_min_cols, when the streaming GEMM's launch gives every SIMD a
+// wave (rows x column units x K slices >= 1024); with fewer (down to 512) when the GEMV would
+// stream enough weight bytes over its passes (32 columns a pass on the MFMA GEMV, 8 on v_dot4):
+// 90 MB.  Q6_K, whose GEMM costs more per MAC, needs 400 MB at any wave count below 256 columns.
+// Else the GEMV's tasks, which split K over work-groups.  Measured (op us, GEMV / GEMM): Q4_K 17408 x 5120 at N = 40-64 44.7-50.8 / 31,
+// 12288 x 5120 at 48 30.0 / 30.0, 5120 x 6144 at 48-64 22-24 / 32-33; Q6_K 5120 x 17408 at 128
+// 96 / 116, at 192 141 / 122, the 151936-row head at 64 446 / 272; IQ4_XS 4096 x 14336 at 48-64
+// 35-38 / 73; Q5_K 17408 x 5120 at 16-48 62-135 / 34-36; config 3's shared expert (Q4_K 512 x
+// 2048, N = 256) 30.4 / 42.8.  QMM_GEMM_MIN_COLS, when set, decides alone.
 static bool use_gemm_for(int type, const WView & w, int64_t N, int64_t nbatch) {
     if (N < gemm_min_cols(type)) return false;
     if (getenv("QMM_GEMM_MIN_COLS")) return true;
     G3Shape sh;
     if (!gemm3_shape(type, w, N, nbatch, &sh)) return true;      // (the shared-tile GEMM)
-    return sh.mbn * sh.nbn * nbatch * sh.U * sh.KS >= 1024;
+    const int64_t waves = sh.mbn * sh.nbn * nbatch * sh.U * sh.KS;
+    const int64_t per = gemv_mma_supported(type) ? kMmaMaxCols : 8;
+    const double passes = (double)((N + per - 1) / per);
+    const double bytes = (double)(w.ntiles * w.G) * (double)w.tg * (double)nbatch;
+    if (type == QMM_TYPE_Q6_K && N < 256) return waves >= 512 && passes >= 2 && passes * bytes >= 400e6;
+    if (waves >= 1024) return true;
+    return waves >= 512 && passes >= 2 && passes * bytes >= 90e6;
 }
 
 // columns per GEMV task: up to 32 on the MFMA kernel (the rows of its A operand), 8 on v_dot4,

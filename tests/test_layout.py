@@ -229,9 +229,10 @@ PLAN_SHAPES = [
     (qmm.Q4_0, 4096, 4096, 1), (qmm.Q4_0, 11008, 4096, 8), (qmm.Q8_0, 4096, 14336, 8), (qmm.IQ4_XS, 14336, 4096, 2),
     (qmm.Q4_0, 352, 65, 3), (qmm.Q4_K, 256, 1, 1), (qmm.Q8_0, 32, 5, 8), (qmm.IQ4_XS, 512, 2048, 5),
     (qmm.Q5_K, 5120, 17408, 1), (qmm.Q5_K, 4096, 4096, 6), (qmm.IQ4_NL, 640, 4096, 1), (qmm.IQ4_NL, 4096, 14336, 8),
-    # wide MFMA tasks: 9..32 columns per weight pass, more in even passes
-    (qmm.Q4_K, 5120, 17408, 16), (qmm.Q4_K, 5120, 17408, 100), (qmm.Q4_0, 4096, 11008, 32), (qmm.Q8_0, 4096, 14336, 24),
-    (qmm.IQ4_XS, 4096, 14336, 40), (qmm.IQ4_NL, 4096, 4096, 9), (qmm.Q6_K, 17408, 5120, 12), (qmm.Q5_K, 5120, 4096, 9),
+    # wide MFMA tasks: 9..32 columns per weight pass, more in even passes (past 32, shapes the
+    # GEMM does not take: few rows or few weight bytes)
+    (qmm.Q4_K, 5120, 17408, 16), (qmm.Q4_K, 5120, 2048, 100), (qmm.Q4_0, 4096, 11008, 32), (qmm.Q8_0, 4096, 14336, 24),
+    (qmm.IQ4_XS, 14336, 4096, 40), (qmm.IQ4_NL, 4096, 4096, 9), (qmm.Q6_K, 17408, 5120, 12), (qmm.Q5_K, 5120, 4096, 9),
 ]
 
 
@@ -321,7 +322,14 @@ def test_gemm_stream_plan(qtype, K, M, N, monkeypatch):
 @pytest.mark.parametrize("qtype,K,M,N,path", [(qmm.Q4_K, 2048, 512, 256, "gemv-mfma"), (qmm.Q4_K, 5120, 17408, 512, "gemm-stream"),
                                               (qmm.Q4_K, 5120, 1024, 512, "gemm-stream"), (qmm.Q4_0, 4096, 4096, 64, "gemv-mfma"),
                                               (qmm.Q4_0, 4096, 4096, 128, "gemm-stream"),
-                                              (qmm.Q4_0, 4096, 4096, 512, "gemm-stream"), (qmm.Q6_K, 17408, 5120, 512, "gemm-stream")])
+                                              (qmm.Q4_0, 4096, 4096, 512, "gemm-stream"), (qmm.Q6_K, 17408, 5120, 512, "gemm-stream"),
+                                              # fewer than 1024 waves: the GEMM when the GEMV's passes stream >= 90 MB
+                                              # (Q6_K 400 MB), measured crossovers
+                                              (qmm.Q4_K, 5120, 17408, 40, "gemm-stream"), (qmm.Q4_K, 5120, 12288, 48, "gemm-stream"),
+                                              (qmm.Q4_K, 6144, 5120, 64, "gemv-mfma"), (qmm.Q4_K, 5120, 17408, 32, "gemv-mfma"),
+                                              (qmm.Q6_K, 17408, 5120, 128, "gemv-mfma"), (qmm.Q6_K, 17408, 5120, 192, "gemm-stream"),
+                                              (qmm.Q6_K, 5120, 151936, 64, "gemm-stream"), (qmm.IQ4_XS, 14336, 4096, 48, "gemv-mfma"),
+                                              (qmm.Q5_K, 5120, 17408, 16, "gemm-stream")])
 def test_gemm_fill_rule(qtype, K, M, N, path):
     fake = qmm.Buffer(ptr=0x1000, size=1 << 44)
     info = qmm.describe_mul_mat(qmm.Tensor(fake, qtype, (K, M)), qmm.Tensor(fake, qmm.F32, (K, N)),
