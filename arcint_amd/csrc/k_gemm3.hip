@@ -218,6 +218,45 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t * lds, u
                                              0, 0);
 }
 
+// Grouped mode's store of a wave's 32 sums per lane (rows m, the unit's 64 slots): each output
+// goes to its pair's dst offset, read from the unit.  Every offset (and gate value) is requested
+// before the first store, and no load or store sits in a branch: through buffer resources over
+// dst's span an offset past it (kNoStore: a slot past the unit) reads zero and drops its store.
+// (Conditional accesses, and loads after stores to dst that might alias them, made each of the 32
+// stores wait for a memory round trip.)  With p.glu >= 0 the launch is the up product of a
+// gate/up pair: act(gate) * up, gate read at the same offset.
+__device__ __forceinline__ void gather_store(const KQParams & p, uint32_t nb, int ncu, int64_t m, int h,
+                                             const v16f & out0, const v16f & out1) {
+    constexpr uint32_t kNoStore = 0xffffffffu;
+    const uint32_t span4 = (uint32_t)(p.dspan * 4);
+    const __amdgpu_buffer_rsrc_t dres = buffer_rsrc(p.dst, span4);
+    uint32_t off[32];
+    float val[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        const int slot = 32 * (i >> 4) + 8 * ((i & 15) >> 2) + 4 * h + (i & 3);   // < 64: in the unit
+        const int64_t o = p.units[nb].c[slot].dst_off + m;
+        off[i] = slot < ncu ? 4u * (uint32_t)o : kNoStore;
+        val[i] = i < 16 ? out0[i] : out1[i - 16];
+    }
+    if (p.glu >= 0) {                                         // uniform
+        const __amdgpu_buffer_rsrc_t gres = buffer_rsrc(p.gsrc, span4);
+        float gv[32];
+#pragma unroll
+        for (int i = 0; i < 32; ++i) gv[i] = __uint_as_float(bld4(gres, off[i], 0));
+        // one branch for the op, then straight-line code over the values
+        switch (p.glu) {
+            case QMM_GLU_REGLU: glu_rows<QMM_GLU_REGLU>(gv, val); break;
+            case QMM_GLU_GEGLU: glu_rows<QMM_GLU_GEGLU>(gv, val); break;
+            case QMM_GLU_SWIGLU: glu_rows<QMM_GLU_SWIGLU>(gv, val); break;
+            case QMM_GLU_GEGLU_ERF: glu_rows<QMM_GLU_GEGLU_ERF>(gv, val); break;
+            default: glu_rows<QMM_GLU_GEGLU_QUICK>(gv, val); break;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 32; ++i) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val[i]), dres, (int)off[i], 0, 0);
+}
+
 template <int U, bool GATHER>
 __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q4k(KQParams p) {
     extern __shared__ __align__(16) uint8_t lds[];
@@ -498,39 +537,7 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q4k(KQParams p) {
     const int64_t m = mtile * kTileRows + 32 * t + j32;
     if (m >= p.w.M) return;
     if constexpr (GATHER) {
-        // every destination offset (and gate value) is requested before the first store, and no
-        // load or store sits in a branch: through buffer resources over dst's span an offset past
-        // it (kNoStore: a slot past the unit) reads zero and drops its store.  (Conditional
-        // accesses, and loads after stores to dst that might alias them, made each of the 32
-        // stores wait for a memory round trip.)
-        constexpr uint32_t kNoStore = 0xffffffffu;
-        const uint32_t span4 = (uint32_t)(p.dspan * 4);
-        const __amdgpu_buffer_rsrc_t dres = buffer_rsrc(p.dst, span4);
-        uint32_t off[32];
-        float val[32];
-#pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            const int slot = 32 * (i >> 4) + 8 * ((i & 15) >> 2) + 4 * h + (i & 3);   // < 64: in the unit
-            const int64_t o = p.units[nb].c[slot].dst_off + m;
-            off[i] = slot < ncu ? 4u * (uint32_t)o : kNoStore;
-            val[i] = i < 16 ? out0[i] : out1[i - 16];
-        }
-        if (p.glu >= 0) {                                         // uniform
-            const __amdgpu_buffer_rsrc_t gres = buffer_rsrc(p.gsrc, span4);
-            float gv[32];
-#pragma unroll
-            for (int i = 0; i < 32; ++i) gv[i] = __uint_as_float(bld4(gres, off[i], 0));
-            // one branch for the op, then straight-line code over the values
-            switch (p.glu) {
-                case QMM_GLU_REGLU: glu_rows<QMM_GLU_REGLU>(gv, val); break;
-                case QMM_GLU_GEGLU: glu_rows<QMM_GLU_GEGLU>(gv, val); break;
-                case QMM_GLU_SWIGLU: glu_rows<QMM_GLU_SWIGLU>(gv, val); break;
-                case QMM_GLU_GEGLU_ERF: glu_rows<QMM_GLU_GEGLU_ERF>(gv, val); break;
-                default: glu_rows<QMM_GLU_GEGLU_QUICK>(gv, val); break;
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < 32; ++i) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val[i]), dres, (int)off[i], 0, 0);
+        gather_store(p, nb, ncu, m, h, out0, out1);
         return;
     }
     // a tail piece: the block's pieces meet first, the holder of a sum stores it
@@ -797,7 +804,7 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q6k(KQParams p) {
 //    planes 9 + h (bit j of byte l: the fifth bit of weight l of sub-block j); codes 0..31; the
 //    min term as k_gemm3_q4k's (two MFMAs per column tile over the split sums and the mins).
 //  * Per super-block and output: out += dx (d isum) (IQ4_XS), dx (d isum - dmin imn) (Q5_K).
-template <int TYPE, int U>
+template <int TYPE, int U, bool GATHER>
 __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_sbs(KQParams p) {
     constexpr bool Q5 = TYPE == QMM_TYPE_Q5_K;
     constexpr int kVm = Q5 ? (6 | (0x7 << 4) | (0xF << 8)) : (10 | (0x7 << 4) | (0xF << 8));   // weight loads a super-block
@@ -812,7 +819,13 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_sbs(KQParams p) {
     const uint32_t mb = L / (uint32_t)p.nbn, nb = L - mb * (uint32_t)p.nbn;
     const uint32_t bz = blockIdx.y;
     const uint32_t i2 = bz % (uint32_t)p.bt.ne12, i3 = bz / (uint32_t)p.bt.ne12;
-    const int64_t mat = (int64_t)(i2 / (uint32_t)p.bt.r2) + (int64_t)(i3 / (uint32_t)p.bt.r3) * p.bt.ne02;
+    int64_t mat = (int64_t)(i2 / (uint32_t)p.bt.r2) + (int64_t)(i3 / (uint32_t)p.bt.r3) * p.bt.ne02;
+    int ncu = 64;                                             // grouped mode: the unit's columns
+    if constexpr (GATHER) {
+        if ((int32_t)nb >= __builtin_amdgcn_readfirstlane(*p.nunits)) return;   // uniform: past the route's units
+        mat = __builtin_amdgcn_readfirstlane(p.units[nb].mat);
+        ncu = __builtin_amdgcn_readfirstlane(p.units[nb].ncols);
+    }
     const int64_t rh_raw = (int64_t)mb * U + u;               // the wave's row half
     const bool row_ok = rh_raw < 2 * p.w.ntiles;              // a missing row half computes a copy, stores nothing
     const int64_t rh = row_ok ? rh_raw : 2 * p.w.ntiles - 1;
@@ -826,10 +839,21 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_sbs(KQParams p) {
     const int s0 = kb + ks * sps;
     const int s1 = std::min(s0 + sps, ke);                    // (every slice has super-blocks)
 
+    if (GATHER && mat < 0) {                                  // invalid ids: zero rows (uniform)
+        const int64_t m = mtile * kTileRows + 32 * t + j32;
+        if (!row_ok || m >= p.w.M || ks > 0) return;
+        for (int n = h; n < ncu; n += 2) p.dst[p.units[nb].c[n].dst_off + m] = 0.0f;
+        return;
+    }
+
     const __amdgpu_buffer_rsrc_t wbuf = buffer_rsrc(tile_group(p.w, mat, mtile, 0), (uint32_t)(p.w.G * p.w.tg));
-    const __amdgpu_buffer_rsrc_t abuf = buffer_rsrc(p.tA + ct0 * p.nsb * 8192, (uint32_t)(nct * p.nsb * 8192));
-    const __amdgpu_buffer_rsrc_t sbuf = buffer_rsrc(p.tS + ct0 * p.nsb * 512, (uint32_t)(nct * p.nsb * 512));
-    const __amdgpu_buffer_rsrc_t dbuf = buffer_rsrc(p.tD + ct0 * p.nsb * 32, (uint32_t)(nct * p.nsb * 128));
+    // (grouped mode: the route's whole quantization, each lane at its own column, as k_gemm3_q4k)
+    const __amdgpu_buffer_rsrc_t abuf = GATHER ? buffer_rsrc(p.codes, (uint32_t)(p.ncols * p.ldk))
+                                               : buffer_rsrc(p.tA + ct0 * p.nsb * 8192, (uint32_t)(nct * p.nsb * 8192));
+    const __amdgpu_buffer_rsrc_t sbuf = GATHER ? buffer_rsrc(p.bsp, (uint32_t)(p.nsb * p.ldT * 16))
+                                               : buffer_rsrc(p.tS + ct0 * p.nsb * 512, (uint32_t)(nct * p.nsb * 512));
+    const __amdgpu_buffer_rsrc_t dbuf = GATHER ? buffer_rsrc(p.dcol, (uint32_t)(p.ncols * p.nsb * 4))
+                                               : buffer_rsrc(p.tD + ct0 * p.nsb * 32, (uint32_t)(nct * p.nsb * 128));
     const uint32_t lane16 = (uint32_t)lane * 16;
 
     // ---- staging: k_gemm3_q4k's 18 units of 1 KB per super-block (the split sums read by Q5_K's
@@ -837,23 +861,56 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_sbs(KQParams p) {
     constexpr int NU = kq_units(U);
     constexpr uint32_t kOut = 0x7ff00000u;
     const uint32_t a_stride = (uint32_t)p.nsb * 8192, s_stride = (uint32_t)p.nsb * 512, d_stride = (uint32_t)p.nsb * 128;
-    const uint32_t s_lane = Q5 ? (uint32_t)(lane >> 5) * s_stride + (uint32_t)j32 * 16 : kOut;
-    const uint32_t d_lane = lane < 16 ? (uint32_t)(lane >> 3) * d_stride + (uint32_t)(lane & 7) * 16 : kOut;
+    uint32_t s_lane = Q5 ? (uint32_t)(lane >> 5) * s_stride + (uint32_t)j32 * 16 : kOut;
+    uint32_t d_lane = lane < 16 ? (uint32_t)(lane >> 3) * d_stride + (uint32_t)(lane & 7) * 16 : kOut;
+    // grouped mode (k_gemm3_q4k's layout): A unit (c, g) holds columns 4 g .. 4 g + 3 of tile c
+    // whole, column i's 16-byte chunk q at LDS slot q ^ (i & 15); S and D by the lane's column
+    uint32_t avo[NU];
+#pragma unroll
+    for (int k = 0; k < NU; ++k) avo[k] = 0;
+    if constexpr (GATHER) {
+        uint32_t gcol[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const int slot = 32 * c + j32;
+            gcol[c] = slot < ncu ? (uint32_t)p.units[nb].c[slot].col : kOut;
+        }
+        const uint32_t gsd = (lane >> 5) ? gcol[1] : gcol[0];
+#pragma unroll
+        for (int k = 0; k < NU; ++k) {
+            const int unit = u + k * U;
+            if (unit < 16) {
+                const int ci = 4 * (unit & 7) + (lane >> 4);  // column of the tile
+                const int slot = 32 * (unit >> 3) + ci;
+                const uint32_t col = slot < ncu ? (uint32_t)p.units[nb].c[slot].col : kOut;
+                const uint32_t q = (uint32_t)((lane & 15) ^ (ci & 15));
+                avo[k] = col == kOut ? kOut : col * (uint32_t)p.ldk + 16 * q;
+            }
+        }
+        s_lane = Q5 && gsd != kOut ? gsd * 16 : kOut;
+        d_lane = gsd == kOut ? kOut : gsd * (uint32_t)p.nsb * 4;
+    }
     uint8_t * const dump = lds + 2 * p.KS * kKQStage;
     auto stage = [&](int s, int b) {
         uint8_t * S = lds + (ks * 2 + b) * kKQStage;
 #pragma unroll
         for (int i = 0; i < NU; ++i) {
             const int unit = u + i * U;                       // wave-uniform
-            if (unit < 16)
-                dma16(abuf, S + unit * 1024, lane16 + (uint32_t)(unit >> 3) * a_stride + (uint32_t)(unit & 7) * 1024,
-                      (uint32_t)s * 8192);
-            else if (unit == 16)
-                dma16(Q5 ? sbuf : dbuf, S + 16 * 1024, s_lane, Q5 ? (uint32_t)s * 512 : 0u);
-            else if (unit == 17)
-                dma16(dbuf, S + 17 * 1024, d_lane, (uint32_t)s * 128);
-            else
+            if (unit < 16) {
+                if (GATHER)
+                    dma16(abuf, S + unit * 1024, avo[i], (uint32_t)s * 256);
+                else
+                    dma16(abuf, S + unit * 1024, lane16 + (uint32_t)(unit >> 3) * a_stride + (uint32_t)(unit & 7) * 1024,
+                          (uint32_t)s * 8192);
+            } else if (unit == 16) {
+                dma16(Q5 ? sbuf : dbuf, S + 16 * 1024, s_lane,
+                      !Q5 ? 0u : GATHER ? (uint32_t)(s * p.ldT * 16) : (uint32_t)s * 512);
+            } else if (unit == 17) {
+                if (GATHER) dma4(dbuf, S + 17 * 1024, d_lane, (uint32_t)s * 4);   // [tile][32] f32 in column order
+                else dma16(dbuf, S + 17 * 1024, d_lane, (uint32_t)s * 128);
+            } else {
                 dma16(dbuf, dump, kOut, 0);                   // (nothing: keeps the count)
+            }
         }
     };
 
@@ -896,7 +953,16 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_sbs(KQParams p) {
             sc47 = chd.x >> 16;                               // scales_h (bits 2 j, 2 j + 1)
         }
         v16i is0 = v16i{}, is1 = v16i{};                      // the super-block's integer sums
-        v4i na0 = *reinterpret_cast<const v4i *>(S + lane16), na1 = *reinterpret_cast<const v4i *>(S + 8192 + lane16);
+        // the A operands of sub-block j of both column tiles (grouped mode: chunk 2 j + h of column
+        // j32 at its swizzled slot), read one sub-block ahead
+        auto aread = [&](int j, v4i & x0, v4i & x1) {
+            const uint32_t aoff = GATHER ? (uint32_t)j32 * 256 + 16 * (uint32_t)((2 * j + h) ^ (j32 & 15))
+                                         : (uint32_t)(j * 1024) + lane16;
+            x0 = *reinterpret_cast<const v4i *>(S + aoff);
+            x1 = *reinterpret_cast<const v4i *>(S + 8192 + aoff);
+        };
+        v4i na0, na1;
+        aread(0, na0, na1);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             v4i bop;
@@ -916,10 +982,7 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_sbs(KQParams p) {
                 pl[j] = bld16(wbuf, pl_off(j), sn);
             }
             const v4i a0 = na0, a1 = na1;
-            if (j < 7) {
-                na0 = *reinterpret_cast<const v4i *>(S + (j + 1) * 1024 + lane16);
-                na1 = *reinterpret_cast<const v4i *>(S + 8192 + (j + 1) * 1024 + lane16);
-            }
+            if (j < 7) aread(j + 1, na0, na1);
             int sc;
             if constexpr (Q5) {
                 sc = (int)__builtin_amdgcn_ubfe(j < 4 ? sc03 : sc47, 8 * (j & 3), 8);
@@ -968,7 +1031,9 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_sbs(KQParams p) {
             float dx[16];
 #pragma unroll
             for (int q4 = 0; q4 < 4; ++q4) {
-                const float4 v = *reinterpret_cast<const float4 *>(S + 17408 + c * 128 + h * 64 + 16 * q4);
+                // (output order; grouped mode: the scales lie in column order)
+                const int off = GATHER ? 4 * (8 * q4 + 4 * h) : h * 64 + 16 * q4;
+                const float4 v = *reinterpret_cast<const float4 *>(S + 17408 + c * 128 + off);
                 dx[4 * q4] = v.x;
                 dx[4 * q4 + 1] = v.y;
                 dx[4 * q4 + 2] = v.z;
@@ -1037,6 +1102,10 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_sbs(KQParams p) {
     if (!row_ok) return;
     const int64_t m = mtile * kTileRows + 32 * t + j32;
     if (m >= p.w.M) return;
+    if constexpr (GATHER) {
+        gather_store(p, nb, ncu, m, h, out0, out1);
+        return;
+    }
     const uint32_t live = piece >= 0 ? kq_meet(p.tree + ((size_t)(L - p.full) * U + u) * (size_t)p.tslots * 2048, piece,
                                                p.ts, out0, out1, lane)
                                      : 0xffffffffu;
@@ -1295,26 +1364,26 @@ hipError_t launch_q6k(const KQParams & q, const G3Shape & sh, const dim3 & g, co
     return hipGetLastError();
 }
 
-template <int TYPE, int U>
+template <int TYPE, int U, bool GATHER>
 hipError_t launch_sbs(const KQParams & q, const G3Shape & sh, const dim3 & g, const dim3 & b, hipStream_t s,
                       const KTime * kt) {
-    static const hipError_t attr = hipFuncSetAttribute((const void *)k_gemm3_sbs<TYPE, U>,
+    static const hipError_t attr = hipFuncSetAttribute((const void *)k_gemm3_sbs<TYPE, U, GATHER>,
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (attr != hipSuccess) return attr;
-    if (kt) hipExtLaunchKernelGGL(k_gemm3_sbs<TYPE, U>, g, b, (uint32_t)sh.lds, s, kt->start, kt->stop, 0, q);
-    else k_gemm3_sbs<TYPE, U><<<g, b, sh.lds, s>>>(q);
+    if (kt) hipExtLaunchKernelGGL(k_gemm3_sbs<TYPE, U, GATHER>, g, b, (uint32_t)sh.lds, s, kt->start, kt->stop, 0, q);
+    else k_gemm3_sbs<TYPE, U, GATHER><<<g, b, sh.lds, s>>>(q);
     return hipGetLastError();
 }
 
-template <int TYPE>
+template <int TYPE, bool GATHER>
 hipError_t launch_sbs_u(const KQParams & q, const G3Shape & sh, const dim3 & g, const dim3 & b, hipStream_t s,
                         const KTime * kt) {
     switch (sh.U) {
-        case 12: return launch_sbs<TYPE, 12>(q, sh, g, b, s, kt);
-        case 6: return launch_sbs<TYPE, 6>(q, sh, g, b, s, kt);
-        case 4: return launch_sbs<TYPE, 4>(q, sh, g, b, s, kt);
-        case 3: return launch_sbs<TYPE, 3>(q, sh, g, b, s, kt);
-        case 2: return launch_sbs<TYPE, 2>(q, sh, g, b, s, kt);
+        case 12: return launch_sbs<TYPE, 12, GATHER>(q, sh, g, b, s, kt);
+        case 6: return launch_sbs<TYPE, 6, GATHER>(q, sh, g, b, s, kt);
+        case 4: return launch_sbs<TYPE, 4, GATHER>(q, sh, g, b, s, kt);
+        case 3: return launch_sbs<TYPE, 3, GATHER>(q, sh, g, b, s, kt);
+        case 2: return launch_sbs<TYPE, 2, GATHER>(q, sh, g, b, s, kt);
         default: return hipErrorInvalidValue;
     }
 }
@@ -1470,11 +1539,12 @@ bool kq_shape(const WView & w, int64_t N, int64_t nbatch, G3Shape * sh, bool blk
 }
 }  // namespace
 
-bool gemm3_id_supported(int type) { return type == QMM_TYPE_Q4_K && gemm3_supported(type); }
+bool gemm3_id_supported(int type) {
+    return (type == QMM_TYPE_Q4_K || type == QMM_TYPE_Q5_K || type == QMM_TYPE_IQ4_XS) && gemm3_supported(type);
+}
 
 bool gemm3_id_shape(const WView & w, int64_t max_units, G3Shape * sh) {
-    return gemm3_id_supported(QMM_TYPE_Q4_K) && max_units > 0 && w.G > 0 && w.ntiles > 0 &&
-           kq_shape_ncp(w, max_units, 1, sh, false, false);
+    return max_units > 0 && w.G > 0 && w.ntiles > 0 && kq_shape_ncp(w, max_units, 1, sh, false, false);
 }
 
 hipError_t launch_gemm3_id(int type, const WView & w, const ActBuf & a, const GemmUnit * units, const int32_t * nunits,
@@ -1515,7 +1585,12 @@ hipError_t launch_gemm3_id(int type, const WView & w, const ActBuf & a, const Ge
     q.glu = glu;
     q.dspan = dst_span;
     const dim3 g((unsigned)(8 * q.fchunk), 1u), b(sh.threads);
-    return launch_kq_u<true>(q, sh, g, b, s, kt);
+    switch (type) {
+        case QMM_TYPE_Q4_K: return launch_kq_u<true>(q, sh, g, b, s, kt);
+        case QMM_TYPE_Q5_K: return launch_sbs_u<QMM_TYPE_Q5_K, true>(q, sh, g, b, s, kt);
+        case QMM_TYPE_IQ4_XS: return launch_sbs_u<QMM_TYPE_IQ4_XS, true>(q, sh, g, b, s, kt);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 // Launch shape of both kernels (kq_shape): U row-half waves per K slice x KS slices.
@@ -1570,8 +1645,8 @@ hipError_t launch_gemm3(int type, const WView & w, const TiledAct & a, int64_t n
     switch (type) {
         case QMM_TYPE_Q4_K: return launch_kq_u<false>(q, sh, g, b, s, kt);
         case QMM_TYPE_Q6_K: return launch_q6k_u(q, sh, g, b, s, kt);
-        case QMM_TYPE_Q5_K: return launch_sbs_u<QMM_TYPE_Q5_K>(q, sh, g, b, s, kt);
-        case QMM_TYPE_IQ4_XS: return launch_sbs_u<QMM_TYPE_IQ4_XS>(q, sh, g, b, s, kt);
+        case QMM_TYPE_Q5_K: return launch_sbs_u<QMM_TYPE_Q5_K, false>(q, sh, g, b, s, kt);
+        case QMM_TYPE_IQ4_XS: return launch_sbs_u<QMM_TYPE_IQ4_XS, false>(q, sh, g, b, s, kt);
         case QMM_TYPE_Q4_0: return launch_blk_u<QMM_TYPE_Q4_0>(q, sh, g, b, s, kt);
         case QMM_TYPE_Q8_0: return launch_blk_u<QMM_TYPE_Q8_0>(q, sh, g, b, s, kt);
         case QMM_TYPE_IQ4_NL: return launch_blk_u<QMM_TYPE_IQ4_NL>(q, sh, g, b, s, kt);

@@ -1325,10 +1325,14 @@ static int route_units(qmm_ctx * ctx, const qmm_tensor * ids, int64_t ne11, int6
 }
 
 // MUL_MAT_ID on the grouped GEMM when the experts average this many pairs or more
-// (QMM_MOE_GEMM_MIN overrides; 0 switches it off)
-static int64_t moe_gemm_min_pairs() {
+// (QMM_MOE_GEMM_MIN overrides; 0 switches it off).  Gate + up + GLU on Q4_K from 64: its GEMV
+// tasks fuse both products and the GLU in one launch on the MFMA GEMV, which the grouped GEMM's
+// route and two launches overtake only past ~60 pairs (16 experts of 512 x 2048, top-10: 37.3
+// against 30.7 us at 40 pairs, 40.2 against 44.1 at 80; IQ4_XS breaks even at 40, Q5_K's v_dot4
+// tasks lose from 25)
+static int64_t moe_gemm_min_pairs(int type = -1, bool glu = false) {
     const char * e = getenv("QMM_MOE_GEMM_MIN");
-    return e ? atoll(e) : 32;
+    return e ? atoll(e) : glu && type == QMM_TYPE_Q4_K ? 64 : 32;
 }
 // floats from a MUL_MAT_ID dst's first element to one past its last (the grouped GEMM stores
 // through 32-bit byte offsets: it takes spans below 2^30 floats)
@@ -1337,8 +1341,8 @@ static int64_t id_dst_span(const qmm_tensor * dst) {
            (dst->ne[3] - 1) * (int64_t)(dst->nb[3] / 4) + dst->ne[0];
 }
 constexpr int64_t kMaxIdSpan = ((int64_t)1 << 30) - 1;
-static bool use_moe_gemm(int type, const WView & w, int64_t npairs, int64_t n_as) {
-    const int64_t mn = moe_gemm_min_pairs();
+static bool use_moe_gemm(int type, const WView & w, int64_t npairs, int64_t n_as, bool glu = false) {
+    const int64_t mn = moe_gemm_min_pairs(type, glu);
     G3Shape sh;
     // (K >= 1024: with fewer super-blocks per wave the GEMV tasks win, measured on 2048 x 512)
     return mn > 0 && npairs >= mn * n_as && w.G >= 4 && gemm3_id_supported(type) &&
@@ -1347,13 +1351,13 @@ static bool use_moe_gemm(int type, const WView & w, int64_t npairs, int64_t n_as
 
 // The route-task path's known costs, as downgrade keys: an expert with more pairs than a task
 // takes (8) streams its weights once per task; past the grouped GEMM's pair threshold the type
-// has no grouped kernel (only Q4_K does) or K is below its 1024
+// has no grouped kernel (Q4_K, Q5_K and IQ4_XS do) or K is below its 1024
 static void note_moe_downgrades(qmm_ctx * ctx, const char * op, int type, const WView & w, int64_t npairs, int64_t n_as,
-                                const char * path) {
+                                const char * path, bool glu = false) {
     if (npairs > (int64_t)kMaxTaskCols * n_as)
         note_downgrade(ctx, "op=%s type=%s k=%lld pairs/expert=%s path=%s reason=expert-weights-per-8-pair-task", op,
                        type_name(type), (long long)w.K, cols_bucket((npairs + n_as - 1) / n_as), path);
-    const int64_t mn = moe_gemm_min_pairs();
+    const int64_t mn = moe_gemm_min_pairs(type, glu);
     if (mn > 0 && npairs >= mn * n_as)
         note_downgrade(ctx, "op=%s type=%s k=%lld pairs/expert=%s path=%s reason=%s", op, type_name(type),
                        (long long)w.K, cols_bucket((npairs + n_as - 1) / n_as), path,
@@ -1453,7 +1457,7 @@ int qmm_mul_mat_id_glu(qmm_ctx * ctx, const qmm_tensor * gate, const qmm_tensor 
         ctx->path = "glu-gemv-id-fq";
         return rc;
     }
-    if (use_moe_gemm(gate->type, wg, npairs, n_as) && id_dst_span(dst) <= kMaxIdSpan) {
+    if (use_moe_gemm(gate->type, wg, npairs, n_as, true) && id_dst_span(dst) <= kMaxIdSpan) {
         // the grouped GEMM: one route and quantization for both products; gate into the scratch
         // at dst's offsets, then up with act(gate) * up applied at its stores
         const int64_t dnb1 = (int64_t)(dst->nb[1] / 4), dnb2 = (int64_t)(dst->nb[2] / 4);
@@ -1498,7 +1502,7 @@ int qmm_mul_mat_id_glu(qmm_ctx * ctx, const qmm_tensor * gate, const qmm_tensor 
     GemvPair pair{ wu.base, in_wg ? 0 : (int64_t)half, in_wg ? glu_op : -1 };
     float * d = (float *)((uint8_t *)dst->buffer->ptr + dst->offs);
     ctx->path = plan.mma ? "glu-gemv-id-mfma" : "glu-gemv-id";
-    note_moe_downgrades(ctx, "MUL_MAT_ID+GLU", gate->type, wg, npairs, n_as, ctx->path.c_str());
+    note_moe_downgrades(ctx, "MUL_MAT_ID+GLU", gate->type, wg, npairs, n_as, ctx->path.c_str(), true);
     KTime kt;
     const KTime * ktp;
     if ((rc = ktime_pair(ctx, &kt, &ktp))) return rc;

@@ -585,13 +585,18 @@ def test_mul_mat_id_many_pairs(be, sc, orc, T):
     assert not got[T - 1, 3].any()
 
 
+GROUPED_TYPES = [qmm.Q4_K, qmm.Q5_K, qmm.IQ4_XS]
+
+
+@pytest.mark.parametrize("qtype", GROUPED_TYPES)
 @pytest.mark.parametrize("bcast", [True, False])
-def test_mul_mat_id_grouped_gemm(be, sc, orc, monkeypatch, bcast):
-    """MUL_MAT_ID on the grouped GEMM (experts averaging >= 32 pairs): 64-column units of one
-    expert, activations gathered from the route's quantization; ragged: 100 rows, 3 of 8
-    experts without pairs, pair counts not a multiple of 64, negative ids (zero rows)"""
-    qtype, E, n_used, M, K, T = qmm.Q4_K, 8, 3, 100, 1280, 300
-    say("mul_mat_id grouped gemm", bcast)
+def test_mul_mat_id_grouped_gemm(be, sc, orc, monkeypatch, qtype, bcast):
+    """MUL_MAT_ID on the grouped GEMM (experts averaging >= 32 pairs) of each type that has one:
+    64-column units of one expert, activations gathered from the route's quantization; ragged:
+    100 rows, 3 of 8 experts without pairs, pair counts not a multiple of 64, negative ids
+    (zero rows)"""
+    E, n_used, M, K, T = 8, 3, 100, 1280, 300
+    say("mul_mat_id grouped gemm", qtype, bcast)
     raw = synth.weights(qtype, E * M, K, seed=81)
     g = np.random.default_rng(82)
     ids = np.stack([g.choice([0, 2, 4, 5, 6], size=n_used, replace=False) for _ in range(T)]).astype(np.int32)
@@ -1231,16 +1236,18 @@ def test_mul_mat_id_glu_per_slot_src1(be, sc, orc):
     assert rel_err(got, ref) <= TOL
 
 
-@pytest.mark.parametrize("op,bcast", [(qmm.GLU_SWIGLU, True), (qmm.GLU_GEGLU, False), (qmm.GLU_REGLU, True)])
-def test_mul_mat_id_glu_grouped_gemm(be, sc, orc, monkeypatch, op, bcast):
+@pytest.mark.parametrize("op,bcast,qtype", [(qmm.GLU_SWIGLU, True, qmm.Q4_K), (qmm.GLU_GEGLU, False, qmm.Q4_K),
+                                            (qmm.GLU_REGLU, True, qmm.Q4_K), (qmm.GLU_SWIGLU, False, qmm.Q5_K),
+                                            (qmm.GLU_GEGLU, True, qmm.IQ4_XS)])
+def test_mul_mat_id_glu_grouped_gemm(be, sc, orc, monkeypatch, op, bcast, qtype):
     """MUL_MAT_ID gate + up + GLU on the grouped GEMM (experts averaging >= 32 pairs): one route
     and quantization, the gate product into a scratch at dst's offsets, the up product storing
     act(gate) * up; ragged (100 rows, 3 of 8 experts without pairs, pair counts not a multiple of
     64), negative ids give zero rows, an id past the expert count is reported; the same op on the
     GEMV tasks agrees"""
     from oracle import glu as G
-    qtype, E, n_used, M, K, T = qmm.Q4_K, 8, 3, 100, 1280, 300
-    say("mul_mat_id_glu grouped gemm", op, bcast)
+    E, n_used, M, K, T = 8, 3, 100, 1280, 300
+    say("mul_mat_id_glu grouped gemm", op, bcast, qtype)
     rg, ru = synth.weights(qtype, E * M, K, seed=191), synth.weights(qtype, E * M, K, seed=192)
     g = np.random.default_rng(193)
     ids = np.stack([g.choice([0, 2, 4, 5, 6], size=n_used, replace=False) for _ in range(T)]).astype(np.int32)
