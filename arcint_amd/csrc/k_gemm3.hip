@@ -574,7 +574,7 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q4k(KQParams p) {
 //    h holds l in [16 h, 16 h + 16): ql chunk plane 4 n + 2 (s & 1) + h, qh plane 8 + 2 n + h.
 //    q - 32 per byte without borrows: (q + 0x60) ^ 0x80 (q + 0x60 <= 0x9f).
 //  * Per super-block and output: out += dx (d isum) (ggml's d_w d_x times the integer sum).
-template <int U>
+template <int U, bool GATHER>
 __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q6k(KQParams p) {
     extern __shared__ __align__(16) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, j32 = lane & 31;
@@ -587,7 +587,13 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q6k(KQParams p) {
     const uint32_t mb = L / (uint32_t)p.nbn, nb = L - mb * (uint32_t)p.nbn;
     const uint32_t bz = blockIdx.y;
     const uint32_t i2 = bz % (uint32_t)p.bt.ne12, i3 = bz / (uint32_t)p.bt.ne12;
-    const int64_t mat = (int64_t)(i2 / (uint32_t)p.bt.r2) + (int64_t)(i3 / (uint32_t)p.bt.r3) * p.bt.ne02;
+    int64_t mat = (int64_t)(i2 / (uint32_t)p.bt.r2) + (int64_t)(i3 / (uint32_t)p.bt.r3) * p.bt.ne02;
+    int ncu = 64;                                             // grouped mode: the unit's columns
+    if constexpr (GATHER) {
+        if ((int32_t)nb >= __builtin_amdgcn_readfirstlane(*p.nunits)) return;   // uniform: past the route's units
+        mat = __builtin_amdgcn_readfirstlane(p.units[nb].mat);
+        ncu = __builtin_amdgcn_readfirstlane(p.units[nb].ncols);
+    }
     const int64_t rh_raw = (int64_t)mb * U + u;               // the wave's row half
     const bool row_ok = rh_raw < 2 * p.w.ntiles;              // a missing row half computes a copy, stores nothing
     const int64_t rh = row_ok ? rh_raw : 2 * p.w.ntiles - 1;
@@ -601,9 +607,19 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q6k(KQParams p) {
     const int s0 = kb + ks * sps;
     const int s1 = std::min(s0 + sps, ke);                    // (every slice has super-blocks)
 
+    if (GATHER && mat < 0) {                                  // invalid ids: zero rows (uniform)
+        const int64_t m = mtile * kTileRows + 32 * t + j32;
+        if (!row_ok || m >= p.w.M || ks > 0) return;
+        for (int n = h; n < ncu; n += 2) p.dst[p.units[nb].c[n].dst_off + m] = 0.0f;
+        return;
+    }
+
     const __amdgpu_buffer_rsrc_t wbuf = buffer_rsrc(tile_group(p.w, mat, mtile, 0), (uint32_t)(p.w.G * p.w.tg));
-    const __amdgpu_buffer_rsrc_t abuf = buffer_rsrc(p.tA + ct0 * p.nsb * 8192, (uint32_t)(nct * p.nsb * 8192));
-    const __amdgpu_buffer_rsrc_t dbuf = buffer_rsrc(p.tD + ct0 * p.nsb * 32, (uint32_t)(nct * p.nsb * 128));
+    // (grouped mode: the route's whole quantization, each lane at its own column, as k_gemm3_q4k)
+    const __amdgpu_buffer_rsrc_t abuf = GATHER ? buffer_rsrc(p.codes, (uint32_t)(p.ncols * p.ldk))
+                                               : buffer_rsrc(p.tA + ct0 * p.nsb * 8192, (uint32_t)(nct * p.nsb * 8192));
+    const __amdgpu_buffer_rsrc_t dbuf = GATHER ? buffer_rsrc(p.dcol, (uint32_t)(p.ncols * p.nsb * 4))
+                                               : buffer_rsrc(p.tD + ct0 * p.nsb * 32, (uint32_t)(nct * p.nsb * 128));
     const uint32_t lane16 = (uint32_t)lane * 16;
 
     // ---- staging: k_gemm3_q4k's 18 units of 1 KB per super-block (A of both tiles; unit 16, the
@@ -612,22 +628,48 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q6k(KQParams p) {
     constexpr int NU = kq_units(U);
     constexpr uint32_t kOut = 0x7ff00000u;
     const uint32_t a_stride = (uint32_t)p.nsb * 8192, d_stride = (uint32_t)p.nsb * 128;
-    const uint32_t d_lane = lane < 16 ? (uint32_t)(lane >> 3) * d_stride + (uint32_t)(lane & 7) * 16 : kOut;
+    uint32_t d_lane = lane < 16 ? (uint32_t)(lane >> 3) * d_stride + (uint32_t)(lane & 7) * 16 : kOut;
+    // grouped mode (k_gemm3_q4k's layout): A unit (c, g) holds columns 4 g .. 4 g + 3 of tile c
+    // whole, column i's 16-byte chunk q at LDS slot q ^ (i & 15); D by the lane's column
+    uint32_t avo[NU];
+#pragma unroll
+    for (int k = 0; k < NU; ++k) avo[k] = 0;
+    if constexpr (GATHER) {
+        const int slot = 32 * (lane >> 5) + j32;
+        const uint32_t gsd = slot < ncu ? (uint32_t)p.units[nb].c[slot].col : kOut;
+#pragma unroll
+        for (int k = 0; k < NU; ++k) {
+            const int unit = u + k * U;
+            if (unit < 16) {
+                const int ci = 4 * (unit & 7) + (lane >> 4);  // column of the tile
+                const int cs = 32 * (unit >> 3) + ci;
+                const uint32_t col = cs < ncu ? (uint32_t)p.units[nb].c[cs].col : kOut;
+                const uint32_t q = (uint32_t)((lane & 15) ^ (ci & 15));
+                avo[k] = col == kOut ? kOut : col * (uint32_t)p.ldk + 16 * q;
+            }
+        }
+        d_lane = gsd == kOut ? kOut : gsd * (uint32_t)p.nsb * 4;
+    }
     uint8_t * const dump = lds + 2 * p.KS * kKQStage;
     auto stage = [&](int s, int b) {
         uint8_t * S = lds + (ks * 2 + b) * kKQStage;
 #pragma unroll
         for (int i = 0; i < NU; ++i) {
             const int unit = u + i * U;                       // wave-uniform
-            if (unit < 16)
-                dma16(abuf, S + unit * 1024, lane16 + (uint32_t)(unit >> 3) * a_stride + (uint32_t)(unit & 7) * 1024,
-                      (uint32_t)s * 8192);
-            else if (unit == 16)
+            if (unit < 16) {
+                if (GATHER)
+                    dma16(abuf, S + unit * 1024, avo[i], (uint32_t)s * 256);
+                else
+                    dma16(abuf, S + unit * 1024, lane16 + (uint32_t)(unit >> 3) * a_stride + (uint32_t)(unit & 7) * 1024,
+                          (uint32_t)s * 8192);
+            } else if (unit == 16) {
                 dma16(dbuf, S + 16 * 1024, kOut, 0);
-            else if (unit == 17)
-                dma16(dbuf, S + 17 * 1024, d_lane, (uint32_t)s * 128);
-            else
+            } else if (unit == 17) {
+                if (GATHER) dma4(dbuf, S + 17 * 1024, d_lane, (uint32_t)s * 4);   // [tile][32] f32 in column order
+                else dma16(dbuf, S + 17 * 1024, d_lane, (uint32_t)s * 128);
+            } else {
                 dma16(dbuf, dump, kOut, 0);                   // (nothing: keeps the count)
+            }
         }
     };
 
@@ -659,7 +701,16 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q6k(KQParams p) {
         const uint32_t sn = (uint32_t)std::min(s + 1, s1 - 1) * tgs;
         const uint32_t cdw = dw;
         v16i is0 = v16i{}, is1 = v16i{};                      // the super-block's integer sums
-        v4i na0 = *reinterpret_cast<const v4i *>(S + lane16), na1 = *reinterpret_cast<const v4i *>(S + 8192 + lane16);
+        // the A operands of sub-block j of both column tiles (grouped mode: chunk 2 j + h of column
+        // j32 at its swizzled slot), read one sub-block ahead
+        auto aread = [&](int j, v4i & x0, v4i & x1) {
+            const uint32_t aoff = GATHER ? (uint32_t)j32 * 256 + 16 * (uint32_t)((2 * j + h) ^ (j32 & 15))
+                                         : (uint32_t)(j * 1024) + lane16;
+            x0 = *reinterpret_cast<const v4i *>(S + aoff);
+            x1 = *reinterpret_cast<const v4i *>(S + 8192 + aoff);
+        };
+        v4i na0, na1;
+        aread(0, na0, na1);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int n = j >> 2, sj = j & 3;
@@ -673,10 +724,7 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q6k(KQParams p) {
             const v4i b0 = v4i{ (int)(w0 & m0), (int)(w1 & m0), (int)(w2 & m0), (int)(w3 & m0) };
             const v4i b1 = v4i{ (int)(w0 & m1), (int)(w1 & m1), (int)(w2 & m1), (int)(w3 & m1) };
             const v4i a0 = na0, a1 = na1;
-            if (j < 7) {
-                na0 = *reinterpret_cast<const v4i *>(S + (j + 1) * 1024 + lane16);
-                na1 = *reinterpret_cast<const v4i *>(S + 8192 + (j + 1) * 1024 + lane16);
-            }
+            if (j < 7) aread(j + 1, na0, na1);
             // the scales of groups 2 j and 2 j + 1 of the lane's row (bytes 2 j, 2 j + 1 of plane 12)
             const uint32_t sw = (j >> 1) == 0 ? sc.x : (j >> 1) == 1 ? sc.y : (j >> 1) == 2 ? sc.z : sc.w;
             const int sc0 = __builtin_amdgcn_sbfe((int)sw, 16 * (j & 1), 8);
@@ -713,7 +761,9 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q6k(KQParams p) {
             float dx[16];
 #pragma unroll
             for (int q4 = 0; q4 < 4; ++q4) {
-                const float4 v = *reinterpret_cast<const float4 *>(S + 17408 + c * 128 + h * 64 + 16 * q4);
+                // (output order; grouped mode: the scales lie in column order)
+                const int off = GATHER ? 4 * (8 * q4 + 4 * h) : h * 64 + 16 * q4;
+                const float4 v = *reinterpret_cast<const float4 *>(S + 17408 + c * 128 + off);
                 dx[4 * q4] = v.x;
                 dx[4 * q4 + 1] = v.y;
                 dx[4 * q4 + 2] = v.z;
@@ -771,6 +821,10 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q6k(KQParams p) {
     if (!row_ok) return;
     const int64_t m = mtile * kTileRows + 32 * t + j32;
     if (m >= p.w.M) return;
+    if constexpr (GATHER) {
+        gather_store(p, nb, ncu, m, h, out0, out1);
+        return;
+    }
     const uint32_t live = piece >= 0 ? kq_meet(p.tree + ((size_t)(L - p.full) * U + u) * (size_t)p.tslots * 2048, piece,
                                                p.ts, out0, out1, lane)
                                      : 0xffffffffu;
@@ -1353,14 +1407,14 @@ hipError_t launch_kq(const KQParams & q, const G3Shape & sh, const dim3 & g, con
     return hipGetLastError();
 }
 
-template <int U>
+template <int U, bool GATHER>
 hipError_t launch_q6k(const KQParams & q, const G3Shape & sh, const dim3 & g, const dim3 & b, hipStream_t s,
                       const KTime * kt) {
-    static const hipError_t attr = hipFuncSetAttribute((const void *)k_gemm3_q6k<U>,
+    static const hipError_t attr = hipFuncSetAttribute((const void *)k_gemm3_q6k<U, GATHER>,
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (attr != hipSuccess) return attr;
-    if (kt) hipExtLaunchKernelGGL(k_gemm3_q6k<U>, g, b, (uint32_t)sh.lds, s, kt->start, kt->stop, 0, q);
-    else k_gemm3_q6k<U><<<g, b, sh.lds, s>>>(q);
+    if (kt) hipExtLaunchKernelGGL(k_gemm3_q6k<U, GATHER>, g, b, (uint32_t)sh.lds, s, kt->start, kt->stop, 0, q);
+    else k_gemm3_q6k<U, GATHER><<<g, b, sh.lds, s>>>(q);
     return hipGetLastError();
 }
 
@@ -1388,14 +1442,15 @@ hipError_t launch_sbs_u(const KQParams & q, const G3Shape & sh, const dim3 & g, 
     }
 }
 
+template <bool GATHER>
 hipError_t launch_q6k_u(const KQParams & q, const G3Shape & sh, const dim3 & g, const dim3 & b, hipStream_t s,
                         const KTime * kt) {
     switch (sh.U) {
-        case 12: return launch_q6k<12>(q, sh, g, b, s, kt);
-        case 6: return launch_q6k<6>(q, sh, g, b, s, kt);
-        case 4: return launch_q6k<4>(q, sh, g, b, s, kt);
-        case 3: return launch_q6k<3>(q, sh, g, b, s, kt);
-        case 2: return launch_q6k<2>(q, sh, g, b, s, kt);
+        case 12: return launch_q6k<12, GATHER>(q, sh, g, b, s, kt);
+        case 6: return launch_q6k<6, GATHER>(q, sh, g, b, s, kt);
+        case 4: return launch_q6k<4, GATHER>(q, sh, g, b, s, kt);
+        case 3: return launch_q6k<3, GATHER>(q, sh, g, b, s, kt);
+        case 2: return launch_q6k<2, GATHER>(q, sh, g, b, s, kt);
         default: return hipErrorInvalidValue;
     }
 }
@@ -1540,7 +1595,8 @@ bool kq_shape(const WView & w, int64_t N, int64_t nbatch, G3Shape * sh, bool blk
 }  // namespace
 
 bool gemm3_id_supported(int type) {
-    return (type == QMM_TYPE_Q4_K || type == QMM_TYPE_Q5_K || type == QMM_TYPE_IQ4_XS) && gemm3_supported(type);
+    return (type == QMM_TYPE_Q4_K || type == QMM_TYPE_Q6_K || type == QMM_TYPE_Q5_K || type == QMM_TYPE_IQ4_XS) &&
+           gemm3_supported(type);
 }
 
 bool gemm3_id_shape(const WView & w, int64_t max_units, G3Shape * sh) {
@@ -1587,6 +1643,7 @@ hipError_t launch_gemm3_id(int type, const WView & w, const ActBuf & a, const Ge
     const dim3 g((unsigned)(8 * q.fchunk), 1u), b(sh.threads);
     switch (type) {
         case QMM_TYPE_Q4_K: return launch_kq_u<true>(q, sh, g, b, s, kt);
+        case QMM_TYPE_Q6_K: return launch_q6k_u<true>(q, sh, g, b, s, kt);
         case QMM_TYPE_Q5_K: return launch_sbs_u<QMM_TYPE_Q5_K, true>(q, sh, g, b, s, kt);
         case QMM_TYPE_IQ4_XS: return launch_sbs_u<QMM_TYPE_IQ4_XS, true>(q, sh, g, b, s, kt);
         default: return hipErrorInvalidValue;
@@ -1644,7 +1701,7 @@ hipError_t launch_gemm3(int type, const WView & w, const TiledAct & a, int64_t n
     const dim3 g((unsigned)(8 * (q.fchunk + q.tchunk)), (unsigned)nbatch), b(sh.threads);
     switch (type) {
         case QMM_TYPE_Q4_K: return launch_kq_u<false>(q, sh, g, b, s, kt);
-        case QMM_TYPE_Q6_K: return launch_q6k_u(q, sh, g, b, s, kt);
+        case QMM_TYPE_Q6_K: return launch_q6k_u<false>(q, sh, g, b, s, kt);
         case QMM_TYPE_Q5_K: return launch_sbs_u<QMM_TYPE_Q5_K, false>(q, sh, g, b, s, kt);
         case QMM_TYPE_IQ4_XS: return launch_sbs_u<QMM_TYPE_IQ4_XS, false>(q, sh, g, b, s, kt);
         case QMM_TYPE_Q4_0: return launch_blk_u<QMM_TYPE_Q4_0>(q, sh, g, b, s, kt);

@@ -1351,7 +1351,7 @@ static bool use_moe_gemm(int type, const WView & w, int64_t npairs, int64_t n_as
 
 // The route-task path's known costs, as downgrade keys: an expert with more pairs than a task
 // takes (8) streams its weights once per task; past the grouped GEMM's pair threshold the type
-// has no grouped kernel (Q4_K, Q5_K and IQ4_XS do) or K is below its 1024
+// has no grouped kernel (Q4_K, Q6_K, Q5_K and IQ4_XS do) or K is below its 1024
 static void note_moe_downgrades(qmm_ctx * ctx, const char * op, int type, const WView & w, int64_t npairs, int64_t n_as,
                                 const char * path, bool glu = false) {
     if (npairs > (int64_t)kMaxTaskCols * n_as)

@@ -405,11 +405,11 @@ bool gemm3_shape(int type, const WView & w, int64_t N, int64_t nbatch, G3Shape *
 size_t gemm3_tree_words(const G3Shape & sh);
 // Grouped MoE GEMM (MUL_MAT_ID with many pairs per expert): the route's 64-column units
 // (*nunits of at most max_units) of one expert each, activations gathered from the route's q8_K
-// quantization a; unit pairs with mat < 0 get zero rows.  Q4_K only.  dst_span: the floats
-// from dst to one past its last element (below 2^30: the stores take 32-bit byte offsets).  With
-// glu >= 0 (QMM_GLU_*) this is the up product of a gate/up pair: each stored value is
-// act(gsrc[o]) * up at its dst offset o, gsrc the gate product's rows at the same offsets
-// (zero rows stay zero).
+// quantization a; unit pairs with mat < 0 get zero rows.  Q4_K, Q6_K, Q5_K and IQ4_XS.
+// dst_span: the floats from dst to one past its last element (below 2^30: the stores take
+// 32-bit byte offsets).  With glu >= 0 (QMM_GLU_*) this is the up product of a gate/up pair:
+// each stored value is act(gsrc[o]) * up at its dst offset o, gsrc the gate product's rows at
+// the same offsets (zero rows stay zero).
 bool gemm3_id_supported(int type);
 bool gemm3_id_shape(const WView & w, int64_t max_units, G3Shape * sh);
 hipError_t launch_gemm3_id(int type, const WView & w, const ActBuf & a, const GemmUnit * units, const int32_t * nunits,

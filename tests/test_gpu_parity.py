@@ -585,7 +585,7 @@ def test_mul_mat_id_many_pairs(be, sc, orc, T):
     assert not got[T - 1, 3].any()
 
 
-GROUPED_TYPES = [qmm.Q4_K, qmm.Q5_K, qmm.IQ4_XS]
+GROUPED_TYPES = [qmm.Q4_K, qmm.Q6_K, qmm.Q5_K, qmm.IQ4_XS]
 
 
 @pytest.mark.parametrize("qtype", GROUPED_TYPES)
@@ -1238,7 +1238,7 @@ def test_mul_mat_id_glu_per_slot_src1(be, sc, orc):
 
 @pytest.mark.parametrize("op,bcast,qtype", [(qmm.GLU_SWIGLU, True, qmm.Q4_K), (qmm.GLU_GEGLU, False, qmm.Q4_K),
                                             (qmm.GLU_REGLU, True, qmm.Q4_K), (qmm.GLU_SWIGLU, False, qmm.Q5_K),
-                                            (qmm.GLU_GEGLU, True, qmm.IQ4_XS)])
+                                            (qmm.GLU_GEGLU, True, qmm.IQ4_XS), (qmm.GLU_SWIGLU, True, qmm.Q6_K)])
 def test_mul_mat_id_glu_grouped_gemm(be, sc, orc, monkeypatch, op, bcast, qtype):
     """MUL_MAT_ID gate + up + GLU on the grouped GEMM (experts averaging >= 32 pairs): one route
     and quantization, the gate product into a scratch at dst's offsets, the up product storing
@@ -1321,24 +1321,26 @@ def test_downgrade_keys(sc, orc, monkeypatch):
         assert keys["src=qmm op=MUL_MAT type=Q5_K k=512 cols=129+ path=gemm-mfma reason=no-streaming-gemm"] == 1
         assert not any("type=Q6_K" in k and "no-streaming-gemm" in k for k in keys), keys
         # MUL_MAT_ID on route tasks: 16 experts, 80 tokens x 8 used = 40 pairs an expert (each expert's
-        # weights stream once per 8-pair task); Q6_K has no grouped GEMM past its 32-pair threshold
+        # weights stream once per 8-pair task), past the grouped GEMM's 32-pair threshold: Q6_K's
+        # grouped GEMM needs K >= 1024, Q8_0 has none
         E, T, k, M, K = 16, 80, 8, 64, 512
-        w = b2.new_tensor(qmm.Q6_K, (K, M, E))
-        b2.set_tensor(w, synth.weights(qmm.Q6_K, M * E, K, 3))
-        x = b2.new_tensor(qmm.F32, (K, 1, T))
-        b2.set_tensor(x, synth.activations(T, K, 4).view(np.uint8).ravel())
-        ids = b2.new_tensor(qmm.I32, (k, T))
-        b2.set_tensor(ids, synth.moe_ids(T, E, k, 5).view(np.uint8).ravel())
-        y = b2.new_tensor(qmm.F32, (M, k, T))
-        b2.mul_mat_id(w, x, ids, y)
-        bufs.extend([w, x, ids, y])
-        b2.synchronize()
-        n, keys = b2.downgrades()
-        path = b2.last_path()
-        assert keys[f"src=qmm op=MUL_MAT_ID type=Q6_K k=512 pairs/expert=33-128 path={path} "
-                    "reason=expert-weights-per-8-pair-task"] == 1
-        assert keys[f"src=qmm op=MUL_MAT_ID type=Q6_K k=512 pairs/expert=33-128 path={path} "
-                    "reason=no-grouped-gemm-for-type"] == 1
+        for qt, name, why in ((qmm.Q6_K, "Q6_K", "grouped-gemm-needs-k-1024"), (qmm.Q8_0, "Q8_0", "no-grouped-gemm-for-type")):
+            w = b2.new_tensor(qt, (K, M, E))
+            b2.set_tensor(w, synth.weights(qt, M * E, K, 3))
+            x = b2.new_tensor(qmm.F32, (K, 1, T))
+            b2.set_tensor(x, synth.activations(T, K, 4).view(np.uint8).ravel())
+            ids = b2.new_tensor(qmm.I32, (k, T))
+            b2.set_tensor(ids, synth.moe_ids(T, E, k, 5).view(np.uint8).ravel())
+            y = b2.new_tensor(qmm.F32, (M, k, T))
+            b2.mul_mat_id(w, x, ids, y)
+            bufs.extend([w, x, ids, y])
+            b2.synchronize()
+            n, keys = b2.downgrades()
+            path = b2.last_path()
+            assert keys[f"src=qmm op=MUL_MAT_ID type={name} k=512 pairs/expert=33-128 path={path} "
+                        "reason=expert-weights-per-8-pair-task"] == 1
+            assert keys[f"src=qmm op=MUL_MAT_ID type={name} k=512 pairs/expert=33-128 path={path} "
+                        f"reason={why}"] == 1
 
 
 
