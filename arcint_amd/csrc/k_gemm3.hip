@@ -206,6 +206,13 @@ __device__ __forceinline__ uint32_t mul_u16x2(uint32_t v, uint32_t s) {
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, v) * __builtin_bit_cast(u16x2, s));
 }
 
+// a times s plus c in both 16-bit halves (v_pk_mad_u16: exact modulo 2^16, so signed too)
+__device__ __forceinline__ uint32_t mad_u16x2(uint32_t a, uint32_t s, uint32_t c) {
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, a) * __builtin_bit_cast(u16x2, s) +
+                                            __builtin_bit_cast(u16x2, c));
+}
+
 // 4 bytes per lane from a buffer into LDS at lds + 4 lane (lds wave-uniform)
 __device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, uint8_t * lds, uint32_t voff, uint32_t soff) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 4, (int)voff, (int)soff,
@@ -691,7 +698,6 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q6k(KQParams p) {
         sc = bld16(wbuf, row16 + 12 * kChunk, sb);
         dw = bld4(wbuf, d_off, sb);
     };
-    const uint32_t m0 = h ? 0u : 0xffffffffu, m1 = ~m0;      // group 2 s (lanes h = 0), 2 s + 1 (h = 1)
 
     v16f out0 = v16f{}, out1 = v16f{};                       // column tiles 0 and 1 of the pair
     auto compute = [&](int b, int s) {
@@ -700,7 +706,12 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q6k(KQParams p) {
         // used it (8 loads in all: the barrier's wait counts them)
         const uint32_t sn = (uint32_t)std::min(s + 1, s1 - 1) * tgs;
         const uint32_t cdw = dw;
-        v16i is0 = v16i{}, is1 = v16i{};                      // the super-block's integer sums
+        // lane (j32, h) holds group 2 j + h of sub-block j: its 16 products p = sc (q - 32) (13
+        // bits signed, in [-4064, 4096]) come from two packed 16-bit multiply-adds per dword, as
+        // t = p + 128, and split as p = 256 H + L: L = (int8) p, the low byte of t with bit 7
+        // flipped, and H = t >> 8 in [-16, 16], t's high byte: two int8 operands, each MFMA
+        // adding into its accumulator over the super-block (isum = 256 ah + al, exact)
+        v16i ah0, ah1, al0, al1;
         // the A operands of sub-block j of both column tiles (grouped mode: chunk 2 j + h of column
         // j32 at its swizzled slot), read one sub-block ahead
         auto aread = [&](int j, v4i & x0, v4i & x1) {
@@ -715,43 +726,40 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q6k(KQParams p) {
         for (int j = 0; j < 8; ++j) {
             const int n = j >> 2, sj = j & 3;
             const uint4 q = ql[2 * n + (sj & 1)], hb = qh[n];
-            auto code = [&](uint32_t lo, uint32_t hi) {
+            // the lane's group scale (byte 2 j + h of plane 12) and 128 - 32 sc, in both 16-bit halves
+            const uint32_t sw = (j >> 1) == 0 ? sc.x : (j >> 1) == 1 ? sc.y : (j >> 1) == 2 ? sc.z : sc.w;
+            const int sg = __builtin_amdgcn_sbfe((int)sw, 16 * (j & 1) + 8 * h, 8);
+            const uint32_t s2 = __builtin_amdgcn_perm((uint32_t)sg, (uint32_t)sg, 0x01000100u);
+            const uint32_t c2 = mad_u16x2(s2, 0xffe0ffe0u, 0x00800080u);   // 128 - 32 sc
+            auto split = [&](uint32_t lo, uint32_t hi, int & bh, int & bl) {
                 const uint32_t nib = (sj < 2 ? lo : lo >> 4) & 0x0F0F0F0Fu;
-                const uint32_t hp = (sj == 0 ? hi << 4 : sj == 1 ? hi << 2 : sj == 2 ? hi : hi >> 2) & 0x30303030u;
-                return (nib + hp + 0x60606060u) ^ 0x80808080u;  // q - 32 per byte
+                const uint32_t hs = sj == 0 ? hi << 4 : sj == 1 ? hi << 2 : sj == 2 ? hi : hi >> 2;
+                // codes 0..63, bytes 0..3 = weights 0..3: (hs & 0x30303030) | nib in one v_bitop3
+                const uint32_t qv = __builtin_amdgcn_bitop3_b32(hs, 0x30303030u, nib, 0xEA);
+                const uint32_t te = mad_u16x2(qv & 0x00ff00ffu, s2, c2);                          // weights 0, 2
+                const uint32_t to = mad_u16x2(__builtin_amdgcn_perm(qv, qv, 0x0c030c01u), s2, c2);   // weights 1, 3
+                // (bytes of the 16-bit lanes back in weight order: te, to, te, to)
+                bh = (int)__builtin_amdgcn_perm(to, te, 0x07030501u);
+                bl = (int)(__builtin_amdgcn_perm(to, te, 0x06020400u) ^ 0x80808080u);
             };
-            const uint32_t w0 = code(q.x, hb.x), w1 = code(q.y, hb.y), w2 = code(q.z, hb.z), w3 = code(q.w, hb.w);
-            const v4i b0 = v4i{ (int)(w0 & m0), (int)(w1 & m0), (int)(w2 & m0), (int)(w3 & m0) };
-            const v4i b1 = v4i{ (int)(w0 & m1), (int)(w1 & m1), (int)(w2 & m1), (int)(w3 & m1) };
+            int h0, h1, h2, h3, l0, l1, l2, l3;
+            split(q.x, hb.x, h0, l0);
+            split(q.y, hb.y, h1, l1);
+            split(q.z, hb.z, h2, l2);
+            split(q.w, hb.w, h3, l3);
+            const v4i bh = v4i{ h0, h1, h2, h3 }, bl = v4i{ l0, l1, l2, l3 };
             const v4i a0 = na0, a1 = na1;
             if (j < 7) aread(j + 1, na0, na1);
-            // the scales of groups 2 j and 2 j + 1 of the lane's row (bytes 2 j, 2 j + 1 of plane 12)
-            const uint32_t sw = (j >> 1) == 0 ? sc.x : (j >> 1) == 1 ? sc.y : (j >> 1) == 2 ? sc.z : sc.w;
-            const int sc0 = __builtin_amdgcn_sbfe((int)sw, 16 * (j & 1), 8);
-            const int sc1 = __builtin_amdgcn_sbfe((int)sw, 16 * (j & 1) + 8, 8);
             if (sj >= 2) ql[2 * n + (sj & 1)] = bld16(wbuf, plane(4 * n + 2 * (sj & 1)), sn);   // (its last use)
             if (sj == 3) qh[n] = bld16(wbuf, plane(8 + 2 * n), sn);
             if (j == 7) {
                 sc = bld16(wbuf, row16 + 12 * kChunk, sn);
                 dw = bld4(wbuf, d_off, sn);
             }
-            const v16i p00 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, v16i{}, 0, 0, 0);
-            const v16i p10 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b0, v16i{}, 0, 0, 0);
-            // (the sums are made opaque after each group: otherwise the compiler reassociates them
-            // across the sub-blocks, keeps every MFMA result for one sum at the end and spills)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) is0[r] = __mul24(sc0, p00[r]) + is0[r];
-#pragma unroll
-            for (int r = 0; r < 16; ++r) is1[r] = __mul24(sc0, p10[r]) + is1[r];
-            asm volatile("" : "+v"(is0), "+v"(is1));
-            const v16i p01 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b1, v16i{}, 0, 0, 0);
-            const v16i p11 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, v16i{}, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) is0[r] = __mul24(sc1, p01[r]) + is0[r];
-#pragma unroll
-            for (int r = 0; r < 16; ++r) is1[r] = __mul24(sc1, p11[r]) + is1[r];
-            asm volatile("" : "+v"(is0), "+v"(is1));
-            __builtin_amdgcn_sched_barrier(0);
+            ah0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bh, j ? ah0 : v16i{}, 0, 0, 0);
+            ah1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bh, j ? ah1 : v16i{}, 0, 0, 0);
+            al0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bl, j ? al0 : v16i{}, 0, 0, 0);
+            al1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bl, j ? al1 : v16i{}, 0, 0, 0);
         }
         // the float combine of each column tile: out += dx (d isum)
         float d = h2f(cdw >> (16 * (row & 1)));
@@ -770,10 +778,11 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q6k(KQParams p) {
                 dx[4 * q4 + 3] = v.w;
             }
             v16f & o = c ? out1 : out0;
-            const v16i & is = c ? is1 : is0;
+            const v16i & ah = c ? ah1 : ah0;
+            const v16i & al = c ? al1 : al0;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int iv = is[r];
+                const int iv = ah[r] * 256 + al[r];
                 o[r] = __builtin_fmaf((float)iv * d, dx[r], o[r]);
             }
         }
