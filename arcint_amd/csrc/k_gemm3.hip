@@ -570,16 +570,19 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q4k(KQParams p) {
 // per 16-weight group times its int8 scale, summed per super-block, then d_w d_x).  The frame is
 // k_gemm3_q4k's (32 rows x 64 columns per wave, q8_K activations staged in LDS one super-block
 // ahead, weights streamed by each wave, K slices met in LDS, the tail in K pieces).
-//  * The scaled weight sc (q - 32) takes 13 bits, so the scale stays out of the operand.  Lane
-//    (j, h)'s 16 weights of sub-block s (32 weights) are exactly one scale group, 2 s + h, so an
-//    MFMA whose B operand is the lane's codes with the other lane half's masked to zero gives that
-//    group's integer dot for the 32 x 32 outputs, and one v_mad_i32_i24 per output adds it times
-//    the output lane's own row scale: 4 MFMAs (2 groups x 2 column tiles) and 64 multiply-adds
-//    per sub-block and wave.
+//  * The scaled weight p = sc (q - 32) takes 13 bits (in [-4064, 4096]), too many for an int8
+//    operand.  Lane (j, h)'s 16 weights of sub-block s (32 weights) are exactly one scale group,
+//    2 s + h, so each lane scales its own codes: two v_pk_mad_u16 per 4 codes give t = p + 128
+//    in 16-bit lanes, and p = 256 H + L splits into two int8 operands, H = t >> 8 in [-16, 16]
+//    (t's high bytes) and L = (int8) p (t's low bytes, bit 7 flipped), picked by v_perm.  Each
+//    half has its own MFMA accumulator per column tile over the super-block: 4 MFMAs per
+//    sub-block and wave, isum = 256 ah + al exact (ggml's per-group integer dots times the
+//    scales).  (First written with the scale out of the operand: one MFMA per group on codes
+//    masked to one lane half, then a v_mad_i32_i24 per output and group, ~870 VALU per
+//    super-block against ~530.)
 //  * Codes: weight k = 128 n + 32 s + l of the super-block is ql[64 n + 32 (s & 1) + l] (low
 //    nibble for s < 2, high for s >= 2) with qh[32 n + l] bits 2 s, 2 s + 1 above it; lane half
 //    h holds l in [16 h, 16 h + 16): ql chunk plane 4 n + 2 (s & 1) + h, qh plane 8 + 2 n + h.
-//    q - 32 per byte without borrows: (q + 0x60) ^ 0x80 (q + 0x60 <= 0x9f).
 //  * Per super-block and output: out += dx (d isum) (ggml's d_w d_x times the integer sum).
 template <int U, bool GATHER>
 __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_q6k(KQParams p) {
