@@ -1564,12 +1564,15 @@ bool kq_shape_ncp(const WView & w, int64_t ncp, int64_t nbatch, G3Shape * sh, bo
     sh->nst = (int)G;
     sh->threads = 64 * sh->U * sh->KS;
     sh->lds = std::max(sh->KS * 2 * kKQStage + (18 % sh->U ? 1024 : 0), (sh->KS - 1) * sh->U * 32 * 64 * 4);
-    // The last partial round (one K slice, one batch) when it holds at most one block per CU:
-    // its blocks run as ts pieces along K on the CUs that it would leave idle.  ts minimizes the
-    // pieces' load per CU, ceil(tail ts / CUs) / ts blocks, below the one block; at least two
+    // The blocks past a whole number per CU (one K slice, one batch) run as ts pieces along K.
+    // The hardware puts a block where one finishes, so each CU runs nwg / CUs whole blocks and
+    // the remainder would keep nwg % CUs CUs a whole block longer than the rest.  ts minimizes
+    // the pieces' load per CU, ceil(tail ts / CUs) / ts blocks, below the one block; at least two
     // stages a piece, ties to fewer pieces.  (Measured at N = 512: IQ4_NL 14336 x 4096, 896
-    // blocks of 4 waves = 768 + 128, 124 -> 108 us in halves; Q4_K 17408 x 5120, 768 + 320,
-    // whose tail already puts two blocks on 64 CUs, 128-140 -> 132-148 us in pieces: not split.)
+    // blocks of 4 waves = 3 x 256 + 128, 124 -> 108 us in halves.  Q4_K 17408 x 5120, 1088
+    // blocks = 4 x 256 + 64: a per-block timeline showed each CU's three resident blocks served
+    // oldest first at a steady ~24 us of CU time per block, 192 CUs done at ~100 us and the 64
+    // with a fifth block at ~120.)
     const int64_t nwg = sh->mbn * ncp;
     sh->full = nwg;
     sh->ts = 1;
@@ -1577,8 +1580,7 @@ bool kq_shape_ncp(const WView & w, int64_t ncp, int64_t nbatch, G3Shape * sh, bo
     sh->tslots = 0;
     const int tail_env = env_int3("QMM_GEMM3_TAIL", 1);       // 0: whole blocks, 2..4: that many pieces (tuning)
     if (tail && nbatch == 1 && sh->KS == 1 && tail_env != 0) {
-        const int64_t slots = (int64_t)cus * (kKQMaxWaves / sh->U);   // (work-groups of U waves a CU holds)
-        const int64_t full = nwg / slots * slots, rest = nwg - full;
+        const int64_t full = nwg / cus * cus, rest = nwg - full;
         int64_t bn = 1, bd = 1;                                 // best load bn / bd (1: whole blocks)
         for (int ts = 2; ts <= 4 && rest > 0 && (rest <= cus || tail_env > 1); ++ts) {
             const int64_t pk = (G + ts - 1) / ts;

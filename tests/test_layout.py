@@ -343,14 +343,13 @@ GEMM3_KQ_SHAPES = [(5120, 17408, 512), (5120, 12288, 512), (5120, 1024, 512), (6
 
 
 def kq_tail(nwg, U, KS, G):
-    """the last partial round of a one-slice launch in K pieces when it holds at most one block
-    per CU: (whole blocks, pieces per tail block); ts in 2..4 minimizes the load per CU
+    """the blocks of a one-slice launch past a whole number per CU (nwg % 256) in K pieces:
+    (whole blocks, pieces per tail block); ts in 2..4 minimizes the load per CU
     ceil(tail ts / 256) / ts below 1, at least two stages a piece and the last piece not empty,
     ties to fewer pieces"""
     if KS != 1:
         return nwg, 1
-    slots = 256 * (12 // U)
-    full = nwg // slots * slots
+    full = nwg // 256 * 256
     rest = nwg - full
     best = (1, 1)                                                 # load per CU: num / den
     for ts in range(2, 5):
@@ -404,12 +403,13 @@ def test_gemm_stream_kquant_plan(qtype, K, M, N):
     check_kq_plan(info, K // 256, M, N, KQ_CANDS)
 
 
-# IQ4_NL 14336 x 4096 x 512: 896 blocks of 4 row-half waves, three a CU; the 768 of the first round
-# run whole, the other 128 as two K halves each (1024 work-groups); QMM_GEMM3_TAIL=0: whole
-# blocks.  Q4_K 17408 x 5120 x 512 (1088 blocks, a tail of 320: two on some CUs) is not split.
+# IQ4_NL 14336 x 4096 x 512: 896 blocks of 4 row-half waves = 3 x 256 + 128; the 768 run whole,
+# the other 128 as two K halves each (1024 work-groups); QMM_GEMM3_TAIL=0: whole blocks.  Q4_K
+# 17408 x 5120 x 512: 1088 blocks = 4 x 256 + 64, the 64 as four K pieces each (1280).
 @pytest.mark.parametrize("qtype,K,M,tail,wgs", [(qmm.IQ4_NL, 4096, 14336, "1", 768 + 2 * 128),
                                                 (qmm.IQ4_NL, 4096, 14336, "0", 896),
-                                                (qmm.Q4_K, 5120, 17408, "1", 1088)])
+                                                (qmm.Q4_K, 5120, 17408, "1", 1024 + 4 * 64),
+                                                (qmm.Q4_K, 5120, 17408, "0", 1088)])
 def test_gemm_tail_split_plan(qtype, K, M, tail, wgs, monkeypatch):
     monkeypatch.setenv("QMM_GEMM3_TAIL", tail)
     fake = qmm.Buffer(ptr=0x1000, size=1 << 44)
