@@ -1341,17 +1341,25 @@ static int64_t id_dst_span(const qmm_tensor * dst) {
            (dst->ne[3] - 1) * (int64_t)(dst->nb[3] / 4) + dst->ne[0];
 }
 constexpr int64_t kMaxIdSpan = ((int64_t)1 << 30) - 1;
+// the K groups (256 weights) from which the grouped GEMM is taken (QMM_MOE_GEMM_KMIN overrides).
+// K = 512, 16 experts of 2048 rows, top-10 at 1024 tokens (640 pairs an expert), grouped
+// against the GEMV tasks: Q4_K 121.7 / 130.4 us, Q6_K 130.3 / 185.4, IQ4_XS 130.8 / 166.6; at
+// 40 pairs 18.7 / 18.0, 19.4 / 23.5, 19.5 / 21.7.  (Before the gathered stores stopped waiting
+// on each offset load, Q4_K lost there: 126 against 110.)  At K = 256 a wave has one stage.
+static int64_t moe_gemm_min_groups() {
+    const char * e = getenv("QMM_MOE_GEMM_KMIN");
+    return e ? atoll(e) : 2;
+}
 static bool use_moe_gemm(int type, const WView & w, int64_t npairs, int64_t n_as, bool glu = false) {
     const int64_t mn = moe_gemm_min_pairs(type, glu);
     G3Shape sh;
-    // (K >= 1024: with fewer super-blocks per wave the GEMV tasks win, measured on 2048 x 512)
-    return mn > 0 && npairs >= mn * n_as && w.G >= 4 && gemm3_id_supported(type) &&
+    return mn > 0 && npairs >= mn * n_as && w.G >= moe_gemm_min_groups() && gemm3_id_supported(type) &&
            gemm3_id_shape(w, route_max_units(npairs, n_as), &sh);
 }
 
 // The route-task path's known costs, as downgrade keys: an expert with more pairs than a task
 // takes (8) streams its weights once per task; past the grouped GEMM's pair threshold the type
-// has no grouped kernel (Q4_K, Q6_K, Q5_K and IQ4_XS do) or K is below its 1024
+// has no grouped kernel (Q4_K, Q6_K, Q5_K and IQ4_XS do) or K is below its 512
 static void note_moe_downgrades(qmm_ctx * ctx, const char * op, int type, const WView & w, int64_t npairs, int64_t n_as,
                                 const char * path, bool glu = false) {
     if (npairs > (int64_t)kMaxTaskCols * n_as)
@@ -1361,7 +1369,7 @@ static void note_moe_downgrades(qmm_ctx * ctx, const char * op, int type, const 
     if (mn > 0 && npairs >= mn * n_as)
         note_downgrade(ctx, "op=%s type=%s k=%lld pairs/expert=%s path=%s reason=%s", op, type_name(type),
                        (long long)w.K, cols_bucket((npairs + n_as - 1) / n_as), path,
-                       !gemm3_id_supported(type) ? "no-grouped-gemm-for-type" : w.G < 4 ? "grouped-gemm-needs-k-1024"
+                       !gemm3_id_supported(type) ? "no-grouped-gemm-for-type" : w.G < moe_gemm_min_groups() ? "grouped-gemm-needs-k-512"
                                                                                     : "grouped-gemm-shape");
 }
 

@@ -589,14 +589,14 @@ GROUPED_TYPES = [qmm.Q4_K, qmm.Q6_K, qmm.Q5_K, qmm.IQ4_XS]
 
 
 @pytest.mark.parametrize("qtype", GROUPED_TYPES)
-@pytest.mark.parametrize("bcast", [True, False])
-def test_mul_mat_id_grouped_gemm(be, sc, orc, monkeypatch, qtype, bcast):
+@pytest.mark.parametrize("bcast,K", [(True, 1280), (False, 1280), (False, 512)])
+def test_mul_mat_id_grouped_gemm(be, sc, orc, monkeypatch, qtype, bcast, K):
     """MUL_MAT_ID on the grouped GEMM (experts averaging >= 32 pairs) of each type that has one:
     64-column units of one expert, activations gathered from the route's quantization; ragged:
     100 rows, 3 of 8 experts without pairs, pair counts not a multiple of 64, negative ids
-    (zero rows)"""
-    E, n_used, M, K, T = 8, 3, 100, 1280, 300
-    say("mul_mat_id grouped gemm", qtype, bcast)
+    (zero rows); K = 512 (two super-blocks, the down shape) is the smallest K it takes"""
+    E, n_used, M, T = 8, 3, 100, 300
+    say("mul_mat_id grouped gemm", qtype, bcast, K)
     raw = synth.weights(qtype, E * M, K, seed=81)
     g = np.random.default_rng(82)
     ids = np.stack([g.choice([0, 2, 4, 5, 6], size=n_used, replace=False) for _ in range(T)]).astype(np.int32)
@@ -1322,9 +1322,10 @@ def test_downgrade_keys(sc, orc, monkeypatch):
         assert not any("type=Q6_K" in k and "no-streaming-gemm" in k for k in keys), keys
         # MUL_MAT_ID on route tasks: 16 experts, 80 tokens x 8 used = 40 pairs an expert (each expert's
         # weights stream once per 8-pair task), past the grouped GEMM's 32-pair threshold: Q6_K's
-        # grouped GEMM needs K >= 1024, Q8_0 has none
-        E, T, k, M, K = 16, 80, 8, 64, 512
-        for qt, name, why in ((qmm.Q6_K, "Q6_K", "grouped-gemm-needs-k-1024"), (qmm.Q8_0, "Q8_0", "no-grouped-gemm-for-type")):
+        # grouped GEMM needs K >= 512 (K = 256 here), Q8_0 has none (K = 512)
+        E, T, k, M = 16, 80, 8, 64
+        for qt, name, why, K in ((qmm.Q6_K, "Q6_K", "grouped-gemm-needs-k-512", 256),
+                                 (qmm.Q8_0, "Q8_0", "no-grouped-gemm-for-type", 512)):
             w = b2.new_tensor(qt, (K, M, E))
             b2.set_tensor(w, synth.weights(qt, M * E, K, 3))
             x = b2.new_tensor(qmm.F32, (K, 1, T))
@@ -1337,9 +1338,9 @@ def test_downgrade_keys(sc, orc, monkeypatch):
             b2.synchronize()
             n, keys = b2.downgrades()
             path = b2.last_path()
-            assert keys[f"src=qmm op=MUL_MAT_ID type={name} k=512 pairs/expert=33-128 path={path} "
+            assert keys[f"src=qmm op=MUL_MAT_ID type={name} k={K} pairs/expert=33-128 path={path} "
                         "reason=expert-weights-per-8-pair-task"] == 1
-            assert keys[f"src=qmm op=MUL_MAT_ID type={name} k=512 pairs/expert=33-128 path={path} "
+            assert keys[f"src=qmm op=MUL_MAT_ID type={name} k={K} pairs/expert=33-128 path={path} "
                         f"reason={why}"] == 1
 
 
