@@ -1525,8 +1525,12 @@ namespace {
 // whole rounds; 4-wave ones go three to a CU and a partial last round costs its fraction (the
 // CUs take the next small group as one finishes; measured on 17408 x 5120 x 512: 4-wave groups
 // 141 us, (6, 2) 145 us, (12, 1) 155 us).  Ties go to the earlier (larger U) candidate.
-// ncp = column pairs (grouped mode: route units) per batch
-bool kq_shape_ncp(const WView & w, int64_t ncp, int64_t nbatch, G3Shape * sh, bool blk, bool tail) {
+// ncp = column pairs (grouped mode: route units) per batch; tail: a dense launch (its U = 2
+// charge and the tail pieces); only >= 0: that candidate alone (the grouped mode's one-slice
+// form, kKQOneSlice); only = -2: every candidate but that one (the grouped mode's split form:
+// there it tied with (2, 2, 3) on 128 experts x 32 pairs and measured 54.8 against 46.8 us)
+constexpr int kKQOneSlice = 4;                                // (4, 1, 3) in the candidates below
+bool kq_shape_ncp(const WView & w, int64_t ncp, int64_t nbatch, G3Shape * sh, bool blk, bool tail, int only) {
     struct Cand { int U, KS, per_cu; };
     static const Cand cands[] = { { 12, 1, 1 }, { 6, 2, 1 }, { 4, 3, 1 }, { 3, 4, 1 }, { 4, 1, 3 }, { 2, 2, 3 } };
     const int64_t nrh = 2 * w.ntiles, G = w.G;
@@ -1535,6 +1539,8 @@ bool kq_shape_ncp(const WView & w, int64_t ncp, int64_t nbatch, G3Shape * sh, bo
     const int forced = env_int3("QMM_GEMM3_KQ", -1);           // index into cands (tuning)
     for (int i = 0; i < (int)(sizeof(cands) / sizeof(cands[0])); ++i) {
         if (forced >= 0 && i != forced) continue;
+        if (forced < 0 && only >= 0 && i != only) continue;
+        if (forced < 0 && only == -2 && i == kKQOneSlice) continue;
         const Cand & c = cands[i];
         // (the block types: two waves per stage share too little of their 2 KB of activations per
         // block; 11008 x 4096 x 512 measured 97 us at (2, 2) against 76 at (12, 1) and (4, 1, 3))
@@ -1604,7 +1610,7 @@ bool kq_shape_ncp(const WView & w, int64_t ncp, int64_t nbatch, G3Shape * sh, bo
     return sh->mbn * ncp < 0x7fffffff && sh->lds <= 160 * 1024 && sh->threads <= 64 * kKQMaxWaves;
 }
 bool kq_shape(const WView & w, int64_t N, int64_t nbatch, G3Shape * sh, bool blk) {
-    return kq_shape_ncp(w, ((N + 31) / 32 + 1) / 2, nbatch, sh, blk, true);
+    return kq_shape_ncp(w, ((N + 31) / 32 + 1) / 2, nbatch, sh, blk, true, -1);
 }
 }  // namespace
 
@@ -1613,20 +1619,21 @@ bool gemm3_id_supported(int type) {
            gemm3_supported(type);
 }
 
-bool gemm3_id_shape(const WView & w, int64_t max_units, G3Shape * sh) {
-    return max_units > 0 && w.G > 0 && w.ntiles > 0 && kq_shape_ncp(w, max_units, 1, sh, false, false);
+bool gemm3_id_shape(const WView & w, int64_t max_units, bool one_slice, G3Shape * sh) {
+    return max_units > 0 && w.G > 0 && w.ntiles > 0 &&
+           kq_shape_ncp(w, max_units, 1, sh, false, false, one_slice ? kKQOneSlice : -2);
 }
 
 hipError_t launch_gemm3_id(int type, const WView & w, const ActBuf & a, const GemmUnit * units, const int32_t * nunits,
-                           int64_t max_units, float * dst, int64_t dst_span, hipStream_t s, const KTime * kt,
-                           const float * gsrc, int glu) {
+                           int64_t max_units, bool one_slice, float * dst, int64_t dst_span, hipStream_t s,
+                           const KTime * kt, const float * gsrc, int glu) {
     G3Shape sh;
     if (!gemm3_id_supported(type) || a.vdt != QMM_TYPE_Q8_K || !a.bsp || !units || !nunits || a.ldk != w.G * 256 ||
         dst_span <= 0 || dst_span >= ((int64_t)1 << 30) ||
         (glu >= 0) != (gsrc != nullptr) ||
         (glu != -1 && glu != QMM_GLU_REGLU && glu != QMM_GLU_GEGLU && glu != QMM_GLU_SWIGLU &&
          glu != QMM_GLU_GEGLU_ERF && glu != QMM_GLU_GEGLU_QUICK) ||
-        !gemm3_id_shape(w, max_units, &sh) || a.ncols * a.ldk >= ((int64_t)1 << 31) ||
+        !gemm3_id_shape(w, max_units, one_slice, &sh) || a.ncols * a.ldk >= ((int64_t)1 << 31) ||
         w.G * a.ldT * 16 >= ((int64_t)1 << 31) || a.ldT < a.ncols)
         return hipErrorInvalidValue;
     KQParams q{};

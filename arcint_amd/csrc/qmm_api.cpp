@@ -1350,11 +1350,24 @@ static int64_t moe_gemm_min_groups() {
     const char * e = getenv("QMM_MOE_GEMM_KMIN");
     return e ? atoll(e) : 2;
 }
+// The grouped GEMM's launch form: 4-wave one-slice blocks, three a CU, when they make a block per
+// CU or more and the experts' 64-pair units are mostly full (48 pairs or more on average) or K
+// is 512 (split, a wave would have one stage); else the launch rule's shape, which splits K over
+// more waves.  Q4_K op, 16 experts of 512 x 2048 top-10 (one-slice against the best split
+// shape): 1024 tokens 48.5 against 61.9 us, 512 tokens 35.8 / 38.4, 256 (192 blocks) 27.7 /
+// 26.0, 128 (40 pairs a unit) 26.1 / 21.2; 128 experts x 512 tokens top-8 (32 pairs a unit)
+// 54.8 / 46.8; 2048 x 512 at 64, 128, 256 and 512 tokens 18.3 / 17.1, 20.7 / 24.1, 26.2 / 32.1
+// and 43.5 / 53.4.
+static bool moe_one_slice(const WView & w, int64_t npairs, int64_t n_as) {
+    const int64_t avg = std::max<int64_t>(1, npairs / n_as), upe = (avg + 63) / 64;
+    const int64_t blocks = (2 * w.ntiles + 3) / 4 * n_as * upe;
+    return blocks >= 256 && (avg / upe >= 48 || w.G <= 2);
+}
 static bool use_moe_gemm(int type, const WView & w, int64_t npairs, int64_t n_as, bool glu = false) {
     const int64_t mn = moe_gemm_min_pairs(type, glu);
     G3Shape sh;
     return mn > 0 && npairs >= mn * n_as && w.G >= moe_gemm_min_groups() && gemm3_id_supported(type) &&
-           gemm3_id_shape(w, route_max_units(npairs, n_as), &sh);
+           gemm3_id_shape(w, route_max_units(npairs, n_as), moe_one_slice(w, npairs, n_as), &sh);
 }
 
 // The route-task path's known costs, as downgrade keys: an expert with more pairs than a task
@@ -1403,7 +1416,8 @@ int qmm_mul_mat_id(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tensor * sr
         KTime kt;
         const KTime * ktp;
         if ((rc = ktime_pair(ctx, &kt, &ktp))) return rc;
-        QMM_HIP(ctx, launch_gemm3_id(src0->type, w, a, units, nunits, max_units, dptr, id_dst_span(dst), ctx->stream, ktp));
+        QMM_HIP(ctx, launch_gemm3_id(src0->type, w, a, units, nunits, max_units, moe_one_slice(w, npairs, n_as), dptr,
+                                     id_dst_span(dst), ctx->stream, ktp));
         return ktime_done(ctx);
     }
     const int64_t max_tasks = route_max_tasks(npairs, n_as);
@@ -1479,8 +1493,10 @@ int qmm_mul_mat_id_glu(qmm_ctx * ctx, const qmm_tensor * gate, const qmm_tensor 
         if ((rc = quantize_src1(ctx, gate->type, src1, false, &a, nullptr, &pr))) return rc;
         float * g = (float *)ctx->glu;
         float * d = (float *)((uint8_t *)dst->buffer->ptr + dst->offs);
-        QMM_HIP(ctx, launch_gemm3_id(gate->type, wg, a, units, nunits, max_units, g, span, ctx->stream));
-        QMM_HIP(ctx, launch_gemm3_id(up->type, wu, a, units, nunits, max_units, d, span, ctx->stream, nullptr, g, glu_op));
+        const bool one = moe_one_slice(wg, npairs, n_as);
+        QMM_HIP(ctx, launch_gemm3_id(gate->type, wg, a, units, nunits, max_units, one, g, span, ctx->stream));
+        QMM_HIP(ctx, launch_gemm3_id(up->type, wu, a, units, nunits, max_units, one, d, span, ctx->stream, nullptr, g,
+                                     glu_op));
         ctx->path = "glu-gemm-id-stream";
         return QMM_OK;
     }

@@ -409,12 +409,13 @@ size_t gemm3_tree_words(const G3Shape & sh);
 // dst_span: the floats from dst to one past its last element (below 2^30: the stores take
 // 32-bit byte offsets).  With glu >= 0 (QMM_GLU_*) this is the up product of a gate/up pair:
 // each stored value is act(gsrc[o]) * up at its dst offset o, gsrc the gate product's rows at
-// the same offsets (zero rows stay zero).
+// the same offsets (zero rows stay zero).  one_slice: 4-wave one-slice blocks, three a CU
+// (mostly full units, a block per CU or more), else the launch rule's shape.
 bool gemm3_id_supported(int type);
-bool gemm3_id_shape(const WView & w, int64_t max_units, G3Shape * sh);
+bool gemm3_id_shape(const WView & w, int64_t max_units, bool one_slice, G3Shape * sh);
 hipError_t launch_gemm3_id(int type, const WView & w, const ActBuf & a, const GemmUnit * units, const int32_t * nunits,
-                           int64_t max_units, float * dst, int64_t dst_span, hipStream_t s, const KTime * kt = nullptr,
-                           const float * gsrc = nullptr, int glu = -1);
+                           int64_t max_units, bool one_slice, float * dst, int64_t dst_span, hipStream_t s,
+                           const KTime * kt = nullptr, const float * gsrc = nullptr, int glu = -1);
 // tree: gemm3_tree_words(shape) words of tree slots, each kTreeEmpty (left so), or nullptr: then
 // the tail blocks run whole
 hipError_t launch_gemm3(int type, const WView & w, const TiledAct & a, int64_t nbatch, const GemmBatch & bt,
