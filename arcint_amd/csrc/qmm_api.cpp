@@ -982,6 +982,13 @@ static bool fused_dense_plan(int type, const WView & w, int64_t N, int64_t nbatc
         const int64_t tgroups = fp->ntasks * w.ntiles * w.G;
         if (w.G <= 8 && tgroups <= fused_small_tgroups()) return true;
         if (fp->ntasks * w.ntiles * fp->W >= fused_min_waves()) return true;
+        // one column with each wave on one group and K whole in its work-group (no exchange
+        // tree), given 3072 waves or more: 14336 x 4096 (3584 waves of 16-wave work-groups)
+        // IQ4_XS 10.3-10.5 -> 9.64 us, IQ4_NL 9.8-10.0 -> 9.0, Q8_0 11.8-12.0 -> 11.36 against
+        // the split form; Q4_0 4096 x 4096 (1024 waves) lost, 5.6 -> 6.5, and two groups a
+        // wave lose everywhere (4096 x 14336: 10.7 -> 27 us)
+        if (N == 1 && fp->spw == 1 && fp->ntasks * w.ntiles * fp->W >= 3072 && fused_min_waves() == INT64_MAX)
+            return true;
     }
     return split && fused_split_for(type, w, N) &&
            gemv_fused_split_plan(type, w, (int)N, nbatch, env_or("QMM_GEMV_FQS_W", type == QMM_TYPE_Q8_0 ? 8 : 4),
