@@ -621,15 +621,18 @@ def test_mul_mat_id_grouped_gemm(be, sc, orc, monkeypatch, qtype, bcast, K):
     assert rel_err(got, be.get_f32(y2).reshape(T, n_used, M)) <= TOL
 
 
-@pytest.mark.parametrize("T", [1024])
-def test_mul_mat_id_grouped_gemm_config3_shape(be, sc, orc, T):
-    """config 3's expert shape (Q4_K 512 x 2048 gate/up, ne11 = 1) with 16 experts, top-10:
-    640 pairs per expert on the grouped GEMM"""
-    qtype, E, n_used, M, K = qmm.Q4_K, 16, 10, 512, 2048
-    say("mul_mat_id grouped gemm config3 shape", T)
+@pytest.mark.parametrize("qtype", GROUPED_TYPES)
+@pytest.mark.parametrize("M,K,ne11,T", [(512, 2048, 1, 1024), (2048, 512, 10, 256)])
+def test_mul_mat_id_grouped_gemm_config3_shape(be, sc, orc, qtype, M, K, ne11, T):
+    """config 3's expert shapes with 16 experts, top-10, on the grouped GEMM's one-slice form
+    (4-wave blocks, one K slice: mostly full units, a block per CU or more): gate/up 512 x 2048
+    at 1024 tokens (ne11 = 1, 640 pairs per expert) and down 2048 x 512 at 256 (ne11 = 10, 160
+    pairs per expert, K = 512)"""
+    E, n_used = 16, 10
+    say("mul_mat_id grouped gemm config3 shape", qtype, M, K, T)
     raw = synth.weights(qtype, E * M, K, seed=84)
     ids = synth.moe_ids(T, E, n_used, seed=85)
-    x = synth.activations(T, K, seed=86).reshape(T, 1, K)
+    x = synth.activations(T * ne11, K, seed=86).reshape(T, ne11, K)
     w = sc.weights(qtype, raw, (K, M, E))
     y = sc.empty_f32((M, n_used, T))
     be.mul_mat_id(w, sc.f32(x), sc.i32(ids), y)
@@ -637,6 +640,25 @@ def test_mul_mat_id_grouped_gemm_config3_shape(be, sc, orc, T):
     assert be.last_path() == "gemm-id-stream"
     got = be.get_f32(y).reshape(T, n_used, M)
     assert rel_err(got, orc.mul_mat_id(qtype, raw, M, K, E, x, ids)) <= TOL
+
+
+def test_mul_mat_id_glu_grouped_gemm_one_slice(be, sc, orc):
+    """gate + up + SwiGLU on the grouped GEMM's one-slice form (16 experts of 512 x 2048 at 1024
+    tokens, top-10): the gate launch, then the up launch applying the GLU at its stores"""
+    from oracle import glu as G
+    qtype, E, n_used, M, K, T = qmm.Q6_K, 16, 10, 512, 2048, 1024
+    say("mul_mat_id_glu grouped gemm one slice", qtype)
+    rg, ru = synth.weights(qtype, E * M, K, seed=87), synth.weights(qtype, E * M, K, seed=88)
+    ids = synth.moe_ids(T, E, n_used, seed=89)
+    x = synth.activations(T, K, seed=90).reshape(T, 1, K)
+    wg, wu = sc.weights(qtype, rg, (K, M, E)), sc.weights(qtype, ru, (K, M, E))
+    y = sc.empty_f32((M, n_used, T))
+    be.mul_mat_id_glu(wg, wu, sc.f32(x), sc.i32(ids), y, qmm.GLU_SWIGLU)
+    be.synchronize()
+    assert be.last_path() == "glu-gemm-id-stream"
+    got = be.get_f32(y).reshape(T, n_used, M)
+    ref = G.glu(qmm.GLU_SWIGLU, orc.mul_mat_id(qtype, rg, M, K, E, x, ids), orc.mul_mat_id(qtype, ru, M, K, E, x, ids))
+    assert rel_err(got, ref) <= TOL
 
 
 def test_mul_mat_id_all_tokens_one_expert(be, sc, orc):
