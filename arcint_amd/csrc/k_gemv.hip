@@ -1508,13 +1508,6 @@ __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
         for (int j = 0; j < NC; ++j) load_x4(p.x, p.K, colv[j], ga, lane, xv[j]);
     }
     load_stage(0);
-    // one-stage types of 9-lane stages: the first two stages are requested together (B, B1), so
-    // a wave of two groups waits for one weight round trip, not two (Q5_K's 11-lane stages
-    // would spill there: it keeps one buffer)
-    constexpr bool RING = NST == 1 && NL <= 9;
-    if constexpr (RING) {
-        if (ST > 1) load_into(B1, 1);
-    }
     if (!xq) quantize();
     __builtin_amdgcn_wave_barrier();
     float acc[NC], accu[NC];
@@ -1525,8 +1518,7 @@ __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
         accu[j] = 0.0f;
         st_state[j] = 0;
     }
-    // the activation slots of stage s's group (gate stages, then up stages)
-    auto xslots = [&](int s) {
+    for (int s = 0; s < ST; ++s) {                                // uniform
         const int sl = s < S ? s : s - S, gi = sl / NST;
         XL<NC> x;
 #pragma unroll
@@ -1536,11 +1528,7 @@ __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
             x.d[j] = reinterpret_cast<const float *>(sj + 256);
             x.s[j] = reinterpret_cast<const int16_t *>(sj + 288);
         }
-        return x;
-    };
-    if constexpr (NST == 2) {
-        for (int s = 0; s < ST; ++s) {                            // uniform (ST is even: whole groups)
-            const XL<NC> x = xslots(s);
+        if constexpr (NST == 2) {                                 // (ST is even: whole groups)
             if (s < S) {
                 T::dot(B, 0, x, nc, acc, st_state);
                 T::dot(B1, 1, x, nc, acc, st_state);
@@ -1550,30 +1538,10 @@ __global__ __launch_bounds__(1024) void k_gemv_fq(FqParams p) {
             }
             ++s;
             if (s + 1 < ST) load_stage(s + 1);                    // (nothing past the last stage)
-        }
-    } else if constexpr (!RING) {
-        for (int s = 0; s < ST; ++s) {                            // uniform
-            const XL<NC> x = xslots(s);
-            if (s < S) T::dot(B, 0, x, nc, acc, st_state);
-            else T::dot(B, 0, x, nc, accu, st_state);
+        } else {
+            if (s < S) T::dot(B, sl % NST, x, nc, acc, st_state);
+            else T::dot(B, sl % NST, x, nc, accu, st_state);
             if (s + 1 < ST) load_stage(s + 1);                    // (nothing past the last stage)
-        }
-    } else {
-        // a two-buffer ring: stage s in B (s even) or B1 (s odd), stage s + 2 requested into the
-        // same buffer once stage s's dot has read it (nothing past the last stage)
-        for (int s = 0; s < ST; s += 2) {                         // uniform
-            {
-                const XL<NC> x = xslots(s);
-                if (s < S) T::dot(B, 0, x, nc, acc, st_state);
-                else T::dot(B, 0, x, nc, accu, st_state);
-                if (s + 2 < ST) load_into(B, s + 2);
-            }
-            if (s + 1 < ST) {
-                const XL<NC> x = xslots(s + 1);
-                if (s + 1 < S) T::dot(B1, 0, x, nc, acc, st_state);
-                else T::dot(B1, 0, x, nc, accu, st_state);
-                if (s + 3 < ST) load_into(B1, s + 3);
-            }
         }
     }
     const int64_t row = (int64_t)tile * kTileRows + lane;
