@@ -1158,7 +1158,7 @@ static int mul_mat_launch(qmm_ctx * ctx, const qmm_tensor * src0, const qmm_tens
         bt.d_nb2 = dn.d_nb2;
         bt.d_nb3 = dn.d_nb3;
         ctx->path = "gemm-stream";
-        // the last partial round's blocks in K pieces meeting in tree slots (grown outside
+        // the blocks past a whole number per CU in K pieces meeting in tree slots (grown outside
         // captures only; without them, and in qmm_mul_mat_noalloc, the blocks run whole)
         uint32_t * tree = nullptr;
         const size_t tw = gemm3_tree_words(g3);

@@ -393,9 +393,9 @@ struct G3Shape {
     int sps, nst;                  // stages per K slice, stages along K
     int threads, lds;
     int64_t workgroups;            // all batches
-    // the last partial round: blocks [full, mbn nbn) run as ts work-groups each, piece i over
-    // stages [i pk, (i + 1) pk) (the pieces meet in tree slots: tslots per output and block);
-    // ts = 1: every block whole
+    // the tail (the blocks past a whole number per CU): blocks [full, mbn nbn) run as ts
+    // work-groups each, piece i over stages [i pk, (i + 1) pk) (the pieces meet in tree slots:
+    // tslots per output and block); ts = 1: every block whole
     int64_t full;
     int ts, pk, tslots;
     int64_t fchunk, tchunk;        // per XCD: whole blocks, tail pieces

@@ -818,7 +818,7 @@ def test_gemm_stream_shapes(be, sc, orc, monkeypatch, qtype, KS):
         assert rel_err(got[i2], ref) <= TOL
 
 
-# the last partial round of a one-slice launch in K pieces that meet in tree slots: 2, 3 and 4
+# the tail blocks of a one-slice launch in K pieces that meet in tree slots: 2, 3 and 4
 # pieces (G = 4, 5 and 17 over the forced 4-wave shape, whose 768 slots the few blocks leave
 # mostly empty), against the oracle, the same bits on a second call (every slot is left empty,
 # and a + b = b + a whichever piece arrives first) and within rounding of whole blocks

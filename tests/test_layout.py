@@ -366,7 +366,7 @@ def check_kq_plan(info, G, M, N, cands):
     """the streaming GEMMs' launch plan: (U, KS) minimizes rounds of work-groups on 256 CUs (12-wave
     groups: one per CU, whole rounds; 4-wave: three per CU, a partial last round counted as its
     fraction) times groups per slice, U = 2 paying 1/16 more (its stage shared by two waves), ties
-    to the earlier candidate; a one-slice launch runs its last partial round's blocks in K pieces
+    to the earlier candidate; a one-slice launch runs its blocks past a whole number per CU in K pieces
     (kq_tail)"""
     nrh, ncp = 2 * -(-M // 64), -(-(-(-N // 32)) // 2)
     best = None
