@@ -1301,6 +1301,7 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_blk(KQParams p) {
         for (int r = 0; r < 16; ++r) acc[r] = __builtin_fmaf(tv[r], dx[r], acc[r]);
     };
     const uint32_t nshift = (uint32_t)(4 - 4 * h);            // Q4_0: the lane half's nibble to the high nibble
+    const Iq4Regs kr = iq4_regs();                             // IQ4_NL: the codebook in VGPRs
     auto compute = [&](int b, int s) {
         const uint8_t * S = lds + (ks * 2 + b) * kKQStage;
         const uint4 dd = wd;
@@ -1314,8 +1315,8 @@ __global__ __launch_bounds__(64 * kKQMaxWaves) void k_gemm3_blk(KQParams p) {
                 bop = v4i{ (int)x.x, (int)x.y, (int)x.z, (int)x.w };
             } else if constexpr (NLQ) {
                 const uint32_t sh = 4u * (uint32_t)h;
-                bop = v4i{ (int)iq4_lookup((x.x >> sh) & 0x0F0F0F0Fu), (int)iq4_lookup((x.y >> sh) & 0x0F0F0F0Fu),
-                           (int)iq4_lookup((x.z >> sh) & 0x0F0F0F0Fu), (int)iq4_lookup((x.w >> sh) & 0x0F0F0F0Fu) };
+                bop = v4i{ (int)iq4_lookup_r(x.x >> sh, kr), (int)iq4_lookup_r(x.y >> sh, kr),
+                           (int)iq4_lookup_r(x.z >> sh, kr), (int)iq4_lookup_r(x.w >> sh, kr) };
             } else {
                 // (q ^ 8) in the high nibble: the int8 byte is 16 (q - 8)
                 bop = v4i{ (int)(((x.x << nshift) & 0xF0F0F0F0u) ^ 0x80808080u),

@@ -321,14 +321,14 @@ template <> struct GV<QMM_TYPE_IQ4_XS> {
         int isum[NC];
 #pragma unroll
         for (int j = 0; j < NC; ++j) isum[j] = 0;
-        const uint32_t m = 0x0F0F0F0Fu;
+        const Iq4Regs kr = iq4_regs();
 #pragma unroll
         for (int ib = 0; ib < 8; ++ib) {
             const uint4 q = r[ib];
             const int ls = (int)(((slo >> (4 * ib)) & 0xFu) | (((shi >> (2 * ib)) & 3u) << 4)) - 32;
-            const uint32_t v0 = iq4_lookup(q.x & m), v1 = iq4_lookup(q.y & m), v2 = iq4_lookup(q.z & m), v3 = iq4_lookup(q.w & m);
-            const uint32_t u0 = iq4_lookup((q.x >> 4) & m), u1 = iq4_lookup((q.y >> 4) & m);
-            const uint32_t u2 = iq4_lookup((q.z >> 4) & m), u3 = iq4_lookup((q.w >> 4) & m);
+            uint32_t v0, v1, v2, v3, u0, u1, u2, u3;
+            iq4_lookup8(q.x, kr, v0, u0); iq4_lookup8(q.y, kr, v1, u1);
+            iq4_lookup8(q.z, kr, v2, u2); iq4_lookup8(q.w, kr, v3, u3);
 #pragma unroll
             for (int j = 0; j < NC; ++j) {
                 if (j < nc) {
@@ -353,13 +353,13 @@ template <> struct GV<QMM_TYPE_IQ4_NL> {
     __device__ static void dot(const uint4 * r, int, const X & x, int nc, float * acc, int *) {
         constexpr int NC = X::NC;
         const uint32_t dw2[4] = { r[8].x, r[8].y, r[8].z, r[8].w };
-        const uint32_t m = 0x0F0F0F0Fu;
+        const Iq4Regs kr = iq4_regs();
 #pragma unroll
         for (int p = 0; p < 8; ++p) {
             const uint4 q = r[p];
-            const uint32_t v0 = iq4_lookup(q.x & m), v1 = iq4_lookup(q.y & m), v2 = iq4_lookup(q.z & m), v3 = iq4_lookup(q.w & m);
-            const uint32_t u0 = iq4_lookup((q.x >> 4) & m), u1 = iq4_lookup((q.y >> 4) & m);
-            const uint32_t u2 = iq4_lookup((q.z >> 4) & m), u3 = iq4_lookup((q.w >> 4) & m);
+            uint32_t v0, v1, v2, v3, u0, u1, u2, u3;
+            iq4_lookup8(q.x, kr, v0, u0); iq4_lookup8(q.y, kr, v1, u1);
+            iq4_lookup8(q.z, kr, v2, u2); iq4_lookup8(q.w, kr, v3, u3);
             const float dw = h2f(dw2[p >> 1] >> (16 * (p & 1)));
 #pragma unroll
             for (int j = 0; j < NC; ++j) {

@@ -37,6 +37,42 @@ __device__ __forceinline__ uint32_t iq4_lookup(uint32_t nib) {
     return perm(hi, lo, sel);
 }
 
+// A constant in a VGPR.  gfx950's three-operand (VOP3) forms take no literal and read one SGPR
+// at most, so with the codebook words and masks as literals each v_perm needs its table in
+// registers anyway and each (x & m) | c becomes a v_and plus a v_or; with both in VGPRs the
+// compiler fuses the pair into one v_and_or_b32.
+template <int C>
+__device__ __forceinline__ uint32_t in_vgpr() {
+    uint32_t v;
+    asm("v_mov_b32 %0, %1" : "=v"(v) : "i"(C));
+    return v;
+}
+
+struct Iq4Regs { uint32_t k0, k1, k2, k3, m4, base; };
+
+__device__ __forceinline__ Iq4Regs iq4_regs() {
+    return { in_vgpr<(int)kv_word(0)>(), in_vgpr<(int)kv_word(1)>(), in_vgpr<(int)kv_word(2)>(),
+             in_vgpr<(int)kv_word(3)>(), in_vgpr<0x04040404>(), in_vgpr<0x03020100>() };
+}
+
+// the eight 4-bit codes of q (both nibbles of its four bytes) -> their codebook values, lo from
+// the low nibbles and hi from the high ones, iq4_lookup's three v_perm each, the selectors'
+// shift shared and their mask-and-offset one v_and_or_b32: 13 VALU for the eight against 15-16
+__device__ __forceinline__ void iq4_lookup8(uint32_t q, const Iq4Regs & k, uint32_t & lo, uint32_t & hi) {
+    const uint32_t t = q >> 4;
+    const uint32_t il = q & 0x07070707u, ih = t & 0x07070707u;
+    const uint32_t sl = ((q >> 1) & k.m4) | k.base, sh = ((t >> 1) & k.m4) | k.base;
+    lo = perm(perm(k.k3, k.k2, il), perm(k.k1, k.k0, il), sl);
+    hi = perm(perm(k.k3, k.k2, ih), perm(k.k1, k.k0, ih), sh);
+}
+
+// iq4_lookup with the constants in VGPRs: the codes in bits 0-3 of each byte of x, bits 4-7
+// ignored (x may be a byte-wise unmasked shift of the packed codes)
+__device__ __forceinline__ uint32_t iq4_lookup_r(uint32_t x, const Iq4Regs & k) {
+    const uint32_t il = x & 0x07070707u, sl = ((x >> 1) & k.m4) | k.base;
+    return perm(perm(k.k3, k.k2, il), perm(k.k1, k.k0, il), sl);
+}
+
 // The GLU activations of ggml's split GLU (ggml-cpu vec.h scalar forms), fp32 with the device
 // library's expf / tanhf / erff; glu_apply(op, x, g) = act(x) * g, REGLU as x > 0 ? x g : 0
 __device__ __forceinline__ float glu_act(int op, float x) {
