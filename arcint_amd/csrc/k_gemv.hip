@@ -685,6 +685,11 @@ __device__ __forceinline__ void swap_rows(uint32_t v, uint32_t & r0, uint32_t & 
     r1 = a[1];
 }
 __device__ __forceinline__ uint4 map4(const uint4 & q, uint32_t (*f)(uint32_t)) { return make_uint4(f(q.x), f(q.y), f(q.z), f(q.w)); }
+// the 32 codes of q through the codebook (iq4_lookup8): lo from the low nibbles, hi from the high
+__device__ __forceinline__ void iq4_map8(const uint4 & q, const Iq4Regs & k, uint4 & lo, uint4 & hi) {
+    iq4_lookup8(q.x, k, lo.x, hi.x); iq4_lookup8(q.y, k, lo.y, hi.y);
+    iq4_lookup8(q.z, k, lo.z, hi.z); iq4_lookup8(q.w, k, lo.w, hi.w);
+}
 __device__ __forceinline__ uint4 nib(const uint4 & q, int sh) {
     const uint32_t m = 0x0F0F0F0Fu;
     return make_uint4((q.x >> sh) & m, (q.y >> sh) & m, (q.z >> sh) & m, (q.w >> sh) & m);
@@ -759,6 +764,7 @@ __device__ __forceinline__ void mma_stage(const uint4 (&rw)[NL], int st, const u
     };
     if constexpr (BF) {
         const uint32_t dw2[4] = { rw[8].x, rw[8].y, rw[8].z, rw[8].w };
+        const Iq4Regs kr = iq4_regs();                        // IQ4_NL: the codebook in VGPRs
         v4i an = a_op(0);                                     // LDS reads one block ahead
         float dn[NR];
         dx_op(0, dn);
@@ -773,8 +779,7 @@ __device__ __forceinline__ void mma_stage(const uint4 (&rw)[NL], int st, const u
                 lo = rw[2 * b];
                 hi = rw[2 * b + 1];
             } else if constexpr (NLQ) {
-                lo = map4(nib(rw[b], 0), iq4_lookup);
-                hi = map4(nib(rw[b], 4), iq4_lookup);
+                iq4_map8(rw[b], kr, lo, hi);
             } else {
                 lo = map4(nib(rw[b], 0), q4_minus8);
                 hi = map4(nib(rw[b], 4), q4_minus8);
@@ -901,6 +906,7 @@ __device__ __forceinline__ void mma_stage(const uint4 (&rw)[NL], int st, const u
         }
     } else if constexpr (IQ) {
         const uint32_t shi = rw[8].x >> 16, slo = rw[8].y;
+        const Iq4Regs kr = iq4_regs();                        // the codebook in VGPRs
         vNi<CM> isum = {};
         v16i pe0, pe1;
         int ps0 = 0, ps1 = 0;
@@ -908,7 +914,9 @@ __device__ __forceinline__ void mma_stage(const uint4 (&rw)[NL], int st, const u
 #pragma unroll
         for (int ib = 0; ib < 8; ++ib) {
             v4i op0, op1;
-            swap_halves(map4(nib(rw[ib], 0), iq4_lookup), map4(nib(rw[ib], 4), iq4_lookup), op0, op1);
+            uint4 lo, hi;
+            iq4_map8(rw[ib], kr, lo, hi);
+            swap_halves(lo, hi, op0, op1);
             uint32_t s0, s1;
             swap_rows(((slo >> (4 * ib)) & 0xFu) | (((shi >> (2 * ib)) & 3u) << 4), s0, s1);
             const v4i av = an;
