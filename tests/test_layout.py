@@ -8,7 +8,9 @@
   image (which nibble meets which activation code, where each scale comes
   from), compared with the CPU oracle's ggml-cpu dot products;
 * the GEMV launch plan: the waves cover the K axis, no work-group is left
-  without groups, and the LDS of the cross-wave sum is what the plan says.
+  without groups, and the LDS of the cross-wave sum is what the plan says;
+* the IQ4 codebook lookup's byte arithmetic (three v_perm_b32 per four codes,
+  emulated) against the oracle's codebook for every byte value.
 """
 import os
 
@@ -417,3 +419,73 @@ def test_gemm_tail_split_plan(qtype, K, M, tail, wgs, monkeypatch):
                                 qmm.Tensor(fake, qmm.F32, (M, 512)))
     assert info["path"] == "gemm-stream" and info["threads"] == 256 and info["k_slices"] == 1
     assert info["workgroups"] == wgs
+
+
+# ---- the IQ4 codebook lookup's byte arithmetic (qmm_device.h: iq4_lookup, iq4_lookup8,
+# iq4_lookup_r), on the CPU: v_perm_b32 emulated for selector bytes 0-7, every byte value in
+# every position, against the oracle's codebook (ggml-quants.c kvalues_iq4nl)
+
+def _perm(hi, lo, sel):
+    """v_perm_b32 for selector bytes 0-7: byte i of the result is byte sel.i of {hi:lo}."""
+    hi, lo, sel = np.broadcast_arrays(np.asarray(hi, np.uint32), np.asarray(lo, np.uint32), np.asarray(sel, np.uint32))
+    both = (hi.astype(np.uint64) << np.uint64(32)) | lo.astype(np.uint64)
+    out = np.zeros(lo.shape, np.uint64)
+    for i in range(4):
+        s = (sel >> np.uint32(8 * i)) & np.uint32(0xFF)
+        assert int(s.max()) <= 7
+        out |= ((both >> (np.uint64(8) * s.astype(np.uint64))) & np.uint64(0xFF)) << np.uint64(8 * i)
+    return out.astype(np.uint32)
+
+
+def _kv_words(kv):
+    b = (np.asarray(kv, np.int64) & 0xFF).astype(np.uint32)
+    return [np.uint32(b[4 * i] | (b[4 * i + 1] << 8) | (b[4 * i + 2] << 16) | (b[4 * i + 3] << 24))
+            for i in range(4)]
+
+
+def _lookup_r(x, k):
+    """iq4_lookup_r: the codes in bits 0-3 of each byte of x, bits 4-7 ignored."""
+    il = x & np.uint32(0x07070707)
+    sl = ((x >> np.uint32(1)) & np.uint32(0x04040404)) | np.uint32(0x03020100)
+    return _perm(_perm(k[3], k[2], il), _perm(k[1], k[0], il), sl)
+
+
+def _lookup8(q, k):
+    """iq4_lookup8: both nibbles of q's four bytes, the shift shared."""
+    t = q >> np.uint32(4)
+    il, ih = q & np.uint32(0x07070707), t & np.uint32(0x07070707)
+    sl = ((q >> np.uint32(1)) & np.uint32(0x04040404)) | np.uint32(0x03020100)
+    sh = ((t >> np.uint32(1)) & np.uint32(0x04040404)) | np.uint32(0x03020100)
+    return (_perm(_perm(k[3], k[2], il), _perm(k[1], k[0], il), sl),
+            _perm(_perm(k[3], k[2], ih), _perm(k[1], k[0], ih), sh))
+
+
+def _codes(v, sh):
+    return [(v >> np.uint32(8 * i + sh)) & np.uint32(0xF) for i in range(4)]
+
+
+def _decoded(v):
+    return [(v >> np.uint32(8 * i)) & np.uint32(0xFF) for i in range(4)]
+
+
+def test_iq4_lookup_bytes(orc):
+    kv = np.array(orc.kvalues(), np.int64)
+    assert kv.tolist() == KV.tolist()
+    k = _kv_words(kv)
+    table = (kv & 0xFF).astype(np.uint32)
+    rng = np.random.default_rng(7)
+    b = np.arange(256, dtype=np.uint32)
+    # every byte value in each of the four positions (the others random), then random dwords
+    qs = [np.concatenate([b << np.uint32(8 * p) | (rng.integers(0, 2**32, 256, dtype=np.uint64).astype(np.uint32)
+                                                  & ~np.uint32(0xFF << (8 * p)))
+                          for p in range(4)]),
+          rng.integers(0, 2**32, 4096, dtype=np.uint64).astype(np.uint32)]
+    for q in qs:
+        lo, hi = _lookup8(q, k)
+        for got, sh in ((lo, 0), (hi, 4)):
+            for g, c in zip(_decoded(got), _codes(q, sh)):
+                assert np.array_equal(g, table[c])
+        # the single-nibble form on an unmasked shift (the streaming GEMM's use)
+        for sh in (0, 4):
+            for g, c in zip(_decoded(_lookup_r(q >> np.uint32(sh), k)), _codes(q, sh)):
+                assert np.array_equal(g, table[c])
